@@ -1,0 +1,192 @@
+/*
+ * lg.h -- C ABI of the MI355X (gfx950) Laya decoder engine.
+ *
+ * Plain pointers, sizes and status codes; no C++ or torch types cross this line.
+ * Every call returns LG_OK (0) or an LG_ERR_* code, and on failure sets a
+ * thread-local message readable through lg_last_error() -- the counterpart of
+ * the reference's `Result<_, String>` (src/models/mod.rs:13-23).  No call aborts
+ * the process; a failed call leaves its handle usable.
+ *
+ * Thread-safety: an lg_engine is not re-entrant (calls on one engine serialise on
+ * its HIP stream); distinct engines are independent.  lg_gguf handles are
+ * read-only after open and may be shared.
+ */
+#ifndef LAYA_LG_H
+#define LAYA_LG_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LG_OK 0
+#define LG_ERR_INVALID 1     /* bad argument, shape or token id */
+#define LG_ERR_FORMAT 2      /* GGUF parse / model validation failure */
+#define LG_ERR_DEVICE 3      /* HIP runtime error */
+#define LG_ERR_OOM 4         /* device arena or KV pages exhausted */
+#define LG_ERR_CANCELED 5    /* the cancel callback returned non-zero */
+#define LG_ERR_UNSUPPORTED 6 /* tensor kind / shape the engine has no kernel for */
+
+/* GGML tensor kinds accepted by src/gguf.rs:81-93. */
+#define LG_F32 0u
+#define LG_F16 1u
+#define LG_Q4_0 2u
+#define LG_Q8_0 8u
+#define LG_Q4_K 12u
+#define LG_Q6_K 14u
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *lg_last_error(void);
+/* "laya-mi355x <version> gfx950" */
+const char *lg_version(void);
+
+/* ---------------------------------------------------------------- formats */
+
+/* (elements per block, bytes per block) of a tensor kind.
+ * Replaces gguf::layout, src/gguf.rs:81-93. */
+int lg_layout(uint32_t kind, uint64_t *block, uint64_t *bytes);
+
+/* IEEE binary16 -> f32, exact incl. subnormals, Inf and NaN payloads.
+ * Replaces gguf::half, src/gguf.rs:226-246. */
+float lg_half(uint16_t bits);
+
+typedef struct lg_gguf lg_gguf;
+
+/* Open and validate a GGUF v3 file through a read-only private mmap.
+ * Replaces Gguf::open, src/gguf.rs:95-179 (and io::Mapping::open, src/io.rs:65-88);
+ * the error messages are the reference's. */
+int lg_gguf_open(const char *path, lg_gguf **out);
+/* Same over caller-owned bytes, borrowed until lg_gguf_close. */
+int lg_gguf_open_memory(const void *bytes, uint64_t len, lg_gguf **out);
+void lg_gguf_close(lg_gguf *g);
+
+int lg_gguf_tensor_count(const lg_gguf *g);
+/* Name of tensor i (file order). */
+const char *lg_gguf_tensor_name(const lg_gguf *g, int i);
+/* Tensor lookup, replaces Gguf::data, src/gguf.rs:193-199.  dims[0] is the row length. */
+int lg_gguf_tensor(const lg_gguf *g, const char *name, uint32_t *kind, uint64_t dims[4], int *nd,
+                   const void **data, uint64_t *len);
+/* Metadata, replaces Gguf::get / Gguf::num, src/gguf.rs:181-189.  *found = 0 when absent. */
+int lg_gguf_meta_num(const lg_gguf *g, const char *key, double *value, int *found);
+int lg_gguf_meta_str(const lg_gguf *g, const char *key, const char **value, int *found);
+
+/* Dequantise `len` bytes of GGUF blocks of `kind` into `dst` (len/bytes*block floats) on
+ * the GPU, bit-identical to gguf::decode, src/gguf.rs:250-336.  Host pointers. */
+int lg_dequant(uint32_t kind, const void *src, uint64_t len, float *dst);
+
+/* ------------------------------------------------------------ synthetic models */
+
+/* Seeded synthetic "laya-decoder" GGUF (general.architecture = "ggmlc",
+ * laya.model_name = "laya-decoder").  `preset` names a workload shape
+ * ("plumbing-f16", "q8-2048", "q4km-7b", "f16-7b", or "tiny-*" test shapes);
+ * n_layers > 0 overrides the layer count.  The image is malloc'd; free it with
+ * lg_synth_free.  Deterministic in (preset, seed, n_layers). */
+int lg_synth_gguf(const char *preset, uint64_t seed, int n_layers, void **image, uint64_t *len);
+/* Write the same image to a file. */
+int lg_synth_gguf_file(const char *preset, uint64_t seed, int n_layers, const char *path);
+void lg_synth_free(void *image);
+
+/* ---------------------------------------------------------------- engine */
+
+typedef struct lg_engine lg_engine;
+
+typedef struct {
+  int device;              /* HIP device ordinal */
+  int kv_pages;            /* 64-token KV pages to reserve (0 = derive from kv_tokens) */
+  int64_t kv_tokens;       /* tokens of KV capacity when kv_pages == 0 (0 = 65536) */
+  int64_t max_batch_tokens;/* largest prefill batch (0 = 65536) */
+} lg_engine_opts;
+
+typedef struct {
+  int layers, d_model, heads, kv_heads, head_dim, ffn, vocab, context;
+  uint32_t kind_attn, kind_ffn, kind_head; /* GGML kinds of the uploaded matrices */
+  int64_t weight_bytes;    /* HBM bytes of the uploaded weight arena */
+  int64_t kv_bytes;        /* HBM bytes of the KV page pool */
+  int kv_pages, kv_page_tokens;
+} lg_model_info;
+
+/* Load a laya-decoder GGUF onto one GPU: validate, upload and repack every matrix into a
+ * hipMalloc'd weight arena, reserve the KV page pool, create the engine's stream.
+ * Replaces Engine::new / models::load / Model::new (src/engine.rs:16-34,
+ * src/models/mod.rs:65-71, src/models/openthai/model.rs:96-191) -- without the F32
+ * expansion at load. */
+int lg_engine_create(const lg_gguf *g, const lg_engine_opts *opts, lg_engine **out);
+void lg_engine_destroy(lg_engine *e);
+/* Replaces Backend::layers, src/models/mod.rs:14, plus the shapes. */
+int lg_engine_info(const lg_engine *e, lg_model_info *info);
+/* Block until all work queued on the engine's stream has finished. */
+int lg_engine_sync(lg_engine *e);
+
+/* y[m][rows] = x[m][cols] . W[rows][cols]^T (+ bias[rows]) with W the named uploaded
+ * matrix.  Host pointers.  Replaces Matrix::apply, src/tensor.rs:10-39. */
+int lg_matmul(lg_engine *e, const char *tensor, const float *x, int m, const float *bias, float *y);
+
+/* ---- sequences over the paged F16 KV cache (no reference counterpart: the reference
+ * recomputes every forward from scratch, src/models/openthai/model.rs:192-241) ---- */
+int lg_seq_create(lg_engine *e, int *seq);
+/* New sequence sharing the first `ntokens` tokens' KV pages of `parent` (whole pages are
+ * shared by reference count; a partially filled last page is copied). */
+int lg_seq_fork(lg_engine *e, int parent, int ntokens, int *child);
+int lg_seq_free(lg_engine *e, int seq);
+int lg_seq_len(lg_engine *e, int seq, int *len);
+
+typedef int (*lg_cancel_fn)(void *arg); /* non-zero = cancel; polled between layers */
+
+/* Append `n` tokens to `seq`, run them through every layer and return logits at the
+ * `npos` positions (indices into the n new tokens) for the head rows `vocab_ids`
+ * (NULL = the full vocabulary, nv ignored).  logits is [npos][nv] (host).
+ * Replaces Model::forward(ids, positions, canceled), src/models/openthai/model.rs:192-241. */
+int lg_forward(lg_engine *e, int seq, const int32_t *ids, int n, const int32_t *positions,
+               int npos, const int32_t *vocab_ids, int nv, float *logits, lg_cancel_fn cancel,
+               void *cancel_arg);
+
+/* One request of a batched prefill. */
+typedef struct {
+  int seq;                  /* sequence to append to */
+  const int32_t *ids;       /* n token ids */
+  int n;
+  const int32_t *positions; /* npos answer positions (indices into ids) */
+  int npos;
+} lg_request;
+
+typedef struct lg_batch lg_batch;
+
+/* Stage a batch of requests in HBM (token ids, positions, page tables).  Replaces the
+ * sequential per-request loop of /v1/decide/batch (src/server.rs:301-319) with one GPU
+ * batch.  The sequences' KV pages are reserved here. */
+int lg_batch_create(lg_engine *e, const lg_request *reqs, int nreq, lg_batch **out);
+void lg_batch_free(lg_engine *e, lg_batch *b);
+/* Run a staged batch: prefill every request, then option scoring at every answer position
+ * over the head rows `option_ids` (k of them) with temperature `temperature`.
+ * Outputs (host, [sum npos][k], NULL to skip): raw logits, probabilities, log-probabilities.
+ * Probabilities follow src/models/openthai/decision.rs:268-279,297-303; log-probabilities
+ * are the option log-softmax of logit/temperature. */
+int lg_batch_run(lg_engine *e, lg_batch *b, const int32_t *option_ids, int k, float temperature,
+                 float *logits, float *probs, float *logprobs, lg_cancel_fn cancel,
+                 void *cancel_arg);
+
+/* Greedy decode: feed `first` and then each argmax for `steps` single-token steps on `seq`
+ * (which must hold its prefilled context).  tokens[steps] receives each step's argmax
+ * (first maximum wins, src/models/openthai/decision.rs:330-335); logits (optional, host,
+ * [steps][vocab]) each step's full-vocabulary logits. */
+int lg_decode(lg_engine *e, int seq, int32_t first, int steps, int32_t *tokens, float *logits);
+
+/* Option scores over host logits, the CPU side of the same rule (for callers that
+ * already hold logits).  Replaces src/models/openthai/decision.rs:268-279. */
+int lg_option_scores(const float *logits, int k, float temperature, float *probs,
+                     float *logprobs);
+
+/* ---- profiling: per-kernel-class HIP event timing on the engine's stream ---- */
+/* When on, every launch of the timed kernel classes is bracketed by HIP events. */
+int lg_profile_enable(lg_engine *e, int on);
+/* Accumulated launches and device milliseconds of one kernel class since the last reset
+ * ("gemm", "gemv", "attn_prefill", "attn_decode", "rope_kv", "rmsnorm", "embed", "head"). */
+int lg_profile_read(lg_engine *e, const char *cls, int64_t *launches, double *ms,
+                    double *bytes, double *flops);
+int lg_profile_reset(lg_engine *e);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,398 @@
+// extern "C" surface of include/lg.h.  Every entry point converts library exceptions into
+// an LG_ERR_* status and a thread-local message; nothing escapes as a C++ exception and no
+// call aborts the process.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "common.h"
+#include "engine.h"
+#include "gguf.h"
+#include "kernels.h"
+#include "lg.h"
+
+namespace lg {
+void synth_image(const char *preset, uint64_t seed, int n_layers, uint8_t **out, uint64_t *out_len);
+}  // namespace lg
+
+struct lg_gguf {
+  lg::Gguf *g;
+};
+struct lg_engine {
+  lg::Engine *e;
+};
+struct lg_batch {
+  lg::BatchPlan *b;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+template <class F>
+int guard(F &&f) {
+  try {
+    f();
+    g_err.clear();
+    return LG_OK;
+  } catch (const lg::Error &e) {
+    g_err = e.what();
+    return e.code;
+  } catch (const std::bad_alloc &) {
+    g_err = "out of host memory";
+    return LG_ERR_OOM;
+  } catch (const std::exception &e) {
+    g_err = e.what();
+    return LG_ERR_INVALID;
+  } catch (...) {
+    g_err = "unknown error";
+    return LG_ERR_INVALID;
+  }
+}
+
+#define NEED(p, what) \
+  if (!(p)) ::lg::fail(LG_ERR_INVALID, "%s must not be null", what)
+
+}  // namespace
+
+extern "C" {
+
+const char *lg_last_error(void) { return g_err.c_str(); }
+
+const char *lg_version(void) { return "laya-mi355x 0.1.0 gfx950"; }
+
+int lg_layout(uint32_t kind, uint64_t *block, uint64_t *bytes) {
+  return guard([&] {
+    if (!lg::layout(kind, block, bytes))
+      lg::fail(LG_ERR_UNSUPPORTED, "unsupported GGML tensor type %u; supported F32/F16/Q4_0/Q8_0/Q4_K/Q6_K", kind);
+  });
+}
+
+float lg_half(uint16_t bits) { return lg::half_to_float(bits); }
+
+int lg_gguf_open(const char *path, lg_gguf **out) {
+  return guard([&] {
+    NEED(path, "path");
+    NEED(out, "out");
+    *out = nullptr;
+    lg::Gguf *g = lg::Gguf::open_file(path);
+    *out = new lg_gguf{g};
+  });
+}
+
+int lg_gguf_open_memory(const void *bytes, uint64_t len, lg_gguf **out) {
+  return guard([&] {
+    NEED(out, "out");
+    *out = nullptr;
+    if (!bytes && len) lg::fail(LG_ERR_INVALID, "bytes must not be null");
+    lg::Gguf *g = lg::Gguf::open_memory(static_cast<const uint8_t *>(bytes), len);
+    *out = new lg_gguf{g};
+  });
+}
+
+void lg_gguf_close(lg_gguf *g) {
+  if (!g) return;
+  delete g->g;
+  delete g;
+}
+
+int lg_gguf_tensor_count(const lg_gguf *g) { return g ? int(g->g->tensors().size()) : 0; }
+
+const char *lg_gguf_tensor_name(const lg_gguf *g, int i) {
+  if (!g || i < 0 || i >= int(g->g->tensors().size())) return nullptr;
+  return g->g->tensors()[i].name.c_str();
+}
+
+int lg_gguf_tensor(const lg_gguf *g, const char *name, uint32_t *kind, uint64_t dims[4], int *nd,
+                   const void **data, uint64_t *len) {
+  return guard([&] {
+    NEED(g, "g");
+    NEED(name, "name");
+    const lg::TensorInfo *t = g->g->tensor(name);
+    if (!t) lg::fail(LG_ERR_INVALID, "missing tensor %s", name);
+    if (kind) *kind = t->kind;
+    if (dims) {
+      for (int i = 0; i < 4; ++i) dims[i] = i < int(t->dims.size()) ? t->dims[i] : 1;
+    }
+    if (nd) *nd = int(t->dims.size());
+    if (data) *data = g->g->data(*t);
+    if (len) *len = t->len;
+  });
+}
+
+int lg_gguf_meta_num(const lg_gguf *g, const char *key, double *value, int *found) {
+  return guard([&] {
+    NEED(g, "g");
+    NEED(key, "key");
+    const lg::MetaValue *v = g->g->meta(key);
+    if (found) *found = v != nullptr;
+    if (value) *value = v ? g->g->num(key, 0) : 0.0;
+  });
+}
+
+int lg_gguf_meta_str(const lg_gguf *g, const char *key, const char **value, int *found) {
+  return guard([&] {
+    NEED(g, "g");
+    NEED(key, "key");
+    const lg::MetaValue *v = g->g->meta(key);
+    if (found) *found = v != nullptr;
+    if (value) *value = v ? v->str.c_str() : "";
+  });
+}
+
+int lg_dequant(uint32_t kind, const void *src, uint64_t len, float *dst) {
+  return guard([&] {
+    uint64_t block, size;
+    if (!lg::layout(kind, &block, &size))
+      lg::fail(LG_ERR_UNSUPPORTED, "unsupported GGML tensor type %u; supported F32/F16/Q4_0/Q8_0/Q4_K/Q6_K", kind);
+    if (len % size) lg::fail(LG_ERR_INVALID, "length %llu is not a whole number of blocks", (unsigned long long)len);
+    if (len == 0) return;
+    NEED(src, "src");
+    NEED(dst, "dst");
+    const uint64_t nblocks = len / size, nelem = nblocks * block;
+    lg::DevBuf dsrc, ddst;
+    dsrc.ensure(len);
+    ddst.ensure(nelem * 4);
+    HIP_CHECK(hipMemcpy(dsrc.p, src, len, hipMemcpyHostToDevice));
+    if (kind == LG_Q4_0 || kind == LG_F32) {
+      lg::launch_dequant(kind, dsrc.as<uint8_t>(), nblocks, ddst.as<float>(), nullptr);
+    } else {
+      // through the engine's repacked layout: the exact arithmetic the GEMV kernels use
+      lg::DevBuf q, s;
+      lg::DevMatrix w;
+      w.kind = kind;
+      w.rows = int(nblocks);
+      w.cols = int(block);
+      LG_REQUIRE(nblocks < (1ull << 31), "too many blocks");
+      const int64_t n = int64_t(nelem);
+      const int64_t qb = kind == LG_F16 ? n * 2 : kind == LG_Q4_K ? n / 2 : n;
+      const int64_t sb = kind == LG_Q8_0 ? n / 32 * 2 : kind == LG_Q4_K ? n / 32 * 8 : kind == LG_Q6_K ? n / 16 * 4 : 0;
+      q.ensure(size_t(qb));
+      w.q = q.p;
+      if (sb) {
+        s.ensure(size_t(sb));
+        w.s = s.p;
+      }
+      lg::launch_repack(kind, dsrc.as<uint8_t>(), w.rows, w.cols, w, nullptr);
+      lg::launch_dequant_repacked(w, ddst.as<float>(), nullptr);
+    }
+    HIP_CHECK(hipDeviceSynchronize());
+    HIP_CHECK(hipMemcpy(dst, ddst.p, nelem * 4, hipMemcpyDeviceToHost));
+  });
+}
+
+int lg_synth_gguf(const char *preset, uint64_t seed, int n_layers, void **image, uint64_t *len) {
+  return guard([&] {
+    NEED(preset, "preset");
+    NEED(image, "image");
+    NEED(len, "len");
+    uint8_t *img = nullptr;
+    lg::synth_image(preset, seed, n_layers, &img, len);
+    *image = img;
+  });
+}
+
+int lg_synth_gguf_file(const char *preset, uint64_t seed, int n_layers, const char *path) {
+  return guard([&] {
+    NEED(preset, "preset");
+    NEED(path, "path");
+    uint8_t *img = nullptr;
+    uint64_t len = 0;
+    lg::synth_image(preset, seed, n_layers, &img, &len);
+    FILE *fp = std::fopen(path, "wb");
+    if (!fp) {
+      std::free(img);
+      lg::fail(LG_ERR_INVALID, "cannot write %s", path);
+    }
+    const size_t w = std::fwrite(img, 1, len, fp);
+    std::fclose(fp);
+    std::free(img);
+    if (w != len) lg::fail(LG_ERR_INVALID, "short write to %s", path);
+  });
+}
+
+void lg_synth_free(void *image) { std::free(image); }
+
+int lg_engine_create(const lg_gguf *g, const lg_engine_opts *opts, lg_engine **out) {
+  return guard([&] {
+    NEED(g, "g");
+    NEED(out, "out");
+    *out = nullptr;
+    lg_engine_opts o{};
+    if (opts) o = *opts;
+    lg::Engine *e = new lg::Engine(*g->g, o);
+    *out = new lg_engine{e};
+  });
+}
+
+void lg_engine_destroy(lg_engine *e) {
+  if (!e) return;
+  try {
+    delete e->e;
+  } catch (...) {
+  }
+  delete e;
+}
+
+int lg_engine_info(const lg_engine *e, lg_model_info *info) {
+  return guard([&] {
+    NEED(e, "engine");
+    NEED(info, "info");
+    *info = e->e->info();
+  });
+}
+
+int lg_engine_sync(lg_engine *e) {
+  return guard([&] {
+    NEED(e, "engine");
+    e->e->sync();
+  });
+}
+
+int lg_matmul(lg_engine *e, const char *tensor, const float *x, int m, const float *bias, float *y) {
+  return guard([&] {
+    NEED(e, "engine");
+    NEED(tensor, "tensor");
+    NEED(x, "x");
+    NEED(y, "y");
+    e->e->matmul(tensor, x, m, bias, y);
+  });
+}
+
+int lg_seq_create(lg_engine *e, int *seq) {
+  return guard([&] {
+    NEED(e, "engine");
+    NEED(seq, "seq");
+    *seq = e->e->seq_create();
+  });
+}
+
+int lg_seq_fork(lg_engine *e, int parent, int ntokens, int *child) {
+  return guard([&] {
+    NEED(e, "engine");
+    NEED(child, "child");
+    *child = e->e->seq_fork(parent, ntokens);
+  });
+}
+
+int lg_seq_free(lg_engine *e, int seq) {
+  return guard([&] {
+    NEED(e, "engine");
+    e->e->seq_free(seq);
+  });
+}
+
+int lg_seq_len(lg_engine *e, int seq, int *len) {
+  return guard([&] {
+    NEED(e, "engine");
+    NEED(len, "len");
+    *len = e->e->seq_len(seq);
+  });
+}
+
+int lg_forward(lg_engine *e, int seq, const int32_t *ids, int n, const int32_t *positions, int npos,
+               const int32_t *vocab_ids, int nv, float *logits, lg_cancel_fn cancel, void *cancel_arg) {
+  return guard([&] {
+    NEED(e, "engine");
+    if (npos > 0) NEED(logits, "logits");
+    if (vocab_ids) LG_REQUIRE(nv > 0 && nv <= 32, "nv must be 1..32 when vocab_ids is given");
+    e->e->forward(seq, ids, n, positions, npos, vocab_ids, nv, logits, cancel, cancel_arg);
+  });
+}
+
+int lg_batch_create(lg_engine *e, const lg_request *reqs, int nreq, lg_batch **out) {
+  return guard([&] {
+    NEED(e, "engine");
+    NEED(out, "out");
+    *out = nullptr;
+    lg::BatchPlan *b = e->e->batch_create(reqs, nreq);
+    *out = new lg_batch{b};
+  });
+}
+
+void lg_batch_free(lg_engine *e, lg_batch *b) {
+  if (!b) return;
+  if (e) e->e->batch_free(b->b);
+  delete b;
+}
+
+int lg_batch_run(lg_engine *e, lg_batch *b, const int32_t *option_ids, int k, float temperature,
+                 float *logits, float *probs, float *logprobs, lg_cancel_fn cancel, void *cancel_arg) {
+  return guard([&] {
+    NEED(e, "engine");
+    NEED(b, "batch");
+    e->e->batch_run(b->b, option_ids, k, temperature, logits, probs, logprobs, cancel, cancel_arg);
+  });
+}
+
+int lg_decode(lg_engine *e, int seq, int32_t first, int steps, int32_t *tokens, float *logits) {
+  return guard([&] {
+    NEED(e, "engine");
+    e->e->decode(seq, first, steps, tokens, logits);
+  });
+}
+
+int lg_option_scores(const float *logits, int k, float temperature, float *probs, float *logprobs) {
+  return guard([&] {
+    NEED(logits, "logits");
+    LG_REQUIRE(k > 0 && k <= 256, "k must be 1..256");
+    LG_REQUIRE(temperature > 0 && std::isfinite(temperature), "temperature must be positive");
+    float z[256], p[256];
+    float m = -INFINITY;
+    for (int i = 0; i < k; ++i) {
+      z[i] = logits[i] / temperature;
+      m = std::fmax(m, z[i]);
+    }
+    float s = 0.0f;
+    for (int i = 0; i < k; ++i) {
+      p[i] = std::exp(z[i] - m);
+      s += p[i];
+    }
+    float sum = 0.0f;
+    for (int i = 0; i < k; ++i) {
+      p[i] /= s;
+      sum += p[i];
+    }
+    sum = std::fmax(sum, 1e-12f);
+    float s2 = 0.0f;
+    for (int i = 0; i < k; ++i) {
+      p[i] /= sum;
+      s2 += p[i];
+    }
+    s2 = std::fmax(s2, 1e-12f);
+    const float lse = std::log(s);
+    for (int i = 0; i < k; ++i) {
+      if (probs) probs[i] = p[i] / s2;
+      if (logprobs) logprobs[i] = z[i] - m - lse;
+    }
+  });
+}
+
+int lg_profile_enable(lg_engine *e, int on) {
+  return guard([&] {
+    NEED(e, "engine");
+    e->e->prof.enable(on != 0);
+  });
+}
+
+int lg_profile_read(lg_engine *e, const char *cls, int64_t *launches, double *ms, double *bytes,
+                    double *flops) {
+  return guard([&] {
+    NEED(e, "engine");
+    NEED(cls, "cls");
+    e->e->prof.read(cls, launches, ms, bytes, flops);
+  });
+}
+
+int lg_profile_reset(lg_engine *e) {
+  return guard([&] {
+    NEED(e, "engine");
+    e->e->prof.reset();
+  });
+}
+
+}  // extern "C"

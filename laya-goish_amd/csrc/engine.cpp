@@ -1,0 +1,761 @@
+// Engine: model upload, paged KV cache, batched prefill and greedy decode drivers.
+#include "engine.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <numeric>
+
+#include "common.h"
+
+namespace lg {
+
+// ------------------------------------------------------------------ DevBuf / Profiler
+void DevBuf::ensure(size_t bytes) {
+  if (bytes <= n) return;
+  if (p) HIP_CHECK(hipFree(p));
+  p = nullptr;
+  n = 0;
+  const size_t want = std::max(bytes, size_t(256));
+  if (hipMalloc(&p, want) != hipSuccess) {
+    p = nullptr;
+    (void)hipGetLastError();
+    fail(LG_ERR_OOM, "cannot allocate %zu bytes of workspace", want);
+  }
+  n = want;
+}
+
+DevBuf::~DevBuf() {
+  if (p) (void)hipFree(p);
+}
+
+void Profiler::begin(const char *cls, hipStream_t st) {
+  if (!on_) return;
+  cur_ = cls;
+  if (pool_.empty()) {
+    hipEvent_t e;
+    HIP_CHECK(hipEventCreate(&e));
+    pool_.push_back(e);
+  }
+  cur_a_ = pool_.back();
+  pool_.pop_back();
+  HIP_CHECK(hipEventRecord(cur_a_, st));
+}
+
+void Profiler::end(double bytes, double flops, hipStream_t st) {
+  if (!on_) return;
+  if (pool_.empty()) {
+    hipEvent_t e;
+    HIP_CHECK(hipEventCreate(&e));
+    pool_.push_back(e);
+  }
+  hipEvent_t b = pool_.back();
+  pool_.pop_back();
+  HIP_CHECK(hipEventRecord(b, st));
+  open_.push_back({cur_, cur_a_, b, bytes, flops});
+  if (open_.size() > 4096) drain();
+}
+
+void Profiler::drain() {
+  for (auto &r : open_) {
+    HIP_CHECK(hipEventSynchronize(r.b));
+    float ms = 0;
+    HIP_CHECK(hipEventElapsedTime(&ms, r.a, r.b));
+    Sum &s = sums_[r.cls];
+    s.launches += 1;
+    s.ms += ms;
+    s.bytes += r.bytes;
+    s.flops += r.flops;
+    pool_.push_back(r.a);
+    pool_.push_back(r.b);
+  }
+  open_.clear();
+}
+
+void Profiler::read(const std::string &cls, int64_t *launches, double *ms, double *bytes, double *flops) {
+  drain();
+  Sum s;
+  auto it = sums_.find(cls);
+  if (it != sums_.end()) s = it->second;
+  if (launches) *launches = s.launches;
+  if (ms) *ms = s.ms;
+  if (bytes) *bytes = s.bytes;
+  if (flops) *flops = s.flops;
+}
+
+void Profiler::reset() {
+  drain();
+  sums_.clear();
+}
+
+Profiler::~Profiler() {
+  for (auto &r : open_) {
+    (void)hipEventDestroy(r.a);
+    (void)hipEventDestroy(r.b);
+  }
+  for (auto e : pool_) (void)hipEventDestroy(e);
+}
+
+// ------------------------------------------------------------------ helpers
+namespace {
+
+int64_t q_row_bytes(uint32_t kind, int cols) {
+  switch (kind) {
+    case LG_F32: return int64_t(cols) * 4;
+    case LG_F16: return int64_t(cols) * 2;
+    case LG_Q8_0: return cols;
+    case LG_Q4_K: return cols / 2;
+    case LG_Q6_K: return cols;
+  }
+  return 0;
+}
+int64_t s_row_bytes(uint32_t kind, int cols) {
+  switch (kind) {
+    case LG_Q8_0: return int64_t(cols / 32) * 2;
+    case LG_Q4_K: return int64_t(cols / 32) * 8;
+    case LG_Q6_K: return int64_t(cols / 16) * 4;
+  }
+  return 0;
+}
+DevMatrix sub_rows(const DevMatrix &m, int row0, int nrows) {
+  DevMatrix s = m;
+  s.rows = nrows;
+  s.q = static_cast<uint8_t *>(m.q) + q_row_bytes(m.kind, m.cols) * row0;
+  if (m.s) s.s = static_cast<uint8_t *>(m.s) + s_row_bytes(m.kind, m.cols) * row0;
+  return s;
+}
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+}  // namespace
+
+// Planned batch: device metadata for one staged prefill batch.
+struct BatchPlan {
+  std::vector<int> seqs;        // engine sequence per request
+  std::vector<int> n, npos;     // tokens and answer positions per request
+  int T = 0, R = 0, ntiles = 0, max_pages = 0;
+  DevBuf meta;                  // ids, tok_seq, tok_pos, pages, tiles..., gather rows
+  int32_t *ids = nullptr, *tok_seq = nullptr, *tok_pos = nullptr, *pages = nullptr;
+  int32_t *tile_seq = nullptr, *tile_row0 = nullptr, *tile_pos0 = nullptr, *tile_n = nullptr;
+  int32_t *gather = nullptr;
+  bool ran = false;
+};
+
+// ------------------------------------------------------------------ construction
+Engine::Engine(const Gguf &g, const lg_engine_opts &opts) {
+  device = opts.device;
+  int ndev = 0;
+  HIP_CHECK(hipGetDeviceCount(&ndev));
+  if (device < 0 || device >= ndev) fail(LG_ERR_INVALID, "device %d out of range (%d devices)", device, ndev);
+  HIP_CHECK(hipSetDevice(device));
+  if (g.str("general.architecture") != "ggmlc" || g.str("laya.model_name") != "laya-decoder")
+    fail(LG_ERR_FORMAT, "unsupported ggmlc model %s", g.str("laya.model_name").c_str());
+  L = int(g.num("laya.decoder.block_count", 0));
+  d = int(g.num("laya.decoder.embedding_length", 0));
+  hq = int(g.num("laya.decoder.head_count", 0));
+  hkv = int(g.num("laya.decoder.head_count_kv", 0));
+  hd = int(g.num("laya.decoder.key_length", 0));
+  f = int(g.num("laya.decoder.feed_forward_length", 0));
+  V = int(g.num("laya.decoder.vocab_size", 0));
+  ctx = int(g.num("laya.decoder.context_length", 0));
+  eps = float(g.num("laya.decoder.layer_norm_rms_epsilon", 1e-5));
+  if (L < 1 || d < 1 || hq < 1 || hkv < 1 || hq % hkv || hd < 2 || hd % 2 || f < 1 || V < 1 || ctx < 1)
+    fail(LG_ERR_FORMAT, "invalid laya-decoder dimensions");
+  if (d % 64 || (hd != 64 && hd != 128))
+    fail(LG_ERR_UNSUPPORTED, "d_model %d / head_dim %d outside the kernels' shapes", d, hd);
+  max_batch_tokens_ = opts.max_batch_tokens > 0 ? opts.max_batch_tokens : 65536;
+  HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+  upload(g);
+  // KV pool: [L][npages][hkv][64][hd] halves for K, then the same for V
+  int64_t pages = opts.kv_pages;
+  if (pages <= 0) {
+    const int64_t toks = opts.kv_tokens > 0 ? opts.kv_tokens : 65536;
+    pages = (toks + 63) / 64;
+  }
+  npages_ = int(pages);
+  page_stride_ = int64_t(hkv) * 64 * hd;
+  const size_t kv_bytes = size_t(2) * L * npages_ * page_stride_ * 2;
+  if (hipMalloc(&kv_, kv_bytes) != hipSuccess) {
+    kv_ = nullptr;
+    (void)hipGetLastError();
+    fail(LG_ERR_OOM, "cannot allocate %zu bytes of KV pages", kv_bytes);
+  }
+  // zero once so never-written slots hold finite values (masked keys multiply V by 0)
+  HIP_CHECK(hipMemsetAsync(kv_, 0, kv_bytes, stream));
+  refcnt_.assign(npages_, 0);
+  free_pages_.resize(npages_);
+  for (int i = 0; i < npages_; ++i) free_pages_[i] = npages_ - 1 - i;
+  HIP_CHECK(hipStreamSynchronize(stream));
+}
+
+Engine::~Engine() {
+  if (stream) (void)hipStreamSynchronize(stream);
+  if (arena_) (void)hipFree(arena_);
+  if (emb_) (void)hipFree(emb_);
+  if (kv_) (void)hipFree(kv_);
+  if (stream) (void)hipStreamDestroy(stream);
+}
+
+void *Engine::carve(size_t bytes) {
+  bytes = align256(bytes);
+  if (arena_used_ + bytes > arena_size_) fail(LG_ERR_OOM, "weight arena exhausted");
+  void *p = static_cast<uint8_t *>(arena_) + arena_used_;
+  arena_used_ += bytes;
+  return p;
+}
+
+float *Engine::upload_vector_f32(const Gguf &g, const std::string &name, int64_t n) {
+  const TensorInfo *t = g.tensor(name);
+  if (!t) fail(LG_ERR_FORMAT, "missing tensor %s", name.c_str());
+  uint64_t count = 1;
+  for (auto v : t->dims) count *= v;
+  if (int64_t(count) != n) fail(LG_ERR_FORMAT, "%s: unexpected vector shape", name.c_str());
+  std::vector<float> h(n);
+  const uint8_t *src = g.data(*t);
+  if (t->kind == LG_F32) std::memcpy(h.data(), src, n * 4);
+  else if (t->kind == LG_F16)
+    for (int64_t i = 0; i < n; ++i) h[i] = half_to_float(uint16_t(src[2 * i] | (src[2 * i + 1] << 8)));
+  else fail(LG_ERR_UNSUPPORTED, "%s: vectors must be F32/F16", name.c_str());
+  float *dptr = static_cast<float *>(carve(n * 4));
+  HIP_CHECK(hipMemcpy(dptr, h.data(), n * 4, hipMemcpyHostToDevice));
+  return dptr;
+}
+
+// Upload one or more GGUF matrices with equal kind and row length as one row-concatenated
+// device matrix (q|k|v or gate|up): row blocks of the same layout are contiguous.
+DevMatrix Engine::upload_matrix(const Gguf &g, const std::vector<std::string> &names, int cols) {
+  DevMatrix m;
+  std::vector<const TensorInfo *> ts;
+  int rows = 0;
+  for (const auto &nm : names) {
+    const TensorInfo *t = g.tensor(nm);
+    if (!t) fail(LG_ERR_FORMAT, "missing tensor %s", nm.c_str());
+    if (t->dims.size() != 2 || t->cols() != uint64_t(cols))
+      fail(LG_ERR_FORMAT, "%s: unexpected matrix shape", nm.c_str());
+    if (!ts.empty() && t->kind != ts[0]->kind) fail(LG_ERR_FORMAT, "%s: mixed kinds in one projection", nm.c_str());
+    ts.push_back(t);
+    rows += int(t->rows());
+  }
+  m.kind = ts[0]->kind;
+  m.rows = rows;
+  m.cols = cols;
+  if (m.kind == LG_Q4_0) fail(LG_ERR_UNSUPPORTED, "Q4_0 matrices have no device kernel");
+  if ((m.kind == LG_Q4_K || m.kind == LG_Q6_K) && cols % 256)
+    fail(LG_ERR_FORMAT, "invalid quantized row alignment");
+  m.q = carve(size_t(q_row_bytes(m.kind, cols)) * rows);
+  if (s_row_bytes(m.kind, cols)) m.s = carve(size_t(s_row_bytes(m.kind, cols)) * rows);
+  size_t maxraw = 0;
+  for (auto *t : ts) maxraw = std::max<size_t>(maxraw, t->len);
+  DevBuf staging;
+  staging.ensure(maxraw);
+  int row0 = 0;
+  for (size_t i = 0; i < ts.size(); ++i) {
+    const TensorInfo *t = ts[i];
+    HIP_CHECK(hipMemcpy(staging.p, g.data(*t), t->len, hipMemcpyHostToDevice));
+    DevMatrix part = sub_rows(m, row0, int(t->rows()));
+    launch_repack(t->kind, staging.as<uint8_t>(), part.rows, cols, part, stream);
+    HIP_CHECK(hipStreamSynchronize(stream));
+    named_[names[i]] = part;
+    row0 += part.rows;
+  }
+  weight_bytes_ += m.gguf_bytes();
+  return m;
+}
+
+void Engine::upload(const Gguf &g) {
+  // size the arena: every matrix/vector tensor except the embedding table, + 256 B slack each
+  size_t total = 0;
+  for (const auto &t : g.tensors()) {
+    if (t.name == "tok_emb.weight") continue;
+    const uint64_t n = t.cols() * t.rows();
+    size_t need;
+    if (t.dims.size() == 1) need = n * 8;  // vectors: f32 copy, plus a fused-bias copy
+    else if (t.name == "cos_full" || t.name == "sin_full") need = n * 4;
+    else need = size_t(q_row_bytes(t.kind, int(t.cols())) + s_row_bytes(t.kind, int(t.cols()))) * t.rows();
+    total += align256(need) + 512;
+  }
+  arena_size_ = total;
+  if (hipMalloc(&arena_, arena_size_) != hipSuccess) {
+    arena_ = nullptr;
+    (void)hipGetLastError();
+    fail(LG_ERR_OOM, "cannot allocate %zu bytes of weights", arena_size_);
+  }
+  // embedding table: raw F16/F32 rows [V][d]
+  const TensorInfo *emb = g.tensor("tok_emb.weight");
+  if (!emb || emb->cols() != uint64_t(d) || emb->rows() != uint64_t(V) ||
+      (emb->kind != LG_F16 && emb->kind != LG_F32))
+    fail(LG_ERR_FORMAT, "tok_emb.weight must be F32/F16 [d, vocab]");
+  emb_kind = emb->kind;
+  HIP_CHECK(hipMalloc(&emb_, emb->len));
+  HIP_CHECK(hipMemcpy(emb_, g.data(*emb), emb->len, hipMemcpyHostToDevice));
+  weight_bytes_ += int64_t(emb->len);
+
+  const int qw = hq * hd, kvw = hkv * hd;
+  layers_.resize(L);
+  for (int l = 0; l < L; ++l) {
+    Layer &ly = layers_[l];
+    const std::string i = std::to_string(l);
+    ly.attn_norm = upload_vector_f32(g, "attn_norm." + i + ".weight", d);
+    ly.ffn_norm = upload_vector_f32(g, "ffn_norm." + i + ".weight", d);
+    if (g.tensor("qkv." + i + ".weight")) {
+      ProjPart p;
+      p.w = upload_matrix(g, {"qkv." + i + ".weight"}, d);
+      if (p.w.rows != qw + 2 * kvw) fail(LG_ERR_FORMAT, "qkv.%d.weight: unexpected matrix shape", l);
+      if (g.tensor("qkv." + i + ".bias")) p.bias = upload_vector_f32(g, "qkv." + i + ".bias", qw + 2 * kvw);
+      ly.qkv.push_back(p);
+    } else {
+      // separate q/k/v: fuse runs of equal kind into one device matrix (one GEMM / GEMV each)
+      const std::string nm[3] = {"q." + i + ".weight", "k." + i + ".weight", "v." + i + ".weight"};
+      const std::string bn[3] = {"q." + i + ".bias", "k." + i + ".bias", "v." + i + ".bias"};
+      const int rows[3] = {qw, kvw, kvw};
+      uint32_t kinds[3];
+      int nbias = 0;
+      for (int j = 0; j < 3; ++j) {
+        const TensorInfo *t = g.tensor(nm[j]);
+        if (!t) fail(LG_ERR_FORMAT, "missing tensor %s", nm[j].c_str());
+        kinds[j] = t->kind;
+        nbias += g.tensor(bn[j]) ? 1 : 0;
+      }
+      if (nbias != 0 && nbias != 3) fail(LG_ERR_FORMAT, "layer %d: q/k/v biases must all be present or all absent", l);
+      int j = 0, col = 0;
+      while (j < 3) {
+        int e = j + 1;
+        while (e < 3 && kinds[e] == kinds[j]) ++e;
+        ProjPart p;
+        p.w = upload_matrix(g, std::vector<std::string>(nm + j, nm + e), d);
+        int nrows = 0;
+        for (int t = j; t < e; ++t) nrows += rows[t];
+        if (p.w.rows != nrows) fail(LG_ERR_FORMAT, "%s: unexpected matrix shape", nm[j].c_str());
+        p.col0 = col;
+        if (nbias) {
+          p.bias = static_cast<float *>(carve(size_t(nrows) * 4));
+          int off = 0;
+          for (int t = j; t < e; ++t) {
+            float *tmp = upload_vector_f32(g, bn[t], rows[t]);
+            HIP_CHECK(hipMemcpy(const_cast<float *>(p.bias) + off, tmp, size_t(rows[t]) * 4, hipMemcpyDeviceToDevice));
+            off += rows[t];
+          }
+        }
+        ly.qkv.push_back(p);
+        col += nrows;
+        j = e;
+      }
+    }
+    ly.wo = upload_matrix(g, {"wo." + i + ".weight"}, qw);
+    if (ly.wo.rows != d) fail(LG_ERR_FORMAT, "wo.%d.weight: unexpected matrix shape", l);
+    if (g.tensor("mlp_wi." + i + ".weight")) ly.wi = upload_matrix(g, {"mlp_wi." + i + ".weight"}, d);
+    else ly.wi = upload_matrix(g, {"gate." + i + ".weight", "up." + i + ".weight"}, d);
+    if (ly.wi.rows != 2 * f) fail(LG_ERR_FORMAT, "mlp_wi.%d.weight: unexpected matrix shape", l);
+    ly.wd = upload_matrix(g, {"mlp_wo." + i + ".weight"}, f);
+    if (ly.wd.rows != d) fail(LG_ERR_FORMAT, "mlp_wo.%d.weight: unexpected matrix shape", l);
+  }
+  final_norm_ = upload_vector_f32(g, "final_norm.weight", d);
+  head_ = upload_matrix(g, {"output.weight"}, d);
+  if (head_.rows != V) fail(LG_ERR_FORMAT, "output.weight: unexpected matrix shape");
+  cos_ = upload_vector_f32(g, "cos_full", int64_t(ctx) * hd);
+  sin_ = upload_vector_f32(g, "sin_full", int64_t(ctx) * hd);
+}
+
+lg_model_info Engine::info() const {
+  lg_model_info i{};
+  i.layers = L;
+  i.d_model = d;
+  i.heads = hq;
+  i.kv_heads = hkv;
+  i.head_dim = hd;
+  i.ffn = f;
+  i.vocab = V;
+  i.context = ctx;
+  i.kind_attn = layers_.empty() ? 0 : layers_[0].wo.kind;
+  i.kind_ffn = layers_.empty() ? 0 : layers_[0].wd.kind;
+  i.kind_head = head_.kind;
+  i.weight_bytes = weight_bytes_;
+  i.kv_bytes = int64_t(2) * L * npages_ * page_stride_ * 2;
+  i.kv_pages = npages_;
+  i.kv_page_tokens = 64;
+  return i;
+}
+
+void Engine::sync() { HIP_CHECK(hipStreamSynchronize(stream)); }
+
+KvGeom Engine::geom() const {
+  KvGeom g;
+  g.page_tokens = 64;
+  g.hkv = hkv;
+  g.hd = hd;
+  g.page_stride = page_stride_;
+  g.layer_stride = int64_t(npages_) * page_stride_;
+  return g;
+}
+_Float16 *Engine::kpool(int layer) const {
+  return static_cast<_Float16 *>(kv_) + int64_t(layer) * npages_ * page_stride_;
+}
+_Float16 *Engine::vpool(int layer) const {
+  return static_cast<_Float16 *>(kv_) + (int64_t(L) + layer) * npages_ * page_stride_;
+}
+
+// ------------------------------------------------------------------ kernels with profiling
+void Engine::gemm(const _Float16 *A, int M, const DevMatrix &W, Epi epi, float *C, _Float16 *C16,
+                  int ldc, const float *bias) {
+  prof.begin("gemm", stream);
+  launch_gemm(A, M, W, epi, C, C16, ldc, bias, stream);
+  prof.end(double(W.bytes()) + double(M) * W.cols * 2, 2.0 * M * double(W.rows) * W.cols, stream);
+}
+
+void Engine::gemv(const float *x, const DevMatrix &W, Epi epi, float *y, const float *bias,
+                  const float *norm_w) {
+  prof.begin("gemv", stream);
+  launch_gemv(x, W, epi, y, bias, norm_w, eps, stream);
+  // algorithmic bytes: the GGUF-encoded weight bytes of the matrix
+  prof.end(double(W.gguf_bytes()), 2.0 * double(W.rows) * W.cols, stream);
+}
+
+// ------------------------------------------------------------------ matmul drop-in
+void Engine::matmul(const std::string &name, const float *x, int m, const float *bias, float *y) {
+  auto it = named_.find(name);
+  if (it == named_.end()) fail(LG_ERR_INVALID, "missing tensor %s", name.c_str());
+  const DevMatrix &W = it->second;
+  LG_REQUIRE(m > 0, "matmul: m must be positive");
+  const size_t xb = size_t(m) * W.cols * 4, yb = size_t(m) * W.rows * 4;
+  DevBuf dx, dy, db, dh;
+  dx.ensure(xb);
+  dy.ensure(yb);
+  HIP_CHECK(hipMemcpyAsync(dx.p, x, xb, hipMemcpyHostToDevice, stream));
+  const float *dbias = nullptr;
+  if (bias) {
+    db.ensure(size_t(W.rows) * 4);
+    HIP_CHECK(hipMemcpyAsync(db.p, bias, size_t(W.rows) * 4, hipMemcpyHostToDevice, stream));
+    dbias = db.as<float>();
+  }
+  const bool tiled = W.kind != LG_F32 && W.cols % 64 == 0 && W.rows % 128 == 0;
+  if (m == 1 && W.cols % 16 == 0 && W.cols * 4 <= 64 * 1024 && W.kind != LG_F32) {
+    gemv(dx.as<float>(), W, Epi::F32, dy.as<float>(), dbias, nullptr);
+  } else if (tiled && m > 1) {
+    dh.ensure(size_t(m) * W.cols * 2);
+    launch_cvt_f16(dx.as<float>(), int64_t(m) * W.cols, dh.as<_Float16>(), stream);
+    gemm(dh.as<_Float16>(), m, W, Epi::F32, dy.as<float>(), nullptr, W.rows, dbias);
+  } else {
+    launch_gemm_generic(dx.as<float>(), m, W, dbias, dy.as<float>(), stream);
+  }
+  HIP_CHECK(hipMemcpyAsync(y, dy.p, yb, hipMemcpyDeviceToHost, stream));
+  HIP_CHECK(hipStreamSynchronize(stream));
+}
+
+// ------------------------------------------------------------------ sequences / pages
+Seq &Engine::seq(int id) {
+  auto it = seqs_.find(id);
+  if (it == seqs_.end()) fail(LG_ERR_INVALID, "unknown sequence %d", id);
+  return it->second;
+}
+
+int Engine::seq_create() {
+  const int id = next_seq_++;
+  seqs_[id] = Seq{};
+  return id;
+}
+
+int Engine::alloc_page() {
+  if (free_pages_.empty()) fail(LG_ERR_OOM, "KV cache exhausted (%d pages)", npages_);
+  const int p = free_pages_.back();
+  free_pages_.pop_back();
+  refcnt_[p] = 1;
+  return p;
+}
+
+void Engine::release_page(int p) {
+  if (--refcnt_[p] == 0) free_pages_.push_back(p);
+}
+
+void Engine::reserve_pages(Seq &s, int upto) {
+  if (upto > ctx) fail(LG_ERR_INVALID, "sequence of %d tokens exceeds the context length %d", upto, ctx);
+  const int need = (upto + 63) / 64;
+  const int extra = need - int(s.pages.size());
+  if (extra > int(free_pages_.size()))
+    fail(LG_ERR_OOM, "KV cache exhausted: need %d more pages, %zu free", extra, free_pages_.size());
+  while (int(s.pages.size()) < need) s.pages.push_back(alloc_page());
+}
+
+int Engine::seq_fork(int parent, int ntokens) {
+  Seq &p = seq(parent);
+  LG_REQUIRE(ntokens >= 0 && ntokens <= p.len, "fork: %d tokens outside the parent's %d", ntokens, p.len);
+  Seq c;
+  c.len = ntokens;
+  const int full = ntokens / 64, rem = ntokens % 64;
+  for (int i = 0; i < full; ++i) {
+    c.pages.push_back(p.pages[i]);
+    ++refcnt_[p.pages[i]];
+  }
+  if (rem) {  // private copy of the partly filled page, all layers, K and V
+    const int np = alloc_page();
+    for (int l = 0; l < L; ++l) {
+      const size_t bytes = size_t(page_stride_) * 2;
+      HIP_CHECK(hipMemcpyAsync(kpool(l) + int64_t(np) * page_stride_, kpool(l) + int64_t(p.pages[full]) * page_stride_,
+                               bytes, hipMemcpyDeviceToDevice, stream));
+      HIP_CHECK(hipMemcpyAsync(vpool(l) + int64_t(np) * page_stride_, vpool(l) + int64_t(p.pages[full]) * page_stride_,
+                               bytes, hipMemcpyDeviceToDevice, stream));
+    }
+    c.pages.push_back(np);
+  }
+  const int id = next_seq_++;
+  seqs_[id] = std::move(c);
+  return id;
+}
+
+void Engine::seq_free(int id) {
+  Seq &s = seq(id);
+  for (int p : s.pages) release_page(p);
+  seqs_.erase(id);
+}
+
+int Engine::seq_len(int id) const {
+  auto it = seqs_.find(id);
+  if (it == seqs_.end()) fail(LG_ERR_INVALID, "unknown sequence %d", id);
+  return it->second.len;
+}
+
+// ------------------------------------------------------------------ batched prefill
+BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
+  LG_REQUIRE(nreq > 0 && reqs, "batch: no requests");
+  auto *b = new BatchPlan();
+  try {
+    std::vector<int32_t> ids, tseq, tpos, tiles_s, tiles_r, tiles_p, tiles_n, gather;
+    int max_pages = 0;
+    for (int r = 0; r < nreq; ++r) {
+      const lg_request &q = reqs[r];
+      Seq &s = seq(q.seq);
+      for (int j = 0; j < r; ++j)
+        if (reqs[j].seq == q.seq) fail(LG_ERR_INVALID, "sequence %d appears twice in one batch", q.seq);
+      LG_REQUIRE(q.n > 0 && q.ids, "request %d: empty token sequence", r);
+      LG_REQUIRE(q.npos >= 0 && (q.npos == 0 || q.positions), "request %d: bad positions", r);
+      for (int i = 0; i < q.n; ++i)
+        if (q.ids[i] < 0 || q.ids[i] >= V) fail(LG_ERR_INVALID, "request %d: token id %d outside the vocabulary", r, q.ids[i]);
+      for (int i = 0; i < q.npos; ++i)
+        if (q.positions[i] < 0 || q.positions[i] >= q.n) fail(LG_ERR_INVALID, "request %d: answer position %d outside the request", r, q.positions[i]);
+      if (s.len + q.n > ctx) fail(LG_ERR_INVALID, "request %d: %d tokens exceed the context length %d", r, s.len + q.n, ctx);
+      max_pages = std::max(max_pages, (s.len + q.n + 63) / 64);
+    }
+    const int64_t T = std::accumulate(reqs, reqs + nreq, int64_t(0), [](int64_t a, const lg_request &q) { return a + q.n; });
+    if (T > max_batch_tokens_) fail(LG_ERR_INVALID, "batch of %lld tokens exceeds max_batch_tokens %lld", (long long)T, (long long)max_batch_tokens_);
+    // reserve pages (all or nothing)
+    int need = 0;
+    for (int r = 0; r < nreq; ++r) {
+      const Seq &s = seq(reqs[r].seq);
+      need += std::max(0, (s.len + reqs[r].n + 63) / 64 - int(s.pages.size()));
+    }
+    if (need > int(free_pages_.size())) fail(LG_ERR_OOM, "KV cache exhausted: batch needs %d pages, %zu free", need, free_pages_.size());
+    std::vector<int32_t> ptab(size_t(nreq) * max_pages, 0);
+    int row = 0;
+    for (int r = 0; r < nreq; ++r) {
+      const lg_request &q = reqs[r];
+      Seq &s = seq(q.seq);
+      reserve_pages(s, s.len + q.n);
+      for (size_t p = 0; p < s.pages.size(); ++p) ptab[size_t(r) * max_pages + p] = s.pages[p];
+      for (int i = 0; i < q.n; ++i) {
+        ids.push_back(q.ids[i]);
+        tseq.push_back(r);
+        tpos.push_back(s.len + i);
+      }
+      for (int i = 0; i < q.n; i += 32) {
+        tiles_s.push_back(r);
+        tiles_r.push_back(row + i);
+        tiles_p.push_back(s.len + i);
+        tiles_n.push_back(std::min(32, q.n - i));
+      }
+      for (int i = 0; i < q.npos; ++i) gather.push_back(row + q.positions[i]);
+      b->seqs.push_back(q.seq);
+      b->n.push_back(q.n);
+      b->npos.push_back(q.npos);
+      row += q.n;
+    }
+    b->T = int(T);
+    b->R = int(gather.size());
+    b->ntiles = int(tiles_s.size());
+    b->max_pages = max_pages;
+    const size_t nints = ids.size() * 3 + ptab.size() + tiles_s.size() * 4 + gather.size() + 64;
+    b->meta.ensure(nints * 4 + 16 * 256);
+    int32_t *base = b->meta.as<int32_t>();
+    size_t off = 0;
+    auto put = [&](const std::vector<int32_t> &v, int32_t *&dst) {
+      dst = base + off;
+      if (!v.empty()) HIP_CHECK(hipMemcpyAsync(dst, v.data(), v.size() * 4, hipMemcpyHostToDevice, stream));
+      off += (v.size() + 63) & ~size_t(63);
+    };
+    put(ids, b->ids);
+    put(tseq, b->tok_seq);
+    put(tpos, b->tok_pos);
+    put(ptab, b->pages);
+    put(tiles_s, b->tile_seq);
+    put(tiles_r, b->tile_row0);
+    put(tiles_p, b->tile_pos0);
+    put(tiles_n, b->tile_n);
+    put(gather, b->gather);
+    HIP_CHECK(hipStreamSynchronize(stream));
+  } catch (...) {
+    delete b;
+    throw;
+  }
+  return b;
+}
+
+void Engine::batch_free(BatchPlan *b) { delete b; }
+
+void Engine::run_layers_prefill(BatchPlan &b, lg_cancel_fn cancel, void *arg) {
+  const int T = b.T, qw = hq * hd, kvw = hkv * hd, qkvw = qw + 2 * kvw;
+  ws_x_.ensure(size_t(T) * d * 4);
+  ws_h16_.ensure(size_t(T) * d * 2);
+  ws_qkv_.ensure(size_t(T) * qkvw * 4);
+  ws_q16_.ensure(size_t(T) * qw * 2);
+  ws_att16_.ensure(size_t(T) * qw * 2);
+  ws_act16_.ensure(size_t(T) * f * 2);
+  float *x = ws_x_.as<float>();
+  _Float16 *h16 = ws_h16_.as<_Float16>();
+  float *qkv = ws_qkv_.as<float>();
+  const KvGeom g = geom();
+  prof.begin("embed", stream);
+  launch_embed(emb_, emb_kind, b.ids, T, d, V, x, stream);
+  prof.end(double(T) * d * (emb_kind == LG_F16 ? 6 : 8), 0, stream);
+  for (int l = 0; l < L; ++l) {
+    if (cancel && cancel(arg)) fail(LG_ERR_CANCELED, "request canceled");
+    const Layer &ly = layers_[l];
+    prof.begin("rmsnorm", stream);
+    launch_rmsnorm_f16(x, T, d, ly.attn_norm, eps, h16, stream);
+    prof.end(double(T) * d * 6, 0, stream);
+    for (const ProjPart &p : ly.qkv) gemm(h16, T, p.w, Epi::F32, qkv + p.col0, nullptr, qkvw, p.bias);
+    prof.begin("rope_kv", stream);
+    launch_rope_kv(qkv, T, hq, g, cos_, sin_, b.tok_seq, b.tok_pos, b.pages, b.max_pages,
+                   ws_q16_.as<_Float16>(), nullptr, kpool(l), vpool(l), stream);
+    prof.end(double(T) * (qkvw * 4 + (qw + 2 * kvw) * 2), 0, stream);
+    prof.begin("attn_prefill", stream);
+    launch_attn_prefill(ws_q16_.as<_Float16>(), T, hq, g, kpool(l), vpool(l), b.pages, b.max_pages,
+                        b.tile_seq, b.tile_row0, b.tile_pos0, b.tile_n, b.ntiles,
+                        ws_att16_.as<_Float16>(), stream);
+    prof.end(0, 0, stream);
+    gemm(ws_att16_.as<_Float16>(), T, ly.wo, Epi::ADD, x, nullptr, d, nullptr);
+    prof.begin("rmsnorm", stream);
+    launch_rmsnorm_f16(x, T, d, ly.ffn_norm, eps, h16, stream);
+    prof.end(double(T) * d * 6, 0, stream);
+    gemm(h16, T, ly.wi, Epi::SWIGLU, nullptr, ws_act16_.as<_Float16>(), f, nullptr);
+    gemm(ws_act16_.as<_Float16>(), T, ly.wd, Epi::ADD, x, nullptr, d, nullptr);
+  }
+}
+
+void Engine::batch_run(BatchPlan *b, const int32_t *option_ids, int k, float temperature,
+                       float *logits, float *probs, float *logprobs, lg_cancel_fn cancel, void *arg) {
+  LG_REQUIRE(b, "batch: null");
+  LG_REQUIRE(!b->ran, "batch: already run (stage a new batch)");
+  LG_REQUIRE(k > 0 && k <= 32 && option_ids, "batch: need 1..32 option ids");
+  LG_REQUIRE(temperature > 0 && std::isfinite(temperature), "batch: temperature must be positive");
+  for (int j = 0; j < k; ++j)
+    if (option_ids[j] < 0 || option_ids[j] >= V) fail(LG_ERR_INVALID, "option id %d outside the vocabulary", option_ids[j]);
+  // sequences must still exist and not have moved since staging
+  for (size_t r = 0; r < b->seqs.size(); ++r) seq(b->seqs[r]);
+  run_layers_prefill(*b, cancel, arg);
+  for (size_t r = 0; r < b->seqs.size(); ++r) seq(b->seqs[r]).len += b->n[r];
+  b->ran = true;
+  const int R = b->R;
+  if (R == 0) {
+    sync();
+    return;
+  }
+  ws_out_.ensure(size_t(R) * k * 12 + 256 + 64 * 4);
+  float *dl = ws_out_.as<float>(), *dp = dl + size_t(R) * k, *dlp = dp + size_t(R) * k;
+  int32_t *dids = reinterpret_cast<int32_t *>(dlp + size_t(R) * k);
+  HIP_CHECK(hipMemcpyAsync(dids, option_ids, size_t(k) * 4, hipMemcpyHostToDevice, stream));
+  prof.begin("head", stream);
+  launch_head_rows(ws_x_.as<float>(), b->gather, R, d, final_norm_, eps, head_, dids, k, dl, stream);
+  launch_option_scores(dl, R, k, temperature, dp, dlp, stream);
+  prof.end(0, 0, stream);
+  if (logits) HIP_CHECK(hipMemcpyAsync(logits, dl, size_t(R) * k * 4, hipMemcpyDeviceToHost, stream));
+  if (probs) HIP_CHECK(hipMemcpyAsync(probs, dp, size_t(R) * k * 4, hipMemcpyDeviceToHost, stream));
+  if (logprobs) HIP_CHECK(hipMemcpyAsync(logprobs, dlp, size_t(R) * k * 4, hipMemcpyDeviceToHost, stream));
+  sync();
+}
+
+void Engine::forward(int sq, const int32_t *ids, int n, const int32_t *positions, int npos,
+                     const int32_t *vocab_ids, int nv, float *logits, lg_cancel_fn cancel, void *arg) {
+  lg_request r{sq, ids, n, positions, npos};
+  BatchPlan *b = batch_create(&r, 1);
+  struct Guard { Engine *e; BatchPlan *b; ~Guard() { e->batch_free(b); } } guard{this, b};
+  if (vocab_ids) {
+    batch_run(b, vocab_ids, nv, 1.0f, logits, nullptr, nullptr, cancel, arg);
+    return;
+  }
+  // full vocabulary: prefill, then one fused-norm GEMV over the head per answer row
+  for (size_t i = 0; i < b->seqs.size(); ++i) seq(b->seqs[i]);
+  run_layers_prefill(*b, cancel, arg);
+  seq(sq).len += n;
+  b->ran = true;
+  if (npos == 0) {
+    sync();
+    return;
+  }
+  ws_out_.ensure(size_t(V) * 4);
+  std::vector<int32_t> rows(npos);
+  for (int i = 0; i < npos; ++i) rows[i] = positions[i];
+  for (int i = 0; i < npos; ++i) {
+    gemv(ws_x_.as<float>() + size_t(rows[i]) * d, head_, Epi::F32, ws_out_.as<float>(), nullptr, final_norm_);
+    HIP_CHECK(hipMemcpyAsync(logits + size_t(i) * V, ws_out_.p, size_t(V) * 4, hipMemcpyDeviceToHost, stream));
+    sync();
+  }
+}
+
+// ------------------------------------------------------------------ greedy decode
+void Engine::decode(int sq, int32_t first, int steps, int32_t *tokens, float *logits) {
+  Seq &s = seq(sq);
+  LG_REQUIRE(steps > 0 && tokens, "decode: need steps > 0 and an output");
+  LG_REQUIRE(first >= 0 && first < V, "decode: token id %d outside the vocabulary", first);
+  LG_REQUIRE(hd == 128, "decode: head_dim %d has no decode attention kernel", hd);
+  const int pos0 = s.len;
+  reserve_pages(s, pos0 + steps);
+  const int qw = hq * hd, kvw = hkv * hd, qkvw = qw + 2 * kvw;
+  const int max_pages = int(s.pages.size());
+  // per-step metadata, uploaded once: token slots, positions, context lengths, page table
+  std::vector<int32_t> meta;
+  meta.push_back(first);
+  meta.resize(steps + 1, 0);                 // [0, steps]: token ids (step i reads slot i)
+  for (int i = 0; i < steps; ++i) meta.push_back(pos0 + i);       // positions
+  for (int i = 0; i < steps; ++i) meta.push_back(pos0 + i + 1);   // context lengths
+  meta.push_back(0);                                                // tok_seq (batch index 0)
+  for (int p : s.pages) meta.push_back(p);
+  const size_t part_floats = size_t(attn_decode_scratch_floats(1, hq, hd, pos0 + steps));
+  const size_t floats = size_t(d) + qkvw + qw + qw + f + V + 64 + part_floats;
+  ws_dec_.ensure(floats * 4 + meta.size() * 4 + 64 * 8 + 4096);
+  float *x = ws_dec_.as<float>();
+  float *qkv = x + d, *q32 = qkv + qkvw, *att = q32 + qw, *act = att + qw, *lg = act + f;
+  float *part_v = lg + V;
+  float *part = part_v + 64;
+  int32_t *dm = reinterpret_cast<int32_t *>(part + part_floats);
+  int32_t *tok = dm, *pos = dm + steps + 1, *clen = pos + steps, *tseq = clen + steps, *pt = tseq + 1;
+  int32_t *part_i = pt + max_pages;
+  HIP_CHECK(hipMemcpyAsync(dm, meta.data(), meta.size() * 4, hipMemcpyHostToDevice, stream));
+  const KvGeom g = geom();
+  for (int i = 0; i < steps; ++i) {
+    prof.begin("embed", stream);
+    launch_embed(emb_, emb_kind, tok + i, 1, d, V, x, stream);
+    prof.end(double(d) * 6, 0, stream);
+    for (int l = 0; l < L; ++l) {
+      const Layer &ly = layers_[l];
+      for (const ProjPart &p : ly.qkv) gemv(x, p.w, Epi::F32, qkv + p.col0, p.bias, ly.attn_norm);
+      prof.begin("rope_kv", stream);
+      launch_rope_kv(qkv, 1, hq, g, cos_, sin_, tseq, pos + i, pt, max_pages, nullptr, q32, kpool(l),
+                     vpool(l), stream);
+      prof.end(double(qkvw) * 4 + double(2 * kvw) * 2, 0, stream);
+      prof.begin("attn_decode", stream);
+      launch_attn_decode(q32, 1, hq, g, kpool(l), vpool(l), pt, max_pages, clen + i, pos0 + i + 1,
+                         part, att, stream);
+      prof.end(double(pos0 + i + 1) * 2 * kvw * 2, 4.0 * double(pos0 + i + 1) * qw, stream);
+      gemv(att, ly.wo, Epi::ADD, x, nullptr, nullptr);
+      gemv(x, ly.wi, Epi::SWIGLU, act, nullptr, ly.ffn_norm);
+      gemv(act, ly.wd, Epi::ADD, x, nullptr, nullptr);
+    }
+    gemv(x, head_, Epi::F32, lg, nullptr, final_norm_);
+    prof.begin("argmax", stream);
+    launch_argmax(lg, V, tok + i + 1, part_v, part_i, stream);
+    prof.end(double(V) * 4, 0, stream);
+    if (logits) HIP_CHECK(hipMemcpyAsync(logits + size_t(i) * V, lg, size_t(V) * 4, hipMemcpyDeviceToHost, stream));
+  }
+  HIP_CHECK(hipMemcpyAsync(tokens, tok + 1, size_t(steps) * 4, hipMemcpyDeviceToHost, stream));
+  sync();
+  s.len = pos0 + steps;
+}
+
+}  // namespace lg

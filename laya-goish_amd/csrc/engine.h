@@ -1,0 +1,147 @@
+// The engine: one model on one GPU with its own stream, weight arena and KV page pool.
+// Host-side counterpart of the reference's Engine + Backend + Model (src/engine.rs:10-48,
+// src/models/mod.rs:13-23, src/models/openthai/model.rs:41-241), for the laya-decoder shape.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "gguf.h"
+#include "kernels.h"
+#include "lg.h"
+
+namespace lg {
+
+// A slice of a projection's output columns computed by one device matrix.
+struct ProjPart {
+  DevMatrix w;
+  int col0 = 0;                 // first output column in the fused output
+  const float *bias = nullptr;  // device, w.rows entries, or null
+};
+
+struct Layer {
+  float *attn_norm = nullptr, *ffn_norm = nullptr;  // device f32 [d]
+  std::vector<ProjPart> qkv;                        // fused q|k|v output [(hq+2hkv)*hd]
+  DevMatrix wo, wi, wd;                             // wi = gate rows then up rows
+};
+
+struct Seq {
+  std::vector<int> pages;
+  int len = 0;
+};
+
+// Grow-only device buffer.
+struct DevBuf {
+  void *p = nullptr;
+  size_t n = 0;
+  void ensure(size_t bytes);
+  ~DevBuf();
+  template <class T>
+  T *as() const { return static_cast<T *>(p); }
+};
+
+class Profiler {
+ public:
+  void enable(bool on) { on_ = on; }
+  bool on() const { return on_; }
+  void begin(const char *cls, hipStream_t st);
+  void end(double bytes, double flops, hipStream_t st);
+  void read(const std::string &cls, int64_t *launches, double *ms, double *bytes, double *flops);
+  void reset();
+  ~Profiler();
+
+ private:
+  struct Rec { std::string cls; hipEvent_t a, b; double bytes, flops; };
+  struct Sum { int64_t launches = 0; double ms = 0, bytes = 0, flops = 0; };
+  void drain();
+  bool on_ = false;
+  std::vector<Rec> open_;
+  std::vector<hipEvent_t> pool_;
+  std::map<std::string, Sum> sums_;
+  std::string cur_;
+  hipEvent_t cur_a_ = nullptr;
+};
+
+struct BatchPlan;
+
+class Engine {
+ public:
+  Engine(const Gguf &g, const lg_engine_opts &opts);
+  ~Engine();
+
+  lg_model_info info() const;
+  void sync();
+
+  // Matrix::apply drop-in on a named uploaded matrix (host pointers).
+  void matmul(const std::string &name, const float *x, int m, const float *bias, float *y);
+
+  int seq_create();
+  int seq_fork(int parent, int ntokens);
+  void seq_free(int id);
+  int seq_len(int id) const;
+
+  BatchPlan *batch_create(const lg_request *reqs, int nreq);
+  void batch_free(BatchPlan *b);
+  void batch_run(BatchPlan *b, const int32_t *option_ids, int k, float temperature, float *logits,
+                 float *probs, float *logprobs, lg_cancel_fn cancel, void *arg);
+  // Single-sequence forward with host ids; vocab_ids == nullptr -> full vocabulary.
+  void forward(int seq, const int32_t *ids, int n, const int32_t *positions, int npos,
+               const int32_t *vocab_ids, int nv, float *logits, lg_cancel_fn cancel, void *arg);
+  void decode(int seq, int32_t first, int steps, int32_t *tokens, float *logits);
+
+  Profiler prof;
+
+ private:
+  void upload(const Gguf &g);
+  DevMatrix upload_matrix(const Gguf &g, const std::vector<std::string> &names, int cols);
+  float *upload_vector_f32(const Gguf &g, const std::string &name, int64_t n);
+  void *carve(size_t bytes);
+  Seq &seq(int id);
+  void reserve_pages(Seq &s, int upto_tokens);
+  int alloc_page();
+  void release_page(int p);
+  void run_layers_prefill(BatchPlan &b, lg_cancel_fn cancel, void *arg);
+  KvGeom geom() const;
+  _Float16 *kpool(int layer) const;
+  _Float16 *vpool(int layer) const;
+
+  // prof-wrapped launch helpers
+  void gemm(const _Float16 *A, int M, const DevMatrix &W, Epi epi, float *C, _Float16 *C16, int ldc,
+            const float *bias);
+  void gemv(const float *x, const DevMatrix &W, Epi epi, float *y, const float *bias,
+            const float *norm_w);
+
+ public:
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int L = 0, d = 0, hq = 0, hkv = 0, hd = 0, f = 0, V = 0, ctx = 0;
+  float eps = 1e-5f;
+  uint32_t emb_kind = 0;
+
+ private:
+  // weights
+  void *arena_ = nullptr;
+  size_t arena_size_ = 0, arena_used_ = 0;
+  void *emb_ = nullptr;
+  float *cos_ = nullptr, *sin_ = nullptr, *final_norm_ = nullptr;
+  std::vector<Layer> layers_;
+  DevMatrix head_;
+  std::map<std::string, DevMatrix> named_;  // GGUF name -> device matrix view
+  int64_t weight_bytes_ = 0;
+  // KV pool
+  void *kv_ = nullptr;
+  int npages_ = 0;
+  int64_t page_stride_ = 0;  // halves per (layer, page) of K (same for V)
+  std::vector<int> free_pages_, refcnt_;
+  std::map<int, Seq> seqs_;
+  int next_seq_ = 1;
+  int64_t max_batch_tokens_ = 65536;
+  // workspaces
+  DevBuf ws_x_, ws_h16_, ws_qkv_, ws_q16_, ws_att16_, ws_act16_, ws_meta_, ws_out_;
+  DevBuf ws_dec_;
+};
+
+}  // namespace lg

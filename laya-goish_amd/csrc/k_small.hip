@@ -1,0 +1,333 @@
+// Small memory-bound kernels of the forward pass: RMSNorm, embedding gather, RoPE fused
+// with the paged KV-cache write, the option head and option scores, full-vocab argmax.
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+
+#include "common.h"
+#include "kernels.h"
+#include "quant.h"
+
+namespace lg {
+namespace {
+
+constexpr int kT = 256;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+__device__ float block_sum(float v, float *red) {
+  v = wave_sum(v);
+  const int t = threadIdx.x;
+  if ((t & 63) == 0) red[t >> 6] = v;
+  __syncthreads();
+  float s = 0.0f;
+  for (int i = 0; i < int(blockDim.x) / 64; ++i) s += red[i];
+  __syncthreads();
+  return s;
+}
+
+// RMSNorm, src/models/openthai/model.rs:84-94: y = (x * (1/sqrt(dot(x,x)/d + eps))) * w.
+template <typename Out>
+__global__ __launch_bounds__(kT) void rmsnorm_kernel(const float *__restrict__ x, int d,
+                                                     const float *__restrict__ w, float eps,
+                                                     Out *__restrict__ y) {
+  __shared__ float red[kT / 64];
+  const float *row = x + int64_t(blockIdx.x) * d;
+  float ss = 0.0f;
+  for (int k = threadIdx.x; k < d; k += kT) ss += row[k] * row[k];
+  const float inv = 1.0f / sqrtf(block_sum(ss, red) / float(d) + eps);
+  Out *out = y + int64_t(blockIdx.x) * d;
+  for (int k = threadIdx.x; k < d; k += kT) out[k] = Out(row[k] * inv * w[k]);
+}
+
+__global__ void embed_kernel(const void *__restrict__ table, uint32_t kind, const int32_t *__restrict__ ids,
+                             int T, int d, int vocab, float *__restrict__ x) {
+  const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= int64_t(T) * d) return;
+  const int t = int(e / d), k = int(e % d);
+  const int id = min(max(ids[t], 0), vocab - 1);  // ids are validated on the host
+  const int64_t src = int64_t(id) * d + k;
+  x[e] = kind == LG_F16 ? half_bits(static_cast<const uint16_t *>(table)[src])
+                        : static_cast<const float *>(table)[src];
+}
+
+// One workgroup per token row.  Rotate-half RoPE with the model's tables
+// (src/tensor.rs:158-172), then q -> q16/q32, k -> K page row, v -> V page column.
+__global__ __launch_bounds__(kT) void rope_kv_kernel(const float *__restrict__ qkv, int hq, KvGeom g,
+                                                     const float *__restrict__ cosT,
+                                                     const float *__restrict__ sinT,
+                                                     const int32_t *__restrict__ tok_seq,
+                                                     const int32_t *__restrict__ tok_pos,
+                                                     const int32_t *__restrict__ pages, int max_pages,
+                                                     _Float16 *__restrict__ q16, float *__restrict__ q32,
+                                                     _Float16 *__restrict__ kpool,
+                                                     _Float16 *__restrict__ vpool) {
+  const int t = blockIdx.x;
+  const int hd = g.hd, half = hd / 2;
+  const int qw = hq * hd, kvw = g.hkv * hd;
+  const float *row = qkv + int64_t(t) * (qw + 2 * kvw);
+  const int pos = tok_pos[t];
+  const int page = pages[int64_t(tok_seq[t]) * max_pages + pos / g.page_tokens];
+  const int slot = pos % g.page_tokens;
+  const float *cs = cosT + int64_t(pos) * hd, *sn = sinT + int64_t(pos) * hd;
+  // q
+  for (int i = threadIdx.x; i < hq * half; i += kT) {
+    const int h = i / half, j = i % half;
+    const float u = row[h * hd + j], v = row[h * hd + j + half];
+    const float a = u * cs[j] - v * sn[j];
+    const float b = v * cs[j + half] + u * sn[j + half];
+    if (q16) {
+      q16[int64_t(t) * qw + h * hd + j] = _Float16(a);
+      q16[int64_t(t) * qw + h * hd + j + half] = _Float16(b);
+    } else {
+      q32[int64_t(t) * qw + h * hd + j] = a;
+      q32[int64_t(t) * qw + h * hd + j + half] = b;
+    }
+  }
+  _Float16 *kp = kpool + int64_t(page) * g.page_stride;
+  _Float16 *vp = vpool + int64_t(page) * g.page_stride;
+  // k -> page rows [hkv][page_tokens][hd]
+  for (int i = threadIdx.x; i < g.hkv * half; i += kT) {
+    const int h = i / half, j = i % half;
+    const float u = row[qw + h * hd + j], v = row[qw + h * hd + j + half];
+    const float a = u * cs[j] - v * sn[j];
+    const float b = v * cs[j + half] + u * sn[j + half];
+    _Float16 *dst = kp + (int64_t(h) * g.page_tokens + slot) * hd;
+    dst[j] = _Float16(a);
+    dst[j + half] = _Float16(b);
+  }
+  // v -> page columns [hkv][hd][page_tokens]
+  for (int i = threadIdx.x; i < kvw; i += kT) {
+    const int h = i / hd, dd = i % hd;
+    vp[(int64_t(h) * hd + dd) * g.page_tokens + slot] = _Float16(row[qw + kvw + i]);
+  }
+}
+
+__device__ float weight_at_head(const DevMatrix &W, int64_t n, int64_t k) {
+  const int64_t cols = W.cols;
+  switch (W.kind) {
+    case LG_F32: return static_cast<const float *>(W.q)[n * cols + k];
+    case LG_F16: return half_bits(static_cast<const uint16_t *>(W.q)[n * cols + k]);
+    case LG_Q8_0:
+      return half_bits(static_cast<const uint16_t *>(W.s)[n * (cols / 32) + k / 32]) *
+             float(static_cast<const int8_t *>(W.q)[n * cols + k]);
+    case LG_Q4_K: {
+      const uint8_t byte = static_cast<const uint8_t *>(W.q)[n * (cols / 2) + (k / 64) * 32 + (k % 32)];
+      const uint32_t nib = (k % 64) >= 32 ? (byte >> 4) : (byte & 15u);
+      const float2 ab = static_cast<const float2 *>(W.s)[n * (cols / 32) + k / 32];
+      return ab.x * float(nib) - ab.y;
+    }
+    case LG_Q6_K:
+      return static_cast<const float *>(W.s)[n * (cols / 16) + k / 16] *
+             float(static_cast<const int8_t *>(W.q)[n * cols + k]);
+  }
+  return 0.0f;
+}
+
+// One workgroup per gathered row: final RMSNorm into LDS, then one wave per option id.
+__global__ __launch_bounds__(kT) void head_rows_kernel(const float *__restrict__ x,
+                                                       const int32_t *__restrict__ rows, int d,
+                                                       const float *__restrict__ norm_w, float eps,
+                                                       DevMatrix W, const int32_t *__restrict__ ids,
+                                                       int nv, float *__restrict__ logits) {
+  extern __shared__ float h[];
+  __shared__ float red[kT / 64];
+  const float *row = x + int64_t(rows[blockIdx.x]) * d;
+  float ss = 0.0f;
+  for (int k = threadIdx.x; k < d; k += kT) ss += row[k] * row[k];
+  const float inv = 1.0f / sqrtf(block_sum(ss, red) / float(d) + eps);
+  for (int k = threadIdx.x; k < d; k += kT) h[k] = row[k] * inv * norm_w[k];
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  for (int j = threadIdx.x >> 6; j < nv; j += kT / 64) {
+    const int64_t n = ids[j];
+    float s = 0.0f;
+    for (int k = lane; k < d; k += 64) s += h[k] * weight_at_head(W, n, k);
+    s = wave_sum(s);
+    if (lane == 0) logits[int64_t(blockIdx.x) * nv + j] = s;
+  }
+}
+
+// Option scores for one answer position per thread (src/models/openthai/decision.rs:268-279,
+// 297-303): z = l / T; p = softmax(z); p /= max(sum p, 1e-12); final renormalisation; and the
+// option log-softmax z - max - log(sum exp(z - max)).
+__global__ void option_scores_kernel(const float *__restrict__ logits, int R, int k, float temp,
+                                     float *__restrict__ probs, float *__restrict__ logprobs) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= R) return;
+  const float *l = logits + int64_t(r) * k;
+  float z[32], p[32];
+  float m = -INFINITY;
+  for (int i = 0; i < k; ++i) {
+    z[i] = l[i] / temp;
+    m = fmaxf(m, z[i]);
+  }
+  float s = 0.0f;
+  for (int i = 0; i < k; ++i) {
+    p[i] = expf(z[i] - m);
+    s += p[i];
+  }
+  const float lse = logf(s);
+  float sum = 0.0f;
+  for (int i = 0; i < k; ++i) {
+    p[i] = p[i] / s;
+    sum += p[i];
+  }
+  sum = fmaxf(sum, 1e-12f);
+  float s2 = 0.0f;
+  for (int i = 0; i < k; ++i) {
+    p[i] = p[i] / sum;
+    s2 += p[i];
+  }
+  s2 = fmaxf(s2, 1e-12f);
+  for (int i = 0; i < k; ++i) {
+    if (probs) probs[int64_t(r) * k + i] = p[i] / s2;
+    if (logprobs) logprobs[int64_t(r) * k + i] = z[i] - m - lse;
+  }
+}
+
+// Two-stage argmax; ties and NaN follow the strict ">" scan (first maximum wins).
+// Each thread scans increasing indices with a strict ">", so it keeps its first maximum;
+// NaN never compares greater.  Merges prefer the larger value, then the smaller index.
+__device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
+  if (v > bv) {
+    bv = v;
+    bi = i;
+  }
+}
+
+__global__ __launch_bounds__(kT) void argmax_stage1(const float *__restrict__ v, int n,
+                                                    float *__restrict__ pv, int32_t *__restrict__ pi) {
+  __shared__ float sv[kT];
+  __shared__ int si[kT];
+  float bv = -INFINITY;
+  int bi = -1;
+  for (int i = blockIdx.x * kT + threadIdx.x; i < n; i += gridDim.x * kT) better(bv, bi, v[i], i);
+  sv[threadIdx.x] = bv;
+  si[threadIdx.x] = bi;
+  __syncthreads();
+  for (int s = kT / 2; s > 0; s >>= 1) {
+    if (int(threadIdx.x) < s) {
+      float ov = sv[threadIdx.x + s];
+      int oi = si[threadIdx.x + s];
+      float cv = sv[threadIdx.x];
+      int ci = si[threadIdx.x];
+      if (oi >= 0 && (ci < 0 || ov > cv || (ov == cv && oi < ci))) {
+        sv[threadIdx.x] = ov;
+        si[threadIdx.x] = oi;
+      }
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    pv[blockIdx.x] = sv[0];
+    pi[blockIdx.x] = si[0];
+  }
+}
+
+__global__ __launch_bounds__(64) void argmax_stage2(const float *__restrict__ pv,
+                                                    const int32_t *__restrict__ pi, int nparts,
+                                                    int32_t *__restrict__ out) {
+  if (threadIdx.x != 0) return;
+  float bv = -INFINITY;
+  int bi = -1;
+  for (int i = 0; i < nparts; ++i) {
+    if (pi[i] < 0) continue;
+    if (bi < 0 || pv[i] > bv || (pv[i] == bv && pi[i] < bi)) {
+      bv = pv[i];
+      bi = pi[i];
+    }
+  }
+  out[0] = bi < 0 ? 0 : bi;
+}
+
+__global__ void cvt_f16_kernel(const float *__restrict__ x, int64_t n, _Float16 *__restrict__ y) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = _Float16(x[i]);
+}
+
+__global__ void fill_i32_kernel(int32_t *p, int n, int32_t v) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+}  // namespace
+
+void launch_rmsnorm_f16(const float *x, int rows, int d, const float *w, float eps, _Float16 *y,
+                        hipStream_t st) {
+  LG_REQUIRE(rows > 0 && d > 0, "rmsnorm: empty");
+  hipLaunchKernelGGL(rmsnorm_kernel<_Float16>, dim3(rows), dim3(kT), 0, st, x, d, w, eps, y);
+  HIP_CHECK(hipGetLastError());
+}
+
+void launch_rmsnorm_f32(const float *x, int rows, int d, const float *w, float eps, float *y,
+                        hipStream_t st) {
+  LG_REQUIRE(rows > 0 && d > 0, "rmsnorm: empty");
+  hipLaunchKernelGGL(rmsnorm_kernel<float>, dim3(rows), dim3(kT), 0, st, x, d, w, eps, y);
+  HIP_CHECK(hipGetLastError());
+}
+
+void launch_embed(const void *table, uint32_t kind, const int32_t *ids, int T, int d, int vocab,
+                  float *x, hipStream_t st) {
+  LG_REQUIRE(kind == LG_F16 || kind == LG_F32, "embed: table must be F16/F32");
+  const int64_t n = int64_t(T) * d;
+  LG_REQUIRE(n > 0 && n / kT < (1ll << 31), "embed: bad size");
+  hipLaunchKernelGGL(embed_kernel, dim3(unsigned((n + kT - 1) / kT)), dim3(kT), 0, st, table, kind, ids,
+                     T, d, vocab, x);
+  HIP_CHECK(hipGetLastError());
+}
+
+void launch_rope_kv(const float *qkv, int T, int hq, const KvGeom &g, const float *cosT,
+                    const float *sinT, const int32_t *tok_seq, const int32_t *tok_pos,
+                    const int32_t *pages, int max_pages, _Float16 *q16, float *q32,
+                    _Float16 *kpool, _Float16 *vpool, hipStream_t st) {
+  LG_REQUIRE(T > 0 && g.hd % 2 == 0 && (q16 || q32), "rope_kv: bad arguments");
+  hipLaunchKernelGGL(rope_kv_kernel, dim3(T), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, tok_seq, tok_pos,
+                     pages, max_pages, q16, q32, kpool, vpool);
+  HIP_CHECK(hipGetLastError());
+}
+
+void launch_head_rows(const float *x, const int32_t *rows, int R, int d, const float *norm_w,
+                      float eps, const DevMatrix &W, const int32_t *vocab_ids, int nv,
+                      float *logits, hipStream_t st) {
+  LG_REQUIRE(R > 0 && nv > 0 && W.cols == d, "head: bad shape");
+  LG_REQUIRE(size_t(d) * 4 <= 64 * 1024, "head: d too large for LDS");
+  hipLaunchKernelGGL(head_rows_kernel, dim3(R), dim3(kT), size_t(d) * 4, st, x, rows, d, norm_w, eps, W,
+                     vocab_ids, nv, logits);
+  HIP_CHECK(hipGetLastError());
+}
+
+void launch_option_scores(const float *logits, int R, int k, float temperature, float *probs,
+                          float *logprobs, hipStream_t st) {
+  LG_REQUIRE(R > 0 && k > 0 && k <= 32, "option scores: need 1..32 options");
+  hipLaunchKernelGGL(option_scores_kernel, dim3((R + 63) / 64), dim3(64), 0, st, logits, R, k,
+                     temperature, probs, logprobs);
+  HIP_CHECK(hipGetLastError());
+}
+
+void launch_argmax(const float *logits, int V, int32_t *out, float *part_v, int32_t *part_i,
+                   hipStream_t st) {
+  LG_REQUIRE(V > 0, "argmax: empty");
+  const int parts = 64;
+  hipLaunchKernelGGL(argmax_stage1, dim3(parts), dim3(kT), 0, st, logits, V, part_v, part_i);
+  hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(64), 0, st, part_v, part_i, parts, out);
+  HIP_CHECK(hipGetLastError());
+}
+
+void launch_cvt_f16(const float *x, int64_t n, _Float16 *y, hipStream_t st) {
+  LG_REQUIRE(n > 0 && n / 256 < (1ll << 31), "cvt_f16: bad size");
+  hipLaunchKernelGGL(cvt_f16_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, x, n, y);
+  HIP_CHECK(hipGetLastError());
+}
+
+void launch_fill_i32(int32_t *p, int n, int32_t v, hipStream_t st) {
+  if (n <= 0) return;
+  hipLaunchKernelGGL(fill_i32_kernel, dim3((n + 255) / 256), dim3(256), 0, st, p, n, v);
+  HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace lg

@@ -1,0 +1,125 @@
+// Host-side launchers of the gfx950 kernels.  Every launcher checks the shapes its kernel
+// and grid assume before launching, and throws lg::Error(LG_ERR_INVALID/UNSUPPORTED)
+// instead of launching anything out of bounds.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace lg {
+
+// Repacked device layout of one weight matrix W[rows][cols] (y = x . W^T).
+//   F32 : q = float[rows][cols]
+//   F16 : q = half[rows][cols]
+//   Q8_0: q = int8[rows][cols] (codes), s = half[rows][cols/32] (block scale d)
+//   Q4_K: q = uint8[rows][cols/2]; each 64-element group is 32 bytes whose byte j holds
+//         element j (low nibble) and j+32 (high nibble), as inside a GGUF Q4_K block;
+//         s = float2[rows][cols/32] = (d*sc, dmin*m) per 32-element sub-block
+//   Q6_K: q = int8[rows][cols] holding (code - 32); s = float[rows][cols/16] = d*sc
+// Dequantised weight (bit-identical to src/gguf.rs:264-332):
+//   Q8_0: half(d) * q     Q4_K: (d*sc)*q - (dmin*m)     Q6_K: (d*sc)*(q-32)
+struct DevMatrix {
+  uint32_t kind = 0;
+  int rows = 0, cols = 0;
+  void *q = nullptr;
+  void *s = nullptr;
+  int64_t bytes() const;  // HBM bytes of q + s
+  int64_t gguf_bytes() const;  // bytes of the same matrix in GGUF blocks
+};
+
+enum class Epi : int {
+  F32 = 0,     // C[m][n]  = acc (+ bias[n])
+  ADD = 1,     // C[m][n] += acc            (residual stream update)
+  F16 = 2,     // C16[m][n] = half(acc (+ bias[n]))
+  SWIGLU = 3,  // C16[m][j] = half(silu(acc_gate) * acc_up), W rows [0,f) gate, [f,2f) up
+};
+
+// Standalone dequant of raw GGUF blocks (device pointers), bit-exact with gguf::decode.
+void launch_dequant(uint32_t kind, const uint8_t *src, uint64_t nblocks, float *dst,
+                    hipStream_t st);
+
+// Repack raw GGUF blocks (device) of a [rows][cols] matrix into the DevMatrix layout.
+void launch_repack(uint32_t kind, const uint8_t *src, int rows, int cols, DevMatrix &w,
+                   hipStream_t st);
+
+// Prefill GEMM: out = A[M][K] (half, row-major, lda = K) . W^T with epilogue `epi`.
+// For Epi::SWIGLU the output has W.rows/2 columns.
+void launch_gemm(const _Float16 *A, int M, const DevMatrix &W, Epi epi, float *C, _Float16 *C16,
+                 int ldc, const float *bias, hipStream_t st);
+
+// Generic f32 GEMM for shapes the tiled kernel does not take (any M, N, K), F32/F16/Q weights.
+void launch_gemm_generic(const float *X, int M, const DevMatrix &W, const float *bias, float *Y,
+                         hipStream_t st);
+
+// Decode GEMV over f32 x[K] (M = 1): y[n] = x . W[n] with epilogue (F32/ADD/SWIGLU-f32).
+// For Epi::SWIGLU, y has W.rows/2 entries (f32).  `x` may be fused with an RMSNorm:
+// when norm_w != nullptr the kernel computes h = x * rsqrt(mean(x^2)+eps) * norm_w first.
+void launch_gemv(const float *x, const DevMatrix &W, Epi epi, float *y, const float *bias,
+                 const float *norm_w, float eps, hipStream_t st);
+
+// Row RMSNorm: y = x * (1/sqrt(dot(x,x)/d + eps)) * w   (src/models/openthai/model.rs:84-94)
+void launch_rmsnorm_f16(const float *x, int rows, int d, const float *w, float eps, _Float16 *y,
+                        hipStream_t st);
+void launch_rmsnorm_f32(const float *x, int rows, int d, const float *w, float eps, float *y,
+                        hipStream_t st);
+
+// Embedding rows (F16 or F32 table [vocab][d]) -> f32 x[T][d].
+void launch_embed(const void *table, uint32_t kind, const int32_t *ids, int T, int d, int vocab,
+                  float *x, hipStream_t st);
+
+// KV page geometry shared by the attention and rope kernels.
+struct KvGeom {
+  int page_tokens = 64;  // tokens per page
+  int hkv = 0, hd = 0;
+  int64_t layer_stride = 0;  // halves between layers of the K (or V) pool
+  int64_t page_stride = 0;   // halves per page of one layer: hkv * page_tokens * hd
+};
+
+// RoPE on q and k of qkv[T][(hq+2hkv)*hd] (f32) with tables cos/sin[ctx][hd]; writes
+// q16[T][hq*hd] and the K page rows [hkv][page_tokens][hd] and V page columns
+// [hkv][hd][page_tokens] of layer pools kpool/vpool.  tok_seq/tok_pos give each row's
+// sequence and position; pages[seq * max_pages + pos / page_tokens] its page.
+void launch_rope_kv(const float *qkv, int T, int hq, const KvGeom &g, const float *cosT,
+                    const float *sinT, const int32_t *tok_seq, const int32_t *tok_pos,
+                    const int32_t *pages, int max_pages, _Float16 *q16, float *q32,
+                    _Float16 *kpool, _Float16 *vpool, hipStream_t st);
+
+// Causal prefill attention over the paged F16 cache.  Work items: tiles of 32 query rows of
+// one sequence (tile_seq, tile_row0 = first batch row, tile_pos0 = its position, tile_n rows).
+void launch_attn_prefill(const _Float16 *q16, int T, int hq, const KvGeom &g,
+                         const _Float16 *kpool, const _Float16 *vpool, const int32_t *pages,
+                         int max_pages, const int32_t *tile_seq, const int32_t *tile_row0,
+                         const int32_t *tile_pos0, const int32_t *tile_n, int ntiles,
+                         _Float16 *out16, hipStream_t st);
+
+// Decode attention: one query row per sequence (batch nseq), context length ctx_len[s]
+// (including the current token), split over chunks of keys, then combined.
+void launch_attn_decode(const float *q32, int nseq, int hq, const KvGeom &g,
+                        const _Float16 *kpool, const _Float16 *vpool, const int32_t *pages,
+                        int max_pages, const int32_t *ctx_len, int max_ctx, float *part,
+                        float *out, hipStream_t st);
+int64_t attn_decode_scratch_floats(int nseq, int hq, int hd, int max_ctx);
+
+// Gather rows, final RMSNorm and the option head: logits[r][j] = h_r . W[ids[j]].
+void launch_head_rows(const float *x, const int32_t *rows, int R, int d, const float *norm_w,
+                      float eps, const DevMatrix &W, const int32_t *vocab_ids, int nv,
+                      float *logits, hipStream_t st);
+
+// Option scoring over logits[R][k]: probabilities and log-softmax at temperature t.
+void launch_option_scores(const float *logits, int R, int k, float temperature, float *probs,
+                          float *logprobs, hipStream_t st);
+
+// Full-vocabulary argmax of logits[V] (first maximum wins) -> out[0]; part: scratch.
+void launch_argmax(const float *logits, int V, int32_t *out, float *part_v, int32_t *part_i,
+                   hipStream_t st);
+
+// f32 -> f16 (round to nearest even), n elements.
+void launch_cvt_f16(const float *x, int64_t n, _Float16 *y, hipStream_t st);
+
+// f32 weights from the repacked layout of W, row-major [rows][cols] (bit-exact dequant).
+void launch_dequant_repacked(const DevMatrix &w, float *dst, hipStream_t st);
+
+// Device int32 fill / copy helpers (small, capture-safe).
+void launch_fill_i32(int32_t *p, int n, int32_t v, hipStream_t st);
+
+}  // namespace lg

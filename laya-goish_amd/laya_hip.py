@@ -1,0 +1,371 @@
+"""ctypes binding of liblaya_hip.so (the C ABI declared in include/lg.h).
+
+Host-side mirror of the reference's model surfaces for the decoder forward path:
+``Gguf`` (src/gguf.rs: open/data/get/num), ``Engine`` (src/engine.rs: new/layers,
+src/models/openthai/model.rs: forward(ids, positions)), ``Engine.matmul``
+(src/tensor.rs: Matrix::apply) and option scoring (src/models/openthai/decision.rs:268-279).
+Errors surface as ``LayaError`` carrying the library's message, as the reference's
+``Result<_, String>`` does.  The library must be built (``make -C laya-goish_amd``); there
+is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liblaya_hip.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "lg.h")
+
+F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
+KIND_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+ERR = {1: "INVALID", 2: "FORMAT", 3: "DEVICE", 4: "OOM", 5: "CANCELED", 6: "UNSUPPORTED"}
+
+
+class LayaError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(msg)
+        self.code = code
+        self.kind = ERR.get(code, str(code))
+
+
+class EngineOpts(ctypes.Structure):
+    _fields_ = [("device", ctypes.c_int), ("kv_pages", ctypes.c_int),
+                ("kv_tokens", ctypes.c_int64), ("max_batch_tokens", ctypes.c_int64)]
+
+
+class ModelInfo(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in
+                ("layers", "d_model", "heads", "kv_heads", "head_dim", "ffn", "vocab", "context")] + \
+               [("kind_attn", ctypes.c_uint32), ("kind_ffn", ctypes.c_uint32), ("kind_head", ctypes.c_uint32),
+                ("weight_bytes", ctypes.c_int64), ("kv_bytes", ctypes.c_int64),
+                ("kv_pages", ctypes.c_int), ("kv_page_tokens", ctypes.c_int)]
+
+    def asdict(self):
+        return {n: getattr(self, n) for n, _ in self._fields_}
+
+
+class Request(ctypes.Structure):
+    _fields_ = [("seq", ctypes.c_int), ("ids", ctypes.POINTER(ctypes.c_int32)), ("n", ctypes.c_int),
+                ("positions", ctypes.POINTER(ctypes.c_int32)), ("npos", ctypes.c_int)]
+
+
+CANCEL_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p)
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load the built library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -C laya-goish_amd`")
+        L = ctypes.CDLL(LIB_PATH)
+        P, I, U32, U64, I64, F = (ctypes.c_void_p, ctypes.c_int, ctypes.c_uint32, ctypes.c_uint64,
+                                  ctypes.c_int64, ctypes.c_float)
+        sig = {
+            "lg_last_error": (ctypes.c_char_p, []),
+            "lg_version": (ctypes.c_char_p, []),
+            "lg_layout": (I, [U32, ctypes.POINTER(U64), ctypes.POINTER(U64)]),
+            "lg_half": (F, [ctypes.c_uint16]),
+            "lg_gguf_open": (I, [ctypes.c_char_p, ctypes.POINTER(P)]),
+            "lg_gguf_open_memory": (I, [P, U64, ctypes.POINTER(P)]),
+            "lg_gguf_close": (None, [P]),
+            "lg_gguf_tensor_count": (I, [P]),
+            "lg_gguf_tensor_name": (ctypes.c_char_p, [P, I]),
+            "lg_gguf_tensor": (I, [P, ctypes.c_char_p, ctypes.POINTER(U32), ctypes.POINTER(U64),
+                                   ctypes.POINTER(I), ctypes.POINTER(P), ctypes.POINTER(U64)]),
+            "lg_gguf_meta_num": (I, [P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(I)]),
+            "lg_gguf_meta_str": (I, [P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(I)]),
+            "lg_dequant": (I, [U32, P, U64, P]),
+            "lg_synth_gguf": (I, [ctypes.c_char_p, U64, I, ctypes.POINTER(P), ctypes.POINTER(U64)]),
+            "lg_synth_gguf_file": (I, [ctypes.c_char_p, U64, I, ctypes.c_char_p]),
+            "lg_synth_free": (None, [P]),
+            "lg_engine_create": (I, [P, ctypes.POINTER(EngineOpts), ctypes.POINTER(P)]),
+            "lg_engine_destroy": (None, [P]),
+            "lg_engine_info": (I, [P, ctypes.POINTER(ModelInfo)]),
+            "lg_engine_sync": (I, [P]),
+            "lg_matmul": (I, [P, ctypes.c_char_p, P, I, P, P]),
+            "lg_seq_create": (I, [P, ctypes.POINTER(I)]),
+            "lg_seq_fork": (I, [P, I, I, ctypes.POINTER(I)]),
+            "lg_seq_free": (I, [P, I]),
+            "lg_seq_len": (I, [P, I, ctypes.POINTER(I)]),
+            "lg_forward": (I, [P, I, P, I, P, I, P, I, P, CANCEL_FN, P]),
+            "lg_batch_create": (I, [P, ctypes.POINTER(Request), I, ctypes.POINTER(P)]),
+            "lg_batch_free": (None, [P, P]),
+            "lg_batch_run": (I, [P, P, P, I, F, P, P, P, CANCEL_FN, P]),
+            "lg_decode": (I, [P, I, ctypes.c_int32, I, P, P]),
+            "lg_option_scores": (I, [P, I, F, P, P]),
+            "lg_profile_enable": (I, [P, I]),
+            "lg_profile_read": (I, [P, ctypes.c_char_p, ctypes.POINTER(I64), ctypes.POINTER(ctypes.c_double),
+                                    ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
+            "lg_profile_reset": (I, [P]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def header_functions() -> list[str]:
+    """Names of every function declared in include/lg.h."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lg_[a-z0-9_]+)\s*\(", text)) - {"lg_cancel_fn"})
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise LayaError(rc, lib().lg_last_error().decode())
+
+
+def _ptr(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dtype) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=dtype))
+
+
+def layout(kind: int) -> tuple[int, int]:
+    b, s = ctypes.c_uint64(), ctypes.c_uint64()
+    check(lib().lg_layout(kind, ctypes.byref(b), ctypes.byref(s)))
+    return b.value, s.value
+
+
+def half(bits: int) -> float:
+    return lib().lg_half(bits)
+
+
+def dequant(kind: int, raw: bytes | np.ndarray) -> np.ndarray:
+    """gguf::decode on the GPU (through the engine's repacked weight layout)."""
+    buf = np.frombuffer(bytes(raw), dtype=np.uint8) if not isinstance(raw, np.ndarray) else _c(raw, np.uint8)
+    block, size = layout(kind)
+    out = np.empty(buf.size // size * block, dtype=np.float32)
+    check(lib().lg_dequant(kind, _ptr(buf), buf.size, _ptr(out)))
+    return out
+
+
+def option_scores(logits, temperature: float = 1.0):
+    z = _c(logits, np.float32)
+    p = np.empty_like(z)
+    lp = np.empty_like(z)
+    check(lib().lg_option_scores(_ptr(z), z.size, temperature, _ptr(p), _ptr(lp)))
+    return p, lp
+
+
+class SynthImage:
+    """A seeded synthetic laya-decoder GGUF image held in library-allocated memory."""
+
+    def __init__(self, preset: str, seed: int = 0, n_layers: int = 0):
+        p, n = ctypes.c_void_p(), ctypes.c_uint64()
+        check(lib().lg_synth_gguf(preset.encode(), seed, n_layers, ctypes.byref(p), ctypes.byref(n)))
+        self.ptr, self.len = p, n.value
+        self.preset, self.seed = preset, seed
+
+    def bytes(self) -> bytes:
+        return ctypes.string_at(self.ptr, self.len)
+
+    def array(self) -> np.ndarray:
+        return np.ctypeslib.as_array(ctypes.cast(self.ptr, ctypes.POINTER(ctypes.c_uint8)), shape=(self.len,))
+
+    def __del__(self):
+        if getattr(self, "ptr", None) and _lib is not None:
+            _lib.lg_synth_free(self.ptr)
+            self.ptr = None
+
+
+def synth_file(preset: str, seed: int, path: str, n_layers: int = 0) -> None:
+    check(lib().lg_synth_gguf_file(preset.encode(), seed, n_layers, path.encode()))
+
+
+class Gguf:
+    """GGUF v3 reader (mirrors src/gguf.rs Gguf::open / data / get / num)."""
+
+    def __init__(self, handle, keep=None):
+        self.h = handle
+        self._keep = keep
+
+    @classmethod
+    def open(cls, path: str) -> "Gguf":
+        h = ctypes.c_void_p()
+        check(lib().lg_gguf_open(path.encode(), ctypes.byref(h)))
+        return cls(h)
+
+    @classmethod
+    def from_bytes(cls, data) -> "Gguf":
+        if isinstance(data, SynthImage):
+            h = ctypes.c_void_p()
+            check(lib().lg_gguf_open_memory(data.ptr, data.len, ctypes.byref(h)))
+            return cls(h, data)
+        buf = np.frombuffer(bytes(data), dtype=np.uint8).copy()
+        h = ctypes.c_void_p()
+        check(lib().lg_gguf_open_memory(_ptr(buf), buf.size, ctypes.byref(h)))
+        return cls(h, buf)
+
+    def names(self) -> list[str]:
+        L = lib()
+        return [L.lg_gguf_tensor_name(self.h, i).decode() for i in range(L.lg_gguf_tensor_count(self.h))]
+
+    def tensor(self, name: str):
+        kind, nd, data, n = ctypes.c_uint32(), ctypes.c_int(), ctypes.c_void_p(), ctypes.c_uint64()
+        dims = (ctypes.c_uint64 * 4)()
+        check(lib().lg_gguf_tensor(self.h, name.encode(), ctypes.byref(kind), dims, ctypes.byref(nd),
+                                   ctypes.byref(data), ctypes.byref(n)))
+        raw = ctypes.string_at(data, n.value)
+        return kind.value, [dims[i] for i in range(nd.value)], raw
+
+    def num(self, key: str, default=None):
+        v, found = ctypes.c_double(), ctypes.c_int()
+        check(lib().lg_gguf_meta_num(self.h, key.encode(), ctypes.byref(v), ctypes.byref(found)))
+        return v.value if found.value else default
+
+    def str(self, key: str, default=None):
+        v, found = ctypes.c_char_p(), ctypes.c_int()
+        check(lib().lg_gguf_meta_str(self.h, key.encode(), ctypes.byref(v), ctypes.byref(found)))
+        return v.value.decode() if found.value else default
+
+    def close(self):
+        if self.h:
+            lib().lg_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.lg_gguf_close(self.h)
+            self.h = None
+
+
+class Batch:
+    def __init__(self, engine: "Engine", handle, requests, total_positions: int):
+        self.engine, self.h, self._keep, self.R = engine, handle, requests, total_positions
+
+    def run(self, option_ids, temperature: float = 1.0, cancel=None):
+        k = len(option_ids)
+        ids = _c(option_ids, np.int32)
+        out = [np.empty((self.R, k), dtype=np.float32) for _ in range(3)]
+        cb = CANCEL_FN(cancel) if cancel else CANCEL_FN(0)
+        check(lib().lg_batch_run(self.engine.h, self.h, _ptr(ids), k, temperature,
+                                 *(_ptr(o) for o in out), cb, None))
+        return tuple(out)
+
+    def free(self):
+        if self.h:
+            lib().lg_batch_free(self.engine.h, self.h)
+            self.h = None
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None and self.engine.h:
+            _lib.lg_batch_free(self.engine.h, self.h)
+            self.h = None
+
+
+class Engine:
+    """One model on one GPU (mirrors src/engine.rs Engine::new / layers / decide)."""
+
+    def __init__(self, gguf: Gguf, device: int = 0, kv_tokens: int = 65536, max_batch_tokens: int = 65536,
+                 kv_pages: int = 0):
+        self.gguf = gguf
+        opts = EngineOpts(device, kv_pages, kv_tokens, max_batch_tokens)
+        h = ctypes.c_void_p()
+        check(lib().lg_engine_create(gguf.h, ctypes.byref(opts), ctypes.byref(h)))
+        self.h = h
+        info = ModelInfo()
+        check(lib().lg_engine_info(self.h, ctypes.byref(info)))
+        self.info = info.asdict()
+
+    def layers(self) -> int:
+        return self.info["layers"]
+
+    def close(self):
+        if self.h:
+            lib().lg_engine_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.lg_engine_destroy(self.h)
+            self.h = None
+
+    def sync(self):
+        check(lib().lg_engine_sync(self.h))
+
+    def matmul(self, tensor: str, x, bias=None) -> np.ndarray:
+        x = _c(x, np.float32)
+        if x.ndim == 1:
+            x = x[None, :]
+        b = None if bias is None else _c(bias, np.float32)
+        kind, dims, _ = self.gguf.tensor(tensor)
+        rows = int(np.prod(dims[1:]))
+        y = np.empty((x.shape[0], rows), dtype=np.float32)
+        check(lib().lg_matmul(self.h, tensor.encode(), _ptr(x), x.shape[0], _ptr(b), _ptr(y)))
+        return y
+
+    def seq_create(self) -> int:
+        s = ctypes.c_int()
+        check(lib().lg_seq_create(self.h, ctypes.byref(s)))
+        return s.value
+
+    def seq_fork(self, parent: int, ntokens: int) -> int:
+        s = ctypes.c_int()
+        check(lib().lg_seq_fork(self.h, parent, ntokens, ctypes.byref(s)))
+        return s.value
+
+    def seq_free(self, seq: int) -> None:
+        check(lib().lg_seq_free(self.h, seq))
+
+    def seq_len(self, seq: int) -> int:
+        n = ctypes.c_int()
+        check(lib().lg_seq_len(self.h, seq, ctypes.byref(n)))
+        return n.value
+
+    def forward(self, seq: int, ids, positions, vocab_ids=None, cancel=None) -> np.ndarray:
+        """Model::forward(ids, positions): logits at `positions` for `vocab_ids` (None = all)."""
+        ids = _c(ids, np.int32)
+        pos = _c(positions, np.int32)
+        vid = None if vocab_ids is None else _c(vocab_ids, np.int32)
+        nv = self.info["vocab"] if vid is None else vid.size
+        out = np.empty((pos.size, nv), dtype=np.float32)
+        cb = CANCEL_FN(cancel) if cancel else CANCEL_FN(0)
+        check(lib().lg_forward(self.h, seq, _ptr(ids), ids.size, _ptr(pos), pos.size, _ptr(vid),
+                               0 if vid is None else vid.size, _ptr(out), cb, None))
+        return out
+
+    def batch(self, requests) -> Batch:
+        """requests: list of (seq, ids, positions)."""
+        keep, arr = [], (Request * len(requests))()
+        total = 0
+        for i, (seq, ids, pos) in enumerate(requests):
+            ids = _c(ids, np.int32)
+            pos = _c(pos, np.int32)
+            keep += [ids, pos]
+            arr[i] = Request(seq, ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), ids.size,
+                             pos.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), pos.size)
+            total += pos.size
+        h = ctypes.c_void_p()
+        check(lib().lg_batch_create(self.h, arr, len(requests), ctypes.byref(h)))
+        return Batch(self, h, (arr, keep), total)
+
+    def decode(self, seq: int, first: int, steps: int, want_logits: bool = False):
+        toks = np.empty(steps, dtype=np.int32)
+        lg = np.empty((steps, self.info["vocab"]), dtype=np.float32) if want_logits else None
+        check(lib().lg_decode(self.h, seq, first, steps, _ptr(toks), _ptr(lg)))
+        return (toks, lg) if want_logits else toks
+
+    def profile(self, on: bool = True) -> None:
+        check(lib().lg_profile_enable(self.h, 1 if on else 0))
+
+    def profile_reset(self) -> None:
+        check(lib().lg_profile_reset(self.h))
+
+    def profile_read(self, cls: str) -> dict:
+        n, ms, b, f = ctypes.c_int64(), ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+        check(lib().lg_profile_read(self.h, cls.encode(), ctypes.byref(n), ctypes.byref(ms), ctypes.byref(b),
+                                    ctypes.byref(f)))
+        return {"launches": n.value, "ms": ms.value, "bytes": b.value, "flops": f.value}

@@ -1,0 +1,90 @@
+/*
+ * CPU oracle for the Laya decoder forward pass -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C restatement of the reference's CPU algorithm for the hot path,
+ * in the reference's f32 operation order.  Only tests, the smoke check and the
+ * bench's CPU-baseline leg may load it, and only as the checker: the product
+ * path never calls into this library.
+ *
+ * Each function cites the reference file:line it restates.  Built with
+ * -ffp-contract=off so that every multiply and add rounds separately unless the
+ * reference itself fuses them (the AVX2 FMA in Matrix::apply).
+ */
+#ifndef LAYA_ORACLE_H
+#define LAYA_ORACLE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { OR_F32 = 0, OR_F16 = 1, OR_Q4_0 = 2, OR_Q8_0 = 8, OR_Q4_K = 12, OR_Q6_K = 14 };
+
+/* src/gguf.rs:81-93 -- (elements per block, bytes per block); -1 if unsupported. */
+int or_layout(uint32_t kind, uint64_t *block, uint64_t *size);
+/* src/gguf.rs:226-246 -- IEEE binary16 -> f32, exact. */
+float or_half(uint16_t x);
+/* src/gguf.rs:250-336 -- dequantise `len` bytes of `kind` into len/size*block floats. */
+int or_decode(uint32_t kind, const uint8_t *b, uint64_t len, float *out);
+
+/* src/gguf.rs:95-179 -- GGUF v3 parse over caller-owned bytes (borrowed for the handle's life). */
+typedef struct or_gguf or_gguf;
+or_gguf *or_gguf_open(const uint8_t *bytes, uint64_t n, char *err, int errlen);
+void or_gguf_close(or_gguf *g);
+int or_gguf_ntensors(const or_gguf *g);
+/* 0 if found; dims[0] is the innermost (column) extent as in the file. */
+int or_gguf_tensor(const or_gguf *g, const char *name, uint32_t *kind, uint64_t dims[4], int *nd,
+                   const uint8_t **data, uint64_t *len);
+double or_gguf_num(const or_gguf *g, const char *key, double dflt);
+const char *or_gguf_str(const or_gguf *g, const char *key);
+
+/* src/tensor.rs:10-102 -- out[m][rows] = x[m][cols] . W[rows][cols]^T (+ bias), 4-row tiles,
+ * 8-lane FMA accumulators, sequential lane sum, separately-rounded tail, then bias. */
+void or_apply(const float *w, int rows, int cols, const float *x, int m, const float *bias,
+              int threads, float *out);
+/* src/tensor.rs:193-195 */
+float or_dot(const float *a, const float *b, int n);
+/* src/tensor.rs:132-140 */
+void or_softmax(const float *x, int n, float *p);
+/* src/models/openthai/model.rs:84-94 with the offset and eps as parameters. */
+void or_rms(const float *x, int rows, int d, const float *w, float offset, float eps, float *y);
+/* src/models/openthai/model.rs:71-76 */
+float or_silu(float x);
+
+/* ---- assembled decoder (Llama/Qwen2 shape) ---- */
+typedef struct or_model or_model;
+or_model *or_model_load(const or_gguf *g, int threads, char *err, int errlen);
+void or_model_free(or_model *m);
+/* layers, d_model, heads, kv_heads, head_dim, ffn, vocab, context */
+void or_model_dims(const or_model *m, int out[8]);
+void or_model_set_threads(or_model *m, int threads);
+
+/* Per-sequence f32 K/V rows (the reference recomputes the whole sequence; rows of K/V
+ * depend only on earlier tokens, so a cache reproduces the full recompute bit for bit). */
+typedef struct or_cache or_cache;
+or_cache *or_cache_new(const or_model *m, int capacity);
+or_cache *or_cache_fork(const or_cache *c, int len);
+void or_cache_free(or_cache *c);
+int or_cache_len(const or_cache *c);
+
+/* Run n tokens starting at the cache's current length; append their K/V; return the
+ * residual-stream rows at `gather` (indices into the n new tokens), [ngather][d].
+ * Layer-loop order follows src/models/openthai/model.rs:214-231. */
+int or_prefill(or_model *m, or_cache *c, const int32_t *ids, int n, const int32_t *gather,
+               int ngather, float *hidden);
+/* Final RMSNorm + head rows `vocab_ids` (NULL = every row), src/models/openthai/model.rs:232-240. */
+int or_head(or_model *m, const float *hidden, int rows, const int32_t *vocab_ids, int nv,
+            float *logits);
+/* First maximum wins (strict >), src/models/openthai/decision.rs:330-335. */
+int or_argmax(const float *v, int n);
+/* Option scores: z = logit / T; softmax over k (+ abstain logit when has_abstain);
+ * probs renormalised over k (max(sum,1e-12)); logprobs = log of probs.
+ * src/models/openthai/decision.rs:268-279,297-303. */
+void or_option_scores(const float *logits, int k, float abstain_logit, int has_abstain,
+                      float temperature, float *probs, float *logprobs, float *abstain);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,240 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so) -- TEST INFRASTRUCTURE ONLY.
+
+Only tests, the smoke check and the bench's CPU-baseline leg load this module, and only as
+the checker.  See oracle.h for the reference file:line each function restates.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -C oracle`")
+        L = ctypes.CDLL(LIB_PATH)
+        P, I, U32, U64, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float
+        sig = {
+            "or_layout": (I, [U32, ctypes.POINTER(U64), ctypes.POINTER(U64)]),
+            "or_half": (F, [ctypes.c_uint16]),
+            "or_decode": (I, [U32, P, U64, P]),
+            "or_gguf_open": (P, [P, U64, ctypes.c_char_p, I]),
+            "or_gguf_close": (None, [P]),
+            "or_gguf_ntensors": (I, [P]),
+            "or_gguf_tensor": (I, [P, ctypes.c_char_p, ctypes.POINTER(U32), ctypes.POINTER(U64),
+                                   ctypes.POINTER(I), ctypes.POINTER(P), ctypes.POINTER(U64)]),
+            "or_gguf_num": (ctypes.c_double, [P, ctypes.c_char_p, ctypes.c_double]),
+            "or_gguf_str": (ctypes.c_char_p, [P, ctypes.c_char_p]),
+            "or_apply": (None, [P, I, I, P, I, P, I, P]),
+            "or_set_scalar_apply": (None, [I]),
+            "or_dot": (F, [P, P, I]),
+            "or_softmax": (None, [P, I, P]),
+            "or_rms": (None, [P, I, I, P, F, F, P]),
+            "or_silu": (F, [F]),
+            "or_model_load": (P, [P, I, ctypes.c_char_p, I]),
+            "or_model_free": (None, [P]),
+            "or_model_dims": (None, [P, P]),
+            "or_model_set_threads": (None, [P, I]),
+            "or_cache_new": (P, [P, I]),
+            "or_cache_fork": (P, [P, I]),
+            "or_cache_free": (None, [P]),
+            "or_cache_len": (I, [P]),
+            "or_prefill": (I, [P, P, P, I, P, I, P]),
+            "or_head": (I, [P, P, I, P, I, P]),
+            "or_argmax": (I, [P, I]),
+            "or_option_scores": (None, [P, I, F, I, F, P, P, P]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(np.asarray(a, dtype=dt))
+
+
+def layout(kind):
+    b, s = ctypes.c_uint64(), ctypes.c_uint64()
+    if lib().or_layout(kind, ctypes.byref(b), ctypes.byref(s)):
+        raise ValueError(f"unsupported kind {kind}")
+    return b.value, s.value
+
+
+def half(bits: int) -> float:
+    return lib().or_half(bits)
+
+
+def decode(kind: int, raw) -> np.ndarray:
+    buf = _c(np.frombuffer(bytes(raw), dtype=np.uint8) if not isinstance(raw, np.ndarray) else raw, np.uint8)
+    block, size = layout(kind)
+    out = np.empty(buf.size // size * block, dtype=np.float32)
+    if lib().or_decode(kind, _p(buf), buf.size, _p(out)):
+        raise ValueError("decode failed")
+    return out
+
+
+def apply(w, x, bias=None, threads=1) -> np.ndarray:
+    w = _c(w, np.float32)
+    x = _c(x, np.float32)
+    if x.ndim == 1:
+        x = x[None, :]
+    rows, cols = w.shape
+    m = x.shape[0]
+    assert x.shape[1] == cols
+    b = None if bias is None else _c(bias, np.float32)
+    out = np.empty((m, rows), dtype=np.float32)
+    lib().or_apply(_p(w), rows, cols, _p(x), m, _p(b), threads, _p(out))
+    return out
+
+
+def set_scalar_apply(on: bool) -> None:
+    lib().or_set_scalar_apply(1 if on else 0)
+
+
+def dot(a, b) -> float:
+    a, b = _c(a, np.float32), _c(b, np.float32)
+    return lib().or_dot(_p(a), _p(b), a.size)
+
+
+def softmax(x) -> np.ndarray:
+    x = _c(x, np.float32)
+    p = np.empty_like(x)
+    lib().or_softmax(_p(x), x.size, _p(p))
+    return p
+
+
+def rms(x, w, offset=0.0, eps=1e-5) -> np.ndarray:
+    x, w = _c(x, np.float32), _c(w, np.float32)
+    rows = x.size // w.size
+    y = np.empty_like(x)
+    lib().or_rms(_p(x), rows, w.size, _p(w), offset, eps, _p(y))
+    return y
+
+
+def silu(v: float) -> float:
+    return lib().or_silu(v)
+
+
+def option_scores(logits, temperature=1.0, abstain=None):
+    z = _c(logits, np.float32)
+    p, lp, ab = np.empty_like(z), np.empty_like(z), ctypes.c_float()
+    lib().or_option_scores(_p(z), z.size, 0.0 if abstain is None else abstain, 0 if abstain is None else 1,
+                           temperature, _p(p), _p(lp), ctypes.byref(ab))
+    return p, lp, ab.value
+
+
+class Gguf:
+    def __init__(self, data):
+        self.buf = _c(np.frombuffer(bytes(data), dtype=np.uint8) if not isinstance(data, np.ndarray) else data,
+                      np.uint8)
+        err = ctypes.create_string_buffer(256)
+        self.h = lib().or_gguf_open(_p(self.buf), self.buf.size, err, 256)
+        if not self.h:
+            raise ValueError(err.value.decode())
+
+    def tensor(self, name):
+        kind, nd, data, n = ctypes.c_uint32(), ctypes.c_int(), ctypes.c_void_p(), ctypes.c_uint64()
+        dims = (ctypes.c_uint64 * 4)()
+        if lib().or_gguf_tensor(self.h, name.encode(), ctypes.byref(kind), dims, ctypes.byref(nd),
+                                ctypes.byref(data), ctypes.byref(n)):
+            raise KeyError(name)
+        return kind.value, [dims[i] for i in range(nd.value)], ctypes.string_at(data, n.value)
+
+    def num(self, key, default=0.0):
+        return lib().or_gguf_num(self.h, key.encode(), default)
+
+    def str(self, key):
+        return lib().or_gguf_str(self.h, key.encode()).decode()
+
+    def ntensors(self):
+        return lib().or_gguf_ntensors(self.h)
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.or_gguf_close(self.h)
+            self.h = None
+
+
+class Model:
+    """The assembled decoder on the CPU: prefill with an f32 K/V cache, head, argmax."""
+
+    def __init__(self, gguf: Gguf, threads: int = 4):
+        self.g = gguf
+        err = ctypes.create_string_buffer(256)
+        self.h = lib().or_model_load(gguf.h, threads, err, 256)
+        if not self.h:
+            raise ValueError(err.value.decode())
+        dims = np.zeros(8, dtype=np.int32)
+        lib().or_model_dims(self.h, _p(dims))
+        (self.L, self.d, self.hq, self.hkv, self.hd, self.f, self.V, self.ctx) = (int(v) for v in dims)
+
+    def set_threads(self, n: int) -> None:
+        lib().or_model_set_threads(self.h, n)
+
+    def cache(self, capacity: int | None = None) -> "Cache":
+        return Cache(self, capacity or self.ctx)
+
+    def prefill(self, cache: "Cache", ids, gather) -> np.ndarray:
+        ids = _c(ids, np.int32)
+        gather = _c(gather, np.int32)
+        out = np.empty((gather.size, self.d), dtype=np.float32)
+        if lib().or_prefill(self.h, cache.h, _p(ids), ids.size, _p(gather), gather.size, _p(out)):
+            raise ValueError("oracle prefill rejected its input")
+        return out
+
+    def head(self, hidden, vocab_ids=None) -> np.ndarray:
+        hidden = _c(hidden, np.float32).reshape(-1, self.d)
+        vid = None if vocab_ids is None else _c(vocab_ids, np.int32)
+        nv = self.V if vid is None else vid.size
+        out = np.empty((hidden.shape[0], nv), dtype=np.float32)
+        if lib().or_head(self.h, _p(hidden), hidden.shape[0], _p(vid), nv, _p(out)):
+            raise ValueError("oracle head rejected its input")
+        return out
+
+    def forward(self, ids, positions, vocab_ids=None) -> np.ndarray:
+        """Full recompute over `ids` (Model::forward): logits at `positions`."""
+        c = self.cache(len(ids))
+        return self.head(self.prefill(c, ids, positions), vocab_ids)
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.or_model_free(self.h)
+            self.h = None
+
+
+class Cache:
+    def __init__(self, model: Model, capacity: int, handle=None):
+        self.model = model
+        self.h = handle or lib().or_cache_new(model.h, capacity)
+
+    def fork(self, ntokens: int) -> "Cache":
+        return Cache(self.model, 0, lib().or_cache_fork(self.h, ntokens))
+
+    def __len__(self):
+        return lib().or_cache_len(self.h)
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.or_cache_free(self.h)
+            self.h = None
+
+
+def argmax(v) -> int:
+    v = _c(v, np.float32)
+    return lib().or_argmax(_p(v), v.size)

@@ -1,0 +1,72 @@
+"""Parity bars shared by the GPU tests.
+
+* dequantised weights: bit-exact (NaN outputs: both NaN, payload not compared -- the
+  hardware multiply quiets NaN payloads like any IEEE multiply);
+* logits: max |gpu - ref| <= 2e-2 * max |ref| over each position's logit vector;
+* option probabilities: max |gpu - ref| <= 1e-3;
+* argmax: equal, except at near-ties -- positions whose oracle top-2 gap is below the logit
+  tolerance are reported separately and not asserted.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+LOGIT_REL = 2e-2
+PROB_ABS = 1e-3
+
+
+def assert_bits_equal(a: np.ndarray, b: np.ndarray) -> None:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    assert a.shape == b.shape
+    ab, bb = a.view(np.uint32), b.view(np.uint32)
+    both_nan = np.isnan(a) & np.isnan(b)
+    bad = (ab != bb) & ~both_nan
+    if bad.any():
+        i = int(np.flatnonzero(bad)[0])
+        raise AssertionError(f"{bad.sum()} mismatches; first at {i}: {a.flat[i]!r} ({ab.flat[i]:#010x}) "
+                             f"vs {b.flat[i]!r} ({bb.flat[i]:#010x})")
+
+
+def logit_error(gpu: np.ndarray, ref: np.ndarray) -> float:
+    """max over rows of max|gpu-ref| / max|ref|."""
+    gpu = np.atleast_2d(gpu)
+    ref = np.atleast_2d(ref)
+    scale = np.maximum(np.abs(ref).max(axis=1), 1e-30)
+    return float((np.abs(gpu - ref).max(axis=1) / scale).max())
+
+
+def assert_logits_close(gpu: np.ndarray, ref: np.ndarray, rel: float = LOGIT_REL) -> float:
+    err = logit_error(gpu, ref)
+    assert np.isfinite(gpu).all(), "non-finite GPU logits"
+    assert err <= rel, f"logits differ: relative error {err:.3e} > {rel}"
+    return err
+
+
+def argmax_report(gpu: np.ndarray, ref: np.ndarray, rel: float = LOGIT_REL):
+    """(mismatches outside near-ties, near-tie count) for row-wise argmax."""
+    gpu = np.atleast_2d(gpu)
+    ref = np.atleast_2d(ref)
+    bad, ties = 0, 0
+    for g, r in zip(gpu, ref):
+        order = np.argsort(-r, kind="stable")
+        gap = r[order[0]] - r[order[1]] if r.size > 1 else np.inf
+        tol = rel * np.abs(r).max()
+        if gap < tol:
+            ties += 1
+            continue
+        if int(np.argmax(g)) != int(np.argmax(r)):
+            bad += 1
+    return bad, ties
+
+
+def assert_argmax_equal(gpu, ref, rel: float = LOGIT_REL) -> int:
+    bad, ties = argmax_report(gpu, ref, rel)
+    assert bad == 0, f"{bad} argmax mismatches outside near-ties ({ties} near-ties)"
+    return ties
+
+
+def assert_probs_close(gpu, ref, tol: float = PROB_ABS) -> float:
+    err = float(np.abs(np.asarray(gpu) - np.asarray(ref)).max())
+    assert err <= tol, f"option probabilities differ by {err:.3e} > {tol}"
+    return err

@@ -1,0 +1,182 @@
+"""GPU forward-pass parity through the C ABI against the CPU oracle.
+
+Reference path: Model::forward (src/models/openthai/model.rs:192-241) with the decoder
+assembled from the reference primitives, option scoring (src/models/openthai/decision.rs:
+268-279), argmax first-max-wins (:330-335).  Invariants the reference's own tests hold
+(validation/smoke.py:25-28 repeat determinism, openthai_edges.py no state leakage) are
+checked as bit-exact properties of the GPU path.
+"""
+import numpy as np
+import pytest
+
+from parity import (assert_argmax_equal, assert_logits_close, assert_probs_close, logit_error)
+
+pytestmark = pytest.mark.gpu
+
+OPTIONS = [3, 17, 42, 99]
+
+
+@pytest.fixture(scope="module", params=["tiny-f16", "tiny-q8", "tiny-q4k", "tiny-f16-128"])
+def pair(request, lh, po):
+    img = lh.SynthImage(request.param, seed=5)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=8192)
+    om = po.Model(po.Gguf(img.array()), threads=8)
+    yield request.param, eng, om
+    eng.close()
+
+
+def _ids(n, vocab, seed):
+    return np.random.default_rng(seed).integers(0, vocab, size=n).astype(np.int32)
+
+
+def test_forward_options_and_probs(pair, lh, po):
+    preset, eng, om = pair
+    ids = _ids(150, om.V, 1)
+    pos = [149, 100, 63, 64, 0]
+    print(f"{preset}: forward 150 tokens", flush=True)
+    s = eng.seq_create()
+    b = eng.batch([(s, ids, pos)])
+    logits, probs, logprobs = b.run(OPTIONS, temperature=1.0)
+    want = om.forward(ids, pos, OPTIONS)
+    assert_logits_close(logits, want)
+    assert_argmax_equal(logits, want)
+    for r in range(len(pos)):
+        p_ref, lp_ref, _ = po.option_scores(want[r])
+        assert_probs_close(probs[r], p_ref)
+        assert np.abs(logprobs[r] - lp_ref).max() < 2e-2 * max(1.0, np.abs(lp_ref).max())
+    eng.seq_free(s)
+
+
+def test_forward_full_vocab(pair):
+    preset, eng, om = pair
+    ids = _ids(77, om.V, 2)
+    s = eng.seq_create()
+    got = eng.forward(s, ids, [76, 30])
+    want = om.forward(ids, [76, 30])
+    assert_logits_close(got, want)
+    assert_argmax_equal(got, want)
+    eng.seq_free(s)
+
+
+def test_repeat_is_bit_identical(pair):
+    preset, eng, om = pair
+    ids = _ids(90, om.V, 3)
+    outs = []
+    for _ in range(3):
+        s = eng.seq_create()
+        outs.append(eng.forward(s, ids, [89, 5], OPTIONS))
+        eng.seq_free(s)
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+
+
+def test_batch_equals_single(pair):
+    """Batch composition must not change any request's result (bit-exact)."""
+    preset, eng, om = pair
+    reqs = [(_ids(n, om.V, 10 + n), [n - 1, n // 2]) for n in (33, 100, 64, 7)]
+    singles = []
+    for ids, pos in reqs:
+        s = eng.seq_create()
+        singles.append(eng.forward(s, ids, pos, OPTIONS))
+        eng.seq_free(s)
+    seqs = [eng.seq_create() for _ in reqs]
+    b = eng.batch([(s, ids, pos) for s, (ids, pos) in zip(seqs, reqs)])
+    logits, _, _ = b.run(OPTIONS)
+    assert np.array_equal(np.concatenate(singles), logits)
+    for s in seqs:
+        eng.seq_free(s)
+
+
+def test_continuation_equals_one_shot(pair):
+    """Prefill in two calls over the KV cache == one call (bit-exact per row)."""
+    preset, eng, om = pair
+    ids = _ids(130, om.V, 4)
+    s1 = eng.seq_create()
+    one = eng.forward(s1, ids, [129], OPTIONS)
+    s2 = eng.seq_create()
+    eng.forward(s2, ids[:70], [], OPTIONS)
+    two = eng.forward(s2, ids[70:], [59], OPTIONS)
+    assert eng.seq_len(s2) == 130
+    assert np.array_equal(one, two)
+    eng.seq_free(s1)
+    eng.seq_free(s2)
+
+
+def test_fork_shared_prefix(pair):
+    """Forked sequences (shared whole pages, copied partial page) == unshared one-shot."""
+    preset, eng, om = pair
+    prefix = _ids(150, om.V, 6)
+    a = eng.seq_create()
+    eng.forward(a, prefix, [], OPTIONS)
+    for cut, seed in ((128, 7), (150, 8), (97, 9)):
+        suffix = _ids(40, om.V, seed)
+        b = eng.seq_fork(a, cut)
+        got = eng.forward(b, suffix, [39, 0], OPTIONS)
+        s = eng.seq_create()
+        ref = eng.forward(s, np.concatenate([prefix[:cut], suffix]), [cut + 39, cut], OPTIONS)
+        assert np.array_equal(got, ref), f"fork at {cut} differs"
+        want = om.forward(np.concatenate([prefix[:cut], suffix]), [cut + 39, cut], OPTIONS)
+        assert_logits_close(got, want)
+        eng.seq_free(b)
+        eng.seq_free(s)
+    eng.seq_free(a)
+
+
+def test_decode_teacher_forced(pair, po):
+    """Greedy decode over the paged cache; every step's argmax and logits vs the oracle fed
+    the same tokens (teacher-forced, so one near-tie cannot desynchronise later steps)."""
+    preset, eng, om = pair
+    if om.hd != 128:
+        pytest.skip("decode attention is built for head_dim 128")
+    ids = _ids(70, om.V, 12)
+    s = eng.seq_create()
+    eng.forward(s, ids[:-1], [], OPTIONS)
+    toks, logits = eng.decode(s, int(ids[-1]), 12, want_logits=True)
+    c = om.cache(200)
+    om.prefill(c, ids[:-1], [])
+    feed = [int(ids[-1])] + [int(t) for t in toks[:-1]]
+    ties = 0
+    for i, t in enumerate(feed):
+        want = om.head(om.prefill(c, [t], [0]))
+        assert_logits_close(logits[i], want)
+        ties += assert_argmax_equal(logits[i][None], want)
+        assert int(toks[i]) == int(np.argmax(logits[i]))
+    print(f"{preset}: decode near-ties {ties}")
+    eng.seq_free(s)
+
+
+def test_errors_are_reported(pair, lh):
+    preset, eng, om = pair
+    s = eng.seq_create()
+    with pytest.raises(lh.LayaError) as e:
+        eng.forward(s, [om.V], [0], OPTIONS)
+    assert e.value.kind == "INVALID" and "vocabulary" in str(e.value)
+    with pytest.raises(lh.LayaError):
+        eng.forward(s, [1, 2, 3], [3], OPTIONS)
+    with pytest.raises(lh.LayaError):
+        eng.forward(s, np.ones(om.ctx + 1, np.int32), [0], OPTIONS)
+    with pytest.raises(lh.LayaError) as e:
+        eng.forward(s, [1, 2], [1], OPTIONS, cancel=lambda _: 1)
+    assert e.value.kind == "CANCELED"
+    # the engine stays usable after errors
+    out = eng.forward(eng.seq_create(), [1, 2, 3], [2], OPTIONS)
+    assert np.isfinite(out).all()
+    eng.seq_free(s)
+
+
+def test_plumbing_model_decision(lh, po):
+    """The CPU-runnable plumbing model: 128-token prompt + one yes/no question block."""
+    img = lh.SynthImage("plumbing-f16", seed=1)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=4096)
+    om = po.Model(po.Gguf(img.array()), threads=8)
+    rng = np.random.default_rng(99)
+    ids = np.concatenate([rng.integers(0, 32000, 128), rng.integers(0, 32000, 16)]).astype(np.int32)
+    yes_no = [1939, 4874]
+    s = eng.seq_create()
+    logits, probs, _ = eng.batch([(s, ids, [143])]).run(yes_no)
+    want = om.forward(ids, [143], yes_no)
+    p_ref, _, _ = po.option_scores(want[0])
+    assert_logits_close(logits, want)
+    assert_probs_close(probs[0], p_ref)
+    assert int(np.argmax(probs[0])) == int(np.argmax(p_ref))
+    print(f"plumbing: logit err {logit_error(logits, want):.2e} probs {probs[0]} ref {p_ref}")
+    eng.close()

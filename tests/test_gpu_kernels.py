@@ -1,0 +1,82 @@
+"""GPU parity of the kernels through the C ABI: bit-exact dequant, GEMV/GEMM vs Matrix::apply.
+
+Reference: src/gguf.rs:250-336 (decode), src/tensor.rs:10-102 (Matrix::apply), restated by
+the CPU oracle.  Bars: see tests/parity.py.
+"""
+import numpy as np
+import pytest
+
+from parity import assert_bits_equal, assert_logits_close
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(20261201)
+
+
+def _blocks(kind, n, lh):
+    block, size = lh.layout(kind)
+    raw = RNG.integers(0, 256, size=n * size, dtype=np.uint8)
+    return raw
+
+
+def _edge_q8():
+    out = []
+    for d in (0x3C00, 0x0001, 0x03FF, 0x0400, 0x7BFF, 0x7C00, 0xFC00, 0x7E01, 0x8000, 0x0000):
+        codes = np.arange(-128, 128, 8, dtype=np.int8)  # 32 codes incl. -128 and 120
+        out.append(np.frombuffer(np.uint16(d).tobytes() + codes.tobytes(), dtype=np.uint8))
+    return np.concatenate(out)
+
+
+@pytest.mark.parametrize("kind", [0, 1, 2, 8, 12, 14])
+def test_dequant_bit_exact(lh, po, kind):
+    print(f"dequant kind={kind}", flush=True)
+    raw = _blocks(kind, 4096 if kind not in (12, 14) else 512, lh)
+    if kind == 8:
+        raw = np.concatenate([raw, _edge_q8()])
+    got = lh.dequant(kind, raw)
+    want = po.decode(kind, raw)
+    assert_bits_equal(got, want)
+
+
+def test_dequant_f16_exhaustive(lh, po):
+    codes = np.arange(65536, dtype=np.uint16)
+    got = lh.dequant(1, codes.view(np.uint8))
+    assert_bits_equal(got, po.decode(1, codes.view(np.uint8)))
+
+
+@pytest.fixture(scope="module", params=["tiny-f16", "tiny-q8", "tiny-q4k"])
+def model(request, lh, po):
+    img = lh.SynthImage(request.param, seed=11)
+    g = lh.Gguf.from_bytes(img)
+    eng = lh.Engine(g, kv_tokens=4096)
+    og = po.Gguf(img.array())
+    yield request.param, img, eng, og
+    eng.close()
+
+
+def _matrices(og):
+    names = []
+    for base in ("qkv.0.weight", "q.0.weight", "k.0.weight", "v.0.weight", "wo.0.weight", "mlp_wi.0.weight",
+                 "mlp_wo.1.weight", "output.weight"):
+        try:
+            og.tensor(base)
+            names.append(base)
+        except KeyError:
+            pass
+    return names
+
+
+@pytest.mark.parametrize("m", [1, 5, 64, 130, 300])
+def test_matmul_vs_apply(model, po, m):
+    preset, img, eng, og = model
+    for name in _matrices(og):
+        kind, dims, raw = og.tensor(name)
+        cols, rows = dims
+        w = po.decode(kind, raw).reshape(rows, cols)
+        x = RNG.standard_normal((m, cols)).astype(np.float32)
+        bias = RNG.standard_normal(rows).astype(np.float32) if m % 2 else None
+        print(f"{preset} {name} m={m}", flush=True)
+        got = eng.matmul(name, x, bias)
+        want = po.apply(w, x, bias, threads=4)
+        # m == 1 runs the f32 GEMV; m > 1 the f16-input MFMA GEMM
+        assert_logits_close(got, want, rel=1e-5 if m == 1 else 1e-2)
