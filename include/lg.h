@@ -91,11 +91,20 @@ void lg_synth_free(void *image);
 
 typedef struct lg_engine lg_engine;
 
+/* Numeric modes of the prefill path (the decode GEMV always computes in f32):
+ * LG_PREC_EXACT: f32-faithful -- activations carried as hi/lo f16 planes into split-precision
+ *   MFMA, weights applied exactly, f32 KV cache.  Matches the f32 reference to its own
+ *   summation-order spread even on ill-conditioned models.  The default.
+ * LG_PREC_FAST: one f16 MFMA pass, weights rounded to f16, f16 KV cache. */
+#define LG_PREC_EXACT 0
+#define LG_PREC_FAST 1
+
 typedef struct {
   int device;              /* HIP device ordinal */
   int kv_pages;            /* 64-token KV pages to reserve (0 = derive from kv_tokens) */
   int64_t kv_tokens;       /* tokens of KV capacity when kv_pages == 0 (0 = 65536) */
   int64_t max_batch_tokens;/* largest prefill batch (0 = 65536) */
+  int precision;           /* LG_PREC_EXACT (0) or LG_PREC_FAST */
 } lg_engine_opts;
 
 typedef struct {
@@ -104,6 +113,8 @@ typedef struct {
   int64_t weight_bytes;    /* HBM bytes of the uploaded weight arena */
   int64_t kv_bytes;        /* HBM bytes of the KV page pool */
   int kv_pages, kv_page_tokens;
+  int precision;           /* LG_PREC_* the engine was created with */
+  int kv_elem_bytes;       /* 4 (f32 cache) or 2 (f16 cache) */
 } lg_model_info;
 
 /* Load a laya-decoder GGUF onto one GPU: validate, upload and repack every matrix into a

@@ -163,9 +163,12 @@ Engine::Engine(const Gguf &g, const lg_engine_opts &opts) {
   if (d % 64 || (hd != 64 && hd != 128))
     fail(LG_ERR_UNSUPPORTED, "d_model %d / head_dim %d outside the kernels' shapes", d, hd);
   max_batch_tokens_ = opts.max_batch_tokens > 0 ? opts.max_batch_tokens : 65536;
+  if (opts.precision != LG_PREC_EXACT && opts.precision != LG_PREC_FAST)
+    fail(LG_ERR_INVALID, "unknown precision mode %d", opts.precision);
+  precision = opts.precision;
   HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
   upload(g);
-  // KV pool: [L][npages][hkv][64][hd] halves for K, then the same for V
+  // KV pool: [L][npages][hkv][64][hd] elements (f32 in EXACT mode, f16 in FAST) for K, then V
   int64_t pages = opts.kv_pages;
   if (pages <= 0) {
     const int64_t toks = opts.kv_tokens > 0 ? opts.kv_tokens : 65536;
@@ -173,7 +176,7 @@ Engine::Engine(const Gguf &g, const lg_engine_opts &opts) {
   }
   npages_ = int(pages);
   page_stride_ = int64_t(hkv) * 64 * hd;
-  const size_t kv_bytes = size_t(2) * L * npages_ * page_stride_ * 2;
+  const size_t kv_bytes = size_t(2) * L * npages_ * page_stride_ * kv_elem();
   if (hipMalloc(&kv_, kv_bytes) != hipSuccess) {
     kv_ = nullptr;
     (void)hipGetLastError();
@@ -369,9 +372,11 @@ lg_model_info Engine::info() const {
   i.kind_ffn = layers_.empty() ? 0 : layers_[0].wd.kind;
   i.kind_head = head_.kind;
   i.weight_bytes = weight_bytes_;
-  i.kv_bytes = int64_t(2) * L * npages_ * page_stride_ * 2;
+  i.kv_bytes = int64_t(2) * L * npages_ * page_stride_ * kv_elem();
   i.kv_pages = npages_;
   i.kv_page_tokens = 64;
+  i.precision = precision;
+  i.kv_elem_bytes = kv_elem();
   return i;
 }
 
@@ -384,20 +389,21 @@ KvGeom Engine::geom() const {
   g.hd = hd;
   g.page_stride = page_stride_;
   g.layer_stride = int64_t(npages_) * page_stride_;
+  g.kv32 = split() ? 1 : 0;
   return g;
 }
-_Float16 *Engine::kpool(int layer) const {
-  return static_cast<_Float16 *>(kv_) + int64_t(layer) * npages_ * page_stride_;
+void *Engine::kpool(int layer) const {
+  return static_cast<uint8_t *>(kv_) + int64_t(layer) * npages_ * page_stride_ * kv_elem();
 }
-_Float16 *Engine::vpool(int layer) const {
-  return static_cast<_Float16 *>(kv_) + (int64_t(L) + layer) * npages_ * page_stride_;
+void *Engine::vpool(int layer) const {
+  return static_cast<uint8_t *>(kv_) + (int64_t(L) + layer) * npages_ * page_stride_ * kv_elem();
 }
 
 // ------------------------------------------------------------------ kernels with profiling
-void Engine::gemm(const _Float16 *A, int M, const DevMatrix &W, Epi epi, float *C, _Float16 *C16,
-                  int ldc, const float *bias) {
+void Engine::gemm(const _Float16 *A, const _Float16 *A_lo, int M, const DevMatrix &W, Epi epi, float *C,
+                  _Float16 *C16, _Float16 *C16_lo, int ldc, const float *bias) {
   prof.begin("gemm", stream);
-  launch_gemm(A, M, W, epi, C, C16, ldc, bias, stream);
+  launch_gemm(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, stream);
   prof.end(double(W.bytes()) + double(M) * W.cols * 2, 2.0 * M * double(W.rows) * W.cols, stream);
 }
 
@@ -430,9 +436,11 @@ void Engine::matmul(const std::string &name, const float *x, int m, const float 
   if (m == 1 && W.cols % 16 == 0 && W.cols * 4 <= 64 * 1024 && W.kind != LG_F32) {
     gemv(dx.as<float>(), W, Epi::F32, dy.as<float>(), dbias, nullptr);
   } else if (tiled && m > 1) {
-    dh.ensure(size_t(m) * W.cols * 2);
-    launch_cvt_f16(dx.as<float>(), int64_t(m) * W.cols, dh.as<_Float16>(), stream);
-    gemm(dh.as<_Float16>(), m, W, Epi::F32, dy.as<float>(), nullptr, W.rows, dbias);
+    const int64_t n = int64_t(m) * W.cols;
+    dh.ensure(size_t(n) * 4);
+    _Float16 *hi = dh.as<_Float16>(), *lo = split() ? hi + n : nullptr;
+    launch_cvt_f16(dx.as<float>(), n, hi, lo, stream);
+    gemm(hi, lo, m, W, Epi::F32, dy.as<float>(), nullptr, nullptr, W.rows, dbias);
   } else {
     launch_gemm_generic(dx.as<float>(), m, W, dbias, dy.as<float>(), stream);
   }
@@ -487,11 +495,10 @@ int Engine::seq_fork(int parent, int ntokens) {
   if (rem) {  // private copy of the partly filled page, all layers, K and V
     const int np = alloc_page();
     for (int l = 0; l < L; ++l) {
-      const size_t bytes = size_t(page_stride_) * 2;
-      HIP_CHECK(hipMemcpyAsync(kpool(l) + int64_t(np) * page_stride_, kpool(l) + int64_t(p.pages[full]) * page_stride_,
-                               bytes, hipMemcpyDeviceToDevice, stream));
-      HIP_CHECK(hipMemcpyAsync(vpool(l) + int64_t(np) * page_stride_, vpool(l) + int64_t(p.pages[full]) * page_stride_,
-                               bytes, hipMemcpyDeviceToDevice, stream));
+      const size_t bytes = size_t(page_stride_) * kv_elem();
+      uint8_t *kb = static_cast<uint8_t *>(kpool(l)), *vb = static_cast<uint8_t *>(vpool(l));
+      HIP_CHECK(hipMemcpyAsync(kb + np * bytes, kb + p.pages[full] * bytes, bytes, hipMemcpyDeviceToDevice, stream));
+      HIP_CHECK(hipMemcpyAsync(vb + np * bytes, vb + p.pages[full] * bytes, bytes, hipMemcpyDeviceToDevice, stream));
     }
     c.pages.push_back(np);
   }
@@ -600,14 +607,19 @@ void Engine::batch_free(BatchPlan *b) { delete b; }
 
 void Engine::run_layers_prefill(BatchPlan &b, lg_cancel_fn cancel, void *arg) {
   const int T = b.T, qw = hq * hd, kvw = hkv * hd, qkvw = qw + 2 * kvw;
+  const int planes = split() ? 2 : 1;  // hi (+ lo) f16 planes per activation
   ws_x_.ensure(size_t(T) * d * 4);
-  ws_h16_.ensure(size_t(T) * d * 2);
+  ws_h16_.ensure(size_t(T) * d * 2 * planes);
   ws_qkv_.ensure(size_t(T) * qkvw * 4);
-  ws_q16_.ensure(size_t(T) * qw * 2);
-  ws_att16_.ensure(size_t(T) * qw * 2);
-  ws_act16_.ensure(size_t(T) * f * 2);
+  ws_q16_.ensure(size_t(T) * qw * 2 * planes);
+  ws_att16_.ensure(size_t(T) * qw * 2 * planes);
+  ws_act16_.ensure(size_t(T) * f * 2 * planes);
+  auto lo = [&](DevBuf &buf, int64_t n) { return split() ? buf.as<_Float16>() + n : nullptr; };
   float *x = ws_x_.as<float>();
-  _Float16 *h16 = ws_h16_.as<_Float16>();
+  _Float16 *h16 = ws_h16_.as<_Float16>(), *h16lo = lo(ws_h16_, int64_t(T) * d);
+  _Float16 *q16 = ws_q16_.as<_Float16>(), *q16lo = lo(ws_q16_, int64_t(T) * qw);
+  _Float16 *att = ws_att16_.as<_Float16>(), *attlo = lo(ws_att16_, int64_t(T) * qw);
+  _Float16 *act = ws_act16_.as<_Float16>(), *actlo = lo(ws_act16_, int64_t(T) * f);
   float *qkv = ws_qkv_.as<float>();
   const KvGeom g = geom();
   prof.begin("embed", stream);
@@ -617,24 +629,24 @@ void Engine::run_layers_prefill(BatchPlan &b, lg_cancel_fn cancel, void *arg) {
     if (cancel && cancel(arg)) fail(LG_ERR_CANCELED, "request canceled");
     const Layer &ly = layers_[l];
     prof.begin("rmsnorm", stream);
-    launch_rmsnorm_f16(x, T, d, ly.attn_norm, eps, h16, stream);
-    prof.end(double(T) * d * 6, 0, stream);
-    for (const ProjPart &p : ly.qkv) gemm(h16, T, p.w, Epi::F32, qkv + p.col0, nullptr, qkvw, p.bias);
+    launch_rmsnorm_f16(x, T, d, ly.attn_norm, eps, h16, h16lo, stream);
+    prof.end(double(T) * d * (4 + 2 * planes), 0, stream);
+    for (const ProjPart &p : ly.qkv)
+      gemm(h16, h16lo, T, p.w, Epi::F32, qkv + p.col0, nullptr, nullptr, qkvw, p.bias);
     prof.begin("rope_kv", stream);
-    launch_rope_kv(qkv, T, hq, g, cos_, sin_, b.tok_seq, b.tok_pos, b.pages, b.max_pages,
-                   ws_q16_.as<_Float16>(), nullptr, kpool(l), vpool(l), stream);
-    prof.end(double(T) * (qkvw * 4 + (qw + 2 * kvw) * 2), 0, stream);
+    launch_rope_kv(qkv, T, hq, g, cos_, sin_, b.tok_seq, b.tok_pos, b.pages, b.max_pages, q16, q16lo,
+                   nullptr, kpool(l), vpool(l), stream);
+    prof.end(double(T) * (qkvw * 4 + qw * 2 * planes + 2 * kvw * kv_elem()), 0, stream);
     prof.begin("attn_prefill", stream);
-    launch_attn_prefill(ws_q16_.as<_Float16>(), T, hq, g, kpool(l), vpool(l), b.pages, b.max_pages,
-                        b.tile_seq, b.tile_row0, b.tile_pos0, b.tile_n, b.ntiles,
-                        ws_att16_.as<_Float16>(), stream);
+    launch_attn_prefill(q16, q16lo, T, hq, g, kpool(l), vpool(l), b.pages, b.max_pages, b.tile_seq,
+                        b.tile_row0, b.tile_pos0, b.tile_n, b.ntiles, att, attlo, stream);
     prof.end(0, 0, stream);
-    gemm(ws_att16_.as<_Float16>(), T, ly.wo, Epi::ADD, x, nullptr, d, nullptr);
+    gemm(att, attlo, T, ly.wo, Epi::ADD, x, nullptr, nullptr, d, nullptr);
     prof.begin("rmsnorm", stream);
-    launch_rmsnorm_f16(x, T, d, ly.ffn_norm, eps, h16, stream);
-    prof.end(double(T) * d * 6, 0, stream);
-    gemm(h16, T, ly.wi, Epi::SWIGLU, nullptr, ws_act16_.as<_Float16>(), f, nullptr);
-    gemm(ws_act16_.as<_Float16>(), T, ly.wd, Epi::ADD, x, nullptr, d, nullptr);
+    launch_rmsnorm_f16(x, T, d, ly.ffn_norm, eps, h16, h16lo, stream);
+    prof.end(double(T) * d * (4 + 2 * planes), 0, stream);
+    gemm(h16, h16lo, T, ly.wi, Epi::SWIGLU, nullptr, act, actlo, f, nullptr);
+    gemm(act, actlo, T, ly.wd, Epi::ADD, x, nullptr, nullptr, d, nullptr);
   }
 }
 
@@ -736,13 +748,13 @@ void Engine::decode(int sq, int32_t first, int steps, int32_t *tokens, float *lo
       const Layer &ly = layers_[l];
       for (const ProjPart &p : ly.qkv) gemv(x, p.w, Epi::F32, qkv + p.col0, p.bias, ly.attn_norm);
       prof.begin("rope_kv", stream);
-      launch_rope_kv(qkv, 1, hq, g, cos_, sin_, tseq, pos + i, pt, max_pages, nullptr, q32, kpool(l),
-                     vpool(l), stream);
-      prof.end(double(qkvw) * 4 + double(2 * kvw) * 2, 0, stream);
+      launch_rope_kv(qkv, 1, hq, g, cos_, sin_, tseq, pos + i, pt, max_pages, nullptr, nullptr, q32,
+                     kpool(l), vpool(l), stream);
+      prof.end(double(qkvw) * 4 + double(2 * kvw) * kv_elem(), 0, stream);
       prof.begin("attn_decode", stream);
       launch_attn_decode(q32, 1, hq, g, kpool(l), vpool(l), pt, max_pages, clen + i, pos0 + i + 1,
                          part, att, stream);
-      prof.end(double(pos0 + i + 1) * 2 * kvw * 2, 4.0 * double(pos0 + i + 1) * qw, stream);
+      prof.end(double(pos0 + i + 1) * 2 * kvw * kv_elem(), 4.0 * double(pos0 + i + 1) * qw, stream);
       gemv(att, ly.wo, Epi::ADD, x, nullptr, nullptr);
       gemv(x, ly.wi, Epi::SWIGLU, act, nullptr, ly.ffn_norm);
       gemv(act, ly.wd, Epi::ADD, x, nullptr, nullptr);

@@ -105,12 +105,13 @@ class Engine {
   void release_page(int p);
   void run_layers_prefill(BatchPlan &b, lg_cancel_fn cancel, void *arg);
   KvGeom geom() const;
-  _Float16 *kpool(int layer) const;
-  _Float16 *vpool(int layer) const;
+  void *kpool(int layer) const;
+  void *vpool(int layer) const;
 
   // prof-wrapped launch helpers
-  void gemm(const _Float16 *A, int M, const DevMatrix &W, Epi epi, float *C, _Float16 *C16, int ldc,
-            const float *bias);
+  // A/A_lo and C16/C16_lo are hi/lo planes in EXACT mode (lo == nullptr in FAST mode)
+  void gemm(const _Float16 *A, const _Float16 *A_lo, int M, const DevMatrix &W, Epi epi, float *C,
+            _Float16 *C16, _Float16 *C16_lo, int ldc, const float *bias);
   void gemv(const float *x, const DevMatrix &W, Epi epi, float *y, const float *bias,
             const float *norm_w);
 
@@ -120,6 +121,9 @@ class Engine {
   int L = 0, d = 0, hq = 0, hkv = 0, hd = 0, f = 0, V = 0, ctx = 0;
   float eps = 1e-5f;
   uint32_t emb_kind = 0;
+  int precision = LG_PREC_EXACT;
+  bool split() const { return precision == LG_PREC_EXACT; }
+  int kv_elem() const { return split() ? 4 : 2; }
 
  private:
   // weights
@@ -134,7 +138,7 @@ class Engine {
   // KV pool
   void *kv_ = nullptr;
   int npages_ = 0;
-  int64_t page_stride_ = 0;  // halves per (layer, page) of K (same for V)
+  int64_t page_stride_ = 0;  // elements per (layer, page) of K (same for V)
   std::vector<int> free_pages_, refcnt_;
   std::map<int, Seq> seqs_;
   int next_seq_ = 1;

@@ -1,20 +1,24 @@
-// Causal GQA attention over the paged F16 KV cache (gfx950).
+// Causal GQA attention over the paged KV cache (gfx950).
 //
 // Reference semantics (src/models/openthai/model.rs:276-294, generalised to hq/hkv heads):
 // for query i of head h, kv head kh = h / (hq/hkv), s_j = dot(q_i, k_j) / sqrt(hd) for
 // j <= pos_i, p = softmax(s), out = sum_j p_j v_j.
 //
-// KV page layout (one layer, one page of P = 64 tokens):
+// KV page layout (one layer, one page of P = 64 tokens), element type f16 or f32:
 //   K: [hkv][P][hd] (row per token)     V: [hkv][hd][P] (column per token)
 //
 // Prefill: one wave per (32-query tile, query head).  S^T = K . Q^T on MFMA 32x32x16 f16, so
 // each lane owns one query column and the online softmax reduces over its own registers plus
-// one lane swap; O^T = V^T . P^T then consumes P straight from registers.
+// one lane swap; O^T = V^T . P^T then consumes P straight from registers.  With an f32 cache
+// and hi/lo query planes every product is split (hi.hi + lo.hi + hi.lo: three MFMAs), which
+// keeps scores and outputs f32-faithful.
 //
-// Decode: one wave per (sequence, kv head, page): coalesced 16 KB reads of the page's K rows
-// and V columns, f32 scores for every query head of the group, partial (max, sum, out) per
-// page; a second kernel combines the pages.
+// Decode: one wave per (sequence, kv head, page): coalesced reads of the page's K rows and
+// V columns, f32 scores for every query head of the group, partial (max, sum, out) per page;
+// a second kernel combines the pages.
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 
 #include "common.h"
 #include "kernels.h"
@@ -29,13 +33,26 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int P = 64;  // tokens per page
 constexpr float kLog2e = 1.4426950408889634f;
 
-template <int HD>
+#define MFMA(a, b, c) __builtin_amdgcn_mfma_f32_32x32x16_f16((a), (b), (c), 0, 0, 0)
+
+__device__ __forceinline__ void split8(const float *v, half8 &hi, half8 &lo) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const _Float16 h = _Float16(v[j]);
+    hi[j] = h;
+    lo[j] = _Float16(v[j] - float(h));
+  }
+}
+
+// SPLIT == false: f16 cache, f16 q.  SPLIT == true: f32 cache, q as hi/lo planes.
+template <int HD, bool SPLIT>
 __global__ __launch_bounds__(64) void attn_prefill_kernel(
-    const _Float16 *__restrict__ q16, int hq, KvGeom g, const _Float16 *__restrict__ kpool,
-    const _Float16 *__restrict__ vpool, const int32_t *__restrict__ pages, int max_pages,
-    const int32_t *__restrict__ tile_seq, const int32_t *__restrict__ tile_row0,
+    const _Float16 *__restrict__ q16, const _Float16 *__restrict__ q16lo, int hq, KvGeom g,
+    const void *__restrict__ kpool, const void *__restrict__ vpool, const int32_t *__restrict__ pages,
+    int max_pages, const int32_t *__restrict__ tile_seq, const int32_t *__restrict__ tile_row0,
     const int32_t *__restrict__ tile_pos0, const int32_t *__restrict__ tile_n,
-    _Float16 *__restrict__ out16) {
+    _Float16 *__restrict__ out16, _Float16 *__restrict__ out16lo) {
+  using KV = typename std::conditional<SPLIT, float, _Float16>::type;
   constexpr int KT = HD / 16;  // k-steps of the QK^T product
   constexpr int DB = HD / 32;  // 32-wide d blocks of the output
   const int tile = blockIdx.x, h = blockIdx.y;
@@ -47,11 +64,14 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(
   const bool live = qi < n;
 
   // Q^T operand: lane holds q[qi][16t + 8*hl .. +8]
-  half8 qr[KT];
+  half8 qr[KT], ql[SPLIT ? KT : 1];
   {
-    const _Float16 *qp = q16 + int64_t(row0 + min(qi, n - 1)) * qw + h * HD + hl * 8;
+    const int64_t off = int64_t(row0 + min(qi, n - 1)) * qw + h * HD + hl * 8;
 #pragma unroll
-    for (int t = 0; t < KT; ++t) qr[t] = *reinterpret_cast<const half8 *>(qp + 16 * t);
+    for (int t = 0; t < KT; ++t) {
+      qr[t] = *reinterpret_cast<const half8 *>(q16 + off + 16 * t);
+      if (SPLIT) ql[t] = *reinterpret_cast<const half8 *>(q16lo + off + 16 * t);
+    }
   }
   f32x16 acc[DB];
 #pragma unroll
@@ -62,21 +82,36 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(
   const float scale = kLog2e / sqrtf(float(HD));
   const int last = pos0 + n - 1;
   const int32_t *ptab = pages + int64_t(seq) * max_pages;
+  const KV *kbase = static_cast<const KV *>(kpool);
+  const KV *vbase = static_cast<const KV *>(vpool);
 
   for (int kt = 0; kt <= last / P; ++kt) {
     const int64_t page = ptab[kt];
-    const _Float16 *Kp = kpool + page * g.page_stride + int64_t(kh) * P * HD;
-    const _Float16 *Vp = vpool + page * g.page_stride + int64_t(kh) * HD * P;
+    const KV *Kp = kbase + page * g.page_stride + int64_t(kh) * P * HD;
+    const KV *Vp = vbase + page * g.page_stride + int64_t(kh) * HD * P;
     f32x16 s[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
-      const _Float16 *kr = Kp + (kb * 32 + qi) * HD + hl * 8;
+      const KV *kr = Kp + (kb * 32 + qi) * HD + hl * 8;
 #pragma unroll
-      for (int t = 0; t < KT; ++t)
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8 *>(kr + 16 * t),
-                                                       qr[t], s[kb], 0, 0, 0);
+      for (int t = 0; t < KT; ++t) {
+        if constexpr (SPLIT) {
+          float kv[8];
+          const float4 a = *reinterpret_cast<const float4 *>(kr + 16 * t);
+          const float4 b = *reinterpret_cast<const float4 *>(kr + 16 * t + 4);
+          kv[0] = a.x; kv[1] = a.y; kv[2] = a.z; kv[3] = a.w;
+          kv[4] = b.x; kv[5] = b.y; kv[6] = b.z; kv[7] = b.w;
+          half8 kh8, kl8;
+          split8(kv, kh8, kl8);
+          s[kb] = MFMA(kh8, qr[t], s[kb]);
+          s[kb] = MFMA(kl8, qr[t], s[kb]);
+          s[kb] = MFMA(kh8, ql[t], s[kb]);
+        } else {
+          s[kb] = MFMA(*reinterpret_cast<const half8 *>(kr + 16 * t), qr[t], s[kb]);
+        }
+      }
     }
     // s[kb][r] <-> key kt*P + kb*32 + (r/4)*8 + hl*4 + r%4, query qi
     float mt = -INFINITY;
@@ -111,45 +146,72 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(
     // O^T += V^T . P^T over four 16-key chunks
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      half8 pb;
+      float pv[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pb[e] = _Float16(s[c >> 1][(c & 1) * 8 + e]);
+      for (int e = 0; e < 8; ++e) pv[e] = s[c >> 1][(c & 1) * 8 + e];
+      half8 ph, pl;
+      if constexpr (SPLIT) split8(pv, ph, pl);
+      else
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ph[e] = _Float16(pv[e]);
 #pragma unroll
       for (int b = 0; b < DB; ++b) {
-        const _Float16 *vr = Vp + (b * 32 + qi) * P + 16 * c + hl * 4;
-        const half4 lo = *reinterpret_cast<const half4 *>(vr);
-        const half4 hi = *reinterpret_cast<const half4 *>(vr + 8);
-        const half8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb, acc[b], 0, 0, 0);
+        const KV *vr = Vp + (b * 32 + qi) * P + 16 * c + hl * 4;
+        if constexpr (SPLIT) {
+          const float4 lo4 = *reinterpret_cast<const float4 *>(vr);
+          const float4 hi4 = *reinterpret_cast<const float4 *>(vr + 8);
+          const float vv[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
+          half8 vh, vl;
+          split8(vv, vh, vl);
+          acc[b] = MFMA(vh, ph, acc[b]);
+          acc[b] = MFMA(vl, ph, acc[b]);
+          acc[b] = MFMA(vh, pl, acc[b]);
+        } else {
+          const half4 lo = *reinterpret_cast<const half4 *>(vr);
+          const half4 hi = *reinterpret_cast<const half4 *>(vr + 8);
+          const half8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          acc[b] = MFMA(va, ph, acc[b]);
+        }
       }
     }
   }
   if (!live) return;
   const float inv = 1.0f / l;
-  _Float16 *op = out16 + int64_t(row0 + qi) * qw + h * HD;
+  const int64_t obase = int64_t(row0 + qi) * qw + h * HD;
   // acc[b][r] <-> d = b*32 + (r/4)*8 + hl*4 + r%4
 #pragma unroll
   for (int b = 0; b < DB; ++b)
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4) {
-      half4 o;
+      half4 o, olo;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) o[j] = _Float16(acc[b][r4 * 4 + j] * inv);
-      *reinterpret_cast<half4 *>(op + b * 32 + r4 * 8 + hl * 4) = o;
+      for (int j = 0; j < 4; ++j) {
+        const float v = acc[b][r4 * 4 + j] * inv;
+        o[j] = _Float16(v);
+        olo[j] = _Float16(v - float(o[j]));
+      }
+      const int64_t at = obase + b * 32 + r4 * 8 + hl * 4;
+      *reinterpret_cast<half4 *>(out16 + at) = o;
+      if (SPLIT) *reinterpret_cast<half4 *>(out16lo + at) = olo;
     }
 }
 
 // ---------------------------------------------------------------- decode
 // part layout: [nseq][hq][max_pages][2 + HD] = (max, sum, out[HD]) of one page.
-template <int HD, int GRP>
+// E = elements per 16-byte load (8 for f16, 4 for f32).
+template <int HD, int GRP, typename KV>
 __global__ __launch_bounds__(64) void attn_decode_kernel(const float *__restrict__ q32, int hq, KvGeom g,
-                                                         const _Float16 *__restrict__ kpool,
-                                                         const _Float16 *__restrict__ vpool,
+                                                         const KV *__restrict__ kpool,
+                                                         const KV *__restrict__ vpool,
                                                          const int32_t *__restrict__ pages,
                                                          int max_pages,
                                                          const int32_t *__restrict__ ctx_len,
                                                          float *__restrict__ part) {
   static_assert(HD == 128, "decode attention is written for head_dim 128");
+  constexpr int E = 16 / sizeof(KV);
+  constexpr int NLD = P * HD / E / 64;      // 16-byte loads per lane per page (16 or 32)
+  constexpr int KL = HD / E;                // lanes sharing one key row
+  constexpr int VL = P / E;                 // lanes sharing one V column-row (d)
   const int pi = blockIdx.x, kh = blockIdx.y, s = blockIdx.z;
   const int lane = threadIdx.x;
   const int len = ctx_len[s];
@@ -166,34 +228,35 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float *__restrict
   const int64_t page = pages[int64_t(s) * max_pages + pi];
   const uint4 *Kp = reinterpret_cast<const uint4 *>(kpool + page * g.page_stride + int64_t(kh) * P * HD);
   const uint4 *Vp = reinterpret_cast<const uint4 *>(vpool + page * g.page_stride + int64_t(kh) * HD * P);
-  uint4 kv[16], vv[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) kv[i] = Kp[i * 64 + lane];  // key lane/16 + 4i, dims (lane%16)*8
-#pragma unroll
-  for (int i = 0; i < 16; ++i) vv[i] = Vp[i * 64 + lane];  // d lane/8 + 8i, keys (lane%8)*8
   __shared__ float sc[GRP][P];
   const float inv_sqrt = 1.0f / sqrtf(float(HD));
+  {
+    uint4 kv[NLD];
 #pragma unroll
-  for (int gq = 0; gq < GRP; ++gq) {
-    const float *q = q32 + int64_t(s) * hq * HD + (kh * GRP + gq) * HD + (lane & 15) * 8;
-    float qv[8];
+    for (int i = 0; i < NLD; ++i) kv[i] = Kp[i * 64 + lane];  // key (i*64+lane)/KL, dims lane%KL*E
 #pragma unroll
-    for (int j = 0; j < 8; ++j) qv[j] = q[j];
+    for (int gq = 0; gq < GRP; ++gq) {
+      const float *q = q32 + int64_t(s) * hq * HD + (kh * GRP + gq) * HD + (lane % KL) * E;
+      float qv[E];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const _Float16 *kh8 = reinterpret_cast<const _Float16 *>(&kv[i]);
-      float d = 0.0f;
+      for (int j = 0; j < E; ++j) qv[j] = q[j];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) d += qv[j] * float(kh8[j]);
-      d += __shfl_xor(d, 1);
-      d += __shfl_xor(d, 2);
-      d += __shfl_xor(d, 4);
-      d += __shfl_xor(d, 8);
-      const int key = (lane >> 4) + 4 * i;
-      if ((lane & 15) == 0) sc[gq][key] = (pi * P + key < len) ? d * inv_sqrt : -INFINITY;
+      for (int i = 0; i < NLD; ++i) {
+        const KV *k8 = reinterpret_cast<const KV *>(&kv[i]);
+        float d = 0.0f;
+#pragma unroll
+        for (int j = 0; j < E; ++j) d += qv[j] * float(k8[j]);
+#pragma unroll
+        for (int off = 1; off < KL; off <<= 1) d += __shfl_xor(d, off);
+        const int key = (i * 64 + lane) / KL;
+        if (lane % KL == 0) sc[gq][key] = (pi * P + key < len) ? d * inv_sqrt : -INFINITY;
+      }
     }
   }
   __syncthreads();
+  uint4 vv[NLD];
+#pragma unroll
+  for (int i = 0; i < NLD; ++i) vv[i] = Vp[i * 64 + lane];  // d (i*64+lane)/VL, keys lane%VL*E
 #pragma unroll
   for (int gq = 0; gq < GRP; ++gq) {
     const float v = sc[gq][lane];
@@ -207,26 +270,21 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float *__restrict
     __syncthreads();
     sc[gq][lane] = p;
     __syncthreads();
-    float o[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const _Float16 *v8 = reinterpret_cast<const _Float16 *>(&vv[i]);
-      float a = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) a += sc[gq][(lane & 7) * 8 + j] * float(v8[j]);
-      a += __shfl_xor(a, 1);
-      a += __shfl_xor(a, 2);
-      a += __shfl_xor(a, 4);
-      o[i] = a;
-    }
     float *pp = pbase + gq * hstride;
     if (lane == 0) {
       pp[0] = mx;
       pp[1] = sum;
     }
-    if ((lane & 7) == 0)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) pp[2 + (lane >> 3) + 8 * i] = o[i];
+    for (int i = 0; i < NLD; ++i) {
+      const KV *v8 = reinterpret_cast<const KV *>(&vv[i]);
+      float a = 0.0f;
+#pragma unroll
+      for (int j = 0; j < E; ++j) a += sc[gq][(lane % VL) * E + j] * float(v8[j]);
+#pragma unroll
+      for (int off = 1; off < VL; off <<= 1) a += __shfl_xor(a, off);
+      if (lane % VL == 0) pp[2 + (i * 64 + lane) / VL] = a;
+    }
   }
 }
 
@@ -253,26 +311,30 @@ __global__ __launch_bounds__(128) void attn_decode_combine(const float *__restri
 
 }  // namespace
 
-void launch_attn_prefill(const _Float16 *q16, int T, int hq, const KvGeom &g,
-                         const _Float16 *kpool, const _Float16 *vpool, const int32_t *pages,
-                         int max_pages, const int32_t *tile_seq, const int32_t *tile_row0,
-                         const int32_t *tile_pos0, const int32_t *tile_n, int ntiles,
-                         _Float16 *out16, hipStream_t st) {
+void launch_attn_prefill(const _Float16 *q16, const _Float16 *q16_lo, int T, int hq,
+                         const KvGeom &g, const void *kpool, const void *vpool,
+                         const int32_t *pages, int max_pages, const int32_t *tile_seq,
+                         const int32_t *tile_row0, const int32_t *tile_pos0,
+                         const int32_t *tile_n, int ntiles, _Float16 *out16, _Float16 *out16_lo,
+                         hipStream_t st) {
   LG_REQUIRE(g.page_tokens == P, "attention: page size must be %d", P);
   LG_REQUIRE(hq % g.hkv == 0, "attention: hq %% hkv != 0");
   LG_REQUIRE(ntiles > 0 && T > 0, "attention: empty batch");
+  const bool split = q16_lo != nullptr;
+  LG_REQUIRE(split == (g.kv32 != 0), "attention: split queries need the f32 cache and vice versa");
+  LG_REQUIRE(!split || out16_lo, "attention: split path needs the lo output plane");
   const dim3 grid(ntiles, hq), block(64);
-  switch (g.hd) {
-    case 64:
-      hipLaunchKernelGGL(attn_prefill_kernel<64>, grid, block, 0, st, q16, hq, g, kpool, vpool, pages,
-                         max_pages, tile_seq, tile_row0, tile_pos0, tile_n, out16);
-      break;
-    case 128:
-      hipLaunchKernelGGL(attn_prefill_kernel<128>, grid, block, 0, st, q16, hq, g, kpool, vpool, pages,
-                         max_pages, tile_seq, tile_row0, tile_pos0, tile_n, out16);
-      break;
-    default: fail(LG_ERR_UNSUPPORTED, "attention: head_dim %d not supported (64, 128)", g.hd);
+#define LAUNCH(HDV, S)                                                                              \
+  hipLaunchKernelGGL((attn_prefill_kernel<HDV, S>), grid, block, 0, st, q16, q16_lo, hq, g, kpool, vpool, \
+                     pages, max_pages, tile_seq, tile_row0, tile_pos0, tile_n, out16, out16_lo)
+  if (g.hd == 64) {
+    if (split) LAUNCH(64, true); else LAUNCH(64, false);
+  } else if (g.hd == 128) {
+    if (split) LAUNCH(128, true); else LAUNCH(128, false);
+  } else {
+    fail(LG_ERR_UNSUPPORTED, "attention: head_dim %d not supported (64, 128)", g.hd);
   }
+#undef LAUNCH
   HIP_CHECK(hipGetLastError());
 }
 
@@ -281,10 +343,10 @@ int64_t attn_decode_scratch_floats(int nseq, int hq, int hd, int max_ctx) {
   return int64_t(nseq) * hq * pages * (2 + hd);
 }
 
-void launch_attn_decode(const float *q32, int nseq, int hq, const KvGeom &g,
-                        const _Float16 *kpool, const _Float16 *vpool, const int32_t *pages,
-                        int max_pages, const int32_t *ctx_len, int max_ctx, float *part,
-                        float *out, hipStream_t st) {
+void launch_attn_decode(const float *q32, int nseq, int hq, const KvGeom &g, const void *kpool,
+                        const void *vpool, const int32_t *pages, int max_pages,
+                        const int32_t *ctx_len, int max_ctx, float *part, float *out,
+                        hipStream_t st) {
   LG_REQUIRE(g.page_tokens == P, "attention: page size must be %d", P);
   LG_REQUIRE(g.hd == 128, "decode attention: head_dim %d not supported (128)", g.hd);
   LG_REQUIRE(nseq > 0 && max_ctx > 0, "decode attention: empty");
@@ -292,16 +354,22 @@ void launch_attn_decode(const float *q32, int nseq, int hq, const KvGeom &g,
   LG_REQUIRE(np <= max_pages, "decode attention: context exceeds the page table");
   const int grp = hq / g.hkv;
   const dim3 grid(np, g.hkv, nseq), block(64);
-  switch (grp) {
-#define CASE(G)                                                                                   \
-  case G:                                                                                         \
-    hipLaunchKernelGGL((attn_decode_kernel<128, G>), grid, block, 0, st, q32, hq, g, kpool, vpool, \
-                       pages, max_pages, ctx_len, part);                                         \
+#define CASE(G)                                                                                     \
+  case G:                                                                                           \
+    if (g.kv32)                                                                                     \
+      hipLaunchKernelGGL((attn_decode_kernel<128, G, float>), grid, block, 0, st, q32, hq, g,        \
+                         static_cast<const float *>(kpool), static_cast<const float *>(vpool), pages, \
+                         max_pages, ctx_len, part);                                                 \
+    else                                                                                            \
+      hipLaunchKernelGGL((attn_decode_kernel<128, G, _Float16>), grid, block, 0, st, q32, hq, g,     \
+                         static_cast<const _Float16 *>(kpool), static_cast<const _Float16 *>(vpool), \
+                         pages, max_pages, ctx_len, part);                                          \
     break;
+  switch (grp) {
     CASE(1) CASE(2) CASE(4) CASE(7) CASE(8)
-#undef CASE
     default: fail(LG_ERR_UNSUPPORTED, "decode attention: group size %d not supported", grp);
   }
+#undef CASE
   hipLaunchKernelGGL(attn_decode_combine, dim3(hq, nseq), dim3(128), 0, st, part, hq, g.hd, max_pages,
                      ctx_len, out);
   HIP_CHECK(hipGetLastError());

@@ -1,10 +1,20 @@
-// Prefill GEMM for gfx950: C = A . W^T, A = activations (f16, [M][K] row-major),
-// W = quantised/F16 weights dequantised to f16 in LDS, f32 accumulation on MFMA
-// v_mfma_f32_32x32x16_f16, epilogue fused (bias, residual add, SwiGLU, f16 store).
+// Prefill GEMM for gfx950: C = A . W^T on MFMA v_mfma_f32_32x32x16_f16, f32 accumulation,
+// weights dequantised into LDS, epilogue fused (bias, residual add, SwiGLU, f16 store).
 //
-// Tile 128 x 128 x 64, 256 threads = 4 wave64s in a 2 x 2 arrangement, each wave a
-// 64 x 64 sub-tile = 2 x 2 MFMA blocks of 32 x 32.  Global loads for the next K tile are
-// issued before the MFMAs of the current one (register double buffering).
+// Three numeric modes (selected by the caller):
+//   FAST  : A in f16, W dequantised to f16 (RNE); one MFMA pass.
+//   SPLIT : A given as two f16 planes (hi = f16(a), lo = f16(a - hi)), so A carries ~22
+//           significand bits.  F16 weights are exact in f16 -> 2 passes (hi, lo).
+//           Q8_0 codes are exact in f16 and the block scale is applied in f32 per 32-element
+//           block (partial sums on MFMA, acc += d * partial) -> 2 passes, weights exact.
+//   SPLIT3: K-quants (Q4_K, Q6_K) whose dequantised f32 weight needs 24 bits: W is split into
+//           hi/lo f16 too and acc += Ah.Bh + Al.Bh + Ah.Bl -> 3 passes.
+// The split modes reproduce f32 arithmetic to ~2^-22 relative per product, which the
+// ill-conditioned synthetic workloads need to stay within the parity bars.
+//
+// Tile 128 x 128 x BK, 256 threads = 4 wave64s in a 2 x 2 arrangement, each wave a 64 x 64
+// sub-tile = 2 x 2 MFMA blocks of 32 x 32.  Global loads for the next K tile are issued
+// before the MFMAs of the current one (register double buffering).
 #include <hip/hip_runtime.h>
 
 #include "common.h"
@@ -15,46 +25,68 @@ namespace lg {
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128, BN = 128, BK = 64;
-constexpr int LDK = BK + 8;  // LDS row stride (halves): 144 B keeps 16-lane b128 reads conflict-free
+constexpr int BM = 128, BN = 128;
+enum Mode { FAST = 0, SPLIT = 1, SPLIT3 = 2 };
 
 __device__ __forceinline__ float silu(float g) { return g * (1.0f / (1.0f + __expf(-g))); }
 
+__device__ __forceinline__ half8 cvt8(const float *v) {
+  half8 h;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) h[j] = _Float16(v[j]);
+  return h;
+}
+// hi/lo split of 8 floats
+__device__ __forceinline__ void split8(const float *v, half8 &hi, half8 &lo) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const _Float16 h = _Float16(v[j]);
+    hi[j] = h;
+    lo[j] = _Float16(v[j] - float(h));
+  }
+}
+
 // ---------------------------------------------------------------- B tile loaders
-// Each loader fetches its share of a BN x BK weight tile into registers (fetch) and later
-// dequantises into LDS rows (store).  `wrow` is the weight row for local row r.
-template <uint32_t KIND>
+// fetch(): global -> registers for this thread's share of a BN x BK tile.
+// store(): registers -> LDS rows (stride LDK halves), dequantised per mode.
+template <uint32_t KIND, int MODE, int BK>
 struct BLoad;
 
-template <>
-struct BLoad<LG_F16> {
-  uint4 v[4];
+// F16 weights (exact in f16 for every mode)
+template <int MODE, int BK>
+struct BLoad<LG_F16, MODE, BK> {
+  static constexpr int kPer = BN * BK / 8 / 256;  // 16-byte chunks per thread
+  static constexpr int kRows = kPer;
+  uint4 v[kPer];
+  __device__ static int row_of(int t, int i) { return (t + 256 * i) / (BK / 8); }
   __device__ void fetch(const DevMatrix &W, const int *wrow, int k0, int t) {
     const _Float16 *q = static_cast<const _Float16 *>(W.q);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = t / 8 + 32 * i, c = (t % 8) * 8;
+    for (int i = 0; i < kPer; ++i) {
+      const int c = ((t + 256 * i) % (BK / 8)) * 8;
       v[i] = *reinterpret_cast<const uint4 *>(q + int64_t(wrow[i]) * W.cols + k0 + c);
     }
   }
-  __device__ void store(_Float16 *Bs, int t) {
+  template <int LDK>
+  __device__ void store(_Float16 *Bs, _Float16 *, float *, int t) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = t / 8 + 32 * i, c = (t % 8) * 8;
+    for (int i = 0; i < kPer; ++i) {
+      const int idx = t + 256 * i, r = idx / (BK / 8), c = (idx % (BK / 8)) * 8;
       *reinterpret_cast<uint4 *>(Bs + r * LDK + c) = v[i];
     }
   }
-  __device__ static int row_of(int t, int i) { return t / 8 + 32 * i; }
-  static constexpr int kRows = 4;
 };
 
-template <>
-struct BLoad<LG_Q8_0> {
+// Q8_0: FAST dequantises f16(d)*code; SPLIT stores the exact codes and the f32 block scale.
+template <int MODE, int BK>
+struct BLoad<LG_Q8_0, MODE, BK> {
+  static_assert(BK == 64, "Q8_0 tiles are 64 wide (two blocks)");
+  static constexpr int kRows = 1;
   uint4 c0, c1;
   uint32_t sb;
+  __device__ static int row_of(int t, int) { return t / 2; }
   __device__ void fetch(const DevMatrix &W, const int *wrow, int k0, int t) {
     const int part = t % 2;
     const int8_t *q = static_cast<const int8_t *>(W.q) + int64_t(wrow[0]) * W.cols + k0 + part * 32;
@@ -62,98 +94,133 @@ struct BLoad<LG_Q8_0> {
     c1 = *reinterpret_cast<const uint4 *>(q + 16);
     sb = static_cast<const uint16_t *>(W.s)[int64_t(wrow[0]) * (W.cols / 32) + k0 / 32 + part];
   }
-  __device__ static void cvt16(uint4 c, _Float16 d, _Float16 *dst) {
+  __device__ static void cvt16(uint4 c, _Float16 d, bool scale, _Float16 *dst) {
     const uint32_t w[4] = {c.x, c.y, c.z, c.w};
     half8 o0, o1;
-    // f16(d) * code is the round-to-nearest f16 of the exact product (d*code is exact in f32)
+    // f16(d) * code rounds the exact product once (d * code is exact in f32)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const uint32_t word = w[j / 4];
-      o0[j] = _Float16(int8_t(word >> (8 * (j % 4)))) * d;
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t word = w[2 + j / 4];
-      o1[j] = _Float16(int8_t(word >> (8 * (j % 4)))) * d;
+      const _Float16 a = _Float16(int8_t(w[j / 4] >> (8 * (j % 4))));
+      const _Float16 b = _Float16(int8_t(w[2 + j / 4] >> (8 * (j % 4))));
+      o0[j] = scale ? a * d : a;
+      o1[j] = scale ? b * d : b;
     }
     *reinterpret_cast<half8 *>(dst) = o0;
     *reinterpret_cast<half8 *>(dst + 8) = o1;
   }
-  __device__ void store(_Float16 *Bs, int t) {
+  template <int LDK>
+  __device__ void store(_Float16 *Bs, _Float16 *, float *Ds, int t) {
     const int r = t / 2, part = t % 2;
     const _Float16 d = __builtin_bit_cast(_Float16, uint16_t(sb));
-    cvt16(c0, d, Bs + r * LDK + part * 32);
-    cvt16(c1, d, Bs + r * LDK + part * 32 + 16);
+    cvt16(c0, d, MODE == FAST, Bs + r * LDK + part * 32);
+    cvt16(c1, d, MODE == FAST, Bs + r * LDK + part * 32 + 16);
+    if (MODE == SPLIT) Ds[r * 2 + part] = half_bits(sb);
   }
-  __device__ static int row_of(int t, int) { return t / 2; }
-  static constexpr int kRows = 1;
 };
 
-template <>
-struct BLoad<LG_Q4_K> {
-  uint4 c;
+// Q4_K: w = (d*sc)*q - (dmin*m) per 32-element sub-block.
+template <int MODE, int BK>
+struct BLoad<LG_Q4_K, MODE, BK> {
+  static constexpr int kRows = 1;
+  uint4 c;      // 16 bytes
   float2 s0, s1;
+  __device__ static int row_of(int t, int) { return t / 2; }
   __device__ void fetch(const DevMatrix &W, const int *wrow, int k0, int t) {
     const int part = t % 2;
-    const uint8_t *q = static_cast<const uint8_t *>(W.q) + int64_t(wrow[0]) * (W.cols / 2) + k0 / 2 + part * 16;
-    c = *reinterpret_cast<const uint4 *>(q);
-    const float2 *s = static_cast<const float2 *>(W.s) + int64_t(wrow[0]) * (W.cols / 32) + k0 / 32;
-    s0 = s[0];
-    s1 = s[1];
+    const uint8_t *rowq = static_cast<const uint8_t *>(W.q) + int64_t(wrow[0]) * (W.cols / 2);
+    const float2 *s = static_cast<const float2 *>(W.s) + int64_t(wrow[0]) * (W.cols / 32);
+    if (BK == 64) {  // both nibbles of bytes [k0/2 + part*16, +16)
+      c = *reinterpret_cast<const uint4 *>(rowq + k0 / 2 + part * 16);
+      s0 = s[k0 / 32];
+      s1 = s[k0 / 32 + 1];
+    } else {  // BK == 32: one nibble plane of bytes [(k0/64)*32 + part*16, +16)
+      c = *reinterpret_cast<const uint4 *>(rowq + (k0 / 64) * 32 + part * 16);
+      s0 = s[k0 / 32];
+    }
   }
-  __device__ void store(_Float16 *Bs, int t) {
+  __device__ static void put16(const float *v, _Float16 *hi, _Float16 *lo) {
+    if (MODE == SPLIT3) {
+      half8 h0, l0, h1, l1;
+      split8(v, h0, l0);
+      split8(v + 8, h1, l1);
+      *reinterpret_cast<half8 *>(hi) = h0;
+      *reinterpret_cast<half8 *>(hi + 8) = h1;
+      *reinterpret_cast<half8 *>(lo) = l0;
+      *reinterpret_cast<half8 *>(lo + 8) = l1;
+    } else {
+      *reinterpret_cast<half8 *>(hi) = cvt8(v);
+      *reinterpret_cast<half8 *>(hi + 8) = cvt8(v + 8);
+    }
+  }
+  template <int LDK>
+  __device__ void store(_Float16 *Bs, _Float16 *Bl, float *, int t) {
     const int r = t / 2, part = t % 2;
     const uint32_t w[4] = {c.x, c.y, c.z, c.w};
-    half8 lo0, lo1, hi0, hi1;
+    float lo[16], hi[16];
+    if (BK == 64) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const uint32_t byte = (w[j / 4] >> (8 * (j % 4))) & 0xffu;
-      const float l = s0.x * float(byte & 15u) - s0.y;
-      const float h = s1.x * float(byte >> 4) - s1.y;
-      if (j < 8) { lo0[j] = _Float16(l); hi0[j] = _Float16(h); }
-      else { lo1[j - 8] = _Float16(l); hi1[j - 8] = _Float16(h); }
+      for (int j = 0; j < 16; ++j) {
+        const uint32_t byte = (w[j / 4] >> (8 * (j % 4))) & 0xffu;
+        lo[j] = s0.x * float(byte & 15u) - s0.y;
+        hi[j] = s1.x * float(byte >> 4) - s1.y;
+      }
+      put16(lo, Bs + r * LDK + part * 16, Bl + r * LDK + part * 16);
+      put16(hi, Bs + r * LDK + 32 + part * 16, Bl + r * LDK + 32 + part * 16);
+    } else {  // one nibble plane, chosen by the tile's position in its 64-element group
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const uint32_t byte = (w[j / 4] >> (8 * (j % 4))) & 0xffu;
+        lo[j] = s0.x * float(plane_ ? (byte >> 4) : (byte & 15u)) - s0.y;
+      }
+      put16(lo, Bs + r * LDK + part * 16, Bl + r * LDK + part * 16);
     }
-    _Float16 *row = Bs + r * LDK;
-    *reinterpret_cast<half8 *>(row + part * 16) = lo0;
-    *reinterpret_cast<half8 *>(row + part * 16 + 8) = lo1;
-    *reinterpret_cast<half8 *>(row + 32 + part * 16) = hi0;
-    *reinterpret_cast<half8 *>(row + 32 + part * 16 + 8) = hi1;
   }
-  __device__ static int row_of(int t, int) { return t / 2; }
-  static constexpr int kRows = 1;
+  int plane_ = 0;
 };
 
-template <>
-struct BLoad<LG_Q6_K> {
-  uint4 c0, c1;
-  float a0, a1;
+// Q6_K: w = (d*sc)*(q-32) per 16-element sub-block; codes stored as (q-32).
+template <int MODE, int BK>
+struct BLoad<LG_Q6_K, MODE, BK> {
+  static constexpr int kRows = 1;
+  static constexpr int kCodes = BK / 2;  // codes per thread
+  uint4 c[kCodes / 16];
+  float a[kCodes / 16];
+  __device__ static int row_of(int t, int) { return t / 2; }
   __device__ void fetch(const DevMatrix &W, const int *wrow, int k0, int t) {
     const int part = t % 2;
-    const int8_t *q = static_cast<const int8_t *>(W.q) + int64_t(wrow[0]) * W.cols + k0 + part * 32;
-    c0 = *reinterpret_cast<const uint4 *>(q);
-    c1 = *reinterpret_cast<const uint4 *>(q + 16);
-    const float *s = static_cast<const float *>(W.s) + int64_t(wrow[0]) * (W.cols / 16) + (k0 + part * 32) / 16;
-    a0 = s[0];
-    a1 = s[1];
-  }
-  __device__ static void cvt16(uint4 c, float a, _Float16 *dst) {
-    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
-    half8 o0, o1;
+    const int8_t *q = static_cast<const int8_t *>(W.q) + int64_t(wrow[0]) * W.cols + k0 + part * kCodes;
+    const float *s = static_cast<const float *>(W.s) + int64_t(wrow[0]) * (W.cols / 16) + (k0 + part * kCodes) / 16;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const float v = a * float(int8_t(w[j / 4] >> (8 * (j % 4))));
-      if (j < 8) o0[j] = _Float16(v); else o1[j - 8] = _Float16(v);
+    for (int i = 0; i < kCodes / 16; ++i) {
+      c[i] = *reinterpret_cast<const uint4 *>(q + 16 * i);
+      a[i] = s[i];
     }
-    *reinterpret_cast<half8 *>(dst) = o0;
-    *reinterpret_cast<half8 *>(dst + 8) = o1;
   }
-  __device__ void store(_Float16 *Bs, int t) {
+  template <int LDK>
+  __device__ void store(_Float16 *Bs, _Float16 *Bl, float *, int t) {
     const int r = t / 2, part = t % 2;
-    cvt16(c0, a0, Bs + r * LDK + part * 32);
-    cvt16(c1, a1, Bs + r * LDK + part * 32 + 16);
+#pragma unroll
+    for (int i = 0; i < kCodes / 16; ++i) {
+      const uint32_t w[4] = {c[i].x, c[i].y, c[i].z, c[i].w};
+      float v[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = a[i] * float(int8_t(w[j / 4] >> (8 * (j % 4))));
+      _Float16 *hi = Bs + r * LDK + part * kCodes + 16 * i;
+      _Float16 *lo = Bl + r * LDK + part * kCodes + 16 * i;
+      if (MODE == SPLIT3) {
+        half8 h0, l0, h1, l1;
+        split8(v, h0, l0);
+        split8(v + 8, h1, l1);
+        *reinterpret_cast<half8 *>(hi) = h0;
+        *reinterpret_cast<half8 *>(hi + 8) = h1;
+        *reinterpret_cast<half8 *>(lo) = l0;
+        *reinterpret_cast<half8 *>(lo + 8) = l1;
+      } else {
+        *reinterpret_cast<half8 *>(hi) = cvt8(v);
+        *reinterpret_cast<half8 *>(hi + 8) = cvt8(v + 8);
+      }
+    }
   }
-  __device__ static int row_of(int t, int) { return t / 2; }
-  static constexpr int kRows = 1;
 };
 
 // Tile order: the hardware hands consecutive workgroups to the 8 XCDs round-robin; give
@@ -171,22 +238,32 @@ __device__ __forceinline__ void tile_coords(int bid, int nblk, int MT, int NT, i
   nt = in / gm;
 }
 
-template <uint32_t KIND, int EPI>
-__global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ A, int M, int K,
+#define MFMA(a, b, c) __builtin_amdgcn_mfma_f32_32x32x16_f16((a), (b), (c), 0, 0, 0)
+
+template <uint32_t KIND, int EPI, int MODE, int BK>
+__global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ A,
+                                                   const _Float16 *__restrict__ Alo, int M, int K,
                                                    DevMatrix W, float *__restrict__ C,
-                                                   _Float16 *__restrict__ C16, int ldc,
+                                                   _Float16 *__restrict__ C16,
+                                                   _Float16 *__restrict__ C16lo, int ldc,
                                                    const float *__restrict__ bias, int MT, int NT,
                                                    int ffn) {
+  constexpr int LDK = BK + 8;  // 16-byte row pad: conflict-free b128 LDS reads
+  constexpr bool kSplitA = MODE != FAST;
+  constexpr bool kSplitB = MODE == SPLIT3;
+  constexpr bool kScaled = MODE == SPLIT && KIND == LG_Q8_0;
   __shared__ __attribute__((aligned(16))) _Float16 As[BM * LDK];
+  __shared__ __attribute__((aligned(16))) _Float16 Al[kSplitA ? BM * LDK : 8];
   __shared__ __attribute__((aligned(16))) _Float16 Bs[BN * LDK];
+  __shared__ __attribute__((aligned(16))) _Float16 Bl[kSplitB ? BN * LDK : 8];
+  __shared__ float Ds[kScaled ? BN * 2 : 1];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   int mt, nt;
   tile_coords(blockIdx.x, gridDim.x, MT, NT, mt, nt);
   const int m0 = mt * BM;
 
-  // weight rows this thread loads
-  using BL = BLoad<KIND>;
+  using BL = BLoad<KIND, MODE, BK>;
   int wrow[BL::kRows];
 #pragma unroll
   for (int i = 0; i < BL::kRows; ++i) {
@@ -199,11 +276,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
     }
   }
   // activation rows this thread loads (clamped; rows >= M are never stored)
-  const _Float16 *arow[4];
+  constexpr int kAPer = BM * BK / 8 / 256;
+  int64_t aoff[kAPer];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = min(m0 + t / 8 + 32 * i, M - 1);
-    arow[i] = A + int64_t(r) * K + (t % 8) * 8;
+  for (int i = 0; i < kAPer; ++i) {
+    const int idx = t + 256 * i;
+    const int r = min(m0 + idx / (BK / 8), M - 1);
+    aoff[i] = int64_t(r) * K + (idx % (BK / 8)) * 8;
   }
 
   f32x16 acc[2][2];
@@ -214,37 +293,107 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  uint4 av[4];
+  uint4 av[kAPer], avl[kSplitA ? kAPer : 1];
   BL bl;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) av[i] = *reinterpret_cast<const uint4 *>(arow[i]);
+  for (int i = 0; i < kAPer; ++i) {
+    av[i] = *reinterpret_cast<const uint4 *>(A + aoff[i]);
+    if (kSplitA) avl[i] = *reinterpret_cast<const uint4 *>(Alo + aoff[i]);
+  }
   bl.fetch(W, wrow, 0, t);
+  if constexpr (KIND == LG_Q4_K && BK == 32) bl.plane_ = 0;
 
   const int nk = K / BK;
   for (int kt = 0; kt < nk; ++kt) {
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<uint4 *>(As + (t / 8 + 32 * i) * LDK + (t % 8) * 8) = av[i];
-    bl.store(Bs, t);
+    for (int i = 0; i < kAPer; ++i) {
+      const int idx = t + 256 * i, r = idx / (BK / 8), c = (idx % (BK / 8)) * 8;
+      *reinterpret_cast<uint4 *>(As + r * LDK + c) = av[i];
+      if (kSplitA) *reinterpret_cast<uint4 *>(Al + r * LDK + c) = avl[i];
+    }
+    bl.template store<LDK>(Bs, Bl, Ds, t);
     __syncthreads();
     if (kt + 1 < nk) {
       const int k1 = (kt + 1) * BK;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = *reinterpret_cast<const uint4 *>(arow[i] + k1);
+      for (int i = 0; i < kAPer; ++i) {
+        av[i] = *reinterpret_cast<const uint4 *>(A + aoff[i] + k1);
+        if (kSplitA) avl[i] = *reinterpret_cast<const uint4 *>(Alo + aoff[i] + k1);
+      }
       bl.fetch(W, wrow, k1, t);
+      if constexpr (KIND == LG_Q4_K && BK == 32) bl.plane_ = (k1 % 64) >= 32;
     }
+    const int ar0 = (wm * 64 + (lane & 31)) * LDK, ar1 = ar0 + 32 * LDK;
+    const int br0 = (wn * 64 + (lane & 31)) * LDK, br1 = br0 + 32 * LDK;
+    if constexpr (kScaled) {
+      // two Q8_0 blocks per tile: partial sums over each block, then acc += d * partial
 #pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      const int kc = kk * 16 + (lane >> 5) * 8;
-      const half8 a0 = *reinterpret_cast<const half8 *>(As + (wm * 64 + (lane & 31)) * LDK + kc);
-      const half8 a1 = *reinterpret_cast<const half8 *>(As + (wm * 64 + 32 + (lane & 31)) * LDK + kc);
-      const half8 b0 = *reinterpret_cast<const half8 *>(Bs + (wn * 64 + (lane & 31)) * LDK + kc);
-      const half8 b1 = *reinterpret_cast<const half8 *>(Bs + (wn * 64 + 32 + (lane & 31)) * LDK + kc);
-      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, acc[0][0], 0, 0, 0);
-      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b1, acc[0][1], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b0, acc[1][0], 0, 0, 0);
-      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b1, acc[1][1], 0, 0, 0);
+      for (int blk = 0; blk < 2; ++blk) {
+        f32x16 p[2][2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) p[i][j][r] = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const int kc = blk * 32 + kk * 16 + (lane >> 5) * 8;
+          const half8 a0 = *reinterpret_cast<const half8 *>(As + ar0 + kc);
+          const half8 a1 = *reinterpret_cast<const half8 *>(As + ar1 + kc);
+          const half8 l0 = *reinterpret_cast<const half8 *>(Al + ar0 + kc);
+          const half8 l1 = *reinterpret_cast<const half8 *>(Al + ar1 + kc);
+          const half8 b0 = *reinterpret_cast<const half8 *>(Bs + br0 + kc);
+          const half8 b1 = *reinterpret_cast<const half8 *>(Bs + br1 + kc);
+          p[0][0] = MFMA(a0, b0, p[0][0]);
+          p[0][1] = MFMA(a0, b1, p[0][1]);
+          p[1][0] = MFMA(a1, b0, p[1][0]);
+          p[1][1] = MFMA(a1, b1, p[1][1]);
+          p[0][0] = MFMA(l0, b0, p[0][0]);
+          p[0][1] = MFMA(l0, b1, p[0][1]);
+          p[1][0] = MFMA(l1, b0, p[1][0]);
+          p[1][1] = MFMA(l1, b1, p[1][1]);
+        }
+        const float d0 = Ds[(wn * 64 + (lane & 31)) * 2 + blk];
+        const float d1 = Ds[(wn * 64 + 32 + (lane & 31)) * 2 + blk];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            acc[i][0][r] += d0 * p[i][0][r];
+            acc[i][1][r] += d1 * p[i][1][r];
+          }
+      }
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < BK / 16; ++kk) {
+        const int kc = kk * 16 + (lane >> 5) * 8;
+        const half8 a0 = *reinterpret_cast<const half8 *>(As + ar0 + kc);
+        const half8 a1 = *reinterpret_cast<const half8 *>(As + ar1 + kc);
+        const half8 b0 = *reinterpret_cast<const half8 *>(Bs + br0 + kc);
+        const half8 b1 = *reinterpret_cast<const half8 *>(Bs + br1 + kc);
+        acc[0][0] = MFMA(a0, b0, acc[0][0]);
+        acc[0][1] = MFMA(a0, b1, acc[0][1]);
+        acc[1][0] = MFMA(a1, b0, acc[1][0]);
+        acc[1][1] = MFMA(a1, b1, acc[1][1]);
+        if constexpr (kSplitA) {
+          const half8 l0 = *reinterpret_cast<const half8 *>(Al + ar0 + kc);
+          const half8 l1 = *reinterpret_cast<const half8 *>(Al + ar1 + kc);
+          acc[0][0] = MFMA(l0, b0, acc[0][0]);
+          acc[0][1] = MFMA(l0, b1, acc[0][1]);
+          acc[1][0] = MFMA(l1, b0, acc[1][0]);
+          acc[1][1] = MFMA(l1, b1, acc[1][1]);
+        }
+        if constexpr (kSplitB) {
+          const half8 c0 = *reinterpret_cast<const half8 *>(Bl + br0 + kc);
+          const half8 c1 = *reinterpret_cast<const half8 *>(Bl + br1 + kc);
+          acc[0][0] = MFMA(a0, c0, acc[0][0]);
+          acc[0][1] = MFMA(a0, c1, acc[0][1]);
+          acc[1][0] = MFMA(a1, c0, acc[1][0]);
+          acc[1][1] = MFMA(a1, c1, acc[1][1]);
+        }
+      }
     }
   }
 
@@ -258,7 +407,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
       if (row >= M) continue;
       if (EPI == int(Epi::SWIGLU)) {
         const int col = nt * 64 + wn * 32 + col_in;
-        C16[int64_t(row) * ldc + col] = _Float16(silu(acc[i][0][r]) * acc[i][1][r]);
+        const float v = silu(acc[i][0][r]) * acc[i][1][r];
+        const _Float16 h = _Float16(v);
+        C16[int64_t(row) * ldc + col] = h;
+        if (C16lo) C16lo[int64_t(row) * ldc + col] = _Float16(v - float(h));
       } else {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -271,7 +423,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
             C[int64_t(row) * ldc + col] += v;
           } else {
             if (bias) v += bias[col];
-            C16[int64_t(row) * ldc + col] = _Float16(v);
+            const _Float16 h = _Float16(v);
+            C16[int64_t(row) * ldc + col] = h;
+            if (C16lo) C16lo[int64_t(row) * ldc + col] = _Float16(v - float(h));
           }
         }
       }
@@ -279,24 +433,34 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
   }
 }
 
-template <uint32_t KIND>
-void launch_kind(const _Float16 *A, int M, const DevMatrix &W, Epi epi, float *C, _Float16 *C16,
-                 int ldc, const float *bias, int MT, int NT, hipStream_t st) {
+template <uint32_t KIND, int MODE, int BK>
+void launch_mode(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
+                 _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, int MT, int NT,
+                 hipStream_t st) {
   const dim3 grid(MT * NT), block(256);
   const int K = W.cols, ffn = W.rows / 2;
+#define LAUNCH(E)                                                                                   \
+  hipLaunchKernelGGL((gemm_kernel<KIND, E, MODE, BK>), grid, block, 0, st, A, Alo, M, K, W, C, C16, \
+                     C16lo, ldc, bias, MT, NT, ffn)
   switch (epi) {
-    case Epi::F32:
-      hipLaunchKernelGGL((gemm_kernel<KIND, 0>), grid, block, 0, st, A, M, K, W, C, C16, ldc, bias, MT, NT, ffn);
-      break;
-    case Epi::ADD:
-      hipLaunchKernelGGL((gemm_kernel<KIND, 1>), grid, block, 0, st, A, M, K, W, C, C16, ldc, bias, MT, NT, ffn);
-      break;
-    case Epi::F16:
-      hipLaunchKernelGGL((gemm_kernel<KIND, 2>), grid, block, 0, st, A, M, K, W, C, C16, ldc, bias, MT, NT, ffn);
-      break;
-    case Epi::SWIGLU:
-      hipLaunchKernelGGL((gemm_kernel<KIND, 3>), grid, block, 0, st, A, M, K, W, C, C16, ldc, bias, MT, NT, ffn);
-      break;
+    case Epi::F32: LAUNCH(0); break;
+    case Epi::ADD: LAUNCH(1); break;
+    case Epi::F16: LAUNCH(2); break;
+    case Epi::SWIGLU: LAUNCH(3); break;
+  }
+#undef LAUNCH
+}
+
+template <uint32_t KIND>
+void launch_kind(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
+                 _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, int MT, int NT,
+                 hipStream_t st) {
+  if (!Alo) {
+    launch_mode<KIND, FAST, 64>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, MT, NT, st);
+  } else if constexpr (KIND == LG_F16 || KIND == LG_Q8_0) {
+    launch_mode<KIND, SPLIT, 64>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, MT, NT, st);
+  } else {
+    launch_mode<KIND, SPLIT3, 32>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, MT, NT, st);
   }
 }
 
@@ -322,7 +486,7 @@ __device__ float weight_at(const DevMatrix &W, int64_t n, int64_t k) {
   return 0.0f;
 }
 
-// One wave per (row m, column n) pair group: lanes split K, wave-reduce.
+// One wave per (row m, column n) pair: lanes split K, wave-reduce.
 __global__ __launch_bounds__(256) void gemm_generic_kernel(const float *__restrict__ X, int M,
                                                            DevMatrix W,
                                                            const float *__restrict__ bias,
@@ -341,11 +505,10 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(const float *__restri
 
 }  // namespace
 
-void launch_gemm(const _Float16 *A, int M, const DevMatrix &W, Epi epi, float *C, _Float16 *C16,
-                 int ldc, const float *bias, hipStream_t st) {
+void launch_gemm(const _Float16 *A, const _Float16 *A_lo, int M, const DevMatrix &W, Epi epi, float *C,
+                 _Float16 *C16, _Float16 *C16_lo, int ldc, const float *bias, hipStream_t st) {
   LG_REQUIRE(M > 0, "gemm: empty activation");
-  if (W.cols % BK != 0)
-    fail(LG_ERR_UNSUPPORTED, "gemm: K=%d is not a multiple of %d", W.cols, BK);
+  if (W.cols % 64 != 0) fail(LG_ERR_UNSUPPORTED, "gemm: K=%d is not a multiple of 64", W.cols);
   if (W.kind == LG_Q4_K || W.kind == LG_Q6_K)
     LG_REQUIRE(W.cols % 256 == 0, "gemm: K-quant rows must be whole super-blocks");
   int NT;
@@ -362,10 +525,10 @@ void launch_gemm(const _Float16 *A, int M, const DevMatrix &W, Epi epi, float *C
   const int MT = (M + BM - 1) / BM;
   LG_REQUIRE(int64_t(MT) * NT < (1ll << 31), "gemm: grid too large");
   switch (W.kind) {
-    case LG_F16: launch_kind<LG_F16>(A, M, W, epi, C, C16, ldc, bias, MT, NT, st); break;
-    case LG_Q8_0: launch_kind<LG_Q8_0>(A, M, W, epi, C, C16, ldc, bias, MT, NT, st); break;
-    case LG_Q4_K: launch_kind<LG_Q4_K>(A, M, W, epi, C, C16, ldc, bias, MT, NT, st); break;
-    case LG_Q6_K: launch_kind<LG_Q6_K>(A, M, W, epi, C, C16, ldc, bias, MT, NT, st); break;
+    case LG_F16: launch_kind<LG_F16>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, MT, NT, st); break;
+    case LG_Q8_0: launch_kind<LG_Q8_0>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, MT, NT, st); break;
+    case LG_Q4_K: launch_kind<LG_Q4_K>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, MT, NT, st); break;
+    case LG_Q6_K: launch_kind<LG_Q6_K>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, MT, NT, st); break;
     default: fail(LG_ERR_UNSUPPORTED, "gemm: no MFMA path for GGML type %u", W.kind);
   }
   HIP_CHECK(hipGetLastError());

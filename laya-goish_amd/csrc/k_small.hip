@@ -34,14 +34,20 @@ __device__ float block_sum(float v, float *red) {
 template <typename Out>
 __global__ __launch_bounds__(kT) void rmsnorm_kernel(const float *__restrict__ x, int d,
                                                      const float *__restrict__ w, float eps,
-                                                     Out *__restrict__ y) {
+                                                     Out *__restrict__ y, Out *__restrict__ ylo) {
   __shared__ float red[kT / 64];
   const float *row = x + int64_t(blockIdx.x) * d;
   float ss = 0.0f;
   for (int k = threadIdx.x; k < d; k += kT) ss += row[k] * row[k];
   const float inv = 1.0f / sqrtf(block_sum(ss, red) / float(d) + eps);
   Out *out = y + int64_t(blockIdx.x) * d;
-  for (int k = threadIdx.x; k < d; k += kT) out[k] = Out(row[k] * inv * w[k]);
+  Out *lo = ylo ? ylo + int64_t(blockIdx.x) * d : nullptr;
+  for (int k = threadIdx.x; k < d; k += kT) {
+    const float v = row[k] * inv * w[k];
+    const Out h = Out(v);
+    out[k] = h;
+    if (lo) lo[k] = Out(v - float(h));
+  }
 }
 
 __global__ void embed_kernel(const void *__restrict__ table, uint32_t kind, const int32_t *__restrict__ ids,
@@ -56,16 +62,17 @@ __global__ void embed_kernel(const void *__restrict__ table, uint32_t kind, cons
 }
 
 // One workgroup per token row.  Rotate-half RoPE with the model's tables
-// (src/tensor.rs:158-172), then q -> q16/q32, k -> K page row, v -> V page column.
+// (src/tensor.rs:158-172), then q -> q16 (+lo plane) / q32, k -> K page row, v -> V page column.
+template <typename KV>
 __global__ __launch_bounds__(kT) void rope_kv_kernel(const float *__restrict__ qkv, int hq, KvGeom g,
                                                      const float *__restrict__ cosT,
                                                      const float *__restrict__ sinT,
                                                      const int32_t *__restrict__ tok_seq,
                                                      const int32_t *__restrict__ tok_pos,
                                                      const int32_t *__restrict__ pages, int max_pages,
-                                                     _Float16 *__restrict__ q16, float *__restrict__ q32,
-                                                     _Float16 *__restrict__ kpool,
-                                                     _Float16 *__restrict__ vpool) {
+                                                     _Float16 *__restrict__ q16, _Float16 *__restrict__ q16lo,
+                                                     float *__restrict__ q32, KV *__restrict__ kpool,
+                                                     KV *__restrict__ vpool) {
   const int t = blockIdx.x;
   const int hd = g.hd, half = hd / 2;
   const int qw = hq * hd, kvw = g.hkv * hd;
@@ -74,36 +81,35 @@ __global__ __launch_bounds__(kT) void rope_kv_kernel(const float *__restrict__ q
   const int page = pages[int64_t(tok_seq[t]) * max_pages + pos / g.page_tokens];
   const int slot = pos % g.page_tokens;
   const float *cs = cosT + int64_t(pos) * hd, *sn = sinT + int64_t(pos) * hd;
-  // q
+  auto putq = [&](int64_t i, float v) {
+    if (q16) {
+      const _Float16 h = _Float16(v);
+      q16[i] = h;
+      if (q16lo) q16lo[i] = _Float16(v - float(h));
+    } else {
+      q32[i] = v;
+    }
+  };
   for (int i = threadIdx.x; i < hq * half; i += kT) {
     const int h = i / half, j = i % half;
     const float u = row[h * hd + j], v = row[h * hd + j + half];
-    const float a = u * cs[j] - v * sn[j];
-    const float b = v * cs[j + half] + u * sn[j + half];
-    if (q16) {
-      q16[int64_t(t) * qw + h * hd + j] = _Float16(a);
-      q16[int64_t(t) * qw + h * hd + j + half] = _Float16(b);
-    } else {
-      q32[int64_t(t) * qw + h * hd + j] = a;
-      q32[int64_t(t) * qw + h * hd + j + half] = b;
-    }
+    putq(int64_t(t) * qw + h * hd + j, u * cs[j] - v * sn[j]);
+    putq(int64_t(t) * qw + h * hd + j + half, v * cs[j + half] + u * sn[j + half]);
   }
-  _Float16 *kp = kpool + int64_t(page) * g.page_stride;
-  _Float16 *vp = vpool + int64_t(page) * g.page_stride;
+  KV *kp = kpool + int64_t(page) * g.page_stride;
+  KV *vp = vpool + int64_t(page) * g.page_stride;
   // k -> page rows [hkv][page_tokens][hd]
   for (int i = threadIdx.x; i < g.hkv * half; i += kT) {
     const int h = i / half, j = i % half;
     const float u = row[qw + h * hd + j], v = row[qw + h * hd + j + half];
-    const float a = u * cs[j] - v * sn[j];
-    const float b = v * cs[j + half] + u * sn[j + half];
-    _Float16 *dst = kp + (int64_t(h) * g.page_tokens + slot) * hd;
-    dst[j] = _Float16(a);
-    dst[j + half] = _Float16(b);
+    KV *dst = kp + (int64_t(h) * g.page_tokens + slot) * hd;
+    dst[j] = KV(u * cs[j] - v * sn[j]);
+    dst[j + half] = KV(v * cs[j + half] + u * sn[j + half]);
   }
   // v -> page columns [hkv][hd][page_tokens]
   for (int i = threadIdx.x; i < kvw; i += kT) {
     const int h = i / hd, dd = i % hd;
-    vp[(int64_t(h) * hd + dd) * g.page_tokens + slot] = _Float16(row[qw + kvw + i]);
+    vp[(int64_t(h) * hd + dd) * g.page_tokens + slot] = KV(row[qw + kvw + i]);
   }
 }
 
@@ -245,9 +251,13 @@ __global__ __launch_bounds__(64) void argmax_stage2(const float *__restrict__ pv
   out[0] = bi < 0 ? 0 : bi;
 }
 
-__global__ void cvt_f16_kernel(const float *__restrict__ x, int64_t n, _Float16 *__restrict__ y) {
+__global__ void cvt_f16_kernel(const float *__restrict__ x, int64_t n, _Float16 *__restrict__ y,
+                               _Float16 *__restrict__ ylo) {
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) y[i] = _Float16(x[i]);
+  if (i >= n) return;
+  const _Float16 h = _Float16(x[i]);
+  y[i] = h;
+  if (ylo) ylo[i] = _Float16(x[i] - float(h));
 }
 
 __global__ void fill_i32_kernel(int32_t *p, int n, int32_t v) {
@@ -258,16 +268,17 @@ __global__ void fill_i32_kernel(int32_t *p, int n, int32_t v) {
 }  // namespace
 
 void launch_rmsnorm_f16(const float *x, int rows, int d, const float *w, float eps, _Float16 *y,
-                        hipStream_t st) {
+                        _Float16 *y_lo, hipStream_t st) {
   LG_REQUIRE(rows > 0 && d > 0, "rmsnorm: empty");
-  hipLaunchKernelGGL(rmsnorm_kernel<_Float16>, dim3(rows), dim3(kT), 0, st, x, d, w, eps, y);
+  hipLaunchKernelGGL(rmsnorm_kernel<_Float16>, dim3(rows), dim3(kT), 0, st, x, d, w, eps, y, y_lo);
   HIP_CHECK(hipGetLastError());
 }
 
 void launch_rmsnorm_f32(const float *x, int rows, int d, const float *w, float eps, float *y,
                         hipStream_t st) {
   LG_REQUIRE(rows > 0 && d > 0, "rmsnorm: empty");
-  hipLaunchKernelGGL(rmsnorm_kernel<float>, dim3(rows), dim3(kT), 0, st, x, d, w, eps, y);
+  hipLaunchKernelGGL(rmsnorm_kernel<float>, dim3(rows), dim3(kT), 0, st, x, d, w, eps, y,
+                     static_cast<float *>(nullptr));
   HIP_CHECK(hipGetLastError());
 }
 
@@ -283,11 +294,17 @@ void launch_embed(const void *table, uint32_t kind, const int32_t *ids, int T, i
 
 void launch_rope_kv(const float *qkv, int T, int hq, const KvGeom &g, const float *cosT,
                     const float *sinT, const int32_t *tok_seq, const int32_t *tok_pos,
-                    const int32_t *pages, int max_pages, _Float16 *q16, float *q32,
-                    _Float16 *kpool, _Float16 *vpool, hipStream_t st) {
+                    const int32_t *pages, int max_pages, _Float16 *q16, _Float16 *q16_lo,
+                    float *q32, void *kpool, void *vpool, hipStream_t st) {
   LG_REQUIRE(T > 0 && g.hd % 2 == 0 && (q16 || q32), "rope_kv: bad arguments");
-  hipLaunchKernelGGL(rope_kv_kernel, dim3(T), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, tok_seq, tok_pos,
-                     pages, max_pages, q16, q32, kpool, vpool);
+  if (g.kv32)
+    hipLaunchKernelGGL(rope_kv_kernel<float>, dim3(T), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, tok_seq,
+                       tok_pos, pages, max_pages, q16, q16_lo, q32, static_cast<float *>(kpool),
+                       static_cast<float *>(vpool));
+  else
+    hipLaunchKernelGGL(rope_kv_kernel<_Float16>, dim3(T), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, tok_seq,
+                       tok_pos, pages, max_pages, q16, q16_lo, q32, static_cast<_Float16 *>(kpool),
+                       static_cast<_Float16 *>(vpool));
   HIP_CHECK(hipGetLastError());
 }
 
@@ -318,9 +335,9 @@ void launch_argmax(const float *logits, int V, int32_t *out, float *part_v, int3
   HIP_CHECK(hipGetLastError());
 }
 
-void launch_cvt_f16(const float *x, int64_t n, _Float16 *y, hipStream_t st) {
+void launch_cvt_f16(const float *x, int64_t n, _Float16 *y, _Float16 *y_lo, hipStream_t st) {
   LG_REQUIRE(n > 0 && n / 256 < (1ll << 31), "cvt_f16: bad size");
-  hipLaunchKernelGGL(cvt_f16_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, x, n, y);
+  hipLaunchKernelGGL(cvt_f16_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, x, n, y, y_lo);
   HIP_CHECK(hipGetLastError());
 }
 

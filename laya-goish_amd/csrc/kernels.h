@@ -43,9 +43,12 @@ void launch_repack(uint32_t kind, const uint8_t *src, int rows, int cols, DevMat
                    hipStream_t st);
 
 // Prefill GEMM: out = A[M][K] (half, row-major, lda = K) . W^T with epilogue `epi`.
+// A_lo == nullptr: one f16 pass.  A_lo != nullptr: A = A + A_lo (hi/lo f16 planes) and the
+// weights are applied exactly (split-precision MFMA, f32-faithful).  f16 outputs (Epi::F16,
+// Epi::SWIGLU) are written as hi/lo planes when C16_lo != nullptr.
 // For Epi::SWIGLU the output has W.rows/2 columns.
-void launch_gemm(const _Float16 *A, int M, const DevMatrix &W, Epi epi, float *C, _Float16 *C16,
-                 int ldc, const float *bias, hipStream_t st);
+void launch_gemm(const _Float16 *A, const _Float16 *A_lo, int M, const DevMatrix &W, Epi epi, float *C,
+                 _Float16 *C16, _Float16 *C16_lo, int ldc, const float *bias, hipStream_t st);
 
 // Generic f32 GEMM for shapes the tiled kernel does not take (any M, N, K), F32/F16/Q weights.
 void launch_gemm_generic(const float *X, int M, const DevMatrix &W, const float *bias, float *Y,
@@ -58,8 +61,9 @@ void launch_gemv(const float *x, const DevMatrix &W, Epi epi, float *y, const fl
                  const float *norm_w, float eps, hipStream_t st);
 
 // Row RMSNorm: y = x * (1/sqrt(dot(x,x)/d + eps)) * w   (src/models/openthai/model.rs:84-94)
+// written as f16 (y) or as hi/lo f16 planes (y, y_lo) when y_lo != nullptr.
 void launch_rmsnorm_f16(const float *x, int rows, int d, const float *w, float eps, _Float16 *y,
-                        hipStream_t st);
+                        _Float16 *y_lo, hipStream_t st);
 void launch_rmsnorm_f32(const float *x, int rows, int d, const float *w, float eps, float *y,
                         hipStream_t st);
 
@@ -71,33 +75,38 @@ void launch_embed(const void *table, uint32_t kind, const int32_t *ids, int T, i
 struct KvGeom {
   int page_tokens = 64;  // tokens per page
   int hkv = 0, hd = 0;
+  int kv32 = 0;              // element type of the pools: 0 = f16, 1 = f32
   int64_t layer_stride = 0;  // halves between layers of the K (or V) pool
   int64_t page_stride = 0;   // halves per page of one layer: hkv * page_tokens * hd
 };
 
-// RoPE on q and k of qkv[T][(hq+2hkv)*hd] (f32) with tables cos/sin[ctx][hd]; writes
-// q16[T][hq*hd] and the K page rows [hkv][page_tokens][hd] and V page columns
-// [hkv][hd][page_tokens] of layer pools kpool/vpool.  tok_seq/tok_pos give each row's
-// sequence and position; pages[seq * max_pages + pos / page_tokens] its page.
+// RoPE on q and k of qkv[T][(hq+2hkv)*hd] (f32) with tables cos/sin[ctx][hd]; writes q as
+// f16 (q16), hi/lo f16 planes (q16, q16_lo) or f32 (q32), and the K page rows
+// [hkv][page_tokens][hd] and V page columns [hkv][hd][page_tokens] of the layer pools
+// (element type per g.kv32).  tok_seq/tok_pos give each row's sequence and position;
+// pages[seq * max_pages + pos / page_tokens] its page.
 void launch_rope_kv(const float *qkv, int T, int hq, const KvGeom &g, const float *cosT,
                     const float *sinT, const int32_t *tok_seq, const int32_t *tok_pos,
-                    const int32_t *pages, int max_pages, _Float16 *q16, float *q32,
-                    _Float16 *kpool, _Float16 *vpool, hipStream_t st);
+                    const int32_t *pages, int max_pages, _Float16 *q16, _Float16 *q16_lo,
+                    float *q32, void *kpool, void *vpool, hipStream_t st);
 
-// Causal prefill attention over the paged F16 cache.  Work items: tiles of 32 query rows of
-// one sequence (tile_seq, tile_row0 = first batch row, tile_pos0 = its position, tile_n rows).
-void launch_attn_prefill(const _Float16 *q16, int T, int hq, const KvGeom &g,
-                         const _Float16 *kpool, const _Float16 *vpool, const int32_t *pages,
-                         int max_pages, const int32_t *tile_seq, const int32_t *tile_row0,
-                         const int32_t *tile_pos0, const int32_t *tile_n, int ntiles,
-                         _Float16 *out16, hipStream_t st);
+// Causal prefill attention over the paged cache.  Work items: tiles of 32 query rows of one
+// sequence (tile_seq, tile_row0 = first batch row, tile_pos0 = its position, tile_n rows).
+// q16_lo != nullptr selects the split-precision path (requires an f32 cache); the output is
+// then written as hi/lo planes (out16, out16_lo).
+void launch_attn_prefill(const _Float16 *q16, const _Float16 *q16_lo, int T, int hq,
+                         const KvGeom &g, const void *kpool, const void *vpool,
+                         const int32_t *pages, int max_pages, const int32_t *tile_seq,
+                         const int32_t *tile_row0, const int32_t *tile_pos0,
+                         const int32_t *tile_n, int ntiles, _Float16 *out16, _Float16 *out16_lo,
+                         hipStream_t st);
 
 // Decode attention: one query row per sequence (batch nseq), context length ctx_len[s]
-// (including the current token), split over chunks of keys, then combined.
-void launch_attn_decode(const float *q32, int nseq, int hq, const KvGeom &g,
-                        const _Float16 *kpool, const _Float16 *vpool, const int32_t *pages,
-                        int max_pages, const int32_t *ctx_len, int max_ctx, float *part,
-                        float *out, hipStream_t st);
+// (including the current token), split over pages, then combined.
+void launch_attn_decode(const float *q32, int nseq, int hq, const KvGeom &g, const void *kpool,
+                        const void *vpool, const int32_t *pages, int max_pages,
+                        const int32_t *ctx_len, int max_ctx, float *part, float *out,
+                        hipStream_t st);
 int64_t attn_decode_scratch_floats(int nseq, int hq, int hd, int max_ctx);
 
 // Gather rows, final RMSNorm and the option head: logits[r][j] = h_r . W[ids[j]].
@@ -113,8 +122,9 @@ void launch_option_scores(const float *logits, int R, int k, float temperature, 
 void launch_argmax(const float *logits, int V, int32_t *out, float *part_v, int32_t *part_i,
                    hipStream_t st);
 
-// f32 -> f16 (round to nearest even), n elements.
-void launch_cvt_f16(const float *x, int64_t n, _Float16 *y, hipStream_t st);
+// f32 -> f16 (round to nearest even), n elements; with y_lo, also the residual plane
+// y_lo = f16(x - y).
+void launch_cvt_f16(const float *x, int64_t n, _Float16 *y, _Float16 *y_lo, hipStream_t st);
 
 // f32 weights from the repacked layout of W, row-major [rows][cols] (bit-exact dequant).
 void launch_dequant_repacked(const DevMatrix &w, float *dst, hipStream_t st);

@@ -21,6 +21,7 @@ LIB_PATH = os.path.join(HERE, "liblaya_hip.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "lg.h")
 
 F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
+PREC_EXACT, PREC_FAST = 0, 1
 KIND_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
 ERR = {1: "INVALID", 2: "FORMAT", 3: "DEVICE", 4: "OOM", 5: "CANCELED", 6: "UNSUPPORTED"}
 
@@ -34,7 +35,8 @@ class LayaError(RuntimeError):
 
 class EngineOpts(ctypes.Structure):
     _fields_ = [("device", ctypes.c_int), ("kv_pages", ctypes.c_int),
-                ("kv_tokens", ctypes.c_int64), ("max_batch_tokens", ctypes.c_int64)]
+                ("kv_tokens", ctypes.c_int64), ("max_batch_tokens", ctypes.c_int64),
+                ("precision", ctypes.c_int)]
 
 
 class ModelInfo(ctypes.Structure):
@@ -42,7 +44,8 @@ class ModelInfo(ctypes.Structure):
                 ("layers", "d_model", "heads", "kv_heads", "head_dim", "ffn", "vocab", "context")] + \
                [("kind_attn", ctypes.c_uint32), ("kind_ffn", ctypes.c_uint32), ("kind_head", ctypes.c_uint32),
                 ("weight_bytes", ctypes.c_int64), ("kv_bytes", ctypes.c_int64),
-                ("kv_pages", ctypes.c_int), ("kv_page_tokens", ctypes.c_int)]
+                ("kv_pages", ctypes.c_int), ("kv_page_tokens", ctypes.c_int),
+                ("precision", ctypes.c_int), ("kv_elem_bytes", ctypes.c_int)]
 
     def asdict(self):
         return {n: getattr(self, n) for n, _ in self._fields_}
@@ -270,9 +273,9 @@ class Engine:
     """One model on one GPU (mirrors src/engine.rs Engine::new / layers / decide)."""
 
     def __init__(self, gguf: Gguf, device: int = 0, kv_tokens: int = 65536, max_batch_tokens: int = 65536,
-                 kv_pages: int = 0):
+                 kv_pages: int = 0, precision: int = PREC_EXACT):
         self.gguf = gguf
-        opts = EngineOpts(device, kv_pages, kv_tokens, max_batch_tokens)
+        opts = EngineOpts(device, kv_pages, kv_tokens, max_batch_tokens, precision)
         h = ctypes.c_void_p()
         check(lib().lg_engine_create(gguf.h, ctypes.byref(opts), ctypes.byref(h)))
         self.h = h

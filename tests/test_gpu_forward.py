@@ -16,12 +16,15 @@ pytestmark = pytest.mark.gpu
 OPTIONS = [3, 17, 42, 99]
 
 
-@pytest.fixture(scope="module", params=["tiny-f16", "tiny-q8", "tiny-q4k", "tiny-f16-128"])
+@pytest.fixture(scope="module", params=[("tiny-f16", 0), ("tiny-q8", 0), ("tiny-q4k", 0), ("tiny-f16-128", 0),
+                                        ("tiny-f16", 1), ("tiny-f16-128", 1)],
+                ids=lambda p: f"{p[0]}-{'exact' if p[1] == 0 else 'fast'}")
 def pair(request, lh, po):
-    img = lh.SynthImage(request.param, seed=5)
-    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=8192)
+    preset, prec = request.param
+    img = lh.SynthImage(preset, seed=5)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=8192, precision=prec)
     om = po.Model(po.Gguf(img.array()), threads=8)
-    yield request.param, eng, om
+    yield preset, eng, om
     eng.close()
 
 
@@ -163,10 +166,11 @@ def test_errors_are_reported(pair, lh):
     eng.seq_free(s)
 
 
-def test_plumbing_model_decision(lh, po):
+@pytest.mark.parametrize("prec", [0, 1], ids=["exact", "fast"])
+def test_plumbing_model_decision(lh, po, prec):
     """The CPU-runnable plumbing model: 128-token prompt + one yes/no question block."""
     img = lh.SynthImage("plumbing-f16", seed=1)
-    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=4096)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=4096, precision=prec)
     om = po.Model(po.Gguf(img.array()), threads=8)
     rng = np.random.default_rng(99)
     ids = np.concatenate([rng.integers(0, 32000, 128), rng.integers(0, 32000, 16)]).astype(np.int32)
@@ -179,4 +183,26 @@ def test_plumbing_model_decision(lh, po):
     assert_probs_close(probs[0], p_ref)
     assert int(np.argmax(probs[0])) == int(np.argmax(p_ref))
     print(f"plumbing: logit err {logit_error(logits, want):.2e} probs {probs[0]} ref {p_ref}")
+    eng.close()
+
+
+@pytest.mark.parametrize("layers,tokens", [(4, 400)])
+def test_q8_2048_full_width(lh, po, layers, tokens):
+    """The Q8_0 d2048 decoder at full width (reduced depth so the oracle finishes in seconds):
+    f32-faithful prefill against the oracle, 12 answer positions, 4 options each."""
+    img = lh.SynthImage("q8-2048", seed=3, n_layers=layers)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=4096)
+    om = po.Model(po.Gguf(img.array()), threads=16)
+    rng = np.random.default_rng(1)
+    ids = rng.integers(0, 32000, tokens).astype(np.int32)
+    pos = np.sort(rng.choice(tokens, 12, replace=False)).astype(np.int32)
+    opts = rng.choice(32000, 4, replace=False).astype(np.int32)
+    s = eng.seq_create()
+    logits, probs, _ = eng.batch([(s, ids, pos)]).run(opts)
+    want = om.forward(ids, pos, opts)
+    p_ref = np.stack([po.option_scores(w)[0] for w in want])
+    err = assert_logits_close(logits, want)
+    perr = assert_probs_close(probs, p_ref)
+    assert_argmax_equal(logits, want)
+    print(f"q8-2048 L{layers} T{tokens}: logit rel {err:.2e} prob {perr:.2e}")
     eng.close()
