@@ -176,6 +176,9 @@ void lg_batch_free(lg_engine *e, lg_batch *b);
 int lg_batch_run(lg_engine *e, lg_batch *b, const int32_t *option_ids, int k, float temperature,
                  float *logits, float *probs, float *logprobs, lg_cancel_fn cancel,
                  void *cancel_arg);
+/* Return every sequence of a batch that has run to its length at staging time (its pages
+ * stay reserved), so the same staged requests can be executed again. */
+int lg_batch_rewind(lg_engine *e, lg_batch *b);
 
 /* Greedy decode: feed `first` and then each argmax for `steps` single-token steps on `seq`
  * (which must hold its prefilled context).  tokens[steps] receives each step's argmax

@@ -329,6 +329,14 @@ int lg_batch_run(lg_engine *e, lg_batch *b, const int32_t *option_ids, int k, fl
   });
 }
 
+int lg_batch_rewind(lg_engine *e, lg_batch *b) {
+  return guard([&] {
+    NEED(e, "engine");
+    NEED(b, "batch");
+    e->e->batch_rewind(b->b);
+  });
+}
+
 int lg_decode(lg_engine *e, int seq, int32_t first, int steps, int32_t *tokens, float *logits) {
   return guard([&] {
     NEED(e, "engine");

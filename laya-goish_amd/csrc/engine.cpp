@@ -132,6 +132,7 @@ size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 struct BatchPlan {
   std::vector<int> seqs;        // engine sequence per request
   std::vector<int> n, npos;     // tokens and answer positions per request
+  std::vector<int> start_len;   // sequence length at staging time
   int T = 0, R = 0, ntiles = 0, max_pages = 0;
   DevBuf meta;                  // ids, tok_seq, tok_pos, pages, tiles..., gather rows
   int32_t *ids = nullptr, *tok_seq = nullptr, *tok_pos = nullptr, *pages = nullptr;
@@ -569,6 +570,7 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
       }
       for (int i = 0; i < q.npos; ++i) gather.push_back(row + q.positions[i]);
       b->seqs.push_back(q.seq);
+      b->start_len.push_back(s.len);
       b->n.push_back(q.n);
       b->npos.push_back(q.npos);
       row += q.n;
@@ -604,6 +606,17 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
 }
 
 void Engine::batch_free(BatchPlan *b) { delete b; }
+
+void Engine::batch_rewind(BatchPlan *b) {
+  LG_REQUIRE(b, "batch: null");
+  for (size_t r = 0; r < b->seqs.size(); ++r) {
+    Seq &s = seq(b->seqs[r]);
+    if (b->ran && s.len != b->start_len[r] + b->n[r])
+      fail(LG_ERR_INVALID, "batch: sequence %d changed since the batch ran", b->seqs[r]);
+    s.len = b->start_len[r];
+  }
+  b->ran = false;
+}
 
 void Engine::run_layers_prefill(BatchPlan &b, lg_cancel_fn cancel, void *arg) {
   const int T = b.T, qw = hq * hd, kvw = hkv * hd, qkvw = qw + 2 * kvw;

@@ -85,6 +85,7 @@ class Engine {
 
   BatchPlan *batch_create(const lg_request *reqs, int nreq);
   void batch_free(BatchPlan *b);
+  void batch_rewind(BatchPlan *b);
   void batch_run(BatchPlan *b, const int32_t *option_ids, int k, float temperature, float *logits,
                  float *probs, float *logprobs, lg_cancel_fn cancel, void *arg);
   // Single-sequence forward with host ids; vocab_ids == nullptr -> full vocabulary.

@@ -101,6 +101,7 @@ def lib() -> ctypes.CDLL:
             "lg_batch_create": (I, [P, ctypes.POINTER(Request), I, ctypes.POINTER(P)]),
             "lg_batch_free": (None, [P, P]),
             "lg_batch_run": (I, [P, P, P, I, F, P, P, P, CANCEL_FN, P]),
+            "lg_batch_rewind": (I, [P, P]),
             "lg_decode": (I, [P, I, ctypes.c_int32, I, P, P]),
             "lg_option_scores": (I, [P, I, F, P, P]),
             "lg_profile_enable": (I, [P, I]),
@@ -257,6 +258,9 @@ class Batch:
         check(lib().lg_batch_run(self.engine.h, self.h, _ptr(ids), k, temperature,
                                  *(_ptr(o) for o in out), cb, None))
         return tuple(out)
+
+    def rewind(self):
+        check(lib().lg_batch_rewind(self.engine.h, self.h))
 
     def free(self):
         if self.h:
