@@ -1,7 +1,7 @@
 // Prefill GEMM for gfx950: C = A . W^T on MFMA v_mfma_f32_32x32x16_f16, f32 accumulation,
 // weights dequantised into LDS, epilogue fused (bias, residual add, SwiGLU, f16 store).
 //
-// Three numeric modes (selected by the caller):
+// Numeric modes (selected by the caller):
 //   FAST  : A in f16, W dequantised to f16 (RNE); one MFMA pass.
 //   SPLIT : A given as two f16 planes (hi = f16(a), lo = f16(a - hi)), so A carries ~22
 //           significand bits.  F16 weights are exact in f16 -> 2 passes (hi, lo).
@@ -12,9 +12,10 @@
 // The split modes reproduce f32 arithmetic to ~2^-22 relative per product, which the
 // ill-conditioned synthetic workloads need to stay within the parity bars.
 //
-// Tile 128 x 128 x BK, 256 threads = 4 wave64s in a 2 x 2 arrangement, each wave a 64 x 64
-// sub-tile = 2 x 2 MFMA blocks of 32 x 32.  Global loads for the next K tile are issued
-// before the MFMAs of the current one (register double buffering).
+// Geometry: 256 threads = 4 wave64s in a 2 x 2 arrangement; each wave owns WTM x WTN MFMA
+// blocks of 32 x 32, so a workgroup tile is (64 WTM) x (64 WTN) x BK.  STAGES = 2 ping-pongs
+// two LDS buffers (one barrier per K step, next tile's global loads in flight during the
+// MFMAs); STAGES = 1 uses one buffer with the next tile prefetched into registers.
 #include <hip/hip_runtime.h>
 
 #include "common.h"
@@ -27,197 +28,131 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128, BN = 128;
 enum Mode { FAST = 0, SPLIT = 1, SPLIT3 = 2 };
 
 __device__ __forceinline__ float silu(float g) { return g * (1.0f / (1.0f + __expf(-g))); }
 
-__device__ __forceinline__ half8 cvt8(const float *v) {
-  half8 h;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) h[j] = _Float16(v[j]);
-  return h;
-}
-// hi/lo split of 8 floats
-__device__ __forceinline__ void split8(const float *v, half8 &hi, half8 &lo) {
+__device__ __forceinline__ void put8(const float *v, _Float16 *hi, _Float16 *lo, bool split) {
+  half8 h, l;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const _Float16 h = _Float16(v[j]);
-    hi[j] = h;
-    lo[j] = _Float16(v[j] - float(h));
+    h[j] = _Float16(v[j]);
+    l[j] = _Float16(v[j] - float(h[j]));
   }
+  *reinterpret_cast<half8 *>(hi) = h;
+  if (split) *reinterpret_cast<half8 *>(lo) = l;
 }
 
 // ---------------------------------------------------------------- B tile loaders
-// fetch(): global -> registers for this thread's share of a BN x BK tile.
-// store(): registers -> LDS rows (stride LDK halves), dequantised per mode.
-template <uint32_t KIND, int MODE, int BK>
-struct BLoad;
+// A BNT x BK weight tile is cut into 16-byte chunks; thread t handles chunks t + 256 i.
+// fetch(): global -> registers;  store(): registers -> LDS rows (stride LDK), dequantised.
+// wrow(r) maps a local tile row to its weight row.
+template <uint32_t KIND, int MODE, int BK, int BNT>
+struct BLoad {
+  // elements of the K dimension covered by one chunk
+  static constexpr int kElems = KIND == LG_F16 ? 8 : (KIND == LG_Q4_K && BK == 64) ? 32 : 16;
+  static constexpr int kCPR = BK / kElems;            // chunks per row
+  static constexpr int kPer = BNT * kCPR / 256;        // chunks per thread
+  static_assert(kPer >= 1 && BNT * kCPR % 256 == 0, "tile does not split over 256 threads");
+  static constexpr bool kQ4 = KIND == LG_Q4_K;
+  // register storage as ext_vectors (arrays of a struct tend to be placed in scratch)
+  typedef uint32_t uvec __attribute__((ext_vector_type(4 * kPer)));
+  typedef float fvec __attribute__((ext_vector_type(kPer)));
+  typedef uint32_t rvec __attribute__((ext_vector_type(kPer)));
+  uvec v;
+  fvec sa, sb;    // scale terms of the chunk (low plane)
+  fvec sa2, sb2;  // Q4_K, BK == 64: high-nibble sub-block
+  rvec raw;       // Q8_0: raw f16 scale bits
+  int plane = 0;  // Q4_K, BK == 32: which nibble of each byte
+  __device__ __forceinline__ void put(int i, uint4 x) {
+    v[4 * i] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
+  }
+  __device__ __forceinline__ uint4 get(int i) const { return make_uint4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]); }
 
-// F16 weights (exact in f16 for every mode)
-template <int MODE, int BK>
-struct BLoad<LG_F16, MODE, BK> {
-  static constexpr int kPer = BN * BK / 8 / 256;  // 16-byte chunks per thread
-  static constexpr int kRows = kPer;
-  uint4 v[kPer];
-  __device__ static int row_of(int t, int i) { return (t + 256 * i) / (BK / 8); }
-  __device__ void fetch(const DevMatrix &W, const int *wrow, int k0, int t) {
-    const _Float16 *q = static_cast<const _Float16 *>(W.q);
+  template <class RowMap>
+  __device__ __forceinline__ void fetch(const DevMatrix &W, RowMap wrow, int k0, int t) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const int c = ((t + 256 * i) % (BK / 8)) * 8;
-      v[i] = *reinterpret_cast<const uint4 *>(q + int64_t(wrow[i]) * W.cols + k0 + c);
+      const int id = t + 256 * i, r = id / kCPR, c = id % kCPR;
+      const int64_t n = wrow(r);
+      if constexpr (KIND == LG_F16) {
+        put(i, *reinterpret_cast<const uint4 *>(static_cast<const _Float16 *>(W.q) + n * W.cols + k0 + c * 8));
+      } else if constexpr (KIND == LG_Q8_0) {
+        const int k = k0 + c * 16;
+        put(i, *reinterpret_cast<const uint4 *>(static_cast<const int8_t *>(W.q) + n * W.cols + k));
+        raw[i] = static_cast<const uint16_t *>(W.s)[n * (W.cols / 32) + k / 32];
+      } else if constexpr (KIND == LG_Q6_K) {
+        const int k = k0 + c * 16;
+        put(i, *reinterpret_cast<const uint4 *>(static_cast<const int8_t *>(W.q) + n * W.cols + k));
+        sa[i] = static_cast<const float *>(W.s)[n * (W.cols / 16) + k / 16];
+      } else {  // Q4_K
+        const uint8_t *rowq = static_cast<const uint8_t *>(W.q) + n * (W.cols / 2);
+        const float2 *s = static_cast<const float2 *>(W.s) + n * (W.cols / 32);
+        if constexpr (BK == 64) {  // bytes [k0/2 + 16c, +16): elements 16c+j (lo) and 32+16c+j (hi)
+          put(i, *reinterpret_cast<const uint4 *>(rowq + k0 / 2 + 16 * c));
+          const float2 s0 = s[k0 / 32], s1 = s[k0 / 32 + 1];
+          sa[i] = s0.x;
+          sb[i] = s0.y;
+          sa2[i] = s1.x;
+          sb2[i] = s1.y;
+        } else {  // one nibble plane: bytes [(k0/64)*32 + 16c, +16)
+          put(i, *reinterpret_cast<const uint4 *>(rowq + (k0 / 64) * 32 + 16 * c));
+          const float2 s0 = s[k0 / 32];
+          sa[i] = s0.x;
+          sb[i] = s0.y;
+        }
+      }
     }
+    if constexpr (kQ4 && BK == 32) plane = (k0 % 64) >= 32;
   }
+
   template <int LDK>
-  __device__ void store(_Float16 *Bs, _Float16 *, float *, int t) {
+  __device__ __forceinline__ void store(_Float16 *Bs, _Float16 *Bl, float *Ds, int t) {
+    constexpr bool kSplitB = MODE == SPLIT3;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const int idx = t + 256 * i, r = idx / (BK / 8), c = (idx % (BK / 8)) * 8;
-      *reinterpret_cast<uint4 *>(Bs + r * LDK + c) = v[i];
-    }
-  }
-};
-
-// Q8_0: FAST dequantises f16(d)*code; SPLIT stores the exact codes and the f32 block scale.
-template <int MODE, int BK>
-struct BLoad<LG_Q8_0, MODE, BK> {
-  static_assert(BK == 64, "Q8_0 tiles are 64 wide (two blocks)");
-  static constexpr int kRows = 1;
-  uint4 c0, c1;
-  uint32_t sb;
-  __device__ static int row_of(int t, int) { return t / 2; }
-  __device__ void fetch(const DevMatrix &W, const int *wrow, int k0, int t) {
-    const int part = t % 2;
-    const int8_t *q = static_cast<const int8_t *>(W.q) + int64_t(wrow[0]) * W.cols + k0 + part * 32;
-    c0 = *reinterpret_cast<const uint4 *>(q);
-    c1 = *reinterpret_cast<const uint4 *>(q + 16);
-    sb = static_cast<const uint16_t *>(W.s)[int64_t(wrow[0]) * (W.cols / 32) + k0 / 32 + part];
-  }
-  __device__ static void cvt16(uint4 c, _Float16 d, bool scale, _Float16 *dst) {
-    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
-    half8 o0, o1;
-    // f16(d) * code rounds the exact product once (d * code is exact in f32)
+      const int id = t + 256 * i, r = id / kCPR, c = id % kCPR;
+      const uint32_t w[4] = {v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
+      if constexpr (KIND == LG_F16) {
+        *reinterpret_cast<uint4 *>(Bs + r * LDK + c * 8) = get(i);
+      } else if constexpr (KIND == LG_Q8_0) {
+        half8 o0, o1;
+        const _Float16 d = __builtin_bit_cast(_Float16, uint16_t(raw[i]));
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const _Float16 a = _Float16(int8_t(w[j / 4] >> (8 * (j % 4))));
-      const _Float16 b = _Float16(int8_t(w[2 + j / 4] >> (8 * (j % 4))));
-      o0[j] = scale ? a * d : a;
-      o1[j] = scale ? b * d : b;
-    }
-    *reinterpret_cast<half8 *>(dst) = o0;
-    *reinterpret_cast<half8 *>(dst + 8) = o1;
-  }
-  template <int LDK>
-  __device__ void store(_Float16 *Bs, _Float16 *, float *Ds, int t) {
-    const int r = t / 2, part = t % 2;
-    const _Float16 d = __builtin_bit_cast(_Float16, uint16_t(sb));
-    cvt16(c0, d, MODE == FAST, Bs + r * LDK + part * 32);
-    cvt16(c1, d, MODE == FAST, Bs + r * LDK + part * 32 + 16);
-    if (MODE == SPLIT) Ds[r * 2 + part] = half_bits(sb);
-  }
-};
-
-// Q4_K: w = (d*sc)*q - (dmin*m) per 32-element sub-block.
-template <int MODE, int BK>
-struct BLoad<LG_Q4_K, MODE, BK> {
-  static constexpr int kRows = 1;
-  uint4 c;      // 16 bytes
-  float2 s0, s1;
-  __device__ static int row_of(int t, int) { return t / 2; }
-  __device__ void fetch(const DevMatrix &W, const int *wrow, int k0, int t) {
-    const int part = t % 2;
-    const uint8_t *rowq = static_cast<const uint8_t *>(W.q) + int64_t(wrow[0]) * (W.cols / 2);
-    const float2 *s = static_cast<const float2 *>(W.s) + int64_t(wrow[0]) * (W.cols / 32);
-    if (BK == 64) {  // both nibbles of bytes [k0/2 + part*16, +16)
-      c = *reinterpret_cast<const uint4 *>(rowq + k0 / 2 + part * 16);
-      s0 = s[k0 / 32];
-      s1 = s[k0 / 32 + 1];
-    } else {  // BK == 32: one nibble plane of bytes [(k0/64)*32 + part*16, +16)
-      c = *reinterpret_cast<const uint4 *>(rowq + (k0 / 64) * 32 + part * 16);
-      s0 = s[k0 / 32];
-    }
-  }
-  __device__ static void put16(const float *v, _Float16 *hi, _Float16 *lo) {
-    if (MODE == SPLIT3) {
-      half8 h0, l0, h1, l1;
-      split8(v, h0, l0);
-      split8(v + 8, h1, l1);
-      *reinterpret_cast<half8 *>(hi) = h0;
-      *reinterpret_cast<half8 *>(hi + 8) = h1;
-      *reinterpret_cast<half8 *>(lo) = l0;
-      *reinterpret_cast<half8 *>(lo + 8) = l1;
-    } else {
-      *reinterpret_cast<half8 *>(hi) = cvt8(v);
-      *reinterpret_cast<half8 *>(hi + 8) = cvt8(v + 8);
-    }
-  }
-  template <int LDK>
-  __device__ void store(_Float16 *Bs, _Float16 *Bl, float *, int t) {
-    const int r = t / 2, part = t % 2;
-    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
-    float lo[16], hi[16];
-    if (BK == 64) {
+        for (int j = 0; j < 8; ++j) {
+          const _Float16 a = _Float16(int8_t(w[j / 4] >> (8 * (j % 4))));
+          const _Float16 b = _Float16(int8_t(w[2 + j / 4] >> (8 * (j % 4))));
+          // FAST: f16(d) * code rounds the exact product once; SPLIT: the exact code
+          o0[j] = MODE == FAST ? a * d : a;
+          o1[j] = MODE == FAST ? b * d : b;
+        }
+        *reinterpret_cast<half8 *>(Bs + r * LDK + c * 16) = o0;
+        *reinterpret_cast<half8 *>(Bs + r * LDK + c * 16 + 8) = o1;
+        if (MODE == SPLIT && (c * 16) % 32 == 0) Ds[r * (BK / 32) + c * 16 / 32] = half_bits(raw[i]);
+      } else if constexpr (KIND == LG_Q6_K) {
+        float f[16];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const uint32_t byte = (w[j / 4] >> (8 * (j % 4))) & 0xffu;
-        lo[j] = s0.x * float(byte & 15u) - s0.y;
-        hi[j] = s1.x * float(byte >> 4) - s1.y;
-      }
-      put16(lo, Bs + r * LDK + part * 16, Bl + r * LDK + part * 16);
-      put16(hi, Bs + r * LDK + 32 + part * 16, Bl + r * LDK + 32 + part * 16);
-    } else {  // one nibble plane, chosen by the tile's position in its 64-element group
+        for (int j = 0; j < 16; ++j) f[j] = sa[i] * float(int8_t(w[j / 4] >> (8 * (j % 4))));
+        put8(f, Bs + r * LDK + c * 16, Bl + r * LDK + c * 16, kSplitB);
+        put8(f + 8, Bs + r * LDK + c * 16 + 8, Bl + r * LDK + c * 16 + 8, kSplitB);
+      } else {  // Q4_K
+        float lo[16], hi[16];
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const uint32_t byte = (w[j / 4] >> (8 * (j % 4))) & 0xffu;
-        lo[j] = s0.x * float(plane_ ? (byte >> 4) : (byte & 15u)) - s0.y;
-      }
-      put16(lo, Bs + r * LDK + part * 16, Bl + r * LDK + part * 16);
-    }
-  }
-  int plane_ = 0;
-};
-
-// Q6_K: w = (d*sc)*(q-32) per 16-element sub-block; codes stored as (q-32).
-template <int MODE, int BK>
-struct BLoad<LG_Q6_K, MODE, BK> {
-  static constexpr int kRows = 1;
-  static constexpr int kCodes = BK / 2;  // codes per thread
-  uint4 c[kCodes / 16];
-  float a[kCodes / 16];
-  __device__ static int row_of(int t, int) { return t / 2; }
-  __device__ void fetch(const DevMatrix &W, const int *wrow, int k0, int t) {
-    const int part = t % 2;
-    const int8_t *q = static_cast<const int8_t *>(W.q) + int64_t(wrow[0]) * W.cols + k0 + part * kCodes;
-    const float *s = static_cast<const float *>(W.s) + int64_t(wrow[0]) * (W.cols / 16) + (k0 + part * kCodes) / 16;
-#pragma unroll
-    for (int i = 0; i < kCodes / 16; ++i) {
-      c[i] = *reinterpret_cast<const uint4 *>(q + 16 * i);
-      a[i] = s[i];
-    }
-  }
-  template <int LDK>
-  __device__ void store(_Float16 *Bs, _Float16 *Bl, float *, int t) {
-    const int r = t / 2, part = t % 2;
-#pragma unroll
-    for (int i = 0; i < kCodes / 16; ++i) {
-      const uint32_t w[4] = {c[i].x, c[i].y, c[i].z, c[i].w};
-      float v[16];
-#pragma unroll
-      for (int j = 0; j < 16; ++j) v[j] = a[i] * float(int8_t(w[j / 4] >> (8 * (j % 4))));
-      _Float16 *hi = Bs + r * LDK + part * kCodes + 16 * i;
-      _Float16 *lo = Bl + r * LDK + part * kCodes + 16 * i;
-      if (MODE == SPLIT3) {
-        half8 h0, l0, h1, l1;
-        split8(v, h0, l0);
-        split8(v + 8, h1, l1);
-        *reinterpret_cast<half8 *>(hi) = h0;
-        *reinterpret_cast<half8 *>(hi + 8) = h1;
-        *reinterpret_cast<half8 *>(lo) = l0;
-        *reinterpret_cast<half8 *>(lo + 8) = l1;
-      } else {
-        *reinterpret_cast<half8 *>(hi) = cvt8(v);
-        *reinterpret_cast<half8 *>(hi + 8) = cvt8(v + 8);
+        for (int j = 0; j < 16; ++j) {
+          const uint32_t byte = (w[j / 4] >> (8 * (j % 4))) & 0xffu;
+          if constexpr (BK == 64) {
+            lo[j] = sa[i] * float(byte & 15u) - sb[i];
+            hi[j] = sa2[i] * float(byte >> 4) - sb2[i];
+          } else {
+            lo[j] = sa[i] * float(plane ? (byte >> 4) : (byte & 15u)) - sb[i];
+          }
+        }
+        put8(lo, Bs + r * LDK + c * 16, Bl + r * LDK + c * 16, kSplitB);
+        put8(lo + 8, Bs + r * LDK + c * 16 + 8, Bl + r * LDK + c * 16 + 8, kSplitB);
+        if constexpr (BK == 64) {
+          put8(hi, Bs + r * LDK + 32 + c * 16, Bl + r * LDK + 32 + c * 16, kSplitB);
+          put8(hi + 8, Bs + r * LDK + 32 + c * 16 + 8, Bl + r * LDK + 32 + c * 16 + 8, kSplitB);
+        }
       }
     }
   }
@@ -240,7 +175,131 @@ __device__ __forceinline__ void tile_coords(int bid, int nblk, int MT, int NT, i
 
 #define MFMA(a, b, c) __builtin_amdgcn_mfma_f32_32x32x16_f16((a), (b), (c), 0, 0, 0)
 
-template <uint32_t KIND, int EPI, int MODE, int BK>
+// Activation tile loader: BMW x BK halves (+ the lo plane), 16-byte chunks per thread.
+// Register storage is an ext_vector (kept in VGPRs); addresses are recomputed per fetch.
+template <int BMW, int BK, bool SPLITA>
+struct ALoad {
+  static constexpr int kPer = BMW * BK / 8 / 256;
+  static constexpr int kRowStep = 256 / (BK / 8);  // rows between a thread's chunks
+  typedef uint32_t vec __attribute__((ext_vector_type(4 * kPer)));
+  vec v, vl;
+  const _Float16 *A, *Alo;
+  int row0, rmax, col, K;
+  __device__ __forceinline__ void init(const _Float16 *A_, const _Float16 *Alo_, int m0, int M, int K_, int t) {
+    A = A_;
+    Alo = Alo_;
+    row0 = m0 + t / (BK / 8);
+    rmax = M - 1;  // rows >= M are clamped, never stored
+    col = (t % (BK / 8)) * 8;
+    K = K_;
+  }
+  __device__ __forceinline__ void fetch(int k0) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int64_t off = int64_t(min(row0 + i * kRowStep, rmax)) * K + col + k0;
+      const uint4 x = *reinterpret_cast<const uint4 *>(A + off);
+      v[4 * i] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
+      if constexpr (SPLITA) {
+        const uint4 y = *reinterpret_cast<const uint4 *>(Alo + off);
+        vl[4 * i] = y.x; vl[4 * i + 1] = y.y; vl[4 * i + 2] = y.z; vl[4 * i + 3] = y.w;
+      }
+    }
+  }
+  template <int LDK>
+  __device__ __forceinline__ void store(_Float16 *As, _Float16 *Al, int t) {
+    const int r = t / (BK / 8), c = (t % (BK / 8)) * 8;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int at = (r + i * kRowStep) * LDK + c;
+      *reinterpret_cast<uint4 *>(As + at) = make_uint4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+      if constexpr (SPLITA)
+        *reinterpret_cast<uint4 *>(Al + at) = make_uint4(vl[4 * i], vl[4 * i + 1], vl[4 * i + 2], vl[4 * i + 3]);
+    }
+  }
+};
+
+// MFMAs of one staged K tile into acc (see the mode table at the top of the file).
+template <uint32_t KIND, int MODE, int BK, int WTM, int WTN, int LDK>
+__device__ __forceinline__ void mma_tile(f32x16 (&acc)[WTM][WTN], const _Float16 *As, const _Float16 *Al,
+                                         const _Float16 *Bs, const _Float16 *Bl, const float *Ds, int wm,
+                                         int wn, int lane) {
+  constexpr bool kSplitA = MODE != FAST;
+  constexpr bool kSplitB = MODE == SPLIT3;
+  constexpr bool kScaled = MODE == SPLIT && KIND == LG_Q8_0;
+  const int arow = (wm * (32 * WTM) + (lane & 31)) * LDK;
+  const int brow = (wn * (32 * WTN) + (lane & 31)) * LDK;
+  if constexpr (kScaled) {
+    // per Q8_0 block: partial sums on MFMA, then acc += d * partial (f32)
+    const f32x16 zero = {};
+#pragma unroll
+    for (int blk = 0; blk < BK / 32; ++blk) {
+      f32x16 p[WTM][WTN];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int kc = blk * 32 + kk * 16 + (lane >> 5) * 8;
+        half8 b[WTN];
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) b[j] = *reinterpret_cast<const half8 *>(Bs + brow + j * 32 * LDK + kc);
+#pragma unroll
+        for (int i = 0; i < WTM; ++i) {
+          const half8 a = *reinterpret_cast<const half8 *>(As + arow + i * 32 * LDK + kc);
+          const half8 l = *reinterpret_cast<const half8 *>(Al + arow + i * 32 * LDK + kc);
+#pragma unroll
+          for (int j = 0; j < WTN; ++j) {
+            p[i][j] = MFMA(a, b[j], kk == 0 ? zero : p[i][j]);
+            p[i][j] = MFMA(l, b[j], p[i][j]);
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < WTN; ++j) {
+        const float dj = Ds[(wn * (32 * WTN) + j * 32 + (lane & 31)) * (BK / 32) + blk];
+#pragma unroll
+        for (int i = 0; i < WTM; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][j][r] += dj * p[i][j][r];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int kc = kk * 16 + (lane >> 5) * 8;
+      half8 b[WTN], c[kSplitB ? WTN : 1];
+#pragma unroll
+      for (int j = 0; j < WTN; ++j) {
+        b[j] = *reinterpret_cast<const half8 *>(Bs + brow + j * 32 * LDK + kc);
+        if constexpr (kSplitB) c[j] = *reinterpret_cast<const half8 *>(Bl + brow + j * 32 * LDK + kc);
+      }
+#pragma unroll
+      for (int i = 0; i < WTM; ++i) {
+        const half8 a = *reinterpret_cast<const half8 *>(As + arow + i * 32 * LDK + kc);
+        half8 l;
+        if constexpr (kSplitA) l = *reinterpret_cast<const half8 *>(Al + arow + i * 32 * LDK + kc);
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) {
+          acc[i][j] = MFMA(a, b[j], acc[i][j]);
+          if constexpr (kSplitA) acc[i][j] = MFMA(l, b[j], acc[i][j]);
+          if constexpr (kSplitB) acc[i][j] = MFMA(a, c[j], acc[i][j]);
+        }
+      }
+    }
+  }
+}
+
+template <int MODE, int BK, int WTM, int WTN, int STAGES>
+struct Cfg {
+  static constexpr int kBM = 64 * WTM, kBN = 64 * WTN;
+  static constexpr int kLDK = BK + 8;  // 16-byte row pad: conflict-free b128 LDS reads
+  static constexpr bool kSplitA = MODE != FAST;
+  static constexpr bool kSplitB = MODE == SPLIT3;
+  static constexpr int kAPlane = kBM * kLDK;   // halves
+  static constexpr int kBPlane = kBN * kLDK;   // halves
+  static constexpr int kStageHalves = kAPlane * (kSplitA ? 2 : 1) + kBPlane * (kSplitB ? 2 : 1);
+  static constexpr int kStageBytes = kStageHalves * 2 + kBN * (BK / 32) * 4;  // + block scales
+  static constexpr int kLdsBytes = STAGES * kStageBytes;
+};
+
+template <uint32_t KIND, int EPI, int MODE, int BK, int WTM, int WTN, int STAGES>
 __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ A,
                                                    const _Float16 *__restrict__ Alo, int M, int K,
                                                    DevMatrix W, float *__restrict__ C,
@@ -248,173 +307,117 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
                                                    _Float16 *__restrict__ C16lo, int ldc,
                                                    const float *__restrict__ bias, int MT, int NT,
                                                    int ffn) {
-  constexpr int LDK = BK + 8;  // 16-byte row pad: conflict-free b128 LDS reads
-  constexpr bool kSplitA = MODE != FAST;
-  constexpr bool kSplitB = MODE == SPLIT3;
+  using CF = Cfg<MODE, BK, WTM, WTN, STAGES>;
+  constexpr int BMW = CF::kBM, BNT = CF::kBN, LDK = CF::kLDK;
+  constexpr bool kSplitA = CF::kSplitA, kSplitB = CF::kSplitB;
   constexpr bool kScaled = MODE == SPLIT && KIND == LG_Q8_0;
-  __shared__ __attribute__((aligned(16))) _Float16 As[BM * LDK];
-  __shared__ __attribute__((aligned(16))) _Float16 Al[kSplitA ? BM * LDK : 8];
-  __shared__ __attribute__((aligned(16))) _Float16 Bs[BN * LDK];
-  __shared__ __attribute__((aligned(16))) _Float16 Bl[kSplitB ? BN * LDK : 8];
-  __shared__ float Ds[kScaled ? BN * 2 : 1];
+  static_assert(WTN % 2 == 0, "SwiGLU pairs gate and up blocks inside a wave");
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   int mt, nt;
   tile_coords(blockIdx.x, gridDim.x, MT, NT, mt, nt);
-  const int m0 = mt * BM;
+  const int m0 = mt * BMW;
 
-  using BL = BLoad<KIND, MODE, BK>;
-  int wrow[BL::kRows];
-#pragma unroll
-  for (int i = 0; i < BL::kRows; ++i) {
-    const int r = BL::row_of(t, i);
+  auto stage_ptrs = [&](int st, _Float16 *&As, _Float16 *&Al, _Float16 *&Bs, _Float16 *&Bl, float *&Ds) {
+    _Float16 *base = reinterpret_cast<_Float16 *>(lds + st * CF::kStageBytes);
+    As = base;
+    Al = kSplitA ? base + CF::kAPlane : base;
+    Bs = base + CF::kAPlane * (kSplitA ? 2 : 1);
+    Bl = kSplitB ? Bs + CF::kBPlane : Bs;
+    Ds = reinterpret_cast<float *>(base + CF::kStageHalves);
+  };
+  // local weight-tile row -> weight row
+  auto wrow = [&](int r) -> int {
     if (EPI == int(Epi::SWIGLU)) {
-      // local row r: wave column r/64, MFMA block (r/32)&1 (0 gate, 1 up), lane r&31
-      wrow[i] = ((r >> 5) & 1) * ffn + nt * 64 + (r >> 6) * 32 + (r & 31);
-    } else {
-      wrow[i] = nt * BN + r;
+      // wave column r/(32 WTN); block jb = (r/32) % WTN: gate for jb < WTN/2, up otherwise
+      const int wc = r / (32 * WTN), jb = (r >> 5) % WTN;
+      const int up = jb >= WTN / 2, jj = jb % (WTN / 2);
+      return up * ffn + nt * (BNT / 2) + wc * (16 * WTN) + jj * 32 + (r & 31);
     }
-  }
-  // activation rows this thread loads (clamped; rows >= M are never stored)
-  constexpr int kAPer = BM * BK / 8 / 256;
-  int64_t aoff[kAPer];
-#pragma unroll
-  for (int i = 0; i < kAPer; ++i) {
-    const int idx = t + 256 * i;
-    const int r = min(m0 + idx / (BK / 8), M - 1);
-    aoff[i] = int64_t(r) * K + (idx % (BK / 8)) * 8;
-  }
+    return nt * BNT + r;
+  };
 
-  f32x16 acc[2][2];
+  using BL = BLoad<KIND, MODE, BK, BNT>;
+  using AL = ALoad<BMW, BK, kSplitA>;
+  AL al;
+  al.init(A, Alo, m0, M, K, t);
+  BL bl;
+  f32x16 acc[WTM][WTN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < WTM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < WTN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  uint4 av[kAPer], avl[kSplitA ? kAPer : 1];
-  BL bl;
-#pragma unroll
-  for (int i = 0; i < kAPer; ++i) {
-    av[i] = *reinterpret_cast<const uint4 *>(A + aoff[i]);
-    if (kSplitA) avl[i] = *reinterpret_cast<const uint4 *>(Alo + aoff[i]);
-  }
-  bl.fetch(W, wrow, 0, t);
-  if constexpr (KIND == LG_Q4_K && BK == 32) bl.plane_ = 0;
-
   const int nk = K / BK;
-  for (int kt = 0; kt < nk; ++kt) {
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < kAPer; ++i) {
-      const int idx = t + 256 * i, r = idx / (BK / 8), c = (idx % (BK / 8)) * 8;
-      *reinterpret_cast<uint4 *>(As + r * LDK + c) = av[i];
-      if (kSplitA) *reinterpret_cast<uint4 *>(Al + r * LDK + c) = avl[i];
+  al.fetch(0);
+  bl.fetch(W, wrow, 0, t);
+  if constexpr (STAGES == 2) {
+    {
+      _Float16 *As, *Al, *Bs, *Bl;
+      float *Ds;
+      stage_ptrs(0, As, Al, Bs, Bl, Ds);
+      al.template store<LDK>(As, Al, t);
+      bl.template store<LDK>(Bs, Bl, Ds, t);
     }
-    bl.template store<LDK>(Bs, Bl, Ds, t);
     __syncthreads();
-    if (kt + 1 < nk) {
-      const int k1 = (kt + 1) * BK;
-#pragma unroll
-      for (int i = 0; i < kAPer; ++i) {
-        av[i] = *reinterpret_cast<const uint4 *>(A + aoff[i] + k1);
-        if (kSplitA) avl[i] = *reinterpret_cast<const uint4 *>(Alo + aoff[i] + k1);
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1;
+      if (kt + 1 < nk) {  // in flight during the MFMAs below
+        al.fetch((kt + 1) * BK);
+        bl.fetch(W, wrow, (kt + 1) * BK, t);
       }
-      bl.fetch(W, wrow, k1, t);
-      if constexpr (KIND == LG_Q4_K && BK == 32) bl.plane_ = (k1 % 64) >= 32;
+      _Float16 *As, *Al, *Bs, *Bl;
+      float *Ds;
+      stage_ptrs(cur, As, Al, Bs, Bl, Ds);
+      mma_tile<KIND, MODE, BK, WTM, WTN, LDK>(acc, As, Al, Bs, Bl, Ds, wm, wn, lane);
+      if (kt + 1 < nk) {
+        stage_ptrs(cur ^ 1, As, Al, Bs, Bl, Ds);
+        al.template store<LDK>(As, Al, t);
+        bl.template store<LDK>(Bs, Bl, Ds, t);
+      }
+      __syncthreads();
     }
-    const int ar0 = (wm * 64 + (lane & 31)) * LDK, ar1 = ar0 + 32 * LDK;
-    const int br0 = (wn * 64 + (lane & 31)) * LDK, br1 = br0 + 32 * LDK;
-    if constexpr (kScaled) {
-      // two Q8_0 blocks per tile: partial sums over each block, then acc += d * partial
-#pragma unroll
-      for (int blk = 0; blk < 2; ++blk) {
-        f32x16 p[2][2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) p[i][j][r] = 0.0f;
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const int kc = blk * 32 + kk * 16 + (lane >> 5) * 8;
-          const half8 a0 = *reinterpret_cast<const half8 *>(As + ar0 + kc);
-          const half8 a1 = *reinterpret_cast<const half8 *>(As + ar1 + kc);
-          const half8 l0 = *reinterpret_cast<const half8 *>(Al + ar0 + kc);
-          const half8 l1 = *reinterpret_cast<const half8 *>(Al + ar1 + kc);
-          const half8 b0 = *reinterpret_cast<const half8 *>(Bs + br0 + kc);
-          const half8 b1 = *reinterpret_cast<const half8 *>(Bs + br1 + kc);
-          p[0][0] = MFMA(a0, b0, p[0][0]);
-          p[0][1] = MFMA(a0, b1, p[0][1]);
-          p[1][0] = MFMA(a1, b0, p[1][0]);
-          p[1][1] = MFMA(a1, b1, p[1][1]);
-          p[0][0] = MFMA(l0, b0, p[0][0]);
-          p[0][1] = MFMA(l0, b1, p[0][1]);
-          p[1][0] = MFMA(l1, b0, p[1][0]);
-          p[1][1] = MFMA(l1, b1, p[1][1]);
-        }
-        const float d0 = Ds[(wn * 64 + (lane & 31)) * 2 + blk];
-        const float d1 = Ds[(wn * 64 + 32 + (lane & 31)) * 2 + blk];
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            acc[i][0][r] += d0 * p[i][0][r];
-            acc[i][1][r] += d1 * p[i][1][r];
-          }
+  } else {
+    _Float16 *As, *Al, *Bs, *Bl;
+    float *Ds;
+    stage_ptrs(0, As, Al, Bs, Bl, Ds);
+    for (int kt = 0; kt < nk; ++kt) {
+      __syncthreads();
+      al.template store<LDK>(As, Al, t);
+      bl.template store<LDK>(Bs, Bl, Ds, t);
+      __syncthreads();
+      if (kt + 1 < nk) {
+        al.fetch((kt + 1) * BK);
+        bl.fetch(W, wrow, (kt + 1) * BK, t);
       }
-    } else {
-#pragma unroll
-      for (int kk = 0; kk < BK / 16; ++kk) {
-        const int kc = kk * 16 + (lane >> 5) * 8;
-        const half8 a0 = *reinterpret_cast<const half8 *>(As + ar0 + kc);
-        const half8 a1 = *reinterpret_cast<const half8 *>(As + ar1 + kc);
-        const half8 b0 = *reinterpret_cast<const half8 *>(Bs + br0 + kc);
-        const half8 b1 = *reinterpret_cast<const half8 *>(Bs + br1 + kc);
-        acc[0][0] = MFMA(a0, b0, acc[0][0]);
-        acc[0][1] = MFMA(a0, b1, acc[0][1]);
-        acc[1][0] = MFMA(a1, b0, acc[1][0]);
-        acc[1][1] = MFMA(a1, b1, acc[1][1]);
-        if constexpr (kSplitA) {
-          const half8 l0 = *reinterpret_cast<const half8 *>(Al + ar0 + kc);
-          const half8 l1 = *reinterpret_cast<const half8 *>(Al + ar1 + kc);
-          acc[0][0] = MFMA(l0, b0, acc[0][0]);
-          acc[0][1] = MFMA(l0, b1, acc[0][1]);
-          acc[1][0] = MFMA(l1, b0, acc[1][0]);
-          acc[1][1] = MFMA(l1, b1, acc[1][1]);
-        }
-        if constexpr (kSplitB) {
-          const half8 c0 = *reinterpret_cast<const half8 *>(Bl + br0 + kc);
-          const half8 c1 = *reinterpret_cast<const half8 *>(Bl + br1 + kc);
-          acc[0][0] = MFMA(a0, c0, acc[0][0]);
-          acc[0][1] = MFMA(a0, c1, acc[0][1]);
-          acc[1][0] = MFMA(a1, c0, acc[1][0]);
-          acc[1][1] = MFMA(a1, c1, acc[1][1]);
-        }
-      }
+      mma_tile<KIND, MODE, BK, WTM, WTN, LDK>(acc, As, Al, Bs, Bl, Ds, wm, wn, lane);
     }
   }
 
   // epilogue: acc[i][j] register r -> row (r/4)*8 + (lane/32)*4 + r%4, column lane%32
   const int col_in = lane & 31;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < WTM; ++i) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+      const int row = m0 + wm * (32 * WTM) + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
       if (row >= M) continue;
       if (EPI == int(Epi::SWIGLU)) {
-        const int col = nt * 64 + wn * 32 + col_in;
-        const float v = silu(acc[i][0][r]) * acc[i][1][r];
-        const _Float16 h = _Float16(v);
-        C16[int64_t(row) * ldc + col] = h;
-        if (C16lo) C16lo[int64_t(row) * ldc + col] = _Float16(v - float(h));
+#pragma unroll
+        for (int jj = 0; jj < WTN / 2; ++jj) {
+          const int col = nt * (BNT / 2) + wn * (16 * WTN) + jj * 32 + col_in;
+          const float v = silu(acc[i][jj][r]) * acc[i][jj + WTN / 2][r];
+          const _Float16 h = _Float16(v);
+          C16[int64_t(row) * ldc + col] = h;
+          if (C16lo) C16lo[int64_t(row) * ldc + col] = _Float16(v - float(h));
+        }
       } else {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int col = nt * BN + wn * 64 + j * 32 + col_in;
+        for (int j = 0; j < WTN; ++j) {
+          const int col = nt * BNT + wn * (32 * WTN) + j * 32 + col_in;
           float v = acc[i][j][r];
           if (EPI == int(Epi::F32)) {
             if (bias) v += bias[col];
@@ -433,15 +436,30 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
   }
 }
 
-template <uint32_t KIND, int MODE, int BK>
-void launch_mode(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
-                 _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, int MT, int NT,
-                 hipStream_t st) {
+template <uint32_t KIND, int MODE, int BK, int WTM, int WTN, int STAGES>
+bool launch_cfg(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
+                _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st) {
+  using CF = Cfg<MODE, BK, WTM, WTN, STAGES>;
+  const int outN = epi == Epi::SWIGLU ? W.rows / 2 : W.rows;
+  const int tileN = epi == Epi::SWIGLU ? CF::kBN / 2 : CF::kBN;
+  if (outN % tileN) return false;
+  const int NT = outN / tileN;
+  const int MT = (M + CF::kBM - 1) / CF::kBM;
+  LG_REQUIRE(int64_t(MT) * NT < (1ll << 31), "gemm: grid too large");
   const dim3 grid(MT * NT), block(256);
   const int K = W.cols, ffn = W.rows / 2;
-#define LAUNCH(E)                                                                                   \
-  hipLaunchKernelGGL((gemm_kernel<KIND, E, MODE, BK>), grid, block, 0, st, A, Alo, M, K, W, C, C16, \
-                     C16lo, ldc, bias, MT, NT, ffn)
+#define LAUNCH(E)                                                                                            \
+  do {                                                                                                       \
+    auto fn = gemm_kernel<KIND, E, MODE, BK, WTM, WTN, STAGES>;                                              \
+    static bool attr = false;                                                                                \
+    if (!attr) {                                                                                             \
+      HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(fn),                                      \
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, CF::kLdsBytes));              \
+      attr = true;                                                                                           \
+    }                                                                                                        \
+    hipLaunchKernelGGL(fn, grid, block, CF::kLdsBytes, st, A, Alo, M, K, W, C, C16, C16lo, ldc, bias, MT, NT, \
+                       ffn);                                                                                 \
+  } while (0)
   switch (epi) {
     case Epi::F32: LAUNCH(0); break;
     case Epi::ADD: LAUNCH(1); break;
@@ -449,20 +467,27 @@ void launch_mode(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix 
     case Epi::SWIGLU: LAUNCH(3); break;
   }
 #undef LAUNCH
+  return true;
 }
 
+#ifndef LG_GEMM_CONFIGS
+// Per-kind, per-mode tile configuration: <MODE, BK, WTM, WTN, STAGES>.
 template <uint32_t KIND>
 void launch_kind(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
-                 _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, int MT, int NT,
-                 hipStream_t st) {
+                 _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st) {
+  // Chosen by a sweep at the 35,840-token Q8_0/F16 prefill shapes; a 256-wide N tile
+  // falls back to 128 when it does not divide the output width.
   if (!Alo) {
-    launch_mode<KIND, FAST, 64>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, MT, NT, st);
+    if (launch_cfg<KIND, FAST, 64, 4, 4, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
+    if (launch_cfg<KIND, FAST, 64, 2, 2, 2>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
   } else if constexpr (KIND == LG_F16 || KIND == LG_Q8_0) {
-    launch_mode<KIND, SPLIT, 64>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, MT, NT, st);
+    if (launch_cfg<KIND, SPLIT, 64, 2, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
   } else {
-    launch_mode<KIND, SPLIT3, 32>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, MT, NT, st);
+    if (launch_cfg<KIND, SPLIT3, 32, 2, 2, 2>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
   }
+  fail(LG_ERR_UNSUPPORTED, "gemm: no tile configuration for N=%d", W.rows);
 }
+#endif
 
 // ---------------------------------------------------------------- generic f32 GEMM
 __device__ float weight_at(const DevMatrix &W, int64_t n, int64_t k) {
@@ -505,30 +530,26 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(const float *__restri
 
 }  // namespace
 
+#ifndef LG_GEMM_CONFIGS
 void launch_gemm(const _Float16 *A, const _Float16 *A_lo, int M, const DevMatrix &W, Epi epi, float *C,
                  _Float16 *C16, _Float16 *C16_lo, int ldc, const float *bias, hipStream_t st) {
   LG_REQUIRE(M > 0, "gemm: empty activation");
   if (W.cols % 64 != 0) fail(LG_ERR_UNSUPPORTED, "gemm: K=%d is not a multiple of 64", W.cols);
   if (W.kind == LG_Q4_K || W.kind == LG_Q6_K)
     LG_REQUIRE(W.cols % 256 == 0, "gemm: K-quant rows must be whole super-blocks");
-  int NT;
   if (epi == Epi::SWIGLU) {
     if (W.rows % 128 != 0) fail(LG_ERR_UNSUPPORTED, "gemm: gate|up rows %d not a multiple of 128", W.rows);
-    NT = (W.rows / 2) / 64;
     LG_REQUIRE(C16 != nullptr && ldc >= W.rows / 2, "gemm: SwiGLU output needs ldc >= ffn");
   } else {
-    if (W.rows % BN != 0) fail(LG_ERR_UNSUPPORTED, "gemm: N=%d is not a multiple of %d", W.rows, BN);
-    NT = W.rows / BN;
+    if (W.rows % 128 != 0) fail(LG_ERR_UNSUPPORTED, "gemm: N=%d is not a multiple of 128", W.rows);
     LG_REQUIRE(ldc >= W.rows, "gemm: ldc %d < N %d", ldc, W.rows);
     LG_REQUIRE(epi == Epi::F16 ? C16 != nullptr : C != nullptr, "gemm: missing output");
   }
-  const int MT = (M + BM - 1) / BM;
-  LG_REQUIRE(int64_t(MT) * NT < (1ll << 31), "gemm: grid too large");
   switch (W.kind) {
-    case LG_F16: launch_kind<LG_F16>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, MT, NT, st); break;
-    case LG_Q8_0: launch_kind<LG_Q8_0>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, MT, NT, st); break;
-    case LG_Q4_K: launch_kind<LG_Q4_K>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, MT, NT, st); break;
-    case LG_Q6_K: launch_kind<LG_Q6_K>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, MT, NT, st); break;
+    case LG_F16: launch_kind<LG_F16>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, st); break;
+    case LG_Q8_0: launch_kind<LG_Q8_0>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, st); break;
+    case LG_Q4_K: launch_kind<LG_Q4_K>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, st); break;
+    case LG_Q6_K: launch_kind<LG_Q6_K>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, st); break;
     default: fail(LG_ERR_UNSUPPORTED, "gemm: no MFMA path for GGML type %u", W.kind);
   }
   HIP_CHECK(hipGetLastError());
@@ -543,5 +564,6 @@ void launch_gemm_generic(const float *X, int M, const DevMatrix &W, const float 
                      bias, Y);
   HIP_CHECK(hipGetLastError());
 }
+#endif
 
 }  // namespace lg
