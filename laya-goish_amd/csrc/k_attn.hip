@@ -13,9 +13,9 @@
 // and hi/lo query planes every product is split (hi.hi + lo.hi + hi.lo: three MFMAs), which
 // keeps scores and outputs f32-faithful.
 //
-// Decode: one wave per (sequence, kv head, page): coalesced reads of the page's K rows and
-// V columns, f32 scores for every query head of the group, partial (max, sum, out) per page;
-// a second kernel combines the pages.
+// Decode: one workgroup per (sequence, kv head, page): coalesced reads of the page's K rows
+// and V columns, f32 scores for every query head of the group, partial (max, sum, out) per
+// page; the last workgroup of each (sequence, kv head) combines the pages.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -198,68 +198,145 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(
 
 // ---------------------------------------------------------------- decode
 // part layout: [nseq][hq][max_pages][2 + HD] = (max, sum, out[HD]) of one page.
-// E = elements per 16-byte load (8 for f16, 4 for f32).
+// One 256-thread workgroup per (page, kv head, sequence).  Every thread issues all of its
+// K and V loads first (16 B each): K rows are split 4 threads per key (32 dims each), V
+// columns 2 threads per dim (32 keys each).  Scores for every query head of the group are
+// reduced over the 4 threads of a key, the page softmax over LDS, then P.V per head.
 template <int HD, int GRP, typename KV>
-__global__ __launch_bounds__(64) void attn_decode_kernel(const float *__restrict__ q32, int hq, KvGeom g,
-                                                         const KV *__restrict__ kpool,
-                                                         const KV *__restrict__ vpool,
-                                                         const int32_t *__restrict__ pages,
-                                                         int max_pages,
-                                                         const int32_t *__restrict__ ctx_len,
-                                                         float *__restrict__ part) {
+__device__ __forceinline__ void attn_decode_page(const float *__restrict__ q32, int hq, const KvGeom &g,
+                                                 const KV *__restrict__ kpool,
+                                                 const KV *__restrict__ vpool,
+                                                 const int32_t *__restrict__ pages, int max_pages,
+                                                 int len, float *pbase, int64_t hstride);
+
+template <int HD, int GRP, typename KV>
+__global__ __launch_bounds__(256) void attn_decode_kernel(const float *__restrict__ q32, int hq, KvGeom g,
+                                                          const KV *__restrict__ kpool,
+                                                          const KV *__restrict__ vpool,
+                                                          const int32_t *__restrict__ pages,
+                                                          int max_pages,
+                                                          const int32_t *__restrict__ ctx_len,
+                                                          float *__restrict__ part) {
   static_assert(HD == 128, "decode attention is written for head_dim 128");
-  constexpr int E = 16 / sizeof(KV);
-  constexpr int NLD = P * HD / E / 64;      // 16-byte loads per lane per page (16 or 32)
-  constexpr int KL = HD / E;                // lanes sharing one key row
-  constexpr int VL = P / E;                 // lanes sharing one V column-row (d)
   const int pi = blockIdx.x, kh = blockIdx.y, s = blockIdx.z;
-  const int lane = threadIdx.x;
+  const int t = threadIdx.x;
   const int len = ctx_len[s];
   float *pbase = part + ((int64_t(s) * hq + kh * GRP) * max_pages + pi) * (2 + HD);
   const int64_t hstride = int64_t(max_pages) * (2 + HD);
-  if (pi * P >= len) {
-    if (lane == 0)
-      for (int gq = 0; gq < GRP; ++gq) {
-        pbase[gq * hstride] = -INFINITY;
-        pbase[gq * hstride + 1] = 0.0f;
-      }
-    return;
+  if (pi * P < len) {
+    attn_decode_page<HD, GRP, KV>(q32, hq, g, kpool, vpool, pages, max_pages, len, pbase, hstride);
+  } else if (t < GRP) {  // pages past the context contribute nothing
+    pbase[t * hstride] = -INFINITY;
+    pbase[t * hstride + 1] = 0.0f;
   }
-  const int64_t page = pages[int64_t(s) * max_pages + pi];
-  const uint4 *Kp = reinterpret_cast<const uint4 *>(kpool + page * g.page_stride + int64_t(kh) * P * HD);
-  const uint4 *Vp = reinterpret_cast<const uint4 *>(vpool + page * g.page_stride + int64_t(kh) * HD * P);
-  __shared__ float sc[GRP][P];
-  const float inv_sqrt = 1.0f / sqrtf(float(HD));
+}
+
+// Combine the per-page partials of one (sequence, query head).  Cross-workgroup hand-off
+// through memory would need an agent-scope release (an L2 write-back on this part) in every
+// page workgroup, so the combine is its own small launch.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_decode_combine(const float *__restrict__ part, int hq,
+                                                           int max_pages,
+                                                           const int32_t *__restrict__ ctx_len,
+                                                           float *__restrict__ out) {
+  const int h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
+  const int np = (ctx_len[s] + P - 1) / P;
+  __shared__ float wm[1024], wl[1024];
+  __shared__ float red[4], sacc[2][HD], sl[2];
   {
-    uint4 kv[NLD];
+    const float *pb = part + ((int64_t(s) * hq + h) * max_pages) * (2 + HD);
+    // page maxima and sums, gathered in parallel
+    float M = -INFINITY;
+    for (int i = t; i < np; i += 256) {
+      wm[i] = pb[int64_t(i) * (2 + HD)];
+      wl[i] = pb[int64_t(i) * (2 + HD) + 1];
+      M = fmaxf(M, wm[i]);
+    }
 #pragma unroll
-    for (int i = 0; i < NLD; ++i) kv[i] = Kp[i * 64 + lane];  // key (i*64+lane)/KL, dims lane%KL*E
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+    if ((t & 63) == 0) red[t >> 6] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int i = t; i < np; i += 256) wm[i] = wm[i] == -INFINITY ? 0.0f : __expf(wm[i] - M);
+    __syncthreads();
+    // weighted sum of the page outputs: thread (d, half) takes every other page, 8 loads in flight
+    const int d = t & (HD - 1), half = t >> 7;
+    float acc = 0.0f, L = 0.0f;
+    for (int i0 = half; i0 < np; i0 += 16) {
+      float v[8];
 #pragma unroll
-    for (int gq = 0; gq < GRP; ++gq) {
-      const float *q = q32 + int64_t(s) * hq * HD + (kh * GRP + gq) * HD + (lane % KL) * E;
-      float qv[E];
+      for (int u = 0; u < 8; ++u) {
+        const int i = i0 + 2 * u;
+        v[u] = i < np ? pb[int64_t(i) * (2 + HD) + 2 + d] : 0.0f;
+      }
 #pragma unroll
-      for (int j = 0; j < E; ++j) qv[j] = q[j];
-#pragma unroll
-      for (int i = 0; i < NLD; ++i) {
-        const KV *k8 = reinterpret_cast<const KV *>(&kv[i]);
-        float d = 0.0f;
-#pragma unroll
-        for (int j = 0; j < E; ++j) d += qv[j] * float(k8[j]);
-#pragma unroll
-        for (int off = 1; off < KL; off <<= 1) d += __shfl_xor(d, off);
-        const int key = (i * 64 + lane) / KL;
-        if (lane % KL == 0) sc[gq][key] = (pi * P + key < len) ? d * inv_sqrt : -INFINITY;
+      for (int u = 0; u < 8; ++u) {
+        const int i = i0 + 2 * u;
+        if (i < np) {
+          acc += v[u] * wm[i];
+          L += wl[i] * wm[i];
+        }
       }
     }
+    sacc[half][d] = acc;
+    if (d == 0) sl[half] = L;
+    __syncthreads();
+    if (t < HD) out[(int64_t(s) * hq + h) * HD + t] = (sacc[0][t] + sacc[1][t]) / (sl[0] + sl[1]);
   }
-  __syncthreads();
-  uint4 vv[NLD];
+}
+
+// One page of one (sequence, kv head): scores, page softmax and P.V for each query head.
+template <int HD, int GRP, typename KV>
+__device__ __forceinline__ void attn_decode_page(const float *__restrict__ q32, int hq, const KvGeom &g,
+                                                 const KV *__restrict__ kpool,
+                                                 const KV *__restrict__ vpool,
+                                                 const int32_t *__restrict__ pages, int max_pages,
+                                                 int len, float *pbase, int64_t hstride) {
+  constexpr int E = 16 / sizeof(KV);   // elements per 16-byte load
+  constexpr int NK = 32 / E;           // loads per thread for its 32-dim K slice
+  constexpr int NV = 32 / E;           // loads per thread for its 32-key V slice
+  typedef uint32_t kvec __attribute__((ext_vector_type(4 * NK)));
+  const int pi = blockIdx.x, kh = blockIdx.y, s = blockIdx.z;
+  const int t = threadIdx.x;
+  const int64_t page = pages[int64_t(s) * max_pages + pi];
+  const KV *Kp = kpool + page * g.page_stride + int64_t(kh) * P * HD;
+  const KV *Vp = vpool + page * g.page_stride + int64_t(kh) * HD * P;
+  const int key = t >> 2, kd0 = (t & 3) * 32;   // K: key row, 32-dim slice
+  const int vd = t >> 1, vk0 = (t & 1) * 32;    // V: dim row, 32-key slice
+  kvec kr, vr;
 #pragma unroll
-  for (int i = 0; i < NLD; ++i) vv[i] = Vp[i * 64 + lane];  // d (i*64+lane)/VL, keys lane%VL*E
+  for (int i = 0; i < NK; ++i) {
+    const uint4 a = *reinterpret_cast<const uint4 *>(Kp + key * HD + kd0 + i * E);
+    kr[4 * i] = a.x; kr[4 * i + 1] = a.y; kr[4 * i + 2] = a.z; kr[4 * i + 3] = a.w;
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const uint4 a = *reinterpret_cast<const uint4 *>(Vp + vd * P + vk0 + i * E);
+    vr[4 * i] = a.x; vr[4 * i + 1] = a.y; vr[4 * i + 2] = a.z; vr[4 * i + 3] = a.w;
+  }
+  __shared__ float sc[GRP][P];
+
+  const float inv_sqrt = 1.0f / sqrtf(float(HD));
+  const bool valid = pi * P + key < len;
 #pragma unroll
   for (int gq = 0; gq < GRP; ++gq) {
-    const float v = sc[gq][lane];
+    const float *q = q32 + int64_t(s) * hq * HD + (kh * GRP + gq) * HD + kd0;
+    float d = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      const KV *k8 = reinterpret_cast<const KV *>(&kr) + i * E;
+#pragma unroll
+      for (int j = 0; j < E; ++j) d += q[i * E + j] * float(k8[j]);
+    }
+    d += __shfl_xor(d, 1);
+    d += __shfl_xor(d, 2);
+    if ((t & 3) == 0) sc[gq][key] = valid ? d * inv_sqrt : -INFINITY;
+  }
+  __syncthreads();
+  // page softmax per query head: wave w < GRP reduces head w's 64 scores
+  for (int gq = t >> 6; gq < GRP; gq += 4) {
+    const int l = t & 63;
+    const float v = sc[gq][l];
     float mx = v;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
@@ -267,46 +344,25 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float *__restrict
     float sum = p;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-    __syncthreads();
-    sc[gq][lane] = p;
-    __syncthreads();
-    float *pp = pbase + gq * hstride;
-    if (lane == 0) {
-      pp[0] = mx;
-      pp[1] = sum;
-    }
-#pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-      const KV *v8 = reinterpret_cast<const KV *>(&vv[i]);
-      float a = 0.0f;
-#pragma unroll
-      for (int j = 0; j < E; ++j) a += sc[gq][(lane % VL) * E + j] * float(v8[j]);
-#pragma unroll
-      for (int off = 1; off < VL; off <<= 1) a += __shfl_xor(a, off);
-      if (lane % VL == 0) pp[2 + (i * 64 + lane) / VL] = a;
+    sc[gq][l] = p;
+    if (l == 0) {
+      pbase[gq * hstride] = mx;
+      pbase[gq * hstride + 1] = sum;
     }
   }
-}
-
-__global__ __launch_bounds__(128) void attn_decode_combine(const float *__restrict__ part, int hq, int hd,
-                                                           int max_pages,
-                                                           const int32_t *__restrict__ ctx_len,
-                                                           float *__restrict__ out) {
-  const int h = blockIdx.x, s = blockIdx.y;
-  const int np = (ctx_len[s] + P - 1) / P;
-  const float *pb = part + (int64_t(s) * hq + h) * max_pages * (2 + hd);
-  float M = -INFINITY;
-  for (int i = 0; i < np; ++i) M = fmaxf(M, pb[int64_t(i) * (2 + hd)]);
-  float L = 0.0f, acc = 0.0f;
-  const int d = threadIdx.x;
-  for (int i = 0; i < np; ++i) {
-    const float *p = pb + int64_t(i) * (2 + hd);
-    if (p[0] == -INFINITY) continue;
-    const float w = __expf(p[0] - M);
-    L += p[1] * w;
-    if (d < hd) acc += p[2 + d] * w;
+  __syncthreads();
+#pragma unroll
+  for (int gq = 0; gq < GRP; ++gq) {
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const KV *v8 = reinterpret_cast<const KV *>(&vr) + i * E;
+#pragma unroll
+      for (int j = 0; j < E; ++j) a += sc[gq][vk0 + i * E + j] * float(v8[j]);
+    }
+    a += __shfl_xor(a, 1);
+    if ((t & 1) == 0) pbase[gq * hstride + 2 + vd] = a;
   }
-  if (d < hd) out[(int64_t(s) * hq + h) * hd + d] = acc / L;
 }
 
 }  // namespace
@@ -352,8 +408,9 @@ void launch_attn_decode(const float *q32, int nseq, int hq, const KvGeom &g, con
   LG_REQUIRE(nseq > 0 && max_ctx > 0, "decode attention: empty");
   const int np = (max_ctx + P - 1) / P;
   LG_REQUIRE(np <= max_pages, "decode attention: context exceeds the page table");
+  LG_REQUIRE(np <= 1024, "decode attention: context of %d pages exceeds the combine stage", np);
   const int grp = hq / g.hkv;
-  const dim3 grid(np, g.hkv, nseq), block(64);
+  const dim3 grid(np, g.hkv, nseq), block(256);
 #define CASE(G)                                                                                     \
   case G:                                                                                           \
     if (g.kv32)                                                                                     \
@@ -370,7 +427,8 @@ void launch_attn_decode(const float *q32, int nseq, int hq, const KvGeom &g, con
     default: fail(LG_ERR_UNSUPPORTED, "decode attention: group size %d not supported", grp);
   }
 #undef CASE
-  hipLaunchKernelGGL(attn_decode_combine, dim3(hq, nseq), dim3(128), 0, st, part, hq, g.hd, max_pages,
+  HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL((attn_decode_combine<128>), dim3(hq, nseq), dim3(256), 0, st, part, hq, max_pages,
                      ctx_len, out);
   HIP_CHECK(hipGetLastError());
 }

@@ -15,7 +15,6 @@ namespace lg {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 4;
 
 __device__ __forceinline__ float silu(float g) { return g * (1.0f / (1.0f + __expf(-g))); }
 
@@ -88,59 +87,22 @@ __device__ __forceinline__ float dot8_f16(uint4 c, const float4 *xs, int plane_s
   return s;
 }
 
-// Partial dot product of weight row n with the staged x, this lane's chunks.
-template <uint32_t KIND>
-__device__ __forceinline__ float row_partial(const DevMatrix &W, int n, const float4 *xs, int lane) {
-  const int K = W.cols;
-  float acc = 0.0f;
-  if constexpr (KIND == LG_Q8_0 || KIND == LG_Q6_K) {
-    const int nchunk = K / 16;
-    const uint4 *q = reinterpret_cast<const uint4 *>(static_cast<const int8_t *>(W.q) + int64_t(n) * K);
-    for (int base = 0; base < nchunk; base += 64 * kUnroll) {
-      uint4 c[kUnroll];
-      float d[kUnroll];
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int ch = base + u * 64 + lane;
-        if (ch < nchunk) {
-          c[u] = q[ch];
-          if constexpr (KIND == LG_Q8_0)
-            d[u] = half_bits(static_cast<const uint16_t *>(W.s)[int64_t(n) * (K / 32) + ch / 2]);
-          else
-            d[u] = static_cast<const float *>(W.s)[int64_t(n) * (K / 16) + ch];
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int ch = base + u * 64 + lane;
-        if (ch < nchunk) acc += d[u] * dot16_i8(c[u], xs, nchunk, ch);
-      }
-    }
-  } else if constexpr (KIND == LG_F16) {
-    const int nchunk = K / 8;
-    const uint4 *q = reinterpret_cast<const uint4 *>(static_cast<const _Float16 *>(W.q) + int64_t(n) * K);
-    for (int base = 0; base < nchunk; base += 64 * kUnroll) {
-      uint4 c[kUnroll];
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int ch = base + u * 64 + lane;
-        if (ch < nchunk) c[u] = q[ch];
-      }
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int ch = base + u * 64 + lane;
-        if (ch < nchunk) acc += dot8_f16(c[u], xs, nchunk, ch);
-      }
-    }
-  }
-  return acc;
-}
-
 // Elements per lane load for each kind (x staging chunk size).
 template <uint32_t KIND>
 constexpr int chunk_elems() { return KIND == LG_F16 ? 8 : 16; }
 
-template <uint32_t KIND, int EPI>
+// Scale of chunk ch of row n (Q8_0: per 32-element block, Q6_K: per 16).
+template <uint32_t KIND>
+__device__ __forceinline__ float chunk_scale(const DevMatrix &W, int64_t n, int ch) {
+  if constexpr (KIND == LG_Q8_0) return half_bits(static_cast<const uint16_t *>(W.s)[n * (W.cols / 32) + ch / 2]);
+  else if constexpr (KIND == LG_Q6_K) return static_cast<const float *>(W.s)[n * (W.cols / 16) + ch];
+  else return 1.0f;
+}
+
+// Each wave owns R outputs (RPO weight rows each: 2 for SwiGLU's gate|up).  All weight loads of
+// a chunk group are issued before the input vector is staged, so the x/RMSNorm prologue
+// overlaps the HBM reads.  Chunk c of a lane covers chunk index g*64*CPL + c*64 + lane.
+template <uint32_t KIND, int EPI, int R, int CPL>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(const float *__restrict__ x, DevMatrix W,
                                                         float *__restrict__ y,
                                                         const float *__restrict__ bias,
@@ -149,20 +111,91 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const float *__restrict_
   extern __shared__ float4 xs[];
   __shared__ float red[4];
   constexpr int E = chunk_elems<KIND>();
-  stage_x<E>(x, W.cols, norm_w, eps, xs, red);
-  const int lane = threadIdx.x & 63;
-  const int o = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-  if (o >= outputs) return;
-  if (EPI == int(Epi::SWIGLU)) {
-    const int f = W.rows / 2;
-    const float g = wave_sum(row_partial<KIND>(W, o, xs, lane));
-    const float u = wave_sum(row_partial<KIND>(W, f + o, xs, lane));
-    if (lane == 0) y[o] = silu(g) * u;
-  } else {
-    const float v = wave_sum(row_partial<KIND>(W, o, xs, lane));
-    if (lane == 0) {
-      if (EPI == int(Epi::ADD)) y[o] += v;
-      else y[o] = v + (bias ? bias[o] : 0.0f);
+  constexpr int RPO = EPI == int(Epi::SWIGLU) ? 2 : 1;
+  constexpr int NR = R * RPO;
+  typedef uint32_t wvec __attribute__((ext_vector_type(4 * NR * CPL)));
+  typedef float svec __attribute__((ext_vector_type(NR * CPL)));
+  typedef float avec __attribute__((ext_vector_type(NR)));
+  const int K = W.cols, nchunk = K / E;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int o0 = (blockIdx.x * (kThreads / 64) + wave) * R;
+  const int f = W.rows / 2;
+  const uint4 *q = static_cast<const uint4 *>(W.q);
+  const int64_t row_chunks = int64_t(K) * (KIND == LG_F16 ? 2 : 1) / 16;  // uint4 per weight row
+  wvec w;
+  svec sc;
+  avec acc;
+#pragma unroll
+  for (int r = 0; r < NR; ++r) acc[r] = 0.0f;
+  const int ngroups = (nchunk + 64 * CPL - 1) / (64 * CPL);
+  for (int g = 0; g < ngroups; ++g) {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const int o = min(o0 + r / RPO, outputs - 1);  // clamped rows are never stored
+      const int64_t n = (r % RPO) ? f + o : o;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const int ch = g * 64 * CPL + c * 64 + lane;
+        const int i = r * CPL + c;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        float s = 0.0f;
+        if (ch < nchunk) {
+          v = q[n * row_chunks + ch];
+          s = chunk_scale<KIND>(W, n, ch);
+        }
+        w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+        sc[i] = s;
+      }
+    }
+    if (g == 0) stage_x<E>(x, K, norm_w, eps, xs, red);  // every wave reaches this barrier
+    // each x chunk is read from LDS once and used for all NR rows of the wave
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int ch = g * 64 * CPL + c * 64 + lane;
+      if (ch < nchunk) {
+        float4 xv[E / 4];
+#pragma unroll
+        for (int p = 0; p < E / 4; ++p) xv[p] = xs[p * nchunk + ch];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          const int i = r * CPL + c;
+          const uint32_t wd[4] = {w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
+          float d = 0.0f;
+          if constexpr (KIND == LG_F16) {
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+              const _Float16 *h0 = reinterpret_cast<const _Float16 *>(&wd[2 * p]);
+              const _Float16 *h1 = reinterpret_cast<const _Float16 *>(&wd[2 * p + 1]);
+              d += float(h0[0]) * xv[p].x + float(h0[1]) * xv[p].y + float(h1[0]) * xv[p].z +
+                   float(h1[1]) * xv[p].w;
+            }
+            acc[r] += d;
+          } else {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+              const uint32_t word = wd[p];
+              d += float(int8_t(word)) * xv[p].x + float(int8_t(word >> 8)) * xv[p].y +
+                   float(int8_t(word >> 16)) * xv[p].z + float(int8_t(word >> 24)) * xv[p].w;
+            }
+            acc[r] += sc[i] * d;
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int o = o0 + r;
+    if (EPI == int(Epi::SWIGLU)) {
+      const float gsum = wave_sum(acc[r * 2]);
+      const float usum = wave_sum(acc[r * 2 + 1]);
+      if (lane == 0 && o < outputs) y[o] = silu(gsum) * usum;
+    } else {
+      const float v = wave_sum(acc[r]);
+      if (lane == 0 && o < outputs) {
+        if (EPI == int(Epi::ADD)) y[o] += v;
+        else y[o] = v + (bias ? bias[o] : 0.0f);
+      }
     }
   }
 }
@@ -212,22 +245,47 @@ __global__ __launch_bounds__(kThreads) void gemv_generic_kernel(const float *__r
   }
 }
 
+template <uint32_t KIND, int EPI, int R, int CPL>
+void launch_rc(const float *x, const DevMatrix &W, float *y, const float *bias, const float *norm_w, float eps,
+               int outputs, hipStream_t st) {
+  const int per_block = (kThreads / 64) * R;
+  const dim3 grid((outputs + per_block - 1) / per_block), block(kThreads);
+  const size_t lds = size_t(W.cols) * sizeof(float);
+  hipLaunchKernelGGL((gemv_kernel<KIND, EPI, R, CPL>), grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
+}
+
+template <uint32_t KIND, int EPI, int R>
+void launch_r(int cpl, const float *x, const DevMatrix &W, float *y, const float *bias, const float *norm_w,
+              float eps, int outputs, hipStream_t st) {
+  switch (cpl) {
+    case 2: launch_rc<KIND, EPI, R, 2>(x, W, y, bias, norm_w, eps, outputs, st); break;
+    case 4: launch_rc<KIND, EPI, R, 4>(x, W, y, bias, norm_w, eps, outputs, st); break;
+    default: launch_rc<KIND, EPI, R, 8>(x, W, y, bias, norm_w, eps, outputs, st); break;
+  }
+}
+
+template <uint32_t KIND, int EPI>
+void launch_e(const float *x, const DevMatrix &W, float *y, const float *bias, const float *norm_w, float eps,
+              hipStream_t st) {
+  const int outputs = EPI == int(Epi::SWIGLU) ? W.rows / 2 : W.rows;
+  const int nchunk = W.cols / chunk_elems<KIND>();
+  const int cpl = nchunk <= 128 ? 2 : nchunk <= 256 ? 4 : 8;
+  // rows per wave: as many as keep >= 512 workgroups (two per CU) in the grid
+  const int r = outputs >= 4 * 4 * 512 ? 4 : outputs >= 4 * 2 * 512 ? 2 : 1;
+  switch (r) {
+    case 4: launch_r<KIND, EPI, 4>(cpl, x, W, y, bias, norm_w, eps, outputs, st); break;
+    case 2: launch_r<KIND, EPI, 2>(cpl, x, W, y, bias, norm_w, eps, outputs, st); break;
+    default: launch_r<KIND, EPI, 1>(cpl, x, W, y, bias, norm_w, eps, outputs, st); break;
+  }
+}
+
 template <uint32_t KIND>
 void launch_gemv_kind(const float *x, const DevMatrix &W, Epi epi, float *y, const float *bias,
                       const float *norm_w, float eps, hipStream_t st) {
-  const int outputs = epi == Epi::SWIGLU ? W.rows / 2 : W.rows;
-  const dim3 grid((outputs + 3) / 4), block(kThreads);
-  const size_t lds = size_t(W.cols) * sizeof(float);
   switch (epi) {
-    case Epi::F32:
-      hipLaunchKernelGGL((gemv_kernel<KIND, 0>), grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
-      break;
-    case Epi::ADD:
-      hipLaunchKernelGGL((gemv_kernel<KIND, 1>), grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
-      break;
-    case Epi::SWIGLU:
-      hipLaunchKernelGGL((gemv_kernel<KIND, 3>), grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
-      break;
+    case Epi::F32: launch_e<KIND, 0>(x, W, y, bias, norm_w, eps, st); break;
+    case Epi::ADD: launch_e<KIND, 1>(x, W, y, bias, norm_w, eps, st); break;
+    case Epi::SWIGLU: launch_e<KIND, 3>(x, W, y, bias, norm_w, eps, st); break;
     default: fail(LG_ERR_UNSUPPORTED, "gemv: f16 epilogue not supported");
   }
 }

@@ -102,7 +102,8 @@ void launch_attn_prefill(const _Float16 *q16, const _Float16 *q16_lo, int T, int
                          hipStream_t st);
 
 // Decode attention: one query row per sequence (batch nseq), context length ctx_len[s]
-// (including the current token), split over pages, then combined.
+// (including the current token), split over pages into `part`
+// (attn_decode_scratch_floats), then combined per (sequence, query head) by a second launch.
 void launch_attn_decode(const float *q32, int nseq, int hq, const KvGeom &g, const void *kpool,
                         const void *vpool, const int32_t *pages, int max_pages,
                         const int32_t *ctx_len, int max_ctx, float *part, float *out,
