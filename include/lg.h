@@ -191,6 +191,14 @@ int lg_decode(lg_engine *e, int seq, int32_t first, int steps, int32_t *tokens, 
 int lg_option_scores(const float *logits, int k, float temperature, float *probs,
                      float *logprobs);
 
+/* Decision confidence of k option probabilities: 1 - H(p)/ln k clamped to [0,1] (1 when
+ * k <= 1), p floored at 1e-12 inside the entropy.  mode 0 computes in f32 with logf, as
+ * src/models/openthai/decision.rs:304-313; mode 1 accumulates in f64, as
+ * src/models/laya/decision.rs:155-167. */
+#define LG_CONF_F32 0
+#define LG_CONF_F64 1
+int lg_option_confidence(const float *probs, int k, int mode, float *confidence);
+
 /* ---- profiling: per-kernel-class HIP event timing on the engine's stream ---- */
 /* When on, every launch of the timed kernel classes is bracketed by HIP events. */
 int lg_profile_enable(lg_engine *e, int on);

@@ -380,6 +380,38 @@ int lg_option_scores(const float *logits, int k, float temperature, float *probs
   });
 }
 
+int lg_option_confidence(const float *probs, int k, int mode, float *confidence) {
+  return guard([&] {
+    NEED(probs, "probs");
+    NEED(confidence, "confidence");
+    LG_REQUIRE(k >= 0, "k must be non-negative");
+    LG_REQUIRE(mode == LG_CONF_F32 || mode == LG_CONF_F64, "unknown confidence mode %d", mode);
+    if (k <= 1) {
+      *confidence = 1.0f;
+      return;
+    }
+    if (mode == LG_CONF_F64) {
+      double h = -0.0;
+      for (int i = 0; i < k; ++i) {
+        const double x = std::fmax(double(probs[i]), 1e-12);
+        h -= x * std::log(x);
+      }
+      double c = 1.0 - h / std::log(double(k));
+      c = c < 0.0 ? 0.0 : (c > 1.0 ? 1.0 : c);
+      *confidence = float(c);
+    } else {
+      float h = -0.0f;
+      for (int i = 0; i < k; ++i) {
+        const float x = std::fmax(probs[i], 1e-12f);
+        h -= x * std::log(x);
+      }
+      float c = 1.0f - h / std::log(float(k));
+      c = c < 0.0f ? 0.0f : (c > 1.0f ? 1.0f : c);
+      *confidence = c;
+    }
+  });
+}
+
 int lg_profile_enable(lg_engine *e, int on) {
   return guard([&] {
     NEED(e, "engine");

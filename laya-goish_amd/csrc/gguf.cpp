@@ -216,12 +216,15 @@ void Gguf::parse() {
     index_[t.name] = order_.size();
     order_.push_back(std::move(t));
   }
-  const MetaValue *a = meta("general.alignment");
-  double av = a ? (a->type == 8 || a->type == 9 ? 0 : a->num) : 32;
-  const uint64_t align = av < 0 ? 0 : uint64_t(av);
+  // general.alignment as a number (a bool, string or array counts as 0), converted to an
+  // integer the saturating way (NaN and negatives -> 0), default 32 (src/gguf.rs:158-165)
+  const double av = num("general.alignment", 32);
+  const uint64_t align = !(av > 0) ? 0 : av >= 18446744073709551616.0 ? UINT64_MAX : uint64_t(av);
   if (align == 0 || (align & (align - 1)) || align > 4096) fail(LG_ERR_FORMAT, "invalid GGUF alignment");
   const uint64_t base = (r.p + align - 1) & ~(align - 1);
-  for (auto &t : order_) {
+  // relocation and bounds checks in name order, like the reference's BTreeMap walk
+  for (const auto &kv : index_) {
+    TensorInfo &t = order_[kv.second];
     if (t.offset % align) fail(LG_ERR_FORMAT, "unaligned GGUF tensor");
     if (t.offset + base < t.offset) fail(LG_ERR_FORMAT, "offset overflow");
     t.offset += base;
@@ -238,7 +241,7 @@ const MetaValue *Gguf::meta(const std::string &key) const {
 double Gguf::num(const std::string &key, double dflt) const {
   const MetaValue *v = meta(key);
   if (!v) return dflt;
-  return (v->type == 8 || v->type == 9) ? 0.0 : v->num;
+  return (v->type == 7 || v->type == 8 || v->type == 9) ? 0.0 : v->num;  // J::num(): numbers only
 }
 
 std::string Gguf::str(const std::string &key) const {

@@ -104,6 +104,7 @@ def lib() -> ctypes.CDLL:
             "lg_batch_rewind": (I, [P, P]),
             "lg_decode": (I, [P, I, ctypes.c_int32, I, P, P]),
             "lg_option_scores": (I, [P, I, F, P, P]),
+            "lg_option_confidence": (I, [P, I, I, ctypes.POINTER(F)]),
             "lg_profile_enable": (I, [P, I]),
             "lg_profile_read": (I, [P, ctypes.c_char_p, ctypes.POINTER(I64), ctypes.POINTER(ctypes.c_double),
                                     ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
@@ -162,6 +163,17 @@ def option_scores(logits, temperature: float = 1.0):
     lp = np.empty_like(z)
     check(lib().lg_option_scores(_ptr(z), z.size, temperature, _ptr(p), _ptr(lp)))
     return p, lp
+
+
+CONF_F32, CONF_F64 = 0, 1
+
+
+def option_confidence(probs, mode: int = CONF_F32) -> float:
+    """1 - H(p)/ln k (decision confidence); mode CONF_F32 or CONF_F64."""
+    p = _c(probs, np.float32)
+    out = ctypes.c_float()
+    check(lib().lg_option_confidence(_ptr(p), p.size, mode, ctypes.byref(out)))
+    return out.value
 
 
 class SynthImage:

@@ -343,19 +343,28 @@ or_gguf *or_gguf_open(const uint8_t *bytes, uint64_t n, char *err, int errlen) {
     }
   }
   if (!r.failed) {
+    /* `v.num() as usize`, src/gguf.rs:158-165: non-numbers read 0, the cast saturates */
     double a = or_gguf_num(g, "general.alignment", 32);
-    uint64_t align = a < 0 ? 0 : (uint64_t)a;
+    uint64_t align = !(a > 0) ? 0 : a >= 18446744073709551616.0 ? UINT64_MAX : (uint64_t)a;
     if (align == 0 || (align & (align - 1)) || align > 4096) fail(&r, "invalid GGUF alignment");
     else {
       uint64_t base = (r.p + align - 1) & ~(align - 1);
+      /* the reference walks its BTreeMap, i.e. tensors in name order */
+      int *ord = (int *)malloc(sizeof(int) * (size_t)(g->nt ? g->nt : 1));
+      for (int i = 0; i < g->nt; ++i) ord[i] = i;
+      for (int i = 1; i < g->nt; ++i) /* insertion sort by name (byte order) */
+        for (int j = i; j > 0 && strcmp(g->t[ord[j - 1]].name, g->t[ord[j]].name) > 0; --j) {
+          int x = ord[j]; ord[j] = ord[j - 1]; ord[j - 1] = x;
+        }
       for (int i = 0; i < g->nt && !r.failed; ++i) {
-        or_tensor *t = &g->t[i];
+        or_tensor *t = &g->t[ord[i]];
         if (t->offset % align) { fail(&r, "unaligned GGUF tensor"); break; }
         if (t->offset + base < t->offset) { fail(&r, "offset overflow"); break; }
         t->offset += base;
         if (t->offset + t->len < t->offset) { fail(&r, "length overflow"); break; }
         if (t->offset + t->len > n) { fail(&r, "truncated tensor data"); break; }
       }
+      free(ord);
     }
   }
   if (r.failed) { or_gguf_close(g); return NULL; }
@@ -381,7 +390,8 @@ int or_gguf_tensor(const or_gguf *g, const char *name, uint32_t *kind, uint64_t 
 
 double or_gguf_num(const or_gguf *g, const char *key, double dflt) {
   for (int i = 0; i < g->nmeta; ++i)
-    if (!strcmp(g->meta[i].key, key)) return g->meta[i].type == 8 || g->meta[i].type == 9 ? 0 : g->meta[i].num;
+    if (!strcmp(g->meta[i].key, key))  /* J::num(): only numbers have a value */
+      return g->meta[i].type == 7 || g->meta[i].type == 8 || g->meta[i].type == 9 ? 0 : g->meta[i].num;
   return dflt;
 }
 
@@ -920,4 +930,30 @@ void or_option_scores(const float *logits, int k, float abstain_logit, int has_a
     float lse = logf(t);
     for (int i = 0; i < kk; ++i) logprobs[i] = z[i] - m - lse;
   }
+}
+
+float or_confidence(const float *p, int k, int f64) {
+  if (k <= 1) return 1.0f;
+  if (f64) {
+    /* laya/decision.rs:159-166: x = max(p, 1e-12) in f64, e = -sum x*ln x (left to right) */
+    double s = -0.0;
+    for (int i = 0; i < k; ++i) {
+      double x = fmax((double)p[i], 1e-12); /* f64::max: a NaN operand yields the other */
+      s = s + x * log(x);
+    }
+    double c = 1.0 - (-s) / log((double)k);
+    if (c < 0.0) c = 0.0;
+    if (c > 1.0) c = 1.0;
+    return (float)c;
+  }
+  /* openthai/decision.rs:304-313: all in f32 with logf */
+  float s = -0.0f;
+  for (int i = 0; i < k; ++i) {
+    float x = fmaxf(p[i], 1e-12f);
+    s = s + x * logf(x);
+  }
+  float c = 1.0f - (-s) / logf((float)k);
+  if (c < 0.0f) c = 0.0f;
+  if (c > 1.0f) c = 1.0f;
+  return c;
 }

@@ -83,6 +83,10 @@ int or_argmax(const float *v, int n);
  * src/models/openthai/decision.rs:268-279,297-303. */
 void or_option_scores(const float *logits, int k, float abstain_logit, int has_abstain,
                       float temperature, float *probs, float *logprobs, float *abstain);
+/* Decision confidence 1 - H(p)/ln k, clamped to [0,1]; 1 when k <= 1.
+ * f64 = 0: f32 entropy with logf, src/models/openthai/decision.rs:304-313.
+ * f64 = 1: f64 entropy with log, src/models/laya/decision.rs:155-167. */
+float or_confidence(const float *p, int k, int f64);
 
 #ifdef __cplusplus
 }

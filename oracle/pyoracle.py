@@ -52,6 +52,7 @@ def lib() -> ctypes.CDLL:
             "or_head": (I, [P, P, I, P, I, P]),
             "or_argmax": (I, [P, I]),
             "or_option_scores": (None, [P, I, F, I, F, P, P, P]),
+            "or_confidence": (F, [P, I, I]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -137,6 +138,11 @@ def option_scores(logits, temperature=1.0, abstain=None):
     lib().or_option_scores(_p(z), z.size, 0.0 if abstain is None else abstain, 0 if abstain is None else 1,
                            temperature, _p(p), _p(lp), ctypes.byref(ab))
     return p, lp, ab.value
+
+
+def confidence(p, f64=False) -> float:
+    p = _c(p, np.float32)
+    return lib().or_confidence(_p(p), p.size, 1 if f64 else 0)
 
 
 class Gguf:

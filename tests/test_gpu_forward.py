@@ -167,6 +167,21 @@ def test_errors_are_reported(pair, lh):
 
 
 @pytest.mark.parametrize("prec", [0, 1], ids=["exact", "fast"])
+def test_golden_logits(lh, prec):
+    """The committed float64 brute-force logits (tests/golden/forward_tiny.npz)."""
+    import os
+    gold = np.load(os.path.join(os.path.dirname(__file__), "golden", "forward_tiny.npz"), allow_pickle=False)
+    for preset in ("tiny-f16", "tiny-q8", "tiny-q4k"):
+        img = lh.SynthImage(preset, seed=int(gold["seed"]))
+        eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=1024, precision=prec)
+        got = eng.forward(eng.seq_create(), gold[f"{preset}/ids"], gold[f"{preset}/pos"])
+        err = assert_logits_close(got, gold[f"{preset}/logits"])
+        assert_argmax_equal(got, gold[f"{preset}/logits"])
+        print(f"{preset} prec {prec}: golden rel {err:.2e}")
+        eng.close()
+
+
+@pytest.mark.parametrize("prec", [0, 1], ids=["exact", "fast"])
 def test_plumbing_model_decision(lh, po, prec):
     """The CPU-runnable plumbing model: 128-token prompt + one yes/no question block."""
     img = lh.SynthImage("plumbing-f16", seed=1)
