@@ -37,8 +37,24 @@ REQUESTS, PROMPT, QBLOCK, QUESTIONS, OPTIONS = 64, 512, 16, 3, 4
 DECODE_CTX, DECODE_STEPS = 2048, 64
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_q8-2048_bench.md")
+
+
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed FETCH_SIZE + WRITE_SIZE counter runs of
+    this workload (lines `traffic.<kernel> <bytes>`), or None when that summary is absent."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            parts = line.split()
+            if len(parts) == 2 and parts[0] == f"traffic.{kernel}":
+                return int(parts[1])
+    except OSError:
+        pass
+    return None
 
 
 def prefill_workload(vocab):
@@ -84,7 +100,7 @@ def bench_prefill(eng, steps, warmup):
     return T, dt, prof, probs
 
 
-def bench_decode(eng):
+def bench_decode(eng, steps):
     rng = np.random.default_rng(SEED + 1)
     ids = rng.integers(0, eng.info["vocab"], DECODE_CTX).astype(np.int32)
     base = eng.seq_create()
@@ -98,7 +114,7 @@ def bench_decode(eng):
             eng.profile(True)
         eng.sync()
         t0 = time.perf_counter()
-        toks = eng.decode(s, first, DECODE_STEPS)
+        toks = eng.decode(s, first, steps)
         eng.sync()
         runs.append((mode, time.perf_counter() - t0, toks))
         if mode == "profiled":
@@ -111,9 +127,9 @@ def bench_decode(eng):
     return dt, prof
 
 
-def cpu_baseline(threads, layers=4):
-    """The oracle on a bounded sample: one 560-token request through `layers` of the 24
-    layers (per-layer cost is identical), scaled to the full model."""
+def cpu_baseline(threads, layers=24):
+    """The oracle on a bounded sample: one 560-token request of the workload through `layers`
+    of the 24 layers (per-layer cost is identical), scaled to the full model."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle as po
 
@@ -125,14 +141,15 @@ def cpu_baseline(threads, layers=4):
     om.forward(ids, pos, option_ids)
     dt = time.perf_counter() - t0
     scale = 24 / layers
+    depth = "all 24 layers" if layers == 24 else f"{layers} of 24 layers, time scaled x{scale:g}"
     return {
         "value": round(len(ids) / (dt * scale), 2),
         "unit": "tok/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"1 request x {len(ids)} tokens through {layers} of 24 layers in {dt:.2f} s, "
-                  f"scaled x{scale:g} to the full model; C restatement of the reference CPU algorithm "
-                  f"(F32 weights expanded at load, 4-row x 8-lane FMA kernel, rows split over "
+        "sample": f"1 of the {REQUESTS} requests ({len(ids)} tokens, {QUESTIONS} answer positions, "
+                  f"{OPTIONS} options) through {depth}: {dt:.2f} s; C restatement of the reference CPU "
+                  f"algorithm (F32 weights expanded at load, 4-row x 8-lane FMA kernel, rows split over "
                   f"{threads} threads)",
     }
 
@@ -145,7 +162,13 @@ def main():
     ap.add_argument("--precision", choices=["exact", "fast"], default="exact")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--decode-steps", type=int, default=DECODE_STEPS,
+                    help="greedy steps per decode run (fewer keeps counter-collection runs short)")
     ap.add_argument("--cpu-threads", type=int, default=4)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="first run the F32 dequant kernel over MIB MiB: a plain copy (4 B read, 4 B written "
+                         "per element), so a counter profile of this command also holds the kernel that "
+                         "scales FETCH_SIZE / WRITE_SIZE to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {args.gpus}); "
@@ -153,6 +176,12 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     prec = lh.PREC_EXACT if args.precision == "exact" else lh.PREC_FAST
+    if args.copy_calibration > 0:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = np.arange(n, dtype=np.float32)
+        for _ in range(2):
+            assert np.array_equal(lh.dequant(lh.F32, src.view(np.uint8)), src)
+        log(f"copy calibration: 2 launches of the F32 dequant kernel, {n * 4} B read + {n * 4} B written each")
     log(f"generating {PRESET} (seed {SEED})")
     t0 = time.perf_counter()
     img = lh.SynthImage(PRESET, seed=SEED)
@@ -203,23 +232,25 @@ def main():
             "peak": PEAK_F16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(gemm_tflops / PEAK_F16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic("gemm"),
+            "traffic_source": "profiles/hbm_traffic_q8-2048_bench.md (FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
             "launches": gp["launches"],
             "avg_launch_ms": round(gp["ms"] / max(1, gp["launches"]), 4),
             "algorithmic_flops_per_step": gp["flops"],
         },
     }
     if not args.no_decode:
-        ddt, dprof = bench_decode(eng)
+        ddt, dprof = bench_decode(eng, args.decode_steps)
         gv = dprof["gemv"]
         gemv_gbs = gv["bytes"] / (gv["ms"] * 1e-3) / 1e9 if gv["ms"] else 0.0
-        log(f"decode: {ddt / DECODE_STEPS * 1e3:.3f} ms/token, gemv {gemv_gbs:.0f} GB/s over {gv['launches']} launches")
+        log(f"decode: {ddt / args.decode_steps * 1e3:.3f} ms/token, gemv {gemv_gbs:.0f} GB/s over {gv['launches']} launches")
         for c, p in dprof.items():
             log(f"  {c:12s} launches {p['launches']:5d}  {p['ms']:8.3f} ms")
         line["decode"] = {
-            "workload": f"Q8_0 batch-1 greedy decode: {DECODE_CTX}-token context, {DECODE_STEPS} steps, same model",
-            "tok_per_s": round(DECODE_STEPS / ddt, 2),
-            "ms_per_token": round(ddt / DECODE_STEPS * 1e3, 4),
+            "workload": f"Q8_0 batch-1 greedy decode: {DECODE_CTX}-token context, {args.decode_steps} steps, "
+                        f"same model",
+            "tok_per_s": round(args.decode_steps / ddt, 2),
+            "ms_per_token": round(ddt / args.decode_steps * 1e3, 4),
             "roofline": {
                 "bound": "hbm",
                 "kernel": "gemv (dequant-fused Q8_0 GEMV, GGUF bytes per launch)",
@@ -227,7 +258,7 @@ def main():
                 "peak": PEAK_HBM_GBS,
                 "unit": "GB/s",
                 "frac": round(gemv_gbs / PEAK_HBM_GBS, 4),
-                "traffic": None,
+                "traffic": measured_traffic("gemv"),
                 "launches": gv["launches"],
                 "avg_launch_ms": round(gv["ms"] / max(1, gv["launches"]), 5),
             },
