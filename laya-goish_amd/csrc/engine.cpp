@@ -647,8 +647,8 @@ void Engine::run_layers_prefill(BatchPlan &b, lg_cancel_fn cancel, void *arg) {
     for (const ProjPart &p : ly.qkv)
       gemm(h16, h16lo, T, p.w, Epi::F32, qkv + p.col0, nullptr, nullptr, qkvw, p.bias);
     prof.begin("rope_kv", stream);
-    launch_rope_kv(qkv, T, hq, g, cos_, sin_, b.tok_seq, b.tok_pos, b.pages, b.max_pages, q16, q16lo,
-                   nullptr, kpool(l), vpool(l), stream);
+    launch_rope_kv_tiles(qkv, hq, g, cos_, sin_, b.pages, b.max_pages, b.tile_seq, b.tile_row0,
+                         b.tile_pos0, b.tile_n, b.ntiles, q16, q16lo, kpool(l), vpool(l), stream);
     prof.end(double(T) * (qkvw * 4 + qw * 2 * planes + 2 * kvw * kv_elem()), 0, stream);
     prof.begin("attn_prefill", stream);
     launch_attn_prefill(q16, q16lo, T, hq, g, kpool(l), vpool(l), b.pages, b.max_pages, b.tile_seq,

@@ -15,7 +15,7 @@
 //
 // Decode: one workgroup per (sequence, kv head, page): coalesced reads of the page's K rows
 // and V columns, f32 scores for every query head of the group, partial (max, sum, out) per
-// page; the last workgroup of each (sequence, kv head) combines the pages.
+// page; a second launch combines the pages of each (sequence, query head).
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -55,7 +55,13 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(
   using KV = typename std::conditional<SPLIT, float, _Float16>::type;
   constexpr int KT = HD / 16;  // k-steps of the QK^T product
   constexpr int DB = HD / 32;  // 32-wide d blocks of the output
-  const int tile = blockIdx.x, h = blockIdx.y;
+  // Workgroups are dealt to the 8 XCDs round-robin (i -> XCD i % 8).  Map them so each XCD
+  // takes one contiguous range of (head, tile) pairs, tiles fastest: all query tiles of one
+  // (sequence, head) then run on one XCD and read that sequence's K/V through one L2.
+  const int total = gridDim.x, ntiles = total / hq;
+  const int xcd = blockIdx.x % 8, per = total / 8, rem = total % 8;
+  const int logical = xcd * per + min(xcd, rem) + blockIdx.x / 8;
+  const int tile = logical % ntiles, h = logical / ntiles;
   const int lane = threadIdx.x, qi = lane & 31, hl = lane >> 5;
   const int seq = tile_seq[tile], row0 = tile_row0[tile], pos0 = tile_pos0[tile], n = tile_n[tile];
   const int kh = h / (hq / g.hkv);
@@ -379,7 +385,8 @@ void launch_attn_prefill(const _Float16 *q16, const _Float16 *q16_lo, int T, int
   const bool split = q16_lo != nullptr;
   LG_REQUIRE(split == (g.kv32 != 0), "attention: split queries need the f32 cache and vice versa");
   LG_REQUIRE(!split || out16_lo, "attention: split path needs the lo output plane");
-  const dim3 grid(ntiles, hq), block(64);
+  LG_REQUIRE(int64_t(ntiles) * hq < (1ll << 31), "attention: too many tiles");
+  const dim3 grid(ntiles * hq), block(64);
 #define LAUNCH(HDV, S)                                                                              \
   hipLaunchKernelGGL((attn_prefill_kernel<HDV, S>), grid, block, 0, st, q16, q16_lo, hq, g, kpool, vpool, \
                      pages, max_pages, tile_seq, tile_row0, tile_pos0, tile_n, out16, out16_lo)

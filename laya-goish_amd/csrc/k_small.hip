@@ -113,6 +113,71 @@ __global__ __launch_bounds__(kT) void rope_kv_kernel(const float *__restrict__ q
   }
 }
 
+// Prefill form: one workgroup per attention tile (<= 32 consecutive tokens of one sequence).
+// q and k are rotated token by token (rows are contiguous); v is staged through LDS per kv
+// head so that its transposed page layout is written as runs of consecutive slots instead of
+// one 4-byte store per cache line.
+template <typename KV>
+__global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
+    const float *__restrict__ qkv, int hq, KvGeom g, const float *__restrict__ cosT,
+    const float *__restrict__ sinT, const int32_t *__restrict__ pages, int max_pages,
+    const int32_t *__restrict__ tile_seq, const int32_t *__restrict__ tile_row0,
+    const int32_t *__restrict__ tile_pos0, const int32_t *__restrict__ tile_n,
+    _Float16 *__restrict__ q16, _Float16 *__restrict__ q16lo, KV *__restrict__ kpool,
+    KV *__restrict__ vpool) {
+  constexpr int TT = 32, HDMAX = 128;
+  __shared__ float vs[TT][HDMAX + 1];
+  const int tile = blockIdx.x, tid = threadIdx.x;
+  const int row0 = tile_row0[tile], pos0 = tile_pos0[tile], n = tile_n[tile];
+  const int32_t *ptab = pages + int64_t(tile_seq[tile]) * max_pages;
+  const int hd = g.hd, half = hd / 2;
+  const int qw = hq * hd, kvw = g.hkv * hd, rw = qw + 2 * kvw;
+  for (int tk = 0; tk < n; ++tk) {
+    const float *row = qkv + int64_t(row0 + tk) * rw;
+    const int pos = pos0 + tk;
+    const float *cs = cosT + int64_t(pos) * hd, *sn = sinT + int64_t(pos) * hd;
+    for (int i = tid; i < hq * half; i += kT) {
+      const int h = i / half, j = i % half;
+      const float u = row[h * hd + j], v = row[h * hd + j + half];
+      const float a = u * cs[j] - v * sn[j], b = v * cs[j + half] + u * sn[j + half];
+      const int64_t at = int64_t(row0 + tk) * qw + h * hd + j;
+      const _Float16 ah = _Float16(a), bh = _Float16(b);
+      q16[at] = ah;
+      q16[at + half] = bh;
+      if (q16lo) {
+        q16lo[at] = _Float16(a - float(ah));
+        q16lo[at + half] = _Float16(b - float(bh));
+      }
+    }
+    KV *kp = kpool + int64_t(ptab[pos / g.page_tokens]) * g.page_stride;
+    const int slot = pos % g.page_tokens;
+    for (int i = tid; i < g.hkv * half; i += kT) {
+      const int h = i / half, j = i % half;
+      const float u = row[qw + h * hd + j], v = row[qw + h * hd + j + half];
+      KV *dst = kp + (int64_t(h) * g.page_tokens + slot) * hd;
+      dst[j] = KV(u * cs[j] - v * sn[j]);
+      dst[j + half] = KV(v * cs[j + half] + u * sn[j + half]);
+    }
+  }
+  for (int h = 0; h < g.hkv; ++h) {
+    for (int i = tid; i < n * hd; i += kT) {
+      const int tk = i / hd, dd = i % hd;
+      vs[tk][dd] = qkv[int64_t(row0 + tk) * rw + qw + kvw + h * hd + dd];
+    }
+    __syncthreads();
+    // thread -> (dim, token) with the token fastest: 32 consecutive slots per dim row
+    for (int i = tid; i < TT * hd; i += kT) {
+      const int tk = i % TT, dd = i / TT;
+      if (tk < n) {
+        const int pos = pos0 + tk;
+        KV *vp = vpool + int64_t(ptab[pos / g.page_tokens]) * g.page_stride;
+        vp[(int64_t(h) * hd + dd) * g.page_tokens + pos % g.page_tokens] = KV(vs[tk][dd]);
+      }
+    }
+    __syncthreads();
+  }
+}
+
 __device__ float weight_at_head(const DevMatrix &W, int64_t n, int64_t k) {
   const int64_t cols = W.cols;
   switch (W.kind) {
@@ -305,6 +370,23 @@ void launch_rope_kv(const float *qkv, int T, int hq, const KvGeom &g, const floa
     hipLaunchKernelGGL(rope_kv_kernel<_Float16>, dim3(T), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, tok_seq,
                        tok_pos, pages, max_pages, q16, q16_lo, q32, static_cast<_Float16 *>(kpool),
                        static_cast<_Float16 *>(vpool));
+  HIP_CHECK(hipGetLastError());
+}
+
+void launch_rope_kv_tiles(const float *qkv, int hq, const KvGeom &g, const float *cosT,
+                          const float *sinT, const int32_t *pages, int max_pages,
+                          const int32_t *tile_seq, const int32_t *tile_row0, const int32_t *tile_pos0,
+                          const int32_t *tile_n, int ntiles, _Float16 *q16, _Float16 *q16_lo,
+                          void *kpool, void *vpool, hipStream_t st) {
+  LG_REQUIRE(ntiles > 0 && g.hd % 2 == 0 && g.hd <= 128 && q16, "rope_kv: bad arguments");
+  if (g.kv32)
+    hipLaunchKernelGGL(rope_kv_tile_kernel<float>, dim3(ntiles), dim3(kT), 0, st, qkv, hq, g, cosT, sinT,
+                       pages, max_pages, tile_seq, tile_row0, tile_pos0, tile_n, q16, q16_lo,
+                       static_cast<float *>(kpool), static_cast<float *>(vpool));
+  else
+    hipLaunchKernelGGL(rope_kv_tile_kernel<_Float16>, dim3(ntiles), dim3(kT), 0, st, qkv, hq, g, cosT, sinT,
+                       pages, max_pages, tile_seq, tile_row0, tile_pos0, tile_n, q16, q16_lo,
+                       static_cast<_Float16 *>(kpool), static_cast<_Float16 *>(vpool));
   HIP_CHECK(hipGetLastError());
 }
 

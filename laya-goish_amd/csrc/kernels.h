@@ -89,6 +89,13 @@ void launch_rope_kv(const float *qkv, int T, int hq, const KvGeom &g, const floa
                     const float *sinT, const int32_t *tok_seq, const int32_t *tok_pos,
                     const int32_t *pages, int max_pages, _Float16 *q16, _Float16 *q16_lo,
                     float *q32, void *kpool, void *vpool, hipStream_t st);
+// The same for a prefill batch, one workgroup per attention tile (<= 32 consecutive tokens
+// of one sequence, rows row0.., positions pos0..); q goes to f16 planes.  head_dim <= 128.
+void launch_rope_kv_tiles(const float *qkv, int hq, const KvGeom &g, const float *cosT,
+                          const float *sinT, const int32_t *pages, int max_pages,
+                          const int32_t *tile_seq, const int32_t *tile_row0, const int32_t *tile_pos0,
+                          const int32_t *tile_n, int ntiles, _Float16 *q16, _Float16 *q16_lo,
+                          void *kpool, void *vpool, hipStream_t st);
 
 // Causal prefill attention over the paged cache.  Work items: tiles of 32 query rows of one
 // sequence (tile_seq, tile_row0 = first batch row, tile_pos0 = its position, tile_n rows).
