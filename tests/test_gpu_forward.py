@@ -140,8 +140,9 @@ def test_decode_teacher_forced(pair, po):
     ties = 0
     for i, t in enumerate(feed):
         want = om.head(om.prefill(c, [t], [0]))
-        assert_logits_close(logits[i], want)
-        ties += assert_argmax_equal(logits[i][None], want)
+        err = assert_logits_close(logits[i], want)
+        # near-ties: top-2 gap under 50x the observed error (at least 1e-4 of the top logit)
+        ties += assert_argmax_equal(logits[i][None], want, rel=max(1e-4, 50 * err))
         assert int(toks[i]) == int(np.argmax(logits[i]))
     print(f"{preset}: decode near-ties {ties}")
     eng.seq_free(s)
