@@ -733,13 +733,11 @@ void Engine::decode(int sq, int32_t first, int steps, int32_t *tokens, float *lo
   reserve_pages(s, pos0 + steps);
   const int qw = hq * hd, kvw = hkv * hd, qkvw = qw + 2 * kvw;
   const int max_pages = int(s.pages.size());
-  // per-step metadata, uploaded once: token slots, positions, context lengths, page table
+  // device metadata, uploaded once: token slots (step i reads slot i, its argmax goes to slot
+  // i + 1) and the page table; positions and context lengths travel as kernel arguments
   std::vector<int32_t> meta;
   meta.push_back(first);
-  meta.resize(steps + 1, 0);                 // [0, steps]: token ids (step i reads slot i)
-  for (int i = 0; i < steps; ++i) meta.push_back(pos0 + i);       // positions
-  for (int i = 0; i < steps; ++i) meta.push_back(pos0 + i + 1);   // context lengths
-  meta.push_back(0);                                                // tok_seq (batch index 0)
+  meta.resize(steps + 1, 0);
   for (int p : s.pages) meta.push_back(p);
   const size_t part_floats = size_t(attn_decode_scratch_floats(1, hq, hd, pos0 + steps));
   const size_t floats = size_t(d) + qkvw + qw + qw + f + V + 64 + part_floats;
@@ -749,7 +747,7 @@ void Engine::decode(int sq, int32_t first, int steps, int32_t *tokens, float *lo
   float *part_v = lg + V;
   float *part = part_v + 64;
   int32_t *dm = reinterpret_cast<int32_t *>(part + part_floats);
-  int32_t *tok = dm, *pos = dm + steps + 1, *clen = pos + steps, *tseq = clen + steps, *pt = tseq + 1;
+  int32_t *tok = dm, *pt = dm + steps + 1;
   int32_t *part_i = pt + max_pages;
   HIP_CHECK(hipMemcpyAsync(dm, meta.data(), meta.size() * 4, hipMemcpyHostToDevice, stream));
   const KvGeom g = geom();
@@ -760,12 +758,13 @@ void Engine::decode(int sq, int32_t first, int steps, int32_t *tokens, float *lo
     for (int l = 0; l < L; ++l) {
       const Layer &ly = layers_[l];
       for (const ProjPart &p : ly.qkv) gemv(x, p.w, Epi::F32, qkv + p.col0, p.bias, ly.attn_norm);
+      // position, page and context length of this step are known here: kernel arguments
       prof.begin("rope_kv", stream);
-      launch_rope_kv(qkv, 1, hq, g, cos_, sin_, tseq, pos + i, pt, max_pages, nullptr, nullptr, q32,
-                     kpool(l), vpool(l), stream);
+      launch_rope_kv_token(qkv, hq, g, cos_, sin_, pos0 + i, s.pages[(pos0 + i) / g.page_tokens], q32,
+                           kpool(l), vpool(l), stream);
       prof.end(double(qkvw) * 4 + double(2 * kvw) * kv_elem(), 0, stream);
       prof.begin("attn_decode", stream);
-      launch_attn_decode(q32, 1, hq, g, kpool(l), vpool(l), pt, max_pages, clen + i, pos0 + i + 1,
+      launch_attn_decode(q32, 1, hq, g, kpool(l), vpool(l), pt, max_pages, nullptr, pos0 + i + 1,
                          part, att, stream);
       prof.end(double(pos0 + i + 1) * 2 * kvw * kv_elem(), 4.0 * double(pos0 + i + 1) * qw, stream);
       gemv(att, ly.wo, Epi::ADD, x, nullptr, nullptr);

@@ -221,12 +221,12 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float *__restric
                                                           const KV *__restrict__ vpool,
                                                           const int32_t *__restrict__ pages,
                                                           int max_pages,
-                                                          const int32_t *__restrict__ ctx_len,
+                                                          const int32_t *__restrict__ ctx_len, int ctx_all,
                                                           float *__restrict__ part) {
   static_assert(HD == 128, "decode attention is written for head_dim 128");
   const int pi = blockIdx.x, kh = blockIdx.y, s = blockIdx.z;
   const int t = threadIdx.x;
-  const int len = ctx_len[s];
+  const int len = ctx_len ? ctx_len[s] : ctx_all;
   float *pbase = part + ((int64_t(s) * hq + kh * GRP) * max_pages + pi) * (2 + HD);
   const int64_t hstride = int64_t(max_pages) * (2 + HD);
   if (pi * P < len) {
@@ -243,10 +243,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float *__restric
 template <int HD>
 __global__ __launch_bounds__(256) void attn_decode_combine(const float *__restrict__ part, int hq,
                                                            int max_pages,
-                                                           const int32_t *__restrict__ ctx_len,
+                                                           const int32_t *__restrict__ ctx_len, int ctx_all,
                                                            float *__restrict__ out) {
   const int h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
-  const int np = (ctx_len[s] + P - 1) / P;
+  const int np = ((ctx_len ? ctx_len[s] : ctx_all) + P - 1) / P;
   __shared__ float wm[1024], wl[1024];
   __shared__ float red[4], sacc[2][HD], sl[2];
   {
@@ -423,11 +423,11 @@ void launch_attn_decode(const float *q32, int nseq, int hq, const KvGeom &g, con
     if (g.kv32)                                                                                     \
       hipLaunchKernelGGL((attn_decode_kernel<128, G, float>), grid, block, 0, st, q32, hq, g,        \
                          static_cast<const float *>(kpool), static_cast<const float *>(vpool), pages, \
-                         max_pages, ctx_len, part);                                                 \
+                         max_pages, ctx_len, max_ctx, part);                                             \
     else                                                                                            \
       hipLaunchKernelGGL((attn_decode_kernel<128, G, _Float16>), grid, block, 0, st, q32, hq, g,     \
                          static_cast<const _Float16 *>(kpool), static_cast<const _Float16 *>(vpool), \
-                         pages, max_pages, ctx_len, part);                                          \
+                         pages, max_pages, ctx_len, max_ctx, part);                                      \
     break;
   switch (grp) {
     CASE(1) CASE(2) CASE(4) CASE(7) CASE(8)
@@ -436,7 +436,7 @@ void launch_attn_decode(const float *q32, int nseq, int hq, const KvGeom &g, con
 #undef CASE
   HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL((attn_decode_combine<128>), dim3(hq, nseq), dim3(256), 0, st, part, hq, max_pages,
-                     ctx_len, out);
+                     ctx_len, max_ctx, out);
   HIP_CHECK(hipGetLastError());
 }
 

@@ -159,12 +159,12 @@ struct BLoad {
 };
 
 // Tile order: the hardware hands consecutive workgroups to the 8 XCDs round-robin; give
-// each XCD a contiguous range of tiles, and inside it walk groups of 8 M-tiles so that the
+// each XCD a contiguous range of tiles, and inside it walk groups of GM M-tiles so that the
 // concurrently running tiles of one XCD share A rows and weight rows through its L2.
 __device__ __forceinline__ void tile_coords(int bid, int nblk, int MT, int NT, int &mt, int &nt) {
   int t = bid;
   if ((nblk & 7) == 0) t = (bid & 7) * (nblk >> 3) + (bid >> 3);
-  constexpr int GM = 8;
+  constexpr int GM = 4;  // from a sweep of 1..32 at the 35,840-token shapes (within 3%)
   const int group = t / (GM * NT);
   const int first = group * GM;
   const int gm = min(MT - first, GM);
@@ -258,6 +258,45 @@ __device__ __forceinline__ void mma_tile(f32x16 (&acc)[WTM][WTN], const _Float16
         for (int i = 0; i < WTM; ++i)
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[i][j][r] += dj * p[i][j][r];
+      }
+    }
+  } else if constexpr (MODE == FAST) {
+    // fragments of step kk+1 are read from LDS while the MFMAs of step kk issue
+    constexpr int KS = BK / 16;
+    half8 ca[WTM], cb[WTN];
+    {
+      const int kc = (lane >> 5) * 8;
+#pragma unroll
+      for (int j = 0; j < WTN; ++j) cb[j] = *reinterpret_cast<const half8 *>(Bs + brow + j * 32 * LDK + kc);
+#pragma unroll
+      for (int i = 0; i < WTM; ++i) ca[i] = *reinterpret_cast<const half8 *>(As + arow + i * 32 * LDK + kc);
+    }
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      half8 na[WTM], nb[WTN];
+      if (kk + 1 < KS) {
+        const int kc = (kk + 1) * 16 + (lane >> 5) * 8;
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) nb[j] = *reinterpret_cast<const half8 *>(Bs + brow + j * 32 * LDK + kc);
+#pragma unroll
+        for (int i = 0; i < WTM; ++i) na[i] = *reinterpret_cast<const half8 *>(As + arow + i * 32 * LDK + kc);
+      }
+#pragma unroll
+      for (int i = 0; i < WTM; ++i)
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) acc[i][j] = MFMA(ca[i], cb[j], acc[i][j]);
+      if (kk + 1 < KS) {
+        // interleave: one LDS read, then a share of the MFMAs
+        constexpr int R = WTM + WTN, Mf = WTM * WTN;
+#pragma unroll
+        for (int q = 0; q < R; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, Mf / R, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < WTM; ++i) ca[i] = na[i];
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) cb[j] = nb[j];
       }
     }
   } else {

@@ -61,55 +61,44 @@ __global__ void embed_kernel(const void *__restrict__ table, uint32_t kind, cons
                         : static_cast<const float *>(table)[src];
 }
 
-// One workgroup per token row.  Rotate-half RoPE with the model's tables
-// (src/tensor.rs:158-172), then q -> q16 (+lo plane) / q32, k -> K page row, v -> V page column.
-template <typename KV>
-__global__ __launch_bounds__(kT) void rope_kv_kernel(const float *__restrict__ qkv, int hq, KvGeom g,
-                                                     const float *__restrict__ cosT,
-                                                     const float *__restrict__ sinT,
-                                                     const int32_t *__restrict__ tok_seq,
-                                                     const int32_t *__restrict__ tok_pos,
-                                                     const int32_t *__restrict__ pages, int max_pages,
-                                                     _Float16 *__restrict__ q16, _Float16 *__restrict__ q16lo,
-                                                     float *__restrict__ q32, KV *__restrict__ kpool,
-                                                     KV *__restrict__ vpool) {
-  const int t = blockIdx.x;
-  const int hd = g.hd, half = hd / 2;
-  const int qw = hq * hd, kvw = g.hkv * hd;
-  const float *row = qkv + int64_t(t) * (qw + 2 * kvw);
-  const int pos = tok_pos[t];
-  const int page = pages[int64_t(tok_seq[t]) * max_pages + pos / g.page_tokens];
-  const int slot = pos % g.page_tokens;
+// One KV value into a pool slot (value index i): f32 pools (KV32) or f16 pools.
+// RoPE everywhere is the rotate-half form with the model's tables (src/tensor.rs:158-172).
+template <bool KV32>
+__device__ __forceinline__ void kv_put(void *pool, int64_t i, float v) {
+  if constexpr (KV32)
+    static_cast<float *>(pool)[i] = v;
+  else
+    static_cast<_Float16 *>(pool)[i] = _Float16(v);
+}
+
+// Decode form: one token whose position and KV page the host already knows (kernel arguments,
+// so the only memory round trip is the q|k|v row and the table rows).  q goes out in f32.
+template <bool KV32>
+__global__ __launch_bounds__(kT) void rope_kv_token_kernel(const float *__restrict__ row, int hq, KvGeom g,
+                                                           const float *__restrict__ cosT,
+                                                           const float *__restrict__ sinT, int pos, int page,
+                                                           float *__restrict__ q32, void *__restrict__ kpool,
+                                                           void *__restrict__ vpool) {
+  const int hd = g.hd, half = hd / 2, qw = hq * hd, kvw = g.hkv * hd;
   const float *cs = cosT + int64_t(pos) * hd, *sn = sinT + int64_t(pos) * hd;
-  auto putq = [&](int64_t i, float v) {
-    if (q16) {
-      const _Float16 h = _Float16(v);
-      q16[i] = h;
-      if (q16lo) q16lo[i] = _Float16(v - float(h));
-    } else {
-      q32[i] = v;
-    }
-  };
-  for (int i = threadIdx.x; i < hq * half; i += kT) {
-    const int h = i / half, j = i % half;
+  const int slot = pos % g.page_tokens;
+  const int64_t pbase = int64_t(page) * g.page_stride;
+  for (int i = threadIdx.x; i < (hq + g.hkv) * half; i += kT) {
+    const int h = i / half, j = i % half;  // heads 0..hq-1 are q, then the kv heads
     const float u = row[h * hd + j], v = row[h * hd + j + half];
-    putq(int64_t(t) * qw + h * hd + j, u * cs[j] - v * sn[j]);
-    putq(int64_t(t) * qw + h * hd + j + half, v * cs[j + half] + u * sn[j + half]);
+    const float a = u * cs[j] - v * sn[j], b = v * cs[j + half] + u * sn[j + half];
+    if (h < hq) {
+      q32[h * hd + j] = a;
+      q32[h * hd + j + half] = b;
+    } else {
+      const int64_t at = pbase + (int64_t(h - hq) * g.page_tokens + slot) * hd;
+      kv_put<KV32>(kpool, at + j, a);
+      kv_put<KV32>(kpool, at + j + half, b);
+    }
   }
-  KV *kp = kpool + int64_t(page) * g.page_stride;
-  KV *vp = vpool + int64_t(page) * g.page_stride;
-  // k -> page rows [hkv][page_tokens][hd]
-  for (int i = threadIdx.x; i < g.hkv * half; i += kT) {
-    const int h = i / half, j = i % half;
-    const float u = row[qw + h * hd + j], v = row[qw + h * hd + j + half];
-    KV *dst = kp + (int64_t(h) * g.page_tokens + slot) * hd;
-    dst[j] = KV(u * cs[j] - v * sn[j]);
-    dst[j + half] = KV(v * cs[j + half] + u * sn[j + half]);
-  }
-  // v -> page columns [hkv][hd][page_tokens]
   for (int i = threadIdx.x; i < kvw; i += kT) {
     const int h = i / hd, dd = i % hd;
-    vp[(int64_t(h) * hd + dd) * g.page_tokens + slot] = KV(row[qw + kvw + i]);
+    kv_put<KV32>(vpool, pbase + (int64_t(h) * hd + dd) * g.page_tokens + slot, row[qw + kvw + i]);
   }
 }
 
@@ -117,14 +106,14 @@ __global__ __launch_bounds__(kT) void rope_kv_kernel(const float *__restrict__ q
 // q and k are rotated token by token (rows are contiguous); v is staged through LDS per kv
 // head so that its transposed page layout is written as runs of consecutive slots instead of
 // one 4-byte store per cache line.
-template <typename KV>
+template <bool KV32>
 __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
     const float *__restrict__ qkv, int hq, KvGeom g, const float *__restrict__ cosT,
     const float *__restrict__ sinT, const int32_t *__restrict__ pages, int max_pages,
     const int32_t *__restrict__ tile_seq, const int32_t *__restrict__ tile_row0,
     const int32_t *__restrict__ tile_pos0, const int32_t *__restrict__ tile_n,
-    _Float16 *__restrict__ q16, _Float16 *__restrict__ q16lo, KV *__restrict__ kpool,
-    KV *__restrict__ vpool) {
+    _Float16 *__restrict__ q16, _Float16 *__restrict__ q16lo, void *__restrict__ kpool,
+    void *__restrict__ vpool) {
   constexpr int TT = 32, HDMAX = 128;
   __shared__ float vs[TT][HDMAX + 1];
   const int tile = blockIdx.x, tid = threadIdx.x;
@@ -149,14 +138,14 @@ __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
         q16lo[at + half] = _Float16(b - float(bh));
       }
     }
-    KV *kp = kpool + int64_t(ptab[pos / g.page_tokens]) * g.page_stride;
+    const int64_t kb = int64_t(ptab[pos / g.page_tokens]) * g.page_stride;
     const int slot = pos % g.page_tokens;
     for (int i = tid; i < g.hkv * half; i += kT) {
       const int h = i / half, j = i % half;
       const float u = row[qw + h * hd + j], v = row[qw + h * hd + j + half];
-      KV *dst = kp + (int64_t(h) * g.page_tokens + slot) * hd;
-      dst[j] = KV(u * cs[j] - v * sn[j]);
-      dst[j + half] = KV(v * cs[j + half] + u * sn[j + half]);
+      const int64_t at = kb + (int64_t(h) * g.page_tokens + slot) * hd;
+      kv_put<KV32>(kpool, at + j, u * cs[j] - v * sn[j]);
+      kv_put<KV32>(kpool, at + j + half, v * cs[j + half] + u * sn[j + half]);
     }
   }
   for (int h = 0; h < g.hkv; ++h) {
@@ -170,8 +159,9 @@ __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
       const int tk = i % TT, dd = i / TT;
       if (tk < n) {
         const int pos = pos0 + tk;
-        KV *vp = vpool + int64_t(ptab[pos / g.page_tokens]) * g.page_stride;
-        vp[(int64_t(h) * hd + dd) * g.page_tokens + pos % g.page_tokens] = KV(vs[tk][dd]);
+        kv_put<KV32>(vpool, int64_t(ptab[pos / g.page_tokens]) * g.page_stride +
+                                   (int64_t(h) * hd + dd) * g.page_tokens + pos % g.page_tokens,
+                        vs[tk][dd]);
       }
     }
     __syncthreads();
@@ -357,19 +347,15 @@ void launch_embed(const void *table, uint32_t kind, const int32_t *ids, int T, i
   HIP_CHECK(hipGetLastError());
 }
 
-void launch_rope_kv(const float *qkv, int T, int hq, const KvGeom &g, const float *cosT,
-                    const float *sinT, const int32_t *tok_seq, const int32_t *tok_pos,
-                    const int32_t *pages, int max_pages, _Float16 *q16, _Float16 *q16_lo,
-                    float *q32, void *kpool, void *vpool, hipStream_t st) {
-  LG_REQUIRE(T > 0 && g.hd % 2 == 0 && (q16 || q32), "rope_kv: bad arguments");
+void launch_rope_kv_token(const float *qkv, int hq, const KvGeom &g, const float *cosT, const float *sinT,
+                          int pos, int page, float *q32, void *kpool, void *vpool, hipStream_t st) {
+  LG_REQUIRE(g.hd % 2 == 0 && q32 && pos >= 0 && page >= 0, "rope_kv: bad arguments");
   if (g.kv32)
-    hipLaunchKernelGGL(rope_kv_kernel<float>, dim3(T), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, tok_seq,
-                       tok_pos, pages, max_pages, q16, q16_lo, q32, static_cast<float *>(kpool),
-                       static_cast<float *>(vpool));
+    hipLaunchKernelGGL(rope_kv_token_kernel<true>, dim3(1), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, pos, page,
+                       q32, kpool, vpool);
   else
-    hipLaunchKernelGGL(rope_kv_kernel<_Float16>, dim3(T), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, tok_seq,
-                       tok_pos, pages, max_pages, q16, q16_lo, q32, static_cast<_Float16 *>(kpool),
-                       static_cast<_Float16 *>(vpool));
+    hipLaunchKernelGGL(rope_kv_token_kernel<false>, dim3(1), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, pos, page,
+                       q32, kpool, vpool);
   HIP_CHECK(hipGetLastError());
 }
 
@@ -380,13 +366,11 @@ void launch_rope_kv_tiles(const float *qkv, int hq, const KvGeom &g, const float
                           void *kpool, void *vpool, hipStream_t st) {
   LG_REQUIRE(ntiles > 0 && g.hd % 2 == 0 && g.hd <= 128 && q16, "rope_kv: bad arguments");
   if (g.kv32)
-    hipLaunchKernelGGL(rope_kv_tile_kernel<float>, dim3(ntiles), dim3(kT), 0, st, qkv, hq, g, cosT, sinT,
-                       pages, max_pages, tile_seq, tile_row0, tile_pos0, tile_n, q16, q16_lo,
-                       static_cast<float *>(kpool), static_cast<float *>(vpool));
+    hipLaunchKernelGGL(rope_kv_tile_kernel<true>, dim3(ntiles), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, pages,
+                       max_pages, tile_seq, tile_row0, tile_pos0, tile_n, q16, q16_lo, kpool, vpool);
   else
-    hipLaunchKernelGGL(rope_kv_tile_kernel<_Float16>, dim3(ntiles), dim3(kT), 0, st, qkv, hq, g, cosT, sinT,
-                       pages, max_pages, tile_seq, tile_row0, tile_pos0, tile_n, q16, q16_lo,
-                       static_cast<_Float16 *>(kpool), static_cast<_Float16 *>(vpool));
+    hipLaunchKernelGGL(rope_kv_tile_kernel<false>, dim3(ntiles), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, pages,
+                       max_pages, tile_seq, tile_row0, tile_pos0, tile_n, q16, q16_lo, kpool, vpool);
   HIP_CHECK(hipGetLastError());
 }
 

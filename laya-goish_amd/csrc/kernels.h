@@ -75,20 +75,17 @@ void launch_embed(const void *table, uint32_t kind, const int32_t *ids, int T, i
 struct KvGeom {
   int page_tokens = 64;  // tokens per page
   int hkv = 0, hd = 0;
-  int kv32 = 0;              // element type of the pools: 0 = f16, 1 = f32
-  int64_t layer_stride = 0;  // halves between layers of the K (or V) pool
-  int64_t page_stride = 0;   // halves per page of one layer: hkv * page_tokens * hd
+  int kv32 = 0;              // value type of the pools: 0 = f16, 1 = f32
+  int64_t layer_stride = 0;  // values between layers of the K (or V) pool
+  int64_t page_stride = 0;   // values per page of one layer: hkv * page_tokens * hd
 };
 
-// RoPE on q and k of qkv[T][(hq+2hkv)*hd] (f32) with tables cos/sin[ctx][hd]; writes q as
-// f16 (q16), hi/lo f16 planes (q16, q16_lo) or f32 (q32), and the K page rows
-// [hkv][page_tokens][hd] and V page columns [hkv][hd][page_tokens] of the layer pools
-// (element type per g.kv32).  tok_seq/tok_pos give each row's sequence and position;
-// pages[seq * max_pages + pos / page_tokens] its page.
-void launch_rope_kv(const float *qkv, int T, int hq, const KvGeom &g, const float *cosT,
-                    const float *sinT, const int32_t *tok_seq, const int32_t *tok_pos,
-                    const int32_t *pages, int max_pages, _Float16 *q16, _Float16 *q16_lo,
-                    float *q32, void *kpool, void *vpool, hipStream_t st);
+// RoPE on q and k of q|k|v rows ((hq+2hkv)*hd f32) with tables cos/sin[ctx][hd], q written
+// out, k and v written into the K page rows [hkv][page_tokens][hd] and V page columns
+// [hkv][hd][page_tokens] of the layer pools (value format per g.kv32).
+// This form: one decode token at a position and KV page known to the host; q to q32.
+void launch_rope_kv_token(const float *qkv, int hq, const KvGeom &g, const float *cosT, const float *sinT,
+                          int pos, int page, float *q32, void *kpool, void *vpool, hipStream_t st);
 // The same for a prefill batch, one workgroup per attention tile (<= 32 consecutive tokens
 // of one sequence, rows row0.., positions pos0..); q goes to f16 planes.  head_dim <= 128.
 void launch_rope_kv_tiles(const float *qkv, int hq, const KvGeom &g, const float *cosT,
