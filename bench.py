@@ -127,6 +127,129 @@ def bench_decode(eng, steps):
     return dt, prof
 
 
+def base_line(metric, value, unit, higher, steps, warmup, ms, prec, workload, **extra):
+    return {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": steps, "warmup": warmup,
+            "ms_per_step": round(ms, 3), "higher_is_better": higher, "scaling": "weak", "vs_baseline": None,
+            "dtype": "f32" if prec == lh.PREC_EXACT else "f16", "data": "synthetic",
+            "config": dict(workload=workload, seed=SEED,
+                           precision="exact" if prec == lh.PREC_EXACT else "fast", **extra)}
+
+
+def bench_plumbing(args, prec):
+    """The CPU-runnable plumbing model (6 layers, d512, 8 x 64 heads, F16): one decide request of a
+    128-token prompt plus one 16-token yes/no question block, scored at its answer position.
+    Latency of the whole request (stage nothing: ids are uploaded inside the timed call)."""
+    img = lh.SynthImage("plumbing-f16", seed=SEED)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=2048, max_batch_tokens=512, precision=prec)
+    ids = np.random.default_rng(SEED + 2).integers(0, 32000, 144).astype(np.int32)
+    yes_no = np.array([1939, 4874], np.int32)
+    for _ in range(max(args.warmup, 3)):
+        s = eng.seq_create()
+        eng.forward(s, ids, [143], yes_no)
+        eng.seq_free(s)
+    times = []
+    for _ in range(max(args.steps, 20)):
+        eng.sync()
+        t0 = time.perf_counter()
+        s = eng.seq_create()
+        logits = eng.forward(s, ids, [143], yes_no)
+        probs, _ = lh.option_scores(logits[0])
+        eng.seq_free(s)
+        times.append(time.perf_counter() - t0)
+    eng.close()
+    med = float(np.median(times)) * 1e3
+    log(f"plumbing: median {med:.3f} ms per decide request (min {min(times) * 1e3:.3f})")
+    return base_line("plumbing decide latency (1 request, 144 tokens, yes/no option scoring)", round(med, 3),
+                     "ms", False, len(times), max(args.warmup, 3), med, prec,
+                     "6 layers, d_model 512, 8 x 64 heads, FFN 1408, vocab 32000, F16 weights N(0, 0.02); "
+                     "128-token prompt + one 16-token noul question block, 2 option tokens",
+                     p50_ms=round(med, 3), min_ms=round(min(times) * 1e3, 3))
+
+
+def bench_q4k(args, prec):
+    """Q4_K/Q6_K 7B shape (28 layers, d3584, GQA 28/4 x 128, FFN 18944, vocab 152064, QKV bias):
+    a batch of 32 requests x 1024 tokens, 4 option tokens scored at the last position."""
+    log("generating q4km-7b (28 layers)")
+    img = lh.SynthImage("q4km-7b", seed=SEED)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=32 * 1024 + 1024, max_batch_tokens=32768, precision=prec)
+    rng = np.random.default_rng(SEED + 3)
+    reqs = [(rng.integers(0, 152064, 1024).astype(np.int32), np.array([1023], np.int32)) for _ in range(32)]
+    opts = rng.choice(152064, 4, replace=False).astype(np.int32)
+    seqs = [eng.seq_create() for _ in reqs]
+    batch = eng.batch([(s, ids, pos) for s, (ids, pos) in zip(seqs, reqs)])
+    for _ in range(args.warmup):
+        batch.run(opts)
+        batch.rewind()
+    eng.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = batch.run(opts)
+        batch.rewind()
+    eng.sync()
+    dt = (time.perf_counter() - t0) / args.steps
+    eng.profile_reset()
+    eng.profile(True)
+    batch.run(opts)
+    eng.profile(False)
+    gp = eng.profile_read("gemm")
+    tf = gp["flops"] / (gp["ms"] * 1e-3) / 1e12
+    assert np.isfinite(out[1]).all()
+    eng.close()
+    log(f"q4km-7b: {dt * 1e3:.1f} ms/step, {32768 / dt:.0f} tok/s, gemm {tf:.1f} TFLOP/s")
+    return base_line("Q4_K/Q6_K 7B batched prefill tok/s (32 x 1024)", round(32768 / dt, 1), "tok/s", True,
+                     args.steps, args.warmup, dt * 1e3, prec,
+                     "28 layers, d_model 3584, GQA 28/4 x 128, FFN 18944, vocab 152064, QKV bias; Q4_K q/k/o/"
+                     "gate/up, Q6_K v/down/output; 32 requests x 1024 tokens, 4 options at the last position",
+                     req_per_s=round(32 / dt, 2), gemm_tflops=round(tf, 1),
+                     gemm_frac=round(tf / PEAK_F16_TFLOPS, 4))
+
+
+def bench_long_context(args, prec):
+    """F16 7B shape with a shared prefix: 16 requests of 8192 tokens sharing their first 6144.
+    One step = the prefix computed once, forked into 16 requests, their 2048 own tokens
+    prefilled as one batch, 8 answer positions each scored over 4 option tokens."""
+    log("generating f16-7b (28 layers)")
+    img = lh.SynthImage("f16-7b", seed=SEED)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=6144 + 16 * 2048 + 2048, max_batch_tokens=32768,
+                    precision=prec)
+    rng = np.random.default_rng(SEED + 4)
+    prefix = rng.integers(0, 152064, 6144).astype(np.int32)
+    own = [rng.integers(0, 152064, 2048).astype(np.int32) for _ in range(16)]
+    pos = np.arange(255, 2048, 256).astype(np.int32)  # 8 questions per request
+    opts = rng.choice(152064, 4, replace=False).astype(np.int32)
+
+    def step():
+        base = eng.seq_create()
+        eng.forward(base, prefix, [], opts)
+        kids = [eng.seq_fork(base, 6144) for _ in own]
+        b = eng.batch([(k, ids, pos) for k, ids in zip(kids, own)])
+        out = b.run(opts)
+        b.free()
+        for k in kids:
+            eng.seq_free(k)
+        eng.seq_free(base)
+        return out
+
+    for _ in range(args.warmup):
+        step()
+    eng.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = step()
+    eng.sync()
+    dt = (time.perf_counter() - t0) / args.steps
+    assert np.isfinite(out[1]).all()
+    eng.close()
+    tokens = 6144 + 16 * 2048
+    log(f"f16-7b long context: {dt * 1e3:.1f} ms/step, {tokens / dt:.0f} computed tok/s, {16 / dt:.2f} req/s")
+    return base_line("F16 7B shared-prefix long-context decide (16 x 8192, 6144 shared)", round(16 * 8192 / dt, 1),
+                     "tok/s", True, args.steps, args.warmup, dt * 1e3, prec,
+                     "28 layers, d_model 3584, GQA 28/4 x 128, FFN 18944, vocab 152064, F16 weights; 16 requests x "
+                     "8192 tokens sharing the first 6144 (computed once, forked), 8 answer positions each, 4 options",
+                     requests_per_s=round(16 / dt, 3), computed_tok_per_s=round(tokens / dt, 1),
+                     note="value counts every request's 8192 tokens; computed_tok_per_s counts tokens prefilled")
+
+
 def cpu_baseline(threads, layers=24):
     """The oracle on a bounded sample: one 560-token request of the workload through `layers`
     of the 24 layers (per-layer cost is identical), scaled to the full model."""
@@ -160,6 +283,9 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--precision", choices=["exact", "fast"], default="exact")
+    ap.add_argument("--workload", choices=["decide", "plumbing", "q4k-prefill", "long-context"], default="decide",
+                    help="decide (default): the Q8_0 d2048 batched decide headline plus batch-1 decode; the "
+                         "others measure the remaining workload shapes, one JSON line each")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=DECODE_STEPS,
@@ -176,6 +302,10 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     prec = lh.PREC_EXACT if args.precision == "exact" else lh.PREC_FAST
+    if args.workload != "decide":
+        fn = {"plumbing": bench_plumbing, "q4k-prefill": bench_q4k, "long-context": bench_long_context}
+        print(json.dumps(fn[args.workload](args, prec)), flush=True)
+        return
     if args.copy_calibration > 0:
         n = args.copy_calibration * (1 << 20) // 4
         src = np.arange(n, dtype=np.float32)
