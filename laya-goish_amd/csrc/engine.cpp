@@ -137,6 +137,8 @@ struct BatchPlan {
   DevBuf meta;                  // ids, tok_seq, tok_pos, pages, tiles..., gather rows
   int32_t *ids = nullptr, *tok_seq = nullptr, *tok_pos = nullptr, *pages = nullptr;
   int32_t *tile_seq = nullptr, *tile_row0 = nullptr, *tile_pos0 = nullptr, *tile_n = nullptr;
+  int ngroups = 0;              // runs of <= 4 consecutive tiles of one sequence
+  int32_t *grp_first = nullptr, *grp_count = nullptr;
   int32_t *gather = nullptr;
   bool ran = false;
 };
@@ -525,7 +527,7 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
   LG_REQUIRE(nreq > 0 && reqs, "batch: no requests");
   auto *b = new BatchPlan();
   try {
-    std::vector<int32_t> ids, tseq, tpos, tiles_s, tiles_r, tiles_p, tiles_n, gather;
+    std::vector<int32_t> ids, tseq, tpos, tiles_s, tiles_r, tiles_p, tiles_n, gather, grp_f, grp_c;
     int max_pages = 0;
     for (int r = 0; r < nreq; ++r) {
       const lg_request &q = reqs[r];
@@ -563,6 +565,10 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
         tpos.push_back(s.len + i);
       }
       for (int i = 0; i < q.n; i += 32) {
+        if ((i / 32) % 4 == 0) {
+          grp_f.push_back(int32_t(tiles_s.size()));
+          grp_c.push_back(std::min(4, (q.n - i + 31) / 32));
+        }
         tiles_s.push_back(r);
         tiles_r.push_back(row + i);
         tiles_p.push_back(s.len + i);
@@ -578,9 +584,10 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
     b->T = int(T);
     b->R = int(gather.size());
     b->ntiles = int(tiles_s.size());
+    b->ngroups = int(grp_f.size());
     b->max_pages = max_pages;
-    const size_t nints = ids.size() * 3 + ptab.size() + tiles_s.size() * 4 + gather.size() + 64;
-    b->meta.ensure(nints * 4 + 16 * 256);
+    const size_t nints = ids.size() * 3 + ptab.size() + tiles_s.size() * 4 + grp_f.size() * 2 + gather.size() + 64;
+    b->meta.ensure(nints * 4 + 20 * 256);
     int32_t *base = b->meta.as<int32_t>();
     size_t off = 0;
     auto put = [&](const std::vector<int32_t> &v, int32_t *&dst) {
@@ -596,6 +603,8 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
     put(tiles_r, b->tile_row0);
     put(tiles_p, b->tile_pos0);
     put(tiles_n, b->tile_n);
+    put(grp_f, b->grp_first);
+    put(grp_c, b->grp_count);
     put(gather, b->gather);
     HIP_CHECK(hipStreamSynchronize(stream));
   } catch (...) {
@@ -652,7 +661,8 @@ void Engine::run_layers_prefill(BatchPlan &b, lg_cancel_fn cancel, void *arg) {
     prof.end(double(T) * (qkvw * 4 + qw * 2 * planes + 2 * kvw * kv_elem()), 0, stream);
     prof.begin("attn_prefill", stream);
     launch_attn_prefill(q16, q16lo, T, hq, g, kpool(l), vpool(l), b.pages, b.max_pages, b.tile_seq,
-                        b.tile_row0, b.tile_pos0, b.tile_n, b.ntiles, att, attlo, stream);
+                        b.tile_row0, b.tile_pos0, b.tile_n, b.ntiles, b.grp_first, b.grp_count,
+                        b.ngroups, att, attlo, stream);
     prof.end(0, 0, stream);
     gemm(att, attlo, T, ly.wo, Epi::ADD, x, nullptr, nullptr, d, nullptr);
     prof.begin("rmsnorm", stream);

@@ -202,6 +202,223 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(
     }
 }
 
+// Position of key k (0..63) inside a V row in LDS: bits 2 and 3 swapped, so the eight keys one
+// lane feeds to the O^T product (16c + 4hl + {0..3}, 16c + 8 + 4hl + {0..3}) sit in one
+// 16-byte run at 16c + 8hl.
+__device__ __forceinline__ int vperm(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
+
+// Prefill, grouped: one workgroup of four waves per (group of <= 4 consecutive query tiles of
+// one sequence, query head).  Each K/V page of the group passes through LDS once, already
+// in MFMA operand form (hi/lo f16 planes with an f32 cache), and serves all four tiles; the
+// next page is fetched into registers while the current one is consumed.  Wave w computes
+// tile w with the arithmetic of attn_prefill_kernel, term for term, so both kernels give
+// bit-identical outputs.
+template <int HD, bool SPLIT>
+__global__ __launch_bounds__(256, 1) void attn_prefill_grp_kernel(
+    const _Float16 *__restrict__ q16, const _Float16 *__restrict__ q16lo, int hq, KvGeom g,
+    const void *__restrict__ kpool, const void *__restrict__ vpool, const int32_t *__restrict__ pages,
+    int max_pages, const int32_t *__restrict__ grp_first, const int32_t *__restrict__ grp_count,
+    const int32_t *__restrict__ tile_seq, const int32_t *__restrict__ tile_row0,
+    const int32_t *__restrict__ tile_pos0, const int32_t *__restrict__ tile_n,
+    _Float16 *__restrict__ out16, _Float16 *__restrict__ out16lo) {
+  using KV = typename std::conditional<SPLIT, float, _Float16>::type;
+  constexpr int KT = HD / 16, DB = HD / 32;
+  constexpr int NPL = SPLIT ? 2 : 1;      // f16 planes per operand
+  constexpr int KS = HD + 8, VS = P + 8;  // padded LDS row strides (halves): conflict-free reads
+  constexpr int EPL = SPLIT ? 4 : 8;      // KV values per 16-byte load
+  constexpr int NLD = P * HD / (256 * EPL);
+  static_assert(NLD * 256 * EPL == P * HD, "page must split evenly over 256 threads");
+  __shared__ __align__(16) _Float16 kls[NPL][P * KS];
+  __shared__ __align__(16) _Float16 vls[NPL][HD * VS];
+
+  // Same XCD-contiguous mapping as attn_prefill_kernel, over (head, group) pairs.
+  const int total = gridDim.x, ngroups = total / hq;
+  const int xcd = blockIdx.x % 8, per = total / 8, rem = total % 8;
+  const int logical = xcd * per + min(xcd, rem) + blockIdx.x / 8;
+  const int grp = logical % ngroups, h = logical / ngroups;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, qi = lane & 31, hl = lane >> 5;
+  const int t0 = grp_first[grp], cnt = grp_count[grp];
+  const bool active = wave < cnt;
+  const int tile = t0 + min(wave, cnt - 1);
+  const int seq = tile_seq[tile], row0 = tile_row0[tile], pos0 = tile_pos0[tile], n = tile_n[tile];
+  const int glast = tile_pos0[t0 + cnt - 1] + tile_n[t0 + cnt - 1] - 1;
+  const int kh = h / (hq / g.hkv);
+  const int qw = hq * HD;
+  const int qpos = pos0 + qi;
+  const bool live = qi < n;
+
+  half8 qr[KT], ql[SPLIT ? KT : 1];
+  {
+    const int64_t off = int64_t(row0 + min(qi, n - 1)) * qw + h * HD + hl * 8;
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      qr[t] = *reinterpret_cast<const half8 *>(q16 + off + 16 * t);
+      if (SPLIT) ql[t] = *reinterpret_cast<const half8 *>(q16lo + off + 16 * t);
+    }
+  }
+  f32x16 acc[DB];
+#pragma unroll
+  for (int b = 0; b < DB; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[b][r] = 0.0f;
+  float m = -INFINITY, l = 0.0f;
+  const float scale = kLog2e / sqrtf(float(HD));
+  const int npages = glast / P + 1;
+  const int mypages = active ? (pos0 + n - 1) / P + 1 : 0;
+  const int32_t *ptab = pages + int64_t(seq) * max_pages;
+  const KV *kbase = static_cast<const KV *>(kpool) + int64_t(kh) * P * HD;
+  const KV *vbase = static_cast<const KV *>(vpool) + int64_t(kh) * HD * P;
+
+  uint4 kreg[NLD], vreg[NLD];
+  {
+    const int64_t page = ptab[0];
+    const uint4 *ks = reinterpret_cast<const uint4 *>(kbase + page * g.page_stride);
+    const uint4 *vs = reinterpret_cast<const uint4 *>(vbase + page * g.page_stride);
+#pragma unroll
+    for (int j = 0; j < NLD; ++j) {
+      kreg[j] = ks[tid + 256 * j];
+      vreg[j] = vs[tid + 256 * j];
+    }
+  }
+
+  for (int kt = 0; kt < npages; ++kt) {
+    __syncthreads();  // every wave is done reading the previous page
+#pragma unroll
+    for (int j = 0; j < NLD; ++j) {
+      const int e0 = (tid + 256 * j) * EPL;  // first value of this load within the page
+      const int kro = (e0 / HD) * KS + e0 % HD;
+      const int vd = e0 / P, vk = e0 % P;
+      if constexpr (SPLIT) {
+        const float4 kf = __builtin_bit_cast(float4, kreg[j]);
+        const float4 vf = __builtin_bit_cast(float4, vreg[j]);
+        const float kv[4] = {kf.x, kf.y, kf.z, kf.w}, vv[4] = {vf.x, vf.y, vf.z, vf.w};
+        half4 khi, klo, vhi, vlo;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          khi[e] = _Float16(kv[e]);
+          klo[e] = _Float16(kv[e] - float(khi[e]));
+          vhi[e] = _Float16(vv[e]);
+          vlo[e] = _Float16(vv[e] - float(vhi[e]));
+        }
+        *reinterpret_cast<half4 *>(&kls[0][kro]) = khi;
+        *reinterpret_cast<half4 *>(&kls[1][kro]) = klo;
+        const int vo = vd * VS + vperm(vk);
+        *reinterpret_cast<half4 *>(&vls[0][vo]) = vhi;
+        *reinterpret_cast<half4 *>(&vls[1][vo]) = vlo;
+      } else {
+        *reinterpret_cast<uint4 *>(&kls[0][kro]) = kreg[j];
+        const half8 v8 = __builtin_bit_cast(half8, vreg[j]);
+        const half4 va = {v8[0], v8[1], v8[2], v8[3]}, vb = {v8[4], v8[5], v8[6], v8[7]};
+        *reinterpret_cast<half4 *>(&vls[0][vd * VS + vperm(vk)]) = va;
+        *reinterpret_cast<half4 *>(&vls[0][vd * VS + vperm(vk + 4)]) = vb;
+      }
+    }
+    __syncthreads();
+    if (kt + 1 < npages) {
+      const int64_t page = ptab[kt + 1];
+      const uint4 *ks = reinterpret_cast<const uint4 *>(kbase + page * g.page_stride);
+      const uint4 *vs = reinterpret_cast<const uint4 *>(vbase + page * g.page_stride);
+#pragma unroll
+      for (int j = 0; j < NLD; ++j) {
+        kreg[j] = ks[tid + 256 * j];
+        vreg[j] = vs[tid + 256 * j];
+      }
+    }
+    if (kt >= mypages) continue;
+
+    f32x16 s[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
+      const int ro = (kb * 32 + qi) * KS + hl * 8;
+#pragma unroll
+      for (int t = 0; t < KT; ++t) {
+        const half8 kh8 = *reinterpret_cast<const half8 *>(&kls[0][ro + 16 * t]);
+        if constexpr (SPLIT) {
+          const half8 kl8 = *reinterpret_cast<const half8 *>(&kls[1][ro + 16 * t]);
+          s[kb] = MFMA(kh8, qr[t], s[kb]);
+          s[kb] = MFMA(kl8, qr[t], s[kb]);
+          s[kb] = MFMA(kh8, ql[t], s[kb]);
+        } else {
+          s[kb] = MFMA(kh8, qr[t], s[kb]);
+        }
+      }
+    }
+    float mt = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kt * P + kb * 32 + (r >> 2) * 8 + hl * 4 + (r & 3);
+        const float v = (key <= qpos && live) ? s[kb][r] * scale : -INFINITY;
+        s[kb][r] = v;
+        mt = fmaxf(mt, v);
+      }
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    const float mn = fmaxf(m, mt);
+    const float alpha = mn == -INFINITY ? 1.0f : exp2f(m - mn);
+    float rs = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = mn == -INFINITY ? 0.0f : exp2f(s[kb][r] - mn);
+        s[kb][r] = p;
+        rs += p;
+      }
+    rs += __shfl_xor(rs, 32);
+    l = l * alpha + rs;
+    m = mn;
+#pragma unroll
+    for (int b = 0; b < DB; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[b][r] *= alpha;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float pv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pv[e] = s[c >> 1][(c & 1) * 8 + e];
+      half8 ph, pl;
+      if constexpr (SPLIT) split8(pv, ph, pl);
+      else
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ph[e] = _Float16(pv[e]);
+#pragma unroll
+      for (int b = 0; b < DB; ++b) {
+        const int vo = (b * 32 + qi) * VS + 16 * c + hl * 8;
+        const half8 vh = *reinterpret_cast<const half8 *>(&vls[0][vo]);
+        if constexpr (SPLIT) {
+          const half8 vl = *reinterpret_cast<const half8 *>(&vls[1][vo]);
+          acc[b] = MFMA(vh, ph, acc[b]);
+          acc[b] = MFMA(vl, ph, acc[b]);
+          acc[b] = MFMA(vh, pl, acc[b]);
+        } else {
+          acc[b] = MFMA(vh, ph, acc[b]);
+        }
+      }
+    }
+  }
+  if (!active || !live) return;
+  const float inv = 1.0f / l;
+  const int64_t obase = int64_t(row0 + qi) * qw + h * HD;
+#pragma unroll
+  for (int b = 0; b < DB; ++b)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      half4 o, olo;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float v = acc[b][r4 * 4 + j] * inv;
+        o[j] = _Float16(v);
+        olo[j] = _Float16(v - float(o[j]));
+      }
+      const int64_t at = obase + b * 32 + r4 * 8 + hl * 4;
+      *reinterpret_cast<half4 *>(out16 + at) = o;
+      if (SPLIT) *reinterpret_cast<half4 *>(out16lo + at) = olo;
+    }
+}
+
 // ---------------------------------------------------------------- decode
 // part layout: [nseq][hq][max_pages][2 + HD] = (max, sum, out[HD]) of one page.
 // One 256-thread workgroup per (page, kv head, sequence).  Every thread issues all of its
@@ -377,8 +594,9 @@ void launch_attn_prefill(const _Float16 *q16, const _Float16 *q16_lo, int T, int
                          const KvGeom &g, const void *kpool, const void *vpool,
                          const int32_t *pages, int max_pages, const int32_t *tile_seq,
                          const int32_t *tile_row0, const int32_t *tile_pos0,
-                         const int32_t *tile_n, int ntiles, _Float16 *out16, _Float16 *out16_lo,
-                         hipStream_t st) {
+                         const int32_t *tile_n, int ntiles, const int32_t *grp_first,
+                         const int32_t *grp_count, int ngroups, _Float16 *out16,
+                         _Float16 *out16_lo, hipStream_t st) {
   LG_REQUIRE(g.page_tokens == P, "attention: page size must be %d", P);
   LG_REQUIRE(hq % g.hkv == 0, "attention: hq %% hkv != 0");
   LG_REQUIRE(ntiles > 0 && T > 0, "attention: empty batch");
@@ -386,6 +604,20 @@ void launch_attn_prefill(const _Float16 *q16, const _Float16 *q16_lo, int T, int
   LG_REQUIRE(split == (g.kv32 != 0), "attention: split queries need the f32 cache and vice versa");
   LG_REQUIRE(!split || out16_lo, "attention: split path needs the lo output plane");
   LG_REQUIRE(int64_t(ntiles) * hq < (1ll << 31), "attention: too many tiles");
+  if (grp_first && g.hd == 128) {
+    LG_REQUIRE(ngroups > 0 && ngroups <= ntiles, "attention: bad tile groups");
+    const dim3 grid(ngroups * hq), block(256);
+    if (split)
+      hipLaunchKernelGGL((attn_prefill_grp_kernel<128, true>), grid, block, 0, st, q16, q16_lo, hq, g,
+                         kpool, vpool, pages, max_pages, grp_first, grp_count, tile_seq, tile_row0,
+                         tile_pos0, tile_n, out16, out16_lo);
+    else
+      hipLaunchKernelGGL((attn_prefill_grp_kernel<128, false>), grid, block, 0, st, q16, q16_lo, hq, g,
+                         kpool, vpool, pages, max_pages, grp_first, grp_count, tile_seq, tile_row0,
+                         tile_pos0, tile_n, out16, out16_lo);
+    HIP_CHECK(hipGetLastError());
+    return;
+  }
   const dim3 grid(ntiles * hq), block(64);
 #define LAUNCH(HDV, S)                                                                              \
   hipLaunchKernelGGL((attn_prefill_kernel<HDV, S>), grid, block, 0, st, q16, q16_lo, hq, g, kpool, vpool, \

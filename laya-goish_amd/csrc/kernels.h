@@ -97,13 +97,16 @@ void launch_rope_kv_tiles(const float *qkv, int hq, const KvGeom &g, const float
 // Causal prefill attention over the paged cache.  Work items: tiles of 32 query rows of one
 // sequence (tile_seq, tile_row0 = first batch row, tile_pos0 = its position, tile_n rows).
 // q16_lo != nullptr selects the split-precision path (requires an f32 cache); the output is
-// then written as hi/lo planes (out16, out16_lo).
+// then written as hi/lo planes (out16, out16_lo).  With grp_first != nullptr (head_dim 128),
+// tiles go in groups of <= 4 consecutive tiles of one sequence (grp_first[i], grp_count[i]
+// for i < ngroups) that share each K/V page through LDS; outputs are bit-identical.
 void launch_attn_prefill(const _Float16 *q16, const _Float16 *q16_lo, int T, int hq,
                          const KvGeom &g, const void *kpool, const void *vpool,
                          const int32_t *pages, int max_pages, const int32_t *tile_seq,
                          const int32_t *tile_row0, const int32_t *tile_pos0,
-                         const int32_t *tile_n, int ntiles, _Float16 *out16, _Float16 *out16_lo,
-                         hipStream_t st);
+                         const int32_t *tile_n, int ntiles, const int32_t *grp_first,
+                         const int32_t *grp_count, int ngroups, _Float16 *out16,
+                         _Float16 *out16_lo, hipStream_t st);
 
 // Decode attention: one query row per sequence (batch nseq), context length ctx_len[s]
 // (including the current token), split over pages into `part`
