@@ -19,6 +19,8 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 #include "quant.h"
@@ -37,6 +39,10 @@ __device__ __forceinline__ float silu(float g) { return g * (1.0f / (1.0f + __ex
 // f16 bits -> f32 with the hardware conversion (exact for every finite value and infinity;
 // a NaN scale gives NaN outputs either way).
 __device__ __forceinline__ float hw_half(uint32_t x) { return float(__builtin_bit_cast(_Float16, uint16_t(x))); }
+
+// Word 3 of a raw buffer resource on gfx9 (32-bit data format, no swizzle); reads beyond
+// num_records return zero.
+constexpr int kBufferFlags = 0x00020000;
 
 __device__ __forceinline__ void put8(const float *v, _Float16 *hi, _Float16 *lo, bool split) {
   half8 h, l;
@@ -70,6 +76,25 @@ struct BLoad {
   fvec sa2, sb2;  // Q4_K, BK == 64: high-nibble sub-block
   rvec raw;       // Q8_0: raw f16 scale bits
   int plane = 0;  // Q4_K, BK == 32: which nibble of each byte
+  // Q8_0: buffer resources of codes and scales; per-chunk byte offsets fixed at init, the K
+  // position goes in the scalar offset (the host keeps rows * cols below 2^31)
+  __amdgpu_buffer_rsrc_t rq, rs;
+  rvec qoff, soff;
+
+  template <class RowMap>
+  __device__ __forceinline__ void init(const DevMatrix &W, RowMap wrow, int t) {
+    if constexpr (KIND == LG_Q8_0) {
+      rq = __builtin_amdgcn_make_buffer_rsrc(W.q, 0, W.rows * W.cols, kBufferFlags);
+      rs = __builtin_amdgcn_make_buffer_rsrc(W.s, 0, W.rows * (W.cols / 32) * 2, kBufferFlags);
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int id = t + 256 * i, r = id / kCPR, c = id % kCPR;
+        const int n = wrow(r);
+        qoff[i] = uint32_t(n * W.cols + c * 16);
+        soff[i] = uint32_t((n * (W.cols / 32) + c * 16 / 32) * 2);
+      }
+    }
+  }
   __device__ __forceinline__ void put(int i, uint4 x) {
     v[4 * i] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
   }
@@ -84,9 +109,8 @@ struct BLoad {
       if constexpr (KIND == LG_F16) {
         put(i, *reinterpret_cast<const uint4 *>(static_cast<const _Float16 *>(W.q) + n * W.cols + k0 + c * 8));
       } else if constexpr (KIND == LG_Q8_0) {
-        const int k = k0 + c * 16;
-        put(i, *reinterpret_cast<const uint4 *>(static_cast<const int8_t *>(W.q) + n * W.cols + k));
-        raw[i] = static_cast<const uint16_t *>(W.s)[n * (W.cols / 32) + k / 32];
+        put(i, __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, qoff[i], k0, 0)));
+        raw[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, soff[i], (k0 / 32) * 2, 0);
       } else if constexpr (KIND == LG_Q6_K) {
         const int k = k0 + c * 16;
         put(i, *reinterpret_cast<const uint4 *>(static_cast<const int8_t *>(W.q) + n * W.cols + k));
@@ -121,20 +145,35 @@ struct BLoad {
       const uint32_t w[4] = {v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
       if constexpr (KIND == LG_F16) {
         *reinterpret_cast<uint4 *>(Bs + r * LDK + c * 8) = get(i);
-      } else if constexpr (KIND == LG_Q8_0) {
+      } else if constexpr (KIND == LG_Q8_0 && MODE == SPLIT) {
+        // exact codes as f16: bytes (q ^ 0x80) under a 0x64 high byte read as f16 are
+        // 1024 + q + 128 exactly; one packed f16 subtraction of 1152 leaves q
+        uint32_t h[8];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint32_t u = w[d] ^ 0x80808080u;
+          h[2 * d] = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+          h[2 * d + 1] = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+        }
+        typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+        const half2v bias = {_Float16(1152.0f), _Float16(1152.0f)};
+        uint32_t q[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, h[e]) - bias);
+        *reinterpret_cast<uint4 *>(Bs + r * LDK + c * 16) = make_uint4(q[0], q[1], q[2], q[3]);
+        *reinterpret_cast<uint4 *>(Bs + r * LDK + c * 16 + 8) = make_uint4(q[4], q[5], q[6], q[7]);
+        if ((c * 16) % 32 == 0) Ds[r * (BK / 32) + c * 16 / 32] = hw_half(raw[i]);
+      } else if constexpr (KIND == LG_Q8_0) {  // FAST: f16(d) * code rounds the exact product once
+        static_assert(MODE == FAST, "Q8_0 tiles are FAST or SPLIT");
         half8 o0, o1;
         const _Float16 d = __builtin_bit_cast(_Float16, uint16_t(raw[i]));
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const _Float16 a = _Float16(int8_t(w[j / 4] >> (8 * (j % 4))));
-          const _Float16 b = _Float16(int8_t(w[2 + j / 4] >> (8 * (j % 4))));
-          // FAST: f16(d) * code rounds the exact product once; SPLIT: the exact code
-          o0[j] = MODE == FAST ? a * d : a;
-          o1[j] = MODE == FAST ? b * d : b;
+          o0[j] = _Float16(int8_t(w[j / 4] >> (8 * (j % 4)))) * d;
+          o1[j] = _Float16(int8_t(w[2 + j / 4] >> (8 * (j % 4)))) * d;
         }
         *reinterpret_cast<half8 *>(Bs + r * LDK + c * 16) = o0;
         *reinterpret_cast<half8 *>(Bs + r * LDK + c * 16 + 8) = o1;
-        if (MODE == SPLIT && (c * 16) % 32 == 0) Ds[r * (BK / 32) + c * 16 / 32] = hw_half(raw[i]);
       } else if constexpr (KIND == LG_Q6_K) {
         float f[16];
 #pragma unroll
@@ -181,32 +220,33 @@ __device__ __forceinline__ void tile_coords(int bid, int nblk, int MT, int NT, i
 
 #define MFMA(a, b, c) __builtin_amdgcn_mfma_f32_32x32x16_f16((a), (b), (c), 0, 0, 0)
 
-// Activation tile loader: BMW x BK halves (+ the lo plane), 16-byte chunks per thread.
-// Register storage is an ext_vector (kept in VGPRs); addresses are recomputed per fetch.
+// Activation tile loader: BMW x BK halves (+ the lo plane), 16-byte chunks per thread, read with
+// buffer loads: the per-thread byte offsets are fixed at init (rows >= M clamped to M - 1, never
+// stored), the K position goes in the scalar offset.  The host keeps M * K * 2 below 2^31.
 template <int BMW, int BK, bool SPLITA>
 struct ALoad {
   static constexpr int kPer = BMW * BK / 8 / 256;
   static constexpr int kRowStep = 256 / (BK / 8);  // rows between a thread's chunks
   typedef uint32_t vec __attribute__((ext_vector_type(4 * kPer)));
+  typedef uint32_t ovec __attribute__((ext_vector_type(kPer < 2 ? 2 : kPer)));
   vec v, vl;
-  const _Float16 *A, *Alo;
-  int row0, rmax, col, K;
-  __device__ __forceinline__ void init(const _Float16 *A_, const _Float16 *Alo_, int m0, int M, int K_, int t) {
-    A = A_;
-    Alo = Alo_;
-    row0 = m0 + t / (BK / 8);
-    rmax = M - 1;  // rows >= M are clamped, never stored
-    col = (t % (BK / 8)) * 8;
-    K = K_;
+  ovec off;
+  __amdgpu_buffer_rsrc_t ra, rl;
+  __device__ __forceinline__ void init(const _Float16 *A_, const _Float16 *Alo_, int m0, int M, int K, int t) {
+    const int bytes = M * K * 2;
+    ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(A_), 0, bytes, kBufferFlags);
+    if constexpr (SPLITA) rl = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(Alo_), 0, bytes, kBufferFlags);
+    const int row0 = m0 + t / (BK / 8), col = (t % (BK / 8)) * 8;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) off[i] = uint32_t((min(row0 + i * kRowStep, M - 1) * K + col) * 2);
   }
   __device__ __forceinline__ void fetch(int k0) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const int64_t off = int64_t(min(row0 + i * kRowStep, rmax)) * K + col + k0;
-      const uint4 x = *reinterpret_cast<const uint4 *>(A + off);
+      const uint4 x = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, off[i], k0 * 2, 0));
       v[4 * i] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
       if constexpr (SPLITA) {
-        const uint4 y = *reinterpret_cast<const uint4 *>(Alo + off);
+        const uint4 y = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rl, off[i], k0 * 2, 0));
         vl[4 * i] = y.x; vl[4 * i + 1] = y.y; vl[4 * i + 2] = y.z; vl[4 * i + 3] = y.w;
       }
     }
@@ -390,6 +430,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
   AL al;
   al.init(A, Alo, m0, M, K, t);
   BL bl;
+  bl.init(W, wrow, t);
   f32x16 acc[WTM][WTN];
 #pragma unroll
   for (int i = 0; i < WTM; ++i)
@@ -491,27 +532,39 @@ bool launch_cfg(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &
   const int tileN = epi == Epi::SWIGLU ? CF::kBN / 2 : CF::kBN;
   if (outN % tileN) return false;
   const int NT = outN / tileN;
-  const int MT = (M + CF::kBM - 1) / CF::kBM;
-  LG_REQUIRE(int64_t(MT) * NT < (1ll << 31), "gemm: grid too large");
-  const dim3 grid(MT * NT), block(256);
   const int K = W.cols, ffn = W.rows / 2;
-#define LAUNCH(E)                                                                                            \
-  do {                                                                                                       \
-    auto fn = gemm_kernel<KIND, E, MODE, BK, WTM, WTN, STAGES>;                                              \
-    static bool attr = false;                                                                                \
-    if (!attr) {                                                                                             \
-      HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(fn),                                      \
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, CF::kLdsBytes));              \
-      attr = true;                                                                                           \
-    }                                                                                                        \
-    hipLaunchKernelGGL(fn, grid, block, CF::kLdsBytes, st, A, Alo, M, K, W, C, C16, C16lo, ldc, bias, MT, NT, \
-                       ffn);                                                                                 \
+  if (KIND == LG_Q8_0)
+    LG_REQUIRE(int64_t(W.rows) * W.cols < (1ll << 31), "gemm: Q8_0 matrix beyond 2 GiB of codes");
+  // buffer offsets of A are 32-bit: launch row blocks of at most 2 GiB of activations each
+  const int64_t rows_cap = ((1ll << 31) - 1) / (int64_t(K) * 2) / CF::kBM * CF::kBM;
+  LG_REQUIRE(rows_cap > 0, "gemm: K=%d too large", K);
+  for (int m0 = 0; m0 < M;) {
+    const int Mc = int(std::min<int64_t>(M - m0, rows_cap));
+    const int MT = (Mc + CF::kBM - 1) / CF::kBM;
+    LG_REQUIRE(int64_t(MT) * NT < (1ll << 31), "gemm: grid too large");
+    const dim3 grid(MT * NT), block(256);
+    const _Float16 *Ac = A + int64_t(m0) * K, *Alc = Alo ? Alo + int64_t(m0) * K : nullptr;
+    float *Cc = C ? C + int64_t(m0) * ldc : nullptr;
+    _Float16 *C16c = C16 ? C16 + int64_t(m0) * ldc : nullptr, *C16lc = C16lo ? C16lo + int64_t(m0) * ldc : nullptr;
+#define LAUNCH(E)                                                                                              \
+  do {                                                                                                         \
+    auto fn = gemm_kernel<KIND, E, MODE, BK, WTM, WTN, STAGES>;                                                \
+    static bool attr = false;                                                                                  \
+    if (!attr) {                                                                                               \
+      HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(fn),                                        \
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, CF::kLdsBytes));                \
+      attr = true;                                                                                             \
+    }                                                                                                          \
+    hipLaunchKernelGGL(fn, grid, block, CF::kLdsBytes, st, Ac, Alc, Mc, K, W, Cc, C16c, C16lc, ldc, bias, MT, NT, \
+                       ffn);                                                                                   \
   } while (0)
-  switch (epi) {
-    case Epi::F32: LAUNCH(0); break;
-    case Epi::ADD: LAUNCH(1); break;
-    case Epi::F16: LAUNCH(2); break;
-    case Epi::SWIGLU: LAUNCH(3); break;
+    switch (epi) {
+      case Epi::F32: LAUNCH(0); break;
+      case Epi::ADD: LAUNCH(1); break;
+      case Epi::F16: LAUNCH(2); break;
+      case Epi::SWIGLU: LAUNCH(3); break;
+    }
+    m0 += Mc;
   }
 #undef LAUNCH
   return true;
