@@ -8,8 +8,8 @@ namespace {
 template <uint32_t KIND>
 void launch_kind(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
                  _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st) {
-  // Chosen by a sweep at the 35,840-token Q8_0/F16 prefill shapes; a 256-wide N tile
-  // falls back to 128 when it does not divide the output width.
+  // Chosen by sweeps at the 35,840-token Q8_0/F16 and 32,768-token Q4_K/Q6_K 7B prefill
+  // shapes; a 256-wide N tile falls back to 128 when it does not divide the output width.
   if (!Alo) {
     if (launch_cfg<KIND, FAST, 64, 4, 4, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
     if (launch_cfg<KIND, FAST, 64, 2, 2, 2>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
@@ -18,7 +18,7 @@ void launch_kind(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix 
   } else if constexpr (KIND == LG_F16) {
     if (launch_cfg<KIND, SPLIT, 64, 2, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
   } else {
-    if (launch_cfg<KIND, SPLIT3, 32, 2, 2, 2>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
+    if (launch_cfg<KIND, SPLIT3, 64, 2, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
   }
   fail(LG_ERR_UNSUPPORTED, "gemm: no tile configuration for N=%d", W.rows);
 }
