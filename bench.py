@@ -120,7 +120,7 @@ def bench_decode(eng, steps):
         if mode == "profiled":
             eng.profile(False)
         eng.seq_free(s)
-    prof = {c: eng.profile_read(c) for c in ("gemv", "attn_decode", "rope_kv", "argmax", "embed")}
+    prof = {c: eng.profile_read(c) for c in ("gemv", "attn_decode", "argmax", "embed")}
     eng.seq_free(base)
     dt = runs[1][1]
     assert np.array_equal(runs[0][2], runs[1][2]), "decode is not deterministic"

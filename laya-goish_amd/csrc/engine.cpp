@@ -750,10 +750,10 @@ void Engine::decode(int sq, int32_t first, int steps, int32_t *tokens, float *lo
   meta.resize(steps + 1, 0);
   for (int p : s.pages) meta.push_back(p);
   const size_t part_floats = size_t(attn_decode_scratch_floats(1, hq, hd, pos0 + steps));
-  const size_t floats = size_t(d) + qkvw + qw + qw + f + V + 64 + part_floats;
+  const size_t floats = size_t(d) + qkvw + qw + f + V + 64 + part_floats;
   ws_dec_.ensure(floats * 4 + meta.size() * 4 + 64 * 8 + 4096);
   float *x = ws_dec_.as<float>();
-  float *qkv = x + d, *q32 = qkv + qkvw, *att = q32 + qw, *act = att + qw, *lg = act + f;
+  float *qkv = x + d, *att = qkv + qkvw, *act = att + qw, *lg = act + f;
   float *part_v = lg + V;
   float *part = part_v + 64;
   int32_t *dm = reinterpret_cast<int32_t *>(part + part_floats);
@@ -768,14 +768,10 @@ void Engine::decode(int sq, int32_t first, int steps, int32_t *tokens, float *lo
     for (int l = 0; l < L; ++l) {
       const Layer &ly = layers_[l];
       for (const ProjPart &p : ly.qkv) gemv(x, p.w, Epi::F32, qkv + p.col0, p.bias, ly.attn_norm);
-      // position, page and context length of this step are known here: kernel arguments
-      prof.begin("rope_kv", stream);
-      launch_rope_kv_token(qkv, hq, g, cos_, sin_, pos0 + i, s.pages[(pos0 + i) / g.page_tokens], q32,
-                           kpool(l), vpool(l), stream);
-      prof.end(double(qkvw) * 4 + double(2 * kvw) * kv_elem(), 0, stream);
+      // the position of this step is a kernel argument; RoPE and the k/v write are fused in
       prof.begin("attn_decode", stream);
-      launch_attn_decode(q32, 1, hq, g, kpool(l), vpool(l), pt, max_pages, nullptr, pos0 + i + 1,
-                         part, att, stream);
+      launch_attn_decode(qkv, hq, g, cos_, sin_, pos0 + i, kpool(l), vpool(l), pt, max_pages, part, att,
+                         stream);
       prof.end(double(pos0 + i + 1) * 2 * kvw * kv_elem(), 4.0 * double(pos0 + i + 1) * qw, stream);
       gemv(att, ly.wo, Epi::ADD, x, nullptr, nullptr);
       gemv(x, ly.wi, Epi::SWIGLU, act, nullptr, ly.ffn_norm);

@@ -13,9 +13,10 @@
 // and hi/lo query planes every product is split (hi.hi + lo.hi + hi.lo: three MFMAs), which
 // keeps scores and outputs f32-faithful.
 //
-// Decode: one workgroup per (sequence, kv head, page): coalesced reads of the page's K rows
-// and V columns, f32 scores for every query head of the group, partial (max, sum, out) per
-// page; a second launch combines the pages of each (sequence, query head).
+// Decode (one new token): one workgroup per (kv head, page): coalesced reads of the page's K
+// rows and V columns, RoPE of the group's query heads (and, on the last page, of the new key,
+// which it also writes into the cache), f32 scores for every query head of the group, partial
+// (max, sum, out) per page; a second launch combines the pages of each query head.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -423,35 +424,31 @@ __global__ __launch_bounds__(256, 1) void attn_prefill_grp_kernel(
 // part layout: [nseq][hq][max_pages][2 + HD] = (max, sum, out[HD]) of one page.
 // One 256-thread workgroup per (page, kv head, sequence).  Every thread issues all of its
 // K and V loads first (16 B each): K rows are split 4 threads per key (32 dims each), V
-// columns 2 threads per dim (32 keys each).  Scores for every query head of the group are
-// reduced over the 4 threads of a key, the page softmax over LDS, then P.V per head.
+// columns 2 threads per dim (32 keys each).  Meanwhile the group's query heads are rotated
+// into LDS and, on the page that holds the new token, its k (rotated) and v are written into
+// the cache and substituted for the stale slot in the registers just loaded.  Scores for
+// every query head of the group are reduced over the 4 threads of a key, the page softmax
+// over LDS, then P.V per head.
 template <int HD, int GRP, typename KV>
-__device__ __forceinline__ void attn_decode_page(const float *__restrict__ q32, int hq, const KvGeom &g,
-                                                 const KV *__restrict__ kpool,
-                                                 const KV *__restrict__ vpool,
-                                                 const int32_t *__restrict__ pages, int max_pages,
-                                                 int len, float *pbase, int64_t hstride);
+__device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, int hq, const KvGeom &g,
+                                                 const float *__restrict__ cosT,
+                                                 const float *__restrict__ sinT, int pos,
+                                                 KV *__restrict__ kpool, KV *__restrict__ vpool,
+                                                 const int32_t *__restrict__ pages, float *pbase,
+                                                 int64_t hstride);
 
 template <int HD, int GRP, typename KV>
-__global__ __launch_bounds__(256) void attn_decode_kernel(const float *__restrict__ q32, int hq, KvGeom g,
-                                                          const KV *__restrict__ kpool,
-                                                          const KV *__restrict__ vpool,
-                                                          const int32_t *__restrict__ pages,
-                                                          int max_pages,
-                                                          const int32_t *__restrict__ ctx_len, int ctx_all,
+__global__ __launch_bounds__(256) void attn_decode_kernel(const float *__restrict__ qkv, int hq, KvGeom g,
+                                                          const float *__restrict__ cosT,
+                                                          const float *__restrict__ sinT, int pos,
+                                                          KV *__restrict__ kpool, KV *__restrict__ vpool,
+                                                          const int32_t *__restrict__ pages, int max_pages,
                                                           float *__restrict__ part) {
   static_assert(HD == 128, "decode attention is written for head_dim 128");
-  const int pi = blockIdx.x, kh = blockIdx.y, s = blockIdx.z;
-  const int t = threadIdx.x;
-  const int len = ctx_len ? ctx_len[s] : ctx_all;
-  float *pbase = part + ((int64_t(s) * hq + kh * GRP) * max_pages + pi) * (2 + HD);
+  const int pi = blockIdx.x, kh = blockIdx.y;
+  float *pbase = part + (int64_t(kh * GRP) * max_pages + pi) * (2 + HD);
   const int64_t hstride = int64_t(max_pages) * (2 + HD);
-  if (pi * P < len) {
-    attn_decode_page<HD, GRP, KV>(q32, hq, g, kpool, vpool, pages, max_pages, len, pbase, hstride);
-  } else if (t < GRP) {  // pages past the context contribute nothing
-    pbase[t * hstride] = -INFINITY;
-    pbase[t * hstride + 1] = 0.0f;
-  }
+  attn_decode_page<HD, GRP, KV>(qkv, hq, g, cosT, sinT, pos, kpool, vpool, pages, pbase, hstride);
 }
 
 // Combine the per-page partials of one (sequence, query head).  Cross-workgroup hand-off
@@ -508,22 +505,25 @@ __global__ __launch_bounds__(256) void attn_decode_combine(const float *__restri
   }
 }
 
-// One page of one (sequence, kv head): scores, page softmax and P.V for each query head.
+// One page of one kv head: scores, page softmax and P.V for each query head.
 template <int HD, int GRP, typename KV>
-__device__ __forceinline__ void attn_decode_page(const float *__restrict__ q32, int hq, const KvGeom &g,
-                                                 const KV *__restrict__ kpool,
-                                                 const KV *__restrict__ vpool,
-                                                 const int32_t *__restrict__ pages, int max_pages,
-                                                 int len, float *pbase, int64_t hstride) {
+__device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, int hq, const KvGeom &g,
+                                                 const float *__restrict__ cosT,
+                                                 const float *__restrict__ sinT, int pos,
+                                                 KV *__restrict__ kpool, KV *__restrict__ vpool,
+                                                 const int32_t *__restrict__ pages, float *pbase,
+                                                 int64_t hstride) {
   constexpr int E = 16 / sizeof(KV);   // elements per 16-byte load
   constexpr int NK = 32 / E;           // loads per thread for its 32-dim K slice
   constexpr int NV = 32 / E;           // loads per thread for its 32-key V slice
+  constexpr int HALF = HD / 2;
   typedef uint32_t kvec __attribute__((ext_vector_type(4 * NK)));
-  const int pi = blockIdx.x, kh = blockIdx.y, s = blockIdx.z;
+  const int pi = blockIdx.x, kh = blockIdx.y;
   const int t = threadIdx.x;
-  const int64_t page = pages[int64_t(s) * max_pages + pi];
-  const KV *Kp = kpool + page * g.page_stride + int64_t(kh) * P * HD;
-  const KV *Vp = vpool + page * g.page_stride + int64_t(kh) * HD * P;
+  const int len = pos + 1;
+  const int64_t page = pages[pi];
+  KV *Kp = kpool + page * g.page_stride + int64_t(kh) * P * HD;
+  KV *Vp = vpool + page * g.page_stride + int64_t(kh) * HD * P;
   const int key = t >> 2, kd0 = (t & 3) * 32;   // K: key row, 32-dim slice
   const int vd = t >> 1, vk0 = (t & 1) * 32;    // V: dim row, 32-key slice
   kvec kr, vr;
@@ -537,13 +537,52 @@ __device__ __forceinline__ void attn_decode_page(const float *__restrict__ q32, 
     const uint4 a = *reinterpret_cast<const uint4 *>(Vp + vd * P + vk0 + i * E);
     vr[4 * i] = a.x; vr[4 * i + 1] = a.y; vr[4 * i + 2] = a.z; vr[4 * i + 3] = a.w;
   }
+  // RoPE (src/models/openthai/model.rs:276-294 applies it to q and k before the dot products)
+  __shared__ float qs[GRP][HD], kn[HD], vn[HD];
+  const float *cs = cosT + int64_t(pos) * HD, *sn = sinT + int64_t(pos) * HD;
+  for (int i = t; i < GRP * HALF; i += 256) {
+    const int gq = i / HALF, j = i % HALF;
+    const float *qr = qkv + (kh * GRP + gq) * HD;
+    const float u = qr[j], v = qr[j + HALF];
+    qs[gq][j] = u * cs[j] - v * sn[j];
+    qs[gq][j + HALF] = v * cs[j + HALF] + u * sn[j + HALF];
+  }
+  const bool cur = pi == pos / P;  // this page holds the new token
+  const int slot = pos % P;
+  if (cur) {
+    if (t < HALF) {
+      const float *kr0 = qkv + (hq + kh) * HD;
+      const float u = kr0[t], v = kr0[t + HALF];
+      const KV a = KV(u * cs[t] - v * sn[t]), b = KV(v * cs[t + HALF] + u * sn[t + HALF]);
+      Kp[slot * HD + t] = a;
+      Kp[slot * HD + t + HALF] = b;
+      kn[t] = float(a);
+      kn[t + HALF] = float(b);
+    } else if (t < HALF + HD) {
+      const int dd = t - HALF;
+      const KV v = KV(qkv[(hq + g.hkv + kh) * HD + dd]);
+      Vp[dd * P + slot] = v;
+      vn[dd] = float(v);
+    }
+  }
+  __syncthreads();
+  if (cur) {  // the registers hold the slot as it was before this step: use the new values
+    KV *k8 = reinterpret_cast<KV *>(&kr);
+    if (key == slot)
+#pragma unroll
+      for (int e = 0; e < 32; ++e) k8[e] = KV(kn[kd0 + e]);
+    KV *v8 = reinterpret_cast<KV *>(&vr);
+#pragma unroll
+    for (int e = 0; e < 32; ++e)
+      if (vk0 + e == slot) v8[e] = KV(vn[vd]);
+  }
   __shared__ float sc[GRP][P];
 
   const float inv_sqrt = 1.0f / sqrtf(float(HD));
   const bool valid = pi * P + key < len;
 #pragma unroll
   for (int gq = 0; gq < GRP; ++gq) {
-    const float *q = q32 + int64_t(s) * hq * HD + (kh * GRP + gq) * HD + kd0;
+    const float *q = &qs[gq][kd0];
     float d = 0.0f;
 #pragma unroll
     for (int i = 0; i < NK; ++i) {
@@ -638,28 +677,27 @@ int64_t attn_decode_scratch_floats(int nseq, int hq, int hd, int max_ctx) {
   return int64_t(nseq) * hq * pages * (2 + hd);
 }
 
-void launch_attn_decode(const float *q32, int nseq, int hq, const KvGeom &g, const void *kpool,
-                        const void *vpool, const int32_t *pages, int max_pages,
-                        const int32_t *ctx_len, int max_ctx, float *part, float *out,
-                        hipStream_t st) {
+void launch_attn_decode(const float *qkv, int hq, const KvGeom &g, const float *cosT, const float *sinT,
+                        int pos, void *kpool, void *vpool, const int32_t *pages, int max_pages,
+                        float *part, float *out, hipStream_t st) {
   LG_REQUIRE(g.page_tokens == P, "attention: page size must be %d", P);
   LG_REQUIRE(g.hd == 128, "decode attention: head_dim %d not supported (128)", g.hd);
-  LG_REQUIRE(nseq > 0 && max_ctx > 0, "decode attention: empty");
-  const int np = (max_ctx + P - 1) / P;
+  LG_REQUIRE(pos >= 0, "decode attention: negative position");
+  const int np = pos / P + 1;
   LG_REQUIRE(np <= max_pages, "decode attention: context exceeds the page table");
   LG_REQUIRE(np <= 1024, "decode attention: context of %d pages exceeds the combine stage", np);
   const int grp = hq / g.hkv;
-  const dim3 grid(np, g.hkv, nseq), block(256);
-#define CASE(G)                                                                                     \
-  case G:                                                                                           \
-    if (g.kv32)                                                                                     \
-      hipLaunchKernelGGL((attn_decode_kernel<128, G, float>), grid, block, 0, st, q32, hq, g,        \
-                         static_cast<const float *>(kpool), static_cast<const float *>(vpool), pages, \
-                         max_pages, ctx_len, max_ctx, part);                                             \
-    else                                                                                            \
-      hipLaunchKernelGGL((attn_decode_kernel<128, G, _Float16>), grid, block, 0, st, q32, hq, g,     \
-                         static_cast<const _Float16 *>(kpool), static_cast<const _Float16 *>(vpool), \
-                         pages, max_pages, ctx_len, max_ctx, part);                                      \
+  const dim3 grid(np, g.hkv), block(256);
+#define CASE(G)                                                                                          \
+  case G:                                                                                                \
+    if (g.kv32)                                                                                          \
+      hipLaunchKernelGGL((attn_decode_kernel<128, G, float>), grid, block, 0, st, qkv, hq, g, cosT, sinT, \
+                         pos, static_cast<float *>(kpool), static_cast<float *>(vpool), pages, max_pages, \
+                         part);                                                                          \
+    else                                                                                                 \
+      hipLaunchKernelGGL((attn_decode_kernel<128, G, _Float16>), grid, block, 0, st, qkv, hq, g, cosT,    \
+                         sinT, pos, static_cast<_Float16 *>(kpool), static_cast<_Float16 *>(vpool), pages, \
+                         max_pages, part);                                                               \
     break;
   switch (grp) {
     CASE(1) CASE(2) CASE(4) CASE(7) CASE(8)
@@ -667,8 +705,8 @@ void launch_attn_decode(const float *q32, int nseq, int hq, const KvGeom &g, con
   }
 #undef CASE
   HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL((attn_decode_combine<128>), dim3(hq, nseq), dim3(256), 0, st, part, hq, max_pages,
-                     ctx_len, max_ctx, out);
+  hipLaunchKernelGGL((attn_decode_combine<128>), dim3(hq, 1), dim3(256), 0, st, part, hq, max_pages,
+                     static_cast<const int32_t *>(nullptr), pos + 1, out);
   HIP_CHECK(hipGetLastError());
 }
 

@@ -94,7 +94,8 @@ constexpr int chunk_elems() { return KIND == LG_F16 ? 8 : 16; }
 // Scale of chunk ch of row n (Q8_0: per 32-element block, Q6_K: per 16).
 template <uint32_t KIND>
 __device__ __forceinline__ float chunk_scale(const DevMatrix &W, int64_t n, int ch) {
-  if constexpr (KIND == LG_Q8_0) return half_bits(static_cast<const uint16_t *>(W.s)[n * (W.cols / 32) + ch / 2]);
+  if constexpr (KIND == LG_Q8_0)  // hardware f16 -> f32: exact for every finite scale and infinity
+    return float(static_cast<const _Float16 *>(W.s)[n * (W.cols / 32) + ch / 2]);
   else if constexpr (KIND == LG_Q6_K) return static_cast<const float *>(W.s)[n * (W.cols / 16) + ch];
   else return 1.0f;
 }

@@ -117,35 +117,6 @@ __device__ __forceinline__ void kv_put(void *pool, int64_t i, float v) {
 
 // Decode form: one token whose position and KV page the host already knows (kernel arguments,
 // so the only memory round trip is the q|k|v row and the table rows).  q goes out in f32.
-template <bool KV32>
-__global__ __launch_bounds__(kT) void rope_kv_token_kernel(const float *__restrict__ row, int hq, KvGeom g,
-                                                           const float *__restrict__ cosT,
-                                                           const float *__restrict__ sinT, int pos, int page,
-                                                           float *__restrict__ q32, void *__restrict__ kpool,
-                                                           void *__restrict__ vpool) {
-  const int hd = g.hd, half = hd / 2, qw = hq * hd, kvw = g.hkv * hd;
-  const float *cs = cosT + int64_t(pos) * hd, *sn = sinT + int64_t(pos) * hd;
-  const int slot = pos % g.page_tokens;
-  const int64_t pbase = int64_t(page) * g.page_stride;
-  for (int i = threadIdx.x; i < (hq + g.hkv) * half; i += kT) {
-    const int h = i / half, j = i % half;  // heads 0..hq-1 are q, then the kv heads
-    const float u = row[h * hd + j], v = row[h * hd + j + half];
-    const float a = u * cs[j] - v * sn[j], b = v * cs[j + half] + u * sn[j + half];
-    if (h < hq) {
-      q32[h * hd + j] = a;
-      q32[h * hd + j + half] = b;
-    } else {
-      const int64_t at = pbase + (int64_t(h - hq) * g.page_tokens + slot) * hd;
-      kv_put<KV32>(kpool, at + j, a);
-      kv_put<KV32>(kpool, at + j + half, b);
-    }
-  }
-  for (int i = threadIdx.x; i < kvw; i += kT) {
-    const int h = i / hd, dd = i % hd;
-    kv_put<KV32>(vpool, pbase + (int64_t(h) * hd + dd) * g.page_tokens + slot, row[qw + kvw + i]);
-  }
-}
-
 // Prefill form: one workgroup per attention tile (<= 32 consecutive tokens of one sequence).
 // q and k are rotated token by token (rows are contiguous); v is staged through LDS per kv
 // head so that its transposed page layout is written as runs of consecutive slots instead of
@@ -391,18 +362,6 @@ void launch_embed(const void *table, uint32_t kind, const int32_t *ids, int T, i
   LG_REQUIRE(n > 0 && n / kT < (1ll << 31), "embed: bad size");
   hipLaunchKernelGGL(embed_kernel, dim3(unsigned((n + kT - 1) / kT)), dim3(kT), 0, st, table, kind, ids,
                      T, d, vocab, x);
-  HIP_CHECK(hipGetLastError());
-}
-
-void launch_rope_kv_token(const float *qkv, int hq, const KvGeom &g, const float *cosT, const float *sinT,
-                          int pos, int page, float *q32, void *kpool, void *vpool, hipStream_t st) {
-  LG_REQUIRE(g.hd % 2 == 0 && q32 && pos >= 0 && page >= 0, "rope_kv: bad arguments");
-  if (g.kv32)
-    hipLaunchKernelGGL(rope_kv_token_kernel<true>, dim3(1), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, pos, page,
-                       q32, kpool, vpool);
-  else
-    hipLaunchKernelGGL(rope_kv_token_kernel<false>, dim3(1), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, pos, page,
-                       q32, kpool, vpool);
   HIP_CHECK(hipGetLastError());
 }
 

@@ -83,10 +83,7 @@ struct KvGeom {
 // RoPE on q and k of q|k|v rows ((hq+2hkv)*hd f32) with tables cos/sin[ctx][hd], q written
 // out, k and v written into the K page rows [hkv][page_tokens][hd] and V page columns
 // [hkv][hd][page_tokens] of the layer pools (value format per g.kv32).
-// This form: one decode token at a position and KV page known to the host; q to q32.
-void launch_rope_kv_token(const float *qkv, int hq, const KvGeom &g, const float *cosT, const float *sinT,
-                          int pos, int page, float *q32, void *kpool, void *vpool, hipStream_t st);
-// The same for a prefill batch, one workgroup per attention tile (<= 32 consecutive tokens
+// This form: a prefill batch, one workgroup per attention tile (<= 32 consecutive tokens
 // of one sequence, rows row0.., positions pos0..); q goes to f16 planes.  head_dim <= 128.
 void launch_rope_kv_tiles(const float *qkv, int hq, const KvGeom &g, const float *cosT,
                           const float *sinT, const int32_t *pages, int max_pages,
@@ -108,13 +105,13 @@ void launch_attn_prefill(const _Float16 *q16, const _Float16 *q16_lo, int T, int
                          const int32_t *grp_count, int ngroups, _Float16 *out16,
                          _Float16 *out16_lo, hipStream_t st);
 
-// Decode attention: one query row per sequence (batch nseq), context length ctx_len[s]
-// (including the current token), split over pages into `part`
-// (attn_decode_scratch_floats), then combined per (sequence, query head) by a second launch.
-void launch_attn_decode(const float *q32, int nseq, int hq, const KvGeom &g, const void *kpool,
-                        const void *vpool, const int32_t *pages, int max_pages,
-                        const int32_t *ctx_len, int max_ctx, float *part, float *out,
-                        hipStream_t st);
+// Decode attention for one new token at position pos of one sequence: q|k|v row `qkv` (before
+// RoPE); RoPE of q and k (tables cos/sin[ctx][hd]) and the k/v write into the cache slot are
+// fused in.  Split over the pages 0..pos/64 into `part` (attn_decode_scratch_floats), then
+// combined per query head by a second launch into out[hq * hd].
+void launch_attn_decode(const float *qkv, int hq, const KvGeom &g, const float *cosT, const float *sinT,
+                        int pos, void *kpool, void *vpool, const int32_t *pages, int max_pages,
+                        float *part, float *out, hipStream_t st);
 int64_t attn_decode_scratch_floats(int nseq, int hq, int hd, int max_ctx);
 
 // Gather rows, final RMSNorm and the option head: logits[r][j] = h_r . W[ids[j]].
