@@ -23,6 +23,7 @@
 
 #include "common.h"
 #include "kernels.h"
+#include "wave.h"
 
 namespace lg {
 namespace {
@@ -422,13 +423,15 @@ __global__ __launch_bounds__(256, 1) void attn_prefill_grp_kernel(
 
 // ---------------------------------------------------------------- decode
 // part layout: [nseq][hq][max_pages][2 + HD] = (max, sum, out[HD]) of one page.
-// One 256-thread workgroup per (page, kv head, sequence).  Every thread issues all of its
-// K and V loads first (16 B each): K rows are split 4 threads per key (32 dims each), V
-// columns 2 threads per dim (32 keys each).  Meanwhile the group's query heads are rotated
-// into LDS and, on the page that holds the new token, its k (rotated) and v are written into
-// the cache and substituted for the stale slot in the registers just loaded.  Scores for
-// every query head of the group are reduced over the 4 threads of a key, the page softmax
-// over LDS, then P.V per head.
+// One 256-thread workgroup per (page, kv head).  Every thread issues its query/RoPE loads, then
+// all of its K and V loads: K rows and V columns of the page are read as consecutive 16-byte
+// words (thread t takes word t + 256 i), so each load instruction covers one contiguous
+// kilobyte per wave.  A thread thus holds E consecutive dims of NL keys (K) and E consecutive
+// keys of NL dims (V).  Meanwhile the group's query heads are rotated into LDS and, on the page
+// that holds the new token, its k (rotated) and v are written into the cache and substituted
+// for the stale slot in the registers just loaded.  Scores are reduced over the lanes of a key
+// with DPP moves, the page softmax runs on one wave per head, then P.V reduces over the lanes
+// of a dim.
 template <int HD, int GRP, typename KV>
 __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, int hq, const KvGeom &g,
                                                  const float *__restrict__ cosT,
@@ -453,56 +456,69 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float *__restric
 
 // Combine the per-page partials of one (sequence, query head).  Cross-workgroup hand-off
 // through memory would need an agent-scope release (an L2 write-back on this part) in every
-// page workgroup, so the combine is its own small launch.
+// page workgroup, so the combine is its own small launch.  Thread (d, half) owns output dim d
+// over the pages half, half + 2, ...; each batch of 2*CB pages is loaded in one round trip
+// together with the page maxima and sums (indices clamped, surplus pages weighted 0).
 template <int HD>
 __global__ __launch_bounds__(256) void attn_decode_combine(const float *__restrict__ part, int hq,
                                                            int max_pages,
                                                            const int32_t *__restrict__ ctx_len, int ctx_all,
                                                            float *__restrict__ out) {
+  static_assert(HD == 128, "two threads per output dim");
+  constexpr int CB = 32;  // pages per thread per batch
   const int h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
   const int np = ((ctx_len ? ctx_len[s] : ctx_all) + P - 1) / P;
   __shared__ float wm[1024], wl[1024];
   __shared__ float red[4], sacc[2][HD], sl[2];
-  {
-    const float *pb = part + ((int64_t(s) * hq + h) * max_pages) * (2 + HD);
-    // page maxima and sums, gathered in parallel
-    float M = -INFINITY;
-    for (int i = t; i < np; i += 256) {
-      wm[i] = pb[int64_t(i) * (2 + HD)];
-      wl[i] = pb[int64_t(i) * (2 + HD) + 1];
-      M = fmaxf(M, wm[i]);
-    }
+  const float *pb = part + ((int64_t(s) * hq + h) * max_pages) * (2 + HD);
+  const int d = t & (HD - 1), half = t >> 7;
+  // page maxima and sums (np <= 1024: four per thread), then the first batch of outputs
+  float m4[4], l4[4];
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
-    if ((t & 63) == 0) red[t >> 6] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int i = t; i < np; i += 256) wm[i] = wm[i] == -INFINITY ? 0.0f : __expf(wm[i] - M);
-    __syncthreads();
-    // weighted sum of the page outputs: thread (d, half) takes every other page, 8 loads in flight
-    const int d = t & (HD - 1), half = t >> 7;
-    float acc = 0.0f, L = 0.0f;
-    for (int i0 = half; i0 < np; i0 += 16) {
-      float v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int i = i0 + 2 * u;
-        v[u] = i < np ? pb[int64_t(i) * (2 + HD) + 2 + d] : 0.0f;
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int i = i0 + 2 * u;
-        if (i < np) {
-          acc += v[u] * wm[i];
-          L += wl[i] * wm[i];
-        }
-      }
-    }
-    sacc[half][d] = acc;
-    if (d == 0) sl[half] = L;
-    __syncthreads();
-    if (t < HD) out[(int64_t(s) * hq + h) * HD + t] = (sacc[0][t] + sacc[1][t]) / (sl[0] + sl[1]);
+  for (int u = 0; u < 4; ++u) {
+    const int i = min(t + 256 * u, np - 1);
+    m4[u] = pb[int64_t(i) * (2 + HD)];
+    l4[u] = pb[int64_t(i) * (2 + HD) + 1];
   }
+  float ov[CB];
+#pragma unroll
+  for (int u = 0; u < CB; ++u) ov[u] = pb[int64_t(min(half + 2 * u, np - 1)) * (2 + HD) + 2 + d];
+  float M = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+    if (t + 256 * u < np) M = fmaxf(M, m4[u]);
+  M = wave_max_dpp(M);
+  if ((t & 63) == 0) red[t >> 6] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int i = t + 256 * u;
+    if (i < np) {
+      wm[i] = m4[u] == -INFINITY ? 0.0f : __expf(m4[u] - M);
+      wl[i] = l4[u];
+    }
+  }
+  __syncthreads();
+  float acc = 0.0f, L = 0.0f;
+  for (int b0 = 0; b0 < np; b0 += 2 * CB) {
+    if (b0 > 0) {
+#pragma unroll
+      for (int u = 0; u < CB; ++u) ov[u] = pb[int64_t(min(b0 + half + 2 * u, np - 1)) * (2 + HD) + 2 + d];
+    }
+#pragma unroll
+    for (int u = 0; u < CB; ++u) {
+      const int i = b0 + half + 2 * u;
+      if (i < np) {
+        acc += ov[u] * wm[i];
+        L += wl[i] * wm[i];
+      }
+    }
+  }
+  sacc[half][d] = acc;
+  if (d == 0) sl[half] = L;
+  __syncthreads();
+  if (t < HD) out[(int64_t(s) * hq + h) * HD + t] = (sacc[0][t] + sacc[1][t]) / (sl[0] + sl[1]);
 }
 
 // One page of one kv head: scores, page softmax and P.V for each query head.
@@ -513,101 +529,128 @@ __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, 
                                                  KV *__restrict__ kpool, KV *__restrict__ vpool,
                                                  const int32_t *__restrict__ pages, float *pbase,
                                                  int64_t hstride) {
-  constexpr int E = 16 / sizeof(KV);   // elements per 16-byte load
-  constexpr int NK = 32 / E;           // loads per thread for its 32-dim K slice
-  constexpr int NV = 32 / E;           // loads per thread for its 32-key V slice
+  constexpr int E = 16 / sizeof(KV);          // elements per 16-byte word: 4 (f32) or 8 (f16)
+  constexpr int NL = P * HD / E / 256;        // words per thread of K (and of V)
+  constexpr int LPK = HD / E;                 // lanes per key row of K
+  constexpr int LPD = P / E;                  // lanes per dim column of V
   constexpr int HALF = HD / 2;
-  typedef uint32_t kvec __attribute__((ext_vector_type(4 * NK)));
+  constexpr int NQP = (GRP * HALF + 255) / 256;  // rotation pairs per thread
+  static_assert(LPK == 16 || LPK == 32, "key rows span 16 or 32 lanes");
+  static_assert(LPD == 8 || LPD == 16, "dim columns span 8 or 16 lanes");
   const int pi = blockIdx.x, kh = blockIdx.y;
-  const int t = threadIdx.x;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int len = pos + 1;
   const int64_t page = pages[pi];
   KV *Kp = kpool + page * g.page_stride + int64_t(kh) * P * HD;
   KV *Vp = vpool + page * g.page_stride + int64_t(kh) * HD * P;
-  const int key = t >> 2, kd0 = (t & 3) * 32;   // K: key row, 32-dim slice
-  const int vd = t >> 1, vk0 = (t & 1) * 32;    // V: dim row, 32-key slice
-  kvec kr, vr;
-#pragma unroll
-  for (int i = 0; i < NK; ++i) {
-    const uint4 a = *reinterpret_cast<const uint4 *>(Kp + key * HD + kd0 + i * E);
-    kr[4 * i] = a.x; kr[4 * i + 1] = a.y; kr[4 * i + 2] = a.z; kr[4 * i + 3] = a.w;
-  }
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const uint4 a = *reinterpret_cast<const uint4 *>(Vp + vd * P + vk0 + i * E);
-    vr[4 * i] = a.x; vr[4 * i + 1] = a.y; vr[4 * i + 2] = a.z; vr[4 * i + 3] = a.w;
-  }
-  // RoPE (src/models/openthai/model.rs:276-294 applies it to q and k before the dot products)
-  __shared__ float qs[GRP][HD], kn[HD], vn[HD];
   const float *cs = cosT + int64_t(pos) * HD, *sn = sinT + int64_t(pos) * HD;
-  for (int i = t; i < GRP * HALF; i += 256) {
-    const int gq = i / HALF, j = i % HALF;
+  // query rotation inputs and the new token's k/v first (small); every load is unconditional
+  // (clamped index) so that none is sunk behind the page loads
+  float qu[NQP], qv[NQP], c0[NQP], c1[NQP], s0[NQP], s1[NQP];
+#pragma unroll
+  for (int e = 0; e < NQP; ++e) {
+    const int idx = min(t + 256 * e, GRP * HALF - 1);
+    const int gq = idx / HALF, j = idx % HALF;
     const float *qr = qkv + (kh * GRP + gq) * HD;
-    const float u = qr[j], v = qr[j + HALF];
-    qs[gq][j] = u * cs[j] - v * sn[j];
-    qs[gq][j + HALF] = v * cs[j + HALF] + u * sn[j + HALF];
+    qu[e] = qr[j];
+    qv[e] = qr[j + HALF];
+    c0[e] = cs[j];
+    c1[e] = cs[j + HALF];
+    s0[e] = sn[j];
+    s1[e] = sn[j + HALF];
   }
-  const bool cur = pi == pos / P;  // this page holds the new token
+  const int jn = t & (HALF - 1);  // new key: thread t < HALF rotates pair (jn, jn + HALF)
+  const float *kr0 = qkv + (hq + kh) * HD;
+  const float nku = kr0[jn], nkv = kr0[jn + HALF];
+  const float nc0 = cs[jn], nc1 = cs[jn + HALF], ns0 = sn[jn], ns1 = sn[jn + HALF];
+  const float nvv = qkv[(hq + g.hkv + kh) * HD + min(max(t - HALF, 0), HD - 1)];
+  __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the page's: they return first
+  uint4 kr[NL], vr[NL];
+#pragma unroll
+  for (int i = 0; i < NL; ++i) kr[i] = reinterpret_cast<const uint4 *>(Kp)[t + 256 * i];
+#pragma unroll
+  for (int i = 0; i < NL; ++i) vr[i] = reinterpret_cast<const uint4 *>(Vp)[t + 256 * i];
+  // RoPE (src/models/openthai/model.rs:276-294 applies it to q and k before the dot products)
+  __shared__ float qs[GRP * HD + HD];  // tail: landing row for idle threads
+  __shared__ float nka[256], nkb[256], nvs[256];  // new k (pairs j, j + HD/2) and v staged per thread
+  __shared__ float sc[GRP][P];
+#pragma unroll
+  for (int e = 0; e < NQP; ++e) {
+    const int idx = t + 256 * e;
+    const int gq = idx / HALF, j = idx % HALF;
+    const int row = idx < GRP * HALF ? gq : GRP;
+    qs[row * HD + j] = qu[e] * c0[e] - qv[e] * s0[e];
+    qs[row * HD + j + HALF] = qv[e] * c1[e] + qu[e] * s1[e];
+  }
+  const bool cur = pi == pos / P;  // this page holds the new token (uniform per workgroup)
   const int slot = pos % P;
-  if (cur) {
-    if (t < HALF) {
-      const float *kr0 = qkv + (hq + kh) * HD;
-      const float u = kr0[t], v = kr0[t + HALF];
-      const KV a = KV(u * cs[t] - v * sn[t]), b = KV(v * cs[t + HALF] + u * sn[t + HALF]);
-      Kp[slot * HD + t] = a;
-      Kp[slot * HD + t + HALF] = b;
-      kn[t] = float(a);
-      kn[t + HALF] = float(b);
-    } else if (t < HALF + HD) {
-      const int dd = t - HALF;
-      const KV v = KV(qkv[(hq + g.hkv + kh) * HD + dd]);
-      Vp[dd * P + slot] = v;
-      vn[dd] = float(v);
+  {  // the new token's rotated k and its v, computed and staged in LDS by every thread (idle
+     // threads write junk to their own slots), so their loads stay ahead of the page's; only
+     // the page that holds the slot stores them into the cache
+    const KV a = KV(nku * nc0 - nkv * ns0), b = KV(nkv * nc1 + nku * ns1), v = KV(nvv);
+    nka[t] = float(a);
+    nkb[t] = float(b);
+    nvs[t] = float(v);
+    if (cur) {
+      if (t < HALF) {
+        Kp[slot * HD + t] = a;
+        Kp[slot * HD + t + HALF] = b;
+      } else if (t < HALF + HD) {
+        Vp[(t - HALF) * P + slot] = v;
+      }
     }
   }
   __syncthreads();
+  const int kd0 = (t * E) % HD;   // K: first dim of this thread's words (same for every i)
+  const int vk0 = (t * E) % P;    // V: first key of this thread's words (same for every i)
   if (cur) {  // the registers hold the slot as it was before this step: use the new values
-    KV *k8 = reinterpret_cast<KV *>(&kr);
-    if (key == slot)
 #pragma unroll
-      for (int e = 0; e < 32; ++e) k8[e] = KV(kn[kd0 + e]);
-    KV *v8 = reinterpret_cast<KV *>(&vr);
+    for (int i = 0; i < NL; ++i) {
+      KV *k8 = reinterpret_cast<KV *>(&kr[i]);
+      if ((t + 256 * i) * E / HD == slot)
 #pragma unroll
-    for (int e = 0; e < 32; ++e)
-      if (vk0 + e == slot) v8[e] = KV(vn[vd]);
+        for (int e = 0; e < E; ++e) {
+          const int dd = kd0 + e;
+          k8[e] = KV(dd < HALF ? nka[dd] : nkb[dd - HALF]);
+        }
+      KV *v8 = reinterpret_cast<KV *>(&vr[i]);
+      const int dim = (t + 256 * i) * E / P;
+#pragma unroll
+      for (int e = 0; e < E; ++e)
+        if (vk0 + e == slot) v8[e] = KV(nvs[HALF + dim]);
+    }
   }
-  __shared__ float sc[GRP][P];
-
   const float inv_sqrt = 1.0f / sqrtf(float(HD));
-  const bool valid = pi * P + key < len;
 #pragma unroll
   for (int gq = 0; gq < GRP; ++gq) {
-    const float *q = &qs[gq][kd0];
-    float d = 0.0f;
+    float q[E];
 #pragma unroll
-    for (int i = 0; i < NK; ++i) {
-      const KV *k8 = reinterpret_cast<const KV *>(&kr) + i * E;
+    for (int e = 0; e < E; ++e) q[e] = qs[gq * HD + kd0 + e];
 #pragma unroll
-      for (int j = 0; j < E; ++j) d += q[i * E + j] * float(k8[j]);
+    for (int i = 0; i < NL; ++i) {
+      const KV *k8 = reinterpret_cast<const KV *>(&kr[i]);
+      float d = 0.0f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) d = fmaf(q[e], float(k8[e]), d);
+      const int key = (t + 256 * i) * E / HD;
+      if constexpr (LPK == 32) {
+        d = half_sum_odd_rows(d);  // lanes 16-31 / 48-63 hold the key's sum
+        if ((lane & 31) == 16) sc[gq][key] = pi * P + key < len ? d * inv_sqrt : -INFINITY;
+      } else {
+        d = row_sum(d);
+        if ((lane & 15) == 0) sc[gq][key] = pi * P + key < len ? d * inv_sqrt : -INFINITY;
+      }
     }
-    d += __shfl_xor(d, 1);
-    d += __shfl_xor(d, 2);
-    if ((t & 3) == 0) sc[gq][key] = valid ? d * inv_sqrt : -INFINITY;
   }
   __syncthreads();
-  // page softmax per query head: wave w < GRP reduces head w's 64 scores
-  for (int gq = t >> 6; gq < GRP; gq += 4) {
-    const int l = t & 63;
-    const float v = sc[gq][l];
-    float mx = v;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  // page softmax per query head: wave w handles heads w, w + 4, ...
+  for (int gq = wave; gq < GRP; gq += 4) {
+    const float v = sc[gq][lane];
+    const float mx = wave_max_dpp(v);
     const float p = v == -INFINITY ? 0.0f : __expf(v - mx);
-    float sum = p;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-    sc[gq][l] = p;
-    if (l == 0) {
+    const float sum = wave_sum_dpp(p);
+    sc[gq][lane] = p;
+    if (lane == 0) {
       pbase[gq * hstride] = mx;
       pbase[gq * hstride + 1] = sum;
     }
@@ -615,15 +658,18 @@ __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, 
   __syncthreads();
 #pragma unroll
   for (int gq = 0; gq < GRP; ++gq) {
-    float a = 0.0f;
+    float p[E];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const KV *v8 = reinterpret_cast<const KV *>(&vr) + i * E;
+    for (int e = 0; e < E; ++e) p[e] = sc[gq][vk0 + e];
 #pragma unroll
-      for (int j = 0; j < E; ++j) a += sc[gq][vk0 + i * E + j] * float(v8[j]);
+    for (int i = 0; i < NL; ++i) {
+      const KV *v8 = reinterpret_cast<const KV *>(&vr[i]);
+      float a = 0.0f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) a = fmaf(p[e], float(v8[e]), a);
+      a = LPD == 16 ? row_sum(a) : group8_sum(a);
+      if ((lane & (LPD - 1)) == 0) pbase[gq * hstride + 2 + (t + 256 * i) * E / P] = a;
     }
-    a += __shfl_xor(a, 1);
-    if ((t & 1) == 0) pbase[gq * hstride + 2 + vd] = a;
   }
 }
 

@@ -10,6 +10,7 @@
 #include "common.h"
 #include "kernels.h"
 #include "quant.h"
+#include "wave.h"
 
 namespace lg {
 namespace {
@@ -18,92 +19,127 @@ constexpr int kThreads = 256;
 
 __device__ __forceinline__ float silu(float g) { return g * (1.0f / (1.0f + __expf(-g))); }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return wave_sum_dpp(v); }
 
-// Stage x (optionally RMS-normalised) into LDS.  Layout: for chunk size E (elements per
-// lane load), float4 index (i * nchunk + c) holds elements c*E + 4i .. c*E + 4i + 3.
+// Stage x (times the RMSNorm weight when norm_w is set) into LDS and return the RMSNorm factor
+// 1/sqrt(mean(x^2) + eps) (1 without a norm), which the caller applies to its finished row sums:
+// y = inv * sum_k W[n][k] * (x[k] * w[k]).  Layout: for chunk size E (elements per lane load),
+// float4 index (i * nchunk + c) holds elements c*E + 4i .. c*E + 4i + 3.  This form serves K
+// beyond the register prologue of gemv_kernel (two float4 of x per thread per round trip).
 template <int E>
-__device__ void stage_x(const float *__restrict__ x, int K, const float *__restrict__ norm_w,
-                        float eps, float4 *xs, float *red) {
-  const int t = threadIdx.x;
-  float inv = 1.0f;
+__device__ float stage_x(const float *__restrict__ x, int K, const float *__restrict__ norm_w,
+                         float eps, float4 *xs, float *red) {
+  constexpr int B = 2;
+  const int t = threadIdx.x, nq = K / 4, nchunk = K / E;
+  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+  const float4 *w4 = reinterpret_cast<const float4 *>(norm_w);
+  float ss = 0.0f;
+  for (int q0 = 0; q0 < nq; q0 += B * kThreads) {
+    float4 v[B], w[B];
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      const int q = q0 + j * kThreads + t;
+      v[j] = q < nq ? x4[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (norm_w) w[j] = q < nq ? w4[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int j = 0; j < B; ++j) {
+      const int q = q0 + j * kThreads + t;
+      if (q >= nq) continue;
+      if (norm_w) {
+        ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+        v[j].x *= w[j].x;
+        v[j].y *= w[j].y;
+        v[j].z *= w[j].z;
+        v[j].w *= w[j].w;
+      }
+      const int c = q / (E / 4), i = q % (E / 4);
+      xs[i * nchunk + c] = v[j];
+    }
+  }
   if (norm_w) {
-    float ss = 0.0f;
-    for (int k = t; k < K; k += kThreads) ss += x[k] * x[k];
     ss = wave_sum(ss);
     if ((t & 63) == 0) red[t >> 6] = ss;
-    __syncthreads();
-    const float tot = red[0] + red[1] + red[2] + red[3];
-    inv = 1.0f / sqrtf(tot / float(K) + eps);
-  }
-  const int nchunk = K / E;
-  for (int q = t; q < K / 4; q += kThreads) {
-    const int c = q / (E / 4), i = q % (E / 4);
-    float4 v = reinterpret_cast<const float4 *>(x)[q];
-    if (norm_w) {
-      const float4 w = reinterpret_cast<const float4 *>(norm_w)[q];
-      v.x = v.x * inv * w.x;
-      v.y = v.y * inv * w.y;
-      v.z = v.z * inv * w.z;
-      v.w = v.w * inv * w.w;
-    }
-    xs[i * nchunk + c] = v;
   }
   __syncthreads();
-}
-
-__device__ __forceinline__ float dot16_i8(uint4 c, const float4 *xs, int plane_stride, int ch) {
-  const uint32_t w[4] = {c.x, c.y, c.z, c.w};
-  float s = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float4 xv = xs[i * plane_stride + ch];
-    const uint32_t word = w[i];
-    s += float(int8_t(word)) * xv.x;
-    s += float(int8_t(word >> 8)) * xv.y;
-    s += float(int8_t(word >> 16)) * xv.z;
-    s += float(int8_t(word >> 24)) * xv.w;
-  }
-  return s;
-}
-
-__device__ __forceinline__ float dot8_f16(uint4 c, const float4 *xs, int plane_stride, int ch) {
-  const uint32_t w[4] = {c.x, c.y, c.z, c.w};
-  float s = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const float4 xv = xs[i * plane_stride + ch];
-    const _Float16 *h0 = reinterpret_cast<const _Float16 *>(&w[2 * i]);
-    const _Float16 *h1 = reinterpret_cast<const _Float16 *>(&w[2 * i + 1]);
-    s += float(h0[0]) * xv.x;
-    s += float(h0[1]) * xv.y;
-    s += float(h1[0]) * xv.z;
-    s += float(h1[1]) * xv.w;
-  }
-  return s;
+  if (!norm_w) return 1.0f;
+  const float tot = red[0] + red[1] + red[2] + red[3];
+  return 1.0f / sqrtf(tot / float(K) + eps);
 }
 
 // Elements per lane load for each kind (x staging chunk size).
 template <uint32_t KIND>
 constexpr int chunk_elems() { return KIND == LG_F16 ? 8 : 16; }
 
-// Scale of chunk ch of row n (Q8_0: per 32-element block, Q6_K: per 16).
+// Scale of chunk ch of row n (Q8_0: per 32-element block, Q6_K: per 16), as stored: the load is
+// kept apart from its f16 -> f32 conversion so that no load waits on an earlier one.
 template <uint32_t KIND>
-__device__ __forceinline__ float chunk_scale(const DevMatrix &W, int64_t n, int ch) {
-  if constexpr (KIND == LG_Q8_0)  // hardware f16 -> f32: exact for every finite scale and infinity
-    return float(static_cast<const _Float16 *>(W.s)[n * (W.cols / 32) + ch / 2]);
-  else if constexpr (KIND == LG_Q6_K) return static_cast<const float *>(W.s)[n * (W.cols / 16) + ch];
-  else return 1.0f;
+__device__ __forceinline__ uint32_t chunk_scale_bits(const DevMatrix &W, int64_t n, int ch) {
+  if constexpr (KIND == LG_Q8_0)
+    return static_cast<const uint16_t *>(W.s)[n * (W.cols / 32) + ch / 2];
+  else if constexpr (KIND == LG_Q6_K) return static_cast<const uint32_t *>(W.s)[n * (W.cols / 16) + ch];
+  else return 0u;
 }
 
-// Each wave owns R outputs (RPO weight rows each: 2 for SwiGLU's gate|up).  All weight loads of
-// a chunk group are issued before the input vector is staged, so the x/RMSNorm prologue
-// overlaps the HBM reads.  Chunk c of a lane covers chunk index g*64*CPL + c*64 + lane.
-template <uint32_t KIND, int EPI, int R, int CPL>
+template <uint32_t KIND>
+__device__ __forceinline__ float scale_value(uint32_t bits) {
+  if constexpr (KIND == LG_Q8_0)  // hardware f16 -> f32: exact for every finite scale and infinity
+    return float(__builtin_bit_cast(_Float16, uint16_t(bits)));
+  else return __builtin_bit_cast(float, bits);
+}
+
+// x (and the RMSNorm weight) for up to XQ float4 per thread, loaded before the weight stream so
+// that the LDS stage waits only for these (vector loads return in issue order).
+template <int XQ>
+__device__ __forceinline__ void load_x_regs(const float *__restrict__ x, const float *__restrict__ norm_w, int nq,
+                                            float4 (&v)[XQ], float4 (&w)[XQ]) {
+  // clamped indices instead of predicated loads: no branch separates a load from its use, and
+  // entries past nq are never stored (store_x_regs)
+  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+#pragma unroll
+  for (int j = 0; j < XQ; ++j) v[j] = x4[min(j * kThreads + int(threadIdx.x), nq - 1)];
+  if (norm_w) {
+    const float4 *w4 = reinterpret_cast<const float4 *>(norm_w);
+#pragma unroll
+    for (int j = 0; j < XQ; ++j) w[j] = w4[min(j * kThreads + int(threadIdx.x), nq - 1)];
+  }
+}
+
+// Store the registers of load_x_regs into the LDS planes layout of stage_x and return the
+// RMSNorm factor (1 without a norm).  Ends with a workgroup barrier.
+template <int E, int XQ>
+__device__ float store_x_regs(const float4 (&v)[XQ], const float4 (&w)[XQ], bool norm, int K, float eps,
+                              float4 *xs, float *red) {
+  const int t = threadIdx.x, nq = K / 4, nchunk = K / E;
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < XQ; ++j) {
+    const int q = j * kThreads + t;
+    if (q >= nq) continue;
+    float4 u = v[j];
+    if (norm) {
+      ss += u.x * u.x + u.y * u.y + u.z * u.z + u.w * u.w;
+      u.x *= w[j].x;
+      u.y *= w[j].y;
+      u.z *= w[j].z;
+      u.w *= w[j].w;
+    }
+    xs[(q % (E / 4)) * nchunk + q / (E / 4)] = u;
+  }
+  if (norm) {
+    ss = wave_sum(ss);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+  }
+  __syncthreads();
+  if (!norm) return 1.0f;
+  return 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / float(K) + eps);
+}
+
+// Each wave owns R outputs (RPO weight rows each: 2 for SwiGLU's gate|up).  Issue order: the
+// input vector x (L2-resident, small), then every weight load of the chunk group, chunk-major so
+// the dot products below consume loads in the order they return; the x stage into LDS waits
+// only for x.  Chunk c of a lane covers chunk index g*64*CPL + c*64 + lane.
+template <uint32_t KIND, int EPI, int R, int CPL, bool BIGK>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(const float *__restrict__ x, DevMatrix W,
                                                         float *__restrict__ y,
                                                         const float *__restrict__ bias,
@@ -115,7 +151,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const float *__restrict_
   constexpr int RPO = EPI == int(Epi::SWIGLU) ? 2 : 1;
   constexpr int NR = R * RPO;
   typedef uint32_t wvec __attribute__((ext_vector_type(4 * NR * CPL)));
-  typedef float svec __attribute__((ext_vector_type(NR * CPL)));
+  typedef uint32_t svec __attribute__((ext_vector_type(NR * CPL)));
   typedef float avec __attribute__((ext_vector_type(NR)));
   const int K = W.cols, nchunk = K / E;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -123,32 +159,37 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const float *__restrict_
   const int f = W.rows / 2;
   const uint4 *q = static_cast<const uint4 *>(W.q);
   const int64_t row_chunks = int64_t(K) * (KIND == LG_F16 ? 2 : 1) / 16;  // uint4 per weight row
+  // without BIGK one chunk group covers K (K <= 64*CPL*E <= 1024*CPL), so x fits in XQ = CPL
+  // prologue registers per thread; BIGK stages x into LDS after the first group's weight loads
+  constexpr int XQ = BIGK ? 1 : CPL;
+  float4 xr[XQ], nr[XQ];
+  if constexpr (!BIGK) load_x_regs(x, norm_w, K / 4, xr, nr);
   wvec w;
   svec sc;
   avec acc;
 #pragma unroll
   for (int r = 0; r < NR; ++r) acc[r] = 0.0f;
   const int ngroups = (nchunk + 64 * CPL - 1) / (64 * CPL);
+  float inv = 1.0f;
   for (int g = 0; g < ngroups; ++g) {
 #pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      const int o = min(o0 + r / RPO, outputs - 1);  // clamped rows are never stored
-      const int64_t n = (r % RPO) ? f + o : o;
+    for (int c = 0; c < CPL; ++c) {
+      const int ch = g * 64 * CPL + c * 64 + lane;
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        const int ch = g * 64 * CPL + c * 64 + lane;
-        const int i = r * CPL + c;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        float s = 0.0f;
-        if (ch < nchunk) {
-          v = q[n * row_chunks + ch];
-          s = chunk_scale<KIND>(W, n, ch);
-        }
+      for (int r = 0; r < NR; ++r) {
+        const int o = min(o0 + r / RPO, outputs - 1);  // clamped rows are never stored
+        const int64_t n = (r % RPO) ? f + o : o;
+        const int i = c * NR + r;
+        const int chc = min(ch, nchunk - 1);  // lanes past the row load a valid chunk and skip it below
+        const uint4 v = q[n * row_chunks + chc];
         w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
-        sc[i] = s;
+        sc[i] = chunk_scale_bits<KIND>(W, n, chc);
       }
     }
-    if (g == 0) stage_x<E>(x, K, norm_w, eps, xs, red);  // every wave reaches this barrier
+    if (g == 0) {  // every wave reaches this barrier
+      if constexpr (BIGK) inv = stage_x<E>(x, K, norm_w, eps, xs, red);
+      else inv = store_x_regs<E, XQ>(xr, nr, norm_w != nullptr, K, eps, xs, red);
+    }
     // each x chunk is read from LDS once and used for all NR rows of the wave
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
@@ -159,26 +200,30 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const float *__restrict_
         for (int p = 0; p < E / 4; ++p) xv[p] = xs[p * nchunk + ch];
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
-          const int i = r * CPL + c;
+          const int i = c * NR + r;
           const uint32_t wd[4] = {w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
-          float d = 0.0f;
+          float d0 = 0.0f, d1 = 0.0f;  // two FMA chains
           if constexpr (KIND == LG_F16) {
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
               const _Float16 *h0 = reinterpret_cast<const _Float16 *>(&wd[2 * p]);
               const _Float16 *h1 = reinterpret_cast<const _Float16 *>(&wd[2 * p + 1]);
-              d += float(h0[0]) * xv[p].x + float(h0[1]) * xv[p].y + float(h1[0]) * xv[p].z +
-                   float(h1[1]) * xv[p].w;
+              d0 = fmaf(float(h0[0]), xv[p].x, d0);
+              d1 = fmaf(float(h0[1]), xv[p].y, d1);
+              d0 = fmaf(float(h1[0]), xv[p].z, d0);
+              d1 = fmaf(float(h1[1]), xv[p].w, d1);
             }
-            acc[r] += d;
+            acc[r] += d0 + d1;
           } else {
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
               const uint32_t word = wd[p];
-              d += float(int8_t(word)) * xv[p].x + float(int8_t(word >> 8)) * xv[p].y +
-                   float(int8_t(word >> 16)) * xv[p].z + float(int8_t(word >> 24)) * xv[p].w;
+              d0 = fmaf(float(int8_t(word)), xv[p].x, d0);
+              d1 = fmaf(float(int8_t(word >> 8)), xv[p].y, d1);
+              d0 = fmaf(float(int8_t(word >> 16)), xv[p].z, d0);
+              d1 = fmaf(float(int8_t(word >> 24)), xv[p].w, d1);
             }
-            acc[r] += sc[i] * d;
+            acc[r] = fmaf(scale_value<KIND>(sc[i]), d0 + d1, acc[r]);
           }
         }
       }
@@ -188,11 +233,11 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const float *__restrict_
   for (int r = 0; r < R; ++r) {
     const int o = o0 + r;
     if (EPI == int(Epi::SWIGLU)) {
-      const float gsum = wave_sum(acc[r * 2]);
-      const float usum = wave_sum(acc[r * 2 + 1]);
+      const float gsum = wave_sum(acc[r * 2]) * inv;
+      const float usum = wave_sum(acc[r * 2 + 1]) * inv;
       if (lane == 0 && o < outputs) y[o] = silu(gsum) * usum;
     } else {
-      const float v = wave_sum(acc[r]);
+      const float v = wave_sum(acc[r]) * inv;
       if (lane == 0 && o < outputs) {
         if (EPI == int(Epi::ADD)) y[o] += v;
         else y[o] = v + (bias ? bias[o] : 0.0f);
@@ -224,7 +269,7 @@ __global__ __launch_bounds__(kThreads) void gemv_generic_kernel(const float *__r
                                                                 float eps, int outputs) {
   extern __shared__ float4 xs[];
   __shared__ float red[4];
-  stage_x<4>(x, W.cols, norm_w, eps, xs, red);  // E = 4: plain order
+  const float inv = stage_x<4>(x, W.cols, norm_w, eps, xs, red);  // E = 4: plain order
   const float *xf = reinterpret_cast<const float *>(xs);
   const int lane = threadIdx.x & 63;
   const int o = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
@@ -232,7 +277,7 @@ __global__ __launch_bounds__(kThreads) void gemv_generic_kernel(const float *__r
   auto rowdot = [&](int n) {
     float s = 0.0f;
     for (int k = lane; k < W.cols; k += 64) s += weight_at_gemv(W, n, k) * xf[k];
-    return wave_sum(s);
+    return wave_sum(s) * inv;
   };
   if (EPI == int(Epi::SWIGLU)) {
     const float g = rowdot(o), u = rowdot(W.rows / 2 + o);
@@ -252,7 +297,13 @@ void launch_rc(const float *x, const DevMatrix &W, float *y, const float *bias, 
   const int per_block = (kThreads / 64) * R;
   const dim3 grid((outputs + per_block - 1) / per_block), block(kThreads);
   const size_t lds = size_t(W.cols) * sizeof(float);
-  hipLaunchKernelGGL((gemv_kernel<KIND, EPI, R, CPL>), grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
+  const bool bigk = W.cols / chunk_elems<KIND>() > 64 * CPL;
+  if (bigk)
+    hipLaunchKernelGGL((gemv_kernel<KIND, EPI, R, CPL, true>), grid, block, lds, st, x, W, y, bias, norm_w, eps,
+                       outputs);
+  else
+    hipLaunchKernelGGL((gemv_kernel<KIND, EPI, R, CPL, false>), grid, block, lds, st, x, W, y, bias, norm_w, eps,
+                       outputs);
 }
 
 template <uint32_t KIND, int EPI, int R>
