@@ -29,6 +29,39 @@ DevBuf::~DevBuf() {
   if (p) (void)hipFree(p);
 }
 
+KernelTimer *&kernel_timer() {
+  thread_local KernelTimer *t = nullptr;
+  return t;
+}
+
+hipEvent_t Profiler::take() {
+  if (pool_.empty()) {
+    hipEvent_t e;
+    HIP_CHECK(hipEventCreate(&e));
+    pool_.push_back(e);
+  }
+  hipEvent_t e = pool_.back();
+  pool_.pop_back();
+  return e;
+}
+
+void Profiler::begin_kernel(const char *cls) {
+  if (!on_) return;
+  cur_ = cls;
+  cur_a_ = take();
+  cur_b_ = take();
+  timer_.start = cur_a_;
+  timer_.stop = cur_b_;
+  kernel_timer() = &timer_;
+}
+
+void Profiler::end_kernel(double bytes, double flops) {
+  if (!on_) return;
+  kernel_timer() = nullptr;
+  open_.push_back({cur_, cur_a_, cur_b_, bytes, flops});
+  if (open_.size() > 4096) drain();
+}
+
 void Profiler::begin(const char *cls, hipStream_t st) {
   if (!on_) return;
   cur_ = cls;
@@ -405,17 +438,17 @@ void *Engine::vpool(int layer) const {
 // ------------------------------------------------------------------ kernels with profiling
 void Engine::gemm(const _Float16 *A, const _Float16 *A_lo, int M, const DevMatrix &W, Epi epi, float *C,
                   _Float16 *C16, _Float16 *C16_lo, int ldc, const float *bias) {
-  prof.begin("gemm", stream);
+  prof.begin_kernel("gemm");
   launch_gemm(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, stream);
-  prof.end(double(W.bytes()) + double(M) * W.cols * 2, 2.0 * M * double(W.rows) * W.cols, stream);
+  prof.end_kernel(double(W.bytes()) + double(M) * W.cols * 2, 2.0 * M * double(W.rows) * W.cols);
 }
 
 void Engine::gemv(const float *x, const DevMatrix &W, Epi epi, float *y, const float *bias,
                   const float *norm_w) {
-  prof.begin("gemv", stream);
+  prof.begin_kernel("gemv");
   launch_gemv(x, W, epi, y, bias, norm_w, eps, stream);
   // algorithmic bytes: the GGUF-encoded weight bytes of the matrix
-  prof.end(double(W.gguf_bytes()), 2.0 * double(W.rows) * W.cols, stream);
+  prof.end_kernel(double(W.gguf_bytes()), 2.0 * double(W.rows) * W.cols);
 }
 
 // ------------------------------------------------------------------ matmul drop-in

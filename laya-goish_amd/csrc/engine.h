@@ -49,6 +49,9 @@ class Profiler {
   bool on() const { return on_; }
   void begin(const char *cls, hipStream_t st);
   void end(double bytes, double flops, hipStream_t st);
+  // one timed kernel (GEMV, GEMM): events recorded at the kernel's own start and end
+  void begin_kernel(const char *cls);
+  void end_kernel(double bytes, double flops);
   void read(const std::string &cls, int64_t *launches, double *ms, double *bytes, double *flops);
   void reset();
   ~Profiler();
@@ -61,8 +64,10 @@ class Profiler {
   std::vector<Rec> open_;
   std::vector<hipEvent_t> pool_;
   std::map<std::string, Sum> sums_;
+  hipEvent_t take();
   std::string cur_;
-  hipEvent_t cur_a_ = nullptr;
+  hipEvent_t cur_a_ = nullptr, cur_b_ = nullptr;
+  KernelTimer timer_;
 };
 
 struct BatchPlan;

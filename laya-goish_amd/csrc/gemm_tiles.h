@@ -538,8 +538,15 @@ bool launch_cfg(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &
   // buffer offsets of A are 32-bit: launch row blocks of at most 2 GiB of activations each
   const int64_t rows_cap = ((1ll << 31) - 1) / (int64_t(K) * 2) / CF::kBM * CF::kBM;
   LG_REQUIRE(rows_cap > 0, "gemm: K=%d too large", K);
+  // an installed kernel timer spans the launches of all row blocks: start on the first, stop on the last
+  KernelTimer *timer = kernel_timer();
+  const KernelTimer whole = timer ? *timer : KernelTimer{};
   for (int m0 = 0; m0 < M;) {
     const int Mc = int(std::min<int64_t>(M - m0, rows_cap));
+    if (timer) {
+      timer->start = m0 == 0 ? whole.start : nullptr;
+      timer->stop = m0 + Mc >= M ? whole.stop : nullptr;
+    }
     const int MT = (Mc + CF::kBM - 1) / CF::kBM;
     LG_REQUIRE(int64_t(MT) * NT < (1ll << 31), "gemm: grid too large");
     const dim3 grid(MT * NT), block(256);
@@ -555,8 +562,8 @@ bool launch_cfg(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &
                                     hipFuncAttributeMaxDynamicSharedMemorySize, CF::kLdsBytes));                \
       attr = true;                                                                                             \
     }                                                                                                          \
-    hipLaunchKernelGGL(fn, grid, block, CF::kLdsBytes, st, Ac, Alc, Mc, K, W, Cc, C16c, C16lc, ldc, bias, MT, NT, \
-                       ffn);                                                                                   \
+    launch_timed(fn, grid, block, CF::kLdsBytes, st, Ac, Alc, Mc, K, W, Cc, C16c, C16lc, ldc, bias, MT, NT,    \
+                 ffn);                                                                                         \
   } while (0)
     switch (epi) {
       case Epi::F32: LAUNCH(0); break;
@@ -566,6 +573,7 @@ bool launch_cfg(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &
     }
     m0 += Mc;
   }
+  if (timer) *timer = whole;
 #undef LAUNCH
   return true;
 }

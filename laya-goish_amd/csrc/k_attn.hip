@@ -272,6 +272,9 @@ __global__ __launch_bounds__(256, 1) void attn_prefill_grp_kernel(
   const KV *vbase = static_cast<const KV *>(vpool) + int64_t(kh) * HD * P;
 
   uint4 kreg[NLD], vreg[NLD];
+  // page-table entry of the page after the one in flight: loaded one iteration ahead, so the
+  // K/V prefetch never waits on a page-table round trip
+  int32_t next_page = ptab[min(1, npages - 1)];
   {
     const int64_t page = ptab[0];
     const uint4 *ks = reinterpret_cast<const uint4 *>(kbase + page * g.page_stride);
@@ -317,7 +320,8 @@ __global__ __launch_bounds__(256, 1) void attn_prefill_grp_kernel(
     }
     __syncthreads();
     if (kt + 1 < npages) {
-      const int64_t page = ptab[kt + 1];
+      const int64_t page = next_page;
+      next_page = ptab[min(kt + 2, npages - 1)];
       const uint4 *ks = reinterpret_cast<const uint4 *>(kbase + page * g.page_stride);
       const uint4 *vs = reinterpret_cast<const uint4 *>(vbase + page * g.page_stride);
 #pragma unroll
@@ -439,7 +443,6 @@ __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, 
                                                  KV *__restrict__ kpool, KV *__restrict__ vpool,
                                                  const int32_t *__restrict__ pages, float *pbase,
                                                  int64_t hstride);
-
 template <int HD, int GRP, typename KV>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const float *__restrict__ qkv, int hq, KvGeom g,
                                                           const float *__restrict__ cosT,
@@ -454,23 +457,19 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float *__restric
   attn_decode_page<HD, GRP, KV>(qkv, hq, g, cosT, sinT, pos, kpool, vpool, pages, pbase, hstride);
 }
 
-// Combine the per-page partials of one (sequence, query head).  Cross-workgroup hand-off
-// through memory would need an agent-scope release (an L2 write-back on this part) in every
-// page workgroup, so the combine is its own small launch.  Thread (d, half) owns output dim d
-// over the pages half, half + 2, ...; each batch of 2*CB pages is loaded in one round trip
-// together with the page maxima and sums (indices clamped, surplus pages weighted 0).
+// Combine the per-page partials (max, sum, out[HD]) of one query head: pb points at its page 0,
+// np pages.  A separate launch: handing the partials over to a last-arriving page workgroup
+// would need an agent-scope release (an L2 write-back on this part) in every page workgroup,
+// which measured slower than the launch.  Thread (d, half) owns output dim d over the pages half, half + 2, ...; each batch
+// of 2*CB pages is loaded in one round trip together with the page maxima and sums (indices
+// clamped, surplus pages weighted 0).  All 256 threads of the workgroup take part.
 template <int HD>
-__global__ __launch_bounds__(256) void attn_decode_combine(const float *__restrict__ part, int hq,
-                                                           int max_pages,
-                                                           const int32_t *__restrict__ ctx_len, int ctx_all,
-                                                           float *__restrict__ out) {
+__device__ __forceinline__ void combine_head(const float *__restrict__ pb, int np, float *__restrict__ outh) {
   static_assert(HD == 128, "two threads per output dim");
   constexpr int CB = 32;  // pages per thread per batch
-  const int h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
-  const int np = ((ctx_len ? ctx_len[s] : ctx_all) + P - 1) / P;
+  const int t = threadIdx.x;
   __shared__ float wm[1024], wl[1024];
   __shared__ float red[4], sacc[2][HD], sl[2];
-  const float *pb = part + ((int64_t(s) * hq + h) * max_pages) * (2 + HD);
   const int d = t & (HD - 1), half = t >> 7;
   // page maxima and sums (np <= 1024: four per thread), then the first batch of outputs
   float m4[4], l4[4];
@@ -518,7 +517,19 @@ __global__ __launch_bounds__(256) void attn_decode_combine(const float *__restri
   sacc[half][d] = acc;
   if (d == 0) sl[half] = L;
   __syncthreads();
-  if (t < HD) out[(int64_t(s) * hq + h) * HD + t] = (sacc[0][t] + sacc[1][t]) / (sl[0] + sl[1]);
+  if (t < HD) outh[t] = (sacc[0][t] + sacc[1][t]) / (sl[0] + sl[1]);
+  __syncthreads();  // the shared arrays are reused by the caller's next head
+}
+
+// Combine as its own launch: one workgroup per (query head, sequence).
+template <int HD>
+__global__ __launch_bounds__(256) void attn_decode_combine(const float *__restrict__ part, int hq,
+                                                           int max_pages,
+                                                           const int32_t *__restrict__ ctx_len, int ctx_all,
+                                                           float *__restrict__ out) {
+  const int h = blockIdx.x, s = blockIdx.y;
+  const int np = ((ctx_len ? ctx_len[s] : ctx_all) + P - 1) / P;
+  combine_head<HD>(part + ((int64_t(s) * hq + h) * max_pages) * (2 + HD), np, out + (int64_t(s) * hq + h) * HD);
 }
 
 // One page of one kv head: scores, page softmax and P.V for each query head.

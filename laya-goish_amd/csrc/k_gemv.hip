@@ -299,11 +299,9 @@ void launch_rc(const float *x, const DevMatrix &W, float *y, const float *bias, 
   const size_t lds = size_t(W.cols) * sizeof(float);
   const bool bigk = W.cols / chunk_elems<KIND>() > 64 * CPL;
   if (bigk)
-    hipLaunchKernelGGL((gemv_kernel<KIND, EPI, R, CPL, true>), grid, block, lds, st, x, W, y, bias, norm_w, eps,
-                       outputs);
+    launch_timed(gemv_kernel<KIND, EPI, R, CPL, true>, grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
   else
-    hipLaunchKernelGGL((gemv_kernel<KIND, EPI, R, CPL, false>), grid, block, lds, st, x, W, y, bias, norm_w, eps,
-                       outputs);
+    launch_timed(gemv_kernel<KIND, EPI, R, CPL, false>, grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
 }
 
 template <uint32_t KIND, int EPI, int R>
@@ -360,13 +358,13 @@ void launch_gemv(const float *x, const DevMatrix &W, Epi epi, float *y, const fl
       const size_t lds = size_t(W.cols) * sizeof(float);
       switch (epi) {
         case Epi::F32:
-          hipLaunchKernelGGL(gemv_generic_kernel<0>, grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
+          launch_timed(gemv_generic_kernel<0>, grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
           break;
         case Epi::ADD:
-          hipLaunchKernelGGL(gemv_generic_kernel<1>, grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
+          launch_timed(gemv_generic_kernel<1>, grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
           break;
         case Epi::SWIGLU:
-          hipLaunchKernelGGL(gemv_generic_kernel<3>, grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
+          launch_timed(gemv_generic_kernel<3>, grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
           break;
         default: fail(LG_ERR_UNSUPPORTED, "gemv: f16 epilogue not supported");
       }

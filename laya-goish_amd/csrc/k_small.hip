@@ -118,10 +118,11 @@ __device__ __forceinline__ void kv_put(void *pool, int64_t i, float v) {
 // Decode form: one token whose position and KV page the host already knows (kernel arguments,
 // so the only memory round trip is the q|k|v row and the table rows).  q goes out in f32.
 // Prefill form: one workgroup per attention tile (<= 32 consecutive tokens of one sequence).
-// q and k are rotated token by token (rows are contiguous); v is staged through LDS per kv
-// head so that its transposed page layout is written as runs of consecutive slots instead of
-// one 4-byte store per cache line.
-template <bool KV32>
+// q and k rotations are flat (token, head, pair) items dealt to the threads in rounds whose
+// loads are all issued before any is used; v is staged through LDS a few kv heads at a time
+// so that its transposed page layout is written as runs of consecutive slots instead of one
+// 4-byte store per cache line.
+template <bool KV32, int HD>
 __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
     const float *__restrict__ qkv, int hq, KvGeom g, const float *__restrict__ cosT,
     const float *__restrict__ sinT, const int32_t *__restrict__ pages, int max_pages,
@@ -129,54 +130,89 @@ __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
     const int32_t *__restrict__ tile_pos0, const int32_t *__restrict__ tile_n,
     _Float16 *__restrict__ q16, _Float16 *__restrict__ q16lo, void *__restrict__ kpool,
     void *__restrict__ vpool) {
-  constexpr int TT = 32, HDMAX = 128;
-  __shared__ float vs[TT][HDMAX + 1];
+  constexpr int TT = 32, HALF = HD / 2, HB = 2;  // tokens per tile, pair offset, V heads per LDS round
+  constexpr int QB = 8;                         // tokens whose loads one round issues together
+  constexpr int TPR = kT / HD, VT = TT / TPR;   // V: token lanes per dim, tokens per thread
+  static_assert(kT % HALF == 0 && kT % HD == 0, "thread blocks must tile the head");
+  __shared__ float vs[HB][TT][HD + 1];
   const int tile = blockIdx.x, tid = threadIdx.x;
   const int row0 = tile_row0[tile], pos0 = tile_pos0[tile], n = tile_n[tile];
   const int32_t *ptab = pages + int64_t(tile_seq[tile]) * max_pages;
-  const int hd = g.hd, half = hd / 2;
-  const int qw = hq * hd, kvw = g.hkv * hd, rw = qw + 2 * kvw;
-  for (int tk = 0; tk < n; ++tk) {
-    const float *row = qkv + int64_t(row0 + tk) * rw;
-    const int pos = pos0 + tk;
-    const float *cs = cosT + int64_t(pos) * hd, *sn = sinT + int64_t(pos) * hd;
-    for (int i = tid; i < hq * half; i += kT) {
-      const int h = i / half, j = i % half;
-      const float u = row[h * hd + j], v = row[h * hd + j + half];
-      const float a = u * cs[j] - v * sn[j], b = v * cs[j + half] + u * sn[j + half];
-      const int64_t at = int64_t(row0 + tk) * qw + h * hd + j;
-      const _Float16 ah = _Float16(a), bh = _Float16(b);
-      q16[at] = ah;
-      q16[at + half] = bh;
-      if (q16lo) {
-        q16lo[at] = _Float16(a - float(ah));
-        q16lo[at + half] = _Float16(b - float(bh));
+  // a tile of <= 32 tokens spans at most two pages (page_tokens >= 32): look both up once
+  const int pg0 = pos0 / g.page_tokens;
+  const int64_t page_lo = ptab[pg0], page_hi = ptab[(pos0 + n - 1) / g.page_tokens];
+  auto page_base = [&](int pos) { return (pos / g.page_tokens == pg0 ? page_lo : page_hi) * g.page_stride; };
+  const int qw = hq * HD, kvw = g.hkv * HD, rw = qw + 2 * kvw;
+  // rotations: thread -> pairs p = tid + 256 m of the q|k heads (pair j = p % HALF is the same
+  // for every m), QB tokens per round with every load issued before any value is used
+  const int npairs = (hq + g.hkv) * HALF;
+  const int j = tid % HALF;
+  for (int p0 = 0; p0 < npairs; p0 += kT) {
+    const int p = p0 + tid;
+    const int hh = min(p, npairs - 1) / HALF;
+    for (int t0 = 0; t0 < n; t0 += QB) {
+      float u[QB], v[QB], c0[QB], c1[QB], s0[QB], s1[QB];
+#pragma unroll
+      for (int b = 0; b < QB; ++b) {
+        const int tk = min(t0 + b, n - 1);
+        const float *row = qkv + int64_t(row0 + tk) * rw + hh * HD;
+        const int64_t cb = int64_t(pos0 + tk) * HD;
+        u[b] = row[j];
+        v[b] = row[j + HALF];
+        c0[b] = cosT[cb + j];
+        c1[b] = cosT[cb + j + HALF];
+        s0[b] = sinT[cb + j];
+        s1[b] = sinT[cb + j + HALF];
+      }
+      if (p >= npairs) continue;
+#pragma unroll
+      for (int b = 0; b < QB; ++b) {
+        const int tk = t0 + b;
+        if (tk >= n) continue;
+        const float a = u[b] * c0[b] - v[b] * s0[b], c = v[b] * c1[b] + u[b] * s1[b];
+        if (hh < hq) {
+          const int64_t at = int64_t(row0 + tk) * qw + hh * HD + j;
+          const _Float16 ah = _Float16(a), ch = _Float16(c);
+          q16[at] = ah;
+          q16[at + HALF] = ch;
+          if (q16lo) {
+            q16lo[at] = _Float16(a - float(ah));
+            q16lo[at + HALF] = _Float16(c - float(ch));
+          }
+        } else {
+          const int pos = pos0 + tk;
+          const int64_t at = page_base(pos) + (int64_t(hh - hq) * g.page_tokens + pos % g.page_tokens) * HD;
+          kv_put<KV32>(kpool, at + j, a);
+          kv_put<KV32>(kpool, at + j + HALF, c);
+        }
       }
     }
-    const int64_t kb = int64_t(ptab[pos / g.page_tokens]) * g.page_stride;
-    const int slot = pos % g.page_tokens;
-    for (int i = tid; i < g.hkv * half; i += kT) {
-      const int h = i / half, j = i % half;
-      const float u = row[qw + h * hd + j], v = row[qw + h * hd + j + half];
-      const int64_t at = kb + (int64_t(h) * g.page_tokens + slot) * hd;
-      kv_put<KV32>(kpool, at + j, u * cs[j] - v * sn[j]);
-      kv_put<KV32>(kpool, at + j + half, v * cs[j + half] + u * sn[j + half]);
-    }
   }
-  for (int h = 0; h < g.hkv; ++h) {
-    for (int i = tid; i < n * hd; i += kT) {
-      const int tk = i / hd, dd = i % hd;
-      vs[tk][dd] = qkv[int64_t(row0 + tk) * rw + qw + kvw + h * hd + dd];
-    }
+  // v: HB kv heads per round staged through LDS (thread -> dim tid % HD, tokens tid / HD + TPR i),
+  // then written as runs of consecutive slots
+  const int dd = tid % HD, tq = tid / HD;
+  for (int h0 = 0; h0 < g.hkv; h0 += HB) {
+    const int nh = min(HB, g.hkv - h0);
+    float val[HB][VT];
+#pragma unroll
+    for (int hh = 0; hh < HB; ++hh)
+#pragma unroll
+      for (int i = 0; i < VT; ++i) {
+        const int tk = min(tq + TPR * i, n - 1), h = min(h0 + hh, g.hkv - 1);
+        val[hh][i] = qkv[int64_t(row0 + tk) * rw + qw + kvw + h * HD + dd];
+      }
+#pragma unroll
+    for (int hh = 0; hh < HB; ++hh)
+#pragma unroll
+      for (int i = 0; i < VT; ++i) vs[hh][tq + TPR * i][dd] = val[hh][i];
     __syncthreads();
-    // thread -> (dim, token) with the token fastest: 32 consecutive slots per dim row
-    for (int i = tid; i < TT * hd; i += kT) {
-      const int tk = i % TT, dd = i / TT;
+    // thread -> (head, dim, token) with the token fastest: 32 consecutive slots per dim row
+    for (int i = tid; i < nh * TT * HD; i += kT) {
+      const int hh = i / (TT * HD), r = i % (TT * HD), tk = r % TT, d2 = r / TT;
       if (tk < n) {
         const int pos = pos0 + tk;
-        kv_put<KV32>(vpool, int64_t(ptab[pos / g.page_tokens]) * g.page_stride +
-                                   (int64_t(h) * hd + dd) * g.page_tokens + pos % g.page_tokens,
-                        vs[tk][dd]);
+        kv_put<KV32>(vpool, page_base(pos) + (int64_t(h0 + hh) * HD + d2) * g.page_tokens + pos % g.page_tokens,
+                     vs[hh][tk][d2]);
       }
     }
     __syncthreads();
@@ -370,13 +406,19 @@ void launch_rope_kv_tiles(const float *qkv, int hq, const KvGeom &g, const float
                           const int32_t *tile_seq, const int32_t *tile_row0, const int32_t *tile_pos0,
                           const int32_t *tile_n, int ntiles, _Float16 *q16, _Float16 *q16_lo,
                           void *kpool, void *vpool, hipStream_t st) {
-  LG_REQUIRE(ntiles > 0 && g.hd % 2 == 0 && g.hd <= 128 && q16, "rope_kv: bad arguments");
-  if (g.kv32)
-    hipLaunchKernelGGL(rope_kv_tile_kernel<true>, dim3(ntiles), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, pages,
-                       max_pages, tile_seq, tile_row0, tile_pos0, tile_n, q16, q16_lo, kpool, vpool);
-  else
-    hipLaunchKernelGGL(rope_kv_tile_kernel<false>, dim3(ntiles), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, pages,
-                       max_pages, tile_seq, tile_row0, tile_pos0, tile_n, q16, q16_lo, kpool, vpool);
+  LG_REQUIRE(ntiles > 0 && q16, "rope_kv: bad arguments");
+  LG_REQUIRE(g.page_tokens >= 32, "rope_kv: a 32-token tile must span at most two pages");
+#define LAUNCH(K32, HDV)                                                                                  \
+  hipLaunchKernelGGL((rope_kv_tile_kernel<K32, HDV>), dim3(ntiles), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, \
+                     pages, max_pages, tile_seq, tile_row0, tile_pos0, tile_n, q16, q16_lo, kpool, vpool)
+  if (g.hd == 128) {
+    if (g.kv32) LAUNCH(true, 128); else LAUNCH(false, 128);
+  } else if (g.hd == 64) {
+    if (g.kv32) LAUNCH(true, 64); else LAUNCH(false, 64);
+  } else {
+    fail(LG_ERR_UNSUPPORTED, "rope_kv: head_dim %d not supported (64, 128)", g.hd);
+  }
+#undef LAUNCH
   HIP_CHECK(hipGetLastError());
 }
 

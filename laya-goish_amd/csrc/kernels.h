@@ -4,9 +4,28 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <hip/hip_ext.h>
+
 #include <cstdint>
 
 namespace lg {
+
+// Kernel timing: while a KernelTimer is installed on the calling thread, the GEMV and GEMM
+// launchers start their (single) kernel with hipExtLaunchKernelGGL, which records `start` and
+// `stop` when that kernel itself starts and ends, so the interval excludes dispatch gaps.
+struct KernelTimer {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+KernelTimer *&kernel_timer();
+
+// hipLaunchKernelGGL, or its timed form when a KernelTimer is installed.
+template <typename F, typename... Args>
+inline void launch_timed(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, Args... args) {
+  if (KernelTimer *t = kernel_timer())
+    hipExtLaunchKernelGGL(kernel, grid, block, uint32_t(lds), st, t->start, t->stop, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
+}
 
 // Repacked device layout of one weight matrix W[rows][cols] (y = x . W^T).
 //   F32 : q = float[rows][cols]
