@@ -209,7 +209,10 @@ struct BLoad {
 __device__ __forceinline__ void tile_coords(int bid, int nblk, int MT, int NT, int &mt, int &nt) {
   int t = bid;
   if ((nblk & 7) == 0) t = (bid & 7) * (nblk >> 3) + (bid >> 3);
-  constexpr int GM = 4;  // from a sweep of 1..32 at the 35,840-token shapes (within 3%)
+#ifndef LG_GEMM_GROUP_M
+#define LG_GEMM_GROUP_M 4
+#endif
+  constexpr int GM = LG_GEMM_GROUP_M;  // from a sweep of 1..32 at the 35,840-token shapes (within 3%)
   const int group = t / (GM * NT);
   const int first = group * GM;
   const int gm = min(MT - first, GM);
