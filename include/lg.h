@@ -169,8 +169,9 @@ typedef struct lg_batch lg_batch;
 int lg_batch_create(lg_engine *e, const lg_request *reqs, int nreq, lg_batch **out);
 void lg_batch_free(lg_engine *e, lg_batch *b);
 /* Run a staged batch: prefill every request, then option scoring at every answer position
- * over the head rows `option_ids` (k of them) with temperature `temperature`.
- * Outputs (host, [sum npos][k], NULL to skip): raw logits, probabilities, log-probabilities.
+ * over the head rows `option_ids` (k of them, 1..256) with temperature `temperature`.
+ * Outputs (host, [sum npos][k], NULL to skip): raw logits, probabilities, log-probabilities
+ * (the last two need k <= 32).
  * Probabilities follow src/models/openthai/decision.rs:268-279,297-303; log-probabilities
  * are the option log-softmax of logit/temperature. */
 int lg_batch_run(lg_engine *e, lg_batch *b, const int32_t *option_ids, int k, float temperature,
@@ -198,6 +199,67 @@ int lg_option_scores(const float *logits, int k, float temperature, float *probs
 #define LG_CONF_F32 0
 #define LG_CONF_F64 1
 int lg_option_confidence(const float *probs, int k, int mode, float *confidence);
+
+/* ---- request-level decide over token ids ----
+ * The reference's decision layer (src/models/openthai/decision.rs) at the token level: the
+ * tokenizer is not on this path, so every text piece arrives as token ids and the control
+ * tokens (state/question/kind/option/answer markers) come from the model's laya.decide.*
+ * metadata, or by default from the top of the vocabulary: option slot s (s < 255) and the
+ * abstain slot 255 are ids V-256+s, then V-257 state, V-258 question, V-259..V-261 the
+ * choice/score/noul kind markers, V-262 answer, V-263 newline, V-264 colon. */
+#define LG_Q_CHOICE 0
+#define LG_Q_SCORE 1
+#define LG_Q_NOUL 2
+
+typedef struct {
+  int32_t kind;                       /* LG_Q_CHOICE (1..255 options), LG_Q_SCORE (2..10 levels),
+                                         LG_Q_NOUL (2 options: no, yes) */
+  const int32_t *instruction;         /* instruction tokens */
+  int32_t n_instruction;
+  int32_t n_options;
+  const int32_t *const *names;        /* [n_options] option name tokens (score levels may be empty) */
+  const int32_t *name_len;
+  const int32_t *const *descs;        /* [n_options] description tokens; NULL / 0 length = none */
+  const int32_t *desc_len;            /* NULL = no descriptions */
+} lg_question;
+
+typedef struct {
+  const int32_t *state;               /* state tokens (truncated to the state budget, first kept) */
+  int32_t n_state;
+  const lg_question *questions;       /* 1..256 */
+  int32_t n_questions;
+  int32_t permutations;               /* 0 = default rule; else 1..32 passes */
+  int32_t order_invariant;            /* -1 unset, 0 false, 1 true */
+} lg_decide_request;
+
+typedef struct {
+  float *probs;                       /* [sum of n_options], question order (caller-owned) */
+  float *abstain;                     /* [n_questions]: abstain slot mass (choice; else 0) */
+  float *confidence;                  /* [n_questions]: 1 - H(p)/ln k */
+  float *score;                       /* [n_questions]: sum_j j p_j (score questions; else 0) */
+  int32_t *choice;                    /* [n_questions]: first most probable option */
+  int32_t input_tokens;               /* tokens of the first pass's prompt */
+  int32_t permutations;               /* passes run */
+  int32_t truncated;                  /* 1 when the state was cut to its budget */
+} lg_decide_result;
+
+/* Decide: encode every option-order pass, prefill all passes as one GPU batch, score the
+ * 256 slot rows at each answer position and aggregate.  Replaces Backend::decide / decide,
+ * src/models/mod.rs:16-22 and src/models/openthai/decision.rs:243-390 (text encoding aside). */
+int lg_decide(lg_engine *e, const lg_decide_request *req, lg_decide_result *out, lg_cancel_fn cancel,
+              void *cancel_arg);
+/* The token layout of pass `pass` of a request for the model in `g` (host only, no GPU):
+ * ids[cap] (n written), positions[n_questions], order[n_questions][255] (option index shown at
+ * each slot), truncated, and the number of passes.  Replaces encode / permutations,
+ * src/models/openthai/decision.rs:140-233. */
+int lg_decide_encode(const lg_gguf *g, const lg_decide_request *req, int pass, int32_t *ids, int cap,
+                     int *n, int32_t *positions, int32_t *order, int *truncated, int *passes);
+
+/* The aggregation of lg_decide over slot logits the caller already holds ([passes][n_questions]
+ * [256], the 256 slot rows at each answer position of each pass), host only.  Replaces the
+ * scoring of src/models/openthai/decision.rs:268-279,297-336. */
+int lg_decide_scores(const lg_gguf *g, const lg_decide_request *req, const float *slot_logits,
+                     lg_decide_result *out);
 
 /* ---- profiling: per-kernel-class HIP event timing on the engine's stream ---- */
 /* When on, every launch of the timed kernel classes is bracketed by HIP events. */

@@ -10,6 +10,7 @@
 #include <string>
 
 #include "common.h"
+#include "decide.h"
 #include "engine.h"
 #include "gguf.h"
 #include "kernels.h"
@@ -299,7 +300,7 @@ int lg_forward(lg_engine *e, int seq, const int32_t *ids, int n, const int32_t *
   return guard([&] {
     NEED(e, "engine");
     if (npos > 0) NEED(logits, "logits");
-    if (vocab_ids) LG_REQUIRE(nv > 0 && nv <= 32, "nv must be 1..32 when vocab_ids is given");
+    if (vocab_ids) LG_REQUIRE(nv > 0 && nv <= 256, "nv must be 1..256 when vocab_ids is given");
     e->e->forward(seq, ids, n, positions, npos, vocab_ids, nv, logits, cancel, cancel_arg);
   });
 }
@@ -341,6 +342,89 @@ int lg_decode(lg_engine *e, int seq, int32_t first, int steps, int32_t *tokens, 
   return guard([&] {
     NEED(e, "engine");
     e->e->decode(seq, first, steps, tokens, logits);
+  });
+}
+
+int lg_decide(lg_engine *e, const lg_decide_request *req, lg_decide_result *out, lg_cancel_fn cancel,
+              void *cancel_arg) {
+  return guard([&] {
+    NEED(e, "engine");
+    NEED(req, "request");
+    NEED(out, "result");
+    NEED(out->probs, "result probabilities");
+    lg::Engine &E = *e->e;
+    const lg::DecideSpec &s = E.decide;
+    lg::decide_validate(s, *req);
+    const int n = lg::decide_passes(*req);
+    // every pass is encoded (and so validated) before any inference, as
+    // src/models/openthai/decision.rs:234-241
+    std::vector<lg::Encoded> enc;
+    for (int p = 0; p < n; ++p) enc.push_back(lg::decide_encode(s, *req, n, p));
+    for (const lg::Encoded &x : enc)
+      LG_REQUIRE(int64_t(x.ids.size()) <= E.ctx, "prompt of %zu tokens exceeds the model context %d", x.ids.size(), E.ctx);
+    // all passes as one batch of sequences; the sequences are released whatever happens
+    struct Seqs {
+      lg::Engine &E;
+      std::vector<int> ids;
+      lg::BatchPlan *b = nullptr;
+      ~Seqs() {
+        try {
+          if (b) E.batch_free(b);
+          for (int q : ids) E.seq_free(q);
+        } catch (...) {
+        }
+      }
+    } held{E, {}};
+    std::vector<lg_request> reqs(n);
+    for (int p = 0; p < n; ++p) {
+      held.ids.push_back(E.seq_create());
+      reqs[p] = {held.ids.back(), enc[p].ids.data(), int(enc[p].ids.size()), enc[p].positions.data(),
+                 req->n_questions};
+    }
+    held.b = E.batch_create(reqs.data(), n);
+    std::vector<float> logits(size_t(n) * req->n_questions * 256);
+    E.batch_run(held.b, s.slot, 256, 1.0f, logits.data(), nullptr, nullptr, cancel, cancel_arg);
+    lg::decide_aggregate(s, *req, n, enc, logits.data(), *out);
+  });
+}
+
+int lg_decide_encode(const lg_gguf *g, const lg_decide_request *req, int pass, int32_t *ids, int cap, int *n,
+                     int32_t *positions, int32_t *order, int *truncated, int *passes) {
+  return guard([&] {
+    NEED(g, "gguf");
+    NEED(req, "request");
+    const lg::DecideSpec s = lg::decide_spec(*g->g);
+    lg::decide_validate(s, *req);
+    const int np = lg::decide_passes(*req);
+    LG_REQUIRE(pass >= 0 && pass < np, "pass %d outside 0..%d", pass, np - 1);
+    const lg::Encoded e = lg::decide_encode(s, *req, np, pass);
+    if (passes) *passes = np;
+    if (n) *n = int(e.ids.size());
+    if (truncated) *truncated = e.truncated ? 1 : 0;
+    if (ids) {
+      LG_REQUIRE(size_t(cap) >= e.ids.size(), "ids capacity %d < %zu tokens", cap, e.ids.size());
+      std::copy(e.ids.begin(), e.ids.end(), ids);
+    }
+    if (positions) std::copy(e.positions.begin(), e.positions.end(), positions);
+    if (order)
+      for (int q = 0; q < req->n_questions; ++q)
+        for (size_t j = 0; j < e.order[q].size(); ++j) order[q * 255 + j] = e.order[q][j];
+  });
+}
+
+int lg_decide_scores(const lg_gguf *g, const lg_decide_request *req, const float *slot_logits, lg_decide_result *out) {
+  return guard([&] {
+    NEED(g, "gguf");
+    NEED(req, "request");
+    NEED(slot_logits, "slot logits");
+    NEED(out, "result");
+    NEED(out->probs, "result probabilities");
+    const lg::DecideSpec s = lg::decide_spec(*g->g);
+    lg::decide_validate(s, *req);
+    const int n = lg::decide_passes(*req);
+    std::vector<lg::Encoded> enc;
+    for (int p = 0; p < n; ++p) enc.push_back(lg::decide_encode(s, *req, n, p));
+    lg::decide_aggregate(s, *req, n, enc, slot_logits, *out);
   });
 }
 

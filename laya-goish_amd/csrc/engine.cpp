@@ -194,6 +194,7 @@ Engine::Engine(const Gguf &g, const lg_engine_opts &opts) {
   V = int(g.num("laya.decoder.vocab_size", 0));
   ctx = int(g.num("laya.decoder.context_length", 0));
   eps = float(g.num("laya.decoder.layer_norm_rms_epsilon", 1e-5));
+  decide = decide_spec(g);
   if (L < 1 || d < 1 || hq < 1 || hkv < 1 || hq % hkv || hd < 2 || hd % 2 || f < 1 || V < 1 || ctx < 1)
     fail(LG_ERR_FORMAT, "invalid laya-decoder dimensions");
   if (d % 64 || (hd != 64 && hd != 128))
@@ -710,7 +711,8 @@ void Engine::batch_run(BatchPlan *b, const int32_t *option_ids, int k, float tem
                        float *logits, float *probs, float *logprobs, lg_cancel_fn cancel, void *arg) {
   LG_REQUIRE(b, "batch: null");
   LG_REQUIRE(!b->ran, "batch: already run (stage a new batch)");
-  LG_REQUIRE(k > 0 && k <= 32 && option_ids, "batch: need 1..32 option ids");
+  LG_REQUIRE(k > 0 && k <= 256 && option_ids, "batch: need 1..256 head rows");
+  LG_REQUIRE(k <= 32 || (!probs && !logprobs), "batch: option scores need 1..32 option ids");
   LG_REQUIRE(temperature > 0 && std::isfinite(temperature), "batch: temperature must be positive");
   for (int j = 0; j < k; ++j)
     if (option_ids[j] < 0 || option_ids[j] >= V) fail(LG_ERR_INVALID, "option id %d outside the vocabulary", option_ids[j]);
@@ -724,13 +726,13 @@ void Engine::batch_run(BatchPlan *b, const int32_t *option_ids, int k, float tem
     sync();
     return;
   }
-  ws_out_.ensure(size_t(R) * k * 12 + 256 + 64 * 4);
+  ws_out_.ensure(size_t(R) * k * 12 + size_t(k) * 4 + 256);  // logits, probs, logprobs, then the k ids
   float *dl = ws_out_.as<float>(), *dp = dl + size_t(R) * k, *dlp = dp + size_t(R) * k;
   int32_t *dids = reinterpret_cast<int32_t *>(dlp + size_t(R) * k);
   HIP_CHECK(hipMemcpyAsync(dids, option_ids, size_t(k) * 4, hipMemcpyHostToDevice, stream));
   prof.begin("head", stream);
   launch_head_rows(ws_x_.as<float>(), b->gather, R, d, final_norm_, eps, head_, dids, k, dl, stream);
-  launch_option_scores(dl, R, k, temperature, dp, dlp, stream);
+  if (k <= 32) launch_option_scores(dl, R, k, temperature, dp, dlp, stream);
   prof.end(0, 0, stream);
   if (logits) HIP_CHECK(hipMemcpyAsync(logits, dl, size_t(R) * k * 4, hipMemcpyDeviceToHost, stream));
   if (probs) HIP_CHECK(hipMemcpyAsync(probs, dp, size_t(R) * k * 4, hipMemcpyDeviceToHost, stream));

@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "gguf.h"
+#include "decide.h"
 #include "kernels.h"
 #include "lg.h"
 
@@ -128,6 +129,7 @@ class Engine {
   float eps = 1e-5f;
   uint32_t emb_kind = 0;
   int precision = LG_PREC_EXACT;
+  DecideSpec decide;  // control tokens and budgets of the request-level decide layout
   bool split() const { return precision == LG_PREC_EXACT; }
   int kv_elem() const { return split() ? 4 : 2; }
 

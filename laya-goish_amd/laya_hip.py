@@ -56,6 +56,129 @@ class Request(ctypes.Structure):
                 ("positions", ctypes.POINTER(ctypes.c_int32)), ("npos", ctypes.c_int)]
 
 
+Q_KINDS = {"choice": 0, "score": 1, "noul": 2}
+_I32P = ctypes.POINTER(ctypes.c_int32)
+
+
+class Question(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int32), ("instruction", _I32P), ("n_instruction", ctypes.c_int32),
+                ("n_options", ctypes.c_int32), ("names", ctypes.POINTER(_I32P)), ("name_len", _I32P),
+                ("descs", ctypes.POINTER(_I32P)), ("desc_len", _I32P)]
+
+
+class DecideRequest(ctypes.Structure):
+    _fields_ = [("state", _I32P), ("n_state", ctypes.c_int32), ("questions", ctypes.POINTER(Question)),
+                ("n_questions", ctypes.c_int32), ("permutations", ctypes.c_int32),
+                ("order_invariant", ctypes.c_int32)]
+
+
+class DecideResult(ctypes.Structure):
+    _fields_ = [("probs", ctypes.POINTER(ctypes.c_float)), ("abstain", ctypes.POINTER(ctypes.c_float)),
+                ("confidence", ctypes.POINTER(ctypes.c_float)), ("score", ctypes.POINTER(ctypes.c_float)),
+                ("choice", _I32P), ("input_tokens", ctypes.c_int32), ("permutations", ctypes.c_int32),
+                ("truncated", ctypes.c_int32)]
+
+
+class DecideArgs:
+    """ctypes form of a token-level decide request:
+    {"state": [ids], "questions": [{"type": "choice"|"score"|"noul", "instruction": [ids],
+      "options": [{"name": [ids], "desc": [ids] | None}, ...]}, ...],
+     "permutations": int | None, "order_invariant": bool | None}
+    (the token-level counterpart of the /v1/decide body, src/models/openthai/decision.rs:20-107).
+    Keeps every array alive for the duration of the call."""
+
+    def __init__(self, req: dict):
+        self.keep = []
+        qs = req.get("questions") or []
+        self.kinds = []
+        self.nopts = []
+        qarr = (Question * max(1, len(qs)))()
+        for i, q in enumerate(qs):
+            if q.get("type") not in Q_KINDS:
+                raise LayaError(1, f"question {i}: invalid question type")
+            opts = q.get("options") or []
+            ins = self._arr(q.get("instruction") or [])
+            names = [self._arr(o.get("name") or []) for o in opts]
+            descs = [self._arr(o.get("desc") or []) for o in opts]
+            name_ptrs = (_I32P * max(1, len(opts)))(*[ctypes.cast(a.ctypes.data, _I32P) for a in names])
+            desc_ptrs = (_I32P * max(1, len(opts)))(*[ctypes.cast(a.ctypes.data, _I32P) for a in descs])
+            name_len = self._arr([len(a) for a in names])
+            desc_len = self._arr([len(a) for a in descs])
+            self.keep += [name_ptrs, desc_ptrs]
+            qarr[i] = Question(Q_KINDS[q["type"]], ctypes.cast(ins.ctypes.data, _I32P), len(ins), len(opts),
+                               name_ptrs, ctypes.cast(name_len.ctypes.data, _I32P), desc_ptrs,
+                               ctypes.cast(desc_len.ctypes.data, _I32P))
+            self.kinds.append(q["type"])
+            self.nopts.append(len(opts))
+        self.keep.append(qarr)
+        state = self._arr(req.get("state") or [])
+        oi = req.get("order_invariant")
+        self.req = DecideRequest(ctypes.cast(state.ctypes.data, _I32P), len(state), qarr, len(qs),
+                                 int(req.get("permutations") or 0), -1 if oi is None else int(bool(oi)))
+
+    def _arr(self, v):
+        a = np.ascontiguousarray(np.asarray(v, dtype=np.int32).reshape(-1))
+        if a.size == 0:
+            a = np.zeros(1, np.int32)[:0]
+        self.keep.append(a)
+        return a
+
+    def result(self):
+        nq = len(self.nopts)
+        self.out = {"probs": np.zeros(max(1, sum(self.nopts)), np.float32), "abstain": np.zeros(max(1, nq), np.float32),
+                    "confidence": np.zeros(max(1, nq), np.float32), "score": np.zeros(max(1, nq), np.float32),
+                    "choice": np.zeros(max(1, nq), np.int32)}
+        o = self.out
+        fp = lambda a: ctypes.cast(a.ctypes.data, ctypes.POINTER(ctypes.c_float))  # noqa: E731
+        self.res = DecideResult(fp(o["probs"]), fp(o["abstain"]), fp(o["confidence"]), fp(o["score"]),
+                                ctypes.cast(o["choice"].ctypes.data, _I32P), 0, 0, 0)
+        return self.res
+
+    def answers(self):
+        o, out, at = self.out, [], 0
+        for i, (kind, k) in enumerate(zip(self.kinds, self.nopts)):
+            p = o["probs"][at:at + k].copy()
+            at += k
+            a = {"type": kind, "probabilities": p, "confidence": float(o["confidence"][i]),
+                 "choice": int(o["choice"][i])}
+            if kind == "choice":
+                a["abstain"] = float(o["abstain"][i])
+            if kind == "score":
+                a["score"] = float(o["score"][i])
+            if kind == "noul":
+                a["noul"] = float(p[1])
+            out.append(a)
+        r = self.res
+        return {"answers": out, "usage": {"input_tokens": int(r.input_tokens), "output_tokens": 0,
+                                          "permutations": int(r.permutations),
+                                          "truncated_state": bool(r.truncated)}}
+
+
+def decide_encode(gguf: "Gguf", req: dict, pass_: int = 0):
+    """Token layout of one pass: (ids, answer positions, option order per question, truncated,
+    passes).  Host only."""
+    a = DecideArgs(req)
+    n, trunc, passes = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    check(lib().lg_decide_encode(gguf.h, ctypes.byref(a.req), pass_, None, 0, ctypes.byref(n), None, None,
+                                 ctypes.byref(trunc), ctypes.byref(passes)))
+    ids = np.zeros(n.value, np.int32)
+    pos = np.zeros(max(1, len(a.nopts)), np.int32)
+    order = np.full((max(1, len(a.nopts)), 255), -1, np.int32)
+    check(lib().lg_decide_encode(gguf.h, ctypes.byref(a.req), pass_, _ptr(ids), n.value, ctypes.byref(n),
+                                 _ptr(pos), _ptr(order), ctypes.byref(trunc), ctypes.byref(passes)))
+    orders = [order[i, :k].tolist() for i, k in enumerate(a.nopts)]
+    return ids, pos[:len(a.nopts)], orders, bool(trunc.value), passes.value
+
+
+def decide_scores(gguf: "Gguf", req: dict, slot_logits) -> dict:
+    """Aggregation of decide over caller-held slot logits [passes][questions][256]."""
+    a = DecideArgs(req)
+    sl = _c(slot_logits, np.float32)
+    res = a.result()
+    check(lib().lg_decide_scores(gguf.h, ctypes.byref(a.req), _ptr(sl), ctypes.byref(res)))
+    return a.answers()
+
+
 CANCEL_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p)
 
 _lib = None
@@ -104,6 +227,10 @@ def lib() -> ctypes.CDLL:
             "lg_batch_rewind": (I, [P, P]),
             "lg_decode": (I, [P, I, ctypes.c_int32, I, P, P]),
             "lg_option_scores": (I, [P, I, F, P, P]),
+            "lg_decide": (I, [P, ctypes.POINTER(DecideRequest), ctypes.POINTER(DecideResult), CANCEL_FN, P]),
+            "lg_decide_encode": (I, [P, ctypes.POINTER(DecideRequest), I, P, I, ctypes.POINTER(I), P, P,
+                                     ctypes.POINTER(I), ctypes.POINTER(I)]),
+            "lg_decide_scores": (I, [P, ctypes.POINTER(DecideRequest), P, ctypes.POINTER(DecideResult)]),
             "lg_option_confidence": (I, [P, I, I, ctypes.POINTER(F)]),
             "lg_profile_enable": (I, [P, I]),
             "lg_profile_read": (I, [P, ctypes.c_char_p, ctypes.POINTER(I64), ctypes.POINTER(ctypes.c_double),
@@ -370,6 +497,15 @@ class Engine:
         h = ctypes.c_void_p()
         check(lib().lg_batch_create(self.h, arr, len(requests), ctypes.byref(h)))
         return Batch(self, h, (arr, keep), total)
+
+    def decide(self, req: dict, cancel=None) -> dict:
+        """Request-level decide over token ids (Backend::decide, src/models/openthai/decision.rs:243-390):
+        every option-order pass prefilled as one GPU batch, slot scoring and aggregation."""
+        a = DecideArgs(req)
+        res = a.result()
+        cb = CANCEL_FN(cancel) if cancel else CANCEL_FN(0)
+        check(lib().lg_decide(self.h, ctypes.byref(a.req), ctypes.byref(res), cb, None))
+        return a.answers()
 
     def decode(self, seq: int, first: int, steps: int, want_logits: bool = False):
         toks = np.empty(steps, dtype=np.int32)

@@ -1,0 +1,157 @@
+"""Token-level restatement of the reference decision layer -- TEST INFRASTRUCTURE ONLY.
+
+Only tests load this module, and only as the checker of lg_decide / lg_decide_encode /
+lg_decide_scores.  It restates src/models/openthai/decision.rs over token ids:
+  passes        decision.rs:140-162
+  orders        decision.rs:125-139 (written as round-half-to-even of j*k/n, an independent form)
+  encode        decision.rs:169-233 (question blocks, state budget keeping its first token)
+  aggregate     decision.rs:268-279 (slot softmax with abstain, pass average) and :297-336
+                (normalisation, entropy confidence, first-max choice, expected score)
+Arithmetic is f32 in the reference's order; softmax and the confidence go through the C oracle
+(tensor::softmax, src/tensor.rs:132-140, over glibc expf/logf).
+"""
+from __future__ import annotations
+
+from fractions import Fraction
+
+import numpy as np
+
+import pyoracle as po
+
+KINDS = {"choice": 0, "score": 1, "noul": 2}
+
+
+def spec(gguf: po.Gguf) -> dict:
+    """Control tokens and budgets: laya.decide.* metadata, else the layout at the top of the
+    vocabulary (slot s = V-256+s, state V-257, question V-258, kinds V-259..V-261, answer V-262,
+    newline V-263, colon V-264)."""
+    V = int(gguf.num("laya.decoder.vocab_size"))
+    ctx = int(gguf.num("laya.decoder.context_length"))
+    base = int(gguf.num("laya.decide.slot_base", V - 256))
+    temps = [float(np.float32(gguf.num(f"laya.decide.temperature_{k}", 1.0))) for k in ("choice", "score", "noul")]
+    return {
+        "V": V,
+        "slot": [base + i for i in range(256)],
+        "state": int(gguf.num("laya.decide.state_id", V - 257)),
+        "question": int(gguf.num("laya.decide.question_id", V - 258)),
+        "kind": [int(gguf.num("laya.decide.choice_id", V - 259)), int(gguf.num("laya.decide.score_id", V - 260)),
+                 int(gguf.num("laya.decide.noul_id", V - 261))],
+        "answer": int(gguf.num("laya.decide.answer_id", V - 262)),
+        "newline": int(gguf.num("laya.decide.newline_id", V - 263)),
+        "colon": int(gguf.num("laya.decide.colon_id", V - 264)),
+        "temperature": temps,
+        "max_tokens": int(gguf.num("laya.decide.context_length", ctx)),
+        "max_state": int(gguf.num("laya.decide.state_length", min(2048, ctx))),
+    }
+
+
+def passes(req: dict) -> int:
+    ks = [len(q["options"]) for q in req["questions"] if q["type"] == "choice"]
+    k = max(ks) if ks else 1
+    if req.get("permutations"):
+        n = int(req["permutations"])
+    elif req.get("order_invariant") is False:
+        n = 1
+    elif req.get("order_invariant") is True:
+        n = 8
+    else:
+        n = 8 if k >= 11 else 1
+    return max(min(n, k), 1)
+
+
+def orders(k: int, n: int) -> list[list[int]]:
+    n = max(min(n, k), 1)
+    offsets = sorted({round(Fraction(j * k, n)) % k for j in range(n)})  # Python rounds half to even
+    return [[(i + off) % k for i in range(k)] for off in offsets]
+
+
+def encode(s: dict, req: dict, n: int, pass_: int):
+    blocks, order = [], []
+    for q in req["questions"]:
+        k = len(q["options"])
+        if q["type"] == "choice":
+            allo = orders(k, n)
+            ord_ = allo[pass_ % len(allo)]
+        else:
+            ord_ = list(range(k))
+        b = [s["question"], s["kind"][KINDS[q["type"]]]] + list(q.get("instruction") or []) + [s["newline"]]
+        for slot, i in enumerate(ord_):
+            o = q["options"][i]
+            b += [s["slot"][slot]] + list(o.get("name") or [])
+            if o.get("desc"):
+                b += [s["colon"]] + list(o["desc"])
+            b += [s["newline"]]
+        b += [s["answer"], s["newline"]]
+        blocks.append(b)
+        order.append(ord_)
+    total = sum(len(b) for b in blocks)
+    if total >= s["max_tokens"]:
+        raise ValueError("question tokens exceed the context budget")
+    ids = [s["state"]] + list(req.get("state") or []) + [s["newline"]]
+    budget = min(s["max_state"], s["max_tokens"] - total)
+    truncated = len(ids) > budget
+    if truncated:
+        ids = ids[:1] + ids[len(ids) - (budget - 1):] if budget > 1 else ids[:1]
+    positions = []
+    for b in blocks:
+        p = max(i for i, t in enumerate(b) if t == s["answer"])
+        positions.append(len(ids) + p)
+        ids += b
+    return np.array(ids, np.int32), np.array(positions, np.int32), order, truncated
+
+
+def aggregate(s: dict, req: dict, n: int, encs, slot_logits) -> dict:
+    f = np.float32
+    qs = req["questions"]
+    sl = np.asarray(slot_logits, np.float32).reshape(n, len(qs), 256)
+    probs = [[f(0)] * len(q["options"]) for q in qs]
+    abstain = [f(0)] * len(qs)
+    for p in range(n):
+        for i, q in enumerate(qs):
+            k = len(q["options"])
+            T = f(s["temperature"][KINDS[q["type"]]])
+            v = [sl[p, i, j] / T for j in range(k)] + [sl[p, i, 255] / T]
+            pr = po.softmax(np.array(v, np.float32))
+            tot = f(0)
+            for j in range(k):
+                tot = f(tot + pr[j])
+            tot = max(tot, f(1e-12))
+            for slot in range(k):
+                idx = encs[p][2][i][slot]
+                probs[i][idx] = f(probs[i][idx] + f(f(pr[slot] / tot) / f(n)))
+            abstain[i] = f(abstain[i] + f(pr[k] / f(n)))
+    out = []
+    for i, q in enumerate(qs):
+        pv = probs[i]
+        tot = f(0)
+        for x in pv:
+            tot = f(tot + x)
+        tot = max(tot, f(1e-12))
+        pv = np.array([f(x / tot) for x in pv], np.float32)
+        conf = f(po.confidence(pv))
+        best = 0
+        for j in range(1, len(pv)):
+            if pv[j] > pv[best]:
+                best = j
+        score = f(0)
+        for j, x in enumerate(pv):
+            score = f(score + f(f(j) * x))
+        a = {"type": q["type"], "probabilities": pv, "confidence": float(conf), "choice": best}
+        if q["type"] == "choice":
+            a["abstain"] = float(abstain[i])
+        if q["type"] == "score":
+            a["score"] = float(score)
+        if q["type"] == "noul":
+            a["noul"] = float(pv[1])
+        out.append(a)
+    return {"answers": out, "input_tokens": len(encs[0][0]), "permutations": n,
+            "truncated_state": any(e[3] for e in encs)}
+
+
+def decide(model: po.Model, gguf: po.Gguf, req: dict) -> dict:
+    """The whole decision on the CPU oracle: every pass's forward, then the aggregation."""
+    s = spec(gguf)
+    n = passes(req)
+    encs = [encode(s, req, n, p) for p in range(n)]
+    logits = np.stack([model.forward(e[0], e[1], s["slot"]) for e in encs])
+    return aggregate(s, req, n, encs, logits), logits

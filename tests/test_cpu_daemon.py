@@ -1,0 +1,82 @@
+"""JSON-lines daemon protocol (src/main.rs:139-151): one JSON line out per non-empty line in, an
+{"error": ...} line for a bad request and the loop goes on; answer shapes of
+src/models/openthai/decision.rs:297-389.  The engine here computes its slot logits from a seeded
+generator and scores them with the library's own host aggregation (lg_decide_scores), so the
+whole daemon path except the GPU forward runs."""
+import io
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import pydecide as pd
+
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "laya-goish_amd"))
+import daemon  # noqa: E402
+
+
+class HostScoredEngine:
+    def __init__(self, lh, gguf, seed=0):
+        self.lh, self.g, self.rng = lh, gguf, np.random.default_rng(seed)
+
+    def decide(self, treq):
+        n = pd.passes(treq)
+        logits = self.rng.normal(size=(n, len(treq["questions"]), 256)).astype(np.float32)
+        return self.lh.decide_scores(self.g, treq, logits)
+
+
+@pytest.fixture(scope="module")
+def gguf(lh):
+    return lh.Gguf.from_bytes(lh.SynthImage("tiny-q8", seed=3))
+
+
+REQ = {"id": "r1", "state": [5, 6, 7, 8],
+       "questions": {"topic": {"type": "choice", "instructions": [9, 10],
+                               "criteria": {"billing": {"name": [11], "desc": [12, 13]}, "refund": {"name": [14]},
+                                            "other": {"name": [22, 23], "desc": None}}},
+                     "urgency": {"type": "score", "instructions": [15], "criteria": [[16], [17], [18, 19]]},
+                     "human": {"type": "noul", "instructions": [20], "criteria": {"true": [21]}}},
+       "permutations": 3}
+
+
+def run(lines, eng):
+    out = io.StringIO()
+    daemon.serve(eng, "laya-decoder test", io.StringIO("".join(l + "\n" for l in lines)), out)
+    return [json.loads(l) for l in out.getvalue().splitlines()]
+
+
+def test_daemon_answers_and_recovers(lh, gguf):
+    eng = HostScoredEngine(lh, gguf)
+    noname = {"questions": {"q": {"type": "choice", "criteria": {"a": [3]}}}}  # a choice option needs name ids
+    outs = run([json.dumps(REQ), "", "{not json", json.dumps({"questions": {}}),
+                json.dumps({"questions": {"q": {"type": "rank"}}}), json.dumps(noname), json.dumps(REQ)], eng)
+    assert len(outs) == 6
+    assert all("error" in o for o in outs[1:5])
+    assert "questions must contain 1..256 named questions" in outs[2]["error"]
+    assert "invalid question type" in outs[3]["error"]
+    assert "option name is empty" in outs[4]["error"]
+    for o in (outs[0], outs[5]):
+        assert o["id"] == "r1" and o["model"] == "laya-decoder test"
+        topic, urg, human = o["answers"]["topic"], o["answers"]["urgency"], o["answers"]["human"]
+        assert set(topic["probabilities"]) == {"billing", "refund", "other"}
+        assert abs(sum(topic["probabilities"].values()) - 1) < 1e-5
+        assert topic["choice"] == max(topic["probabilities"], key=topic["probabilities"].get)
+        assert 0 <= topic["abstain"] <= 1 and 0 <= topic["confidence"] <= 1
+        assert set(urg["probabilities"]) == {"0", "1", "2"} and urg["legend"] == {"0": [16], "1": [17], "2": [18, 19]}
+        assert abs(urg["score"] - sum(int(k) * v for k, v in urg["probabilities"].items())) < 1e-5
+        assert set(human) == {"type", "noul"} and 0 <= human["noul"] <= 1
+        assert o["usage"]["permutations"] == 3 and o["usage"]["output_tokens"] == 0
+
+
+def test_daemon_request_validation():
+    bad = [({"questions": {"q": {"type": "choice", "criteria": [1]}}}, "choice requires 1..255 options"),
+           ({"questions": {"q": {"type": "score", "criteria": {"a": 1}}}}, "score requires 2..10 levels"),
+           ({"questions": {"q": {"type": "noul", "criteria": {"maybe": None}}}}, "noul criteria keys must be false/true"),
+           ({"questions": {"q": {"type": "noul"}}, "permutations": 0}, "permutations must be 1..32"),
+           ({"questions": {"q": {"type": "noul"}}, "order_invariant": "yes"}, "order_invariant must be boolean"),
+           ({"questions": {"q": {"type": "noul"}}, "state": "text"}, "state must be a list of token ids")]
+    for req, msg in bad:
+        with pytest.raises(daemon.RequestError, match=msg):
+            daemon.to_tokens_request(req)
