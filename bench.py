@@ -250,6 +250,65 @@ def bench_long_context(args, prec):
                      note="value counts every request's 8192 tokens; computed_tok_per_s counts tokens prefilled")
 
 
+def decide_request(vocab, seed):
+    """One token-level /v1/decide body: a 480-token state, a 6-option choice question, a 5-level
+    score and a yes/no question, 6 option-order passes."""
+    rng = np.random.default_rng(seed)
+
+    def toks(n):
+        return rng.integers(0, vocab - 300, n).tolist()
+    return {"state": toks(480),
+            "questions": [{"type": "choice", "instruction": toks(12),
+                           "options": [{"name": toks(2), "desc": toks(6)} for _ in range(6)]},
+                          {"type": "score", "instruction": toks(10), "options": [{"name": [], "desc": toks(4)}
+                                                                                 for _ in range(5)]},
+                          {"type": "noul", "instruction": toks(8), "options": [{"name": toks(1)}, {"name": toks(1)}]}],
+            "permutations": 6}
+
+
+def bench_decide_request(args, prec):
+    """Request-level decide (lg_decide) on the Q8_0 d2048 model: every option-order pass of one
+    request encoded and prefilled as one GPU batch, the 256 slot rows scored at each answer
+    position, passes averaged.  Requests run one after another, as the reference serves them."""
+    img = lh.SynthImage(PRESET, seed=SEED)
+    g = lh.Gguf.from_bytes(img)
+    eng = lh.Engine(g, kv_tokens=16384, max_batch_tokens=8192, precision=prec)
+    req = decide_request(eng.info["vocab"], SEED + 5)
+    out = None
+    for _ in range(max(args.warmup, 1)):
+        out = eng.decide(req)
+    eng.sync()
+    steps = max(args.steps, 10)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = eng.decide(req)
+    dt = (time.perf_counter() - t0) / steps
+    eng.close()
+    toks = out["usage"]["input_tokens"] * out["usage"]["permutations"]
+    log(f"decide request: {dt * 1e3:.2f} ms per request ({out['usage']['permutations']} passes, {toks} tokens)")
+    line = base_line("decide requests/s (Q8_0 d2048, one request of 6 option-order passes)", round(1 / dt, 2),
+                     "req/s", True, steps, max(args.warmup, 1), dt * 1e3, prec,
+                     "24 layers, d_model 2048, 16 x 128, FFN 5632, vocab 32000, Q8_0; request: 480-token state, "
+                     "choice (6 options), score (5 levels), noul; 6 passes prefilled as one batch",
+                     tokens_per_request=toks, prefill_tok_per_s=round(toks / dt, 1))
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import pydecide
+        import pyoracle as po
+        layers = 2
+        small = lh.SynthImage(PRESET, seed=SEED, n_layers=layers)
+        og = po.Gguf(small.array())
+        om = po.Model(og, threads=args.cpu_threads)
+        t0 = time.perf_counter()
+        pydecide.decide(om, og, req)
+        cdt = (time.perf_counter() - t0) * 24 / layers
+        line["cpu_baseline"] = {"value": round(1 / cdt, 5), "unit": "req/s", "cores": args.cpu_threads, "kind": "port",
+                                "sample": f"the same request through {layers} of 24 layers (passes run one after "
+                                          f"another, as the reference does), time scaled x{24 // layers}: "
+                                          f"{cdt:.1f} s per request"}
+    return line
+
+
 def cpu_baseline(threads, layers=24):
     """The oracle on a bounded sample: one 560-token request of the workload through `layers`
     of the 24 layers (per-layer cost is identical), scaled to the full model."""
@@ -283,7 +342,8 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--precision", choices=["exact", "fast"], default="exact")
-    ap.add_argument("--workload", choices=["decide", "plumbing", "q4k-prefill", "long-context"], default="decide",
+    ap.add_argument("--workload", choices=["decide", "plumbing", "q4k-prefill", "long-context", "decide-request"],
+                    default="decide",
                     help="decide (default): the Q8_0 d2048 batched decide headline plus batch-1 decode; the "
                          "others measure the remaining workload shapes, one JSON line each")
     ap.add_argument("--no-decode", action="store_true")
@@ -303,7 +363,8 @@ def main():
         sys.exit(2)
     prec = lh.PREC_EXACT if args.precision == "exact" else lh.PREC_FAST
     if args.workload != "decide":
-        fn = {"plumbing": bench_plumbing, "q4k-prefill": bench_q4k, "long-context": bench_long_context}
+        fn = {"plumbing": bench_plumbing, "q4k-prefill": bench_q4k, "long-context": bench_long_context,
+              "decide-request": bench_decide_request}
         print(json.dumps(fn[args.workload](args, prec)), flush=True)
         return
     if args.copy_calibration > 0:
