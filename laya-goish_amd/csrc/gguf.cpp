@@ -120,7 +120,10 @@ struct Cursor {
         uint32_t et = get<uint32_t>();
         uint64_t count = get<uint64_t>();
         if (count > 1000000) fail(LG_ERR_FORMAT, "GGUF array too large");
-        for (uint64_t i = 0; i < count; ++i) value(et, depth + 1);
+        for (uint64_t i = 0; i < count; ++i) {
+          MetaValue e = value(et, depth + 1);
+          if (et == 8) v.strs.push_back(std::move(e.str));  // kept: token lists name control tokens
+        }
         v.count = count;
       } break;
       case 10: v.num = double(get<uint64_t>()); break;

@@ -19,6 +19,7 @@ struct MetaValue {
   double num = 0;     // numeric kinds and bool
   std::string str;    // kind 8
   uint64_t count = 0; // kind 9: element count
+  std::vector<std::string> strs;  // kind 9 over strings: the elements
 };
 
 struct TensorInfo {

@@ -69,7 +69,7 @@ uint16_t float_to_half(float f) {
   return uint16_t(sign | h);
 }
 
-enum class Fill { Normal, Ones, NearOne, Q8, Q4K, Q6K, Cos, Sin };
+enum class Fill { Normal, Ones, NearOne, Q8, Q4K, Q6K, Cos, Sin, LogUniform };
 
 struct Spec {
   std::string name;
@@ -136,6 +136,13 @@ struct Writer {
   void kv_u64(const std::string &k, uint64_t v) { str(k); put<uint32_t>(10); put<uint64_t>(v); }
   void kv_f32(const std::string &k, float v) { str(k); put<uint32_t>(6); put<float>(v); }
   void kv_str(const std::string &k, const std::string &v) { str(k); put<uint32_t>(8); str(v); }
+  void kv_strs(const std::string &k, const std::vector<std::string> &v) {
+    str(k);
+    put<uint32_t>(9);
+    put<uint32_t>(8);
+    put<uint64_t>(v.size());
+    for (const auto &e : v) str(e);
+  }
 };
 
 Fill weight_fill(uint32_t kind) {
@@ -153,11 +160,13 @@ void fill_tensor(const Spec &s, uint64_t seed, uint64_t tidx, uint8_t *dst, uint
   switch (s.fill) {
     case Fill::Normal:
     case Fill::Ones:
-    case Fill::NearOne: {
+    case Fill::NearOne:
+    case Fill::LogUniform: {
       for (uint64_t e = lo; e < hi; ++e) {
         float v;
         if (s.fill == Fill::Ones) v = 1.0f;
         else if (s.fill == Fill::NearOne) v = float(0.75 + 0.5 * rng.uniform(e));
+        else if (s.fill == Fill::LogUniform) v = float(std::log(1.0 + 15.0 * rng.uniform(e)));
         else v = float(s.sigma * rng.normal(2 * e));
         if (s.kind == LG_F32) std::memcpy(dst + 4 * e, &v, 4);
         else {
@@ -249,10 +258,184 @@ uint64_t units(const Spec &s) {
   }
 }
 
+// Lays out the tensors (32-byte aligned data; `meta` must carry general.alignment = 32), writes
+// header + `meta` (nmeta key/values) + tensor table, and fills the data section in parallel.
+void emit_image(std::vector<Spec> &specs, const Writer &meta, int nmeta, uint64_t seed, const Preset &p,
+                uint8_t **out, uint64_t *out_len) {
+  const uint64_t align = 32;
+  uint64_t off = 0;
+  for (auto &s : specs) {
+    uint64_t count = 1;
+    for (auto v : s.dims) count *= v;
+    uint64_t block, size;
+    layout(s.kind, &block, &size);
+    s.bytes = count / block * size;
+    s.offset = off;
+    off = (off + s.bytes + align - 1) & ~(align - 1);
+  }
+  Writer w;
+  w.bytes("GGUF", 4);
+  w.put<uint32_t>(3);
+  w.put<uint64_t>(specs.size());
+  w.put<uint64_t>(uint64_t(nmeta));
+  w.bytes(meta.head.data(), meta.head.size());
+  for (const auto &s : specs) {
+    w.str(s.name);
+    w.put<uint32_t>(uint32_t(s.dims.size()));
+    for (auto v : s.dims) w.put<uint64_t>(v);
+    w.put<uint32_t>(s.kind);
+    w.put<uint64_t>(s.offset);
+  }
+  const uint64_t data_start = (w.head.size() + align - 1) & ~(align - 1);
+  const uint64_t total = data_start + off;
+  uint8_t *img = static_cast<uint8_t *>(std::malloc(total));
+  if (!img) fail(LG_ERR_OOM, "cannot allocate %llu bytes for the synthetic image",
+                 (unsigned long long)total);
+  std::memcpy(img, w.head.data(), w.head.size());
+  std::memset(img + w.head.size(), 0, data_start - w.head.size());
+  for (size_t i = 0; i < specs.size(); ++i) {
+    const auto &s = specs[i];
+    const uint64_t end = (i + 1 < specs.size()) ? specs[i + 1].offset : off;
+    std::memset(img + data_start + s.offset + s.bytes, 0, end - s.offset - s.bytes);
+  }
+  // parallel fill over (tensor, unit range) chunks
+  struct Chunk { size_t t; uint64_t lo, hi; };
+  std::vector<Chunk> chunks;
+  for (size_t t = 0; t < specs.size(); ++t) {
+    const uint64_t n = units(specs[t]);
+    const uint64_t step = 1 << 16;
+    for (uint64_t lo = 0; lo < n; lo += step) chunks.push_back({t, lo, std::min(n, lo + step)});
+  }
+  unsigned nth = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  std::vector<std::thread> pool;
+  std::atomic<size_t> next{0};
+  for (unsigned t = 0; t < nth; ++t)
+    pool.emplace_back([&] {
+      for (size_t c; (c = next.fetch_add(1)) < chunks.size();) {
+        const auto &ch = chunks[c];
+        fill_tensor(specs[ch.t], seed, ch.t, img + data_start + specs[ch.t].offset, ch.lo, ch.hi, p);
+      }
+    });
+  for (auto &t : pool) t.join();
+  *out = img;
+  *out_len = total;
+}
+
+// ---- OpenThai-SystemOne (Qwen3.5 hybrid text tower + 256-slot head) ----
+// Tensor names, shapes and kinds as written by scripts/convert-openthai.py:52-85 (F16 for
+// every tensor of rank >= 2, F32 vectors); config keys as checked by
+// src/models/openthai/model.rs:97-126.  Every fourth layer is full attention, the rest are
+// gated DeltaNet, as in the Qwen3.5 layer_types list.
+struct OtPreset {
+  const char *name;
+  int L, d, f, hq, hkv, nh, V, ctx, state;
+  int answer;     // answer_token_id
+  int opt_base;   // id of <|ts_opt_0|>; slots 0..254 follow
+  int ctl_base;   // ids of <|ts_q|>, <|ts_state|>, <|ts_choice|>, <|ts_score|>, <|ts_noul|>
+};
+
+const OtPreset kOtPresets[] = {
+    // The reference checkpoint's shape: 24 layers (18 DeltaNet + 6 full), d 1024, FFN 3584,
+    // 8/2 heads x 256, 16 linear heads x 128, vocab 248339.
+    {"openthai-0.8b", 24, 1024, 3584, 8, 2, 16, 248339, 4096, 2048, 248082, 247800, 248070},
+    // Small test shape with the same head geometry (8/2 heads x 256 dims, 128-dim
+    // linear heads, conv 4): 4 layers (3 DeltaNet + 1 full), d 256, 2 linear heads.
+    {"openthai-tiny", 4, 256, 512, 8, 2, 2, 1024, 1024, 512, 970, 700, 960},
+};
+
+const OtPreset *find_ot_preset(const char *name) {
+  for (const auto &p : kOtPresets)
+    if (!std::strcmp(p.name, name)) return &p;
+  return nullptr;
+}
+
+void synth_openthai(OtPreset p, uint64_t seed, int n_layers, uint8_t **out, uint64_t *out_len) {
+  if (n_layers > 0) p.L = n_layers;
+  const uint64_t d = p.d, f = p.f, hd = 256, lk = 128, nh = p.nh;
+  const uint64_t cd = 3 * nh * lk;  // conv channels: q | k | v
+  std::vector<Spec> specs;
+  auto add = [&](const std::string &n, std::vector<uint64_t> dims, uint32_t kind, Fill fill, double sigma) {
+    specs.push_back(Spec{n, std::move(dims), kind, fill, sigma});
+  };
+  std::string types;
+  add("model.embed_tokens.weight", {d, uint64_t(p.V)}, LG_F16, Fill::Normal, 0.02);
+  for (int l = 0; l < p.L; ++l) {
+    const std::string i = "model.layers." + std::to_string(l) + ".";
+    const bool full = l % 4 == 3;
+    types += std::string(l ? "," : "") + (full ? "\"full_attention\"" : "\"linear_attention\"");
+    add(i + "input_layernorm.weight", {d}, LG_F32, Fill::Normal, 0.1);  // zero-centred (offset 1)
+    if (full) {
+      add(i + "self_attn.q_proj.weight", {d, 2 * p.hq * hd}, LG_F16, Fill::Normal, 0.02);
+      add(i + "self_attn.k_proj.weight", {d, p.hkv * hd}, LG_F16, Fill::Normal, 0.02);
+      add(i + "self_attn.v_proj.weight", {d, p.hkv * hd}, LG_F16, Fill::Normal, 0.02);
+      add(i + "self_attn.o_proj.weight", {p.hq * hd, d}, LG_F16, Fill::Normal, 0.02);
+      add(i + "self_attn.q_norm.weight", {hd}, LG_F32, Fill::Normal, 0.1);
+      add(i + "self_attn.k_norm.weight", {hd}, LG_F32, Fill::Normal, 0.1);
+    } else {
+      add(i + "linear_attn.in_proj_qkv.weight", {d, cd}, LG_F16, Fill::Normal, 0.02);
+      add(i + "linear_attn.in_proj_z.weight", {d, nh * lk}, LG_F16, Fill::Normal, 0.02);
+      add(i + "linear_attn.in_proj_a.weight", {d, nh}, LG_F16, Fill::Normal, 0.02);
+      add(i + "linear_attn.in_proj_b.weight", {d, nh}, LG_F16, Fill::Normal, 0.02);
+      add(i + "linear_attn.out_proj.weight", {nh * lk, d}, LG_F16, Fill::Normal, 0.02);
+      add(i + "linear_attn.conv1d.weight", {4, 1, cd}, LG_F16, Fill::Normal, 0.3);
+      add(i + "linear_attn.dt_bias", {nh}, LG_F32, Fill::Normal, 0.5);
+      add(i + "linear_attn.A_log", {nh}, LG_F32, Fill::LogUniform, 0);
+      add(i + "linear_attn.norm.weight", {lk}, LG_F32, Fill::NearOne, 0);
+    }
+    add(i + "post_attention_layernorm.weight", {d}, LG_F32, Fill::Normal, 0.1);
+    add(i + "mlp.gate_proj.weight", {d, f}, LG_F16, Fill::Normal, 0.02);
+    add(i + "mlp.up_proj.weight", {d, f}, LG_F16, Fill::Normal, 0.02);
+    add(i + "mlp.down_proj.weight", {f, d}, LG_F16, Fill::Normal, 0.02);
+  }
+  add("model.norm.weight", {d}, LG_F32, Fill::Normal, 0.1);
+  add("slot_head.weight", {d, 256}, LG_F16, Fill::Normal, 0.02);
+  add("slot_head.bias", {256}, LG_F32, Fill::Normal, 0.1);
+  add("log_temperature", {3}, LG_F32, Fill::Normal, 0.1);
+
+  char cfg[2048];
+  std::snprintf(cfg, sizeof cfg,
+                "{\"model_type\":\"openthai_systemone\",\"n_slots\":256,\"abstain_slot\":255,"
+                "\"answer_token_id\":%d,\"text_config\":{\"hidden_size\":%d,\"intermediate_size\":%d,"
+                "\"num_hidden_layers\":%d,\"head_dim\":256,\"num_attention_heads\":%d,"
+                "\"num_key_value_heads\":%d,\"linear_conv_kernel_dim\":4,\"linear_key_head_dim\":128,"
+                "\"linear_value_head_dim\":128,\"linear_num_key_heads\":%d,\"linear_num_value_heads\":%d,"
+                "\"vocab_size\":%d,\"rms_norm_eps\":1e-06,\"rope_parameters\":{\"rope_theta\":10000000,"
+                "\"partial_rotary_factor\":0.25,\"rope_type\":\"default\"},\"layer_types\":[",
+                p.answer, p.d, p.f, p.L, p.hq, p.hkv, p.nh, p.nh, p.V);
+  const std::string config = std::string(cfg) + types + "]}}";
+  // token strings: placeholders, then the decide control tokens at their ids
+  std::vector<std::string> tokens(p.V);
+  for (int i = 0; i < p.V; ++i) tokens[i] = "t" + std::to_string(i);
+  tokens[198] = "\xc4\x8a";  // byte-level BPE newline
+  tokens[25] = ":";
+  for (int s = 0; s < 255; ++s) tokens[p.opt_base + s] = "<|ts_opt_" + std::to_string(s) + "|>";
+  const char *ctl[5] = {"<|ts_q|>", "<|ts_state|>", "<|ts_choice|>", "<|ts_score|>", "<|ts_noul|>"};
+  for (int j = 0; j < 5; ++j) tokens[p.ctl_base + j] = ctl[j];
+  tokens[p.answer] = "<|ts_answer|>";
+
+  Writer w;
+  w.kv_str("general.architecture", "openthai_systemone");
+  w.kv_str("general.name", std::string("OpenThai-SystemOne synthetic ") + p.name);
+  w.kv_u32("general.alignment", 32);
+  w.kv_str("openthai.config", config);
+  w.kv_u32("openthai.context_length", uint32_t(p.ctx));
+  w.kv_u32("openthai.state_length", uint32_t(p.state));
+  w.kv_str("tokenizer.ggml.model", "gpt2");
+  w.kv_strs("tokenizer.ggml.tokens", tokens);
+  w.kv_u64("laya.synthetic.seed", seed);
+  w.kv_str("laya.synthetic.preset", p.name);
+  Preset none{};
+  emit_image(specs, w, 10, seed, none, out, out_len);
+}
+
 }  // namespace
 
 // Builds the image; caller frees with free().
 void synth_image(const char *preset, uint64_t seed, int n_layers, uint8_t **out, uint64_t *out_len) {
+  if (const OtPreset *op = find_ot_preset(preset)) {
+    synth_openthai(*op, seed, n_layers, out, out_len);
+    return;
+  }
   const Preset *pp = find_preset(preset);
   if (!pp) fail(LG_ERR_INVALID, "unknown synthetic preset %s", preset);
   Preset p = *pp;
@@ -294,25 +477,10 @@ void synth_image(const char *preset, uint64_t seed, int n_layers, uint8_t **out,
   add("cos_full", {uint64_t(p.hd), uint64_t(p.ctx)}, LG_F32, Fill::Cos, 0);
   add("sin_full", {uint64_t(p.hd), uint64_t(p.ctx)}, LG_F32, Fill::Sin, 0);
 
-  const uint64_t align = 32;
-  uint64_t off = 0;
-  for (auto &s : specs) {
-    uint64_t count = 1;
-    for (auto v : s.dims) count *= v;
-    uint64_t block, size;
-    layout(s.kind, &block, &size);
-    s.bytes = count / block * size;
-    s.offset = off;
-    off = (off + s.bytes + align - 1) & ~(align - 1);
-  }
   Writer w;
-  w.bytes("GGUF", 4);
-  w.put<uint32_t>(3);
-  w.put<uint64_t>(specs.size());
-  w.put<uint64_t>(17);
   w.kv_str("general.architecture", "ggmlc");
   w.kv_str("general.name", std::string("laya-decoder synthetic ") + p.name);
-  w.kv_u32("general.alignment", uint32_t(align));
+  w.kv_u32("general.alignment", 32);
   w.kv_str("laya.model_name", "laya-decoder");
   w.kv_u32("laya.mask_token_id", 0);
   w.kv_u32("laya.decoder.block_count", uint32_t(p.L));
@@ -327,46 +495,7 @@ void synth_image(const char *preset, uint64_t seed, int n_layers, uint8_t **out,
   w.kv_f32("laya.decoder.rope_freq_base", float(p.theta));
   w.kv_u64("laya.synthetic.seed", seed);
   w.kv_str("laya.synthetic.preset", p.name);
-  for (const auto &s : specs) {
-    w.str(s.name);
-    w.put<uint32_t>(uint32_t(s.dims.size()));
-    for (auto v : s.dims) w.put<uint64_t>(v);
-    w.put<uint32_t>(s.kind);
-    w.put<uint64_t>(s.offset);
-  }
-  const uint64_t data_start = (w.head.size() + align - 1) & ~(align - 1);
-  const uint64_t total = data_start + off;
-  uint8_t *img = static_cast<uint8_t *>(std::malloc(total));
-  if (!img) fail(LG_ERR_OOM, "cannot allocate %llu bytes for the synthetic image",
-                 (unsigned long long)total);
-  std::memcpy(img, w.head.data(), w.head.size());
-  std::memset(img + w.head.size(), 0, data_start - w.head.size());
-  for (size_t i = 0; i < specs.size(); ++i) {
-    const auto &s = specs[i];
-    const uint64_t end = (i + 1 < specs.size()) ? specs[i + 1].offset : off;
-    std::memset(img + data_start + s.offset + s.bytes, 0, end - s.offset - s.bytes);
-  }
-  // parallel fill over (tensor, unit range) chunks
-  struct Chunk { size_t t; uint64_t lo, hi; };
-  std::vector<Chunk> chunks;
-  for (size_t t = 0; t < specs.size(); ++t) {
-    const uint64_t n = units(specs[t]);
-    const uint64_t step = 1 << 16;
-    for (uint64_t lo = 0; lo < n; lo += step) chunks.push_back({t, lo, std::min(n, lo + step)});
-  }
-  unsigned nth = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
-  std::vector<std::thread> pool;
-  std::atomic<size_t> next{0};
-  for (unsigned t = 0; t < nth; ++t)
-    pool.emplace_back([&] {
-      for (size_t c; (c = next.fetch_add(1)) < chunks.size();) {
-        const auto &ch = chunks[c];
-        fill_tensor(specs[ch.t], seed, ch.t, img + data_start + specs[ch.t].offset, ch.lo, ch.hi, p);
-      }
-    });
-  for (auto &t : pool) t.join();
-  *out = img;
-  *out_len = total;
+  emit_image(specs, w, 17, seed, p, out, out_len);
 }
 
 }  // namespace lg

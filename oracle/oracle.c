@@ -4,6 +4,7 @@
  */
 #define _GNU_SOURCE
 #include "oracle.h"
+#include "internal.h"
 
 #include <math.h>
 #include <pthread.h>
@@ -430,6 +431,7 @@ static void parallel(int n, int workers, range_fn f, void *ctx) {
   f(ctx, 0, per < n ? per : n);
   for (int t = 1; t <= started; ++t) pthread_join(th[t], NULL);
 }
+void or_parallel(int n, int workers, void (*f)(void *, int, int), void *ctx) { parallel(n, workers, f, ctx); }
 
 /* ------------------------------------------------------------------------- */
 /* src/tensor.rs:59-102: per (r, c): 8 FMA lanes over k in steps of 8, lanes   */

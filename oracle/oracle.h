@@ -88,6 +88,30 @@ void or_option_scores(const float *logits, int k, float abstain_logit, int has_a
  * f64 = 1: f64 entropy with log, src/models/laya/decision.rs:155-167. */
 float or_confidence(const float *p, int k, int f64);
 
+/* ---- OpenThai-SystemOne text tower (openthai.c), src/models/openthai/model.rs ---- */
+typedef struct or_openthai or_openthai;
+/* dims = {hidden, ffn, layers, heads, kv_heads, linear_heads, vocab}; full[l] != 0 marks a
+ * full-attention layer (else gated DeltaNet).  model.rs:96-191. */
+or_openthai *or_openthai_load(const or_gguf *g, const int dims[7], const int32_t *full, int threads,
+                              char *err, int errlen);
+void or_openthai_free(or_openthai *m);
+void or_openthai_dims(const or_openthai *m, int out[7]);
+void or_openthai_set_threads(or_openthai *m, int threads);
+/* model.rs:192-241: slot logits [npos][256] (final norm, slot head + bias). */
+int or_openthai_forward(or_openthai *m, const int32_t *ids, int n, const int32_t *pos, int npos,
+                        float *logits);
+/* Pieces of the forward, exposed for invariant tests:
+ * model.rs:306-318 causal conv (kernel 4) + silu over raw[s][ch], conv[ch][4];
+ * model.rs:319-358 gated delta rule over conv output qkv[s][3*nh*128], a/b[s][nh] -> out[s][nh*128];
+ * model.rs:260-275 partial RoPE (64 of 256 dims) in place over buf[s][heads][256];
+ * model.rs:276-294 causal GQA (scores / 16) over q[s][hq][256], k/v[s][hkv][256]. */
+void or_ot_conv_silu(const float *raw, int s, int ch, const float *conv, float *out);
+void or_ot_gated_delta(const float *qkv, const float *a, const float *b, const float *alog,
+                       const float *dt, int s, int nh, int threads, float *out);
+void or_ot_rope(float *buf, int s, int heads);
+void or_ot_attention(const float *q, const float *k, const float *v, int s, int hq, int hkv, int threads,
+                     float *out);
+
 #ifdef __cplusplus
 }
 #endif

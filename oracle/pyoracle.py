@@ -53,6 +53,15 @@ def lib() -> ctypes.CDLL:
             "or_argmax": (I, [P, I]),
             "or_option_scores": (None, [P, I, F, I, F, P, P, P]),
             "or_confidence": (F, [P, I, I]),
+            "or_openthai_load": (P, [P, P, P, I, ctypes.c_char_p, I]),
+            "or_openthai_free": (None, [P]),
+            "or_openthai_dims": (None, [P, P]),
+            "or_openthai_set_threads": (None, [P, I]),
+            "or_openthai_forward": (I, [P, P, I, P, I, P]),
+            "or_ot_conv_silu": (None, [P, I, I, P, P]),
+            "or_ot_gated_delta": (None, [P, P, P, P, P, I, I, I, P]),
+            "or_ot_rope": (None, [P, I, I]),
+            "or_ot_attention": (None, [P, P, P, I, I, I, I, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -244,3 +253,82 @@ class Cache:
 def argmax(v) -> int:
     v = _c(v, np.float32)
     return lib().or_argmax(_p(v), v.size)
+
+
+# ---- OpenThai-SystemOne (openthai.c) ----
+
+def openthai_config(gguf: Gguf) -> dict:
+    """Dimensions and layer kinds from the openthai.config JSON (src/models/openthai/model.rs:97-126)."""
+    import json
+    cfg = json.loads(gguf.str("openthai.config"))
+    c = cfg["text_config"]
+    full = [1 if t == "full_attention" else 0 for t in c["layer_types"][: int(c["num_hidden_layers"])]]
+    return {"d": int(c["hidden_size"]), "f": int(c["intermediate_size"]), "L": int(c["num_hidden_layers"]),
+            "hq": int(c["num_attention_heads"]), "hkv": int(c["num_key_value_heads"]),
+            "nh": int(c["linear_num_value_heads"]), "V": int(c["vocab_size"]), "full": full,
+            "answer": int(cfg["answer_token_id"]),
+            "max_tokens": int(gguf.num("openthai.context_length", 4096)),
+            "max_state": int(gguf.num("openthai.state_length", 2048))}
+
+
+class OpenThai:
+    """The OpenThai text tower on the CPU: Model::forward -> slot logits [npos][256]."""
+
+    def __init__(self, gguf: Gguf, threads: int = 4):
+        self.g = gguf
+        self.cfg = openthai_config(gguf)
+        c = self.cfg
+        dims = np.array([c["d"], c["f"], c["L"], c["hq"], c["hkv"], c["nh"], c["V"]], dtype=np.int32)
+        self._full = np.array(c["full"], dtype=np.int32)
+        err = ctypes.create_string_buffer(256)
+        self.h = lib().or_openthai_load(gguf.h, _p(dims), _p(self._full), threads, err, 256)
+        if not self.h:
+            raise ValueError(err.value.decode())
+        self.d, self.V, self.L = c["d"], c["V"], c["L"]
+
+    def set_threads(self, n: int) -> None:
+        lib().or_openthai_set_threads(self.h, n)
+
+    def forward(self, ids, positions) -> np.ndarray:
+        ids, pos = _c(ids, np.int32), _c(positions, np.int32)
+        out = np.empty((pos.size, 256), dtype=np.float32)
+        if lib().or_openthai_forward(self.h, _p(ids), ids.size, _p(pos), pos.size, _p(out)):
+            raise ValueError("invalid OpenThai token sequence")
+        return out
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.or_openthai_free(self.h)
+            self.h = None
+
+
+def ot_conv_silu(raw, conv) -> np.ndarray:
+    raw, conv = _c(raw, np.float32), _c(conv, np.float32)
+    s, ch = raw.shape
+    out = np.empty_like(raw)
+    lib().or_ot_conv_silu(_p(raw), s, ch, _p(conv), _p(out))
+    return out
+
+
+def ot_gated_delta(qkv, a, b, alog, dt, threads=1) -> np.ndarray:
+    qkv, a, b = _c(qkv, np.float32), _c(a, np.float32), _c(b, np.float32)
+    alog, dt = _c(alog, np.float32), _c(dt, np.float32)
+    s, nh = a.shape
+    out = np.empty((s, nh * 128), dtype=np.float32)
+    lib().or_ot_gated_delta(_p(qkv), _p(a), _p(b), _p(alog), _p(dt), s, nh, threads, _p(out))
+    return out
+
+
+def ot_rope(buf) -> np.ndarray:
+    buf = _c(buf, np.float32).copy()
+    s, heads = buf.shape[0], buf.shape[1] // 256
+    lib().or_ot_rope(_p(buf), s, heads)
+    return buf
+
+
+def ot_attention(q, k, v, threads=1) -> np.ndarray:
+    q, k, v = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32)
+    s, hq, hkv = q.shape[0], q.shape[1] // 256, k.shape[1] // 256
+    out = np.empty_like(q)
+    lib().or_ot_attention(_p(q), _p(k), _p(v), s, hq, hkv, threads, _p(out))
+    return out
