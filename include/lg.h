@@ -115,7 +115,15 @@ typedef struct {
   int kv_pages, kv_page_tokens;
   int precision;           /* LG_PREC_* the engine was created with */
   int kv_elem_bytes;       /* 4 (f32 cache) or 2 (f16 cache) */
+  int arch;                /* LG_ARCH_* */
+  int linear_heads;        /* OpenThai: gated DeltaNet heads (128-dim); 0 otherwise */
+  int full_layers;         /* OpenThai: full-attention layers (the rest are DeltaNet) */
 } lg_model_info;
+
+/* Model families (general.architecture): "ggmlc" + laya.model_name "laya-decoder", and
+ * "openthai_systemone" (src/models/mod.rs:65-71). */
+#define LG_ARCH_LAYA_DECODER 0
+#define LG_ARCH_OPENTHAI 1
 
 /* Load a laya-decoder GGUF onto one GPU: validate, upload and repack every matrix into a
  * hipMalloc'd weight arena, reserve the KV page pool, create the engine's stream.

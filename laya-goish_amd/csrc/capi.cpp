@@ -383,7 +383,7 @@ int lg_decide(lg_engine *e, const lg_decide_request *req, lg_decide_result *out,
     }
     held.b = E.batch_create(reqs.data(), n);
     std::vector<float> logits(size_t(n) * req->n_questions * 256);
-    E.batch_run(held.b, s.slot, 256, 1.0f, logits.data(), nullptr, nullptr, cancel, cancel_arg);
+    E.batch_run(held.b, s.head_row, 256, 1.0f, logits.data(), nullptr, nullptr, cancel, cancel_arg);
     lg::decide_aggregate(s, *req, n, enc, logits.data(), *out);
   });
 }

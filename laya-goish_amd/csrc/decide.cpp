@@ -6,14 +6,76 @@
 
 #include <algorithm>
 #include <cmath>
+#include <map>
 #include <set>
 
 #include "common.h"
 #include "gguf.h"
+#include "json.h"
 
 namespace lg {
 
+namespace {
+
+void read_temperatures(const Gguf &g, DecideSpec &s) {
+  // expf of a 3-element F32 tensor log_temperature when the model has one, as
+  // src/models/openthai/model.rs:175-178; else metadata; else 1
+  s.temperature[0] = float(g.num("laya.decide.temperature_choice", 1.0));
+  s.temperature[1] = float(g.num("laya.decide.temperature_score", 1.0));
+  s.temperature[2] = float(g.num("laya.decide.temperature_noul", 1.0));
+  if (const TensorInfo *t = g.tensor("log_temperature")) {
+    if (t->kind != LG_F32 || t->cols() * t->rows() != 3) fail(LG_ERR_FORMAT, "log_temperature must be F32 [3]");
+    const float *v = reinterpret_cast<const float *>(g.data(*t));
+    for (int i = 0; i < 3; ++i) s.temperature[i] = std::exp(v[i]);
+  }
+  for (float T : s.temperature)
+    if (!(T > 0.0f) || !std::isfinite(T)) fail(LG_ERR_FORMAT, "decide temperatures must be positive");
+}
+
+DecideSpec openthai_spec(const Gguf &g) {
+  DecideSpec s;
+  const Json cfg = Json::parse(g.str("openthai.config"), "openthai.config");
+  s.vocab = int(cfg.get("text_config").get("vocab_size").num());
+  s.answer = int(cfg.get("answer_token_id").num());
+  s.max_tokens = int(g.num("openthai.context_length", 4096));
+  s.max_state = int(g.num("openthai.state_length", 2048));
+  for (int i = 0; i < 256; ++i) s.head_row[i] = i;
+  read_temperatures(g, s);
+  const MetaValue *tv = g.meta("tokenizer.ggml.tokens");
+  if (!tv || tv->strs.empty()) {
+    s.error = "OpenThai model has no tokenizer.ggml.tokens to take its decide control tokens from";
+    return s;
+  }
+  std::map<std::string, int32_t> index;
+  for (size_t i = 0; i < tv->strs.size(); ++i) index.emplace(tv->strs[i], int32_t(i));
+  auto find = [&](const std::string &tok, int32_t &dst) {
+    auto it = index.find(tok);
+    if (it == index.end()) {
+      if (s.error.empty()) s.error = "OpenThai tokenizer lacks the decide control token " + tok;
+      dst = 0;
+    } else {
+      dst = it->second;
+    }
+  };
+  for (int i = 0; i < 255; ++i) find("<|ts_opt_" + std::to_string(i) + "|>", s.slot[i]);
+  s.slot[255] = s.slot[254];  // the abstain slot has no prompt marker
+  find("<|ts_state|>", s.state);
+  find("<|ts_q|>", s.question);
+  find("<|ts_choice|>", s.kind[0]);
+  find("<|ts_score|>", s.kind[1]);
+  find("<|ts_noul|>", s.kind[2]);
+  find("\xc4\x8a", s.newline);  // byte-level BPE spelling of "\n"
+  find(":", s.colon);
+  int32_t answer_tok = 0;
+  find("<|ts_answer|>", answer_tok);
+  if (s.error.empty() && answer_tok != s.answer) s.error = "missing OpenThai answer token";
+  return s;
+}
+
+}  // namespace
+
 DecideSpec decide_spec(const Gguf &g) {
+  if (g.str("general.architecture") == "openthai_systemone") return openthai_spec(g);
   DecideSpec s;
   const int V = int(g.num("laya.decoder.vocab_size", 0));
   const int ctx = int(g.num("laya.decoder.context_length", 0));
@@ -28,18 +90,8 @@ DecideSpec decide_spec(const Gguf &g) {
   s.answer = int(g.num("laya.decide.answer_id", V - 262));
   s.newline = int(g.num("laya.decide.newline_id", V - 263));
   s.colon = int(g.num("laya.decide.colon_id", V - 264));
-  // temperatures: expf of a 3-element F32 tensor log_temperature when the model has one, as
-  // src/models/openthai/model.rs:175-178; else metadata; else 1
-  s.temperature[0] = float(g.num("laya.decide.temperature_choice", 1.0));
-  s.temperature[1] = float(g.num("laya.decide.temperature_score", 1.0));
-  s.temperature[2] = float(g.num("laya.decide.temperature_noul", 1.0));
-  if (const TensorInfo *t = g.tensor("log_temperature")) {
-    if (t->kind != LG_F32 || t->cols() * t->rows() != 3) fail(LG_ERR_FORMAT, "log_temperature must be F32 [3]");
-    const float *v = reinterpret_cast<const float *>(g.data(*t));
-    for (int i = 0; i < 3; ++i) s.temperature[i] = std::exp(v[i]);
-  }
-  for (float T : s.temperature)
-    if (!(T > 0.0f) || !std::isfinite(T)) fail(LG_ERR_FORMAT, "decide temperatures must be positive");
+  for (int i = 0; i < 256; ++i) s.head_row[i] = s.slot[i];
+  read_temperatures(g, s);
   s.max_tokens = int(g.num("laya.decide.context_length", ctx));
   s.max_state = int(g.num("laya.decide.state_length", std::min(2048, ctx)));
   return s;
@@ -60,8 +112,10 @@ int desc_len(const lg_question &q, int i) { return q.desc_len && q.descs && q.de
 }  // namespace
 
 void decide_validate(const DecideSpec &s, const lg_decide_request &r) {
-  for (int32_t id : {s.slot[0], s.slot[255], s.state, s.question, s.kind[0], s.kind[1], s.kind[2], s.answer, s.newline,
-                     s.colon})
+  if (!s.error.empty()) fail(LG_ERR_FORMAT, "%s", s.error.c_str());
+  for (int32_t id : {s.state, s.question, s.kind[0], s.kind[1], s.kind[2], s.answer, s.newline, s.colon})
+    if (id < 0 || id >= s.vocab) fail(LG_ERR_FORMAT, "decide control token %d outside the vocabulary of %d", id, s.vocab);
+  for (int32_t id : s.slot)
     if (id < 0 || id >= s.vocab) fail(LG_ERR_FORMAT, "decide control token %d outside the vocabulary of %d", id, s.vocab);
   if (r.n_questions < 1 || r.n_questions > 256 || !r.questions)
     fail(LG_ERR_INVALID, "questions must contain 1..256 named questions");

@@ -17,17 +17,24 @@ namespace lg {
 
 class Gguf;
 
-// Control tokens and budgets of the decide layout.  Read from laya.decide.* metadata when the
-// model has it; otherwise the top of the vocabulary: slot s (s < 255: option marker s, 255:
-// abstain) = V - 256 + s, then state, question, the three kind markers, answer, newline and
-// colon below it.
+// Control tokens and budgets of the decide layout.
+// laya-decoder models: laya.decide.* metadata when the model has it; otherwise the top of the
+// vocabulary: slot s (s < 255: option marker s, 255: abstain) = V - 256 + s, then state,
+// question, the three kind markers, answer, newline and colon below it.  The scored head rows
+// are the slot tokens' rows of the language-model head.
+// OpenThai models: the special tokens of the embedded tokenizer (<|ts_opt_s|>, <|ts_state|>,
+// <|ts_q|>, <|ts_choice|>, <|ts_score|>, <|ts_noul|>, byte-level newline, ":"), the config's
+// answer_token_id, openthai.context_length / state_length; the scored rows are the 256 rows of
+// the slot head (src/models/openthai/decision.rs:185-224, model.rs:116-132).
 struct DecideSpec {
   int32_t slot[256];
+  int32_t head_row[256];  // head row scored for slot s
   int32_t state = 0, question = 0, kind[3] = {0, 0, 0}, answer = 0, newline = 0, colon = 0;
   float temperature[3] = {1.0f, 1.0f, 1.0f};  // per question kind (choice, score, noul)
   int max_tokens = 0;                         // prompt budget (context_length)
   int max_state = 0;                          // state budget (state_length)
   int vocab = 0;
+  std::string error;  // non-empty: the model cannot encode decide prompts (reported on use)
 };
 
 DecideSpec decide_spec(const Gguf &g);

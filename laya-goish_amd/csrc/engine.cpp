@@ -130,8 +130,6 @@ Profiler::~Profiler() {
 }
 
 // ------------------------------------------------------------------ helpers
-namespace {
-
 int64_t q_row_bytes(uint32_t kind, int cols) {
   switch (kind) {
     case LG_F32: return int64_t(cols) * 4;
@@ -159,23 +157,6 @@ DevMatrix sub_rows(const DevMatrix &m, int row0, int nrows) {
 }
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
-}  // namespace
-
-// Planned batch: device metadata for one staged prefill batch.
-struct BatchPlan {
-  std::vector<int> seqs;        // engine sequence per request
-  std::vector<int> n, npos;     // tokens and answer positions per request
-  std::vector<int> start_len;   // sequence length at staging time
-  int T = 0, R = 0, ntiles = 0, max_pages = 0;
-  DevBuf meta;                  // ids, tok_seq, tok_pos, pages, tiles..., gather rows
-  int32_t *ids = nullptr, *tok_seq = nullptr, *tok_pos = nullptr, *pages = nullptr;
-  int32_t *tile_seq = nullptr, *tile_row0 = nullptr, *tile_pos0 = nullptr, *tile_n = nullptr;
-  int ngroups = 0;              // runs of <= 4 consecutive tiles of one sequence
-  int32_t *grp_first = nullptr, *grp_count = nullptr;
-  int32_t *gather = nullptr;
-  bool ran = false;
-};
-
 // ------------------------------------------------------------------ construction
 Engine::Engine(const Gguf &g, const lg_engine_opts &opts) {
   device = opts.device;
@@ -183,6 +164,27 @@ Engine::Engine(const Gguf &g, const lg_engine_opts &opts) {
   HIP_CHECK(hipGetDeviceCount(&ndev));
   if (device < 0 || device >= ndev) fail(LG_ERR_INVALID, "device %d out of range (%d devices)", device, ndev);
   HIP_CHECK(hipSetDevice(device));
+  max_batch_tokens_ = opts.max_batch_tokens > 0 ? opts.max_batch_tokens : 65536;
+  if (opts.precision != LG_PREC_EXACT && opts.precision != LG_PREC_FAST)
+    fail(LG_ERR_INVALID, "unknown precision mode %d", opts.precision);
+  precision = opts.precision;
+  try {
+    if (g.str("general.architecture") == "openthai_systemone") {
+      arch = Arch::OpenThai;
+      HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+      load_openthai(g);
+      decide = decide_spec(g);
+      HIP_CHECK(hipStreamSynchronize(stream));
+      return;
+    }
+    load_decoder(g, opts);
+  } catch (...) {
+    release();
+    throw;
+  }
+}
+
+void Engine::load_decoder(const Gguf &g, const lg_engine_opts &opts) {
   if (g.str("general.architecture") != "ggmlc" || g.str("laya.model_name") != "laya-decoder")
     fail(LG_ERR_FORMAT, "unsupported ggmlc model %s", g.str("laya.model_name").c_str());
   L = int(g.num("laya.decoder.block_count", 0));
@@ -199,10 +201,6 @@ Engine::Engine(const Gguf &g, const lg_engine_opts &opts) {
     fail(LG_ERR_FORMAT, "invalid laya-decoder dimensions");
   if (d % 64 || (hd != 64 && hd != 128))
     fail(LG_ERR_UNSUPPORTED, "d_model %d / head_dim %d outside the kernels' shapes", d, hd);
-  max_batch_tokens_ = opts.max_batch_tokens > 0 ? opts.max_batch_tokens : 65536;
-  if (opts.precision != LG_PREC_EXACT && opts.precision != LG_PREC_FAST)
-    fail(LG_ERR_INVALID, "unknown precision mode %d", opts.precision);
-  precision = opts.precision;
   HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
   upload(g);
   // KV pool: [L][npages][hkv][64][hd] elements (f32 in EXACT mode, f16 in FAST) for K, then V
@@ -227,12 +225,16 @@ Engine::Engine(const Gguf &g, const lg_engine_opts &opts) {
   HIP_CHECK(hipStreamSynchronize(stream));
 }
 
-Engine::~Engine() {
+Engine::~Engine() { release(); }
+
+void Engine::release() {
   if (stream) (void)hipStreamSynchronize(stream);
   if (arena_) (void)hipFree(arena_);
   if (emb_) (void)hipFree(emb_);
   if (kv_) (void)hipFree(kv_);
   if (stream) (void)hipStreamDestroy(stream);
+  arena_ = emb_ = kv_ = nullptr;
+  stream = nullptr;
 }
 
 void *Engine::carve(size_t bytes) {
@@ -243,7 +245,7 @@ void *Engine::carve(size_t bytes) {
   return p;
 }
 
-float *Engine::upload_vector_f32(const Gguf &g, const std::string &name, int64_t n) {
+float *Engine::upload_vector_f32(const Gguf &g, const std::string &name, int64_t n, float offset) {
   const TensorInfo *t = g.tensor(name);
   if (!t) fail(LG_ERR_FORMAT, "missing tensor %s", name.c_str());
   uint64_t count = 1;
@@ -255,6 +257,8 @@ float *Engine::upload_vector_f32(const Gguf &g, const std::string &name, int64_t
   else if (t->kind == LG_F16)
     for (int64_t i = 0; i < n; ++i) h[i] = half_to_float(uint16_t(src[2 * i] | (src[2 * i + 1] << 8)));
   else fail(LG_ERR_UNSUPPORTED, "%s: vectors must be F32/F16", name.c_str());
+  if (offset != 0.0f)
+    for (int64_t i = 0; i < n; ++i) h[i] = offset + h[i];
   float *dptr = static_cast<float *>(carve(n * 4));
   HIP_CHECK(hipMemcpy(dptr, h.data(), n * 4, hipMemcpyHostToDevice));
   return dptr;
@@ -262,7 +266,7 @@ float *Engine::upload_vector_f32(const Gguf &g, const std::string &name, int64_t
 
 // Upload one or more GGUF matrices with equal kind and row length as one row-concatenated
 // device matrix (q|k|v or gate|up): row blocks of the same layout are contiguous.
-DevMatrix Engine::upload_matrix(const Gguf &g, const std::vector<std::string> &names, int cols) {
+DevMatrix Engine::upload_matrix(const Gguf &g, const std::vector<std::string> &names, int cols, int pad_to) {
   DevMatrix m;
   std::vector<const TensorInfo *> ts;
   int rows = 0;
@@ -281,8 +285,9 @@ DevMatrix Engine::upload_matrix(const Gguf &g, const std::vector<std::string> &n
   if (m.kind == LG_Q4_0) fail(LG_ERR_UNSUPPORTED, "Q4_0 matrices have no device kernel");
   if ((m.kind == LG_Q4_K || m.kind == LG_Q6_K) && cols % 256)
     fail(LG_ERR_FORMAT, "invalid quantized row alignment");
-  m.q = carve(size_t(q_row_bytes(m.kind, cols)) * rows);
-  if (s_row_bytes(m.kind, cols)) m.s = carve(size_t(s_row_bytes(m.kind, cols)) * rows);
+  const int alloc_rows = pad_to > 0 ? (rows + pad_to - 1) / pad_to * pad_to : rows;
+  m.q = carve(size_t(q_row_bytes(m.kind, cols)) * alloc_rows);
+  if (s_row_bytes(m.kind, cols)) m.s = carve(size_t(s_row_bytes(m.kind, cols)) * alloc_rows);
   size_t maxraw = 0;
   for (auto *t : ts) maxraw = std::max<size_t>(maxraw, t->len);
   DevBuf staging;
@@ -298,6 +303,13 @@ DevMatrix Engine::upload_matrix(const Gguf &g, const std::vector<std::string> &n
     row0 += part.rows;
   }
   weight_bytes_ += m.gguf_bytes();
+  if (alloc_rows > rows) {  // zero weights in the pad rows: their outputs are 0 and never read
+    DevMatrix pad = sub_rows(m, rows, alloc_rows - rows);
+    HIP_CHECK(hipMemsetAsync(pad.q, 0, size_t(q_row_bytes(m.kind, cols)) * pad.rows, stream));
+    if (pad.s) HIP_CHECK(hipMemsetAsync(pad.s, 0, size_t(s_row_bytes(m.kind, cols)) * pad.rows, stream));
+    HIP_CHECK(hipStreamSynchronize(stream));
+    m.rows = alloc_rows;
+  }
   return m;
 }
 
@@ -405,8 +417,8 @@ lg_model_info Engine::info() const {
   i.ffn = f;
   i.vocab = V;
   i.context = ctx;
-  i.kind_attn = layers_.empty() ? 0 : layers_[0].wo.kind;
-  i.kind_ffn = layers_.empty() ? 0 : layers_[0].wd.kind;
+  i.kind_attn = !layers_.empty() ? layers_[0].wo.kind : !ot_.empty() ? ot_[0].out.kind : 0;
+  i.kind_ffn = !layers_.empty() ? layers_[0].wd.kind : !ot_.empty() ? ot_[0].wd.kind : 0;
   i.kind_head = head_.kind;
   i.weight_bytes = weight_bytes_;
   i.kv_bytes = int64_t(2) * L * npages_ * page_stride_ * kv_elem();
@@ -414,6 +426,10 @@ lg_model_info Engine::info() const {
   i.kv_page_tokens = 64;
   i.precision = precision;
   i.kv_elem_bytes = kv_elem();
+  i.arch = int(arch);
+  i.linear_heads = nh;
+  i.full_layers = 0;
+  for (const OtLayer &y : ot_) i.full_layers += y.full ? 1 : 0;
   return i;
 }
 
@@ -520,6 +536,7 @@ void Engine::reserve_pages(Seq &s, int upto) {
 }
 
 int Engine::seq_fork(int parent, int ntokens) {
+  if (arch == Arch::OpenThai) fail(LG_ERR_UNSUPPORTED, "fork: OpenThai sequences keep no cache to share");
   Seq &p = seq(parent);
   LG_REQUIRE(ntokens >= 0 && ntokens <= p.len, "fork: %d tokens outside the parent's %d", ntokens, p.len);
   Seq c;
@@ -560,8 +577,9 @@ int Engine::seq_len(int id) const {
 BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
   LG_REQUIRE(nreq > 0 && reqs, "batch: no requests");
   auto *b = new BatchPlan();
+  const bool ot = arch == Arch::OpenThai;
   try {
-    std::vector<int32_t> ids, tseq, tpos, tiles_s, tiles_r, tiles_p, tiles_n, gather, grp_f, grp_c;
+    std::vector<int32_t> ids, tseq, tpos, tiles_s, tiles_r, tiles_p, tiles_n, gather, grp_f, grp_c, srow0, sn;
     int max_pages = 0;
     for (int r = 0; r < nreq; ++r) {
       const lg_request &q = reqs[r];
@@ -574,14 +592,17 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
         if (q.ids[i] < 0 || q.ids[i] >= V) fail(LG_ERR_INVALID, "request %d: token id %d outside the vocabulary", r, q.ids[i]);
       for (int i = 0; i < q.npos; ++i)
         if (q.positions[i] < 0 || q.positions[i] >= q.n) fail(LG_ERR_INVALID, "request %d: answer position %d outside the request", r, q.positions[i]);
+      if (ot && s.len != 0)  // model.rs:2: the recurrent state lives only inside one forward
+        fail(LG_ERR_INVALID, "request %d: sequence %d already holds %d tokens; an OpenThai forward starts from an empty sequence",
+             r, q.seq, s.len);
       if (s.len + q.n > ctx) fail(LG_ERR_INVALID, "request %d: %d tokens exceed the context length %d", r, s.len + q.n, ctx);
-      max_pages = std::max(max_pages, (s.len + q.n + 63) / 64);
+      if (!ot) max_pages = std::max(max_pages, (s.len + q.n + 63) / 64);
     }
     const int64_t T = std::accumulate(reqs, reqs + nreq, int64_t(0), [](int64_t a, const lg_request &q) { return a + q.n; });
     if (T > max_batch_tokens_) fail(LG_ERR_INVALID, "batch of %lld tokens exceeds max_batch_tokens %lld", (long long)T, (long long)max_batch_tokens_);
     // reserve pages (all or nothing)
     int need = 0;
-    for (int r = 0; r < nreq; ++r) {
+    for (int r = 0; r < nreq && !ot; ++r) {
       const Seq &s = seq(reqs[r].seq);
       need += std::max(0, (s.len + reqs[r].n + 63) / 64 - int(s.pages.size()));
     }
@@ -591,8 +612,12 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
     for (int r = 0; r < nreq; ++r) {
       const lg_request &q = reqs[r];
       Seq &s = seq(q.seq);
-      reserve_pages(s, s.len + q.n);
-      for (size_t p = 0; p < s.pages.size(); ++p) ptab[size_t(r) * max_pages + p] = s.pages[p];
+      if (!ot) {
+        reserve_pages(s, s.len + q.n);
+        for (size_t p = 0; p < s.pages.size(); ++p) ptab[size_t(r) * max_pages + p] = s.pages[p];
+      }
+      srow0.push_back(row);
+      sn.push_back(q.n);
       for (int i = 0; i < q.n; ++i) {
         ids.push_back(q.ids[i]);
         tseq.push_back(r);
@@ -620,8 +645,9 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
     b->ntiles = int(tiles_s.size());
     b->ngroups = int(grp_f.size());
     b->max_pages = max_pages;
-    const size_t nints = ids.size() * 3 + ptab.size() + tiles_s.size() * 4 + grp_f.size() * 2 + gather.size() + 64;
-    b->meta.ensure(nints * 4 + 20 * 256);
+    const size_t nints = ids.size() * 3 + ptab.size() + tiles_s.size() * 4 + grp_f.size() * 2 + gather.size() +
+                         srow0.size() * 2 + 64;
+    b->meta.ensure(nints * 4 + 24 * 256);
     int32_t *base = b->meta.as<int32_t>();
     size_t off = 0;
     auto put = [&](const std::vector<int32_t> &v, int32_t *&dst) {
@@ -640,6 +666,8 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
     put(grp_f, b->grp_first);
     put(grp_c, b->grp_count);
     put(gather, b->gather);
+    put(srow0, b->seq_row0);
+    put(sn, b->seq_n);
     HIP_CHECK(hipStreamSynchronize(stream));
   } catch (...) {
     delete b;
@@ -715,10 +743,13 @@ void Engine::batch_run(BatchPlan *b, const int32_t *option_ids, int k, float tem
   LG_REQUIRE(k <= 32 || (!probs && !logprobs), "batch: option scores need 1..32 option ids");
   LG_REQUIRE(temperature > 0 && std::isfinite(temperature), "batch: temperature must be positive");
   for (int j = 0; j < k; ++j)
-    if (option_ids[j] < 0 || option_ids[j] >= V) fail(LG_ERR_INVALID, "option id %d outside the vocabulary", option_ids[j]);
+    if (option_ids[j] < 0 || option_ids[j] >= head_rows())
+      fail(LG_ERR_INVALID, arch == Arch::OpenThai ? "slot %d outside the 256 slots" : "option id %d outside the vocabulary",
+           option_ids[j]);
   // sequences must still exist and not have moved since staging
   for (size_t r = 0; r < b->seqs.size(); ++r) seq(b->seqs[r]);
-  run_layers_prefill(*b, cancel, arg);
+  if (arch == Arch::OpenThai) run_openthai(*b, cancel, arg);
+  else run_layers_prefill(*b, cancel, arg);
   for (size_t r = 0; r < b->seqs.size(); ++r) seq(b->seqs[r]).len += b->n[r];
   b->ran = true;
   const int R = b->R;
@@ -731,7 +762,7 @@ void Engine::batch_run(BatchPlan *b, const int32_t *option_ids, int k, float tem
   int32_t *dids = reinterpret_cast<int32_t *>(dlp + size_t(R) * k);
   HIP_CHECK(hipMemcpyAsync(dids, option_ids, size_t(k) * 4, hipMemcpyHostToDevice, stream));
   prof.begin("head", stream);
-  launch_head_rows(ws_x_.as<float>(), b->gather, R, d, final_norm_, eps, head_, dids, k, dl, stream);
+  launch_head_rows(ws_x_.as<float>(), b->gather, R, d, final_norm_, eps, head_, head_bias_, dids, k, dl, stream);
   if (k <= 32) launch_option_scores(dl, R, k, temperature, dp, dlp, stream);
   prof.end(0, 0, stream);
   if (logits) HIP_CHECK(hipMemcpyAsync(logits, dl, size_t(R) * k * 4, hipMemcpyDeviceToHost, stream));
@@ -747,6 +778,12 @@ void Engine::forward(int sq, const int32_t *ids, int n, const int32_t *positions
   struct Guard { Engine *e; BatchPlan *b; ~Guard() { e->batch_free(b); } } guard{this, b};
   if (vocab_ids) {
     batch_run(b, vocab_ids, nv, 1.0f, logits, nullptr, nullptr, cancel, arg);
+    return;
+  }
+  if (arch == Arch::OpenThai) {  // every slot row of the slot head
+    int32_t slots[256];
+    for (int i = 0; i < 256; ++i) slots[i] = i;
+    batch_run(b, slots, 256, 1.0f, logits, nullptr, nullptr, cancel, arg);
     return;
   }
   // full vocabulary: prefill, then one fused-norm GEMV over the head per answer row
@@ -770,6 +807,7 @@ void Engine::forward(int sq, const int32_t *ids, int n, const int32_t *positions
 
 // ------------------------------------------------------------------ greedy decode
 void Engine::decode(int sq, int32_t first, int steps, int32_t *tokens, float *logits) {
+  if (arch == Arch::OpenThai) fail(LG_ERR_UNSUPPORTED, "decode: an OpenThai model has a slot head, not a language-model head");
   Seq &s = seq(sq);
   LG_REQUIRE(steps > 0 && tokens, "decode: need steps > 0 and an output");
   LG_REQUIRE(first >= 0 && first < V, "decode: token id %d outside the vocabulary", first);

@@ -1,6 +1,7 @@
 // The engine: one model on one GPU with its own stream, weight arena and KV page pool.
 // Host-side counterpart of the reference's Engine + Backend + Model (src/engine.rs:10-48,
-// src/models/mod.rs:13-23, src/models/openthai/model.rs:41-241), for the laya-decoder shape.
+// src/models/mod.rs:13-23, src/models/openthai/model.rs:41-241), for the laya-decoder shape
+// and the OpenThai-SystemOne text tower (dispatch on general.architecture, mod.rs:65-71).
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -15,6 +16,12 @@
 #include "lg.h"
 
 namespace lg {
+
+// Bytes per row of a repacked matrix: codes/values (q) and scales (s); rows [row0, row0+n) view.
+int64_t q_row_bytes(uint32_t kind, int cols);
+int64_t s_row_bytes(uint32_t kind, int cols);
+DevMatrix sub_rows(const DevMatrix &m, int row0, int nrows);
+size_t align256(size_t n);
 
 // A slice of a projection's output columns computed by one device matrix.
 struct ProjPart {
@@ -71,7 +78,37 @@ class Profiler {
   KernelTimer timer_;
 };
 
-struct BatchPlan;
+// Planned batch: device metadata for one staged prefill batch.
+struct BatchPlan {
+  std::vector<int> seqs;        // engine sequence per request
+  std::vector<int> n, npos;     // tokens and answer positions per request
+  std::vector<int> start_len;   // sequence length at staging time
+  int T = 0, R = 0, ntiles = 0, max_pages = 0;
+  DevBuf meta;                  // ids, tok_seq, tok_pos, pages, tiles..., gather rows
+  int32_t *ids = nullptr, *tok_seq = nullptr, *tok_pos = nullptr, *pages = nullptr;
+  int32_t *tile_seq = nullptr, *tile_row0 = nullptr, *tile_pos0 = nullptr, *tile_n = nullptr;
+  int ngroups = 0;              // runs of <= 4 consecutive tiles of one sequence
+  int32_t *grp_first = nullptr, *grp_count = nullptr;
+  int32_t *gather = nullptr;
+  int32_t *seq_row0 = nullptr, *seq_n = nullptr;  // first batch row and token count per request
+  bool ran = false;
+};
+
+enum class Arch { Decoder = 0, OpenThai = 1 };
+
+// One OpenThai-SystemOne layer (src/models/openthai/model.rs:10-40).  Norm weights are stored
+// as 1 + w (the zero-centred RMSNorm's offset applied once at upload, an exact f32 add).
+struct OtLayer {
+  bool full = false;
+  float *n1 = nullptr, *n2 = nullptr;
+  // full: rows [(q 256 | gate 256) x hq | k 256 x hkv | v 256 x hkv];
+  // DeltaNet: rows [q|k|v (3*nh*128) | z (nh*128) | a (nh) | b (nh) | zero rows to a multiple of 128]
+  DevMatrix proj;
+  DevMatrix out;               // o_proj / out_proj
+  DevMatrix wi, wd;            // gate rows then up rows; down
+  float *qn1 = nullptr, *kn1 = nullptr;                                      // full: 1 + q_norm, 1 + k_norm
+  float *conv = nullptr, *dt = nullptr, *alog = nullptr, *norm = nullptr;  // DeltaNet
+};
 
 class Engine {
  public:
@@ -102,15 +139,21 @@ class Engine {
   Profiler prof;
 
  private:
+  void load_decoder(const Gguf &g, const lg_engine_opts &opts);
   void upload(const Gguf &g);
-  DevMatrix upload_matrix(const Gguf &g, const std::vector<std::string> &names, int cols);
-  float *upload_vector_f32(const Gguf &g, const std::string &name, int64_t n);
+  void load_openthai(const Gguf &g);
+  void release();
+  // pad_to > 0: rows rounded up to a multiple of pad_to with zero weights
+  DevMatrix upload_matrix(const Gguf &g, const std::vector<std::string> &names, int cols, int pad_to = 0);
+  // offset != 0: stores offset + w (the zero-centred RMSNorm weight)
+  float *upload_vector_f32(const Gguf &g, const std::string &name, int64_t n, float offset = 0.0f);
   void *carve(size_t bytes);
   Seq &seq(int id);
   void reserve_pages(Seq &s, int upto_tokens);
   int alloc_page();
   void release_page(int p);
   void run_layers_prefill(BatchPlan &b, lg_cancel_fn cancel, void *arg);
+  void run_openthai(BatchPlan &b, lg_cancel_fn cancel, void *arg);
   KvGeom geom() const;
   void *kpool(int layer) const;
   void *vpool(int layer) const;
@@ -125,7 +168,10 @@ class Engine {
  public:
   int device = 0;
   hipStream_t stream = nullptr;
+  Arch arch = Arch::Decoder;
   int L = 0, d = 0, hq = 0, hkv = 0, hd = 0, f = 0, V = 0, ctx = 0;
+  int nh = 0;          // OpenThai: gated DeltaNet heads (128-dim)
+  int head_rows() const { return arch == Arch::OpenThai ? 256 : V; }
   float eps = 1e-5f;
   uint32_t emb_kind = 0;
   int precision = LG_PREC_EXACT;
@@ -141,6 +187,9 @@ class Engine {
   float *cos_ = nullptr, *sin_ = nullptr, *final_norm_ = nullptr;
   std::vector<Layer> layers_;
   DevMatrix head_;
+  float *head_bias_ = nullptr;                 // OpenThai slot-head bias [256]
+  std::vector<OtLayer> ot_;                    // OpenThai layers
+  int ldp_full_ = 0, ldp_delta_ = 0;           // OpenThai projection row widths
   std::map<std::string, DevMatrix> named_;  // GGUF name -> device matrix view
   int64_t weight_bytes_ = 0;
   // KV pool
@@ -154,6 +203,7 @@ class Engine {
   // workspaces
   DevBuf ws_x_, ws_h16_, ws_qkv_, ws_q16_, ws_att16_, ws_act16_, ws_meta_, ws_out_;
   DevBuf ws_dec_;
+  DevBuf ws_ot_qk_, ws_ot_v_, ws_ot_gb_, ws_ot_o_;  // OpenThai mixer workspaces
 };
 
 }  // namespace lg

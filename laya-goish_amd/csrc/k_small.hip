@@ -244,7 +244,8 @@ __device__ float weight_at_head(const DevMatrix &W, int64_t n, int64_t k) {
 __global__ __launch_bounds__(kT) void head_rows_kernel(const float *__restrict__ x,
                                                        const int32_t *__restrict__ rows, int d,
                                                        const float *__restrict__ norm_w, float eps,
-                                                       DevMatrix W, const int32_t *__restrict__ ids,
+                                                       DevMatrix W, const float *__restrict__ bias,
+                                                       const int32_t *__restrict__ ids,
                                                        int nv, float *__restrict__ logits) {
   extern __shared__ float h[];
   __shared__ float red[kT / 64];
@@ -260,6 +261,7 @@ __global__ __launch_bounds__(kT) void head_rows_kernel(const float *__restrict__
     float s = 0.0f;
     for (int k = lane; k < d; k += 64) s += h[k] * weight_at_head(W, n, k);
     s = wave_sum(s);
+    if (bias) s = s + bias[n];
     if (lane == 0) logits[int64_t(blockIdx.x) * nv + j] = s;
   }
 }
@@ -423,12 +425,12 @@ void launch_rope_kv_tiles(const float *qkv, int hq, const KvGeom &g, const float
 }
 
 void launch_head_rows(const float *x, const int32_t *rows, int R, int d, const float *norm_w,
-                      float eps, const DevMatrix &W, const int32_t *vocab_ids, int nv,
+                      float eps, const DevMatrix &W, const float *bias, const int32_t *vocab_ids, int nv,
                       float *logits, hipStream_t st) {
   LG_REQUIRE(R > 0 && nv > 0 && W.cols == d, "head: bad shape");
   LG_REQUIRE(size_t(d) * 4 <= 64 * 1024, "head: d too large for LDS");
   hipLaunchKernelGGL(head_rows_kernel, dim3(R), dim3(kT), size_t(d) * 4, st, x, rows, d, norm_w, eps, W,
-                     vocab_ids, nv, logits);
+                     bias, vocab_ids, nv, logits);
   HIP_CHECK(hipGetLastError());
 }
 

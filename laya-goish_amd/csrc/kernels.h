@@ -133,9 +133,9 @@ void launch_attn_decode(const float *qkv, int hq, const KvGeom &g, const float *
                         float *part, float *out, hipStream_t st);
 int64_t attn_decode_scratch_floats(int nseq, int hq, int hd, int max_ctx);
 
-// Gather rows, final RMSNorm and the option head: logits[r][j] = h_r . W[ids[j]].
+// Gather rows, final RMSNorm and the option head: logits[r][j] = h_r . W[ids[j]] (+ bias[ids[j]]).
 void launch_head_rows(const float *x, const int32_t *rows, int R, int d, const float *norm_w,
-                      float eps, const DevMatrix &W, const int32_t *vocab_ids, int nv,
+                      float eps, const DevMatrix &W, const float *bias, const int32_t *vocab_ids, int nv,
                       float *logits, hipStream_t st);
 
 // Option scoring over logits[R][k]: probabilities and log-softmax at temperature t.
@@ -152,6 +152,31 @@ void launch_cvt_f16(const float *x, int64_t n, _Float16 *y, _Float16 *y_lo, hipS
 
 // f32 weights from the repacked layout of W, row-major [rows][cols] (bit-exact dequant).
 void launch_dequant_repacked(const DevMatrix &w, float *dst, hipStream_t st);
+
+// ---- OpenThai-SystemOne mixers (k_openthai.hip), src/models/openthai/model.rs:244-362 ----
+// Gated DeltaNet, per token: causal conv (kernel 4) + silu over the q|k|v columns of the
+// projection row [q|k|v (3*nh*128) | z (nh*128) | a (nh) | b (nh) | pad] (ldp floats), then
+// qk[T][nh][query 128 | key 128] (L2-normalised; query also / sqrt(128)), vbuf[T][nh*128],
+// gb[T][nh][decay, beta].  tok_pos = index of each row in its sequence.
+void launch_ot_delta_prep(const float *proj, int ldp, int T, const int32_t *tok_pos, const float *conv,
+                          const float *alog, const float *dt, int nh, float *qk, float *vbuf, float *gb,
+                          hipStream_t st);
+// The recurrent scan over each sequence (rows seq_row0[s] .. + seq_n[s]): out[T][nh*128].
+void launch_ot_delta_scan(const float *qk, const float *vbuf, const float *gb, const int32_t *seq_row0,
+                          const int32_t *seq_n, int nseq, int nh, float *out, hipStream_t st);
+// rms(out head, norm_w) * silu(z) with z at column zcol of the projection row -> f16 planes.
+void launch_ot_delta_out(const float *o, int T, int nh, const float *norm_w, const float *proj, int ldp, int zcol,
+                         _Float16 *y, _Float16 *ylo, hipStream_t st);
+// Full attention: per-head q/k rms (weights 1 + w) + partial RoPE (tables [pos][32]) from the
+// projection row [(q 256 | gate 256) x hq | k 256 x hkv | v 256 x hkv] into Qb[T][hq][256],
+// Kb[T][hkv][256]; then causal GQA over 32-token tiles (tile_*: first row, position, count)
+// with the output * sigmoid(gate) -> f16 planes [T][hq*256].
+void launch_ot_attn_prep(const float *proj, int ldp, int T, int hq, int hkv, const int32_t *tok_pos,
+                         const float *qn1, const float *kn1, const float *cosT, const float *sinT, float *Qb,
+                         float *Kb, hipStream_t st);
+void launch_ot_attn(const float *Qb, const float *Kb, const float *proj, int ldp, int hq, int hkv,
+                    const int32_t *tile_row0, const int32_t *tile_pos0, const int32_t *tile_n, int ntiles,
+                    _Float16 *y, _Float16 *ylo, hipStream_t st);
 
 // Device int32 fill / copy helpers (small, capture-safe).
 void launch_fill_i32(int32_t *p, int n, int32_t v, hipStream_t st);

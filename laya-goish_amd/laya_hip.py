@@ -22,6 +22,7 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "lg.h")
 
 F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
 PREC_EXACT, PREC_FAST = 0, 1
+ARCH_LAYA_DECODER, ARCH_OPENTHAI = 0, 1
 KIND_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
 ERR = {1: "INVALID", 2: "FORMAT", 3: "DEVICE", 4: "OOM", 5: "CANCELED", 6: "UNSUPPORTED"}
 
@@ -45,7 +46,8 @@ class ModelInfo(ctypes.Structure):
                [("kind_attn", ctypes.c_uint32), ("kind_ffn", ctypes.c_uint32), ("kind_head", ctypes.c_uint32),
                 ("weight_bytes", ctypes.c_int64), ("kv_bytes", ctypes.c_int64),
                 ("kv_pages", ctypes.c_int), ("kv_page_tokens", ctypes.c_int),
-                ("precision", ctypes.c_int), ("kv_elem_bytes", ctypes.c_int)]
+                ("precision", ctypes.c_int), ("kv_elem_bytes", ctypes.c_int),
+                ("arch", ctypes.c_int), ("linear_heads", ctypes.c_int), ("full_layers", ctypes.c_int)]
 
     def asdict(self):
         return {n: getattr(self, n) for n, _ in self._fields_}
@@ -390,9 +392,11 @@ class Batch:
         self.engine, self.h, self._keep, self.R = engine, handle, requests, total_positions
 
     def run(self, option_ids, temperature: float = 1.0, cancel=None):
+        """Head rows `option_ids` at every answer position: (logits, probs, logprobs); option
+        scores only for k <= 32 (else None)."""
         k = len(option_ids)
         ids = _c(option_ids, np.int32)
-        out = [np.empty((self.R, k), dtype=np.float32) for _ in range(3)]
+        out = [np.empty((self.R, k), dtype=np.float32) if i == 0 or k <= 32 else None for i in range(3)]
         cb = CANCEL_FN(cancel) if cancel else CANCEL_FN(0)
         check(lib().lg_batch_run(self.engine.h, self.h, _ptr(ids), k, temperature,
                                  *(_ptr(o) for o in out), cb, None))
@@ -476,7 +480,8 @@ class Engine:
         ids = _c(ids, np.int32)
         pos = _c(positions, np.int32)
         vid = None if vocab_ids is None else _c(vocab_ids, np.int32)
-        nv = self.info["vocab"] if vid is None else vid.size
+        full = 256 if self.info["arch"] == ARCH_OPENTHAI else self.info["vocab"]  # slot head or LM head rows
+        nv = full if vid is None else vid.size
         out = np.empty((pos.size, nv), dtype=np.float32)
         cb = CANCEL_FN(cancel) if cancel else CANCEL_FN(0)
         check(lib().lg_forward(self.h, seq, _ptr(ids), ids.size, _ptr(pos), pos.size, _ptr(vid),

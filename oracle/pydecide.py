@@ -21,17 +21,97 @@ import pyoracle as po
 KINDS = {"choice": 0, "score": 1, "noul": 2}
 
 
+_SIZES = {0: 1, 1: 1, 2: 2, 3: 2, 4: 4, 5: 4, 6: 4, 7: 1, 10: 8, 11: 8, 12: 8}
+
+
+def gguf_strings(buf, key: str) -> list:
+    """The string array stored under `key` in a GGUF v3 image (src/gguf.rs:48-79 value kinds),
+    read independently of both GGUF readers under test."""
+    import struct
+    b = bytes(buf)
+    off = 24
+    n_kv = struct.unpack_from("<Q", b, 16)[0]
+
+    def rstr(o):
+        n = struct.unpack_from("<Q", b, o)[0]
+        return b[o + 8:o + 8 + n].decode("utf-8"), o + 8 + n
+
+    def skip(t, o):
+        if t in _SIZES:
+            return o + _SIZES[t]
+        if t == 8:
+            return rstr(o)[1]
+        et, cnt = struct.unpack_from("<IQ", b, o)
+        o += 12
+        for _ in range(cnt):
+            o = skip(et, o)
+        return o
+
+    for _ in range(n_kv):
+        k, off = rstr(off)
+        t = struct.unpack_from("<I", b, off)[0]
+        off += 4
+        if k == key and t == 9:
+            et, cnt = struct.unpack_from("<IQ", b, off)
+            off += 12
+            out = []
+            for _ in range(cnt):
+                v, off = rstr(off)
+                out.append(v)
+            return out if et == 8 else []
+        off = skip(t, off)
+    return []
+
+
+def _expf(v: float) -> float:
+    import ctypes
+    libm = ctypes.CDLL("libm.so.6")
+    libm.expf.restype, libm.expf.argtypes = ctypes.c_float, [ctypes.c_float]
+    return float(np.float32(libm.expf(v)))
+
+
+def _temperatures(gguf: po.Gguf, temps: list) -> list:
+    """expf(log_temperature) when the model has the tensor (src/models/openthai/model.rs:175-178)."""
+    try:
+        kind, dims, raw = gguf.tensor("log_temperature")
+    except KeyError:
+        return temps
+    return [_expf(float(v)) for v in np.frombuffer(raw, "<f4")]
+
+
+def _openthai_spec(gguf: po.Gguf) -> dict:
+    """OpenThai: the tokenizer's special tokens (decision.rs:185-224), the config's answer id,
+    openthai.context_length / state_length; the 256 slot-head rows are scored."""
+    cfg = po.openthai_config(gguf)
+    index = {}
+    for i, t in enumerate(gguf_strings(gguf.buf, "tokenizer.ggml.tokens")):
+        index.setdefault(t, i)
+    slot = [index[f"<|ts_opt_{i}|>"] for i in range(255)]
+    return {
+        "V": cfg["V"], "slot": slot + [slot[254]], "head_rows": list(range(256)),
+        "state": index["<|ts_state|>"], "question": index["<|ts_q|>"],
+        "kind": [index["<|ts_choice|>"], index["<|ts_score|>"], index["<|ts_noul|>"]],
+        "answer": cfg["answer"], "newline": index["\u010a"], "colon": index[":"],
+        "temperature": _temperatures(gguf, [1.0, 1.0, 1.0]),
+        "max_tokens": cfg["max_tokens"], "max_state": cfg["max_state"],
+    }
+
+
 def spec(gguf: po.Gguf) -> dict:
     """Control tokens and budgets: laya.decide.* metadata, else the layout at the top of the
     vocabulary (slot s = V-256+s, state V-257, question V-258, kinds V-259..V-261, answer V-262,
-    newline V-263, colon V-264)."""
+    newline V-263, colon V-264).  OpenThai models: _openthai_spec."""
+    if gguf.str("general.architecture") == "openthai_systemone":
+        return _openthai_spec(gguf)
     V = int(gguf.num("laya.decoder.vocab_size"))
     ctx = int(gguf.num("laya.decoder.context_length"))
     base = int(gguf.num("laya.decide.slot_base", V - 256))
     temps = [float(np.float32(gguf.num(f"laya.decide.temperature_{k}", 1.0))) for k in ("choice", "score", "noul")]
+    temps = _temperatures(gguf, temps)
     return {
         "V": V,
         "slot": [base + i for i in range(256)],
+        "head_rows": [base + i for i in range(256)],
         "state": int(gguf.num("laya.decide.state_id", V - 257)),
         "question": int(gguf.num("laya.decide.question_id", V - 258)),
         "kind": [int(gguf.num("laya.decide.choice_id", V - 259)), int(gguf.num("laya.decide.score_id", V - 260)),
@@ -153,5 +233,8 @@ def decide(model: po.Model, gguf: po.Gguf, req: dict) -> dict:
     s = spec(gguf)
     n = passes(req)
     encs = [encode(s, req, n, p) for p in range(n)]
-    logits = np.stack([model.forward(e[0], e[1], s["slot"]) for e in encs])
+    if isinstance(model, po.OpenThai):  # slot head: all 256 rows
+        logits = np.stack([model.forward(e[0], e[1]) for e in encs])
+    else:
+        logits = np.stack([model.forward(e[0], e[1], s["head_rows"]) for e in encs])
     return aggregate(s, req, n, encs, logits), logits

@@ -166,3 +166,55 @@ def test_forward_rejects_invalid_sequences(tiny):
     for ids, pos in (([], []), ([1, 2, 1024], [0]), ([1, 2, 3], [3]), ([1, -1], [0])):
         with pytest.raises(ValueError, match="invalid OpenThai token sequence"):
             m.forward(ids, pos)
+
+
+# ---- request-level decide on an OpenThai model (host side: lg_decide_encode / lg_decide_scores)
+
+def _req(rng, V, nq, perms=None, state_len=50):
+    kinds = ["choice", "score", "noul"]
+    qs = []
+    for i in range(nq):
+        kind = kinds[i % 3]
+        k = {"choice": int(rng.integers(2, 9)), "score": int(rng.integers(2, 11)), "noul": 2}[kind]
+        opts = [{"name": rng.integers(0, 600, int(rng.integers(1, 3))).tolist(),
+                 "desc": rng.integers(0, 600, int(rng.integers(0, 3))).tolist()} for _ in range(k)]
+        qs.append({"type": kind, "instruction": rng.integers(0, 600, int(rng.integers(0, 6))).tolist(), "options": opts})
+    return {"state": rng.integers(0, 600, state_len).tolist(), "questions": qs, "permutations": perms}
+
+
+def test_decide_control_tokens_come_from_the_tokenizer(tiny, lh):
+    import pydecide as pd
+    img, g, _ = tiny
+    s = pd.spec(g)
+    # where the synthetic writer put them (the openthai-tiny preset)
+    assert (s["question"], s["state"], s["kind"], s["answer"]) == (960, 961, [962, 963, 964], 970)
+    assert s["slot"][:3] == [700, 701, 702] and s["slot"][254] == 954 and (s["newline"], s["colon"]) == (198, 25)
+    assert s["head_rows"] == list(range(256)) and (s["max_tokens"], s["max_state"]) == (1024, 512)
+    req = {"state": [5, 6], "questions": [{"type": "noul", "instruction": [7], "options": [{"name": [8]}, {"name": [9]}]}]}
+    ids, pos, _, _, _ = lh.decide_encode(lh.Gguf.from_bytes(img), req, 0)
+    assert ids.tolist() == [961, 5, 6, 198, 960, 964, 7, 198, 700, 8, 198, 701, 9, 198, 970, 198]
+    assert pos.tolist() == [14]
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_decide_encode_and_scores_match_oracle(tiny, lh, seed):
+    import pydecide as pd
+    img, g, _ = tiny
+    lg = lh.Gguf.from_bytes(img)
+    rng = np.random.default_rng(40 + seed)
+    req = _req(rng, 1024, int(rng.integers(1, 5)), perms=[None, 3, 8][seed % 3], state_len=int(rng.integers(0, 900)))
+    s = pd.spec(g)
+    n = pd.passes(req)
+    encs = []
+    for p in range(n):
+        ids, pos, order, trunc, npass = lh.decide_encode(lg, req, p)
+        want = pd.encode(s, req, n, p)
+        assert npass == n and np.array_equal(ids, want[0]) and np.array_equal(pos, want[1])
+        assert order == want[2] and trunc == want[3]
+        encs.append(want)
+    logits = (rng.normal(size=(n, len(req["questions"]), 256)) * 2).astype(np.float32)
+    got = lh.decide_scores(lg, req, logits)
+    want = pd.aggregate(s, req, n, encs, logits)
+    for a, b in zip(got["answers"], want["answers"]):
+        assert np.array_equal(a["probabilities"], b["probabilities"])
+        assert a["confidence"] == b["confidence"] and a["choice"] == b["choice"]

@@ -1,0 +1,140 @@
+"""OpenThai-SystemOne on the GPU (gated DeltaNet + gated full attention + slot head) against the
+CPU oracle (oracle/openthai.c, itself pinned in test_cpu_openthai.py).
+
+Reference: Model::forward (src/models/openthai/model.rs:192-241) -> slot logits; decide
+(src/models/openthai/decision.rs:243-390).  Bars: slot logits within 2e-3 absolute
+(validation/openthai_check.py:31) in the EXACT mode, option probabilities within 1e-3.
+"""
+import numpy as np
+import pytest
+
+import pydecide as pd
+
+pytestmark = pytest.mark.gpu
+
+TOL = {0: 2e-3, 1: 5e-2}  # EXACT, FAST
+
+
+@pytest.fixture(scope="module", params=[0, 1], ids=["exact", "fast"])
+def tiny(request, lh, po):
+    img = lh.SynthImage("openthai-tiny", seed=21)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), precision=request.param)
+    og = po.Gguf(img.array())
+    yield request.param, eng, po.OpenThai(og, threads=8), og
+    eng.close()
+
+
+def test_info(tiny, lh):
+    _, eng, _, _ = tiny
+    i = eng.info
+    assert i["arch"] == lh.ARCH_OPENTHAI and i["linear_heads"] == 2 and i["full_layers"] == 1
+    assert (i["layers"], i["d_model"], i["heads"], i["kv_heads"], i["head_dim"], i["vocab"]) == (4, 256, 8, 2, 256, 1024)
+
+
+@pytest.mark.parametrize("n", [1, 3, 16, 17, 33, 100, 300])
+def test_forward_matches_oracle(tiny, n):
+    prec, eng, om, _ = tiny
+    ids = np.random.default_rng(n).integers(0, 960, n)
+    pos = sorted({0, n // 3, n - 1})
+    print(f"openthai-tiny prec {prec}: forward n={n}", flush=True)
+    s = eng.seq_create()
+    got = eng.forward(s, ids, pos)
+    eng.seq_free(s)
+    want = om.forward(ids, pos)
+    err = float(np.abs(got - want).max())
+    assert got.shape == (len(pos), 256) and err <= TOL[prec], f"slot logits differ by {err:.3e}"
+
+
+def test_batch_equals_single_and_repeats(tiny):
+    """Ragged batch of fresh sequences: each row equals its own single-sequence forward, bit for
+    bit, and a repeat gives the same bits (validation/smoke.py:25-28)."""
+    prec, eng, om, _ = tiny
+    rng = np.random.default_rng(5)
+    reqs = [(rng.integers(0, 960, n), [n - 1, n // 2]) for n in (40, 7, 129, 64, 1)]
+    seqs = [eng.seq_create() for _ in reqs]
+    b = eng.batch([(s, ids, pos) for s, (ids, pos) in zip(seqs, reqs)])
+    slots = list(range(256))
+    logits, _, _ = b.run(slots)
+    b.free()
+    row = 0
+    for s, (ids, pos) in zip(seqs, reqs):
+        eng.seq_free(s)
+        s2 = eng.seq_create()
+        single = eng.forward(s2, ids, pos)
+        eng.seq_free(s2)
+        assert np.array_equal(logits[row:row + len(pos)], single)
+        row += len(pos)
+
+
+def test_slot_subset_and_errors(tiny, lh):
+    prec, eng, om, _ = tiny
+    ids = np.arange(10, 60)
+    s = eng.seq_create()
+    part = eng.forward(s, ids, [49], [3, 255, 0])
+    full_s = eng.seq_create()
+    full = eng.forward(full_s, ids, [49])
+    assert np.array_equal(part[0], full[0, [3, 255, 0]])
+    # a second forward on a used sequence: the recurrent state is local to one forward
+    with pytest.raises(lh.LayaError) as ei:
+        eng.forward(s, ids, [0])
+    assert ei.value.kind == "INVALID" and "empty sequence" in str(ei.value)
+    with pytest.raises(lh.LayaError) as ei:
+        eng.decode(full_s, 5, 2)
+    assert ei.value.kind == "UNSUPPORTED"
+    with pytest.raises(lh.LayaError) as ei:
+        eng.seq_fork(full_s, 10)
+    assert ei.value.kind == "UNSUPPORTED"
+    s3 = eng.seq_create()
+    with pytest.raises(lh.LayaError) as ei:
+        eng.forward(s3, ids, [0], [256])
+    assert ei.value.kind == "INVALID" and "256 slots" in str(ei.value)
+    with pytest.raises(lh.LayaError):
+        eng.forward(s3, [1, 2, 1024], [0])
+    for q in (s, full_s, s3):
+        eng.seq_free(q)
+
+
+def _request(rng, perms):
+    def toks(lo, hi):
+        return rng.integers(0, 600, int(rng.integers(lo, hi))).tolist()
+    return {"state": toks(80, 300),
+            "questions": [
+                {"type": "choice", "instruction": toks(3, 8), "options": [{"name": toks(1, 3), "desc": toks(0, 4)} for _ in range(6)]},
+                {"type": "score", "instruction": toks(2, 5), "options": [{"name": [], "desc": toks(1, 3)} for _ in range(5)]},
+                {"type": "noul", "instruction": toks(2, 5), "options": [{"name": toks(1, 2)}, {"name": toks(1, 2)}]}],
+            "permutations": perms}
+
+
+@pytest.mark.parametrize("perms", [1, 4])
+def test_decide_matches_oracle(tiny, perms):
+    prec, eng, om, og = tiny
+    req = _request(np.random.default_rng(perms + 10), perms)
+    print(f"openthai-tiny prec {prec}: decide, {perms} passes", flush=True)
+    got = eng.decide(req)
+    want, _ = pd.decide(om, og, req)
+    assert got["usage"]["permutations"] == want["permutations"] == perms
+    assert got["usage"]["input_tokens"] == want["input_tokens"]
+    bar = 1e-3 if prec == 0 else 2e-2
+    for a, b in zip(got["answers"], want["answers"]):
+        err = float(np.abs(a["probabilities"] - b["probabilities"]).max())
+        assert err <= bar, f"{a['type']}: probability error {err:.3e}"
+        top = np.sort(b["probabilities"])[::-1]
+        if top[0] - top[1] > bar:
+            assert a["choice"] == b["choice"]
+
+
+def test_full_width_layers_match_oracle(lh, po):
+    """The first four layers of the 0.8B shape (d 1024, 16 linear heads, 8/2 x 256 attention,
+    vocab 248339): three DeltaNet layers and one full-attention layer, 160 tokens."""
+    img = lh.SynthImage("openthai-0.8b", seed=3, n_layers=4)
+    eng = lh.Engine(lh.Gguf.from_bytes(img))
+    om = po.OpenThai(po.Gguf(img.array()), threads=8)
+    ids = np.random.default_rng(0).integers(0, 247000, 160)
+    pos = [0, 77, 159]
+    print("openthai-0.8b (4 layers): forward n=160", flush=True)
+    s = eng.seq_create()
+    got = eng.forward(s, ids, pos)
+    eng.close()
+    want = om.forward(ids, pos)
+    err = float(np.abs(got - want).max())
+    assert err <= 2e-3, f"slot logits differ by {err:.3e}"
