@@ -309,6 +309,98 @@ def bench_decide_request(args, prec):
     return line
 
 
+OT_PRESET = "openthai-0.8b"
+
+
+def openthai_requests(seed):
+    """Token-level counterparts of the reference's timed OpenThai cases
+    (validation/openthai.requests.json; timings in validation/openthai-summary.json:11-39):
+    case 7, one 255-option choice question in 1 pass, 1437 prompt tokens (57,884 ms on the
+    reference's CPU x4); case 8, an 11-option choice question, default 8 passes of 60 tokens
+    (13,191 ms)."""
+    rng = np.random.default_rng(seed)
+
+    def toks(n):
+        return rng.integers(0, 247000, n).tolist()
+    # 1437 = state block 7 (marker, 5 ids, newline) + header 6 (marker, kind, 3 ids, newline)
+    #        + 255 x (slot marker, name, newline) with 912 name ids + answer block 2
+    names = [4] * 147 + [3] * 108
+    big = {"state": toks(5), "permutations": 1,
+           "questions": [{"type": "choice", "instruction": toks(3), "options": [{"name": toks(n)} for n in names]}]}
+    # 60 = 7 + 6 + 11 x 2 + 23 name ids + 2; 11 options -> the default 8 option-order passes
+    small = {"state": toks(5),
+             "questions": [{"type": "choice", "instruction": toks(3),
+                            "options": [{"name": toks(n)} for n in [3] + [2] * 10]}]}
+    return big, small
+
+
+def bench_openthai(args, prec):
+    """OpenThai-SystemOne decide on the 0.8B shape (24 layers: 18 gated DeltaNet + 6 gated full
+    attention, d 1024, FFN 3584, vocab 248339, F16 weights as the converter writes them): the
+    reference's two timed request shapes, each lg_decide call end to end (encode, one GPU batch
+    of all passes, slot scoring), requests one after another."""
+    img = lh.SynthImage(OT_PRESET, seed=SEED)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), precision=prec)
+    big, small = openthai_requests(SEED + 7)
+    steps = max(args.steps, 5)
+    res = {}
+    for name, req, want in (("1437x1", big, 1437), ("60x8", small, 60)):
+        out = None
+        for _ in range(max(args.warmup, 1)):
+            out = eng.decide(req)
+        eng.sync()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            out = eng.decide(req)
+        dt = (time.perf_counter() - t0) / steps
+        assert out["usage"]["input_tokens"] == want, out["usage"]
+        res[name] = (dt, out["usage"]["permutations"])
+        log(f"openthai {name}: {dt * 1e3:.2f} ms per request ({out['usage']['permutations']} passes)")
+    eng.profile_reset()
+    eng.profile(True)
+    eng.decide(big)
+    eng.profile(False)
+    classes = ("gemm", "ot_attn", "ot_attn_prep", "ot_delta_prep", "ot_delta_scan", "ot_delta_out", "rmsnorm",
+               "embed")
+    prof = {c: eng.profile_read(c) for c in classes}
+    for c in classes:
+        p = prof[c]
+        log(f"  {c:14s} {p['launches']:4d} launches {p['ms']:8.3f} ms")
+    eng.close()
+    g = prof["gemm"]
+    gemm_tflops = g["flops"] / (g["ms"] * 1e-3) / 1e12 if g["ms"] > 0 else 0.0
+    dt_big, _ = res["1437x1"]
+    dt_small, np_small = res["60x8"]
+    line = base_line("OpenThai decide req/s (0.8B shape, 1437-token request)", round(1 / dt_big, 3), "req/s", True,
+                     steps, max(args.warmup, 1), dt_big * 1e3, prec,
+                     "OpenThai-SystemOne 0.8B shape (24 layers: 18 gated DeltaNet + 6 gated full attention, "
+                     "d 1024, FFN 3584, 8/2 x 256 heads, 16 linear heads x 128, vocab 248339, F16); request: "
+                     "1 choice question of 255 options, 1437 tokens, 1 pass",
+                     ms_per_request=round(dt_big * 1e3, 2),
+                     ms_per_request_60x8=round(dt_small * 1e3, 2), passes_60x8=np_small,
+                     reference_cpu_ms={"1437x1": 57884, "60x8": 13191},
+                     kernel_ms={c: round(prof[c]["ms"], 3) for c in classes})
+    line["roofline"] = {"bound": "mfma", "achieved": round(gemm_tflops, 1), "peak": PEAK_F16_TFLOPS,
+                        "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_F16_TFLOPS, 4), "traffic": None,
+                        "kernel": "gemm (every projection and MLP matrix of the 1437-token forward)"}
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import pydecide
+        import pyoracle as po
+        layers = 4
+        smallimg = lh.SynthImage(OT_PRESET, seed=SEED, n_layers=layers)
+        og = po.Gguf(smallimg.array())
+        om = po.OpenThai(og, threads=args.cpu_threads)
+        t0 = time.perf_counter()
+        pydecide.decide(om, og, big)
+        cdt = (time.perf_counter() - t0) * 24 / layers
+        line["cpu_baseline"] = {"value": round(1 / cdt, 5), "unit": "req/s", "cores": args.cpu_threads, "kind": "port",
+                                "sample": f"the 1437-token request through {layers} of 24 layers (3 DeltaNet + 1 "
+                                          f"full attention, the model's own 3:1 mix), time scaled x{24 // layers}: "
+                                          f"{cdt:.1f} s per request"}
+    return line
+
+
 def cpu_baseline(threads, layers=24):
     """The oracle on a bounded sample: one 560-token request of the workload through `layers`
     of the 24 layers (per-layer cost is identical), scaled to the full model."""
@@ -342,7 +434,8 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--precision", choices=["exact", "fast"], default="exact")
-    ap.add_argument("--workload", choices=["decide", "plumbing", "q4k-prefill", "long-context", "decide-request"],
+    ap.add_argument("--workload", choices=["decide", "plumbing", "q4k-prefill", "long-context", "decide-request",
+                                           "openthai-decide"],
                     default="decide",
                     help="decide (default): the Q8_0 d2048 batched decide headline plus batch-1 decode; the "
                          "others measure the remaining workload shapes, one JSON line each")
@@ -364,7 +457,7 @@ def main():
     prec = lh.PREC_EXACT if args.precision == "exact" else lh.PREC_FAST
     if args.workload != "decide":
         fn = {"plumbing": bench_plumbing, "q4k-prefill": bench_q4k, "long-context": bench_long_context,
-              "decide-request": bench_decide_request}
+              "decide-request": bench_decide_request, "openthai-decide": bench_openthai}
         print(json.dumps(fn[args.workload](args, prec)), flush=True)
         return
     if args.copy_calibration > 0:
