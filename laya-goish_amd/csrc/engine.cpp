@@ -580,6 +580,7 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
   const bool ot = arch == Arch::OpenThai;
   try {
     std::vector<int32_t> ids, tseq, tpos, tiles_s, tiles_r, tiles_p, tiles_n, gather, grp_f, grp_c, srow0, sn;
+    std::vector<int32_t> it_r, it_p, it_n, it_lo, it_hi, cb_r, cb_n, cb_f, cb_c;
     int max_pages = 0;
     for (int r = 0; r < nreq; ++r) {
       const lg_request &q = reqs[r];
@@ -633,6 +634,21 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
         tiles_p.push_back(s.len + i);
         tiles_n.push_back(std::min(32, q.n - i));
       }
+      if (ot)  // attention work of a fresh sequence: 16 query rows x key ranges of <= 256
+        for (int i = 0; i < q.n; i += 16) {
+          const int nq = std::min(16, q.n - i), kend = i + nq;
+          cb_r.push_back(row + i);
+          cb_n.push_back(nq);
+          cb_f.push_back(int32_t(it_r.size()));
+          cb_c.push_back((kend + 255) / 256);
+          for (int k0 = 0; k0 < kend; k0 += 256) {
+            it_r.push_back(row + i);
+            it_p.push_back(i);
+            it_n.push_back(nq);
+            it_lo.push_back(k0);
+            it_hi.push_back(std::min(kend, k0 + 256));
+          }
+        }
       for (int i = 0; i < q.npos; ++i) gather.push_back(row + q.positions[i]);
       b->seqs.push_back(q.seq);
       b->start_len.push_back(s.len);
@@ -646,8 +662,8 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
     b->ngroups = int(grp_f.size());
     b->max_pages = max_pages;
     const size_t nints = ids.size() * 3 + ptab.size() + tiles_s.size() * 4 + grp_f.size() * 2 + gather.size() +
-                         srow0.size() * 2 + 64;
-    b->meta.ensure(nints * 4 + 24 * 256);
+                         srow0.size() * 2 + it_r.size() * 5 + cb_r.size() * 4 + 64;
+    b->meta.ensure(nints * 4 + 34 * 256);
     int32_t *base = b->meta.as<int32_t>();
     size_t off = 0;
     auto put = [&](const std::vector<int32_t> &v, int32_t *&dst) {
@@ -668,6 +684,17 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
     put(gather, b->gather);
     put(srow0, b->seq_row0);
     put(sn, b->seq_n);
+    put(it_r, b->it_row0);
+    put(it_p, b->it_pos0);
+    put(it_n, b->it_nq);
+    put(it_lo, b->it_klo);
+    put(it_hi, b->it_khi);
+    put(cb_r, b->cb_row0);
+    put(cb_n, b->cb_nq);
+    put(cb_f, b->cb_first);
+    put(cb_c, b->cb_n);
+    b->nitems = int(it_r.size());
+    b->ncomb = int(cb_r.size());
     HIP_CHECK(hipStreamSynchronize(stream));
   } catch (...) {
     delete b;

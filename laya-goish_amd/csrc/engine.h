@@ -91,6 +91,10 @@ struct BatchPlan {
   int32_t *grp_first = nullptr, *grp_count = nullptr;
   int32_t *gather = nullptr;
   int32_t *seq_row0 = nullptr, *seq_n = nullptr;  // first batch row and token count per request
+  // OpenThai attention work: items (16 query rows x <= 256 keys) and per-16-row merges
+  int nitems = 0, ncomb = 0;
+  int32_t *it_row0 = nullptr, *it_pos0 = nullptr, *it_nq = nullptr, *it_klo = nullptr, *it_khi = nullptr;
+  int32_t *cb_row0 = nullptr, *cb_nq = nullptr, *cb_first = nullptr, *cb_n = nullptr;
   bool ran = false;
 };
 
@@ -204,6 +208,7 @@ class Engine {
   DevBuf ws_x_, ws_h16_, ws_qkv_, ws_q16_, ws_att16_, ws_act16_, ws_meta_, ws_out_;
   DevBuf ws_dec_;
   DevBuf ws_ot_qk_, ws_ot_v_, ws_ot_gb_, ws_ot_o_;  // OpenThai mixer workspaces
+  DevBuf ws_ot_part_;                               // OpenThai attention partials
 };
 
 }  // namespace lg

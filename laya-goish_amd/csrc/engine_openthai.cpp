@@ -176,7 +176,15 @@ void Engine::run_openthai(BatchPlan &b, lg_cancel_fn cancel, void *arg) {
       launch_ot_attn_prep(proj, ldp_full_, T, hq, hkv, b.tok_pos, y.qn1, y.kn1, cos_, sin_, qk, vb, stream);
       prof.end(double(T) * (qw + kvw) * 8, 0, stream);
       prof.begin("ot_attn", stream);
-      launch_ot_attn(qk, vb, proj, ldp_full_, hq, hkv, b.tile_row0, b.tile_pos0, b.tile_n, b.ntiles, att, attlo, stream);
+      if ((hq / hkv) % 4 == 0) {
+        ws_ot_part_.ensure(size_t(ot_attn_part_floats(b.nitems, hq)) * 4);
+        launch_ot_attn_mfma(qk, vb, proj, ldp_full_, hq, hkv, b.it_row0, b.it_pos0, b.it_nq, b.it_klo, b.it_khi,
+                            b.nitems, b.cb_row0, b.cb_nq, b.cb_first, b.cb_n, b.ncomb, ws_ot_part_.as<float>(), att,
+                            attlo, stream);
+      } else {
+        launch_ot_attn(qk, vb, proj, ldp_full_, hq, hkv, b.tile_row0, b.tile_pos0, b.tile_n, b.ntiles, att, attlo,
+                       stream);
+      }
       prof.end(0, 0, stream);
       gemm(att, attlo, T, y.out, Epi::ADD, x, nullptr, nullptr, d, nullptr);
     } else {

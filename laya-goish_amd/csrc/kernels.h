@@ -177,6 +177,16 @@ void launch_ot_attn_prep(const float *proj, int ldp, int T, int hq, int hkv, con
 void launch_ot_attn(const float *Qb, const float *Kb, const float *proj, int ldp, int hq, int hkv,
                     const int32_t *tile_row0, const int32_t *tile_pos0, const int32_t *tile_n, int ntiles,
                     _Float16 *y, _Float16 *ylo, hipStream_t st);
+// The same attention on f32 MFMA, split over keys: work items (first row, position, rows <= 16,
+// key range [klo, khi) of <= 256 keys) write partials (ot_attn_part_floats(nitems, hq) floats),
+// then each 16-row tile (cb_*: first row, rows, first item, items) is merged into the planes.
+// Needs (hq / hkv) % 4 == 0.
+int64_t ot_attn_part_floats(int nitems, int hq);
+void launch_ot_attn_mfma(const float *Qb, const float *Kb, const float *proj, int ldp, int hq, int hkv,
+                         const int32_t *it_row0, const int32_t *it_pos0, const int32_t *it_nq, const int32_t *it_klo,
+                         const int32_t *it_khi, int nitems, const int32_t *cb_row0, const int32_t *cb_nq,
+                         const int32_t *cb_first, const int32_t *cb_n, int ncomb, float *part, _Float16 *y,
+                         _Float16 *ylo, hipStream_t st);
 
 // Device int32 fill / copy helpers (small, capture-safe).
 void launch_fill_i32(int32_t *p, int n, int32_t v, hipStream_t st);
