@@ -16,6 +16,11 @@ void launch_kind(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix 
   } else if constexpr (KIND == LG_Q8_0) {
     if (launch_gemm_q8_exact(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
   } else if constexpr (KIND == LG_F16) {
+    // fewer 128 x 128 tiles than CUs (short prefills, narrow outputs): 64 x 128 tiles, twice
+    // the workgroups; the per-element K order is the same, so the results are too
+    const int outN = epi == Epi::SWIGLU ? W.rows / 2 : W.rows;
+    const int64_t tiles = int64_t((M + 127) / 128) * (outN / (epi == Epi::SWIGLU ? 64 : 128));
+    if (tiles < 256 && launch_cfg<KIND, SPLIT, 64, 1, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
     if (launch_cfg<KIND, SPLIT, 64, 2, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
   } else {
     if (launch_cfg<KIND, SPLIT3, 64, 2, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;

@@ -7,6 +7,7 @@
 #include "common.h"
 #include "kernels.h"
 #include "quant.h"
+#include "wave.h"
 
 namespace lg {
 namespace {
@@ -240,7 +241,9 @@ __device__ float weight_at_head(const DevMatrix &W, int64_t n, int64_t k) {
   return 0.0f;
 }
 
-// One workgroup per gathered row: final RMSNorm into LDS, then one wave per option id.
+// Workgroup (gathered row, block of 16 head rows): final RMSNorm of the row into LDS, then each
+// wave computes 4 head rows with their loads interleaved, reduced by DPP.  Rows past nv repeat
+// the last id and are not written.
 __global__ __launch_bounds__(kT) void head_rows_kernel(const float *__restrict__ x,
                                                        const int32_t *__restrict__ rows, int d,
                                                        const float *__restrict__ norm_w, float eps,
@@ -256,13 +259,21 @@ __global__ __launch_bounds__(kT) void head_rows_kernel(const float *__restrict__
   for (int k = threadIdx.x; k < d; k += kT) h[k] = row[k] * inv * norm_w[k];
   __syncthreads();
   const int lane = threadIdx.x & 63;
-  for (int j = threadIdx.x >> 6; j < nv; j += kT / 64) {
-    const int64_t n = ids[j];
-    float s = 0.0f;
-    for (int k = lane; k < d; k += 64) s += h[k] * weight_at_head(W, n, k);
-    s = wave_sum(s);
-    if (bias) s = s + bias[n];
-    if (lane == 0) logits[int64_t(blockIdx.x) * nv + j] = s;
+  const int j0 = blockIdx.y * 16 + (threadIdx.x >> 6) * 4;
+  int64_t n[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) n[r] = ids[min(j0 + r, nv - 1)];
+  float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int k = lane; k < d; k += 64) {
+    const float hk = h[k];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[r] += hk * weight_at_head(W, n[r], k);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float v = wave_sum_dpp(s[r]);
+    if (bias) v = v + bias[n[r]];
+    if (lane == 0 && j0 + r < nv) logits[int64_t(blockIdx.x) * nv + j0 + r] = v;
   }
 }
 
@@ -429,7 +440,7 @@ void launch_head_rows(const float *x, const int32_t *rows, int R, int d, const f
                       float *logits, hipStream_t st) {
   LG_REQUIRE(R > 0 && nv > 0 && W.cols == d, "head: bad shape");
   LG_REQUIRE(size_t(d) * 4 <= 64 * 1024, "head: d too large for LDS");
-  hipLaunchKernelGGL(head_rows_kernel, dim3(R), dim3(kT), size_t(d) * 4, st, x, rows, d, norm_w, eps, W,
+  hipLaunchKernelGGL(head_rows_kernel, dim3(R, (nv + 15) / 16), dim3(kT), size_t(d) * 4, st, x, rows, d, norm_w, eps, W,
                      bias, vocab_ids, nv, logits);
   HIP_CHECK(hipGetLastError());
 }
