@@ -263,6 +263,15 @@ int lg_decide(lg_engine *e, const lg_decide_request *req, lg_decide_result *out,
 int lg_decide_encode(const lg_gguf *g, const lg_decide_request *req, int pass, int32_t *ids, int cap,
                      int *n, int32_t *positions, int32_t *order, int *truncated, int *passes);
 
+/* Several decide requests at once: the states of /v1/decide/batch (src/server.rs:235-319, which
+ * runs one decide per state while a global busy flag turns other requests away).  Every request
+ * is validated and every pass encoded before any inference (at most 256 requests and 256
+ * questions in total, as server.rs:238-283); then all passes of all requests run as GPU
+ * batches of at most max_batch_tokens tokens (as few batches as the budget allows) and each
+ * request is aggregated into its own result.  Results equal lg_decide on each request alone. */
+int lg_decide_batch(lg_engine *e, const lg_decide_request *reqs, int n, lg_decide_result *outs,
+                    lg_cancel_fn cancel, void *cancel_arg);
+
 /* The aggregation of lg_decide over slot logits the caller already holds ([passes][n_questions]
  * [256], the 256 slot rows at each answer position of each pass), host only.  Replaces the
  * scoring of src/models/openthai/decision.rs:268-279,297-336. */

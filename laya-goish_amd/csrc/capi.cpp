@@ -345,24 +345,43 @@ int lg_decode(lg_engine *e, int seq, int32_t first, int steps, int32_t *tokens, 
   });
 }
 
-int lg_decide(lg_engine *e, const lg_decide_request *req, lg_decide_result *out, lg_cancel_fn cancel,
-              void *cancel_arg) {
-  return guard([&] {
-    NEED(e, "engine");
-    NEED(req, "request");
-    NEED(out, "result");
-    NEED(out->probs, "result probabilities");
-    lg::Engine &E = *e->e;
-    const lg::DecideSpec &s = E.decide;
-    lg::decide_validate(s, *req);
-    const int n = lg::decide_passes(*req);
-    // every pass is encoded (and so validated) before any inference, as
-    // src/models/openthai/decision.rs:234-241
-    std::vector<lg::Encoded> enc;
-    for (int p = 0; p < n; ++p) enc.push_back(lg::decide_encode(s, *req, n, p));
-    for (const lg::Encoded &x : enc)
+namespace {
+
+// Runs every pass of `reqs` through the engine (GPU batches of at most the engine's batch token
+// budget, passes of one request kept in one batch when they fit) and aggregates each request.
+void decide_many(lg::Engine &E, const lg_decide_request *reqs, int n, lg_decide_result *outs, lg_cancel_fn cancel,
+                 void *cancel_arg) {
+  const lg::DecideSpec &s = E.decide;
+  std::vector<int> passes(n);
+  std::vector<std::vector<lg::Encoded>> enc(n);
+  // validate and encode everything before any inference (src/models/openthai/decision.rs:234-241,
+  // src/server.rs:259-283)
+  for (int r = 0; r < n; ++r) {
+    lg::decide_validate(s, reqs[r]);
+    passes[r] = lg::decide_passes(reqs[r]);
+    for (int p = 0; p < passes[r]; ++p) enc[r].push_back(lg::decide_encode(s, reqs[r], passes[r], p));
+    for (const lg::Encoded &x : enc[r])
       LG_REQUIRE(int64_t(x.ids.size()) <= E.ctx, "prompt of %zu tokens exceeds the model context %d", x.ids.size(), E.ctx);
-    // all passes as one batch of sequences; the sequences are released whatever happens
+  }
+  std::vector<std::vector<float>> logits(n);
+  for (int r = 0; r < n; ++r) logits[r].resize(size_t(passes[r]) * reqs[r].n_questions * 256);
+  // (request, pass) work in order, packed greedily into batches under the token budget
+  struct Item { int r, p; };
+  std::vector<Item> items;
+  for (int r = 0; r < n; ++r)
+    for (int p = 0; p < passes[r]; ++p) items.push_back({r, p});
+  const int64_t budget = E.max_batch_tokens();
+  size_t i0 = 0;
+  while (i0 < items.size()) {
+    size_t i1 = i0;
+    int64_t toks = 0;
+    while (i1 < items.size()) {
+      const int64_t t = int64_t(enc[items[i1].r][items[i1].p].ids.size());
+      if (i1 > i0 && toks + t > budget) break;
+      toks += t;
+      ++i1;
+    }
+    // the sequences and the plan are released whatever happens
     struct Seqs {
       lg::Engine &E;
       std::vector<int> ids;
@@ -375,16 +394,56 @@ int lg_decide(lg_engine *e, const lg_decide_request *req, lg_decide_result *out,
         }
       }
     } held{E, {}};
-    std::vector<lg_request> reqs(n);
-    for (int p = 0; p < n; ++p) {
+    std::vector<lg_request> rq;
+    int rows = 0;
+    for (size_t i = i0; i < i1; ++i) {
+      const lg::Encoded &x = enc[items[i].r][items[i].p];
       held.ids.push_back(E.seq_create());
-      reqs[p] = {held.ids.back(), enc[p].ids.data(), int(enc[p].ids.size()), enc[p].positions.data(),
-                 req->n_questions};
+      rq.push_back({held.ids.back(), x.ids.data(), int(x.ids.size()), x.positions.data(), int(x.positions.size())});
+      rows += int(x.positions.size());
     }
-    held.b = E.batch_create(reqs.data(), n);
-    std::vector<float> logits(size_t(n) * req->n_questions * 256);
-    E.batch_run(held.b, s.head_row, 256, 1.0f, logits.data(), nullptr, nullptr, cancel, cancel_arg);
-    lg::decide_aggregate(s, *req, n, enc, logits.data(), *out);
+    held.b = E.batch_create(rq.data(), int(rq.size()));
+    std::vector<float> out(size_t(rows) * 256);
+    E.batch_run(held.b, s.head_row, 256, 1.0f, out.data(), nullptr, nullptr, cancel, cancel_arg);
+    size_t row = 0;
+    for (size_t i = i0; i < i1; ++i) {
+      const int r = items[i].r, nq = reqs[r].n_questions;
+      std::copy(out.begin() + row * 256, out.begin() + (row + nq) * 256,
+                logits[r].begin() + size_t(items[i].p) * nq * 256);
+      row += nq;
+    }
+    i0 = i1;
+  }
+  for (int r = 0; r < n; ++r) lg::decide_aggregate(s, reqs[r], passes[r], enc[r], logits[r].data(), outs[r]);
+}
+
+}  // namespace
+
+int lg_decide(lg_engine *e, const lg_decide_request *req, lg_decide_result *out, lg_cancel_fn cancel,
+              void *cancel_arg) {
+  return guard([&] {
+    NEED(e, "engine");
+    NEED(req, "request");
+    NEED(out, "result");
+    NEED(out->probs, "result probabilities");
+    decide_many(*e->e, req, 1, out, cancel, cancel_arg);
+  });
+}
+
+int lg_decide_batch(lg_engine *e, const lg_decide_request *reqs, int n, lg_decide_result *outs,
+                    lg_cancel_fn cancel, void *cancel_arg) {
+  return guard([&] {
+    NEED(e, "engine");
+    NEED(reqs, "requests");
+    NEED(outs, "results");
+    LG_REQUIRE(n >= 1 && n <= 256, "states must be an array of 1..256 states");
+    int64_t questions = 0;
+    for (int r = 0; r < n; ++r) {
+      NEED(outs[r].probs, "result probabilities");
+      questions += reqs[r].n_questions;
+    }
+    LG_REQUIRE(questions <= 256, "At most 256 total questions per request");
+    decide_many(*e->e, reqs, n, outs, cancel, cancel_arg);
   });
 }
 

@@ -176,6 +176,7 @@ class Engine {
   int L = 0, d = 0, hq = 0, hkv = 0, hd = 0, f = 0, V = 0, ctx = 0;
   int nh = 0;          // OpenThai: gated DeltaNet heads (128-dim)
   int head_rows() const { return arch == Arch::OpenThai ? 256 : V; }
+  int64_t max_batch_tokens() const { return max_batch_tokens_; }
   float eps = 1e-5f;
   uint32_t emb_kind = 0;
   int precision = LG_PREC_EXACT;

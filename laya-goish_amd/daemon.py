@@ -22,7 +22,11 @@ choice -> probabilities by option, confidence, choice, abstain; score -> probabi
 confidence, score, legend (level -> description ids); noul -> noul (P(yes)); plus usage and the
 echoed id.
 
-  python3 laya-goish_amd/daemon.py MODEL.gguf [--device N] [--precision exact|fast]
+A body with "states": [state, ...] instead of "state" is a /v1/decide/batch request
+(src/server.rs:235-258): one result per state, every pass of every state run as GPU batches.
+
+  python3 laya-goish_amd/daemon.py MODEL.gguf [--model MODEL2.gguf ...] [--default-model NAME]
+                                   [--device N] [--precision exact|fast]
 """
 from __future__ import annotations
 
@@ -122,36 +126,166 @@ def answer_json(model_name, req, labels, res, t0) -> dict:
     return out
 
 
+def states_requests(req) -> tuple[list, list]:
+    """A /v1/decide/batch body (src/server.rs:235-258): one request per state, all sharing the
+    questions and options of the body."""
+    states = req.get("states")
+    if not isinstance(states, list) or not 1 <= len(states) <= 256:
+        raise RequestError("states must be an array of 1..256 states")
+    out, labels = [], None
+    for st in states:
+        one = {k: req.get(k) for k in ("questions", "permutations", "order_invariant")}
+        one["state"] = st
+        t, labels = to_tokens_request(one)
+        out.append(t)
+    if sum(len(t["questions"]) for t in out) > 256:
+        raise RequestError("At most 256 total questions per request")
+    return out, labels
+
+
+def handle(engine, model_name, req, t0) -> dict:
+    """One parsed body -> its answer (a single request, or a "states" batch run as GPU batches)."""
+    if not isinstance(req, dict):
+        raise RequestError("request body must be a JSON object")
+    if "states" in req:
+        treqs, labels = states_requests(req)
+        res = engine.decide_batch(treqs)
+        out = {"model": model_name, "results": [answer_json(model_name, {}, labels, r, t0) for r in res]}
+        if req.get("id") is not None:
+            out["id"] = req["id"]
+        return out
+    treq, labels = to_tokens_request(req)
+    return answer_json(model_name, req, labels, engine.decide(treq), t0)
+
+
+class RegistryError(Exception):
+    pass
+
+
+class Registry:
+    """Loaded models by name (src/registry.rs:10-74): every file is opened and every name checked
+    before any weights load; one engine (one HIP stream) per model; requests pick a model with
+    "model" or get the default."""
+
+    def __init__(self, paths, default=None, open_engine=None):
+        if not paths:
+            raise RegistryError("at least one model is required")
+        self.names, ggufs = {}, []
+        for i, path in enumerate(paths):
+            g = lh.Gguf.open(path)
+            name = g.str("general.name", "") or os.path.basename(path)
+            if name in self.names:
+                raise RegistryError(f"duplicate model name or alias {name}; load one checkpoint per model")
+            self.names[name] = i
+            ggufs.append(g)
+        if default is not None and default not in self.names:
+            raise RegistryError(f"unknown default model {default}")
+        self.default = self.names[default] if default is not None else 0
+        self.model_names = list(self.names)
+        self.engines = [open_engine(g) for g in ggufs]
+
+    def select(self, req) -> int:
+        if not isinstance(req, dict):
+            raise RequestError("request body must be a JSON object")
+        m = req.get("model")
+        if m is None:
+            return self.default
+        if not isinstance(m, str):
+            raise RequestError("model must be a string naming a loaded model")
+        if m not in self.names:
+            raise RequestError(f"unknown model {m}; see /v1/models")
+        return self.names[m]
+
+    def close(self):
+        for e in self.engines:
+            e.close()
+
+
 def serve(engine, model_name, fin, fout) -> None:
+    """One model, requests answered in order."""
     for line in fin:
         if not line.strip():
             continue
         t0 = time.perf_counter()
         try:
-            req = json.loads(line)
-            treq, labels = to_tokens_request(req)
-            res = engine.decide(treq)
-            out = answer_json(model_name, req, labels, res, t0)
+            out = handle(engine, model_name, json.loads(line), t0)
         except (ValueError, RequestError, lh.LayaError) as e:
             out = {"error": str(e)}
         fout.write(json.dumps(out) + "\n")
         fout.flush()
 
 
+def serve_registry(reg: Registry, fin, fout) -> None:
+    """Several models: one worker thread and FIFO queue per model (in place of the reference's
+    global busy flag, src/server.rs:283-297), so models run concurrently on their own streams
+    while each model answers its requests in arrival order.  Lines for different models may be
+    answered out of input order; "id" is echoed to match them."""
+    import queue
+    import threading
+
+    lock = threading.Lock()
+
+    def write(obj):
+        with lock:
+            fout.write(json.dumps(obj) + "\n")
+            fout.flush()
+
+    queues = [queue.Queue() for _ in reg.engines]
+
+    def worker(i):
+        while True:
+            item = queues[i].get()
+            if item is None:
+                return
+            req, t0 = item
+            try:
+                write(handle(reg.engines[i], reg.model_names[i], req, t0))
+            except (ValueError, RequestError, lh.LayaError) as e:
+                write({"error": str(e)} if not isinstance(req, dict) or req.get("id") is None
+                      else {"error": str(e), "id": req["id"]})
+
+    threads = [threading.Thread(target=worker, args=(i,), daemon=True) for i in range(len(queues))]
+    for t in threads:
+        t.start()
+    for line in fin:
+        if not line.strip():
+            continue
+        t0 = time.perf_counter()
+        try:
+            req = json.loads(line)
+            queues[reg.select(req)].put((req, t0))
+        except (ValueError, RequestError) as e:
+            write({"error": str(e)})
+    for q in queues:
+        q.put(None)
+    for t in threads:
+        t.join()
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description="JSON-lines decide daemon (token-level requests)")
-    ap.add_argument("model", help="laya-decoder GGUF file")
+    ap.add_argument("model", help="model GGUF file (laya-decoder or OpenThai-SystemOne)")
+    ap.add_argument("--model", dest="more", action="append", default=[], metavar="GGUF",
+                    help="another model to serve (requests select one with \"model\": NAME)")
+    ap.add_argument("--default-model", default=None, metavar="NAME")
     ap.add_argument("--device", type=int, default=0)
     ap.add_argument("--precision", choices=["exact", "fast"], default="exact")
     ap.add_argument("--kv-tokens", type=int, default=65536)
     args = ap.parse_args()
-    g = lh.Gguf.open(args.model)
-    eng = lh.Engine(g, device=args.device, kv_tokens=args.kv_tokens,
-                    precision=lh.PREC_EXACT if args.precision == "exact" else lh.PREC_FAST)
-    name = g.str("general.name", "laya-decoder") or "laya-decoder"
-    print(f"loaded {args.model} ({eng.layers()} layers, device {args.device})", file=sys.stderr, flush=True)
-    serve(eng, name, sys.stdin, sys.stdout)
-    eng.close()
+    prec = lh.PREC_EXACT if args.precision == "exact" else lh.PREC_FAST
+    opener = lambda g: lh.Engine(g, device=args.device, kv_tokens=args.kv_tokens, precision=prec)  # noqa: E731
+    try:
+        reg = Registry([args.model] + args.more, args.default_model, opener)
+    except (RegistryError, lh.LayaError) as e:
+        print(f"error: {e}", file=sys.stderr, flush=True)
+        return 1
+    for name, e in zip(reg.model_names, reg.engines):
+        print(f"loaded {name} ({e.layers()} layers, device {args.device})", file=sys.stderr, flush=True)
+    if len(reg.engines) == 1:
+        serve(reg.engines[0], reg.model_names[0], sys.stdin, sys.stdout)
+    else:
+        serve_registry(reg, sys.stdin, sys.stdout)
+    reg.close()
     return 0
 
 

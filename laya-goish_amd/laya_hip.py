@@ -230,6 +230,7 @@ def lib() -> ctypes.CDLL:
             "lg_decode": (I, [P, I, ctypes.c_int32, I, P, P]),
             "lg_option_scores": (I, [P, I, F, P, P]),
             "lg_decide": (I, [P, ctypes.POINTER(DecideRequest), ctypes.POINTER(DecideResult), CANCEL_FN, P]),
+            "lg_decide_batch": (I, [P, ctypes.POINTER(DecideRequest), I, ctypes.POINTER(DecideResult), CANCEL_FN, P]),
             "lg_decide_encode": (I, [P, ctypes.POINTER(DecideRequest), I, P, I, ctypes.POINTER(I), P, P,
                                      ctypes.POINTER(I), ctypes.POINTER(I)]),
             "lg_decide_scores": (I, [P, ctypes.POINTER(DecideRequest), P, ctypes.POINTER(DecideResult)]),
@@ -511,6 +512,21 @@ class Engine:
         cb = CANCEL_FN(cancel) if cancel else CANCEL_FN(0)
         check(lib().lg_decide(self.h, ctypes.byref(a.req), ctypes.byref(res), cb, None))
         return a.answers()
+
+    def decide_batch(self, reqs: list, cancel=None) -> list:
+        """Several requests at once (the states of /v1/decide/batch, src/server.rs:235-319): all
+        validated and encoded first, every pass of every request run as GPU batches, one answer
+        per request."""
+        args = [DecideArgs(r) for r in reqs]
+        arr = (DecideRequest * max(1, len(args)))(*[a.req for a in args])
+        outs = (DecideResult * max(1, len(args)))(*[a.result() for a in args])
+        cb = CANCEL_FN(cancel) if cancel else CANCEL_FN(0)
+        check(lib().lg_decide_batch(self.h, arr, len(args), outs, cb, None))
+        res = []
+        for a, o in zip(args, outs):
+            a.res = o
+            res.append(a.answers())
+        return res
 
     def decode(self, seq: int, first: int, steps: int, want_logits: bool = False):
         toks = np.empty(steps, dtype=np.int32)

@@ -26,6 +26,15 @@ class HostScoredEngine:
         logits = self.rng.normal(size=(n, len(treq["questions"]), 256)).astype(np.float32)
         return self.lh.decide_scores(self.g, treq, logits)
 
+    def decide_batch(self, treqs):
+        return [self.decide(t) for t in treqs]
+
+    def layers(self):
+        return 2
+
+    def close(self):
+        pass
+
 
 @pytest.fixture(scope="module")
 def gguf(lh):
@@ -80,3 +89,68 @@ def test_daemon_request_validation():
     for req, msg in bad:
         with pytest.raises(daemon.RequestError, match=msg):
             daemon.to_tokens_request(req)
+
+
+def test_daemon_states_batch(lh, gguf):
+    """A /v1/decide/batch body (src/server.rs:235-283): one result per state, limits checked first."""
+    eng = HostScoredEngine(lh, gguf, seed=1)
+    body = {k: v for k, v in REQ.items() if k != "state"}
+    body["states"] = [[5, 6], [7, 8, 9], []]
+    outs = run([json.dumps(body), json.dumps(dict(body, states=[])),
+                json.dumps(dict(body, states=[[1]] * 86))], eng)
+    assert len(outs) == 3 and outs[0]["id"] == "r1" and len(outs[0]["results"]) == 3
+    for r in outs[0]["results"]:
+        assert set(r["answers"]) == {"topic", "urgency", "human"} and r["usage"]["permutations"] == 3
+    assert "states must be an array of 1..256 states" in outs[1]["error"]
+    assert "At most 256 total questions per request" in outs[2]["error"]
+
+
+def _two_models(lh, tmp_path):
+    a, b = str(tmp_path / "a.gguf"), str(tmp_path / "b.gguf")
+    lh.synth_file("tiny-q8", 3, a)
+    lh.synth_file("tiny-f16", 3, b)
+    return a, b
+
+
+def test_registry_preflight_and_selection(lh, tmp_path):
+    a, b = _two_models(lh, tmp_path)
+    opened = []
+
+    def opener(g):
+        opened.append(g)
+        return HostScoredEngine(lh, g)
+    with pytest.raises(daemon.RegistryError, match="duplicate model name or alias"):
+        daemon.Registry([a, a], None, opener)
+    with pytest.raises(daemon.RegistryError, match="unknown default model nope"):
+        daemon.Registry([a, b], "nope", opener)
+    assert not opened  # nothing was loaded for a rejected registry
+    reg = daemon.Registry([a, b], "laya-decoder synthetic tiny-f16", opener)
+    assert reg.model_names == ["laya-decoder synthetic tiny-q8", "laya-decoder synthetic tiny-f16"]
+    assert reg.select({}) == 1 and reg.select({"model": "laya-decoder synthetic tiny-q8"}) == 0
+    with pytest.raises(daemon.RequestError, match="unknown model x; see /v1/models"):
+        reg.select({"model": "x"})
+    with pytest.raises(daemon.RequestError, match="model must be a string"):
+        reg.select({"model": 3})
+
+
+def test_serve_registry_routes_per_model(lh, tmp_path):
+    """Per-model queues: each model answers its own requests in order; every line gets one answer."""
+    a, b = _two_models(lh, tmp_path)
+    reg = daemon.Registry([a, b], None, lambda g: HostScoredEngine(lh, g))
+    lines = []
+    for i in range(6):
+        r = dict(REQ, id=i)
+        if i % 2:
+            r["model"] = "laya-decoder synthetic tiny-f16"
+        lines.append(json.dumps(r))
+    lines.append(json.dumps(dict(REQ, id=99, model="missing")))
+    out = io.StringIO()
+    daemon.serve_registry(reg, io.StringIO("".join(l + "\n" for l in lines)), out)
+    outs = [json.loads(l) for l in out.getvalue().splitlines()]
+    assert len(outs) == 7
+    answered = [o for o in outs if "answers" in o]
+    assert sorted(o["id"] for o in answered) == list(range(6))
+    for m in ("laya-decoder synthetic tiny-q8", "laya-decoder synthetic tiny-f16"):
+        ids = [o["id"] for o in answered if o["model"] == m]
+        assert ids == sorted(ids)  # in order within one model
+    assert any("unknown model missing" in o.get("error", "") for o in outs)

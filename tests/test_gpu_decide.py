@@ -144,3 +144,23 @@ def test_daemon_process_matches_engine(lh, tmp_path):
         else:
             assert [got[qid]["probabilities"][n] for n in names] == [float(x) for x in a["probabilities"]]
             assert got[qid]["choice"] == names[a["choice"]]
+
+
+def test_decide_batch_equals_single_requests(setup, lh):
+    """lg_decide_batch (the states of /v1/decide/batch, src/server.rs:235-319) gives every request
+    the same bits as lg_decide on it alone, and rejects a batch before running any of it."""
+    preset, eng, om, og = setup
+    reqs = [_request(np.random.default_rng(30 + i), om.V, i % 3 + 1) for i in range(4)]
+    got = eng.decide_batch(reqs)
+    for r, g in zip(reqs, got):
+        want = eng.decide(r)
+        assert g["usage"] == want["usage"]
+        for a, b in zip(g["answers"], want["answers"]):
+            assert np.array_equal(a["probabilities"], b["probabilities"]) and a["choice"] == b["choice"]
+    bad = dict(reqs[0], permutations=40)
+    with pytest.raises(lh.LayaError, match="permutations must be 1..32"):
+        eng.decide_batch([reqs[1], bad])
+    with pytest.raises(lh.LayaError, match="At most 256 total questions"):
+        eng.decide_batch([reqs[0]] * 86)
+    with pytest.raises(lh.LayaError, match="1..256 states"):
+        eng.decide_batch([])

@@ -138,3 +138,61 @@ def test_full_width_layers_match_oracle(lh, po):
     want = om.forward(ids, pos)
     err = float(np.abs(got - want).max())
     assert err <= 2e-3, f"slot logits differ by {err:.3e}"
+
+
+def test_decide_batch_equals_single_requests(tiny):
+    prec, eng, om, og = tiny
+    reqs = [_request(np.random.default_rng(50 + i), [1, 2, 4][i % 3]) for i in range(5)]
+    got = eng.decide_batch(reqs)
+    for r, g in zip(reqs, got):
+        want = eng.decide(r)
+        assert g["usage"] == want["usage"]
+        for a, b in zip(g["answers"], want["answers"]):
+            assert np.array_equal(a["probabilities"], b["probabilities"]) and a["choice"] == b["choice"]
+
+
+def test_daemon_serves_two_models(lh, tmp_path):
+    """The daemon with an OpenThai model and a laya-decoder model loaded side by side, one engine
+    (one stream) each: requests routed by "model", answers equal in-process lg_decide, and a
+    "states" body answered per state."""
+    import json
+    import os
+    import subprocess
+    import sys
+
+    ot, dec = str(tmp_path / "ot.gguf"), str(tmp_path / "dec.gguf")
+    lh.synth_file("openthai-tiny", 21, ot)
+    lh.synth_file("tiny-q8", 11, dec)
+    q = {"pick": {"type": "choice", "instructions": [1, 2, 3],
+                  "criteria": {f"o{i}": {"name": [30 + i], "desc": [40 + i]} for i in range(4)}},
+         "flag": {"type": "noul", "instructions": [4], "criteria": {"false": [5], "true": [6]}}}
+    lines = [{"id": 1, "state": list(range(20, 90)), "questions": q, "permutations": 2},
+             {"id": 2, "model": "laya-decoder synthetic tiny-q8", "state": list(range(20, 60)), "questions": q},
+             {"id": 3, "states": [list(range(5, 40)), list(range(50, 70))], "questions": q}]
+    script = os.path.join(os.path.dirname(lh.__file__), "daemon.py")
+    print("daemon: two models", flush=True)
+    proc = subprocess.run([sys.executable, script, ot, "--model", dec, "--kv-tokens", "8192"],
+                          input="".join(json.dumps(l) + "\n" for l in lines), capture_output=True, text=True, timeout=240)
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    outs = {o["id"]: o for o in map(json.loads, proc.stdout.splitlines())}
+    assert set(outs) == {1, 2, 3} and outs[2]["model"] == "laya-decoder synthetic tiny-q8"
+    sys.path.insert(0, os.path.dirname(script))
+    import daemon
+    for path, ids in ((ot, [1, 3]), (dec, [2])):
+        eng = lh.Engine(lh.Gguf.open(path), kv_tokens=8192)
+        for i in ids:
+            body = lines[i - 1]
+            if "states" in body:
+                treqs, labels = daemon.states_requests(body)
+                wants = eng.decide_batch(treqs)
+                gots = outs[i]["results"]
+            else:
+                treq, labels = daemon.to_tokens_request(body)
+                wants, gots = [eng.decide(treq)], [outs[i]]
+            for got, want in zip(gots, wants):
+                for (qid, kind, names, _), a in zip(labels, want["answers"]):
+                    if kind == "noul":
+                        assert got["answers"][qid]["noul"] == float(a["probabilities"][1])
+                    else:
+                        assert [got["answers"][qid]["probabilities"][n] for n in names] == [float(x) for x in a["probabilities"]]
+        eng.close()
