@@ -309,6 +309,60 @@ def bench_decide_request(args, prec):
     return line
 
 
+def decide_batch_body(vocab, seed, states=REQUESTS, state_len=PROMPT):
+    """A token-level /v1/decide/batch body (src/server.rs:235-258): `states` states of `state_len`
+    ids sharing three 4-option choice questions (the headline workload's shape, through the
+    request-level decide path)."""
+    rng = np.random.default_rng(seed)
+
+    def toks(n):
+        return rng.integers(0, vocab - 300, n).tolist()
+    qs = [{"type": "choice", "instruction": toks(4), "options": [{"name": toks(1), "desc": toks(2)} for _ in range(4)]}
+          for _ in range(QUESTIONS)]
+    return [{"state": toks(state_len), "questions": qs} for _ in range(states)]
+
+
+def bench_decide_batch(args, prec):
+    """lg_decide_batch on the Q8_0 d2048 model: 64 states x 512 ids with three 4-option questions
+    (one pass each by the default rule), every state's prompt prefilled in one GPU batch, 256 slot
+    rows scored per answer position, one answer per state."""
+    img = lh.SynthImage(PRESET, seed=SEED)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=65536, precision=prec)
+    reqs = decide_batch_body(eng.info["vocab"], SEED + 9)
+    out = None
+    for _ in range(max(args.warmup, 1)):
+        out = eng.decide_batch(reqs)
+    eng.sync()
+    steps = max(args.steps, 3)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = eng.decide_batch(reqs)
+    dt = (time.perf_counter() - t0) / steps
+    eng.close()
+    toks = sum(o["usage"]["input_tokens"] * o["usage"]["permutations"] for o in out)
+    log(f"decide batch: {dt * 1e3:.1f} ms per body of {len(reqs)} states ({toks} tokens)")
+    line = base_line("decide req/s through lg_decide_batch (Q8_0 d2048, /v1/decide/batch of 64 states)",
+                     round(len(reqs) / dt, 1), "req/s", True, steps, max(args.warmup, 1), dt * 1e3, prec,
+                     f"24 layers, d_model 2048, 16 x 128, FFN 5632, vocab 32000, Q8_0; {len(reqs)} states x {PROMPT} ids, "
+                     f"{QUESTIONS} choice questions of {OPTIONS} options, 1 pass each, one lg_decide_batch call",
+                     tokens_per_body=toks, prefill_tok_per_s=round(toks / dt, 1))
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import pydecide
+        import pyoracle as po
+        layers = 2
+        small = lh.SynthImage(PRESET, seed=SEED, n_layers=layers)
+        og = po.Gguf(small.array())
+        om = po.Model(og, threads=args.cpu_threads)
+        t0 = time.perf_counter()
+        pydecide.decide(om, og, reqs[0])
+        cdt = (time.perf_counter() - t0) * 24 / layers
+        line["cpu_baseline"] = {"value": round(1 / cdt, 4), "unit": "req/s", "cores": args.cpu_threads, "kind": "port",
+                                "sample": f"1 of the {len(reqs)} states through {layers} of 24 layers, time scaled "
+                                          f"x{24 // layers}: {cdt:.1f} s per state (the reference runs states one after another)"}
+    return line
+
+
 OT_PRESET = "openthai-0.8b"
 
 
@@ -435,7 +489,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--precision", choices=["exact", "fast"], default="exact")
     ap.add_argument("--workload", choices=["decide", "plumbing", "q4k-prefill", "long-context", "decide-request",
-                                           "openthai-decide"],
+                                           "decide-batch", "openthai-decide"],
                     default="decide",
                     help="decide (default): the Q8_0 d2048 batched decide headline plus batch-1 decode; the "
                          "others measure the remaining workload shapes, one JSON line each")
@@ -457,7 +511,8 @@ def main():
     prec = lh.PREC_EXACT if args.precision == "exact" else lh.PREC_FAST
     if args.workload != "decide":
         fn = {"plumbing": bench_plumbing, "q4k-prefill": bench_q4k, "long-context": bench_long_context,
-              "decide-request": bench_decide_request, "openthai-decide": bench_openthai}
+              "decide-request": bench_decide_request, "decide-batch": bench_decide_batch,
+              "openthai-decide": bench_openthai}
         print(json.dumps(fn[args.workload](args, prec)), flush=True)
         return
     if args.copy_calibration > 0:
