@@ -239,7 +239,8 @@ void fill_tensor(const Spec &s, uint64_t seed, uint64_t tidx, uint8_t *dst, uint
       for (uint64_t e = lo; e < hi; ++e) {
         const uint64_t pos = e / hd;
         const int j = int(e % hd) % half;
-        const double ang = double(pos) * std::pow(p.theta, -2.0 * j / hd);
+        const double theta = s.sigma > 0 ? s.sigma : p.theta;  // per-table base when the spec carries one
+        const double ang = double(pos) * std::pow(theta, -2.0 * j / hd);
         const float v = float(s.fill == Fill::Cos ? std::cos(ang) : std::sin(ang));
         std::memcpy(dst + 4 * e, &v, 4);
       }
@@ -428,10 +429,161 @@ void synth_openthai(OtPreset p, uint64_t seed, int n_layers, uint8_t **out, uint
   emit_image(specs, w, 10, seed, none, out, out_len);
 }
 
+// ---- Laya (ModernBERT encoder + 2-layer decision head) ----
+// Tensor names, metadata and the compiled-graph description (ggmlc.graph_spec) as the reference
+// loader reads them (src/models/laya/model.rs:60-291): linears are graph nodes of opcode 29
+// (inputs weight, x[, bias]) and opcode 200 (bias add on a linear's output), layer norms nodes of
+// opcode 201 named layer_norm, layer_norm_1, ... (inputs x[, weight[, bias]], attribute eps),
+// attentions nodes of opcode 74 whose last input is the mask (the global layers share the first
+// attention's mask).  Every third trunk layer is global (0, 3, 6, ...), the rest use the local
+// window.
+struct LayaPreset {
+  const char *name;
+  int L, d, hd, f, V, max_len, head_f, act_f;
+};
+
+const LayaPreset kLayaPresets[] = {
+    // ModernBERT-base shape: 22 layers, d 768, 12 heads x 64, GeGLU 1152, vocab 50368.
+    {"laya-english", 22, 768, 64, 1152, 50368, 512, 768, 256},
+    // Small test shape: 4 layers (0 and 3 global), d 128, 2 heads x 64.
+    {"laya-tiny", 4, 128, 64, 192, 1024, 512, 128, 64},
+};
+
+const LayaPreset *find_laya_preset(const char *name) {
+  for (const auto &p : kLayaPresets)
+    if (!std::strcmp(p.name, name)) return &p;
+  return nullptr;
+}
+
+void synth_laya(LayaPreset p, uint64_t seed, int n_layers, uint8_t **out, uint64_t *out_len) {
+  if (n_layers > 0) p.L = n_layers;
+  const uint64_t d = p.d, f = p.f;
+  std::vector<Spec> specs;
+  auto add = [&](const std::string &n, std::vector<uint64_t> dims, uint32_t kind, Fill fill, double sigma) {
+    specs.push_back(Spec{n, std::move(dims), kind, fill, sigma});
+  };
+  // graph description
+  std::string tensors, nodes;
+  int next_id = 0;
+  auto tid = [&](const std::string &name) {
+    const int id = next_id++;
+    tensors += (tensors.empty() ? "" : ",") + std::string("\"") + std::to_string(id) + "\":{\"name\":\"" + name + "\"}";
+    return id;
+  };
+  auto node = [&](const std::string &body) { nodes += (nodes.empty() ? "" : ",") + body; };
+  int x = tid("input");
+  int norm_index = 0;
+  auto layer_norm = [&](bool weight, bool bias) {
+    const std::string nm = norm_index == 0 ? "layer_norm" : "layer_norm_" + std::to_string(norm_index);
+    std::string ins = std::to_string(x);
+    if (weight) {
+      add("ln." + std::to_string(norm_index) + ".weight", {d}, LG_F32, Fill::NearOne, 0);
+      ins += "," + std::to_string(tid("ln." + std::to_string(norm_index) + ".weight"));
+    }
+    if (bias) {
+      add("ln." + std::to_string(norm_index) + ".bias", {d}, LG_F32, Fill::Normal, 0.05);
+      ins += "," + std::to_string(tid("ln." + std::to_string(norm_index) + ".bias"));
+    }
+    const int y = tid(nm + ".out");
+    node("{\"opcode\":201,\"name\":\"" + nm + "\",\"inputs\":[" + ins + "],\"outputs\":[" + std::to_string(y) +
+         "],\"attributes\":{\"eps\":1e-05}}");
+    ++norm_index;
+    x = y;
+  };
+  // bias_mode: 0 none, 1 as the linear's third input, 2 as a separate add node
+  auto linear = [&](const std::string &key, uint64_t cols, uint64_t rows, int bias_mode, double sigma) {
+    add(key + ".weight", rows == 1 ? std::vector<uint64_t>{cols} : std::vector<uint64_t>{cols, rows}, LG_F16,
+        Fill::Normal, sigma);
+    std::string ins = std::to_string(tid(key + ".weight")) + "," + std::to_string(x);
+    if (bias_mode == 1) {
+      add(key + ".bias", {rows}, LG_F32, Fill::Normal, 0.05);
+      ins += "," + std::to_string(tid(key + ".bias"));
+    }
+    const int y = tid(key + ".out");
+    node("{\"opcode\":29,\"name\":\"" + key + "\",\"inputs\":[" + ins + "],\"outputs\":[" + std::to_string(y) + "]}");
+    if (bias_mode == 2) {
+      add(key + ".bias_add", {rows}, LG_F32, Fill::Normal, 0.05);
+      const int y2 = tid(key + ".biased");
+      node("{\"opcode\":200,\"inputs\":[" + std::to_string(y) + "," + std::to_string(tid(key + ".bias_add")) +
+           "],\"outputs\":[" + std::to_string(y2) + "]}");
+      x = y2;
+    } else {
+      x = y;
+    }
+  };
+  const int mask_full = tid("mask_full"), mask_local = tid("mask_local");
+  auto attention = [&](bool full) {
+    const int y = tid("attn.out");
+    node("{\"opcode\":74,\"inputs\":[" + std::to_string(x) + "," + std::to_string(full ? mask_full : mask_local) +
+         "],\"outputs\":[" + std::to_string(y) + "]}");
+    x = y;
+  };
+  add("tok_emb.weight", {d, uint64_t(p.V)}, LG_F16, Fill::Normal, 0.5);
+  layer_norm(true, false);  // embedding norm
+  for (int l = 0; l < p.L; ++l) {
+    const std::string i = std::to_string(l);
+    if (l > 0) layer_norm(true, false);
+    linear("qkv." + i, d, 3 * d, l == 1 ? 1 : 0, 0.03);
+    attention(l % 3 == 0);
+    linear("wo." + i, d, d, l == 2 ? 2 : 0, 0.03);
+    layer_norm(true, false);
+    linear("mlp_wi." + i, d, 2 * f, 0, 0.03);
+    linear("mlp_wo." + i, f, d, 0, 0.03);
+  }
+  layer_norm(true, false);  // final norm
+  add("type_emb.weight", {d, 3}, LG_F32, Fill::Normal, 0.1);
+  for (int h = 0; h < 2; ++h) {
+    const std::string i = std::to_string(h);
+    layer_norm(true, true);
+    linear("head_qkv." + i, d, 3 * d, 1, 0.03);
+    attention(true);
+    linear("head_wo." + i, d, d, 1, 0.03);
+    layer_norm(true, true);
+    linear("head_fc1." + i, d, uint64_t(p.head_f), 1, 0.05);
+    linear("head_fc2." + i, uint64_t(p.head_f), d, 1, 0.03);
+  }
+  layer_norm(true, true);  // scorer norm
+  linear("scorer_fc1", d, d, 1, 0.05);
+  linear("scorer_fc2", d, 1, 1, 0.05);
+  linear("act_fc1", d + 4, uint64_t(p.act_f), 1, 0.05);
+  linear("act_fc2", uint64_t(p.act_f), 2, 1, 0.05);
+  // RoPE tables [max_len][hd]: rotate-half frequencies, theta 160000 (global) and 10000 (local)
+  add("cos_full", {uint64_t(p.hd), uint64_t(p.max_len)}, LG_F32, Fill::Cos, 160000.0);
+  add("sin_full", {uint64_t(p.hd), uint64_t(p.max_len)}, LG_F32, Fill::Sin, 160000.0);
+  add("cos_slide", {uint64_t(p.hd), uint64_t(p.max_len)}, LG_F32, Fill::Cos, 10000.0);
+  add("sin_slide", {uint64_t(p.hd), uint64_t(p.max_len)}, LG_F32, Fill::Sin, 10000.0);
+  const std::string graph = "{\"tensors\":{" + tensors + "},\"nodes\":[" + nodes + "]}";
+
+  Writer w;
+  w.kv_str("general.architecture", "ggmlc");
+  w.kv_str("general.name", std::string("Laya synthetic ") + p.name);
+  w.kv_u32("general.alignment", 32);
+  w.kv_str("laya.model_name", "laya");
+  w.kv_str("laya.checkpoint", std::string("laya-synthetic-") + p.name);
+  w.kv_u32("laya.max_opts", 16);
+  w.kv_u32("laya.max_len", uint32_t(p.max_len));
+  w.kv_u32("laya.head_max_len", 192);
+  w.kv_u32("laya.cls_token_id", uint32_t(p.V - 3));
+  w.kv_u32("laya.sep_token_id", uint32_t(p.V - 2));
+  w.kv_u32("laya.mask_token_id", uint32_t(p.V - 1));
+  w.kv_str("laya.temperature", "[1.25,0.9,1.1]");
+  w.kv_str("laya.temperature_by_options", "{\"choice:2\":1.05,\"choice:3-5\":1.2}");
+  w.kv_str("ggmlc.graph_spec", graph);
+  w.kv_u64("laya.synthetic.seed", seed);
+  w.kv_str("laya.synthetic.preset", p.name);
+  Preset rope{};
+  rope.hd = p.hd;
+  emit_image(specs, w, 16, seed, rope, out, out_len);
+}
+
 }  // namespace
 
 // Builds the image; caller frees with free().
 void synth_image(const char *preset, uint64_t seed, int n_layers, uint8_t **out, uint64_t *out_len) {
+  if (const LayaPreset *lp = find_laya_preset(preset)) {
+    synth_laya(*lp, seed, n_layers, out, out_len);
+    return;
+  }
   if (const OtPreset *op = find_ot_preset(preset)) {
     synth_openthai(*op, seed, n_layers, out, out_len);
     return;

@@ -112,6 +112,32 @@ void or_ot_rope(float *buf, int s, int heads);
 void or_ot_attention(const float *q, const float *k, const float *v, int s, int hq, int hkv, int threads,
                      float *out);
 
+/* ---- Laya encoder (laya.c), src/models/laya/model.rs + src/tensor.rs:103-195 ---- */
+typedef struct { const float *w, *b; float eps; } or_ln;             /* w/b NULL = absent */
+typedef struct { const float *w, *b; int rows, cols; } or_lin;       /* w [rows][cols]; b NULL = none */
+typedef struct { or_ln n1, n2; or_lin qkv, wo, wi, down; int has_n1, full; } or_laya_layer;
+typedef struct {
+  int layers, d, hd, vocab, max_len, threads;
+  const float *emb;                              /* [vocab][d] */
+  or_ln embnorm, finalnorm, scorenorm;
+  const or_laya_layer *trunk;                    /* [layers] */
+  const or_laya_layer *head;                     /* [2] */
+  const float *type_emb;                         /* [3][d] */
+  or_lin score1, score2, act1, act2;
+  const float *cos_full, *sin_full, *cos_slide, *sin_slide; /* [max_len][hd] */
+} or_laya;
+/* src/tensor.rs:103-122 */
+void or_layer_norm(const float *x, int rows, int d, const float *w, const float *b, float eps, float *y);
+/* src/tensor.rs:129-131 */
+float or_gelu(float x);
+/* src/tensor.rs:141-192 over q|k|v rows [s][3d]; cos == NULL: no RoPE; window < 0: all keys */
+void or_laya_attention(const float *qkv, int s, int d, int hd, const float *cs, const float *sn, int window,
+                       float *out);
+/* src/models/laya/model.rs:301-416: option logits [k] and act logits [2]; -1 invalid shape,
+ * -2 token out of range, -3 non-finite output. */
+int or_laya_forward(const or_laya *m, const int32_t *ids, int s, const int32_t *markers, int k, int qtype,
+                    float *logits, float *act);
+
 #ifdef __cplusplus
 }
 #endif

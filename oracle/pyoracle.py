@@ -62,6 +62,10 @@ def lib() -> ctypes.CDLL:
             "or_ot_gated_delta": (None, [P, P, P, P, P, I, I, I, P]),
             "or_ot_rope": (None, [P, I, I]),
             "or_ot_attention": (None, [P, P, P, I, I, I, I, P]),
+            "or_layer_norm": (None, [P, I, I, P, P, F, P]),
+            "or_gelu": (F, [F]),
+            "or_laya_attention": (None, [P, I, I, I, P, P, I, P]),
+            "or_laya_forward": (I, [P, P, I, P, I, I, P, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -331,4 +335,172 @@ def ot_attention(q, k, v, threads=1) -> np.ndarray:
     s, hq, hkv = q.shape[0], q.shape[1] // 256, k.shape[1] // 256
     out = np.empty_like(q)
     lib().or_ot_attention(_p(q), _p(k), _p(v), s, hq, hkv, threads, _p(out))
+    return out
+
+
+# ---- Laya encoder (laya.c) ----
+
+class _Ln(ctypes.Structure):
+    _fields_ = [("w", ctypes.c_void_p), ("b", ctypes.c_void_p), ("eps", ctypes.c_float)]
+
+
+class _Lin(ctypes.Structure):
+    _fields_ = [("w", ctypes.c_void_p), ("b", ctypes.c_void_p), ("rows", ctypes.c_int), ("cols", ctypes.c_int)]
+
+
+class _LayaLayer(ctypes.Structure):
+    _fields_ = [("n1", _Ln), ("n2", _Ln), ("qkv", _Lin), ("wo", _Lin), ("wi", _Lin), ("down", _Lin),
+                ("has_n1", ctypes.c_int), ("full", ctypes.c_int)]
+
+
+class _Laya(ctypes.Structure):
+    _fields_ = [("layers", ctypes.c_int), ("d", ctypes.c_int), ("hd", ctypes.c_int), ("vocab", ctypes.c_int),
+                ("max_len", ctypes.c_int), ("threads", ctypes.c_int), ("emb", ctypes.c_void_p),
+                ("embnorm", _Ln), ("finalnorm", _Ln), ("scorenorm", _Ln),
+                ("trunk", ctypes.POINTER(_LayaLayer)), ("head", ctypes.POINTER(_LayaLayer)),
+                ("type_emb", ctypes.c_void_p), ("score1", _Lin), ("score2", _Lin), ("act1", _Lin), ("act2", _Lin),
+                ("cos_full", ctypes.c_void_p), ("sin_full", ctypes.c_void_p), ("cos_slide", ctypes.c_void_p),
+                ("sin_slide", ctypes.c_void_p)]
+
+
+class Laya:
+    """The Laya encoder on the CPU (src/models/laya/model.rs): the layers are resolved from the
+    GGUF's ggmlc.graph_spec here, as model.rs:60-291 does, and the forward runs in laya.c."""
+
+    def __init__(self, gguf: Gguf, threads: int = 4):
+        import json
+        self.g, self.keep = gguf, []
+        graph = json.loads(gguf.str("ggmlc.graph_spec"))
+        self.graph = graph
+        names = {int(k): v["name"] for k, v in graph["tensors"].items()}
+        nodes = graph["nodes"]
+        have = lambda n: self._has(n)  # noqa: E731
+        L = 0
+        while have(f"qkv.{L}.weight"):
+            L += 1
+        H = 0
+        while have(f"head_qkv.{H}.weight"):
+            H += 1
+        if L == 0 or L > 64 or H != 2:
+            raise ValueError("unsupported Laya encoder/head layout")
+        kind, dims, _ = gguf.tensor("tok_emb.weight")
+        d, vocab = dims[0], dims[1]
+        hd = gguf.tensor("cos_full")[1][0]
+        attns = [n for n in nodes if n["opcode"] == 74]
+        if len(attns) != L + H:
+            raise ValueError("unexpected attention graph")
+        fullmask = attns[0]["inputs"][-1]
+
+        def floats(name):
+            k, dm, raw = gguf.tensor(name)
+            a = decode(k, raw)
+            self.keep.append(a)
+            return a
+
+        def ptr(a):
+            return None if a is None else a.ctypes.data
+
+        def linear(key):
+            weight = key + ".weight"
+            k, dm, raw = gguf.tensor(weight)
+            cols, rows = dm[0], (dm[1] if len(dm) > 1 else 1)
+            node = next((n for n in nodes if n["opcode"] == 29 and n["inputs"] and names[n["inputs"][0]] == weight), None)
+            if node is None:
+                raise ValueError(f"graph lacks linear {key}")
+            biases = [names[node["inputs"][2]]] if len(node["inputs"]) > 2 else []
+            for n in nodes:
+                if n["opcode"] == 200 and n["inputs"][0] == node["outputs"][0]:
+                    biases.append(names[n["inputs"][1]])
+            b = None
+            if biases:
+                b = np.zeros(rows, np.float32)
+                for bn in biases:
+                    b = (b + floats(bn)).astype(np.float32)
+                self.keep.append(b)
+            w = floats(weight)
+            return _Lin(ptr(w), ptr(b), rows, cols), (rows, cols)
+
+        def norm(i):
+            key = "layer_norm" if i == 0 else f"layer_norm_{i}"
+            node = next((n for n in nodes if n.get("name") == key and n["opcode"] == 201), None)
+            if node is None:
+                raise ValueError(f"missing {key}")
+            ins = node["inputs"]
+            w = floats(names[ins[1]]) if len(ins) > 1 else None
+            b = floats(names[ins[2]]) if len(ins) > 2 else None
+            eps = float(np.float32(node["attributes"]["eps"]))
+            if not 0 < eps < 0.1:
+                raise ValueError("invalid layer norm epsilon")
+            return _Ln(ptr(w), ptr(b), eps)
+
+        trunk = (_LayaLayer * L)()
+        for i in range(L):
+            qkv, _ = linear(f"qkv.{i}")
+            wo, _ = linear(f"wo.{i}")
+            wi, _ = linear(f"mlp_wi.{i}")
+            down, _ = linear(f"mlp_wo.{i}")
+            trunk[i] = _LayaLayer(norm(2 * i) if i else _Ln(None, None, 1e-5), norm(2 * i + 1), qkv, wo, wi, down,
+                                  1 if i else 0, 1 if attns[i]["inputs"][-1] == fullmask else 0)
+        head = (_LayaLayer * 2)()
+        for i in range(2):
+            qkv, _ = linear(f"head_qkv.{i}")
+            wo, _ = linear(f"head_wo.{i}")
+            wi, _ = linear(f"head_fc1.{i}")
+            down, _ = linear(f"head_fc2.{i}")
+            head[i] = _LayaLayer(norm(2 * L + 1 + 2 * i), norm(2 * L + 2 + 2 * i), qkv, wo, wi, down, 1, 1)
+        self.keep += [trunk, head]
+        emb = floats("tok_emb.weight")
+        m = _Laya(L, d, hd, vocab, int(gguf.num("laya.max_len", 512)), threads, ptr(emb), norm(0), norm(2 * L),
+                  norm(2 * L + 1 + 2 * H), trunk, head, ptr(floats("type_emb.weight")), linear("scorer_fc1")[0],
+                  linear("scorer_fc2")[0], linear("act_fc1")[0], linear("act_fc2")[0], ptr(floats("cos_full")),
+                  ptr(floats("sin_full")), ptr(floats("cos_slide")), ptr(floats("sin_slide")))
+        self.m = m
+        self.L, self.d, self.hd, self.V = L, d, hd, vocab
+        self.full = [bool(trunk[i].full) for i in range(L)]
+
+    def _has(self, name):
+        try:
+            self.g.tensor(name)
+            return True
+        except KeyError:
+            return False
+
+    def set_threads(self, n: int) -> None:
+        self.m.threads = n
+
+    def forward(self, ids, markers, qtype):
+        """Model::forward(ids, markers, qtype) -> (option logits [k], act logits [2])."""
+        ids, mk = _c(ids, np.int32), _c(markers, np.int32)
+        logits, act = np.empty(mk.size, np.float32), np.empty(2, np.float32)
+        rc = lib().or_laya_forward(ctypes.byref(self.m), _p(ids), ids.size, _p(mk), mk.size, int(qtype), _p(logits),
+                                   _p(act))
+        if rc == -1:
+            raise ValueError("invalid inference input shape")
+        if rc == -2:
+            raise ValueError("token ID out of range")
+        if rc == -3:
+            raise ValueError("non-finite model output")
+        return logits, act
+
+
+def layer_norm(x, w=None, b=None, eps=1e-5):
+    x = _c(x, np.float32)
+    d = x.shape[-1]
+    y = np.empty_like(x)
+    lib().or_layer_norm(_p(x), x.size // d, d, _p(None if w is None else _c(w, np.float32)),
+                        _p(None if b is None else _c(b, np.float32)), eps, _p(y))
+    return y
+
+
+def gelu(v: float) -> float:
+    return lib().or_gelu(v)
+
+
+def laya_attention(qkv, hd, cos=None, sin=None, window=-1):
+    qkv = _c(qkv, np.float32)
+    s, d = qkv.shape[0], qkv.shape[1] // 3
+    out = np.empty((s, d), np.float32)
+    cs = None if cos is None else _c(cos, np.float32)
+    sn = None if sin is None else _c(sin, np.float32)
+    lib().or_laya_attention(_p(qkv), s, d, hd, _p(cs), _p(sn), window, _p(out))
     return out
