@@ -120,10 +120,12 @@ typedef struct {
   int full_layers;         /* OpenThai: full-attention layers (the rest are DeltaNet) */
 } lg_model_info;
 
-/* Model families (general.architecture): "ggmlc" + laya.model_name "laya-decoder", and
- * "openthai_systemone" (src/models/mod.rs:65-71). */
+/* Model families (general.architecture): "ggmlc" + laya.model_name "laya-decoder", the
+ * "openthai_systemone" text tower, and the compiled Laya encoder ("ggmlc" with a laya.checkpoint
+ * and a ggmlc.graph_spec) (src/models/mod.rs:65-71). */
 #define LG_ARCH_LAYA_DECODER 0
 #define LG_ARCH_OPENTHAI 1
+#define LG_ARCH_LAYA 2
 
 /* Load a laya-decoder GGUF onto one GPU: validate, upload and repack every matrix into a
  * hipMalloc'd weight arena, reserve the KV page pool, create the engine's stream.
@@ -262,6 +264,23 @@ int lg_decide(lg_engine *e, const lg_decide_request *req, lg_decide_result *out,
  * src/models/openthai/decision.rs:140-233. */
 int lg_decide_encode(const lg_gguf *g, const lg_decide_request *req, int pass, int32_t *ids, int cap,
                      int *n, int32_t *positions, int32_t *order, int *truncated, int *passes);
+
+/* One input of the Laya encoder: token ids (<= laya.max_len), the positions of the option markers
+ * (1..16) and the question type (0 choice, 1 score, 2 noul). */
+typedef struct {
+  const int32_t *ids;
+  int32_t n;
+  const int32_t *markers;
+  int32_t k;
+  int32_t qtype;
+} lg_laya_input;
+
+/* Laya Model::forward (src/models/laya/model.rs:303-416) for n inputs as one GPU batch: option
+ * logits (k of each input, concatenated, host) and act logits [n][2] (host).  Errors as the
+ * reference: "invalid inference input shape", "token ID out of range", "non-finite model output".
+ * LG_ERR_UNSUPPORTED on other model families. */
+int lg_laya_forward(lg_engine *e, const lg_laya_input *in, int n, float *logits, float *act, lg_cancel_fn cancel,
+                    void *cancel_arg);
 
 /* Several decide requests at once: the states of /v1/decide/batch (src/server.rs:235-319, which
  * runs one decide per state while a global busy flag turns other requests away).  Every request

@@ -430,6 +430,14 @@ int lg_decide(lg_engine *e, const lg_decide_request *req, lg_decide_result *out,
   });
 }
 
+int lg_laya_forward(lg_engine *e, const lg_laya_input *in, int n, float *logits, float *act, lg_cancel_fn cancel,
+                    void *cancel_arg) {
+  return guard([&] {
+    NEED(e, "engine");
+    e->e->laya_forward(in, n, logits, act, cancel, cancel_arg);
+  });
+}
+
 int lg_decide_batch(lg_engine *e, const lg_decide_request *reqs, int n, lg_decide_result *outs,
                     lg_cancel_fn cancel, void *cancel_arg) {
   return guard([&] {

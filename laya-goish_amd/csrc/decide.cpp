@@ -76,6 +76,12 @@ DecideSpec openthai_spec(const Gguf &g) {
 
 DecideSpec decide_spec(const Gguf &g) {
   if (g.str("general.architecture") == "openthai_systemone") return openthai_spec(g);
+  if (g.str("general.architecture") == "ggmlc" && g.str("laya.model_name") != "laya-decoder") {
+    DecideSpec s;
+    for (int i = 0; i < 256; ++i) s.slot[i] = s.head_row[i] = 0;
+    s.error = "a Laya encoder decides per question through lg_laya_forward, not the slot layout of lg_decide";
+    return s;
+  }
   DecideSpec s;
   const int V = int(g.num("laya.decoder.vocab_size", 0));
   const int ctx = int(g.num("laya.decoder.context_length", 0));

@@ -177,6 +177,15 @@ Engine::Engine(const Gguf &g, const lg_engine_opts &opts) {
       HIP_CHECK(hipStreamSynchronize(stream));
       return;
     }
+    if (g.str("general.architecture") == "ggmlc" && g.str("laya.model_name") != "laya-decoder" &&
+        g.meta("ggmlc.graph_spec")) {
+      arch = Arch::Laya;
+      HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+      load_laya(g);
+      decide = decide_spec(g);
+      HIP_CHECK(hipStreamSynchronize(stream));
+      return;
+    }
     load_decoder(g, opts);
   } catch (...) {
     release();
@@ -536,7 +545,7 @@ void Engine::reserve_pages(Seq &s, int upto) {
 }
 
 int Engine::seq_fork(int parent, int ntokens) {
-  if (arch == Arch::OpenThai) fail(LG_ERR_UNSUPPORTED, "fork: OpenThai sequences keep no cache to share");
+  if (fresh_only()) fail(LG_ERR_UNSUPPORTED, "fork: sequences of this model keep no cache to share");
   Seq &p = seq(parent);
   LG_REQUIRE(ntokens >= 0 && ntokens <= p.len, "fork: %d tokens outside the parent's %d", ntokens, p.len);
   Seq c;
@@ -577,7 +586,7 @@ int Engine::seq_len(int id) const {
 BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
   LG_REQUIRE(nreq > 0 && reqs, "batch: no requests");
   auto *b = new BatchPlan();
-  const bool ot = arch == Arch::OpenThai;
+  const bool ot = arch == Arch::OpenThai, fresh = fresh_only();
   try {
     std::vector<int32_t> ids, tseq, tpos, tiles_s, tiles_r, tiles_p, tiles_n, gather, grp_f, grp_c, srow0, sn;
     std::vector<int32_t> it_r, it_p, it_n, it_lo, it_hi, cb_r, cb_n, cb_f, cb_c;
@@ -593,17 +602,17 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
         if (q.ids[i] < 0 || q.ids[i] >= V) fail(LG_ERR_INVALID, "request %d: token id %d outside the vocabulary", r, q.ids[i]);
       for (int i = 0; i < q.npos; ++i)
         if (q.positions[i] < 0 || q.positions[i] >= q.n) fail(LG_ERR_INVALID, "request %d: answer position %d outside the request", r, q.positions[i]);
-      if (ot && s.len != 0)  // model.rs:2: the recurrent state lives only inside one forward
-        fail(LG_ERR_INVALID, "request %d: sequence %d already holds %d tokens; an OpenThai forward starts from an empty sequence",
+      if (fresh && s.len != 0)  // OpenThai: the recurrent state lives only inside one forward (model.rs:2); Laya: bidirectional
+        fail(LG_ERR_INVALID, "request %d: sequence %d already holds %d tokens; a forward of this model starts from an empty sequence",
              r, q.seq, s.len);
       if (s.len + q.n > ctx) fail(LG_ERR_INVALID, "request %d: %d tokens exceed the context length %d", r, s.len + q.n, ctx);
-      if (!ot) max_pages = std::max(max_pages, (s.len + q.n + 63) / 64);
+      if (!fresh) max_pages = std::max(max_pages, (s.len + q.n + 63) / 64);
     }
     const int64_t T = std::accumulate(reqs, reqs + nreq, int64_t(0), [](int64_t a, const lg_request &q) { return a + q.n; });
     if (T > max_batch_tokens_) fail(LG_ERR_INVALID, "batch of %lld tokens exceeds max_batch_tokens %lld", (long long)T, (long long)max_batch_tokens_);
     // reserve pages (all or nothing)
     int need = 0;
-    for (int r = 0; r < nreq && !ot; ++r) {
+    for (int r = 0; r < nreq && !fresh; ++r) {
       const Seq &s = seq(reqs[r].seq);
       need += std::max(0, (s.len + reqs[r].n + 63) / 64 - int(s.pages.size()));
     }
@@ -613,7 +622,7 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
     for (int r = 0; r < nreq; ++r) {
       const lg_request &q = reqs[r];
       Seq &s = seq(q.seq);
-      if (!ot) {
+      if (!fresh) {
         reserve_pages(s, s.len + q.n);
         for (size_t p = 0; p < s.pages.size(); ++p) ptab[size_t(r) * max_pages + p] = s.pages[p];
       }
@@ -773,6 +782,7 @@ void Engine::batch_run(BatchPlan *b, const int32_t *option_ids, int k, float tem
     if (option_ids[j] < 0 || option_ids[j] >= head_rows())
       fail(LG_ERR_INVALID, arch == Arch::OpenThai ? "slot %d outside the 256 slots" : "option id %d outside the vocabulary",
            option_ids[j]);
+  if (arch == Arch::Laya) fail(LG_ERR_UNSUPPORTED, "batch: a Laya encoder scores option markers; use lg_laya_forward");
   // sequences must still exist and not have moved since staging
   for (size_t r = 0; r < b->seqs.size(); ++r) seq(b->seqs[r]);
   if (arch == Arch::OpenThai) run_openthai(*b, cancel, arg);
@@ -813,6 +823,7 @@ void Engine::forward(int sq, const int32_t *ids, int n, const int32_t *positions
     batch_run(b, slots, 256, 1.0f, logits, nullptr, nullptr, cancel, arg);
     return;
   }
+  if (arch == Arch::Laya) fail(LG_ERR_UNSUPPORTED, "forward: a Laya encoder scores option markers; use lg_laya_forward");
   // full vocabulary: prefill, then one fused-norm GEMV over the head per answer row
   for (size_t i = 0; i < b->seqs.size(); ++i) seq(b->seqs[i]);
   run_layers_prefill(*b, cancel, arg);
@@ -834,7 +845,7 @@ void Engine::forward(int sq, const int32_t *ids, int n, const int32_t *positions
 
 // ------------------------------------------------------------------ greedy decode
 void Engine::decode(int sq, int32_t first, int steps, int32_t *tokens, float *logits) {
-  if (arch == Arch::OpenThai) fail(LG_ERR_UNSUPPORTED, "decode: an OpenThai model has a slot head, not a language-model head");
+  if (arch != Arch::Decoder) fail(LG_ERR_UNSUPPORTED, "decode: this model has a decision head, not a language-model head");
   Seq &s = seq(sq);
   LG_REQUIRE(steps > 0 && tokens, "decode: need steps > 0 and an output");
   LG_REQUIRE(first >= 0 && first < V, "decode: token id %d outside the vocabulary", first);

@@ -12,6 +12,7 @@
 
 #include "gguf.h"
 #include "decide.h"
+#include "json.h"
 #include "kernels.h"
 #include "lg.h"
 
@@ -98,7 +99,22 @@ struct BatchPlan {
   bool ran = false;
 };
 
-enum class Arch { Decoder = 0, OpenThai = 1 };
+enum class Arch { Decoder = 0, OpenThai = 1, Laya = 2 };
+
+// Laya encoder layer (src/models/laya/model.rs:29-40); norms with optional weight and bias
+struct LayaNorm {
+  const float *w = nullptr, *b = nullptr;
+  float eps = 1e-5f;
+};
+struct LayaLinear {
+  DevMatrix w;
+  const float *b = nullptr;  // summed biases of the graph, or null
+};
+struct LayaLayer {
+  bool has_n1 = false, full = false;
+  LayaNorm n1, n2;
+  LayaLinear qkv, wo, wi, down;
+};
 
 // One OpenThai-SystemOne layer (src/models/openthai/model.rs:10-40).  Norm weights are stored
 // as 1 + w (the zero-centred RMSNorm's offset applied once at upload, an exact f32 add).
@@ -139,6 +155,9 @@ class Engine {
   void forward(int seq, const int32_t *ids, int n, const int32_t *positions, int npos,
                const int32_t *vocab_ids, int nv, float *logits, lg_cancel_fn cancel, void *arg);
   void decode(int seq, int32_t first, int steps, int32_t *tokens, float *logits);
+  // Laya Model::forward (src/models/laya/model.rs:303-416) for n inputs as one batch:
+  // option logits (k_i per input, concatenated) and act logits [n][2].
+  void laya_forward(const lg_laya_input *in, int n, float *logits, float *act, lg_cancel_fn cancel, void *arg);
 
   Profiler prof;
 
@@ -146,6 +165,9 @@ class Engine {
   void load_decoder(const Gguf &g, const lg_engine_opts &opts);
   void upload(const Gguf &g);
   void load_openthai(const Gguf &g);
+  void load_laya(const Gguf &g);
+  LayaLinear laya_linear(const Gguf &g, const Json &graph, const std::string &key);
+  LayaNorm laya_norm(const Gguf &g, const Json &graph, int i);
   void release();
   // pad_to > 0: rows rounded up to a multiple of pad_to with zero weights
   DevMatrix upload_matrix(const Gguf &g, const std::vector<std::string> &names, int cols, int pad_to = 0);
@@ -158,6 +180,7 @@ class Engine {
   void release_page(int p);
   void run_layers_prefill(BatchPlan &b, lg_cancel_fn cancel, void *arg);
   void run_openthai(BatchPlan &b, lg_cancel_fn cancel, void *arg);
+  void run_laya(BatchPlan &b, const int32_t *qtype_dev, lg_cancel_fn cancel, void *arg);
   KvGeom geom() const;
   void *kpool(int layer) const;
   void *vpool(int layer) const;
@@ -176,6 +199,7 @@ class Engine {
   int L = 0, d = 0, hq = 0, hkv = 0, hd = 0, f = 0, V = 0, ctx = 0;
   int nh = 0;          // OpenThai: gated DeltaNet heads (128-dim)
   int head_rows() const { return arch == Arch::OpenThai ? 256 : V; }
+  bool fresh_only() const { return arch != Arch::Decoder; }  // forwards start from empty sequences
   int64_t max_batch_tokens() const { return max_batch_tokens_; }
   float eps = 1e-5f;
   uint32_t emb_kind = 0;
@@ -195,6 +219,13 @@ class Engine {
   float *head_bias_ = nullptr;                 // OpenThai slot-head bias [256]
   std::vector<OtLayer> ot_;                    // OpenThai layers
   int ldp_full_ = 0, ldp_delta_ = 0;           // OpenThai projection row widths
+  // Laya encoder
+  std::vector<LayaLayer> laya_trunk_, laya_head_;
+  LayaNorm laya_embnorm_, laya_finalnorm_, laya_scorenorm_;
+  const float *laya_type_emb_ = nullptr;
+  LayaLinear laya_score1_, laya_score2_, laya_act1_, laya_act2_;
+  const float *laya_cos_full_ = nullptr, *laya_sin_full_ = nullptr, *laya_cos_slide_ = nullptr, *laya_sin_slide_ = nullptr;
+  int laya_f_ = 0, laya_head_f_ = 0;
   std::map<std::string, DevMatrix> named_;  // GGUF name -> device matrix view
   int64_t weight_bytes_ = 0;
   // KV pool

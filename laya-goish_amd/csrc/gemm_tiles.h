@@ -35,6 +35,10 @@ enum Mode { FAST = 0, SPLIT = 1, SPLIT3 = 2 };
 
 
 __device__ __forceinline__ float silu(float g) { return g * (1.0f / (1.0f + __expf(-g))); }
+// tanh-approximated GELU of src/tensor.rs:129-131
+__device__ __forceinline__ float gelu_tanh(float x) {
+  return 0.5f * x * (1.0f + tanhf(0.7978845608028654f * x * (1.0f + 0.044715f * x * x)));
+}
 
 // f16 bits -> f32 with the hardware conversion (exact for every finite value and infinity;
 // a NaN scale gives NaN outputs either way).
@@ -419,7 +423,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
   };
   // local weight-tile row -> weight row
   auto wrow = [&](int r) -> int {
-    if (EPI == int(Epi::SWIGLU)) {
+    if (EPI == int(Epi::SWIGLU) || EPI == int(Epi::GEGLU)) {
       // wave column r/(32 WTN); block jb = (r/32) % WTN: gate for jb < WTN/2, up otherwise
       const int wc = r / (32 * WTN), jb = (r >> 5) % WTN;
       const int up = jb >= WTN / 2, jj = jb % (WTN / 2);
@@ -496,11 +500,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
     for (int r = 0; r < 16; ++r) {
       const int row = m0 + wm * (32 * WTM) + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
       if (row >= M) continue;
-      if (EPI == int(Epi::SWIGLU)) {
+      if (EPI == int(Epi::SWIGLU) || EPI == int(Epi::GEGLU)) {
 #pragma unroll
         for (int jj = 0; jj < WTN / 2; ++jj) {
           const int col = nt * (BNT / 2) + wn * (16 * WTN) + jj * 32 + col_in;
-          const float v = silu(acc[i][jj][r]) * acc[i][jj + WTN / 2][r];
+          const float g = acc[i][jj][r];
+          const float v = (EPI == int(Epi::SWIGLU) ? silu(g) : gelu_tanh(g)) * acc[i][jj + WTN / 2][r];
           const _Float16 h = _Float16(v);
           C16[int64_t(row) * ldc + col] = h;
           if (C16lo) C16lo[int64_t(row) * ldc + col] = _Float16(v - float(h));
@@ -514,9 +519,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
             if (bias) v += bias[col];
             C[int64_t(row) * ldc + col] = v;
           } else if (EPI == int(Epi::ADD)) {
+            if (bias) v += bias[col];
             C[int64_t(row) * ldc + col] += v;
           } else {
             if (bias) v += bias[col];
+            if (EPI == int(Epi::RELU16)) v = fmaxf(v, 0.0f);
             const _Float16 h = _Float16(v);
             C16[int64_t(row) * ldc + col] = h;
             if (C16lo) C16lo[int64_t(row) * ldc + col] = _Float16(v - float(h));
@@ -531,8 +538,9 @@ template <uint32_t KIND, int MODE, int BK, int WTM, int WTN, int STAGES>
 bool launch_cfg(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
                 _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st) {
   using CF = Cfg<MODE, BK, WTM, WTN, STAGES>;
-  const int outN = epi == Epi::SWIGLU ? W.rows / 2 : W.rows;
-  const int tileN = epi == Epi::SWIGLU ? CF::kBN / 2 : CF::kBN;
+  const bool glu = epi == Epi::SWIGLU || epi == Epi::GEGLU;
+  const int outN = glu ? W.rows / 2 : W.rows;
+  const int tileN = glu ? CF::kBN / 2 : CF::kBN;
   if (outN % tileN) return false;
   const int NT = outN / tileN;
   const int K = W.cols, ffn = W.rows / 2;
@@ -573,6 +581,8 @@ bool launch_cfg(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &
       case Epi::ADD: LAUNCH(1); break;
       case Epi::F16: LAUNCH(2); break;
       case Epi::SWIGLU: LAUNCH(3); break;
+      case Epi::GEGLU: LAUNCH(4); break;
+      case Epi::RELU16: LAUNCH(5); break;
     }
     m0 += Mc;
   }

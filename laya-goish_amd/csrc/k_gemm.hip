@@ -18,8 +18,9 @@ void launch_kind(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix 
   } else if constexpr (KIND == LG_F16) {
     // fewer 128 x 128 tiles than CUs (short prefills, narrow outputs): 64 x 128 tiles, twice
     // the workgroups; the per-element K order is the same, so the results are too
-    const int outN = epi == Epi::SWIGLU ? W.rows / 2 : W.rows;
-    const int64_t tiles = int64_t((M + 127) / 128) * (outN / (epi == Epi::SWIGLU ? 64 : 128));
+    const bool glu = epi == Epi::SWIGLU || epi == Epi::GEGLU;
+    const int outN = glu ? W.rows / 2 : W.rows;
+    const int64_t tiles = int64_t((M + 127) / 128) * (outN / (glu ? 64 : 128));
     if (tiles < 256 && launch_cfg<KIND, SPLIT, 64, 1, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
     if (launch_cfg<KIND, SPLIT, 64, 2, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
   } else {
@@ -75,13 +76,13 @@ void launch_gemm(const _Float16 *A, const _Float16 *A_lo, int M, const DevMatrix
   if (W.cols % 64 != 0) fail(LG_ERR_UNSUPPORTED, "gemm: K=%d is not a multiple of 64", W.cols);
   if (W.kind == LG_Q4_K || W.kind == LG_Q6_K)
     LG_REQUIRE(W.cols % 256 == 0, "gemm: K-quant rows must be whole super-blocks");
-  if (epi == Epi::SWIGLU) {
+  if (epi == Epi::SWIGLU || epi == Epi::GEGLU) {
     if (W.rows % 128 != 0) fail(LG_ERR_UNSUPPORTED, "gemm: gate|up rows %d not a multiple of 128", W.rows);
-    LG_REQUIRE(C16 != nullptr && ldc >= W.rows / 2, "gemm: SwiGLU output needs ldc >= ffn");
+    LG_REQUIRE(C16 != nullptr && ldc >= W.rows / 2, "gemm: gated output needs ldc >= ffn");
   } else {
     if (W.rows % 128 != 0) fail(LG_ERR_UNSUPPORTED, "gemm: N=%d is not a multiple of 128", W.rows);
     LG_REQUIRE(ldc >= W.rows, "gemm: ldc %d < N %d", ldc, W.rows);
-    LG_REQUIRE(epi == Epi::F16 ? C16 != nullptr : C != nullptr, "gemm: missing output");
+    LG_REQUIRE(epi == Epi::F16 || epi == Epi::RELU16 ? C16 != nullptr : C != nullptr, "gemm: missing output");
   }
   switch (W.kind) {
     case LG_F16: launch_kind<LG_F16>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, st); break;

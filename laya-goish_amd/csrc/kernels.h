@@ -48,9 +48,11 @@ struct DevMatrix {
 
 enum class Epi : int {
   F32 = 0,     // C[m][n]  = acc (+ bias[n])
-  ADD = 1,     // C[m][n] += acc            (residual stream update)
+  ADD = 1,     // C[m][n] += acc (+ bias[n]) (residual stream update)
   F16 = 2,     // C16[m][n] = half(acc (+ bias[n]))
   SWIGLU = 3,  // C16[m][j] = half(silu(acc_gate) * acc_up), W rows [0,f) gate, [f,2f) up
+  GEGLU = 4,   // as SWIGLU with the tanh GELU of src/tensor.rs:129-131 (prefill GEMM only)
+  RELU16 = 5,  // C16[m][n] = half(max(acc + bias[n], 0)) (prefill GEMM only)
 };
 
 // Standalone dequant of raw GGUF blocks (device pointers), bit-exact with gguf::decode.
@@ -187,6 +189,24 @@ void launch_ot_attn_mfma(const float *Qb, const float *Kb, const float *proj, in
                          const int32_t *it_khi, int nitems, const int32_t *cb_row0, const int32_t *cb_nq,
                          const int32_t *cb_first, const int32_t *cb_n, int ncomb, float *part, _Float16 *y,
                          _Float16 *ylo, hipStream_t st);
+
+// ---- Laya encoder (k_laya.hip), src/models/laya/model.rs:301-416, src/tensor.rs:103-192 ----
+// LayerNorm of rows (rows[r] of x when rows != nullptr), w/b optional, + add[sel[seq[r]]] when
+// add != nullptr, into f16 planes (y16, y16lo) or f32 (y32).  d % 4 == 0, d <= 4096.
+void launch_layer_norm(const float *x, const int32_t *rows, int nrows, int d, const float *w, const float *b, float eps,
+                       const float *add, const int32_t *seq, const int32_t *sel, _Float16 *y16, _Float16 *y16lo,
+                       float *y32, hipStream_t st);
+// Bidirectional attention over q|k|v rows [T][3d] (head dim 64), keys |i - j| <= window
+// (window < 0: all), RoPE from tables [pos][64] when cosT != nullptr; 32-token tiles (tile_*),
+// tile_seq -> sequence, seq_n -> its length.  Output f16 planes [T][d].
+void launch_laya_attn(const float *qkv, int d, int hd, int window, const float *cosT, const float *sinT,
+                      const int32_t *tile_row0, const int32_t *tile_pos0, const int32_t *tile_n, const int32_t *tile_seq,
+                      const int32_t *seq_n, int ntiles, _Float16 *y, _Float16 *ylo, hipStream_t st);
+void launch_gelu_inplace(float *x, int64_t n, hipStream_t st);
+// pooled[s] = [h[seq_row0[s]] (d), top1, top1 - top2, entropy, max(k,2)/255] over the option
+// logits logits[lg_first[s] .. + lg_count[s]] (model.rs:392-403).
+void launch_laya_act_features(const float *h, int d, const int32_t *seq_row0, const int32_t *lg_first,
+                              const int32_t *lg_count, const float *logits, int nseq, float *pooled, hipStream_t st);
 
 // Device int32 fill / copy helpers (small, capture-safe).
 void launch_fill_i32(int32_t *p, int n, int32_t v, hipStream_t st);

@@ -22,7 +22,7 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "lg.h")
 
 F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
 PREC_EXACT, PREC_FAST = 0, 1
-ARCH_LAYA_DECODER, ARCH_OPENTHAI = 0, 1
+ARCH_LAYA_DECODER, ARCH_OPENTHAI, ARCH_LAYA = 0, 1, 2
 KIND_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
 ERR = {1: "INVALID", 2: "FORMAT", 3: "DEVICE", 4: "OOM", 5: "CANCELED", 6: "UNSUPPORTED"}
 
@@ -79,6 +79,11 @@ class DecideResult(ctypes.Structure):
                 ("confidence", ctypes.POINTER(ctypes.c_float)), ("score", ctypes.POINTER(ctypes.c_float)),
                 ("choice", _I32P), ("input_tokens", ctypes.c_int32), ("permutations", ctypes.c_int32),
                 ("truncated", ctypes.c_int32)]
+
+
+class LayaInput(ctypes.Structure):
+    _fields_ = [("ids", _I32P), ("n", ctypes.c_int32), ("markers", _I32P), ("k", ctypes.c_int32),
+                ("qtype", ctypes.c_int32)]
 
 
 class DecideArgs:
@@ -230,6 +235,7 @@ def lib() -> ctypes.CDLL:
             "lg_decode": (I, [P, I, ctypes.c_int32, I, P, P]),
             "lg_option_scores": (I, [P, I, F, P, P]),
             "lg_decide": (I, [P, ctypes.POINTER(DecideRequest), ctypes.POINTER(DecideResult), CANCEL_FN, P]),
+            "lg_laya_forward": (I, [P, ctypes.POINTER(LayaInput), I, P, P, CANCEL_FN, P]),
             "lg_decide_batch": (I, [P, ctypes.POINTER(DecideRequest), I, ctypes.POINTER(DecideResult), CANCEL_FN, P]),
             "lg_decide_encode": (I, [P, ctypes.POINTER(DecideRequest), I, P, I, ctypes.POINTER(I), P, P,
                                      ctypes.POINTER(I), ctypes.POINTER(I)]),
@@ -527,6 +533,27 @@ class Engine:
             a.res = o
             res.append(a.answers())
         return res
+
+    def laya_forward(self, inputs, cancel=None):
+        """Laya Model::forward (src/models/laya/model.rs:303-416) for [(ids, markers, qtype), ...] as
+        one GPU batch -> [(option logits [k], act logits [2]), ...]."""
+        keep, arr = [], (LayaInput * max(1, len(inputs)))()
+        ks = []
+        for i, (ids, markers, qtype) in enumerate(inputs):
+            ids, mk = _c(ids, np.int32), _c(markers, np.int32)
+            keep += [ids, mk]
+            arr[i] = LayaInput(ctypes.cast(ids.ctypes.data, _I32P), ids.size, ctypes.cast(mk.ctypes.data, _I32P), mk.size,
+                               int(qtype))
+            ks.append(mk.size)
+        logits = np.empty(max(1, sum(ks)), np.float32)
+        act = np.empty((max(1, len(inputs)), 2), np.float32)
+        cb = CANCEL_FN(cancel) if cancel else CANCEL_FN(0)
+        check(lib().lg_laya_forward(self.h, arr, len(inputs), _ptr(logits), _ptr(act), cb, None))
+        out, at = [], 0
+        for i, k in enumerate(ks):
+            out.append((logits[at:at + k].copy(), act[i].copy()))
+            at += k
+        return out
 
     def decode(self, seq: int, first: int, steps: int, want_logits: bool = False):
         toks = np.empty(steps, dtype=np.int32)

@@ -1,0 +1,79 @@
+"""Laya encoder on the GPU against the CPU oracle (oracle/laya.c, pinned in test_cpu_laya.py).
+
+Reference: Model::forward (src/models/laya/model.rs:303-416) -> option logits at the marker
+positions and the act logits.  Bars: 2e-3 absolute in EXACT mode (the reference's own F16
+check allows 0.03 on logits, validation/check.py:41-54), 3e-2 in FAST.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL = {0: 2e-3, 1: 3e-2}
+
+
+@pytest.fixture(scope="module", params=[0, 1], ids=["exact", "fast"])
+def tiny(request, lh, po):
+    img = lh.SynthImage("laya-tiny", seed=13)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), precision=request.param)
+    yield request.param, eng, po.Laya(po.Gguf(img.array()), threads=8)
+    eng.close()
+
+
+def test_info(tiny, lh):
+    _, eng, _ = tiny
+    i = eng.info
+    assert i["arch"] == lh.ARCH_LAYA and (i["layers"], i["d_model"], i["head_dim"], i["vocab"], i["context"]) == (4, 128, 64, 1024, 512)
+
+
+@pytest.mark.parametrize("n,markers,qtype", [(1, [0], 0), (9, [1, 4], 2), (33, [0, 5, 31, 32], 1), (130, [5, 9, 60, 127], 0),
+                                             (512, list(range(3, 19)), 2)])
+def test_forward_matches_oracle(tiny, n, markers, qtype):
+    prec, eng, om = tiny
+    ids = np.random.default_rng(n).integers(0, 1000, n)
+    print(f"laya-tiny prec {prec}: forward n={n}", flush=True)
+    (got_l, got_a), = eng.laya_forward([(ids, markers, qtype)])
+    want_l, want_a = om.forward(ids, markers, qtype)
+    assert np.abs(got_l - want_l).max() <= TOL[prec] and np.abs(got_a - want_a).max() <= TOL[prec]
+
+
+def test_batch_equals_single(tiny):
+    prec, eng, om = tiny
+    rng = np.random.default_rng(3)
+    inputs = [(rng.integers(0, 1000, n), sorted(rng.choice(n, min(n, k), replace=False).tolist()), q)
+              for n, k, q in ((70, 4, 0), (200, 16, 1), (5, 2, 2), (300, 3, 0))]
+    batch = eng.laya_forward(inputs)
+    for inp, (bl, ba) in zip(inputs, batch):
+        (sl, sa), = eng.laya_forward([inp])
+        assert np.array_equal(bl, sl) and np.array_equal(ba, sa)
+
+
+def test_errors_follow_reference(tiny, lh):
+    _, eng, _ = tiny
+    for inp, msg in (([1, 2], [2], 0), "invalid inference input shape"), (([1] * 513, [0], 0), "invalid inference input shape"), \
+                    (([1, 2], [0], 3), "invalid inference input shape"), (([1, 2], list(range(2)) * 9, 0), "invalid inference input shape"), \
+                    (([1, 5000], [0], 0), "token ID out of range"):
+        with pytest.raises(lh.LayaError, match=msg):
+            eng.laya_forward([inp])
+    s = eng.seq_create()
+    with pytest.raises(lh.LayaError) as ei:
+        eng.forward(s, [1, 2, 3], [0])
+    assert ei.value.kind == "UNSUPPORTED"
+    with pytest.raises(lh.LayaError, match="lg_laya_forward"):
+        eng.decide({"state": [1], "questions": [{"type": "noul", "options": [{"name": [1]}, {"name": [2]}]}]})
+    eng.seq_free(s)
+
+
+def test_full_width_matches_oracle(lh, po):
+    """The ModernBERT-base shape (22 layers, d 768, 12 x 64 heads, GeGLU 1152, vocab 50368) on a
+    full 512-token input with 16 markers."""
+    img = lh.SynthImage("laya-english", seed=5)
+    eng = lh.Engine(lh.Gguf.from_bytes(img))
+    om = po.Laya(po.Gguf(img.array()), threads=8)
+    ids = np.random.default_rng(1).integers(0, 50000, 512)
+    markers = list(range(20, 36))
+    print("laya-english: forward n=512", flush=True)
+    (gl, ga), = eng.laya_forward([(ids, markers, 1)])
+    eng.close()
+    wl, wa = om.forward(ids, markers, 1)
+    assert np.abs(gl - wl).max() <= 2e-3 and np.abs(ga - wa).max() <= 2e-3
