@@ -482,6 +482,106 @@ def cpu_baseline(threads, layers=24):
     }
 
 
+LAYA_PRESET = "laya-english"
+LAYA_CPU_MS = {"refund": 1232, "types": 4967, "unicode": 2035, "truncation": 23884}
+
+
+def laya_requests(seed):
+    """Token-level counterparts of the reference's four timed Laya English cases
+    (validation/check.py:14-21, latencies in validation/laya_english_f16.report.json): refund (1 noul
+    question, 45 tokens), types (a 3-option choice, a 3-level score and a noul question, 183
+    tokens over the three forwards), unicode (1 noul question, 68 tokens) and truncation (1 noul
+    question whose state is cut to the 512-token context).  Instruction and option token counts
+    follow the English texts ("noul question: Does the customer ask for money back?" is 12
+    tokens, the two default noul options 9 and 7)."""
+    rng = np.random.default_rng(seed)
+
+    def toks(n):
+        return rng.integers(0, 50000, n).tolist()
+
+    def noul():
+        return {"type": "noul", "instruction": toks(12), "options": [{"name": toks(9)}, {"name": toks(7)}]}
+    # per question: [cls] ins [sep] ([mask] option)... [sep] state [sep]
+    refund = {"state": toks(11), "questions": [noul()]}  # 1 + 12 + 1 + 18 + 1 + 11 + 1 = 45
+    types = {"state": toks(23), "questions": [  # 66 + 60 + 57 = 183 with a 23-token state
+        {"type": "choice", "instruction": toks(12), "options": [{"name": toks(n)} for n in (9, 8, 7)]},
+        {"type": "score", "instruction": toks(9), "options": [{"name": toks(n)} for n in (6, 7, 8)]},
+        noul()]}
+    unicode = {"state": toks(34), "questions": [noul()]}  # 34 + 34 = 68
+    truncation = {"state": toks(1100), "questions": [noul()]}
+    return {"refund": (refund, 45), "types": (types, 183), "unicode": (unicode, 68), "truncation": (truncation, 512)}
+
+
+def bench_laya(args, prec):
+    """Laya English decide on the ModernBERT-base shape (22 layers, d 768, 12 x 64 heads, GeGLU
+    1152, window-64 local / global RoPE attention every third layer, vocab 50368, F16 weights): the
+    reference's four timed request shapes through lg_decide one after another, then 64 states of
+    the 512-token case through lg_decide_batch."""
+    img = lh.SynthImage(LAYA_PRESET, seed=SEED)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), precision=prec)
+    cases = laya_requests(SEED + 9)
+    steps = max(args.steps, 5)
+    res = {}
+    for name, (req, want) in cases.items():
+        out = None
+        for _ in range(max(args.warmup, 1)):
+            out = eng.decide(req)
+        eng.sync()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            out = eng.decide(req)
+        dt = (time.perf_counter() - t0) / steps
+        assert out["usage"]["input_tokens"] == want, (name, out["usage"])
+        res[name] = dt
+        log(f"laya {name}: {dt * 1e3:.2f} ms per request ({want} tokens; reference CPU x4 {LAYA_CPU_MS[name]} ms)")
+    big = cases["truncation"][0]
+    states = [big] * 64
+    eng.decide_batch(states)
+    eng.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        eng.decide_batch(states)
+    dtb = (time.perf_counter() - t0) / steps
+    log(f"laya batch: 64 x 512-token states in {dtb * 1e3:.2f} ms ({64 / dtb:.1f} req/s)")
+    eng.profile_reset()
+    eng.profile(True)
+    eng.decide_batch(states)
+    eng.profile(False)
+    classes = ("gemm", "laya_attn", "layer_norm", "laya_tail", "embed")
+    prof = {c: eng.profile_read(c) for c in classes}
+    for c in classes:
+        p = prof[c]
+        log(f"  {c:12s} {p['launches']:4d} launches {p['ms']:8.3f} ms")
+    eng.close()
+    g = prof["gemm"]
+    gemm_tflops = g["flops"] / (g["ms"] * 1e-3) / 1e12 if g["ms"] > 0 else 0.0
+    dt = res["truncation"]
+    line = base_line("Laya decide req/s (512-token request)", round(1 / dt, 3), "req/s", True, steps,
+                     max(args.warmup, 1), dt * 1e3, prec,
+                     "Laya English ModernBERT-base shape (22 layers, d 768, 12 x 64 heads, GeGLU 1152, "
+                     "local window 64 / global every 3rd layer, 2 head layers, vocab 50368, F16); request: 1 noul "
+                     "question, state cut to the 512-token context",
+                     ms_per_request={k: round(v * 1e3, 3) for k, v in res.items()},
+                     reference_cpu_ms=LAYA_CPU_MS,
+                     batch64_req_s=round(64 / dtb, 1), batch64_ms=round(dtb * 1e3, 2),
+                     kernel_ms_batch64={c: round(prof[c]["ms"], 3) for c in classes})
+    line["roofline"] = {"bound": "mfma", "achieved": round(gemm_tflops, 1), "peak": PEAK_F16_TFLOPS,
+                        "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_F16_TFLOPS, 4), "traffic": None,
+                        "kernel": "gemm (every projection and MLP matrix of the 64 x 512-token batch)"}
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import pydecide
+        import pyoracle as po
+        og = po.Gguf(img.array())
+        om = po.Laya(og, threads=args.cpu_threads)
+        t0 = time.perf_counter()
+        pydecide.laya_decide(om, og, big)
+        cdt = time.perf_counter() - t0
+        line["cpu_baseline"] = {"value": round(1 / cdt, 5), "unit": "req/s", "cores": args.cpu_threads, "kind": "port",
+                                "sample": f"the 512-token request through all 22 layers: {cdt:.1f} s per request"}
+    return line
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -489,7 +589,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--precision", choices=["exact", "fast"], default="exact")
     ap.add_argument("--workload", choices=["decide", "plumbing", "q4k-prefill", "long-context", "decide-request",
-                                           "decide-batch", "openthai-decide"],
+                                           "decide-batch", "openthai-decide", "laya-decide"],
                     default="decide",
                     help="decide (default): the Q8_0 d2048 batched decide headline plus batch-1 decode; the "
                          "others measure the remaining workload shapes, one JSON line each")
@@ -512,7 +612,7 @@ def main():
     if args.workload != "decide":
         fn = {"plumbing": bench_plumbing, "q4k-prefill": bench_q4k, "long-context": bench_long_context,
               "decide-request": bench_decide_request, "decide-batch": bench_decide_batch,
-              "openthai-decide": bench_openthai}
+              "openthai-decide": bench_openthai, "laya-decide": bench_laya}
         print(json.dumps(fn[args.workload](args, prec)), flush=True)
         return
     if args.copy_calibration > 0:

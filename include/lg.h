@@ -244,7 +244,8 @@ typedef struct {
 
 typedef struct {
   float *probs;                       /* [sum of n_options], question order (caller-owned) */
-  float *abstain;                     /* [n_questions]: abstain slot mass (choice; else 0) */
+  float *abstain;                     /* [n_questions]: abstain slot mass (choice; else 0); for a
+                                         Laya encoder the act probability of every question */
   float *confidence;                  /* [n_questions]: 1 - H(p)/ln k */
   float *score;                       /* [n_questions]: sum_j j p_j (score questions; else 0) */
   int32_t *choice;                    /* [n_questions]: first most probable option */
@@ -255,7 +256,9 @@ typedef struct {
 
 /* Decide: encode every option-order pass, prefill all passes as one GPU batch, score the
  * 256 slot rows at each answer position and aggregate.  Replaces Backend::decide / decide,
- * src/models/mod.rs:16-22 and src/models/openthai/decision.rs:243-390 (text encoding aside). */
+ * src/models/mod.rs:16-22 and src/models/openthai/decision.rs:243-390 (text encoding aside).
+ * For a Laya encoder: one forward per question (src/models/laya/decision.rs:168-318), all the
+ * questions as GPU batches; one pass, truncated 0, input_tokens summed over the questions. */
 int lg_decide(lg_engine *e, const lg_decide_request *req, lg_decide_result *out, lg_cancel_fn cancel,
               void *cancel_arg);
 /* The token layout of pass `pass` of a request for the model in `g` (host only, no GPU):
@@ -281,6 +284,18 @@ typedef struct {
  * LG_ERR_UNSUPPORTED on other model families. */
 int lg_laya_forward(lg_engine *e, const lg_laya_input *in, int n, float *logits, float *act, lg_cancel_fn cancel,
                     void *cancel_arg);
+
+/* The Laya token layout of question `question` of a request (host only, no GPU): ids[cap] (n
+ * written) and markers[n_options] (the [mask] position of each option).  The instruction tokens
+ * stand for the encoded "<kind> question: <instructions>" and each option's name + description
+ * tokens for its encoded text.  Replaces encode, src/models/laya/decision.rs:100-154. */
+int lg_laya_decide_encode(const lg_gguf *g, const lg_decide_request *req, int question, int32_t *ids, int cap,
+                          int *n, int32_t *markers);
+/* The Laya aggregation over logits the caller already holds (host only): option logits (k of
+ * every question, concatenated) and act logits [n_questions][2].  abstain[q] receives the
+ * act probability (softmax of the act logits, entry 0).  Replaces decision.rs:185-298. */
+int lg_laya_decide_scores(const lg_gguf *g, const lg_decide_request *req, const float *logits, const float *act,
+                          lg_decide_result *out);
 
 /* Several decide requests at once: the states of /v1/decide/batch (src/server.rs:235-319, which
  * runs one decide per state while a global busy flag turns other requests away).  Every request

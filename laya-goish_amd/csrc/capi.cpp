@@ -347,10 +347,52 @@ int lg_decode(lg_engine *e, int seq, int32_t first, int steps, int32_t *tokens, 
 
 namespace {
 
+// The Laya decide of `reqs` (src/models/laya/decision.rs:168-318, one forward per question):
+// every question of every request validated and encoded first, then run through the encoder as
+// GPU batches of at most the engine's batch token budget, then aggregated per request.
+void laya_decide_many(lg::Engine &E, const lg_decide_request *reqs, int n, lg_decide_result *outs,
+                      lg_cancel_fn cancel, void *cancel_arg) {
+  const lg::LayaSpec &s = E.laya_decide;
+  std::vector<std::vector<lg::LayaEncoded>> enc(n);
+  std::vector<int> tokens(n, 0);
+  for (int r = 0; r < n; ++r) {
+    lg::laya_validate(s, reqs[r]);
+    for (int q = 0; q < reqs[r].n_questions; ++q) {
+      enc[r].push_back(lg::laya_encode(s, reqs[r], q));
+      tokens[r] += int(enc[r].back().ids.size());
+    }
+  }
+  std::vector<lg_laya_input> in;
+  std::vector<size_t> koff{0};
+  for (int r = 0; r < n; ++r)
+    for (int q = 0; q < reqs[r].n_questions; ++q) {
+      const lg::LayaEncoded &x = enc[r][q];
+      in.push_back({x.ids.data(), int32_t(x.ids.size()), x.markers.data(), int32_t(x.markers.size()),
+                    reqs[r].questions[q].kind});
+      koff.push_back(koff.back() + x.markers.size());
+    }
+  std::vector<float> logits(koff.back()), act(2 * in.size());
+  const int64_t budget = E.max_batch_tokens();
+  size_t i0 = 0;
+  while (i0 < in.size()) {
+    size_t i1 = i0;
+    int64_t toks = 0;
+    while (i1 < in.size() && (i1 == i0 || toks + in[i1].n <= budget)) toks += in[i1++].n;
+    E.laya_forward(in.data() + i0, int(i1 - i0), logits.data() + koff[i0], act.data() + 2 * i0, cancel, cancel_arg);
+    i0 = i1;
+  }
+  size_t at = 0;
+  for (int r = 0; r < n; ++r) {
+    lg::laya_aggregate(s, reqs[r], logits.data() + koff[at], act.data() + 2 * at, tokens[r], outs[r]);
+    at += size_t(reqs[r].n_questions);
+  }
+}
+
 // Runs every pass of `reqs` through the engine (GPU batches of at most the engine's batch token
 // budget, passes of one request kept in one batch when they fit) and aggregates each request.
 void decide_many(lg::Engine &E, const lg_decide_request *reqs, int n, lg_decide_result *outs, lg_cancel_fn cancel,
                  void *cancel_arg) {
+  if (E.arch == lg::Arch::Laya) return laya_decide_many(E, reqs, n, outs, cancel, cancel_arg);
   const lg::DecideSpec &s = E.decide;
   std::vector<int> passes(n);
   std::vector<std::vector<lg::Encoded>> enc(n);
@@ -492,6 +534,42 @@ int lg_decide_scores(const lg_gguf *g, const lg_decide_request *req, const float
     std::vector<lg::Encoded> enc;
     for (int p = 0; p < n; ++p) enc.push_back(lg::decide_encode(s, *req, n, p));
     lg::decide_aggregate(s, *req, n, enc, slot_logits, *out);
+  });
+}
+
+int lg_laya_decide_encode(const lg_gguf *g, const lg_decide_request *req, int question, int32_t *ids, int cap,
+                          int *n, int32_t *markers) {
+  return guard([&] {
+    NEED(g, "gguf");
+    NEED(req, "request");
+    const lg::LayaSpec s = lg::laya_spec(*g->g);
+    lg::laya_validate(s, *req);
+    LG_REQUIRE(question >= 0 && question < req->n_questions, "question %d outside 0..%d", question,
+               req->n_questions - 1);
+    const lg::LayaEncoded e = lg::laya_encode(s, *req, question);
+    if (n) *n = int(e.ids.size());
+    if (ids) {
+      LG_REQUIRE(size_t(cap) >= e.ids.size(), "ids capacity %d < %zu tokens", cap, e.ids.size());
+      std::copy(e.ids.begin(), e.ids.end(), ids);
+    }
+    if (markers) std::copy(e.markers.begin(), e.markers.end(), markers);
+  });
+}
+
+int lg_laya_decide_scores(const lg_gguf *g, const lg_decide_request *req, const float *logits, const float *act,
+                          lg_decide_result *out) {
+  return guard([&] {
+    NEED(g, "gguf");
+    NEED(req, "request");
+    NEED(logits, "logits");
+    NEED(act, "act logits");
+    NEED(out, "result");
+    NEED(out->probs, "result probabilities");
+    const lg::LayaSpec s = lg::laya_spec(*g->g);
+    lg::laya_validate(s, *req);
+    int tokens = 0;
+    for (int q = 0; q < req->n_questions; ++q) tokens += int(lg::laya_encode(s, *req, q).ids.size());
+    lg::laya_aggregate(s, *req, logits, act, tokens, *out);
   });
 }
 

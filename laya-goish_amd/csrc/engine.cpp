@@ -183,6 +183,7 @@ Engine::Engine(const Gguf &g, const lg_engine_opts &opts) {
       HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
       load_laya(g);
       decide = decide_spec(g);
+      laya_decide = laya_spec(g);
       HIP_CHECK(hipStreamSynchronize(stream));
       return;
     }

@@ -12,6 +12,7 @@
 
 #include "gguf.h"
 #include "decide.h"
+#include "laya_decide.h"
 #include "json.h"
 #include "kernels.h"
 #include "lg.h"
@@ -205,6 +206,7 @@ class Engine {
   uint32_t emb_kind = 0;
   int precision = LG_PREC_EXACT;
   DecideSpec decide;  // control tokens and budgets of the request-level decide layout
+  LayaSpec laya_decide;  // budgets, special ids and temperatures of the Laya decide
   bool split() const { return precision == LG_PREC_EXACT; }
   int kv_elem() const { return split() ? 4 : 2; }
 

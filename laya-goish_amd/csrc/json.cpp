@@ -101,6 +101,9 @@ struct Reader {
         ws();
         if (i >= t.size() || t[i] != ':') bad();
         ++i;
+        // a repeated key makes the whole text invalid (src/json.rs:157-166)
+        for (const auto &kv : v.o)
+          if (kv.first == k) bad();
         v.o.emplace_back(std::move(k), value(depth + 1));
         ws();
         if (i < t.size() && t[i] == ',') { ++i; continue; }

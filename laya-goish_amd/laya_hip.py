@@ -141,14 +141,18 @@ class DecideArgs:
                                 ctypes.cast(o["choice"].ctypes.data, _I32P), 0, 0, 0)
         return self.res
 
-    def answers(self):
+    def answers(self, laya: bool = False):
+        """Per-question answers; for a Laya encoder the abstain entry carries the act probability
+        (src/models/laya/decision.rs:286-289)."""
         o, out, at = self.out, [], 0
         for i, (kind, k) in enumerate(zip(self.kinds, self.nopts)):
             p = o["probs"][at:at + k].copy()
             at += k
             a = {"type": kind, "probabilities": p, "confidence": float(o["confidence"][i]),
                  "choice": int(o["choice"][i])}
-            if kind == "choice":
+            if laya:
+                a["act_probability"] = float(o["abstain"][i])
+            elif kind == "choice":
                 a["abstain"] = float(o["abstain"][i])
             if kind == "score":
                 a["score"] = float(o["score"][i])
@@ -184,6 +188,28 @@ def decide_scores(gguf: "Gguf", req: dict, slot_logits) -> dict:
     res = a.result()
     check(lib().lg_decide_scores(gguf.h, ctypes.byref(a.req), _ptr(sl), ctypes.byref(res)))
     return a.answers()
+
+
+def laya_decide_encode(gguf: "Gguf", req: dict, question: int = 0):
+    """Laya token layout of one question: (ids, option marker positions).  Host only."""
+    a = DecideArgs(req)
+    n = ctypes.c_int()
+    check(lib().lg_laya_decide_encode(gguf.h, ctypes.byref(a.req), question, None, 0, ctypes.byref(n), None))
+    ids = np.zeros(n.value, np.int32)
+    k = a.nopts[question] if 0 <= question < len(a.nopts) else 0
+    mk = np.zeros(max(1, k), np.int32)
+    check(lib().lg_laya_decide_encode(gguf.h, ctypes.byref(a.req), question, _ptr(ids), n.value, ctypes.byref(n),
+                                      _ptr(mk)))
+    return ids, mk[:k]
+
+
+def laya_decide_scores(gguf: "Gguf", req: dict, logits, act) -> dict:
+    """Laya aggregation over caller-held option logits (concatenated) and act logits [questions][2]."""
+    a = DecideArgs(req)
+    lg_, ac = _c(logits, np.float32), _c(act, np.float32)
+    res = a.result()
+    check(lib().lg_laya_decide_scores(gguf.h, ctypes.byref(a.req), _ptr(lg_), _ptr(ac), ctypes.byref(res)))
+    return a.answers(laya=True)
 
 
 CANCEL_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p)
@@ -240,6 +266,8 @@ def lib() -> ctypes.CDLL:
             "lg_decide_encode": (I, [P, ctypes.POINTER(DecideRequest), I, P, I, ctypes.POINTER(I), P, P,
                                      ctypes.POINTER(I), ctypes.POINTER(I)]),
             "lg_decide_scores": (I, [P, ctypes.POINTER(DecideRequest), P, ctypes.POINTER(DecideResult)]),
+            "lg_laya_decide_encode": (I, [P, ctypes.POINTER(DecideRequest), I, P, I, ctypes.POINTER(I), P]),
+            "lg_laya_decide_scores": (I, [P, ctypes.POINTER(DecideRequest), P, P, ctypes.POINTER(DecideResult)]),
             "lg_option_confidence": (I, [P, I, I, ctypes.POINTER(F)]),
             "lg_profile_enable": (I, [P, I]),
             "lg_profile_read": (I, [P, ctypes.c_char_p, ctypes.POINTER(I64), ctypes.POINTER(ctypes.c_double),
@@ -517,7 +545,7 @@ class Engine:
         res = a.result()
         cb = CANCEL_FN(cancel) if cancel else CANCEL_FN(0)
         check(lib().lg_decide(self.h, ctypes.byref(a.req), ctypes.byref(res), cb, None))
-        return a.answers()
+        return a.answers(laya=self.info["arch"] == ARCH_LAYA)
 
     def decide_batch(self, reqs: list, cancel=None) -> list:
         """Several requests at once (the states of /v1/decide/batch, src/server.rs:235-319): all
@@ -531,7 +559,7 @@ class Engine:
         res = []
         for a, o in zip(args, outs):
             a.res = o
-            res.append(a.answers())
+            res.append(a.answers(laya=self.info["arch"] == ARCH_LAYA))
         return res
 
     def laya_forward(self, inputs, cancel=None):

@@ -238,3 +238,108 @@ def decide(model: po.Model, gguf: po.Gguf, req: dict) -> dict:
     else:
         logits = np.stack([model.forward(e[0], e[1], s["head_rows"]) for e in encs])
     return aggregate(s, req, n, encs, logits), logits
+
+
+# ---- Laya encoder decide (src/models/laya/decision.rs), token level ----
+
+LAYA_KINDS = ("choice", "score", "noul")
+
+
+def _laya_json(gguf: po.Gguf, key: str):
+    """json::parse of a metadata string; unparsable (or repeated keys) counts as absent
+    (decision.rs:181-182, src/json.rs:157-166)."""
+    import json
+
+    def pairs(kv):
+        keys = [k for k, _ in kv]
+        if len(keys) != len(set(keys)):
+            raise ValueError("duplicate JSON key")
+        return dict(kv)
+
+    try:
+        return json.loads(gguf.str(key), object_pairs_hook=pairs)
+    except (ValueError, KeyError, TypeError):
+        return None
+
+
+def laya_spec(gguf: po.Gguf) -> dict:
+    """laya.max_len / head_max_len, the [mask]/[sep]/[cls] ids (decision.rs:104-113) and the two
+    temperature tables (decision.rs:180-182)."""
+    return {
+        "max": int(gguf.num("laya.max_len", 512)), "head_max": int(gguf.num("laya.head_max_len", 192)),
+        "mask": int(gguf.num("laya.mask_token_id", 50284)), "sep": int(gguf.num("laya.sep_token_id", 50282)),
+        "cls": int(gguf.num("laya.cls_token_id", 50281)),
+        "temperature": _laya_json(gguf, "laya.temperature"), "buckets": _laya_json(gguf, "laya.temperature_by_options"),
+    }
+
+
+def laya_encode(s: dict, req: dict, qi: int):
+    """decision.rs:100-154 over token ids: -> (ids, markers)."""
+    q = req["questions"][qi]
+    if s["head_max"] < 32 or s["head_max"] >= s["max"]:
+        raise ValueError("invalid sequence budgets")
+    head = list(q.get("instruction") or [])
+    opts = []
+    for o in q["options"]:
+        tok = (list(o.get("name") or []) + list(o.get("desc") or []))[:48]
+        opts.append([s["mask"]] + tok)
+    total = sum(map(len, opts))
+    if s["head_max"] - total < 16:
+        per = max((s["head_max"] - 16) // len(opts), 4)
+        opts = [o[:per] for o in opts]
+        total = sum(map(len, opts))
+    head = head[:max(s["head_max"] - total, 0, 8)]
+    ids, markers = [s["cls"], *head, s["sep"]], []
+    for o in opts:
+        markers.append(len(ids))
+        ids += o
+    ids.append(s["sep"])
+    room = max(s["max"] - (len(ids) + 1), 0)
+    ids = (ids + list(req.get("state") or [])[:room] + [s["sep"]])[:s["max"]]
+    if any(m >= len(ids) for m in markers):
+        raise ValueError("option markers exceed context")
+    return ids, markers
+
+
+def laya_temperature(s: dict, kind: str, k: int) -> np.float32:
+    """The options bucket, else the kind's entry, else 1; at least 1e-3 (decision.rs:190-212)."""
+    bucket = f"{kind}:{'2' if k <= 2 else '3-5' if k <= 5 else '6-10' if k <= 10 else '11+'}"
+    num = lambda v: float(v) if isinstance(v, (int, float)) and not isinstance(v, bool) else 0.0  # noqa: E731
+    b = s["buckets"]
+    if isinstance(b, dict) and b.get(bucket) is not None:
+        t = np.float32(num(b[bucket]))
+    elif isinstance(s["temperature"], list) and LAYA_KINDS.index(kind) < len(s["temperature"]):
+        t = np.float32(num(s["temperature"][LAYA_KINDS.index(kind)]))
+    else:
+        t = np.float32(1.0)
+    return max(t, np.float32(1e-3))
+
+
+def laya_aggregate(s: dict, req: dict, outs, tokens: int) -> dict:
+    """decision.rs:185-298: softmax(z / T), act probability, choice, expected score, confidence."""
+    f = np.float32
+    answers = []
+    for q, (z, act) in zip(req["questions"], outs):
+        kind, k = q["type"], len(z)
+        T = laya_temperature(s, kind, k)
+        p = po.softmax(np.array([f(v) / T for v in z], np.float32))
+        ap = float(po.softmax(np.asarray(act, np.float32))[0])
+        best = max(range(k), key=lambda i: (p[i], -i))
+        a = {"type": kind, "probabilities": p, "choice": best, "act_probability": ap}
+        if kind == "noul":
+            a["confidence"] = float(max(p[1], f(f(1) - p[1])))
+            a["noul"] = float(p[1])
+        else:
+            a["confidence"] = float(po.confidence(p, f64=True))
+        if kind == "score":
+            a["score"] = float(sum(i * float(v) for i, v in enumerate(p)))
+        answers.append(a)
+    return {"answers": answers, "input_tokens": tokens}
+
+
+def laya_decide(model: po.Laya, gguf: po.Gguf, req: dict):
+    """The whole Laya decision on the CPU oracle: one forward per question, then the aggregation."""
+    s = laya_spec(gguf)
+    encs = [laya_encode(s, req, i) for i in range(len(req["questions"]))]
+    outs = [model.forward(ids, mk, LAYA_KINDS.index(q["type"])) for (ids, mk), q in zip(encs, req["questions"])]
+    return laya_aggregate(s, req, outs, sum(len(e[0]) for e in encs)), outs

@@ -59,8 +59,6 @@ def test_errors_follow_reference(tiny, lh):
     with pytest.raises(lh.LayaError) as ei:
         eng.forward(s, [1, 2, 3], [0])
     assert ei.value.kind == "UNSUPPORTED"
-    with pytest.raises(lh.LayaError, match="lg_laya_forward"):
-        eng.decide({"state": [1], "questions": [{"type": "noul", "options": [{"name": [1]}, {"name": [2]}]}]})
     eng.seq_free(s)
 
 
@@ -77,3 +75,72 @@ def test_full_width_matches_oracle(lh, po):
     eng.close()
     wl, wa = om.forward(ids, markers, 1)
     assert np.abs(gl - wl).max() <= 2e-3 and np.abs(ga - wa).max() <= 2e-3
+
+
+def _request(rng, nq):
+    kinds = ("choice", "score", "noul")
+    qs = []
+    for i in range(nq):
+        kind = kinds[i % 3]
+        k = 2 if kind == "noul" else int(rng.integers(2, 17))
+        qs.append({"type": kind, "instruction": rng.integers(0, 1000, int(rng.integers(1, 200))).tolist(),
+                   "options": [{"name": rng.integers(0, 1000, int(rng.integers(1, 40))).tolist(),
+                                "desc": rng.integers(0, 1000, 5).tolist() if j % 2 else None} for j in range(k)]})
+    return {"state": rng.integers(0, 1000, int(rng.integers(0, 600))).tolist(), "questions": qs}
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_decide_matches_oracle(tiny, po, seed):
+    """lg_decide on a Laya encoder (src/models/laya/decision.rs:168-318) against the token-level
+    restatement over the CPU oracle's forward."""
+    import pydecide as pd
+    prec, eng, om = tiny
+    req = _request(np.random.default_rng(seed), 4)
+    print(f"laya-tiny prec {prec}: decide seed {seed}", flush=True)
+    got = eng.decide(req)
+    want, _ = pd.laya_decide(om, om.g, req)
+    assert got["usage"]["input_tokens"] == want["input_tokens"]
+    for a, b in zip(got["answers"], want["answers"]):
+        assert np.abs(a["probabilities"] - b["probabilities"]).max() <= TOL[prec]
+        assert abs(a["act_probability"] - b["act_probability"]) <= TOL[prec]
+        p = np.sort(b["probabilities"])
+        if len(p) < 2 or p[-1] - p[-2] > 4 * TOL[prec]:
+            assert a["choice"] == b["choice"]
+        if "score" in b:
+            assert abs(a["score"] - b["score"]) <= TOL[prec] * len(p) ** 2
+
+
+def test_decide_is_forward_then_scores(tiny, lh):
+    """lg_decide equals lg_laya_decide_encode -> lg_laya_forward -> lg_laya_decide_scores bit for bit."""
+    prec, eng, om = tiny
+    req = _request(np.random.default_rng(7), 5)
+    h = lh.Gguf.from_bytes(lh.SynthImage("laya-tiny", seed=13))
+    encs = [lh.laya_decide_encode(h, req, i) for i in range(5)]
+    outs = eng.laya_forward([(ids, mk, ("choice", "score", "noul").index(q["type"]))
+                             for (ids, mk), q in zip(encs, req["questions"])])
+    want = lh.laya_decide_scores(h, req, np.concatenate([o[0] for o in outs]), np.stack([o[1] for o in outs]))
+    got = eng.decide(req)
+    assert got["usage"]["input_tokens"] == sum(len(e[0]) for e in encs)
+    for a, b in zip(got["answers"], want["answers"]):
+        assert np.array_equal(a["probabilities"], b["probabilities"])
+        assert {k: v for k, v in a.items() if k != "probabilities"} == {k: v for k, v in b.items() if k != "probabilities"}
+
+
+def test_decide_batch_and_budget_split(tiny, lh):
+    """lg_decide_batch (every question of every state in GPU batches) and an engine whose batch
+    budget splits the questions give the results of lg_decide on each request alone."""
+    prec, eng, om = tiny
+    rng = np.random.default_rng(11)
+    reqs = [_request(rng, n) for n in (3, 1, 6)]
+    single = [eng.decide(r) for r in reqs]
+    batch = eng.decide_batch(reqs)
+    small = lh.Engine(lh.Gguf.from_bytes(lh.SynthImage("laya-tiny", seed=13)), precision=prec, max_batch_tokens=600)
+    try:
+        split = [small.decide(r) for r in reqs]
+    finally:
+        small.close()
+    for s, b, t in zip(single, batch, split):
+        for x, y, z in zip(s["answers"], b["answers"], t["answers"]):
+            assert np.array_equal(x["probabilities"], y["probabilities"])
+            assert np.array_equal(x["probabilities"], z["probabilities"])
+            assert x["act_probability"] == y["act_probability"] == z["act_probability"]
