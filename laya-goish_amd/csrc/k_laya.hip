@@ -85,143 +85,166 @@ __global__ __launch_bounds__(kT) void layer_norm_kernel(const float *__restrict_
   }
 }
 
-// Bidirectional attention over q|k|v rows [T][3d] (f32), head dim 64: one workgroup per (32-query
-// tile of one sequence, head).  Keys j with |i - j| <= window (window < 0: the whole sequence);
-// RoPE from tables [pos][64] (pairs j, j + 32) applied as Q and K tiles are staged; scores
+// Bidirectional attention over q|k|v rows [T][3d] (f32), head dim 64, on v_mfma_f32_16x16x4_f32
+// (f32 operands and accumulation).  One workgroup per (32-query tile of one sequence, head), two
+// waves of 16 query rows each.  Keys j with |i - j| <= window (window < 0: the whole sequence);
+// RoPE from tables [pos][64] (pairs j, j + 32) applied as Q and K tiles are staged in LDS; scores
 // q.k * (1/sqrt(64)); online softmax in f32.  Output f16 planes [T][d].
+//   S = Q K^T per 32-key tile: lane (li = l%16, kg = l/16) supplies Q[li][16g + 4kg + c] at step
+//   4g + c (a permutation of the 64-dim contraction, applied to K alike, so every operand is one
+//   float4 LDS read per 4 MFMAs); D layout: lane l holds S[4kg + r][16 blk + li], r < 4.
+//   Online softmax per row with 16-lane DPP reductions; P goes through LDS into the A layout;
+//   O += P V with V transposed in LDS.
 constexpr int kHD = 64, kAT = 32, kHDp = kHD + 4;
+constexpr int kVTp = 36;  // padded row of the transposed V tile [64 dims][32 keys]
+constexpr int kPp = 36;   // padded row of the P tile [16 rows][32 keys]
+constexpr int kAW = 128;  // two waves
 
-__global__ __launch_bounds__(kT) void laya_attn_kernel(const float *__restrict__ qkv, int d, int window,
-                                                       const float *__restrict__ cosT, const float *__restrict__ sinT,
-                                                       const int32_t *__restrict__ tile_row0,
-                                                       const int32_t *__restrict__ tile_pos0,
-                                                       const int32_t *__restrict__ tile_n,
-                                                       const int32_t *__restrict__ seq_of_tile,
-                                                       const int32_t *__restrict__ seq_n,
-                                                       _Float16 *__restrict__ y, _Float16 *__restrict__ ylo) {
-  __shared__ __align__(16) float sQ[kAT * kHDp];
-  __shared__ __align__(16) float sK[kAT * kHDp];
-  __shared__ __align__(16) float sV[kAT * kHD];
-  __shared__ float sP[kAT * 33];
+// RoPE of one float4 of a row (dims j0..j0+3) given the partner float4 (dims j0+32.. mod 64).
+__device__ __forceinline__ float4 rope4(float4 v, float4 o, const float *cs, const float *sn, int j0) {
+  const float a[4] = {v.x, v.y, v.z, v.w}, b[4] = {o.x, o.y, o.z, o.w};
+  float out[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) out[k] = j0 < kHD / 2 ? a[k] * cs[k] - b[k] * sn[k] : a[k] * cs[k] + b[k] * sn[k];
+  return make_float4(out[0], out[1], out[2], out[3]);
+}
+
+__global__ __launch_bounds__(kAW) void laya_attn_kernel(const float *__restrict__ qkv, int d, int window,
+                                                        const float *__restrict__ cosT, const float *__restrict__ sinT,
+                                                        const int32_t *__restrict__ tile_row0,
+                                                        const int32_t *__restrict__ tile_pos0,
+                                                        const int32_t *__restrict__ tile_n,
+                                                        const int32_t *__restrict__ seq_of_tile,
+                                                        const int32_t *__restrict__ seq_n,
+                                                        _Float16 *__restrict__ y, _Float16 *__restrict__ ylo) {
+  __shared__ __align__(16) float sK[kAT * kHDp];      // [32 keys][68]
+  __shared__ __align__(16) float sVT[kHD * kVTp];     // [64 dims][36]
+  __shared__ __align__(16) float sQ[2][16 * kHDp];    // per wave [16 rows][68]
+  __shared__ __align__(16) float sP[2][16 * kPp];     // per wave [16 rows][36]
   const int tile = blockIdx.x, h = blockIdx.y;
   const int row0 = tile_row0[tile], pos0 = tile_pos0[tile], nq = tile_n[tile];
   const int n = seq_n[seq_of_tile[tile]];
   const int srow = row0 - pos0;
-  const int tid = threadIdx.x, r = tid >> 3, sub = tid & 7;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, kg = l >> 4;
   const int ld = 3 * d;
-  // stage a [32][64] tile of q (part 0) or k (part 1) rows with RoPE, rows past `cnt` zero
-  auto stage_rot = [&](float *dst, int part, int t0, int cnt) {
-    for (int e = tid; e < kAT * (kHD / 4); e += kT) {
-      const int i = e / (kHD / 4), c4 = e % (kHD / 4);
-      float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if (i < cnt) {
-        const float *src = qkv + int64_t(srow + t0 + i) * ld + part * d + h * kHD;
-        v = *reinterpret_cast<const float4 *>(src + c4 * 4);
-        if (cosT) {
-          const int p = t0 + i, j0 = c4 * 4;
-          const float4 o = *reinterpret_cast<const float4 *>(src + (j0 + kHD / 2) % kHD);
-          const float *cs = cosT + int64_t(p) * kHD + j0, *sn = sinT + int64_t(p) * kHD + j0;
-          const float a[4] = {v.x, v.y, v.z, v.w}, b[4] = {o.x, o.y, o.z, o.w};
-          float out[4];
+  const int wq = nq - 16 * w;  // this wave's valid rows (may be <= 0)
+  // this wave's Q rows, rotated (rows past the tile repeat its last row and are never written)
+  float *myQ = sQ[w];
 #pragma unroll
-          for (int k = 0; k < 4; ++k)
-            out[k] = j0 < kHD / 2 ? a[k] * cs[k] - b[k] * sn[k] : a[k] * cs[k] + b[k] * sn[k];
-          v = make_float4(out[0], out[1], out[2], out[3]);
-        }
-      }
-      *reinterpret_cast<float4 *>(dst + i * kHDp + c4 * 4) = v;
-    }
-  };
-  stage_rot(sQ, 0, pos0, nq);
+  for (int k = 0; k < 4; ++k) {
+    const int e = l + 64 * k, i = e >> 4, c4 = e & 15, j0 = c4 * 4;
+    const int p = pos0 + min(16 * w + i, nq - 1);
+    const float *src = qkv + int64_t(srow + p) * ld + h * kHD;
+    float4 v = reinterpret_cast<const float4 *>(src)[c4];
+    if (cosT) v = rope4(v, reinterpret_cast<const float4 *>(src)[((j0 + kHD / 2) % kHD) / 4], cosT + int64_t(p) * kHD + j0,
+                        sinT + int64_t(p) * kHD + j0, j0);
+    *reinterpret_cast<float4 *>(myQ + i * kHDp + j0) = v;
+  }
+  // key ranges: the workgroup's (staged) and this wave's (computed)
   const int klo = window < 0 ? 0 : max(0, pos0 - window);
-  const int khi = window < 0 ? n : min(n, pos0 + nq - 1 + window + 1);
-  const float scale = 1.0f / sqrtf(float(kHD));
-  float acc[8];
+  const int khi = window < 0 ? n : min(n, pos0 + nq + window);
+  const int qlo = pos0 + 16 * w, qhi = pos0 + min(16 * w + 16, nq);  // this wave's positions [qlo, qhi)
+  const int wlo = window < 0 ? 0 : max(0, qlo - window);
+  const int whi = window < 0 ? n : min(n, qhi - 1 + window + 1);
+  float4v acc[4];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-  float m = -FLT_MAX, l = 0.0f;
-  bool seen = false;
-  const int qpos = pos0 + r;
-  for (int k0 = klo; k0 < khi; k0 += kAT) {
-    const int cnt = min(kAT, khi - k0);
-    __syncthreads();
-    stage_rot(sK, 1, k0, cnt);
-    for (int e = tid; e < kAT * (kHD / 4); e += kT) {
-      const int i = e / (kHD / 4), c4 = e % (kHD / 4);
-      const float4 v = i < cnt ? *reinterpret_cast<const float4 *>(qkv + int64_t(srow + k0 + i) * ld + 2 * d + h * kHD + c4 * 4)
-                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      *reinterpret_cast<float4 *>(sV + i * kHD + c4 * 4) = v;
+  for (int b = 0; b < 4; ++b) acc[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+  float m[4], lsum[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    m[r] = -FLT_MAX;
+    lsum[r] = 0.0f;
+  }
+  float *myP = sP[w];
+  for (int k0 = (klo / kAT) * kAT; k0 < khi; k0 += kAT) {
+    __syncthreads();  // previous tile's readers are done
+    // stage K (rotated) and V^T for keys k0..k0+31, clamped to the sequence (masked below)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int e = tid + kAW * k, i = e >> 4, c4 = e & 15, j0 = c4 * 4;
+      const int p = min(k0 + i, n - 1);
+      const float *src = qkv + int64_t(srow + p) * ld + d + h * kHD;
+      float4 kv = reinterpret_cast<const float4 *>(src)[c4];
+      if (cosT) kv = rope4(kv, reinterpret_cast<const float4 *>(src)[((j0 + kHD / 2) % kHD) / 4],
+                           cosT + int64_t(p) * kHD + j0, sinT + int64_t(p) * kHD + j0, j0);
+      *reinterpret_cast<float4 *>(sK + i * kHDp + j0) = kv;
+      const float4 vv = reinterpret_cast<const float4 *>(src + d)[c4];
+      sVT[(j0 + 0) * kVTp + i] = vv.x;
+      sVT[(j0 + 1) * kVTp + i] = vv.y;
+      sVT[(j0 + 2) * kVTp + i] = vv.z;
+      sVT[(j0 + 3) * kVTp + i] = vv.w;
     }
     __syncthreads();
-    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 4
-    for (int dd = 0; dd < kHD; dd += 4) {
-      const float4 q = *reinterpret_cast<const float4 *>(sQ + r * kHDp + dd);
+    if (wq <= 0 || k0 >= whi || k0 + kAT <= wlo) continue;  // wave-uniform: nothing visible here
+    float4v s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float4 k = *reinterpret_cast<const float4 *>(sK + (sub + 8 * i) * kHDp + dd);
-        s[i] = fmaf(q.x, k.x, s[i]);
-        s[i] = fmaf(q.y, k.y, s[i]);
-        s[i] = fmaf(q.z, k.z, s[i]);
-        s[i] = fmaf(q.w, k.w, s[i]);
+    for (int g = 0; g < 4; ++g) {
+      const float4 qg = *reinterpret_cast<const float4 *>(myQ + li * kHDp + 16 * g + 4 * kg);
+      const float4 ka = *reinterpret_cast<const float4 *>(sK + li * kHDp + 16 * g + 4 * kg);
+      const float4 kb = *reinterpret_cast<const float4 *>(sK + (16 + li) * kHDp + 16 * g + 4 * kg);
+      s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.x, ka.x, s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.x, kb.x, s1, 0, 0, 0);
+      s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.y, ka.y, s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.y, kb.y, s1, 0, 0, 0);
+      s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.z, ka.z, s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.z, kb.z, s1, 0, 0, 0);
+      s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.w, ka.w, s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.w, kb.w, s1, 0, 0, 0);
+    }
+    const int key0 = k0 + li, key1 = key0 + 16;
+    float corr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 4 * kg + r, qpos = qlo + row;
+      const bool rv = row < wq;
+      const bool ok0 = rv && key0 < n && (window < 0 || (key0 - qpos <= window && qpos - key0 <= window));
+      const bool ok1 = rv && key1 < n && (window < 0 || (key1 - qpos <= window && qpos - key1 <= window));
+      const float a = s0[r] * 0.125f, b = s1[r] * 0.125f;
+      const float mt = row_max16(fmaxf(ok0 ? a : -FLT_MAX, ok1 ? b : -FLT_MAX));
+      const float mn = fmaxf(m[r], mt);
+      const float p0 = ok0 ? expf(a - mn) : 0.0f, p1 = ok1 ? expf(b - mn) : 0.0f;
+      const float ps = row_sum(p0 + p1);
+      corr[r] = 1.0f;
+      if (mt > -FLT_MAX) {
+        corr[r] = m[r] > -FLT_MAX ? expf(m[r] - mn) : 0.0f;
+        lsum[r] = lsum[r] * corr[r] + ps;
+        m[r] = mn;
       }
+      myP[row * kPp + li] = p0;
+      myP[row * kPp + 16 + li] = p1;
     }
-    bool ok[4];
-    float mt = -FLT_MAX;
+    if (__any(corr[0] != 1.0f || corr[1] != 1.0f || corr[2] != 1.0f || corr[3] != 1.0f)) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = k0 + sub + 8 * i;
-      ok[i] = sub + 8 * i < cnt && r < nq && (window < 0 || (key - qpos <= window && qpos - key <= window));
-      s[i] = s[i] * scale;
-      if (ok[i]) mt = fmaxf(mt, s[i]);
-    }
-    mt = fmaxf(mt, dpp_move<0xB1>(mt));
-    mt = fmaxf(mt, dpp_move<0x4E>(mt));
-    mt = fmaxf(mt, dpp_move<0x141>(mt));
-    const bool any = mt > -FLT_MAX;
-    const float mn = fmaxf(m, mt);
-    float p[4], ps = 0.0f;
+      for (int b = 0; b < 4; ++b)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      p[i] = ok[i] ? expf(s[i] - mn) : 0.0f;
-      ps += p[i];
-    }
-    ps = group8_sum(ps);
-    if (any) {
-      const float corr = seen ? expf(m - mn) : 0.0f;
-      l = l * corr + ps;
-      m = mn;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] *= corr;
-      seen = true;
+        for (int r = 0; r < 4; ++r) acc[b][r] *= corr[r];
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sP[r * 33 + sub + 8 * i] = p[i];
-    __syncthreads();
-    for (int c = 0; c < cnt; ++c) {
-      const float pc = sP[r * 33 + c];
-      const float4 v0 = *reinterpret_cast<const float4 *>(sV + c * kHD + sub * 4);
-      const float4 v1 = *reinterpret_cast<const float4 *>(sV + c * kHD + 32 + sub * 4);
-      acc[0] = fmaf(pc, v0.x, acc[0]);
-      acc[1] = fmaf(pc, v0.y, acc[1]);
-      acc[2] = fmaf(pc, v0.z, acc[2]);
-      acc[3] = fmaf(pc, v0.w, acc[3]);
-      acc[4] = fmaf(pc, v1.x, acc[4]);
-      acc[5] = fmaf(pc, v1.y, acc[5]);
-      acc[6] = fmaf(pc, v1.z, acc[6]);
-      acc[7] = fmaf(pc, v1.w, acc[7]);
+    for (int u = 0; u < 2; ++u) {
+      const float4 pa = *reinterpret_cast<const float4 *>(myP + li * kPp + 16 * u + 4 * kg);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const float4 vb = *reinterpret_cast<const float4 *>(sVT + (16 * b + li) * kVTp + 16 * u + 4 * kg);
+        acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.x, vb.x, acc[b], 0, 0, 0);
+        acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.y, vb.y, acc[b], 0, 0, 0);
+        acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.z, vb.z, acc[b], 0, 0, 0);
+        acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.w, vb.w, acc[b], 0, 0, 0);
+      }
     }
   }
-  if (r >= nq) return;
-  const float inv = 1.0f / l;
-  const int64_t base = int64_t(row0 + r) * d + h * kHD;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int dd = (e < 4 ? 0 : 32) + sub * 4 + (e & 3);
-    const float o = acc[e] * inv;
-    const _Float16 hh = _Float16(o);
-    y[base + dd] = hh;
-    if (ylo) ylo[base + dd] = _Float16(o - float(hh));
+  for (int r = 0; r < 4; ++r) {
+    const int row = 4 * kg + r;
+    if (row >= wq) continue;
+    const float inv = 1.0f / lsum[r];
+    const int64_t base = int64_t(row0 + 16 * w + row) * d + h * kHD;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const float o = acc[b][r] * inv;
+      const _Float16 hh = _Float16(o);
+      y[base + 16 * b + li] = hh;
+      if (ylo) ylo[base + 16 * b + li] = _Float16(o - float(hh));
+    }
   }
 }
 
@@ -289,7 +312,7 @@ void launch_laya_attn(const float *qkv, int d, int hd, int window, const float *
   LG_REQUIRE(hd == kHD, "laya attention: head_dim %d (kernel is built for 64)", hd);
   LG_REQUIRE(ntiles > 0 && d % kHD == 0 && d >= kHD, "laya attention: bad shape");
   LG_REQUIRE((cosT == nullptr) == (sinT == nullptr), "laya attention: RoPE needs both tables");
-  hipLaunchKernelGGL(laya_attn_kernel, dim3(ntiles, d / kHD), dim3(kT), 0, st, qkv, d, window, cosT, sinT, tile_row0,
+  hipLaunchKernelGGL(laya_attn_kernel, dim3(ntiles, d / kHD), dim3(kAW), 0, st, qkv, d, window, cosT, sinT, tile_row0,
                      tile_pos0, tile_n, tile_seq, seq_n, y, ylo);
   HIP_CHECK(hipGetLastError());
 }

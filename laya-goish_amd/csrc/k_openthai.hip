@@ -424,19 +424,10 @@ __global__ __launch_bounds__(256, 1) void ot_attn_kernel(const float *__restrict
 //   Online softmax per row (16-lane DPP row reductions); P goes through LDS to the A layout.
 //   O += P V over keys 16u + 4kg + c (V transposed in LDS, so again one float4 per 4 MFMAs).
 // Partial (m, l, O) per item and head; ot_attn_combine_kernel merges an item's key ranges.
-typedef float float4v __attribute__((ext_vector_type(4)));
 constexpr int kQT = 16;    // query rows per item
 constexpr int kKC = 256;   // keys per item
 constexpr int kVTp = 36;   // padded row of the transposed V tile [256 dims][32 keys]
 constexpr int kPp = 36;    // padded row of the P tile [16 rows][32 keys]
-
-__device__ __forceinline__ float row_max16(float v) {
-  v = fmaxf(v, dpp_move<0xB1>(v));
-  v = fmaxf(v, dpp_move<0x4E>(v));
-  v = fmaxf(v, dpp_move<0x141>(v));
-  v = fmaxf(v, dpp_move<0x140>(v));
-  return v;
-}
 
 // One 32-key tile of K rows and V rows (from the projection) for 256 threads, 8 float4 each;
 // keys past khi are clamped to khi - 1 (masked by the caller).

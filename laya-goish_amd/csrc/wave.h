@@ -47,6 +47,18 @@ __device__ __forceinline__ float row_sum(float v) {
   return v;
 }
 
+// Maximum over each 16-lane row (every lane of the row receives it).
+__device__ __forceinline__ float row_max16(float v) {
+  v = fmaxf(v, dpp_move<0xB1>(v));
+  v = fmaxf(v, dpp_move<0x4E>(v));
+  v = fmaxf(v, dpp_move<0x141>(v));
+  v = fmaxf(v, dpp_move<0x140>(v));
+  return v;
+}
+
+// Native 4-float vector (register operand of the 16x16x4 f32 MFMA; copies stay in registers).
+typedef float float4v __attribute__((ext_vector_type(4)));
+
 // Sum over each 32-lane half of the wave; valid in rows 1 and 3 (lanes 16-31 and 48-63).
 __device__ __forceinline__ float half_sum_odd_rows(float v) {
   v = row_sum(v);
