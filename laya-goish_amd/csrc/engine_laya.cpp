@@ -236,10 +236,11 @@ void Engine::run_laya(BatchPlan &b, const int32_t *qtype_dev, lg_cancel_fn cance
   auto attention = [&](const LayaLayer &y, bool rope) {
     gemm(x16, x16lo, T, y.qkv.w, Epi::F32, qkv, nullptr, nullptr, 3 * d, y.qkv.b);
     prof.begin("laya_attn", stream);
-    const float *cs = !rope ? nullptr : y.full ? laya_cos_full_ : laya_cos_slide_;
-    const float *sn = !rope ? nullptr : y.full ? laya_sin_full_ : laya_sin_slide_;
-    launch_laya_attn(qkv, d, hd, y.full ? -1 : 64, cs, sn, b.tile_row0, b.tile_pos0, b.tile_n, b.tile_seq, b.seq_n,
-                     b.ntiles, att, attlo, stream);
+    if (rope)
+      launch_laya_rope(qkv, T, d, hd, y.full ? laya_cos_full_ : laya_cos_slide_, y.full ? laya_sin_full_ : laya_sin_slide_,
+                       b.tok_pos, stream);
+    launch_laya_attn(qkv, d, hd, y.full ? -1 : 64, b.tile_row0, b.tile_pos0, b.tile_n, b.tile_seq, b.seq_n, b.ntiles,
+                     att, attlo, stream);
     prof.end(0, 0, stream);
     gemm(att, attlo, T, y.wo.w, Epi::ADD, h, nullptr, nullptr, d, y.wo.b);
   };

@@ -85,67 +85,88 @@ __global__ __launch_bounds__(kT) void layer_norm_kernel(const float *__restrict_
   }
 }
 
-// Bidirectional attention over q|k|v rows [T][3d] (f32), head dim 64, on v_mfma_f32_16x16x4_f32
-// (f32 operands and accumulation).  One workgroup per (32-query tile of one sequence, head), two
-// waves of 16 query rows each.  Keys j with |i - j| <= window (window < 0: the whole sequence);
-// RoPE from tables [pos][64] (pairs j, j + 32) applied as Q and K tiles are staged in LDS; scores
-// q.k * (1/sqrt(64)); online softmax in f32.  Output f16 planes [T][d].
-//   S = Q K^T per 32-key tile: lane (li = l%16, kg = l/16) supplies Q[li][16g + 4kg + c] at step
-//   4g + c (a permutation of the 64-dim contraction, applied to K alike, so every operand is one
-//   float4 LDS read per 4 MFMAs); D layout: lane l holds S[4kg + r][16 blk + li], r < 4.
-//   Online softmax per row with 16-lane DPP reductions; P goes through LDS into the A layout;
-//   O += P V with V transposed in LDS.
-constexpr int kHD = 64, kAT = 32, kHDp = kHD + 4;
-constexpr int kVTp = 36;  // padded row of the transposed V tile [64 dims][32 keys]
-constexpr int kPp = 36;   // padded row of the P tile [16 rows][32 keys]
-constexpr int kAW = 128;  // two waves
+constexpr int kHD = 64;
 
-// RoPE of one float4 of a row (dims j0..j0+3) given the partner float4 (dims j0+32.. mod 64).
-__device__ __forceinline__ float4 rope4(float4 v, float4 o, const float *cs, const float *sn, int j0) {
-  const float a[4] = {v.x, v.y, v.z, v.w}, b[4] = {o.x, o.y, o.z, o.w};
-  float out[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) out[k] = j0 < kHD / 2 ? a[k] * cs[k] - b[k] * sn[k] : a[k] * cs[k] + b[k] * sn[k];
-  return make_float4(out[0], out[1], out[2], out[3]);
+// RoPE in place on the q and k parts of q|k|v rows [T][3d] (model.rs:336-350 rotates q and k
+// before attention): pairs (j, j + 32) of every 64-wide head, angle tables [pos][64].
+__global__ __launch_bounds__(kT) void laya_rope_kernel(float *__restrict__ qkv, int d, const float *__restrict__ cosT,
+                                                       const float *__restrict__ sinT,
+                                                       const int32_t *__restrict__ tok_pos) {
+  const int t = blockIdx.x;
+  const int p = tok_pos[t];
+  float *row = qkv + int64_t(t) * 3 * d;
+  const float *cs = cosT + int64_t(p) * kHD, *sn = sinT + int64_t(p) * kHD;
+  for (int e = threadIdx.x; e < d; e += kT) {  // 2 parts x (d / 64) heads x 32 pairs
+    const int part = e / (d / 2), rem = e % (d / 2), hh = rem / 32, j = rem % 32;
+    float *x = row + part * d + hh * kHD;
+    const float a = x[j], b = x[j + 32];
+    x[j] = a * cs[j] - b * sn[j];
+    x[j + 32] = b * cs[j + 32] + a * sn[j + 32];
+  }
 }
 
-__global__ __launch_bounds__(kAW) void laya_attn_kernel(const float *__restrict__ qkv, int d, int window,
-                                                        const float *__restrict__ cosT, const float *__restrict__ sinT,
+// Bidirectional attention over q|k|v rows [T][3d] (f32, q and k already rotated), head dim 64,
+// on v_mfma_f32_16x16x4_f32 (f32 operands and accumulation).  One workgroup per (16 query rows of
+// one sequence, head); its four waves split the visible keys into four ranges of 16-key blocks
+// and merge their (m, l, O) in LDS at the end.  Keys j with |i - j| <= window (window < 0: the
+// whole sequence); scores q.k * (1/sqrt(64)); online softmax in f32.  Output f16 planes [T][d].
+//   S = Q K^T per block: lane (li = l%16, kg = l/16) supplies Q[li][16g + 4kg + c] at step 4g + c
+//   (a permutation of the 64-dim contraction, applied to K alike); operands come straight from
+//   the q|k|v rows as float4 loads, the next block's K and V prefetched in registers.
+//   D layout: lane l holds S[4kg + r][li], r < 4.  P goes through LDS into the A layout;
+//   O += P V with V[4kg + c][16b + li] as the B operand.
+constexpr int kPp = 20;  // padded row of a wave's P block [16 rows][16 keys]
+constexpr int kOp = 68;  // padded row of a wave's partial O [16 rows][64]
+
+struct KVBlock {
+  float4v k[4];
+  float v[16];
+};
+
+__device__ __forceinline__ void laya_load_kv(KVBlock &blk, const float *__restrict__ kbase, int ld, int d, int k0,
+                                             int n, int li, int kg) {
+  const float *kr = kbase + int64_t(min(k0 + li, n - 1)) * ld;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) blk.k[g] = *reinterpret_cast<const float4v *>(kr + 16 * g + 4 * kg);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const float *vr = kbase + int64_t(min(k0 + 4 * kg + c, n - 1)) * ld + d;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) blk.v[4 * b + c] = vr[16 * b + li];
+  }
+}
+
+__global__ __launch_bounds__(256) void laya_attn_kernel(const float *__restrict__ qkv, int d, int window,
                                                         const int32_t *__restrict__ tile_row0,
                                                         const int32_t *__restrict__ tile_pos0,
                                                         const int32_t *__restrict__ tile_n,
                                                         const int32_t *__restrict__ seq_of_tile,
                                                         const int32_t *__restrict__ seq_n,
                                                         _Float16 *__restrict__ y, _Float16 *__restrict__ ylo) {
-  __shared__ __align__(16) float sK[kAT * kHDp];      // [32 keys][68]
-  __shared__ __align__(16) float sVT[kHD * kVTp];     // [64 dims][36]
-  __shared__ __align__(16) float sQ[2][16 * kHDp];    // per wave [16 rows][68]
-  __shared__ __align__(16) float sP[2][16 * kPp];     // per wave [16 rows][36]
-  const int tile = blockIdx.x, h = blockIdx.y;
-  const int row0 = tile_row0[tile], pos0 = tile_pos0[tile], nq = tile_n[tile];
+  __shared__ __align__(16) float sP[4][16 * kPp];
+  __shared__ __align__(16) float sO[4][16 * kOp];
+  __shared__ float sML[4][16][2];
+  const int tile = blockIdx.x, h = blockIdx.y, z = blockIdx.z;
+  const int nsub = tile_n[tile] - 16 * z;  // rows of this 16-row half of the tile
+  if (nsub <= 0) return;                   // whole workgroup, before any barrier
+  const int row0 = tile_row0[tile] + 16 * z, pos0 = tile_pos0[tile] + 16 * z;
   const int n = seq_n[seq_of_tile[tile]];
   const int srow = row0 - pos0;
   const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, li = l & 15, kg = l >> 4;
   const int ld = 3 * d;
-  const int wq = nq - 16 * w;  // this wave's valid rows (may be <= 0)
-  // this wave's Q rows, rotated (rows past the tile repeat its last row and are never written)
-  float *myQ = sQ[w];
+  const float *kbase = qkv + int64_t(srow) * ld + d + h * kHD;  // key rows of the sequence
+  // Q operands: row li (rows past nsub repeat the last row and are never written)
+  float4v q[4];
+  {
+    const float *qr = qkv + int64_t(row0 + min(li, nsub - 1)) * ld + h * kHD;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int e = l + 64 * k, i = e >> 4, c4 = e & 15, j0 = c4 * 4;
-    const int p = pos0 + min(16 * w + i, nq - 1);
-    const float *src = qkv + int64_t(srow + p) * ld + h * kHD;
-    float4 v = reinterpret_cast<const float4 *>(src)[c4];
-    if (cosT) v = rope4(v, reinterpret_cast<const float4 *>(src)[((j0 + kHD / 2) % kHD) / 4], cosT + int64_t(p) * kHD + j0,
-                        sinT + int64_t(p) * kHD + j0, j0);
-    *reinterpret_cast<float4 *>(myQ + i * kHDp + j0) = v;
+    for (int g = 0; g < 4; ++g) q[g] = *reinterpret_cast<const float4v *>(qr + 16 * g + 4 * kg);
   }
-  // key ranges: the workgroup's (staged) and this wave's (computed)
-  const int klo = window < 0 ? 0 : max(0, pos0 - window);
-  const int khi = window < 0 ? n : min(n, pos0 + nq + window);
-  const int qlo = pos0 + 16 * w, qhi = pos0 + min(16 * w + 16, nq);  // this wave's positions [qlo, qhi)
-  const int wlo = window < 0 ? 0 : max(0, qlo - window);
-  const int whi = window < 0 ? n : min(n, qhi - 1 + window + 1);
+  // visible keys of the 16 rows, in 16-key blocks split over the four waves
+  const int wlo = window < 0 ? 0 : max(0, pos0 - window);
+  const int whi = window < 0 ? n : min(n, pos0 + nsub + window);
+  const int b0 = wlo / 16, nb = (whi + 15) / 16 - b0;
+  const int bw0 = b0 + (nb * w) / 4, bw1 = b0 + (nb * (w + 1)) / 4;
   float4v acc[4];
 #pragma unroll
   for (int b = 0; b < 4; ++b) acc[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
@@ -156,62 +177,36 @@ __global__ __launch_bounds__(kAW) void laya_attn_kernel(const float *__restrict_
     lsum[r] = 0.0f;
   }
   float *myP = sP[w];
-  for (int k0 = (klo / kAT) * kAT; k0 < khi; k0 += kAT) {
-    __syncthreads();  // previous tile's readers are done
-    // stage K (rotated) and V^T for keys k0..k0+31, clamped to the sequence (masked below)
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int e = tid + kAW * k, i = e >> 4, c4 = e & 15, j0 = c4 * 4;
-      const int p = min(k0 + i, n - 1);
-      const float *src = qkv + int64_t(srow + p) * ld + d + h * kHD;
-      float4 kv = reinterpret_cast<const float4 *>(src)[c4];
-      if (cosT) kv = rope4(kv, reinterpret_cast<const float4 *>(src)[((j0 + kHD / 2) % kHD) / 4],
-                           cosT + int64_t(p) * kHD + j0, sinT + int64_t(p) * kHD + j0, j0);
-      *reinterpret_cast<float4 *>(sK + i * kHDp + j0) = kv;
-      const float4 vv = reinterpret_cast<const float4 *>(src + d)[c4];
-      sVT[(j0 + 0) * kVTp + i] = vv.x;
-      sVT[(j0 + 1) * kVTp + i] = vv.y;
-      sVT[(j0 + 2) * kVTp + i] = vv.z;
-      sVT[(j0 + 3) * kVTp + i] = vv.w;
-    }
-    __syncthreads();
-    if (wq <= 0 || k0 >= whi || k0 + kAT <= wlo) continue;  // wave-uniform: nothing visible here
-    float4v s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
+  KVBlock cur, nxt;
+  if (bw0 < bw1) laya_load_kv(cur, kbase, ld, d, 16 * bw0, n, li, kg);
+  for (int bi = bw0; bi < bw1; ++bi) {
+    laya_load_kv(nxt, kbase, ld, d, 16 * min(bi + 1, bw1 - 1), n, li, kg);  // the last one reloads its own
+    float4v s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const float4 qg = *reinterpret_cast<const float4 *>(myQ + li * kHDp + 16 * g + 4 * kg);
-      const float4 ka = *reinterpret_cast<const float4 *>(sK + li * kHDp + 16 * g + 4 * kg);
-      const float4 kb = *reinterpret_cast<const float4 *>(sK + (16 + li) * kHDp + 16 * g + 4 * kg);
-      s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.x, ka.x, s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.x, kb.x, s1, 0, 0, 0);
-      s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.y, ka.y, s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.y, kb.y, s1, 0, 0, 0);
-      s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.z, ka.z, s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.z, kb.z, s1, 0, 0, 0);
-      s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.w, ka.w, s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.w, kb.w, s1, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x4f32(q[g][0], cur.k[g][0], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x4f32(q[g][1], cur.k[g][1], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x4f32(q[g][2], cur.k[g][2], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_16x16x4f32(q[g][3], cur.k[g][3], s, 0, 0, 0);
     }
-    const int key0 = k0 + li, key1 = key0 + 16;
+    const int key = 16 * bi + li;
     float corr[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = 4 * kg + r, qpos = qlo + row;
-      const bool rv = row < wq;
-      const bool ok0 = rv && key0 < n && (window < 0 || (key0 - qpos <= window && qpos - key0 <= window));
-      const bool ok1 = rv && key1 < n && (window < 0 || (key1 - qpos <= window && qpos - key1 <= window));
-      const float a = s0[r] * 0.125f, b = s1[r] * 0.125f;
-      const float mt = row_max16(fmaxf(ok0 ? a : -FLT_MAX, ok1 ? b : -FLT_MAX));
+      const int row = 4 * kg + r, qpos = pos0 + row;
+      const bool ok = row < nsub && key < n && (window < 0 || (key - qpos <= window && qpos - key <= window));
+      const float a = s[r] * 0.125f;
+      const float mt = row_max16(ok ? a : -FLT_MAX);
       const float mn = fmaxf(m[r], mt);
-      const float p0 = ok0 ? expf(a - mn) : 0.0f, p1 = ok1 ? expf(b - mn) : 0.0f;
-      const float ps = row_sum(p0 + p1);
+      const float p = ok ? expf(a - mn) : 0.0f;
+      const float ps = row_sum(p);
       corr[r] = 1.0f;
       if (mt > -FLT_MAX) {
         corr[r] = m[r] > -FLT_MAX ? expf(m[r] - mn) : 0.0f;
         lsum[r] = lsum[r] * corr[r] + ps;
         m[r] = mn;
       }
-      myP[row * kPp + li] = p0;
-      myP[row * kPp + 16 + li] = p1;
+      myP[row * kPp + li] = p;
     }
     if (__any(corr[0] != 1.0f || corr[1] != 1.0f || corr[2] != 1.0f || corr[3] != 1.0f)) {
 #pragma unroll
@@ -219,32 +214,48 @@ __global__ __launch_bounds__(kAW) void laya_attn_kernel(const float *__restrict_
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[b][r] *= corr[r];
     }
+    const float4v pa = *reinterpret_cast<const float4v *>(myP + li * kPp + 4 * kg);
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const float4 pa = *reinterpret_cast<const float4 *>(myP + li * kPp + 16 * u + 4 * kg);
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const float4 vb = *reinterpret_cast<const float4 *>(sVT + (16 * b + li) * kVTp + 16 * u + 4 * kg);
-        acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.x, vb.x, acc[b], 0, 0, 0);
-        acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.y, vb.y, acc[b], 0, 0, 0);
-        acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.z, vb.z, acc[b], 0, 0, 0);
-        acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.w, vb.w, acc[b], 0, 0, 0);
-      }
-    }
+      for (int b = 0; b < 4; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[c], cur.v[4 * b + c], acc[b], 0, 0, 0);
+    cur = nxt;
   }
+  // merge the four key ranges: O = sum_w e^(m_w - M) O_w / sum_w e^(m_w - M) l_w
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int row = 4 * kg + r;
-    if (row >= wq) continue;
-    const float inv = 1.0f / lsum[r];
-    const int64_t base = int64_t(row0 + 16 * w + row) * d + h * kHD;
+  for (int b = 0; b < 4; ++b)
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const float o = acc[b][r] * inv;
-      const _Float16 hh = _Float16(o);
-      y[base + 16 * b + li] = hh;
-      if (ylo) ylo[base + 16 * b + li] = _Float16(o - float(hh));
+    for (int r = 0; r < 4; ++r) sO[w][(4 * kg + r) * kOp + 16 * b + li] = acc[b][r];
+  if (li == 0)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sML[w][4 * kg + r][0] = m[r];
+      sML[w][4 * kg + r][1] = lsum[r];
     }
+  __syncthreads();
+  const int row = tid >> 4, d4 = (tid & 15) * 4;
+  if (row >= nsub) return;
+  float M = -FLT_MAX;
+#pragma unroll
+  for (int v = 0; v < 4; ++v)
+    if (sML[v][row][1] > 0.0f) M = fmaxf(M, sML[v][row][0]);
+  float L = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    if (!(sML[v][row][1] > 0.0f)) continue;
+    const float f = expf(sML[v][row][0] - M);
+    L += f * sML[v][row][1];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] += f * sO[v][row * kOp + d4 + e];
+  }
+  const float inv = 1.0f / L;
+  const int64_t base = int64_t(row0 + row) * d + h * kHD + d4;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float ov = o[e] * inv;
+    const _Float16 hh = _Float16(ov);
+    y[base + e] = hh;
+    if (ylo) ylo[base + e] = _Float16(ov - float(hh));
   }
 }
 
@@ -306,14 +317,21 @@ void launch_layer_norm(const float *x, const int32_t *rows, int nrows, int d, co
   HIP_CHECK(hipGetLastError());
 }
 
-void launch_laya_attn(const float *qkv, int d, int hd, int window, const float *cosT, const float *sinT,
-                      const int32_t *tile_row0, const int32_t *tile_pos0, const int32_t *tile_n, const int32_t *tile_seq,
-                      const int32_t *seq_n, int ntiles, _Float16 *y, _Float16 *ylo, hipStream_t st) {
+void launch_laya_rope(float *qkv, int T, int d, int hd, const float *cosT, const float *sinT, const int32_t *tok_pos,
+                      hipStream_t st) {
+  LG_REQUIRE(hd == kHD && T > 0 && d % kHD == 0 && cosT && sinT && tok_pos, "laya rope: bad shape");
+  hipLaunchKernelGGL(laya_rope_kernel, dim3(T), dim3(kT), 0, st, qkv, d, cosT, sinT, tok_pos);
+  HIP_CHECK(hipGetLastError());
+}
+
+void launch_laya_attn(const float *qkv, int d, int hd, int window, const int32_t *tile_row0, const int32_t *tile_pos0,
+                      const int32_t *tile_n, const int32_t *tile_seq, const int32_t *seq_n, int ntiles, _Float16 *y,
+                      _Float16 *ylo, hipStream_t st) {
   LG_REQUIRE(hd == kHD, "laya attention: head_dim %d (kernel is built for 64)", hd);
   LG_REQUIRE(ntiles > 0 && d % kHD == 0 && d >= kHD, "laya attention: bad shape");
-  LG_REQUIRE((cosT == nullptr) == (sinT == nullptr), "laya attention: RoPE needs both tables");
-  hipLaunchKernelGGL(laya_attn_kernel, dim3(ntiles, d / kHD), dim3(kAW), 0, st, qkv, d, window, cosT, sinT, tile_row0,
-                     tile_pos0, tile_n, tile_seq, seq_n, y, ylo);
+  // tiles hold at most 32 rows: two 16-row halves per tile (grid z)
+  hipLaunchKernelGGL(laya_attn_kernel, dim3(ntiles, d / kHD, 2), dim3(256), 0, st, qkv, d, window, tile_row0, tile_pos0,
+                     tile_n, tile_seq, seq_n, y, ylo);
   HIP_CHECK(hipGetLastError());
 }
 

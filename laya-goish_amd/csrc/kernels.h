@@ -199,9 +199,15 @@ void launch_layer_norm(const float *x, const int32_t *rows, int nrows, int d, co
 // Bidirectional attention over q|k|v rows [T][3d] (head dim 64), keys |i - j| <= window
 // (window < 0: all), RoPE from tables [pos][64] when cosT != nullptr; 32-token tiles (tile_*),
 // tile_seq -> sequence, seq_n -> its length.  Output f16 planes [T][d].
-void launch_laya_attn(const float *qkv, int d, int hd, int window, const float *cosT, const float *sinT,
-                      const int32_t *tile_row0, const int32_t *tile_pos0, const int32_t *tile_n, const int32_t *tile_seq,
-                      const int32_t *seq_n, int ntiles, _Float16 *y, _Float16 *ylo, hipStream_t st);
+// RoPE in place on the q and k parts of q|k|v rows [T][3d]: pairs (j, j + 32) of each head,
+// tables [pos][hd], row positions tok_pos[T].
+void launch_laya_rope(float *qkv, int T, int d, int hd, const float *cosT, const float *sinT, const int32_t *tok_pos,
+                      hipStream_t st);
+// Bidirectional attention over rotated q|k|v rows of fresh sequences in tiles of <= 32 rows;
+// window < 0: all keys of the sequence.  Output f16 planes [T][d].
+void launch_laya_attn(const float *qkv, int d, int hd, int window, const int32_t *tile_row0, const int32_t *tile_pos0,
+                      const int32_t *tile_n, const int32_t *tile_seq, const int32_t *seq_n, int ntiles, _Float16 *y,
+                      _Float16 *ylo, hipStream_t st);
 void launch_gelu_inplace(float *x, int64_t n, hipStream_t st);
 // pooled[s] = [h[seq_row0[s]] (d), top1, top1 - top2, entropy, max(k,2)/255] over the option
 // logits logits[lg_first[s] .. + lg_count[s]] (model.rs:392-403).
