@@ -17,10 +17,14 @@ void launch_kind(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix 
     if (launch_gemm_q8_exact(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
   } else if constexpr (KIND == LG_F16) {
     // fewer 128 x 128 tiles than CUs (short prefills, narrow outputs): 64 x 128 tiles, twice
-    // the workgroups; the per-element K order is the same, so the results are too
+    // the workgroups, and 128-deep K steps when K allows (half the load round trips of these
+    // latency-bound launches); the per-element K order is the same, so the results are too
     const bool glu = epi == Epi::SWIGLU || epi == Epi::GEGLU;
     const int outN = glu ? W.rows / 2 : W.rows;
     const int64_t tiles = int64_t((M + 127) / 128) * (outN / (glu ? 64 : 128));
+    if (tiles < 256 && W.cols % 128 == 0 &&
+        launch_cfg<KIND, SPLIT, 128, 1, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st))
+      return;
     if (tiles < 256 && launch_cfg<KIND, SPLIT, 64, 1, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
     if (launch_cfg<KIND, SPLIT, 64, 2, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
   } else {
