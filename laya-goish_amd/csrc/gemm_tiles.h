@@ -405,7 +405,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
   constexpr int BMW = CF::kBM, BNT = CF::kBN, LDK = CF::kLDK;
   constexpr bool kSplitA = CF::kSplitA, kSplitB = CF::kSplitB;
   constexpr bool kScaled = MODE == SPLIT && KIND == LG_Q8_0;
-  static_assert(WTN % 2 == 0, "SwiGLU pairs gate and up blocks inside a wave");
+  static_assert(WTN % 2 == 0 || (EPI != int(Epi::SWIGLU) && EPI != int(Epi::GEGLU)),
+                "gated epilogues pair gate and up blocks inside a wave");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -539,6 +540,7 @@ bool launch_cfg(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &
                 _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st) {
   using CF = Cfg<MODE, BK, WTM, WTN, STAGES>;
   const bool glu = epi == Epi::SWIGLU || epi == Epi::GEGLU;
+  if (glu && WTN % 2) return false;  // gated epilogues need gate and up blocks in one wave
   const int outN = glu ? W.rows / 2 : W.rows;
   const int tileN = glu ? CF::kBN / 2 : CF::kBN;
   if (outN % tileN) return false;
@@ -580,8 +582,12 @@ bool launch_cfg(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &
       case Epi::F32: LAUNCH(0); break;
       case Epi::ADD: LAUNCH(1); break;
       case Epi::F16: LAUNCH(2); break;
-      case Epi::SWIGLU: LAUNCH(3); break;
-      case Epi::GEGLU: LAUNCH(4); break;
+      case Epi::SWIGLU:
+        if constexpr (WTN % 2 == 0) LAUNCH(3);
+        break;
+      case Epi::GEGLU:
+        if constexpr (WTN % 2 == 0) LAUNCH(4);
+        break;
       case Epi::RELU16: LAUNCH(5); break;
     }
     m0 += Mc;

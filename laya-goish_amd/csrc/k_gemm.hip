@@ -22,6 +22,10 @@ void launch_kind(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix 
     const bool glu = epi == Epi::SWIGLU || epi == Epi::GEGLU;
     const int outN = glu ? W.rows / 2 : W.rows;
     const int64_t tiles = int64_t((M + 127) / 128) * (outN / (glu ? 64 : 128));
+    // a handful of 64 x 128 tiles (a few dozen rows, narrow outputs): 64 x 64 tiles, twice again
+    if (!glu && (M + 63) / 64 * (outN / 128) < 64 && W.cols % 128 == 0 &&
+        launch_cfg<KIND, SPLIT, 128, 1, 1, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st))
+      return;
     if (tiles < 256 && W.cols % 128 == 0 &&
         launch_cfg<KIND, SPLIT, 128, 1, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st))
       return;
