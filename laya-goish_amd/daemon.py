@@ -20,7 +20,8 @@ The tokenizer is not on this path, so requests carry token ids where the referen
 A criterion may also be a bare list of description ids.  Answers follow decision.rs:297-389:
 choice -> probabilities by option, confidence, choice, abstain; score -> probabilities by level,
 confidence, score, legend (level -> description ids); noul -> noul (P(yes)); plus usage and the
-echoed id.
+echoed id.  A Laya encoder's answers follow laya/decision.rs:213-289 instead: every kind carries
+confidence, probabilities and action.act_probability (no abstain).
 
 A body with "states": [state, ...] instead of "state" is a /v1/decide/batch request
 (src/server.rs:235-258): one result per state, every pass of every state run as GPU batches.
@@ -107,6 +108,21 @@ def answer_json(model_name, req, labels, res, t0) -> dict:
     answers = {}
     for (qid, kind, names, opts), a in zip(labels, res["answers"]):
         p = [float(x) for x in a["probabilities"]]
+        if "act_probability" in a:  # Laya encoder answers (src/models/laya/decision.rs:213-289)
+            ans = {"type": kind}
+            if kind == "choice":
+                ans["choice"] = names[a["choice"]]
+            elif kind == "score":
+                ans["score"] = a["score"]
+                ans["legend"] = {str(j): o["desc"] if o["desc"] else str(j) for j, o in enumerate(opts)}
+            else:
+                ans["noul"] = p[1]
+            ans["confidence"] = a["confidence"]
+            keys = [str(j) for j in range(len(p))] if kind == "score" else ["false", "true"] if kind == "noul" else names
+            ans["probabilities"] = dict(zip(keys, p))
+            ans["action"] = {"act_probability": a["act_probability"]}
+            answers[qid] = ans
+            continue
         if kind == "noul":
             answers[qid] = {"type": kind, "noul": p[1]}
             continue

@@ -154,3 +154,41 @@ def test_serve_registry_routes_per_model(lh, tmp_path):
         ids = [o["id"] for o in answered if o["model"] == m]
         assert ids == sorted(ids)  # in order within one model
     assert any("unknown model missing" in o.get("error", "") for o in outs)
+
+
+class LayaScoredEngine:
+    """Laya encoder stand-in: seeded option and act logits scored by lg_laya_decide_scores."""
+
+    def __init__(self, lh, gguf, seed=0):
+        self.lh, self.g, self.rng = lh, gguf, np.random.default_rng(seed)
+
+    def decide(self, treq):
+        ks = [len(q["options"]) for q in treq["questions"]]
+        logits = self.rng.normal(size=sum(ks)).astype(np.float32)
+        act = self.rng.normal(size=(len(ks), 2)).astype(np.float32)
+        return self.lh.laya_decide_scores(self.g, treq, logits, act)
+
+    def decide_batch(self, treqs):
+        return [self.decide(t) for t in treqs]
+
+    def layers(self):
+        return 4
+
+    def close(self):
+        pass
+
+
+def test_daemon_laya_answer_shape(lh):
+    """A Laya encoder's answers carry confidence, probabilities and action.act_probability for every
+    kind, noul probabilities keyed false/true (src/models/laya/decision.rs:213-289)."""
+    eng = LayaScoredEngine(lh, lh.Gguf.from_bytes(lh.SynthImage("laya-tiny", seed=7)))
+    req = {k: v for k, v in REQ.items() if k != "permutations"}
+    o, = run([json.dumps(req)], eng)
+    topic, urg, human = o["answers"]["topic"], o["answers"]["urgency"], o["answers"]["human"]
+    for a in (topic, urg, human):
+        assert 0 <= a["action"]["act_probability"] <= 1 and 0 <= a["confidence"] <= 1
+        assert abs(sum(a["probabilities"].values()) - 1) < 1e-5 and "abstain" not in a
+    assert topic["choice"] == max(topic["probabilities"], key=topic["probabilities"].get)
+    assert set(urg["probabilities"]) == {"0", "1", "2"} and urg["legend"] == {"0": [16], "1": [17], "2": [18, 19]}
+    assert set(human["probabilities"]) == {"false", "true"} and human["noul"] == human["probabilities"]["true"]
+    assert human["confidence"] == pytest.approx(max(human["noul"], 1 - human["noul"]), abs=1e-6)
