@@ -106,17 +106,38 @@ __global__ __launch_bounds__(kT) void laya_rope_kernel(float *__restrict__ qkv, 
 }
 
 // Bidirectional attention over q|k|v rows [T][3d] (f32, q and k already rotated), head dim 64,
-// on v_mfma_f32_16x16x4_f32 (f32 operands and accumulation).  One workgroup per (16 query rows of
+// on v_mfma_f32_16x16x16_f16 with every f32 operand split into f16 hi + lo parts and three
+// products per pair (lo*hi, hi*lo, hi*hi; the lo*lo term is below f32 rounding), f32
+// accumulation.  One workgroup per (16 query rows of
 // one sequence, head); its four waves split the visible keys into four ranges of 16-key blocks
 // and merge their (m, l, O) in LDS at the end.  Keys j with |i - j| <= window (window < 0: the
 // whole sequence); scores q.k * (1/sqrt(64)); online softmax in f32.  Output f16 planes [T][d].
-//   S = Q K^T per block: lane (li = l%16, kg = l/16) supplies Q[li][16g + 4kg + c] at step 4g + c
-//   (a permutation of the 64-dim contraction, applied to K alike); operands come straight from
-//   the q|k|v rows as float4 loads, the next block's K and V prefetched in registers.
-//   D layout: lane l holds S[4kg + r][li], r < 4.  P goes through LDS into the A layout;
-//   O += P V with V[4kg + c][16b + li] as the B operand.
+//   S = Q K^T per block: lane (li = l%16, kg = l/16) supplies Q[li][16g + 4kg + c], c < 4, as the
+//   A operand of k-step g (a permutation of the 64-dim contraction, applied to K alike); operands
+//   come straight from the q|k|v rows as float4 loads, the next block's K and V prefetched in
+//   registers.
+//   D layout: lane l holds S[4kg + r][li], r < 4.  P goes through LDS into the A layout
+//   (P[li][4kg + c]); O += P V with V[4kg + c][16b + li], c < 4, as the B operand.
 constexpr int kPp = 20;  // padded row of a wave's P block [16 rows][16 keys]
 constexpr int kOp = 68;  // padded row of a wave's partial O [16 rows][64]
+
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+
+// x = hi + lo with hi = f16(x), lo = f16(x - hi): ~22 significant bits
+__device__ __forceinline__ void split_hl(float4v x, half4v &hi, half4v &lo) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const _Float16 h = _Float16(x[c]);
+    hi[c] = h;
+    lo[c] = _Float16(x[c] - float(h));
+  }
+}
+
+__device__ __forceinline__ float4v mfma3(half4v ah, half4v al, half4v bh, half4v bl, float4v acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x16f16(al, bh, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bl, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(ah, bh, acc, 0, 0, 0);
+}
 
 struct KVBlock {
   float4v k[4];
@@ -156,11 +177,11 @@ __global__ __launch_bounds__(256) void laya_attn_kernel(const float *__restrict_
   const int ld = 3 * d;
   const float *kbase = qkv + int64_t(srow) * ld + d + h * kHD;  // key rows of the sequence
   // Q operands: row li (rows past nsub repeat the last row and are never written)
-  float4v q[4];
+  half4v qh[4], ql[4];
   {
     const float *qr = qkv + int64_t(row0 + min(li, nsub - 1)) * ld + h * kHD;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) q[g] = *reinterpret_cast<const float4v *>(qr + 16 * g + 4 * kg);
+    for (int g = 0; g < 4; ++g) split_hl(*reinterpret_cast<const float4v *>(qr + 16 * g + 4 * kg), qh[g], ql[g]);
   }
   // visible keys of the 16 rows, in 16-key blocks split over the four waves
   const int wlo = window < 0 ? 0 : max(0, pos0 - window);
@@ -184,10 +205,9 @@ __global__ __launch_bounds__(256) void laya_attn_kernel(const float *__restrict_
     float4v s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      s = __builtin_amdgcn_mfma_f32_16x16x4f32(q[g][0], cur.k[g][0], s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_16x16x4f32(q[g][1], cur.k[g][1], s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_16x16x4f32(q[g][2], cur.k[g][2], s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_16x16x4f32(q[g][3], cur.k[g][3], s, 0, 0, 0);
+      half4v kh, kl;
+      split_hl(cur.k[g], kh, kl);
+      s = mfma3(qh[g], ql[g], kh, kl, s);
     }
     const int key = 16 * bi + li;
     float corr[4];
@@ -214,11 +234,14 @@ __global__ __launch_bounds__(256) void laya_attn_kernel(const float *__restrict_
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[b][r] *= corr[r];
     }
-    const float4v pa = *reinterpret_cast<const float4v *>(myP + li * kPp + 4 * kg);
+    half4v ph, pl;
+    split_hl(*reinterpret_cast<const float4v *>(myP + li * kPp + 4 * kg), ph, pl);
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int b = 0; b < 4; ++b) acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[c], cur.v[4 * b + c], acc[b], 0, 0, 0);
+    for (int b = 0; b < 4; ++b) {
+      half4v vh, vl;
+      split_hl(float4v{cur.v[4 * b], cur.v[4 * b + 1], cur.v[4 * b + 2], cur.v[4 * b + 3]}, vh, vl);
+      acc[b] = mfma3(ph, pl, vh, vl, acc[b]);
+    }
     cur = nxt;
   }
   // merge the four key ranges: O = sum_w e^(m_w - M) O_w / sum_w e^(m_w - M) l_w
