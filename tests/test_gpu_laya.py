@@ -144,3 +144,18 @@ def test_decide_batch_and_budget_split(tiny, lh):
             assert np.array_equal(x["probabilities"], y["probabilities"])
             assert np.array_equal(x["probabilities"], z["probabilities"])
             assert x["act_probability"] == y["act_probability"] == z["act_probability"]
+
+
+def test_large_batch_equals_single(tiny):
+    """64 inputs of 512 tokens (the GEMMs then take 128 x 128 tiles, the attention 12,288
+    workgroups) give the results of each input alone bit for bit, and match the oracle."""
+    prec, eng, om = tiny
+    rng = np.random.default_rng(21)
+    inputs = [(rng.integers(0, 1000, 512), sorted(rng.choice(512, 4, replace=False).tolist()), i % 3) for i in range(64)]
+    print(f"laya-tiny prec {prec}: 64 x 512 batch", flush=True)
+    batch = eng.laya_forward(inputs)
+    for i in (0, 17, 63):
+        (sl, sa), = eng.laya_forward([inputs[i]])
+        assert np.array_equal(batch[i][0], sl) and np.array_equal(batch[i][1], sa)
+        wl, wa = om.forward(*inputs[i])
+        assert np.abs(sl - wl).max() <= TOL[prec] and np.abs(sa - wa).max() <= TOL[prec]
