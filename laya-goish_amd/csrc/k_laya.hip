@@ -111,7 +111,8 @@ __global__ __launch_bounds__(kT) void laya_rope_kernel(float *__restrict__ qkv, 
 // accumulation.  One workgroup per (16 query rows of
 // one sequence, head); its four waves split the visible keys into four ranges of 16-key blocks
 // and merge their (m, l, O) in LDS at the end.  Keys j with |i - j| <= window (window < 0: the
-// whole sequence); scores q.k * (1/sqrt(64)); online softmax in f32.  Output f16 planes [T][d].
+// whole sequence); scores q.k * (1/sqrt(64)); online softmax in f32 (base 2).  Output f16
+// planes [T][d].
 //   S = Q K^T per block: lane (li = l%16, kg = l/16) supplies Q[li][16g + 4kg + c], c < 4, as the
 //   A operand of k-step g (a permutation of the 64-dim contraction, applied to K alike); operands
 //   come straight from the q|k|v rows as float4 loads, the next block's K and V prefetched in
@@ -119,6 +120,9 @@ __global__ __launch_bounds__(kT) void laya_rope_kernel(float *__restrict__ qkv, 
 //   D layout: lane l holds S[4kg + r][li], r < 4.  P goes through LDS into the A layout
 //   (P[li][4kg + c]); O += P V with V[4kg + c][16b + li], c < 4, as the B operand.
 constexpr int kPp = 20;  // padded row of a wave's P block [16 rows][16 keys]
+// scores are kept as log2(e) q.k / 8 and exponentiated with the hardware exp2 (v_exp_f32,
+// ~1 ulp): softmax is invariant to the base, and exp2 of a difference costs one instruction
+constexpr float kScoreLog2 = 0.125f * 1.44269504088896341f;
 constexpr int kOp = 68;  // padded row of a wave's partial O [16 rows][64]
 
 typedef _Float16 half4v __attribute__((ext_vector_type(4)));
@@ -215,14 +219,14 @@ __global__ __launch_bounds__(256) void laya_attn_kernel(const float *__restrict_
     for (int r = 0; r < 4; ++r) {
       const int row = 4 * kg + r, qpos = pos0 + row;
       const bool ok = row < nsub && key < n && (window < 0 || (key - qpos <= window && qpos - key <= window));
-      const float a = s[r] * 0.125f;
+      const float a = s[r] * kScoreLog2;  // q.k / sqrt(64) in base-2 units
       const float mt = row_max16(ok ? a : -FLT_MAX);
       const float mn = fmaxf(m[r], mt);
-      const float p = ok ? expf(a - mn) : 0.0f;
+      const float p = ok ? __builtin_amdgcn_exp2f(a - mn) : 0.0f;
       const float ps = row_sum(p);
       corr[r] = 1.0f;
       if (mt > -FLT_MAX) {
-        corr[r] = m[r] > -FLT_MAX ? expf(m[r] - mn) : 0.0f;
+        corr[r] = m[r] == mn ? 1.0f : m[r] > -FLT_MAX ? __builtin_amdgcn_exp2f(m[r] - mn) : 0.0f;
         lsum[r] = lsum[r] * corr[r] + ps;
         m[r] = mn;
       }
@@ -266,7 +270,7 @@ __global__ __launch_bounds__(256) void laya_attn_kernel(const float *__restrict_
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     if (!(sML[v][row][1] > 0.0f)) continue;
-    const float f = expf(sML[v][row][0] - M);
+    const float f = __builtin_amdgcn_exp2f(sML[v][row][0] - M);
     L += f * sML[v][row][1];
 #pragma unroll
     for (int e = 0; e < 4; ++e) o[e] += f * sO[v][row * kOp + d4 + e];
