@@ -151,6 +151,11 @@ int lg_seq_create(lg_engine *e, int *seq);
 int lg_seq_fork(lg_engine *e, int parent, int ntokens, int *child);
 int lg_seq_free(lg_engine *e, int seq);
 int lg_seq_len(lg_engine *e, int seq, int *len);
+/* Read back the cached keys (after RoPE) and values of positions [pos0, pos0 + n) of one layer of a
+ * sequence, as f32 [n][kv_heads * head_dim] each (host).  For tests and debugging: the reference keeps
+ * no cache (src/models/openthai/model.rs:276-294 recomputes k and v every forward); this exposes the
+ * k/v rows that its attention loop would read. */
+int lg_seq_kv_read(lg_engine *e, int seq, int layer, int pos0, int n, float *k, float *v);
 
 typedef int (*lg_cancel_fn)(void *arg); /* non-zero = cancel; polled between layers */
 

@@ -295,6 +295,13 @@ int lg_seq_len(lg_engine *e, int seq, int *len) {
   });
 }
 
+int lg_seq_kv_read(lg_engine *e, int seq, int layer, int pos0, int n, float *k, float *v) {
+  return guard([&] {
+    NEED(e, "engine");
+    e->e->seq_kv_read(seq, layer, pos0, n, k, v);
+  });
+}
+
 int lg_forward(lg_engine *e, int seq, const int32_t *ids, int n, const int32_t *positions, int npos,
                const int32_t *vocab_ids, int nv, float *logits, lg_cancel_fn cancel, void *cancel_arg) {
   return guard([&] {

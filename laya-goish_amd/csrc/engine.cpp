@@ -583,6 +583,45 @@ int Engine::seq_len(int id) const {
   return it->second.len;
 }
 
+void Engine::seq_kv_read(int id, int layer, int pos0, int n, float *k, float *v) {
+  LG_REQUIRE(arch == Arch::Decoder, "kv read: the model keeps no KV cache");
+  const Seq &s = seq(id);
+  LG_REQUIRE(layer >= 0 && layer < L, "kv read: layer %d outside 0..%d", layer, L - 1);
+  LG_REQUIRE(pos0 >= 0 && n >= 0 && int64_t(pos0) + n <= s.len, "kv read: positions [%d, %d) outside the sequence's %d",
+             pos0, pos0 + n, s.len);
+  LG_REQUIRE(k && v, "kv read: missing output");
+  const int kvw = hkv * hd, es = kv_elem();
+  std::vector<uint8_t> kp(size_t(page_stride_) * es), vp(size_t(page_stride_) * es);
+  HIP_CHECK(hipStreamSynchronize(stream));
+  int loaded = -1;
+  for (int i = 0; i < n; ++i) {
+    const int pos = pos0 + i, pi = pos / 64, slot = pos % 64;
+    if (pi != loaded) {
+      const size_t off = size_t(s.pages[pi]) * page_stride_ * es;
+      HIP_CHECK(hipMemcpy(kp.data(), static_cast<uint8_t *>(kpool(layer)) + off, kp.size(), hipMemcpyDeviceToHost));
+      HIP_CHECK(hipMemcpy(vp.data(), static_cast<uint8_t *>(vpool(layer)) + off, vp.size(), hipMemcpyDeviceToHost));
+      loaded = pi;
+    }
+    for (int h = 0; h < hkv; ++h)
+      for (int j = 0; j < hd; ++j) {
+        const size_t ki = (size_t(h) * 64 + slot) * hd + j, vi = (size_t(h) * hd + j) * 64 + slot;  // K rows, V columns
+        float kf, vf;
+        if (es == 4) {
+          std::memcpy(&kf, kp.data() + ki * 4, 4);
+          std::memcpy(&vf, vp.data() + vi * 4, 4);
+        } else {
+          _Float16 kh, vh;
+          std::memcpy(&kh, kp.data() + ki * 2, 2);
+          std::memcpy(&vh, vp.data() + vi * 2, 2);
+          kf = float(kh);
+          vf = float(vh);
+        }
+        k[size_t(i) * kvw + h * hd + j] = kf;
+        v[size_t(i) * kvw + h * hd + j] = vf;
+      }
+  }
+}
+
 // ------------------------------------------------------------------ batched prefill
 BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
   LG_REQUIRE(nreq > 0 && reqs, "batch: no requests");

@@ -146,6 +146,8 @@ class Engine {
   int seq_fork(int parent, int ntokens);
   void seq_free(int id);
   int seq_len(int id) const;
+  // Cached K (after RoPE) and V rows of positions [pos0, pos0 + n) of one layer, as f32 [n][hkv * hd].
+  void seq_kv_read(int id, int layer, int pos0, int n, float *k, float *v);
 
   BatchPlan *batch_create(const lg_request *reqs, int nreq);
   void batch_free(BatchPlan *b);

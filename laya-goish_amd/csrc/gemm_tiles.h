@@ -23,6 +23,7 @@
 
 #include "common.h"
 #include "kernels.h"
+#include "f16split.h"
 #include "quant.h"
 
 namespace lg {
@@ -52,8 +53,10 @@ __device__ __forceinline__ void put8(const float *v, _Float16 *hi, _Float16 *lo,
   half8 h, l;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    h[j] = _Float16(v[j]);
-    l[j] = _Float16(v[j] - float(h[j]));
+    _Float16 a, b;
+    split_f16(v[j], a, b);
+    h[j] = a;
+    l[j] = b;
   }
   *reinterpret_cast<half8 *>(hi) = h;
   if (split) *reinterpret_cast<half8 *>(lo) = l;
@@ -507,9 +510,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
           const int col = nt * (BNT / 2) + wn * (16 * WTN) + jj * 32 + col_in;
           const float g = acc[i][jj][r];
           const float v = (EPI == int(Epi::SWIGLU) ? silu(g) : gelu_tanh(g)) * acc[i][jj + WTN / 2][r];
-          const _Float16 h = _Float16(v);
+          _Float16 h, hl;
+          split_f16(v, h, hl);
           C16[int64_t(row) * ldc + col] = h;
-          if (C16lo) C16lo[int64_t(row) * ldc + col] = _Float16(v - float(h));
+          if (C16lo) C16lo[int64_t(row) * ldc + col] = hl;
         }
       } else {
 #pragma unroll
@@ -525,9 +529,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
           } else {
             if (bias) v += bias[col];
             if (EPI == int(Epi::RELU16)) v = fmaxf(v, 0.0f);
-            const _Float16 h = _Float16(v);
+            _Float16 h, hl;
+            split_f16(v, h, hl);
             C16[int64_t(row) * ldc + col] = h;
-            if (C16lo) C16lo[int64_t(row) * ldc + col] = _Float16(v - float(h));
+            if (C16lo) C16lo[int64_t(row) * ldc + col] = hl;
           }
         }
       }

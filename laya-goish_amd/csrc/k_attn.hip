@@ -23,6 +23,7 @@
 
 #include "common.h"
 #include "kernels.h"
+#include "f16split.h"
 #include "wave.h"
 
 namespace lg {
@@ -40,9 +41,10 @@ constexpr float kLog2e = 1.4426950408889634f;
 __device__ __forceinline__ void split8(const float *v, half8 &hi, half8 &lo) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const _Float16 h = _Float16(v[j]);
+    _Float16 h, l;
+    split_f16(v[j], h, l);
     hi[j] = h;
-    lo[j] = _Float16(v[j] - float(h));
+    lo[j] = l;
   }
 }
 
@@ -194,9 +196,10 @@ __global__ __launch_bounds__(64) void attn_prefill_kernel(
       half4 o, olo;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float v = acc[b][r4 * 4 + j] * inv;
-        o[j] = _Float16(v);
-        olo[j] = _Float16(v - float(o[j]));
+        _Float16 oh, ol;
+        split_f16(acc[b][r4 * 4 + j] * inv, oh, ol);
+        o[j] = oh;
+        olo[j] = ol;
       }
       const int64_t at = obase + b * 32 + r4 * 8 + hl * 4;
       *reinterpret_cast<half4 *>(out16 + at) = o;
@@ -300,10 +303,13 @@ __global__ __launch_bounds__(256, 1) void attn_prefill_grp_kernel(
         half4 khi, klo, vhi, vlo;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          khi[e] = _Float16(kv[e]);
-          klo[e] = _Float16(kv[e] - float(khi[e]));
-          vhi[e] = _Float16(vv[e]);
-          vlo[e] = _Float16(vv[e] - float(vhi[e]));
+          _Float16 a, b, c, d;
+          split_f16(kv[e], a, b);
+          split_f16(vv[e], c, d);
+          khi[e] = a;
+          klo[e] = b;
+          vhi[e] = c;
+          vlo[e] = d;
         }
         *reinterpret_cast<half4 *>(&kls[0][kro]) = khi;
         *reinterpret_cast<half4 *>(&kls[1][kro]) = klo;
@@ -415,9 +421,10 @@ __global__ __launch_bounds__(256, 1) void attn_prefill_grp_kernel(
       half4 o, olo;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float v = acc[b][r4 * 4 + j] * inv;
-        o[j] = _Float16(v);
-        olo[j] = _Float16(v - float(o[j]));
+        _Float16 oh, ol;
+        split_f16(acc[b][r4 * 4 + j] * inv, oh, ol);
+        o[j] = oh;
+        olo[j] = ol;
       }
       const int64_t at = obase + b * 32 + r4 * 8 + hl * 4;
       *reinterpret_cast<half4 *>(out16 + at) = o;

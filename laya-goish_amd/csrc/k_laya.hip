@@ -9,6 +9,7 @@
 
 #include "common.h"
 #include "kernels.h"
+#include "f16split.h"
 #include "wave.h"
 
 namespace lg {
@@ -77,9 +78,10 @@ __global__ __launch_bounds__(kT) void layer_norm_kernel(const float *__restrict_
       if (y32) {
         y32[at] = o;
       } else {
-        const _Float16 h = _Float16(o);
+        _Float16 h, hl;
+        split_f16(o, h, hl);
         y16[at] = h;
-        if (y16lo) y16lo[at] = _Float16(o - float(h));
+        if (y16lo) y16lo[at] = hl;
       }
     }
   }
@@ -131,9 +133,10 @@ typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void split_hl(float4v x, half4v &hi, half4v &lo) {
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    const _Float16 h = _Float16(x[c]);
+    _Float16 h, l;
+    split_f16(x[c], h, l);
     hi[c] = h;
-    lo[c] = _Float16(x[c] - float(h));
+    lo[c] = l;
   }
 }
 
@@ -238,8 +241,14 @@ __global__ __launch_bounds__(256) void laya_attn_kernel(const float *__restrict_
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[b][r] *= corr[r];
     }
+    // P moves between the lanes of this wave through its own LDS rows: the wave barriers order the
+    // stores above before the read below, and this read before the next block's stores
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     half4v ph, pl;
     split_hl(*reinterpret_cast<const float4v *>(myP + li * kPp + 4 * kg), ph, pl);
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       half4v vh, vl;
@@ -279,10 +288,10 @@ __global__ __launch_bounds__(256) void laya_attn_kernel(const float *__restrict_
   const int64_t base = int64_t(row0 + row) * d + h * kHD + d4;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const float ov = o[e] * inv;
-    const _Float16 hh = _Float16(ov);
+    _Float16 hh, hl;
+    split_f16(o[e] * inv, hh, hl);
     y[base + e] = hh;
-    if (ylo) ylo[base + e] = _Float16(ov - float(hh));
+    if (ylo) ylo[base + e] = hl;
   }
 }
 

@@ -9,6 +9,7 @@
 
 #include "common.h"
 #include "kernels.h"
+#include "f16split.h"
 #include "wave.h"
 
 namespace lg {
@@ -30,9 +31,10 @@ __device__ __forceinline__ float group8_max(float v) {
 }
 
 __device__ __forceinline__ void store_planes(_Float16 *hi, _Float16 *lo, int64_t i, float v) {
-  const _Float16 h = _Float16(v);
+  _Float16 h, l;
+  split_f16(v, h, l);
   hi[i] = h;
-  if (lo) lo[i] = _Float16(v - float(h));
+  if (lo) lo[i] = l;
 }
 
 // ---------------------------------------------------------------- DeltaNet: conv + norms

@@ -7,6 +7,7 @@
 #include "common.h"
 #include "kernels.h"
 #include "quant.h"
+#include "f16split.h"
 #include "wave.h"
 
 namespace lg {
@@ -44,7 +45,7 @@ __global__ __launch_bounds__(kT) void rmsnorm_kernel(const float *__restrict__ x
   Out *out = y + int64_t(blockIdx.x) * d;
   Out *lo = ylo ? ylo + int64_t(blockIdx.x) * d : nullptr;
   for (int k = threadIdx.x; k < d; k += kT) {
-    const float v = row[k] * inv * w[k];
+    const float v = f32_pin(row[k] * inv * w[k]);
     const Out h = Out(v);
     out[k] = h;
     if (lo) lo[k] = Out(v - float(h));
@@ -86,8 +87,10 @@ __global__ __launch_bounds__(kT) void rmsnorm_f16_vec_kernel(const float *__rest
       half4 h, l;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        h[e] = _Float16(r[e]);
-        l[e] = _Float16(r[e] - float(h[e]));
+        _Float16 a, b;
+        split_f16(r[e], a, b);
+        h[e] = a;
+        l[e] = b;
       }
       out[k] = h;
       if (lo) lo[k] = l;
@@ -173,12 +176,14 @@ __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
         const float a = u[b] * c0[b] - v[b] * s0[b], c = v[b] * c1[b] + u[b] * s1[b];
         if (hh < hq) {
           const int64_t at = int64_t(row0 + tk) * qw + hh * HD + j;
-          const _Float16 ah = _Float16(a), ch = _Float16(c);
+          _Float16 ah, al, ch, cl;
+          split_f16(a, ah, al);
+          split_f16(c, ch, cl);
           q16[at] = ah;
           q16[at + HALF] = ch;
           if (q16lo) {
-            q16lo[at] = _Float16(a - float(ah));
-            q16lo[at + HALF] = _Float16(c - float(ch));
+            q16lo[at] = al;
+            q16lo[at + HALF] = cl;
           }
         } else {
           const int pos = pos0 + tk;
@@ -374,9 +379,10 @@ __global__ void cvt_f16_kernel(const float *__restrict__ x, int64_t n, _Float16 
                                _Float16 *__restrict__ ylo) {
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const _Float16 h = _Float16(x[i]);
+  _Float16 h, l;
+  split_f16(x[i], h, l);
   y[i] = h;
-  if (ylo) ylo[i] = _Float16(x[i] - float(h));
+  if (ylo) ylo[i] = l;
 }
 
 __global__ void fill_i32_kernel(int32_t *p, int n, int32_t v) {

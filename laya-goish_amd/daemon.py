@@ -46,13 +46,27 @@ class RequestError(Exception):
     pass
 
 
+def _ids(v, what):
+    """A token-id list: JSON integers in [0, 2^31) (the C ABI's int32 ids; the engine checks
+    them against the vocabulary)."""
+    if v is None:
+        return []
+    if not isinstance(v, list):
+        raise RequestError(f"{what} must be a list of token ids")
+    for t in v:
+        if isinstance(t, bool) or not isinstance(t, int) or not 0 <= t < 2 ** 31:
+            raise RequestError(f"{what}: token id {json.dumps(t)} is not an integer in [0, 2^31)")
+    return v
+
+
 def _option(v, what):
     if v is None:
         return {"name": [], "desc": []}
     if isinstance(v, list):
-        return {"name": [], "desc": v}
+        return {"name": [], "desc": _ids(v, f"{what}: criterion")}
     if isinstance(v, dict):
-        return {"name": v.get("name") or [], "desc": v.get("desc") or []}
+        return {"name": _ids(v.get("name"), f"{what}: criterion name"),
+                "desc": _ids(v.get("desc"), f"{what}: criterion desc")}
     raise RequestError(f"{what}: criteria entries must be token lists, objects or null")
 
 
@@ -63,9 +77,7 @@ def to_tokens_request(req) -> tuple[dict, list]:
     qs = req.get("questions")
     if not isinstance(qs, dict) or not 1 <= len(qs) <= 256:
         raise RequestError("questions must contain 1..256 named questions")
-    state = req.get("state", [])
-    if not isinstance(state, list):
-        raise RequestError("state must be a list of token ids")
+    state = _ids(req.get("state", []), "state")
     out, labels = [], []
     for qid, q in qs.items():
         if not isinstance(q, dict):
@@ -90,9 +102,7 @@ def to_tokens_request(req) -> tuple[dict, list]:
             opts = [_option(crit.get("false"), qid), _option(crit.get("true"), qid)]
         else:
             raise RequestError(f"{qid}: invalid question type")
-        ins = q.get("instructions", [])
-        if not isinstance(ins, list):
-            raise RequestError(f"{qid}: instructions must be a list of token ids")
+        ins = _ids(q.get("instructions", []), f"{qid}: instructions")
         out.append({"type": kind, "instruction": ins, "options": opts})
         labels.append((qid, kind, names, opts))
     perms = req.get("permutations")
@@ -114,7 +124,7 @@ def answer_json(model_name, req, labels, res, t0) -> dict:
                 ans["choice"] = names[a["choice"]]
             elif kind == "score":
                 ans["score"] = a["score"]
-                ans["legend"] = {str(j): o["desc"] if o["desc"] else str(j) for j, o in enumerate(opts)}
+                ans["legend"] = {str(j): o["desc"] for j, o in enumerate(opts)}  # an empty label stays empty
             else:
                 ans["noul"] = p[1]
             ans["confidence"] = a["confidence"]
@@ -198,6 +208,10 @@ class Registry:
             raise RegistryError(f"unknown default model {default}")
         self.default = self.names[default] if default is not None else 0
         self.model_names = list(self.names)
+        # answers of a Laya encoder name laya.model_name (src/models/laya/decision.rs:293)
+        self.answer_names = [g.str("laya.model_name", "") if g.str("ggmlc.graph_spec", "") else ""
+                             for g in ggufs]
+        self.answer_names = [a or n for a, n in zip(self.answer_names, self.model_names)]
         self.engines = [open_engine(g) for g in ggufs]
 
     def select(self, req) -> int:
@@ -217,16 +231,28 @@ class Registry:
             e.close()
 
 
+def error_json(e, req) -> dict:
+    """{"error": message} for a request that failed, with its "id" echoed when it has one."""
+    out = {"error": str(e) if isinstance(e, (ValueError, RequestError, lh.LayaError))
+           else f"{type(e).__name__}: {e}"}
+    if isinstance(req, dict) and req.get("id") is not None:
+        out["id"] = req["id"]
+    return out
+
+
 def serve(engine, model_name, fin, fout) -> None:
-    """One model, requests answered in order."""
+    """One model, requests answered in order.  Any failure of one request becomes its error line
+    and the loop goes on."""
     for line in fin:
         if not line.strip():
             continue
         t0 = time.perf_counter()
+        req = None
         try:
-            out = handle(engine, model_name, json.loads(line), t0)
-        except (ValueError, RequestError, lh.LayaError) as e:
-            out = {"error": str(e)}
+            req = json.loads(line)
+            out = handle(engine, model_name, req, t0)
+        except Exception as e:  # noqa: BLE001 -- one JSON line per request, whatever went wrong
+            out = error_json(e, req)
         fout.write(json.dumps(out) + "\n")
         fout.flush()
 
@@ -255,10 +281,10 @@ def serve_registry(reg: Registry, fin, fout) -> None:
                 return
             req, t0 = item
             try:
-                write(handle(reg.engines[i], reg.model_names[i], req, t0))
-            except (ValueError, RequestError, lh.LayaError) as e:
-                write({"error": str(e)} if not isinstance(req, dict) or req.get("id") is None
-                      else {"error": str(e), "id": req["id"]})
+                out = handle(reg.engines[i], reg.answer_names[i], req, t0)
+            except Exception as e:  # noqa: BLE001 -- the worker outlives any one request
+                out = error_json(e, req)
+            write(out)
 
     threads = [threading.Thread(target=worker, args=(i,), daemon=True) for i in range(len(queues))]
     for t in threads:
@@ -267,11 +293,12 @@ def serve_registry(reg: Registry, fin, fout) -> None:
         if not line.strip():
             continue
         t0 = time.perf_counter()
+        req = None
         try:
             req = json.loads(line)
             queues[reg.select(req)].put((req, t0))
-        except (ValueError, RequestError) as e:
-            write({"error": str(e)})
+        except Exception as e:  # noqa: BLE001
+            write(error_json(e, req))
     for q in queues:
         q.put(None)
     for t in threads:
@@ -298,7 +325,7 @@ def main() -> int:
     for name, e in zip(reg.model_names, reg.engines):
         print(f"loaded {name} ({e.layers()} layers, device {args.device})", file=sys.stderr, flush=True)
     if len(reg.engines) == 1:
-        serve(reg.engines[0], reg.model_names[0], sys.stdin, sys.stdout)
+        serve(reg.engines[0], reg.answer_names[0], sys.stdin, sys.stdout)
     else:
         serve_registry(reg, sys.stdin, sys.stdout)
     reg.close()

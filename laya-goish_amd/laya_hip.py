@@ -124,6 +124,12 @@ class DecideArgs:
                                  int(req.get("permutations") or 0), -1 if oi is None else int(bool(oi)))
 
     def _arr(self, v):
+        if not isinstance(v, (list, tuple, np.ndarray)):
+            raise LayaError(1, "token ids must be a list of integers")
+        if not isinstance(v, np.ndarray):
+            for t in v:  # int32 ids; the library checks them against the vocabulary
+                if isinstance(t, bool) or not isinstance(t, (int, np.integer)) or not -2 ** 31 <= int(t) < 2 ** 31:
+                    raise LayaError(1, f"token id {t!r} is not a 32-bit integer")
         a = np.ascontiguousarray(np.asarray(v, dtype=np.int32).reshape(-1))
         if a.size == 0:
             a = np.zeros(1, np.int32)[:0]
@@ -160,6 +166,8 @@ class DecideArgs:
                 a["noul"] = float(p[1])
             out.append(a)
         r = self.res
+        if laya:  # src/models/laya/decision.rs:293-303: no option-order passes, no state budget
+            return {"answers": out, "usage": {"input_tokens": int(r.input_tokens), "output_tokens": 0}}
         return {"answers": out, "usage": {"input_tokens": int(r.input_tokens), "output_tokens": 0,
                                           "permutations": int(r.permutations),
                                           "truncated_state": bool(r.truncated)}}
@@ -253,6 +261,7 @@ def lib() -> ctypes.CDLL:
             "lg_seq_fork": (I, [P, I, I, ctypes.POINTER(I)]),
             "lg_seq_free": (I, [P, I]),
             "lg_seq_len": (I, [P, I, ctypes.POINTER(I)]),
+            "lg_seq_kv_read": (I, [P, I, I, I, I, P, P]),
             "lg_forward": (I, [P, I, P, I, P, I, P, I, P, CANCEL_FN, P]),
             "lg_batch_create": (I, [P, ctypes.POINTER(Request), I, ctypes.POINTER(P)]),
             "lg_batch_free": (None, [P, P]),
@@ -509,6 +518,14 @@ class Engine:
         n = ctypes.c_int()
         check(lib().lg_seq_len(self.h, seq, ctypes.byref(n)))
         return n.value
+
+    def seq_kv_read(self, seq: int, layer: int, pos0: int, n: int):
+        """(K, V) cached rows of positions [pos0, pos0 + n) of one layer, f32 [n][kv_heads * head_dim]."""
+        w = self.info["kv_heads"] * self.info["head_dim"]
+        k = np.empty((n, w), np.float32)
+        v = np.empty((n, w), np.float32)
+        check(lib().lg_seq_kv_read(self.h, seq, layer, pos0, n, _ptr(k), _ptr(v)))
+        return k, v
 
     def forward(self, seq: int, ids, positions, vocab_ids=None, cancel=None) -> np.ndarray:
         """Model::forward(ids, positions): logits at `positions` for `vocab_ids` (None = all)."""

@@ -498,14 +498,110 @@ __attribute__((target("avx2,fma"))) static void apply_rows_avx2(const apply_ctx 
 }
 #endif
 
+#if defined(__x86_64__)
+/* The same per-(r, c) arithmetic as apply_rows_avx2 with a cache-friendly loop nest (the
+ * blocked mode, or_set_blocked): columns in blocks whose weight rows stay in L2 while every
+ * 4-row tile of the worker passes over them, two columns per pass over a tile's x rows.  Each
+ * output still gets its own 8 lane accumulators over k in order, the same fold and the same
+ * tail, so the results are bit-identical to the reference loop order; only memory traffic
+ * differs.  The reference loop order stays the default (the CPU baseline times it). */
+__attribute__((target("avx2,fma"))) static void finish_col(const apply_ctx *a, int r, int nr, int c, int j,
+                                                           const __m256 *acc) {
+  int k = a->k, n = a->n;
+  const float *wr = a->w + (size_t)c * k;
+  for (int t = 0; t < nr; ++t) {
+    float lanes[8];
+    _mm256_storeu_ps(lanes, acc[t]);
+    float v = lane_sum(lanes);
+    for (int q = j; q < k; ++q) v = v + wr[q] * a->x[(size_t)(r + t) * k + q];
+    if (a->bias) v = v + a->bias[c];
+    a->out[(size_t)(r + t) * n + c] = v;
+  }
+}
+
+__attribute__((target("avx2,fma"))) static void apply_block(const apply_ctx *a, int start, int end,
+                                                             int col_lo, int col_hi) {
+  int k = a->k;
+  int cb = 262144 / (4 * (k > 0 ? k : 1));
+  if (cb < 2) cb = 2;
+  cb &= ~1;
+  for (int c0 = col_lo; c0 < col_hi; c0 += cb) {
+    int c1 = c0 + cb < col_hi ? c0 + cb : col_hi;
+    for (int r = start; r < end; r += 4) {
+      int nr = end - r < 4 ? end - r : 4;
+      const float *x0 = a->x + (size_t)r * k;
+      int c = c0;
+      for (; c + 2 <= c1; c += 2) {
+        const float *w0 = a->w + (size_t)c * k, *w1 = w0 + k;
+        __m256 p[4], q[4];
+        for (int t = 0; t < 4; ++t) p[t] = q[t] = _mm256_setzero_ps();
+        int j = 0;
+        if (nr == 4) {
+          for (; j + 8 <= k; j += 8) {
+            __m256 v0 = _mm256_loadu_ps(w0 + j), v1 = _mm256_loadu_ps(w1 + j);
+            __m256 a0 = _mm256_loadu_ps(x0 + j), a1 = _mm256_loadu_ps(x0 + k + j);
+            __m256 a2 = _mm256_loadu_ps(x0 + 2 * (size_t)k + j), a3 = _mm256_loadu_ps(x0 + 3 * (size_t)k + j);
+            p[0] = _mm256_fmadd_ps(v0, a0, p[0]);
+            q[0] = _mm256_fmadd_ps(v1, a0, q[0]);
+            p[1] = _mm256_fmadd_ps(v0, a1, p[1]);
+            q[1] = _mm256_fmadd_ps(v1, a1, q[1]);
+            p[2] = _mm256_fmadd_ps(v0, a2, p[2]);
+            q[2] = _mm256_fmadd_ps(v1, a2, q[2]);
+            p[3] = _mm256_fmadd_ps(v0, a3, p[3]);
+            q[3] = _mm256_fmadd_ps(v1, a3, q[3]);
+          }
+        } else {
+          for (; j + 8 <= k; j += 8) {
+            __m256 v0 = _mm256_loadu_ps(w0 + j), v1 = _mm256_loadu_ps(w1 + j);
+            for (int t = 0; t < nr; ++t) {
+              __m256 xv = _mm256_loadu_ps(x0 + (size_t)t * k + j);
+              p[t] = _mm256_fmadd_ps(v0, xv, p[t]);
+              q[t] = _mm256_fmadd_ps(v1, xv, q[t]);
+            }
+          }
+        }
+        finish_col(a, r, nr, c, j, p);
+        finish_col(a, r, nr, c + 1, j, q);
+      }
+      for (; c < c1; ++c) {
+        const float *w0 = a->w + (size_t)c * k;
+        __m256 p[4];
+        for (int t = 0; t < 4; ++t) p[t] = _mm256_setzero_ps();
+        int j = 0;
+        for (; j + 8 <= k; j += 8) {
+          __m256 v0 = _mm256_loadu_ps(w0 + j);
+          for (int t = 0; t < nr; ++t) p[t] = _mm256_fmadd_ps(v0, _mm256_loadu_ps(x0 + (size_t)t * k + j), p[t]);
+        }
+        finish_col(a, r, nr, c, j, p);
+      }
+    }
+  }
+}
+
+static void apply_rows_avx2_blocked(const apply_ctx *a, int start, int end) { apply_block(a, start, end, 0, a->n); }
+
+/* Few rows (a decode step): the workers split the columns instead of the rows. */
+typedef struct { const apply_ctx *a; int m, per; } colsplit_ctx;
+static void apply_cols(void *p, int lo, int hi) {
+  const colsplit_ctx *cs = (const colsplit_ctx *)p;
+  int c0 = lo * cs->per, c1 = hi * cs->per < cs->a->n ? hi * cs->per : cs->a->n;
+  if (c0 < c1) apply_block(cs->a, 0, cs->m, c0, c1);
+}
+#endif
+
 static int g_force_scalar = 0;
+static int g_blocked = 0;
 void or_set_scalar_apply(int on) { g_force_scalar = on; }
+void or_set_blocked(int on) { g_blocked = on; }
 
 static void apply_tiles(void *p, int lo, int hi) {
   const apply_ctx *a = (const apply_ctx *)p;
 #if defined(__x86_64__)
   if (!g_force_scalar && __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma")) {
-    apply_rows_avx2(a, lo, hi);
+    if (g_blocked)
+      apply_rows_avx2_blocked(a, lo, hi);
+    else
+      apply_rows_avx2(a, lo, hi);
     return;
   }
 #endif
@@ -519,6 +615,14 @@ void or_apply(const float *w, int rows, int cols, const float *x, int m, const f
    * ranges are multiples of... any split gives the same per-row results. */
   int count = threads < (m + 3) / 4 ? threads : (m + 3) / 4;
   if (count < 1) count = 1;
+#if defined(__x86_64__)
+  if (g_blocked && !g_force_scalar && count < threads && rows >= 64 * threads &&
+      __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma")) {
+    colsplit_ctx cs = {&a, m, 32};
+    parallel((rows + 31) / 32, threads, apply_cols, &cs);
+    return;
+  }
+#endif
   parallel(m, count, apply_tiles, &a);
 }
 
@@ -771,6 +875,15 @@ void or_cache_free(or_cache *c) {
 }
 int or_cache_len(const or_cache *c) { return c->len; }
 
+/* Cached K (after RoPE) and V rows [pos0, pos0 + n) of one layer, [n][hkv*hd] each. */
+int or_cache_read(const or_cache *c, int layer, int pos0, int n, float *k, float *v) {
+  if (layer < 0 || layer >= c->L || pos0 < 0 || n < 0 || pos0 + n > c->len) return -1;
+  size_t off = ((size_t)layer * c->cap + (size_t)pos0) * c->kvw;
+  memcpy(k, c->k + off, (size_t)n * c->kvw * sizeof(float));
+  memcpy(v, c->v + off, (size_t)n * c->kvw * sizeof(float));
+  return 0;
+}
+
 /* Table RoPE, src/tensor.rs:158-172 (rotate-half pairs (j, j+hd/2)). */
 static void rope_rows(float *a, int n, int stride, int heads, int hd, int pos0, const float *cs,
                       const float *sn) {
@@ -825,6 +938,73 @@ static void attn_heads(void *p, int lo, int hi) {
   free(prob);
 }
 
+#if defined(__x86_64__)
+/* attn_heads in the blocked mode: the same operations per score and per output element,
+ * eight at a time.  Eight keys' dot products run in the eight lanes (each lane its own
+ * sequential sum from -0.0 over the head dimension, mul then add, from a transposed copy of
+ * the head's keys), and out[z] += p_j v_j[z] runs over eight z at a time in increasing j.
+ * Bit-identical to attn_heads. */
+__attribute__((target("avx2"))) static void attn_heads_avx2(void *p, int lo, int hi) {
+  const attn_ctx *a = (const attn_ctx *)p;
+  const or_model *m = a->m;
+  int hd = m->hd, qw = m->hq * hd, kvw = m->hkv * hd, grp = m->hq / m->hkv;
+  int total = a->pos0 + a->n;
+  int tp = (total + 7) & ~7;
+  float *score = (float *)malloc((size_t)tp * sizeof(float));
+  float *prob = (float *)malloc((size_t)total * sizeof(float));
+  float *kt = (float *)malloc((size_t)hd * tp * sizeof(float));
+  float scale = sqrtf((float)hd);
+  const __m256 vscale = _mm256_set1_ps(scale);
+  int built = -1;
+  for (int h = lo; h < hi; ++h) {
+    int kh = h / grp;
+    if (kh != built) {
+      for (int j = 0; j < total; ++j) {
+        const float *kr = a->K + (size_t)j * kvw + (size_t)kh * hd;
+        for (int z = 0; z < hd; ++z) kt[(size_t)z * tp + j] = kr[z];
+      }
+      built = kh;
+    }
+    for (int i = 0; i < a->n; ++i) {
+      int upto = a->pos0 + i;
+      const float *q = a->q + (size_t)i * qw + (size_t)h * hd;
+      int j = 0;
+      for (; j + 8 <= upto + 1; j += 8) {
+        __m256 s = _mm256_set1_ps(-0.0f);
+        for (int z = 0; z < hd; ++z)
+          s = _mm256_add_ps(s, _mm256_mul_ps(_mm256_set1_ps(q[z]), _mm256_loadu_ps(kt + (size_t)z * tp + j)));
+        _mm256_storeu_ps(score + j, _mm256_div_ps(s, vscale));
+      }
+      for (; j <= upto; ++j) score[j] = or_dot(q, a->K + (size_t)j * kvw + (size_t)kh * hd, hd) / scale;
+      or_softmax(score, upto + 1, prob);
+      float *o = a->out + (size_t)i * qw + (size_t)h * hd;
+      for (int z0 = 0; z0 < hd; z0 += 64) {
+        int zn = hd - z0 < 64 ? hd - z0 : 64;
+        if (zn == 64) {
+          __m256 acc[8];
+          for (int u = 0; u < 8; ++u) acc[u] = _mm256_setzero_ps();
+          for (int jj = 0; jj <= upto; ++jj) {
+            const float *v = a->V + (size_t)jj * kvw + (size_t)kh * hd + z0;
+            __m256 pj = _mm256_set1_ps(prob[jj]);
+            for (int u = 0; u < 8; ++u) acc[u] = _mm256_add_ps(acc[u], _mm256_mul_ps(pj, _mm256_loadu_ps(v + 8 * u)));
+          }
+          for (int u = 0; u < 8; ++u) _mm256_storeu_ps(o + z0 + 8 * u, acc[u]);
+        } else {
+          for (int z = z0; z < z0 + zn; ++z) o[z] = 0.0f;
+          for (int jj = 0; jj <= upto; ++jj) {
+            const float *v = a->V + (size_t)jj * kvw + (size_t)kh * hd;
+            for (int z = z0; z < z0 + zn; ++z) o[z] = o[z] + prob[jj] * v[z];
+          }
+        }
+      }
+    }
+  }
+  free(kt);
+  free(score);
+  free(prob);
+}
+#endif
+
 int or_prefill(or_model *m, or_cache *c, const int32_t *ids, int n, const int32_t *gather,
                int ngather, float *hidden) {
   int d = m->d, hq = m->hq, hkv = m->hkv, hd = m->hd, f = m->f;
@@ -860,7 +1040,12 @@ int or_prefill(or_model *m, or_cache *c, const int32_t *ids, int n, const int32_
     rope_rows(q, n, qw, hq, hd, pos0, m->cosf_, m->sinf_);
     rope_rows(K + (size_t)pos0 * kvw, n, kvw, hkv, hd, pos0, m->cosf_, m->sinf_);
     attn_ctx ac = {m, q, K, V, att, n, pos0};
-    parallel(hq, m->threads, attn_heads, &ac);
+#if defined(__x86_64__)
+    if (g_blocked && !g_force_scalar && __builtin_cpu_supports("avx2"))
+      parallel(hq, m->threads, attn_heads_avx2, &ac);
+    else
+#endif
+      parallel(hq, m->threads, attn_heads, &ac);
     or_apply(ly->wo, d, qw, att, n, NULL, m->threads, y);
     for (size_t i = 0; i < (size_t)n * d; ++i) x[i] = x[i] + y[i];
     or_rms(x, n, d, ly->ffn_norm, 0.0f, m->eps, h);

@@ -43,6 +43,11 @@ const char *or_gguf_str(const or_gguf *g, const char *key);
  * 8-lane FMA accumulators, sequential lane sum, separately-rounded tail, then bias. */
 void or_apply(const float *w, int rows, int cols, const float *x, int m, const float *bias,
               int threads, float *out);
+/* Loop-nest switches (process-wide), none of which changes a result bit: scalar forces the
+ * scalar apply; blocked selects the cache-blocked AVX2 apply and the eight-wide attention
+ * (for long full-depth parity runs).  The default is the reference's own loop order. */
+void or_set_scalar_apply(int on);
+void or_set_blocked(int on);
 /* src/tensor.rs:193-195 */
 float or_dot(const float *a, const float *b, int n);
 /* src/tensor.rs:132-140 */
@@ -67,6 +72,8 @@ or_cache *or_cache_new(const or_model *m, int capacity);
 or_cache *or_cache_fork(const or_cache *c, int len);
 void or_cache_free(or_cache *c);
 int or_cache_len(const or_cache *c);
+/* Cached K (after RoPE) and V rows [pos0, pos0 + n) of one layer, [n][hkv*hd] each; -1 if outside. */
+int or_cache_read(const or_cache *c, int layer, int pos0, int n, float *k, float *v);
 
 /* Run n tokens starting at the cache's current length; append their K/V; return the
  * residual-stream rows at `gather` (indices into the n new tokens), [ngather][d].

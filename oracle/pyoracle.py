@@ -36,6 +36,7 @@ def lib() -> ctypes.CDLL:
             "or_gguf_str": (ctypes.c_char_p, [P, ctypes.c_char_p]),
             "or_apply": (None, [P, I, I, P, I, P, I, P]),
             "or_set_scalar_apply": (None, [I]),
+            "or_set_blocked": (None, [I]),
             "or_dot": (F, [P, P, I]),
             "or_softmax": (None, [P, I, P]),
             "or_rms": (None, [P, I, I, P, F, F, P]),
@@ -48,6 +49,7 @@ def lib() -> ctypes.CDLL:
             "or_cache_fork": (P, [P, I]),
             "or_cache_free": (None, [P]),
             "or_cache_len": (I, [P]),
+            "or_cache_read": (I, [P, I, I, I, P, P]),
             "or_prefill": (I, [P, P, P, I, P, I, P]),
             "or_head": (I, [P, P, I, P, I, P]),
             "or_argmax": (I, [P, I]),
@@ -119,6 +121,12 @@ def apply(w, x, bias=None, threads=1) -> np.ndarray:
 
 def set_scalar_apply(on: bool) -> None:
     lib().or_set_scalar_apply(1 if on else 0)
+
+
+def set_blocked(on: bool) -> None:
+    """Cache-blocked apply and eight-wide attention: the same bits as the reference loop order,
+    several times faster on long inputs (the full-depth parity tests use it)."""
+    lib().or_set_blocked(1 if on else 0)
 
 
 def dot(a, b) -> float:
@@ -247,6 +255,15 @@ class Cache:
 
     def __len__(self):
         return lib().or_cache_len(self.h)
+
+    def read(self, layer: int, pos0: int, n: int):
+        """(K, V) rows of positions [pos0, pos0 + n) of one layer, f32 [n][hkv*hd]."""
+        w = self.model.hkv * self.model.hd
+        k = np.empty((n, w), np.float32)
+        v = np.empty((n, w), np.float32)
+        if lib().or_cache_read(self.h, layer, pos0, n, _p(k), _p(v)):
+            raise ValueError("cache read outside the cached positions")
+        return k, v
 
     def __del__(self):
         if getattr(self, "h", None) and _lib is not None:

@@ -23,9 +23,12 @@ MISTAKES = ("swap_gate_up", "kv_head_mod", "no_sqrt_scale", "rope_adjacent_pairs
 
 
 class F64Model:
-    def __init__(self, gguf, mistake: str | None = None):
-        """gguf: any reader with .tensor(name) -> (kind, dims, raw) and .num(key)."""
+    def __init__(self, gguf, mistake: str | None = None, dtype=np.float64):
+        """gguf: any reader with .tensor(name) -> (kind, dims, raw) and .num(key).  dtype float32
+        runs the same textbook forward in f32 with numpy's (BLAS) summation orders: another
+        correct f32 ordering, used to measure how far two f32 implementations drift apart."""
         self.mistake = mistake
+        self.dtype = np.dtype(dtype)
         num = gguf.num
         self.L = int(num("laya.decoder.block_count"))
         self.d = int(num("laya.decoder.embedding_length"))
@@ -39,7 +42,7 @@ class F64Model:
 
     def _t(self, name):
         kind, dims, raw = self.g.tensor(name)
-        a = np_ref.decode(kind, raw).astype(np.float64)
+        a = np_ref.decode(kind, raw).astype(self.dtype)
         return a.reshape(list(reversed(dims))) if len(dims) > 1 else a
 
     def _has(self, name):
@@ -90,8 +93,8 @@ class F64Model:
             q = self._rope(qkv[:, :hq * hd], pos, hq, cos, sin)
             k = self._rope(qkv[:, hq * hd:(hq + hkv) * hd], pos, hkv, cos, sin)
             v = qkv[:, (hq + hkv) * hd:]
-            att = np.zeros((n, hq * hd))
-            scale = 1.0 if self.mistake == "no_sqrt_scale" else np.sqrt(hd)
+            att = np.zeros((n, hq * hd), self.dtype)
+            scale = self.dtype.type(1.0 if self.mistake == "no_sqrt_scale" else np.sqrt(hd))
             for hh in range(hq):
                 kh = hh % hkv if self.mistake == "kv_head_mod" else hh // grp
                 qh = q[:, hh * hd:(hh + 1) * hd]

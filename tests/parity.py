@@ -4,8 +4,13 @@
   hardware multiply quiets NaN payloads like any IEEE multiply);
 * logits: max |gpu - ref| <= 2e-2 * max |ref| over each position's logit vector;
 * option probabilities: max |gpu - ref| <= 1e-3;
-* argmax: equal, except at near-ties -- positions whose oracle top-2 gap is below the logit
-  tolerance are reported separately and not asserted.
+* argmax: equal, except at near-ties -- positions whose oracle top-2 gap is below a window tied
+  to the measured logit error of the precision mode under test are reported separately and not
+  asserted.  The exact mode (hi/lo split operands, f32 cache) stays within ~1e-5 of the largest
+  |logit| at the depths these tests run (up to 4 layers: measured 2e-6 median, 6e-5 worst row at 4
+  layers of the d2048 model), so its window is 1e-4 of the largest |logit|; the fast mode (f16
+  operands and cache) errs by up to ~5e-3, so its window is 2e-2.  The 24-layer tests derive their
+  window from the run's own measured error.
 """
 from __future__ import annotations
 
@@ -13,6 +18,22 @@ import numpy as np
 
 LOGIT_REL = 2e-2
 PROB_ABS = 1e-3
+TIE_EXACT = 1e-4
+TIE_FAST = 2e-2
+
+
+EXACT_LOGIT_REL = 1e-4  # the exact mode's own bar at test depths (measured <= 6e-5 at 4 layers of d2048)
+
+
+def tie_window(prec: int) -> float:
+    """Near-tie window (relative to the row's largest |logit|) of a precision mode (0 exact, 1 fast)."""
+    return TIE_EXACT if prec == 0 else TIE_FAST
+
+
+def logit_bar(prec: int) -> float:
+    """Logit bar of a precision mode: the north star's 2e-2 for the fast mode, and for the exact mode
+    a bar tight enough that an f16-only operand anywhere on the path (~1e-3) fails it."""
+    return EXACT_LOGIT_REL if prec == 0 else LOGIT_REL
 
 
 def assert_bits_equal(a: np.ndarray, b: np.ndarray) -> None:
@@ -43,7 +64,7 @@ def assert_logits_close(gpu: np.ndarray, ref: np.ndarray, rel: float = LOGIT_REL
     return err
 
 
-def argmax_report(gpu: np.ndarray, ref: np.ndarray, rel: float = LOGIT_REL):
+def argmax_report(gpu: np.ndarray, ref: np.ndarray, rel: float = TIE_EXACT):
     """(mismatches outside near-ties, near-tie count) for row-wise argmax."""
     gpu = np.atleast_2d(gpu)
     ref = np.atleast_2d(ref)
@@ -60,7 +81,7 @@ def argmax_report(gpu: np.ndarray, ref: np.ndarray, rel: float = LOGIT_REL):
     return bad, ties
 
 
-def assert_argmax_equal(gpu, ref, rel: float = LOGIT_REL) -> int:
+def assert_argmax_equal(gpu, ref, rel: float = TIE_EXACT) -> int:
     bad, ties = argmax_report(gpu, ref, rel)
     assert bad == 0, f"{bad} argmax mismatches outside near-ties ({ties} near-ties)"
     return ties

@@ -79,6 +79,38 @@ def test_daemon_answers_and_recovers(lh, gguf):
         assert o["usage"]["permutations"] == 3 and o["usage"]["output_tokens"] == 0
 
 
+# token fields that are not lists of int32-range integers: each gets its error line (with the id)
+BAD_TOKENS = [
+    dict(REQ, id="big", state=[5, 2 ** 40]),
+    dict(REQ, id="dict", questions={"q": {"type": "choice", "criteria": {"a": {"name": {"a": 1}}}}}),
+    dict(REQ, id="float", questions={"q": {"type": "noul", "instructions": [1.5]}}),
+    dict(REQ, id="str", state="hello"),
+    dict(REQ, id="bool", questions={"q": {"type": "score", "criteria": [[True], [2]]}}),
+]
+
+
+def test_daemon_rejects_bad_token_fields_and_goes_on(lh, gguf):
+    eng = HostScoredEngine(lh, gguf)
+    outs = run([json.dumps(r) for r in BAD_TOKENS] + [json.dumps(REQ)], eng)
+    assert len(outs) == len(BAD_TOKENS) + 1
+    for r, o in zip(BAD_TOKENS, outs):
+        assert "error" in o and o["id"] == r["id"], o
+        assert "token id" in o["error"] or "list of token ids" in o["error"], o
+    assert outs[-1]["id"] == "r1" and "answers" in outs[-1]
+
+
+def test_daemon_survives_unexpected_engine_errors(lh, gguf):
+    """An exception the request checks do not anticipate still becomes that request's error line."""
+    class Flaky(HostScoredEngine):
+        def decide(self, treq):
+            if treq["state"] == [666]:
+                raise OverflowError("engine blew up")
+            return super().decide(treq)
+    outs = run([json.dumps(dict(REQ, id="x", state=[666])), json.dumps(REQ)], Flaky(lh, gguf))
+    assert outs[0] == {"error": "OverflowError: engine blew up", "id": "x"}
+    assert outs[1]["id"] == "r1" and "answers" in outs[1]
+
+
 def test_daemon_request_validation():
     bad = [({"questions": {"q": {"type": "choice", "criteria": [1]}}}, "choice requires 1..255 options"),
            ({"questions": {"q": {"type": "score", "criteria": {"a": 1}}}}, "score requires 2..10 levels"),
@@ -156,6 +188,21 @@ def test_serve_registry_routes_per_model(lh, tmp_path):
     assert any("unknown model missing" in o.get("error", "") for o in outs)
 
 
+def test_serve_registry_bad_lines_keep_the_worker_alive(lh, tmp_path):
+    """A bad token field in a request for one model answers with an error line; the model's worker
+    goes on answering the requests queued after it."""
+    a, b = _two_models(lh, tmp_path)
+    reg = daemon.Registry([a, b], None, lambda g: HostScoredEngine(lh, g))
+    lines = [json.dumps(r) for r in BAD_TOKENS] + [json.dumps(dict(REQ, id=i)) for i in range(3)] + ["[1, 2]"]
+    out = io.StringIO()
+    daemon.serve_registry(reg, io.StringIO("".join(l + "\n" for l in lines)), out)
+    outs = [json.loads(l) for l in out.getvalue().splitlines()]
+    assert len(outs) == len(lines)
+    errs = {o.get("id"): o for o in outs if "error" in o}
+    assert set(r["id"] for r in BAD_TOKENS) <= set(errs)
+    assert sorted(o["id"] for o in outs if "answers" in o) == [0, 1, 2]
+
+
 class LayaScoredEngine:
     """Laya encoder stand-in: seeded option and act logits scored by lg_laya_decide_scores."""
 
@@ -192,3 +239,28 @@ def test_daemon_laya_answer_shape(lh):
     assert set(urg["probabilities"]) == {"0", "1", "2"} and urg["legend"] == {"0": [16], "1": [17], "2": [18, 19]}
     assert set(human["probabilities"]) == {"false", "true"} and human["noul"] == human["probabilities"]["true"]
     assert human["confidence"] == pytest.approx(max(human["noul"], 1 - human["noul"]), abs=1e-6)
+    # src/models/laya/decision.rs:293-303: usage has no option-order passes or state truncation
+    assert set(o["usage"]) == {"input_tokens", "output_tokens", "latency_ms"}
+
+
+def test_daemon_laya_empty_score_label_stays_empty(lh):
+    """A score level without a description keeps its empty label in the legend
+    (src/models/laya/decision.rs:247-257); the level index is OpenThai's fallback, not Laya's."""
+    eng = LayaScoredEngine(lh, lh.Gguf.from_bytes(lh.SynthImage("laya-tiny", seed=7)))
+    req = {"id": 1, "state": [5, 6], "questions": {"u": {"type": "score", "instructions": [15],
+                                                          "criteria": [[16], None, [18]]}}}
+    o, = run([json.dumps(req)], eng)
+    assert o["answers"]["u"]["legend"] == {"0": [16], "1": [], "2": [18]}
+
+
+def test_registry_laya_answers_name_laya_model_name(lh, tmp_path):
+    """Laya answers report laya.model_name (src/models/laya/decision.rs:293); requests still select the
+    model by its registry name."""
+    path = str(tmp_path / "laya.gguf")
+    lh.synth_file("laya-tiny", 7, path)
+    reg = daemon.Registry([path], None, lambda g: LayaScoredEngine(lh, g))
+    assert reg.model_names == ["Laya synthetic laya-tiny"] and reg.answer_names == ["laya"]
+    out = io.StringIO()
+    req = {k: v for k, v in REQ.items() if k != "permutations"}
+    daemon.serve(reg.engines[0], reg.answer_names[0], io.StringIO(json.dumps(req) + "\n"), out)
+    assert json.loads(out.getvalue())["model"] == "laya"

@@ -245,6 +245,44 @@ def test_apply_shapes(po, m, rows, K):
     assert np.abs(po.apply(w, x, b) - ref64).max() <= 1e-5 * max(1.0, np.abs(ref64).max()) * np.sqrt(K)
 
 
+@pytest.mark.parametrize("m,rows,K", [(1, 3, 5), (1, 1100, 37), (2, 2048, 64), (5, 7, 8), (7, 130, 2048),
+                                      (13, 601, 99), (64, 96, 5632)])
+def test_apply_blocked_mode_same_bits(po, m, rows, K):
+    """The cache-blocked loop nest (column blocks, two columns per pass, column split for few rows)
+    gives the bits of the numpy restatement of the reference order, tails and bias included."""
+    rng = np.random.default_rng(m * 7 + rows + K)
+    w = rng.normal(0, 1, (rows, K)).astype(np.float32)
+    x = rng.normal(0, 1, (m, K)).astype(np.float32)
+    b = rng.normal(0, 1, rows).astype(np.float32)
+    want = np_ref.kernel(w, x, b)
+    po.set_blocked(True)
+    try:
+        for threads in (1, 3, 8):
+            assert np.array_equal(bits(po.apply(w, x, b, threads)), bits(want))
+    finally:
+        po.set_blocked(False)
+
+
+def test_forward_blocked_mode_same_bits(lh, po):
+    """A whole forward (GQA attention over a cache, continuation by one token) in the blocked mode
+    equals the reference loop order bit for bit."""
+    img = lh.SynthImage("tiny-q4k", seed=3)
+    om = po.Model(po.Gguf(img.array()), threads=4)
+    ids = np.random.default_rng(4).integers(0, om.V, 70).astype(np.int32)
+    outs = []
+    for blocked in (False, True):
+        po.set_blocked(blocked)
+        try:
+            c = om.cache(128)
+            h1 = om.prefill(c, ids[:-1], [68, 3, 40])
+            h2 = om.prefill(c, ids[-1:], [0])
+            outs.append((om.head(h1), om.head(h2)))
+        finally:
+            po.set_blocked(False)
+    for a, b in zip(outs[0], outs[1]):
+        assert np.array_equal(bits(a), bits(b))
+
+
 # ------------------------------------------------------------------ elementwise rules
 
 def test_dot_is_sequential(po):

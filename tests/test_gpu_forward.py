@@ -9,7 +9,8 @@ checked as bit-exact properties of the GPU path.
 import numpy as np
 import pytest
 
-from parity import (assert_argmax_equal, assert_logits_close, assert_probs_close, logit_error)
+from parity import (assert_argmax_equal, assert_logits_close, assert_probs_close, logit_bar, logit_error,
+                    tie_window)
 
 pytestmark = pytest.mark.gpu
 
@@ -41,8 +42,9 @@ def test_forward_options_and_probs(pair, lh, po):
     b = eng.batch([(s, ids, pos)])
     logits, probs, logprobs = b.run(OPTIONS, temperature=1.0)
     want = om.forward(ids, pos, OPTIONS)
-    assert_logits_close(logits, want)
-    assert_argmax_equal(logits, want)
+    prec = eng.info["precision"]
+    assert_logits_close(logits, want, rel=logit_bar(prec))
+    assert_argmax_equal(logits, want, rel=tie_window(prec))
     for r in range(len(pos)):
         p_ref, lp_ref, _ = po.option_scores(want[r])
         assert_probs_close(probs[r], p_ref)
@@ -56,8 +58,9 @@ def test_forward_full_vocab(pair):
     s = eng.seq_create()
     got = eng.forward(s, ids, [76, 30])
     want = om.forward(ids, [76, 30])
-    assert_logits_close(got, want)
-    assert_argmax_equal(got, want)
+    prec = eng.info["precision"]
+    assert_logits_close(got, want, rel=logit_bar(prec))
+    assert_argmax_equal(got, want, rel=tie_window(prec))
     eng.seq_free(s)
 
 
@@ -176,8 +179,8 @@ def test_golden_logits(lh, prec):
         img = lh.SynthImage(preset, seed=int(gold["seed"]))
         eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=1024, precision=prec)
         got = eng.forward(eng.seq_create(), gold[f"{preset}/ids"], gold[f"{preset}/pos"])
-        err = assert_logits_close(got, gold[f"{preset}/logits"])
-        assert_argmax_equal(got, gold[f"{preset}/logits"])
+        err = assert_logits_close(got, gold[f"{preset}/logits"], rel=logit_bar(prec))
+        assert_argmax_equal(got, gold[f"{preset}/logits"], rel=tie_window(prec))
         print(f"{preset} prec {prec}: golden rel {err:.2e}")
         eng.close()
 
@@ -195,7 +198,7 @@ def test_plumbing_model_decision(lh, po, prec):
     logits, probs, _ = eng.batch([(s, ids, [143])]).run(yes_no)
     want = om.forward(ids, [143], yes_no)
     p_ref, _, _ = po.option_scores(want[0])
-    assert_logits_close(logits, want)
+    assert_logits_close(logits, want, rel=logit_bar(prec))
     assert_probs_close(probs[0], p_ref)
     assert int(np.argmax(probs[0])) == int(np.argmax(p_ref))
     print(f"plumbing: logit err {logit_error(logits, want):.2e} probs {probs[0]} ref {p_ref}")
@@ -217,8 +220,11 @@ def test_q8_2048_full_width(lh, po, layers, tokens):
     logits, probs, _ = eng.batch([(s, ids, pos)]).run(opts)
     want = om.forward(ids, pos, opts)
     p_ref = np.stack([po.option_scores(w)[0] for w in want])
-    err = assert_logits_close(logits, want)
+    # this model amplifies f32 rounding layer over layer: at 4 layers two correct f32 orders already
+    # sit up to 2.1e-4 apart (the oracle against a float64 forward), so the exact mode's bar here is
+    # 5e-4 -- still a quarter of what one f16-only operand costs at a single layer (~2e-3)
+    err = assert_logits_close(logits, want, rel=5e-4)
     perr = assert_probs_close(probs, p_ref)
-    assert_argmax_equal(logits, want)
+    assert_argmax_equal(logits, want, rel=1e-3)
     print(f"q8-2048 L{layers} T{tokens}: logit rel {err:.2e} prob {perr:.2e}")
     eng.close()

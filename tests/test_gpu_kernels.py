@@ -44,13 +44,16 @@ def test_dequant_f16_exhaustive(lh, po):
     assert_bits_equal(got, po.decode(1, codes.view(np.uint8)))
 
 
-@pytest.fixture(scope="module", params=["tiny-f16", "tiny-q8", "tiny-q4k"])
+@pytest.fixture(scope="module", params=[("tiny-f16", 0), ("tiny-q8", 0), ("tiny-q4k", 0), ("tiny-f16", 1),
+                                        ("tiny-q8", 1)],
+                ids=lambda p: f"{p[0]}-{'exact' if p[1] == 0 else 'fast'}")
 def model(request, lh, po):
-    img = lh.SynthImage(request.param, seed=11)
+    preset, prec = request.param
+    img = lh.SynthImage(preset, seed=11)
     g = lh.Gguf.from_bytes(img)
-    eng = lh.Engine(g, kv_tokens=4096)
+    eng = lh.Engine(g, kv_tokens=4096, precision=prec)
     og = po.Gguf(img.array())
-    yield request.param, img, eng, og
+    yield f"{preset}-{'exact' if prec == 0 else 'fast'}", img, eng, og
     eng.close()
 
 
@@ -78,5 +81,13 @@ def test_matmul_vs_apply(model, po, m):
         print(f"{preset} {name} m={m}", flush=True)
         got = eng.matmul(name, x, bias)
         want = po.apply(w, x, bias, threads=4)
-        # m == 1 runs the f32 GEMV; m > 1 the f16-input MFMA GEMM
-        assert_logits_close(got, want, rel=1e-5 if m == 1 else 1e-2)
+        # m == 1 runs the f32 GEMV in both modes.  m > 1 runs the MFMA GEMM: in the exact mode on
+        # hi/lo f16 planes of x with the weights applied exactly (about 2^-22 per product, so
+        # 1e-5 of the largest output; a GEMM that dropped the lo plane errs by ~1e-3), in the
+        # fast mode on f16 x and f16-rounded weights (within 1e-2, and measurably above 1e-5:
+        # the exact-mode bar tells the two apart).
+        if m == 1 or preset.endswith("exact"):
+            assert_logits_close(got, want, rel=1e-5)
+        else:
+            err = assert_logits_close(got, want, rel=1e-2)
+            assert err > 1e-5, f"fast-mode error {err:.2e} is inside the exact-mode bar"
