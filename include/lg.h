@@ -201,6 +201,16 @@ int lg_batch_rewind(lg_engine *e, lg_batch *b);
  * (first maximum wins, src/models/openthai/decision.rs:330-335); logits (optional, host,
  * [steps][vocab]) each step's full-vocabulary logits. */
 int lg_decode(lg_engine *e, int seq, int32_t first, int steps, int32_t *tokens, float *logits);
+/* lg_decode without any device allocation: its workspace (activations, attention page partials,
+ * argmax partials, token slots and page table) lives in a fixed 16 MiB scratch array that every GPU
+ * the library runs on holds until the process ends, so the call makes no hipMalloc/hipFree.  No
+ * counterpart in the reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Results equal lg_decode.
+ * A run whose workspace exceeds the scratch (long contexts or many steps; about 30k tokens of
+ * context on the 7B shape) fails with LG_ERR_INVALID and changes nothing.  Every call on one GPU
+ * shares that GPU's scratch: calls that overlap on one GPU (engines driven from several threads)
+ * race, and must be serialised by the caller. */
+int lg_decode_noalloc(lg_engine *e, int seq, int32_t first, int steps, int32_t *tokens, float *logits);
 
 /* Option scores over host logits, the CPU side of the same rule (for callers that
  * already hold logits).  Replaces src/models/openthai/decision.rs:268-279. */

@@ -352,6 +352,13 @@ int lg_decode(lg_engine *e, int seq, int32_t first, int steps, int32_t *tokens, 
   });
 }
 
+int lg_decode_noalloc(lg_engine *e, int seq, int32_t first, int steps, int32_t *tokens, float *logits) {
+  return guard([&] {
+    NEED(e, "engine");
+    e->e->decode_noalloc(seq, first, steps, tokens, logits);
+  });
+}
+
 namespace {
 
 // The Laya decide of `reqs` (src/models/laya/decision.rs:168-318, one forward per question):

@@ -7,6 +7,7 @@
 #include <numeric>
 
 #include "common.h"
+#include "noalloc.h"
 
 namespace lg {
 
@@ -884,14 +885,49 @@ void Engine::forward(int sq, const int32_t *ids, int n, const int32_t *positions
 }
 
 // ------------------------------------------------------------------ greedy decode
-void Engine::decode(int sq, int32_t first, int steps, int32_t *tokens, float *logits) {
+void Engine::decode_check(const Seq &s, int32_t first, int steps, const int32_t *tokens) const {
   if (arch != Arch::Decoder) fail(LG_ERR_UNSUPPORTED, "decode: this model has a decision head, not a language-model head");
-  Seq &s = seq(sq);
   LG_REQUIRE(steps > 0 && tokens, "decode: need steps > 0 and an output");
   LG_REQUIRE(first >= 0 && first < V, "decode: token id %d outside the vocabulary", first);
   LG_REQUIRE(hd == 128, "decode: head_dim %d has no decode attention kernel", hd);
+  if (int64_t(s.len) + steps > ctx)
+    fail(LG_ERR_INVALID, "sequence of %lld tokens exceeds the context length %d", (long long)s.len + steps, ctx);
+}
+
+// Workspace of a decode run: x, q|k|v, attention output, SwiGLU output, logits, argmax partial maxima,
+// attention page partials (f32), then the token slots, the page table and the argmax partial indices.
+size_t Engine::decode_ws_bytes(int pos0, int steps) const {
+  const int qw = hq * hd, qkvw = qw + 2 * hkv * hd;
+  const size_t part_floats = size_t(attn_decode_scratch_floats(1, hq, hd, pos0 + steps));
+  const size_t floats = size_t(d) + qkvw + qw + f + V + 64 + part_floats;
+  const size_t pages = size_t(pos0 + steps + 63) / 64;
+  return floats * 4 + (size_t(steps) + 1 + pages) * 4 + 64 * 4 + 256;
+}
+
+void Engine::decode(int sq, int32_t first, int steps, int32_t *tokens, float *logits) {
+  Seq &s = seq(sq);
+  decode_check(s, first, steps, tokens);
+  reserve_pages(s, s.len + steps);
+  ws_dec_.ensure(decode_ws_bytes(s.len, steps));
+  decode_run(s, first, steps, tokens, logits, ws_dec_.p);
+}
+
+void Engine::decode_noalloc(int sq, int32_t first, int steps, int32_t *tokens, float *logits) {
+  Seq &s = seq(sq);
+  decode_check(s, first, steps, tokens);
+  const size_t need = decode_ws_bytes(s.len, steps);
+  if (need > kNoAllocScratchBytes)
+    fail(LG_ERR_INVALID,
+         "decode_noalloc: %d steps after %d tokens need %zu bytes of scratch; the per-GPU limit is %zu "
+         "(use lg_decode for longer contexts)",
+         steps, s.len, need, kNoAllocScratchBytes);
+  void *ws = noalloc_scratch(device);
+  reserve_pages(s, s.len + steps);
+  decode_run(s, first, steps, tokens, logits, ws);
+}
+
+void Engine::decode_run(Seq &s, int32_t first, int steps, int32_t *tokens, float *logits, void *ws) {
   const int pos0 = s.len;
-  reserve_pages(s, pos0 + steps);
   const int qw = hq * hd, kvw = hkv * hd, qkvw = qw + 2 * kvw;
   const int max_pages = int(s.pages.size());
   // device metadata, uploaded once: token slots (step i reads slot i, its argmax goes to slot
@@ -901,9 +937,7 @@ void Engine::decode(int sq, int32_t first, int steps, int32_t *tokens, float *lo
   meta.resize(steps + 1, 0);
   for (int p : s.pages) meta.push_back(p);
   const size_t part_floats = size_t(attn_decode_scratch_floats(1, hq, hd, pos0 + steps));
-  const size_t floats = size_t(d) + qkvw + qw + f + V + 64 + part_floats;
-  ws_dec_.ensure(floats * 4 + meta.size() * 4 + 64 * 8 + 4096);
-  float *x = ws_dec_.as<float>();
+  float *x = static_cast<float *>(ws);
   float *qkv = x + d, *att = qkv + qkvw, *act = att + qw, *lg = act + f;
   float *part_v = lg + V;
   float *part = part_v + 64;

@@ -268,6 +268,7 @@ def lib() -> ctypes.CDLL:
             "lg_batch_run": (I, [P, P, P, I, F, P, P, P, CANCEL_FN, P]),
             "lg_batch_rewind": (I, [P, P]),
             "lg_decode": (I, [P, I, ctypes.c_int32, I, P, P]),
+            "lg_decode_noalloc": (I, [P, I, ctypes.c_int32, I, P, P]),
             "lg_option_scores": (I, [P, I, F, P, P]),
             "lg_decide": (I, [P, ctypes.POINTER(DecideRequest), ctypes.POINTER(DecideResult), CANCEL_FN, P]),
             "lg_laya_forward": (I, [P, ctypes.POINTER(LayaInput), I, P, P, CANCEL_FN, P]),
@@ -600,10 +601,13 @@ class Engine:
             at += k
         return out
 
-    def decode(self, seq: int, first: int, steps: int, want_logits: bool = False):
+    def decode(self, seq: int, first: int, steps: int, want_logits: bool = False, noalloc: bool = False):
+        """Greedy decode (lg_decode); noalloc=True runs lg_decode_noalloc (workspace in the per-GPU
+        scratch, no device allocation)."""
         toks = np.empty(steps, dtype=np.int32)
         lg = np.empty((steps, self.info["vocab"]), dtype=np.float32) if want_logits else None
-        check(lib().lg_decode(self.h, seq, first, steps, _ptr(toks), _ptr(lg)))
+        fn = lib().lg_decode_noalloc if noalloc else lib().lg_decode
+        check(fn(self.h, seq, first, steps, _ptr(toks), _ptr(lg)))
         return (toks, lg) if want_logits else toks
 
     def profile(self, on: bool = True) -> None:
