@@ -8,11 +8,18 @@ One step = one full batch: embedding, 24 layers of dequant-fused MFMA GEMMs + pa
 attention, head rows and option softmax.  Inputs (token ids, page tables) are staged in HBM
 before the timed region; the staged batch is rewound and re-executed each step.
 
-Also reported: batch-1 Q8_0 decode over a 2048-token context (64 greedy steps) with the
-GEMV HBM roofline, and the CPU oracle (the reference algorithm restated in C, AVX2 8-lane FMA
-kernel, rows split over threads) timed on a bounded sample on this host.
+Nested under `configs`, each with its own `roofline` and `cpu_baseline` (4 threads, the reference's
+default) and `cpu_baseline_all_cores` (16 threads, this job's host share):
+  C1  plumbing decide latency (6-layer d512 F16 model, 144-token request);
+  C3  batch-1 Q8_0 greedy decode over a 2048-token context, 64 steps (GEMV HBM roofline);
+  C4  Q4_K/Q6_K 7B-shape prefill, 32 x 1024 tokens (MFMA roofline);
+  C5  F16 7B-shape long context, 16 x 8192 tokens sharing a 6144-token prefix (MFMA roofline of the
+      GEMMs and of the attention).
+The CPU baselines are the oracle (the reference algorithm restated in C: F32 weights, 4-row x 8-lane
+FMA kernel, rows split over threads) timed on bounded samples on this host; each says what it timed
+and how it was scaled.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--precision exact|fast]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--precision exact|fast] [--configs C1,C3,C4,C5]
 """
 import argparse
 import json
@@ -100,7 +107,54 @@ def bench_prefill(eng, steps, warmup):
     return T, dt, prof, probs
 
 
-def bench_decode(eng, steps):
+def roofline(bound, achieved, peak, unit, kernel, launches=None, avg_launch_ms=None, traffic=None, **extra):
+    r = {"bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
+         "frac": round(achieved / peak, 4), "traffic": traffic, "kernel": kernel}
+    if launches is not None:
+        r["launches"] = launches
+    if avg_launch_ms is not None:
+        r["avg_launch_ms"] = round(avg_launch_ms, 5)
+    r.update(extra)
+    return r
+
+
+def rate(p, what):
+    """TFLOP/s (what = "flops") or GB/s ("bytes") of a profiled kernel class."""
+    if not p["ms"]:
+        return 0.0
+    return p[what] / (p["ms"] * 1e-3) / (1e12 if what == "flops" else 1e9)
+
+
+def cpu_entry(value, unit, cores, sample):
+    return {"value": value, "unit": unit, "cores": cores, "kind": "port", "sample": sample}
+
+
+def oracle_modules():
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as po
+    return po
+
+
+def cpu_threads(args):
+    """(thread counts to time): the reference's default 4, and the host share this job may use."""
+    return [t for t in dict.fromkeys([args.cpu_threads, args.cpu_threads_all]) if t > 0]
+
+
+def cpu_pair(entries):
+    """cpu_baseline (the first thread count) plus, when timed, cpu_baseline_all_cores."""
+    out = {}
+    if entries:
+        out["cpu_baseline"] = entries[0]
+    if len(entries) > 1:
+        out["cpu_baseline_all_cores"] = entries[1]
+    return out
+
+
+# ---------------------------------------------------------------- C3: batch-1 greedy decode
+def c3_decode(eng, args):
+    """The benchmark's 2048-token context on the Q8_0 d2048 model, then DECODE_STEPS greedy steps
+    (one forked sequence per run, so every run decodes the same positions)."""
+    steps = args.decode_steps
     rng = np.random.default_rng(SEED + 1)
     ids = rng.integers(0, eng.info["vocab"], DECODE_CTX).astype(np.int32)
     base = eng.seq_create()
@@ -122,106 +176,222 @@ def bench_decode(eng, steps):
         eng.seq_free(s)
     prof = {c: eng.profile_read(c) for c in ("gemv", "attn_decode", "argmax", "embed")}
     eng.seq_free(base)
-    dt = runs[1][1]
     assert np.array_equal(runs[0][2], runs[1][2]), "decode is not deterministic"
-    return dt, prof
+    dt = runs[1][1]
+    gv, at = prof["gemv"], prof["attn_decode"]
+    log(f"C3 decode: {dt / steps * 1e3:.3f} ms/token, gemv {rate(gv, 'bytes'):.0f} GB/s over {gv['launches']} "
+        f"launches, attention {rate(at, 'bytes'):.0f} GB/s")
+    for c, p in prof.items():
+        log(f"  {c:12s} launches {p['launches']:5d}  {p['ms']:8.3f} ms")
+    out = {
+        "workload": f"Q8_0 batch-1 greedy decode: {DECODE_CTX}-token context, {steps} steps; 24 layers, d_model 2048, "
+                    f"16 x 128 heads, FFN 5632, vocab 32000, Q8_0 matrices and head",
+        "value": round(steps / dt, 2), "unit": "tok/s", "higher_is_better": True, "steps": steps,
+        "ms_per_token": round(dt / steps * 1e3, 4),
+        "roofline": roofline("hbm", rate(gv, "bytes"), PEAK_HBM_GBS, "GB/s",
+                             "gemv (dequant-fused Q8_0 GEMV, GGUF bytes per launch)", gv["launches"],
+                             gv["ms"] / max(1, gv["launches"]), measured_traffic("gemv")),
+        "attention": roofline("hbm", rate(at, "bytes"), PEAK_HBM_GBS, "GB/s",
+                              "attn_decode (f32 KV bytes read per launch, incl. the page-combine launch)",
+                              at["launches"], at["ms"] / max(1, at["launches"])),
+        "kernel_ms_per_token": {c: round(p["ms"] / steps, 4) for c, p in prof.items()},
+    }
+    if not args.no_cpu:
+        po = oracle_modules()
+        layers = 2
+        img = lh.SynthImage(PRESET, seed=SEED, n_layers=layers)
+        om = po.Model(po.Gguf(img.array()), threads=args.cpu_threads_all)
+        c = om.cache(DECODE_CTX + 8)
+        po.set_blocked(True)  # the context is set-up, not timed: same bits, faster
+        om.prefill(c, ids, [])
+        po.set_blocked(False)
+        feed = [first] + [int(t) for t in runs[1][2][:3]]
+        t0 = time.perf_counter()
+        for t in feed:
+            h = om.prefill(c, [t], [0])
+            om.head(h)
+        t_steps = (time.perf_counter() - t0) / len(feed)
+        t0 = time.perf_counter()
+        for _ in range(4):
+            om.head(h)
+        t_head = (time.perf_counter() - t0) / 4
+        per_token = (t_steps - t_head) * (24 / layers) + t_head
+        out["cpu_baseline"] = cpu_entry(
+            round(1 / per_token, 3), "tok/s", 1,
+            f"{len(feed)} KV-cached decode steps after the {DECODE_CTX}-token context through {layers} of 24 layers "
+            f"({t_steps * 1e3:.0f} ms per step, of which the 32000-row head {t_head * 1e3:.0f} ms), layer part scaled "
+            f"x{24 // layers}: {per_token * 1e3:.0f} ms per token. One row per step is one worker in the reference's "
+            f"row split (tensor.rs:17-18), whatever the thread count; a KV cache is the oracle's addition (the "
+            f"reference recomputes the whole sequence every call)")
+        del om
+    return out
 
 
-def base_line(metric, value, unit, higher, steps, warmup, ms, prec, workload, **extra):
-    return {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": steps, "warmup": warmup,
-            "ms_per_step": round(ms, 3), "higher_is_better": higher, "scaling": "weak", "vs_baseline": None,
-            "dtype": "f32" if prec == lh.PREC_EXACT else "f16", "data": "synthetic",
-            "config": dict(workload=workload, seed=SEED,
-                           precision="exact" if prec == lh.PREC_EXACT else "fast", **extra)}
-
-
-def bench_plumbing(args, prec):
+# ---------------------------------------------------------------- C1: plumbing latency
+def c1_plumbing(args, prec):
     """The CPU-runnable plumbing model (6 layers, d512, 8 x 64 heads, F16): one decide request of a
     128-token prompt plus one 16-token yes/no question block, scored at its answer position.
-    Latency of the whole request (stage nothing: ids are uploaded inside the timed call)."""
+    Latency of the whole request (ids uploaded, forward, option scores read back)."""
     img = lh.SynthImage("plumbing-f16", seed=SEED)
     eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=2048, max_batch_tokens=512, precision=prec)
     ids = np.random.default_rng(SEED + 2).integers(0, 32000, 144).astype(np.int32)
     yes_no = np.array([1939, 4874], np.int32)
-    for _ in range(max(args.warmup, 3)):
-        s = eng.seq_create()
-        eng.forward(s, ids, [143], yes_no)
-        eng.seq_free(s)
-    times = []
-    for _ in range(max(args.steps, 20)):
-        eng.sync()
-        t0 = time.perf_counter()
+
+    def one():
         s = eng.seq_create()
         logits = eng.forward(s, ids, [143], yes_no)
         probs, _ = lh.option_scores(logits[0])
         eng.seq_free(s)
+        return probs
+    for _ in range(max(args.warmup, 3)):
+        one()
+    times = []
+    for _ in range(max(args.steps, 20)):
+        eng.sync()
+        t0 = time.perf_counter()
+        one()
         times.append(time.perf_counter() - t0)
+    eng.profile_reset()
+    eng.profile(True)
+    one()
+    eng.profile(False)
+    gp = eng.profile_read("gemm")
     eng.close()
     med = float(np.median(times)) * 1e3
-    log(f"plumbing: median {med:.3f} ms per decide request (min {min(times) * 1e3:.3f})")
-    return base_line("plumbing decide latency (1 request, 144 tokens, yes/no option scoring)", round(med, 3),
-                     "ms", False, len(times), max(args.warmup, 3), med, prec,
-                     "6 layers, d_model 512, 8 x 64 heads, FFN 1408, vocab 32000, F16 weights N(0, 0.02); "
-                     "128-token prompt + one 16-token noul question block, 2 option tokens",
-                     p50_ms=round(med, 3), min_ms=round(min(times) * 1e3, 3))
+    log(f"C1 plumbing: median {med:.3f} ms per decide request (min {min(times) * 1e3:.3f}), gemm "
+        f"{rate(gp, 'flops'):.1f} TFLOP/s over {gp['launches']} launches")
+    out = {
+        "workload": "plumbing decide request: 6 layers, d_model 512, 8 x 64 heads, FFN 1408, vocab 32000, F16 weights "
+                    "N(0, 0.02); 128-token prompt + one 16-token noul question block, 2 option tokens",
+        "value": round(med, 3), "unit": "ms per request", "higher_is_better": False, "steps": len(times),
+        "p50_ms": round(med, 3), "min_ms": round(min(times) * 1e3, 3),
+        "roofline": roofline("mfma", rate(gp, "flops"), PEAK_F16_TFLOPS, "TFLOP/s",
+                             "gemm (every projection of the 144-token forward; launch-bound at this size)",
+                             gp["launches"], gp["ms"] / max(1, gp["launches"])),
+    }
+    if not args.no_cpu:
+        po = oracle_modules()
+        om = po.Model(po.Gguf(img.array()), threads=1)
+        entries = []
+        for t in cpu_threads(args):
+            om.set_threads(t)
+            ts = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                w = om.forward(ids, [143], yes_no)
+                po.option_scores(w[0])
+                ts.append(time.perf_counter() - t0)
+            cm = float(np.median(ts)) * 1e3
+            entries.append(cpu_entry(round(cm, 2), "ms per request", t,
+                                     f"the same request through all 6 layers, median of 3: {cm:.1f} ms"))
+        out.update(cpu_pair(entries))
+        del om
+    return out
 
 
-def bench_q4k(args, prec):
+# ---------------------------------------------------------------- C4: Q4_K/Q6_K 7B prefill
+Q4K_REQS, Q4K_TOKENS = 32, 1024
+C5_REQS, C5_PREFIX, C5_OWN, C5_QUESTIONS = 16, 6144, 2048, 8
+
+
+def cpu_layer_cost_7b(args, po):
+    """The oracle on one layer of the 7B shape (d3584, GQA 28/4 x 128, FFN 18944): seconds for one
+    1024-token request through one layer, per thread count (F32 weights after the load-time expansion,
+    so the cost is the same for the Q4_K/Q6_K and F16 files)."""
+    img = lh.SynthImage("q4km-7b", seed=SEED, n_layers=1)
+    om = po.Model(po.Gguf(img.array()), threads=1)
+    ids = np.random.default_rng(SEED + 3).integers(0, 152064, Q4K_TOKENS).astype(np.int32)
+    cost = {}
+    for t in cpu_threads(args):
+        om.set_threads(t)
+        t0 = time.perf_counter()
+        om.forward(ids, [Q4K_TOKENS - 1], [1, 2, 3, 4])
+        cost[t] = time.perf_counter() - t0
+        log(f"  oracle 7B shape, one layer, {Q4K_TOKENS} tokens, {t} threads: {cost[t]:.2f} s")
+    del om
+    return cost
+
+
+def c4_q4k(args, prec, layer_cost):
     """Q4_K/Q6_K 7B shape (28 layers, d3584, GQA 28/4 x 128, FFN 18944, vocab 152064, QKV bias):
     a batch of 32 requests x 1024 tokens, 4 option tokens scored at the last position."""
-    log("generating q4km-7b (28 layers)")
+    t0 = time.perf_counter()
     img = lh.SynthImage("q4km-7b", seed=SEED)
-    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=32 * 1024 + 1024, max_batch_tokens=32768, precision=prec)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=Q4K_REQS * Q4K_TOKENS + 1024, max_batch_tokens=32768,
+                    precision=prec)
+    log(f"C4 model ready in {time.perf_counter() - t0:.1f}s")
     rng = np.random.default_rng(SEED + 3)
-    reqs = [(rng.integers(0, 152064, 1024).astype(np.int32), np.array([1023], np.int32)) for _ in range(32)]
+    reqs = [(rng.integers(0, 152064, Q4K_TOKENS).astype(np.int32), np.array([Q4K_TOKENS - 1], np.int32))
+            for _ in range(Q4K_REQS)]
     opts = rng.choice(152064, 4, replace=False).astype(np.int32)
     seqs = [eng.seq_create() for _ in reqs]
     batch = eng.batch([(s, ids, pos) for s, (ids, pos) in zip(seqs, reqs)])
-    for _ in range(args.warmup):
+    warm, steps = 2, args.config_steps
+    for _ in range(warm):
         batch.run(opts)
         batch.rewind()
     eng.sync()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         out = batch.run(opts)
         batch.rewind()
     eng.sync()
-    dt = (time.perf_counter() - t0) / args.steps
+    dt = (time.perf_counter() - t0) / steps
     eng.profile_reset()
     eng.profile(True)
     batch.run(opts)
     eng.profile(False)
-    gp = eng.profile_read("gemm")
-    tf = gp["flops"] / (gp["ms"] * 1e-3) / 1e12
+    prof = {c: eng.profile_read(c) for c in ("gemm", "attn_prefill", "rope_kv", "rmsnorm", "head")}
     assert np.isfinite(out[1]).all()
     eng.close()
-    log(f"q4km-7b: {dt * 1e3:.1f} ms/step, {32768 / dt:.0f} tok/s, gemm {tf:.1f} TFLOP/s")
-    return base_line("Q4_K/Q6_K 7B batched prefill tok/s (32 x 1024)", round(32768 / dt, 1), "tok/s", True,
-                     args.steps, args.warmup, dt * 1e3, prec,
-                     "28 layers, d_model 3584, GQA 28/4 x 128, FFN 18944, vocab 152064, QKV bias; Q4_K q/k/o/"
-                     "gate/up, Q6_K v/down/output; 32 requests x 1024 tokens, 4 options at the last position",
-                     req_per_s=round(32 / dt, 2), gemm_tflops=round(tf, 1),
-                     gemm_frac=round(tf / PEAK_F16_TFLOPS, 4))
+    T = Q4K_REQS * Q4K_TOKENS
+    gp = prof["gemm"]
+    log(f"C4 q4km-7b: {dt * 1e3:.1f} ms/step, {T / dt:.0f} tok/s, gemm {rate(gp, 'flops'):.1f} TFLOP/s")
+    for c, p in prof.items():
+        log(f"  {c:12s} launches {p['launches']:5d}  {p['ms']:8.3f} ms")
+    res = {
+        "workload": "Q4_K/Q6_K 7B-shape batched prefill: 28 layers, d_model 3584, GQA 28/4 x 128, FFN 18944, vocab "
+                    "152064, QKV bias; Q4_K q/k/o/gate/up, Q6_K v/down/output; 32 requests x 1024 tokens, 4 option "
+                    "tokens at the last position",
+        "value": round(T / dt, 1), "unit": "tok/s", "higher_is_better": True, "steps": steps, "warmup": warm,
+        "ms_per_step": round(dt * 1e3, 2), "req_per_s": round(Q4K_REQS / dt, 2),
+        "roofline": roofline("mfma", rate(gp, "flops"), PEAK_F16_TFLOPS, "TFLOP/s",
+                             "gemm (dequant-fused K-quant MFMA GEMM; three f16 passes per product, so the "
+                             "arithmetic ceiling is a third of the f16 rate)", gp["launches"],
+                             gp["ms"] / max(1, gp["launches"])),
+        "kernel_ms_per_step": {c: round(p["ms"], 3) for c, p in prof.items()},
+    }
+    if layer_cost:
+        entries = []
+        for t, sec in layer_cost.items():
+            per_req = sec * 28
+            entries.append(cpu_entry(round(Q4K_TOKENS / per_req, 2), "tok/s", t,
+                                     f"one 1024-token request through 1 of 28 layers ({sec:.2f} s; weights "
+                                     f"expanded to F32 at load as the reference does), scaled x28: {per_req:.0f} s "
+                                     f"per request, requests one after another"))
+        res.update(cpu_pair(entries))
+    return res
 
 
-def bench_long_context(args, prec):
+def c5_long_context(args, prec, layer_cost):
     """F16 7B shape with a shared prefix: 16 requests of 8192 tokens sharing their first 6144.
-    One step = the prefix computed once, forked into 16 requests, their 2048 own tokens
-    prefilled as one batch, 8 answer positions each scored over 4 option tokens."""
-    log("generating f16-7b (28 layers)")
+    One step = the prefix computed once, forked into 16 requests, their 2048 own tokens prefilled as
+    one batch, 8 answer positions each scored over 4 option tokens."""
+    t0 = time.perf_counter()
     img = lh.SynthImage("f16-7b", seed=SEED)
-    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=6144 + 16 * 2048 + 2048, max_batch_tokens=32768,
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=C5_PREFIX + C5_REQS * C5_OWN + 2048, max_batch_tokens=32768,
                     precision=prec)
+    log(f"C5 model ready in {time.perf_counter() - t0:.1f}s")
     rng = np.random.default_rng(SEED + 4)
-    prefix = rng.integers(0, 152064, 6144).astype(np.int32)
-    own = [rng.integers(0, 152064, 2048).astype(np.int32) for _ in range(16)]
-    pos = np.arange(255, 2048, 256).astype(np.int32)  # 8 questions per request
+    prefix = rng.integers(0, 152064, C5_PREFIX).astype(np.int32)
+    own = [rng.integers(0, 152064, C5_OWN).astype(np.int32) for _ in range(C5_REQS)]
+    pos = np.arange(C5_OWN // C5_QUESTIONS - 1, C5_OWN, C5_OWN // C5_QUESTIONS).astype(np.int32)
     opts = rng.choice(152064, 4, replace=False).astype(np.int32)
 
     def step():
         base = eng.seq_create()
         eng.forward(base, prefix, [], opts)
-        kids = [eng.seq_fork(base, 6144) for _ in own]
+        kids = [eng.seq_fork(base, C5_PREFIX) for _ in own]
         b = eng.batch([(k, ids, pos) for k, ids in zip(kids, own)])
         out = b.run(opts)
         b.free()
@@ -230,24 +400,99 @@ def bench_long_context(args, prec):
         eng.seq_free(base)
         return out
 
-    for _ in range(args.warmup):
+    warm, steps = 1, args.config_steps
+    for _ in range(warm):
         step()
     eng.sync()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         out = step()
     eng.sync()
-    dt = (time.perf_counter() - t0) / args.steps
+    dt = (time.perf_counter() - t0) / steps
+    eng.profile_reset()
+    eng.profile(True)
+    step()
+    eng.profile(False)
+    prof = {c: eng.profile_read(c) for c in ("gemm", "attn_prefill", "rope_kv", "rmsnorm", "head")}
     assert np.isfinite(out[1]).all()
     eng.close()
-    tokens = 6144 + 16 * 2048
-    log(f"f16-7b long context: {dt * 1e3:.1f} ms/step, {tokens / dt:.0f} computed tok/s, {16 / dt:.2f} req/s")
-    return base_line("F16 7B shared-prefix long-context decide (16 x 8192, 6144 shared)", round(16 * 8192 / dt, 1),
-                     "tok/s", True, args.steps, args.warmup, dt * 1e3, prec,
-                     "28 layers, d_model 3584, GQA 28/4 x 128, FFN 18944, vocab 152064, F16 weights; 16 requests x "
-                     "8192 tokens sharing the first 6144 (computed once, forked), 8 answer positions each, 4 options",
-                     requests_per_s=round(16 / dt, 3), computed_tok_per_s=round(tokens / dt, 1),
-                     note="value counts every request's 8192 tokens; computed_tok_per_s counts tokens prefilled")
+    hq, hd, L = 28, 128, 28
+    pairs = C5_PREFIX * (C5_PREFIX + 1) // 2 + C5_REQS * (C5_OWN * C5_PREFIX + C5_OWN * (C5_OWN + 1) // 2)
+    att_flops = 4.0 * hd * hq * L * pairs
+    ap, gp = prof["attn_prefill"], prof["gemm"]
+    att_tf = att_flops / (ap["ms"] * 1e-3) / 1e12 if ap["ms"] else 0.0
+    computed = C5_PREFIX + C5_REQS * C5_OWN
+    log(f"C5 f16-7b long context: {dt * 1e3:.1f} ms/step, {C5_REQS / dt:.2f} req/s, gemm {rate(gp, 'flops'):.1f} "
+        f"TFLOP/s, attention {att_tf:.1f} TFLOP/s")
+    for c, p in prof.items():
+        log(f"  {c:12s} launches {p['launches']:5d}  {p['ms']:8.3f} ms")
+    res = {
+        "workload": "F16 7B-shape shared-prefix long context: 28 layers, d_model 3584, GQA 28/4 x 128, FFN 18944, "
+                    "vocab 152064, F16 weights; 16 requests x 8192 tokens sharing the first 6144 (prefilled once, "
+                    "forked), 8 answer positions per request, 4 option tokens each",
+        "value": round(C5_REQS / dt, 3), "unit": "req/s", "higher_is_better": True, "steps": steps, "warmup": warm,
+        "ms_per_step": round(dt * 1e3, 2), "context_tok_per_s": round(C5_REQS * 8192 / dt, 1),
+        "computed_tok_per_s": round(computed / dt, 1),
+        "roofline": roofline("mfma", rate(gp, "flops"), PEAK_F16_TFLOPS, "TFLOP/s",
+                             "gemm (F16 weights, hi/lo split activations: two f16 passes per product)",
+                             gp["launches"], gp["ms"] / max(1, gp["launches"])),
+        "attention": roofline("mfma", att_tf, PEAK_F16_TFLOPS, "TFLOP/s",
+                              "attn_prefill (causal GQA over the paged f32 cache; three f16 passes per product)",
+                              ap["launches"], ap["ms"] / max(1, ap["launches"]),
+                              algorithmic_flops_per_step=att_flops),
+        "kernel_ms_per_step": {c: round(p["ms"], 3) for c, p in prof.items()},
+    }
+    if layer_cost:
+        po = oracle_modules()
+        nq, ctx = 64, 8192
+        r = np.random.default_rng(5)
+        q = r.standard_normal((nq, hq * hd)).astype(np.float32)
+        k = r.standard_normal((ctx, 4 * hd)).astype(np.float32)
+        v = r.standard_normal((ctx, 4 * hd)).astype(np.float32)
+        sample_pairs = sum(ctx - nq + i + 1 for i in range(nq))
+        req_pairs = ctx * (ctx + 1) // 2
+        entries = []
+        for t, sec in layer_cost.items():
+            t0 = time.perf_counter()
+            po.attention(q, k, v, ctx - nq, hq, 4, threads=t)
+            ta = (time.perf_counter() - t0) * req_pairs / sample_pairs
+            per_layer = sec / Q4K_TOKENS * ctx + ta
+            per_req = per_layer * L
+            entries.append(cpu_entry(
+                round(1 / per_req, 6), "req/s", t,
+                f"one 8192-token request, computed whole as the reference does (no prefix reuse): projections and "
+                f"MLP from one 1024-token layer ({sec:.2f} s) scaled x8, causal attention from the last {nq} query "
+                f"rows over 8192 keys scaled by the (query, key) pair count x{req_pairs / sample_pairs:.0f} "
+                f"({ta:.1f} s per layer); per layer {per_layer:.1f} s, x28 layers = {per_req:.0f} s per request"))
+        res.update(cpu_pair(entries))
+    return res
+
+
+def bench_single(args, prec, name):
+    """One of the extra configurations as its own JSON line (--workload plumbing|q4k-prefill|long-context)."""
+    po = None if args.no_cpu else oracle_modules()
+    if name == "plumbing":
+        r = c1_plumbing(args, prec)
+        metric = "plumbing decide latency (1 request, 144 tokens, yes/no option scoring)"
+    elif name == "q4k-prefill":
+        r = c4_q4k(args, prec, None if po is None else cpu_layer_cost_7b(args, po))
+        metric = "Q4_K/Q6_K 7B batched prefill tok/s (32 x 1024)"
+    else:
+        r = c5_long_context(args, prec, None if po is None else cpu_layer_cost_7b(args, po))
+        metric = "F16 7B shared-prefix long-context decide req/s (16 x 8192, 6144 shared)"
+    line = base_line(metric, r.pop("value"), r.pop("unit"), r.pop("higher_is_better"), r.get("steps", args.steps),
+                     r.get("warmup", args.warmup), r.get("ms_per_step", r.get("p50_ms", 0.0)), prec,
+                     r.pop("workload"))
+    line.update(r)
+    return line
+
+
+def base_line(metric, value, unit, higher, steps, warmup, ms, prec, workload, **extra):
+    return {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": steps, "warmup": warmup,
+            "ms_per_step": round(ms, 3), "higher_is_better": higher, "scaling": "weak", "vs_baseline": None,
+            "dtype": "f32" if prec == lh.PREC_EXACT else "f16", "data": "synthetic",
+            "config": dict(workload=workload, seed=SEED,
+                           precision="exact" if prec == lh.PREC_EXACT else "fast", **extra)}
 
 
 def decide_request(vocab, seed):
@@ -455,31 +700,28 @@ def bench_openthai(args, prec):
     return line
 
 
-def cpu_baseline(threads, layers=24):
-    """The oracle on a bounded sample: one 560-token request of the workload through `layers`
-    of the 24 layers (per-layer cost is identical), scaled to the full model."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import pyoracle as po
-
-    img = lh.SynthImage(PRESET, seed=SEED, n_layers=layers)
-    om = po.Model(po.Gguf(img.array()), threads=threads)
+def c2_cpu_baseline(args):
+    """The oracle on a bounded sample of the headline workload: one 560-token request through all 24
+    layers (the reference's loop order), per thread count."""
+    po = oracle_modules()
+    img = lh.SynthImage(PRESET, seed=SEED)
+    om = po.Model(po.Gguf(img.array()), threads=1)
     reqs, option_ids = prefill_workload(om.V)
     ids, pos = reqs[0]
-    t0 = time.perf_counter()
-    om.forward(ids, pos, option_ids)
-    dt = time.perf_counter() - t0
-    scale = 24 / layers
-    depth = "all 24 layers" if layers == 24 else f"{layers} of 24 layers, time scaled x{scale:g}"
-    return {
-        "value": round(len(ids) / (dt * scale), 2),
-        "unit": "tok/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": f"1 of the {REQUESTS} requests ({len(ids)} tokens, {QUESTIONS} answer positions, "
-                  f"{OPTIONS} options) through {depth}: {dt:.2f} s; C restatement of the reference CPU "
-                  f"algorithm (F32 weights expanded at load, 4-row x 8-lane FMA kernel, rows split over "
-                  f"{threads} threads)",
-    }
+    entries = []
+    for t in cpu_threads(args):
+        om.set_threads(t)
+        t0 = time.perf_counter()
+        om.forward(ids, pos, option_ids)
+        dt = time.perf_counter() - t0
+        log(f"  oracle C2 request, 24 layers, {t} threads: {dt:.2f} s")
+        entries.append(cpu_entry(
+            round(len(ids) / dt, 2), "tok/s", t,
+            f"1 of the {REQUESTS} requests ({len(ids)} tokens, {QUESTIONS} answer positions, {OPTIONS} options) "
+            f"through all 24 layers: {dt:.2f} s; C restatement of the reference CPU algorithm (F32 weights "
+            f"expanded at load, 4-row x 8-lane FMA kernel, rows split over {t} threads)"))
+    del om
+    return entries
 
 
 LAYA_PRESET = "laya-english"
@@ -591,13 +833,18 @@ def main():
     ap.add_argument("--workload", choices=["decide", "plumbing", "q4k-prefill", "long-context", "decide-request",
                                            "decide-batch", "openthai-decide", "laya-decide"],
                     default="decide",
-                    help="decide (default): the Q8_0 d2048 batched decide headline plus batch-1 decode; the "
-                         "others measure the remaining workload shapes, one JSON line each")
-    ap.add_argument("--no-decode", action="store_true")
+                    help="decide (default): the Q8_0 d2048 batched decide headline with the other four workload "
+                         "configurations (C1 plumbing, C3 decode, C4 Q4_K 7B prefill, C5 long context) nested in "
+                         "`configs`; the others run one configuration as its own JSON line")
+    ap.add_argument("--configs", default="C1,C3,C4,C5",
+                    help="nested configurations of the default run (comma list; empty for the headline only)")
+    ap.add_argument("--config-steps", type=int, default=3, help="timed steps of C4 and C5 (about 1.5 s each)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=DECODE_STEPS,
                     help="greedy steps per decode run (fewer keeps counter-collection runs short)")
-    ap.add_argument("--cpu-threads", type=int, default=4)
+    ap.add_argument("--cpu-threads", type=int, default=4, help="threads of the CPU baseline (the reference's default)")
+    ap.add_argument("--cpu-threads-all", type=int, default=16,
+                    help="threads of the second CPU baseline: the host cores this job may use (0 to skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first run the F32 dequant kernel over MIB MiB: a plain copy (4 B read, 4 B written "
                          "per element), so a counter profile of this command also holds the kernel that "
@@ -609,12 +856,15 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     prec = lh.PREC_EXACT if args.precision == "exact" else lh.PREC_FAST
+    if args.workload in ("plumbing", "q4k-prefill", "long-context"):
+        print(json.dumps(bench_single(args, prec, args.workload)), flush=True)
+        return
     if args.workload != "decide":
-        fn = {"plumbing": bench_plumbing, "q4k-prefill": bench_q4k, "long-context": bench_long_context,
-              "decide-request": bench_decide_request, "decide-batch": bench_decide_batch,
+        fn = {"decide-request": bench_decide_request, "decide-batch": bench_decide_batch,
               "openthai-decide": bench_openthai, "laya-decide": bench_laya}
         print(json.dumps(fn[args.workload](args, prec)), flush=True)
         return
+    wanted = [c.strip().upper() for c in args.configs.split(",") if c.strip()]
     if args.copy_calibration > 0:
         n = args.copy_calibration * (1 << 20) // 4
         src = np.arange(n, dtype=np.float32)
@@ -633,8 +883,8 @@ def main():
     ms = dt / args.steps * 1e3
     tok_s = T * args.steps / dt
     gp = prof["gemm"]
-    gemm_tflops = gp["flops"] / (gp["ms"] * 1e-3) / 1e12 if gp["ms"] else 0.0
-    log(f"prefill: {ms:.2f} ms/step, {tok_s:.0f} tok/s, gemm {gemm_tflops:.1f} TFLOP/s over "
+    gemm_tflops = rate(gp, "flops")
+    log(f"C2 prefill: {ms:.2f} ms/step, {tok_s:.0f} tok/s, gemm {gemm_tflops:.1f} TFLOP/s over "
         f"{gp['launches']} launches ({gp['ms']:.2f} ms)")
     for c, p in prof.items():
         log(f"  {c:12s} launches {p['launches']:5d}  {p['ms']:8.3f} ms")
@@ -664,48 +914,35 @@ def main():
                            if prec == lh.PREC_EXACT else "f16 MFMA, f32 accumulation, f16 KV cache"),
         },
         "decide_req_per_s": round(REQUESTS * args.steps / dt, 2),
-        "roofline": {
-            "bound": "mfma",
-            "kernel": "gemm (dequant-fused Q8_0 MFMA GEMM)",
-            "achieved": round(gemm_tflops, 1),
-            "peak": PEAK_F16_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(gemm_tflops / PEAK_F16_TFLOPS, 4),
-            "traffic": measured_traffic("gemm"),
-            "traffic_source": "profiles/hbm_traffic_q8-2048_bench.md (FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
-            "launches": gp["launches"],
-            "avg_launch_ms": round(gp["ms"] / max(1, gp["launches"]), 4),
-            "algorithmic_flops_per_step": gp["flops"],
-        },
+        "roofline": roofline("mfma", gemm_tflops, PEAK_F16_TFLOPS, "TFLOP/s", "gemm (dequant-fused Q8_0 MFMA GEMM)",
+                             gp["launches"], gp["ms"] / max(1, gp["launches"]), measured_traffic("gemm"),
+                             traffic_source="profiles/hbm_traffic_q8-2048_bench.md (FETCH_SIZE + WRITE_SIZE, "
+                                            "copy-calibrated)",
+                             algorithmic_flops_per_step=gp["flops"]),
+        "kernel_ms_per_step": {c: round(p["ms"], 3) for c, p in prof.items()},
     }
-    if not args.no_decode:
-        ddt, dprof = bench_decode(eng, args.decode_steps)
-        gv = dprof["gemv"]
-        gemv_gbs = gv["bytes"] / (gv["ms"] * 1e-3) / 1e9 if gv["ms"] else 0.0
-        log(f"decode: {ddt / args.decode_steps * 1e3:.3f} ms/token, gemv {gemv_gbs:.0f} GB/s over {gv['launches']} launches")
-        for c, p in dprof.items():
-            log(f"  {c:12s} launches {p['launches']:5d}  {p['ms']:8.3f} ms")
-        line["decode"] = {
-            "workload": f"Q8_0 batch-1 greedy decode: {DECODE_CTX}-token context, {args.decode_steps} steps, "
-                        f"same model",
-            "tok_per_s": round(args.decode_steps / ddt, 2),
-            "ms_per_token": round(ddt / args.decode_steps * 1e3, 4),
-            "roofline": {
-                "bound": "hbm",
-                "kernel": "gemv (dequant-fused Q8_0 GEMV, GGUF bytes per launch)",
-                "achieved": round(gemv_gbs, 1),
-                "peak": PEAK_HBM_GBS,
-                "unit": "GB/s",
-                "frac": round(gemv_gbs / PEAK_HBM_GBS, 4),
-                "traffic": measured_traffic("gemv"),
-                "launches": gv["launches"],
-                "avg_launch_ms": round(gv["ms"] / max(1, gv["launches"]), 5),
-            },
-        }
+    configs = {}
+    if "C3" in wanted:
+        configs["C3"] = c3_decode(eng, args)
     eng.close()
+    del g, img
+    if "C1" in wanted:
+        configs["C1"] = c1_plumbing(args, prec)
+    layer_cost = None
+    if ("C4" in wanted or "C5" in wanted) and not args.no_cpu:
+        layer_cost = cpu_layer_cost_7b(args, oracle_modules())
+    if "C4" in wanted:
+        configs["C4"] = c4_q4k(args, prec, layer_cost)
+    if "C5" in wanted:
+        configs["C5"] = c5_long_context(args, prec, layer_cost)
     if not args.no_cpu:
-        log(f"CPU baseline ({args.cpu_threads} threads)")
-        line["cpu_baseline"] = cpu_baseline(args.cpu_threads)
+        log("C2 CPU baseline")
+        line.update(cpu_pair(c2_cpu_baseline(args)))
+        if "C3" in configs and "cpu_baseline" in line:
+            # the reference has no cache: every step recomputes the whole 2049-token sequence
+            per_tok = line["cpu_baseline"]["value"]
+            configs["C3"]["cpu_baseline"]["reference_without_cache_s_per_token"] = round((DECODE_CTX + 1) / per_tok, 1)
+    line["configs"] = configs
     print(json.dumps(line), flush=True)
 
 

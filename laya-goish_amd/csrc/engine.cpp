@@ -218,10 +218,14 @@ void Engine::load_decoder(const Gguf &g, const lg_engine_opts &opts) {
   int64_t pages = opts.kv_pages;
   if (pages <= 0) {
     const int64_t toks = opts.kv_tokens > 0 ? opts.kv_tokens : 65536;
-    pages = (toks + 63) / 64;
+    pages = toks / 64 + (toks % 64 != 0);
   }
-  npages_ = int(pages);
   page_stride_ = int64_t(hkv) * 64 * hd;
+  // bytes of the pool; anything past 2^47 (128 TiB) is no device's memory and is refused up front
+  const double want = 2.0 * double(L) * double(pages) * double(page_stride_) * kv_elem();
+  if (pages > (1 << 30) || want > double(int64_t(1) << 47))
+    fail(LG_ERR_OOM, "cannot allocate %.3g bytes of KV pages (%lld pages)", want, (long long)pages);
+  npages_ = int(pages);
   const size_t kv_bytes = size_t(2) * L * npages_ * page_stride_ * kv_elem();
   if (hipMalloc(&kv_, kv_bytes) != hipSuccess) {
     kv_ = nullptr;
@@ -843,10 +847,24 @@ void Engine::batch_run(BatchPlan *b, const int32_t *option_ids, int k, float tem
   launch_head_rows(ws_x_.as<float>(), b->gather, R, d, final_norm_, eps, head_, head_bias_, dids, k, dl, stream);
   if (k <= 32) launch_option_scores(dl, R, k, temperature, dp, dlp, stream);
   prof.end(0, 0, stream);
-  if (logits) HIP_CHECK(hipMemcpyAsync(logits, dl, size_t(R) * k * 4, hipMemcpyDeviceToHost, stream));
+  std::vector<float> staged;
+  float *hl = logits;
+  if (!hl) {
+    staged.resize(size_t(R) * k);
+    hl = staged.data();
+  }
+  HIP_CHECK(hipMemcpyAsync(hl, dl, size_t(R) * k * 4, hipMemcpyDeviceToHost, stream));
   if (probs) HIP_CHECK(hipMemcpyAsync(probs, dp, size_t(R) * k * 4, hipMemcpyDeviceToHost, stream));
   if (logprobs) HIP_CHECK(hipMemcpyAsync(logprobs, dlp, size_t(R) * k * 4, hipMemcpyDeviceToHost, stream));
   sync();
+  // a non-finite output is an error, as the reference's (src/models/laya/model.rs:412-414); the
+  // sequences go back to their lengths before this batch
+  for (size_t i = 0; i < size_t(R) * k; ++i)
+    if (!std::isfinite(hl[i])) {
+      for (size_t r = 0; r < b->seqs.size(); ++r) seq(b->seqs[r]).len -= b->n[r];
+      b->ran = false;
+      fail(LG_ERR_INVALID, "non-finite model output");
+    }
 }
 
 void Engine::forward(int sq, const int32_t *ids, int n, const int32_t *positions, int npos,
@@ -881,6 +899,11 @@ void Engine::forward(int sq, const int32_t *ids, int n, const int32_t *positions
     gemv(ws_x_.as<float>() + size_t(rows[i]) * d, head_, Epi::F32, ws_out_.as<float>(), nullptr, final_norm_);
     HIP_CHECK(hipMemcpyAsync(logits + size_t(i) * V, ws_out_.p, size_t(V) * 4, hipMemcpyDeviceToHost, stream));
     sync();
+    for (int j = 0; j < V; ++j)
+      if (!std::isfinite(logits[size_t(i) * V + j])) {
+        seq(sq).len -= n;
+        fail(LG_ERR_INVALID, "non-finite model output");
+      }
   }
 }
 
@@ -889,7 +912,6 @@ void Engine::decode_check(const Seq &s, int32_t first, int steps, const int32_t 
   if (arch != Arch::Decoder) fail(LG_ERR_UNSUPPORTED, "decode: this model has a decision head, not a language-model head");
   LG_REQUIRE(steps > 0 && tokens, "decode: need steps > 0 and an output");
   LG_REQUIRE(first >= 0 && first < V, "decode: token id %d outside the vocabulary", first);
-  LG_REQUIRE(hd == 128, "decode: head_dim %d has no decode attention kernel", hd);
   if (int64_t(s.len) + steps > ctx)
     fail(LG_ERR_INVALID, "sequence of %lld tokens exceeds the context length %d", (long long)s.len + steps, ctx);
 }
@@ -970,6 +992,9 @@ void Engine::decode_run(Seq &s, int32_t first, int steps, int32_t *tokens, float
   }
   HIP_CHECK(hipMemcpyAsync(tokens, tok + 1, size_t(steps) * 4, hipMemcpyDeviceToHost, stream));
   sync();
+  // the argmax writes -1 for a step whose logits have no finite maximum
+  for (int i = 0; i < steps; ++i)
+    if (tokens[i] < 0) fail(LG_ERR_INVALID, "non-finite model output");
   s.len = pos0 + steps;
 }
 

@@ -457,7 +457,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float *__restric
                                                           KV *__restrict__ kpool, KV *__restrict__ vpool,
                                                           const int32_t *__restrict__ pages, int max_pages,
                                                           float *__restrict__ part) {
-  static_assert(HD == 128, "decode attention is written for head_dim 128");
+  static_assert(HD == 64 || HD == 128, "decode attention is written for head_dim 64 and 128");
   const int pi = blockIdx.x, kh = blockIdx.y;
   float *pbase = part + (int64_t(kh * GRP) * max_pages + pi) * (2 + HD);
   const int64_t hstride = int64_t(max_pages) * (2 + HD);
@@ -472,12 +472,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float *__restric
 // clamped, surplus pages weighted 0).  All 256 threads of the workgroup take part.
 template <int HD>
 __device__ __forceinline__ void combine_head(const float *__restrict__ pb, int np, float *__restrict__ outh) {
-  static_assert(HD == 128, "two threads per output dim");
-  constexpr int CB = 32;  // pages per thread per batch
+  constexpr int NPART = 256 / HD;  // threads per output dim: 2 (head_dim 128) or 4 (64)
+  static_assert(NPART * HD == 256, "256 threads over the output dims");
+  constexpr int CB = 64 / NPART;   // pages per thread per batch
   const int t = threadIdx.x;
   __shared__ float wm[1024], wl[1024];
-  __shared__ float red[4], sacc[2][HD], sl[2];
-  const int d = t & (HD - 1), half = t >> 7;
+  __shared__ float red[4], sacc[NPART][HD], sl[NPART];
+  const int d = t & (HD - 1), part = t / HD;
   // page maxima and sums (np <= 1024: four per thread), then the first batch of outputs
   float m4[4], l4[4];
 #pragma unroll
@@ -488,7 +489,7 @@ __device__ __forceinline__ void combine_head(const float *__restrict__ pb, int n
   }
   float ov[CB];
 #pragma unroll
-  for (int u = 0; u < CB; ++u) ov[u] = pb[int64_t(min(half + 2 * u, np - 1)) * (2 + HD) + 2 + d];
+  for (int u = 0; u < CB; ++u) ov[u] = pb[int64_t(min(part + NPART * u, np - 1)) * (2 + HD) + 2 + d];
   float M = -INFINITY;
 #pragma unroll
   for (int u = 0; u < 4; ++u)
@@ -507,24 +508,32 @@ __device__ __forceinline__ void combine_head(const float *__restrict__ pb, int n
   }
   __syncthreads();
   float acc = 0.0f, L = 0.0f;
-  for (int b0 = 0; b0 < np; b0 += 2 * CB) {
+  for (int b0 = 0; b0 < np; b0 += NPART * CB) {
     if (b0 > 0) {
 #pragma unroll
-      for (int u = 0; u < CB; ++u) ov[u] = pb[int64_t(min(b0 + half + 2 * u, np - 1)) * (2 + HD) + 2 + d];
+      for (int u = 0; u < CB; ++u) ov[u] = pb[int64_t(min(b0 + part + NPART * u, np - 1)) * (2 + HD) + 2 + d];
     }
 #pragma unroll
     for (int u = 0; u < CB; ++u) {
-      const int i = b0 + half + 2 * u;
+      const int i = b0 + part + NPART * u;
       if (i < np) {
         acc += ov[u] * wm[i];
         L += wl[i] * wm[i];
       }
     }
   }
-  sacc[half][d] = acc;
-  if (d == 0) sl[half] = L;
+  sacc[part][d] = acc;
+  if (d == 0) sl[part] = L;
   __syncthreads();
-  if (t < HD) outh[t] = (sacc[0][t] + sacc[1][t]) / (sl[0] + sl[1]);
+  if (t < HD) {
+    float a = 0.0f, l = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NPART; ++q) {
+      a += sacc[q][t];
+      l += sl[q];
+    }
+    outh[t] = a / l;
+  }
   __syncthreads();  // the shared arrays are reused by the caller's next head
 }
 
@@ -553,7 +562,7 @@ __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, 
   constexpr int LPD = P / E;                  // lanes per dim column of V
   constexpr int HALF = HD / 2;
   constexpr int NQP = (GRP * HALF + 255) / 256;  // rotation pairs per thread
-  static_assert(LPK == 16 || LPK == 32, "key rows span 16 or 32 lanes");
+  static_assert(LPK == 8 || LPK == 16 || LPK == 32, "key rows span 8, 16 or 32 lanes");
   static_assert(LPD == 8 || LPD == 16, "dim columns span 8 or 16 lanes");
   const int pi = blockIdx.x, kh = blockIdx.y;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -654,9 +663,12 @@ __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, 
       if constexpr (LPK == 32) {
         d = half_sum_odd_rows(d);  // lanes 16-31 / 48-63 hold the key's sum
         if ((lane & 31) == 16) sc[gq][key] = pi * P + key < len ? d * inv_sqrt : -INFINITY;
-      } else {
+      } else if constexpr (LPK == 16) {
         d = row_sum(d);
         if ((lane & 15) == 0) sc[gq][key] = pi * P + key < len ? d * inv_sqrt : -INFINITY;
+      } else {
+        d = group8_sum(d);
+        if ((lane & 7) == 0) sc[gq][key] = pi * P + key < len ? d * inv_sqrt : -INFINITY;
       }
     }
   }
@@ -745,32 +757,43 @@ void launch_attn_decode(const float *qkv, int hq, const KvGeom &g, const float *
                         int pos, void *kpool, void *vpool, const int32_t *pages, int max_pages,
                         float *part, float *out, hipStream_t st) {
   LG_REQUIRE(g.page_tokens == P, "attention: page size must be %d", P);
-  LG_REQUIRE(g.hd == 128, "decode attention: head_dim %d not supported (128)", g.hd);
+  LG_REQUIRE(g.hd == 128 || g.hd == 64, "decode attention: head_dim %d not supported (64, 128)", g.hd);
   LG_REQUIRE(pos >= 0, "decode attention: negative position");
   const int np = pos / P + 1;
   LG_REQUIRE(np <= max_pages, "decode attention: context exceeds the page table");
   LG_REQUIRE(np <= 1024, "decode attention: context of %d pages exceeds the combine stage", np);
   const int grp = hq / g.hkv;
   const dim3 grid(np, g.hkv), block(256);
-#define CASE(G)                                                                                          \
+#define CASE(HDV, G)                                                                                     \
   case G:                                                                                                \
     if (g.kv32)                                                                                          \
-      hipLaunchKernelGGL((attn_decode_kernel<128, G, float>), grid, block, 0, st, qkv, hq, g, cosT, sinT, \
+      hipLaunchKernelGGL((attn_decode_kernel<HDV, G, float>), grid, block, 0, st, qkv, hq, g, cosT, sinT, \
                          pos, static_cast<float *>(kpool), static_cast<float *>(vpool), pages, max_pages, \
                          part);                                                                          \
     else                                                                                                 \
-      hipLaunchKernelGGL((attn_decode_kernel<128, G, _Float16>), grid, block, 0, st, qkv, hq, g, cosT,    \
+      hipLaunchKernelGGL((attn_decode_kernel<HDV, G, _Float16>), grid, block, 0, st, qkv, hq, g, cosT,    \
                          sinT, pos, static_cast<_Float16 *>(kpool), static_cast<_Float16 *>(vpool), pages, \
                          max_pages, part);                                                               \
     break;
-  switch (grp) {
-    CASE(1) CASE(2) CASE(4) CASE(7) CASE(8)
-    default: fail(LG_ERR_UNSUPPORTED, "decode attention: group size %d not supported", grp);
+  if (g.hd == 128) {
+    switch (grp) {
+      CASE(128, 1) CASE(128, 2) CASE(128, 4) CASE(128, 7) CASE(128, 8)
+      default: fail(LG_ERR_UNSUPPORTED, "decode attention: group size %d not supported", grp);
+    }
+  } else {
+    switch (grp) {
+      CASE(64, 1) CASE(64, 2) CASE(64, 4) CASE(64, 7) CASE(64, 8)
+      default: fail(LG_ERR_UNSUPPORTED, "decode attention: group size %d not supported", grp);
+    }
   }
 #undef CASE
   HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL((attn_decode_combine<128>), dim3(hq, 1), dim3(256), 0, st, part, hq, max_pages,
-                     static_cast<const int32_t *>(nullptr), pos + 1, out);
+  if (g.hd == 128)
+    hipLaunchKernelGGL((attn_decode_combine<128>), dim3(hq, 1), dim3(256), 0, st, part, hq, max_pages,
+                       static_cast<const int32_t *>(nullptr), pos + 1, out);
+  else
+    hipLaunchKernelGGL((attn_decode_combine<64>), dim3(hq, 1), dim3(256), 0, st, part, hq, max_pages,
+                       static_cast<const int32_t *>(nullptr), pos + 1, out);
   HIP_CHECK(hipGetLastError());
 }
 

@@ -291,6 +291,31 @@ __global__ __launch_bounds__(kThreads) void gemv_generic_kernel(const float *__r
   }
 }
 
+// Largest LDS block a workgroup may take on the current device (160 KiB on gfx950).
+size_t lds_limit() {
+  static int bytes = -1;
+  if (bytes < 0) {
+    int dev = 0, v = 0;
+    HIP_CHECK(hipGetDevice(&dev));
+    HIP_CHECK(hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
+    bytes = v;
+  }
+  return size_t(bytes);
+}
+
+// Launch with `lds` bytes of dynamic LDS, raising the kernel's limit first when it passes the
+// 64 KiB every kernel may take without asking (once per kernel and size).
+template <typename F, typename... Args>
+void launch_lds(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, Args... args) {
+  static size_t granted = 64 * 1024;
+  if (lds > granted) {
+    HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  int(lds)));
+    granted = lds;
+  }
+  launch_timed(kernel, grid, block, lds, st, args...);
+}
+
 template <uint32_t KIND, int EPI, int R, int CPL>
 void launch_rc(const float *x, const DevMatrix &W, float *y, const float *bias, const float *norm_w, float eps,
                int outputs, hipStream_t st) {
@@ -299,9 +324,9 @@ void launch_rc(const float *x, const DevMatrix &W, float *y, const float *bias, 
   const size_t lds = size_t(W.cols) * sizeof(float);
   const bool bigk = W.cols / chunk_elems<KIND>() > 64 * CPL;
   if (bigk)
-    launch_timed(gemv_kernel<KIND, EPI, R, CPL, true>, grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
+    launch_lds(gemv_kernel<KIND, EPI, R, CPL, true>, grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
   else
-    launch_timed(gemv_kernel<KIND, EPI, R, CPL, false>, grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
+    launch_lds(gemv_kernel<KIND, EPI, R, CPL, false>, grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
 }
 
 template <uint32_t KIND, int EPI, int R>
@@ -346,7 +371,7 @@ void launch_gemv(const float *x, const DevMatrix &W, Epi epi, float *y, const fl
                  const float *norm_w, float eps, hipStream_t st) {
   LG_REQUIRE(W.rows > 0 && W.cols > 0, "gemv: empty matrix");
   LG_REQUIRE(W.cols % 16 == 0, "gemv: K=%d must be a multiple of 16", W.cols);
-  LG_REQUIRE(size_t(W.cols) * 4 <= 64 * 1024, "gemv: K=%d exceeds the 64 KiB LDS stage", W.cols);
+  LG_REQUIRE(size_t(W.cols) * 4 + 64 <= lds_limit(), "gemv: K=%d exceeds the %zu-byte LDS stage", W.cols, lds_limit());
   if (epi == Epi::SWIGLU) LG_REQUIRE(W.rows % 2 == 0, "gemv: gate|up needs an even row count");
   switch (W.kind) {
     case LG_Q8_0: launch_gemv_kind<LG_Q8_0>(x, W, epi, y, bias, norm_w, eps, st); break;
@@ -358,13 +383,13 @@ void launch_gemv(const float *x, const DevMatrix &W, Epi epi, float *y, const fl
       const size_t lds = size_t(W.cols) * sizeof(float);
       switch (epi) {
         case Epi::F32:
-          launch_timed(gemv_generic_kernel<0>, grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
+          launch_lds(gemv_generic_kernel<0>, grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
           break;
         case Epi::ADD:
-          launch_timed(gemv_generic_kernel<1>, grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
+          launch_lds(gemv_generic_kernel<1>, grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
           break;
         case Epi::SWIGLU:
-          launch_timed(gemv_generic_kernel<3>, grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
+          launch_lds(gemv_generic_kernel<3>, grid, block, lds, st, x, W, y, bias, norm_w, eps, outputs);
           break;
         default: fail(LG_ERR_UNSUPPORTED, "gemv: f16 epilogue not supported");
       }

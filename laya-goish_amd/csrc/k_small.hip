@@ -372,7 +372,7 @@ __global__ __launch_bounds__(64) void argmax_stage2(const float *__restrict__ pv
       bi = pi[i];
     }
   }
-  out[0] = bi < 0 ? 0 : bi;
+  out[0] = bi >= 0 && bv > -INFINITY && bv < INFINITY ? bi : -1;  // -1: no finite maximum
 }
 
 __global__ void cvt_f16_kernel(const float *__restrict__ x, int64_t n, _Float16 *__restrict__ y,

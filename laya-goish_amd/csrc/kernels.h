@@ -144,7 +144,8 @@ void launch_head_rows(const float *x, const int32_t *rows, int R, int d, const f
 void launch_option_scores(const float *logits, int R, int k, float temperature, float *probs,
                           float *logprobs, hipStream_t st);
 
-// Full-vocabulary argmax of logits[V] (first maximum wins) -> out[0]; part: scratch.
+// Full-vocabulary argmax of logits[V] (first maximum wins) -> out[0], or -1 when the maximum is not
+// finite (inf or no comparable value); part: scratch.
 void launch_argmax(const float *logits, int V, int32_t *out, float *part_v, int32_t *part_i,
                    hipStream_t st);
 

@@ -1005,6 +1005,27 @@ __attribute__((target("avx2"))) static void attn_heads_avx2(void *p, int lo, int
 }
 #endif
 
+/* The causal GQA attention of one layer on caller-held rows (the loop of or_prefill, for timing the
+ * reference's attention on a sample of query rows and for tests): q [n][hq*hd] of positions pos0..,
+ * k/v [pos0 + n][hkv*hd] (already rotated), out [n][hq*hd].  src/models/openthai/model.rs:276-294. */
+int or_attention(const float *q, const float *k, const float *v, int n, int pos0, int hq, int hkv, int hd,
+                 int threads, float *out) {
+  if (n < 1 || pos0 < 0 || hq < 1 || hkv < 1 || hq % hkv || hd < 1) return -1;
+  or_model m;
+  memset(&m, 0, sizeof m);
+  m.hq = hq;
+  m.hkv = hkv;
+  m.hd = hd;
+  attn_ctx ac = {&m, q, k, v, out, n, pos0};
+#if defined(__x86_64__)
+  if (g_blocked && !g_force_scalar && __builtin_cpu_supports("avx2"))
+    parallel(hq, threads, attn_heads_avx2, &ac);
+  else
+#endif
+    parallel(hq, threads, attn_heads, &ac);
+  return 0;
+}
+
 int or_prefill(or_model *m, or_cache *c, const int32_t *ids, int n, const int32_t *gather,
                int ngather, float *hidden) {
   int d = m->d, hq = m->hq, hkv = m->hkv, hd = m->hd, f = m->f;

@@ -78,6 +78,10 @@ int or_cache_read(const or_cache *c, int layer, int pos0, int n, float *k, float
 /* Run n tokens starting at the cache's current length; append their K/V; return the
  * residual-stream rows at `gather` (indices into the n new tokens), [ngather][d].
  * Layer-loop order follows src/models/openthai/model.rs:214-231. */
+/* Causal GQA attention of one layer on caller-held rotated rows: q [n][hq*hd] at positions
+ * pos0 .. pos0+n-1, k/v [pos0+n][hkv*hd], out [n][hq*hd] (src/models/openthai/model.rs:276-294). */
+int or_attention(const float *q, const float *k, const float *v, int n, int pos0, int hq, int hkv, int hd,
+                 int threads, float *out);
 int or_prefill(or_model *m, or_cache *c, const int32_t *ids, int n, const int32_t *gather,
                int ngather, float *hidden);
 /* Final RMSNorm + head rows `vocab_ids` (NULL = every row), src/models/openthai/model.rs:232-240. */

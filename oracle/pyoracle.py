@@ -50,6 +50,7 @@ def lib() -> ctypes.CDLL:
             "or_cache_free": (None, [P]),
             "or_cache_len": (I, [P]),
             "or_cache_read": (I, [P, I, I, I, P, P]),
+            "or_attention": (I, [P, P, P, I, I, I, I, I, I, P]),
             "or_prefill": (I, [P, P, P, I, P, I, P]),
             "or_head": (I, [P, P, I, P, I, P]),
             "or_argmax": (I, [P, I]),
@@ -183,6 +184,15 @@ class Gguf:
             raise KeyError(name)
         return kind.value, [dims[i] for i in range(nd.value)], ctypes.string_at(data, n.value)
 
+    def offset(self, name) -> int:
+        """Byte offset of a tensor's data inside the buffer (to patch bytes in tests)."""
+        kind, nd, data, n = ctypes.c_uint32(), ctypes.c_int(), ctypes.c_void_p(), ctypes.c_uint64()
+        dims = (ctypes.c_uint64 * 4)()
+        if lib().or_gguf_tensor(self.h, name.encode(), ctypes.byref(kind), dims, ctypes.byref(nd),
+                                ctypes.byref(data), ctypes.byref(n)):
+            raise KeyError(name)
+        return data.value - self.buf.ctypes.data
+
     def num(self, key, default=0.0):
         return lib().or_gguf_num(self.h, key.encode(), default)
 
@@ -269,6 +279,18 @@ class Cache:
         if getattr(self, "h", None) and _lib is not None:
             _lib.or_cache_free(self.h)
             self.h = None
+
+
+def attention(q, k, v, pos0, hq, hkv, threads=1) -> np.ndarray:
+    """Causal GQA attention (src/models/openthai/model.rs:276-294) of query rows q [n][hq*hd] at
+    positions pos0.. over rotated keys/values k, v [pos0+n][hkv*hd]."""
+    q, k, v = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32)
+    n, hd = q.shape[0], q.shape[1] // hq
+    assert k.shape == v.shape == (pos0 + n, hkv * hd)
+    out = np.empty_like(q)
+    if lib().or_attention(_p(q), _p(k), _p(v), n, pos0, hq, hkv, hd, threads, _p(out)):
+        raise ValueError("attention: bad shape")
+    return out
 
 
 def argmax(v) -> int:

@@ -376,3 +376,33 @@ def test_confidence_closed_form(po, lh):
                 assert np.float32(lh.option_confidence(p, mode)) == np.float32(c)
     # an all-zero vector floors every entry at 1e-12: entropy ~ k*1e-12*27.6 -> confidence 1
     assert po.confidence([0.0, 0.0, 0.0]) == lh.option_confidence([0.0, 0.0, 0.0]) == 1.0
+
+
+@pytest.mark.parametrize("hq,hkv,hd,pos0,n", [(4, 2, 16, 7, 5), (28, 4, 128, 60, 9), (8, 8, 64, 0, 33)])
+def test_attention_against_float64(po, hq, hkv, hd, pos0, n):
+    """or_attention (src/models/openthai/model.rs:276-294): causal, head h reads kv head h // (hq/hkv),
+    scores / sqrt(hd); float64 textbook within f32 rounding; a kv-head map of h % hkv would not match;
+    the blocked mode gives the same bits."""
+    rng = np.random.default_rng(hq + hd + n)
+    q = rng.standard_normal((n, hq * hd)).astype(np.float32)
+    k = rng.standard_normal((pos0 + n, hkv * hd)).astype(np.float32)
+    v = rng.standard_normal((pos0 + n, hkv * hd)).astype(np.float32)
+    got = po.attention(q, k, v, pos0, hq, hkv, threads=3)
+
+    def ref(kv_head):
+        out = np.zeros((n, hq * hd))
+        for i in range(n):
+            for h in range(hq):
+                kh = kv_head(h)
+                s = k[:pos0 + i + 1, kh * hd:(kh + 1) * hd].astype(np.float64) @ q[i, h * hd:(h + 1) * hd] / np.sqrt(hd)
+                p = np.exp(s - s.max())
+                out[i, h * hd:(h + 1) * hd] = (p / p.sum()) @ v[:pos0 + i + 1, kh * hd:(kh + 1) * hd]
+        return out
+    assert np.abs(got - ref(lambda h: h // (hq // hkv))).max() < 1e-5
+    if hkv != hq and hkv > 1:
+        assert np.abs(got - ref(lambda h: h % hkv)).max() > 1e-2
+    po.set_blocked(True)
+    try:
+        assert np.array_equal(bits(po.attention(q, k, v, pos0, hq, hkv, threads=2)), bits(got))
+    finally:
+        po.set_blocked(False)

@@ -75,6 +75,31 @@ def test_q4km_7b_shape_batched(lh, po):
     eng.close()
 
 
+def test_q4km_7b_shape_decode_gqa7(lh, po):
+    """Batch-1 decode at the 7B shape (GQA 28/4: seven query heads per KV head, QKV bias, a 152064-row
+    Q6_K head), one layer, teacher-forced against the oracle's KV-cached decode."""
+    img = lh.SynthImage("q4km-7b", seed=11, n_layers=1)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=1024)
+    om = po.Model(po.Gguf(img.array()), threads=16)
+    ids = _ids(200, om.V, 21)
+    s = eng.seq_create()
+    eng.forward(s, ids[:-1], [], [0])
+    steps = 5
+    print(f"q4km-7b L1: decode {steps} steps after 199 tokens", flush=True)
+    toks, logits = eng.decode(s, int(ids[-1]), steps, want_logits=True)
+    c = om.cache(300)
+    om.prefill(c, ids[:-1], [])
+    feed = [int(ids[-1])] + [int(t) for t in toks[:-1]]
+    worst = 0.0
+    for i, t in enumerate(feed):
+        want = om.head(om.prefill(c, [t], [0]))
+        worst = max(worst, assert_logits_close(logits[i], want, rel=logit_bar(0)))
+        assert_argmax_equal(logits[i][None], want)
+        assert int(toks[i]) == int(np.argmax(logits[i]))
+    print(f"q4km-7b decode: worst logit rel {worst:.2e}")
+    eng.close()
+
+
 def test_f16_7b_shared_prefix_against_oracle(lh, po):
     img = lh.SynthImage("f16-7b", seed=13, n_layers=1)
     eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=8192)
