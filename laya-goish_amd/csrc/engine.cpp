@@ -457,7 +457,7 @@ KvGeom Engine::geom() const {
   g.hd = hd;
   g.page_stride = page_stride_;
   g.layer_stride = int64_t(npages_) * page_stride_;
-  g.kv32 = split() ? 1 : 0;
+  g.split = split() ? 1 : 0;
   return g;
 }
 void *Engine::kpool(int layer) const {
@@ -609,18 +609,17 @@ void Engine::seq_kv_read(int id, int layer, int pos0, int n, float *k, float *v)
     }
     for (int h = 0; h < hkv; ++h)
       for (int j = 0; j < hd; ++j) {
-        const size_t ki = (size_t(h) * 64 + slot) * hd + j, vi = (size_t(h) * hd + j) * 64 + slot;  // K rows, V columns
-        float kf, vf;
-        if (es == 4) {
-          std::memcpy(&kf, kp.data() + ki * 4, 4);
-          std::memcpy(&vf, vp.data() + vi * 4, 4);
-        } else {
-          _Float16 kh, vh;
-          std::memcpy(&kh, kp.data() + ki * 2, 2);
-          std::memcpy(&vh, vp.data() + vi * 2, 2);
-          kf = float(kh);
-          vf = float(vh);
+        // K rows, V columns; a split page holds per kv head an f16 hi plane then an f16 lo plane
+        const size_t plane = size_t(64) * hd, npl = es == 4 ? 2 : 1;
+        const size_t ki = h * npl * plane + size_t(slot) * hd + j, vi = h * npl * plane + size_t(j) * 64 + slot;
+        _Float16 kh, vh, kl = 0, vl = 0;
+        std::memcpy(&kh, kp.data() + ki * 2, 2);
+        std::memcpy(&vh, vp.data() + vi * 2, 2);
+        if (npl == 2) {
+          std::memcpy(&kl, kp.data() + (ki + plane) * 2, 2);
+          std::memcpy(&vl, vp.data() + (vi + plane) * 2, 2);
         }
+        const float kf = float(kh) + float(kl), vf = float(vh) + float(vl);
         k[size_t(i) * kvw + h * hd + j] = kf;
         v[size_t(i) * kvw + h * hd + j] = vf;
       }
@@ -634,6 +633,7 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
   const bool ot = arch == Arch::OpenThai, fresh = fresh_only();
   try {
     std::vector<int32_t> ids, tseq, tpos, tiles_s, tiles_r, tiles_p, tiles_n, gather, grp_f, grp_c, srow0, sn;
+    const int gtiles = arch == Arch::Decoder ? attn_prefill_group_tiles(hq, hkv) : 4;
     std::vector<int32_t> it_r, it_p, it_n, it_lo, it_hi, cb_r, cb_n, cb_f, cb_c;
     int max_pages = 0;
     for (int r = 0; r < nreq; ++r) {
@@ -679,9 +679,9 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
         tpos.push_back(s.len + i);
       }
       for (int i = 0; i < q.n; i += 32) {
-        if ((i / 32) % 4 == 0) {
+        if ((i / 32) % gtiles == 0) {
           grp_f.push_back(int32_t(tiles_s.size()));
-          grp_c.push_back(std::min(4, (q.n - i + 31) / 32));
+          grp_c.push_back(std::min(gtiles, (q.n - i + 31) / 32));
         }
         tiles_s.push_back(r);
         tiles_r.push_back(row + i);

@@ -4,14 +4,14 @@
 // for query i of head h, kv head kh = h / (hq/hkv), s_j = dot(q_i, k_j) / sqrt(hd) for
 // j <= pos_i, p = softmax(s), out = sum_j p_j v_j.
 //
-// KV page layout (one layer, one page of P = 64 tokens), element type f16 or f32:
-//   K: [hkv][P][hd] (row per token)     V: [hkv][hd][P] (column per token)
+// KV page layout (one layer, one page of P = 64 tokens), per kv head:
+//   K: [P][hd] (row per token)     V: [hd][P] (column per token)
+// in f16 (FAST) or as two f16 planes (EXACT: the hi plane hi = f16(v), then the lo plane
+// lo = f16(v - hi), each of that layout; hi + lo holds v to about 22 significant bits).
 //
-// Prefill: one wave per (32-query tile, query head).  S^T = K . Q^T on MFMA 32x32x16 f16, so
-// each lane owns one query column and the online softmax reduces over its own registers plus
-// one lane swap; O^T = V^T . P^T then consumes P straight from registers.  With an f32 cache
-// and hi/lo query planes every product is split (hi.hi + lo.hi + hi.lo: three MFMAs), which
-// keeps scores and outputs f32-faithful.
+// Prefill: one workgroup per (group of query tiles, kv head, block of the kv head's query
+// heads), MFMA 32x32x16 f16; with split planes every product is hi.hi + lo.hi + hi.lo (three
+// MFMAs), which keeps scores and outputs f32-faithful.
 //
 // Decode (one new token): one workgroup per (kv head, page): coalesced reads of the page's K
 // rows and V columns, RoPE of the group's query heads (and, on the last page, of the new key,
@@ -48,217 +48,116 @@ __device__ __forceinline__ void split8(const float *v, half8 &hi, half8 &lo) {
   }
 }
 
-// SPLIT == false: f16 cache, f16 q.  SPLIT == true: f32 cache, q as hi/lo planes.
-template <int HD, bool SPLIT>
-__global__ __launch_bounds__(64) void attn_prefill_kernel(
-    const _Float16 *__restrict__ q16, const _Float16 *__restrict__ q16lo, int hq, KvGeom g,
-    const void *__restrict__ kpool, const void *__restrict__ vpool, const int32_t *__restrict__ pages,
-    int max_pages, const int32_t *__restrict__ tile_seq, const int32_t *__restrict__ tile_row0,
-    const int32_t *__restrict__ tile_pos0, const int32_t *__restrict__ tile_n,
-    _Float16 *__restrict__ out16, _Float16 *__restrict__ out16lo) {
-  using KV = typename std::conditional<SPLIT, float, _Float16>::type;
-  constexpr int KT = HD / 16;  // k-steps of the QK^T product
-  constexpr int DB = HD / 32;  // 32-wide d blocks of the output
-  // Workgroups are dealt to the 8 XCDs round-robin (i -> XCD i % 8).  Map them so each XCD
-  // takes one contiguous range of (head, tile) pairs, tiles fastest: all query tiles of one
-  // (sequence, head) then run on one XCD and read that sequence's K/V through one L2.
-  const int total = gridDim.x, ntiles = total / hq;
-  const int xcd = blockIdx.x % 8, per = total / 8, rem = total % 8;
-  const int logical = xcd * per + min(xcd, rem) + blockIdx.x / 8;
-  const int tile = logical % ntiles, h = logical / ntiles;
-  const int lane = threadIdx.x, qi = lane & 31, hl = lane >> 5;
-  const int seq = tile_seq[tile], row0 = tile_row0[tile], pos0 = tile_pos0[tile], n = tile_n[tile];
-  const int kh = h / (hq / g.hkv);
-  const int qw = hq * HD;
-  const int qpos = pos0 + qi;
-  const bool live = qi < n;
+// Prefill.  Work item: (tile group, kv head kh, head block hb).  A tile group is <= T
+// consecutive 32-query tiles of one sequence, a head block GB consecutive query heads of kh's
+// group of G = hq / hkv.  Wave w computes head kh * G + hb * GB + w % GB on tile w / GB of the
+// group, so all W = GB * T waves read the same K/V pages: each page passes through LDS once per
+// workgroup.  Pages are copied global -> LDS by LDS-DMA loads (16 bytes a lane, no registers),
+// double-buffered: page kt + 1 is in flight while page kt is consumed, one barrier per page.
+// LDS rows carry one 16-byte pad slot, so each 16 lanes of an MFMA operand read hit 16 distinct
+// 16-byte bank groups.
+//
+// S^T = K . Q^T on MFMA 32x32x16 f16, keys as rows and queries as columns: a lane owns one
+// query column and the online softmax reduces over its own registers plus one lane swap.  Lane
+// qi feeds key row kb * 32 + swap23(qi) (bits 2 and 3 of qi exchanged), which makes the eight
+// scores of register group j of a lane the consecutive keys kb * 32 + 16 j + 8 hl + 0..7: the
+// eight keys its P^T operand of O^T = V^T . P^T takes against one 16-byte run of a V row.
+// NPL = 2: split cache, queries and P as hi/lo planes, three MFMAs a product (hi.hi + lo.hi +
+// hi.lo); NPL = 1: f16 cache and queries, one MFMA.
+__device__ __forceinline__ int swap23(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
 
-  // Q^T operand: lane holds q[qi][16t + 8*hl .. +8]
-  half8 qr[KT], ql[SPLIT ? KT : 1];
-  {
-    const int64_t off = int64_t(row0 + min(qi, n - 1)) * qw + h * HD + hl * 8;
-#pragma unroll
-    for (int t = 0; t < KT; ++t) {
-      qr[t] = *reinterpret_cast<const half8 *>(q16 + off + 16 * t);
-      if (SPLIT) ql[t] = *reinterpret_cast<const half8 *>(q16lo + off + 16 * t);
-    }
-  }
-  f32x16 acc[DB];
-#pragma unroll
-  for (int b = 0; b < DB; ++b)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[b][r] = 0.0f;
-  float m = -INFINITY, l = 0.0f;
-  const float scale = kLog2e / sqrtf(float(HD));
-  const int last = pos0 + n - 1;
-  const int32_t *ptab = pages + int64_t(seq) * max_pages;
-  const KV *kbase = static_cast<const KV *>(kpool);
-  const KV *vbase = static_cast<const KV *>(vpool);
+template <int HD, int NPL>
+struct PrefillStage {
+  static constexpr int KC = HD / 8, KRS = KC + 1;  // 16-byte chunks per K row, slots per K row
+  static constexpr int VC = P / 8, VRS = VC + 1;   // the same for a V row (one dim, 64 keys)
+  static constexpr int KPL = P * KRS, VPL = HD * VRS;  // slots per plane
+  static_assert(KPL % 64 == 0 && VPL % 64 == 0, "planes fill whole 64-slot blocks");
+  static constexpr int KSLOTS = NPL * KPL, SLOTS = NPL * (KPL + VPL);
+  static constexpr int BLOCKS = SLOTS / 64;  // one LDS-DMA instruction of one wave per block
+  static constexpr int BYTES = SLOTS * 16;
+};
 
-  for (int kt = 0; kt <= last / P; ++kt) {
-    const int64_t page = ptab[kt];
-    const KV *Kp = kbase + page * g.page_stride + int64_t(kh) * P * HD;
-    const KV *Vp = vbase + page * g.page_stride + int64_t(kh) * HD * P;
-    f32x16 s[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
-      const KV *kr = Kp + (kb * 32 + qi) * HD + hl * 8;
-#pragma unroll
-      for (int t = 0; t < KT; ++t) {
-        if constexpr (SPLIT) {
-          float kv[8];
-          const float4 a = *reinterpret_cast<const float4 *>(kr + 16 * t);
-          const float4 b = *reinterpret_cast<const float4 *>(kr + 16 * t + 4);
-          kv[0] = a.x; kv[1] = a.y; kv[2] = a.z; kv[3] = a.w;
-          kv[4] = b.x; kv[5] = b.y; kv[6] = b.z; kv[7] = b.w;
-          half8 kh8, kl8;
-          split8(kv, kh8, kl8);
-          s[kb] = MFMA(kh8, qr[t], s[kb]);
-          s[kb] = MFMA(kl8, qr[t], s[kb]);
-          s[kb] = MFMA(kh8, ql[t], s[kb]);
-        } else {
-          s[kb] = MFMA(*reinterpret_cast<const half8 *>(kr + 16 * t), qr[t], s[kb]);
-        }
-      }
-    }
-    // s[kb][r] <-> key kt*P + kb*32 + (r/4)*8 + hl*4 + r%4, query qi
-    float mt = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kt * P + kb * 32 + (r >> 2) * 8 + hl * 4 + (r & 3);
-        const float v = (key <= qpos && live) ? s[kb][r] * scale : -INFINITY;
-        s[kb][r] = v;
-        mt = fmaxf(mt, v);
-      }
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
-    const float mn = fmaxf(m, mt);
-    const float alpha = mn == -INFINITY ? 1.0f : exp2f(m - mn);
-    float rs = 0.0f;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = mn == -INFINITY ? 0.0f : exp2f(s[kb][r] - mn);
-        s[kb][r] = p;
-        rs += p;
-      }
-    rs += __shfl_xor(rs, 32);
-    l = l * alpha + rs;
-    m = mn;
-#pragma unroll
-    for (int b = 0; b < DB; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[b][r] *= alpha;
-    // O^T += V^T . P^T over four 16-key chunks
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      float pv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pv[e] = s[c >> 1][(c & 1) * 8 + e];
-      half8 ph, pl;
-      if constexpr (SPLIT) split8(pv, ph, pl);
-      else
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ph[e] = _Float16(pv[e]);
-#pragma unroll
-      for (int b = 0; b < DB; ++b) {
-        const KV *vr = Vp + (b * 32 + qi) * P + 16 * c + hl * 4;
-        if constexpr (SPLIT) {
-          const float4 lo4 = *reinterpret_cast<const float4 *>(vr);
-          const float4 hi4 = *reinterpret_cast<const float4 *>(vr + 8);
-          const float vv[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
-          half8 vh, vl;
-          split8(vv, vh, vl);
-          acc[b] = MFMA(vh, ph, acc[b]);
-          acc[b] = MFMA(vl, ph, acc[b]);
-          acc[b] = MFMA(vh, pl, acc[b]);
-        } else {
-          const half4 lo = *reinterpret_cast<const half4 *>(vr);
-          const half4 hi = *reinterpret_cast<const half4 *>(vr + 8);
-          const half8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          acc[b] = MFMA(va, ph, acc[b]);
-        }
-      }
-    }
-  }
-  if (!live) return;
-  const float inv = 1.0f / l;
-  const int64_t obase = int64_t(row0 + qi) * qw + h * HD;
-  // acc[b][r] <-> d = b*32 + (r/4)*8 + hl*4 + r%4
-#pragma unroll
-  for (int b = 0; b < DB; ++b)
-#pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      half4 o, olo;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        _Float16 oh, ol;
-        split_f16(acc[b][r4 * 4 + j] * inv, oh, ol);
-        o[j] = oh;
-        olo[j] = ol;
-      }
-      const int64_t at = obase + b * 32 + r4 * 8 + hl * 4;
-      *reinterpret_cast<half4 *>(out16 + at) = o;
-      if (SPLIT) *reinterpret_cast<half4 *>(out16lo + at) = olo;
-    }
+__device__ __forceinline__ half8 lds_half8(const unsigned char *base, int slot) {
+  return *reinterpret_cast<const half8 *>(base + slot * 16);
 }
 
-// Position of key k (0..63) inside a V row in LDS: bits 2 and 3 swapped, so the eight keys one
-// lane feeds to the O^T product (16c + 4hl + {0..3}, 16c + 8 + 4hl + {0..3}) sit in one
-// 16-byte run at 16c + 8hl.
-__device__ __forceinline__ int vperm(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
-
-// Prefill, grouped: one workgroup of four waves per (group of <= 4 consecutive query tiles of
-// one sequence, query head).  Each K/V page of the group passes through LDS once, already
-// in MFMA operand form (hi/lo f16 planes with an f32 cache), and serves all four tiles; the
-// next page is fetched into registers while the current one is consumed.  Wave w computes
-// tile w with the arithmetic of attn_prefill_kernel, term for term, so both kernels give
-// bit-identical outputs.
-template <int HD, bool SPLIT>
-__global__ __launch_bounds__(256, 1) void attn_prefill_grp_kernel(
+template <int HD, int NPL, int W, int GB>
+__global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
     const _Float16 *__restrict__ q16, const _Float16 *__restrict__ q16lo, int hq, KvGeom g,
-    const void *__restrict__ kpool, const void *__restrict__ vpool, const int32_t *__restrict__ pages,
+    const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ vpool, const int32_t *__restrict__ pages,
     int max_pages, const int32_t *__restrict__ grp_first, const int32_t *__restrict__ grp_count,
     const int32_t *__restrict__ tile_seq, const int32_t *__restrict__ tile_row0,
     const int32_t *__restrict__ tile_pos0, const int32_t *__restrict__ tile_n,
     _Float16 *__restrict__ out16, _Float16 *__restrict__ out16lo) {
-  using KV = typename std::conditional<SPLIT, float, _Float16>::type;
+  using S = PrefillStage<HD, NPL>;
   constexpr int KT = HD / 16, DB = HD / 32;
-  constexpr int NPL = SPLIT ? 2 : 1;      // f16 planes per operand
-  constexpr int KS = HD + 8, VS = P + 8;  // padded LDS row strides (halves): conflict-free reads
-  constexpr int EPL = SPLIT ? 4 : 8;      // KV values per 16-byte load
-  constexpr int NLD = P * HD / (256 * EPL);
-  static_assert(NLD * 256 * EPL == P * HD, "page must split evenly over 256 threads");
-  __shared__ __align__(16) _Float16 kls[NPL][P * KS];
-  __shared__ __align__(16) _Float16 vls[NPL][HD * VS];
+  constexpr int NI = (S::BLOCKS + W - 1) / W;  // LDS-DMA instructions per wave per page
+  constexpr uint32_t kPad = 0xffffffffu;
+  __shared__ __align__(16) unsigned char lds[2 * S::BYTES];
 
-  // Same XCD-contiguous mapping as attn_prefill_kernel, over (head, group) pairs.
-  const int total = gridDim.x, ngroups = total / hq;
+  // XCD-contiguous mapping: workgroups are dealt to the 8 XCDs round-robin (i -> XCD i % 8);
+  // each XCD takes one contiguous range of (head block, tile group) pairs, groups fastest, so
+  // the pages of one sequence and kv head are read through one L2.
+  const int G = hq / g.hkv, nhb = G / GB;
+  const int total = gridDim.x, ngroups = total / (g.hkv * nhb);
   const int xcd = blockIdx.x % 8, per = total / 8, rem = total % 8;
   const int logical = xcd * per + min(xcd, rem) + blockIdx.x / 8;
-  const int grp = logical % ngroups, h = logical / ngroups;
+  const int grp = logical % ngroups, hsel = logical / ngroups;
+  const int kh = hsel / nhb, hb = hsel % nhb;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, qi = lane & 31, hl = lane >> 5;
   const int t0 = grp_first[grp], cnt = grp_count[grp];
-  const bool active = wave < cnt;
-  const int tile = t0 + min(wave, cnt - 1);
-  const int seq = tile_seq[tile], row0 = tile_row0[tile], pos0 = tile_pos0[tile], n = tile_n[tile];
+  const bool active = wave / GB < cnt;
+  const int tile = t0 + min(wave / GB, cnt - 1);
+  const int h = kh * G + hb * GB + wave % GB;
+  const int row0 = tile_row0[tile], pos0 = tile_pos0[tile], n = tile_n[tile];
+  const int seq = tile_seq[t0];  // every tile of a group belongs to one sequence
   const int glast = tile_pos0[t0 + cnt - 1] + tile_n[t0 + cnt - 1] - 1;
-  const int kh = h / (hq / g.hkv);
   const int qw = hq * HD;
   const int qpos = pos0 + qi;
   const bool live = qi < n;
 
-  half8 qr[KT], ql[SPLIT ? KT : 1];
+  // this lane's byte offset inside the kv head's K (or V) block for each of its DMA slots
+  uint32_t off[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int b = i * W + wave, slot = b * 64 + lane;
+    uint32_t o = kPad;
+    if (b < S::BLOCKS) {
+      if (slot < S::KSLOTS) {
+        const int p = slot / S::KPL, r = slot % S::KPL, row = r / S::KRS, x = r % S::KRS;
+        if (x < S::KC) o = uint32_t(((p * P + row) * HD + x * 8) * 2);
+      } else {
+        const int s2 = slot - S::KSLOTS, p = s2 / S::VPL, r = s2 % S::VPL, d = r / S::VRS, x = r % S::VRS;
+        if (x < S::VC) o = uint32_t(((p * HD + d) * P + x * 8) * 2);
+      }
+    }
+    off[i] = o;
+  }
+  const int32_t *ptab = pages + int64_t(seq) * max_pages;
+  const int64_t page_halves = int64_t(NPL) * g.page_stride;  // halves per page of one layer
+  const int64_t head_halves = int64_t(NPL) * P * HD;         // halves per kv head of one page
+  auto issue = [&](int32_t page, int st) {
+    const int64_t base = int64_t(page) * page_halves + kh * head_halves;
+    const unsigned char *kb = reinterpret_cast<const unsigned char *>(kpool + base);
+    const unsigned char *vb = reinterpret_cast<const unsigned char *>(vpool + base);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int b = i * W + wave;
+      if (b >= S::BLOCKS) break;
+      const unsigned char *src = (b * 64 < S::KSLOTS ? kb : vb) + off[i];
+      if (off[i] != kPad)
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(lds + st * S::BYTES + b * 1024),
+                                         16, 0, 0);
+    }
+  };
+
+  half8 qr[KT], ql[NPL == 2 ? KT : 1];
   {
-    const int64_t off = int64_t(row0 + min(qi, n - 1)) * qw + h * HD + hl * 8;
+    const int64_t qo = int64_t(row0 + min(qi, n - 1)) * qw + h * HD + hl * 8;
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
-      qr[t] = *reinterpret_cast<const half8 *>(q16 + off + 16 * t);
-      if (SPLIT) ql[t] = *reinterpret_cast<const half8 *>(q16lo + off + 16 * t);
+      qr[t] = *reinterpret_cast<const half8 *>(q16 + qo + 16 * t);
+      if constexpr (NPL == 2) ql[t] = *reinterpret_cast<const half8 *>(q16lo + qo + 16 * t);
     }
   }
   f32x16 acc[DB];
@@ -270,150 +169,107 @@ __global__ __launch_bounds__(256, 1) void attn_prefill_grp_kernel(
   const float scale = kLog2e / sqrtf(float(HD));
   const int npages = glast / P + 1;
   const int mypages = active ? (pos0 + n - 1) / P + 1 : 0;
-  const int32_t *ptab = pages + int64_t(seq) * max_pages;
-  const KV *kbase = static_cast<const KV *>(kpool) + int64_t(kh) * P * HD;
-  const KV *vbase = static_cast<const KV *>(vpool) + int64_t(kh) * HD * P;
+  const int krow = swap23(qi);
 
-  uint4 kreg[NLD], vreg[NLD];
-  // page-table entry of the page after the one in flight: loaded one iteration ahead, so the
-  // K/V prefetch never waits on a page-table round trip
+  issue(ptab[0], 0);
+  // page-table entry of the page after the one in flight, read one iteration ahead so that no
+  // DMA issue waits on a page-table round trip
   int32_t next_page = ptab[min(1, npages - 1)];
-  {
-    const int64_t page = ptab[0];
-    const uint4 *ks = reinterpret_cast<const uint4 *>(kbase + page * g.page_stride);
-    const uint4 *vs = reinterpret_cast<const uint4 *>(vbase + page * g.page_stride);
-#pragma unroll
-    for (int j = 0; j < NLD; ++j) {
-      kreg[j] = ks[tid + 256 * j];
-      vreg[j] = vs[tid + 256 * j];
-    }
-  }
-
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
   for (int kt = 0; kt < npages; ++kt) {
-    __syncthreads();  // every wave is done reading the previous page
-#pragma unroll
-    for (int j = 0; j < NLD; ++j) {
-      const int e0 = (tid + 256 * j) * EPL;  // first value of this load within the page
-      const int kro = (e0 / HD) * KS + e0 % HD;
-      const int vd = e0 / P, vk = e0 % P;
-      if constexpr (SPLIT) {
-        const float4 kf = __builtin_bit_cast(float4, kreg[j]);
-        const float4 vf = __builtin_bit_cast(float4, vreg[j]);
-        const float kv[4] = {kf.x, kf.y, kf.z, kf.w}, vv[4] = {vf.x, vf.y, vf.z, vf.w};
-        half4 khi, klo, vhi, vlo;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          _Float16 a, b, c, d;
-          split_f16(kv[e], a, b);
-          split_f16(vv[e], c, d);
-          khi[e] = a;
-          klo[e] = b;
-          vhi[e] = c;
-          vlo[e] = d;
-        }
-        *reinterpret_cast<half4 *>(&kls[0][kro]) = khi;
-        *reinterpret_cast<half4 *>(&kls[1][kro]) = klo;
-        const int vo = vd * VS + vperm(vk);
-        *reinterpret_cast<half4 *>(&vls[0][vo]) = vhi;
-        *reinterpret_cast<half4 *>(&vls[1][vo]) = vlo;
-      } else {
-        *reinterpret_cast<uint4 *>(&kls[0][kro]) = kreg[j];
-        const half8 v8 = __builtin_bit_cast(half8, vreg[j]);
-        const half4 va = {v8[0], v8[1], v8[2], v8[3]}, vb = {v8[4], v8[5], v8[6], v8[7]};
-        *reinterpret_cast<half4 *>(&vls[0][vd * VS + vperm(vk)]) = va;
-        *reinterpret_cast<half4 *>(&vls[0][vd * VS + vperm(vk + 4)]) = vb;
-      }
-    }
-    __syncthreads();
+    const int st = kt & 1;
     if (kt + 1 < npages) {
-      const int64_t page = next_page;
+      const int32_t page = next_page;
       next_page = ptab[min(kt + 2, npages - 1)];
-      const uint4 *ks = reinterpret_cast<const uint4 *>(kbase + page * g.page_stride);
-      const uint4 *vs = reinterpret_cast<const uint4 *>(vbase + page * g.page_stride);
-#pragma unroll
-      for (int j = 0; j < NLD; ++j) {
-        kreg[j] = ks[tid + 256 * j];
-        vreg[j] = vs[tid + 256 * j];
-      }
+      issue(page, st ^ 1);
     }
-    if (kt >= mypages) continue;
-
-    f32x16 s[2];
+    if (kt < mypages) {
+      const unsigned char *stage = lds + st * S::BYTES;
+      const unsigned char *kl_ = stage + S::KPL * 16 * (NPL - 1);  // K lo plane (= hi when NPL 1)
+      const unsigned char *vh_ = stage + S::KSLOTS * 16, *vl_ = vh_ + S::VPL * 16 * (NPL - 1);
+      f32x16 s[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+      for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
-      const int ro = (kb * 32 + qi) * KS + hl * 8;
+        for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
+        const int ro = (kb * 32 + krow) * S::KRS + hl;
 #pragma unroll
-      for (int t = 0; t < KT; ++t) {
-        const half8 kh8 = *reinterpret_cast<const half8 *>(&kls[0][ro + 16 * t]);
-        if constexpr (SPLIT) {
-          const half8 kl8 = *reinterpret_cast<const half8 *>(&kls[1][ro + 16 * t]);
-          s[kb] = MFMA(kh8, qr[t], s[kb]);
-          s[kb] = MFMA(kl8, qr[t], s[kb]);
-          s[kb] = MFMA(kh8, ql[t], s[kb]);
-        } else {
-          s[kb] = MFMA(kh8, qr[t], s[kb]);
+        for (int t = 0; t < KT; ++t) {
+          const half8 kh8 = lds_half8(stage, ro + 2 * t);
+          if constexpr (NPL == 2) {
+            const half8 kl8 = lds_half8(kl_, ro + 2 * t);
+            s[kb] = MFMA(kh8, qr[t], s[kb]);
+            s[kb] = MFMA(kl8, qr[t], s[kb]);
+            s[kb] = MFMA(kh8, ql[t], s[kb]);
+          } else {
+            s[kb] = MFMA(kh8, qr[t], s[kb]);
+          }
+        }
+      }
+      // s[kb][8 j + e] <-> key kt * P + kb * 32 + 16 j + 8 hl + e, query qi
+      float mt = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kt * P + kb * 32 + (r >> 3) * 16 + hl * 8 + (r & 7);
+          const float v = (key <= qpos && live) ? s[kb][r] * scale : -INFINITY;
+          s[kb][r] = v;
+          mt = fmaxf(mt, v);
+        }
+      mt = fmaxf(mt, __shfl_xor(mt, 32));
+      const float mn = fmaxf(m, mt);
+      const float alpha = mn == -INFINITY ? 1.0f : exp2f(m - mn);
+      float rs = 0.0f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = mn == -INFINITY ? 0.0f : exp2f(s[kb][r] - mn);
+          s[kb][r] = p;
+          rs += p;
+        }
+      rs += __shfl_xor(rs, 32);
+      l = l * alpha + rs;
+      m = mn;
+#pragma unroll
+      for (int b = 0; b < DB; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[b][r] *= alpha;
+      // O^T += V^T . P^T over four 16-key chunks: chunk c takes keys 16 c + 8 hl + 0..7 of this lane
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float pv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pv[e] = s[c >> 1][(c & 1) * 8 + e];
+        half8 ph, pl;
+        if constexpr (NPL == 2) split8(pv, ph, pl);
+        else
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ph[e] = _Float16(pv[e]);
+#pragma unroll
+        for (int b = 0; b < DB; ++b) {
+          const int vo = (b * 32 + qi) * S::VRS + 2 * c + hl;
+          const half8 vh = lds_half8(vh_, vo);
+          if constexpr (NPL == 2) {
+            const half8 vl = lds_half8(vl_, vo);
+            acc[b] = MFMA(vh, ph, acc[b]);
+            acc[b] = MFMA(vl, ph, acc[b]);
+            acc[b] = MFMA(vh, pl, acc[b]);
+          } else {
+            acc[b] = MFMA(vh, ph, acc[b]);
+          }
         }
       }
     }
-    float mt = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kt * P + kb * 32 + (r >> 2) * 8 + hl * 4 + (r & 3);
-        const float v = (key <= qpos && live) ? s[kb][r] * scale : -INFINITY;
-        s[kb][r] = v;
-        mt = fmaxf(mt, v);
-      }
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
-    const float mn = fmaxf(m, mt);
-    const float alpha = mn == -INFINITY ? 1.0f : exp2f(m - mn);
-    float rs = 0.0f;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = mn == -INFINITY ? 0.0f : exp2f(s[kb][r] - mn);
-        s[kb][r] = p;
-        rs += p;
-      }
-    rs += __shfl_xor(rs, 32);
-    l = l * alpha + rs;
-    m = mn;
-#pragma unroll
-    for (int b = 0; b < DB; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[b][r] *= alpha;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      float pv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pv[e] = s[c >> 1][(c & 1) * 8 + e];
-      half8 ph, pl;
-      if constexpr (SPLIT) split8(pv, ph, pl);
-      else
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ph[e] = _Float16(pv[e]);
-#pragma unroll
-      for (int b = 0; b < DB; ++b) {
-        const int vo = (b * 32 + qi) * VS + 16 * c + hl * 8;
-        const half8 vh = *reinterpret_cast<const half8 *>(&vls[0][vo]);
-        if constexpr (SPLIT) {
-          const half8 vl = *reinterpret_cast<const half8 *>(&vls[1][vo]);
-          acc[b] = MFMA(vh, ph, acc[b]);
-          acc[b] = MFMA(vl, ph, acc[b]);
-          acc[b] = MFMA(vh, pl, acc[b]);
-        } else {
-          acc[b] = MFMA(vh, ph, acc[b]);
-        }
-      }
-    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of page kt + 1 has landed
+    __syncthreads();
   }
   if (!active || !live) return;
   const float inv = 1.0f / l;
   const int64_t obase = int64_t(row0 + qi) * qw + h * HD;
+  // acc[b][r] <-> d = b * 32 + (r / 4) * 8 + hl * 4 + r % 4
 #pragma unroll
   for (int b = 0; b < DB; ++b)
 #pragma unroll
@@ -428,7 +284,7 @@ __global__ __launch_bounds__(256, 1) void attn_prefill_grp_kernel(
       }
       const int64_t at = obase + b * 32 + r4 * 8 + hl * 4;
       *reinterpret_cast<half4 *>(out16 + at) = o;
-      if (SPLIT) *reinterpret_cast<half4 *>(out16lo + at) = olo;
+      if constexpr (NPL == 2) *reinterpret_cast<half4 *>(out16lo + at) = olo;
     }
 }
 
@@ -443,18 +299,34 @@ __global__ __launch_bounds__(256, 1) void attn_prefill_grp_kernel(
 // for the stale slot in the registers just loaded.  Scores are reduced over the lanes of a key
 // with DPP moves, the page softmax runs on one wave per head, then P.V reduces over the lanes
 // of a dim.
+// Pool value formats: float, _Float16, or SplitKV: per (page, kv head) block an f16 hi plane and
+// then an f16 lo plane (hi = f16(v), lo = f16(v - hi)), each laid out as the f16 pool is.
+struct SplitKV {};
+template <typename KV>
+struct KvFmt {
+  using elem = KV;
+  static constexpr int NPL = 1;
+};
+template <>
+struct KvFmt<SplitKV> {
+  using elem = _Float16;
+  static constexpr int NPL = 2;
+};
+
 template <int HD, int GRP, typename KV>
 __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, int hq, const KvGeom &g,
                                                  const float *__restrict__ cosT,
                                                  const float *__restrict__ sinT, int pos,
-                                                 KV *__restrict__ kpool, KV *__restrict__ vpool,
+                                                 typename KvFmt<KV>::elem *__restrict__ kpool,
+                                                 typename KvFmt<KV>::elem *__restrict__ vpool,
                                                  const int32_t *__restrict__ pages, float *pbase,
                                                  int64_t hstride);
 template <int HD, int GRP, typename KV>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const float *__restrict__ qkv, int hq, KvGeom g,
                                                           const float *__restrict__ cosT,
                                                           const float *__restrict__ sinT, int pos,
-                                                          KV *__restrict__ kpool, KV *__restrict__ vpool,
+                                                          typename KvFmt<KV>::elem *__restrict__ kpool,
+                                                          typename KvFmt<KV>::elem *__restrict__ vpool,
                                                           const int32_t *__restrict__ pages, int max_pages,
                                                           float *__restrict__ part) {
   static_assert(HD == 64 || HD == 128, "decode attention is written for head_dim 64 and 128");
@@ -553,11 +425,14 @@ template <int HD, int GRP, typename KV>
 __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, int hq, const KvGeom &g,
                                                  const float *__restrict__ cosT,
                                                  const float *__restrict__ sinT, int pos,
-                                                 KV *__restrict__ kpool, KV *__restrict__ vpool,
+                                                 typename KvFmt<KV>::elem *__restrict__ kpool,
+                                                 typename KvFmt<KV>::elem *__restrict__ vpool,
                                                  const int32_t *__restrict__ pages, float *pbase,
                                                  int64_t hstride) {
-  constexpr int E = 16 / sizeof(KV);          // elements per 16-byte word: 4 (f32) or 8 (f16)
-  constexpr int NL = P * HD / E / 256;        // words per thread of K (and of V)
+  using T = typename KvFmt<KV>::elem;
+  constexpr int NPL = KvFmt<KV>::NPL;
+  constexpr int E = 16 / sizeof(T);           // values per 16-byte word: 4 (f32) or 8 (f16 planes)
+  constexpr int NL = P * HD / E / 256;        // words per thread of K (and of V), per plane
   constexpr int LPK = HD / E;                 // lanes per key row of K
   constexpr int LPD = P / E;                  // lanes per dim column of V
   constexpr int HALF = HD / 2;
@@ -568,8 +443,10 @@ __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int len = pos + 1;
   const int64_t page = pages[pi];
-  KV *Kp = kpool + page * g.page_stride + int64_t(kh) * P * HD;
-  KV *Vp = vpool + page * g.page_stride + int64_t(kh) * HD * P;
+  // hi plane (the only one unless split); the lo plane follows one plane (P * HD values) later
+  T *Kp = kpool + page * (NPL * g.page_stride) + int64_t(kh) * NPL * P * HD;
+  T *Vp = vpool + page * (NPL * g.page_stride) + int64_t(kh) * NPL * HD * P;
+  constexpr int PLANE = P * HD;
   const float *cs = cosT + int64_t(pos) * HD, *sn = sinT + int64_t(pos) * HD;
   // query rotation inputs and the new token's k/v first (small); every load is unconditional
   // (clamped index) so that none is sunk behind the page loads
@@ -592,11 +469,17 @@ __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, 
   const float nc0 = cs[jn], nc1 = cs[jn + HALF], ns0 = sn[jn], ns1 = sn[jn + HALF];
   const float nvv = qkv[(hq + g.hkv + kh) * HD + min(max(t - HALF, 0), HD - 1)];
   __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the page's: they return first
-  uint4 kr[NL], vr[NL];
+  uint4 kr[NL], vr[NL], krl[NPL == 2 ? NL : 1], vrl[NPL == 2 ? NL : 1];
 #pragma unroll
-  for (int i = 0; i < NL; ++i) kr[i] = reinterpret_cast<const uint4 *>(Kp)[t + 256 * i];
+  for (int i = 0; i < NL; ++i) {
+    kr[i] = reinterpret_cast<const uint4 *>(Kp)[t + 256 * i];
+    if constexpr (NPL == 2) krl[i] = reinterpret_cast<const uint4 *>(Kp + PLANE)[t + 256 * i];
+  }
 #pragma unroll
-  for (int i = 0; i < NL; ++i) vr[i] = reinterpret_cast<const uint4 *>(Vp)[t + 256 * i];
+  for (int i = 0; i < NL; ++i) {
+    vr[i] = reinterpret_cast<const uint4 *>(Vp)[t + 256 * i];
+    if constexpr (NPL == 2) vrl[i] = reinterpret_cast<const uint4 *>(Vp + PLANE)[t + 256 * i];
+  }
   // RoPE (src/models/openthai/model.rs:276-294 applies it to q and k before the dot products)
   __shared__ float qs[GRP * HD + HD];  // tail: landing row for idle threads
   __shared__ float nka[256], nkb[256], nvs[256];  // new k (pairs j, j + HD/2) and v staged per thread
@@ -611,40 +494,77 @@ __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, 
   }
   const bool cur = pi == pos / P;  // this page holds the new token (uniform per workgroup)
   const int slot = pos % P;
-  {  // the new token's rotated k and its v, computed and staged in LDS by every thread (idle
-     // threads write junk to their own slots), so their loads stay ahead of the page's; only
-     // the page that holds the slot stores them into the cache
-    const KV a = KV(nku * nc0 - nkv * ns0), b = KV(nkv * nc1 + nku * ns1), v = KV(nvv);
-    nka[t] = float(a);
-    nkb[t] = float(b);
-    nvs[t] = float(v);
-    if (cur) {
-      if (t < HALF) {
-        Kp[slot * HD + t] = a;
-        Kp[slot * HD + t + HALF] = b;
-      } else if (t < HALF + HD) {
-        Vp[(t - HALF) * P + slot] = v;
+  {  // the new token's rotated k and its v, computed and staged in LDS (as the cache holds them)
+     // by every thread (idle threads write junk to their own slots), so their loads stay ahead
+     // of the page's; only the page that holds the slot stores them into the cache
+    const float a = nku * nc0 - nkv * ns0, b = nkv * nc1 + nku * ns1;
+    if constexpr (NPL == 2) {
+      _Float16 ah, al, bh, bl, vh, vl;
+      split_f16(a, ah, al);
+      split_f16(b, bh, bl);
+      split_f16(nvv, vh, vl);
+      nka[t] = float(ah) + float(al);
+      nkb[t] = float(bh) + float(bl);
+      nvs[t] = float(vh) + float(vl);
+      if (cur) {
+        if (t < HALF) {
+          Kp[slot * HD + t] = ah;
+          Kp[PLANE + slot * HD + t] = al;
+          Kp[slot * HD + t + HALF] = bh;
+          Kp[PLANE + slot * HD + t + HALF] = bl;
+        } else if (t < HALF + HD) {
+          Vp[(t - HALF) * P + slot] = vh;
+          Vp[PLANE + (t - HALF) * P + slot] = vl;
+        }
+      }
+    } else {
+      const T ac = T(a), bc = T(b), vc = T(nvv);
+      nka[t] = float(ac);
+      nkb[t] = float(bc);
+      nvs[t] = float(vc);
+      if (cur) {
+        if (t < HALF) {
+          Kp[slot * HD + t] = ac;
+          Kp[slot * HD + t + HALF] = bc;
+        } else if (t < HALF + HD) {
+          Vp[(t - HALF) * P + slot] = vc;
+        }
       }
     }
   }
   __syncthreads();
   const int kd0 = (t * E) % HD;   // K: first dim of this thread's words (same for every i)
   const int vk0 = (t * E) % P;    // V: first key of this thread's words (same for every i)
+  // element e of word w (+ its lo plane word wl when split), as the value the cache holds
+  auto put = [&](uint4 &w, uint4 &wl, int e, float v) {
+    if constexpr (NPL == 2) {
+      _Float16 hi, lo;
+      split_f16(v, hi, lo);  // v = hi + lo exactly: this gives back the stored planes
+      reinterpret_cast<_Float16 *>(&w)[e] = hi;
+      reinterpret_cast<_Float16 *>(&wl)[e] = lo;
+    } else {
+      reinterpret_cast<T *>(&w)[e] = T(v);
+    }
+  };
+  auto get = [&](const uint4 &w, const uint4 &wl, int e) -> float {
+    if constexpr (NPL == 2)
+      return float(reinterpret_cast<const _Float16 *>(&w)[e]) + float(reinterpret_cast<const _Float16 *>(&wl)[e]);
+    else
+      return float(reinterpret_cast<const T *>(&w)[e]);
+  };
   if (cur) {  // the registers hold the slot as it was before this step: use the new values
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
-      KV *k8 = reinterpret_cast<KV *>(&kr[i]);
       if ((t + 256 * i) * E / HD == slot)
 #pragma unroll
         for (int e = 0; e < E; ++e) {
           const int dd = kd0 + e;
-          k8[e] = KV(dd < HALF ? nka[dd] : nkb[dd - HALF]);
+          put(kr[i], krl[NPL == 2 ? i : 0], e, dd < HALF ? nka[dd] : nkb[dd - HALF]);
         }
-      KV *v8 = reinterpret_cast<KV *>(&vr[i]);
       const int dim = (t + 256 * i) * E / P;
 #pragma unroll
       for (int e = 0; e < E; ++e)
-        if (vk0 + e == slot) v8[e] = KV(nvs[HALF + dim]);
+        if (vk0 + e == slot) put(vr[i], vrl[NPL == 2 ? i : 0], e, nvs[HALF + dim]);
     }
   }
   const float inv_sqrt = 1.0f / sqrtf(float(HD));
@@ -655,10 +575,9 @@ __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, 
     for (int e = 0; e < E; ++e) q[e] = qs[gq * HD + kd0 + e];
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
-      const KV *k8 = reinterpret_cast<const KV *>(&kr[i]);
       float d = 0.0f;
 #pragma unroll
-      for (int e = 0; e < E; ++e) d = fmaf(q[e], float(k8[e]), d);
+      for (int e = 0; e < E; ++e) d = fmaf(q[e], get(kr[i], krl[NPL == 2 ? i : 0], e), d);
       const int key = (t + 256 * i) * E / HD;
       if constexpr (LPK == 32) {
         d = half_sum_odd_rows(d);  // lanes 16-31 / 48-63 hold the key's sum
@@ -693,10 +612,9 @@ __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, 
     for (int e = 0; e < E; ++e) p[e] = sc[gq][vk0 + e];
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
-      const KV *v8 = reinterpret_cast<const KV *>(&vr[i]);
       float a = 0.0f;
 #pragma unroll
-      for (int e = 0; e < E; ++e) a = fmaf(p[e], float(v8[e]), a);
+      for (int e = 0; e < E; ++e) a = fmaf(p[e], get(vr[i], vrl[NPL == 2 ? i : 0], e), a);
       a = LPD == 16 ? row_sum(a) : group8_sum(a);
       if ((lane & (LPD - 1)) == 0) pbase[gq * hstride + 2 + (t + 256 * i) * E / P] = a;
     }
@@ -704,6 +622,25 @@ __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, 
 }
 
 }  // namespace
+
+namespace {
+// (GB, T): query heads per workgroup and tiles per group for a GQA group of G heads.  Eight
+// waves (two per SIMD) where G allows; G = 7 takes seven.
+struct PrefillShape {
+  int gb, t;
+};
+PrefillShape prefill_shape(int G) {
+  switch (G) {
+    case 2: return {2, 4};
+    case 4: return {4, 2};
+    case 7: return {7, 1};
+    case 8: return {8, 1};
+    default: return {1, 8};
+  }
+}
+}  // namespace
+
+int attn_prefill_group_tiles(int hq, int hkv) { return prefill_shape(hq / hkv).t; }
 
 void launch_attn_prefill(const _Float16 *q16, const _Float16 *q16_lo, int T, int hq,
                          const KvGeom &g, const void *kpool, const void *vpool,
@@ -713,37 +650,38 @@ void launch_attn_prefill(const _Float16 *q16, const _Float16 *q16_lo, int T, int
                          const int32_t *grp_count, int ngroups, _Float16 *out16,
                          _Float16 *out16_lo, hipStream_t st) {
   LG_REQUIRE(g.page_tokens == P, "attention: page size must be %d", P);
-  LG_REQUIRE(hq % g.hkv == 0, "attention: hq %% hkv != 0");
+  LG_REQUIRE(g.hkv > 0 && hq % g.hkv == 0, "attention: hq %% hkv != 0");
   LG_REQUIRE(ntiles > 0 && T > 0, "attention: empty batch");
   const bool split = q16_lo != nullptr;
-  LG_REQUIRE(split == (g.kv32 != 0), "attention: split queries need the f32 cache and vice versa");
+  LG_REQUIRE(split == (g.split != 0), "attention: split queries need the split cache and vice versa");
   LG_REQUIRE(!split || out16_lo, "attention: split path needs the lo output plane");
-  LG_REQUIRE(int64_t(ntiles) * hq < (1ll << 31), "attention: too many tiles");
-  if (grp_first && g.hd == 128) {
-    LG_REQUIRE(ngroups > 0 && ngroups <= ntiles, "attention: bad tile groups");
-    const dim3 grid(ngroups * hq), block(256);
-    if (split)
-      hipLaunchKernelGGL((attn_prefill_grp_kernel<128, true>), grid, block, 0, st, q16, q16_lo, hq, g,
-                         kpool, vpool, pages, max_pages, grp_first, grp_count, tile_seq, tile_row0,
-                         tile_pos0, tile_n, out16, out16_lo);
-    else
-      hipLaunchKernelGGL((attn_prefill_grp_kernel<128, false>), grid, block, 0, st, q16, q16_lo, hq, g,
-                         kpool, vpool, pages, max_pages, grp_first, grp_count, tile_seq, tile_row0,
-                         tile_pos0, tile_n, out16, out16_lo);
-    HIP_CHECK(hipGetLastError());
-    return;
+  LG_REQUIRE(grp_first && grp_count && ngroups > 0 && ngroups <= ntiles, "attention: bad tile groups");
+  const int G = hq / g.hkv;
+  const PrefillShape sh = prefill_shape(G);
+  const int64_t nwg = int64_t(ngroups) * g.hkv * (G / sh.gb);
+  LG_REQUIRE(nwg < (1ll << 31), "attention: too many tiles");
+  const dim3 grid{static_cast<uint32_t>(nwg)}, block{static_cast<uint32_t>(64 * sh.gb * sh.t)};
+  const _Float16 *kp = static_cast<const _Float16 *>(kpool), *vp = static_cast<const _Float16 *>(vpool);
+#define LAUNCH(HDV, NPLV, WV, GBV)                                                                          \
+  hipLaunchKernelGGL((attn_prefill_kernel<HDV, NPLV, WV, GBV>), grid, block, 0, st, q16, q16_lo, hq, g, kp, vp, \
+                     pages, max_pages, grp_first, grp_count, tile_seq, tile_row0, tile_pos0, tile_n, out16,    \
+                     out16_lo)
+#define SHAPES(HDV, NPLV)                  \
+  switch (sh.gb) {                         \
+    case 2: LAUNCH(HDV, NPLV, 8, 2); break; \
+    case 4: LAUNCH(HDV, NPLV, 8, 4); break; \
+    case 7: LAUNCH(HDV, NPLV, 7, 7); break; \
+    case 8: LAUNCH(HDV, NPLV, 8, 8); break; \
+    default: LAUNCH(HDV, NPLV, 8, 1); break; \
   }
-  const dim3 grid(ntiles * hq), block(64);
-#define LAUNCH(HDV, S)                                                                              \
-  hipLaunchKernelGGL((attn_prefill_kernel<HDV, S>), grid, block, 0, st, q16, q16_lo, hq, g, kpool, vpool, \
-                     pages, max_pages, tile_seq, tile_row0, tile_pos0, tile_n, out16, out16_lo)
-  if (g.hd == 64) {
-    if (split) LAUNCH(64, true); else LAUNCH(64, false);
-  } else if (g.hd == 128) {
-    if (split) LAUNCH(128, true); else LAUNCH(128, false);
+  if (g.hd == 128) {
+    if (split) { SHAPES(128, 2) } else { SHAPES(128, 1) }
+  } else if (g.hd == 64) {
+    if (split) { SHAPES(64, 2) } else { SHAPES(64, 1) }
   } else {
     fail(LG_ERR_UNSUPPORTED, "attention: head_dim %d not supported (64, 128)", g.hd);
   }
+#undef SHAPES
 #undef LAUNCH
   HIP_CHECK(hipGetLastError());
 }
@@ -766,10 +704,10 @@ void launch_attn_decode(const float *qkv, int hq, const KvGeom &g, const float *
   const dim3 grid(np, g.hkv), block(256);
 #define CASE(HDV, G)                                                                                     \
   case G:                                                                                                \
-    if (g.kv32)                                                                                          \
-      hipLaunchKernelGGL((attn_decode_kernel<HDV, G, float>), grid, block, 0, st, qkv, hq, g, cosT, sinT, \
-                         pos, static_cast<float *>(kpool), static_cast<float *>(vpool), pages, max_pages, \
-                         part);                                                                          \
+    if (g.split)                                                                                         \
+      hipLaunchKernelGGL((attn_decode_kernel<HDV, G, SplitKV>), grid, block, 0, st, qkv, hq, g, cosT, sinT, \
+                         pos, static_cast<_Float16 *>(kpool), static_cast<_Float16 *>(vpool), pages,    \
+                         max_pages, part);                                                               \
     else                                                                                                 \
       hipLaunchKernelGGL((attn_decode_kernel<HDV, G, _Float16>), grid, block, 0, st, qkv, hq, g, cosT,    \
                          sinT, pos, static_cast<_Float16 *>(kpool), static_cast<_Float16 *>(vpool), pages, \

@@ -109,14 +109,21 @@ __global__ void embed_kernel(const void *__restrict__ table, uint32_t kind, cons
                         : static_cast<const float *>(table)[src];
 }
 
-// One KV value into a pool slot (value index i): f32 pools (KV32) or f16 pools.
+// One KV value into a pool: offset r inside the (page, kv head) block that starts at value
+// `block` (page * page_stride + head * plane).  Split pools hold the block as an f16 hi plane
+// and then an f16 lo plane of `plane` values each; f16 pools as one plane.
 // RoPE everywhere is the rotate-half form with the model's tables (src/tensor.rs:158-172).
-template <bool KV32>
-__device__ __forceinline__ void kv_put(void *pool, int64_t i, float v) {
-  if constexpr (KV32)
-    static_cast<float *>(pool)[i] = v;
-  else
-    static_cast<_Float16 *>(pool)[i] = _Float16(v);
+template <bool SPLIT>
+__device__ __forceinline__ void kv_put(void *pool, int64_t block, int r, int plane, float v) {
+  _Float16 *p = static_cast<_Float16 *>(pool);
+  if constexpr (SPLIT) {
+    _Float16 hi, lo;
+    split_f16(v, hi, lo);
+    p[2 * block + r] = hi;
+    p[2 * block + plane + r] = lo;
+  } else {
+    p[block + r] = _Float16(v);
+  }
 }
 
 // Decode form: one token whose position and KV page the host already knows (kernel arguments,
@@ -126,7 +133,7 @@ __device__ __forceinline__ void kv_put(void *pool, int64_t i, float v) {
 // loads are all issued before any is used; v is staged through LDS a few kv heads at a time
 // so that its transposed page layout is written as runs of consecutive slots instead of one
 // 4-byte store per cache line.
-template <bool KV32, int HD>
+template <bool SPLIT, int HD>
 __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
     const float *__restrict__ qkv, int hq, KvGeom g, const float *__restrict__ cosT,
     const float *__restrict__ sinT, const int32_t *__restrict__ pages, int max_pages,
@@ -146,6 +153,7 @@ __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
   const int pg0 = pos0 / g.page_tokens;
   const int64_t page_lo = ptab[pg0], page_hi = ptab[(pos0 + n - 1) / g.page_tokens];
   auto page_base = [&](int pos) { return (pos / g.page_tokens == pg0 ? page_lo : page_hi) * g.page_stride; };
+  const int plane = g.page_tokens * HD;  // values per plane of one (page, kv head) block
   const int qw = hq * HD, kvw = g.hkv * HD, rw = qw + 2 * kvw;
   // rotations: thread -> pairs p = tid + 256 m of the q|k heads (pair j = p % HALF is the same
   // for every m), QB tokens per round with every load issued before any value is used
@@ -187,9 +195,10 @@ __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
           }
         } else {
           const int pos = pos0 + tk;
-          const int64_t at = page_base(pos) + (int64_t(hh - hq) * g.page_tokens + pos % g.page_tokens) * HD;
-          kv_put<KV32>(kpool, at + j, a);
-          kv_put<KV32>(kpool, at + j + HALF, c);
+          const int64_t blk = page_base(pos) + int64_t(hh - hq) * plane;
+          const int r = (pos % g.page_tokens) * HD + j;
+          kv_put<SPLIT>(kpool, blk, r, plane, a);
+          kv_put<SPLIT>(kpool, blk, r + HALF, plane, c);
         }
       }
     }
@@ -217,8 +226,8 @@ __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
       const int hh = i / (TT * HD), r = i % (TT * HD), tk = r % TT, d2 = r / TT;
       if (tk < n) {
         const int pos = pos0 + tk;
-        kv_put<KV32>(vpool, page_base(pos) + (int64_t(h0 + hh) * HD + d2) * g.page_tokens + pos % g.page_tokens,
-                     vs[hh][tk][d2]);
+        kv_put<SPLIT>(vpool, page_base(pos) + int64_t(h0 + hh) * plane, d2 * g.page_tokens + pos % g.page_tokens,
+                      plane, vs[hh][tk][d2]);
       }
     }
     __syncthreads();
@@ -431,9 +440,9 @@ void launch_rope_kv_tiles(const float *qkv, int hq, const KvGeom &g, const float
   hipLaunchKernelGGL((rope_kv_tile_kernel<K32, HDV>), dim3(ntiles), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, \
                      pages, max_pages, tile_seq, tile_row0, tile_pos0, tile_n, q16, q16_lo, kpool, vpool)
   if (g.hd == 128) {
-    if (g.kv32) LAUNCH(true, 128); else LAUNCH(false, 128);
+    if (g.split) LAUNCH(true, 128); else LAUNCH(false, 128);
   } else if (g.hd == 64) {
-    if (g.kv32) LAUNCH(true, 64); else LAUNCH(false, 64);
+    if (g.split) LAUNCH(true, 64); else LAUNCH(false, 64);
   } else {
     fail(LG_ERR_UNSUPPORTED, "rope_kv: head_dim %d not supported (64, 128)", g.hd);
   }

@@ -96,14 +96,17 @@ void launch_embed(const void *table, uint32_t kind, const int32_t *ids, int T, i
 struct KvGeom {
   int page_tokens = 64;  // tokens per page
   int hkv = 0, hd = 0;
-  int kv32 = 0;              // value type of the pools: 0 = f16, 1 = f32
+  int split = 0;             // value format of the pools: 0 = f16, 1 = f16 hi plane + f16 lo plane
   int64_t layer_stride = 0;  // values between layers of the K (or V) pool
   int64_t page_stride = 0;   // values per page of one layer: hkv * page_tokens * hd
 };
+// Pool layout of one layer: [page][kv head][plane][...] where a plane is K rows [page_tokens][hd]
+// or V columns [hd][page_tokens] of f16; a split pool has two planes per (page, kv head), hi
+// then lo (hi = f16(v), lo = f16(v - hi)), an f16 pool one.
 
 // RoPE on q and k of q|k|v rows ((hq+2hkv)*hd f32) with tables cos/sin[ctx][hd], q written
 // out, k and v written into the K page rows [hkv][page_tokens][hd] and V page columns
-// [hkv][hd][page_tokens] of the layer pools (value format per g.kv32).
+// [hkv][hd][page_tokens] of the layer pools (value format per g.split).
 // This form: a prefill batch, one workgroup per attention tile (<= 32 consecutive tokens
 // of one sequence, rows row0.., positions pos0..); q goes to f16 planes.  head_dim <= 128.
 void launch_rope_kv_tiles(const float *qkv, int hq, const KvGeom &g, const float *cosT,
@@ -114,10 +117,12 @@ void launch_rope_kv_tiles(const float *qkv, int hq, const KvGeom &g, const float
 
 // Causal prefill attention over the paged cache.  Work items: tiles of 32 query rows of one
 // sequence (tile_seq, tile_row0 = first batch row, tile_pos0 = its position, tile_n rows).
-// q16_lo != nullptr selects the split-precision path (requires an f32 cache); the output is
-// then written as hi/lo planes (out16, out16_lo).  With grp_first != nullptr (head_dim 128),
-// tiles go in groups of <= 4 consecutive tiles of one sequence (grp_first[i], grp_count[i]
-// for i < ngroups) that share each K/V page through LDS; outputs are bit-identical.
+// q16_lo != nullptr selects the split-precision path (requires the split cache); the output is
+// then written as hi/lo planes (out16, out16_lo).  Tiles go in groups (grp_first[i],
+// grp_count[i] for i < ngroups) of at most attn_prefill_group_tiles(hq, hkv) consecutive tiles
+// of one sequence; each group's workgroups share every K/V page through LDS.  head_dim 64 or 128.
+// A query's output does not depend on which group or batch its tile is in.
+int attn_prefill_group_tiles(int hq, int hkv);
 void launch_attn_prefill(const _Float16 *q16, const _Float16 *q16_lo, int T, int hq,
                          const KvGeom &g, const void *kpool, const void *vpool,
                          const int32_t *pages, int max_pages, const int32_t *tile_seq,
