@@ -34,7 +34,6 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int P = 64;  // tokens per page
-constexpr float kLog2e = 1.4426950408889634f;
 
 #define MFMA(a, b, c) __builtin_amdgcn_mfma_f32_32x32x16_f16((a), (b), (c), 0, 0, 0)
 
@@ -166,7 +165,6 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[b][r] = 0.0f;
   float m = -INFINITY, l = 0.0f;
-  const float scale = kLog2e / sqrtf(float(HD));
   const int npages = glast / P + 1;
   const int mypages = active ? (pos0 + n - 1) / P + 1 : 0;
   const int krow = swap23(qi);
@@ -207,36 +205,52 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
           }
         }
       }
-      // s[kb][8 j + e] <-> key kt * P + kb * 32 + 16 j + 8 hl + e, query qi
+      // s[kb][8 j + e] <-> key kt * P + kb * 32 + 16 j + 8 hl + e, query qi.  The queries come
+      // pre-multiplied by log2(e) / sqrt(hd), so s is the base-2 logit.  Only a page that reaches
+      // past the tile's first query needs the causal mask; rows past the tile's end (qi >= n)
+      // repeat row n - 1's query and are never stored.
+      if (kt * P + P - 1 > pos0) {
+        const int lim = qpos - kt * P - hl * 8;  // mask offsets kb * 32 + 16 j + e above this
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (kb * 32 + (r >> 3) * 16 + (r & 7) > lim) s[kb][r] = -INFINITY;
+      }
       float mt = -INFINITY;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kt * P + kb * 32 + (r >> 3) * 16 + hl * 8 + (r & 7);
-          const float v = (key <= qpos && live) ? s[kb][r] * scale : -INFINITY;
-          s[kb][r] = v;
-          mt = fmaxf(mt, v);
-        }
+        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][r]);
       mt = fmaxf(mt, __shfl_xor(mt, 32));
-      const float mn = fmaxf(m, mt);
-      const float alpha = mn == -INFINITY ? 1.0f : exp2f(m - mn);
+      // A lane's exponent base m moves only when one of its scores exceeds it by more than 8,
+      // so p = 2^(s - m) <= 256; l and acc carry the same base, so out = acc / l is unchanged.
+      // The rescale is skipped unless some lane of the wave moves; the others multiply by
+      // exactly 1, so a query's arithmetic never depends on the other queries of its wave.
+      // Key 0 is visible to every query, so m is finite from the first page on and
+      // 2^(-inf - m) = 0 drops masked keys.
+      const bool grow = mt > m + 8.0f;
+      if (__any(grow)) {
+        const float mn = grow ? mt : m;
+        const float alpha = __builtin_amdgcn_exp2f(m - mn);
+        l *= alpha;
+#pragma unroll
+        for (int b = 0; b < DB; ++b)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[b][r] *= alpha;
+        m = mn;
+      }
       float rs = 0.0f;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const float p = mn == -INFINITY ? 0.0f : exp2f(s[kb][r] - mn);
+          const float p = __builtin_amdgcn_exp2f(s[kb][r] - m);
           s[kb][r] = p;
           rs += p;
         }
       rs += __shfl_xor(rs, 32);
-      l = l * alpha + rs;
-      m = mn;
-#pragma unroll
-      for (int b = 0; b < DB; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[b][r] *= alpha;
+      l += rs;
       // O^T += V^T . P^T over four 16-key chunks: chunk c takes keys 16 c + 8 hl + 0..7 of this lane
 #pragma unroll
       for (int c = 0; c < 4; ++c) {

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cfloat>
+#include <cmath>
 
 #include "common.h"
 #include "kernels.h"
@@ -140,7 +141,7 @@ __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
     const int32_t *__restrict__ tile_seq, const int32_t *__restrict__ tile_row0,
     const int32_t *__restrict__ tile_pos0, const int32_t *__restrict__ tile_n,
     _Float16 *__restrict__ q16, _Float16 *__restrict__ q16lo, void *__restrict__ kpool,
-    void *__restrict__ vpool) {
+    void *__restrict__ vpool, float qscale) {
   constexpr int TT = 32, HALF = HD / 2, HB = 2;  // tokens per tile, pair offset, V heads per LDS round
   constexpr int QB = 8;                         // tokens whose loads one round issues together
   constexpr int TPR = kT / HD, VT = TT / TPR;   // V: token lanes per dim, tokens per thread
@@ -185,8 +186,8 @@ __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
         if (hh < hq) {
           const int64_t at = int64_t(row0 + tk) * qw + hh * HD + j;
           _Float16 ah, al, ch, cl;
-          split_f16(a, ah, al);
-          split_f16(c, ch, cl);
+          split_f16(a * qscale, ah, al);
+          split_f16(c * qscale, ch, cl);
           q16[at] = ah;
           q16[at + HALF] = ch;
           if (q16lo) {
@@ -436,9 +437,11 @@ void launch_rope_kv_tiles(const float *qkv, int hq, const KvGeom &g, const float
                           void *kpool, void *vpool, hipStream_t st) {
   LG_REQUIRE(ntiles > 0 && q16, "rope_kv: bad arguments");
   LG_REQUIRE(g.page_tokens >= 32, "rope_kv: a 32-token tile must span at most two pages");
+  // the attention consumes base-2 logits: fold log2(e) / sqrt(hd) into q once here
+  const float qscale = 1.4426950408889634f / std::sqrt(float(g.hd));
 #define LAUNCH(K32, HDV)                                                                                  \
   hipLaunchKernelGGL((rope_kv_tile_kernel<K32, HDV>), dim3(ntiles), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, \
-                     pages, max_pages, tile_seq, tile_row0, tile_pos0, tile_n, q16, q16_lo, kpool, vpool)
+                     pages, max_pages, tile_seq, tile_row0, tile_pos0, tile_n, q16, q16_lo, kpool, vpool, qscale)
   if (g.hd == 128) {
     if (g.split) LAUNCH(true, 128); else LAUNCH(false, 128);
   } else if (g.hd == 64) {

@@ -108,14 +108,16 @@ struct KvGeom {
 // out, k and v written into the K page rows [hkv][page_tokens][hd] and V page columns
 // [hkv][hd][page_tokens] of the layer pools (value format per g.split).
 // This form: a prefill batch, one workgroup per attention tile (<= 32 consecutive tokens
-// of one sequence, rows row0.., positions pos0..); q goes to f16 planes.  head_dim <= 128.
+// of one sequence, rows row0.., positions pos0..); q goes to f16 planes, multiplied by
+// log2(e) / sqrt(hd) (the scaled base-2 logit form launch_attn_prefill expects).  head_dim <= 128.
 void launch_rope_kv_tiles(const float *qkv, int hq, const KvGeom &g, const float *cosT,
                           const float *sinT, const int32_t *pages, int max_pages,
                           const int32_t *tile_seq, const int32_t *tile_row0, const int32_t *tile_pos0,
                           const int32_t *tile_n, int ntiles, _Float16 *q16, _Float16 *q16_lo,
                           void *kpool, void *vpool, hipStream_t st);
 
-// Causal prefill attention over the paged cache.  Work items: tiles of 32 query rows of one
+// Causal prefill attention over the paged cache, queries as launch_rope_kv_tiles leaves them
+// (pre-scaled by log2(e) / sqrt(hd)).  Work items: tiles of 32 query rows of one
 // sequence (tile_seq, tile_row0 = first batch row, tile_pos0 = its position, tile_n rows).
 // q16_lo != nullptr selects the split-precision path (requires the split cache); the output is
 // then written as hi/lo planes (out16, out16_lo).  Tiles go in groups (grp_first[i],
