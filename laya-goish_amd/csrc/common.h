@@ -13,6 +13,10 @@
 
 namespace lg {
 
+// Word 3 of a raw buffer resource on gfx9 (32-bit data format, no swizzle); reads beyond
+// num_records return zero.
+constexpr int kBufferFlags = 0x00020000;
+
 struct Error : std::runtime_error {
   int code;
   Error(int c, const std::string &m) : std::runtime_error(m), code(c) {}

@@ -21,4 +21,35 @@ __device__ __forceinline__ void split_f16(float v, _Float16 &hi, _Float16 &lo) {
   lo = _Float16(v - float(hi));
 }
 
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// v - float(h[SEL]) in one v_fma_mix_f32 (v + h * -1, the f16 operand widened inside the
+// instruction).  The difference of v and its own f16 rounding is exact in f32, as in split_f16.
+template <int SEL>
+__device__ __forceinline__ float sub_f16(float v, f16x2 h) {
+  float d;
+  if constexpr (SEL == 0)
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(h), "v"(v));
+  else
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(h), "v"(v));
+  return d;
+}
+
+// split_f16 of eight values, two at a time (packed conversions): the same hi and lo bits in
+// two instructions a value instead of four.
+__device__ __forceinline__ void split8_pk(const float *v, f16x8 &hi, f16x8 &lo) {
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const f32x2 w = {f32_pin(v[e]), f32_pin(v[e + 1])};
+    const f16x2 h = __builtin_convertvector(w, f16x2);
+    const f16x2 l = __builtin_convertvector((f32x2{sub_f16<0>(w[0], h), sub_f16<1>(w[1], h)}), f16x2);
+    hi[e] = h[0];
+    hi[e + 1] = h[1];
+    lo[e] = l[0];
+    lo[e + 1] = l[1];
+  }
+}
+
 }  // namespace lg

@@ -45,10 +45,6 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 // a NaN scale gives NaN outputs either way).
 __device__ __forceinline__ float hw_half(uint32_t x) { return float(__builtin_bit_cast(_Float16, uint16_t(x))); }
 
-// Word 3 of a raw buffer resource on gfx9 (32-bit data format, no swizzle); reads beyond
-// num_records return zero.
-constexpr int kBufferFlags = 0x00020000;
-
 __device__ __forceinline__ void put8(const float *v, _Float16 *hi, _Float16 *lo, bool split) {
   half8 h, l;
 #pragma unroll

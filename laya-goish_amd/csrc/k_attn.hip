@@ -37,16 +37,6 @@ constexpr int P = 64;  // tokens per page
 
 #define MFMA(a, b, c) __builtin_amdgcn_mfma_f32_32x32x16_f16((a), (b), (c), 0, 0, 0)
 
-__device__ __forceinline__ void split8(const float *v, half8 &hi, half8 &lo) {
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    _Float16 h, l;
-    split_f16(v[j], h, l);
-    hi[j] = h;
-    lo[j] = l;
-  }
-}
-
 // Prefill.  Work item: (tile group, kv head kh, head block hb).  A tile group is <= T
 // consecutive 32-query tiles of one sequence, a head block GB consecutive query heads of kh's
 // group of G = hq / hkv.  Wave w computes head kh * G + hb * GB + w % GB on tile w / GB of the
@@ -91,7 +81,6 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
   using S = PrefillStage<HD, NPL>;
   constexpr int KT = HD / 16, DB = HD / 32;
   constexpr int NI = (S::BLOCKS + W - 1) / W;  // LDS-DMA instructions per wave per page
-  constexpr uint32_t kPad = 0xffffffffu;
   __shared__ __align__(16) unsigned char lds[2 * S::BYTES];
 
   // XCD-contiguous mapping: workgroups are dealt to the 8 XCDs round-robin (i -> XCD i % 8);
@@ -115,12 +104,14 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
   const int qpos = pos0 + qi;
   const bool live = qi < n;
 
-  // this lane's byte offset inside the kv head's K (or V) block for each of its DMA slots
+  // this lane's byte offset inside the kv head's K (or V) block for each of its DMA slots; pad
+  // slots get an offset past the block, which the buffer load turns into zeros without a read
+  constexpr uint32_t kHeadBytes = uint32_t(NPL) * P * HD * 2;
   uint32_t off[NI];
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
     const int b = i * W + wave, slot = b * 64 + lane;
-    uint32_t o = kPad;
+    uint32_t o = kHeadBytes;
     if (b < S::BLOCKS) {
       if (slot < S::KSLOTS) {
         const int p = slot / S::KPL, r = slot % S::KPL, row = r / S::KRS, x = r % S::KRS;
@@ -137,16 +128,21 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
   const int64_t head_halves = int64_t(NPL) * P * HD;         // halves per kv head of one page
   auto issue = [&](int32_t page, int st) {
     const int64_t base = int64_t(page) * page_halves + kh * head_halves;
-    const unsigned char *kb = reinterpret_cast<const unsigned char *>(kpool + base);
-    const unsigned char *vb = reinterpret_cast<const unsigned char *>(vpool + base);
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(kpool + base), 0, kHeadBytes, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(vpool + base), 0, kHeadBytes, kBufferFlags);
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int b = i * W + wave;
       if (b >= S::BLOCKS) break;
-      const unsigned char *src = (b * 64 < S::KSLOTS ? kb : vb) + off[i];
-      if (off[i] != kPad)
-        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)(lds + st * S::BYTES + b * 1024),
-                                         16, 0, 0);
+#if defined(__HIP_DEVICE_COMPILE__)
+      // device pass only: with a run-time voffset this builtin keeps the host pass from
+      // emitting the kernel's launch stub (the host never runs kernel bodies)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(b * 64 < S::KSLOTS ? rk : rv,
+                                               (__attribute__((address_space(3))) void *)(lds + st * S::BYTES + b * 1024),
+                                               16, off[i], 0, 0, 0);
+#endif
     }
   };
 
@@ -258,7 +254,7 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
 #pragma unroll
         for (int e = 0; e < 8; ++e) pv[e] = s[c >> 1][(c & 1) * 8 + e];
         half8 ph, pl;
-        if constexpr (NPL == 2) split8(pv, ph, pl);
+        if constexpr (NPL == 2) split8_pk(pv, ph, pl);
         else
 #pragma unroll
           for (int e = 0; e < 8; ++e) ph[e] = _Float16(pv[e]);
