@@ -192,7 +192,7 @@ def c3_decode(eng, args):
                              "gemv (dequant-fused Q8_0 GEMV, GGUF bytes per launch)", gv["launches"],
                              gv["ms"] / max(1, gv["launches"]), measured_traffic("gemv")),
         "attention": roofline("hbm", rate(at, "bytes"), PEAK_HBM_GBS, "GB/s",
-                              "attn_decode (f32 KV bytes read per launch, incl. the page-combine launch)",
+                              "attn_decode (KV bytes read per launch: f16 hi + lo planes in the exact mode; incl. the page-combine launch)",
                               at["launches"], at["ms"] / max(1, at["launches"])),
         "kernel_ms_per_token": {c: round(p["ms"] / steps, 4) for c, p in prof.items()},
     }
@@ -437,7 +437,7 @@ def c5_long_context(args, prec, layer_cost):
                              "gemm (F16 weights, hi/lo split activations: two f16 passes per product)",
                              gp["launches"], gp["ms"] / max(1, gp["launches"])),
         "attention": roofline("mfma", att_tf, PEAK_F16_TFLOPS, "TFLOP/s",
-                              "attn_prefill (causal GQA over the paged f32 cache; three f16 passes per product)",
+                              "attn_prefill (causal GQA over the paged KV cache as f16 hi/lo planes; three f16 passes per product)",
                               ap["launches"], ap["ms"] / max(1, ap["launches"]),
                               algorithmic_flops_per_step=att_flops),
         "kernel_ms_per_step": {c: round(p["ms"], 3) for c, p in prof.items()},
@@ -910,7 +910,7 @@ def main():
             "tokens_per_step": T,
             "seed": SEED,
             "precision": args.precision,
-            "arithmetic": ("f16 hi/lo split MFMA with f32 accumulation, exact Q8_0 block scaling, f32 KV cache"
+            "arithmetic": ("f16 hi/lo split MFMA with f32 accumulation, exact Q8_0 block scaling, KV cache as f16 hi/lo planes"
                            if prec == lh.PREC_EXACT else "f16 MFMA, f32 accumulation, f16 KV cache"),
         },
         "decide_req_per_s": round(REQUESTS * args.steps / dt, 2),

@@ -328,6 +328,14 @@ DevMatrix Engine::upload_matrix(const Gguf &g, const std::vector<std::string> &n
   return m;
 }
 
+void Engine::add_prefill_copy(DevMatrix &m) {
+  if (!split() || m.kind != LG_Q8_0 || m.cols % 32) return;
+  m.pc = static_cast<_Float16 *>(carve(size_t(m.rows) * m.cols * 2));
+  m.pcs = static_cast<float *>(carve(size_t(m.rows) * (m.cols / 32) * 4));
+  launch_q8x_prefill_copy(m, stream);
+  HIP_CHECK(hipStreamSynchronize(stream));
+}
+
 void Engine::upload(const Gguf &g) {
   // size the arena: every matrix/vector tensor except the embedding table, + 256 B slack each
   size_t total = 0;
@@ -338,6 +346,8 @@ void Engine::upload(const Gguf &g) {
     if (t.dims.size() == 1) need = n * 8;  // vectors: f32 copy, plus a fused-bias copy
     else if (t.name == "cos_full" || t.name == "sin_full") need = n * 4;
     else need = size_t(q_row_bytes(t.kind, int(t.cols())) + s_row_bytes(t.kind, int(t.cols()))) * t.rows();
+    if (split() && t.kind == LG_Q8_0 && t.dims.size() == 2 && t.name != "output.weight")
+      need += q8x_copy_bytes(int(t.rows()), int(t.cols())) + 512;
     total += align256(need) + 512;
   }
   arena_size_ = total;
@@ -414,6 +424,10 @@ void Engine::upload(const Gguf &g) {
     if (ly.wi.rows != 2 * f) fail(LG_ERR_FORMAT, "mlp_wi.%d.weight: unexpected matrix shape", l);
     ly.wd = upload_matrix(g, {"mlp_wo." + i + ".weight"}, f);
     if (ly.wd.rows != d) fail(LG_ERR_FORMAT, "mlp_wo.%d.weight: unexpected matrix shape", l);
+    for (ProjPart &p : ly.qkv) add_prefill_copy(p.w);
+    add_prefill_copy(ly.wo);
+    add_prefill_copy(ly.wi);
+    add_prefill_copy(ly.wd);
   }
   final_norm_ = upload_vector_f32(g, "final_norm.weight", d);
   head_ = upload_matrix(g, {"output.weight"}, d);

@@ -176,6 +176,8 @@ class Engine {
   void release();
   // pad_to > 0: rows rounded up to a multiple of pad_to with zero weights
   DevMatrix upload_matrix(const Gguf &g, const std::vector<std::string> &names, int cols, int pad_to = 0);
+  // exact mode, Q8_0: the f16-code / f32-scale copy the large-batch prefill GEMM reads
+  void add_prefill_copy(DevMatrix &m);
   // offset != 0: stores offset + w (the zero-centred RMSNorm weight)
   float *upload_vector_f32(const Gguf &g, const std::string &name, int64_t n, float offset = 0.0f);
   void *carve(size_t bytes);

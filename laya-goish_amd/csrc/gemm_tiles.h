@@ -606,4 +606,11 @@ bool launch_gemm_q8_exact(const _Float16 *A, const _Float16 *Alo, int M, const D
                           float *C, _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias,
                           hipStream_t st);
 
+// Exact Q8_0 GEMM on 256 x 256 tiles over the weight's prefill copy (gemm_q8x.h), for launches
+// with at least as many tiles as the device has CUs.  Same per-element operation order as
+// launch_gemm_q8_exact, so the two give the same bits.  Returns false (nothing launched) when
+// the matrix has no prefill copy or the shape or epilogue is not one it takes.
+bool launch_gemm_q8x(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
+                     _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st);
+
 }  // namespace lg

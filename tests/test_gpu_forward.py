@@ -9,8 +9,8 @@ checked as bit-exact properties of the GPU path.
 import numpy as np
 import pytest
 
-from parity import (assert_argmax_equal, assert_logits_close, assert_probs_close, logit_bar, logit_error,
-                    tie_window)
+from parity import (assert_argmax_equal, assert_bits_equal, assert_logits_close, assert_probs_close, logit_bar,
+                    logit_error, tie_window)
 
 pytestmark = pytest.mark.gpu
 
@@ -225,4 +225,30 @@ def test_q8_2048_full_width(lh, po, layers, tokens):
     perr = assert_probs_close(probs, p_ref)
     assert_argmax_equal(logits, want, rel=1e-3)
     print(f"q8-2048 L{layers} T{tokens}: logit rel {err:.2e} prob {perr:.2e}")
+    eng.close()
+
+
+def test_q8_large_batch_tiles_equal_single_requests(lh, po):
+    """Exact Q8_0 prefill GEMMs take 256 x 256 tiles over the weights' prefill copy once a launch has
+    at least one tile per CU, and 128 x 128 tiles below that.  Both must give the same bits: a batch of
+    16 x 512 tokens (every projection on the large tiles) equals each request run alone (small tiles),
+    and a request of the batch matches the oracle at the exact mode's bar."""
+    img = lh.SynthImage("q8-2048", seed=11, n_layers=2)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=16 * 576, max_batch_tokens=16 * 512)
+    rng = np.random.default_rng(7)
+    reqs = [(rng.integers(0, 32000, 512).astype(np.int32), [7, 100, 511]) for _ in range(16)]
+    opts = [5, 77, 901, 31999]
+    seqs = [eng.seq_create() for _ in reqs]
+    logits, _, _ = eng.batch([(s, ids, pos) for s, (ids, pos) in zip(seqs, reqs)]).run(opts)
+    for s in seqs:
+        eng.seq_free(s)
+    for r in (0, 9, 15):
+        s = eng.seq_create()
+        single = eng.forward(s, reqs[r][0], reqs[r][1], opts)
+        eng.seq_free(s)
+        assert_bits_equal(single, logits[3 * r:3 * r + 3])
+    om = po.Model(po.Gguf(img.array()), threads=16)
+    want = om.forward(reqs[9][0], reqs[9][1], opts)
+    err = assert_logits_close(logits[27:30], want, rel=logit_bar(0))
+    print(f"q8-2048 L2 16 x 512: bit-identical to single requests; logit rel {err:.2e} vs oracle")
     eng.close()
