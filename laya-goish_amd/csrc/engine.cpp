@@ -329,10 +329,22 @@ DevMatrix Engine::upload_matrix(const Gguf &g, const std::vector<std::string> &n
 }
 
 void Engine::add_prefill_copy(DevMatrix &m) {
-  if (!split() || m.kind != LG_Q8_0 || m.cols % 32) return;
-  m.pc = static_cast<_Float16 *>(carve(size_t(m.rows) * m.cols * 2));
-  m.pcs = static_cast<float *>(carve(size_t(m.rows) * (m.cols / 32) * 4));
-  launch_q8x_prefill_copy(m, stream);
+  if (!split()) return;
+  const size_t n = size_t(m.rows) * m.cols;
+  if (m.kind == LG_F16) {
+    m.pc = static_cast<_Float16 *>(m.q);
+    return;
+  }
+  if (m.kind == LG_Q8_0) {
+    m.pc = static_cast<_Float16 *>(carve(n * 2));
+    m.pcs = static_cast<float *>(carve(size_t(m.rows) * (m.cols / 32) * 4));
+  } else if (m.kind == LG_Q4_K || m.kind == LG_Q6_K) {
+    m.pc = static_cast<_Float16 *>(carve(n * 2));
+    m.pcl = static_cast<_Float16 *>(carve(n * 2));
+  } else {
+    return;
+  }
+  launch_prefill_copy(m, stream);
   HIP_CHECK(hipStreamSynchronize(stream));
 }
 
@@ -346,8 +358,8 @@ void Engine::upload(const Gguf &g) {
     if (t.dims.size() == 1) need = n * 8;  // vectors: f32 copy, plus a fused-bias copy
     else if (t.name == "cos_full" || t.name == "sin_full") need = n * 4;
     else need = size_t(q_row_bytes(t.kind, int(t.cols())) + s_row_bytes(t.kind, int(t.cols()))) * t.rows();
-    if (split() && t.kind == LG_Q8_0 && t.dims.size() == 2 && t.name != "output.weight")
-      need += q8x_copy_bytes(int(t.rows()), int(t.cols())) + 512;
+    if (split() && t.dims.size() == 2 && t.name != "output.weight")
+      need += prefill_copy_bytes(t.kind, int(t.rows()), int(t.cols())) + 512;
     total += align256(need) + 512;
   }
   arena_size_ = total;

@@ -180,7 +180,7 @@ struct BLoad {
       } else if constexpr (KIND == LG_Q6_K) {
         float f[16];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) f[j] = sa[i] * float(int8_t(w[j / 4] >> (8 * (j % 4))));
+        for (int j = 0; j < 16; ++j) f[j] = kq6_weight(sa[i], int8_t(w[j / 4] >> (8 * (j % 4))));
         put8(f, Bs + r * LDK + c * 16, Bl + r * LDK + c * 16, kSplitB);
         put8(f + 8, Bs + r * LDK + c * 16 + 8, Bl + r * LDK + c * 16 + 8, kSplitB);
       } else {  // Q4_K
@@ -189,10 +189,10 @@ struct BLoad {
         for (int j = 0; j < 16; ++j) {
           const uint32_t byte = (w[j / 4] >> (8 * (j % 4))) & 0xffu;
           if constexpr (BK == 64) {
-            lo[j] = sa[i] * float(byte & 15u) - sb[i];
-            hi[j] = sa2[i] * float(byte >> 4) - sb2[i];
+            lo[j] = kq4_weight(sa[i], byte & 15u, sb[i]);
+            hi[j] = kq4_weight(sa2[i], byte >> 4, sb2[i]);
           } else {
-            lo[j] = sa[i] * float(plane ? (byte >> 4) : (byte & 15u)) - sb[i];
+            lo[j] = kq4_weight(sa[i], plane ? (byte >> 4) : (byte & 15u), sb[i]);
           }
         }
         put8(lo, Bs + r * LDK + c * 16, Bl + r * LDK + c * 16, kSplitB);
@@ -606,11 +606,12 @@ bool launch_gemm_q8_exact(const _Float16 *A, const _Float16 *Alo, int M, const D
                           float *C, _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias,
                           hipStream_t st);
 
-// Exact Q8_0 GEMM on 256 x 256 tiles over the weight's prefill copy (gemm_q8x.h), for launches
-// with at least as many tiles as the device has CUs.  Same per-element operation order as
-// launch_gemm_q8_exact, so the two give the same bits.  Returns false (nothing launched) when
-// the matrix has no prefill copy or the shape or epilogue is not one it takes.
-bool launch_gemm_q8x(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
-                     _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st);
+// Exact GEMM on 256 x 256 tiles over the weight's prefill copy (gemm_wide.h: Q8_0, F16, Q4_K,
+// Q6_K), for launches with at least as many tiles as the device has CUs.  Same per-element
+// operation order as the exact 128 x 128 tiles, so the two give the same bits.  Returns false
+// (nothing launched) when the matrix has no prefill copy or the shape or epilogue is not one it
+// takes.
+bool launch_gemm_wide(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
+                      _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st);
 
 }  // namespace lg

@@ -1,0 +1,263 @@
+// Exact prefill GEMM for large batches (gfx950): C = A . W^T with A given as f16 hi/lo planes
+// and W read from its prefill copy (DevMatrix::pc, pcl, pcs), written once at upload so that
+// every operand byte reaches LDS by LDS-DMA (buffer_load ... lds, 16 bytes a lane) with no
+// register staging and no conversion.  Three weight forms (MODE):
+//   WQ8: Q8_0 -- codes as f16 (exact) [N][K] and block scales as f32 [K/32][N].  Per 32 x 32
+//        output block and Q8_0 block the partial sum is one chain of four MFMAs (A hi and lo
+//        against the codes, two 16-deep k halves), then acc += d * partial in f32.
+//   W1 : F16 weights [N][K] (the weights themselves, no copy): per 16-deep k chunk
+//        acc += A_hi . W, then acc += A_lo . W.
+//   W2 : Q4_K / Q6_K -- the dequantised f32 weight split into f16 hi and lo planes [N][K]:
+//        per 16-deep k chunk acc += A_hi . W_hi, A_lo . W_hi, A_hi . W_lo.
+// Each mode keeps the per-element operation order of the 128 x 128 tiles in gemm_tiles.h, so
+// both give the same bits (all on v_mfma_f32_32x32x16_f16 with f32 accumulation).
+//
+// Geometry: 512 threads = 8 wave64s (2 per SIMD), workgroup tile 256 x 256, K steps of 32.
+// WQ8 and W1 keep three LDS stages (stage k + 2 in flight while stage k is consumed), W2 two
+// (its stage holds four planes); one barrier per step.  Wave w owns rows 64 (w / 2) .. + 64
+// and columns 128 (w % 2) .. + 128 of the tile (2 x 4 MFMA blocks).
+//
+// LDS rows are 64 bytes (four 16-byte chunks); logical chunk c of row r sits in slot
+// c ^ ((r >> 2) & 3), so the 16 lanes of each quarter of an operand read fall in 16 distinct
+// 16-byte bank groups.  The DMA side writes whole 1 KiB blocks: lane L of a block fetches the
+// global chunk that belongs in its slot.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+#include "f16split.h"
+#include "kernels.h"
+
+namespace lg {
+namespace wide {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+enum Mode { WQ8 = 0, W1 = 1, W2 = 2 };
+
+constexpr int BM = 256, BN = 256, BK = 32, WAVES = 8, THREADS = 64 * WAVES;
+constexpr int ROWB = BK * 2;      // bytes per LDS row of one plane
+constexpr int PLANE = BM * ROWB;  // 16 KiB
+static_assert(BM == BN, "A and B planes share one slot layout");
+static_assert(PLANE / 1024 == 2 * WAVES, "two 1 KiB blocks of each plane per wave");
+
+template <int MODE>
+struct Geo {
+  static constexpr int kBPlanes = MODE == W2 ? 2 : 1;
+  static constexpr bool kScales = MODE == WQ8;
+  static constexpr int kAHi = 0, kALo = PLANE, kBHi = 2 * PLANE, kBLo = 3 * PLANE;
+  static constexpr int kScl = (2 + kBPlanes) * PLANE;
+  static constexpr int kStageBytes = kScl + (kScales ? BN * 4 : 0);
+  static constexpr int kStages = MODE == W2 ? 2 : 3;
+  static constexpr int kLdsBytes = kStages * kStageBytes;  // WQ8 150,528; W1 147,456; W2 131,072
+  static constexpr int kDmaPerWave = 2 * (2 + kBPlanes);   // per stage (wave 0: + 1 scale block)
+};
+
+__device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
+
+#define WIDE_MFMA(a, b, c) __builtin_amdgcn_mfma_f32_32x32x16_f16((a), (b), (c), 0, 0, 0)
+
+__device__ __forceinline__ float silu_f(float g) { return g * (1.0f / (1.0f + __expf(-g))); }
+
+// EPI: Epi values (F32, ADD, SWIGLU).  For SWIGLU the workgroup's 256 weight rows are 128 gate
+// rows and the 128 matching up rows: wave column wn holds gate rows in its blocks 0, 1 and the
+// up rows of the same output columns in blocks 2, 3.
+template <int EPI, int MODE>
+__global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
+    const _Float16 *__restrict__ A, const _Float16 *__restrict__ Alo, int M, int K,
+    const _Float16 *__restrict__ Wh, const _Float16 *__restrict__ Wl, const float *__restrict__ Ws, int N,
+    float *__restrict__ C, _Float16 *__restrict__ C16, _Float16 *__restrict__ C16lo, int ldc,
+    const float *__restrict__ bias, int MT, int NT, int ffn) {
+  using G = Geo<MODE>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr bool kGlu = EPI == int(Epi::SWIGLU);
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: scalar DMA setup
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // tile order: consecutive workgroups go to the 8 XCDs round-robin; each XCD takes a
+  // contiguous range of tiles, walked in groups of 4 M-tiles so that the concurrently
+  // resident tiles of one XCD share A rows and weight rows through its L2
+  int mt, nt;
+  {
+    const int nblk = gridDim.x;
+    int id = blockIdx.x;
+    if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);
+    constexpr int GM = 4;
+    const int group = id / (GM * NT), first = group * GM;
+    const int gm = min(MT - first, GM), in = id - group * GM * NT;
+    mt = first + in % gm;
+    nt = in / gm;
+  }
+  const int m0 = mt * BM;
+
+  // weight row of local B row r
+  auto wrow = [&](int r) -> int {
+    if constexpr (kGlu) {
+      const int wc = r >> 7, jb = (r >> 5) & 3, up = jb >> 1, jj = jb & 1;
+      return up * ffn + nt * (BN / 2) + wc * 64 + jj * 32 + (r & 31);
+    } else {
+      return nt * BN + r;
+    }
+  };
+
+  // DMA: wave w issues blocks w and w + 8 of each plane (A hi, A lo, W hi, W lo) and wave 0
+  // also the scale block.  Rows past M sit past the end of the A buffers: the buffer unit
+  // answers them with zeros.
+  const uint32_t abytes = uint32_t(M) * uint32_t(K) * 2u, wbytes = uint32_t(N) * uint32_t(K) * 2u;
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(A), 0, abytes, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(Alo), 0, abytes, kBufferFlags);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(Wh), 0, wbytes, kBufferFlags);
+  __amdgpu_buffer_rsrc_t rc = rb, rs = rb;
+  if constexpr (MODE == W2) rc = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(Wl), 0, wbytes, kBufferFlags);
+  if constexpr (MODE == WQ8)
+    rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(Ws), 0, uint32_t(N) * uint32_t(K / 32) * 4u, kBufferFlags);
+  uint32_t aoff[2], boff[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int slot = (wave + WAVES * h) * 64 + lane;  // 16-byte slot inside a plane
+    const int row = slot >> 2, c = (slot & 3) ^ swz(row);
+    aoff[h] = uint32_t(m0 + row) * uint32_t(K) * 2u + uint32_t(c) * 16u;
+    boff[h] = uint32_t(wrow(row)) * uint32_t(K) * 2u + uint32_t(c) * 16u;
+  }
+  const uint32_t soff = uint32_t(wrow(4 * lane)) * 4u;  // four consecutive weight rows' scales
+  const int nk = K / BK;
+  auto issue = [&](int kt, int st) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    // device pass only: with a run-time voffset this builtin keeps the host pass from
+    // emitting the kernel's launch stub (the host never runs kernel bodies)
+    typedef __attribute__((address_space(3))) void *lds_ptr;
+    uint8_t *base = lds + st * G::kStageBytes;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int blk = (wave + WAVES * h) * 1024;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr)(base + G::kAHi + blk), 16, aoff[h], kt * BK * 2, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, (lds_ptr)(base + G::kALo + blk), 16, aoff[h], kt * BK * 2, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr)(base + G::kBHi + blk), 16, boff[h], kt * BK * 2, 0, 0);
+      if constexpr (MODE == W2)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (lds_ptr)(base + G::kBLo + blk), 16, boff[h], kt * BK * 2, 0, 0);
+    }
+    if constexpr (MODE == WQ8)
+      if (wave == 0) __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(base + G::kScl), 16, soff, kt * N * 4, 0, 0);
+#endif
+  };
+
+  f32x16 acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  // operand read offsets: row (lane & 31) of each 32-row block, chunk 2 kk + (lane >> 5)
+  const int lr = lane & 31, sw = swz(lr);
+  const int ac0 = (wm * 64 + lr) * ROWB, bc0 = (wn * 128 + lr) * ROWB;
+  const int ch0 = ((0 + (lane >> 5)) ^ sw) * 16, ch1 = ((2 + (lane >> 5)) ^ sw) * 16;
+  const f32x16 zero = {};
+
+#pragma unroll
+  for (int s = 0; s < G::kStages - 1; ++s)
+    if (s < nk) issue(s, s);
+  for (int kt = 0; kt < nk; ++kt) {
+    // wait for this wave's part of stage kt; with three stages, stage kt + 1 stays in flight
+    if (G::kStages == 3 && kt + 1 < nk)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(G::kDmaPerWave) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // every wave has its part of stage kt in LDS and is done reading stage kt - 1; a bare
+    // barrier (no fence), so the DMA issued below stays in flight across the next one
+    asm volatile("s_barrier" ::: "memory");
+    if (kt + G::kStages - 1 < nk) issue(kt + G::kStages - 1, (kt + G::kStages - 1) % G::kStages);
+    const uint8_t *st = lds + (kt % G::kStages) * G::kStageBytes;
+    half8 ah[2][2], al[2][2], b[2][4], c[2][4];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int ch = kk ? ch1 : ch0;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        ah[kk][i] = *reinterpret_cast<const half8 *>(st + G::kAHi + ac0 + i * 32 * ROWB + ch);
+        al[kk][i] = *reinterpret_cast<const half8 *>(st + G::kALo + ac0 + i * 32 * ROWB + ch);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        b[kk][j] = *reinterpret_cast<const half8 *>(st + G::kBHi + bc0 + j * 32 * ROWB + ch);
+        if constexpr (MODE == W2) c[kk][j] = *reinterpret_cast<const half8 *>(st + G::kBLo + bc0 + j * 32 * ROWB + ch);
+      }
+    }
+    if constexpr (MODE == WQ8) {
+      float d[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) d[j] = *reinterpret_cast<const float *>(st + G::kScl + (wn * 128 + j * 32 + lr) * 4);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          f32x16 p = WIDE_MFMA(ah[0][i], b[0][j], zero);
+          p = WIDE_MFMA(al[0][i], b[0][j], p);
+          p = WIDE_MFMA(ah[1][i], b[1][j], p);
+          p = WIDE_MFMA(al[1][i], b[1][j], p);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][j][r] += d[j] * p[r];
+        }
+    } else {
+      // per element: for each 16-deep chunk kk, A_hi.W_hi, A_lo.W_hi (, A_hi.W_lo); the
+      // eight blocks of a wave interleave, so no MFMA waits on the one before it
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = WIDE_MFMA(ah[kk][i], b[kk][j], acc[i][j]);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = WIDE_MFMA(al[kk][i], b[kk][j], acc[i][j]);
+        if constexpr (MODE == W2) {
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = WIDE_MFMA(ah[kk][i], c[kk][j], acc[i][j]);
+        }
+      }
+    }
+  }
+
+  // epilogue: acc[i][j] register r -> row (r/4)*8 + (lane/32)*4 + r%4, column lane%32
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+      if (row >= M) continue;
+      if constexpr (kGlu) {
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          const int col = nt * (BN / 2) + wn * 64 + jj * 32 + lr;
+          const float v = silu_f(acc[i][jj][r]) * acc[i][jj + 2][r];
+          _Float16 h, hl;
+          split_f16(v, h, hl);
+          C16[int64_t(row) * ldc + col] = h;
+          if (C16lo) C16lo[int64_t(row) * ldc + col] = hl;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int col = nt * BN + wn * 128 + j * 32 + lr;
+          float v = acc[i][j][r];
+          if (bias) v += bias[col];
+          if constexpr (EPI == int(Epi::F32)) {
+            C[int64_t(row) * ldc + col] = v;
+          } else {
+            C[int64_t(row) * ldc + col] += v;
+          }
+        }
+      }
+    }
+  }
+}
+#undef WIDE_MFMA
+
+}  // namespace wide
+}  // namespace lg

@@ -13,8 +13,9 @@ void launch_kind(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix 
   if (!Alo) {
     if (launch_cfg<KIND, FAST, 64, 4, 4, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
     if (launch_cfg<KIND, FAST, 64, 2, 2, 2>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
+  } else if (launch_gemm_wide(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) {
+    return;
   } else if constexpr (KIND == LG_Q8_0) {
-    if (launch_gemm_q8x(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
     if (launch_gemm_q8_exact(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
   } else if constexpr (KIND == LG_F16) {
     // fewer 128 x 128 tiles than CUs (short prefills, narrow outputs): 64 x 128 tiles, twice

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include "common.h"
+#include "f16split.h"
 #include "kernels.h"
 #include "quant.h"
 
@@ -117,6 +118,19 @@ __global__ void repack_q6k(const uint8_t *__restrict__ src, uint64_t nblocks, in
 }
 
 // f32 weight from the repacked layout -- the arithmetic the GEMV kernels use.
+// Q4_K / Q6_K weight (n, k) of the repacked layout.
+__device__ __forceinline__ float kquant_weight(const DevMatrix &W, uint64_t n, uint64_t k) {
+  const uint64_t cols = uint64_t(W.cols);
+  if (W.kind == LG_Q4_K) {
+    const uint8_t byte = static_cast<const uint8_t *>(W.q)[n * (cols / 2) + (k / 64) * 32 + (k % 32)];
+    const uint32_t nib = (k % 64) >= 32 ? (byte >> 4) : (byte & 15u);
+    const float2 ab = static_cast<const float2 *>(W.s)[n * (cols / 32) + k / 32];
+    return kq4_weight(ab.x, nib, ab.y);
+  }
+  return kq6_weight(static_cast<const float *>(W.s)[n * (cols / 16) + k / 16],
+                    static_cast<const int8_t *>(W.q)[n * cols + k]);
+}
+
 __global__ void dequant_repacked(DevMatrix W, float *__restrict__ dst) {
   const uint64_t e = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   const uint64_t cols = uint64_t(W.cols);
@@ -130,18 +144,36 @@ __global__ void dequant_repacked(DevMatrix W, float *__restrict__ dst) {
       v = __fmul_rn(half_bits(static_cast<const uint16_t *>(W.s)[n * (cols / 32) + k / 32]),
                     float(static_cast<const int8_t *>(W.q)[e]));
       break;
-    case LG_Q4_K: {
-      const uint8_t byte = static_cast<const uint8_t *>(W.q)[n * (cols / 2) + (k / 64) * 32 + (k % 32)];
-      const uint32_t nib = (k % 64) >= 32 ? (byte >> 4) : (byte & 15u);
-      const float2 ab = static_cast<const float2 *>(W.s)[n * (cols / 32) + k / 32];
-      v = __fsub_rn(__fmul_rn(ab.x, float(nib)), ab.y);
-    } break;
-    case LG_Q6_K:
-      v = __fmul_rn(static_cast<const float *>(W.s)[n * (cols / 16) + k / 16],
-                    float(static_cast<const int8_t *>(W.q)[e]));
-      break;
+    case LG_Q4_K:
+    case LG_Q6_K: v = kquant_weight(W, n, k); break;
   }
   dst[e] = v;
+}
+
+// Prefill copy of a K-quant matrix: the weight split into f16 hi / lo planes, one element each.
+__global__ void split_planes_kernel(DevMatrix W, _Float16 *__restrict__ hi, _Float16 *__restrict__ lo) {
+  const uint64_t e = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const uint64_t cols = uint64_t(W.cols);
+  if (e >= uint64_t(W.rows) * cols) return;
+  _Float16 h, l;
+  split_f16(kquant_weight(W, e / cols, e % cols), h, l);
+  hi[e] = h;
+  lo[e] = l;
+}
+
+// Prefill copy of a Q8_0 matrix: codes [rows][cols] int8 -> f16, scales [rows][cols/32] f16 -> f32
+// transposed to [cols/32][rows].  One 32-element block per thread.
+__global__ void q8_prefill_copy_kernel(const int8_t *__restrict__ q, const uint16_t *__restrict__ s, int rows,
+                                       int cols, _Float16 *__restrict__ codes, float *__restrict__ scales) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int nb = cols / 32;
+  if (i >= int64_t(rows) * nb) return;
+  const int n = int(i / nb), kb = int(i % nb);
+  const int8_t *src = q + int64_t(n) * cols + kb * 32;
+  _Float16 *dst = codes + int64_t(n) * cols + kb * 32;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) dst[e] = _Float16(float(src[e]));
+  scales[int64_t(kb) * rows + n] = half_bits(s[i]);
 }
 
 inline unsigned grid_for(uint64_t n, unsigned block) { return unsigned((n + block - 1) / block); }
@@ -194,6 +226,36 @@ void launch_repack(uint32_t kind, const uint8_t *src, int rows, int cols, DevMat
       break;
     default:
       fail(LG_ERR_UNSUPPORTED, "no device layout for GGML tensor type %u", kind);
+  }
+  HIP_CHECK(hipGetLastError());
+}
+
+size_t prefill_copy_bytes(uint32_t kind, int rows, int cols) {
+  const size_t n = size_t(rows) * size_t(cols);
+  switch (kind) {
+    case LG_Q8_0: return n * 2 + size_t(rows) * size_t(cols / 32) * 4;
+    case LG_Q4_K:
+    case LG_Q6_K: return n * 4;
+  }
+  return 0;
+}
+
+void launch_prefill_copy(const DevMatrix &w, hipStream_t st) {
+  const int64_t n = int64_t(w.rows) * w.cols;
+  LG_REQUIRE(w.rows > 0 && w.cols > 0 && w.pc, "prefill copy: bad matrix");
+  if (w.kind == LG_Q8_0) {
+    LG_REQUIRE(w.pcs && w.cols % 32 == 0, "prefill copy: Q8_0 needs scales and whole blocks");
+    const int64_t blocks = n / 32;
+    LG_REQUIRE((blocks + 255) / 256 < (int64_t(1) << 31), "prefill copy: matrix too large");
+    hipLaunchKernelGGL(q8_prefill_copy_kernel, dim3(unsigned((blocks + 255) / 256)), dim3(256), 0, st,
+                       static_cast<const int8_t *>(w.q), static_cast<const uint16_t *>(w.s), w.rows, w.cols, w.pc,
+                       w.pcs);
+  } else if (w.kind == LG_Q4_K || w.kind == LG_Q6_K) {
+    LG_REQUIRE(w.pcl && w.cols % 256 == 0, "prefill copy: K-quant needs both planes and whole super-blocks");
+    LG_REQUIRE((n + 255) / 256 < (int64_t(1) << 31), "prefill copy: matrix too large");
+    hipLaunchKernelGGL(split_planes_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, w, w.pc, w.pcl);
+  } else {
+    fail(LG_ERR_UNSUPPORTED, "prefill copy: GGML type %u has none", w.kind);
   }
   HIP_CHECK(hipGetLastError());
 }

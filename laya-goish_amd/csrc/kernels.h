@@ -42,10 +42,13 @@ struct DevMatrix {
   int rows = 0, cols = 0;
   void *q = nullptr;
   void *s = nullptr;
-  // Q8_0 prefill copy (exact-mode decoder matrices, written once at upload; null otherwise):
-  // pc = codes as f16 [rows][cols], pcs = block scales as f32 [cols/32][rows].  The large-batch
-  // GEMM (gemm_q8x.h) moves these bytes to LDS by DMA with no conversion on the way.
+  // Prefill copy (exact-mode decoder matrices, set once at upload; null otherwise), the operand
+  // form the large-batch GEMM (gemm_wide.h) moves to LDS by DMA with no conversion on the way:
+  //   Q8_0 : pc = codes as f16 [rows][cols], pcs = block scales as f32 [cols/32][rows]
+  //   F16  : pc = q (the weights themselves; no copy)
+  //   Q4_K, Q6_K: pc / pcl = f16 hi / lo planes [rows][cols] of the dequantised f32 weight
   _Float16 *pc = nullptr;
+  _Float16 *pcl = nullptr;
   float *pcs = nullptr;
   int64_t bytes() const;  // HBM bytes of q + s
   int64_t gguf_bytes() const;  // bytes of the same matrix in GGUF blocks
@@ -68,10 +71,12 @@ void launch_dequant(uint32_t kind, const uint8_t *src, uint64_t nblocks, float *
 void launch_repack(uint32_t kind, const uint8_t *src, int rows, int cols, DevMatrix &w,
                    hipStream_t st);
 
-// Q8_0 prefill copy (DevMatrix::pc, pcs) of a repacked Q8_0 matrix: device bytes it needs, and
-// the conversion from w.q / w.s into the buffers w.pc / w.pcs already point at.
-size_t q8x_copy_bytes(int rows, int cols);
-void launch_q8x_prefill_copy(const DevMatrix &w, hipStream_t st);
+// Prefill copy (DevMatrix::pc, pcl, pcs) of a repacked Q8_0 / Q4_K / Q6_K matrix: device bytes
+// it needs (0 for kinds that need none), and the conversion from w.q / w.s into the buffers
+// w.pc, w.pcl, w.pcs already point at.  The K-quant planes split the weight exactly as the
+// exact-mode GEMM tiles do (gemm_tiles.h), so both GEMMs see the same operand bits.
+size_t prefill_copy_bytes(uint32_t kind, int rows, int cols);
+void launch_prefill_copy(const DevMatrix &w, hipStream_t st);
 
 // Prefill GEMM: out = A[M][K] (half, row-major, lda = K) . W^T with epilogue `epi`.
 // A_lo == nullptr: one f16 pass.  A_lo != nullptr: A = A + A_lo (hi/lo f16 planes) and the
