@@ -255,7 +255,7 @@ __device__ float weight_at_gemv(const DevMatrix &W, int64_t n, int64_t k) {
       const uint8_t byte = static_cast<const uint8_t *>(W.q)[n * (cols / 2) + (k / 64) * 32 + (k % 32)];
       const uint32_t nib = (k % 64) >= 32 ? (byte >> 4) : (byte & 15u);
       const float2 ab = static_cast<const float2 *>(W.s)[n * (cols / 32) + k / 32];
-      return ab.x * float(nib) - ab.y;
+      return kq4_weight(ab.x, nib, ab.y);
     }
   }
   return 0.0f;
