@@ -312,6 +312,14 @@ def cpu_layer_cost_7b(args, po):
     return cost
 
 
+def load_entry(eng):
+    """Engine load (lg_engine_create: streamed upload, repack, prefill copies, KV pool) of a model."""
+    info = eng.info
+    sec = info["load_seconds"]
+    return {"seconds": round(sec, 3), "gguf_bytes": info["weight_bytes"],
+            "GB_per_s": round(info["weight_bytes"] / sec / 1e9, 2) if sec > 0 else None}
+
+
 def c4_q4k(args, prec, layer_cost):
     """Q4_K/Q6_K 7B shape (28 layers, d3584, GQA 28/4 x 128, FFN 18944, vocab 152064, QKV bias):
     a batch of 32 requests x 1024 tokens, 4 option tokens scored at the last position."""
@@ -319,7 +327,9 @@ def c4_q4k(args, prec, layer_cost):
     img = lh.SynthImage("q4km-7b", seed=SEED)
     eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=Q4K_REQS * Q4K_TOKENS + 1024, max_batch_tokens=32768,
                     precision=prec)
-    log(f"C4 model ready in {time.perf_counter() - t0:.1f}s")
+    load = load_entry(eng)
+    log(f"C4 model ready in {time.perf_counter() - t0:.1f}s (engine load {load['seconds']} s, "
+        f"{load['GB_per_s']} GB/s of GGUF weights)")
     rng = np.random.default_rng(SEED + 3)
     reqs = [(rng.integers(0, 152064, Q4K_TOKENS).astype(np.int32), np.array([Q4K_TOKENS - 1], np.int32))
             for _ in range(Q4K_REQS)]
@@ -354,10 +364,10 @@ def c4_q4k(args, prec, layer_cost):
                     "152064, QKV bias; Q4_K q/k/o/gate/up, Q6_K v/down/output; 32 requests x 1024 tokens, 4 option "
                     "tokens at the last position",
         "value": round(T / dt, 1), "unit": "tok/s", "higher_is_better": True, "steps": steps, "warmup": warm,
-        "ms_per_step": round(dt * 1e3, 2), "req_per_s": round(Q4K_REQS / dt, 2),
+        "ms_per_step": round(dt * 1e3, 2), "req_per_s": round(Q4K_REQS / dt, 2), "load": load,
         "roofline": roofline("mfma", rate(gp, "flops"), PEAK_F16_TFLOPS, "TFLOP/s",
-                             "gemm (dequant-fused K-quant MFMA GEMM; three f16 passes per product, so the "
-                             "arithmetic ceiling is a third of the f16 rate)", gp["launches"],
+                             "gemm (exact K-quant MFMA GEMM over f16 hi/lo weight planes; three f16 passes per "
+                             "product, so the arithmetic ceiling is a third of the f16 rate)", gp["launches"],
                              gp["ms"] / max(1, gp["launches"])),
         "kernel_ms_per_step": {c: round(p["ms"], 3) for c, p in prof.items()},
     }
@@ -381,7 +391,9 @@ def c5_long_context(args, prec, layer_cost):
     img = lh.SynthImage("f16-7b", seed=SEED)
     eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=C5_PREFIX + C5_REQS * C5_OWN + 2048, max_batch_tokens=32768,
                     precision=prec)
-    log(f"C5 model ready in {time.perf_counter() - t0:.1f}s")
+    load = load_entry(eng)
+    log(f"C5 model ready in {time.perf_counter() - t0:.1f}s (engine load {load['seconds']} s, "
+        f"{load['GB_per_s']} GB/s of GGUF weights)")
     rng = np.random.default_rng(SEED + 4)
     prefix = rng.integers(0, 152064, C5_PREFIX).astype(np.int32)
     own = [rng.integers(0, 152064, C5_OWN).astype(np.int32) for _ in range(C5_REQS)]
@@ -432,7 +444,7 @@ def c5_long_context(args, prec, layer_cost):
                     "forked), 8 answer positions per request, 4 option tokens each",
         "value": round(C5_REQS / dt, 3), "unit": "req/s", "higher_is_better": True, "steps": steps, "warmup": warm,
         "ms_per_step": round(dt * 1e3, 2), "context_tok_per_s": round(C5_REQS * 8192 / dt, 1),
-        "computed_tok_per_s": round(computed / dt, 1),
+        "computed_tok_per_s": round(computed / dt, 1), "load": load,
         "roofline": roofline("mfma", rate(gp, "flops"), PEAK_F16_TFLOPS, "TFLOP/s",
                              "gemm (F16 weights, hi/lo split activations: two f16 passes per product)",
                              gp["launches"], gp["ms"] / max(1, gp["launches"])),
@@ -914,7 +926,8 @@ def main():
                            if prec == lh.PREC_EXACT else "f16 MFMA, f32 accumulation, f16 KV cache"),
         },
         "decide_req_per_s": round(REQUESTS * args.steps / dt, 2),
-        "roofline": roofline("mfma", gemm_tflops, PEAK_F16_TFLOPS, "TFLOP/s", "gemm (dequant-fused Q8_0 MFMA GEMM)",
+        "roofline": roofline("mfma", gemm_tflops, PEAK_F16_TFLOPS, "TFLOP/s",
+                             "gemm (exact Q8_0 MFMA GEMM: f16 codes and block scales, two f16 passes per product)",
                              gp["launches"], gp["ms"] / max(1, gp["launches"]), measured_traffic("gemm"),
                              traffic_source="profiles/hbm_traffic_q8-2048_bench.md (FETCH_SIZE + WRITE_SIZE, "
                                             "copy-calibrated)",

@@ -114,10 +114,11 @@ typedef struct {
   int64_t kv_bytes;        /* HBM bytes of the KV page pool */
   int kv_pages, kv_page_tokens;
   int precision;           /* LG_PREC_* the engine was created with */
-  int kv_elem_bytes;       /* 4 (f32 cache) or 2 (f16 cache) */
+  int kv_elem_bytes;       /* 4 (f16 hi + lo planes, exact mode) or 2 (f16, fast mode) */
   int arch;                /* LG_ARCH_* */
   int linear_heads;        /* OpenThai: gated DeltaNet heads (128-dim); 0 otherwise */
   int full_layers;         /* OpenThai: full-attention layers (the rest are DeltaNet) */
+  double load_seconds;     /* wall time of lg_engine_create: upload, repack, prefill copies, KV pool */
 } lg_model_info;
 
 /* Model families (general.architecture): "ggmlc" + laya.model_name "laya-decoder", the
@@ -126,6 +127,28 @@ typedef struct {
 #define LG_ARCH_LAYA_DECODER 0
 #define LG_ARCH_OPENTHAI 1
 #define LG_ARCH_LAYA 2
+
+/* ---- model description and registry preflight (host only; no weight is read) ---- */
+typedef struct {
+  char name[128];          /* the registry name: "openthai-systemone", laya.model_name, or the decoder's general.name */
+  char family[64];
+  char architecture[64];   /* general.architecture */
+  char aliases[4][64];
+  int n_aliases;
+  char release_date[16];   /* "" for the decoder family */
+} lg_model_desc;
+
+/* Replaces models::describe, src/models/mod.rs:32-64 ("ggmlc" Laya encoders and
+ * "openthai_systemone"), plus this build's decoder family ("ggmlc" with laya.model_name
+ * "laya-decoder", which the reference does not load: named by its general.name, no aliases).
+ * Errors (LG_ERR_FORMAT): "unsupported ggmlc model X", "unsupported GGUF architecture X". */
+int lg_model_describe(const lg_gguf *g, lg_model_desc *out);
+
+/* Replaces the preflight of Registry::load, src/registry.rs:16-39, run before any weights
+ * load: every path is opened (header and tensor table) and described, and an empty list, a
+ * name or alias used twice and an unknown default are refused with the reference's messages.
+ * On success *default_index is the default model's index (0 when default_name is NULL). */
+int lg_registry_preflight(const char *const *paths, int n, const char *default_name, int *default_index);
 
 /* Load a laya-decoder GGUF onto one GPU: validate, upload and repack every matrix into a
  * hipMalloc'd weight arena, reserve the KV page pool, create the engine's stream.

@@ -8,6 +8,7 @@
 #include <cstring>
 #include <new>
 #include <string>
+#include <vector>
 
 #include "common.h"
 #include "decide.h"
@@ -15,6 +16,7 @@
 #include "gguf.h"
 #include "kernels.h"
 #include "lg.h"
+#include "registry.h"
 
 namespace lg {
 void synth_image(const char *preset, uint64_t seed, int n_layers, uint8_t **out, uint64_t *out_len);
@@ -217,6 +219,38 @@ int lg_synth_gguf_file(const char *preset, uint64_t seed, int n_layers, const ch
 }
 
 void lg_synth_free(void *image) { std::free(image); }
+
+int lg_model_describe(const lg_gguf *g, lg_model_desc *out) {
+  return guard([&] {
+    NEED(g, "gguf");
+    NEED(out, "out");
+    const lg::ModelDesc d = lg::describe(*g->g);
+    lg_model_desc r{};
+    auto put = [](char *dst, size_t cap, const std::string &v) {
+      if (v.size() >= cap) ::lg::fail(LG_ERR_FORMAT, "model name %s is too long", v.c_str());
+      std::memcpy(dst, v.c_str(), v.size() + 1);
+    };
+    put(r.name, sizeof(r.name), d.name);
+    put(r.family, sizeof(r.family), d.family);
+    put(r.architecture, sizeof(r.architecture), d.architecture);
+    put(r.release_date, sizeof(r.release_date), d.release_date);
+    for (const std::string &a : d.aliases) put(r.aliases[r.n_aliases++], sizeof(r.aliases[0]), a);
+    *out = r;
+  });
+}
+
+int lg_registry_preflight(const char *const *paths, int n, const char *default_name, int *default_index) {
+  return guard([&] {
+    NEED(default_index, "default_index");
+    LG_REQUIRE(n >= 0 && (n == 0 || paths), "registry: bad path list");
+    std::vector<std::string> ps;
+    for (int i = 0; i < n; ++i) {
+      NEED(paths[i], "path");
+      ps.emplace_back(paths[i]);
+    }
+    *default_index = lg::registry_preflight(ps, default_name);
+  });
+}
 
 int lg_engine_create(const lg_gguf *g, const lg_engine_opts *opts, lg_engine **out) {
   return guard([&] {

@@ -2,6 +2,7 @@
 #include "engine.h"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstring>
 #include <numeric>
@@ -158,8 +159,84 @@ DevMatrix sub_rows(const DevMatrix &m, int row0, int nrows) {
 }
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
+// ------------------------------------------------------------------ streamed upload
+Uploader::Uploader(hipStream_t st) : st_(st) {
+  for (int i = 0; i < 2; ++i) {
+    if (hipHostMalloc(&host_[i], kChunk, hipHostMallocDefault) != hipSuccess) {
+      host_[i] = nullptr;
+      (void)hipGetLastError();
+      fail(LG_ERR_OOM, "cannot allocate %zu bytes of pinned upload staging", kChunk);
+    }
+    if (hipMalloc(&dev_[i], kChunk) != hipSuccess) {
+      dev_[i] = nullptr;
+      (void)hipGetLastError();
+      fail(LG_ERR_OOM, "cannot allocate %zu bytes of upload staging", kChunk);
+    }
+    HIP_CHECK(hipEventCreateWithFlags(&done_[i], hipEventDisableTiming));
+  }
+}
+
+Uploader::~Uploader() {
+  if (st_) (void)hipStreamSynchronize(st_);
+  for (int i = 0; i < 2; ++i) {
+    if (done_[i]) (void)hipEventDestroy(done_[i]);
+    if (host_[i]) (void)hipHostFree(host_[i]);
+    if (dev_[i]) (void)hipFree(dev_[i]);
+  }
+}
+
+int Uploader::take() {
+  const int s = next_;
+  next_ ^= 1;
+  if (used_[s]) HIP_CHECK(hipEventSynchronize(done_[s]));
+  used_[s] = true;
+  return s;
+}
+
+void Uploader::bytes(const uint8_t *src, size_t n, void *dst) {
+  for (size_t off = 0; off < n; off += kChunk) {
+    const size_t c = std::min(kChunk, n - off);
+    const int s = take();
+    std::memcpy(host_[s], src + off, c);
+    HIP_CHECK(hipMemcpyAsync(static_cast<uint8_t *>(dst) + off, host_[s], c, hipMemcpyHostToDevice, st_));
+    HIP_CHECK(hipEventRecord(done_[s], st_));
+  }
+}
+
+void Uploader::matrix(uint32_t kind, const uint8_t *src, int rows, size_t row_bytes, const DevMatrix &m) {
+  LG_REQUIRE(row_bytes > 0 && row_bytes <= kChunk, "upload: %zu-byte rows do not fit the staging", row_bytes);
+  const int per = int(std::min<size_t>(kChunk / row_bytes, size_t(rows)));
+  for (int r0 = 0; r0 < rows; r0 += per) {
+    const int n = std::min(per, rows - r0);
+    const size_t c = size_t(n) * row_bytes;
+    const int s = take();
+    std::memcpy(host_[s], src + size_t(r0) * row_bytes, c);
+    HIP_CHECK(hipMemcpyAsync(dev_[s], host_[s], c, hipMemcpyHostToDevice, st_));
+    DevMatrix part = sub_rows(m, r0, n);
+    launch_repack(kind, static_cast<const uint8_t *>(dev_[s]), n, m.cols, part, st_);
+    HIP_CHECK(hipEventRecord(done_[s], st_));
+  }
+}
+
+void Uploader::finish() { HIP_CHECK(hipStreamSynchronize(st_)); }
+
+Uploader &Engine::uploader() {
+  if (!up_) up_ = new Uploader(stream);
+  return *up_;
+}
+
+void Engine::finish_upload() {
+  if (up_) {
+    up_->finish();
+    delete up_;
+    up_ = nullptr;
+  }
+  HIP_CHECK(hipStreamSynchronize(stream));
+}
+
 // ------------------------------------------------------------------ construction
 Engine::Engine(const Gguf &g, const lg_engine_opts &opts) {
+  const auto t_load = std::chrono::steady_clock::now();
   device = opts.device;
   int ndev = 0;
   HIP_CHECK(hipGetDeviceCount(&ndev));
@@ -175,7 +252,8 @@ Engine::Engine(const Gguf &g, const lg_engine_opts &opts) {
       HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
       load_openthai(g);
       decide = decide_spec(g);
-      HIP_CHECK(hipStreamSynchronize(stream));
+      finish_upload();
+      load_s_ = std::chrono::duration<double>(std::chrono::steady_clock::now() - t_load).count();
       return;
     }
     if (g.str("general.architecture") == "ggmlc" && g.str("laya.model_name") != "laya-decoder" &&
@@ -185,10 +263,12 @@ Engine::Engine(const Gguf &g, const lg_engine_opts &opts) {
       load_laya(g);
       decide = decide_spec(g);
       laya_decide = laya_spec(g);
-      HIP_CHECK(hipStreamSynchronize(stream));
+      finish_upload();
+      load_s_ = std::chrono::duration<double>(std::chrono::steady_clock::now() - t_load).count();
       return;
     }
     load_decoder(g, opts);
+    load_s_ = std::chrono::duration<double>(std::chrono::steady_clock::now() - t_load).count();
   } catch (...) {
     release();
     throw;
@@ -214,6 +294,7 @@ void Engine::load_decoder(const Gguf &g, const lg_engine_opts &opts) {
     fail(LG_ERR_UNSUPPORTED, "d_model %d / head_dim %d outside the kernels' shapes", d, hd);
   HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
   upload(g);
+  finish_upload();
   // KV pool: [L][npages][hkv][64][hd] elements (f32 in EXACT mode, f16 in FAST) for K, then V
   int64_t pages = opts.kv_pages;
   if (pages <= 0) {
@@ -244,6 +325,8 @@ Engine::~Engine() { release(); }
 
 void Engine::release() {
   if (stream) (void)hipStreamSynchronize(stream);
+  delete up_;
+  up_ = nullptr;
   if (arena_) (void)hipFree(arena_);
   if (emb_) (void)hipFree(emb_);
   if (kv_) (void)hipFree(kv_);
@@ -303,17 +386,11 @@ DevMatrix Engine::upload_matrix(const Gguf &g, const std::vector<std::string> &n
   const int alloc_rows = pad_to > 0 ? (rows + pad_to - 1) / pad_to * pad_to : rows;
   m.q = carve(size_t(q_row_bytes(m.kind, cols)) * alloc_rows);
   if (s_row_bytes(m.kind, cols)) m.s = carve(size_t(s_row_bytes(m.kind, cols)) * alloc_rows);
-  size_t maxraw = 0;
-  for (auto *t : ts) maxraw = std::max<size_t>(maxraw, t->len);
-  DevBuf staging;
-  staging.ensure(maxraw);
   int row0 = 0;
   for (size_t i = 0; i < ts.size(); ++i) {
     const TensorInfo *t = ts[i];
-    HIP_CHECK(hipMemcpy(staging.p, g.data(*t), t->len, hipMemcpyHostToDevice));
     DevMatrix part = sub_rows(m, row0, int(t->rows()));
-    launch_repack(t->kind, staging.as<uint8_t>(), part.rows, cols, part, stream);
-    HIP_CHECK(hipStreamSynchronize(stream));
+    uploader().matrix(t->kind, g.data(*t), part.rows, size_t(t->len / t->rows()), part);
     named_[names[i]] = part;
     row0 += part.rows;
   }
@@ -322,7 +399,6 @@ DevMatrix Engine::upload_matrix(const Gguf &g, const std::vector<std::string> &n
     DevMatrix pad = sub_rows(m, rows, alloc_rows - rows);
     HIP_CHECK(hipMemsetAsync(pad.q, 0, size_t(q_row_bytes(m.kind, cols)) * pad.rows, stream));
     if (pad.s) HIP_CHECK(hipMemsetAsync(pad.s, 0, size_t(s_row_bytes(m.kind, cols)) * pad.rows, stream));
-    HIP_CHECK(hipStreamSynchronize(stream));
     m.rows = alloc_rows;
   }
   return m;
@@ -345,7 +421,6 @@ void Engine::add_prefill_copy(DevMatrix &m) {
     return;
   }
   launch_prefill_copy(m, stream);
-  HIP_CHECK(hipStreamSynchronize(stream));
 }
 
 void Engine::upload(const Gguf &g) {
@@ -375,7 +450,7 @@ void Engine::upload(const Gguf &g) {
     fail(LG_ERR_FORMAT, "tok_emb.weight must be F32/F16 [d, vocab]");
   emb_kind = emb->kind;
   HIP_CHECK(hipMalloc(&emb_, emb->len));
-  HIP_CHECK(hipMemcpy(emb_, g.data(*emb), emb->len, hipMemcpyHostToDevice));
+  uploader().bytes(g.data(*emb), emb->len, emb_);
   weight_bytes_ += int64_t(emb->len);
 
   const int qw = hq * hd, kvw = hkv * hd;
@@ -471,6 +546,7 @@ lg_model_info Engine::info() const {
   i.linear_heads = nh;
   i.full_layers = 0;
   for (const OtLayer &y : ot_) i.full_layers += y.full ? 1 : 0;
+  i.load_seconds = load_s_;
   return i;
 }
 

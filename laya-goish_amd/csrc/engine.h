@@ -131,6 +131,32 @@ struct OtLayer {
   float *conv = nullptr, *dt = nullptr, *alog = nullptr, *norm = nullptr;  // DeltaNet
 };
 
+// Streamed host -> HBM upload of GGUF bytes: two pinned host buffers and two device staging
+// buffers of kChunk bytes.  While the DMA engine copies chunk i and the repack kernel converts it,
+// the host copies chunk i + 1 out of the (memory-mapped) file into the other pinned buffer.  Large
+// matrices (a 152,064-row head) go through in row slices, so staging never exceeds 2 x kChunk.
+class Uploader {
+ public:
+  static constexpr size_t kChunk = size_t(64) << 20;
+  explicit Uploader(hipStream_t st);
+  ~Uploader();
+  Uploader(const Uploader &) = delete;
+  Uploader &operator=(const Uploader &) = delete;
+  // n bytes of host memory to device memory
+  void bytes(const uint8_t *src, size_t n, void *dst);
+  // rows of GGUF blocks (row_bytes raw bytes each), repacked into the rows of `m`
+  void matrix(uint32_t kind, const uint8_t *src, int rows, size_t row_bytes, const DevMatrix &m);
+  void finish();  // everything queued has landed; the host buffers are free
+
+ private:
+  int take();  // the next slot, once its previous copy and repack have finished
+  hipStream_t st_;
+  void *host_[2] = {nullptr, nullptr}, *dev_[2] = {nullptr, nullptr};
+  hipEvent_t done_[2] = {nullptr, nullptr};
+  bool used_[2] = {false, false};
+  int next_ = 0;
+};
+
 class Engine {
  public:
   Engine(const Gguf &g, const lg_engine_opts &opts);
@@ -176,8 +202,10 @@ class Engine {
   void release();
   // pad_to > 0: rows rounded up to a multiple of pad_to with zero weights
   DevMatrix upload_matrix(const Gguf &g, const std::vector<std::string> &names, int cols, int pad_to = 0);
-  // exact mode, Q8_0: the f16-code / f32-scale copy the large-batch prefill GEMM reads
+  // exact mode: the operand form the large-batch prefill GEMM reads (DevMatrix::pc, pcl, pcs)
   void add_prefill_copy(DevMatrix &m);
+  Uploader &uploader();  // created on first use
+  void finish_upload();  // waits for the queued upload work and frees the staging
   // offset != 0: stores offset + w (the zero-centred RMSNorm weight)
   float *upload_vector_f32(const Gguf &g, const std::string &name, int64_t n, float offset = 0.0f);
   void *carve(size_t bytes);
@@ -224,6 +252,8 @@ class Engine {
   // weights
   void *arena_ = nullptr;
   size_t arena_size_ = 0, arena_used_ = 0;
+  Uploader *up_ = nullptr;  // live while the constructor uploads weights
+  double load_s_ = 0.0;     // wall time of the constructor (upload, repack, prefill copies)
   void *emb_ = nullptr;
   float *cos_ = nullptr, *sin_ = nullptr, *final_norm_ = nullptr;
   std::vector<Layer> layers_;

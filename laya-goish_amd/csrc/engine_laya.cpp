@@ -53,7 +53,7 @@ LayaLinear Engine::laya_linear(const Gguf &g, const Json &graph, const std::stri
     l.w.cols = cols;
     if (t->kind != LG_F16 && t->kind != LG_F32) fail(LG_ERR_UNSUPPORTED, "%s: vector linears must be F16/F32", weight.c_str());
     l.w.q = carve(t->len);
-    HIP_CHECK(hipMemcpy(l.w.q, g.data(*t), t->len, hipMemcpyHostToDevice));
+    uploader().bytes(g.data(*t), t->len, l.w.q);
     named_[weight] = l.w;
     weight_bytes_ += int64_t(t->len);
   }
@@ -154,7 +154,7 @@ void Engine::load_laya(const Gguf &g) {
     (void)hipGetLastError();
     fail(LG_ERR_OOM, "cannot allocate %llu bytes of embeddings", (unsigned long long)et->len);
   }
-  HIP_CHECK(hipMemcpy(emb_, g.data(*et), et->len, hipMemcpyHostToDevice));
+  uploader().bytes(g.data(*et), et->len, emb_);
   weight_bytes_ += int64_t(et->len);
 
   auto layer = [&](int i, bool head) {

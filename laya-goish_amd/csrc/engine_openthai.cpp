@@ -85,7 +85,7 @@ void Engine::load_openthai(const Gguf &g) {
     (void)hipGetLastError();
     fail(LG_ERR_OOM, "cannot allocate %llu bytes of embeddings", (unsigned long long)emb->len);
   }
-  HIP_CHECK(hipMemcpy(emb_, g.data(*emb), emb->len, hipMemcpyHostToDevice));
+  uploader().bytes(g.data(*emb), emb->len, emb_);
   weight_bytes_ += int64_t(emb->len);
 
   for (int l = 0; l < L; ++l) {

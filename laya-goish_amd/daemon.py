@@ -194,24 +194,23 @@ class Registry:
     "model" or get the default."""
 
     def __init__(self, paths, default=None, open_engine=None):
-        if not paths:
-            raise RegistryError("at least one model is required")
-        self.names, ggufs = {}, []
+        # the library's preflight: every file opened and described, names and aliases unique, the
+        # default known -- before any weights load
+        try:
+            self.default = lh.registry_preflight(list(paths), default)
+        except lh.LayaError as e:
+            raise RegistryError(str(e)) from None
+        self.names, ggufs, self.model_names = {}, [], []
         for i, path in enumerate(paths):
             g = lh.Gguf.open(path)
-            name = g.str("general.name", "") or os.path.basename(path)
-            if name in self.names:
-                raise RegistryError(f"duplicate model name or alias {name}; load one checkpoint per model")
-            self.names[name] = i
+            d = lh.describe(g)
+            for n in [d["name"]] + d["aliases"]:
+                self.names[n] = i
+            self.model_names.append(d["name"])
             ggufs.append(g)
-        if default is not None and default not in self.names:
-            raise RegistryError(f"unknown default model {default}")
-        self.default = self.names[default] if default is not None else 0
-        self.model_names = list(self.names)
-        # answers of a Laya encoder name laya.model_name (src/models/laya/decision.rs:293)
-        self.answer_names = [g.str("laya.model_name", "") if g.str("ggmlc.graph_spec", "") else ""
-                             for g in ggufs]
-        self.answer_names = [a or n for a, n in zip(self.answer_names, self.model_names)]
+        # answers name the model as the reference's engine does (a Laya encoder: laya.model_name,
+        # src/models/laya/decision.rs:293)
+        self.answer_names = list(self.model_names)
         self.engines = [open_engine(g) for g in ggufs]
 
     def select(self, req) -> int:

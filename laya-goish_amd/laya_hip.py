@@ -47,7 +47,8 @@ class ModelInfo(ctypes.Structure):
                 ("weight_bytes", ctypes.c_int64), ("kv_bytes", ctypes.c_int64),
                 ("kv_pages", ctypes.c_int), ("kv_page_tokens", ctypes.c_int),
                 ("precision", ctypes.c_int), ("kv_elem_bytes", ctypes.c_int),
-                ("arch", ctypes.c_int), ("linear_heads", ctypes.c_int), ("full_layers", ctypes.c_int)]
+                ("arch", ctypes.c_int), ("linear_heads", ctypes.c_int), ("full_layers", ctypes.c_int),
+                ("load_seconds", ctypes.c_double)]
 
     def asdict(self):
         return {n: getattr(self, n) for n, _ in self._fields_}
@@ -283,6 +284,8 @@ def lib() -> ctypes.CDLL:
             "lg_profile_read": (I, [P, ctypes.c_char_p, ctypes.POINTER(I64), ctypes.POINTER(ctypes.c_double),
                                     ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
             "lg_profile_reset": (I, [P]),
+            "lg_model_describe": (I, [P, P]),
+            "lg_registry_preflight": (I, [P, I, ctypes.c_char_p, ctypes.POINTER(I)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -373,6 +376,29 @@ class SynthImage:
 
 def synth_file(preset: str, seed: int, path: str, n_layers: int = 0) -> None:
     check(lib().lg_synth_gguf_file(preset.encode(), seed, n_layers, path.encode()))
+
+
+class ModelDesc(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 128), ("family", ctypes.c_char * 64), ("architecture", ctypes.c_char * 64),
+                ("aliases", (ctypes.c_char * 64) * 4), ("n_aliases", ctypes.c_int), ("release_date", ctypes.c_char * 16)]
+
+
+def describe(g: "Gguf") -> dict:
+    """models::describe (src/models/mod.rs:32-64): name, family, architecture, aliases, release date."""
+    d = ModelDesc()
+    check(lib().lg_model_describe(g.h, ctypes.byref(d)))
+    return {"name": d.name.decode(), "family": d.family.decode(), "architecture": d.architecture.decode(),
+            "aliases": [d.aliases[i].value.decode() for i in range(d.n_aliases)],
+            "release_date": d.release_date.decode()}
+
+
+def registry_preflight(paths, default=None) -> int:
+    """Registry::load's preflight (src/registry.rs:16-39) before any weights load; the default's index."""
+    arr = (ctypes.c_char_p * max(1, len(paths)))(*[p.encode() for p in paths])
+    idx = ctypes.c_int()
+    check(lib().lg_registry_preflight(arr, len(paths), None if default is None else default.encode(),
+                                      ctypes.byref(idx)))
+    return idx.value
 
 
 class Gguf:

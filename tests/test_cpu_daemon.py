@@ -259,7 +259,8 @@ def test_registry_laya_answers_name_laya_model_name(lh, tmp_path):
     path = str(tmp_path / "laya.gguf")
     lh.synth_file("laya-tiny", 7, path)
     reg = daemon.Registry([path], None, lambda g: LayaScoredEngine(lh, g))
-    assert reg.model_names == ["Laya synthetic laya-tiny"] and reg.answer_names == ["laya"]
+    assert reg.model_names == ["laya"] and reg.answer_names == ["laya"]
+    assert reg.select({"model": "jev-latest"}) == 0 and reg.select({"model": "english"}) == 0
     out = io.StringIO()
     req = {k: v for k, v in REQ.items() if k != "permutations"}
     daemon.serve(reg.engines[0], reg.answer_names[0], io.StringIO(json.dumps(req) + "\n"), out)

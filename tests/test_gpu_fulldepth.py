@@ -136,5 +136,7 @@ def test_q8_decode_24_layers_64_steps(lh, po, q8_full):
     for i, gap in ties:
         print(f"  near-tie at step {i}: oracle top-2 gap {gap:.3e} < window {window:.3e}", flush=True)
     gaps = [float(np.sort(w)[-1] - np.sort(w)[-2]) for w in want]
-    print(f"argmax: {steps - len(ties)} steps asserted, {len(ties)} near-ties, smallest gap {min(gaps):.3e}")
+    flips = [i for i, _ in ties if int(np.argmax(logits[i])) != int(np.argmax(want[i]))]
+    print(f"argmax: {steps - len(ties)} steps asserted, {len(ties)} near-ties (argmax differs at {flips}), "
+          f"smallest gap {min(gaps):.3e}")
     assert not bad, f"argmax mismatches (step, gap, gpu, oracle): {bad}"
