@@ -496,6 +496,17 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
   const int col_in = lane & 31;
 #pragma unroll
   for (int i = 0; i < WTM; ++i) {
+    // the residual add reads a 32-row block's values first, all in one round trip (rows past M read
+    // row M - 1 and are not stored)
+    float cv[16][EPI == int(Epi::ADD) ? WTN : 1];
+    if constexpr (EPI == int(Epi::ADD)) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = min(m0 + wm * (32 * WTM) + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3), M - 1);
+#pragma unroll
+        for (int j = 0; j < WTN; ++j) cv[r][j] = C[int64_t(row) * ldc + nt * BNT + wn * (32 * WTN) + j * 32 + col_in];
+      }
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int row = m0 + wm * (32 * WTM) + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
@@ -519,9 +530,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
           if (EPI == int(Epi::F32)) {
             if (bias) v += bias[col];
             C[int64_t(row) * ldc + col] = v;
-          } else if (EPI == int(Epi::ADD)) {
+          } else if constexpr (EPI == int(Epi::ADD)) {
             if (bias) v += bias[col];
-            C[int64_t(row) * ldc + col] += v;
+            C[int64_t(row) * ldc + col] = cv[r][j] + v;
           } else {
             if (bias) v += bias[col];
             if (EPI == int(Epi::RELU16)) v = fmaxf(v, 0.0f);

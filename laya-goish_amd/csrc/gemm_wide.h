@@ -225,13 +225,13 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
   }
 
   // epilogue: acc[i][j] register r -> row (r/4)*8 + (lane/32)*4 + r%4, column lane%32
+  if constexpr (kGlu) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < 2; ++i) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
-      if (row >= M) continue;
-      if constexpr (kGlu) {
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        if (row >= M) continue;
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
           const int col = nt * (BN / 2) + wn * 64 + jj * 32 + lr;
@@ -241,17 +241,36 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
           C16[int64_t(row) * ldc + col] = h;
           if (C16lo) C16lo[int64_t(row) * ldc + col] = hl;
         }
-      } else {
+      }
+    }
+  } else {
+    float bv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bv[j] = bias ? bias[nt * BN + wn * 128 + j * 32 + lr] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      // the residual add reads a 32-row block's 64 values per lane in one round trip (rows past M
+      // read row M - 1 and are not stored), then adds and stores
+      float cv[16][4];
+      if constexpr (EPI == int(Epi::ADD)) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = min(m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3), M - 1);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) cv[r][j] = C[int64_t(row) * ldc + nt * BN + wn * 128 + j * 32 + lr];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+        if (row >= M) continue;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int col = nt * BN + wn * 128 + j * 32 + lr;
           float v = acc[i][j][r];
-          if (bias) v += bias[col];
-          if constexpr (EPI == int(Epi::F32)) {
-            C[int64_t(row) * ldc + col] = v;
-          } else {
-            C[int64_t(row) * ldc + col] += v;
-          }
+          if (bias) v += bv[j];
+          if constexpr (EPI == int(Epi::F32)) C[int64_t(row) * ldc + col] = v;
+          else C[int64_t(row) * ldc + col] = cv[r][j] + v;
         }
       }
     }
