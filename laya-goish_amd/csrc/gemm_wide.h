@@ -190,17 +190,38 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
       float d[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) d[j] = *reinterpret_cast<const float *>(st + G::kScl + (wn * 128 + j * 32 + lr) * 4);
+      // software pipeline over the wave's eight (i, j) blocks: the four MFMAs of block c issue
+      // between the sixteen scale FMAs of block c - 1 (two partial-sum registers), so the MFMA
+      // pipe runs while the VALU applies the previous block's scale
+      f32x16 p[2];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          f32x16 p = WIDE_MFMA(ah[0][i], b[0][j], zero);
-          p = WIDE_MFMA(al[0][i], b[0][j], p);
-          p = WIDE_MFMA(ah[1][i], b[1][j], p);
-          p = WIDE_MFMA(al[1][i], b[1][j], p);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[i][j][r] += d[j] * p[r];
+      for (int c = 0; c <= 8; ++c) {
+        if (c < 8) {
+          const int i = c & 1, j = c >> 1;
+          f32x16 q = WIDE_MFMA(ah[0][i], b[0][j], zero);
+          q = WIDE_MFMA(al[0][i], b[0][j], q);
+          q = WIDE_MFMA(ah[1][i], b[1][j], q);
+          q = WIDE_MFMA(al[1][i], b[1][j], q);
+          p[c & 1] = q;
         }
+        if (c > 0) {
+          const int i = (c - 1) & 1, j = (c - 1) >> 1;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][j][r] += d[j] * p[(c - 1) & 1][r];
+        }
+        if (c == 0) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 18, 0);  // every operand and scale read of the step
+          __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);   // block 0's MFMAs
+        } else if (c < 8) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA of block c
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four FMAs of block c - 1
+          }
+        } else {
+          __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);  // block 7's FMAs
+        }
+      }
     } else {
       // per element: for each 16-deep chunk kk, A_hi.W_hi, A_lo.W_hi (, A_hi.W_lo); the
       // eight blocks of a wave interleave, so no MFMA waits on the one before it
