@@ -143,7 +143,7 @@ __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
     _Float16 *__restrict__ q16, _Float16 *__restrict__ q16lo, void *__restrict__ kpool,
     void *__restrict__ vpool, float qscale) {
   constexpr int TT = 32, HALF = HD / 2, HB = 2;  // tokens per tile, pair offset, V heads per LDS round
-  constexpr int QB = 8;                         // tokens whose loads one round issues together
+  constexpr int QB = 4;                         // tokens whose loads one round issues together
   constexpr int TPR = kT / HD, VT = TT / TPR;   // V: token lanes per dim, tokens per thread
   static_assert(kT % HALF == 0 && kT % HD == 0, "thread blocks must tile the head");
   __shared__ float vs[HB][TT][HD + 1];
@@ -156,50 +156,94 @@ __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
   auto page_base = [&](int pos) { return (pos / g.page_tokens == pg0 ? page_lo : page_hi) * g.page_stride; };
   const int plane = g.page_tokens * HD;  // values per plane of one (page, kv head) block
   const int qw = hq * HD, kvw = g.hkv * HD, rw = qw + 2 * kvw;
-  // rotations: thread -> pairs p = tid + 256 m of the q|k heads (pair j = p % HALF is the same
-  // for every m), QB tokens per round with every load issued before any value is used
-  const int npairs = (hq + g.hkv) * HALF;
-  const int j = tid % HALF;
-  for (int p0 = 0; p0 < npairs; p0 += kT) {
+  // rotations: thread -> four consecutive pairs j..j+3 of a q|k head (quad p = tid + 256 m; the
+  // quad's j is the same for every m), QB tokens per round with every load issued before any value
+  // is used; float4 loads, 8-byte stores of four f16
+  constexpr int QPH = HALF / 4;  // quads per head
+  static_assert(kT % QPH == 0, "thread blocks must tile the quads of a head");
+  const int nquads = (hq + g.hkv) * QPH;
+  const int j = (tid % QPH) * 4;
+  typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+  for (int p0 = 0; p0 < nquads; p0 += kT) {
     const int p = p0 + tid;
-    const int hh = min(p, npairs - 1) / HALF;
+    const int hh = min(p, nquads - 1) / QPH;
     for (int t0 = 0; t0 < n; t0 += QB) {
-      float u[QB], v[QB], c0[QB], c1[QB], s0[QB], s1[QB];
+      float4 u[QB], v[QB], c0[QB], c1[QB], s0[QB], s1[QB];
 #pragma unroll
       for (int b = 0; b < QB; ++b) {
         const int tk = min(t0 + b, n - 1);
         const float *row = qkv + int64_t(row0 + tk) * rw + hh * HD;
         const int64_t cb = int64_t(pos0 + tk) * HD;
-        u[b] = row[j];
-        v[b] = row[j + HALF];
-        c0[b] = cosT[cb + j];
-        c1[b] = cosT[cb + j + HALF];
-        s0[b] = sinT[cb + j];
-        s1[b] = sinT[cb + j + HALF];
+        u[b] = *reinterpret_cast<const float4 *>(row + j);
+        v[b] = *reinterpret_cast<const float4 *>(row + j + HALF);
+        c0[b] = *reinterpret_cast<const float4 *>(cosT + cb + j);
+        c1[b] = *reinterpret_cast<const float4 *>(cosT + cb + j + HALF);
+        s0[b] = *reinterpret_cast<const float4 *>(sinT + cb + j);
+        s1[b] = *reinterpret_cast<const float4 *>(sinT + cb + j + HALF);
       }
-      if (p >= npairs) continue;
+      if (p >= nquads) continue;
 #pragma unroll
       for (int b = 0; b < QB; ++b) {
         const int tk = t0 + b;
         if (tk >= n) continue;
-        const float a = u[b] * c0[b] - v[b] * s0[b], c = v[b] * c1[b] + u[b] * s1[b];
+        const float uu[4] = {u[b].x, u[b].y, u[b].z, u[b].w}, vv[4] = {v[b].x, v[b].y, v[b].z, v[b].w};
+        const float cc0[4] = {c0[b].x, c0[b].y, c0[b].z, c0[b].w}, cc1[4] = {c1[b].x, c1[b].y, c1[b].z, c1[b].w};
+        const float ss0[4] = {s0[b].x, s0[b].y, s0[b].z, s0[b].w}, ss1[4] = {s1[b].x, s1[b].y, s1[b].z, s1[b].w};
+        float a[4], c[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          a[e] = uu[e] * cc0[e] - vv[e] * ss0[e];
+          c[e] = vv[e] * cc1[e] + uu[e] * ss1[e];
+        }
         if (hh < hq) {
           const int64_t at = int64_t(row0 + tk) * qw + hh * HD + j;
-          _Float16 ah, al, ch, cl;
-          split_f16(a * qscale, ah, al);
-          split_f16(c * qscale, ch, cl);
-          q16[at] = ah;
-          q16[at + HALF] = ch;
+          half4 ah, al, ch, cl;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            _Float16 x, y;
+            split_f16(a[e] * qscale, x, y);
+            ah[e] = x;
+            al[e] = y;
+            split_f16(c[e] * qscale, x, y);
+            ch[e] = x;
+            cl[e] = y;
+          }
+          *reinterpret_cast<half4 *>(q16 + at) = ah;
+          *reinterpret_cast<half4 *>(q16 + at + HALF) = ch;
           if (q16lo) {
-            q16lo[at] = al;
-            q16lo[at + HALF] = cl;
+            *reinterpret_cast<half4 *>(q16lo + at) = al;
+            *reinterpret_cast<half4 *>(q16lo + at + HALF) = cl;
           }
         } else {
           const int pos = pos0 + tk;
           const int64_t blk = page_base(pos) + int64_t(hh - hq) * plane;
           const int r = (pos % g.page_tokens) * HD + j;
-          kv_put<SPLIT>(kpool, blk, r, plane, a);
-          kv_put<SPLIT>(kpool, blk, r + HALF, plane, c);
+          _Float16 *kp = static_cast<_Float16 *>(kpool);
+          half4 ah, al, ch, cl;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if constexpr (SPLIT) {
+              _Float16 x, y;
+              split_f16(a[e], x, y);
+              ah[e] = x;
+              al[e] = y;
+              split_f16(c[e], x, y);
+              ch[e] = x;
+              cl[e] = y;
+            } else {
+              ah[e] = _Float16(a[e]);
+              ch[e] = _Float16(c[e]);
+            }
+          }
+          if constexpr (SPLIT) {
+            *reinterpret_cast<half4 *>(kp + 2 * blk + r) = ah;
+            *reinterpret_cast<half4 *>(kp + 2 * blk + r + HALF) = ch;
+            *reinterpret_cast<half4 *>(kp + 2 * blk + plane + r) = al;
+            *reinterpret_cast<half4 *>(kp + 2 * blk + plane + r + HALF) = cl;
+          } else {
+            *reinterpret_cast<half4 *>(kp + blk + r) = ah;
+            *reinterpret_cast<half4 *>(kp + blk + r + HALF) = ch;
+          }
         }
       }
     }
