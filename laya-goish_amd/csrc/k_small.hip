@@ -266,13 +266,40 @@ __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
 #pragma unroll
       for (int i = 0; i < VT; ++i) vs[hh][tq + TPR * i][dd] = val[hh][i];
     __syncthreads();
-    // thread -> (head, dim, token) with the token fastest: 32 consecutive slots per dim row
-    for (int i = tid; i < nh * TT * HD; i += kT) {
-      const int hh = i / (TT * HD), r = i % (TT * HD), tk = r % TT, d2 = r / TT;
-      if (tk < n) {
-        const int pos = pos0 + tk;
-        kv_put<SPLIT>(vpool, page_base(pos) + int64_t(h0 + hh) * plane, d2 * g.page_tokens + pos % g.page_tokens,
-                      plane, vs[hh][tk][d2]);
+    // thread -> (head, dim, four tokens) with the tokens fastest: runs of consecutive slots per dim row,
+    // four slots (one 8-byte store per plane) when the quad is whole and 4-aligned in its page
+    for (int i = tid; i < nh * (TT / 4) * HD; i += kT) {
+      const int hh = i / ((TT / 4) * HD), r = i % ((TT / 4) * HD), tk0 = (r % (TT / 4)) * 4, d2 = r / (TT / 4);
+      if (tk0 >= n) continue;
+      if ((pos0 & 3) == 0 && tk0 + 3 < n) {
+        const int pos = pos0 + tk0;
+        const int64_t blk = page_base(pos) + int64_t(h0 + hh) * plane;
+        const int idx = d2 * g.page_tokens + pos % g.page_tokens;
+        _Float16 *vp = static_cast<_Float16 *>(vpool);
+        half4 vh, vl;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (SPLIT) {
+            _Float16 x, y;
+            split_f16(vs[hh][tk0 + e][d2], x, y);
+            vh[e] = x;
+            vl[e] = y;
+          } else {
+            vh[e] = _Float16(vs[hh][tk0 + e][d2]);
+          }
+        }
+        if constexpr (SPLIT) {
+          *reinterpret_cast<half4 *>(vp + 2 * blk + idx) = vh;
+          *reinterpret_cast<half4 *>(vp + 2 * blk + plane + idx) = vl;
+        } else {
+          *reinterpret_cast<half4 *>(vp + blk + idx) = vh;
+        }
+      } else {
+        for (int tk = tk0; tk < min(tk0 + 4, n); ++tk) {
+          const int pos = pos0 + tk;
+          kv_put<SPLIT>(vpool, page_base(pos) + int64_t(h0 + hh) * plane, d2 * g.page_tokens + pos % g.page_tokens,
+                        plane, vs[hh][tk][d2]);
+        }
       }
     }
     __syncthreads();
