@@ -84,7 +84,10 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
     const int nblk = gridDim.x;
     int id = blockIdx.x;
     if ((nblk & 7) == 0) id = (id & 7) * (nblk >> 3) + (id >> 3);
-    constexpr int GM = 4;
+#ifndef LG_WIDE_GROUP_M
+#define LG_WIDE_GROUP_M 4
+#endif
+    constexpr int GM = LG_WIDE_GROUP_M;
     const int group = id / (GM * NT), first = group * GM;
     const int gm = min(MT - first, GM), in = id - group * GM * NT;
     mt = first + in % gm;
