@@ -52,4 +52,16 @@ __device__ __forceinline__ void split8_pk(const float *v, f16x8 &hi, f16x8 &lo) 
   }
 }
 
+// Rotate-half RoPE of one pair (u at dim j, v at dim j + hd/2) with the table entries of both dims
+// (src/tensor.rs:158-172): a = u cos_j - v sin_j, c = v cos_{j+hd/2} + u sin_{j+hd/2}, every product
+// and sum rounded on its own as the reference forms them (no contraction into FMA here, whatever
+// the including file allows).  Shared by every kernel that writes the KV cache, so a token's
+// cached k has the same bits whichever kernel rotated it.
+__device__ __forceinline__ void rope_pair(float u, float v, float c0, float s0, float c1, float s1, float &a,
+                                          float &c) {
+#pragma clang fp contract(off)
+  a = u * c0 - v * s0;
+  c = v * c1 + u * s1;
+}
+
 }  // namespace lg

@@ -499,15 +499,18 @@ __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, 
     const int idx = t + 256 * e;
     const int gq = idx / HALF, j = idx % HALF;
     const int row = idx < GRP * HALF ? gq : GRP;
-    qs[row * HD + j] = qu[e] * c0[e] - qv[e] * s0[e];
-    qs[row * HD + j + HALF] = qv[e] * c1[e] + qu[e] * s1[e];
+    float ra, rc;
+    rope_pair(qu[e], qv[e], c0[e], s0[e], c1[e], s1[e], ra, rc);
+    qs[row * HD + j] = ra;
+    qs[row * HD + j + HALF] = rc;
   }
   const bool cur = pi == pos / P;  // this page holds the new token (uniform per workgroup)
   const int slot = pos % P;
   {  // the new token's rotated k and its v, computed and staged in LDS (as the cache holds them)
      // by every thread (idle threads write junk to their own slots), so their loads stay ahead
      // of the page's; only the page that holds the slot stores them into the cache
-    const float a = nku * nc0 - nkv * ns0, b = nkv * nc1 + nku * ns1;
+    float a, b;
+    rope_pair(nku, nkv, nc0, ns0, nc1, ns1, a, b);
     if constexpr (NPL == 2) {
       _Float16 ah, al, bh, bl, vh, vl;
       split_f16(a, ah, al);

@@ -191,10 +191,7 @@ __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
         const float ss0[4] = {s0[b].x, s0[b].y, s0[b].z, s0[b].w}, ss1[4] = {s1[b].x, s1[b].y, s1[b].z, s1[b].w};
         float a[4], c[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          a[e] = uu[e] * cc0[e] - vv[e] * ss0[e];
-          c[e] = vv[e] * cc1[e] + uu[e] * ss1[e];
-        }
+        for (int e = 0; e < 4; ++e) rope_pair(uu[e], vv[e], cc0[e], ss0[e], cc1[e], ss1[e], a[e], c[e]);
         if (hh < hq) {
           const int64_t at = int64_t(row0 + tk) * qw + hh * HD + j;
           half4 ah, al, ch, cl;

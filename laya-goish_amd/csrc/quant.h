@@ -52,9 +52,16 @@ __device__ __forceinline__ uint32_t q6k_code(const uint8_t *c, int w, int &scale
 }
 
 // Dequantised weight of the repacked layouts (kernels.h), each product and difference rounded
-// on its own as src/gguf.rs:301-303 and :326-330 form them: Q4_K (d*sc) * q - (dmin*m) from the
-// pair (a, b) = (d*sc, dmin*m); Q6_K (d*sc) * (code - 32).
-__device__ __forceinline__ float kq4_weight(float a, uint32_t q, float b) { return __fsub_rn(__fmul_rn(a, float(q)), b); }
-__device__ __forceinline__ float kq6_weight(float a, int q) { return __fmul_rn(a, float(q)); }
+// on its own as src/gguf.rs:301-303 and :326-330 form them (no contraction into FMA here, whatever
+// the including file allows): Q4_K (d*sc) * q - (dmin*m) from the pair (a, b) = (d*sc, dmin*m);
+// Q6_K (d*sc) * (code - 32).
+__device__ __forceinline__ float kq4_weight(float a, uint32_t q, float b) {
+#pragma clang fp contract(off)
+  return a * float(q) - b;
+}
+__device__ __forceinline__ float kq6_weight(float a, int q) {
+#pragma clang fp contract(off)
+  return a * float(q);
+}
 
 }  // namespace lg
