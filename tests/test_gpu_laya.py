@@ -159,3 +159,25 @@ def test_large_batch_equals_single(tiny):
         assert np.array_equal(batch[i][0], sl) and np.array_equal(batch[i][1], sa)
         wl, wa = om.forward(*inputs[i])
         assert np.abs(sl - wl).max() <= TOL[prec] and np.abs(sa - wa).max() <= TOL[prec]
+
+
+@pytest.mark.parametrize("layers", [1, 4])
+def test_exact_attention_precision(lh, po, layers):
+    """The exact mode's split-operand MFMAs (three f16 products per pair, ~22 significant bits) in
+    the Laya attention and GEMMs: option and act logits within 5e-6 of the largest |logit| at one
+    layer (layer 0 is a global-attention layer) and at full depth (measured 1.7e-7 to 2.8e-7).  One
+    f16-only operand anywhere costs ~1e-3, two hundred times this bar."""
+    img = lh.SynthImage("laya-tiny", seed=17, n_layers=layers)
+    eng = lh.Engine(lh.Gguf.from_bytes(img))
+    om = po.Laya(po.Gguf(img.array()), threads=8)
+    worst = 0.0
+    for n, markers, qtype in ((200, [3, 50, 120, 199], 1), (512, list(range(40, 56)), 0)):
+        ids = np.random.default_rng(n + layers).integers(0, 1000, n)
+        (gl, ga), = eng.laya_forward([(ids, markers, qtype)])
+        wl, wa = om.forward(ids, markers, qtype)
+        scale = max(np.abs(wl).max(), np.abs(wa).max())
+        err = max(np.abs(gl - wl).max(), np.abs(ga - wa).max()) / scale
+        print(f"laya-tiny L{layers} n={n}: relative logit error {err:.2e}", flush=True)
+        worst = max(worst, err)
+    eng.close()
+    assert worst <= 5e-6
