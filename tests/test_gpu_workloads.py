@@ -152,3 +152,30 @@ def test_f16_7b_full_length_prefix_reuse(lh, prec):
         eng.seq_free(child)
         eng.seq_free(fresh)
     eng.close()
+
+
+def test_q4km_7b_large_batch_equals_single_requests(lh, po):
+    """The K-quant wide GEMM (256 x 256 tiles over the weights' f16 hi/lo planes) takes the launches
+    of a 12 x 700-token batch (8400 rows: the last M tile is partial); requests alone take the 128 x 128
+    tiles.  Both give the same bits, and a request of the batch matches the oracle."""
+    img = lh.SynthImage("q4km-7b", seed=19, n_layers=1)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=12 * 768 + 1024, max_batch_tokens=8400)
+    V = eng.info["vocab"]
+    rng = np.random.default_rng(23)
+    reqs = [(_ids(700, V, 40 + i), [699, 350, 3]) for i in range(12)]
+    opts = rng.choice(V, 4, replace=False).astype(np.int32)
+    seqs = [eng.seq_create() for _ in reqs]
+    print("q4km-7b L1: batch of 12 x 700 tokens", flush=True)
+    logits, _, _ = eng.batch([(s, ids, pos) for s, (ids, pos) in zip(seqs, reqs)]).run(opts)
+    for s in seqs:
+        eng.seq_free(s)
+    for r in (0, 7, 11):
+        s = eng.seq_create()
+        single = eng.forward(s, reqs[r][0], reqs[r][1], opts)
+        eng.seq_free(s)
+        assert np.array_equal(single, logits[3 * r:3 * r + 3]), f"request {r}: batch != alone"
+    om = po.Model(po.Gguf(img.array()), threads=16)
+    want = om.forward(reqs[11][0], reqs[11][1], opts)
+    err = assert_logits_close(logits[33:36], want, rel=logit_bar(0))
+    print(f"q4km-7b 12 x 700: bit-identical to single requests; logit rel {err:.2e} vs oracle")
+    eng.close()
