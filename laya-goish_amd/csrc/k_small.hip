@@ -161,12 +161,16 @@ __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
   // is used; float4 loads, 8-byte stores of four f16
   constexpr int QPH = HALF / 4;  // quads per head
   static_assert(kT % QPH == 0, "thread blocks must tile the quads of a head");
-  const int nquads = (hq + g.hkv) * QPH;
+  // the tile's work is split over four workgroups (blockIdx.y): the first and second half of the q
+  // heads, the k heads, the v heads
+  const int part = blockIdx.y;
+  const int h_lo = part == 0 ? 0 : part == 1 ? hq / 2 : hq, h_hi = part == 0 ? hq / 2 : part == 1 ? hq : hq + g.hkv;
+  const int nquads = part < 3 ? (h_hi - h_lo) * QPH : 0;
   const int j = (tid % QPH) * 4;
   typedef _Float16 half4 __attribute__((ext_vector_type(4)));
   for (int p0 = 0; p0 < nquads; p0 += kT) {
     const int p = p0 + tid;
-    const int hh = min(p, nquads - 1) / QPH;
+    const int hh = h_lo + min(p, nquads - 1) / QPH;
     for (int t0 = 0; t0 < n; t0 += QB) {
       float4 u[QB], v[QB], c0[QB], c1[QB], s0[QB], s1[QB];
 #pragma unroll
@@ -245,6 +249,7 @@ __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
       }
     }
   }
+  if (part != 3) return;
   // v: HB kv heads per round staged through LDS (thread -> dim tid % HD, tokens tid / HD + TPR i),
   // then written as runs of consecutive slots
   const int dd = tid % HD, tq = tid / HD;
@@ -508,7 +513,7 @@ void launch_rope_kv_tiles(const float *qkv, int hq, const KvGeom &g, const float
   // the attention consumes base-2 logits: fold log2(e) / sqrt(hd) into q once here
   const float qscale = 1.4426950408889634f / std::sqrt(float(g.hd));
 #define LAUNCH(K32, HDV)                                                                                  \
-  hipLaunchKernelGGL((rope_kv_tile_kernel<K32, HDV>), dim3(ntiles), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, \
+  hipLaunchKernelGGL((rope_kv_tile_kernel<K32, HDV>), dim3(ntiles, 4), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, \
                      pages, max_pages, tile_seq, tile_row0, tile_pos0, tile_n, q16, q16_lo, kpool, vpool, qscale)
   if (g.hd == 128) {
     if (g.split) LAUNCH(true, 128); else LAUNCH(false, 128);
