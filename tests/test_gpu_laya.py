@@ -181,3 +181,24 @@ def test_exact_attention_precision(lh, po, layers):
         worst = max(worst, err)
     eng.close()
     assert worst <= 5e-6
+
+
+def test_activations_beyond_f16_range_are_reported(lh, po):
+    """The exact mode splits activations into f16 hi/lo planes, which hold |x| <= 65504.  A q
+    projection row of 60000s in layer 0 drives q past that range for every token: the forward then
+    fails with the reference's "non-finite model output" (src/models/laya/model.rs:412-414) instead
+    of returning values, while the f32 reference would still produce finite logits."""
+    img = lh.SynthImage("laya-tiny", seed=13)
+    arr = img.array().copy()
+    og = po.Gguf(arr)
+    kind, dims, _ = og.tensor("qkv.0.weight")
+    assert kind == 1  # F16
+    off, d = og.offset("qkv.0.weight"), dims[0]
+    arr[off:off + 2 * d] = np.frombuffer(np.full(d, 0x7B53, np.uint16).tobytes(), np.uint8)  # 60000.0
+    eng = lh.Engine(lh.Gguf.from_bytes(arr))
+    ids = np.random.default_rng(5).integers(0, 1000, 64)
+    with pytest.raises(lh.LayaError, match="non-finite model output"):
+        eng.laya_forward([(ids, [3, 9], 0)])
+    want_l, want_a = po.Laya(po.Gguf(arr), threads=8).forward(ids, [3, 9], 0)
+    assert np.isfinite(want_l).all() and np.isfinite(want_a).all()
+    eng.close()
