@@ -235,6 +235,14 @@ int lg_decode(lg_engine *e, int seq, int32_t first, int steps, int32_t *tokens, 
  * race, and must be serialised by the caller. */
 int lg_decode_noalloc(lg_engine *e, int seq, int32_t first, int steps, int32_t *tokens, float *logits);
 
+/* lg_decode (no logits) with the whole step loop -- every kernel of every step -- captured into one
+ * HIP graph after the metadata upload and launched once; the wall time of the capture and
+ * instantiation and that of the graph launch (through its completion) are returned.  No reference
+ * counterpart: it measures whether launching the decode as a graph changes its GPU time.  Tokens
+ * and the sequence's new length equal lg_decode's; kernel profiling must be off. */
+int lg_decode_graph(lg_engine *e, int seq, int32_t first, int steps, int32_t *tokens, double *capture_ms,
+                    double *run_ms);
+
 /* Option scores over host logits, the CPU side of the same rule (for callers that
  * already hold logits).  Replaces src/models/openthai/decision.rs:268-279. */
 int lg_option_scores(const float *logits, int k, float temperature, float *probs,

@@ -386,6 +386,14 @@ int lg_decode(lg_engine *e, int seq, int32_t first, int steps, int32_t *tokens, 
   });
 }
 
+int lg_decode_graph(lg_engine *e, int seq, int32_t first, int steps, int32_t *tokens, double *capture_ms,
+                    double *run_ms) {
+  return guard([&] {
+    NEED(e, "engine");
+    e->e->decode_graph(seq, first, steps, tokens, capture_ms, run_ms);
+  });
+}
+
 int lg_decode_noalloc(lg_engine *e, int seq, int32_t first, int steps, int32_t *tokens, float *logits) {
   return guard([&] {
     NEED(e, "engine");

@@ -1050,7 +1050,21 @@ void Engine::decode_noalloc(int sq, int32_t first, int steps, int32_t *tokens, f
   decode_run(s, first, steps, tokens, logits, ws);
 }
 
-void Engine::decode_run(Seq &s, int32_t first, int steps, int32_t *tokens, float *logits, void *ws) {
+void Engine::decode_graph(int sq, int32_t first, int steps, int32_t *tokens, double *capture_ms, double *run_ms) {
+  Seq &s = seq(sq);
+  decode_check(s, first, steps, tokens);
+  LG_REQUIRE(capture_ms && run_ms, "decode_graph: need both time outputs");
+  LG_REQUIRE(!prof.on(), "decode_graph: turn kernel profiling off first");
+  reserve_pages(s, s.len + steps);
+  ws_dec_.ensure(decode_ws_bytes(s.len, steps));
+  decode_run(s, first, steps, tokens, nullptr, ws_dec_.p, capture_ms, run_ms);
+}
+
+// With capture_ms / run_ms set, the step loop (kernels only: no copies, no memsets) is captured into a
+// HIP graph after the metadata upload and launched once.
+void Engine::decode_run(Seq &s, int32_t first, int steps, int32_t *tokens, float *logits, void *ws,
+                        double *capture_ms, double *run_ms) {
+  const bool graph = capture_ms != nullptr;
   const int pos0 = s.len;
   const int qw = hq * hd, kvw = hkv * hd, qkvw = qw + 2 * kvw;
   const int max_pages = int(s.pages.size());
@@ -1070,27 +1084,67 @@ void Engine::decode_run(Seq &s, int32_t first, int steps, int32_t *tokens, float
   int32_t *part_i = pt + max_pages;
   HIP_CHECK(hipMemcpyAsync(dm, meta.data(), meta.size() * 4, hipMemcpyHostToDevice, stream));
   const KvGeom g = geom();
-  for (int i = 0; i < steps; ++i) {
-    prof.begin("embed", stream);
-    launch_embed(emb_, emb_kind, tok + i, 1, d, V, x, stream);
-    prof.end(double(d) * 6, 0, stream);
-    for (int l = 0; l < L; ++l) {
-      const Layer &ly = layers_[l];
-      for (const ProjPart &p : ly.qkv) gemv(x, p.w, Epi::F32, qkv + p.col0, p.bias, ly.attn_norm);
-      // the position of this step is a kernel argument; RoPE and the k/v write are fused in
-      prof.begin("attn_decode", stream);
-      launch_attn_decode(qkv, hq, g, cos_, sin_, pos0 + i, kpool(l), vpool(l), pt, max_pages, part, att,
-                         stream);
-      prof.end(double(pos0 + i + 1) * 2 * kvw * kv_elem(), 4.0 * double(pos0 + i + 1) * qw, stream);
-      gemv(att, ly.wo, Epi::ADD, x, nullptr, nullptr);
-      gemv(x, ly.wi, Epi::SWIGLU, act, nullptr, ly.ffn_norm);
-      gemv(act, ly.wd, Epi::ADD, x, nullptr, nullptr);
+  hipGraph_t hg = nullptr;
+  hipGraphExec_t hx = nullptr;
+  std::chrono::steady_clock::time_point t0;
+  if (graph) {
+    sync();
+    t0 = std::chrono::steady_clock::now();
+    HIP_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+  }
+  auto step_loop = [&] {
+    for (int i = 0; i < steps; ++i) {
+      prof.begin("embed", stream);
+      launch_embed(emb_, emb_kind, tok + i, 1, d, V, x, stream);
+      prof.end(double(d) * 6, 0, stream);
+      for (int l = 0; l < L; ++l) {
+        const Layer &ly = layers_[l];
+        for (const ProjPart &p : ly.qkv) gemv(x, p.w, Epi::F32, qkv + p.col0, p.bias, ly.attn_norm);
+        // the position of this step is a kernel argument; RoPE and the k/v write are fused in
+        prof.begin("attn_decode", stream);
+        launch_attn_decode(qkv, hq, g, cos_, sin_, pos0 + i, kpool(l), vpool(l), pt, max_pages, part, att,
+                           stream);
+        prof.end(double(pos0 + i + 1) * 2 * kvw * kv_elem(), 4.0 * double(pos0 + i + 1) * qw, stream);
+        gemv(att, ly.wo, Epi::ADD, x, nullptr, nullptr);
+        gemv(x, ly.wi, Epi::SWIGLU, act, nullptr, ly.ffn_norm);
+        gemv(act, ly.wd, Epi::ADD, x, nullptr, nullptr);
+      }
+      gemv(x, head_, Epi::F32, lg, nullptr, final_norm_);
+      prof.begin("argmax", stream);
+      launch_argmax(lg, V, tok + i + 1, part_v, part_i, stream);
+      prof.end(double(V) * 4, 0, stream);
+      if (logits) HIP_CHECK(hipMemcpyAsync(logits + size_t(i) * V, lg, size_t(V) * 4, hipMemcpyDeviceToHost, stream));
     }
-    gemv(x, head_, Epi::F32, lg, nullptr, final_norm_);
-    prof.begin("argmax", stream);
-    launch_argmax(lg, V, tok + i + 1, part_v, part_i, stream);
-    prof.end(double(V) * 4, 0, stream);
-    if (logits) HIP_CHECK(hipMemcpyAsync(logits + size_t(i) * V, lg, size_t(V) * 4, hipMemcpyDeviceToHost, stream));
+  };
+  if (!graph) {
+    step_loop();
+  } else {
+    // an error raised while capturing ends the capture first, so the stream stays usable
+    try {
+      step_loop();
+    } catch (...) {
+      hipGraph_t dropped = nullptr;
+      (void)hipStreamEndCapture(stream, &dropped);
+      if (dropped) (void)hipGraphDestroy(dropped);
+      throw;
+    }
+    const hipError_t ce = hipStreamEndCapture(stream, &hg);
+    hipError_t ie = hipErrorUnknown;
+    if (ce == hipSuccess) ie = hipGraphInstantiate(&hx, hg, nullptr, nullptr, 0);
+    if (ce != hipSuccess || ie != hipSuccess) {
+      if (hg) (void)hipGraphDestroy(hg);
+      fail(LG_ERR_DEVICE, "decode_graph: capture failed (%s)", hipGetErrorString(ce != hipSuccess ? ce : ie));
+    }
+    const auto t1 = std::chrono::steady_clock::now();
+    const hipError_t le = hipGraphLaunch(hx, stream);
+    const hipError_t se = hipStreamSynchronize(stream);
+    const auto t2 = std::chrono::steady_clock::now();
+    (void)hipGraphExecDestroy(hx);
+    (void)hipGraphDestroy(hg);
+    HIP_CHECK(le);
+    HIP_CHECK(se);
+    *capture_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    *run_ms = std::chrono::duration<double, std::milli>(t2 - t1).count();
   }
   HIP_CHECK(hipMemcpyAsync(tokens, tok + 1, size_t(steps) * 4, hipMemcpyDeviceToHost, stream));
   sync();

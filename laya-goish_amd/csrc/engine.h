@@ -186,6 +186,9 @@ class Engine {
   void decode(int seq, int32_t first, int steps, int32_t *tokens, float *logits);
   // decode with its workspace in the per-device no-alloc scratch: no device allocation at all
   void decode_noalloc(int seq, int32_t first, int steps, int32_t *tokens, float *logits);
+  // decode with the whole step loop captured into one HIP graph, then launched once; wall times of
+  // the capture + instantiation and of the graph launch
+  void decode_graph(int seq, int32_t first, int steps, int32_t *tokens, double *capture_ms, double *run_ms);
   // Laya Model::forward (src/models/laya/model.rs:303-416) for n inputs as one batch:
   // option logits (k_i per input, concatenated) and act logits [n][2].
   void laya_forward(const lg_laya_input *in, int n, float *logits, float *act, lg_cancel_fn cancel, void *arg);
@@ -217,7 +220,8 @@ class Engine {
   // decode: argument checks, then the steps with the workspace `ws` (decode_ws_bytes of it)
   void decode_check(const Seq &s, int32_t first, int steps, const int32_t *tokens) const;
   size_t decode_ws_bytes(int pos0, int steps) const;
-  void decode_run(Seq &s, int32_t first, int steps, int32_t *tokens, float *logits, void *ws);
+  void decode_run(Seq &s, int32_t first, int steps, int32_t *tokens, float *logits, void *ws,
+                  double *capture_ms = nullptr, double *run_ms = nullptr);
   void run_openthai(BatchPlan &b, lg_cancel_fn cancel, void *arg);
   void run_laya(BatchPlan &b, const int32_t *qtype_dev, lg_cancel_fn cancel, void *arg);
   KvGeom geom() const;

@@ -270,6 +270,8 @@ def lib() -> ctypes.CDLL:
             "lg_batch_rewind": (I, [P, P]),
             "lg_decode": (I, [P, I, ctypes.c_int32, I, P, P]),
             "lg_decode_noalloc": (I, [P, I, ctypes.c_int32, I, P, P]),
+            "lg_decode_graph": (I, [P, I, ctypes.c_int32, I, P, ctypes.POINTER(ctypes.c_double),
+                                    ctypes.POINTER(ctypes.c_double)]),
             "lg_option_scores": (I, [P, I, F, P, P]),
             "lg_decide": (I, [P, ctypes.POINTER(DecideRequest), ctypes.POINTER(DecideResult), CANCEL_FN, P]),
             "lg_laya_forward": (I, [P, ctypes.POINTER(LayaInput), I, P, P, CANCEL_FN, P]),
@@ -635,6 +637,14 @@ class Engine:
         fn = lib().lg_decode_noalloc if noalloc else lib().lg_decode
         check(fn(self.h, seq, first, steps, _ptr(toks), _ptr(lg)))
         return (toks, lg) if want_logits else toks
+
+    def decode_graph(self, seq: int, first: int, steps: int):
+        """lg_decode_graph: the step loop captured into one HIP graph and launched once.
+        (tokens, capture + instantiation ms, graph launch ms)."""
+        toks = np.empty(steps, dtype=np.int32)
+        cap, run = ctypes.c_double(), ctypes.c_double()
+        check(lib().lg_decode_graph(self.h, seq, first, steps, _ptr(toks), ctypes.byref(cap), ctypes.byref(run)))
+        return toks, cap.value, run.value
 
     def profile(self, on: bool = True) -> None:
         check(lib().lg_profile_enable(self.h, 1 if on else 0))

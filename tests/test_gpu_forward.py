@@ -149,6 +149,30 @@ def test_decode_teacher_forced(pair, po):
     eng.seq_free(s)
 
 
+def test_decode_graph_equals_stream_decode(pair):
+    """lg_decode_graph (every step's kernels captured into one HIP graph) gives the same tokens as
+    lg_decode and leaves the sequence as long, with the same cache contents."""
+    preset, eng, om = pair
+    ids = _ids(40, om.V, 13)
+    s = eng.seq_create()
+    eng.forward(s, ids[:-1], [], OPTIONS)
+    a, b = eng.seq_fork(s, len(ids) - 1), eng.seq_fork(s, len(ids) - 1)
+    want = eng.decode(a, int(ids[-1]), 9)
+    for _ in range(2):                       # twice: the second capture starts from a longer sequence
+        got, cap_ms, run_ms = eng.decode_graph(b, int(ids[-1]) if _ == 0 else int(want[-1]), 9)
+        if _ == 0:
+            np.testing.assert_array_equal(got, want)
+            assert eng.seq_len(b) == eng.seq_len(a)
+            ka, kb = eng.seq_kv_read(a, 0, 0, eng.seq_len(a)), eng.seq_kv_read(b, 0, 0, eng.seq_len(b))
+            for x, y in zip(ka, kb):
+                np.testing.assert_array_equal(x, y)
+        assert cap_ms > 0 and run_ms > 0
+    more = eng.decode(a, int(want[-1]), 9)
+    np.testing.assert_array_equal(got, more)
+    for q in (a, b, s):
+        eng.seq_free(q)
+
+
 def test_errors_are_reported(pair, lh):
     preset, eng, om = pair
     s = eng.seq_create()
