@@ -1018,28 +1018,31 @@ void Engine::decode_check(const Seq &s, int32_t first, int steps, const int32_t 
     fail(LG_ERR_INVALID, "sequence of %lld tokens exceeds the context length %d", (long long)s.len + steps, ctx);
 }
 
-// Workspace of a decode run: x, q|k|v, attention output, SwiGLU output, logits, argmax partial maxima,
-// attention page partials (f32), then the token slots, the page table and the argmax partial indices.
-size_t Engine::decode_ws_bytes(int pos0, int steps) const {
+// Workspace of a decode run over a sequence holding `npages` pages (its whole page table, which a
+// canceled forward can leave longer than the tokens need): x, q|k|v, attention output, SwiGLU
+// output, logits, argmax partial maxima, attention page partials (f32, laid out by the page table's
+// length), then the token slots, the page table and the argmax partial indices.
+size_t Engine::decode_ws_bytes(int npages, int steps) const {
   const int qw = hq * hd, qkvw = qw + 2 * hkv * hd;
-  const size_t part_floats = size_t(attn_decode_scratch_floats(1, hq, hd, pos0 + steps));
+  const size_t part_floats = size_t(attn_decode_scratch_floats(hq, hd, npages));
   const size_t floats = size_t(d) + qkvw + qw + f + V + 64 + part_floats;
-  const size_t pages = size_t(pos0 + steps + 63) / 64;
-  return floats * 4 + (size_t(steps) + 1 + pages) * 4 + 64 * 4 + 256;
+  return floats * 4 + (size_t(steps) + 1 + npages) * 4 + 64 * 4 + 256;
 }
 
 void Engine::decode(int sq, int32_t first, int steps, int32_t *tokens, float *logits) {
   Seq &s = seq(sq);
   decode_check(s, first, steps, tokens);
   reserve_pages(s, s.len + steps);
-  ws_dec_.ensure(decode_ws_bytes(s.len, steps));
+  ws_dec_.ensure(decode_ws_bytes(int(s.pages.size()), steps));
   decode_run(s, first, steps, tokens, logits, ws_dec_.p);
 }
 
 void Engine::decode_noalloc(int sq, int32_t first, int steps, int32_t *tokens, float *logits) {
   Seq &s = seq(sq);
   decode_check(s, first, steps, tokens);
-  const size_t need = decode_ws_bytes(s.len, steps);
+  // the page table as reserve_pages below leaves it (checked first, so a refusal reserves nothing)
+  const int npages = std::max(int(s.pages.size()), (s.len + steps + 63) / 64);
+  const size_t need = decode_ws_bytes(npages, steps);
   if (need > kNoAllocScratchBytes)
     fail(LG_ERR_INVALID,
          "decode_noalloc: %d steps after %d tokens need %zu bytes of scratch; the per-GPU limit is %zu "
@@ -1056,7 +1059,7 @@ void Engine::decode_graph(int sq, int32_t first, int steps, int32_t *tokens, dou
   LG_REQUIRE(capture_ms && run_ms, "decode_graph: need both time outputs");
   LG_REQUIRE(!prof.on(), "decode_graph: turn kernel profiling off first");
   reserve_pages(s, s.len + steps);
-  ws_dec_.ensure(decode_ws_bytes(s.len, steps));
+  ws_dec_.ensure(decode_ws_bytes(int(s.pages.size()), steps));
   decode_run(s, first, steps, tokens, nullptr, ws_dec_.p, capture_ms, run_ms);
 }
 
@@ -1074,7 +1077,7 @@ void Engine::decode_run(Seq &s, int32_t first, int steps, int32_t *tokens, float
   meta.push_back(first);
   meta.resize(steps + 1, 0);
   for (int p : s.pages) meta.push_back(p);
-  const size_t part_floats = size_t(attn_decode_scratch_floats(1, hq, hd, pos0 + steps));
+  const size_t part_floats = size_t(attn_decode_scratch_floats(hq, hd, max_pages));
   float *x = static_cast<float *>(ws);
   float *qkv = x + d, *att = qkv + qkvw, *act = att + qw, *lg = act + f;
   float *part_v = lg + V;

@@ -219,7 +219,7 @@ class Engine {
   void run_layers_prefill(BatchPlan &b, lg_cancel_fn cancel, void *arg);
   // decode: argument checks, then the steps with the workspace `ws` (decode_ws_bytes of it)
   void decode_check(const Seq &s, int32_t first, int steps, const int32_t *tokens) const;
-  size_t decode_ws_bytes(int pos0, int steps) const;
+  size_t decode_ws_bytes(int npages, int steps) const;
   void decode_run(Seq &s, int32_t first, int steps, int32_t *tokens, float *logits, void *ws,
                   double *capture_ms = nullptr, double *run_ms = nullptr);
   void run_openthai(BatchPlan &b, lg_cancel_fn cancel, void *arg);

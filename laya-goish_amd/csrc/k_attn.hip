@@ -299,16 +299,18 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
 }
 
 // ---------------------------------------------------------------- decode
-// part layout: [nseq][hq][max_pages][2 + HD] = (max, sum, out[HD]) of one page.
+// part layout: [hq][max_pages][2 + HD] = (max, sum, out[HD]) of one page.
 // One 256-thread workgroup per (page, kv head).  Every thread issues its query/RoPE loads, then
 // all of its K and V loads: K rows and V columns of the page are read as consecutive 16-byte
 // words (thread t takes word t + 256 i), so each load instruction covers one contiguous
 // kilobyte per wave.  A thread thus holds E consecutive dims of NL keys (K) and E consecutive
 // keys of NL dims (V).  Meanwhile the group's query heads are rotated into LDS and, on the page
-// that holds the new token, its k (rotated) and v are written into the cache and substituted
-// for the stale slot in the registers just loaded.  Scores are reduced over the lanes of a key
-// with DPP moves, the page softmax runs on one wave per head, then P.V reduces over the lanes
-// of a dim.
+// that holds the new token, its k (rotated) and v are substituted for the stale slot in the
+// registers just loaded.  Scores are reduced over the lanes of a key with DPP moves, the page
+// softmax runs on one wave per head, then P.V reduces over the lanes of a dim.  The new token's
+// k and v are stored into the cache by an extra workgroup per kv head (grid column np), which
+// reads no page and so finishes long before the page workgroups: a store in the page's own
+// workgroup would hold it, one of the launch's last to finish, until the write is acknowledged.
 // Pool value formats: float, _Float16, or SplitKV: per (page, kv head) block an f16 hi plane and
 // then an f16 lo plane (hi = f16(v), lo = f16(v - hi)), each laid out as the f16 pool is.
 struct SplitKV {};
@@ -322,6 +324,54 @@ struct KvFmt<SplitKV> {
   using elem = _Float16;
   static constexpr int NPL = 2;
 };
+
+// The new token's rotated k and its v (f16, or hi/lo planes) into slot pos % P of its page, for
+// kv head kh; threads 0 .. HD-1 take part (k pair (t, t + HD/2) for t < HD/2, v dim t).  The same
+// rope_pair and split as the page workgroup that substitutes the slot in its registers, so the
+// cache holds the values that step's scores used.
+template <int HD, typename KV>
+__device__ __forceinline__ void store_new_kv(const float *__restrict__ qkv, int hq, const KvGeom &g,
+                                             const float *__restrict__ cosT, const float *__restrict__ sinT,
+                                             int pos, typename KvFmt<KV>::elem *__restrict__ kpool,
+                                             typename KvFmt<KV>::elem *__restrict__ vpool,
+                                             const int32_t *__restrict__ pages, int kh) {
+  using T = typename KvFmt<KV>::elem;
+  constexpr int NPL = KvFmt<KV>::NPL, HALF = HD / 2, PLANE = P * HD;
+  const int t = threadIdx.x;
+  if (t >= HD) return;
+  const int64_t page = pages[pos / P];
+  const int slot = pos % P;
+  T *Kp = kpool + page * (NPL * g.page_stride) + int64_t(kh) * NPL * P * HD;
+  T *Vp = vpool + page * (NPL * g.page_stride) + int64_t(kh) * NPL * HD * P;
+  const float *cs = cosT + int64_t(pos) * HD, *sn = sinT + int64_t(pos) * HD;
+  const int j = t & (HALF - 1);
+  const float *kr0 = qkv + (hq + kh) * HD;
+  const float ku = kr0[j], kv = kr0[j + HALF], c0 = cs[j], c1 = cs[j + HALF], s0 = sn[j], s1 = sn[j + HALF];
+  const float nv = qkv[(hq + g.hkv + kh) * HD + t];
+  float a, b;
+  rope_pair(ku, kv, c0, s0, c1, s1, a, b);
+  if constexpr (NPL == 2) {
+    _Float16 vh, vl;
+    split_f16(nv, vh, vl);
+    Vp[t * P + slot] = vh;
+    Vp[PLANE + t * P + slot] = vl;
+    if (t < HALF) {
+      _Float16 ah, al, bh, bl;
+      split_f16(a, ah, al);
+      split_f16(b, bh, bl);
+      Kp[slot * HD + t] = ah;
+      Kp[PLANE + slot * HD + t] = al;
+      Kp[slot * HD + t + HALF] = bh;
+      Kp[PLANE + slot * HD + t + HALF] = bl;
+    }
+  } else {
+    Vp[t * P + slot] = T(nv);
+    if (t < HALF) {
+      Kp[slot * HD + t] = T(a);
+      Kp[slot * HD + t + HALF] = T(b);
+    }
+  }
+}
 
 template <int HD, int GRP, typename KV>
 __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, int hq, const KvGeom &g,
@@ -341,93 +391,75 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float *__restric
                                                           float *__restrict__ part) {
   static_assert(HD == 64 || HD == 128, "decode attention is written for head_dim 64 and 128");
   const int pi = blockIdx.x, kh = blockIdx.y;
+  if (pi == pos / P + 1) {  // the extra column: store the new token's k and v, read no page
+    store_new_kv<HD, KV>(qkv, hq, g, cosT, sinT, pos, kpool, vpool, pages, kh);
+    return;
+  }
   float *pbase = part + (int64_t(kh * GRP) * max_pages + pi) * (2 + HD);
   const int64_t hstride = int64_t(max_pages) * (2 + HD);
   attn_decode_page<HD, GRP, KV>(qkv, hq, g, cosT, sinT, pos, kpool, vpool, pages, pbase, hstride);
 }
 
-// Combine the per-page partials (max, sum, out[HD]) of one query head: pb points at its page 0,
-// np pages.  A separate launch: handing the partials over to a last-arriving page workgroup
-// would need an agent-scope release (an L2 write-back on this part) in every page workgroup,
-// which measured slower than the launch.  Thread (d, half) owns output dim d over the pages half, half + 2, ...; each batch
-// of 2*CB pages is loaded in one round trip together with the page maxima and sums (indices
-// clamped, surplus pages weighted 0).  All 256 threads of the workgroup take part.
+// Combine launch: one 256-thread workgroup per query head h: out = sum_i w_i out_i / sum_i w_i sum_i
+// over the page partials (max_i, sum_i, out_i) of h, with w_i = exp(max_i - M) and M the largest
+// page maximum.  Thread (d, part) owns output dim d over the pages part, part + NPART, ...
+// (NPART = 256 / HD; one part per wave), so its page index is wave-uniform.  Every wave finds M
+// and the total sum_i w_i sum_i itself from lane-distributed maxima and sums (lane j: pages j,
+// j + 64, ...), and takes the weight of a page from the lane that computed it, so the only
+// barrier is the final sum over the parts.  The maxima and the first batch of 64 pages are loaded
+// before the first is waited for.  A separate launch: handing the partials over to a
+// last-arriving page workgroup would need an agent-scope release (an L2 write-back on this part)
+// in every page workgroup, which measured slower than the launch.
 template <int HD>
-__device__ __forceinline__ void combine_head(const float *__restrict__ pb, int np, float *__restrict__ outh) {
+__global__ __launch_bounds__(256) void attn_decode_combine(const float *__restrict__ part, int max_pages, int np,
+                                                           float *__restrict__ out) {
   constexpr int NPART = 256 / HD;  // threads per output dim: 2 (head_dim 128) or 4 (64)
   static_assert(NPART * HD == 256, "256 threads over the output dims");
-  constexpr int CB = 64 / NPART;   // pages per thread per batch
-  const int t = threadIdx.x;
-  __shared__ float wm[1024], wl[1024];
-  __shared__ float red[4], sacc[NPART][HD], sl[NPART];
-  const int d = t & (HD - 1), part = t / HD;
-  // page maxima and sums (np <= 1024: four per thread), then the first batch of outputs
-  float m4[4], l4[4];
+  constexpr int CB = 64 / NPART;   // pages per thread per batch of 64
+  constexpr int ROW = 2 + HD;
+  const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, d = t & (HD - 1);
+  const int pw = __builtin_amdgcn_readfirstlane(t / HD);  // this wave's part
+  const float *pb = part + int64_t(h) * max_pages * ROW;
+  float mx[16];  // page maxima, np <= 1024
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int i = min(t + 256 * u, np - 1);
-    m4[u] = pb[int64_t(i) * (2 + HD)];
-    l4[u] = pb[int64_t(i) * (2 + HD) + 1];
-  }
-  float ov[CB];
+  for (int c = 0; c < 16; ++c)
+    if (c * 64 < np) mx[c] = pb[int64_t(min(c * 64 + lane, np - 1)) * ROW];
+  float mb, lb, ov[CB];
+  auto load_batch = [&](int b0) {
+    const int i = min(b0 + lane, np - 1);
+    mb = pb[int64_t(i) * ROW];
+    lb = pb[int64_t(i) * ROW + 1];
 #pragma unroll
-  for (int u = 0; u < CB; ++u) ov[u] = pb[int64_t(min(part + NPART * u, np - 1)) * (2 + HD) + 2 + d];
+    for (int u = 0; u < CB; ++u) ov[u] = pb[int64_t(min(b0 + pw + NPART * u, np - 1)) * ROW + 2 + d];
+  };
+  load_batch(0);
   float M = -INFINITY;
 #pragma unroll
-  for (int u = 0; u < 4; ++u)
-    if (t + 256 * u < np) M = fmaxf(M, m4[u]);
+  for (int c = 0; c < 16; ++c)
+    if (c * 64 < np) M = fmaxf(M, mx[c]);
   M = wave_max_dpp(M);
-  if ((t & 63) == 0) red[t >> 6] = M;
-  __syncthreads();
-  M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int i = t + 256 * u;
-    if (i < np) {
-      wm[i] = m4[u] == -INFINITY ? 0.0f : __expf(m4[u] - M);
-      wl[i] = l4[u];
-    }
-  }
-  __syncthreads();
-  float acc = 0.0f, L = 0.0f;
-  for (int b0 = 0; b0 < np; b0 += NPART * CB) {
-    if (b0 > 0) {
-#pragma unroll
-      for (int u = 0; u < CB; ++u) ov[u] = pb[int64_t(min(b0 + part + NPART * u, np - 1)) * (2 + HD) + 2 + d];
-    }
+  float acc = 0.0f, lsum = 0.0f;
+  for (int b0 = 0; b0 < np; b0 += 64) {
+    if (b0 > 0) load_batch(b0);
+    // weight of page b0 + lane (0 past the last page)
+    const float w = b0 + lane < np && mb != -INFINITY ? __expf(mb - M) : 0.0f;
+    lsum = fmaf(lb, w, lsum);
 #pragma unroll
     for (int u = 0; u < CB; ++u) {
-      const int i = b0 + part + NPART * u;
-      if (i < np) {
-        acc += ov[u] * wm[i];
-        L += wl[i] * wm[i];
-      }
+      const int k = pw + NPART * u;  // wave-uniform page of the batch
+      if (b0 + k < np) acc = fmaf(ov[u], lane_value(w, k), acc);
     }
   }
-  sacc[part][d] = acc;
-  if (d == 0) sl[part] = L;
+  const float L = wave_sum_dpp(lsum);
+  __shared__ float sacc[NPART][HD];
+  sacc[pw][d] = acc;
   __syncthreads();
   if (t < HD) {
-    float a = 0.0f, l = 0.0f;
+    float a = 0.0f;
 #pragma unroll
-    for (int q = 0; q < NPART; ++q) {
-      a += sacc[q][t];
-      l += sl[q];
-    }
-    outh[t] = a / l;
+    for (int q = 0; q < NPART; ++q) a += sacc[q][t];
+    out[int64_t(h) * HD + t] = a / L;
   }
-  __syncthreads();  // the shared arrays are reused by the caller's next head
-}
-
-// Combine as its own launch: one workgroup per (query head, sequence).
-template <int HD>
-__global__ __launch_bounds__(256) void attn_decode_combine(const float *__restrict__ part, int hq,
-                                                           int max_pages,
-                                                           const int32_t *__restrict__ ctx_len, int ctx_all,
-                                                           float *__restrict__ out) {
-  const int h = blockIdx.x, s = blockIdx.y;
-  const int np = ((ctx_len ? ctx_len[s] : ctx_all) + P - 1) / P;
-  combine_head<HD>(part + ((int64_t(s) * hq + h) * max_pages) * (2 + HD), np, out + (int64_t(s) * hq + h) * HD);
 }
 
 // One page of one kv head: scores, page softmax and P.V for each query head.
@@ -506,9 +538,9 @@ __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, 
   }
   const bool cur = pi == pos / P;  // this page holds the new token (uniform per workgroup)
   const int slot = pos % P;
-  {  // the new token's rotated k and its v, computed and staged in LDS (as the cache holds them)
-     // by every thread (idle threads write junk to their own slots), so their loads stay ahead
-     // of the page's; only the page that holds the slot stores them into the cache
+  {  // the new token's rotated k and its v as the cache holds them (store_new_kv, in the extra
+     // workgroup column, stores the same values), staged in LDS by every thread (idle threads
+     // write junk to their own slots) so that their loads stay ahead of the page's
     float a, b;
     rope_pair(nku, nkv, nc0, ns0, nc1, ns1, a, b);
     if constexpr (NPL == 2) {
@@ -519,30 +551,10 @@ __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, 
       nka[t] = float(ah) + float(al);
       nkb[t] = float(bh) + float(bl);
       nvs[t] = float(vh) + float(vl);
-      if (cur) {
-        if (t < HALF) {
-          Kp[slot * HD + t] = ah;
-          Kp[PLANE + slot * HD + t] = al;
-          Kp[slot * HD + t + HALF] = bh;
-          Kp[PLANE + slot * HD + t + HALF] = bl;
-        } else if (t < HALF + HD) {
-          Vp[(t - HALF) * P + slot] = vh;
-          Vp[PLANE + (t - HALF) * P + slot] = vl;
-        }
-      }
     } else {
-      const T ac = T(a), bc = T(b), vc = T(nvv);
-      nka[t] = float(ac);
-      nkb[t] = float(bc);
-      nvs[t] = float(vc);
-      if (cur) {
-        if (t < HALF) {
-          Kp[slot * HD + t] = ac;
-          Kp[slot * HD + t + HALF] = bc;
-        } else if (t < HALF + HD) {
-          Vp[(t - HALF) * P + slot] = vc;
-        }
-      }
+      nka[t] = float(T(a));
+      nkb[t] = float(T(b));
+      nvs[t] = float(T(nvv));
     }
   }
   __syncthreads();
@@ -699,10 +711,7 @@ void launch_attn_prefill(const _Float16 *q16, const _Float16 *q16_lo, int T, int
   HIP_CHECK(hipGetLastError());
 }
 
-int64_t attn_decode_scratch_floats(int nseq, int hq, int hd, int max_ctx) {
-  const int64_t pages = (max_ctx + P - 1) / P;
-  return int64_t(nseq) * hq * pages * (2 + hd);
-}
+int64_t attn_decode_scratch_floats(int hq, int hd, int max_pages) { return int64_t(hq) * max_pages * (2 + hd); }
 
 void launch_attn_decode(const float *qkv, int hq, const KvGeom &g, const float *cosT, const float *sinT,
                         int pos, void *kpool, void *vpool, const int32_t *pages, int max_pages,
@@ -714,7 +723,7 @@ void launch_attn_decode(const float *qkv, int hq, const KvGeom &g, const float *
   LG_REQUIRE(np <= max_pages, "decode attention: context exceeds the page table");
   LG_REQUIRE(np <= 1024, "decode attention: context of %d pages exceeds the combine stage", np);
   const int grp = hq / g.hkv;
-  const dim3 grid(np, g.hkv), block(256);
+  const dim3 grid(np + 1, g.hkv), block(256);  // column np stores the new token
 #define CASE(HDV, G)                                                                                     \
   case G:                                                                                                \
     if (g.split)                                                                                         \
@@ -740,11 +749,9 @@ void launch_attn_decode(const float *qkv, int hq, const KvGeom &g, const float *
 #undef CASE
   HIP_CHECK(hipGetLastError());
   if (g.hd == 128)
-    hipLaunchKernelGGL((attn_decode_combine<128>), dim3(hq, 1), dim3(256), 0, st, part, hq, max_pages,
-                       static_cast<const int32_t *>(nullptr), pos + 1, out);
+    hipLaunchKernelGGL((attn_decode_combine<128>), dim3(hq), dim3(256), 0, st, part, max_pages, np, out);
   else
-    hipLaunchKernelGGL((attn_decode_combine<64>), dim3(hq, 1), dim3(256), 0, st, part, hq, max_pages,
-                       static_cast<const int32_t *>(nullptr), pos + 1, out);
+    hipLaunchKernelGGL((attn_decode_combine<64>), dim3(hq), dim3(256), 0, st, part, max_pages, np, out);
   HIP_CHECK(hipGetLastError());
 }
 

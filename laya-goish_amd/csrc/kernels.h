@@ -150,12 +150,13 @@ void launch_attn_prefill(const _Float16 *q16, const _Float16 *q16_lo, int T, int
 
 // Decode attention for one new token at position pos of one sequence: q|k|v row `qkv` (before
 // RoPE); RoPE of q and k (tables cos/sin[ctx][hd]) and the k/v write into the cache slot are
-// fused in.  Split over the pages 0..pos/64 into `part` (attn_decode_scratch_floats), then
-// combined per query head by a second launch into out[hq * hd].
+// fused in.  Split over the pages 0..pos/64 into `part` (attn_decode_scratch_floats(hq, hd,
+// max_pages) floats, max_pages = the length of the page table), then combined per query head by
+// a second launch into out[hq * hd].
 void launch_attn_decode(const float *qkv, int hq, const KvGeom &g, const float *cosT, const float *sinT,
                         int pos, void *kpool, void *vpool, const int32_t *pages, int max_pages,
                         float *part, float *out, hipStream_t st);
-int64_t attn_decode_scratch_floats(int nseq, int hq, int hd, int max_ctx);
+int64_t attn_decode_scratch_floats(int hq, int hd, int max_pages);
 
 // Gather rows, final RMSNorm and the option head: logits[r][j] = h_r . W[ids[j]] (+ bias[ids[j]]).
 void launch_head_rows(const float *x, const int32_t *rows, int R, int d, const float *norm_w,

@@ -173,6 +173,26 @@ def test_decode_graph_equals_stream_decode(pair):
         eng.seq_free(q)
 
 
+def test_decode_after_canceled_forward(pair, lh):
+    """A canceled forward keeps the pages it reserved, so the sequence's page table outgrows its
+    tokens; decode then lays its attention partials out by the whole table and gives the tokens of
+    an untouched sequence (stream and no-allocation entry points)."""
+    preset, eng, om = pair
+    ids = _ids(20, om.V, 17)
+    a, b = eng.seq_create(), eng.seq_create()
+    eng.forward(a, ids, [], OPTIONS)
+    eng.forward(b, ids, [], OPTIONS)
+    n = min(300, om.ctx - 40)
+    with pytest.raises(lh.LayaError) as e:
+        eng.forward(b, _ids(n, om.V, 18), [n - 1], OPTIONS, cancel=lambda _: 1)
+    assert e.value.kind == "CANCELED" and eng.seq_len(b) == 20
+    want = eng.decode(a, 5, 6)
+    np.testing.assert_array_equal(eng.decode(b, 5, 6), want)
+    np.testing.assert_array_equal(eng.decode(b, int(want[-1]), 3, noalloc=True), eng.decode(a, int(want[-1]), 3))
+    for q in (a, b):
+        eng.seq_free(q)
+
+
 def test_errors_are_reported(pair, lh):
     preset, eng, om = pair
     s = eng.seq_create()
