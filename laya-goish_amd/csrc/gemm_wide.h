@@ -14,8 +14,10 @@
 //
 // Geometry: 512 threads = 8 wave64s (2 per SIMD), workgroup tile 256 x 256, K steps of 32.
 // WQ8 and W1 keep three LDS stages (stage k + 2 in flight while stage k is consumed), W2 two
-// (its stage holds four planes); one barrier per step.  Wave w owns rows 64 (w / 2) .. + 64
-// and columns 128 (w % 2) .. + 128 of the tile (2 x 4 MFMA blocks).
+// (its stage holds four planes).  Wave w owns rows 64 (w / 2) .. + 64 and columns
+// 128 (w % 2) .. + 128 of the tile (2 x 4 MFMA blocks).  With three stages the two wave groups
+// of a workgroup run half a step apart (ping-pong, below), one barrier per half step; W2 runs
+// all eight waves in step, one barrier per step (measured faster for its two stages).
 //
 // LDS rows are 64 bytes (four 16-byte chunks); logical chunk c of row r sits in slot
 // c ^ ((r >> 2) & 3), so the 16 lanes of each quarter of an operand read fall in 16 distinct
@@ -51,7 +53,7 @@ struct Geo {
   static constexpr int kStageBytes = kScl + (kScales ? BN * 4 : 0);
   static constexpr int kStages = MODE == W2 ? 2 : 3;
   static constexpr int kLdsBytes = kStages * kStageBytes;  // WQ8 150,528; W1 147,456; W2 131,072
-  static constexpr int kDmaPerWave = 2 * (2 + kBPlanes);   // per stage (wave 0: + 1 scale block)
+  static constexpr int kDmaPerWave = (kStages == 3 ? 4 : 2) * (2 + kBPlanes);  // per stage and moving wave (wave 0: + 1 scale block)
 };
 
 __device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
@@ -105,9 +107,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
     }
   };
 
-  // DMA: wave w issues blocks w and w + 8 of each plane (A hi, A lo, W hi, W lo) and wave 0
-  // also the scale block.  Rows past M sit past the end of the A buffers: the buffer unit
-  // answers them with zeros.
+  // DMA.  Rows past M sit past the end of the A buffers: the buffer unit answers them with zeros.
   const uint32_t abytes = uint32_t(M) * uint32_t(K) * 2u, wbytes = uint32_t(N) * uint32_t(K) * 2u;
   const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(A), 0, abytes, kBufferFlags);
   const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(Alo), 0, abytes, kBufferFlags);
@@ -116,13 +116,20 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
   if constexpr (MODE == W2) rc = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(Wl), 0, wbytes, kBufferFlags);
   if constexpr (MODE == WQ8)
     rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(Ws), 0, uint32_t(N) * uint32_t(K / 32) * 4u, kBufferFlags);
-  uint32_t aoff[2], boff[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int slot = (wave + WAVES * h) * 64 + lane;  // 16-byte slot inside a plane
+  // Ping-pong (three-stage modes, below): group 0 (waves 0-3) moves every block, wave w the blocks
+  // w, w + 4, w + 8, w + 12 of each plane.  Two-stage mode (W2): all eight waves, wave w the
+  // blocks w and w + 8.  Block b + step q holds the rows of block b shifted by 64 q / 4 ... 16 q,
+  // which for A and for every weight row map (wrow) is a wave-uniform byte offset: the buffer
+  // instruction's scalar offset.  Wave 0 also moves the scale block.
+  constexpr bool kPingPong = G::kStages == 3;
+  constexpr int NB = kPingPong ? 4 : 2, BSTEP = kPingPong ? 4 : 8;  // blocks per wave, block stride
+  const int grp = wave >> 2, wb = kPingPong ? (wave & 3) : wave;
+  uint32_t aoff, boff;
+  {
+    const int slot = wb * 64 + lane;  // 16-byte slot inside a plane (block wb)
     const int row = slot >> 2, c = (slot & 3) ^ swz(row);
-    aoff[h] = uint32_t(m0 + row) * uint32_t(K) * 2u + uint32_t(c) * 16u;
-    boff[h] = uint32_t(wrow(row)) * uint32_t(K) * 2u + uint32_t(c) * 16u;
+    aoff = uint32_t(m0 + row) * uint32_t(K) * 2u + uint32_t(c) * 16u;
+    boff = uint32_t(wrow(row)) * uint32_t(K) * 2u + uint32_t(c) * 16u;
   }
   const uint32_t soff = uint32_t(wrow(4 * lane)) * 4u;  // four consecutive weight rows' scales
   const int nk = K / BK;
@@ -133,13 +140,15 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
     typedef __attribute__((address_space(3))) void *lds_ptr;
     uint8_t *base = lds + st * G::kStageBytes;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int blk = (wave + WAVES * h) * 1024;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr)(base + G::kAHi + blk), 16, aoff[h], kt * BK * 2, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, (lds_ptr)(base + G::kALo + blk), 16, aoff[h], kt * BK * 2, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr)(base + G::kBHi + blk), 16, boff[h], kt * BK * 2, 0, 0);
+    for (int h = 0; h < NB; ++h) {
+      const int blk = (wb + BSTEP * h) * 1024, dr = 16 * BSTEP * h;  // block, row shift
+      const uint32_t ka = uint32_t(kt * BK * 2) + uint32_t(dr) * uint32_t(K) * 2u;
+      const uint32_t kb = uint32_t(kt * BK * 2) + uint32_t(wrow(dr) - wrow(0)) * uint32_t(K) * 2u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr)(base + G::kAHi + blk), 16, aoff, ka, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, (lds_ptr)(base + G::kALo + blk), 16, aoff, ka, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr)(base + G::kBHi + blk), 16, boff, kb, 0, 0);
       if constexpr (MODE == W2)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (lds_ptr)(base + G::kBLo + blk), 16, boff[h], kt * BK * 2, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (lds_ptr)(base + G::kBLo + blk), 16, boff, kb, 0, 0);
     }
     if constexpr (MODE == WQ8)
       if (wave == 0) __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(base + G::kScl), 16, soff, kt * N * 4, 0, 0);
@@ -159,67 +168,62 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
   const int ac0 = (wm * 64 + lr) * ROWB, bc0 = (wn * 128 + lr) * ROWB;
   const int ch0 = ((0 + (lane >> 5)) ^ sw) * 16, ch1 = ((2 + (lane >> 5)) ^ sw) * 16;
   const f32x16 zero = {};
-
-#pragma unroll
-  for (int s = 0; s < G::kStages - 1; ++s)
-    if (s < nk) issue(s, s);
-  for (int kt = 0; kt < nk; ++kt) {
-    // wait for this wave's part of stage kt; with three stages, stage kt + 1 stays in flight
-    if (G::kStages == 3 && kt + 1 < nk)
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(G::kDmaPerWave) : "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    // every wave has its part of stage kt in LDS and is done reading stage kt - 1; a bare
-    // barrier (no fence), so the DMA issued below stays in flight across the next one
-    asm volatile("s_barrier" ::: "memory");
-    if (kt + G::kStages - 1 < nk) issue(kt + G::kStages - 1, (kt + G::kStages - 1) % G::kStages);
-    const uint8_t *st = lds + (kt % G::kStages) * G::kStageBytes;
+  // one step's operands, read from LDS stage k % S by read_step and consumed by compute_step
+  struct Frag {
     half8 ah[2][2], al[2][2], b[2][4], c[2][4];
+    float d[4];
+  };
+  auto read_step = [&](int k, Frag &f) {
+    const uint8_t *st = lds + (k % G::kStages) * G::kStageBytes;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       const int ch = kk ? ch1 : ch0;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        ah[kk][i] = *reinterpret_cast<const half8 *>(st + G::kAHi + ac0 + i * 32 * ROWB + ch);
-        al[kk][i] = *reinterpret_cast<const half8 *>(st + G::kALo + ac0 + i * 32 * ROWB + ch);
+        f.ah[kk][i] = *reinterpret_cast<const half8 *>(st + G::kAHi + ac0 + i * 32 * ROWB + ch);
+        f.al[kk][i] = *reinterpret_cast<const half8 *>(st + G::kALo + ac0 + i * 32 * ROWB + ch);
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        b[kk][j] = *reinterpret_cast<const half8 *>(st + G::kBHi + bc0 + j * 32 * ROWB + ch);
-        if constexpr (MODE == W2) c[kk][j] = *reinterpret_cast<const half8 *>(st + G::kBLo + bc0 + j * 32 * ROWB + ch);
+        f.b[kk][j] = *reinterpret_cast<const half8 *>(st + G::kBHi + bc0 + j * 32 * ROWB + ch);
+        if constexpr (MODE == W2) f.c[kk][j] = *reinterpret_cast<const half8 *>(st + G::kBLo + bc0 + j * 32 * ROWB + ch);
       }
     }
     if constexpr (MODE == WQ8) {
-      float d[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) d[j] = *reinterpret_cast<const float *>(st + G::kScl + (wn * 128 + j * 32 + lr) * 4);
+      for (int j = 0; j < 4; ++j) f.d[j] = *reinterpret_cast<const float *>(st + G::kScl + (wn * 128 + j * 32 + lr) * 4);
+    }
+    // the reads have returned: the barrier after this phase frees the stage for the DMA
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  };
+  auto compute_step = [&](const Frag &f) {
+    if constexpr (MODE == WQ8) {
       // software pipeline over the wave's eight (i, j) blocks: the four MFMAs of block c issue
       // between the sixteen scale FMAs of block c - 1 (two partial-sum registers), so the MFMA
       // pipe runs while the VALU applies the previous block's scale
       f32x16 p[2];
 #pragma unroll
-      for (int c = 0; c <= 8; ++c) {
-        if (c < 8) {
-          const int i = c & 1, j = c >> 1;
-          f32x16 q = WIDE_MFMA(ah[0][i], b[0][j], zero);
-          q = WIDE_MFMA(al[0][i], b[0][j], q);
-          q = WIDE_MFMA(ah[1][i], b[1][j], q);
-          q = WIDE_MFMA(al[1][i], b[1][j], q);
-          p[c & 1] = q;
+      for (int cb = 0; cb <= 8; ++cb) {
+        if (cb < 8) {
+          const int i = cb & 1, j = cb >> 1;
+          f32x16 q = WIDE_MFMA(f.ah[0][i], f.b[0][j], zero);
+          q = WIDE_MFMA(f.al[0][i], f.b[0][j], q);
+          q = WIDE_MFMA(f.ah[1][i], f.b[1][j], q);
+          q = WIDE_MFMA(f.al[1][i], f.b[1][j], q);
+          p[cb & 1] = q;
         }
-        if (c > 0) {
-          const int i = (c - 1) & 1, j = (c - 1) >> 1;
+        if (cb > 0) {
+          const int i = (cb - 1) & 1, j = (cb - 1) >> 1;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[i][j][r] += d[j] * p[(c - 1) & 1][r];
+          for (int r = 0; r < 16; ++r) acc[i][j][r] += f.d[j] * p[(cb - 1) & 1][r];
         }
-        if (c == 0) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 18, 0);  // every operand and scale read of the step
-          __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);   // block 0's MFMAs
-        } else if (c < 8) {
+        if (cb == 0) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // block 0's MFMAs
+        } else if (cb < 8) {
 #pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA of block c
-            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four FMAs of block c - 1
+          for (int q = 0; q < 4; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA of block cb
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four FMAs of block cb - 1
           }
         } else {
           __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);  // block 7's FMAs
@@ -233,18 +237,72 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[i][j] = WIDE_MFMA(ah[kk][i], b[kk][j], acc[i][j]);
+          for (int j = 0; j < 4; ++j) acc[i][j] = WIDE_MFMA(f.ah[kk][i], f.b[kk][j], acc[i][j]);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[i][j] = WIDE_MFMA(al[kk][i], b[kk][j], acc[i][j]);
+          for (int j = 0; j < 4; ++j) acc[i][j] = WIDE_MFMA(f.al[kk][i], f.b[kk][j], acc[i][j]);
         if constexpr (MODE == W2) {
 #pragma unroll
           for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = WIDE_MFMA(ah[kk][i], c[kk][j], acc[i][j]);
+            for (int j = 0; j < 4; ++j) acc[i][j] = WIDE_MFMA(f.ah[kk][i], f.c[kk][j], acc[i][j]);
         }
       }
+    }
+  };
+  // a bare barrier (no fence): the DMA in flight stays in flight across it; no instruction is
+  // scheduled across it, so a phase's MFMAs and FMAs stay in that phase
+  auto barrier = [] {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Ping-pong (WQ8, W1): the two wave groups (waves 0-3 and 4-7, one of each per SIMD) alternate between
+  // reading a step's operands from LDS into registers (read_step) and computing on them
+  // (compute_step), half a step apart: in phase 2k group 0 reads step k while group 1 computes
+  // step k - 1, in phase 2k + 1 group 0 computes step k while group 1 reads it, one barrier after
+  // each phase.  So every SIMD always has one wave issuing MFMAs while the other waits on LDS.
+  // Group 0 also moves the stages: at the start of its read phase of step k it issues the DMA of
+  // step k + S - 1 (S stages; that buffer held step k - 1, which group 1 finished reading in the
+  // phase before), and at the end of its compute phase it waits until its part of step k + 1 is
+  // in LDS, so after the barrier all of it is.  Steps past the last are fetched too (the buffer
+  // unit answers reads past the end with zeros and nothing reads those stages): every wait then
+  // has the same count and no branch separates the MFMAs from it.  A read phase ends when its LDS
+  // reads have returned, so the barrier after it also frees the stage for the DMA that follows.
+  // Both groups run the same loop and pass 2 nk + 2 barriers.
+  constexpr int S = G::kStages, DMA = G::kDmaPerWave;
+  if constexpr (kPingPong) {
+    if (grp == 0) {
+#pragma unroll
+      for (int st = 0; st < S - 1; ++st) issue(st, st);
+    }
+    // steps 0 .. S - 2 in flight: wait for step 0 (a no-op for group 1, which issues no loads)
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA * (S - 2)) : "memory");
+    barrier();
+    if (grp == 1) barrier();  // group 1 runs half a step behind
+    for (int k = 0; k < nk; ++k) {
+      Frag f;
+      if (grp == 0) issue(k + S - 1, (k + S - 1) % S);
+      read_step(k, f);
+      barrier();
+      compute_step(f);
+      // steps k + 1 .. k + S - 1 in flight: wait for step k + 1, which group 0 reads next
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA * (S - 2)) : "memory");
+      barrier();
+    }
+    if (grp == 0) barrier();
+  } else {
+    // two stages, all waves together: step k + 1 in flight while step k is read and consumed
+    issue(0, 0);
+    for (int k = 0; k < nk; ++k) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of step k
+      barrier();  // all of step k in LDS; everyone done reading step k - 1
+      if (k + 1 < nk) issue(k + 1, (k + 1) % S);
+      Frag f;
+      read_step(k, f);
+      compute_step(f);
     }
   }
 
