@@ -1,5 +1,6 @@
-// Prefill GEMM tiles for gfx950 (shared by the k_gemm*.hip translation units): C = A . W^T on MFMA v_mfma_f32_32x32x16_f16, f32 accumulation,
-// weights dequantised into LDS, epilogue fused (bias, residual add, SwiGLU, f16 store).
+// Prefill GEMM tiles for gfx950 (shared by the k_gemm*.hip translation units): C = A . W^T on MFMA
+// v_mfma_f32_16x16x32_f16 (each instruction one 32-deep K chunk), f32 accumulation, weights
+// dequantised into LDS, epilogue fused (bias, residual add, SwiGLU, f16 store).
 //
 // Numeric modes (selected by the caller):
 //   FAST  : A in f16, W dequantised to f16 (RNE); one MFMA pass.
@@ -12,8 +13,8 @@
 // The split modes reproduce f32 arithmetic to ~2^-22 relative per product, which the
 // ill-conditioned synthetic workloads need to stay within the parity bars.
 //
-// Geometry: 256 threads = 4 wave64s in a 2 x 2 arrangement; each wave owns WTM x WTN MFMA
-// blocks of 32 x 32, so a workgroup tile is (64 WTM) x (64 WTN) x BK.  STAGES = 2 ping-pongs
+// Geometry: 256 threads = 4 wave64s in a 2 x 2 arrangement; each wave owns a (32 WTM) x (32 WTN)
+// tile, (2 WTM) x (2 WTN) MFMA blocks of 16 x 16, so a workgroup tile is (64 WTM) x (64 WTN) x BK.  STAGES = 2 ping-pongs
 // two LDS buffers (one barrier per K step, next tile's global loads in flight during the
 // MFMAs); STAGES = 1 uses one buffer with the next tile prefetched into registers.
 #pragma once
@@ -30,7 +31,7 @@ namespace lg {
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 enum Mode { FAST = 0, SPLIT = 1, SPLIT3 = 2 };
 
@@ -224,7 +225,7 @@ __device__ __forceinline__ void tile_coords(int bid, int nblk, int MT, int NT, i
   nt = in / gm;
 }
 
-#define MFMA(a, b, c) __builtin_amdgcn_mfma_f32_32x32x16_f16((a), (b), (c), 0, 0, 0)
+#define MFMA(a, b, c) __builtin_amdgcn_mfma_f32_16x16x32_f16((a), (b), (c), 0, 0, 0)
 
 // Activation tile loader: BMW x BK halves (+ the lo plane), 16-byte chunks per thread, read with
 // buffer loads: the per-thread byte offsets are fixed at init (rows >= M clamped to M - 1, never
@@ -270,111 +271,64 @@ struct ALoad {
   }
 };
 
-// MFMAs of one staged K tile into acc (see the mode table at the top of the file).
+// MFMAs of one staged K tile into acc (see the mode table at the top of the file).  Operand
+// layout of v_mfma_f32_16x16x32_f16: lane l holds row (l % 16) of a 16-row A block and column
+// (l % 16) of a 16-column B block, k = 8 (l / 16) .. + 8 of the 32-deep chunk; the result block
+// holds rows 4 (l / 16) .. + 4 of column l % 16.  Per output element and 32-deep chunk the
+// operation sequence is (acc as f32):
+//   FAST  : acc += A.W
+//   SPLIT : F16 weights: acc += A_hi.W, acc += A_lo.W;  Q8_0 codes: p = A_hi.W, p += A_lo.W,
+//           acc += d * p (d the chunk's Q8_0 block scale, f32 FMA)
+//   SPLIT3: acc += A_hi.W_hi, acc += A_lo.W_hi, acc += A_hi.W_lo
+// gemm_wide.h keeps the same sequences, so both tilings give the same bits.
 template <uint32_t KIND, int MODE, int BK, int WTM, int WTN, int LDK>
-__device__ __forceinline__ void mma_tile(f32x16 (&acc)[WTM][WTN], const _Float16 *As, const _Float16 *Al,
+__device__ __forceinline__ void mma_tile(f32x4 (&acc)[2 * WTM][2 * WTN], const _Float16 *As, const _Float16 *Al,
                                          const _Float16 *Bs, const _Float16 *Bl, const float *Ds, int wm,
                                          int wn, int lane) {
   constexpr bool kSplitA = MODE != FAST;
   constexpr bool kSplitB = MODE == SPLIT3;
   constexpr bool kScaled = MODE == SPLIT && KIND == LG_Q8_0;
-  const int arow = (wm * (32 * WTM) + (lane & 31)) * LDK;
-  const int brow = (wn * (32 * WTN) + (lane & 31)) * LDK;
-  if constexpr (kScaled) {
-    // per Q8_0 block and output block: a 4-MFMA chain into a partial p, then acc += d * p.
-    // One partial is live at a time, so it stays in VGPRs and the scale FMAs of one chain
-    // can issue under the MFMAs of the next.  Same operation order as the variant below.
-    const f32x16 zero = {};
+  constexpr int MI = 2 * WTM, NJ = 2 * WTN;
+  const int arow = (wm * (32 * WTM) + (lane & 15)) * LDK;
+  const int brow = (wn * (32 * WTN) + (lane & 15)) * LDK;
+  const int kl = (lane >> 4) * 8;
+  const f32x4 zero = {};
 #pragma unroll
-    for (int blk = 0; blk < BK / 32; ++blk) {
-      half8 ah[2][WTM], al[2][WTM], b[2][WTN];
+  for (int blk = 0; blk < BK / 32; ++blk) {
+    const int kc = blk * 32 + kl;
+    half8 ah[MI], al[kSplitA ? MI : 1], b[NJ], c[kSplitB ? NJ : 1];
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const int kc = blk * 32 + kk * 16 + (lane >> 5) * 8;
-#pragma unroll
-        for (int j = 0; j < WTN; ++j) b[kk][j] = *reinterpret_cast<const half8 *>(Bs + brow + j * 32 * LDK + kc);
-#pragma unroll
-        for (int i = 0; i < WTM; ++i) {
-          ah[kk][i] = *reinterpret_cast<const half8 *>(As + arow + i * 32 * LDK + kc);
-          al[kk][i] = *reinterpret_cast<const half8 *>(Al + arow + i * 32 * LDK + kc);
-        }
-      }
-      float dj[WTN];
-#pragma unroll
-      for (int j = 0; j < WTN; ++j) dj[j] = Ds[(wn * (32 * WTN) + j * 32 + (lane & 31)) * (BK / 32) + blk];
-#pragma unroll
-      for (int i = 0; i < WTM; ++i)
-#pragma unroll
-        for (int j = 0; j < WTN; ++j) {
-          f32x16 p = MFMA(ah[0][i], b[0][j], zero);
-          p = MFMA(al[0][i], b[0][j], p);
-          p = MFMA(ah[1][i], b[1][j], p);
-          p = MFMA(al[1][i], b[1][j], p);
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[i][j][r] += dj[j] * p[r];
-        }
-    }
-  } else if constexpr (MODE == FAST) {
-    // fragments of step kk+1 are read from LDS while the MFMAs of step kk issue
-    constexpr int KS = BK / 16;
-    half8 ca[WTM], cb[WTN];
-    {
-      const int kc = (lane >> 5) * 8;
-#pragma unroll
-      for (int j = 0; j < WTN; ++j) cb[j] = *reinterpret_cast<const half8 *>(Bs + brow + j * 32 * LDK + kc);
-#pragma unroll
-      for (int i = 0; i < WTM; ++i) ca[i] = *reinterpret_cast<const half8 *>(As + arow + i * 32 * LDK + kc);
+    for (int j = 0; j < NJ; ++j) {
+      b[j] = *reinterpret_cast<const half8 *>(Bs + brow + j * 16 * LDK + kc);
+      if constexpr (kSplitB) c[j] = *reinterpret_cast<const half8 *>(Bl + brow + j * 16 * LDK + kc);
     }
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-      half8 na[WTM], nb[WTN];
-      if (kk + 1 < KS) {
-        const int kc = (kk + 1) * 16 + (lane >> 5) * 8;
-#pragma unroll
-        for (int j = 0; j < WTN; ++j) nb[j] = *reinterpret_cast<const half8 *>(Bs + brow + j * 32 * LDK + kc);
-#pragma unroll
-        for (int i = 0; i < WTM; ++i) na[i] = *reinterpret_cast<const half8 *>(As + arow + i * 32 * LDK + kc);
-      }
-#pragma unroll
-      for (int i = 0; i < WTM; ++i)
-#pragma unroll
-        for (int j = 0; j < WTN; ++j) acc[i][j] = MFMA(ca[i], cb[j], acc[i][j]);
-      if (kk + 1 < KS) {
-        // interleave: one LDS read, then a share of the MFMAs
-        constexpr int R = WTM + WTN, Mf = WTM * WTN;
-#pragma unroll
-        for (int q = 0; q < R; ++q) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x008, Mf / R, 0);
-        }
-#pragma unroll
-        for (int i = 0; i < WTM; ++i) ca[i] = na[i];
-#pragma unroll
-        for (int j = 0; j < WTN; ++j) cb[j] = nb[j];
-      }
+    for (int i = 0; i < MI; ++i) {
+      ah[i] = *reinterpret_cast<const half8 *>(As + arow + i * 16 * LDK + kc);
+      if constexpr (kSplitA) al[i] = *reinterpret_cast<const half8 *>(Al + arow + i * 16 * LDK + kc);
     }
-  } else {
+    if constexpr (kScaled) {
+      float dj[NJ];
 #pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      const int kc = kk * 16 + (lane >> 5) * 8;
-      half8 b[WTN], c[kSplitB ? WTN : 1];
+      for (int j = 0; j < NJ; ++j) dj[j] = Ds[(wn * (32 * WTN) + j * 16 + (lane & 15)) * (BK / 32) + blk];
 #pragma unroll
-      for (int j = 0; j < WTN; ++j) {
-        b[j] = *reinterpret_cast<const half8 *>(Bs + brow + j * 32 * LDK + kc);
-        if constexpr (kSplitB) c[j] = *reinterpret_cast<const half8 *>(Bl + brow + j * 32 * LDK + kc);
-      }
+      for (int j = 0; j < NJ; ++j)
 #pragma unroll
-      for (int i = 0; i < WTM; ++i) {
-        const half8 a = *reinterpret_cast<const half8 *>(As + arow + i * 32 * LDK + kc);
-        half8 l;
-        if constexpr (kSplitA) l = *reinterpret_cast<const half8 *>(Al + arow + i * 32 * LDK + kc);
+        for (int i = 0; i < MI; ++i) {
+          f32x4 p = MFMA(ah[i], b[j], zero);
+          p = MFMA(al[i], b[j], p);
 #pragma unroll
-        for (int j = 0; j < WTN; ++j) {
-          acc[i][j] = MFMA(a, b[j], acc[i][j]);
-          if constexpr (kSplitA) acc[i][j] = MFMA(l, b[j], acc[i][j]);
-          if constexpr (kSplitB) acc[i][j] = MFMA(a, c[j], acc[i][j]);
+          for (int r = 0; r < 4; ++r) acc[i][j][r] += dj[j] * p[r];
         }
-      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          acc[i][j] = MFMA(ah[i], b[j], acc[i][j]);
+          if constexpr (kSplitA) acc[i][j] = MFMA(al[i], b[j], acc[i][j]);
+          if constexpr (kSplitB) acc[i][j] = MFMA(ah[i], c[j], acc[i][j]);
+        }
     }
   }
 }
@@ -438,13 +392,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
   al.init(A, Alo, m0, M, K, t);
   BL bl;
   bl.init(W, wrow, t);
-  f32x16 acc[WTM][WTN];
+  constexpr int MI = 2 * WTM, NJ = 2 * WTN;
+  f32x4 acc[MI][NJ];
 #pragma unroll
-  for (int i = 0; i < WTM; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < WTN; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+      for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.0f;
 
   const int nk = K / BK;
   al.fetch(0);
@@ -492,31 +447,33 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
     }
   }
 
-  // epilogue: acc[i][j] register r -> row (r/4)*8 + (lane/32)*4 + r%4, column lane%32
-  const int col_in = lane & 31;
+  // epilogue: acc[i][j] register r -> row 16 i + 4 (lane / 16) + r, column 16 j + lane % 16 of the
+  // wave tile
+  const int col_in = lane & 15;
 #pragma unroll
-  for (int i = 0; i < WTM; ++i) {
-    // the residual add reads a 32-row block's values first, all in one round trip (rows past M read
+  for (int i = 0; i < MI; ++i) {
+    // the residual add reads a 16-row block's values first, all in one round trip (rows past M read
     // row M - 1 and are not stored)
-    float cv[16][EPI == int(Epi::ADD) ? WTN : 1];
+    float cv[4][EPI == int(Epi::ADD) ? NJ : 1];
     if constexpr (EPI == int(Epi::ADD)) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = min(m0 + wm * (32 * WTM) + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3), M - 1);
+      for (int r = 0; r < 4; ++r) {
+        const int row = min(m0 + wm * (32 * WTM) + i * 16 + (lane >> 4) * 4 + r, M - 1);
 #pragma unroll
-        for (int j = 0; j < WTN; ++j) cv[r][j] = C[int64_t(row) * ldc + nt * BNT + wn * (32 * WTN) + j * 32 + col_in];
+        for (int j = 0; j < NJ; ++j) cv[r][j] = C[int64_t(row) * ldc + nt * BNT + wn * (32 * WTN) + j * 16 + col_in];
       }
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = m0 + wm * (32 * WTM) + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+    for (int r = 0; r < 4; ++r) {
+      const int row = m0 + wm * (32 * WTM) + i * 16 + (lane >> 4) * 4 + r;
       if (row >= M) continue;
       if (EPI == int(Epi::SWIGLU) || EPI == int(Epi::GEGLU)) {
+        // gate block j pairs with up block j + NJ / 2 (the same output columns)
 #pragma unroll
-        for (int jj = 0; jj < WTN / 2; ++jj) {
-          const int col = nt * (BNT / 2) + wn * (16 * WTN) + jj * 32 + col_in;
-          const float g = acc[i][jj][r];
-          const float v = (EPI == int(Epi::SWIGLU) ? silu(g) : gelu_tanh(g)) * acc[i][jj + WTN / 2][r];
+        for (int j = 0; j < NJ / 2; ++j) {
+          const int col = nt * (BNT / 2) + wn * (16 * WTN) + j * 16 + col_in;
+          const float g = acc[i][j][r];
+          const float v = (EPI == int(Epi::SWIGLU) ? silu(g) : gelu_tanh(g)) * acc[i][j + NJ / 2][r];
           _Float16 h, hl;
           split_f16(v, h, hl);
           C16[int64_t(row) * ldc + col] = h;
@@ -524,8 +481,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < WTN; ++j) {
-          const int col = nt * BNT + wn * (32 * WTN) + j * 32 + col_in;
+        for (int j = 0; j < NJ; ++j) {
+          const int col = nt * BNT + wn * (32 * WTN) + j * 16 + col_in;
           float v = acc[i][j][r];
           if (EPI == int(Epi::F32)) {
             if (bias) v += bias[col];

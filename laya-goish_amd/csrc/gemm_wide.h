@@ -2,26 +2,27 @@
 // and W read from its prefill copy (DevMatrix::pc, pcl, pcs), written once at upload so that
 // every operand byte reaches LDS by LDS-DMA (buffer_load ... lds, 16 bytes a lane) with no
 // register staging and no conversion.  Three weight forms (MODE):
-//   WQ8: Q8_0 -- codes as f16 (exact) [N][K] and block scales as f32 [K/32][N].  Per 32 x 32
-//        output block and Q8_0 block the partial sum is one chain of four MFMAs (A hi and lo
-//        against the codes, two 16-deep k halves), then acc += d * partial in f32.
-//   W1 : F16 weights [N][K] (the weights themselves, no copy): per 16-deep k chunk
+//   WQ8: Q8_0 -- codes as f16 (exact) [N][K] and block scales as f32 [K/32][N].  Per 16 x 16
+//        output block and Q8_0 block the partial sum is a chain of two MFMAs (A hi, then A lo,
+//        against the codes), then acc += d * partial in f32.
+//   W1 : F16 weights [N][K] (the weights themselves, no copy): per 32-deep k chunk
 //        acc += A_hi . W, then acc += A_lo . W.
 //   W2 : Q4_K / Q6_K -- the dequantised f32 weight split into f16 hi and lo planes [N][K]:
-//        per 16-deep k chunk acc += A_hi . W_hi, A_lo . W_hi, A_hi . W_lo.
+//        per 32-deep k chunk acc += A_hi . W_hi, A_lo . W_hi, A_hi . W_lo.
 // Each mode keeps the per-element operation order of the 128 x 128 tiles in gemm_tiles.h, so
-// both give the same bits (all on v_mfma_f32_32x32x16_f16 with f32 accumulation).
+// both give the same bits (all on v_mfma_f32_16x16x32_f16 with f32 accumulation: one
+// instruction per 32-deep chunk).
 //
 // Geometry: 512 threads = 8 wave64s (2 per SIMD), workgroup tile 256 x 256, K steps of 32.
 // WQ8 and W1 keep three LDS stages (stage k + 2 in flight while stage k is consumed), W2 two
 // (its stage holds four planes).  Wave w owns rows 64 (w / 2) .. + 64 and columns
-// 128 (w % 2) .. + 128 of the tile (2 x 4 MFMA blocks).  With three stages the two wave groups
+// 128 (w % 2) .. + 128 of the tile (4 x 8 MFMA blocks of 16 x 16).  With three stages the two wave groups
 // of a workgroup run half a step apart (ping-pong, below), one barrier per half step; W2 runs
 // all eight waves in step, one barrier per step (measured faster for its two stages).
 //
 // LDS rows are 64 bytes (four 16-byte chunks); logical chunk c of row r sits in slot
-// c ^ ((r >> 2) & 3), so the 16 lanes of each quarter of an operand read fall in 16 distinct
-// 16-byte bank groups.  The DMA side writes whole 1 KiB blocks: lane L of a block fetches the
+// c ^ ((r >> 2) & 3), so the 16 lanes of each quarter of an operand read (16 rows, one chunk)
+// fall in 16 distinct 16-byte bank groups.  The DMA side writes whole 1 KiB blocks: lane L of a block fetches the
 // global chunk that belongs in its slot.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -34,7 +35,7 @@ namespace lg {
 namespace wide {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 enum Mode { WQ8 = 0, W1 = 1, W2 = 2 };
 
@@ -58,13 +59,13 @@ struct Geo {
 
 __device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
 
-#define WIDE_MFMA(a, b, c) __builtin_amdgcn_mfma_f32_32x32x16_f16((a), (b), (c), 0, 0, 0)
+#define WIDE_MFMA(a, b, c) __builtin_amdgcn_mfma_f32_16x16x32_f16((a), (b), (c), 0, 0, 0)
 
 __device__ __forceinline__ float silu_f(float g) { return g * (1.0f / (1.0f + __expf(-g))); }
 
 // EPI: Epi values (F32, ADD, SWIGLU).  For SWIGLU the workgroup's 256 weight rows are 128 gate
-// rows and the 128 matching up rows: wave column wn holds gate rows in its blocks 0, 1 and the
-// up rows of the same output columns in blocks 2, 3.
+// rows and the 128 matching up rows: wave column wn holds gate rows in its column blocks 0-3 and
+// the up rows of the same output columns in blocks 4-7.
 template <int EPI, int MODE>
 __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
     const _Float16 *__restrict__ A, const _Float16 *__restrict__ Alo, int M, int K,
@@ -155,99 +156,92 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
 #endif
   };
 
-  f32x16 acc[2][4];
+  f32x4 acc[4][8];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 8; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+      for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.0f;
 
-  // operand read offsets: row (lane & 31) of each 32-row block, chunk 2 kk + (lane >> 5)
-  const int lr = lane & 31, sw = swz(lr);
-  const int ac0 = (wm * 64 + lr) * ROWB, bc0 = (wn * 128 + lr) * ROWB;
-  const int ch0 = ((0 + (lane >> 5)) ^ sw) * 16, ch1 = ((2 + (lane >> 5)) ^ sw) * 16;
-  const f32x16 zero = {};
+  // operand reads: lane l takes row (l % 16) of each 16-row block and chunk l / 16 of its 64-byte
+  // row; every block starts at a multiple of 16 rows, so the slot swizzle depends on the lane only
+  const int lr = lane & 15;
+  const int ach = ((lane >> 4) ^ swz(lr)) * 16;
+  const int ac0 = (wm * 64 + lr) * ROWB + ach, bc0 = (wn * 128 + lr) * ROWB + ach;
+  const f32x4 zero = {};
   // one step's operands, read from LDS stage k % S by read_step and consumed by compute_step
   struct Frag {
-    half8 ah[2][2], al[2][2], b[2][4], c[2][4];
-    float d[4];
+    half8 ah[4], al[4], b[8], c[8];
+    float d[8];
   };
   auto read_step = [&](int k, Frag &f) {
     const uint8_t *st = lds + (k % G::kStages) * G::kStageBytes;
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int ch = kk ? ch1 : ch0;
+    for (int i = 0; i < 4; ++i) {
+      f.ah[i] = *reinterpret_cast<const half8 *>(st + G::kAHi + ac0 + i * 16 * ROWB);
+      f.al[i] = *reinterpret_cast<const half8 *>(st + G::kALo + ac0 + i * 16 * ROWB);
+    }
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        f.ah[kk][i] = *reinterpret_cast<const half8 *>(st + G::kAHi + ac0 + i * 32 * ROWB + ch);
-        f.al[kk][i] = *reinterpret_cast<const half8 *>(st + G::kALo + ac0 + i * 32 * ROWB + ch);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        f.b[kk][j] = *reinterpret_cast<const half8 *>(st + G::kBHi + bc0 + j * 32 * ROWB + ch);
-        if constexpr (MODE == W2) f.c[kk][j] = *reinterpret_cast<const half8 *>(st + G::kBLo + bc0 + j * 32 * ROWB + ch);
-      }
+    for (int j = 0; j < 8; ++j) {
+      f.b[j] = *reinterpret_cast<const half8 *>(st + G::kBHi + bc0 + j * 16 * ROWB);
+      if constexpr (MODE == W2) f.c[j] = *reinterpret_cast<const half8 *>(st + G::kBLo + bc0 + j * 16 * ROWB);
     }
     if constexpr (MODE == WQ8) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) f.d[j] = *reinterpret_cast<const float *>(st + G::kScl + (wn * 128 + j * 32 + lr) * 4);
+      for (int j = 0; j < 8; ++j) f.d[j] = *reinterpret_cast<const float *>(st + G::kScl + (wn * 128 + j * 16 + lr) * 4);
     }
     // the reads have returned: the barrier after this phase frees the stage for the DMA
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   };
   auto compute_step = [&](const Frag &f) {
     if constexpr (MODE == WQ8) {
-      // software pipeline over the wave's eight (i, j) blocks: the four MFMAs of block c issue
-      // between the sixteen scale FMAs of block c - 1 (two partial-sum registers), so the MFMA
-      // pipe runs while the VALU applies the previous block's scale
-      f32x16 p[2];
+      // software pipeline over the wave's eight column blocks j: the eight MFMAs of column j (the
+      // hi then lo chains of its four row blocks, interleaved) issue between the sixteen scale
+      // FMAs of column j - 1 (two sets of four partial sums)
+      f32x4 p[2][4];
 #pragma unroll
-      for (int cb = 0; cb <= 8; ++cb) {
-        if (cb < 8) {
-          const int i = cb & 1, j = cb >> 1;
-          f32x16 q = WIDE_MFMA(f.ah[0][i], f.b[0][j], zero);
-          q = WIDE_MFMA(f.al[0][i], f.b[0][j], q);
-          q = WIDE_MFMA(f.ah[1][i], f.b[1][j], q);
-          q = WIDE_MFMA(f.al[1][i], f.b[1][j], q);
-          p[cb & 1] = q;
+      for (int j = 0; j <= 8; ++j) {
+        if (j < 8) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) p[j & 1][i] = WIDE_MFMA(f.ah[i], f.b[j], zero);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) p[j & 1][i] = WIDE_MFMA(f.al[i], f.b[j], p[j & 1][i]);
         }
-        if (cb > 0) {
-          const int i = (cb - 1) & 1, j = (cb - 1) >> 1;
+        if (j > 0) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[i][j][r] += f.d[j] * p[(cb - 1) & 1][r];
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[i][j - 1][r] += f.d[j - 1] * p[(j - 1) & 1][i][r];
         }
-        if (cb == 0) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // block 0's MFMAs
-        } else if (cb < 8) {
+        if (j == 0) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // column 0's MFMAs
+        } else if (j < 8) {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA of block cb
-            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four FMAs of block cb - 1
+          for (int q = 0; q < 8; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA of column j
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // two FMAs of column j - 1
           }
         } else {
-          __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);  // block 7's FMAs
+          __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);  // column 7's FMAs
         }
       }
     } else {
-      // per element: for each 16-deep chunk kk, A_hi.W_hi, A_lo.W_hi (, A_hi.W_lo); the
-      // eight blocks of a wave interleave, so no MFMA waits on the one before it
+      // per element: A_hi.W_hi, A_lo.W_hi (, A_hi.W_lo); the 32 blocks of a wave interleave, so
+      // no MFMA waits on the one before it
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int j = 0; j < 8; ++j) acc[i][j] = WIDE_MFMA(f.ah[i], f.b[j], acc[i][j]);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[i][j] = WIDE_MFMA(f.ah[kk][i], f.b[kk][j], acc[i][j]);
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int j = 0; j < 8; ++j) acc[i][j] = WIDE_MFMA(f.al[i], f.b[j], acc[i][j]);
+      if constexpr (MODE == W2) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) acc[i][j] = WIDE_MFMA(f.al[kk][i], f.b[kk][j], acc[i][j]);
-        if constexpr (MODE == W2) {
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = WIDE_MFMA(f.ah[kk][i], f.c[kk][j], acc[i][j]);
-        }
+          for (int j = 0; j < 8; ++j) acc[i][j] = WIDE_MFMA(f.ah[i], f.c[j], acc[i][j]);
       }
     }
   };
@@ -306,18 +300,19 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
     }
   }
 
-  // epilogue: acc[i][j] register r -> row (r/4)*8 + (lane/32)*4 + r%4, column lane%32
+  // epilogue: acc[i][j] register r -> row 16 i + 4 (lane / 16) + r, column 16 j + lane % 16 of the
+  // wave tile
   if constexpr (kGlu) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < 4; ++i) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * 64 + i * 16 + (lane >> 4) * 4 + r;
         if (row >= M) continue;
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          const int col = nt * (BN / 2) + wn * 64 + jj * 32 + lr;
-          const float v = silu_f(acc[i][jj][r]) * acc[i][jj + 2][r];
+        for (int j = 0; j < 4; ++j) {
+          const int col = nt * (BN / 2) + wn * 64 + j * 16 + lr;
+          const float v = silu_f(acc[i][j][r]) * acc[i][j + 4][r];
           _Float16 h, hl;
           split_f16(v, h, hl);
           C16[int64_t(row) * ldc + col] = h;
@@ -326,29 +321,29 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
       }
     }
   } else {
-    float bv[4];
+    float bv[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) bv[j] = bias ? bias[nt * BN + wn * 128 + j * 32 + lr] : 0.0f;
+    for (int j = 0; j < 8; ++j) bv[j] = bias ? bias[nt * BN + wn * 128 + j * 16 + lr] : 0.0f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      // the residual add reads a 32-row block's 64 values per lane in one round trip (rows past M
+    for (int i = 0; i < 4; ++i) {
+      // the residual add reads a 16-row block's 32 values per lane in one round trip (rows past M
       // read row M - 1 and are not stored), then adds and stores
-      float cv[16][4];
+      float cv[4][8];
       if constexpr (EPI == int(Epi::ADD)) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = min(m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3), M - 1);
+        for (int r = 0; r < 4; ++r) {
+          const int row = min(m0 + wm * 64 + i * 16 + (lane >> 4) * 4 + r, M - 1);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) cv[r][j] = C[int64_t(row) * ldc + nt * BN + wn * 128 + j * 32 + lr];
+          for (int j = 0; j < 8; ++j) cv[r][j] = C[int64_t(row) * ldc + nt * BN + wn * 128 + j * 16 + lr];
         }
       }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * 64 + i * 16 + (lane >> 4) * 4 + r;
         if (row >= M) continue;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int col = nt * BN + wn * 128 + j * 32 + lr;
+        for (int j = 0; j < 8; ++j) {
+          const int col = nt * BN + wn * 128 + j * 16 + lr;
           float v = acc[i][j][r];
           if (bias) v += bv[j];
           if constexpr (EPI == int(Epi::F32)) C[int64_t(row) * ldc + col] = v;
