@@ -54,7 +54,6 @@ struct Geo {
   static constexpr int kStageBytes = kScl + (kScales ? BN * 4 : 0);
   static constexpr int kStages = MODE == W2 ? 2 : 3;
   static constexpr int kLdsBytes = kStages * kStageBytes;  // WQ8 150,528; W1 147,456; W2 131,072
-  static constexpr int kDmaPerWave = (kStages == 3 ? 4 : 2) * (2 + kBPlanes);  // per stage and moving wave (wave 0: + 1 scale block)
 };
 
 __device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
@@ -117,43 +116,55 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
   if constexpr (MODE == W2) rc = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(Wl), 0, wbytes, kBufferFlags);
   if constexpr (MODE == WQ8)
     rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(Ws), 0, uint32_t(N) * uint32_t(K / 32) * 4u, kBufferFlags);
-  // Ping-pong (three-stage modes, below): group 0 (waves 0-3) moves every block, wave w the blocks
-  // w, w + 4, w + 8, w + 12 of each plane.  Two-stage mode (W2): all eight waves, wave w the
-  // blocks w and w + 8.  Block b + step q holds the rows of block b shifted by 64 q / 4 ... 16 q,
-  // which for A and for every weight row map (wrow) is a wave-uniform byte offset: the buffer
-  // instruction's scalar offset.  Wave 0 also moves the scale block.
+  // Every wave moves the blocks wave and wave + 8 of each plane (A hi, A lo, W hi, W lo); block
+  // w + 8 holds the rows of block w shifted by 128, which for A and for every weight row map
+  // (wrow) is a wave-uniform byte offset: the buffer instruction's scalar offset.  Wave 0 also
+  // moves the scale block.
   constexpr bool kPingPong = G::kStages == 3;
-  constexpr int NB = kPingPong ? 4 : 2, BSTEP = kPingPong ? 4 : 8;  // blocks per wave, block stride
-  const int grp = wave >> 2, wb = kPingPong ? (wave & 3) : wave;
+  const int grp = wave >> 2;
   uint32_t aoff, boff;
   {
-    const int slot = wb * 64 + lane;  // 16-byte slot inside a plane (block wb)
+    const int slot = wave * 64 + lane;  // 16-byte slot inside a plane (block wave)
     const int row = slot >> 2, c = (slot & 3) ^ swz(row);
     aoff = uint32_t(m0 + row) * uint32_t(K) * 2u + uint32_t(c) * 16u;
     boff = uint32_t(wrow(row)) * uint32_t(K) * 2u + uint32_t(c) * 16u;
   }
   const uint32_t soff = uint32_t(wrow(4 * lane)) * 4u;  // four consecutive weight rows' scales
   const int nk = K / BK;
-  auto issue = [&](int kt, int st) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef __attribute__((address_space(3))) void *lds_ptr;
+#endif
+  // one DMA instruction of step kt into stage st: plane pl (0 A hi, 1 A lo, 2 W hi, 3 W lo) of
+  // block wave + 8 h
+  auto dma = [&](int kt, int st, int pl, int h) {
 #if defined(__HIP_DEVICE_COMPILE__)
     // device pass only: with a run-time voffset this builtin keeps the host pass from
     // emitting the kernel's launch stub (the host never runs kernel bodies)
-    typedef __attribute__((address_space(3))) void *lds_ptr;
     uint8_t *base = lds + st * G::kStageBytes;
-#pragma unroll
-    for (int h = 0; h < NB; ++h) {
-      const int blk = (wb + BSTEP * h) * 1024, dr = 16 * BSTEP * h;  // block, row shift
-      const uint32_t ka = uint32_t(kt * BK * 2) + uint32_t(dr) * uint32_t(K) * 2u;
-      const uint32_t kb = uint32_t(kt * BK * 2) + uint32_t(wrow(dr) - wrow(0)) * uint32_t(K) * 2u;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr)(base + G::kAHi + blk), 16, aoff, ka, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, (lds_ptr)(base + G::kALo + blk), 16, aoff, ka, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr)(base + G::kBHi + blk), 16, boff, kb, 0, 0);
-      if constexpr (MODE == W2)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (lds_ptr)(base + G::kBLo + blk), 16, boff, kb, 0, 0);
-    }
-    if constexpr (MODE == WQ8)
-      if (wave == 0) __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(base + G::kScl), 16, soff, kt * N * 4, 0, 0);
+    const int blk = (wave + 8 * h) * 1024, dr = 128 * h;  // block, row shift
+    const uint32_t ka = uint32_t(kt * BK * 2) + uint32_t(dr) * uint32_t(K) * 2u;
+    const uint32_t kb = uint32_t(kt * BK * 2) + uint32_t(wrow(dr) - wrow(0)) * uint32_t(K) * 2u;
+    if (pl == 0) __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr)(base + G::kAHi + blk), 16, aoff, ka, 0, 0);
+    if (pl == 1) __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, (lds_ptr)(base + G::kALo + blk), 16, aoff, ka, 0, 0);
+    if (pl == 2) __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr)(base + G::kBHi + blk), 16, boff, kb, 0, 0);
+    if (pl == 3) __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (lds_ptr)(base + G::kBLo + blk), 16, boff, kb, 0, 0);
 #endif
+  };
+  auto dma_scale = [&](int kt, int st) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    if constexpr (MODE == WQ8)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(lds + st * G::kStageBytes + G::kScl), 16, soff,
+                                               kt * N * 4, 0, 0);
+#endif
+  };
+  constexpr int NPL = 2 + G::kBPlanes;  // planes per stage
+  // this wave's part of step kt: 2 NPL instructions (wave 0: + the scale block)
+  auto issue = [&](int kt, int st) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int pl = 0; pl < NPL; ++pl) dma(kt, st, pl, h);
+    if (wave == 0) dma_scale(kt, st);
   };
 
   f32x4 acc[4][8];
@@ -194,7 +205,9 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
     // the reads have returned: the barrier after this phase frees the stage for the DMA
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   };
-  auto compute_step = [&](const Frag &f) {
+  // dkt >= 0: the six A/W DMA instructions of this wave's part of step dkt (into stage dst) issue
+  // one per column block j = 1 .. 6, between the MFMAs
+  auto compute_step = [&](const Frag &f, int dkt, int dst) {
     if constexpr (MODE == WQ8) {
       // software pipeline over the wave's eight column blocks j: the eight MFMAs of column j (the
       // hi then lo chains of its four row blocks, interleaved) issue between the sixteen scale
@@ -214,6 +227,8 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[i][j - 1][r] += f.d[j - 1] * p[(j - 1) & 1][i][r];
         }
+        const bool dm = dkt >= 0 && j >= 1 && j <= 6;
+        if (dm) dma(dkt, dst, (j - 1) % 3, (j - 1) / 3);
         if (j == 0) {
           __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // column 0's MFMAs
         } else if (j < 8) {
@@ -221,14 +236,31 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
           for (int q = 0; q < 8; ++q) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA of column j
             __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // two FMAs of column j - 1
+            if (dm && q == 3) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one DMA
           }
         } else {
           __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);  // column 7's FMAs
         }
       }
+    } else if constexpr (MODE == W1) {
+      // per element: A_hi.W, then A_lo.W; column by column, the four row blocks' chains interleaved
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i][j] = WIDE_MFMA(f.ah[i], f.b[j], acc[i][j]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i][j] = WIDE_MFMA(f.al[i], f.b[j], acc[i][j]);
+        const bool dm = dkt >= 0 && j >= 1 && j <= 6;
+        if (dm) {
+          dma(dkt, dst, (j - 1) % 3, (j - 1) / 3);
+          __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        }
+      }
     } else {
-      // per element: A_hi.W_hi, A_lo.W_hi (, A_hi.W_lo); the 32 blocks of a wave interleave, so
-      // no MFMA waits on the one before it
+      // per element: A_hi.W_hi, A_lo.W_hi, A_hi.W_lo; the 32 blocks of a wave interleave, so no
+      // MFMA waits on the one before it
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -237,7 +269,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[i][j] = WIDE_MFMA(f.al[i], f.b[j], acc[i][j]);
-      if constexpr (MODE == W2) {
+      {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -253,37 +285,53 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // Ping-pong (WQ8, W1): the two wave groups (waves 0-3 and 4-7, one of each per SIMD) alternate between
-  // reading a step's operands from LDS into registers (read_step) and computing on them
+  // Ping-pong (WQ8, W1): the two wave groups (waves 0-3 and 4-7, one of each per SIMD) alternate
+  // between reading a step's operands from LDS into registers (read_step) and computing on them
   // (compute_step), half a step apart: in phase 2k group 0 reads step k while group 1 computes
   // step k - 1, in phase 2k + 1 group 0 computes step k while group 1 reads it, one barrier after
-  // each phase.  So every SIMD always has one wave issuing MFMAs while the other waits on LDS.
-  // Group 0 also moves the stages: at the start of its read phase of step k it issues the DMA of
-  // step k + S - 1 (S stages; that buffer held step k - 1, which group 1 finished reading in the
-  // phase before), and at the end of its compute phase it waits until its part of step k + 1 is
-  // in LDS, so after the barrier all of it is.  Steps past the last are fetched too (the buffer
-  // unit answers reads past the end with zeros and nothing reads those stages): every wait then
-  // has the same count and no branch separates the MFMAs from it.  A read phase ends when its LDS
-  // reads have returned, so the barrier after it also frees the stage for the DMA that follows.
-  // Both groups run the same loop and pass 2 nk + 2 barriers.
-  constexpr int S = G::kStages, DMA = G::kDmaPerWave;
+  // each phase.  So every SIMD always has one wave issuing MFMAs while the other waits on LDS, and
+  // the reading wave runs at the higher issue priority, so its LDS reads overlap the MFMAs.
+  // DMA, interleaved with the MFMAs of the compute phases so that no phase waits on the buffer
+  // unit: group 0 moves its part of step k + 2 while computing step k (phase 2k + 1), group 1 its
+  // part of step k + 3 while computing step k (phase 2k + 2); wave 0 moves the scales of step
+  // k + 2 when it starts reading step k (phase 2k).  Each of those stages last held a step both
+  // groups have finished reading (k - 1 and k), and a read phase ends when its LDS reads have
+  // returned, so the barrier after it also frees the stage.  Every wave ends each phase waiting
+  // for all but its last six DMA instructions: that completes group 0's part of step k + 1 by the
+  // end of phase 2k + 1 and group 1's by the end of phase 2k + 1 (its read of step k), before
+  // group 0 reads step k + 1 in phase 2k + 2.  Steps past the last are fetched too (the buffer
+  // unit answers reads past the end with zeros and nothing reads those stages), so every wait has
+  // the same count and no branch separates the MFMAs from the DMA.  Both groups run the same loop
+  // and pass 2 nk + 2 barriers.
+  constexpr int S = G::kStages;
   if constexpr (kPingPong) {
-    if (grp == 0) {
+    static_assert(S == 3 && NPL == 3, "ping-pong: three stages of three planes");
+    // prologue: both groups' parts of steps 0 and 1, group 1's part of step 2
+    issue(0, 0);
+    issue(1, 1);
+    if (grp == 1) {
 #pragma unroll
-      for (int st = 0; st < S - 1; ++st) issue(st, st);
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl) dma(2, 2, pl, h);
+      asm volatile("s_waitcnt vmcnt(12)" ::: "memory");  // step 0
+    } else if (MODE == WQ8 && wave == 0) {
+      asm volatile("s_waitcnt vmcnt(7)" ::: "memory");  // step 0 and its scales
+    } else {
+      asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
     }
-    // steps 0 .. S - 2 in flight: wait for step 0 (a no-op for group 1, which issues no loads)
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA * (S - 2)) : "memory");
     barrier();
     if (grp == 1) barrier();  // group 1 runs half a step behind
     for (int k = 0; k < nk; ++k) {
       Frag f;
-      if (grp == 0) issue(k + S - 1, (k + S - 1) % S);
+      __builtin_amdgcn_s_setprio(2);
+      if (wave == 0) dma_scale(k + 2, (k + 2) % S);
       read_step(k, f);
+      asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
       barrier();
-      compute_step(f);
-      // steps k + 1 .. k + S - 1 in flight: wait for step k + 1, which group 0 reads next
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(DMA * (S - 2)) : "memory");
+      __builtin_amdgcn_s_setprio(0);
+      compute_step(f, k + 2 + grp, (k + 2 + grp) % S);
+      asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
       barrier();
     }
     if (grp == 0) barrier();
@@ -296,7 +344,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
       if (k + 1 < nk) issue(k + 1, (k + 1) % S);
       Frag f;
       read_step(k, f);
-      compute_step(f);
+      compute_step(f, -1, 0);
     }
   }
 
