@@ -442,20 +442,25 @@ __global__ __launch_bounds__(kT) void argmax_stage1(const float *__restrict__ v,
   }
 }
 
+// One wave: lane i takes partial i (nparts <= 64, one load round trip), then a butterfly of the same
+// merge rule (larger value, then smaller index; a partial without an index loses).  The rule is a
+// total order, so the order of the merges does not change the result.
 __global__ __launch_bounds__(64) void argmax_stage2(const float *__restrict__ pv,
                                                     const int32_t *__restrict__ pi, int nparts,
                                                     int32_t *__restrict__ out) {
-  if (threadIdx.x != 0) return;
-  float bv = -INFINITY;
-  int bi = -1;
-  for (int i = 0; i < nparts; ++i) {
-    if (pi[i] < 0) continue;
-    if (bi < 0 || pv[i] > bv || (pv[i] == bv && pi[i] < bi)) {
-      bv = pv[i];
-      bi = pi[i];
+  const int lane = threadIdx.x;
+  float bv = lane < nparts ? pv[lane] : -INFINITY;
+  int bi = lane < nparts ? pi[lane] : -1;
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const float ov = __shfl_xor(bv, m);
+    const int oi = __shfl_xor(bi, m);
+    if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
+      bv = ov;
+      bi = oi;
     }
   }
-  out[0] = bi >= 0 && bv > -INFINITY && bv < INFINITY ? bi : -1;  // -1: no finite maximum
+  if (lane == 0) out[0] = bi >= 0 && bv > -INFINITY && bv < INFINITY ? bi : -1;  // -1: no finite maximum
 }
 
 __global__ void cvt_f16_kernel(const float *__restrict__ x, int64_t n, _Float16 *__restrict__ y,
@@ -547,7 +552,7 @@ void launch_option_scores(const float *logits, int R, int k, float temperature, 
 void launch_argmax(const float *logits, int V, int32_t *out, float *part_v, int32_t *part_i,
                    hipStream_t st) {
   LG_REQUIRE(V > 0, "argmax: empty");
-  const int parts = 64;
+  const int parts = 64;  // one per lane of argmax_stage2's wave
   hipLaunchKernelGGL(argmax_stage1, dim3(parts), dim3(kT), 0, st, logits, V, part_v, part_i);
   hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(64), 0, st, part_v, part_i, parts, out);
   HIP_CHECK(hipGetLastError());

@@ -193,6 +193,34 @@ def test_decode_after_canceled_forward(pair, lh):
         eng.seq_free(q)
 
 
+@pytest.mark.parametrize("zeroed", [0, 100])
+def test_decode_argmax_ties_keep_the_first_index(lh, po, zeroed):
+    """The decode's full-vocab argmax keeps the first maximum (src/models/openthai/decision.rs:330-335).
+    Every head row set to row 1 makes all logits tie bit for bit, so each step emits token 0; with rows
+    0..99 zeroed as well, the first tied maximum is 0 or 100 by the sign of the shared logit."""
+    img = lh.SynthImage("tiny-f16", seed=3)  # keeps the image's memory alive while it is copied
+    arr = img.array().copy()
+    og = po.Gguf(arr)
+    kind, (cols, rows), _ = og.tensor("output.weight")
+    assert kind == 1  # F16
+    off = og.offset("output.weight")
+    head = arr[off:off + rows * cols * 2].reshape(rows, cols * 2)
+    head[:] = head[1]
+    head[:zeroed] = 0
+    eng = lh.Engine(lh.Gguf.from_bytes(arr), kv_tokens=1024)
+    s = eng.seq_create()
+    eng.forward(s, [3, 4, 5], [], OPTIONS)
+    toks, logits = eng.decode(s, 6, 5, want_logits=True)
+    for i in range(5):
+        assert int(toks[i]) == int(np.argmax(logits[i]))
+        if zeroed == 0:
+            assert int(toks[i]) == 0 and (logits[i] == logits[i][0]).all()
+        else:
+            assert int(toks[i]) == (100 if logits[i][100] > 0 else 0)
+    eng.seq_free(s)
+    eng.close()
+
+
 def test_errors_are_reported(pair, lh):
     preset, eng, om = pair
     s = eng.seq_create()
