@@ -31,11 +31,11 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int P = 64;  // tokens per page
 
-#define MFMA(a, b, c) __builtin_amdgcn_mfma_f32_32x32x16_f16((a), (b), (c), 0, 0, 0)
+#define MFMA(a, b, c) __builtin_amdgcn_mfma_f32_16x16x32_f16((a), (b), (c), 0, 0, 0)
 
 // Prefill.  Work item: (tile group, kv head kh, head block hb).  A tile group is <= T
 // consecutive 32-query tiles of one sequence, a head block GB consecutive query heads of kh's
@@ -43,23 +43,32 @@ constexpr int P = 64;  // tokens per page
 // group, so all W = GB * T waves read the same K/V pages: each page passes through LDS once per
 // workgroup.  Pages are copied global -> LDS by LDS-DMA loads (16 bytes a lane, no registers),
 // double-buffered: page kt + 1 is in flight while page kt is consumed, one barrier per page.
-// LDS rows carry one 16-byte pad slot, so each 16 lanes of an MFMA operand read hit 16 distinct
-// 16-byte bank groups.
 //
-// S^T = K . Q^T on MFMA 32x32x16 f16, keys as rows and queries as columns: a lane owns one
-// query column and the online softmax reduces over its own registers plus one lane swap.  Lane
-// qi feeds key row kb * 32 + swap23(qi) (bits 2 and 3 of qi exchanged), which makes the eight
-// scores of register group j of a lane the consecutive keys kb * 32 + 16 j + 8 hl + 0..7: the
-// eight keys its P^T operand of O^T = V^T . P^T takes against one 16-byte run of a V row.
+// S^T = K . Q^T on MFMA 16x16x32 f16 (one instruction per 32-deep chunk of the head dim), keys as
+// rows and queries as columns, in 16 x 16 blocks: a wave's 32 queries are two query blocks qb, a
+// page's 64 keys four key blocks (ck, h) of two 32-key chunks ck.  Lane l feeds row r = l % 16 of a
+// key block, and row r of block (ck, h) is key ck * 32 + 8 (r / 4) + 4 h + r % 4: the result leaves
+// lane l (query l % 16 of its block) with keys ck * 32 + 8 g + 4 h + 0..3, g = l / 16, so its scores
+// of (ck, 0) and (ck, 1) together are the eight keys ck * 32 + 8 g + 0..7 that its P^T operand of
+// O^T = V^T . P^T takes against one 16-byte run of a V row.  A query's 64 scores of a page sit in the
+// four lanes l % 16 + 16 g; the online softmax reduces over them with two lane swaps.  Each wave
+// runs eight independent score chains and sixteen output chains, so no MFMA waits on the one
+// before it.
+// LDS: K rows unpadded, the 16-byte chunk x of key row R at slot x ^ kswz(R), so the sixteen rows
+// an operand read takes fall in distinct 16-byte bank groups; V rows (one dim, 64 keys) carry one
+// pad slot for the same reason.
 // NPL = 2: split cache, queries and P as hi/lo planes, three MFMAs a product (hi.hi + lo.hi +
 // hi.lo); NPL = 1: f16 cache and queries, one MFMA.
-__device__ __forceinline__ int swap23(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
+template <int HD>
+__device__ __forceinline__ int kswz(int row) {
+  return HD == 128 ? ((row & 3) | (((row >> 3) & 3) << 2)) : ((row & 3) | (((row >> 3) & 1) << 2));
+}
 
 template <int HD, int NPL>
 struct PrefillStage {
-  static constexpr int KC = HD / 8, KRS = KC + 1;  // 16-byte chunks per K row, slots per K row
-  static constexpr int VC = P / 8, VRS = VC + 1;   // the same for a V row (one dim, 64 keys)
-  static constexpr int KPL = P * KRS, VPL = HD * VRS;  // slots per plane
+  static constexpr int KC = HD / 8;                // 16-byte chunks per K row (no pad)
+  static constexpr int VC = P / 8, VRS = VC + 1;   // chunks and slots per V row (one dim, 64 keys)
+  static constexpr int KPL = P * KC, VPL = HD * VRS;  // slots per plane
   static_assert(KPL % 64 == 0 && VPL % 64 == 0, "planes fill whole 64-slot blocks");
   static constexpr int KSLOTS = NPL * KPL, SLOTS = NPL * (KPL + VPL);
   static constexpr int BLOCKS = SLOTS / 64;  // one LDS-DMA instruction of one wave per block
@@ -79,7 +88,7 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
     const int32_t *__restrict__ tile_pos0, const int32_t *__restrict__ tile_n,
     _Float16 *__restrict__ out16, _Float16 *__restrict__ out16lo) {
   using S = PrefillStage<HD, NPL>;
-  constexpr int KT = HD / 16, DB = HD / 32;
+  constexpr int NC = HD / 32, DB = HD / 16;  // 32-deep chunks of the head dim, 16-dim output blocks
   constexpr int NI = (S::BLOCKS + W - 1) / W;  // LDS-DMA instructions per wave per page
   __shared__ __align__(16) unsigned char lds[2 * S::BYTES];
 
@@ -92,7 +101,7 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
   const int logical = xcd * per + min(xcd, rem) + blockIdx.x / 8;
   const int grp = logical % ngroups, hsel = logical / ngroups;
   const int kh = hsel / nhb, hb = hsel % nhb;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, qi = lane & 31, hl = lane >> 5;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 15, qg = lane >> 4;
   const int t0 = grp_first[grp], cnt = grp_count[grp];
   const bool active = wave / GB < cnt;
   const int tile = t0 + min(wave / GB, cnt - 1);
@@ -101,8 +110,6 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
   const int seq = tile_seq[t0];  // every tile of a group belongs to one sequence
   const int glast = tile_pos0[t0 + cnt - 1] + tile_n[t0 + cnt - 1] - 1;
   const int qw = hq * HD;
-  const int qpos = pos0 + qi;
-  const bool live = qi < n;
 
   // this lane's byte offset inside the kv head's K (or V) block for each of its DMA slots; pad
   // slots get an offset past the block, which the buffer load turns into zeros without a read
@@ -114,8 +121,8 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
     uint32_t o = kHeadBytes;
     if (b < S::BLOCKS) {
       if (slot < S::KSLOTS) {
-        const int p = slot / S::KPL, r = slot % S::KPL, row = r / S::KRS, x = r % S::KRS;
-        if (x < S::KC) o = uint32_t(((p * P + row) * HD + x * 8) * 2);
+        const int p = slot / S::KPL, r = slot % S::KPL, row = r / S::KC, x = (r % S::KC) ^ kswz<HD>(row);
+        o = uint32_t(((p * P + row) * HD + x * 8) * 2);
       } else {
         const int s2 = slot - S::KSLOTS, p = s2 / S::VPL, r = s2 % S::VPL, d = r / S::VRS, x = r % S::VRS;
         if (x < S::VC) o = uint32_t(((p * HD + d) * P + x * 8) * 2);
@@ -146,24 +153,31 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
     }
   };
 
-  half8 qr[KT], ql[NPL == 2 ? KT : 1];
-  {
-    const int64_t qo = int64_t(row0 + min(qi, n - 1)) * qw + h * HD + hl * 8;
+  // queries qb * 16 + lr of the tile (rows past n repeat row n - 1 and are never stored), the eight
+  // dims 32 c + 8 g .. + 8 of each 32-deep chunk c
+  half8 qr[2][NC], ql[2][NPL == 2 ? NC : 1];
 #pragma unroll
-    for (int t = 0; t < KT; ++t) {
-      qr[t] = *reinterpret_cast<const half8 *>(q16 + qo + 16 * t);
-      if constexpr (NPL == 2) ql[t] = *reinterpret_cast<const half8 *>(q16lo + qo + 16 * t);
+  for (int qb = 0; qb < 2; ++qb) {
+    const int64_t qo = int64_t(row0 + min(qb * 16 + lr, n - 1)) * qw + h * HD + qg * 8;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      qr[qb][c] = *reinterpret_cast<const half8 *>(q16 + qo + 32 * c);
+      if constexpr (NPL == 2) ql[qb][c] = *reinterpret_cast<const half8 *>(q16lo + qo + 32 * c);
     }
   }
-  f32x16 acc[DB];
+  f32x4 acc[2][DB];
 #pragma unroll
-  for (int b = 0; b < DB; ++b)
+  for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[b][r] = 0.0f;
-  float m = -INFINITY, l = 0.0f;
+    for (int b = 0; b < DB; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[qb][b][r] = 0.0f;
+  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
   const int npages = glast / P + 1;
   const int mypages = active ? (pos0 + n - 1) / P + 1 : 0;
-  const int krow = swap23(qi);
+  // this lane's K operand rows: key ck * 32 + 8 (lr / 4) + 4 h + lr % 4 of block (ck, h); their
+  // chunk swizzle depends on lr only
+  const int kr0 = 8 * (lr >> 2) + (lr & 3), ksw = kswz<HD>(kr0);
 
   issue(ptab[0], 0);
   // page-table entry of the page after the one in flight, read one iteration ahead so that no
@@ -182,93 +196,128 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
       const unsigned char *stage = lds + st * S::BYTES;
       const unsigned char *kl_ = stage + S::KPL * 16 * (NPL - 1);  // K lo plane (= hi when NPL 1)
       const unsigned char *vh_ = stage + S::KSLOTS * 16, *vl_ = vh_ + S::VPL * 16 * (NPL - 1);
-      f32x16 s[2];
+      f32x4 s[2][2][2];  // [qb][ck][h]
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+      for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[kb][r] = 0.0f;
-        const int ro = (kb * 32 + krow) * S::KRS + hl;
+        for (int ck = 0; ck < 2; ++ck)
 #pragma unroll
-        for (int t = 0; t < KT; ++t) {
-          const half8 kh8 = lds_half8(stage, ro + 2 * t);
-          if constexpr (NPL == 2) {
-            const half8 kl8 = lds_half8(kl_, ro + 2 * t);
-            s[kb] = MFMA(kh8, qr[t], s[kb]);
-            s[kb] = MFMA(kl8, qr[t], s[kb]);
-            s[kb] = MFMA(kh8, ql[t], s[kb]);
-          } else {
-            s[kb] = MFMA(kh8, qr[t], s[kb]);
+          for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s[qb][ck][hh][r] = 0.0f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int ck = 0; ck < 2; ++ck)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const int slot = (ck * 32 + kr0 + 4 * hh) * S::KC + ((4 * c + qg) ^ ksw);
+            const half8 kh8 = lds_half8(stage, slot);
+            if constexpr (NPL == 2) {
+              const half8 kl8 = lds_half8(kl_, slot);
+#pragma unroll
+              for (int qb = 0; qb < 2; ++qb) {
+                s[qb][ck][hh] = MFMA(kh8, qr[qb][c], s[qb][ck][hh]);
+                s[qb][ck][hh] = MFMA(kl8, qr[qb][c], s[qb][ck][hh]);
+                s[qb][ck][hh] = MFMA(kh8, ql[qb][c], s[qb][ck][hh]);
+              }
+            } else {
+#pragma unroll
+              for (int qb = 0; qb < 2; ++qb) s[qb][ck][hh] = MFMA(kh8, qr[qb][c], s[qb][ck][hh]);
+            }
           }
-        }
-      }
-      // s[kb][8 j + e] <-> key kt * P + kb * 32 + 16 j + 8 hl + e, query qi.  The queries come
-      // pre-multiplied by log2(e) / sqrt(hd), so s is the base-2 logit.  Only a page that reaches
-      // past the tile's first query needs the causal mask; rows past the tile's end (qi >= n)
-      // repeat row n - 1's query and are never stored.
+      // s[qb][ck][h][e] <-> key kt * P + ck * 32 + 8 qg + 4 h + e, query qb * 16 + lr.  The queries
+      // come pre-multiplied by log2(e) / sqrt(hd), so s is the base-2 logit.  Only a page that
+      // reaches past the tile's first query needs the causal mask.
       if (kt * P + P - 1 > pos0) {
-        const int lim = qpos - kt * P - hl * 8;  // mask offsets kb * 32 + 16 j + e above this
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int qb = 0; qb < 2; ++qb) {
+          const int lim = pos0 + qb * 16 + lr - kt * P - 8 * qg;  // mask offsets ck * 32 + 4 h + e above
 #pragma unroll
-          for (int r = 0; r < 16; ++r)
-            if (kb * 32 + (r >> 3) * 16 + (r & 7) > lim) s[kb][r] = -INFINITY;
-      }
-      float mt = -INFINITY;
+          for (int ck = 0; ck < 2; ++ck)
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+            for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, s[kb][r]);
-      mt = fmaxf(mt, __shfl_xor(mt, 32));
-      // A lane's exponent base m moves only when one of its scores exceeds it by more than 8,
-      // so p = 2^(s - m) <= 256; l and acc carry the same base, so out = acc / l is unchanged.
-      // The rescale is skipped unless some lane of the wave moves; the others multiply by
-      // exactly 1, so a query's arithmetic never depends on the other queries of its wave.
-      // Key 0 is visible to every query, so m is finite from the first page on and
-      // 2^(-inf - m) = 0 drops masked keys.
-      const bool grow = mt > m + 8.0f;
-      if (__any(grow)) {
-        const float mn = grow ? mt : m;
-        const float alpha = __builtin_amdgcn_exp2f(m - mn);
-        l *= alpha;
-#pragma unroll
-        for (int b = 0; b < DB; ++b)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[b][r] *= alpha;
-        m = mn;
-      }
-      float rs = 0.0f;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = __builtin_amdgcn_exp2f(s[kb][r] - m);
-          s[kb][r] = p;
-          rs += p;
+              for (int e = 0; e < 4; ++e)
+                if (ck * 32 + 4 * hh + e > lim) s[qb][ck][hh][e] = -INFINITY;
         }
-      rs += __shfl_xor(rs, 32);
-      l += rs;
-      // O^T += V^T . P^T over four 16-key chunks: chunk c takes keys 16 c + 8 hl + 0..7 of this lane
+      }
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        float pv[8];
+      for (int qb = 0; qb < 2; ++qb) {
+        float mt = -INFINITY;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pv[e] = s[c >> 1][(c & 1) * 8 + e];
-        half8 ph, pl;
-        if constexpr (NPL == 2) split8_pk(pv, ph, pl);
-        else
+        for (int ck = 0; ck < 2; ++ck)
 #pragma unroll
-          for (int e = 0; e < 8; ++e) ph[e] = _Float16(pv[e]);
+          for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mt = fmaxf(mt, s[qb][ck][hh][e]);
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        // A lane's exponent base m moves only when one of its query's scores exceeds it by more
+        // than 8, so p = 2^(s - m) <= 256; l and acc carry the same base, so out = acc / l is
+        // unchanged.  The rescale is skipped unless some lane of the wave moves; the others
+        // multiply by exactly 1, so a query's arithmetic never depends on the other queries of its
+        // wave.  Key 0 is visible to every query, so m is finite from the first page on and
+        // 2^(-inf - m) = 0 drops masked keys.
+        const bool grow = mt > m[qb] + 8.0f;
+        if (__any(grow)) {
+          const float mn = grow ? mt : m[qb];
+          const float alpha = __builtin_amdgcn_exp2f(m[qb] - mn);
+          l[qb] *= alpha;
+#pragma unroll
+          for (int b = 0; b < DB; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[qb][b][r] *= alpha;
+          m[qb] = mn;
+        }
+        float rs = 0.0f;
+#pragma unroll
+        for (int ck = 0; ck < 2; ++ck)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float p = __builtin_amdgcn_exp2f(s[qb][ck][hh][e] - m[qb]);
+              s[qb][ck][hh][e] = p;
+              rs += p;
+            }
+        rs += __shfl_xor(rs, 16);
+        rs += __shfl_xor(rs, 32);
+        l[qb] += rs;
+      }
+      // O^T += V^T . P^T over the two 32-key chunks: lane l's P^T operand is keys ck * 32 + 8 qg + 0..7
+      // of its query, against dims 16 b + lr of V at the same keys
+#pragma unroll
+      for (int ck = 0; ck < 2; ++ck) {
+        half8 ph[2], pl[2];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          float pv[8];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            pv[e] = s[qb][ck][0][e];
+            pv[4 + e] = s[qb][ck][1][e];
+          }
+          if constexpr (NPL == 2) split8_pk(pv, ph[qb], pl[qb]);
+          else
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ph[qb][e] = _Float16(pv[e]);
+        }
 #pragma unroll
         for (int b = 0; b < DB; ++b) {
-          const int vo = (b * 32 + qi) * S::VRS + 2 * c + hl;
+          const int vo = (b * 16 + lr) * S::VRS + 4 * ck + qg;
           const half8 vh = lds_half8(vh_, vo);
           if constexpr (NPL == 2) {
             const half8 vl = lds_half8(vl_, vo);
-            acc[b] = MFMA(vh, ph, acc[b]);
-            acc[b] = MFMA(vl, ph, acc[b]);
-            acc[b] = MFMA(vh, pl, acc[b]);
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+              acc[qb][b] = MFMA(vh, ph[qb], acc[qb][b]);
+              acc[qb][b] = MFMA(vl, ph[qb], acc[qb][b]);
+              acc[qb][b] = MFMA(vh, pl[qb], acc[qb][b]);
+            }
           } else {
-            acc[b] = MFMA(vh, ph, acc[b]);
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) acc[qb][b] = MFMA(vh, ph[qb], acc[qb][b]);
           }
         }
       }
@@ -276,26 +325,28 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of page kt + 1 has landed
     __syncthreads();
   }
-  if (!active || !live) return;
-  const float inv = 1.0f / l;
-  const int64_t obase = int64_t(row0 + qi) * qw + h * HD;
-  // acc[b][r] <-> d = b * 32 + (r / 4) * 8 + hl * 4 + r % 4
+  if (!active) return;
+  // acc[qb][b][r] <-> dim 16 b + 4 qg + r of query qb * 16 + lr
 #pragma unroll
-  for (int b = 0; b < DB; ++b)
+  for (int qb = 0; qb < 2; ++qb) {
+    if (qb * 16 + lr >= n) continue;
+    const float inv = 1.0f / l[qb];
+    const int64_t obase = int64_t(row0 + qb * 16 + lr) * qw + h * HD + 4 * qg;
 #pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
+    for (int b = 0; b < DB; ++b) {
       half4 o, olo;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         _Float16 oh, ol;
-        split_f16(acc[b][r4 * 4 + j] * inv, oh, ol);
+        split_f16(acc[qb][b][j] * inv, oh, ol);
         o[j] = oh;
         olo[j] = ol;
       }
-      const int64_t at = obase + b * 32 + r4 * 8 + hl * 4;
+      const int64_t at = obase + b * 16;
       *reinterpret_cast<half4 *>(out16 + at) = o;
       if constexpr (NPL == 2) *reinterpret_cast<half4 *>(out16lo + at) = olo;
     }
+  }
 }
 
 // ---------------------------------------------------------------- decode
