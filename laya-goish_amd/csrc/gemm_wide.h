@@ -14,16 +14,15 @@
 // instruction per 32-deep chunk).
 //
 // Geometry: 512 threads = 8 wave64s (2 per SIMD), workgroup tile 256 x 256, K steps of 32.
-// WQ8 and W1 keep three LDS stages (stage k + 2 in flight while stage k is consumed), W2 two
-// (its stage holds four planes).  Wave w owns rows 64 (w / 2) .. + 64 and columns
-// 128 (w % 2) .. + 128 of the tile (4 x 8 MFMA blocks of 16 x 16).  With three stages the two wave groups
-// of a workgroup run half a step apart (ping-pong, below), one barrier per half step; W2 runs
-// all eight waves in step, one barrier per step (measured faster for its two stages).
+// WQ8 and W1 keep three LDS stages, W2 two (its stage holds four planes).  Wave w owns rows
+// 64 (w / 2) .. + 64 and columns 128 (w % 2) .. + 128 of the tile (4 x 8 MFMA blocks of
+// 16 x 16).  The two wave groups of a workgroup (waves 0-3 and 4-7) run half a step apart
+// (ping-pong, below), one barrier per half step.
 //
 // LDS rows are 64 bytes (four 16-byte chunks); logical chunk c of row r sits in slot
 // c ^ ((r >> 2) & 3), so the 16 lanes of each quarter of an operand read (16 rows, one chunk)
-// fall in 16 distinct 16-byte bank groups.  The DMA side writes whole 1 KiB blocks: lane L of a block fetches the
-// global chunk that belongs in its slot.
+// fall in 16 distinct 16-byte bank groups.  The DMA side writes whole 1 KiB blocks: lane L of a
+// block fetches the global chunk that belongs in its slot.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -116,15 +115,16 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
   if constexpr (MODE == W2) rc = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(Wl), 0, wbytes, kBufferFlags);
   if constexpr (MODE == WQ8)
     rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(Ws), 0, uint32_t(N) * uint32_t(K / 32) * 4u, kBufferFlags);
-  // Every wave moves the blocks wave and wave + 8 of each plane (A hi, A lo, W hi, W lo); block
-  // w + 8 holds the rows of block w shifted by 128, which for A and for every weight row map
-  // (wrow) is a wave-uniform byte offset: the buffer instruction's scalar offset.  Wave 0 also
-  // moves the scale block.
-  constexpr bool kPingPong = G::kStages == 3;
-  const int grp = wave >> 2;
+  // WQ8 and W1: every wave moves the blocks wave and wave + 8 of each plane (A hi, A lo, W hi);
+  // wave 0 also moves the scale block.  W2: the four waves of group 1 move everything, wave
+  // 4 + b the blocks b, b + 4, b + 8, b + 12 of each of the four planes.  Block b + q holds the
+  // rows of block b shifted by 16 q, which for A and for every weight row map (wrow) is a
+  // wave-uniform byte offset: the buffer instruction's scalar offset.
+  constexpr int BSTEP = MODE == W2 ? 4 : 8;  // block stride of a wave's blocks
+  const int grp = wave >> 2, wb = MODE == W2 ? (wave & 3) : wave;
   uint32_t aoff, boff;
   {
-    const int slot = wave * 64 + lane;  // 16-byte slot inside a plane (block wave)
+    const int slot = wb * 64 + lane;  // 16-byte slot inside a plane (block wb)
     const int row = slot >> 2, c = (slot & 3) ^ swz(row);
     aoff = uint32_t(m0 + row) * uint32_t(K) * 2u + uint32_t(c) * 16u;
     boff = uint32_t(wrow(row)) * uint32_t(K) * 2u + uint32_t(c) * 16u;
@@ -135,13 +135,13 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
   typedef __attribute__((address_space(3))) void *lds_ptr;
 #endif
   // one DMA instruction of step kt into stage st: plane pl (0 A hi, 1 A lo, 2 W hi, 3 W lo) of
-  // block wave + 8 h
+  // block wb + BSTEP h
   auto dma = [&](int kt, int st, int pl, int h) {
 #if defined(__HIP_DEVICE_COMPILE__)
     // device pass only: with a run-time voffset this builtin keeps the host pass from
     // emitting the kernel's launch stub (the host never runs kernel bodies)
     uint8_t *base = lds + st * G::kStageBytes;
-    const int blk = (wave + 8 * h) * 1024, dr = 128 * h;  // block, row shift
+    const int blk = (wb + BSTEP * h) * 1024, dr = 16 * BSTEP * h;  // block, row shift
     const uint32_t ka = uint32_t(kt * BK * 2) + uint32_t(dr) * uint32_t(K) * 2u;
     const uint32_t kb = uint32_t(kt * BK * 2) + uint32_t(wrow(dr) - wrow(0)) * uint32_t(K) * 2u;
     if (pl == 0) __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr)(base + G::kAHi + blk), 16, aoff, ka, 0, 0);
@@ -158,10 +158,11 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
 #endif
   };
   constexpr int NPL = 2 + G::kBPlanes;  // planes per stage
-  // this wave's part of step kt: 2 NPL instructions (wave 0: + the scale block)
+  constexpr int NBW = 16 / BSTEP;          // blocks per plane of a moving wave
+  // this wave's part of step kt: NBW * NPL instructions (wave 0: + the scale block)
   auto issue = [&](int kt, int st) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < NBW; ++h)
 #pragma unroll
       for (int pl = 0; pl < NPL; ++pl) dma(kt, st, pl, h);
     if (wave == 0) dma_scale(kt, st);
@@ -259,21 +260,24 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
         }
       }
     } else {
-      // per element: A_hi.W_hi, A_lo.W_hi, A_hi.W_lo; the 32 blocks of a wave interleave, so no
-      // MFMA waits on the one before it
+      // per element: A_hi.W_hi, A_lo.W_hi, A_hi.W_lo; column by column, the four row blocks'
+      // chains interleaved; dkt >= 0 (group 1): its sixteen DMA instructions, two per column
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int j = 0; j < 8; ++j) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = WIDE_MFMA(f.ah[i], f.b[j], acc[i][j]);
+        for (int i = 0; i < 4; ++i) acc[i][j] = WIDE_MFMA(f.ah[i], f.b[j], acc[i][j]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i) acc[i][j] = WIDE_MFMA(f.al[i], f.b[j], acc[i][j]);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = WIDE_MFMA(f.al[i], f.b[j], acc[i][j]);
-      {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 8; ++j) acc[i][j] = WIDE_MFMA(f.ah[i], f.c[j], acc[i][j]);
+        for (int i = 0; i < 4; ++i) acc[i][j] = WIDE_MFMA(f.ah[i], f.c[j], acc[i][j]);
+        if (dkt >= 0) {
+          dma(dkt, dst, (2 * j) % 4, (2 * j) / 4);
+          dma(dkt, dst, (2 * j + 1) % 4, (2 * j + 1) / 4);
+          __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
       }
     }
   };
@@ -304,7 +308,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
   // the same count and no branch separates the MFMAs from the DMA.  Both groups run the same loop
   // and pass 2 nk + 2 barriers.
   constexpr int S = G::kStages;
-  if constexpr (kPingPong) {
+  if constexpr (MODE != W2) {
     static_assert(S == 3 && NPL == 3, "ping-pong: three stages of three planes");
     // prologue: both groups' parts of steps 0 and 1, group 1's part of step 2
     issue(0, 0);
@@ -336,16 +340,28 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
     }
     if (grp == 0) barrier();
   } else {
-    // two stages, all waves together: step k + 1 in flight while step k is read and consumed
-    issue(0, 0);
-    for (int k = 0; k < nk; ++k) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of step k
-      barrier();  // all of step k in LDS; everyone done reading step k - 1
-      if (k + 1 < nk) issue(k + 1, (k + 1) % S);
-      Frag f;
-      read_step(k, f);
-      compute_step(f, -1, 0);
+    // W2, two stages of four planes: the same ping-pong, group 1 moving every block.  In phase
+    // 2k + 2 it moves step k + 2 (into the stage step k held, which both groups finished reading
+    // by phase 2k + 1) between the MFMAs of its compute phase of step k; it waits for that step at
+    // the end of its read phase of step k + 1 (phase 2k + 3), before group 0 reads it in 2k + 4.
+    if (grp == 1) {
+      issue(0, 0);
+      issue(1, 1);
+      asm volatile("s_waitcnt vmcnt(16)" ::: "memory");  // step 0
     }
+    barrier();
+    if (grp == 1) barrier();
+    for (int k = 0; k < nk; ++k) {
+      Frag f;
+      __builtin_amdgcn_s_setprio(2);
+      read_step(k, f);
+      if (grp == 1) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // step k + 1
+      barrier();
+      __builtin_amdgcn_s_setprio(0);
+      compute_step(f, grp == 1 ? k + 2 : -1, k % S);  // one call: two would spill
+      barrier();
+    }
+    if (grp == 0) barrier();
   }
 
   // epilogue: acc[i][j] register r -> row 16 i + 4 (lane / 16) + r, column 16 j + lane % 16 of the
