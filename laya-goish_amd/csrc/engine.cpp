@@ -734,7 +734,7 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
   auto *b = new BatchPlan();
   const bool ot = arch == Arch::OpenThai, fresh = fresh_only();
   try {
-    std::vector<int32_t> ids, tseq, tpos, tiles_s, tiles_r, tiles_p, tiles_n, gather, grp_f, grp_c, srow0, sn;
+    std::vector<int32_t> ids, tseq, tpos, tpage, tiles_s, tiles_r, tiles_p, tiles_n, gather, grp_f, grp_c, srow0, sn;
     const int gtiles = arch == Arch::Decoder ? attn_prefill_group_tiles(hq, hkv) : 4;
     std::vector<int32_t> it_r, it_p, it_n, it_lo, it_hi, cb_r, cb_n, cb_f, cb_c;
     int max_pages = 0;
@@ -779,6 +779,7 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
         ids.push_back(q.ids[i]);
         tseq.push_back(r);
         tpos.push_back(s.len + i);
+        tpage.push_back(fresh ? 0 : ptab[size_t(r) * max_pages + (s.len + i) / 64]);
       }
       for (int i = 0; i < q.n; i += 32) {
         if ((i / 32) % gtiles == 0) {
@@ -817,7 +818,7 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
     b->ntiles = int(tiles_s.size());
     b->ngroups = int(grp_f.size());
     b->max_pages = max_pages;
-    const size_t nints = ids.size() * 3 + ptab.size() + tiles_s.size() * 4 + grp_f.size() * 2 + gather.size() +
+    const size_t nints = ids.size() * 4 + ptab.size() + tiles_s.size() * 4 + grp_f.size() * 2 + gather.size() +
                          srow0.size() * 2 + it_r.size() * 5 + cb_r.size() * 4 + 64;
     b->meta.ensure(nints * 4 + 34 * 256);
     int32_t *base = b->meta.as<int32_t>();
@@ -830,6 +831,7 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
     put(ids, b->ids);
     put(tseq, b->tok_seq);
     put(tpos, b->tok_pos);
+    put(tpage, b->tok_page);
     put(ptab, b->pages);
     put(tiles_s, b->tile_seq);
     put(tiles_r, b->tile_row0);
@@ -877,7 +879,12 @@ void Engine::run_layers_prefill(BatchPlan &b, lg_cancel_fn cancel, void *arg) {
   const int planes = split() ? 2 : 1;  // hi (+ lo) f16 planes per activation
   ws_x_.ensure(size_t(T) * d * 4);
   ws_h16_.ensure(size_t(T) * d * 2 * planes);
-  ws_qkv_.ensure(size_t(T) * qkvw * 4);
+  // q|k|v projections whose GEMM also rotates and stores q, k and v (the 256 x 256 exact GEMM's
+  // fused epilogue) leave no f32 q|k|v rows to stage
+  bool fused = split() && hd == 128;
+  for (int l = 0; l < L && fused; ++l)
+    for (const ProjPart &p : layers_[l].qkv) fused = fused && p.col0 % 128 == 0 && gemm_wide_takes(T, p.w, Epi::F32);
+  if (!fused) ws_qkv_.ensure(size_t(T) * qkvw * 4);
   ws_q16_.ensure(size_t(T) * qw * 2 * planes);
   ws_att16_.ensure(size_t(T) * qw * 2 * planes);
   ws_act16_.ensure(size_t(T) * f * 2 * planes);
@@ -887,7 +894,7 @@ void Engine::run_layers_prefill(BatchPlan &b, lg_cancel_fn cancel, void *arg) {
   _Float16 *q16 = ws_q16_.as<_Float16>(), *q16lo = lo(ws_q16_, int64_t(T) * qw);
   _Float16 *att = ws_att16_.as<_Float16>(), *attlo = lo(ws_att16_, int64_t(T) * qw);
   _Float16 *act = ws_act16_.as<_Float16>(), *actlo = lo(ws_act16_, int64_t(T) * f);
-  float *qkv = ws_qkv_.as<float>();
+  float *qkv = fused ? nullptr : ws_qkv_.as<float>();
   const KvGeom g = geom();
   prof.begin("embed", stream);
   launch_embed(emb_, emb_kind, b.ids, T, d, V, x, stream);
@@ -898,12 +905,36 @@ void Engine::run_layers_prefill(BatchPlan &b, lg_cancel_fn cancel, void *arg) {
     prof.begin("rmsnorm", stream);
     launch_rmsnorm_f16(x, T, d, ly.attn_norm, eps, h16, h16lo, stream);
     prof.end(double(T) * d * (4 + 2 * planes), 0, stream);
-    for (const ProjPart &p : ly.qkv)
-      gemm(h16, h16lo, T, p.w, Epi::F32, qkv + p.col0, nullptr, nullptr, qkvw, p.bias);
-    prof.begin("rope_kv", stream);
-    launch_rope_kv_tiles(qkv, hq, g, cos_, sin_, b.pages, b.max_pages, b.tile_seq, b.tile_row0,
-                         b.tile_pos0, b.tile_n, b.ntiles, q16, q16lo, kpool(l), vpool(l), stream);
-    prof.end(double(T) * (qkvw * 4 + qw * 2 * planes + 2 * kvw * kv_elem()), 0, stream);
+    if (fused) {
+      RopeKvOut ro;
+      ro.cosT = cos_;
+      ro.sinT = sin_;
+      ro.tok_pos = b.tok_pos;
+      ro.tok_page = b.tok_page;
+      ro.q16 = q16;
+      ro.q16lo = q16lo;
+      ro.kpool = static_cast<_Float16 *>(kpool(l));
+      ro.vpool = static_cast<_Float16 *>(vpool(l));
+      ro.page_stride = g.page_stride;
+      ro.hq = hq;
+      ro.hkv = hkv;
+      ro.page_tokens = g.page_tokens;
+      ro.qscale = attn_q_scale(hd);
+      for (const ProjPart &p : ly.qkv) {
+        ro.col0 = p.col0;
+        prof.begin_kernel("gemm");
+        if (!launch_gemm_wide_rope(h16, h16lo, T, p.w, p.bias, ro, stream))
+          fail(LG_ERR_UNSUPPORTED, "gemm: fused q|k|v launch refused");
+        prof.end_kernel(double(p.w.bytes()) + double(T) * p.w.cols * 2, 2.0 * T * double(p.w.rows) * p.w.cols);
+      }
+    } else {
+      for (const ProjPart &p : ly.qkv)
+        gemm(h16, h16lo, T, p.w, Epi::F32, qkv + p.col0, nullptr, nullptr, qkvw, p.bias);
+      prof.begin("rope_kv", stream);
+      launch_rope_kv_tiles(qkv, hq, g, cos_, sin_, b.pages, b.max_pages, b.tile_seq, b.tile_row0,
+                           b.tile_pos0, b.tile_n, b.ntiles, q16, q16lo, kpool(l), vpool(l), stream);
+      prof.end(double(T) * (qkvw * 4 + qw * 2 * planes + 2 * kvw * kv_elem()), 0, stream);
+    }
     prof.begin("attn_prefill", stream);
     launch_attn_prefill(q16, q16lo, T, hq, g, kpool(l), vpool(l), b.pages, b.max_pages, b.tile_seq,
                         b.tile_row0, b.tile_pos0, b.tile_n, b.ntiles, b.grp_first, b.grp_count,

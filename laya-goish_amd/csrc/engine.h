@@ -88,6 +88,7 @@ struct BatchPlan {
   int T = 0, R = 0, ntiles = 0, max_pages = 0;
   DevBuf meta;                  // ids, tok_seq, tok_pos, pages, tiles..., gather rows
   int32_t *ids = nullptr, *tok_seq = nullptr, *tok_pos = nullptr, *pages = nullptr;
+  int32_t *tok_page = nullptr;  // per batch row: the page its position falls in
   int32_t *tile_seq = nullptr, *tile_row0 = nullptr, *tile_pos0 = nullptr, *tile_n = nullptr;
   int ngroups = 0;              // runs of <= 4 consecutive tiles of one sequence
   int32_t *grp_first = nullptr, *grp_count = nullptr;

@@ -37,6 +37,8 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 enum Mode { WQ8 = 0, W1 = 1, W2 = 2 };
+// epilogue of the fused q|k|v projection (RoPE, q planes, KV cache stores; RopeKvOut)
+constexpr int kEpiRopeKv = 16;
 
 constexpr int BM = 256, BN = 256, BK = 32, WAVES = 8, THREADS = 64 * WAVES;
 constexpr int ROWB = BK * 2;      // bytes per LDS row of one plane
@@ -61,7 +63,7 @@ __device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
 
 __device__ __forceinline__ float silu_f(float g) { return g * (1.0f / (1.0f + __expf(-g))); }
 
-// EPI: Epi values (F32, ADD, SWIGLU).  For SWIGLU the workgroup's 256 weight rows are 128 gate
+// EPI: Epi values (F32, ADD, SWIGLU) or kEpiRopeKv.  For SWIGLU the workgroup's 256 weight rows are 128 gate
 // rows and the 128 matching up rows: wave column wn holds gate rows in its column blocks 0-3 and
 // the up rows of the same output columns in blocks 4-7.
 template <int EPI, int MODE>
@@ -69,7 +71,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
     const _Float16 *__restrict__ A, const _Float16 *__restrict__ Alo, int M, int K,
     const _Float16 *__restrict__ Wh, const _Float16 *__restrict__ Wl, const float *__restrict__ Ws, int N,
     float *__restrict__ C, _Float16 *__restrict__ C16, _Float16 *__restrict__ C16lo, int ldc,
-    const float *__restrict__ bias, int MT, int NT, int ffn) {
+    const float *__restrict__ bias, int MT, int NT, int ffn, RopeKvOut ro) {
   using G = Geo<MODE>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr bool kGlu = EPI == int(Epi::SWIGLU);
@@ -381,6 +383,114 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
           split_f16(v, h, hl);
           C16[int64_t(row) * ldc + col] = h;
           if (C16lo) C16lo[int64_t(row) * ldc + col] = hl;
+        }
+      }
+    }
+  } else if constexpr (EPI == kEpiRopeKv) {
+    // the wave's 128 columns are one head: q (rotated, scaled, hi/lo planes [M][hq * 128]), k
+    // (rotated, K page rows) or v (V page columns); each value is the f32 acc (+ bias) the F32
+    // epilogue would store, rotated by rope_pair and split by split_f16 as the RoPE kernel does
+    const int head = (ro.col0 + nt * BN + wn * 128) >> 7;
+    const int part = head < ro.hq ? 0 : head < ro.hq + ro.hkv ? 1 : 2;  // q, k, v
+    const int PT = ro.page_tokens, plane = PT * 128;
+    float bv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) bv[j] = bias ? bias[nt * BN + wn * 128 + j * 16 + lr] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rb = m0 + wm * 64 + i * 16 + (lane >> 4) * 4;  // this lane's four rows rb .. rb + 3
+      int pos[4], page[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = min(rb + r, M - 1);
+        pos[r] = ro.tok_pos[row];
+        page[r] = ro.tok_page[row];
+      }
+      float v[8][4];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          v[j][r] = acc[i][j][r];
+          if (bias) v[j][r] += bv[j];
+        }
+      if (part < 2) {
+        // rotate-half pairs (d, d + 64): column blocks j and j + 4 of the same lane
+        float cs[4][4][4];  // [r][j][cos d, sin d, cos d + 64, sin d + 64]
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int64_t tb = int64_t(pos[r]) * 128 + j * 16 + lr;
+            cs[r][j][0] = ro.cosT[tb];
+            cs[r][j][1] = ro.sinT[tb];
+            cs[r][j][2] = ro.cosT[tb + 64];
+            cs[r][j][3] = ro.sinT[tb + 64];
+          }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = rb + r;
+          if (row >= M) continue;
+          _Float16 *dh, *dl;
+          if (part == 0) {
+            dh = ro.q16 + int64_t(row) * (ro.hq * 128) + head * 128;
+            dl = ro.q16lo + int64_t(row) * (ro.hq * 128) + head * 128;
+          } else {
+            const int64_t blk = int64_t(page[r]) * ro.page_stride + int64_t(head - ro.hq) * plane;
+            dh = ro.kpool + 2 * blk + (pos[r] % PT) * 128;
+            dl = dh + plane;
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            float a, c;
+            rope_pair(v[j][r], v[j + 4][r], cs[r][j][0], cs[r][j][1], cs[r][j][2], cs[r][j][3], a, c);
+            if (part == 0) {
+              a *= ro.qscale;
+              c *= ro.qscale;
+            }
+            _Float16 h, l;
+            split_f16(a, h, l);
+            dh[j * 16 + lr] = h;
+            dl[j * 16 + lr] = l;
+            split_f16(c, h, l);
+            dh[j * 16 + lr + 64] = h;
+            dl[j * 16 + lr + 64] = l;
+          }
+        }
+      } else {
+        // V page columns [128][PT]: the four rows are four consecutive slots of a column when they
+        // are consecutive positions of one page starting at a multiple of 4 (one 8-byte store a
+        // plane), else one slot at a time
+        bool quad = rb + 3 < M && (pos[0] & 3) == 0;
+#pragma unroll
+        for (int r = 1; r < 4; ++r) quad = quad && pos[r] == pos[0] + r && page[r] == page[0];
+        typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int d = j * 16 + lr;
+          half4 h4, l4;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            _Float16 h, l;
+            split_f16(v[j][r], h, l);
+            h4[r] = h;
+            l4[r] = l;
+          }
+          if (quad) {
+            const int64_t blk = int64_t(page[0]) * ro.page_stride + int64_t(head - ro.hq - ro.hkv) * plane;
+            _Float16 *dh = ro.vpool + 2 * blk + int64_t(d) * PT + (pos[0] % PT);
+            *reinterpret_cast<half4 *>(dh) = h4;
+            *reinterpret_cast<half4 *>(dh + plane) = l4;
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              if (rb + r >= M) continue;
+              const int64_t blk = int64_t(page[r]) * ro.page_stride + int64_t(head - ro.hq - ro.hkv) * plane;
+              _Float16 *dh = ro.vpool + 2 * blk + int64_t(d) * PT + (pos[r] % PT);
+              dh[0] = h4[r];
+              dh[plane] = l4[r];
+            }
+          }
         }
       }
     }

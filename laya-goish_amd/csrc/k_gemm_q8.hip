@@ -31,45 +31,59 @@ int device_cus() {
 }
 }  // namespace
 
-bool launch_gemm_wide(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
-                      _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st) {
+namespace {
+// the wide kernel's mode for W, or -1 when it does not take an M-row launch of W with epilogue
+// EPI (an Epi value or wide::kEpiRopeKv)
+int wide_mode(int M, const DevMatrix &W, int EPI) {
   using namespace wide;
-  if (!A || !Alo || M <= 0 || !W.pc) return false;
+  if (M <= 0 || !W.pc) return -1;
   int mode;
   switch (W.kind) {
-    case LG_Q8_0: mode = WQ8; if (!W.pcs) return false; break;
+    case LG_Q8_0: mode = WQ8; if (!W.pcs) return -1; break;
     case LG_F16: mode = W1; break;
     case LG_Q4_K:
-    case LG_Q6_K: mode = W2; if (!W.pcl) return false; break;
-    default: return false;
+    case LG_Q6_K: mode = W2; if (!W.pcl) return -1; break;
+    default: return -1;
   }
-  if (epi != Epi::F32 && epi != Epi::ADD && epi != Epi::SWIGLU) return false;
-  const bool glu = epi == Epi::SWIGLU;
+  if (EPI != int(Epi::F32) && EPI != int(Epi::ADD) && EPI != int(Epi::SWIGLU) && EPI != kEpiRopeKv) return -1;
+  const bool glu = EPI == int(Epi::SWIGLU);
   const int N = W.rows, K = W.cols;
-  if (K % BK != 0 || N % BN != 0) return false;  // gated: 128 gate + 128 up rows a tile
+  if (K % BK != 0 || N % BN != 0) return -1;  // gated: 128 gate + 128 up rows a tile
   const int NT = glu ? (N / 2) / (BN / 2) : N / BN;
-  if (int64_t(N) * K * 2 >= (int64_t(1) << 32)) return false;  // 32-bit buffer offsets of the weights
+  if (int64_t(N) * K * 2 >= (int64_t(1) << 32)) return -1;  // 32-bit buffer offsets of the weights
   // fewer 256 x 256 tiles than CUs leaves CUs idle: the 128 x 128 tiles fill the device better
-  if (int64_t((M + BM - 1) / BM) * NT < device_cus()) return false;
-  if (glu ? (C16 == nullptr || ldc < N / 2) : (C == nullptr || ldc < N)) return false;
+  if (int64_t((M + BM - 1) / BM) * NT < device_cus()) return -1;
+  return mode;
+}
 
-  // one kernel per (epilogue, mode); the LDS limit is raised once per kernel
-  typedef void (*Fn)(const _Float16 *, const _Float16 *, int, int, const _Float16 *, const _Float16 *,
-                     const float *, int, float *, _Float16 *, _Float16 *, int, const float *, int, int, int);
-  static const Fn fns[3][3] = {
-      {gemm_wide_kernel<int(Epi::F32), WQ8>, gemm_wide_kernel<int(Epi::F32), W1>, gemm_wide_kernel<int(Epi::F32), W2>},
-      {gemm_wide_kernel<int(Epi::ADD), WQ8>, gemm_wide_kernel<int(Epi::ADD), W1>, gemm_wide_kernel<int(Epi::ADD), W2>},
-      {gemm_wide_kernel<int(Epi::SWIGLU), WQ8>, gemm_wide_kernel<int(Epi::SWIGLU), W1>,
-       gemm_wide_kernel<int(Epi::SWIGLU), W2>}};
+typedef void (*WideFn)(const _Float16 *, const _Float16 *, int, int, const _Float16 *, const _Float16 *,
+                       const float *, int, float *, _Float16 *, _Float16 *, int, const float *, int, int, int,
+                       RopeKvOut);
+
+// one kernel per (epilogue, mode); the LDS limit is raised once per kernel
+template <int EPI>
+WideFn wide_fn(int mode) {
+  using namespace wide;
+  static const WideFn fns[3] = {gemm_wide_kernel<EPI, WQ8>, gemm_wide_kernel<EPI, W1>, gemm_wide_kernel<EPI, W2>};
+  static bool attr[3] = {};
   static const int lds_bytes[3] = {Geo<WQ8>::kLdsBytes, Geo<W1>::kLdsBytes, Geo<W2>::kLdsBytes};
-  static bool attr[3][3] = {};
-  const int ei = epi == Epi::F32 ? 0 : epi == Epi::ADD ? 1 : 2;
-  const Fn fn = fns[ei][mode];
-  if (!attr[ei][mode]) {
-    HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  lds_bytes[mode]));
-    attr[ei][mode] = true;
+  if (!attr[mode]) {
+    HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(fns[mode]),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes[mode]));
+    attr[mode] = true;
   }
+  return fns[mode];
+}
+
+// launches fn over the M rows in chunks whose activation planes stay within 32-bit buffer offsets
+void launch_wide(WideFn fn, int mode, const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W,
+                 bool glu, float *C, _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, const RopeKvOut &ro,
+                 hipStream_t st) {
+  using namespace wide;
+  static const int lds_bytes[3] = {Geo<WQ8>::kLdsBytes, Geo<W1>::kLdsBytes, Geo<W2>::kLdsBytes};
+  const int N = W.rows, K = W.cols;
+  const int NT = glu ? (N / 2) / (BN / 2) : N / BN;
+  const bool rope = ro.tok_pos != nullptr;
   // activation rows per launch: the planes' buffer offsets are 32-bit
   const int64_t rows_cap = ((int64_t(1) << 31) - 1) / (int64_t(K) * 2) / BM * BM;
   LG_REQUIRE(rows_cap > 0, "gemm: K=%d too large", K);
@@ -86,12 +100,51 @@ bool launch_gemm_wide(const _Float16 *A, const _Float16 *Alo, int M, const DevMa
     const _Float16 *Ac = A + int64_t(m0) * K, *Alc = Alo + int64_t(m0) * K;
     float *Cc = C ? C + int64_t(m0) * ldc : nullptr;
     _Float16 *C16c = C16 ? C16 + int64_t(m0) * ldc : nullptr, *C16lc = C16lo ? C16lo + int64_t(m0) * ldc : nullptr;
+    RopeKvOut rc = ro;
+    if (rope) {
+      rc.tok_pos += m0;
+      rc.tok_page += m0;
+      rc.q16 += int64_t(m0) * ro.hq * 128;
+      rc.q16lo += int64_t(m0) * ro.hq * 128;
+    }
     launch_timed(fn, dim3(MT * NT), dim3(THREADS), lds_bytes[mode], st, Ac, Alc, Mc, K,
                  static_cast<const _Float16 *>(W.pc), static_cast<const _Float16 *>(W.pcl),
-                 static_cast<const float *>(W.pcs), N, Cc, C16c, C16lc, ldc, bias, MT, NT, N / 2);
+                 static_cast<const float *>(W.pcs), N, Cc, C16c, C16lc, ldc, bias, MT, NT, N / 2, rc);
     m0 += Mc;
   }
   if (timer) *timer = whole;
+}
+}  // namespace
+
+bool gemm_wide_takes(int M, const DevMatrix &W, Epi epi) { return wide_mode(M, W, int(epi)) >= 0; }
+
+bool launch_gemm_wide(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
+                      _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st) {
+  using namespace wide;
+  if (!A || !Alo) return false;
+  const int mode = wide_mode(M, W, int(epi));
+  if (mode < 0) return false;
+  const bool glu = epi == Epi::SWIGLU;
+  const int N = W.rows;
+  if (glu ? (C16 == nullptr || ldc < N / 2) : (C == nullptr || ldc < N)) return false;
+  const WideFn fn = epi == Epi::F32   ? wide_fn<int(Epi::F32)>(mode)
+                    : epi == Epi::ADD ? wide_fn<int(Epi::ADD)>(mode)
+                                      : wide_fn<int(Epi::SWIGLU)>(mode);
+  launch_wide(fn, mode, A, Alo, M, W, glu, C, C16, C16lo, ldc, bias, RopeKvOut{}, st);
+  return true;
+}
+
+bool launch_gemm_wide_rope(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, const float *bias,
+                           const RopeKvOut &ro, hipStream_t st) {
+  using namespace wide;
+  if (!A || !Alo) return false;
+  const int mode = wide_mode(M, W, kEpiRopeKv);
+  if (mode < 0) return false;
+  if (ro.col0 % 128 != 0 || ro.col0 / 128 + W.rows / 128 > ro.hq + 2 * ro.hkv) return false;
+  LG_REQUIRE(ro.cosT && ro.sinT && ro.tok_pos && ro.tok_page && ro.q16 && ro.q16lo && ro.kpool && ro.vpool,
+             "gemm rope: missing output");
+  LG_REQUIRE(ro.page_tokens >= 4 && ro.page_tokens % 4 == 0 && ro.page_stride > 0, "gemm rope: bad page geometry");
+  launch_wide(wide_fn<kEpiRopeKv>(mode), mode, A, Alo, M, W, false, nullptr, nullptr, nullptr, 0, bias, ro, st);
   return true;
 }
 

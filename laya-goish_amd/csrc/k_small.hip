@@ -516,7 +516,7 @@ void launch_rope_kv_tiles(const float *qkv, int hq, const KvGeom &g, const float
   LG_REQUIRE(ntiles > 0 && q16, "rope_kv: bad arguments");
   LG_REQUIRE(g.page_tokens >= 32, "rope_kv: a 32-token tile must span at most two pages");
   // the attention consumes base-2 logits: fold log2(e) / sqrt(hd) into q once here
-  const float qscale = 1.4426950408889634f / std::sqrt(float(g.hd));
+  const float qscale = attn_q_scale(g.hd);
 #define LAUNCH(K32, HDV)                                                                                  \
   hipLaunchKernelGGL((rope_kv_tile_kernel<K32, HDV>), dim3(ntiles, 4), dim3(kT), 0, st, qkv, hq, g, cosT, sinT, \
                      pages, max_pages, tile_seq, tile_row0, tile_pos0, tile_n, q16, q16_lo, kpool, vpool, qscale)

@@ -6,6 +6,7 @@
 
 #include <hip/hip_ext.h>
 
+#include <cmath>
 #include <cstdint>
 
 namespace lg {
@@ -118,6 +119,35 @@ struct KvGeom {
 // Pool layout of one layer: [page][kv head][plane][...] where a plane is K rows [page_tokens][hd]
 // or V columns [hd][page_tokens] of f16; a split pool has two planes per (page, kv head), hi
 // then lo (hi = f16(v), lo = f16(v - hi)), an f16 pool one.
+
+// The factor launch_rope_kv_tiles (and the fused q|k|v epilogue) folds into q: log2(e) / sqrt(hd),
+// so that the attention kernels work on base-2 logits.
+inline float attn_q_scale(int hd) { return 1.4426950408889634f / std::sqrt(float(hd)); }
+
+// Outputs of the q|k|v projection's fused epilogue (launch_gemm_wide_rope): the f32 result
+// (+ bias) is rotated and stored exactly as launch_rope_kv_tiles stores it from the f32 rows.
+// head_dim 128; the launch's output columns are heads col0 / 128 .. of the q|k|v layout (q heads,
+// then k heads, then v heads).
+struct RopeKvOut {
+  const float *cosT = nullptr, *sinT = nullptr;          // [ctx][128]
+  const int32_t *tok_pos = nullptr, *tok_page = nullptr;  // per activation row: position, its page
+  _Float16 *q16 = nullptr, *q16lo = nullptr;              // [M][hq * 128] hi / lo planes
+  _Float16 *kpool = nullptr, *vpool = nullptr;            // the layer's split pools
+  int64_t page_stride = 0;                                // as KvGeom::page_stride
+  int hq = 0, hkv = 0, page_tokens = 64, col0 = 0;
+  float qscale = 1.0f;                                    // attn_q_scale(128)
+};
+
+// The 256 x 256 exact GEMM (gemm_wide.h) of a q|k|v projection, or a column range of it, with the
+// RoPE and KV cache stores of launch_rope_kv_tiles as its epilogue: q to f16 hi/lo planes
+// (scaled), k and v into the split pools at each row's position and page.  Returns false (nothing
+// launched) when the wide kernel does not take the launch (gemm_wide_takes) or the layout is not
+// one the epilogue covers (head_dim 128, col0 a multiple of 128).
+bool launch_gemm_wide_rope(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, const float *bias,
+                           const RopeKvOut &ro, hipStream_t st);
+// Whether the 256 x 256 exact GEMM takes an M-row launch of W with epilogue epi (shape, prefill
+// copy and tile count; pointers are checked at launch).
+bool gemm_wide_takes(int M, const DevMatrix &W, Epi epi);
 
 // RoPE on q and k of q|k|v rows ((hq+2hkv)*hd f32) with tables cos/sin[ctx][hd], q written
 // out, k and v written into the K page rows [hkv][page_tokens][hd] and V page columns

@@ -324,3 +324,47 @@ def test_q8_large_batch_tiles_equal_single_requests(lh, po):
     err = assert_logits_close(logits[27:30], want, rel=logit_bar(0))
     print(f"q8-2048 L2 16 x 512: bit-identical to single requests; logit rel {err:.2e} vs oracle")
     eng.close()
+
+
+def test_q8_fused_qkv_epilogue_ragged_continuations(lh, po):
+    """A batch big enough for the 256 x 256 q|k|v GEMM stores q, k and v from its own epilogue
+    (RoPE, q planes, K page rows, V page columns); requests alone keep the f32 q|k|v rows and the
+    RoPE kernel.  Ragged requests continue sequences that already hold 0..130 tokens, so rows meet
+    positions that are not multiples of 4 and quads of rows that straddle a sequence or a page: the
+    V columns' four-slot stores and their one-slot fallback both run.  Batch == alone, bit for bit,
+    at positions in every request, and one request matches the oracle."""
+    img = lh.SynthImage("q8-2048", seed=29, n_layers=2)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=2 * 4608, max_batch_tokens=4096)
+    rng = np.random.default_rng(31)
+    # tokens each sequence holds before the batch: request 0's rows and positions agree mod 4 (the
+    # four-slot V stores), every other request's do not
+    heads = [36, 0, 61, 5, 0, 130, 2]
+    lens = [701, 1290, 333, 999, 517, 65, 7]  # 3912 batch rows: 16 row tiles x 24 column tiles
+    opts = [5, 77, 901, 31999]
+    ctx = [rng.integers(0, 32000, h + n).astype(np.int32) for h, n in zip(heads, lens)]
+    pos = [sorted({0, 1, 2, 3, n // 2, n - 2, n - 1} & set(range(n))) for n in lens]
+    seqs = []
+    for h, ids in zip(heads, ctx):
+        s = eng.seq_create()
+        if h:
+            eng.forward(s, ids[:h], [], opts)
+        seqs.append(s)
+    print(f"q8-2048 L2: ragged batch of {sum(lens)} rows after heads {heads}", flush=True)
+    logits, _, _ = eng.batch([(s, ids[h:], p) for s, h, ids, p in zip(seqs, heads, ctx, pos)]).run(opts)
+    row = 0
+    for r, (h, ids, p) in enumerate(zip(heads, ctx, pos)):
+        s = eng.seq_create()
+        if h:
+            eng.forward(s, ids[:h], [], opts)
+        single = eng.forward(s, ids[h:], p, opts)
+        eng.seq_free(s)
+        assert_bits_equal(single, logits[row:row + len(p)])
+        row += len(p)
+    om = po.Model(po.Gguf(img.array()), threads=16)
+    want = om.forward(ctx[5], [heads[5] + q for q in pos[5]], opts)
+    first = sum(len(p) for p in pos[:5])
+    err = assert_logits_close(logits[first:first + len(pos[5])], want, rel=logit_bar(0))
+    print(f"q8-2048 ragged continuations: bit-identical to single requests; logit rel {err:.2e} vs oracle")
+    for s in seqs:
+        eng.seq_free(s)
+    eng.close()
