@@ -4,30 +4,6 @@
 namespace lg {
 namespace {
 
-template <uint32_t KIND>
-void launch_kind(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
-                 _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st);
-
-// Rows [0, m1) on the 256 x 256 tiles, the rest (if any) on the 128 x 128 exact tiles: the same bits.
-// An installed kernel timer spans both launches.  False (nothing launched) if the wide kernel
-// refuses the launch.
-template <uint32_t KIND>
-bool wide_then_tiles(int m1, const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
-                     _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st) {
-  KernelTimer *timer = kernel_timer();
-  const KernelTimer whole = timer ? *timer : KernelTimer{};
-  if (timer && m1 < M) timer->stop = nullptr;
-  const bool ok = launch_gemm_wide(A, Alo, m1, W, epi, C, C16, C16lo, ldc, bias, st);
-  if (ok && m1 < M) {
-    if (timer) *timer = KernelTimer{nullptr, whole.stop};
-    const int64_t K = W.cols, r = m1;
-    launch_kind<KIND>(A + r * K, Alo + r * K, M - m1, W, epi, C ? C + r * ldc : nullptr, C16 ? C16 + r * ldc : nullptr,
-                      C16lo ? C16lo + r * ldc : nullptr, ldc, bias, st);
-  }
-  if (timer) *timer = whole;
-  return ok;
-}
-
 // Per-kind, per-mode tile configuration: <MODE, BK, WTM, WTN, STAGES>.
 template <uint32_t KIND>
 void launch_kind(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
@@ -37,7 +13,7 @@ void launch_kind(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix 
   if (!Alo) {
     if (launch_cfg<KIND, FAST, 64, 4, 4, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
     if (launch_cfg<KIND, FAST, 64, 2, 2, 2>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
-  } else if (const int m1 = gemm_wide_rows(M, W, epi); m1 > 0 && wide_then_tiles<KIND>(m1, A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) {
+  } else if (launch_gemm_wide(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) {
     return;
   } else if constexpr (KIND == LG_Q8_0) {
     if (launch_gemm_q8_exact(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;

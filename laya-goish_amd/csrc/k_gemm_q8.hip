@@ -118,25 +118,6 @@ void launch_wide(WideFn fn, int mode, const _Float16 *A, const _Float16 *Alo, in
 
 bool gemm_wide_takes(int M, const DevMatrix &W, Epi epi) { return wide_mode(M, W, int(epi)) >= 0; }
 
-int gemm_wide_rows(int M, const DevMatrix &W, Epi epi) {
-  using namespace wide;
-  if (wide_mode(M, W, int(epi)) < 0) return 0;
-  // Rounds of 256 x 256 tiles (one workgroup a CU): a last round with few tiles takes as long as a
-  // full one.  Cut the launch after the last full round when the rows left over (less than one
-  // round of wide tiles) take less time on the 128 x 128 tiles (two workgroups a CU, each a
-  // quarter of a wide tile's work at about three quarters of its rate: two thirds of a wide round
-  // per round of them), with a quarter-round margin.
-  const int cus = device_cus(), NT = W.rows / BN, MT = (M + BM - 1) / BM;
-  const int64_t tiles = int64_t(MT) * NT;
-  if (tiles % cus == 0) return M;
-  const int MT1 = int(tiles / cus * cus / NT);
-  if (MT1 <= 0) return M;
-  const int64_t rounds_all = tiles / cus + 1, rounds1 = (int64_t(MT1) * NT + cus - 1) / cus;
-  const int64_t small = int64_t((M - MT1 * BM + 127) / 128) * (W.rows / 128);
-  const double small_rounds = double((small + 2 * cus - 1) / (2 * cus)) * (2.0 / 3.0);
-  return double(rounds1) + small_rounds + 0.25 <= double(rounds_all) ? MT1 * BM : M;
-}
-
 bool launch_gemm_wide(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
                       _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st) {
   using namespace wide;

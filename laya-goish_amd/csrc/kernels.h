@@ -148,10 +148,6 @@ bool launch_gemm_wide_rope(const _Float16 *A, const _Float16 *Alo, int M, const 
 // Whether the 256 x 256 exact GEMM takes an M-row launch of W with epilogue epi (shape, prefill
 // copy and tile count; pointers are checked at launch).
 bool gemm_wide_takes(int M, const DevMatrix &W, Epi epi);
-// Rows of an M-row launch the 256 x 256 exact GEMM should take: 0 (none), M, or a multiple of 256
-// below M after which the rest (less than one round of its tiles) runs faster on the 128 x 128
-// exact tiles.
-int gemm_wide_rows(int M, const DevMatrix &W, Epi epi);
 
 // RoPE on q and k of q|k|v rows ((hq+2hkv)*hd f32) with tables cos/sin[ctx][hd], q written
 // out, k and v written into the K page rows [hkv][page_tokens][hd] and V page columns

@@ -326,29 +326,6 @@ def test_q8_large_batch_tiles_equal_single_requests(lh, po):
     eng.close()
 
 
-def test_q8_wide_rounds_then_tiles_equal_single_requests(lh):
-    """18 x 512 = 9216 rows: 36 row tiles of 256.  The o, down and gate|up launches have a last
-    round of 256 x 256 tiles with few tiles in it (288 and 792 tiles over 256 CUs), so they run
-    their full rounds on the wide kernel and the remaining 1024 and 512 rows on the 128 x 128
-    tiles.  The batch equals each request alone (128 x 128 tiles only), bit for bit."""
-    img = lh.SynthImage("q8-2048", seed=37, n_layers=2)
-    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=18 * 576, max_batch_tokens=18 * 512)
-    rng = np.random.default_rng(41)
-    reqs = [(rng.integers(0, 32000, 512).astype(np.int32), [0, 255, 511]) for _ in range(18)]
-    opts = [5, 77, 901, 31999]
-    seqs = [eng.seq_create() for _ in reqs]
-    print("q8-2048 L2: batch of 18 x 512 tokens", flush=True)
-    logits, _, _ = eng.batch([(s, ids, pos) for s, (ids, pos) in zip(seqs, reqs)]).run(opts)
-    for s in seqs:
-        eng.seq_free(s)
-    for r in (0, 16, 17):  # 16: rows 8192.. (the o/down remainder); 17: rows 8704.. (every remainder)
-        s = eng.seq_create()
-        single = eng.forward(s, reqs[r][0], reqs[r][1], opts)
-        eng.seq_free(s)
-        assert_bits_equal(single, logits[3 * r:3 * r + 3])
-    eng.close()
-
-
 def test_q8_fused_qkv_epilogue_ragged_continuations(lh, po):
     """A batch big enough for the 256 x 256 q|k|v GEMM stores q, k and v from its own epilogue
     (RoPE, q planes, K page rows, V page columns); requests alone keep the f32 q|k|v rows and the
