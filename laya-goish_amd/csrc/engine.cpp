@@ -781,11 +781,16 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
         tpos.push_back(s.len + i);
         tpage.push_back(fresh ? 0 : ptab[size_t(r) * max_pages + (s.len + i) / 64]);
       }
+      // attention groups of <= gtiles consecutive tiles, cut from the request's end and listed last
+      // first: the leftover short group is the one nearest the start (the fewest pages), not a
+      // group of one or two tiles that reads every page with most of its waves idle
+      const int t_first = int(tiles_s.size()), ntl = (q.n + 31) / 32;
+      for (int e = ntl; e > 0; e -= gtiles) {
+        const int b = std::max(0, e - gtiles);
+        grp_f.push_back(t_first + b);
+        grp_c.push_back(e - b);
+      }
       for (int i = 0; i < q.n; i += 32) {
-        if ((i / 32) % gtiles == 0) {
-          grp_f.push_back(int32_t(tiles_s.size()));
-          grp_c.push_back(std::min(gtiles, (q.n - i + 31) / 32));
-        }
         tiles_s.push_back(r);
         tiles_r.push_back(row + i);
         tiles_p.push_back(s.len + i);
