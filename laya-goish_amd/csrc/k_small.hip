@@ -403,7 +403,7 @@ __global__ void option_scores_kernel(const float *__restrict__ logits, int R, in
   }
 }
 
-// Two-stage argmax; ties and NaN follow the strict ">" scan (first maximum wins).
+// Argmax: ties and NaN follow the strict ">" scan (first maximum wins).
 // Each thread scans increasing indices with a strict ">", so it keeps its first maximum;
 // NaN never compares greater.  Merges prefer the larger value, then the smaller index.
 __device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
@@ -413,53 +413,53 @@ __device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
   }
 }
 
-__global__ __launch_bounds__(kT) void argmax_stage1(const float *__restrict__ v, int n,
-                                                    float *__restrict__ pv, int32_t *__restrict__ pi) {
-  __shared__ float sv[kT];
-  __shared__ int si[kT];
+// One workgroup of 1024 threads over the whole vector (one launch: a decode step's argmax sits between
+// two dependent launches).  Thread t takes float4 words t, t + 1024, ... (their elements in index
+// order, so the strict `better` keeps the first of equal values), then the merge rule of the two-stage
+// form over the wave (butterfly) and over the 16 waves.  The rule is a total order (larger value,
+// then smaller index; no index loses), so the merge order does not change the result.
+__global__ __launch_bounds__(1024) void argmax_one(const float *__restrict__ v, int n, int32_t *__restrict__ out) {
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   float bv = -INFINITY;
   int bi = -1;
-  for (int i = blockIdx.x * kT + threadIdx.x; i < n; i += gridDim.x * kT) better(bv, bi, v[i], i);
-  sv[threadIdx.x] = bv;
-  si[threadIdx.x] = bi;
-  __syncthreads();
-  for (int s = kT / 2; s > 0; s >>= 1) {
-    if (int(threadIdx.x) < s) {
-      float ov = sv[threadIdx.x + s];
-      int oi = si[threadIdx.x + s];
-      float cv = sv[threadIdx.x];
-      int ci = si[threadIdx.x];
-      if (oi >= 0 && (ci < 0 || ov > cv || (ov == cv && oi < ci))) {
-        sv[threadIdx.x] = ov;
-        si[threadIdx.x] = oi;
+  const int n4 = (reinterpret_cast<uintptr_t>(v) & 15) == 0 ? n >> 2 : 0;
+  const float4 *v4 = reinterpret_cast<const float4 *>(v);
+  for (int k0 = t; k0 < n4; k0 += 8 * 1024) {
+    float4 w[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) w[u] = v4[min(k0 + u * 1024, n4 - 1)];  // all loads before any compare
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + u * 1024;
+      if (k < n4) {
+        better(bv, bi, w[u].x, 4 * k);
+        better(bv, bi, w[u].y, 4 * k + 1);
+        better(bv, bi, w[u].z, 4 * k + 2);
+        better(bv, bi, w[u].w, 4 * k + 3);
       }
     }
-    __syncthreads();
   }
-  if (threadIdx.x == 0) {
-    pv[blockIdx.x] = sv[0];
-    pi[blockIdx.x] = si[0];
-  }
-}
-
-// One wave: lane i takes partial i (nparts <= 64, one load round trip), then a butterfly of the same
-// merge rule (larger value, then smaller index; a partial without an index loses).  The rule is a
-// total order, so the order of the merges does not change the result.
-__global__ __launch_bounds__(64) void argmax_stage2(const float *__restrict__ pv,
-                                                    const int32_t *__restrict__ pi, int nparts,
-                                                    int32_t *__restrict__ out) {
-  const int lane = threadIdx.x;
-  float bv = lane < nparts ? pv[lane] : -INFINITY;
-  int bi = lane < nparts ? pi[lane] : -1;
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) {
-    const float ov = __shfl_xor(bv, m);
-    const int oi = __shfl_xor(bi, m);
+  for (int i = 4 * n4 + t; i < n; i += 1024) better(bv, bi, v[i], i);  // the tail (or all, unaligned)
+  auto merge = [&](float ov, int oi) {
     if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
       bv = ov;
       bi = oi;
     }
+  };
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) merge(__shfl_xor(bv, m), __shfl_xor(bi, m));
+  if (lane == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
   }
+  __syncthreads();
+  if (wave != 0) return;
+  bv = lane < 16 ? sv[lane] : -INFINITY;
+  bi = lane < 16 ? si[lane] : -1;
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) merge(__shfl_xor(bv, m), __shfl_xor(bi, m));
   if (lane == 0) out[0] = bi >= 0 && bv > -INFINITY && bv < INFINITY ? bi : -1;  // -1: no finite maximum
 }
 
@@ -552,9 +552,9 @@ void launch_option_scores(const float *logits, int R, int k, float temperature, 
 void launch_argmax(const float *logits, int V, int32_t *out, float *part_v, int32_t *part_i,
                    hipStream_t st) {
   LG_REQUIRE(V > 0, "argmax: empty");
-  const int parts = 64;  // one per lane of argmax_stage2's wave
-  hipLaunchKernelGGL(argmax_stage1, dim3(parts), dim3(kT), 0, st, logits, V, part_v, part_i);
-  hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(64), 0, st, part_v, part_i, parts, out);
+  (void)part_v;  // the single-workgroup form needs no partials
+  (void)part_i;
+  hipLaunchKernelGGL(argmax_one, dim3(1), dim3(1024), 0, st, logits, V, out);
   HIP_CHECK(hipGetLastError());
 }
 

@@ -198,7 +198,8 @@ void launch_option_scores(const float *logits, int R, int k, float temperature, 
                           float *logprobs, hipStream_t st);
 
 // Full-vocabulary argmax of logits[V] (first maximum wins) -> out[0], or -1 when the maximum is not
-// finite (inf or no comparable value); part: scratch.
+// finite (inf or no comparable value).  One launch of one workgroup; part_v / part_i (64 entries each,
+// reserved by the decode workspaces) are not used by it.
 void launch_argmax(const float *logits, int V, int32_t *out, float *part_v, int32_t *part_i,
                    hipStream_t st);
 
