@@ -1133,9 +1133,11 @@ void Engine::decode_run(Seq &s, int32_t first, int steps, int32_t *tokens, float
   }
   auto step_loop = [&] {
     for (int i = 0; i < steps; ++i) {
-      prof.begin("embed", stream);
-      launch_embed(emb_, emb_kind, tok + i, 1, d, V, x, stream);
-      prof.end(double(d) * 6, 0, stream);
+      if (i == 0) {  // later steps' rows come from the previous step's argmax launch
+        prof.begin("embed", stream);
+        launch_embed(emb_, emb_kind, tok + i, 1, d, V, x, stream);
+        prof.end(double(d) * 6, 0, stream);
+      }
       for (int l = 0; l < L; ++l) {
         const Layer &ly = layers_[l];
         for (const ProjPart &p : ly.qkv) gemv(x, p.w, Epi::F32, qkv + p.col0, p.bias, ly.attn_norm);
@@ -1150,7 +1152,8 @@ void Engine::decode_run(Seq &s, int32_t first, int steps, int32_t *tokens, float
       }
       gemv(x, head_, Epi::F32, lg, nullptr, final_norm_);
       prof.begin("argmax", stream);
-      launch_argmax(lg, V, tok + i + 1, part_v, part_i, stream);
+      if (i + 1 < steps) launch_argmax_embed(lg, V, tok + i + 1, emb_, emb_kind, d, x, stream);
+      else launch_argmax(lg, V, tok + i + 1, part_v, part_i, stream);
       prof.end(double(V) * 4, 0, stream);
       if (logits) HIP_CHECK(hipMemcpyAsync(logits + size_t(i) * V, lg, size_t(V) * 4, hipMemcpyDeviceToHost, stream));
     }

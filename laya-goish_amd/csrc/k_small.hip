@@ -418,9 +418,15 @@ __device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
 // order, so the strict `better` keeps the first of equal values), then the merge rule of the two-stage
 // form over the wave (butterfly) and over the 16 waves.  The rule is a total order (larger value,
 // then smaller index; no index loses), so the merge order does not change the result.
-__global__ __launch_bounds__(1024) void argmax_one(const float *__restrict__ v, int n, int32_t *__restrict__ out) {
+// EMB: the workgroup then writes the token's embedding row (ids clamped as embed_kernel clamps
+// them) to x, the next decode step's input, which saves that step its embedding launch.
+template <bool EMB>
+__global__ __launch_bounds__(1024) void argmax_one(const float *__restrict__ v, int n, int32_t *__restrict__ out,
+                                                   const void *__restrict__ table, uint32_t kind, int d,
+                                                   float *__restrict__ x) {
   __shared__ float sv[16];
   __shared__ int si[16];
+  __shared__ int stok;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   float bv = -INFINITY;
   int bi = -1;
@@ -455,12 +461,24 @@ __global__ __launch_bounds__(1024) void argmax_one(const float *__restrict__ v, 
     si[wave] = bi;
   }
   __syncthreads();
-  if (wave != 0) return;
-  bv = lane < 16 ? sv[lane] : -INFINITY;
-  bi = lane < 16 ? si[lane] : -1;
+  if (wave == 0) {
+    bv = lane < 16 ? sv[lane] : -INFINITY;
+    bi = lane < 16 ? si[lane] : -1;
 #pragma unroll
-  for (int m = 1; m < 64; m <<= 1) merge(__shfl_xor(bv, m), __shfl_xor(bi, m));
-  if (lane == 0) out[0] = bi >= 0 && bv > -INFINITY && bv < INFINITY ? bi : -1;  // -1: no finite maximum
+    for (int m = 1; m < 64; m <<= 1) merge(__shfl_xor(bv, m), __shfl_xor(bi, m));
+    if (lane == 0) {
+      const int tok = bi >= 0 && bv > -INFINITY && bv < INFINITY ? bi : -1;  // -1: no finite maximum
+      out[0] = tok;
+      stok = tok;
+    }
+  }
+  if constexpr (EMB) {
+    __syncthreads();
+    const int64_t row = int64_t(min(max(stok, 0), n - 1)) * d;
+    for (int k = t; k < d; k += 1024)
+      x[k] = kind == LG_F16 ? half_bits(static_cast<const uint16_t *>(table)[row + k])
+                            : static_cast<const float *>(table)[row + k];
+  }
 }
 
 __global__ void cvt_f16_kernel(const float *__restrict__ x, int64_t n, _Float16 *__restrict__ y,
@@ -554,7 +572,16 @@ void launch_argmax(const float *logits, int V, int32_t *out, float *part_v, int3
   LG_REQUIRE(V > 0, "argmax: empty");
   (void)part_v;  // the single-workgroup form needs no partials
   (void)part_i;
-  hipLaunchKernelGGL(argmax_one, dim3(1), dim3(1024), 0, st, logits, V, out);
+  hipLaunchKernelGGL(argmax_one<false>, dim3(1), dim3(1024), 0, st, logits, V, out, static_cast<const void *>(nullptr),
+                     0u, 0, static_cast<float *>(nullptr));
+  HIP_CHECK(hipGetLastError());
+}
+
+void launch_argmax_embed(const float *logits, int V, int32_t *out, const void *table, uint32_t kind, int d, float *x,
+                         hipStream_t st) {
+  LG_REQUIRE(V > 0 && d > 0 && table && x, "argmax: bad arguments");
+  LG_REQUIRE(kind == LG_F16 || kind == LG_F32, "embed: table must be F16/F32");
+  hipLaunchKernelGGL(argmax_one<true>, dim3(1), dim3(1024), 0, st, logits, V, out, table, kind, d, x);
   HIP_CHECK(hipGetLastError());
 }
 

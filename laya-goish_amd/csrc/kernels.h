@@ -202,6 +202,10 @@ void launch_option_scores(const float *logits, int R, int k, float temperature, 
 // reserved by the decode workspaces) are not used by it.
 void launch_argmax(const float *logits, int V, int32_t *out, float *part_v, int32_t *part_i,
                    hipStream_t st);
+// launch_argmax, then the chosen token's embedding row (table[V][d], F16 or F32, the vocabulary of the
+// logits) into x[d] by the same workgroup: the next decode step's input without its own launch.
+void launch_argmax_embed(const float *logits, int V, int32_t *out, const void *table, uint32_t kind, int d, float *x,
+                         hipStream_t st);
 
 // f32 -> f16 (round to nearest even), n elements; with y_lo, also the residual plane
 // y_lo = f16(x - y).
