@@ -923,6 +923,7 @@ void Engine::run_layers_prefill(BatchPlan &b, lg_cancel_fn cancel, void *arg) {
       ro.page_stride = g.page_stride;
       ro.hq = hq;
       ro.hkv = hkv;
+      ro.hd = hd;
       ro.page_tokens = g.page_tokens;
       ro.qscale = attn_q_scale(hd);
       for (const ProjPart &p : ly.qkv) {

@@ -140,7 +140,7 @@ bool launch_gemm_wide_rope(const _Float16 *A, const _Float16 *Alo, int M, const 
   if (!A || !Alo) return false;
   const int mode = wide_mode(M, W, kEpiRopeKv);
   if (mode < 0) return false;
-  if (ro.col0 % 128 != 0 || ro.col0 / 128 + W.rows / 128 > ro.hq + 2 * ro.hkv) return false;
+  if (ro.hd != 128 || ro.col0 % 128 != 0 || ro.col0 / 128 + W.rows / 128 > ro.hq + 2 * ro.hkv) return false;
   LG_REQUIRE(ro.cosT && ro.sinT && ro.tok_pos && ro.tok_page && ro.q16 && ro.q16lo && ro.kpool && ro.vpool,
              "gemm rope: missing output");
   LG_REQUIRE(ro.page_tokens >= 4 && ro.page_tokens % 4 == 0 && ro.page_stride > 0, "gemm rope: bad page geometry");

@@ -134,7 +134,7 @@ struct RopeKvOut {
   _Float16 *q16 = nullptr, *q16lo = nullptr;              // [M][hq * 128] hi / lo planes
   _Float16 *kpool = nullptr, *vpool = nullptr;            // the layer's split pools
   int64_t page_stride = 0;                                // as KvGeom::page_stride
-  int hq = 0, hkv = 0, page_tokens = 64, col0 = 0;
+  int hq = 0, hkv = 0, hd = 128, page_tokens = 64, col0 = 0;  // hd: must be 128
   float qscale = 1.0f;                                    // attn_q_scale(128)
 };
 
