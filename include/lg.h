@@ -161,6 +161,11 @@ void lg_engine_destroy(lg_engine *e);
 int lg_engine_info(const lg_engine *e, lg_model_info *info);
 /* Block until all work queued on the engine's stream has finished. */
 int lg_engine_sync(lg_engine *e);
+/* Device memory held by the engine's grow-only workspaces (activations, the decode workspace, output
+ * staging), in bytes: weights and the KV page pool are not counted.  No reference counterpart (the
+ * reference holds no device memory); for serving-side memory accounting, and it shows that
+ * lg_decode_noalloc grows nothing. */
+int lg_engine_workspace_bytes(const lg_engine *e, int64_t *bytes);
 
 /* y[m][rows] = x[m][cols] . W[rows][cols]^T (+ bias[rows]) with W the named uploaded
  * matrix.  Host pointers.  Replaces Matrix::apply, src/tensor.rs:10-39. */
@@ -222,17 +227,21 @@ int lg_batch_rewind(lg_engine *e, lg_batch *b);
 /* Greedy decode: feed `first` and then each argmax for `steps` single-token steps on `seq`
  * (which must hold its prefilled context).  tokens[steps] receives each step's argmax
  * (first maximum wins, src/models/openthai/decision.rs:330-335); logits (optional, host,
- * [steps][vocab]) each step's full-vocabulary logits. */
+ * [steps][vocab]) each step's full-vocabulary logits.  The context after the last step may hold at
+ * most 65,536 tokens (the decode attention's 1024 pages); a longer run fails with LG_ERR_INVALID
+ * before any step runs. */
 int lg_decode(lg_engine *e, int seq, int32_t first, int steps, int32_t *tokens, float *logits);
 /* lg_decode without any device allocation: its workspace (activations, attention page partials,
  * argmax partials, token slots and page table) lives in a fixed 16 MiB scratch array that every GPU
  * the library runs on holds until the process ends, so the call makes no hipMalloc/hipFree.  No
  * counterpart in the reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Results equal lg_decode.
- * A run whose workspace exceeds the scratch (long contexts or many steps; about 30k tokens of
- * context on the 7B shape) fails with LG_ERR_INVALID and changes nothing.  Every call on one GPU
- * shares that GPU's scratch: calls that overlap on one GPU (engines driven from several threads)
- * race, and must be serialised by the caller. */
+ * A run whose workspace exceeds the scratch fails with LG_ERR_INVALID and changes nothing; the
+ * workspace grows by hq x (2 + head_dim) x 4 bytes per 64-token page of context, so the scratch would
+ * hold about 70k tokens of context on the 7B shape and 127k on d2048, beyond the 65,536 tokens that
+ * decode accepts at all.  Every call on one GPU shares that GPU's scratch: a call holds a per-GPU
+ * lock from its first launch until its stream has drained, so calls from engines on several threads
+ * run one after another. */
 int lg_decode_noalloc(lg_engine *e, int seq, int32_t first, int steps, int32_t *tokens, float *logits);
 
 /* lg_decode (no logits) with the whole step loop -- every kernel of every step -- captured into one

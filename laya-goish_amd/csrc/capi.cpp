@@ -288,6 +288,14 @@ int lg_engine_sync(lg_engine *e) {
   });
 }
 
+int lg_engine_workspace_bytes(const lg_engine *e, int64_t *bytes) {
+  return guard([&] {
+    NEED(e, "engine");
+    NEED(bytes, "bytes");
+    *bytes = int64_t(e->e->workspace_bytes());
+  });
+}
+
 int lg_matmul(lg_engine *e, const char *tensor, const float *x, int m, const float *bias, float *y) {
   return guard([&] {
     NEED(e, "engine");

@@ -996,9 +996,11 @@ void Engine::batch_run(BatchPlan *b, const int32_t *option_ids, int k, float tem
   if (probs) HIP_CHECK(hipMemcpyAsync(probs, dp, size_t(R) * k * 4, hipMemcpyDeviceToHost, stream));
   if (logprobs) HIP_CHECK(hipMemcpyAsync(logprobs, dlp, size_t(R) * k * 4, hipMemcpyDeviceToHost, stream));
   sync();
-  // a non-finite output is an error, as the reference's (src/models/laya/model.rs:412-414); the
-  // sequences go back to their lengths before this batch
-  for (size_t i = 0; i < size_t(R) * k; ++i)
+  // a non-finite output is an error, as the reference's Laya forward makes it
+  // (src/models/laya/model.rs:412-414); the sequences go back to their lengths before this batch.
+  // The OpenThai forward returns its slot logits as they are (src/models/openthai/model.rs:232-240:
+  // no such check), so its decide sees what the reference's would.
+  for (size_t i = 0; arch != Arch::OpenThai && i < size_t(R) * k; ++i)
     if (!std::isfinite(hl[i])) {
       for (size_t r = 0; r < b->seqs.size(); ++r) seq(b->seqs[r]).len -= b->n[r];
       b->ran = false;
@@ -1046,6 +1048,14 @@ void Engine::forward(int sq, const int32_t *ids, int n, const int32_t *positions
   }
 }
 
+size_t Engine::workspace_bytes() const {
+  size_t n = 0;
+  for (const DevBuf *b : {&ws_x_, &ws_h16_, &ws_qkv_, &ws_q16_, &ws_att16_, &ws_act16_, &ws_meta_, &ws_out_, &ws_dec_,
+                          &ws_ot_qk_, &ws_ot_v_, &ws_ot_gb_, &ws_ot_o_, &ws_ot_part_})
+    n += b->n;
+  return n;
+}
+
 // ------------------------------------------------------------------ greedy decode
 void Engine::decode_check(const Seq &s, int32_t first, int steps, const int32_t *tokens) const {
   if (arch != Arch::Decoder) fail(LG_ERR_UNSUPPORTED, "decode: this model has a decision head, not a language-model head");
@@ -1053,6 +1063,11 @@ void Engine::decode_check(const Seq &s, int32_t first, int steps, const int32_t 
   LG_REQUIRE(first >= 0 && first < V, "decode: token id %d outside the vocabulary", first);
   if (int64_t(s.len) + steps > ctx)
     fail(LG_ERR_INVALID, "sequence of %lld tokens exceeds the context length %d", (long long)s.len + steps, ctx);
+  // the decode attention combines at most 1024 pages (65,536 tokens) of context; refused here,
+  // before any page is reserved or any step runs
+  const int64_t last_pages = (int64_t(s.len) + steps - 1) / 64 + 1;
+  if (last_pages > 1024)
+    fail(LG_ERR_INVALID, "decode: a context of %lld tokens exceeds the decode attention's 65536", (long long)s.len + steps);
 }
 
 // Workspace of a decode run over a sequence holding `npages` pages (its whole page table, which a
@@ -1085,9 +1100,16 @@ void Engine::decode_noalloc(int sq, int32_t first, int steps, int32_t *tokens, f
          "decode_noalloc: %d steps after %d tokens need %zu bytes of scratch; the per-GPU limit is %zu "
          "(use lg_decode for longer contexts)",
          steps, s.len, need, kNoAllocScratchBytes);
+  // one user of this GPU's scratch at a time, from the first launch until the stream has drained
+  std::lock_guard<std::mutex> lock(noalloc_mutex(device));
   void *ws = noalloc_scratch(device);
   reserve_pages(s, s.len + steps);
-  decode_run(s, first, steps, tokens, logits, ws);
+  try {
+    decode_run(s, first, steps, tokens, logits, ws);
+  } catch (...) {
+    (void)hipStreamSynchronize(stream);  // launches already queued still use the scratch
+    throw;
+  }
 }
 
 void Engine::decode_graph(int sq, int32_t first, int steps, int32_t *tokens, double *capture_ms, double *run_ms) {

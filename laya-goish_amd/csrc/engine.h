@@ -165,6 +165,8 @@ class Engine {
 
   lg_model_info info() const;
   void sync();
+  // bytes held by the grow-only workspaces (not weights, not the KV pool)
+  size_t workspace_bytes() const;
 
   // Matrix::apply drop-in on a named uploaded matrix (host pointers).
   void matmul(const std::string &name, const float *x, int m, const float *bias, float *y);

@@ -538,12 +538,7 @@ bool launch_cfg(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &
 #define LAUNCH(E)                                                                                              \
   do {                                                                                                         \
     auto fn = gemm_kernel<KIND, E, MODE, BK, WTM, WTN, STAGES>;                                                \
-    static bool attr = false;                                                                                  \
-    if (!attr) {                                                                                               \
-      HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(fn),                                        \
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, CF::kLdsBytes));                \
-      attr = true;                                                                                             \
-    }                                                                                                          \
+    grant_lds(reinterpret_cast<const void *>(fn), CF::kLdsBytes);                                              \
     launch_timed(fn, grid, block, CF::kLdsBytes, st, Ac, Alc, Mc, K, W, Cc, C16c, C16lc, ldc, bias, MT, NT,    \
                  ffn);                                                                                         \
   } while (0)

@@ -60,18 +60,13 @@ typedef void (*WideFn)(const _Float16 *, const _Float16 *, int, int, const _Floa
                        const float *, int, float *, _Float16 *, _Float16 *, int, const float *, int, int, int,
                        RopeKvOut);
 
-// one kernel per (epilogue, mode); the LDS limit is raised once per kernel
+// one kernel per (epilogue, mode), its LDS limit raised on the current device
 template <int EPI>
 WideFn wide_fn(int mode) {
   using namespace wide;
   static const WideFn fns[3] = {gemm_wide_kernel<EPI, WQ8>, gemm_wide_kernel<EPI, W1>, gemm_wide_kernel<EPI, W2>};
-  static bool attr[3] = {};
   static const int lds_bytes[3] = {Geo<WQ8>::kLdsBytes, Geo<W1>::kLdsBytes, Geo<W2>::kLdsBytes};
-  if (!attr[mode]) {
-    HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(fns[mode]),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, lds_bytes[mode]));
-    attr[mode] = true;
-  }
+  grant_lds(reinterpret_cast<const void *>(fns[mode]), size_t(lds_bytes[mode]));
   return fns[mode];
 }
 

@@ -7,6 +7,10 @@
 // reduces them with cross-lane shuffles; the epilogue adds bias / residual or applies SwiGLU.
 #include <hip/hip_runtime.h>
 
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "common.h"
 #include "kernels.h"
 #include "quant.h"
@@ -293,26 +297,20 @@ __global__ __launch_bounds__(kThreads) void gemv_generic_kernel(const float *__r
 
 // Largest LDS block a workgroup may take on the current device (160 KiB on gfx950).
 size_t lds_limit() {
-  static int bytes = -1;
-  if (bytes < 0) {
-    int dev = 0, v = 0;
+  static std::once_flag once;
+  static int bytes = 0;
+  std::call_once(once, [] {
+    int dev = 0;
     HIP_CHECK(hipGetDevice(&dev));
-    HIP_CHECK(hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
-    bytes = v;
-  }
+    HIP_CHECK(hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
+  });
   return size_t(bytes);
 }
 
-// Launch with `lds` bytes of dynamic LDS, raising the kernel's limit first when it passes the
-// 64 KiB every kernel may take without asking (once per kernel and size).
+// Launch with `lds` bytes of dynamic LDS.
 template <typename F, typename... Args>
 void launch_lds(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t st, Args... args) {
-  static size_t granted = 64 * 1024;
-  if (lds > granted) {
-    HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  int(lds)));
-    granted = lds;
-  }
+  grant_lds(reinterpret_cast<const void *>(kernel), lds);
   launch_timed(kernel, grid, block, lds, st, args...);
 }
 
@@ -366,6 +364,24 @@ void launch_gemv_kind(const float *x, const DevMatrix &W, Epi epi, float *y, con
 }
 
 }  // namespace
+
+// Raise `kernel`'s dynamic LDS limit on the current device to `lds` bytes when it passes the 64 KiB
+// every kernel may take without asking.  The size granted so far is kept per (device, kernel) under
+// a lock: engines on other threads launch the same kernels, and every GEMV instance has the same
+// parameter list, so a counter per launcher template would be shared between kernels.
+void grant_lds(const void *kernel, size_t lds) {
+  if (lds <= 64 * 1024) return;
+  static std::mutex mu;
+  static std::map<std::pair<int, const void *>, size_t> granted;
+  int dev = 0;
+  HIP_CHECK(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(mu);
+  size_t &g = granted[{dev, kernel}];
+  if (lds > g) {
+    HIP_CHECK(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+    g = lds;
+  }
+}
 
 void launch_gemv(const float *x, const DevMatrix &W, Epi epi, float *y, const float *bias,
                  const float *norm_w, float eps, hipStream_t st) {

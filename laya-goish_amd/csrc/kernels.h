@@ -28,6 +28,10 @@ inline void launch_timed(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_
     hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
 }
 
+// Raise `kernel`'s dynamic LDS limit on the current device to `lds` bytes (no-op up to 64 KiB); done
+// once per (device, kernel, size), thread-safe.
+void grant_lds(const void *kernel, size_t lds);
+
 // Repacked device layout of one weight matrix W[rows][cols] (y = x . W^T).
 //   F32 : q = float[rows][cols]
 //   F16 : q = half[rows][cols]

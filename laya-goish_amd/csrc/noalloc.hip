@@ -13,8 +13,15 @@ namespace lg {
 
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
+constexpr int kMaxDevices = 64;
+
+std::mutex &noalloc_mutex(int device) {
+  static std::mutex mu[kMaxDevices];
+  LG_REQUIRE(device >= 0 && device < kMaxDevices, "no-alloc scratch: device %d out of range", device);
+  return mu[device];
+}
+
 void *noalloc_scratch(int device) {
-  constexpr int kMaxDevices = 64;
   static std::mutex mu;
   static void *ptr[kMaxDevices] = {};
   LG_REQUIRE(device >= 0 && device < kMaxDevices, "no-alloc scratch: device %d out of range", device);

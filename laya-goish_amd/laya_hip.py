@@ -257,6 +257,7 @@ def lib() -> ctypes.CDLL:
             "lg_engine_destroy": (None, [P]),
             "lg_engine_info": (I, [P, ctypes.POINTER(ModelInfo)]),
             "lg_engine_sync": (I, [P]),
+            "lg_engine_workspace_bytes": (I, [P, ctypes.POINTER(ctypes.c_int64)]),
             "lg_matmul": (I, [P, ctypes.c_char_p, P, I, P, P]),
             "lg_seq_create": (I, [P, ctypes.POINTER(I)]),
             "lg_seq_fork": (I, [P, I, I, ctypes.POINTER(I)]),
@@ -518,6 +519,12 @@ class Engine:
 
     def sync(self):
         check(lib().lg_engine_sync(self.h))
+
+    def workspace_bytes(self) -> int:
+        """Device bytes held by the engine's grow-only workspaces (lg_engine_workspace_bytes)."""
+        n = ctypes.c_int64()
+        check(lib().lg_engine_workspace_bytes(self.h, ctypes.byref(n)))
+        return n.value
 
     def matmul(self, tensor: str, x, bias=None) -> np.ndarray:
         x = _c(x, np.float32)

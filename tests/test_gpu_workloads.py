@@ -179,3 +179,30 @@ def test_q4km_7b_large_batch_equals_single_requests(lh, po):
     err = assert_logits_close(logits[33:36], want, rel=logit_bar(0))
     print(f"q4km-7b 12 x 700: bit-identical to single requests; logit rel {err:.2e} vs oracle")
     eng.close()
+
+
+def test_two_engines_large_k_gemv_kernels(lh, po):
+    """Two 7B-shape engines in one process whose down projections (K = 18944: an x stage of 74 KiB, past
+    the 64 KiB of LDS a kernel gets without asking) take different GEMV kernels, Q6_K and F16.  Both
+    engines exist before either decodes, and each decodes like the oracle: the raised LDS limit is kept
+    per kernel, not per launcher."""
+    engines = []
+    for preset, seed in (("q4km-7b", 31), ("f16-7b", 32)):
+        img = lh.SynthImage(preset, seed=seed, n_layers=1)
+        engines.append((preset, img, lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=512)))
+    for preset, img, eng in engines:
+        om = po.Model(po.Gguf(img.array()), threads=16)
+        ids = _ids(120, om.V, 33)
+        s = eng.seq_create()
+        eng.forward(s, ids[:-1], [], [0])
+        print(f"{preset} L1: decode 3 steps with the other engine loaded", flush=True)
+        toks, logits = eng.decode(s, int(ids[-1]), 3, want_logits=True)
+        c = om.cache(200)
+        om.prefill(c, ids[:-1], [])
+        for i, t in enumerate([int(ids[-1])] + [int(t) for t in toks[:-1]]):
+            want = om.head(om.prefill(c, [t], [0]))
+            assert_logits_close(logits[i], want, rel=logit_bar(0))
+            assert_argmax_equal(logits[i][None], want)
+        del om
+    for _, _, eng in engines:
+        eng.close()

@@ -2,9 +2,10 @@
 
 Both run the same kernels on the same sequence state, so tokens and every step's full-vocabulary
 logits must be bit-identical.  Two calls in a row, the second with a shorter context and fewer
-steps, so a stale scratch from the first call would show.  (The 16 MiB scratch limit is not
-reachable with the shipped model shapes: the largest, the 7B shape at its full context, needs
-under 3 MiB.)
+steps, so a stale scratch from the first call would show.  On a fresh engine the allocation-free
+decode grows none of the engine's device workspaces (lg_engine_workspace_bytes), while lg_decode
+then grows its decode workspace.  (The 16 MiB scratch is not reachable with the shipped model
+shapes: decode refuses contexts beyond 65,536 tokens, and the 7B shape would need it at ~70k.)
 """
 import numpy as np
 import pytest
@@ -34,6 +35,24 @@ def test_decode_noalloc_equals_decode(lh, preset, layers):
         assert np.array_equal(eng.decode(c, int(ids[-1]), steps, noalloc=True), want_t)
         for s in (a, b, c, base):
             eng.seq_free(s)
+    eng.close()
+
+
+def test_decode_noalloc_allocates_nothing(lh):
+    img = lh.SynthImage("tiny-q8", seed=22)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=2048)
+    V = eng.info["vocab"]
+    ids = np.random.default_rng(5).integers(0, V, 200).astype(np.int32)
+    s = eng.seq_create()
+    eng.forward(s, ids, [], [0])
+    before = eng.workspace_bytes()
+    print(f"fresh engine: {before} workspace bytes before the first decode", flush=True)
+    a, b = eng.seq_fork(s, 200), eng.seq_fork(s, 200)
+    got = eng.decode(a, int(ids[-1]), 6, noalloc=True)
+    assert eng.workspace_bytes() == before, "lg_decode_noalloc grew a device workspace"
+    want = eng.decode(b, int(ids[-1]), 6)
+    assert eng.workspace_bytes() > before, "lg_decode's workspace is not visible to the query"
+    assert np.array_equal(got, want)
     eng.close()
 
 
