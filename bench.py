@@ -309,6 +309,26 @@ Q4K_REQS, Q4K_TOKENS = 32, 1024
 C5_REQS, C5_PREFIX, C5_OWN, C5_QUESTIONS = 16, 6144, 2048, 8
 
 
+def q4k_workload():
+    """The C4 batch: 32 requests of 1024 random ids, the last position scored over 4 option ids."""
+    rng = np.random.default_rng(SEED + 3)
+    reqs = [(rng.integers(0, 152064, Q4K_TOKENS).astype(np.int32), np.array([Q4K_TOKENS - 1], np.int32))
+            for _ in range(Q4K_REQS)]
+    opts = rng.choice(152064, 4, replace=False).astype(np.int32)
+    return reqs, opts
+
+
+def c5_workload():
+    """The C5 step's inputs: the shared 6144-id prefix, 16 own 2048-id suffixes, the 8 answer positions
+    of each suffix (every 256th token) and 4 option ids."""
+    rng = np.random.default_rng(SEED + 4)
+    prefix = rng.integers(0, 152064, C5_PREFIX).astype(np.int32)
+    own = [rng.integers(0, 152064, C5_OWN).astype(np.int32) for _ in range(C5_REQS)]
+    pos = np.arange(C5_OWN // C5_QUESTIONS - 1, C5_OWN, C5_OWN // C5_QUESTIONS).astype(np.int32)
+    opts = rng.choice(152064, 4, replace=False).astype(np.int32)
+    return prefix, own, pos, opts
+
+
 def cpu_layer_cost_7b(args, po):
     """The oracle on one layer of the 7B shape (d3584, GQA 28/4 x 128, FFN 18944): seconds for one
     1024-token request through one layer, per thread count (F32 weights after the load-time expansion,
@@ -345,10 +365,7 @@ def c4_q4k(args, prec, layer_cost):
     load = load_entry(eng)
     log(f"C4 model ready in {time.perf_counter() - t0:.1f}s (engine load {load['seconds']} s, "
         f"{load['GB_per_s']} GB/s of GGUF weights)")
-    rng = np.random.default_rng(SEED + 3)
-    reqs = [(rng.integers(0, 152064, Q4K_TOKENS).astype(np.int32), np.array([Q4K_TOKENS - 1], np.int32))
-            for _ in range(Q4K_REQS)]
-    opts = rng.choice(152064, 4, replace=False).astype(np.int32)
+    reqs, opts = q4k_workload()
     seqs = [eng.seq_create() for _ in reqs]
     batch = eng.batch([(s, ids, pos) for s, (ids, pos) in zip(seqs, reqs)])
     warm, steps = 2, args.config_steps
@@ -409,11 +426,7 @@ def c5_long_context(args, prec, layer_cost):
     load = load_entry(eng)
     log(f"C5 model ready in {time.perf_counter() - t0:.1f}s (engine load {load['seconds']} s, "
         f"{load['GB_per_s']} GB/s of GGUF weights)")
-    rng = np.random.default_rng(SEED + 4)
-    prefix = rng.integers(0, 152064, C5_PREFIX).astype(np.int32)
-    own = [rng.integers(0, 152064, C5_OWN).astype(np.int32) for _ in range(C5_REQS)]
-    pos = np.arange(C5_OWN // C5_QUESTIONS - 1, C5_OWN, C5_OWN // C5_QUESTIONS).astype(np.int32)
-    opts = rng.choice(152064, 4, replace=False).astype(np.int32)
+    prefix, own, pos, opts = c5_workload()
 
     def step():
         base = eng.seq_create()
@@ -851,6 +864,55 @@ def bench_laya(args, prec):
     return line
 
 
+VENDOR_SHAPES = {
+    "C2 q|k|v": (35840, 6144, 2048), "C2 o": (35840, 2048, 2048), "C2 gate|up": (35840, 11264, 2048),
+    "C2 down": (35840, 2048, 5632), "7B q|k|v": (32768, 4608, 3584), "7B o": (32768, 3584, 3584),
+    "7B gate|up": (32768, 37888, 3584), "7B down": (32768, 3584, 18944),
+}
+
+
+def bench_vendor_gemm(args, prec):
+    """The practical f16 MFMA rate at the prefill projection shapes: torch.matmul (x[M][K] . W[N][K]^T in
+    f16 with f32 accumulation, ROCm's vendor GEMM libraries) on the same GPU.  One f16 pass per product,
+    so half this rate bounds a two-pass (hi/lo split) GEMM of the same shape built on the same libraries.
+    Not a path of this build: a measured anchor for the roofline fractions."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    libs = [("hipblaslt", "cublaslt"), ("rocblas", "cublas")]
+    rows = {}
+    for label, (M, N, K) in VENDOR_SHAPES.items():
+        g = torch.Generator(device=dev).manual_seed(1)
+        a = torch.randn(M, K, device=dev, dtype=torch.float16, generator=g)
+        w = torch.randn(N, K, device=dev, dtype=torch.float16, generator=g)
+        row = {"M": M, "N": N, "K": K}
+        for name, key in libs:
+            try:
+                torch.backends.cuda.preferred_blas_library(key)
+                for _ in range(3):
+                    torch.matmul(a, w.t())
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                reps = 10
+                e0.record()
+                for _ in range(reps):
+                    torch.matmul(a, w.t())
+                e1.record()
+                torch.cuda.synchronize()
+                ms = e0.elapsed_time(e1) / reps
+                tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+                row[name] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac": round(tf / PEAK_F16_TFLOPS, 4)}
+                log(f"vendor f16 GEMM {label:12s} {M} x {N} x {K} ({name}): {ms:.3f} ms, {tf:.1f} TFLOP/s")
+            except RuntimeError as e:  # a library that refuses the shape or is absent
+                row[name] = {"error": str(e)[:200]}
+        rows[label] = row
+        del a, w
+    torch.backends.cuda.preferred_blas_library("cublaslt")
+    return {"workload": "vendor f16 GEMM at the prefill projection shapes (torch.matmul, f16 operands, f32 "
+                        "accumulation): a measured practical MFMA rate, not part of this build's path",
+            "peak_TFLOP/s": PEAK_F16_TFLOPS, "shapes": rows}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -858,7 +920,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--precision", choices=["exact", "fast"], default="exact")
     ap.add_argument("--workload", choices=["decide", "plumbing", "q4k-prefill", "long-context", "decide-request",
-                                           "decide-batch", "openthai-decide", "laya-decide"],
+                                           "decide-batch", "openthai-decide", "laya-decide", "vendor-gemm"],
                     default="decide",
                     help="decide (default): the Q8_0 d2048 batched decide headline with the other four workload "
                          "configurations (C1 plumbing, C3 decode, C4 Q4_K 7B prefill, C5 long context) nested in "
@@ -890,7 +952,7 @@ def main():
         return
     if args.workload != "decide":
         fn = {"decide-request": bench_decide_request, "decide-batch": bench_decide_batch,
-              "openthai-decide": bench_openthai, "laya-decide": bench_laya}
+              "openthai-decide": bench_openthai, "laya-decide": bench_laya, "vendor-gemm": bench_vendor_gemm}
         print(json.dumps(fn[args.workload](args, prec)), flush=True)
         return
     wanted = [c.strip().upper() for c in args.configs.split(",") if c.strip()]

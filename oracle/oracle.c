@@ -668,6 +668,8 @@ typedef struct {
 struct or_model {
   int L, d, hq, hkv, hd, f, V, ctx, threads;
   float eps;
+  const or_gguf *g; /* the file the weights are decoded from (borrowed) */
+  int streamed;     /* layers decoded at each use and freed after it (or_model_load_streamed) */
   const uint8_t *emb; /* raw embedding rows in the GGUF */
   uint32_t emb_kind;
   or_layer *layers;
@@ -689,26 +691,56 @@ static int set_err(char *err, int errlen, const char *fmt, ...) {
   return -1;
 }
 
-/* Decode a tensor with dims [cols, rows] (gguf.rs order) into a fresh f32 buffer. */
-static float *load_f32(const or_gguf *g, const char *name, uint64_t cols, uint64_t rows, char *err,
-                       int errlen) {
+/* Decode whole blocks [lo, hi) of one tensor (each worker its own range; gguf.rs:250-336 per block). */
+typedef struct {
   uint32_t kind;
+  const uint8_t *data;
+  uint64_t bsize, belems;
+  float *out;
+} decode_ctx;
+static void decode_blocks(void *p, int lo, int hi) {
+  const decode_ctx *c = (const decode_ctx *)p;
+  or_decode(c->kind, c->data + (uint64_t)lo * c->bsize, (uint64_t)(hi - lo) * c->bsize,
+            c->out + (uint64_t)lo * c->belems);
+}
+
+/* Find a tensor with dims [cols, rows] (gguf.rs order); 0 if present with that shape. */
+static int find_tensor(const or_gguf *g, const char *name, uint64_t cols, uint64_t rows, uint32_t *kind,
+                       const uint8_t **data, uint64_t *len, char *err, int errlen) {
   uint64_t dims[4];
   int nd;
-  const uint8_t *data;
-  uint64_t len;
-  if (or_gguf_tensor(g, name, &kind, dims, &nd, &data, &len)) {
+  if (or_gguf_tensor(g, name, kind, dims, &nd, data, len)) {
     set_err(err, errlen, "missing tensor %s", name);
-    return NULL;
+    return -1;
   }
   uint64_t count = 1;
   for (int i = 0; i < nd; ++i) count *= dims[i];
   if (count != cols * rows || dims[0] != cols) {
     set_err(err, errlen, "%s: unexpected shape", name);
+    return -1;
+  }
+  return 0;
+}
+
+/* Decode a tensor with dims [cols, rows] into a fresh f32 buffer, its blocks split over `threads`
+ * workers (the decode of each block does not depend on the split). */
+static float *load_f32(const or_gguf *g, const char *name, uint64_t cols, uint64_t rows, int threads, char *err,
+                       int errlen) {
+  uint32_t kind;
+  const uint8_t *data;
+  uint64_t len, block, size;
+  if (find_tensor(g, name, cols, rows, &kind, &data, &len, err, errlen)) return NULL;
+  float *o = (float *)malloc(cols * rows * sizeof(float));
+  if (!o) {
+    set_err(err, errlen, "%s: out of memory", name);
     return NULL;
   }
-  float *o = (float *)malloc(count * sizeof(float));
-  or_decode(kind, data, len, o);
+  if (or_layout(kind, &block, &size) || len % size || len / size > 0x7fffffffULL) {
+    or_decode(kind, data, len, o);
+  } else {
+    decode_ctx c = {kind, data, size, block, o};
+    parallel((int)(len / size), threads, decode_blocks, &c);
+  }
   return o;
 }
 
@@ -728,14 +760,16 @@ static float *cat_rows(float *a, size_t na, float *b, size_t nb, float *c, size_
   return o;
 }
 
+static void free_layer(or_layer *y) {
+  free(y->attn_norm); free(y->ffn_norm); free(y->wqkv); free(y->bqkv);
+  free(y->wo); free(y->wi); free(y->wd);
+  memset(y, 0, sizeof *y);
+}
+
 void or_model_free(or_model *m) {
   if (!m) return;
   if (m->layers)
-    for (int l = 0; l < m->L; ++l) {
-      or_layer *y = &m->layers[l];
-      free(y->attn_norm); free(y->ffn_norm); free(y->wqkv); free(y->bqkv);
-      free(y->wo); free(y->wi); free(y->wd);
-    }
+    for (int l = 0; l < m->L; ++l) free_layer(&m->layers[l]);
   free(m->layers);
   free(m->final_norm);
   free(m->head);
@@ -744,13 +778,73 @@ void or_model_free(or_model *m) {
   free(m);
 }
 
-or_model *or_model_load(const or_gguf *g, int threads, char *err, int errlen) {
+/* Decode layer l's tensors into y (check != 0: only verify that they exist with their shapes, and
+ * leave y empty).  Fused q|k|v and gate|up tensors, or their parts concatenated by rows.  0 on success;
+ * on failure y holds whatever was decoded, for free_layer. */
+static int load_layer(const or_model *m, int l, or_layer *y, int check, char *err, int errlen) {
+  const or_gguf *g = m->g;
+  int d = m->d, f = m->f, qrows = m->hq * m->hd, kvrows = m->hkv * m->hd;
+  char name[128];
+  memset(y, 0, sizeof *y);
+#define LOAD(dst, fmt, cols, rows)                                                                         \
+  do {                                                                                                     \
+    snprintf(name, sizeof name, fmt, l);                                                                   \
+    if (check) {                                                                                           \
+      uint32_t k_;                                                                                         \
+      const uint8_t *d_;                                                                                   \
+      uint64_t n_;                                                                                         \
+      if (find_tensor(g, name, (uint64_t)(cols), (uint64_t)(rows), &k_, &d_, &n_, err, errlen)) return -1; \
+      dst = NULL;                                                                                          \
+    } else if (!(dst = load_f32(g, name, (uint64_t)(cols), (uint64_t)(rows), m->threads, err, errlen))) { \
+      return -1;                                                                                           \
+    }                                                                                                      \
+  } while (0)
+  LOAD(y->attn_norm, "attn_norm.%d.weight", d, 1);
+  LOAD(y->ffn_norm, "ffn_norm.%d.weight", d, 1);
+  snprintf(name, sizeof name, "qkv.%d.weight", l);
+  if (has(g, name)) {
+    LOAD(y->wqkv, "qkv.%d.weight", d, qrows + 2 * kvrows);
+    snprintf(name, sizeof name, "qkv.%d.bias", l);
+    if (has(g, name)) LOAD(y->bqkv, "qkv.%d.bias", qrows + 2 * kvrows, 1);
+  } else {
+    float *q, *k, *v;
+    LOAD(q, "q.%d.weight", d, qrows);
+    LOAD(k, "k.%d.weight", d, kvrows);
+    LOAD(v, "v.%d.weight", d, kvrows);
+    if (!check) y->wqkv = cat_rows(q, (size_t)qrows * d, k, (size_t)kvrows * d, v, (size_t)kvrows * d);
+    snprintf(name, sizeof name, "q.%d.bias", l);
+    if (has(g, name)) {
+      float *bq, *bk, *bv;
+      LOAD(bq, "q.%d.bias", qrows, 1);
+      LOAD(bk, "k.%d.bias", kvrows, 1);
+      LOAD(bv, "v.%d.bias", kvrows, 1);
+      if (!check) y->bqkv = cat_rows(bq, (size_t)qrows, bk, (size_t)kvrows, bv, (size_t)kvrows);
+    }
+  }
+  LOAD(y->wo, "wo.%d.weight", qrows, d);
+  snprintf(name, sizeof name, "mlp_wi.%d.weight", l);
+  if (has(g, name)) {
+    LOAD(y->wi, "mlp_wi.%d.weight", d, 2 * f);
+  } else {
+    float *ga, *up;
+    LOAD(ga, "gate.%d.weight", d, f);
+    LOAD(up, "up.%d.weight", d, f);
+    if (!check) y->wi = cat_rows(ga, (size_t)f * d, up, (size_t)f * d, NULL, 0);
+  }
+  LOAD(y->wd, "mlp_wo.%d.weight", f, d);
+#undef LOAD
+  return 0;
+}
+
+static or_model *model_open(const or_gguf *g, int threads, int streamed, char *err, int errlen) {
   if (strcmp(or_gguf_str(g, "general.architecture"), "ggmlc") ||
       strcmp(or_gguf_str(g, "laya.model_name"), "laya-decoder")) {
     set_err(err, errlen, "not a laya-decoder GGUF");
     return NULL;
   }
   or_model *m = (or_model *)calloc(1, sizeof(*m));
+  m->g = g;
+  m->streamed = streamed;
   m->L = (int)or_gguf_num(g, "laya.decoder.block_count", 0);
   m->d = (int)or_gguf_num(g, "laya.decoder.embedding_length", 0);
   m->hq = (int)or_gguf_num(g, "laya.decoder.head_count", 0);
@@ -767,7 +861,7 @@ or_model *or_model_load(const or_gguf *g, int threads, char *err, int errlen) {
     or_model_free(m);
     return NULL;
   }
-  int d = m->d, hq = m->hq, hkv = m->hkv, hd = m->hd, f = m->f;
+  int d = m->d, hd = m->hd;
   uint32_t kind;
   uint64_t dims[4];
   int nd;
@@ -780,61 +874,27 @@ or_model *or_model_load(const or_gguf *g, int threads, char *err, int errlen) {
   }
   m->emb_kind = kind;
   m->layers = (or_layer *)calloc((size_t)m->L, sizeof(or_layer));
-  char name[128];
-  int qrows = hq * hd, kvrows = hkv * hd;
-  for (int l = 0; l < m->L; ++l) {
-    or_layer *y = &m->layers[l];
-#define LOAD(dst, fmt, cols, rows)                                              \
-  do {                                                                          \
-    snprintf(name, sizeof name, fmt, l);                                        \
-    if (!(dst = load_f32(g, name, (uint64_t)(cols), (uint64_t)(rows), err, errlen))) { \
-      or_model_free(m);                                                         \
-      return NULL;                                                              \
-    }                                                                           \
-  } while (0)
-    LOAD(y->attn_norm, "attn_norm.%d.weight", d, 1);
-    LOAD(y->ffn_norm, "ffn_norm.%d.weight", d, 1);
-    snprintf(name, sizeof name, "qkv.%d.weight", l);
-    if (has(g, name)) {
-      LOAD(y->wqkv, "qkv.%d.weight", d, qrows + 2 * kvrows);
-      snprintf(name, sizeof name, "qkv.%d.bias", l);
-      if (has(g, name)) LOAD(y->bqkv, "qkv.%d.bias", qrows + 2 * kvrows, 1);
-    } else {
-      float *q, *k, *v;
-      LOAD(q, "q.%d.weight", d, qrows);
-      LOAD(k, "k.%d.weight", d, kvrows);
-      LOAD(v, "v.%d.weight", d, kvrows);
-      y->wqkv = cat_rows(q, (size_t)qrows * d, k, (size_t)kvrows * d, v, (size_t)kvrows * d);
-      snprintf(name, sizeof name, "q.%d.bias", l);
-      if (has(g, name)) {
-        float *bq, *bk, *bv;
-        LOAD(bq, "q.%d.bias", qrows, 1);
-        LOAD(bk, "k.%d.bias", kvrows, 1);
-        LOAD(bv, "v.%d.bias", kvrows, 1);
-        y->bqkv = cat_rows(bq, (size_t)qrows, bk, (size_t)kvrows, bv, (size_t)kvrows);
-      }
+  for (int l = 0; l < m->L; ++l)
+    if (load_layer(m, l, &m->layers[l], streamed, err, errlen)) {
+      or_model_free(m);
+      return NULL;
     }
-    LOAD(y->wo, "wo.%d.weight", qrows, d);
-    snprintf(name, sizeof name, "mlp_wi.%d.weight", l);
-    if (has(g, name)) {
-      LOAD(y->wi, "mlp_wi.%d.weight", d, 2 * f);
-    } else {
-      float *ga, *up;
-      LOAD(ga, "gate.%d.weight", d, f);
-      LOAD(up, "up.%d.weight", d, f);
-      y->wi = cat_rows(ga, (size_t)f * d, up, (size_t)f * d, NULL, 0);
-    }
-    LOAD(y->wd, "mlp_wo.%d.weight", f, d);
-#undef LOAD
-  }
-  if (!(m->final_norm = load_f32(g, "final_norm.weight", (uint64_t)d, 1, err, errlen)) ||
-      !(m->head = load_f32(g, "output.weight", (uint64_t)d, (uint64_t)m->V, err, errlen)) ||
-      !(m->cosf_ = load_f32(g, "cos_full", (uint64_t)hd, (uint64_t)m->ctx, err, errlen)) ||
-      !(m->sinf_ = load_f32(g, "sin_full", (uint64_t)hd, (uint64_t)m->ctx, err, errlen))) {
+  if (!(m->final_norm = load_f32(g, "final_norm.weight", (uint64_t)d, 1, m->threads, err, errlen)) ||
+      !(m->head = load_f32(g, "output.weight", (uint64_t)d, (uint64_t)m->V, m->threads, err, errlen)) ||
+      !(m->cosf_ = load_f32(g, "cos_full", (uint64_t)hd, (uint64_t)m->ctx, m->threads, err, errlen)) ||
+      !(m->sinf_ = load_f32(g, "sin_full", (uint64_t)hd, (uint64_t)m->ctx, m->threads, err, errlen))) {
     or_model_free(m);
     return NULL;
   }
   return m;
+}
+
+or_model *or_model_load(const or_gguf *g, int threads, char *err, int errlen) {
+  return model_open(g, threads, 0, err, errlen);
+}
+
+or_model *or_model_load_streamed(const or_gguf *g, int threads, char *err, int errlen) {
+  return model_open(g, threads, 1, err, errlen);
 }
 
 void or_model_dims(const or_model *m, int out[8]) {
@@ -1047,8 +1107,19 @@ int or_prefill(or_model *m, or_cache *c, const int32_t *ids, int n, const int32_
   float *y = (float *)malloc((size_t)n * d * sizeof(float));
   float *gu = (float *)malloc((size_t)n * 2 * f * sizeof(float));
   float *act = (float *)malloc((size_t)n * f * sizeof(float));
+  or_layer streamed_layer;
+  memset(&streamed_layer, 0, sizeof streamed_layer);
+  int rc = 0;
   for (int l = 0; l < m->L; ++l) {
     const or_layer *ly = &m->layers[l];
+    if (m->streamed) {  /* this layer's weights only while it runs */
+      free_layer(&streamed_layer);
+      if (load_layer(m, l, &streamed_layer, 0, NULL, 0)) {
+        rc = -1;
+        break;
+      }
+      ly = &streamed_layer;
+    }
     float *K = c->k + (size_t)l * c->cap * kvw, *V = c->v + (size_t)l * c->cap * kvw;
     or_rms(x, n, d, ly->attn_norm, 0.0f, m->eps, h);
     or_apply(ly->wqkv, qkvw, d, h, n, ly->bqkv, m->threads, qkv);
@@ -1077,11 +1148,14 @@ int or_prefill(or_model *m, or_cache *c, const int32_t *ids, int n, const int32_
     or_apply(ly->wd, d, f, act, n, NULL, m->threads, y);
     for (size_t i = 0; i < (size_t)n * d; ++i) x[i] = x[i] + y[i];
   }
-  for (int i = 0; i < ngather; ++i)
-    memcpy(hidden + (size_t)i * d, x + (size_t)gather[i] * d, (size_t)d * sizeof(float));
-  c->len = pos0 + n;
+  free_layer(&streamed_layer);
+  if (rc == 0) {
+    for (int i = 0; i < ngather; ++i)
+      memcpy(hidden + (size_t)i * d, x + (size_t)gather[i] * d, (size_t)d * sizeof(float));
+    c->len = pos0 + n;
+  }
   free(x); free(h); free(qkv); free(q); free(att); free(y); free(gu); free(act);
-  return 0;
+  return rc;
 }
 
 int or_head(or_model *m, const float *hidden, int rows, const int32_t *vocab_ids, int nv,

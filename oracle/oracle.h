@@ -60,6 +60,11 @@ float or_silu(float x);
 /* ---- assembled decoder (Llama/Qwen2 shape) ---- */
 typedef struct or_model or_model;
 or_model *or_model_load(const or_gguf *g, int threads, char *err, int errlen);
+/* The same model with its layers decoded only while they run: or_prefill decodes layer l's weights
+ * to F32 (the same gguf.rs:250-336 decode), runs it and frees it, so a full-depth forward of a 7B
+ * shape holds one layer of F32 weights instead of all of them.  Results are bit-identical to
+ * or_model_load's.  The GGUF handle must outlive the model. */
+or_model *or_model_load_streamed(const or_gguf *g, int threads, char *err, int errlen);
 void or_model_free(or_model *m);
 /* layers, d_model, heads, kv_heads, head_dim, ffn, vocab, context */
 void or_model_dims(const or_model *m, int out[8]);

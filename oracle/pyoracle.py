@@ -42,6 +42,7 @@ def lib() -> ctypes.CDLL:
             "or_rms": (None, [P, I, I, P, F, F, P]),
             "or_silu": (F, [F]),
             "or_model_load": (P, [P, I, ctypes.c_char_p, I]),
+            "or_model_load_streamed": (P, [P, I, ctypes.c_char_p, I]),
             "or_model_free": (None, [P]),
             "or_model_dims": (None, [P, P]),
             "or_model_set_threads": (None, [P, I]),
@@ -211,10 +212,13 @@ class Gguf:
 class Model:
     """The assembled decoder on the CPU: prefill with an f32 K/V cache, head, argmax."""
 
-    def __init__(self, gguf: Gguf, threads: int = 4):
+    def __init__(self, gguf: Gguf, threads: int = 4, streamed: bool = False):
+        """streamed=True decodes each layer's weights only while it runs (or_model_load_streamed):
+        one layer of F32 weights resident instead of the whole model, the same results."""
         self.g = gguf
         err = ctypes.create_string_buffer(256)
-        self.h = lib().or_model_load(gguf.h, threads, err, 256)
+        load = lib().or_model_load_streamed if streamed else lib().or_model_load
+        self.h = load(gguf.h, threads, err, 256)
         if not self.h:
             raise ValueError(err.value.decode())
         dims = np.zeros(8, dtype=np.int32)

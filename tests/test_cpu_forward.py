@@ -168,3 +168,24 @@ def test_gqa_equals_mha_with_duplicated_heads(lh, po):
     a = po.Model(g, threads=2).forward(ids, [44, 3, 20])
     b = po.Model(mha, threads=2).forward(ids, [44, 3, 20])
     assert np.array_equal(a, b)
+
+
+def test_streamed_layers_bit_exact(model):
+    """The layer-streamed oracle (each layer's weights decoded only while it runs, over 1 or 7 decode
+    workers) gives the eager oracle's bits: one-shot forwards, cache continuation and a fork."""
+    name, g, om, _ = model
+    ids = _ids(70, om.V, 9)
+    pos = [69, 31, 0]
+    want = om.forward(ids, pos)
+    for t in (1, 7):
+        sm = type(om)(g, threads=t, streamed=True)
+        got = sm.forward(ids, pos)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"{name}: streamed ({t}) != eager"
+        c = sm.cache(100)
+        sm.prefill(c, ids[:40], [])
+        k = c.fork(40)
+        h = sm.head(sm.prefill(k, ids[40:], [29, 0]))
+        ce = om.cache(100)
+        om.prefill(ce, ids[:40], [])
+        he = om.head(om.prefill(ce.fork(40), ids[40:], [29, 0]))
+        assert np.array_equal(h.view(np.uint32), he.view(np.uint32)), f"{name}: streamed fork != eager"

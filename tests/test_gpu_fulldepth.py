@@ -8,10 +8,17 @@
   steps; the oracle is fed the same tokens (teacher forcing) through its KV-cached decode and
   every step's full-vocabulary logits and argmax are compared.
 
+  Q4_K/Q6_K 7B-shape prefill (28 layers, d3584, GQA 28/4, FFN 18944, vocab 152064, QKV bias): the
+  benchmark's own batch of 32 x 1024 tokens on the GPU, three of its requests again alone (bit for
+  bit), and one request through all 28 layers of the layer-streamed oracle (full-vocabulary logits).
+  F16 7B-shape shared prefix (28 layers): a 1024-token prefix computed once and forked into two
+  requests of 256 own tokens with 8 answer positions each, against the oracle's forked cache, and
+  against the same request computed unshared (bit for bit).  Both precision modes.
+
 Bars (north star): logits within 2e-2 of the largest |logit| per row, option probabilities within
-1e-3 absolute, argmax equal.  A step whose oracle top-2 gap is below an absolute window tied to
-the largest measured logit error of the run is a near-tie: it is reported with its gap and not
-asserted.  The measured errors are printed.
+1e-3 absolute, argmax equal.  For the decode's argmax, a step whose oracle top-2 gap is below twice
+the oracle's own distance to a float64 forward of the same steps is a near-tie, and is decided
+against the float64 argmax instead.  The measured errors are printed.
 
 Reference path: Model::forward (src/models/openthai/model.rs:192-241), option scoring
 (src/models/openthai/decision.rs:268-279), greedy argmax with the first maximum winning
@@ -55,7 +62,7 @@ def _near_tie_report(gpu, ref, window):
     return bad, ties
 
 
-def test_q8_prefill_decide_24_layers(lh, po, q8_full):
+def test_q8_prefill_decide_24_layers(lh, po, q8_full, tmp_path):
     import bench
     import np_model
 
@@ -84,7 +91,7 @@ def test_q8_prefill_decide_24_layers(lh, po, q8_full):
         got_l = logits[r * npos:(r + 1) * npos]
         got_p = probs[r * npos:(r + 1) * npos]
         p_ref, p_ex, p_ot = P(want), P(exact), P(other)
-        np.save(f"gpurun_out/c2_req{r}.npy", np.stack([got_l.astype(np.float64), want, exact, other]))
+        np.save(tmp_path / f"c2_req{r}.npy", np.stack([got_l.astype(np.float64), want, exact, other]))
         for what, a, b, pa, pb in (("gpu-oracle", got_l, want, got_p, p_ref), ("gpu-f64", got_l, exact, got_p, p_ex),
                                    ("oracle-f64", want, exact, p_ref, p_ex), ("npf32-f64", other, exact, p_ot, p_ex),
                                    ("oracle-npf32", want, other, p_ref, p_ot)):
@@ -98,6 +105,7 @@ def test_q8_prefill_decide_24_layers(lh, po, q8_full):
 
 def test_q8_decode_24_layers_64_steps(lh, po, q8_full):
     import bench
+    import np_model
 
     img, om = q8_full
     V = 32000
@@ -130,13 +138,166 @@ def test_q8_decode_24_layers_64_steps(lh, po, q8_full):
     print(f"decode logits: worst rel {max(per_step):.3e} (step {int(np.argmax(per_step))}), worst abs "
           f"{abs_err:.3e}, median rel {float(np.median(per_step)):.3e}", flush=True)
     assert max(per_step) <= LOGIT_REL
-    # near-tie window: four times the worst absolute logit error measured in this run
-    window = 4.0 * abs_err
+
+    # The near-tie window comes from the oracle alone: the same 64 steps in float64 (one forward over the
+    # context and the fed tokens), and twice the oracle's largest distance to them, the room two correct
+    # f32 orders have on either side of the exact value.  A step outside the window must give the
+    # oracle's argmax; a step inside it must give the float64 argmax.
+    t0 = time.perf_counter()
+    seq = np.concatenate([ids, np.asarray(feed, np.int32)])
+    exact = np_model.F64Model(po.Gguf(img.array())).logits(seq, np.arange(bench.DECODE_CTX, bench.DECODE_CTX + steps))
+    print(f"float64 forward over {len(seq)} tokens: {time.perf_counter() - t0:.1f}s", flush=True)
+    oracle_spread = float(np.abs(want - exact).max())
+    gpu_f64 = float(np.abs(logits - exact).max())
+    window = 2.0 * oracle_spread
+    print(f"largest |oracle - f64| {oracle_spread:.3e}, |gpu - f64| {gpu_f64:.3e}; near-tie window {window:.3e}",
+          flush=True)
     bad, ties = _near_tie_report(logits, want, window)
+    flips = []
     for i, gap in ties:
-        print(f"  near-tie at step {i}: oracle top-2 gap {gap:.3e} < window {window:.3e}", flush=True)
+        g, o, x = int(np.argmax(logits[i])), int(np.argmax(want[i])), int(np.argmax(exact[i]))
+        top = np.sort(exact[i])
+        print(f"  near-tie at step {i}: oracle gap {gap:.3e}, f64 gap {top[-1] - top[-2]:.3e}; argmax gpu {g}, "
+              f"oracle {o}, f64 {x}", flush=True)
+        if g != x:
+            flips.append((i, g, x))
     gaps = [float(np.sort(w)[-1] - np.sort(w)[-2]) for w in want]
-    flips = [i for i, _ in ties if int(np.argmax(logits[i])) != int(np.argmax(want[i]))]
-    print(f"argmax: {steps - len(ties)} steps asserted, {len(ties)} near-ties (argmax differs at {flips}), "
-          f"smallest gap {min(gaps):.3e}")
-    assert not bad, f"argmax mismatches (step, gap, gpu, oracle): {bad}"
+    print(f"argmax: {steps - len(ties)} steps asserted against the oracle, {len(ties)} near-ties decided in "
+          f"float64, GPU != f64 at {flips}; smallest oracle gap {min(gaps):.3e}", flush=True)
+    assert not bad, f"argmax mismatches outside near-ties (step, gap, gpu, oracle): {bad}"
+    assert not flips, f"near-tie steps where the GPU's argmax is not the float64 one (step, gpu, f64): {flips}"
+
+
+def _argmax_ok(gpu, ref, window):
+    """Row-wise argmax equal wherever the reference's top-2 gap is at least `window`; returns the
+    smallest gap seen."""
+    gaps = []
+    for g, r in zip(np.atleast_2d(gpu), np.atleast_2d(ref)):
+        top = np.sort(r)
+        gaps.append(float(top[-1] - top[-2]))
+        if gaps[-1] >= window:
+            assert int(np.argmax(g)) == int(np.argmax(r)), f"argmax {int(np.argmax(g))} != {int(np.argmax(r))}"
+    return min(gaps)
+
+
+@pytest.fixture(scope="module")
+def q4k_full(lh, po):
+    """The C4 model and workload, and the layer-streamed oracle's answer for request 0 (full vocabulary at
+    its scored position)."""
+    import bench
+
+    img = lh.SynthImage("q4km-7b", seed=SEED)
+    reqs, opts = bench.q4k_workload()
+    t0 = time.perf_counter()
+    po.set_blocked(True)
+    om = po.Model(po.Gguf(img.array()), threads=THREADS, streamed=True)
+    ids, pos = reqs[0]
+    full = om.forward(ids, pos)
+    po.set_blocked(False)
+    print(f"\noracle q4km-7b L28, request 0 ({len(ids)} tokens): {time.perf_counter() - t0:.1f}s", flush=True)
+    del om
+    yield img, reqs, opts, full
+
+
+def fast_out_of_bar(measured):
+    """The fast mode (f16 operands and KV cache) misses a north-star bar at full depth of these synthetic
+    models; a strict expected failure, so a fast mode that came within the bars would be noticed."""
+    return pytest.mark.xfail(strict=True, reason=f"fast mode outside the north-star bars at full depth ({measured}); "
+                                                 "the exact mode is the measured one")
+
+
+@pytest.mark.parametrize("prec", [0, pytest.param(1, marks=fast_out_of_bar(
+    "measured: logits 7.3e-2 of the largest, option probabilities 5.7e-2"))], ids=["exact", "fast"])
+def test_q4km_7b_prefill_28_layers(lh, po, q4k_full, prec):
+    img, reqs, opts, want_full = q4k_full
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=len(reqs) * 1024 + 2048, max_batch_tokens=32768,
+                    precision=prec)
+    seqs = [eng.seq_create() for _ in reqs]
+    print(f"GPU ({'exact' if prec == 0 else 'fast'}): {len(reqs)} x {len(reqs[0][0])} tokens, 28 layers", flush=True)
+    logits, probs, _ = eng.batch([(s, ids, pos) for s, (ids, pos) in zip(seqs, reqs)]).run(opts)
+    for s in seqs:
+        eng.seq_free(s)
+    assert np.isfinite(logits).all() and np.isfinite(probs).all()
+    for r in (0, 13, 31):  # the wide 256 x 256 launches of the batch == a request alone
+        s = eng.seq_create()
+        single = eng.forward(s, reqs[r][0], reqs[r][1], opts)
+        eng.seq_free(s)
+        assert np.array_equal(single.view(np.uint32), logits[r:r + 1].view(np.uint32)), f"request {r}: batch != alone"
+    s = eng.seq_create()
+    full = eng.forward(s, reqs[0][0], reqs[0][1])  # full vocabulary (the head GEMV)
+    eng.close()
+    want_opts = want_full[:, opts]
+    p_ref = np.stack([po.option_scores(w)[0] for w in want_opts])
+    err_full, err_opt = logit_error(full, want_full), logit_error(logits[:1], want_opts)
+    perr = float(np.abs(probs[:1] - p_ref).max())
+    gap = _argmax_ok(full, want_full, 0.0)
+    print(f"q4km-7b L28 {'exact' if prec == 0 else 'fast'}: full-vocab logits rel {err_full:.3e}, option logits rel "
+          f"{err_opt:.3e}, option probs abs {perr:.3e}, argmax {int(np.argmax(full))} (oracle "
+          f"{int(np.argmax(want_full))}, oracle top-2 gap {gap:.3e})", flush=True)
+    assert err_full <= LOGIT_REL and err_opt <= LOGIT_REL
+    assert perr <= PROB_ABS
+    assert int(np.argmax(full)) == int(np.argmax(want_full))
+
+
+C5_SMALL_PREFIX, C5_SMALL_OWN, C5_SMALL_REQS = 1024, 256, 2
+
+
+@pytest.fixture(scope="module")
+def f16_full(lh, po):
+    """The C5 model, a shortened C5 workload (the bench's own prefix and suffixes cut to 1024 + 2 x 256
+    tokens, 8 answer positions per suffix) and the layer-streamed oracle's answers: the prefix prefilled
+    once, its cache forked per request."""
+    import bench
+
+    img = lh.SynthImage("f16-7b", seed=SEED)
+    prefix, own, _, opts = bench.c5_workload()
+    prefix = prefix[:C5_SMALL_PREFIX]
+    own = [o[:C5_SMALL_OWN] for o in own[:C5_SMALL_REQS]]
+    pos = np.arange(C5_SMALL_OWN // 8 - 1, C5_SMALL_OWN, C5_SMALL_OWN // 8).astype(np.int32)
+    t0 = time.perf_counter()
+    po.set_blocked(True)
+    om = po.Model(po.Gguf(img.array()), threads=THREADS, streamed=True)
+    c = om.cache(C5_SMALL_PREFIX + C5_SMALL_OWN + 8)
+    om.prefill(c, prefix, [])
+    want, full = [], None
+    for r, ids in enumerate(own):
+        hid = om.prefill(c.fork(C5_SMALL_PREFIX), ids, pos)
+        want.append(om.head(hid, opts))
+        if r == 0:
+            full = om.head(hid[-1:])
+    po.set_blocked(False)
+    print(f"\noracle f16-7b L28, {C5_SMALL_PREFIX}-token prefix + {C5_SMALL_REQS} x {C5_SMALL_OWN}: "
+          f"{time.perf_counter() - t0:.1f}s", flush=True)
+    del om
+    yield img, prefix, own, pos, opts, np.concatenate(want), full
+
+
+@pytest.mark.parametrize("prec", [0, pytest.param(1, marks=fast_out_of_bar(
+    "measured: logits 9.8e-3 of the largest, within 2e-2, but option probabilities 2.8e-3 against 1e-3"))],
+    ids=["exact", "fast"])
+def test_f16_7b_shared_prefix_28_layers(lh, po, f16_full, prec):
+    img, prefix, own, pos, opts, want, want_full = f16_full
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=8192, max_batch_tokens=8192, precision=prec)
+    print(f"GPU ({'exact' if prec == 0 else 'fast'}): {len(prefix)}-token prefix forked into {len(own)} x "
+          f"{len(own[0])}, 28 layers", flush=True)
+    base = eng.seq_create()
+    eng.forward(base, prefix, [], opts)
+    kids = [eng.seq_fork(base, len(prefix)) for _ in own]
+    logits, probs, _ = eng.batch([(k, ids, pos) for k, ids in zip(kids, own)]).run(opts)
+    k0 = eng.seq_fork(base, len(prefix))
+    full = eng.forward(k0, own[0], pos[-1:])
+    fresh = eng.seq_create()
+    unshared = eng.forward(fresh, np.concatenate([prefix, own[0]]), len(prefix) + pos, opts)
+    eng.close()
+    assert np.isfinite(logits).all() and np.isfinite(probs).all()
+    assert np.array_equal(unshared.view(np.uint32), logits[:len(pos)].view(np.uint32)), "fork != unshared"
+    p_ref = np.stack([po.option_scores(w)[0] for w in want])
+    err, err_full = logit_error(logits, want), logit_error(full, want_full)
+    perr = float(np.abs(probs - p_ref).max())
+    gap = _argmax_ok(logits, want, 0.0)
+    print(f"f16-7b L28 {'exact' if prec == 0 else 'fast'}: option logits rel {err:.3e}, probs abs {perr:.3e}, "
+          f"full-vocab logits rel {err_full:.3e}, argmax {int(np.argmax(full))} (oracle {int(np.argmax(want_full))}); "
+          f"smallest option top-2 gap {gap:.3e}", flush=True)
+    assert err <= LOGIT_REL and err_full <= LOGIT_REL
+    assert perr <= PROB_ABS
+    assert int(np.argmax(full)) == int(np.argmax(want_full))
