@@ -383,7 +383,7 @@ def c4_q4k(args, prec, layer_cost):
     eng.profile(True)
     batch.run(opts)
     eng.profile(False)
-    prof = {c: eng.profile_read(c) for c in ("gemm", "attn_prefill", "rope_kv", "rmsnorm", "head")}
+    prof = {c: eng.profile_read(c) for c in ("gemm", "ksum", "attn_prefill", "rope_kv", "rmsnorm", "head")}
     assert np.isfinite(out[1]).all()
     eng.close()
     T = Q4K_REQS * Q4K_TOKENS
@@ -398,8 +398,8 @@ def c4_q4k(args, prec, layer_cost):
         "value": round(T / dt, 1), "unit": "tok/s", "higher_is_better": True, "steps": steps, "warmup": warm,
         "ms_per_step": round(dt * 1e3, 2), "req_per_s": round(Q4K_REQS / dt, 2), "load": load,
         "roofline": roofline("mfma", rate(gp, "flops"), PEAK_F16_TFLOPS, "TFLOP/s",
-                             "gemm (exact K-quant MFMA GEMM over f16 hi/lo weight planes; three f16 passes per "
-                             "product, so the arithmetic ceiling is a third of the f16 rate)", gp["launches"],
+                             "gemm (exact K-quant MFMA GEMM: Q4_K in two f16 passes over exact codes with a depth-K/32 "
+                             "correction, Q6_K in three passes over f16 hi/lo weight planes)", gp["launches"],
                              gp["ms"] / max(1, gp["launches"])),
         "kernel_ms_per_step": {c: round(p["ms"], 3) for c, p in prof.items()},
     }
@@ -453,7 +453,7 @@ def c5_long_context(args, prec, layer_cost):
     eng.profile(True)
     step()
     eng.profile(False)
-    prof = {c: eng.profile_read(c) for c in ("gemm", "attn_prefill", "rope_kv", "rmsnorm", "head")}
+    prof = {c: eng.profile_read(c) for c in ("gemm", "ksum", "attn_prefill", "rope_kv", "rmsnorm", "head")}
     assert np.isfinite(out[1]).all()
     eng.close()
     hq, hd, L = 28, 128, 28

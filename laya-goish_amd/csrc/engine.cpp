@@ -414,7 +414,13 @@ void Engine::add_prefill_copy(DevMatrix &m) {
   if (m.kind == LG_Q8_0) {
     m.pc = static_cast<_Float16 *>(carve(n * 2));
     m.pcs = static_cast<float *>(carve(size_t(m.rows) * (m.cols / 32) * 4));
-  } else if (m.kind == LG_Q4_K || m.kind == LG_Q6_K) {
+  } else if (m.kind == LG_Q4_K) {  // two-pass form: codes, sub-block scales, correction planes
+    m.pkp = ksum_cols(m.cols);
+    m.pc = static_cast<_Float16 *>(carve(n * 2));
+    m.pcs = static_cast<float *>(carve(size_t(m.rows) * (m.cols / 32) * 4));
+    m.pcl = static_cast<_Float16 *>(carve(size_t(m.rows) * m.pkp * 4));
+    m.pcr = static_cast<float *>(carve(size_t(m.rows) * 4));
+  } else if (m.kind == LG_Q6_K) {
     m.pc = static_cast<_Float16 *>(carve(n * 2));
     m.pcl = static_cast<_Float16 *>(carve(n * 2));
   } else {
@@ -434,7 +440,7 @@ void Engine::upload(const Gguf &g) {
     else if (t.name == "cos_full" || t.name == "sin_full") need = n * 4;
     else need = size_t(q_row_bytes(t.kind, int(t.cols())) + s_row_bytes(t.kind, int(t.cols()))) * t.rows();
     if (split() && t.dims.size() == 2 && t.name != "output.weight")
-      need += prefill_copy_bytes(t.kind, int(t.rows()), int(t.cols())) + 512;
+      need += prefill_copy_bytes(t.kind, int(t.rows()), int(t.cols())) + 1024;  // up to four 256-B aligned carves
     total += align256(need) + 512;
   }
   arena_size_ = total;
@@ -570,10 +576,20 @@ void *Engine::vpool(int layer) const {
 }
 
 // ------------------------------------------------------------------ kernels with profiling
+const _Float16 *Engine::chunk_sums(const _Float16 *A, const _Float16 *A_lo, int M, const DevMatrix &W) {
+  if (!A_lo || !needs_ksum(W)) return nullptr;
+  ws_ksum_.ensure(size_t(M) * W.pkp * 4);
+  prof.begin("ksum", stream);
+  launch_chunk_sums(A, A_lo, M, W.cols, W.pkp, ws_ksum_.as<_Float16>(), stream);
+  prof.end(double(M) * W.cols * 4 + double(M) * W.pkp * 4, double(M) * W.cols * 2, stream);
+  return ws_ksum_.as<_Float16>();
+}
+
 void Engine::gemm(const _Float16 *A, const _Float16 *A_lo, int M, const DevMatrix &W, Epi epi, float *C,
                   _Float16 *C16, _Float16 *C16_lo, int ldc, const float *bias) {
+  const _Float16 *ks = chunk_sums(A, A_lo, M, W);
   prof.begin_kernel("gemm");
-  launch_gemm(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, stream);
+  launch_gemm(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, stream, ks);
   prof.end_kernel(double(W.bytes()) + double(M) * W.cols * 2, 2.0 * M * double(W.rows) * W.cols);
 }
 
@@ -928,8 +944,9 @@ void Engine::run_layers_prefill(BatchPlan &b, lg_cancel_fn cancel, void *arg) {
       ro.qscale = attn_q_scale(hd);
       for (const ProjPart &p : ly.qkv) {
         ro.col0 = p.col0;
+        const _Float16 *ks = chunk_sums(h16, h16lo, T, p.w);
         prof.begin_kernel("gemm");
-        if (!launch_gemm_wide_rope(h16, h16lo, T, p.w, p.bias, ro, stream))
+        if (!launch_gemm_wide_rope(h16, h16lo, T, p.w, p.bias, ro, stream, ks))
           fail(LG_ERR_UNSUPPORTED, "gemm: fused q|k|v launch refused");
         prof.end_kernel(double(p.w.bytes()) + double(T) * p.w.cols * 2, 2.0 * T * double(p.w.rows) * p.w.cols);
       }
@@ -1050,7 +1067,7 @@ void Engine::forward(int sq, const int32_t *ids, int n, const int32_t *positions
 
 size_t Engine::workspace_bytes() const {
   size_t n = 0;
-  for (const DevBuf *b : {&ws_x_, &ws_h16_, &ws_qkv_, &ws_q16_, &ws_att16_, &ws_act16_, &ws_meta_, &ws_out_, &ws_dec_,
+  for (const DevBuf *b : {&ws_x_, &ws_h16_, &ws_qkv_, &ws_q16_, &ws_att16_, &ws_act16_, &ws_ksum_, &ws_meta_, &ws_out_, &ws_dec_,
                           &ws_ot_qk_, &ws_ot_v_, &ws_ot_gb_, &ws_ot_o_, &ws_ot_part_})
     n += b->n;
   return n;

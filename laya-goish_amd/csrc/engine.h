@@ -233,6 +233,9 @@ class Engine {
 
   // prof-wrapped launch helpers
   // A/A_lo and C16/C16_lo are hi/lo planes in EXACT mode (lo == nullptr in FAST mode)
+  // exact Q4_K launches (two-pass prefill copy): the activation's chunk sums in ws_ksum_ (nullptr when W
+  // does not need them)
+  const _Float16 *chunk_sums(const _Float16 *A, const _Float16 *A_lo, int M, const DevMatrix &W);
   void gemm(const _Float16 *A, const _Float16 *A_lo, int M, const DevMatrix &W, Epi epi, float *C,
             _Float16 *C16, _Float16 *C16_lo, int ldc, const float *bias);
   void gemv(const float *x, const DevMatrix &W, Epi epi, float *y, const float *bias,
@@ -286,7 +289,7 @@ class Engine {
   int next_seq_ = 1;
   int64_t max_batch_tokens_ = 65536;
   // workspaces
-  DevBuf ws_x_, ws_h16_, ws_qkv_, ws_q16_, ws_att16_, ws_act16_, ws_meta_, ws_out_;
+  DevBuf ws_x_, ws_h16_, ws_qkv_, ws_q16_, ws_att16_, ws_act16_, ws_ksum_, ws_meta_, ws_out_;
   DevBuf ws_dec_;
   DevBuf ws_ot_qk_, ws_ot_v_, ws_ot_gb_, ws_ot_o_;  // OpenThai mixer workspaces
   DevBuf ws_ot_part_;                               // OpenThai attention partials

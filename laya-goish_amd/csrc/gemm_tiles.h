@@ -8,6 +8,10 @@
 //           significand bits.  F16 weights are exact in f16 -> 2 passes (hi, lo).
 //           Q8_0 codes are exact in f16 and the block scale is applied in f32 per 32-element
 //           block (partial sums on MFMA, acc += d * partial) -> 2 passes, weights exact.
+//           Q4_K with the two-pass prefill copy (DevMatrix::pcr): w = A q - B per 32-element
+//           sub-block, codes q exact in f16 and A applied per sub-block as the Q8_0 scale (2 passes),
+//           after a correction GEMM of depth K/32 over the activation's chunk sums and -B (3 passes):
+//           x.w = sum_c A_c (x_c . q_c) - sum_c B_c (sum x_c).
 //   SPLIT3: K-quants (Q4_K, Q6_K) whose dequantised f32 weight needs 24 bits: W is split into
 //           hi/lo f16 too and acc += Ah.Bh + Al.Bh + Ah.Bl -> 3 passes.
 // The split modes reproduce f32 arithmetic to ~2^-22 relative per product, which the
@@ -178,6 +182,35 @@ struct BLoad {
         }
         *reinterpret_cast<half8 *>(Bs + r * LDK + c * 16) = o0;
         *reinterpret_cast<half8 *>(Bs + r * LDK + c * 16 + 8) = o1;
+      } else if constexpr (KIND == LG_Q4_K && MODE == SPLIT) {
+        // two-pass form: the codes as f16 (exact, 0..15; bytes under a 0x64 high byte read as f16 are
+        // 1024 + q, one packed subtraction leaves q) and the sub-block scales A = d*sc; the low nibbles
+        // are elements 16c + j of the 64-deep step, the high nibbles 32 + 16c + j
+        static_assert(BK == 64, "two-pass Q4_K tiles take 64-deep K steps");
+        typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+        const half2v bias = {_Float16(1024.0f), _Float16(1024.0f)};
+        uint32_t lo8[8], hi8[8];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint32_t ul = w[d] & 0x0f0f0f0fu, uh = (w[d] >> 4) & 0x0f0f0f0fu;
+          lo8[2 * d] = __builtin_amdgcn_perm(0x64646464u, ul, 0x04010400u);
+          lo8[2 * d + 1] = __builtin_amdgcn_perm(0x64646464u, ul, 0x04030402u);
+          hi8[2 * d] = __builtin_amdgcn_perm(0x64646464u, uh, 0x04010400u);
+          hi8[2 * d + 1] = __builtin_amdgcn_perm(0x64646464u, uh, 0x04030402u);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          lo8[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, lo8[e]) - bias);
+          hi8[e] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, hi8[e]) - bias);
+        }
+        *reinterpret_cast<uint4 *>(Bs + r * LDK + c * 16) = make_uint4(lo8[0], lo8[1], lo8[2], lo8[3]);
+        *reinterpret_cast<uint4 *>(Bs + r * LDK + c * 16 + 8) = make_uint4(lo8[4], lo8[5], lo8[6], lo8[7]);
+        *reinterpret_cast<uint4 *>(Bs + r * LDK + 32 + c * 16) = make_uint4(hi8[0], hi8[1], hi8[2], hi8[3]);
+        *reinterpret_cast<uint4 *>(Bs + r * LDK + 32 + c * 16 + 8) = make_uint4(hi8[4], hi8[5], hi8[6], hi8[7]);
+        if (c == 0) {
+          Ds[r * 2] = sa[i];
+          Ds[r * 2 + 1] = sa2[i];
+        }
       } else if constexpr (KIND == LG_Q6_K) {
         float f[16];
 #pragma unroll
@@ -277,8 +310,10 @@ struct ALoad {
 // holds rows 4 (l / 16) .. + 4 of column l % 16.  Per output element and 32-deep chunk the
 // operation sequence is (acc as f32):
 //   FAST  : acc += A.W
-//   SPLIT : F16 weights: acc += A_hi.W, acc += A_lo.W;  Q8_0 codes: p = A_hi.W, p += A_lo.W,
-//           acc += d * p (d the chunk's Q8_0 block scale, f32 FMA)
+//   SPLIT : F16 weights: acc += A_hi.W, acc += A_lo.W;  Q8_0 / Q4_K codes: p = A_hi.W, p += A_lo.W,
+//           acc += d * p (d the chunk's Q8_0 block scale or Q4_K sub-block scale d*sc, f32 FMA);
+//           a two-pass Q4_K launch first runs its correction (SPLIT3 order over the chunk sums and
+//           the -B 2^e planes) and multiplies acc by 2^-e per column
 //   SPLIT3: acc += A_hi.W_hi, acc += A_lo.W_hi, acc += A_hi.W_lo
 // gemm_wide.h keeps the same sequences, so both tilings give the same bits.
 template <uint32_t KIND, int MODE, int BK, int WTM, int WTN, int LDK>
@@ -287,7 +322,7 @@ __device__ __forceinline__ void mma_tile(f32x4 (&acc)[2 * WTM][2 * WTN], const _
                                          int wn, int lane) {
   constexpr bool kSplitA = MODE != FAST;
   constexpr bool kSplitB = MODE == SPLIT3;
-  constexpr bool kScaled = MODE == SPLIT && KIND == LG_Q8_0;
+  constexpr bool kScaled = MODE == SPLIT && (KIND == LG_Q8_0 || KIND == LG_Q4_K);
   constexpr int MI = 2 * WTM, NJ = 2 * WTN;
   const int arow = (wm * (32 * WTM) + (lane & 15)) * LDK;
   const int brow = (wn * (32 * WTN) + (lane & 15)) * LDK;
@@ -346,6 +381,15 @@ struct Cfg {
   static constexpr int kLdsBytes = STAGES * kStageBytes;
 };
 
+// LDS of one launch: a two-pass Q4_K launch's correction stages four planes (SPLIT3) in the same space.
+template <uint32_t KIND, int MODE, int BK, int WTM, int WTN, int STAGES>
+constexpr int lds_bytes() {
+  constexpr int main = Cfg<MODE, BK, WTM, WTN, STAGES>::kLdsBytes;
+  constexpr int corr = Cfg<SPLIT3, BK, WTM, WTN, 1>::kStageBytes;
+  return KIND == LG_Q4_K && MODE == SPLIT && corr > main ? corr : main;
+}
+
+// ks / kslo: the chunk-sum planes of a two-pass Q4_K launch ([M][W.pkp] each), unused otherwise.
 template <uint32_t KIND, int EPI, int MODE, int BK, int WTM, int WTN, int STAGES>
 __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ A,
                                                    const _Float16 *__restrict__ Alo, int M, int K,
@@ -353,11 +397,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
                                                    _Float16 *__restrict__ C16,
                                                    _Float16 *__restrict__ C16lo, int ldc,
                                                    const float *__restrict__ bias, int MT, int NT,
-                                                   int ffn) {
+                                                   int ffn, const _Float16 *__restrict__ ks,
+                                                   const _Float16 *__restrict__ kslo) {
   using CF = Cfg<MODE, BK, WTM, WTN, STAGES>;
   constexpr int BMW = CF::kBM, BNT = CF::kBN, LDK = CF::kLDK;
   constexpr bool kSplitA = CF::kSplitA, kSplitB = CF::kSplitB;
-  constexpr bool kScaled = MODE == SPLIT && KIND == LG_Q8_0;
+  constexpr bool kScaled = MODE == SPLIT && (KIND == LG_Q8_0 || KIND == LG_Q4_K);
   static_assert(WTN % 2 == 0 || (EPI != int(Epi::SWIGLU) && EPI != int(Epi::GEGLU)),
                 "gated epilogues pair gate and up blocks inside a wave");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -400,6 +445,51 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
     for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.0f;
+
+  if constexpr (KIND == LG_Q4_K && MODE == SPLIT) {
+    // correction of the two-pass form: acc = (sum_c ks[m][c] (-B[n][c] 2^e_n)) 2^-e_n, a GEMM of depth
+    // W.pkp over the chunk sums and the correction planes (f16 hi/lo each, SPLIT3 order), staged
+    // four planes at a time through one LDS buffer with the next step prefetched into registers
+    using CC = Cfg<SPLIT3, BK, WTM, WTN, 1>;
+    const int kp = W.pkp;
+    DevMatrix Ch = W;  // the correction planes read as F16 matrices [rows][kp]
+    Ch.kind = LG_F16;
+    Ch.cols = kp;
+    Ch.q = W.pcl;
+    DevMatrix Cl = Ch;
+    Cl.q = W.pcl + int64_t(W.rows) * kp;
+    ALoad<BMW, BK, true> ka;
+    ka.init(ks, kslo, m0, M, kp, t);
+    BLoad<LG_F16, SPLIT3, BK, BNT> ch, cl;
+    _Float16 *Cs = reinterpret_cast<_Float16 *>(lds);
+    _Float16 *Csl = Cs + CC::kAPlane, *Cb = Cs + 2 * CC::kAPlane, *Cbl = Cb + CC::kBPlane;
+    const int nkc = kp / BK;
+    ka.fetch(0);
+    ch.fetch(Ch, wrow, 0, t);
+    cl.fetch(Cl, wrow, 0, t);
+    for (int kt = 0; kt < nkc; ++kt) {
+      if (kt) __syncthreads();
+      ka.template store<LDK>(Cs, Csl, t);
+      ch.template store<LDK>(Cb, Cb, nullptr, t);
+      cl.template store<LDK>(Cbl, Cbl, nullptr, t);
+      __syncthreads();
+      if (kt + 1 < nkc) {
+        ka.fetch((kt + 1) * BK);
+        ch.fetch(Ch, wrow, (kt + 1) * BK, t);
+        cl.fetch(Cl, wrow, (kt + 1) * BK, t);
+      }
+      mma_tile<LG_F16, SPLIT3, BK, WTM, WTN, LDK>(acc, Cs, Csl, Cb, Cbl, nullptr, wm, wn, lane);
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const float rs = W.pcr[wrow(wn * (32 * WTN) + j * 16 + (lane & 15))];
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][j][r] *= rs;
+    }
+    __syncthreads();  // the main loop's stores reuse the LDS
+  }
 
   const int nk = K / BK;
   al.fetch(0);
@@ -506,7 +596,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
 
 template <uint32_t KIND, int MODE, int BK, int WTM, int WTN, int STAGES>
 bool launch_cfg(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
-                _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st) {
+                _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st,
+                const _Float16 *ks = nullptr) {
   using CF = Cfg<MODE, BK, WTM, WTN, STAGES>;
   const bool glu = epi == Epi::SWIGLU || epi == Epi::GEGLU;
   if (glu && WTN % 2) return false;  // gated epilogues need gate and up blocks in one wave
@@ -535,12 +626,15 @@ bool launch_cfg(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &
     const _Float16 *Ac = A + int64_t(m0) * K, *Alc = Alo ? Alo + int64_t(m0) * K : nullptr;
     float *Cc = C ? C + int64_t(m0) * ldc : nullptr;
     _Float16 *C16c = C16 ? C16 + int64_t(m0) * ldc : nullptr, *C16lc = C16lo ? C16lo + int64_t(m0) * ldc : nullptr;
+    const _Float16 *ksc = ks ? ks + int64_t(m0) * W.pkp : nullptr;
+    const _Float16 *kslc = ks ? ks + (int64_t(M) + m0) * W.pkp : nullptr;
+    constexpr int lds = lds_bytes<KIND, MODE, BK, WTM, WTN, STAGES>();
 #define LAUNCH(E)                                                                                              \
   do {                                                                                                         \
     auto fn = gemm_kernel<KIND, E, MODE, BK, WTM, WTN, STAGES>;                                                \
-    grant_lds(reinterpret_cast<const void *>(fn), CF::kLdsBytes);                                              \
-    launch_timed(fn, grid, block, CF::kLdsBytes, st, Ac, Alc, Mc, K, W, Cc, C16c, C16lc, ldc, bias, MT, NT,    \
-                 ffn);                                                                                         \
+    grant_lds(reinterpret_cast<const void *>(fn), lds);                                                        \
+    launch_timed(fn, grid, block, lds, st, Ac, Alc, Mc, K, W, Cc, C16c, C16lc, ldc, bias, MT, NT, ffn, ksc,     \
+                 kslc);                                                                                        \
   } while (0)
     switch (epi) {
       case Epi::F32: LAUNCH(0); break;
@@ -568,6 +662,11 @@ bool launch_cfg(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &
 bool launch_gemm_q8_exact(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi,
                           float *C, _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias,
                           hipStream_t st);
+// Exact two-pass Q4_K tiles (the same translation unit): codes, sub-block scales and the correction
+// over the activation's chunk sums ks.
+bool launch_gemm_q4_exact(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi,
+                          float *C, _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias,
+                          hipStream_t st, const _Float16 *ks);
 
 // Exact GEMM on 256 x 256 tiles over the weight's prefill copy (gemm_wide.h: Q8_0, F16, Q4_K,
 // Q6_K), for launches with at least as many tiles as the device has CUs.  Same per-element
@@ -575,6 +674,7 @@ bool launch_gemm_q8_exact(const _Float16 *A, const _Float16 *Alo, int M, const D
 // (nothing launched) when the matrix has no prefill copy or the shape or epilogue is not one it
 // takes.
 bool launch_gemm_wide(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
-                      _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st);
+                      _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st,
+                      const _Float16 *ks = nullptr);
 
 }  // namespace lg

@@ -7,8 +7,12 @@
 //        against the codes), then acc += d * partial in f32.
 //   W1 : F16 weights [N][K] (the weights themselves, no copy): per 32-deep k chunk
 //        acc += A_hi . W, then acc += A_lo . W.
-//   W2 : Q4_K / Q6_K -- the dequantised f32 weight split into f16 hi and lo planes [N][K]:
-//        per 32-deep k chunk acc += A_hi . W_hi, A_lo . W_hi, A_hi . W_lo.
+//   W2 : Q6_K (and Q4_K without the two-pass copy) -- the dequantised f32 weight split into f16 hi
+//        and lo planes [N][K]: per 32-deep k chunk acc += A_hi . W_hi, A_lo . W_hi, A_hi . W_lo.
+//   WQ4: Q4_K in the two-pass form w = A q - B (A = d*sc, B = dmin*m per 32-element sub-block):
+//        first the correction acc = (sum_c ks[m][c] (-B[n][c] 2^e_n)) 2^-e_n over the activation's
+//        chunk sums (KqCorr; W2's order and stage layout, depth K/32 rounded up to 128), then WQ8's
+//        loop over the codes (exact in f16) with A as the per-chunk scale.
 // Each mode keeps the per-element operation order of the 128 x 128 tiles in gemm_tiles.h, so
 // both give the same bits (all on v_mfma_f32_16x16x32_f16 with f32 accumulation: one
 // instruction per 32-deep chunk).
@@ -36,7 +40,7 @@ namespace wide {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-enum Mode { WQ8 = 0, W1 = 1, W2 = 2 };
+enum Mode { WQ8 = 0, W1 = 1, W2 = 2, WQ4 = 3 };
 // epilogue of the fused q|k|v projection (RoPE, q planes, KV cache stores; RopeKvOut)
 constexpr int kEpiRopeKv = 16;
 
@@ -46,15 +50,24 @@ constexpr int PLANE = BM * ROWB;  // 16 KiB
 static_assert(BM == BN, "A and B planes share one slot layout");
 static_assert(PLANE / 1024 == 2 * WAVES, "two 1 KiB blocks of each plane per wave");
 
+// Q4_K correction operands of one two-pass launch (WQ4): the activation's chunk sums and the weight's
+// -B 2^e planes, f16 hi and lo [rows][kp] each, and 2^-e per weight row (DevMatrix::pcl, pcr).
+struct KqCorr {
+  const _Float16 *ks = nullptr, *kslo = nullptr;
+  const _Float16 *bh = nullptr, *bl = nullptr;
+  const float *rs = nullptr;
+  int kp = 0;
+};
+
 template <int MODE>
 struct Geo {
   static constexpr int kBPlanes = MODE == W2 ? 2 : 1;
-  static constexpr bool kScales = MODE == WQ8;
+  static constexpr bool kScales = MODE == WQ8 || MODE == WQ4;
   static constexpr int kAHi = 0, kALo = PLANE, kBHi = 2 * PLANE, kBLo = 3 * PLANE;
   static constexpr int kScl = (2 + kBPlanes) * PLANE;
   static constexpr int kStageBytes = kScl + (kScales ? BN * 4 : 0);
   static constexpr int kStages = MODE == W2 ? 2 : 3;
-  static constexpr int kLdsBytes = kStages * kStageBytes;  // WQ8 150,528; W1 147,456; W2 131,072
+  static constexpr int kLdsBytes = kStages * kStageBytes;  // WQ8, WQ4 150,528; W1 147,456; W2 131,072
 };
 
 __device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
@@ -71,8 +84,9 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
     const _Float16 *__restrict__ A, const _Float16 *__restrict__ Alo, int M, int K,
     const _Float16 *__restrict__ Wh, const _Float16 *__restrict__ Wl, const float *__restrict__ Ws, int N,
     float *__restrict__ C, _Float16 *__restrict__ C16, _Float16 *__restrict__ C16lo, int ldc,
-    const float *__restrict__ bias, int MT, int NT, int ffn, RopeKvOut ro) {
+    const float *__restrict__ bias, int MT, int NT, int ffn, RopeKvOut ro, KqCorr kq) {
   using G = Geo<MODE>;
+  constexpr bool kScaled = G::kScales;  // WQ8, WQ4: per-chunk scale FMAs over code partial sums
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr bool kGlu = EPI == int(Epi::SWIGLU);
   const int t = threadIdx.x, lane = t & 63;
@@ -115,7 +129,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
   const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(Wh), 0, wbytes, kBufferFlags);
   __amdgpu_buffer_rsrc_t rc = rb, rs = rb;
   if constexpr (MODE == W2) rc = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(Wl), 0, wbytes, kBufferFlags);
-  if constexpr (MODE == WQ8)
+  if constexpr (kScaled)
     rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(Ws), 0, uint32_t(N) * uint32_t(K / 32) * 4u, kBufferFlags);
   // WQ8 and W1: every wave moves the blocks wave and wave + 8 of each plane (A hi, A lo, W hi);
   // wave 0 also moves the scale block.  W2: the four waves of group 1 move everything, wave
@@ -154,7 +168,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
   };
   auto dma_scale = [&](int kt, int st) {
 #if defined(__HIP_DEVICE_COMPILE__)
-    if constexpr (MODE == WQ8)
+    if constexpr (kScaled)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(lds + st * G::kStageBytes + G::kScl), 16, soff,
                                                kt * N * 4, 0, 0);
 #endif
@@ -201,7 +215,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
       f.b[j] = *reinterpret_cast<const half8 *>(st + G::kBHi + bc0 + j * 16 * ROWB);
       if constexpr (MODE == W2) f.c[j] = *reinterpret_cast<const half8 *>(st + G::kBLo + bc0 + j * 16 * ROWB);
     }
-    if constexpr (MODE == WQ8) {
+    if constexpr (kScaled) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) f.d[j] = *reinterpret_cast<const float *>(st + G::kScl + (wn * 128 + j * 16 + lr) * 4);
     }
@@ -211,7 +225,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
   // dkt >= 0: the six A/W DMA instructions of this wave's part of step dkt (into stage dst) issue
   // one per column block j = 1 .. 6, between the MFMAs
   auto compute_step = [&](const Frag &f, int dkt, int dst) {
-    if constexpr (MODE == WQ8) {
+    if constexpr (kScaled) {
       // software pipeline over the wave's eight column blocks j: the eight MFMAs of column j (the
       // hi then lo chains of its four row blocks, interleaved) issue between the sixteen scale
       // FMAs of column j - 1 (two sets of four partial sums)
@@ -309,6 +323,86 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
   // unit answers reads past the end with zeros and nothing reads those stages), so every wait has
   // the same count and no branch separates the MFMAs from the DMA.  Both groups run the same loop
   // and pass 2 nk + 2 barriers.
+  if constexpr (MODE == WQ4) {
+    // The correction of the two-pass Q4_K form, before the main loop: acc = (sum_c ks[m][c]
+    // (-B[n][c] 2^e_n)) 2^-e_n over kq.kp sub-block columns, in W2's per-element order and stage
+    // layout (four planes, two stages).  Every wave moves blocks wave and wave + 8 of each plane, one
+    // step ahead of the reads.
+    using GC = Geo<W2>;
+    static_assert(GC::kStages * GC::kStageBytes <= G::kLdsBytes, "the correction's stages fit the LDS");
+    const int kp = kq.kp;
+    const uint32_t ksb = uint32_t(M) * uint32_t(kp) * 2u, kbb = uint32_t(N) * uint32_t(kp) * 2u;
+    const __amdgpu_buffer_rsrc_t r0 = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(kq.ks), 0, ksb, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t r1 = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(kq.kslo), 0, ksb, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t r2 = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(kq.bh), 0, kbb, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t r3 = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(kq.bl), 0, kbb, kBufferFlags);
+    uint32_t kao, kbo;
+    {
+      const int slot = wave * 64 + lane, row = slot >> 2, c = (slot & 3) ^ swz(row);
+      kao = uint32_t(m0 + row) * uint32_t(kp) * 2u + uint32_t(c) * 16u;
+      kbo = uint32_t(wrow(row)) * uint32_t(kp) * 2u + uint32_t(c) * 16u;
+    }
+    auto cdma = [&](int kt, int st) {
+#if defined(__HIP_DEVICE_COMPILE__)
+      uint8_t *base = lds + st * GC::kStageBytes;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int blk = (wave + 8 * h) * 1024, dr = 128 * h;  // block, row shift
+        const uint32_t ka = uint32_t(kt * BK * 2) + uint32_t(dr) * uint32_t(kp) * 2u;
+        const uint32_t kb = uint32_t(kt * BK * 2) + uint32_t(wrow(dr) - wrow(0)) * uint32_t(kp) * 2u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r0, (lds_ptr)(base + GC::kAHi + blk), 16, kao, ka, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r1, (lds_ptr)(base + GC::kALo + blk), 16, kao, ka, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r2, (lds_ptr)(base + GC::kBHi + blk), 16, kbo, kb, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r3, (lds_ptr)(base + GC::kBLo + blk), 16, kbo, kb, 0, 0);
+      }
+#endif
+    };
+    const int nkc = kp / BK;
+    cdma(0, 0);
+    for (int kt = 0; kt < nkc; ++kt) {
+      if (kt + 1 < nkc) {  // step kt + 1 into the other stage, which every wave finished reading
+        cdma(kt + 1, (kt + 1) & 1);
+        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      barrier();
+      const uint8_t *st = lds + (kt & 1) * GC::kStageBytes;
+      half8 ah[4], al[4], b[8], c[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ah[i] = *reinterpret_cast<const half8 *>(st + GC::kAHi + ac0 + i * 16 * ROWB);
+        al[i] = *reinterpret_cast<const half8 *>(st + GC::kALo + ac0 + i * 16 * ROWB);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        b[j] = *reinterpret_cast<const half8 *>(st + GC::kBHi + bc0 + j * 16 * ROWB);
+        c[j] = *reinterpret_cast<const half8 *>(st + GC::kBLo + bc0 + j * 16 * ROWB);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i][j] = WIDE_MFMA(ah[i], b[j], acc[i][j]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i][j] = WIDE_MFMA(al[i], b[j], acc[i][j]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i][j] = WIDE_MFMA(ah[i], c[j], acc[i][j]);
+      }
+      barrier();  // the stage is free for step kt + 2
+    }
+    float rsc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) rsc[j] = kq.rs[wrow(wn * 128 + j * 16 + lr)];
+    // the scale loads land before the main loop's DMA, whose waits count only its own instructions
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][j][r] *= rsc[j];
+  }
+
   constexpr int S = G::kStages;
   if constexpr (MODE != W2) {
     static_assert(S == 3 && NPL == 3, "ping-pong: three stages of three planes");
@@ -321,7 +415,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
 #pragma unroll
         for (int pl = 0; pl < 3; ++pl) dma(2, 2, pl, h);
       asm volatile("s_waitcnt vmcnt(12)" ::: "memory");  // step 0
-    } else if (MODE == WQ8 && wave == 0) {
+    } else if (kScaled && wave == 0) {
       asm volatile("s_waitcnt vmcnt(7)" ::: "memory");  // step 0 and its scales
     } else {
       asm volatile("s_waitcnt vmcnt(6)" ::: "memory");

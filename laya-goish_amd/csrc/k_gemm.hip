@@ -7,14 +7,16 @@ namespace {
 // Per-kind, per-mode tile configuration: <MODE, BK, WTM, WTN, STAGES>.
 template <uint32_t KIND>
 void launch_kind(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
-                 _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st) {
+                 _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st, const _Float16 *ks) {
   // Chosen by sweeps at the 35,840-token Q8_0/F16 and 32,768-token Q4_K/Q6_K 7B prefill
   // shapes; a 256-wide N tile falls back to 128 when it does not divide the output width.
   if (!Alo) {
     if (launch_cfg<KIND, FAST, 64, 4, 4, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
     if (launch_cfg<KIND, FAST, 64, 2, 2, 2>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
-  } else if (launch_gemm_wide(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) {
+  } else if (launch_gemm_wide(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st, ks)) {
     return;
+  } else if (KIND == LG_Q4_K && needs_ksum(W)) {
+    if (launch_gemm_q4_exact(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st, ks)) return;
   } else if constexpr (KIND == LG_Q8_0) {
     if (launch_gemm_q8_exact(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
   } else if constexpr (KIND == LG_F16) {
@@ -81,8 +83,9 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(const float *__restri
 }  // namespace
 
 void launch_gemm(const _Float16 *A, const _Float16 *A_lo, int M, const DevMatrix &W, Epi epi, float *C,
-                 _Float16 *C16, _Float16 *C16_lo, int ldc, const float *bias, hipStream_t st) {
+                 _Float16 *C16, _Float16 *C16_lo, int ldc, const float *bias, hipStream_t st, const _Float16 *ks) {
   LG_REQUIRE(M > 0, "gemm: empty activation");
+  LG_REQUIRE(!A_lo || !needs_ksum(W) || ks, "gemm: an exact Q4_K launch needs its activation's chunk sums");
   if (W.cols % 64 != 0) fail(LG_ERR_UNSUPPORTED, "gemm: K=%d is not a multiple of 64", W.cols);
   if (W.kind == LG_Q4_K || W.kind == LG_Q6_K)
     LG_REQUIRE(W.cols % 256 == 0, "gemm: K-quant rows must be whole super-blocks");
@@ -95,10 +98,10 @@ void launch_gemm(const _Float16 *A, const _Float16 *A_lo, int M, const DevMatrix
     LG_REQUIRE(epi == Epi::F16 || epi == Epi::RELU16 ? C16 != nullptr : C != nullptr, "gemm: missing output");
   }
   switch (W.kind) {
-    case LG_F16: launch_kind<LG_F16>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, st); break;
-    case LG_Q8_0: launch_kind<LG_Q8_0>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, st); break;
-    case LG_Q4_K: launch_kind<LG_Q4_K>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, st); break;
-    case LG_Q6_K: launch_kind<LG_Q6_K>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, st); break;
+    case LG_F16: launch_kind<LG_F16>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, st, ks); break;
+    case LG_Q8_0: launch_kind<LG_Q8_0>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, st, ks); break;
+    case LG_Q4_K: launch_kind<LG_Q4_K>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, st, ks); break;
+    case LG_Q6_K: launch_kind<LG_Q6_K>(A, A_lo, M, W, epi, C, C16, C16_lo, ldc, bias, st, ks); break;
     default: fail(LG_ERR_UNSUPPORTED, "gemm: no MFMA path for GGML type %u", W.kind);
   }
   HIP_CHECK(hipGetLastError());

@@ -18,6 +18,14 @@ bool launch_gemm_q8_exact(const _Float16 *A, const _Float16 *Alo, int M, const D
   return launch_cfg<LG_Q8_0, SPLIT, 64, 2, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st);
 }
 
+bool launch_gemm_q4_exact(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi,
+                          float *C, _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias,
+                          hipStream_t st, const _Float16 *ks) {
+  // the Q8_0 geometry: 128 x 128 x 64 tiles, one LDS stage (the correction's four planes size it)
+  LG_REQUIRE(ks, "gemm: an exact Q4_K launch needs its activation's chunk sums");
+  return launch_cfg<LG_Q4_K, SPLIT, 64, 2, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st, ks);
+}
+
 namespace {
 int device_cus() {
   static thread_local int dev = -1, cus = 0;
@@ -41,7 +49,15 @@ int wide_mode(int M, const DevMatrix &W, int EPI) {
   switch (W.kind) {
     case LG_Q8_0: mode = WQ8; if (!W.pcs) return -1; break;
     case LG_F16: mode = W1; break;
-    case LG_Q4_K:
+    case LG_Q4_K:  // the two-pass copy (codes, scales, correction planes), or hi/lo planes
+      if (needs_ksum(W)) {
+        mode = WQ4;
+        if (!W.pcs || !W.pcl) return -1;
+      } else {
+        mode = W2;
+        if (!W.pcl) return -1;
+      }
+      break;
     case LG_Q6_K: mode = W2; if (!W.pcl) return -1; break;
     default: return -1;
   }
@@ -58,14 +74,15 @@ int wide_mode(int M, const DevMatrix &W, int EPI) {
 
 typedef void (*WideFn)(const _Float16 *, const _Float16 *, int, int, const _Float16 *, const _Float16 *,
                        const float *, int, float *, _Float16 *, _Float16 *, int, const float *, int, int, int,
-                       RopeKvOut);
+                       RopeKvOut, wide::KqCorr);
 
 // one kernel per (epilogue, mode), its LDS limit raised on the current device
 template <int EPI>
 WideFn wide_fn(int mode) {
   using namespace wide;
-  static const WideFn fns[3] = {gemm_wide_kernel<EPI, WQ8>, gemm_wide_kernel<EPI, W1>, gemm_wide_kernel<EPI, W2>};
-  static const int lds_bytes[3] = {Geo<WQ8>::kLdsBytes, Geo<W1>::kLdsBytes, Geo<W2>::kLdsBytes};
+  static const WideFn fns[4] = {gemm_wide_kernel<EPI, WQ8>, gemm_wide_kernel<EPI, W1>, gemm_wide_kernel<EPI, W2>,
+                                gemm_wide_kernel<EPI, WQ4>};
+  static const int lds_bytes[4] = {Geo<WQ8>::kLdsBytes, Geo<W1>::kLdsBytes, Geo<W2>::kLdsBytes, Geo<WQ4>::kLdsBytes};
   grant_lds(reinterpret_cast<const void *>(fns[mode]), size_t(lds_bytes[mode]));
   return fns[mode];
 }
@@ -73,9 +90,9 @@ WideFn wide_fn(int mode) {
 // launches fn over the M rows in chunks whose activation planes stay within 32-bit buffer offsets
 void launch_wide(WideFn fn, int mode, const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W,
                  bool glu, float *C, _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, const RopeKvOut &ro,
-                 hipStream_t st) {
+                 hipStream_t st, const _Float16 *ks) {
   using namespace wide;
-  static const int lds_bytes[3] = {Geo<WQ8>::kLdsBytes, Geo<W1>::kLdsBytes, Geo<W2>::kLdsBytes};
+  static const int lds_bytes[4] = {Geo<WQ8>::kLdsBytes, Geo<W1>::kLdsBytes, Geo<W2>::kLdsBytes, Geo<WQ4>::kLdsBytes};
   const int N = W.rows, K = W.cols;
   const int NT = glu ? (N / 2) / (BN / 2) : N / BN;
   const bool rope = ro.tok_pos != nullptr;
@@ -102,9 +119,18 @@ void launch_wide(WideFn fn, int mode, const _Float16 *A, const _Float16 *Alo, in
       rc.q16 += int64_t(m0) * ro.hq * 128;
       rc.q16lo += int64_t(m0) * ro.hq * 128;
     }
+    KqCorr kq;
+    if (mode == WQ4) {
+      kq.kp = W.pkp;
+      kq.ks = ks + int64_t(m0) * W.pkp;
+      kq.kslo = ks + (int64_t(M) + m0) * W.pkp;
+      kq.bh = W.pcl;
+      kq.bl = W.pcl + int64_t(N) * W.pkp;
+      kq.rs = W.pcr;
+    }
     launch_timed(fn, dim3(MT * NT), dim3(THREADS), lds_bytes[mode], st, Ac, Alc, Mc, K,
                  static_cast<const _Float16 *>(W.pc), static_cast<const _Float16 *>(W.pcl),
-                 static_cast<const float *>(W.pcs), N, Cc, C16c, C16lc, ldc, bias, MT, NT, N / 2, rc);
+                 static_cast<const float *>(W.pcs), N, Cc, C16c, C16lc, ldc, bias, MT, NT, N / 2, rc, kq);
     m0 += Mc;
   }
   if (timer) *timer = whole;
@@ -114,32 +140,34 @@ void launch_wide(WideFn fn, int mode, const _Float16 *A, const _Float16 *Alo, in
 bool gemm_wide_takes(int M, const DevMatrix &W, Epi epi) { return wide_mode(M, W, int(epi)) >= 0; }
 
 bool launch_gemm_wide(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
-                      _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st) {
+                      _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st, const _Float16 *ks) {
   using namespace wide;
   if (!A || !Alo) return false;
   const int mode = wide_mode(M, W, int(epi));
   if (mode < 0) return false;
+  LG_REQUIRE(mode != WQ4 || ks, "gemm: an exact Q4_K launch needs its activation's chunk sums");
   const bool glu = epi == Epi::SWIGLU;
   const int N = W.rows;
   if (glu ? (C16 == nullptr || ldc < N / 2) : (C == nullptr || ldc < N)) return false;
   const WideFn fn = epi == Epi::F32   ? wide_fn<int(Epi::F32)>(mode)
                     : epi == Epi::ADD ? wide_fn<int(Epi::ADD)>(mode)
                                       : wide_fn<int(Epi::SWIGLU)>(mode);
-  launch_wide(fn, mode, A, Alo, M, W, glu, C, C16, C16lo, ldc, bias, RopeKvOut{}, st);
+  launch_wide(fn, mode, A, Alo, M, W, glu, C, C16, C16lo, ldc, bias, RopeKvOut{}, st, ks);
   return true;
 }
 
 bool launch_gemm_wide_rope(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, const float *bias,
-                           const RopeKvOut &ro, hipStream_t st) {
+                           const RopeKvOut &ro, hipStream_t st, const _Float16 *ks) {
   using namespace wide;
   if (!A || !Alo) return false;
   const int mode = wide_mode(M, W, kEpiRopeKv);
   if (mode < 0) return false;
+  LG_REQUIRE(mode != WQ4 || ks, "gemm: an exact Q4_K launch needs its activation's chunk sums");
   if (ro.hd != 128 || ro.col0 % 128 != 0 || ro.col0 / 128 + W.rows / 128 > ro.hq + 2 * ro.hkv) return false;
   LG_REQUIRE(ro.cosT && ro.sinT && ro.tok_pos && ro.tok_page && ro.q16 && ro.q16lo && ro.kpool && ro.vpool,
              "gemm rope: missing output");
   LG_REQUIRE(ro.page_tokens >= 4 && ro.page_tokens % 4 == 0 && ro.page_stride > 0, "gemm rope: bad page geometry");
-  launch_wide(wide_fn<kEpiRopeKv>(mode), mode, A, Alo, M, W, false, nullptr, nullptr, nullptr, 0, bias, ro, st);
+  launch_wide(wide_fn<kEpiRopeKv>(mode), mode, A, Alo, M, W, false, nullptr, nullptr, nullptr, 0, bias, ro, st, ks);
   return true;
 }
 

@@ -176,6 +176,77 @@ __global__ void q8_prefill_copy_kernel(const int8_t *__restrict__ q, const uint1
   scales[int64_t(kb) * rows + n] = half_bits(s[i]);
 }
 
+// Prefill copy of a Q4_K matrix in the two-pass form (DevMatrix::pc, pcs, pcl, pcr), one wave per
+// row: codes as f16, the sub-block scales A = d*sc transposed, and the correction planes of -B =
+// -(dmin*m) scaled by the row's power of two 2^e (its largest |B| into [2^13, 2^14), so the f16 lo
+// plane stays out of the subnormals) with 2^-e kept per row.  Scaling by 2^e is exact.
+__global__ __launch_bounds__(256) void q4k_prefill_copy_kernel(const uint8_t *__restrict__ q, const float2 *__restrict__ s,
+                                                               int rows, int cols, int kp, _Float16 *__restrict__ codes,
+                                                               float *__restrict__ ascale, _Float16 *__restrict__ bh,
+                                                               _Float16 *__restrict__ bl, float *__restrict__ rs) {
+  const int row = int(blockIdx.x) * 4 + int(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const int nb = cols / 32;
+  const float2 *sr = s + int64_t(row) * nb;
+  float mx = 0.0f;
+  for (int c = lane; c < nb; c += 64) mx = fmaxf(mx, fabsf(sr[c].y));
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  int e = 0;  // a zero or non-finite maximum leaves the row unscaled
+  if (mx > 0.0f && mx <= 3.4e38f) {
+    int ex;
+    (void)frexpf(mx, &ex);  // mx = f 2^ex, f in [0.5, 1)
+    e = 14 - ex;
+  }
+  const float up = ldexpf(1.0f, e);
+  if (lane == 0) rs[row] = ldexpf(1.0f, -e);
+  for (int c = lane; c < kp; c += 64) {
+    _Float16 h = _Float16(0.0f), l = _Float16(0.0f);
+    if (c < nb) {
+      split_f16(-(sr[c].y * up), h, l);
+      ascale[int64_t(c) * rows + row] = sr[c].x;
+    }
+    bh[int64_t(row) * kp + c] = h;
+    bl[int64_t(row) * kp + c] = l;
+  }
+  // byte j of each 64-element group holds element j (low nibble) and j + 32 (high nibble)
+  const uint8_t *qr = q + int64_t(row) * (cols / 2);
+  for (int k = lane; k < cols; k += 64) {
+    const uint32_t byte = qr[(k / 64) * 32 + (k % 32)];
+    codes[int64_t(row) * cols + k] = _Float16(float((k % 64) >= 32 ? (byte >> 4) : (byte & 15u)));
+  }
+}
+
+// Chunk sums of hi/lo activation planes (launch_chunk_sums): one 32-element chunk per thread.
+__global__ __launch_bounds__(256) void chunk_sums_kernel(const _Float16 *__restrict__ A, const _Float16 *__restrict__ Alo,
+                                                         int M, int K, int kp, _Float16 *__restrict__ ks) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= int64_t(M) * kp) return;
+  const int m = int(i / kp), c = int(i % kp);
+  float sum = 0.0f;
+  if (c < K / 32) {
+    const uint4 *h = reinterpret_cast<const uint4 *>(A + int64_t(m) * K + c * 32);
+    const uint4 *l = reinterpret_cast<const uint4 *>(Alo + int64_t(m) * K + c * 32);
+    uint4 hv[4], lv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      hv[u] = h[u];
+      lv[u] = l[u];
+    }
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const h8 a = __builtin_bit_cast(h8, hv[u]), b = __builtin_bit_cast(h8, lv[u]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sum += f32_pin(float(a[e]) + float(b[e]));  // hi + lo is exact in f32
+    }
+  }
+  _Float16 hh, ll;
+  split_f16(sum, hh, ll);
+  ks[i] = hh;
+  ks[int64_t(M) * kp + i] = ll;
+}
+
 inline unsigned grid_for(uint64_t n, unsigned block) { return unsigned((n + block - 1) / block); }
 
 }  // namespace
@@ -235,9 +306,18 @@ size_t prefill_copy_bytes(uint32_t kind, int rows, int cols) {
   switch (kind) {
     case LG_Q8_0: return n * 2 + size_t(rows) * size_t(cols / 32) * 4;
     case LG_Q4_K:
+      return n * 2 + size_t(rows) * size_t(cols / 32) * 4 + size_t(rows) * size_t(ksum_cols(cols)) * 4 + size_t(rows) * 4;
     case LG_Q6_K: return n * 4;
   }
   return 0;
+}
+
+void launch_chunk_sums(const _Float16 *A, const _Float16 *Alo, int M, int K, int kp, _Float16 *ks, hipStream_t st) {
+  LG_REQUIRE(A && Alo && ks && M > 0 && K % 32 == 0 && kp >= K / 32, "chunk sums: bad arguments");
+  const int64_t n = int64_t(M) * kp;
+  LG_REQUIRE((n + 255) / 256 < (int64_t(1) << 31), "chunk sums: too many rows");
+  hipLaunchKernelGGL(chunk_sums_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, A, Alo, M, K, kp, ks);
+  HIP_CHECK(hipGetLastError());
 }
 
 void launch_prefill_copy(const DevMatrix &w, hipStream_t st) {
@@ -250,7 +330,13 @@ void launch_prefill_copy(const DevMatrix &w, hipStream_t st) {
     hipLaunchKernelGGL(q8_prefill_copy_kernel, dim3(unsigned((blocks + 255) / 256)), dim3(256), 0, st,
                        static_cast<const int8_t *>(w.q), static_cast<const uint16_t *>(w.s), w.rows, w.cols, w.pc,
                        w.pcs);
-  } else if (w.kind == LG_Q4_K || w.kind == LG_Q6_K) {
+  } else if (w.kind == LG_Q4_K) {
+    LG_REQUIRE(w.pcs && w.pcl && w.pcr && w.cols % 256 == 0 && w.pkp == ksum_cols(w.cols),
+               "prefill copy: Q4_K needs codes, scales, correction planes and whole super-blocks");
+    hipLaunchKernelGGL(q4k_prefill_copy_kernel, dim3(unsigned((w.rows + 3) / 4)), dim3(256), 0, st,
+                       static_cast<const uint8_t *>(w.q), static_cast<const float2 *>(w.s), w.rows, w.cols, w.pkp, w.pc,
+                       w.pcs, w.pcl, w.pcl + int64_t(w.rows) * w.pkp, w.pcr);
+  } else if (w.kind == LG_Q6_K) {
     LG_REQUIRE(w.pcl && w.cols % 256 == 0, "prefill copy: K-quant needs both planes and whole super-blocks");
     LG_REQUIRE((n + 255) / 256 < (int64_t(1) << 31), "prefill copy: matrix too large");
     hipLaunchKernelGGL(split_planes_kernel, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, w, w.pc, w.pcl);

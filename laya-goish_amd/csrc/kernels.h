@@ -9,6 +9,8 @@
 #include <cmath>
 #include <cstdint>
 
+#include "lg.h"
+
 namespace lg {
 
 // Kernel timing: while a KernelTimer is installed on the calling thread, the GEMV and GEMM
@@ -51,10 +53,17 @@ struct DevMatrix {
   // form the large-batch GEMM (gemm_wide.h) moves to LDS by DMA with no conversion on the way:
   //   Q8_0 : pc = codes as f16 [rows][cols], pcs = block scales as f32 [cols/32][rows]
   //   F16  : pc = q (the weights themselves; no copy)
-  //   Q4_K, Q6_K: pc / pcl = f16 hi / lo planes [rows][cols] of the dequantised f32 weight
+  //   Q4_K : the two-pass form of w = A q - B (A = d*sc, B = dmin*m per 32-element sub-block):
+  //          pc = codes q as f16 [rows][cols], pcs = A as f32 [cols/32][rows] (the Q8_0 form), and
+  //          the correction sum_c B[n][c] * ksum[m][c] as a GEMM of depth pkp = ksum_cols(cols):
+  //          pcl = -B[n][c] * 2^e_n split into f16 hi [rows][pkp] then lo [rows][pkp] (zero past
+  //          cols/32), pcr = 2^-e_n [rows], e_n putting the row's largest |B| in [2^13, 2^14)
+  //   Q6_K : pc / pcl = f16 hi / lo planes [rows][cols] of the dequantised f32 weight
   _Float16 *pc = nullptr;
   _Float16 *pcl = nullptr;
   float *pcs = nullptr;
+  float *pcr = nullptr;
+  int pkp = 0;
   int64_t bytes() const;  // HBM bytes of q + s
   int64_t gguf_bytes() const;  // bytes of the same matrix in GGUF blocks
 };
@@ -83,13 +92,25 @@ void launch_repack(uint32_t kind, const uint8_t *src, int rows, int cols, DevMat
 size_t prefill_copy_bytes(uint32_t kind, int rows, int cols);
 void launch_prefill_copy(const DevMatrix &w, hipStream_t st);
 
+// Depth of the Q4_K correction GEMM: one column per 32-element sub-block, rounded up to 128.
+inline int ksum_cols(int cols) { return (cols / 32 + 127) / 128 * 128; }
+// Chunk sums of an activation given as f16 hi/lo planes [M][K]: ks[m][c] = sum over the 32 elements
+// k of chunk c of (hi + lo), left to right in f32, split into f16 hi [M][kp] then lo [M][kp] planes
+// (zero for c >= K/32).  The Q4_K correction GEMM's activation operand.
+void launch_chunk_sums(const _Float16 *A, const _Float16 *Alo, int M, int K, int kp, _Float16 *ks, hipStream_t st);
+
 // Prefill GEMM: out = A[M][K] (half, row-major, lda = K) . W^T with epilogue `epi`.
 // A_lo == nullptr: one f16 pass.  A_lo != nullptr: A = A + A_lo (hi/lo f16 planes) and the
 // weights are applied exactly (split-precision MFMA, f32-faithful).  f16 outputs (Epi::F16,
 // Epi::SWIGLU) are written as hi/lo planes when C16_lo != nullptr.
 // For Epi::SWIGLU the output has W.rows/2 columns.
+// ks: the chunk sums of A (launch_chunk_sums, hi plane then lo plane of M x W.pkp), required by an
+// exact Q4_K launch whose matrix has the two-pass prefill copy (W.pcr), ignored otherwise.
 void launch_gemm(const _Float16 *A, const _Float16 *A_lo, int M, const DevMatrix &W, Epi epi, float *C,
-                 _Float16 *C16, _Float16 *C16_lo, int ldc, const float *bias, hipStream_t st);
+                 _Float16 *C16, _Float16 *C16_lo, int ldc, const float *bias, hipStream_t st,
+                 const _Float16 *ks = nullptr);
+// True when an exact launch of W needs the chunk sums of its activation (Q4_K, two-pass copy).
+inline bool needs_ksum(const DevMatrix &W) { return W.kind == LG_Q4_K && W.pcr != nullptr; }
 
 // Generic f32 GEMM for shapes the tiled kernel does not take (any M, N, K), F32/F16/Q weights.
 void launch_gemm_generic(const float *X, int M, const DevMatrix &W, const float *bias, float *Y,
@@ -148,7 +169,7 @@ struct RopeKvOut {
 // launched) when the wide kernel does not take the launch (gemm_wide_takes) or the layout is not
 // one the epilogue covers (head_dim 128, col0 a multiple of 128).
 bool launch_gemm_wide_rope(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, const float *bias,
-                           const RopeKvOut &ro, hipStream_t st);
+                           const RopeKvOut &ro, hipStream_t st, const _Float16 *ks = nullptr);
 // Whether the 256 x 256 exact GEMM takes an M-row launch of W with epilogue epi (shape, prefill
 // copy and tile count; pointers are checked at launch).
 bool gemm_wide_takes(int M, const DevMatrix &W, Epi epi);
