@@ -45,17 +45,19 @@ DECODE_CTX, DECODE_STEPS = 2048, 64
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_q8-2048_bench.md")
+TRAFFIC_FILE_C4 = os.path.join(ROOT, "profiles", "hbm_traffic_q4km-7b_prefill.md")
+TRAFFIC_FILE_C5 = os.path.join(ROOT, "profiles", "hbm_traffic_f16-7b_long-context.md")
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def measured_traffic(kernel):
+def measured_traffic(kernel, path=TRAFFIC_FILE):
     """HBM bytes per launch of `kernel` from the committed FETCH_SIZE + WRITE_SIZE counter runs of
-    this workload (lines `traffic.<kernel> <bytes>`), or None when that summary is absent."""
+    a workload (lines `traffic.<kernel> <bytes>` of its summary), or None when that summary is absent."""
     try:
-        for line in open(TRAFFIC_FILE):
+        for line in open(path):
             parts = line.split()
             if len(parts) == 2 and parts[0] == f"traffic.{kernel}":
                 return int(parts[1])
@@ -400,7 +402,9 @@ def c4_q4k(args, prec, layer_cost):
         "roofline": roofline("mfma", rate(gp, "flops"), PEAK_F16_TFLOPS, "TFLOP/s",
                              "gemm (exact K-quant MFMA GEMM: Q4_K in two f16 passes over exact codes with a depth-K/32 "
                              "correction, Q6_K in three passes over f16 hi/lo weight planes)", gp["launches"],
-                             gp["ms"] / max(1, gp["launches"])),
+                             gp["ms"] / max(1, gp["launches"]), measured_traffic("gemm", TRAFFIC_FILE_C4),
+                             traffic_source="profiles/hbm_traffic_q4km-7b_prefill.md (FETCH_SIZE + WRITE_SIZE, "
+                                            "copy-calibrated)"),
         "kernel_ms_per_step": {c: round(p["ms"], 3) for c, p in prof.items()},
     }
     if layer_cost:
@@ -475,7 +479,9 @@ def c5_long_context(args, prec, layer_cost):
         "computed_tok_per_s": round(computed / dt, 1), "load": load,
         "roofline": roofline("mfma", rate(gp, "flops"), PEAK_F16_TFLOPS, "TFLOP/s",
                              "gemm (F16 weights, hi/lo split activations: two f16 passes per product)",
-                             gp["launches"], gp["ms"] / max(1, gp["launches"])),
+                             gp["launches"], gp["ms"] / max(1, gp["launches"]), measured_traffic("gemm", TRAFFIC_FILE_C5),
+                             traffic_source="profiles/hbm_traffic_f16-7b_long-context.md (FETCH_SIZE + WRITE_SIZE, "
+                                            "copy-calibrated)"),
         "attention": roofline("mfma", att_tf, PEAK_F16_TFLOPS, "TFLOP/s",
                               "attn_prefill (causal GQA over the paged KV cache as f16 hi/lo planes; three f16 passes per product)",
                               ap["launches"], ap["ms"] / max(1, ap["launches"]),
@@ -913,6 +919,48 @@ def bench_vendor_gemm(args, prec):
             "peak_TFLOP/s": PEAK_F16_TFLOPS, "shapes": rows}
 
 
+DECODE_MATRIX_BYTES = {"o": 4456448, "down": 12255232, "q|k|v": 13369344, "gate|up": 24510464, "head": 69632000}
+
+
+def bench_launch_floor(args, prec):
+    """The GPU-side cost of one dependent launch at the decode matrix sizes: chains of 200 back-to-back
+    plain read kernels (torch.sum over an f32 buffer of each matrix's GGUF byte count: every byte read once,
+    one float written), timed with events on one stream, plus a one-element sum for the launch alone.  A
+    line through the sizes gives the fixed cost per launch and the streaming rate that the decode GEMV's
+    launches are measured against."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    chain = 200
+    rows = {}
+    sizes = dict(DECODE_MATRIX_BYTES)
+    sizes["empty"] = 4
+    for label, nbytes in sizes.items():
+        t = torch.ones(max(1, nbytes // 4), device=dev, dtype=torch.float32)
+        out = torch.empty((), device=dev, dtype=torch.float32)
+        for _ in range(20):
+            torch.sum(t, out=out)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(chain):
+            torch.sum(t, out=out)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / chain
+        rows[label] = {"bytes": nbytes, "us_per_launch": round(us, 3),
+                       "GB_per_s": round(nbytes / (us * 1e-6) / 1e9, 1) if label != "empty" else None}
+        log(f"launch floor {label:8s} {nbytes:10d} B: {us:7.3f} us per launch")
+        del t, out
+    xs = np.array([v["bytes"] for k, v in rows.items() if k != "empty"], np.float64)
+    ys = np.array([v["us_per_launch"] for k, v in rows.items() if k != "empty"], np.float64)
+    slope, icpt = np.polyfit(xs, ys, 1)
+    return {"workload": "launch floor at the decode matrix sizes: chains of 200 dependent plain read kernels "
+                        "(torch.sum over f32 buffers of each matrix's GGUF bytes) on one stream",
+            "sizes": rows, "fit": {"fixed_us": round(float(icpt), 3),
+                                   "streaming_TB_per_s": round(1e-6 / float(slope), 2)}}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -920,7 +968,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--precision", choices=["exact", "fast"], default="exact")
     ap.add_argument("--workload", choices=["decide", "plumbing", "q4k-prefill", "long-context", "decide-request",
-                                           "decide-batch", "openthai-decide", "laya-decide", "vendor-gemm"],
+                                           "decide-batch", "openthai-decide", "laya-decide", "vendor-gemm", "launch-floor"],
                     default="decide",
                     help="decide (default): the Q8_0 d2048 batched decide headline with the other four workload "
                          "configurations (C1 plumbing, C3 decode, C4 Q4_K 7B prefill, C5 long context) nested in "
@@ -947,21 +995,21 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     prec = lh.PREC_EXACT if args.precision == "exact" else lh.PREC_FAST
-    if args.workload in ("plumbing", "q4k-prefill", "long-context"):
-        print(json.dumps(bench_single(args, prec, args.workload)), flush=True)
-        return
-    if args.workload != "decide":
-        fn = {"decide-request": bench_decide_request, "decide-batch": bench_decide_batch,
-              "openthai-decide": bench_openthai, "laya-decide": bench_laya, "vendor-gemm": bench_vendor_gemm}
-        print(json.dumps(fn[args.workload](args, prec)), flush=True)
-        return
-    wanted = [c.strip().upper() for c in args.configs.split(",") if c.strip()]
     if args.copy_calibration > 0:
         n = args.copy_calibration * (1 << 20) // 4
         src = np.arange(n, dtype=np.float32)
         for _ in range(2):
             assert np.array_equal(lh.dequant(lh.F32, src.view(np.uint8)), src)
         log(f"copy calibration: 2 launches of the F32 dequant kernel, {n * 4} B read + {n * 4} B written each")
+    if args.workload in ("plumbing", "q4k-prefill", "long-context"):
+        print(json.dumps(bench_single(args, prec, args.workload)), flush=True)
+        return
+    if args.workload != "decide":
+        fn = {"decide-request": bench_decide_request, "decide-batch": bench_decide_batch,
+              "openthai-decide": bench_openthai, "laya-decide": bench_laya, "vendor-gemm": bench_vendor_gemm, "launch-floor": bench_launch_floor}
+        print(json.dumps(fn[args.workload](args, prec)), flush=True)
+        return
+    wanted = [c.strip().upper() for c in args.configs.split(",") if c.strip()]
     log(f"generating {PRESET} (seed {SEED})")
     t0 = time.perf_counter()
     img = lh.SynthImage(PRESET, seed=SEED)

@@ -843,11 +843,15 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
                          srow0.size() * 2 + it_r.size() * 5 + cb_r.size() * 4 + 64;
     b->meta.ensure(nints * 4 + 34 * 256);
     int32_t *base = b->meta.as<int32_t>();
+    // every table goes into one host image at its 256-byte aligned offset, uploaded by one copy
+    std::vector<int32_t> image;
+    image.reserve(nints + 34 * 64);
     size_t off = 0;
     auto put = [&](const std::vector<int32_t> &v, int32_t *&dst) {
       dst = base + off;
-      if (!v.empty()) HIP_CHECK(hipMemcpyAsync(dst, v.data(), v.size() * 4, hipMemcpyHostToDevice, stream));
+      image.insert(image.end(), v.begin(), v.end());
       off += (v.size() + 63) & ~size_t(63);
+      image.resize(off, 0);
     };
     put(ids, b->ids);
     put(tseq, b->tok_seq);
@@ -872,6 +876,8 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
     put(cb_n, b->cb_nq);
     put(cb_f, b->cb_first);
     put(cb_c, b->cb_n);
+    LG_REQUIRE(image.size() * 4 <= b->meta.n, "batch: metadata image exceeds its buffer");
+    if (!image.empty()) HIP_CHECK(hipMemcpyAsync(base, image.data(), image.size() * 4, hipMemcpyHostToDevice, stream));
     b->nitems = int(it_r.size());
     b->ncomb = int(cb_r.size());
     HIP_CHECK(hipStreamSynchronize(stream));
