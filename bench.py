@@ -924,41 +924,27 @@ DECODE_MATRIX_BYTES = {"o": 4456448, "down": 12255232, "q|k|v": 13369344, "gate|
 
 def bench_launch_floor(args, prec):
     """The GPU-side cost of one dependent launch at the decode matrix sizes: chains of 200 back-to-back
-    plain read kernels (torch.sum over an f32 buffer of each matrix's GGUF byte count: every byte read once,
-    one float written), timed with events on one stream, plus a one-element sum for the launch alone.  A
-    line through the sizes gives the fixed cost per launch and the streaming rate that the decode GEMV's
-    launches are measured against."""
-    import torch
-
-    dev = torch.device("cuda:0")
+    launches of the library's plain read kernel (lg_probe_read: 16-byte loads, nothing written), each over
+    its own slice of each matrix's GGUF byte count (about 2 GiB of slices, so the bytes come from HBM as
+    the decode's distinct matrices do), timed with events on one stream, and one 16-byte read for the
+    launch alone.  A line through the sizes gives the fixed cost per launch and the streaming rate
+    that the decode GEMV's launches are measured against."""
     chain = 200
     rows = {}
     sizes = dict(DECODE_MATRIX_BYTES)
-    sizes["empty"] = 4
+    sizes["empty"] = 16
     for label, nbytes in sizes.items():
-        t = torch.ones(max(1, nbytes // 4), device=dev, dtype=torch.float32)
-        out = torch.empty((), device=dev, dtype=torch.float32)
-        for _ in range(20):
-            torch.sum(t, out=out)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(chain):
-            torch.sum(t, out=out)
-        e1.record()
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / chain
+        us = lh.probe_read(nbytes, chain)
         rows[label] = {"bytes": nbytes, "us_per_launch": round(us, 3),
                        "GB_per_s": round(nbytes / (us * 1e-6) / 1e9, 1) if label != "empty" else None}
         log(f"launch floor {label:8s} {nbytes:10d} B: {us:7.3f} us per launch")
-        del t, out
     xs = np.array([v["bytes"] for k, v in rows.items() if k != "empty"], np.float64)
     ys = np.array([v["us_per_launch"] for k, v in rows.items() if k != "empty"], np.float64)
     slope, icpt = np.polyfit(xs, ys, 1)
-    return {"workload": "launch floor at the decode matrix sizes: chains of 200 dependent plain read kernels "
-                        "(torch.sum over f32 buffers of each matrix's GGUF bytes) on one stream",
-            "sizes": rows, "fit": {"fixed_us": round(float(icpt), 3),
-                                   "streaming_TB_per_s": round(1e-6 / float(slope), 2)}}
+    return {"workload": "launch floor at the decode matrix sizes: chains of 200 dependent launches of a plain "
+                        "read kernel (lg_probe_read), each over its own slice of each matrix's GGUF bytes (about 2 GiB of slices: "
+                        "HBM reads), on one stream",
+            "sizes": rows, "fit": {"fixed_us": round(float(icpt), 3), "streaming_TB_per_s": round(1e-6 / float(slope), 2)}}
 
 
 def main():

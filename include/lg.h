@@ -252,6 +252,14 @@ int lg_decode_noalloc(lg_engine *e, int seq, int32_t first, int steps, int32_t *
 int lg_decode_graph(lg_engine *e, int seq, int32_t first, int steps, int32_t *tokens, double *capture_ms,
                     double *run_ms);
 
+/* Launch-floor probe on the current device: `launches` dependent launches of a plain read kernel
+ * (16-byte loads, four per thread issued together, nothing written), each over its own zero-filled slice
+ * of `bytes` (slices of about 2 GiB in all, so the reads come from HBM rather than the memory-side cache),
+ * timed with events on a stream of its own; *us_per_launch receives the average.  No
+ * reference counterpart: it measures the fixed cost of a dependent launch and the streaming rate that
+ * the decode GEMV's launches are compared against. */
+int lg_probe_read(uint64_t bytes, int launches, double *us_per_launch);
+
 /* Option scores over host logits, the CPU side of the same rule (for callers that
  * already hold logits).  Replaces src/models/openthai/decision.rs:268-279. */
 int lg_option_scores(const float *logits, int k, float temperature, float *probs,

@@ -77,6 +77,13 @@ int lg_layout(uint32_t kind, uint64_t *block, uint64_t *bytes) {
 
 float lg_half(uint16_t bits) { return lg::half_to_float(bits); }
 
+int lg_probe_read(uint64_t bytes, int launches, double *us_per_launch) {
+  return guard([&] {
+    NEED(us_per_launch, "us_per_launch");
+    *us_per_launch = lg::probe_read_chain(size_t(bytes), launches);
+  });
+}
+
 int lg_gguf_open(const char *path, lg_gguf **out) {
   return guard([&] {
     NEED(path, "path");

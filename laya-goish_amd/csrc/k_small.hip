@@ -2,6 +2,8 @@
 // with the paged KV-cache write, the option head and option scores, full-vocab argmax.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include <cfloat>
 #include <cmath>
 
@@ -595,6 +597,73 @@ void launch_fill_i32(int32_t *p, int n, int32_t v, hipStream_t st) {
   if (n <= 0) return;
   hipLaunchKernelGGL(fill_i32_kernel, dim3((n + 255) / 256), dim3(256), 0, st, p, n, v);
   HIP_CHECK(hipGetLastError());
+}
+
+namespace {
+// Plain read of n16 16-byte words for the launch-floor probe: each thread issues its four loads
+// before using any, one workgroup covers 16 KiB; the single store is conditional on a value the
+// zero-filled buffer never holds, so the kernel writes nothing.
+__global__ __launch_bounds__(256) void probe_read_kernel(const uint4 *__restrict__ p, int64_t n16,
+                                                         uint32_t *__restrict__ sink) {
+  constexpr int PER = 4;
+  const int64_t base = int64_t(blockIdx.x) * 256 * PER + threadIdx.x;
+  uint4 v[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) v[i] = p[min(base + int64_t(i) * 256, n16 - 1)];
+  uint32_t acc = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+  if (acc == 0x9e3779b9u) sink[blockIdx.x & 255] = acc;
+}
+}  // namespace
+
+double probe_read_chain(size_t bytes, int launches) {
+  LG_REQUIRE(bytes >= 16 && launches > 0 && launches <= 100000, "probe: need >= 16 bytes and 1..100000 launches");
+  const int64_t n16 = int64_t(bytes / 16);
+  const int64_t blocks = (n16 + 1023) / 1024;
+  LG_REQUIRE(blocks < (int64_t(1) << 31), "probe: buffer too large");
+  // consecutive launches read distinct slices, about 2 GiB in all (8x the memory-side cache), so the
+  // bytes come from HBM as a decode step's distinct weight matrices do
+  const size_t stride = (size_t(n16) * 16 + 255) / 256 * 256;
+  const int64_t nslice = std::max<int64_t>(1, std::min<int64_t>(launches, int64_t((size_t(2) << 30) / stride) + 1));
+  void *buf = nullptr, *sink = nullptr;
+  hipStream_t st = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  struct Cleanup {
+    void *&b, *&s;
+    hipStream_t &st;
+    hipEvent_t &a, &z;
+    ~Cleanup() {
+      if (st) (void)hipStreamSynchronize(st);
+      if (b) (void)hipFree(b);
+      if (s) (void)hipFree(s);
+      if (a) (void)hipEventDestroy(a);
+      if (z) (void)hipEventDestroy(z);
+      if (st) (void)hipStreamDestroy(st);
+    }
+  } cleanup{buf, sink, st, e0, e1};
+  HIP_CHECK(hipMalloc(&buf, stride * size_t(nslice)));
+  HIP_CHECK(hipMalloc(&sink, 256 * 4));
+  HIP_CHECK(hipStreamCreate(&st));
+  HIP_CHECK(hipMemsetAsync(buf, 0, stride * size_t(nslice), st));
+  HIP_CHECK(hipEventCreate(&e0));
+  HIP_CHECK(hipEventCreate(&e1));
+  auto run = [&](int k) {
+    for (int i = 0; i < k; ++i) {
+      const uint4 *slice = reinterpret_cast<const uint4 *>(static_cast<const uint8_t *>(buf) + stride * size_t(i % nslice));
+      hipLaunchKernelGGL(probe_read_kernel, dim3(unsigned(blocks)), dim3(256), 0, st, slice, n16,
+                         static_cast<uint32_t *>(sink));
+    }
+  };
+  run(std::min(launches, 20));  // warm-up
+  HIP_CHECK(hipEventRecord(e0, st));
+  run(launches);
+  HIP_CHECK(hipEventRecord(e1, st));
+  HIP_CHECK(hipEventSynchronize(e1));
+  HIP_CHECK(hipGetLastError());
+  float ms = 0.0f;
+  HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+  return double(ms) * 1e3 / launches;
 }
 
 }  // namespace lg

@@ -129,6 +129,11 @@ void launch_rmsnorm_f16(const float *x, int rows, int d, const float *w, float e
 void launch_rmsnorm_f32(const float *x, int rows, int d, const float *w, float eps, float *y,
                         hipStream_t st);
 
+// Launch-floor probe: `launches` dependent launches of a plain read kernel, each over its own zero-filled
+// slice of `bytes` (~2 GiB of slices in all: HBM reads), on a stream of its own (current device); returns
+// the average microseconds per launch.
+double probe_read_chain(size_t bytes, int launches);
+
 // Embedding rows (F16 or F32 table [vocab][d]) -> f32 x[T][d].
 void launch_embed(const void *table, uint32_t kind, const int32_t *ids, int T, int d, int vocab,
                   float *x, hipStream_t st);

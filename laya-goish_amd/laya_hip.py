@@ -257,6 +257,7 @@ def lib() -> ctypes.CDLL:
             "lg_engine_destroy": (None, [P]),
             "lg_engine_info": (I, [P, ctypes.POINTER(ModelInfo)]),
             "lg_engine_sync": (I, [P]),
+            "lg_probe_read": (I, [ctypes.c_uint64, I, ctypes.POINTER(ctypes.c_double)]),
             "lg_engine_workspace_bytes": (I, [P, ctypes.POINTER(ctypes.c_int64)]),
             "lg_matmul": (I, [P, ctypes.c_char_p, P, I, P, P]),
             "lg_seq_create": (I, [P, ctypes.POINTER(I)]),
@@ -326,6 +327,13 @@ def layout(kind: int) -> tuple[int, int]:
 
 def half(bits: int) -> float:
     return lib().lg_half(bits)
+
+
+def probe_read(nbytes: int, launches: int = 200) -> float:
+    """lg_probe_read: microseconds per dependent launch of a plain read kernel over nbytes."""
+    us = ctypes.c_double()
+    check(lib().lg_probe_read(nbytes, launches, ctypes.byref(us)))
+    return us.value
 
 
 def dequant(kind: int, raw: bytes | np.ndarray) -> np.ndarray:

@@ -91,3 +91,16 @@ def test_matmul_vs_apply(model, po, m):
         else:
             err = assert_logits_close(got, want, rel=1e-2)
             assert err > 1e-5, f"fast-mode error {err:.2e} is inside the exact-mode bar"
+
+
+def test_probe_read_launch_floor(lh):
+    """lg_probe_read (the launch-floor probe): a plain read chain gives a positive time per launch that
+    grows with the bytes read, and bad arguments are refused without launching."""
+    small = lh.probe_read(16, 50)
+    big = lh.probe_read(64 << 20, 50)
+    print(f"probe: 16 B {small:.2f} us, 64 MiB {big:.2f} us per launch", flush=True)
+    assert 0.0 < small < big
+    with pytest.raises(lh.LayaError):
+        lh.probe_read(8, 10)
+    with pytest.raises(lh.LayaError):
+        lh.probe_read(1024, 0)
