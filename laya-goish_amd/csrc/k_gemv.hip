@@ -168,6 +168,18 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const float *__restrict_
   constexpr int XQ = BIGK ? 1 : CPL;
   float4 xr[XQ], nr[XQ];
   if constexpr (!BIGK) load_x_regs(x, norm_w, K / 4, xr, nr);
+  // the epilogue's other operand (the residual row for ADD, the bias for F32) loaded with x, ahead of
+  // the weights, so the store at the end waits on no further memory round trip; the index is kept in
+  // a vector register so each lane issues the (uniform) load itself
+  float ep[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    int oi = min(o0 + r, outputs - 1);
+    asm volatile("" : "+v"(oi));
+    ep[r] = 0.0f;
+    if constexpr (EPI == int(Epi::ADD)) ep[r] = y[oi];
+    else if constexpr (EPI == int(Epi::F32)) ep[r] = bias ? bias[oi] : 0.0f;
+  }
   wvec w;
   svec sc;
   avec acc;
@@ -243,8 +255,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const float *__restrict_
     } else {
       const float v = wave_sum(acc[r]) * inv;
       if (lane == 0 && o < outputs) {
-        if (EPI == int(Epi::ADD)) y[o] += v;
-        else y[o] = v + (bias ? bias[o] : 0.0f);
+        if (EPI == int(Epi::ADD)) y[o] = ep[r] + v;
+        else y[o] = v + ep[r];
       }
     }
   }
