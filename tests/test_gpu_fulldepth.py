@@ -1,9 +1,9 @@
 """Full-depth GPU parity on the headline workloads, against the oracle at the same depth.
 
   Q8_0 batched prefill decide (24 layers, d2048, 16 x 128 heads, FFN 5632, vocab 32000): the
-  benchmark's own batch of 64 requests x 560 tokens runs on the GPU; its first and last
-  requests (3 answer positions x 4 option tokens each) are recomputed by the oracle through all
-  24 layers.
+  benchmark's own batch of 64 requests x 560 tokens runs on the GPU; eight of its requests (3
+  answer positions x 4 option tokens each) are recomputed by the oracle through all 24 layers,
+  the first and last also by a float64 and a numpy f32 forward.
   Q8_0 batch-1 greedy decode (same model): the benchmark's 2048-token context, then 64 greedy
   steps; the oracle is fed the same tokens (teacher forcing) through its KV-cached decode and
   every step's full-vocabulary logits and argmax are compared.
@@ -79,6 +79,22 @@ def test_q8_prefill_decide_24_layers(lh, po, q8_full, tmp_path):
     def P(L):
         return np.stack([po.option_scores(np.float32(r))[0] for r in L])
 
+    # eight requests across the batch against the oracle; the first and last also against float64
+    # and a numpy f32 forward with its own operation order (the noise floor of two correct f32 orders)
+    worst_l, worst_p = 0.0, 0.0
+    for r in (9, 18, 27, 36, 45, 54):
+        ids, pos = reqs[r]
+        want = om.forward(ids, pos, option_ids)
+        got_l = logits[r * npos:(r + 1) * npos]
+        got_p = probs[r * npos:(r + 1) * npos]
+        el, ep = logit_error(got_l, want), float(np.abs(got_p - P(want)).max())
+        worst_l, worst_p = max(worst_l, el), max(worst_p, ep)
+        print(f"request {r} gpu-oracle   : logits rel {el:.3e}, probs abs {ep:.3e}", flush=True)
+        assert np.isfinite(got_l).all() and np.isfinite(got_p).all()
+        assert el <= LOGIT_REL
+        assert (np.argmax(got_l, axis=1) == np.argmax(want, axis=1)).all()
+        assert ep <= PROB_ABS
+    print(f"requests 9-54: worst logits rel {worst_l:.3e}, worst probs abs {worst_p:.3e}", flush=True)
     for r in (0, len(reqs) - 1):
         ids, pos = reqs[r]
         t0 = time.perf_counter()
