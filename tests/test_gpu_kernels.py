@@ -104,3 +104,47 @@ def test_probe_read_launch_floor(lh):
         lh.probe_read(8, 10)
     with pytest.raises(lh.LayaError):
         lh.probe_read(1024, 0)
+
+
+def _uncentred_q4k(nblocks, rng):
+    """Q4_K blocks drawn as the letter of the config reads (d and dmin f16(|N(0, 1e-3)|) drawn
+    independently, every 6-bit scale and min any value, nibbles uniform): the block minimum does not
+    cancel the nibble mean, so the two terms of the two-pass form, A (x . q) and B sum(x), are large
+    against their difference."""
+    out = np.empty((nblocks, 144), np.uint8)
+    out[:, 0:2] = np.abs(rng.normal(0, 1e-3, nblocks)).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    out[:, 2:4] = np.abs(rng.normal(0, 1e-3, nblocks)).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    out[:, 4:] = rng.integers(0, 256, (nblocks, 140), dtype=np.uint8)
+    return out
+
+
+@pytest.mark.parametrize("mean", [0.0, 2.0], ids=["x-zero-mean", "x-mean-2"])
+def test_q4k_two_pass_on_uncentred_blocks(lh, po, mean):
+    """The exact Q4_K GEMM (two passes over the codes plus the depth-K/32 correction) against
+    Matrix::apply on Q4_K matrices whose blocks are not zero-centred, with activations of zero and of
+    large mean (the correction's chunk sums then dominate): the 128 x 128 tiles (130 and 300 rows) and
+    the 256 x 256 kernel (16,384 rows), each within the exact mode's 1e-5 of the largest output."""
+    rng = np.random.default_rng(31)
+    img = lh.SynthImage("tiny-q4k", seed=12)
+    buf = img.array().copy()
+    og0 = po.Gguf(buf)
+    names = [n for n in _matrices(og0) if og0.tensor(n)[0] == 12]
+    assert names, "the preset holds Q4_K matrices"
+    for n in names:
+        _, _, raw = og0.tensor(n)
+        off = og0.offset(n)
+        buf[off:off + len(raw)] = _uncentred_q4k(len(raw) // 144, rng).ravel()
+    og = po.Gguf(buf)
+    eng = lh.Engine(lh.Gguf.from_bytes(buf), kv_tokens=1024, max_batch_tokens=16384)
+    for n in names:
+        kind, dims, raw = og.tensor(n)
+        cols, rows = dims
+        w = po.decode(kind, raw).reshape(rows, cols)
+        for m in (130, 300, 16384):
+            x = (mean + rng.standard_normal((m, cols))).astype(np.float32)
+            print(f"{n} ({rows} x {cols}) m={m} x mean {mean}", flush=True)
+            got = eng.matmul(n, x)
+            want = po.apply(w, x, None, threads=16)
+            err = assert_logits_close(got, want, rel=1e-5)
+            print(f"  max err / max |out| {err:.2e}", flush=True)
+    eng.close()
