@@ -153,9 +153,10 @@ def cpu_pair(entries):
 
 
 # ---------------------------------------------------------------- C3: batch-1 greedy decode
-def c3_decode(eng, args):
+def c3_decode(eng, args, extras=True):
     """The benchmark's 2048-token context on the Q8_0 d2048 model, then DECODE_STEPS greedy steps
-    (one forked sequence per run, so every run decodes the same positions)."""
+    (one forked sequence per run, so every run decodes the same positions).  extras: also the
+    HIP-graph decode and the CPU baseline."""
     steps = args.decode_steps
     rng = np.random.default_rng(SEED + 1)
     ids = rng.integers(0, eng.info["vocab"], DECODE_CTX).astype(np.int32)
@@ -180,7 +181,7 @@ def c3_decode(eng, args):
     # the same decode with every kernel of every step captured into one HIP graph and launched once:
     # the GPU time of the launch (through its completion) against the stream-launched run above
     graph = None
-    if not args.no_graph:
+    if extras and not args.no_graph:
         s = eng.seq_fork(base, DECODE_CTX)
         gtoks, cap_ms, graph_ms = eng.decode_graph(s, first, steps)
         eng.seq_free(s)
@@ -207,13 +208,14 @@ def c3_decode(eng, args):
                              "gemv (dequant-fused Q8_0 GEMV, GGUF bytes per launch)", gv["launches"],
                              gv["ms"] / max(1, gv["launches"]), measured_traffic("gemv")),
         "attention": roofline("hbm", rate(at, "bytes"), PEAK_HBM_GBS, "GB/s",
-                              "attn_decode (KV bytes read per launch: f16 hi + lo planes in the exact mode; incl. the page-combine launch)",
+                              "attn_decode (KV bytes read per launch: f16 hi + lo planes in the exact mode, f16 in "
+                              "the kv16 and fast modes; incl. the page-combine launch)",
                               at["launches"], at["ms"] / max(1, at["launches"])),
         "kernel_ms_per_token": {c: round(p["ms"] / steps, 4) for c, p in prof.items()},
     }
     if graph:
         out["graph"] = graph
-    if not args.no_cpu:
+    if extras and not args.no_cpu:
         po = oracle_modules()
         layers = 2
         img = lh.SynthImage(PRESET, seed=SEED, n_layers=layers)
@@ -536,9 +538,10 @@ def bench_single(args, prec, name):
 def base_line(metric, value, unit, higher, steps, warmup, ms, prec, workload, **extra):
     return {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": steps, "warmup": warmup,
             "ms_per_step": round(ms, 3), "higher_is_better": higher, "scaling": "weak", "vs_baseline": None,
-            "dtype": "f32" if prec == lh.PREC_EXACT else "f16", "data": "synthetic",
+            "dtype": "f16" if prec == lh.PREC_FAST else "f32", "data": "synthetic",
             "config": dict(workload=workload, seed=SEED,
-                           precision="exact" if prec == lh.PREC_EXACT else "fast", **extra)}
+                           precision={lh.PREC_EXACT: "exact", lh.PREC_FAST: "fast", lh.PREC_KV16: "kv16"}[prec],
+                           **extra)}
 
 
 def decide_request(vocab, seed):
@@ -952,7 +955,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--precision", choices=["exact", "fast"], default="exact")
+    ap.add_argument("--precision", choices=["exact", "fast", "kv16"], default="exact")
     ap.add_argument("--workload", choices=["decide", "plumbing", "q4k-prefill", "long-context", "decide-request",
                                            "decide-batch", "openthai-decide", "laya-decide", "vendor-gemm", "launch-floor"],
                     default="decide",
@@ -980,7 +983,7 @@ def main():
               "the workload's requests are independent, so N GPUs would each run their own batch.",
               file=sys.stderr)
         sys.exit(2)
-    prec = lh.PREC_EXACT if args.precision == "exact" else lh.PREC_FAST
+    prec = {"exact": lh.PREC_EXACT, "fast": lh.PREC_FAST, "kv16": lh.PREC_KV16}[args.precision]
     if args.copy_calibration > 0:
         n = args.copy_calibration * (1 << 20) // 4
         src = np.arange(n, dtype=np.float32)
@@ -1024,7 +1027,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if prec == lh.PREC_EXACT else "f16",
+        "dtype": "f16" if prec == lh.PREC_FAST else "f32",
         "data": "synthetic",
         "config": {
             "workload": f"Q8_0 batched prefill decide: {REQUESTS} requests x {PROMPT + QUESTIONS * QBLOCK} tokens "
@@ -1035,8 +1038,11 @@ def main():
             "tokens_per_step": T,
             "seed": SEED,
             "precision": args.precision,
-            "arithmetic": ("f16 hi/lo split MFMA with f32 accumulation, exact Q8_0 block scaling, KV cache as f16 hi/lo planes"
-                           if prec == lh.PREC_EXACT else "f16 MFMA, f32 accumulation, f16 KV cache"),
+            "arithmetic": {lh.PREC_EXACT: "f16 hi/lo split MFMA with f32 accumulation, exact Q8_0 block scaling, KV "
+                                          "cache as f16 hi/lo planes",
+                           lh.PREC_KV16: "f16 hi/lo split MFMA with f32 accumulation, exact Q8_0 block scaling, f16 KV "
+                                         "cache",
+                           lh.PREC_FAST: "f16 MFMA, f32 accumulation, f16 KV cache"}[prec],
         },
         "decide_req_per_s": round(REQUESTS * args.steps / dt, 2),
         "roofline": roofline("mfma", gemm_tflops, PEAK_F16_TFLOPS, "TFLOP/s",
@@ -1051,6 +1057,19 @@ def main():
     if "C3" in wanted:
         configs["C3"] = c3_decode(eng, args)
     eng.close()
+    if "C3" in wanted and prec == lh.PREC_EXACT:
+        # the north star's f16 KV cache: the same decode over an f16 cache (the kv16 mode).  Reported beside
+        # the measured line only: at 24 layers of this model its logits miss the 2e-2 bar
+        eng = lh.Engine(g, device=0, kv_tokens=DECODE_CTX * 3 + 512, precision=lh.PREC_KV16)
+        kv = c3_decode(eng, args, extras=False)
+        eng.close()
+        configs["C3"]["kv16"] = {
+            "ms_per_token": kv["ms_per_token"], "value": kv["value"], "unit": "tok/s",
+            "kernel_ms_per_token": kv["kernel_ms_per_token"], "attention": kv["attention"],
+            "parity": "outside the north-star bars: decode logits up to 9.2e-2 of the largest |logit| against "
+                      "2e-2, and the greedy argmax differs from the oracle at 5 of 64 steps outside the near-tie "
+                      "window (tests/test_gpu_fulldepth.py, strict xfail); not the measured value",
+        }
     del g, img
     if "C1" in wanted:
         configs["C1"] = c1_plumbing(args, prec)

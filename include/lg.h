@@ -93,18 +93,25 @@ typedef struct lg_engine lg_engine;
 
 /* Numeric modes of the prefill path (the decode GEMV always computes in f32):
  * LG_PREC_EXACT: f32-faithful -- activations carried as hi/lo f16 planes into split-precision
- *   MFMA, weights applied exactly, f32 KV cache.  Matches the f32 reference to its own
- *   summation-order spread even on ill-conditioned models.  The default.
+ *   MFMA, weights applied exactly, KV cache as hi/lo f16 planes (4 bytes a value, about 22
+ *   significant bits).  Matches the f32 reference to its own summation-order spread even on
+ *   ill-conditioned models.  The default.
+ * LG_PREC_KV16: LG_PREC_EXACT's projections (hi/lo activation planes, exact weights) over an
+ *   f16 KV cache (2 bytes a value, k and v rounded to nearest f16): decode attention reads half
+ *   the bytes and prefill attention takes two f16 MFMA passes a product instead of three.
+ *   Queries and attention probabilities stay hi/lo planes.  Only the decoder family keeps a KV
+ *   cache; for the other families this mode is LG_PREC_EXACT.
  * LG_PREC_FAST: one f16 MFMA pass, weights rounded to f16, f16 KV cache. */
 #define LG_PREC_EXACT 0
 #define LG_PREC_FAST 1
+#define LG_PREC_KV16 2
 
 typedef struct {
   int device;              /* HIP device ordinal */
   int kv_pages;            /* 64-token KV pages to reserve (0 = derive from kv_tokens) */
   int64_t kv_tokens;       /* tokens of KV capacity when kv_pages == 0 (0 = 65536) */
   int64_t max_batch_tokens;/* largest prefill batch (0 = 65536) */
-  int precision;           /* LG_PREC_EXACT (0) or LG_PREC_FAST */
+  int precision;           /* LG_PREC_EXACT (0), LG_PREC_FAST or LG_PREC_KV16 */
 } lg_engine_opts;
 
 typedef struct {
@@ -114,7 +121,7 @@ typedef struct {
   int64_t kv_bytes;        /* HBM bytes of the KV page pool */
   int kv_pages, kv_page_tokens;
   int precision;           /* LG_PREC_* the engine was created with */
-  int kv_elem_bytes;       /* 4 (f16 hi + lo planes, exact mode) or 2 (f16, fast mode) */
+  int kv_elem_bytes;       /* 4 (f16 hi + lo planes, exact mode) or 2 (f16: kv16 and fast modes) */
   int arch;                /* LG_ARCH_* */
   int linear_heads;        /* OpenThai: gated DeltaNet heads (128-dim); 0 otherwise */
   int full_layers;         /* OpenThai: full-attention layers (the rest are DeltaNet) */

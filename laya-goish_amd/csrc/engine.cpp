@@ -243,7 +243,7 @@ Engine::Engine(const Gguf &g, const lg_engine_opts &opts) {
   if (device < 0 || device >= ndev) fail(LG_ERR_INVALID, "device %d out of range (%d devices)", device, ndev);
   HIP_CHECK(hipSetDevice(device));
   max_batch_tokens_ = opts.max_batch_tokens > 0 ? opts.max_batch_tokens : 65536;
-  if (opts.precision != LG_PREC_EXACT && opts.precision != LG_PREC_FAST)
+  if (opts.precision != LG_PREC_EXACT && opts.precision != LG_PREC_FAST && opts.precision != LG_PREC_KV16)
     fail(LG_ERR_INVALID, "unknown precision mode %d", opts.precision);
   precision = opts.precision;
   try {
@@ -565,7 +565,7 @@ KvGeom Engine::geom() const {
   g.hd = hd;
   g.page_stride = page_stride_;
   g.layer_stride = int64_t(npages_) * page_stride_;
-  g.split = split() ? 1 : 0;
+  g.split = kv_split() ? 1 : 0;
   return g;
 }
 void *Engine::kpool(int layer) const {
@@ -948,6 +948,7 @@ void Engine::run_layers_prefill(BatchPlan &b, lg_cancel_fn cancel, void *arg) {
       ro.hd = hd;
       ro.page_tokens = g.page_tokens;
       ro.qscale = attn_q_scale(hd);
+      ro.kv_planes = kv_split() ? 2 : 1;
       for (const ProjPart &p : ly.qkv) {
         ro.col0 = p.col0;
         const _Float16 *ks = chunk_sums(h16, h16lo, T, p.w);

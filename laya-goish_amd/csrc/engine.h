@@ -255,8 +255,9 @@ class Engine {
   int precision = LG_PREC_EXACT;
   DecideSpec decide;  // control tokens and budgets of the request-level decide layout
   LayaSpec laya_decide;  // budgets, special ids and temperatures of the Laya decide
-  bool split() const { return precision == LG_PREC_EXACT; }
-  int kv_elem() const { return split() ? 4 : 2; }
+  bool split() const { return precision != LG_PREC_FAST; }     // hi/lo activation planes
+  bool kv_split() const { return precision == LG_PREC_EXACT; }  // hi/lo KV cache planes
+  int kv_elem() const { return kv_split() ? 4 : 2; }
 
  private:
   // weights

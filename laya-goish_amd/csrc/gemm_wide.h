@@ -487,6 +487,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
     const int head = (ro.col0 + nt * BN + wn * 128) >> 7;
     const int part = head < ro.hq ? 0 : head < ro.hq + ro.hkv ? 1 : 2;  // q, k, v
     const int PT = ro.page_tokens, plane = PT * 128;
+    const int kvp = ro.kv_planes;  // pool planes: 2 (hi, lo) or 1 (f16, the hi value)
     float bv[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) bv[j] = bias ? bias[nt * BN + wn * 128 + j * 16 + lr] : 0.0f;
@@ -531,9 +532,10 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
             dl = ro.q16lo + int64_t(row) * (ro.hq * 128) + head * 128;
           } else {
             const int64_t blk = int64_t(page[r]) * ro.page_stride + int64_t(head - ro.hq) * plane;
-            dh = ro.kpool + 2 * blk + (pos[r] % PT) * 128;
+            dh = ro.kpool + kvp * blk + (pos[r] % PT) * 128;
             dl = dh + plane;
           }
+          const bool lo = part == 0 || kvp == 2;
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             float a, c;
@@ -545,10 +547,10 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
             _Float16 h, l;
             split_f16(a, h, l);
             dh[j * 16 + lr] = h;
-            dl[j * 16 + lr] = l;
+            if (lo) dl[j * 16 + lr] = l;
             split_f16(c, h, l);
             dh[j * 16 + lr + 64] = h;
-            dl[j * 16 + lr + 64] = l;
+            if (lo) dl[j * 16 + lr + 64] = l;
           }
         }
       } else {
@@ -572,17 +574,17 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
           }
           if (quad) {
             const int64_t blk = int64_t(page[0]) * ro.page_stride + int64_t(head - ro.hq - ro.hkv) * plane;
-            _Float16 *dh = ro.vpool + 2 * blk + int64_t(d) * PT + (pos[0] % PT);
+            _Float16 *dh = ro.vpool + kvp * blk + int64_t(d) * PT + (pos[0] % PT);
             *reinterpret_cast<half4 *>(dh) = h4;
-            *reinterpret_cast<half4 *>(dh + plane) = l4;
+            if (kvp == 2) *reinterpret_cast<half4 *>(dh + plane) = l4;
           } else {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               if (rb + r >= M) continue;
               const int64_t blk = int64_t(page[r]) * ro.page_stride + int64_t(head - ro.hq - ro.hkv) * plane;
-              _Float16 *dh = ro.vpool + 2 * blk + int64_t(d) * PT + (pos[r] % PT);
+              _Float16 *dh = ro.vpool + kvp * blk + int64_t(d) * PT + (pos[r] % PT);
               dh[0] = h4[r];
-              dh[plane] = l4[r];
+              if (kvp == 2) dh[plane] = l4[r];
             }
           }
         }

@@ -6,12 +6,14 @@
 //
 // KV page layout (one layer, one page of P = 64 tokens), per kv head:
 //   K: [P][hd] (row per token)     V: [hd][P] (column per token)
-// in f16 (FAST) or as two f16 planes (EXACT: the hi plane hi = f16(v), then the lo plane
+// in f16 (FAST, KV16) or as two f16 planes (EXACT: the hi plane hi = f16(v), then the lo plane
 // lo = f16(v - hi), each of that layout; hi + lo holds v to about 22 significant bits).
 //
 // Prefill: one workgroup per (group of query tiles, kv head, block of the kv head's query
-// heads), MFMA 32x32x16 f16; with split planes every product is hi.hi + lo.hi + hi.lo (three
-// MFMAs), which keeps scores and outputs f32-faithful.
+// heads), MFMA 16x16x32 f16.  Queries and probabilities as hi/lo planes over a split cache make
+// every product hi.hi + lo.hi + hi.lo (three MFMAs), which keeps scores and outputs f32-faithful;
+// over an f16 cache, hi.c + lo.c (two MFMAs): exact in the query and probability, the cache value
+// as stored.
 //
 // Decode (one new token): one workgroup per (kv head, page): coalesced reads of the page's K
 // rows and V columns, RoPE of the group's query heads (and, on the last page, of the new key,
@@ -57,8 +59,9 @@ constexpr int P = 64;  // tokens per page
 // LDS: K rows unpadded, the 16-byte chunk x of key row R at slot x ^ kswz(R), so the sixteen rows
 // an operand read takes fall in distinct 16-byte bank groups; V rows (one dim, 64 keys) carry one
 // pad slot for the same reason.
-// NPL = 2: split cache, queries and P as hi/lo planes, three MFMAs a product (hi.hi + lo.hi +
-// hi.lo); NPL = 1: f16 cache and queries, one MFMA.
+// NQ: planes of the queries and of P (2: hi/lo, 1: f16); NKV: planes of the cache (2: hi/lo,
+// 1: f16).  (2, 2): three MFMAs a product (hi.hi + lo.hi + hi.lo); (2, 1): two (hi.c + lo.c);
+// (1, 1): one.
 template <int HD>
 __device__ __forceinline__ int kswz(int row) {
   return HD == 128 ? ((row & 3) | (((row >> 3) & 3) << 2)) : ((row & 3) | (((row >> 3) & 1) << 2));
@@ -79,7 +82,7 @@ __device__ __forceinline__ half8 lds_half8(const unsigned char *base, int slot) 
   return *reinterpret_cast<const half8 *>(base + slot * 16);
 }
 
-template <int HD, int NPL, int W, int GB>
+template <int HD, int NQ, int NKV, int W, int GB>
 __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
     const _Float16 *__restrict__ q16, const _Float16 *__restrict__ q16lo, int hq, KvGeom g,
     const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ vpool, const int32_t *__restrict__ pages,
@@ -87,7 +90,8 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
     const int32_t *__restrict__ tile_seq, const int32_t *__restrict__ tile_row0,
     const int32_t *__restrict__ tile_pos0, const int32_t *__restrict__ tile_n,
     _Float16 *__restrict__ out16, _Float16 *__restrict__ out16lo) {
-  using S = PrefillStage<HD, NPL>;
+  static_assert(NKV <= NQ, "an f16 query over a split cache is not a mode");
+  using S = PrefillStage<HD, NKV>;
   constexpr int NC = HD / 32, DB = HD / 16;  // 32-deep chunks of the head dim, 16-dim output blocks
   constexpr int NI = (S::BLOCKS + W - 1) / W;  // LDS-DMA instructions per wave per page
   __shared__ __align__(16) unsigned char lds[2 * S::BYTES];
@@ -113,7 +117,7 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
 
   // this lane's byte offset inside the kv head's K (or V) block for each of its DMA slots; pad
   // slots get an offset past the block, which the buffer load turns into zeros without a read
-  constexpr uint32_t kHeadBytes = uint32_t(NPL) * P * HD * 2;
+  constexpr uint32_t kHeadBytes = uint32_t(NKV) * P * HD * 2;
   uint32_t off[NI];
 #pragma unroll
   for (int i = 0; i < NI; ++i) {
@@ -131,8 +135,8 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
     off[i] = o;
   }
   const int32_t *ptab = pages + int64_t(seq) * max_pages;
-  const int64_t page_halves = int64_t(NPL) * g.page_stride;  // halves per page of one layer
-  const int64_t head_halves = int64_t(NPL) * P * HD;         // halves per kv head of one page
+  const int64_t page_halves = int64_t(NKV) * g.page_stride;  // halves per page of one layer
+  const int64_t head_halves = int64_t(NKV) * P * HD;         // halves per kv head of one page
   auto issue = [&](int32_t page, int st) {
     const int64_t base = int64_t(page) * page_halves + kh * head_halves;
     const __amdgpu_buffer_rsrc_t rk =
@@ -155,14 +159,14 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
 
   // queries qb * 16 + lr of the tile (rows past n repeat row n - 1 and are never stored), the eight
   // dims 32 c + 8 g .. + 8 of each 32-deep chunk c
-  half8 qr[2][NC], ql[2][NPL == 2 ? NC : 1];
+  half8 qr[2][NC], ql[2][NQ == 2 ? NC : 1];
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     const int64_t qo = int64_t(row0 + min(qb * 16 + lr, n - 1)) * qw + h * HD + qg * 8;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       qr[qb][c] = *reinterpret_cast<const half8 *>(q16 + qo + 32 * c);
-      if constexpr (NPL == 2) ql[qb][c] = *reinterpret_cast<const half8 *>(q16lo + qo + 32 * c);
+      if constexpr (NQ == 2) ql[qb][c] = *reinterpret_cast<const half8 *>(q16lo + qo + 32 * c);
     }
   }
   f32x4 acc[2][DB];
@@ -194,8 +198,8 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
     }
     if (kt < mypages) {
       const unsigned char *stage = lds + st * S::BYTES;
-      const unsigned char *kl_ = stage + S::KPL * 16 * (NPL - 1);  // K lo plane (= hi when NPL 1)
-      const unsigned char *vh_ = stage + S::KSLOTS * 16, *vl_ = vh_ + S::VPL * 16 * (NPL - 1);
+      const unsigned char *kl_ = stage + S::KPL * 16 * (NKV - 1);  // K lo plane (= hi when NKV 1)
+      const unsigned char *vh_ = stage + S::KSLOTS * 16, *vl_ = vh_ + S::VPL * 16 * (NKV - 1);
       f32x4 s[2][2][2];  // [qb][ck][h]
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb)
@@ -213,12 +217,18 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
           for (int hh = 0; hh < 2; ++hh) {
             const int slot = (ck * 32 + kr0 + 4 * hh) * S::KC + ((4 * c + qg) ^ ksw);
             const half8 kh8 = lds_half8(stage, slot);
-            if constexpr (NPL == 2) {
+            if constexpr (NQ == 2 && NKV == 2) {
               const half8 kl8 = lds_half8(kl_, slot);
 #pragma unroll
               for (int qb = 0; qb < 2; ++qb) {
                 s[qb][ck][hh] = MFMA(kh8, qr[qb][c], s[qb][ck][hh]);
                 s[qb][ck][hh] = MFMA(kl8, qr[qb][c], s[qb][ck][hh]);
+                s[qb][ck][hh] = MFMA(kh8, ql[qb][c], s[qb][ck][hh]);
+              }
+            } else if constexpr (NQ == 2) {
+#pragma unroll
+              for (int qb = 0; qb < 2; ++qb) {
+                s[qb][ck][hh] = MFMA(kh8, qr[qb][c], s[qb][ck][hh]);
                 s[qb][ck][hh] = MFMA(kh8, ql[qb][c], s[qb][ck][hh]);
               }
             } else {
@@ -298,7 +308,7 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
             pv[e] = s[qb][ck][0][e];
             pv[4 + e] = s[qb][ck][1][e];
           }
-          if constexpr (NPL == 2) split8_pk(pv, ph[qb], pl[qb]);
+          if constexpr (NQ == 2) split8_pk(pv, ph[qb], pl[qb]);
           else
 #pragma unroll
             for (int e = 0; e < 8; ++e) ph[qb][e] = _Float16(pv[e]);
@@ -307,12 +317,18 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
         for (int b = 0; b < DB; ++b) {
           const int vo = (b * 16 + lr) * S::VRS + 4 * ck + qg;
           const half8 vh = lds_half8(vh_, vo);
-          if constexpr (NPL == 2) {
+          if constexpr (NQ == 2 && NKV == 2) {
             const half8 vl = lds_half8(vl_, vo);
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
               acc[qb][b] = MFMA(vh, ph[qb], acc[qb][b]);
               acc[qb][b] = MFMA(vl, ph[qb], acc[qb][b]);
+              acc[qb][b] = MFMA(vh, pl[qb], acc[qb][b]);
+            }
+          } else if constexpr (NQ == 2) {
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+              acc[qb][b] = MFMA(vh, ph[qb], acc[qb][b]);
               acc[qb][b] = MFMA(vh, pl[qb], acc[qb][b]);
             }
           } else {
@@ -344,7 +360,7 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
       }
       const int64_t at = obase + b * 16;
       *reinterpret_cast<half4 *>(out16 + at) = o;
-      if constexpr (NPL == 2) *reinterpret_cast<half4 *>(out16lo + at) = olo;
+      if constexpr (NQ == 2) *reinterpret_cast<half4 *>(out16lo + at) = olo;
     }
   }
 }
@@ -729,7 +745,7 @@ void launch_attn_prefill(const _Float16 *q16, const _Float16 *q16_lo, int T, int
   LG_REQUIRE(g.hkv > 0 && hq % g.hkv == 0, "attention: hq %% hkv != 0");
   LG_REQUIRE(ntiles > 0 && T > 0, "attention: empty batch");
   const bool split = q16_lo != nullptr;
-  LG_REQUIRE(split == (g.split != 0), "attention: split queries need the split cache and vice versa");
+  LG_REQUIRE(split || !g.split, "attention: the split cache needs split queries");
   LG_REQUIRE(!split || out16_lo, "attention: split path needs the lo output plane");
   LG_REQUIRE(grp_first && grp_count && ngroups > 0 && ngroups <= ntiles, "attention: bad tile groups");
   const int G = hq / g.hkv;
@@ -738,22 +754,22 @@ void launch_attn_prefill(const _Float16 *q16, const _Float16 *q16_lo, int T, int
   LG_REQUIRE(nwg < (1ll << 31), "attention: too many tiles");
   const dim3 grid{static_cast<uint32_t>(nwg)}, block{static_cast<uint32_t>(64 * sh.gb * sh.t)};
   const _Float16 *kp = static_cast<const _Float16 *>(kpool), *vp = static_cast<const _Float16 *>(vpool);
-#define LAUNCH(HDV, NPLV, WV, GBV)                                                                          \
-  hipLaunchKernelGGL((attn_prefill_kernel<HDV, NPLV, WV, GBV>), grid, block, 0, st, q16, q16_lo, hq, g, kp, vp, \
+#define LAUNCH(HDV, NQV, NKVV, WV, GBV)                                                                   \
+  hipLaunchKernelGGL((attn_prefill_kernel<HDV, NQV, NKVV, WV, GBV>), grid, block, 0, st, q16, q16_lo, hq, g, kp, vp, \
                      pages, max_pages, grp_first, grp_count, tile_seq, tile_row0, tile_pos0, tile_n, out16,    \
                      out16_lo)
-#define SHAPES(HDV, NPLV)                  \
-  switch (sh.gb) {                         \
-    case 2: LAUNCH(HDV, NPLV, 8, 2); break; \
-    case 4: LAUNCH(HDV, NPLV, 8, 4); break; \
-    case 7: LAUNCH(HDV, NPLV, 7, 7); break; \
-    case 8: LAUNCH(HDV, NPLV, 8, 8); break; \
-    default: LAUNCH(HDV, NPLV, 8, 1); break; \
+#define SHAPES(HDV, NQV, NKVV)                   \
+  switch (sh.gb) {                               \
+    case 2: LAUNCH(HDV, NQV, NKVV, 8, 2); break; \
+    case 4: LAUNCH(HDV, NQV, NKVV, 8, 4); break; \
+    case 7: LAUNCH(HDV, NQV, NKVV, 7, 7); break; \
+    case 8: LAUNCH(HDV, NQV, NKVV, 8, 8); break; \
+    default: LAUNCH(HDV, NQV, NKVV, 8, 1); break; \
   }
   if (g.hd == 128) {
-    if (split) { SHAPES(128, 2) } else { SHAPES(128, 1) }
+    if (g.split) { SHAPES(128, 2, 2) } else if (split) { SHAPES(128, 2, 1) } else { SHAPES(128, 1, 1) }
   } else if (g.hd == 64) {
-    if (split) { SHAPES(64, 2) } else { SHAPES(64, 1) }
+    if (g.split) { SHAPES(64, 2, 2) } else if (split) { SHAPES(64, 2, 1) } else { SHAPES(64, 1, 1) }
   } else {
     fail(LG_ERR_UNSUPPORTED, "attention: head_dim %d not supported (64, 128)", g.hd);
   }

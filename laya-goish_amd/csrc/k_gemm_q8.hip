@@ -167,6 +167,7 @@ bool launch_gemm_wide_rope(const _Float16 *A, const _Float16 *Alo, int M, const 
   LG_REQUIRE(ro.cosT && ro.sinT && ro.tok_pos && ro.tok_page && ro.q16 && ro.q16lo && ro.kpool && ro.vpool,
              "gemm rope: missing output");
   LG_REQUIRE(ro.page_tokens >= 4 && ro.page_tokens % 4 == 0 && ro.page_stride > 0, "gemm rope: bad page geometry");
+  LG_REQUIRE(ro.kv_planes == 1 || ro.kv_planes == 2, "gemm rope: KV pools hold 1 or 2 planes, not %d", ro.kv_planes);
   launch_wide(wide_fn<kEpiRopeKv>(mode), mode, A, Alo, M, W, false, nullptr, nullptr, nullptr, 0, bias, ro, st, ks);
   return true;
 }

@@ -162,15 +162,17 @@ struct RopeKvOut {
   const float *cosT = nullptr, *sinT = nullptr;          // [ctx][128]
   const int32_t *tok_pos = nullptr, *tok_page = nullptr;  // per activation row: position, its page
   _Float16 *q16 = nullptr, *q16lo = nullptr;              // [M][hq * 128] hi / lo planes
-  _Float16 *kpool = nullptr, *vpool = nullptr;            // the layer's split pools
+  _Float16 *kpool = nullptr, *vpool = nullptr;            // the layer's pools
   int64_t page_stride = 0;                                // as KvGeom::page_stride
   int hq = 0, hkv = 0, hd = 128, page_tokens = 64, col0 = 0;  // hd: must be 128
   float qscale = 1.0f;                                    // attn_q_scale(128)
+  int kv_planes = 2;                                      // 2: hi/lo pool planes; 1: f16 pools
 };
 
 // The 256 x 256 exact GEMM (gemm_wide.h) of a q|k|v projection, or a column range of it, with the
 // RoPE and KV cache stores of launch_rope_kv_tiles as its epilogue: q to f16 hi/lo planes
-// (scaled), k and v into the split pools at each row's position and page.  Returns false (nothing
+// (scaled), k and v into the pools (hi/lo planes, or f16 when ro.kv_planes is 1) at each row's
+// position and page.  Returns false (nothing
 // launched) when the wide kernel does not take the launch (gemm_wide_takes) or the layout is not
 // one the epilogue covers (head_dim 128, col0 a multiple of 128).
 bool launch_gemm_wide_rope(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, const float *bias,
@@ -194,8 +196,9 @@ void launch_rope_kv_tiles(const float *qkv, int hq, const KvGeom &g, const float
 // Causal prefill attention over the paged cache, queries as launch_rope_kv_tiles leaves them
 // (pre-scaled by log2(e) / sqrt(hd)).  Work items: tiles of 32 query rows of one
 // sequence (tile_seq, tile_row0 = first batch row, tile_pos0 = its position, tile_n rows).
-// q16_lo != nullptr selects the split-precision path (requires the split cache); the output is
-// then written as hi/lo planes (out16, out16_lo).  Tiles go in groups (grp_first[i],
+// q16_lo != nullptr selects the split-precision path, over the split cache (g.split) or an f16
+// one; the output is then written as hi/lo planes (out16, out16_lo).  f16 queries need the f16
+// cache.  Tiles go in groups (grp_first[i],
 // grp_count[i] for i < ngroups) of at most attn_prefill_group_tiles(hq, hkv) consecutive tiles
 // of one sequence; each group's workgroups share every K/V page through LDS.  head_dim 64 or 128.
 // A query's output does not depend on which group or batch its tile is in.

@@ -21,7 +21,7 @@ LIB_PATH = os.path.join(HERE, "liblaya_hip.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "lg.h")
 
 F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
-PREC_EXACT, PREC_FAST = 0, 1
+PREC_EXACT, PREC_FAST, PREC_KV16 = 0, 1, 2
 ARCH_LAYA_DECODER, ARCH_OPENTHAI, ARCH_LAYA = 0, 1, 2
 KIND_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
 ERR = {1: "INVALID", 2: "FORMAT", 3: "DEVICE", 4: "OOM", 5: "CANCELED", 6: "UNSUPPORTED"}

@@ -15,8 +15,9 @@ import pydecide as pd
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(scope="module", params=[("tiny-q8", 0), ("tiny-f16", 0), ("plumbing-f16", 0), ("tiny-f16", 1)],
-                ids=lambda p: f"{p[0]}-{'exact' if p[1] == 0 else 'fast'}")
+@pytest.fixture(scope="module", params=[("tiny-q8", 0), ("tiny-f16", 0), ("plumbing-f16", 0), ("tiny-f16", 1),
+                                        ("tiny-f16", 2)],
+                ids=lambda p: f"{p[0]}-{('exact', 'fast', 'kv16')[p[1]]}")
 def setup(request, lh, po):
     preset, prec = request.param
     img = lh.SynthImage(preset, seed=11, n_layers=2 if preset == "plumbing-f16" else 0)

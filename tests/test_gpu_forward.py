@@ -9,8 +9,8 @@ checked as bit-exact properties of the GPU path.
 import numpy as np
 import pytest
 
-from parity import (assert_argmax_equal, assert_bits_equal, assert_logits_close, assert_probs_close, logit_bar,
-                    logit_error, tie_window)
+from parity import (PREC_NAMES, assert_argmax_equal, assert_bits_equal, assert_logits_close, assert_probs_close,
+                    logit_bar, logit_error, tie_window)
 
 pytestmark = pytest.mark.gpu
 
@@ -18,8 +18,9 @@ OPTIONS = [3, 17, 42, 99]
 
 
 @pytest.fixture(scope="module", params=[("tiny-f16", 0), ("tiny-q8", 0), ("tiny-q4k", 0), ("tiny-f16-128", 0),
-                                        ("tiny-f16", 1), ("tiny-f16-128", 1)],
-                ids=lambda p: f"{p[0]}-{'exact' if p[1] == 0 else 'fast'}")
+                                        ("tiny-f16", 1), ("tiny-f16-128", 1),
+                                        ("tiny-f16", 2), ("tiny-q4k", 2), ("tiny-f16-128", 2)],
+                ids=lambda p: f"{p[0]}-{PREC_NAMES[p[1]]}")
 def pair(request, lh, po):
     preset, prec = request.param
     img = lh.SynthImage(preset, seed=5)
@@ -240,7 +241,7 @@ def test_errors_are_reported(pair, lh):
     eng.seq_free(s)
 
 
-@pytest.mark.parametrize("prec", [0, 1], ids=["exact", "fast"])
+@pytest.mark.parametrize("prec", [0, 1, 2], ids=["exact", "fast", "kv16"])
 def test_golden_logits(lh, prec):
     """The committed float64 brute-force logits (tests/golden/forward_tiny.npz)."""
     import os
@@ -255,7 +256,7 @@ def test_golden_logits(lh, prec):
         eng.close()
 
 
-@pytest.mark.parametrize("prec", [0, 1], ids=["exact", "fast"])
+@pytest.mark.parametrize("prec", [0, 1, 2], ids=["exact", "fast", "kv16"])
 def test_plumbing_model_decision(lh, po, prec):
     """The CPU-runnable plumbing model: 128-token prompt + one yes/no question block."""
     img = lh.SynthImage("plumbing-f16", seed=1)
@@ -326,15 +327,17 @@ def test_q8_large_batch_tiles_equal_single_requests(lh, po):
     eng.close()
 
 
-def test_q8_fused_qkv_epilogue_ragged_continuations(lh, po):
+@pytest.mark.parametrize("prec", [0, 2], ids=["exact", "kv16"])
+def test_q8_fused_qkv_epilogue_ragged_continuations(lh, po, prec):
     """A batch big enough for the 256 x 256 q|k|v GEMM stores q, k and v from its own epilogue
     (RoPE, q planes, K page rows, V page columns); requests alone keep the f32 q|k|v rows and the
     RoPE kernel.  Ragged requests continue sequences that already hold 0..130 tokens, so rows meet
     positions that are not multiples of 4 and quads of rows that straddle a sequence or a page: the
     V columns' four-slot stores and their one-slot fallback both run.  Batch == alone, bit for bit,
-    at positions in every request, and one request matches the oracle."""
+    at positions in every request, and one request matches the oracle.  Both cache formats (hi/lo
+    planes, f16)."""
     img = lh.SynthImage("q8-2048", seed=29, n_layers=2)
-    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=2 * 4608, max_batch_tokens=4096)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=2 * 4608, max_batch_tokens=4096, precision=prec)
     rng = np.random.default_rng(31)
     # tokens each sequence holds before the batch: request 0's rows and positions agree mod 4 (the
     # four-slot V stores), every other request's do not
@@ -363,8 +366,54 @@ def test_q8_fused_qkv_epilogue_ragged_continuations(lh, po):
     om = po.Model(po.Gguf(img.array()), threads=16)
     want = om.forward(ctx[5], [heads[5] + q for q in pos[5]], opts)
     first = sum(len(p) for p in pos[:5])
-    err = assert_logits_close(logits[first:first + len(pos[5])], want, rel=logit_bar(0))
-    print(f"q8-2048 ragged continuations: bit-identical to single requests; logit rel {err:.2e} vs oracle")
+    err = assert_logits_close(logits[first:first + len(pos[5])], want, rel=logit_bar(prec))
+    print(f"q8-2048 ragged continuations ({PREC_NAMES[prec]}): bit-identical to single requests; logit rel "
+          f"{err:.2e} vs oracle")
     for s in seqs:
         eng.seq_free(s)
     eng.close()
+
+
+def test_kv16_cache_holds_the_exact_values_rounded(lh):
+    """The kv16 mode's cache holds each k and v the exact mode holds (as hi + lo planes) rounded to the
+    nearest f16, from every writer: the fused q|k|v epilogue (a 16 x 512 batch), the RoPE kernel (a
+    request alone) and the decode step.  Layer 0 only: from layer 1 on the two modes' inputs differ by
+    the cache rounding itself."""
+    img = lh.SynthImage("q8-2048", seed=41, n_layers=2)
+    rng = np.random.default_rng(43)
+    reqs = [rng.integers(0, 32000, 512).astype(np.int32) for _ in range(16)]
+    alone = rng.integers(0, 32000, 200).astype(np.int32)
+    got = {}
+    for prec in (0, 2):
+        eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=16 * 576 + 1024, max_batch_tokens=16 * 512,
+                        precision=prec)
+        assert eng.info["kv_elem_bytes"] == (4 if prec == 0 else 2)
+        seqs = [eng.seq_create() for _ in reqs]
+        eng.batch([(s, ids, [511]) for s, ids in zip(seqs, reqs)]).run([1, 2])
+        one = eng.seq_create()
+        eng.forward(one, alone, [], [1, 2])
+        toks = eng.decode(one, 7, 3)
+        got[prec] = ([eng.seq_kv_read(s, 0, 0, 512) for s in (seqs[0], seqs[9], seqs[15])],
+                     eng.seq_kv_read(one, 0, 0, 203), toks)
+        eng.close()
+    (bx, ox, tx), (bh, oh, th) = got[0], got[2]
+    n_one = 201 + int(np.argmin(tx[:2] == th[:2])) if not np.array_equal(tx[:2], th[:2]) else 203
+    pairs = [(x, h) for bxr, bhr in zip(bx, bh) for x, h in zip(bxr, bhr)]
+    pairs += [(x[:n_one], h[:n_one]) for x, h in zip(ox, oh)]
+    # the kv16 value is the exact mode's hi plane, f16(k); f16(hi + lo) equals it except where lo is
+    # exactly half an f16 step of hi (a tie the sum rounds to even, while hi was rounded from k itself)
+    worst, mism, total = 0.0, 0, 0
+    for x, h in pairs:
+        r16 = x.astype(np.float16)
+        ulp = np.spacing(np.abs(h.astype(np.float16))).astype(np.float64)
+        dist = np.abs(h.astype(np.float64) - x.astype(np.float64)) / ulp
+        worst = max(worst, float(dist.max()))
+        off = r16.astype(np.float32) != h
+        x64 = x.astype(np.float64)
+        assert (np.abs(x64 - h)[off] == np.abs(x64 - r16.astype(np.float64))[off]).all(), \
+            "a kv16 value that is neither the exact value rounded nor the other side of a tie"
+        mism += int(off.sum())
+        total += h.size
+    print(f"kv16 cache vs exact cache: worst distance {worst:.4f} f16 steps, {mism} of {total} values at an "
+          f"exact half-step tie of the hi + lo sum", flush=True)
+    assert worst <= 0.5

@@ -127,7 +127,7 @@ def test_f16_7b_shared_prefix_against_oracle(lh, po):
     eng.close()
 
 
-@pytest.mark.parametrize("prec", [0, 1], ids=["exact", "fast"])
+@pytest.mark.parametrize("prec", [0, 1, 2], ids=["exact", "fast", "kv16"])
 def test_f16_7b_full_length_prefix_reuse(lh, prec):
     """At the full 8192-token length: 6144 shared + 2048 own tokens, the prefix computed once and
     forked, equals each request computed from scratch (bit-exact), across several answer
