@@ -131,11 +131,11 @@ __device__ __forceinline__ void kv_put(void *pool, int64_t block, int r, int pla
 
 // Decode form: one token whose position and KV page the host already knows (kernel arguments,
 // so the only memory round trip is the q|k|v row and the table rows).  q goes out in f32.
-// Prefill form: one workgroup per attention tile (<= 32 consecutive tokens of one sequence).
-// q and k rotations are flat (token, head, pair) items dealt to the threads in rounds whose
-// loads are all issued before any is used; v is staged through LDS a few kv heads at a time
-// so that its transposed page layout is written as runs of consecutive slots instead of one
-// 4-byte store per cache line.
+// Prefill form: one workgroup per (attention tile of <= 32 consecutive tokens of one sequence,
+// part: first or second half of the q heads, the k heads, the v heads).  q and k rotations are
+// flat (token, quad of pairs) items dealt to the threads in rounds whose loads are all issued
+// before any is used; v is staged through LDS a few kv heads at a time so that its transposed
+// page layout is written as runs of consecutive slots instead of one 4-byte store per cache line.
 template <bool SPLIT, int HD>
 __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
     const float *__restrict__ qkv, int hq, KvGeom g, const float *__restrict__ cosT,
@@ -144,9 +144,10 @@ __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
     const int32_t *__restrict__ tile_pos0, const int32_t *__restrict__ tile_n,
     _Float16 *__restrict__ q16, _Float16 *__restrict__ q16lo, void *__restrict__ kpool,
     void *__restrict__ vpool, float qscale) {
-  constexpr int TT = 32, HALF = HD / 2, HB = 2;  // tokens per tile, pair offset, V heads per LDS round
-  constexpr int QB = 4;                         // tokens whose loads one round issues together
-  constexpr int TPR = kT / HD, VT = TT / TPR;   // V: token lanes per dim, tokens per thread
+  constexpr int TT = 32, HALF = HD / 2;        // tokens per tile, pair offset
+  constexpr int HB = HD == 64 ? 4 : 2;         // V heads per LDS round (32 values per thread)
+  constexpr int RI = 4;                        // rotation items whose loads one round issues together
+  constexpr int TPR = kT / HD, VT = TT / TPR;  // V: token lanes per dim, tokens per thread
   static_assert(kT % HALF == 0 && kT % HD == 0, "thread blocks must tile the head");
   __shared__ float vs[HB][TT][HD + 1];
   const int tile = blockIdx.x, tid = threadIdx.x;
@@ -158,106 +159,106 @@ __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
   auto page_base = [&](int pos) { return (pos / g.page_tokens == pg0 ? page_lo : page_hi) * g.page_stride; };
   const int plane = g.page_tokens * HD;  // values per plane of one (page, kv head) block
   const int qw = hq * HD, kvw = g.hkv * HD, rw = qw + 2 * kvw;
-  // rotations: thread -> four consecutive pairs j..j+3 of a q|k head (quad p = tid + 256 m; the
-  // quad's j is the same for every m), QB tokens per round with every load issued before any value
-  // is used; float4 loads, 8-byte stores of four f16
+  // rotations: flat items (token, quad of four consecutive pairs j..j+3 of a q|k head), quads
+  // fastest so that neighbouring threads read neighbouring 16 bytes of a row and of the tables;
+  // RI items per thread per round with every load issued before any value is used (one memory
+  // round trip per round: a 32-token tile of the d512 model's q heads is one round); float4
+  // loads, 8-byte stores of four f16
   constexpr int QPH = HALF / 4;  // quads per head
-  static_assert(kT % QPH == 0, "thread blocks must tile the quads of a head");
   // the tile's work is split over four workgroups (blockIdx.y): the first and second half of the q
   // heads, the k heads, the v heads
   const int part = blockIdx.y;
   const int h_lo = part == 0 ? 0 : part == 1 ? hq / 2 : hq, h_hi = part == 0 ? hq / 2 : part == 1 ? hq : hq + g.hkv;
   const int nquads = part < 3 ? (h_hi - h_lo) * QPH : 0;
-  const int j = (tid % QPH) * 4;
+  const int items = n * nquads;
   typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-  for (int p0 = 0; p0 < nquads; p0 += kT) {
-    const int p = p0 + tid;
-    const int hh = h_lo + min(p, nquads - 1) / QPH;
-    for (int t0 = 0; t0 < n; t0 += QB) {
-      float4 u[QB], v[QB], c0[QB], c1[QB], s0[QB], s1[QB];
+  for (int i0 = 0; i0 < items; i0 += RI * kT) {
+    float4 u[RI], v[RI], c0[RI], c1[RI], s0[RI], s1[RI];
 #pragma unroll
-      for (int b = 0; b < QB; ++b) {
-        const int tk = min(t0 + b, n - 1);
-        const float *row = qkv + int64_t(row0 + tk) * rw + hh * HD;
-        const int64_t cb = int64_t(pos0 + tk) * HD;
-        u[b] = *reinterpret_cast<const float4 *>(row + j);
-        v[b] = *reinterpret_cast<const float4 *>(row + j + HALF);
-        c0[b] = *reinterpret_cast<const float4 *>(cosT + cb + j);
-        c1[b] = *reinterpret_cast<const float4 *>(cosT + cb + j + HALF);
-        s0[b] = *reinterpret_cast<const float4 *>(sinT + cb + j);
-        s1[b] = *reinterpret_cast<const float4 *>(sinT + cb + j + HALF);
-      }
-      if (p >= nquads) continue;
+    for (int b = 0; b < RI; ++b) {
+      const int it = min(i0 + b * kT + tid, items - 1);  // past the end: a valid item, not stored
+      const int tk = it / nquads, p = it % nquads;
+      const int hh = h_lo + p / QPH, j = (p % QPH) * 4;
+      const float *row = qkv + int64_t(row0 + tk) * rw + hh * HD;
+      const int64_t cb = int64_t(pos0 + tk) * HD;
+      u[b] = *reinterpret_cast<const float4 *>(row + j);
+      v[b] = *reinterpret_cast<const float4 *>(row + j + HALF);
+      c0[b] = *reinterpret_cast<const float4 *>(cosT + cb + j);
+      c1[b] = *reinterpret_cast<const float4 *>(cosT + cb + j + HALF);
+      s0[b] = *reinterpret_cast<const float4 *>(sinT + cb + j);
+      s1[b] = *reinterpret_cast<const float4 *>(sinT + cb + j + HALF);
+    }
 #pragma unroll
-      for (int b = 0; b < QB; ++b) {
-        const int tk = t0 + b;
-        if (tk >= n) continue;
-        const float uu[4] = {u[b].x, u[b].y, u[b].z, u[b].w}, vv[4] = {v[b].x, v[b].y, v[b].z, v[b].w};
-        const float cc0[4] = {c0[b].x, c0[b].y, c0[b].z, c0[b].w}, cc1[4] = {c1[b].x, c1[b].y, c1[b].z, c1[b].w};
-        const float ss0[4] = {s0[b].x, s0[b].y, s0[b].z, s0[b].w}, ss1[4] = {s1[b].x, s1[b].y, s1[b].z, s1[b].w};
-        float a[4], c[4];
+    for (int b = 0; b < RI; ++b) {
+      const int it = i0 + b * kT + tid;
+      if (it >= items) continue;
+      const int tk = it / nquads, p = it % nquads;
+      const int hh = h_lo + p / QPH, j = (p % QPH) * 4;
+      const float uu[4] = {u[b].x, u[b].y, u[b].z, u[b].w}, vv[4] = {v[b].x, v[b].y, v[b].z, v[b].w};
+      const float cc0[4] = {c0[b].x, c0[b].y, c0[b].z, c0[b].w}, cc1[4] = {c1[b].x, c1[b].y, c1[b].z, c1[b].w};
+      const float ss0[4] = {s0[b].x, s0[b].y, s0[b].z, s0[b].w}, ss1[4] = {s1[b].x, s1[b].y, s1[b].z, s1[b].w};
+      float a[4], c[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) rope_pair(uu[e], vv[e], cc0[e], ss0[e], cc1[e], ss1[e], a[e], c[e]);
-        if (hh < hq) {
-          const int64_t at = int64_t(row0 + tk) * qw + hh * HD + j;
-          half4 ah, al, ch, cl;
+      for (int e = 0; e < 4; ++e) rope_pair(uu[e], vv[e], cc0[e], ss0[e], cc1[e], ss1[e], a[e], c[e]);
+      if (hh < hq) {
+        const int64_t at = int64_t(row0 + tk) * qw + hh * HD + j;
+        half4 ah, al, ch, cl;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
+        for (int e = 0; e < 4; ++e) {
+          _Float16 x, y;
+          split_f16(a[e] * qscale, x, y);
+          ah[e] = x;
+          al[e] = y;
+          split_f16(c[e] * qscale, x, y);
+          ch[e] = x;
+          cl[e] = y;
+        }
+        *reinterpret_cast<half4 *>(q16 + at) = ah;
+        *reinterpret_cast<half4 *>(q16 + at + HALF) = ch;
+        if (q16lo) {
+          *reinterpret_cast<half4 *>(q16lo + at) = al;
+          *reinterpret_cast<half4 *>(q16lo + at + HALF) = cl;
+        }
+      } else {
+        const int pos = pos0 + tk;
+        const int64_t blk = page_base(pos) + int64_t(hh - hq) * plane;
+        const int r = (pos % g.page_tokens) * HD + j;
+        _Float16 *kp = static_cast<_Float16 *>(kpool);
+        half4 ah, al, ch, cl;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (SPLIT) {
             _Float16 x, y;
-            split_f16(a[e] * qscale, x, y);
+            split_f16(a[e], x, y);
             ah[e] = x;
             al[e] = y;
-            split_f16(c[e] * qscale, x, y);
+            split_f16(c[e], x, y);
             ch[e] = x;
             cl[e] = y;
-          }
-          *reinterpret_cast<half4 *>(q16 + at) = ah;
-          *reinterpret_cast<half4 *>(q16 + at + HALF) = ch;
-          if (q16lo) {
-            *reinterpret_cast<half4 *>(q16lo + at) = al;
-            *reinterpret_cast<half4 *>(q16lo + at + HALF) = cl;
-          }
-        } else {
-          const int pos = pos0 + tk;
-          const int64_t blk = page_base(pos) + int64_t(hh - hq) * plane;
-          const int r = (pos % g.page_tokens) * HD + j;
-          _Float16 *kp = static_cast<_Float16 *>(kpool);
-          half4 ah, al, ch, cl;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if constexpr (SPLIT) {
-              _Float16 x, y;
-              split_f16(a[e], x, y);
-              ah[e] = x;
-              al[e] = y;
-              split_f16(c[e], x, y);
-              ch[e] = x;
-              cl[e] = y;
-            } else {
-              ah[e] = _Float16(a[e]);
-              ch[e] = _Float16(c[e]);
-            }
-          }
-          if constexpr (SPLIT) {
-            *reinterpret_cast<half4 *>(kp + 2 * blk + r) = ah;
-            *reinterpret_cast<half4 *>(kp + 2 * blk + r + HALF) = ch;
-            *reinterpret_cast<half4 *>(kp + 2 * blk + plane + r) = al;
-            *reinterpret_cast<half4 *>(kp + 2 * blk + plane + r + HALF) = cl;
           } else {
-            *reinterpret_cast<half4 *>(kp + blk + r) = ah;
-            *reinterpret_cast<half4 *>(kp + blk + r + HALF) = ch;
+            ah[e] = _Float16(a[e]);
+            ch[e] = _Float16(c[e]);
           }
+        }
+        if constexpr (SPLIT) {
+          *reinterpret_cast<half4 *>(kp + 2 * blk + r) = ah;
+          *reinterpret_cast<half4 *>(kp + 2 * blk + r + HALF) = ch;
+          *reinterpret_cast<half4 *>(kp + 2 * blk + plane + r) = al;
+          *reinterpret_cast<half4 *>(kp + 2 * blk + plane + r + HALF) = cl;
+        } else {
+          *reinterpret_cast<half4 *>(kp + blk + r) = ah;
+          *reinterpret_cast<half4 *>(kp + blk + r + HALF) = ch;
         }
       }
     }
   }
   if (part != 3) return;
   // v: HB kv heads per round staged through LDS (thread -> dim tid % HD, tokens tid / HD + TPR i),
-  // then written as runs of consecutive slots
+  // then written as runs of consecutive slots; the next round's loads are issued before this
+  // round's stores, so one memory round trip overlaps the stores of the round before
   const int dd = tid % HD, tq = tid / HD;
-  for (int h0 = 0; h0 < g.hkv; h0 += HB) {
-    const int nh = min(HB, g.hkv - h0);
-    float val[HB][VT];
+  float val[HB][VT];
+  auto load_v = [&](int h0) {
 #pragma unroll
     for (int hh = 0; hh < HB; ++hh)
 #pragma unroll
@@ -265,11 +266,16 @@ __global__ __launch_bounds__(kT) void rope_kv_tile_kernel(
         const int tk = min(tq + TPR * i, n - 1), h = min(h0 + hh, g.hkv - 1);
         val[hh][i] = qkv[int64_t(row0 + tk) * rw + qw + kvw + h * HD + dd];
       }
+  };
+  load_v(0);
+  for (int h0 = 0; h0 < g.hkv; h0 += HB) {
+    const int nh = min(HB, g.hkv - h0);
 #pragma unroll
     for (int hh = 0; hh < HB; ++hh)
 #pragma unroll
       for (int i = 0; i < VT; ++i) vs[hh][tq + TPR * i][dd] = val[hh][i];
     __syncthreads();
+    if (h0 + HB < g.hkv) load_v(h0 + HB);
     // thread -> (head, dim, four tokens) with the tokens fastest: runs of consecutive slots per dim row,
     // four slots (one 8-byte store per plane) when the quad is whole and 4-aligned in its page
     for (int i = tid; i < nh * (TT / 4) * HD; i += kT) {
