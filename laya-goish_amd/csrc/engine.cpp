@@ -295,7 +295,8 @@ void Engine::load_decoder(const Gguf &g, const lg_engine_opts &opts) {
   HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
   upload(g);
   finish_upload();
-  // KV pool: [L][npages][hkv][64][hd] elements (f32 in EXACT mode, f16 in FAST) for K, then V
+  // KV pool: [L][npages][hkv][64][hd] elements (hi/lo f16 planes in EXACT mode, f16 in KV16 and
+  // FAST) for K, then V
   int64_t pages = opts.kv_pages;
   if (pages <= 0) {
     const int64_t toks = opts.kv_tokens > 0 ? opts.kv_tokens : 65536;

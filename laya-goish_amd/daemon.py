@@ -27,7 +27,7 @@ A body with "states": [state, ...] instead of "state" is a /v1/decide/batch requ
 (src/server.rs:235-258): one result per state, every pass of every state run as GPU batches.
 
   python3 laya-goish_amd/daemon.py MODEL.gguf [--model MODEL2.gguf ...] [--default-model NAME]
-                                   [--device N] [--precision exact|fast]
+                                   [--device N] [--precision exact|kv16|fast]
 """
 from __future__ import annotations
 
@@ -311,10 +311,10 @@ def main() -> int:
                     help="another model to serve (requests select one with \"model\": NAME)")
     ap.add_argument("--default-model", default=None, metavar="NAME")
     ap.add_argument("--device", type=int, default=0)
-    ap.add_argument("--precision", choices=["exact", "fast"], default="exact")
+    ap.add_argument("--precision", choices=["exact", "kv16", "fast"], default="exact")
     ap.add_argument("--kv-tokens", type=int, default=65536)
     args = ap.parse_args()
-    prec = lh.PREC_EXACT if args.precision == "exact" else lh.PREC_FAST
+    prec = {"exact": lh.PREC_EXACT, "kv16": lh.PREC_KV16, "fast": lh.PREC_FAST}[args.precision]
     opener = lambda g: lh.Engine(g, device=args.device, kv_tokens=args.kv_tokens, precision=prec)  # noqa: E731
     try:
         reg = Registry([args.model] + args.more, args.default_model, opener)
