@@ -202,3 +202,17 @@ def test_activations_beyond_f16_range_are_reported(lh, po):
     want_l, want_a = po.Laya(po.Gguf(arr), threads=8).forward(ids, [3, 9], 0)
     assert np.isfinite(want_l).all() and np.isfinite(want_a).all()
     eng.close()
+
+
+def test_kv16_mode_is_the_exact_mode(lh):
+    """The Laya encoder keeps no KV cache, so an engine created in the kv16 mode computes exactly as the
+    exact mode does: the same option and act logits, bit for bit."""
+    img = lh.SynthImage("laya-tiny", seed=13)
+    ids = np.random.default_rng(6).integers(0, 1000, 130)
+    out = []
+    for prec in (lh.PREC_EXACT, lh.PREC_KV16):
+        eng = lh.Engine(lh.Gguf.from_bytes(img), precision=prec)
+        out.append(eng.laya_forward([(ids, [5, 9, 60, 127], 0)])[0])
+        eng.close()
+    for a, b in zip(out[0], out[1]):
+        assert np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))

@@ -196,3 +196,16 @@ def test_daemon_serves_two_models(lh, tmp_path):
                     else:
                         assert [got["answers"][qid]["probabilities"][n] for n in names] == [float(x) for x in a["probabilities"]]
         eng.close()
+
+
+def test_kv16_mode_is_the_exact_mode(lh):
+    """The OpenThai family keeps no KV cache, so an engine created in the kv16 mode computes exactly as
+    the exact mode does: the same slot logits, bit for bit."""
+    img = lh.SynthImage("openthai-tiny", seed=21)
+    ids = np.random.default_rng(5).integers(0, 960, 90)
+    out = []
+    for prec in (lh.PREC_EXACT, lh.PREC_KV16):
+        eng = lh.Engine(lh.Gguf.from_bytes(img), precision=prec)
+        out.append(eng.forward(eng.seq_create(), ids, [0, 44, 89]))
+        eng.close()
+    assert np.array_equal(out[0].view(np.uint32), out[1].view(np.uint32))
