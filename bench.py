@@ -1058,8 +1058,8 @@ def main():
         configs["C3"] = c3_decode(eng, args)
     eng.close()
     if "C3" in wanted and prec == lh.PREC_EXACT:
-        # the north star's f16 KV cache: the same decode over an f16 cache (the kv16 mode).  Reported beside
-        # the measured line only: at 24 layers of this model its logits miss the 2e-2 bar
+        # the same decode over an f16 paged KV cache (the kv16 mode).  Reported beside the measured line
+        # only: at 24 layers of this model its logits miss the 2e-2 bar
         eng = lh.Engine(g, device=0, kv_tokens=DECODE_CTX * 3 + 512, precision=lh.PREC_KV16)
         kv = c3_decode(eng, args, extras=False)
         eng.close()
