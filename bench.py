@@ -1066,7 +1066,7 @@ def main():
         configs["C3"]["kv16"] = {
             "ms_per_token": kv["ms_per_token"], "value": kv["value"], "unit": "tok/s",
             "kernel_ms_per_token": kv["kernel_ms_per_token"], "attention": kv["attention"],
-            "parity": "outside the north-star bars: decode logits up to 9.2e-2 of the largest |logit| against "
+            "parity": "outside the parity bars: decode logits up to 9.2e-2 of the largest |logit| against "
                       "2e-2, and the greedy argmax differs from the oracle at 5 of 64 steps outside the near-tie "
                       "window (tests/test_gpu_fulldepth.py, strict xfail); not the measured value",
         }

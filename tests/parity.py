@@ -10,7 +10,7 @@
   |logit| at the depths these tests run (up to 4 layers: measured 2e-6 median, 6e-5 worst row at 4
   layers of the d2048 model), so its window is 1e-4 of the largest |logit|; the fast mode (f16
   operands and cache) errs by up to ~5e-3, so its window is 2e-2; the kv16 mode (the exact mode's
-  projections over an f16 cache) takes the north-star bar and the fast mode's window.  The full-depth
+  projections over an f16 cache) takes the 2e-2 logit bar and the fast mode's window.  The full-depth
   tests derive their window from the oracle's own distance to a float64 forward.
 """
 from __future__ import annotations
@@ -33,7 +33,7 @@ def tie_window(prec: int) -> float:
 
 
 def logit_bar(prec: int) -> float:
-    """Logit bar of a precision mode: the north star's 2e-2 for the fast and kv16 modes, and for the
+    """Logit bar of a precision mode: the 2e-2 bar for the fast and kv16 modes, and for the
     exact mode a bar tight enough that an f16-only operand anywhere on the path (~1e-3) fails it."""
     return EXACT_LOGIT_REL if prec == 0 else LOGIT_REL
 

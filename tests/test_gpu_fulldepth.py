@@ -19,7 +19,7 @@ Every workload runs in the exact mode (hi/lo KV planes) and in the kv16 mode (th
 over an f16 KV cache); the 7B workloads also in the fast mode, which misses a bar (strict xfail).
 The oracle's answers are computed once per module and shared by the modes.
 
-Bars (north star): logits within 2e-2 of the largest |logit| per row, option probabilities within
+Bars: logits within 2e-2 of the largest |logit| per row, option probabilities within
 1e-3 absolute, argmax equal.  For the decode's argmax, a step whose oracle top-2 gap is below twice
 the oracle's own distance to a float64 forward of the same steps is a near-tie, and is decided
 against the float64 argmax instead.  The measured errors are printed.
@@ -55,9 +55,9 @@ def q8_full(lh, po):
 
 def out_of_bar(mode, measured):
     """A mode with an f16 KV cache (kv16: the exact projections over it; fast: f16 operands as well) misses
-    a north-star bar at full depth of these synthetic models; a strict expected failure, so a mode that
+    a parity bar at full depth of these synthetic models; a strict expected failure, so a mode that
     came within the bars would be noticed."""
-    return pytest.mark.xfail(strict=True, reason=f"{mode} mode outside the north-star bars at full depth ({measured}); "
+    return pytest.mark.xfail(strict=True, reason=f"{mode} mode outside the parity bars at full depth ({measured}); "
                                                  "the exact mode is the measured one")
 
 
