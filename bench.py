@@ -884,7 +884,7 @@ def bench_vendor_gemm(args, prec):
     """The practical f16 MFMA rate at the prefill projection shapes: torch.matmul (x[M][K] . W[N][K]^T in
     f16 with f32 accumulation, ROCm's vendor GEMM libraries) on the same GPU.  One f16 pass per product,
     so half this rate bounds a two-pass (hi/lo split) GEMM of the same shape built on the same libraries.
-    Not a path of this build: a measured anchor for the roofline fractions."""
+    Not a path of the library: a measured anchor for the roofline fractions."""
     import torch
 
     dev = torch.device("cuda:0")
@@ -918,7 +918,7 @@ def bench_vendor_gemm(args, prec):
         del a, w
     torch.backends.cuda.preferred_blas_library("cublaslt")
     return {"workload": "vendor f16 GEMM at the prefill projection shapes (torch.matmul, f16 operands, f32 "
-                        "accumulation): a measured practical MFMA rate, not part of this build's path",
+                        "accumulation): a measured practical MFMA rate, not part of the library's path",
             "peak_TFLOP/s": PEAK_F16_TFLOPS, "shapes": rows}
 
 
@@ -979,7 +979,7 @@ def main():
                          "scales FETCH_SIZE / WRITE_SIZE to bytes")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {args.gpus}); "
+        print(f"bench.py measures one GPU: the library has no multi-GPU path (asked for {args.gpus}); "
               "the workload's requests are independent, so N GPUs would each run their own batch.",
               file=sys.stderr)
         sys.exit(2)

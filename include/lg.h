@@ -146,7 +146,7 @@ typedef struct {
 } lg_model_desc;
 
 /* Replaces models::describe, src/models/mod.rs:32-64 ("ggmlc" Laya encoders and
- * "openthai_systemone"), plus this build's decoder family ("ggmlc" with laya.model_name
+ * "openthai_systemone"), plus the laya-decoder family ("ggmlc" with laya.model_name
  * "laya-decoder", which the reference does not load: named by its general.name, no aliases).
  * Errors (LG_ERR_FORMAT): "unsupported ggmlc model X", "unsupported GGUF architecture X". */
 int lg_model_describe(const lg_gguf *g, lg_model_desc *out);

@@ -13,7 +13,7 @@ struct ModelDesc {
   std::vector<std::string> aliases;
 };
 
-// models::describe, src/models/mod.rs:32-64, plus this build's decoder family ("ggmlc" with
+// models::describe, src/models/mod.rs:32-64, plus the laya-decoder family ("ggmlc" with
 // laya.model_name "laya-decoder", named by its general.name).  Throws LG_ERR_FORMAT with the
 // reference's messages for anything else.
 ModelDesc describe(const Gguf &g);

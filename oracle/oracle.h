@@ -3,8 +3,8 @@
  *
  * A plain-C restatement of the reference's CPU algorithm for the hot path,
  * in the reference's f32 operation order.  Only tests, the smoke check and the
- * bench's CPU-baseline leg may load it, and only as the checker: the product
- * path never calls into this library.
+ * bench's CPU-baseline leg may load it, and only to check (or time beside) the GPU
+ * path's results: the product path never calls into this library.
  *
  * Each function cites the reference file:line it restates.  Built with
  * -ffp-contract=off so that every multiply and add rounds separately unless the

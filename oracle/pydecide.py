@@ -1,6 +1,6 @@
 """Token-level restatement of the reference decision layer -- TEST INFRASTRUCTURE ONLY.
 
-Only tests load this module, and only as the checker of lg_decide / lg_decide_encode /
+Only tests load this module, and only to check the results of lg_decide / lg_decide_encode /
 lg_decide_scores.  It restates src/models/openthai/decision.rs over token ids:
   passes        decision.rs:140-162
   orders        decision.rs:125-139 (written as round-half-to-even of j*k/n, an independent form)

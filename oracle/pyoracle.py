@@ -1,7 +1,7 @@
 """ctypes binding of the CPU oracle (oracle/liboracle.so) -- TEST INFRASTRUCTURE ONLY.
 
-Only tests, the smoke check and the bench's CPU-baseline leg load this module, and only as
-the checker.  See oracle.h for the reference file:line each function restates.
+Only tests, the smoke check and the bench's CPU-baseline leg load this module, and only to
+check (or time beside) the GPU path's results.  See oracle.h for the reference file:line each function restates.
 """
 from __future__ import annotations
 

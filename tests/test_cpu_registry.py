@@ -26,7 +26,7 @@ def test_describe_each_family(lh, tmp_path):
                                                    ("laya.model_name", gw.STR, model)])
         d = lh.describe(lh.Gguf.open(p))
         assert (d["name"], d["family"], d["aliases"]) == (model, family, [family])
-    # this build's decoder family: named by general.name, no aliases
+    # the laya-decoder family: named by general.name, no aliases
     dec = lh.describe(lh.Gguf.from_bytes(lh.SynthImage("tiny-q8", seed=1)))
     assert dec["name"] == "laya-decoder synthetic tiny-q8" and dec["family"] == "laya-decoder"
     assert dec["aliases"] == [] and dec["release_date"] == ""
