@@ -6,7 +6,7 @@ the CPU oracle.  Bars: see tests/parity.py.
 import numpy as np
 import pytest
 
-from parity import assert_bits_equal, assert_logits_close
+from parity import assert_argmax_equal, assert_bits_equal, assert_logits_close
 
 pytestmark = pytest.mark.gpu
 
@@ -120,10 +120,11 @@ def _uncentred_q4k(nblocks, rng):
 
 @pytest.mark.parametrize("mean", [0.0, 2.0], ids=["x-zero-mean", "x-mean-2"])
 def test_q4k_two_pass_on_uncentred_blocks(lh, po, mean):
-    """The exact Q4_K GEMM (two passes over the codes plus the depth-K/32 correction) against
-    Matrix::apply on Q4_K matrices whose blocks are not zero-centred, with activations of zero and of
-    large mean (the correction's chunk sums then dominate): the 128 x 128 tiles (130 and 300 rows) and
-    the 256 x 256 kernel (16,384 rows), each within the exact mode's 1e-5 of the largest output."""
+    """The exact Q4_K GEMM (two passes over the codes plus the depth-K/32 correction) and the Q4_K GEMV
+    (A sum(x q) - B sum(x) per half sub-block) against Matrix::apply on Q4_K matrices whose blocks are not
+    zero-centred, with activations of zero and of large mean (the correction's chunk sums then dominate):
+    the GEMV (1 row), the 128 x 128 tiles (130 and 300 rows) and the 256 x 256 kernel (16,384 rows), each
+    within the exact mode's 1e-5 of the largest output."""
     rng = np.random.default_rng(31)
     img = lh.SynthImage("tiny-q4k", seed=12)
     buf = img.array().copy()
@@ -140,7 +141,7 @@ def test_q4k_two_pass_on_uncentred_blocks(lh, po, mean):
         kind, dims, raw = og.tensor(n)
         cols, rows = dims
         w = po.decode(kind, raw).reshape(rows, cols)
-        for m in (130, 300, 16384):
+        for m in (1, 130, 300, 16384):
             x = (mean + rng.standard_normal((m, cols))).astype(np.float32)
             print(f"{n} ({rows} x {cols}) m={m} x mean {mean}", flush=True)
             got = eng.matmul(n, x)
@@ -148,3 +149,49 @@ def test_q4k_two_pass_on_uncentred_blocks(lh, po, mean):
             err = assert_logits_close(got, want, rel=1e-5)
             print(f"  max err / max |out| {err:.2e}", flush=True)
     eng.close()
+
+
+def test_q4k_gemv_wide_rows(lh, po):
+    """The Q4_K GEMV at rows wider than its register prologue: K = 5120 (four words a lane, x loaded
+    ahead of the weights) and K = 9472 (down: x staged after the first words' loads, three chunk groups),
+    with and without a bias, against Matrix::apply at 1e-5 of the largest output, on the F32 epilogue of
+    lg_matmul; the fused epilogues run in the decode test of the same model."""
+    rng = np.random.default_rng(37)
+    img = lh.SynthImage("wide-q4k", seed=5)
+    og = po.Gguf(img.array())
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=1024)
+    for name in ("q.0.weight", "wo.0.weight", "mlp_wi.0.weight", "mlp_wo.0.weight"):
+        kind, dims, raw = og.tensor(name)
+        assert kind == 12
+        cols, rows = dims
+        w = po.decode(kind, raw).reshape(rows, cols)
+        for mean, bias in ((0.0, None), (1.5, rng.standard_normal(rows).astype(np.float32))):
+            x = (mean + rng.standard_normal((1, cols))).astype(np.float32)
+            got = eng.matmul(name, x, bias)
+            want = po.apply(w, x, bias, threads=16)
+            err = assert_logits_close(got, want, rel=1e-5)
+            print(f"{name} ({rows} x {cols}) x mean {mean}: max err / max |out| {err:.2e}", flush=True)
+    eng.close()
+
+
+def test_q4k_gemv_decode_wide_model(lh, po):
+    """Greedy decode on the one-layer wide Q4_K model (every layer matrix Q4_K: the q|k|v GEMV with bias,
+    o with the residual add, gate|up with SwiGLU at K = 5120, down at K = 9472), teacher-forced against the
+    oracle's KV-cached decode: logits within 1e-4 of the largest, argmax equal."""
+    img = lh.SynthImage("wide-q4k", seed=5)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=1024)
+    om = po.Model(po.Gguf(img.array()), threads=16)
+    ids = np.random.default_rng(41).integers(0, 1000, 60).astype(np.int32)
+    s = eng.seq_create()
+    eng.forward(s, ids[:-1], [], [1, 2])
+    toks, logits = eng.decode(s, int(ids[-1]), 6, want_logits=True)
+    eng.close()
+    c = om.cache(100)
+    om.prefill(c, ids[:-1], [])
+    feed = [int(ids[-1])] + [int(t) for t in toks[:-1]]
+    for i, t in enumerate(feed):
+        want = om.head(om.prefill(c, [t], [0]))
+        err = assert_logits_close(logits[i], want, rel=1e-4)
+        assert_argmax_equal(logits[i][None], want, rel=1e-4)
+        print(f"step {i}: logits rel {err:.2e}", flush=True)
+
