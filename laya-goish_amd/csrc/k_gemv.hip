@@ -581,8 +581,9 @@ void launch_e(const float *x, const DevMatrix &W, float *y, const float *bias, c
   }
 }
 
-// Q4_K: two words per lane and chunk group (four past 4096 columns), as many rows per wave as keep
-// >= 512 workgroups, at most eight words' registers (weights and scale pairs) per lane.
+// Q4_K: two words per lane and chunk group (four past 4096 columns), at most eight words' registers
+// (weights and scale pairs) per lane; rows per wave measured at the 7B decode shapes (K 3584): one
+// for SwiGLU's gate|up (two: 7% slower), two from 2048 outputs (o, q|k: 5% faster than one).
 template <int EPI, int R, int CPL>
 void launch_q4k_rc(const float *x, const DevMatrix &W, float *y, const float *bias, const float *norm_w, float eps,
                    int outputs, hipStream_t st) {
@@ -602,9 +603,8 @@ void launch_q4k_e(const float *x, const DevMatrix &W, float *y, const float *bia
   const bool glu = EPI == int(Epi::SWIGLU);
   const int outputs = glu ? W.rows / 2 : W.rows;
   const bool wide = W.cols / 32 > 128;
-  int r = outputs >= 4 * 4 * 512 ? 4 : outputs >= 4 * 2 * 512 ? 2 : 1;
-  if (wide) r = std::min(r, glu ? 1 : 2);
-  else if (glu) r = std::min(r, 2);
+  int r = glu ? 1 : outputs >= 4 * 4 * 1024 ? 4 : outputs >= 2048 ? 2 : 1;
+  if (wide) r = std::min(r, 2);
   if (wide) {
     if constexpr (EPI != int(Epi::SWIGLU)) {
       if (r == 2) return launch_q4k_rc<EPI, 2, 4>(x, W, y, bias, norm_w, eps, outputs, st);
