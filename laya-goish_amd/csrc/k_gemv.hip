@@ -572,8 +572,11 @@ void launch_e(const float *x, const DevMatrix &W, float *y, const float *bias, c
   const int outputs = EPI == int(Epi::SWIGLU) ? W.rows / 2 : W.rows;
   const int nchunk = W.cols / chunk_elems<KIND>();
   const int cpl = nchunk <= 128 ? 2 : nchunk <= 256 ? 4 : 8;
-  // rows per wave: as many as keep >= 512 workgroups (two per CU) in the grid
-  const int r = outputs >= 4 * 4 * 512 ? 4 : outputs >= 4 * 2 * 512 ? 2 : 1;
+  // rows per wave: as many as keep >= 512 workgroups (two per CU) in the grid; rows longer than one
+  // chunk group (BIGK) take at least two from 2048 outputs (7B down projection, Q6_K, K 18944: 25.5 ->
+  // 21.0 us; the d2048 shapes keep the rule, measured best at each)
+  int r = outputs >= 4 * 4 * 512 ? 4 : outputs >= 4 * 2 * 512 ? 2 : 1;
+  if (nchunk > 64 * cpl && r == 1 && outputs >= 2048) r = 2;
   switch (r) {
     case 4: launch_r<KIND, EPI, 4>(cpl, x, W, y, bias, norm_w, eps, outputs, st); break;
     case 2: launch_r<KIND, EPI, 2>(cpl, x, W, y, bias, norm_w, eps, outputs, st); break;
