@@ -359,12 +359,49 @@ def load_entry(eng):
             "GB_per_s": round(info["weight_bytes"] / sec / 1e9, 2) if sec > 0 else None}
 
 
+def q4k_decode(eng, ids, args, steps=32):
+    """Batch-1 greedy decode on the C4 model after one of its 1024-token requests: the dequant-fused Q4_K
+    and Q6_K GEMVs (q|k, o, gate|up Q4_K; v, down, head Q6_K) and the GQA-7 decode attention.  Reported
+    beside the prefill line (the configuration is a prefill one)."""
+    base = eng.seq_create()
+    eng.forward(base, ids, [], None)
+    first = int(ids[-1])
+    times = []
+    for mode in ("warm", "timed", "profiled"):
+        s = eng.seq_fork(base, len(ids))
+        if mode == "profiled":
+            eng.profile_reset()
+            eng.profile(True)
+        eng.sync()
+        t0 = time.perf_counter()
+        toks = eng.decode(s, first, steps)
+        eng.sync()
+        times.append(time.perf_counter() - t0)
+        if mode == "profiled":
+            eng.profile(False)
+        eng.seq_free(s)
+    eng.seq_free(base)
+    assert (toks >= 0).all()
+    dt = times[1]
+    gv, at = eng.profile_read("gemv"), eng.profile_read("attn_decode")
+    log(f"C4 decode: {dt / steps * 1e3:.3f} ms/token, gemv {rate(gv, 'bytes'):.0f} GB/s over {gv['launches']} launches, "
+        f"attention {rate(at, 'bytes'):.0f} GB/s")
+    return {
+        "workload": f"batch-1 greedy decode on the same model: {len(ids)}-token context, {steps} steps",
+        "value": round(steps / dt, 2), "unit": "tok/s", "ms_per_token": round(dt / steps * 1e3, 4),
+        "roofline": roofline("hbm", rate(gv, "bytes"), PEAK_HBM_GBS, "GB/s",
+                             "gemv (dequant-fused Q4_K and Q6_K GEMVs, GGUF bytes per launch)", gv["launches"],
+                             gv["ms"] / max(1, gv["launches"])),
+        "kernel_ms_per_token": {"gemv": round(gv["ms"] / steps, 4), "attn_decode": round(at["ms"] / steps, 4)},
+    }
+
+
 def c4_q4k(args, prec, layer_cost):
     """Q4_K/Q6_K 7B shape (28 layers, d3584, GQA 28/4 x 128, FFN 18944, vocab 152064, QKV bias):
     a batch of 32 requests x 1024 tokens, 4 option tokens scored at the last position."""
     t0 = time.perf_counter()
     img = lh.SynthImage("q4km-7b", seed=SEED)
-    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=Q4K_REQS * Q4K_TOKENS + 1024, max_batch_tokens=32768,
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=Q4K_REQS * Q4K_TOKENS + 2048, max_batch_tokens=32768,
                     precision=prec)
     load = load_entry(eng)
     log(f"C4 model ready in {time.perf_counter() - t0:.1f}s (engine load {load['seconds']} s, "
@@ -389,6 +426,7 @@ def c4_q4k(args, prec, layer_cost):
     eng.profile(False)
     prof = {c: eng.profile_read(c) for c in ("gemm", "ksum", "attn_prefill", "rope_kv", "rmsnorm", "head")}
     assert np.isfinite(out[1]).all()
+    decode = q4k_decode(eng, reqs[0][0], args)
     eng.close()
     T = Q4K_REQS * Q4K_TOKENS
     gp = prof["gemm"]
@@ -408,6 +446,7 @@ def c4_q4k(args, prec, layer_cost):
                              traffic_source="profiles/hbm_traffic_q4km-7b_prefill.md (FETCH_SIZE + WRITE_SIZE, "
                                             "copy-calibrated)"),
         "kernel_ms_per_step": {c: round(p["ms"], 3) for c, p in prof.items()},
+        "decode": decode,
     }
     if layer_cost:
         entries = []
