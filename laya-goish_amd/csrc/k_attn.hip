@@ -447,7 +447,10 @@ __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, 
                                                  typename KvFmt<KV>::elem *__restrict__ kpool,
                                                  typename KvFmt<KV>::elem *__restrict__ vpool,
                                                  const int32_t *__restrict__ pages, float *pbase,
-                                                 int64_t hstride);
+                                                 int64_t hstride, int kh, int qh0);
+// Grid (np + 1, hkv * split): workgroup row y serves query heads y * GRP .. y * GRP + GRP - 1 of kv head
+// y / split (split = query heads per kv head / GRP: a kv head's group of query heads dealt over `split`
+// workgroups when the grid would otherwise be too small to fill the part).
 template <int HD, int GRP, typename KV>
 __global__ __launch_bounds__(256) void attn_decode_kernel(const float *__restrict__ qkv, int hq, KvGeom g,
                                                           const float *__restrict__ cosT,
@@ -455,16 +458,16 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const float *__restric
                                                           typename KvFmt<KV>::elem *__restrict__ kpool,
                                                           typename KvFmt<KV>::elem *__restrict__ vpool,
                                                           const int32_t *__restrict__ pages, int max_pages,
-                                                          float *__restrict__ part) {
+                                                          float *__restrict__ part, int split) {
   static_assert(HD == 64 || HD == 128, "decode attention is written for head_dim 64 and 128");
-  const int pi = blockIdx.x, kh = blockIdx.y;
+  const int pi = blockIdx.x, kh = blockIdx.y / split, qh0 = blockIdx.y * GRP;
   if (pi == pos / P + 1) {  // the extra column: store the new token's k and v, read no page
-    store_new_kv<HD, KV>(qkv, hq, g, cosT, sinT, pos, kpool, vpool, pages, kh);
+    if (blockIdx.y % split == 0) store_new_kv<HD, KV>(qkv, hq, g, cosT, sinT, pos, kpool, vpool, pages, kh);
     return;
   }
-  float *pbase = part + (int64_t(kh * GRP) * max_pages + pi) * (2 + HD);
+  float *pbase = part + (int64_t(qh0) * max_pages + pi) * (2 + HD);
   const int64_t hstride = int64_t(max_pages) * (2 + HD);
-  attn_decode_page<HD, GRP, KV>(qkv, hq, g, cosT, sinT, pos, kpool, vpool, pages, pbase, hstride);
+  attn_decode_page<HD, GRP, KV>(qkv, hq, g, cosT, sinT, pos, kpool, vpool, pages, pbase, hstride, kh, qh0);
 }
 
 // Combine launch: one 256-thread workgroup per query head h: out = sum_i w_i out_i / sum_i w_i sum_i
@@ -537,7 +540,7 @@ __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, 
                                                  typename KvFmt<KV>::elem *__restrict__ kpool,
                                                  typename KvFmt<KV>::elem *__restrict__ vpool,
                                                  const int32_t *__restrict__ pages, float *pbase,
-                                                 int64_t hstride) {
+                                                 int64_t hstride, int kh, int qh0) {
   using T = typename KvFmt<KV>::elem;
   constexpr int NPL = KvFmt<KV>::NPL;
   constexpr int E = 16 / sizeof(T);           // values per 16-byte word: 4 (f32) or 8 (f16 planes)
@@ -548,7 +551,7 @@ __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, 
   constexpr int NQP = (GRP * HALF + 255) / 256;  // rotation pairs per thread
   static_assert(LPK == 8 || LPK == 16 || LPK == 32, "key rows span 8, 16 or 32 lanes");
   static_assert(LPD == 8 || LPD == 16, "dim columns span 8 or 16 lanes");
-  const int pi = blockIdx.x, kh = blockIdx.y;
+  const int pi = blockIdx.x;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int len = pos + 1;
   const int64_t page = pages[pi];
@@ -564,7 +567,7 @@ __device__ __forceinline__ void attn_decode_page(const float *__restrict__ qkv, 
   for (int e = 0; e < NQP; ++e) {
     const int idx = min(t + 256 * e, GRP * HALF - 1);
     const int gq = idx / HALF, j = idx % HALF;
-    const float *qr = qkv + (kh * GRP + gq) * HD;
+    const float *qr = qkv + (qh0 + gq) * HD;
     qu[e] = qr[j];
     qv[e] = qr[j + HALF];
     c0[e] = cs[j];
@@ -790,25 +793,32 @@ void launch_attn_decode(const float *qkv, int hq, const KvGeom &g, const float *
   LG_REQUIRE(np <= max_pages, "decode attention: context exceeds the page table");
   LG_REQUIRE(np <= 1024, "decode attention: context of %d pages exceeds the combine stage", np);
   const int grp = hq / g.hkv;
-  const dim3 grid(np + 1, g.hkv), block(256);  // column np stores the new token
+  // a grid of few (page, kv head) workgroups (short contexts, few kv heads: 68 at 1024 tokens of the 7B
+  // shape) cannot keep the part busy: then each workgroup serves one query head, `grp` per page and kv
+  // head (their page reads meet in the caches); every query head's arithmetic is the same either way
+  // (group sizes without their own instance always take this form)
+  const bool inst = grp == 1 || grp == 2 || grp == 4 || grp == 7 || grp == 8;
+  const bool by_head = grp > 1 && (!inst || int64_t(np + 1) * g.hkv < 512);
+  const int gsel = by_head ? 1 : grp, split = by_head ? grp : 1;
+  const dim3 grid(np + 1, g.hkv * split), block(256);  // column np stores the new token
 #define CASE(HDV, G)                                                                                     \
   case G:                                                                                                \
     if (g.split)                                                                                         \
       hipLaunchKernelGGL((attn_decode_kernel<HDV, G, SplitKV>), grid, block, 0, st, qkv, hq, g, cosT, sinT, \
                          pos, static_cast<_Float16 *>(kpool), static_cast<_Float16 *>(vpool), pages,    \
-                         max_pages, part);                                                               \
+                         max_pages, part, split);                                                        \
     else                                                                                                 \
       hipLaunchKernelGGL((attn_decode_kernel<HDV, G, _Float16>), grid, block, 0, st, qkv, hq, g, cosT,    \
                          sinT, pos, static_cast<_Float16 *>(kpool), static_cast<_Float16 *>(vpool), pages, \
-                         max_pages, part);                                                               \
+                         max_pages, part, split);                                                        \
     break;
   if (g.hd == 128) {
-    switch (grp) {
+    switch (gsel) {
       CASE(128, 1) CASE(128, 2) CASE(128, 4) CASE(128, 7) CASE(128, 8)
       default: fail(LG_ERR_UNSUPPORTED, "decode attention: group size %d not supported", grp);
     }
   } else {
-    switch (grp) {
+    switch (gsel) {
       CASE(64, 1) CASE(64, 2) CASE(64, 4) CASE(64, 7) CASE(64, 8)
       default: fail(LG_ERR_UNSUPPORTED, "decode attention: group size %d not supported", grp);
     }
