@@ -111,6 +111,9 @@ const Preset kPresets[] = {
      LG_Q6_K, LG_Q4_K, LG_Q4_K, LG_Q4_K, LG_Q6_K, LG_Q6_K, true, false, true, false, 0.02},
     {"tiny-f16-128", 2, 512, 4, 2, 128, 512, 1024, 512, 1e-5, 1e4, LG_F16, LG_F32, LG_F16, LG_F16,
      LG_F16, LG_F16, LG_F16, LG_F16, LG_F16, LG_F16, true, true, true, false, 0.03},
+    // tiny-f16 with a RoPE table past the decode attention's 65,536 tokens (its longest-context test)
+    {"tiny-long", 2, 256, 4, 2, 64, 512, 512, 65600, 1e-5, 1e4, LG_F16, LG_F32, LG_F16, LG_F16,
+     LG_F16, LG_F16, LG_F16, LG_F16, LG_F16, LG_F16, true, true, true, false, 0.05},
     // Q4_K rows wider than the decode GEMV's register prologue: K 5120 (q, k, v, o, gate, up) and
     // 9472 (down), GQA 40/5, one layer.
     {"wide-q4k", 1, 5120, 40, 5, 128, 9472, 1024, 512, 1e-6, 1e6, LG_F16, LG_F32, LG_Q4_K, LG_Q4_K,

@@ -417,3 +417,34 @@ def test_kv16_cache_holds_the_exact_values_rounded(lh):
     print(f"kv16 cache vs exact cache: worst distance {worst:.4f} f16 steps, {mism} of {total} values at an "
           f"exact half-step tie of the hi + lo sum", flush=True)
     assert worst <= 0.5
+
+
+def test_decode_at_the_combine_limit(lh):
+    """Decode at the longest context the decode attention combines (1024 pages of 64 = 65,536 tokens): the
+    step at position 65,535 gives the logits the prefill path gives at that position (within 1e-4 of the
+    largest |logit|: the two paths sum in different orders; both are checked against the oracle at smaller
+    sizes), and a step that would open a 1025th page is refused before any page is reserved."""
+    img = lh.SynthImage("tiny-long", seed=7)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=2 * 65536 + 512, max_batch_tokens=65536)
+    ids = np.random.default_rng(19).integers(0, eng.info["vocab"], 65536).astype(np.int32)
+    a, b = eng.seq_create(), eng.seq_create()
+    print("tiny-long: 65,535-token prefill, one decode step at position 65,535", flush=True)
+    eng.forward(a, ids[:-1], [], OPTIONS)
+    toks, logits = eng.decode(a, int(ids[-1]), 1, want_logits=True)
+    want = eng.forward(b, ids, [65535])
+    err = assert_logits_close(logits, want, rel=1e-4)
+    assert_argmax_equal(logits, want, rel=1e-4)
+    print(f"decode at 1024 pages against prefill: logits rel {err:.2e}", flush=True)
+    assert eng.seq_len(a) == 65536
+    with pytest.raises(lh.LayaError) as e:
+        eng.decode(a, int(toks[0]), 1)
+    assert e.value.kind == "INVALID" and "65536" in str(e.value)
+    assert eng.seq_len(a) == 65536
+    # the refused step reserved nothing: the pool's last 8 pages (2056 - 2 x 1024) still take 500 tokens
+    assert eng.info["kv_pages"] == 2056
+    c = eng.seq_create()
+    eng.forward(c, ids[:500], [], OPTIONS)
+    for q in (a, b, c):
+        eng.seq_free(q)
+    eng.close()
+
