@@ -235,6 +235,10 @@ def test_errors_are_reported(pair, lh):
     with pytest.raises(lh.LayaError) as e:
         eng.forward(s, [1, 2], [1], OPTIONS, cancel=lambda _: 1)
     assert e.value.kind == "CANCELED"
+    with pytest.raises(lh.LayaError) as e:  # an empty request is refused, not run
+        eng.forward(s, np.zeros(0, np.int32), [], OPTIONS)
+    assert e.value.kind == "INVALID" and "empty" in str(e.value)
+    assert eng.seq_len(s) == 0
     # the engine stays usable after errors
     out = eng.forward(eng.seq_create(), [1, 2, 3], [2], OPTIONS)
     assert np.isfinite(out).all()
