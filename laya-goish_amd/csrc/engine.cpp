@@ -752,9 +752,8 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
   const bool ot = arch == Arch::OpenThai, fresh = fresh_only();
   try {
     std::vector<int32_t> ids, tseq, tpos, tpage, tiles_s, tiles_r, tiles_p, tiles_n, gather, grp_f, grp_c, srow0, sn;
-    const int gtiles = arch == Arch::Decoder ? attn_prefill_group_tiles(hq, hkv) : 4;
     std::vector<int32_t> it_r, it_p, it_n, it_lo, it_hi, cb_r, cb_n, cb_f, cb_c;
-    int max_pages = 0;
+    int max_pages = 0, max_len = 0;  // max_len: the longest sequence of the batch once its tokens are in
     for (int r = 0; r < nreq; ++r) {
       const lg_request &q = reqs[r];
       Seq &s = seq(q.seq);
@@ -771,7 +770,10 @@ BatchPlan *Engine::batch_create(const lg_request *reqs, int nreq) {
              r, q.seq, s.len);
       if (s.len + q.n > ctx) fail(LG_ERR_INVALID, "request %d: %d tokens exceed the context length %d", r, s.len + q.n, ctx);
       if (!fresh) max_pages = std::max(max_pages, (s.len + q.n + 63) / 64);
+      max_len = std::max(max_len, s.len + q.n);
     }
+    const int gtiles = arch == Arch::Decoder ? attn_prefill_group_tiles(hq, hkv, max_len) : 4;
+    b->gtiles = gtiles;
     const int64_t T = std::accumulate(reqs, reqs + nreq, int64_t(0), [](int64_t a, const lg_request &q) { return a + q.n; });
     if (T > max_batch_tokens_) fail(LG_ERR_INVALID, "batch of %lld tokens exceeds max_batch_tokens %lld", (long long)T, (long long)max_batch_tokens_);
     // reserve pages (all or nothing)
@@ -969,7 +971,7 @@ void Engine::run_layers_prefill(BatchPlan &b, lg_cancel_fn cancel, void *arg) {
     prof.begin("attn_prefill", stream);
     launch_attn_prefill(q16, q16lo, T, hq, g, kpool(l), vpool(l), b.pages, b.max_pages, b.tile_seq,
                         b.tile_row0, b.tile_pos0, b.tile_n, b.ntiles, b.grp_first, b.grp_count,
-                        b.ngroups, att, attlo, stream);
+                        b.ngroups, b.gtiles, att, attlo, stream);
     prof.end(0, 0, stream);
     gemm(att, attlo, T, ly.wo, Epi::ADD, x, nullptr, nullptr, d, nullptr);
     prof.begin("rmsnorm", stream);

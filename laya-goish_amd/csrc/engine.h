@@ -90,7 +90,8 @@ struct BatchPlan {
   int32_t *ids = nullptr, *tok_seq = nullptr, *tok_pos = nullptr, *pages = nullptr;
   int32_t *tok_page = nullptr;  // per batch row: the page its position falls in
   int32_t *tile_seq = nullptr, *tile_row0 = nullptr, *tile_pos0 = nullptr, *tile_n = nullptr;
-  int ngroups = 0;              // runs of <= 4 consecutive tiles of one sequence
+  int ngroups = 0;              // runs of <= gtiles consecutive tiles of one sequence
+  int gtiles = 0;               // attention tiles per group (attn_prefill_group_tiles)
   int32_t *grp_first = nullptr, *grp_count = nullptr;
   int32_t *gather = nullptr;
   int32_t *seq_row0 = nullptr, *seq_n = nullptr;  // first batch row and token count per request

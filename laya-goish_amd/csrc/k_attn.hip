@@ -82,8 +82,12 @@ __device__ __forceinline__ half8 lds_half8(const unsigned char *base, int slot) 
   return *reinterpret_cast<const half8 *>(base + slot * 16);
 }
 
-template <int HD, int NQ, int NKV, int W, int GB>
-__global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
+// STG: LDS stages of K/V pages.  2: page kt + 1 is in flight while page kt is consumed (one workgroup of
+// up to 8 waves per CU: 128 KiB of LDS at head_dim 128).  1: each page is loaded, then consumed, and
+// two workgroups of 4 waves share a CU, one computing while the other waits for its page (the short
+// sequences, where a workgroup's start and its few pages' waits dominate).
+template <int HD, int NQ, int NKV, int W, int GB, int STG>
+__global__ __launch_bounds__(64 * W, STG == 1 ? 2 : 1) void attn_prefill_kernel(
     const _Float16 *__restrict__ q16, const _Float16 *__restrict__ q16lo, int hq, KvGeom g,
     const _Float16 *__restrict__ kpool, const _Float16 *__restrict__ vpool, const int32_t *__restrict__ pages,
     int max_pages, const int32_t *__restrict__ grp_first, const int32_t *__restrict__ grp_count,
@@ -94,7 +98,8 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
   using S = PrefillStage<HD, NKV>;
   constexpr int NC = HD / 32, DB = HD / 16;  // 32-deep chunks of the head dim, 16-dim output blocks
   constexpr int NI = (S::BLOCKS + W - 1) / W;  // LDS-DMA instructions per wave per page
-  __shared__ __align__(16) unsigned char lds[2 * S::BYTES];
+  static_assert(STG == 1 || STG == 2, "one or two LDS stages");
+  __shared__ __align__(16) unsigned char lds[STG * S::BYTES];
 
   // XCD-contiguous mapping: workgroups are dealt to the 8 XCDs round-robin (i -> XCD i % 8);
   // each XCD takes one contiguous range of (head block, tile group) pairs, groups fastest, so
@@ -190,8 +195,8 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   for (int kt = 0; kt < npages; ++kt) {
-    const int st = kt & 1;
-    if (kt + 1 < npages) {
+    const int st = STG == 2 ? kt & 1 : 0;
+    if (STG == 2 && kt + 1 < npages) {
       const int32_t page = next_page;
       next_page = ptab[min(kt + 2, npages - 1)];
       issue(page, st ^ 1);
@@ -337,6 +342,12 @@ __global__ __launch_bounds__(64 * W) void attn_prefill_kernel(
           }
         }
       }
+    }
+    if (STG == 1 && kt + 1 < npages) {  // every wave is done with the stage: load page kt + 1 into it
+      __syncthreads();
+      const int32_t page = next_page;
+      next_page = ptab[min(kt + 2, npages - 1)];
+      issue(page, 0);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of page kt + 1 has landed
     __syncthreads();
@@ -733,16 +744,21 @@ PrefillShape prefill_shape(int G) {
     default: return {1, 8};
   }
 }
+// Sequences up to this long take the single-stage form for one query head per kv head (MHA): groups of
+// 4 tiles, 4 waves, two workgroups per CU.
+constexpr int kShortSeq = 1024;
 }  // namespace
 
-int attn_prefill_group_tiles(int hq, int hkv) { return prefill_shape(hq / hkv).t; }
+int attn_prefill_group_tiles(int hq, int hkv, int max_len) {
+  return hq == hkv && max_len <= kShortSeq ? 4 : prefill_shape(hq / hkv).t;
+}
 
 void launch_attn_prefill(const _Float16 *q16, const _Float16 *q16_lo, int T, int hq,
                          const KvGeom &g, const void *kpool, const void *vpool,
                          const int32_t *pages, int max_pages, const int32_t *tile_seq,
                          const int32_t *tile_row0, const int32_t *tile_pos0,
                          const int32_t *tile_n, int ntiles, const int32_t *grp_first,
-                         const int32_t *grp_count, int ngroups, _Float16 *out16,
+                         const int32_t *grp_count, int ngroups, int group_tiles, _Float16 *out16,
                          _Float16 *out16_lo, hipStream_t st) {
   LG_REQUIRE(g.page_tokens == P, "attention: page size must be %d", P);
   LG_REQUIRE(g.hkv > 0 && hq % g.hkv == 0, "attention: hq %% hkv != 0");
@@ -752,22 +768,28 @@ void launch_attn_prefill(const _Float16 *q16, const _Float16 *q16_lo, int T, int
   LG_REQUIRE(!split || out16_lo, "attention: split path needs the lo output plane");
   LG_REQUIRE(grp_first && grp_count && ngroups > 0 && ngroups <= ntiles, "attention: bad tile groups");
   const int G = hq / g.hkv;
-  const PrefillShape sh = prefill_shape(G);
+  const bool single = G == 1 && group_tiles == 4;  // attn_prefill_group_tiles' short-sequence form
+  const PrefillShape sh = single ? PrefillShape{1, 4} : prefill_shape(G);
+  LG_REQUIRE(group_tiles == sh.t, "attention: groups of %d tiles, kernel shape of %d", group_tiles, sh.t);
   const int64_t nwg = int64_t(ngroups) * g.hkv * (G / sh.gb);
   LG_REQUIRE(nwg < (1ll << 31), "attention: too many tiles");
   const dim3 grid{static_cast<uint32_t>(nwg)}, block{static_cast<uint32_t>(64 * sh.gb * sh.t)};
   const _Float16 *kp = static_cast<const _Float16 *>(kpool), *vp = static_cast<const _Float16 *>(vpool);
-#define LAUNCH(HDV, NQV, NKVV, WV, GBV)                                                                   \
-  hipLaunchKernelGGL((attn_prefill_kernel<HDV, NQV, NKVV, WV, GBV>), grid, block, 0, st, q16, q16_lo, hq, g, kp, vp, \
+#define LAUNCH(HDV, NQV, NKVV, WV, GBV, STGV)                                                             \
+  hipLaunchKernelGGL((attn_prefill_kernel<HDV, NQV, NKVV, WV, GBV, STGV>), grid, block, 0, st, q16, q16_lo, hq, g, kp, vp, \
                      pages, max_pages, grp_first, grp_count, tile_seq, tile_row0, tile_pos0, tile_n, out16,    \
                      out16_lo)
-#define SHAPES(HDV, NQV, NKVV)                   \
-  switch (sh.gb) {                               \
-    case 2: LAUNCH(HDV, NQV, NKVV, 8, 2); break; \
-    case 4: LAUNCH(HDV, NQV, NKVV, 8, 4); break; \
-    case 7: LAUNCH(HDV, NQV, NKVV, 7, 7); break; \
-    case 8: LAUNCH(HDV, NQV, NKVV, 8, 8); break; \
-    default: LAUNCH(HDV, NQV, NKVV, 8, 1); break; \
+#define SHAPES(HDV, NQV, NKVV)                                                 \
+  if (single) {                                                                \
+    LAUNCH(HDV, NQV, NKVV, 4, 1, 1);                                           \
+  } else {                                                                     \
+    switch (sh.gb) {                                                           \
+      case 2: LAUNCH(HDV, NQV, NKVV, 8, 2, 2); break;                          \
+      case 4: LAUNCH(HDV, NQV, NKVV, 8, 4, 2); break;                          \
+      case 7: LAUNCH(HDV, NQV, NKVV, 7, 7, 2); break;                          \
+      case 8: LAUNCH(HDV, NQV, NKVV, 8, 8, 2); break;                          \
+      default: LAUNCH(HDV, NQV, NKVV, 8, 1, 2); break;                         \
+    }                                                                          \
   }
   if (g.hd == 128) {
     if (g.split) { SHAPES(128, 2, 2) } else if (split) { SHAPES(128, 2, 1) } else { SHAPES(128, 1, 1) }

@@ -199,16 +199,17 @@ void launch_rope_kv_tiles(const float *qkv, int hq, const KvGeom &g, const float
 // q16_lo != nullptr selects the split-precision path, over the split cache (g.split) or an f16
 // one; the output is then written as hi/lo planes (out16, out16_lo).  f16 queries need the f16
 // cache.  Tiles go in groups (grp_first[i],
-// grp_count[i] for i < ngroups) of at most attn_prefill_group_tiles(hq, hkv) consecutive tiles
-// of one sequence; each group's workgroups share every K/V page through LDS.  head_dim 64 or 128.
+// grp_count[i] for i < ngroups) of at most group_tiles = attn_prefill_group_tiles(hq, hkv, max_len)
+// consecutive tiles of one sequence (max_len: the longest sequence of the batch, its own tokens
+// included); each group's workgroups share every K/V page through LDS.  head_dim 64 or 128.
 // A query's output does not depend on which group or batch its tile is in.
-int attn_prefill_group_tiles(int hq, int hkv);
+int attn_prefill_group_tiles(int hq, int hkv, int max_len);
 void launch_attn_prefill(const _Float16 *q16, const _Float16 *q16_lo, int T, int hq,
                          const KvGeom &g, const void *kpool, const void *vpool,
                          const int32_t *pages, int max_pages, const int32_t *tile_seq,
                          const int32_t *tile_row0, const int32_t *tile_pos0,
                          const int32_t *tile_n, int ntiles, const int32_t *grp_first,
-                         const int32_t *grp_count, int ngroups, _Float16 *out16,
+                         const int32_t *grp_count, int ngroups, int group_tiles, _Float16 *out16,
                          _Float16 *out16_lo, hipStream_t st);
 
 // Decode attention for one new token at position pos of one sequence: q|k|v row `qkv` (before
