@@ -166,3 +166,31 @@ def test_truncation_at_every_byte(lh, po):
     for n in range(len(data)):
         m1, m2 = _open_both(lh, po, data[:n])
         assert m1 is not None and m1 == m2, (n, m1, m2)
+
+
+def test_random_mutations_read_alike(lh, po):
+    """4000 seeded mutations of a valid file (one to three byte overwrites, bit flips, deletions or
+    insertions each): the engine's reader and the oracle's accept the same files and reject the rest
+    with the same message, and neither crashes on any of them."""
+    import random
+    base = _mk()
+    rng = random.Random(20261202)
+    accepted, seen = 0, set()
+    for i in range(4000):
+        d = bytearray(base)
+        for _ in range(rng.randint(1, 3)):
+            op, p = rng.random(), rng.randrange(len(d))
+            if op < 0.5:
+                d[p] = rng.randrange(256)
+            elif op < 0.8:
+                d[p] ^= 1 << rng.randrange(8)
+            elif op < 0.9:
+                del d[p]
+            else:
+                d.insert(p, rng.randrange(256))
+        m1, m2 = _open_both(lh, po, bytes(d))
+        assert m1 == m2, (i, m1, m2)
+        accepted += m1 is None
+        seen.add(m1)
+    # the mutations reach acceptance and at least eight distinct rejections
+    assert 0 < accepted < 4000 and len(seen) >= 9, (accepted, sorted(map(str, seen)))
