@@ -17,8 +17,8 @@
 // The split modes reproduce f32 arithmetic to ~2^-22 relative per product, which the
 // ill-conditioned synthetic workloads need to stay within the parity bars.
 //
-// Geometry: 256 threads = 4 wave64s in a 2 x 2 arrangement; each wave owns a (32 WTM) x (32 WTN)
-// tile, (2 WTM) x (2 WTN) MFMA blocks of 16 x 16, so a workgroup tile is (64 WTM) x (64 WTN) x BK.  STAGES = 2 ping-pongs
+// Geometry: 256 threads = 4 wave64s in a 2 x 2 arrangement; each wave owns a (16 HM) x (16 HN)
+// tile, HM x HN MFMA blocks of 16 x 16, so a workgroup tile is (32 HM) x (32 HN) x BK.  STAGES = 2 ping-pongs
 // two LDS buffers (one barrier per K step, next tile's global loads in flight during the
 // MFMAs); STAGES = 1 uses one buffer with the next tile prefetched into registers.
 #pragma once
@@ -316,16 +316,16 @@ struct ALoad {
 //           the -B 2^e planes) and multiplies acc by 2^-e per column
 //   SPLIT3: acc += A_hi.W_hi, acc += A_lo.W_hi, acc += A_hi.W_lo
 // gemm_wide.h keeps the same sequences, so both tilings give the same bits.
-template <uint32_t KIND, int MODE, int BK, int WTM, int WTN, int LDK>
-__device__ __forceinline__ void mma_tile(f32x4 (&acc)[2 * WTM][2 * WTN], const _Float16 *As, const _Float16 *Al,
+template <uint32_t KIND, int MODE, int BK, int HM, int HN, int LDK>
+__device__ __forceinline__ void mma_tile(f32x4 (&acc)[HM][HN], const _Float16 *As, const _Float16 *Al,
                                          const _Float16 *Bs, const _Float16 *Bl, const float *Ds, int wm,
                                          int wn, int lane) {
   constexpr bool kSplitA = MODE != FAST;
   constexpr bool kSplitB = MODE == SPLIT3;
   constexpr bool kScaled = MODE == SPLIT && (KIND == LG_Q8_0 || KIND == LG_Q4_K);
-  constexpr int MI = 2 * WTM, NJ = 2 * WTN;
-  const int arow = (wm * (32 * WTM) + (lane & 15)) * LDK;
-  const int brow = (wn * (32 * WTN) + (lane & 15)) * LDK;
+  constexpr int MI = HM, NJ = HN;
+  const int arow = (wm * (16 * HM) + (lane & 15)) * LDK;
+  const int brow = (wn * (16 * HN) + (lane & 15)) * LDK;
   const int kl = (lane >> 4) * 8;
   const f32x4 zero = {};
 #pragma unroll
@@ -345,7 +345,7 @@ __device__ __forceinline__ void mma_tile(f32x4 (&acc)[2 * WTM][2 * WTN], const _
     if constexpr (kScaled) {
       float dj[NJ];
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) dj[j] = Ds[(wn * (32 * WTN) + j * 16 + (lane & 15)) * (BK / 32) + blk];
+      for (int j = 0; j < NJ; ++j) dj[j] = Ds[(wn * (16 * HN) + j * 16 + (lane & 15)) * (BK / 32) + blk];
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
 #pragma unroll
@@ -368,9 +368,9 @@ __device__ __forceinline__ void mma_tile(f32x4 (&acc)[2 * WTM][2 * WTN], const _
   }
 }
 
-template <int MODE, int BK, int WTM, int WTN, int STAGES>
+template <int MODE, int BK, int HM, int HN, int STAGES>
 struct Cfg {
-  static constexpr int kBM = 64 * WTM, kBN = 64 * WTN;
+  static constexpr int kBM = 32 * HM, kBN = 32 * HN;
   static constexpr int kLDK = BK + 8;  // 16-byte row pad: conflict-free b128 LDS reads
   static constexpr bool kSplitA = MODE != FAST;
   static constexpr bool kSplitB = MODE == SPLIT3;
@@ -382,15 +382,15 @@ struct Cfg {
 };
 
 // LDS of one launch: a two-pass Q4_K launch's correction stages four planes (SPLIT3) in the same space.
-template <uint32_t KIND, int MODE, int BK, int WTM, int WTN, int STAGES>
+template <uint32_t KIND, int MODE, int BK, int HM, int HN, int STAGES>
 constexpr int lds_bytes() {
-  constexpr int main = Cfg<MODE, BK, WTM, WTN, STAGES>::kLdsBytes;
-  constexpr int corr = Cfg<SPLIT3, BK, WTM, WTN, 1>::kStageBytes;
+  constexpr int main = Cfg<MODE, BK, HM, HN, STAGES>::kLdsBytes;
+  constexpr int corr = Cfg<SPLIT3, BK, HM, HN, 1>::kStageBytes;
   return KIND == LG_Q4_K && MODE == SPLIT && corr > main ? corr : main;
 }
 
 // ks / kslo: the chunk-sum planes of a two-pass Q4_K launch ([M][W.pkp] each), unused otherwise.
-template <uint32_t KIND, int EPI, int MODE, int BK, int WTM, int WTN, int STAGES>
+template <uint32_t KIND, int EPI, int MODE, int BK, int HM, int HN, int STAGES>
 __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ A,
                                                    const _Float16 *__restrict__ Alo, int M, int K,
                                                    DevMatrix W, float *__restrict__ C,
@@ -399,11 +399,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
                                                    const float *__restrict__ bias, int MT, int NT,
                                                    int ffn, const _Float16 *__restrict__ ks,
                                                    const _Float16 *__restrict__ kslo) {
-  using CF = Cfg<MODE, BK, WTM, WTN, STAGES>;
+  using CF = Cfg<MODE, BK, HM, HN, STAGES>;
   constexpr int BMW = CF::kBM, BNT = CF::kBN, LDK = CF::kLDK;
   constexpr bool kSplitA = CF::kSplitA, kSplitB = CF::kSplitB;
   constexpr bool kScaled = MODE == SPLIT && (KIND == LG_Q8_0 || KIND == LG_Q4_K);
-  static_assert(WTN % 2 == 0 || (EPI != int(Epi::SWIGLU) && EPI != int(Epi::GEGLU)),
+  static_assert(HN % 2 == 0 || (EPI != int(Epi::SWIGLU) && EPI != int(Epi::GEGLU)),
                 "gated epilogues pair gate and up blocks inside a wave");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -423,10 +423,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
   // local weight-tile row -> weight row
   auto wrow = [&](int r) -> int {
     if (EPI == int(Epi::SWIGLU) || EPI == int(Epi::GEGLU)) {
-      // wave column r/(32 WTN); block jb = (r/32) % WTN: gate for jb < WTN/2, up otherwise
-      const int wc = r / (32 * WTN), jb = (r >> 5) % WTN;
-      const int up = jb >= WTN / 2, jj = jb % (WTN / 2);
-      return up * ffn + nt * (BNT / 2) + wc * (16 * WTN) + jj * 32 + (r & 31);
+      // wave column r/(16 HN); 16-row block jb = (r/16) % HN: gate for jb < HN/2, up otherwise
+      const int wc = r / (16 * HN), jb = (r >> 4) % HN;
+      const int up = jb >= HN / 2, jj = jb % (HN / 2);
+      return up * ffn + nt * (BNT / 2) + wc * (8 * HN) + jj * 16 + (r & 15);
     }
     return nt * BNT + r;
   };
@@ -437,7 +437,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
   al.init(A, Alo, m0, M, K, t);
   BL bl;
   bl.init(W, wrow, t);
-  constexpr int MI = 2 * WTM, NJ = 2 * WTN;
+  constexpr int MI = HM, NJ = HN;
   f32x4 acc[MI][NJ];
 #pragma unroll
   for (int i = 0; i < MI; ++i)
@@ -450,7 +450,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
     // correction of the two-pass form: acc = (sum_c ks[m][c] (-B[n][c] 2^e_n)) 2^-e_n, a GEMM of depth
     // W.pkp over the chunk sums and the correction planes (f16 hi/lo each, SPLIT3 order), staged
     // four planes at a time through one LDS buffer with the next step prefetched into registers
-    using CC = Cfg<SPLIT3, BK, WTM, WTN, 1>;
+    using CC = Cfg<SPLIT3, BK, HM, HN, 1>;
     const int kp = W.pkp;
     DevMatrix Ch = W;  // the correction planes read as F16 matrices [rows][kp]
     Ch.kind = LG_F16;
@@ -478,11 +478,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
         ch.fetch(Ch, wrow, (kt + 1) * BK, t);
         cl.fetch(Cl, wrow, (kt + 1) * BK, t);
       }
-      mma_tile<LG_F16, SPLIT3, BK, WTM, WTN, LDK>(acc, Cs, Csl, Cb, Cbl, nullptr, wm, wn, lane);
+      mma_tile<LG_F16, SPLIT3, BK, HM, HN, LDK>(acc, Cs, Csl, Cb, Cbl, nullptr, wm, wn, lane);
     }
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      const float rs = W.pcr[wrow(wn * (32 * WTN) + j * 16 + (lane & 15))];
+      const float rs = W.pcr[wrow(wn * (16 * HN) + j * 16 + (lane & 15))];
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
@@ -512,7 +512,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
       _Float16 *As, *Al, *Bs, *Bl;
       float *Ds;
       stage_ptrs(cur, As, Al, Bs, Bl, Ds);
-      mma_tile<KIND, MODE, BK, WTM, WTN, LDK>(acc, As, Al, Bs, Bl, Ds, wm, wn, lane);
+      mma_tile<KIND, MODE, BK, HM, HN, LDK>(acc, As, Al, Bs, Bl, Ds, wm, wn, lane);
       if (kt + 1 < nk) {
         stage_ptrs(cur ^ 1, As, Al, Bs, Bl, Ds);
         al.template store<LDK>(As, Al, t);
@@ -533,7 +533,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
         al.fetch((kt + 1) * BK);
         bl.fetch(W, wrow, (kt + 1) * BK, t);
       }
-      mma_tile<KIND, MODE, BK, WTM, WTN, LDK>(acc, As, Al, Bs, Bl, Ds, wm, wn, lane);
+      mma_tile<KIND, MODE, BK, HM, HN, LDK>(acc, As, Al, Bs, Bl, Ds, wm, wn, lane);
     }
   }
 
@@ -548,20 +548,20 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
     if constexpr (EPI == int(Epi::ADD)) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = min(m0 + wm * (32 * WTM) + i * 16 + (lane >> 4) * 4 + r, M - 1);
+        const int row = min(m0 + wm * (16 * HM) + i * 16 + (lane >> 4) * 4 + r, M - 1);
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) cv[r][j] = C[int64_t(row) * ldc + nt * BNT + wn * (32 * WTN) + j * 16 + col_in];
+        for (int j = 0; j < NJ; ++j) cv[r][j] = C[int64_t(row) * ldc + nt * BNT + wn * (16 * HN) + j * 16 + col_in];
       }
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = m0 + wm * (32 * WTM) + i * 16 + (lane >> 4) * 4 + r;
+      const int row = m0 + wm * (16 * HM) + i * 16 + (lane >> 4) * 4 + r;
       if (row >= M) continue;
       if (EPI == int(Epi::SWIGLU) || EPI == int(Epi::GEGLU)) {
         // gate block j pairs with up block j + NJ / 2 (the same output columns)
 #pragma unroll
         for (int j = 0; j < NJ / 2; ++j) {
-          const int col = nt * (BNT / 2) + wn * (16 * WTN) + j * 16 + col_in;
+          const int col = nt * (BNT / 2) + wn * (8 * HN) + j * 16 + col_in;
           const float g = acc[i][j][r];
           const float v = (EPI == int(Epi::SWIGLU) ? silu(g) : gelu_tanh(g)) * acc[i][j + NJ / 2][r];
           _Float16 h, hl;
@@ -572,7 +572,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
       } else {
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-          const int col = nt * BNT + wn * (32 * WTN) + j * 16 + col_in;
+          const int col = nt * BNT + wn * (16 * HN) + j * 16 + col_in;
           float v = acc[i][j][r];
           if (EPI == int(Epi::F32)) {
             if (bias) v += bias[col];
@@ -594,13 +594,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
   }
 }
 
-template <uint32_t KIND, int MODE, int BK, int WTM, int WTN, int STAGES>
+template <uint32_t KIND, int MODE, int BK, int HM, int HN, int STAGES>
 bool launch_cfg(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
                 _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st,
                 const _Float16 *ks = nullptr) {
-  using CF = Cfg<MODE, BK, WTM, WTN, STAGES>;
+  using CF = Cfg<MODE, BK, HM, HN, STAGES>;
   const bool glu = epi == Epi::SWIGLU || epi == Epi::GEGLU;
-  if (glu && WTN % 2) return false;  // gated epilogues need gate and up blocks in one wave
+  if (glu && HN % 2) return false;  // gated epilogues need gate and up blocks in one wave
   const int outN = glu ? W.rows / 2 : W.rows;
   const int tileN = glu ? CF::kBN / 2 : CF::kBN;
   if (outN % tileN) return false;
@@ -628,10 +628,10 @@ bool launch_cfg(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &
     _Float16 *C16c = C16 ? C16 + int64_t(m0) * ldc : nullptr, *C16lc = C16lo ? C16lo + int64_t(m0) * ldc : nullptr;
     const _Float16 *ksc = ks ? ks + int64_t(m0) * W.pkp : nullptr;
     const _Float16 *kslc = ks ? ks + (int64_t(M) + m0) * W.pkp : nullptr;
-    constexpr int lds = lds_bytes<KIND, MODE, BK, WTM, WTN, STAGES>();
+    constexpr int lds = lds_bytes<KIND, MODE, BK, HM, HN, STAGES>();
 #define LAUNCH(E)                                                                                              \
   do {                                                                                                         \
-    auto fn = gemm_kernel<KIND, E, MODE, BK, WTM, WTN, STAGES>;                                                \
+    auto fn = gemm_kernel<KIND, E, MODE, BK, HM, HN, STAGES>;                                                  \
     grant_lds(reinterpret_cast<const void *>(fn), lds);                                                        \
     launch_timed(fn, grid, block, lds, st, Ac, Alc, Mc, K, W, Cc, C16c, C16lc, ldc, bias, MT, NT, ffn, ksc,     \
                  kslc);                                                                                        \
@@ -641,10 +641,10 @@ bool launch_cfg(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &
       case Epi::ADD: LAUNCH(1); break;
       case Epi::F16: LAUNCH(2); break;
       case Epi::SWIGLU:
-        if constexpr (WTN % 2 == 0) LAUNCH(3);
+        if constexpr (HN % 2 == 0) LAUNCH(3);
         break;
       case Epi::GEGLU:
-        if constexpr (WTN % 2 == 0) LAUNCH(4);
+        if constexpr (HN % 2 == 0) LAUNCH(4);
         break;
       case Epi::RELU16: LAUNCH(5); break;
     }

@@ -4,15 +4,15 @@
 namespace lg {
 namespace {
 
-// Per-kind, per-mode tile configuration: <MODE, BK, WTM, WTN, STAGES>.
+// Per-kind, per-mode tile configuration: <MODE, BK, HM, HN, STAGES> (workgroup tile 32 HM x 32 HN).
 template <uint32_t KIND>
 void launch_kind(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi, float *C,
                  _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias, hipStream_t st, const _Float16 *ks) {
   // Chosen by sweeps at the 35,840-token Q8_0/F16 and 32,768-token Q4_K/Q6_K 7B prefill
   // shapes; a 256-wide N tile falls back to 128 when it does not divide the output width.
   if (!Alo) {
-    if (launch_cfg<KIND, FAST, 64, 4, 4, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
-    if (launch_cfg<KIND, FAST, 64, 2, 2, 2>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
+    if (launch_cfg<KIND, FAST, 64, 8, 8, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
+    if (launch_cfg<KIND, FAST, 64, 4, 4, 2>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
   } else if (launch_gemm_wide(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st, ks)) {
     return;
   } else if (KIND == LG_Q4_K && needs_ksum(W)) {
@@ -26,17 +26,24 @@ void launch_kind(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix 
     const bool glu = epi == Epi::SWIGLU || epi == Epi::GEGLU;
     const int outN = glu ? W.rows / 2 : W.rows;
     const int64_t tiles = int64_t((M + 127) / 128) * (outN / (glu ? 64 : 128));
+    // few 64 x 64 tiles (a short request): 32 x 32 tiles (32 x 64 weight rows for gate|up) over two LDS
+    // stages, four times the workgroups and a quarter of each K step's LDS traffic per workgroup (C1's
+    // 144-token request 0.49-0.51 -> 0.40 ms; 128-deep K steps with one stage 0.41-0.43, 64-deep 0.45)
+    if (int64_t((M + 63) / 64) * (outN / 64) < 128 && W.cols % 128 == 0 &&
+        (glu ? launch_cfg<KIND, SPLIT, 128, 1, 2, 2>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)
+             : launch_cfg<KIND, SPLIT, 128, 1, 1, 2>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)))
+      return;
     // a handful of 64 x 128 tiles (a few dozen rows, narrow outputs): 64 x 64 tiles, twice again
     if (!glu && (M + 63) / 64 * (outN / 128) < 64 && W.cols % 128 == 0 &&
-        launch_cfg<KIND, SPLIT, 128, 1, 1, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st))
+        launch_cfg<KIND, SPLIT, 128, 2, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st))
       return;
     if (tiles < 256 && W.cols % 128 == 0 &&
-        launch_cfg<KIND, SPLIT, 128, 1, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st))
+        launch_cfg<KIND, SPLIT, 128, 2, 4, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st))
       return;
-    if (tiles < 256 && launch_cfg<KIND, SPLIT, 64, 1, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
-    if (launch_cfg<KIND, SPLIT, 64, 2, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
+    if (tiles < 256 && launch_cfg<KIND, SPLIT, 64, 2, 4, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
+    if (launch_cfg<KIND, SPLIT, 64, 4, 4, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
   } else {
-    if (launch_cfg<KIND, SPLIT3, 64, 2, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
+    if (launch_cfg<KIND, SPLIT3, 64, 4, 4, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)) return;
   }
   fail(LG_ERR_UNSUPPORTED, "gemm: no tile configuration for N=%d", W.rows);
 }

@@ -15,7 +15,7 @@ bool launch_gemm_q8_exact(const _Float16 *A, const _Float16 *Alo, int M, const D
                           hipStream_t st) {
   // 128 x 128 x 64 tiles, one LDS stage with register prefetch: best of a sweep at the
   // 35,840-token shapes (two workgroups per CU, 244 VGPRs).
-  return launch_cfg<LG_Q8_0, SPLIT, 64, 2, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st);
+  return launch_cfg<LG_Q8_0, SPLIT, 64, 4, 4, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st);
 }
 
 bool launch_gemm_q4_exact(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi,
@@ -23,7 +23,7 @@ bool launch_gemm_q4_exact(const _Float16 *A, const _Float16 *Alo, int M, const D
                           hipStream_t st, const _Float16 *ks) {
   // the Q8_0 geometry: 128 x 128 x 64 tiles, one LDS stage (the correction's four planes size it)
   LG_REQUIRE(ks, "gemm: an exact Q4_K launch needs its activation's chunk sums");
-  return launch_cfg<LG_Q4_K, SPLIT, 64, 2, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st, ks);
+  return launch_cfg<LG_Q4_K, SPLIT, 64, 4, 4, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st, ks);
 }
 
 namespace {
