@@ -338,8 +338,10 @@ __device__ float weight_at_head(const DevMatrix &W, int64_t n, int64_t k) {
 }
 
 // Workgroup (gathered row, block of 16 head rows): final RMSNorm of the row into LDS, then each
-// wave computes 4 head rows with their loads interleaved, reduced by DPP.  Rows past nv repeat
-// the last id and are not written.
+// wave computes 4 head rows, reduced by DPP.  The weights of 8 columns per lane are loaded together
+// (the first 8 before the RMSNorm, which does not feed their addresses), then used in column order,
+// so a lane's sums run over k = lane, lane + 64, ... as one load at a time would.  Rows past nv
+// repeat the last id and are not written.
 __global__ __launch_bounds__(kT) void head_rows_kernel(const float *__restrict__ x,
                                                        const int32_t *__restrict__ rows, int d,
                                                        const float *__restrict__ norm_w, float eps,
@@ -348,22 +350,38 @@ __global__ __launch_bounds__(kT) void head_rows_kernel(const float *__restrict__
                                                        int nv, float *__restrict__ logits) {
   extern __shared__ float h[];
   __shared__ float red[kT / 64];
+  constexpr int U = 8;
+  const int lane = threadIdx.x & 63;
+  const int j0 = blockIdx.y * 16 + (threadIdx.x >> 6) * 4;
+  int64_t n[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) n[r] = ids[min(j0 + r, nv - 1)];
+  float w[U][4];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) w[u][r] = weight_at_head(W, n[r], min(k0 + 64 * u, d - 1));
+  };
+  load(lane);
   const float *row = x + int64_t(rows[blockIdx.x]) * d;
   float ss = 0.0f;
   for (int k = threadIdx.x; k < d; k += kT) ss += row[k] * row[k];
   const float inv = 1.0f / sqrtf(block_sum(ss, red) / float(d) + eps);
   for (int k = threadIdx.x; k < d; k += kT) h[k] = row[k] * inv * norm_w[k];
   __syncthreads();
-  const int lane = threadIdx.x & 63;
-  const int j0 = blockIdx.y * 16 + (threadIdx.x >> 6) * 4;
-  int64_t n[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) n[r] = ids[min(j0 + r, nv - 1)];
   float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int k = lane; k < d; k += 64) {
-    const float hk = h[k];
+  for (int k0 = lane; k0 < d; k0 += 64 * U) {
+    if (k0 != lane) load(k0);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) s[r] += hk * weight_at_head(W, n[r], k);
+    for (int u = 0; u < U; ++u) {
+      const int k = k0 + 64 * u;
+      if (k < d) {
+        const float hk = h[k];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s[r] += hk * w[u][r];
+      }
+    }
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
