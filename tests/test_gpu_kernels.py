@@ -195,3 +195,25 @@ def test_q4k_gemv_decode_wide_model(lh, po):
         assert_argmax_equal(logits[i][None], want, rel=1e-4)
         print(f"step {i}: logits rel {err:.2e}", flush=True)
 
+
+
+@pytest.mark.parametrize("preset", ["plumbing-f16", "tiny-f16"])
+def test_exact_gemm_tilings_agree(lh, preset):
+    """The exact F16 GEMM takes 32 x 32 tiles over two LDS stages for short launches and 64 x 64, 64 x 128
+    or 128 x 128 tiles for longer ones: every tiling runs the same per-element MFMA sequence, so the
+    first rows of a 2048-row product equal the same rows computed alone at any row count, bit for bit
+    (with and without a bias)."""
+    img = lh.SynthImage(preset, seed=13)
+    eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=1024)
+    rng = np.random.default_rng(17)
+    for name in ("qkv.0.weight", "wo.0.weight", "mlp_wi.0.weight", "mlp_wo.0.weight"):
+        _, dims, _ = eng.gguf.tensor(name)
+        cols, rows = dims[0], int(np.prod(dims[1:]))
+        x = rng.standard_normal((2048, cols)).astype(np.float32)
+        bias = rng.standard_normal(rows).astype(np.float32)
+        big, big_b = eng.matmul(name, x), eng.matmul(name, x, bias)
+        for M in (2, 17, 33, 100, 256, 700):
+            print(f"{preset} {name} ({rows} x {cols}) M={M}", flush=True)
+            assert_bits_equal(eng.matmul(name, x[:M]), big[:M])
+            assert_bits_equal(eng.matmul(name, x[:M], bias), big_b[:M])
+    eng.close()
