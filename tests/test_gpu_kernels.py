@@ -197,16 +197,25 @@ def test_q4k_gemv_decode_wide_model(lh, po):
 
 
 
-@pytest.mark.parametrize("preset", ["plumbing-f16", "tiny-f16"])
+@pytest.mark.parametrize("preset", ["plumbing-f16", "tiny-f16", "tiny-q8", "tiny-q4k"])
 def test_exact_gemm_tilings_agree(lh, preset):
-    """The exact F16 GEMM takes 32 x 32 tiles over two LDS stages for short launches and 64 x 64, 64 x 128
-    or 128 x 128 tiles for longer ones: every tiling runs the same per-element MFMA sequence, so the
-    first rows of a 2048-row product equal the same rows computed alone at any row count, bit for bit
-    (with and without a bias)."""
+    """The exact GEMM takes small tiles over two LDS stages for short launches (32 x 32; 32 x 128 for Q4_K)
+    and 64 x 64, 64 x 128 or 128 x 128 tiles for longer ones: every tiling runs the same per-element MFMA
+    sequence, so the first rows of a 2048-row product equal the same rows computed alone at any row
+    count, bit for bit (with and without a bias).  F16, Q8_0 (block scales per 32-deep chunk) and the
+    K-quants' three-pass form over dequantised hi/lo planes."""
     img = lh.SynthImage(preset, seed=13)
     eng = lh.Engine(lh.Gguf.from_bytes(img), kv_tokens=1024)
     rng = np.random.default_rng(17)
-    for name in ("qkv.0.weight", "wo.0.weight", "mlp_wi.0.weight", "mlp_wo.0.weight"):
+    names = []
+    for name in ("qkv.0.weight", "q.0.weight", "v.0.weight", "wo.0.weight", "mlp_wi.0.weight", "mlp_wo.0.weight"):
+        try:
+            eng.gguf.tensor(name)
+            names.append(name)
+        except (KeyError, lh.LayaError):
+            pass
+    assert len(names) >= 4, names
+    for name in names:
         _, dims, _ = eng.gguf.tensor(name)
         cols, rows = dims[0], int(np.prod(dims[1:]))
         x = rng.standard_normal((2048, cols)).astype(np.float32)
