@@ -389,7 +389,13 @@ constexpr int lds_bytes() {
   return KIND == LG_Q4_K && MODE == SPLIT && corr > main ? corr : main;
 }
 
+// Epilogue of a q|k|v projection that rotates and stores q, k and v itself (RopeKvOut), as the RoPE
+// kernel would from the f32 rows: tiles of 64 weight rows (HN == 2), each wave's two 16-row blocks a
+// rotate-half pair of 16 dims each (d and d + hd/2 of one head), so the pair sits in one lane.
+constexpr int kTileEpiRope = 16;
+
 // ks / kslo: the chunk-sum planes of a two-pass Q4_K launch ([M][W.pkp] each), unused otherwise.
+// ro: the q|k|v outputs of EPI == kTileEpiRope (row r of the launch is ro's row ro_row0 + r).
 template <uint32_t KIND, int EPI, int MODE, int BK, int HM, int HN, int STAGES>
 __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ A,
                                                    const _Float16 *__restrict__ Alo, int M, int K,
@@ -398,13 +404,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
                                                    _Float16 *__restrict__ C16lo, int ldc,
                                                    const float *__restrict__ bias, int MT, int NT,
                                                    int ffn, const _Float16 *__restrict__ ks,
-                                                   const _Float16 *__restrict__ kslo) {
+                                                   const _Float16 *__restrict__ kslo, RopeKvOut ro, int ro_row0) {
   using CF = Cfg<MODE, BK, HM, HN, STAGES>;
   constexpr int BMW = CF::kBM, BNT = CF::kBN, LDK = CF::kLDK;
   constexpr bool kSplitA = CF::kSplitA, kSplitB = CF::kSplitB;
   constexpr bool kScaled = MODE == SPLIT && (KIND == LG_Q8_0 || KIND == LG_Q4_K);
   static_assert(HN % 2 == 0 || (EPI != int(Epi::SWIGLU) && EPI != int(Epi::GEGLU)),
                 "gated epilogues pair gate and up blocks inside a wave");
+  static_assert(EPI != kTileEpiRope || HN == 2, "the rotating epilogue takes 64-row tiles");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -427,6 +434,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
       const int wc = r / (16 * HN), jb = (r >> 4) % HN;
       const int up = jb >= HN / 2, jj = jb % (HN / 2);
       return up * ffn + nt * (BNT / 2) + wc * (8 * HN) + jj * 16 + (r & 15);
+    }
+    if (EPI == kTileEpiRope) {
+      // tile nt: pair offsets 32 (nt % (hd/64)) .. + 32 of head nt / (hd/64) of this part; wave column
+      // r/32 takes 16 of them, block (r/16) % 2 the first or the second dim of each pair
+      const int hpt = ro.hd / 64, p = (nt % hpt) * 32 + (r / 32) * 16 + (r & 15);
+      return (nt / hpt) * ro.hd + p + ((r >> 4) & 1) * (ro.hd / 2);
     }
     return nt * BNT + r;
   };
@@ -537,6 +550,70 @@ __global__ __launch_bounds__(256) void gemm_kernel(const _Float16 *__restrict__ 
     }
   }
 
+  if constexpr (EPI == kTileEpiRope) {
+    // each lane holds dims d = p and d + hd/2 (blocks 0 and 1) of four rows; the values are the f32
+    // acc (+ bias) an F32 epilogue would store, rotated by rope_pair and split by split_f16 as the RoPE
+    // kernel does: q to scaled hi/lo planes [M][hq hd], k to its K page row, v to its V page column
+    const int hd = ro.hd, half = hd / 2, hpt = hd / 64;
+    const int p = (nt % hpt) * 32 + wn * 16 + (lane & 15);
+    const int pcol = (nt / hpt) * hd + p;  // output column of dim p within this part
+    const int head = (ro.col0 + pcol) / hd;
+    const int part = head < ro.hq ? 0 : head < ro.hq + ro.hkv ? 1 : 2;  // q, k, v
+    const int PT = ro.page_tokens, plane = PT * hd, kvp = ro.kv_planes;
+    const float b0 = bias ? bias[pcol] : 0.0f, b1 = bias ? bias[pcol + half] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * (16 * HM) + i * 16 + (lane >> 4) * 4 + r;
+        if (row >= M) continue;
+        const int grow = ro_row0 + row;
+        const int pos = ro.tok_pos[grow];
+        const int64_t page = ro.tok_page[grow];
+        float v0 = acc[i][0][r], v1 = acc[i][1][r];
+        if (bias) {
+          v0 += b0;
+          v1 += b1;
+        }
+        _Float16 h, l;
+        if (part < 2) {
+          const int64_t tb = int64_t(pos) * hd + p;
+          float a, c;
+          rope_pair(v0, v1, ro.cosT[tb], ro.sinT[tb], ro.cosT[tb + half], ro.sinT[tb + half], a, c);
+          if (part == 0) {
+            _Float16 *dh = ro.q16 + int64_t(grow) * (ro.hq * hd) + head * hd + p;
+            _Float16 *dl = ro.q16lo + int64_t(grow) * (ro.hq * hd) + head * hd + p;
+            split_f16(a * ro.qscale, h, l);
+            dh[0] = h;
+            dl[0] = l;
+            split_f16(c * ro.qscale, h, l);
+            dh[half] = h;
+            dl[half] = l;
+          } else {
+            const int64_t blk = page * ro.page_stride + int64_t(head - ro.hq) * plane;
+            _Float16 *dh = ro.kpool + kvp * blk + (pos % PT) * hd + p;
+            split_f16(a, h, l);
+            dh[0] = h;
+            if (kvp == 2) dh[plane] = l;
+            split_f16(c, h, l);
+            dh[half] = h;
+            if (kvp == 2) dh[plane + half] = l;
+          }
+        } else {
+          const int64_t blk = page * ro.page_stride + int64_t(head - ro.hq - ro.hkv) * plane;
+          _Float16 *dh = ro.vpool + kvp * blk + int64_t(p) * PT + (pos % PT);
+          split_f16(v0, h, l);
+          dh[0] = h;
+          if (kvp == 2) dh[plane] = l;
+          split_f16(v1, h, l);
+          dh[int64_t(half) * PT] = h;
+          if (kvp == 2) dh[plane + int64_t(half) * PT] = l;
+        }
+      }
+    }
+    return;
+  }
+
   // epilogue: acc[i][j] register r -> row 16 i + 4 (lane / 16) + r, column 16 j + lane % 16 of the
   // wave tile
   const int col_in = lane & 15;
@@ -634,7 +711,7 @@ bool launch_cfg(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &
     auto fn = gemm_kernel<KIND, E, MODE, BK, HM, HN, STAGES>;                                                  \
     grant_lds(reinterpret_cast<const void *>(fn), lds);                                                        \
     launch_timed(fn, grid, block, lds, st, Ac, Alc, Mc, K, W, Cc, C16c, C16lc, ldc, bias, MT, NT, ffn, ksc,     \
-                 kslc);                                                                                        \
+                 kslc, RopeKvOut{}, 0);                                                                        \
   } while (0)
     switch (epi) {
       case Epi::F32: LAUNCH(0); break;
@@ -655,6 +732,27 @@ bool launch_cfg(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &
   return true;
 }
 
+// The q|k|v projection (or a column range of it, ro.col0 a multiple of hd) on tiles of BM x 64 weight
+// rows with the rotating epilogue; false (nothing launched) when the shape does not fit.
+template <uint32_t KIND, int MODE, int BK, int HM, int STAGES>
+bool launch_cfg_rope(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, const float *bias,
+                     const RopeKvOut &ro, hipStream_t st, const _Float16 *ks = nullptr) {
+  using CF = Cfg<MODE, BK, HM, 2, STAGES>;
+  if ((ro.hd != 64 && ro.hd != 128) || W.rows % ro.hd || ro.col0 % ro.hd || !Alo || !ro.q16lo) return false;
+  const int K = W.cols, NT = W.rows / 64;
+  const int64_t rows_cap = ((1ll << 31) - 1) / (int64_t(K) * 2) / CF::kBM * CF::kBM;
+  if (int64_t(M) > rows_cap) return false;
+  const int MT = (M + CF::kBM - 1) / CF::kBM;
+  const dim3 grid(MT * NT), block(256);
+  constexpr int lds = lds_bytes<KIND, MODE, BK, HM, 2, STAGES>();
+  auto fn = gemm_kernel<KIND, kTileEpiRope, MODE, BK, HM, 2, STAGES>;
+  grant_lds(reinterpret_cast<const void *>(fn), lds);
+  const _Float16 *kslc = ks ? ks + int64_t(M) * W.pkp : nullptr;
+  launch_timed(fn, grid, block, lds, st, A, Alo, M, K, W, static_cast<float *>(nullptr), static_cast<_Float16 *>(nullptr),
+               static_cast<_Float16 *>(nullptr), 0, bias, MT, NT, W.rows / 2, ks, kslc, ro, 0);
+  return true;
+}
+
 }  // namespace
 
 // Exact Q8_0 tiles, built in their own translation unit (k_gemm_q8.hip) with MFMA results in
@@ -662,6 +760,9 @@ bool launch_cfg(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &
 bool launch_gemm_q8_exact(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi,
                           float *C, _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias,
                           hipStream_t st);
+// launch_gemm_small_rope for Q8_0 weights (the exact Q8_0 tiles' translation unit).
+bool launch_gemm_q8_small_rope(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, const float *bias,
+                               const RopeKvOut &ro, hipStream_t st);
 // Exact two-pass Q4_K tiles (the same translation unit): codes, sub-block scales and the correction
 // over the activation's chunk sums ks.
 bool launch_gemm_q4_exact(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi,

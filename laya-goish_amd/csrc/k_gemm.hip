@@ -107,6 +107,20 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(const float *__restri
 
 }  // namespace
 
+bool gemm_small_rope_takes(int M, const DevMatrix &W, int hd) {
+  return M > 0 && (W.kind == LG_F16 || W.kind == LG_Q8_0) && (hd == 64 || hd == 128) && W.rows % hd == 0 &&
+         W.cols % 128 == 0 && int64_t((M + 63) / 64) * (W.rows / 64) < 128;
+}
+
+bool launch_gemm_small_rope(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, const float *bias,
+                            const RopeKvOut &ro, hipStream_t st) {
+  if (!gemm_small_rope_takes(M, W, ro.hd) || !Alo) return false;
+  if (W.kind == LG_Q8_0) return launch_gemm_q8_small_rope(A, Alo, M, W, bias, ro, st);
+  const bool ok = launch_cfg_rope<LG_F16, SPLIT, 128, 1, 2>(A, Alo, M, W, bias, ro, st);
+  if (ok) HIP_CHECK(hipGetLastError());
+  return ok;
+}
+
 void launch_gemm(const _Float16 *A, const _Float16 *A_lo, int M, const DevMatrix &W, Epi epi, float *C,
                  _Float16 *C16, _Float16 *C16_lo, int ldc, const float *bias, hipStream_t st, const _Float16 *ks) {
   LG_REQUIRE(M > 0, "gemm: empty activation");

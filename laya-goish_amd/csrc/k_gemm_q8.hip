@@ -33,6 +33,13 @@ bool launch_gemm_q8_exact(const _Float16 *A, const _Float16 *Alo, int M, const D
   return launch_cfg<LG_Q8_0, SPLIT, 64, 4, 4, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st);
 }
 
+bool launch_gemm_q8_small_rope(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, const float *bias,
+                               const RopeKvOut &ro, hipStream_t st) {
+  const bool ok = launch_cfg_rope<LG_Q8_0, SPLIT, 128, 1, 2>(A, Alo, M, W, bias, ro, st);
+  if (ok) HIP_CHECK(hipGetLastError());
+  return ok;
+}
+
 bool launch_gemm_q4_exact(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, Epi epi,
                           float *C, _Float16 *C16, _Float16 *C16lo, int ldc, const float *bias,
                           hipStream_t st, const _Float16 *ks) {

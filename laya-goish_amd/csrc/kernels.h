@@ -180,6 +180,13 @@ bool launch_gemm_wide_rope(const _Float16 *A, const _Float16 *Alo, int M, const 
 // Whether the 256 x 256 exact GEMM takes an M-row launch of W with epilogue epi (shape, prefill
 // copy and tile count; pointers are checked at launch).
 bool gemm_wide_takes(int M, const DevMatrix &W, Epi epi);
+// Short launches (fewer than 128 tiles of 64 x 64) of an F16 or Q8_0 q|k|v projection in the exact
+// split mode: the 32-row tile GEMM with the same rotating epilogue as launch_gemm_wide_rope (head_dim
+// 64 or 128, ro.col0 a multiple of it), the same bits as the F32 GEMM followed by the RoPE kernel.
+// gemm_small_rope_takes tells whether launch_gemm_small_rope launches (it returns false otherwise).
+bool gemm_small_rope_takes(int M, const DevMatrix &W, int hd);
+bool launch_gemm_small_rope(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, const float *bias,
+                            const RopeKvOut &ro, hipStream_t st);
 
 // RoPE on q and k of q|k|v rows ((hq+2hkv)*hd f32) with tables cos/sin[ctx][hd], q written
 // out, k and v written into the K page rows [hkv][page_tokens][hd] and V page columns
