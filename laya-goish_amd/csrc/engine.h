@@ -295,6 +295,7 @@ class Engine {
   DevBuf ws_dec_;
   DevBuf ws_ot_qk_, ws_ot_v_, ws_ot_gb_, ws_ot_o_;  // OpenThai mixer workspaces
   DevBuf ws_ot_part_;                               // OpenThai attention partials
+  DevBuf ws_ot_chunk_;                              // OpenThai DeltaNet chunk records
 };
 
 }  // namespace lg

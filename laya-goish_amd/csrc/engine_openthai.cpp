@@ -154,6 +154,8 @@ void Engine::run_openthai(BatchPlan &b, lg_cancel_fn cancel, void *arg) {
   ws_ot_v_.ensure(size_t(T) * std::max(lw, kvw) * 4);
   ws_ot_gb_.ensure(size_t(T) * nh * 2 * 4);
   ws_ot_o_.ensure(size_t(T) * lw * 4);
+  ws_ot_chunk_.ensure(ot_delta_chunk_floats(T, nseq, nh) * 4);
+  const int max_n = *std::max_element(b.n.begin(), b.n.end());
   auto lo = [&](DevBuf &buf, int64_t n) { return split() ? buf.as<_Float16>() + n : nullptr; };
   float *x = ws_x_.as<float>(), *proj = ws_qkv_.as<float>();
   _Float16 *h16 = ws_h16_.as<_Float16>(), *h16lo = lo(ws_h16_, int64_t(T) * d);
@@ -194,7 +196,7 @@ void Engine::run_openthai(BatchPlan &b, lg_cancel_fn cancel, void *arg) {
       launch_ot_delta_prep(proj, ldp_delta_, T, b.tok_pos, y.conv, y.alog, y.dt, nh, qk, vb, gb, stream);
       prof.end(double(T) * (3 * lw * 4 * 2 + lw * 4 + nh * 8), 0, stream);
       prof.begin("ot_delta_scan", stream);
-      launch_ot_delta_scan(qk, vb, gb, b.seq_row0, b.seq_n, nseq, nh, o, stream);
+      launch_ot_delta_scan(qk, vb, gb, b.seq_row0, b.seq_n, nseq, max_n, nh, ws_ot_chunk_.as<float>(), o, stream);
       prof.end(double(T) * (3 * lw + 2 * nh + lw) * 4, 4.0 * double(T) * nh * 128 * 128, stream);
       prof.begin("ot_delta_out", stream);
       launch_ot_delta_out(o, T, nh, y.norm, proj, ldp_delta_, 3 * lw, att, attlo, stream);

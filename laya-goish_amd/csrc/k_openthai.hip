@@ -41,7 +41,7 @@ __device__ __forceinline__ void store_planes(_Float16 *hi, _Float16 *lo, int64_t
 // One workgroup per token.  proj row: [q|k|v raw (3*lw) | z (lw) | a (nh) | b (nh) | pad].
 // Causal depthwise conv over the token and the 3 before it within its sequence (pos = index
 // in the sequence; rows of one sequence are consecutive), silu, then per head
-// query = q / |q| / sqrt(128), key = k / |k| (|x| = sqrt(x.x + 1e-6)), decay and beta.
+// query = q / |q| / sqrt(128), key = k / |k| (|x| = sqrt(x.x + 1e-6)), log-decay and beta.
 // model.rs:306-318 (conv), :323-331 (scales, decay, beta).
 __global__ __launch_bounds__(256) void ot_delta_prep_kernel(const float *__restrict__ proj, int ldp,
                                                             const int32_t *__restrict__ tok_pos,
@@ -81,152 +81,316 @@ __global__ __launch_bounds__(256) void ot_delta_prep_kernel(const float *__restr
   if (threadIdx.x < nh) {
     const int h = threadIdx.x;
     const float a = row[cd + lw + h], b = row[cd + lw + nh + h];
-    const float decay = expf(-expf(alog[h]) * softplusf_(a + dt[h]));
-    gb[(int64_t(t) * nh + h) * 2] = decay;
+    // the log of the decay a_t = exp(-exp(A_log) softplus(a + dt)); the chunked scan takes exp of sums of these
+    gb[(int64_t(t) * nh + h) * 2] = -expf(alog[h]) * softplusf_(a + dt[h]);
     gb[(int64_t(t) * nh + h) * 2 + 1] = sigmoidf_(b);
   }
 }
 
-// ---------------------------------------------------------------- DeltaNet: recurrent scan
-// model.rs:319-358, per head a [key j][value d] = 128 x 128 state S:
-//   S *= decay;  delta = (v - S^T key) * beta;  S += key delta^T;  o = S^T query.
-// Columns d are independent.  A 16-lane row of a wave owns one column: lane g of the row keeps
-// S[8g .. 8g+7][d] in registers, and the two sums over j are 16-lane DPP row reductions (no
-// LDS round trip on the token-to-token dependency chain).  A workgroup (4 waves) owns 16
-// columns of one head of one sequence: a sequence's 16 x 8 = 128 workgroups per layer run side
-// by side.  Tokens go in chunks of kCh staged in LDS, double buffered: the next chunk's global
-// loads are in flight while the current one is scanned.
-constexpr int kCh = 16;
-constexpr int kLpc = 16;                  // lanes per column
-constexpr int kJpl = kLK / kLpc;          // keys per lane
-constexpr int kCols = 4 * (64 / kLpc);    // columns per workgroup
+// ---------------------------------------------------------------- DeltaNet: chunked scan
+// model.rs:319-358, per head a [key j][value d] = 128 x 128 state S, token by token:
+//   S *= a_t;  delta_t = (v_t - S^T k_t) * beta_t;  S += k_t delta_t^T;  o_t = S^T q_t.
+// Taken here over chunks of kDC tokens in the chunk's WY form (the same mathematics, another rounding
+// order).  With S0 the state entering a chunk and gam_t = sum_{r <= t} log a_r inside it:
+//   (I + A) X = [diag(beta) V | diag(beta e^gam) K],   A_ts = beta_t e^(gam_t - gam_s) (k_t . k_s), s < t
+//   X = [U | W];   Delta = U - W S0                    (the rows delta_t of the token loop)
+//   O = diag(e^gam) Q S0 + P Delta,                    P_ts = e^(gam_t - gam_s) (q_t . k_s), s <= t
+//   S = e^gam_last S0 + K^T diag(e^(gam_last - gam)) Delta.
+// ot_delta_chunk_kernel builds A and P and solves for X by forward substitution, every chunk of every
+// head at once; ot_delta_state_kernel walks a sequence's chunks in order, carrying S.  Products on
+// v_mfma_f32_16x16x4_f32 (f32 operands and accumulation); gam is summed in f64, so each decay factor
+// e^(gam_t - gam_s) is exp of a difference that is exact to f32 rounding.  Tokens past a sequence's end
+// carry beta 0 and log-decay 0 (with zero k, q, v in the chunk kernel), which leave S unchanged.
+constexpr int kDC = 32;   // tokens per chunk
+constexpr int kDP = 132;  // LDS row stride (floats) of a chunk's [kDC][128] operands
+constexpr int kDA = 36;   // LDS row stride of A
+// one (chunk, head) record of the workspace, floats: U [kDC][128], W [kDC][128], P [kDC][kDC],
+// e^gam_t [kDC], e^(gam_last - gam_t) [kDC]
+constexpr int kOffU = 0, kOffW = kDC * kLK, kOffP = 2 * kDC * kLK, kOffE = kOffP + kDC * kDC;
+constexpr int kOffL = kOffE + kDC, kChunkFloats = kOffL + kDC;
+// a chunk's record: sequences own consecutive slots, chunk c of sequence sq (first batch row row0)
+// in slot sq + row0 / kDC + c; fewer than nseq + T / kDC + 1 slots in all
+__device__ __forceinline__ int64_t ot_chunk_slot(int sq, int row0, int c) { return int64_t(sq) + row0 / kDC + c; }
 
-// Sum over each 32-lane half of the wave, every lane receiving its half's sum: 16-lane DPP
-// row sums, then the other row's sum through ds_swizzle (bitmask mode, lane ^ 16 within 32).
-__device__ __forceinline__ float half_sum32(float v) {
-  v = row_sum(v);
-  const float other = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
-  return v + other;
-}
-
-template <int LPC>
-__device__ __forceinline__ float column_sum(float v) {
-  if constexpr (LPC == 32) return half_sum32(v);
-  else return row_sum(v);
-}
-
-__global__ __launch_bounds__(256) void ot_delta_scan_kernel(const float *__restrict__ qk,
-                                                            const float *__restrict__ vbuf,
-                                                            const float *__restrict__ gb,
-                                                            const int32_t *__restrict__ seq_row0,
-                                                            const int32_t *__restrict__ seq_n, int nh,
-                                                            float *__restrict__ out) {
-  __shared__ float4 s_qk[2][kCh][64];  // per token: query (float4 0..31) | key (32..63)
-  __shared__ float s_v[2][kCh][kCols];
-  __shared__ float2 s_gb[2][kCh];
-  __shared__ float s_o[kCh][kCols];
-  const int sq = blockIdx.x, h = blockIdx.y, cb = blockIdx.z;
-  const int row0 = seq_row0[sq], n = seq_n[sq];
+__global__ __launch_bounds__(256) void ot_delta_chunk_kernel(const float *__restrict__ qk,
+                                                             const float *__restrict__ vbuf,
+                                                             const float *__restrict__ gb,
+                                                             const int32_t *__restrict__ seq_row0,
+                                                             const int32_t *__restrict__ seq_n, int nh,
+                                                             float *__restrict__ ws) {
+  __shared__ __align__(16) float sK[kDC * kDP], sQ[kDC * kDP], sV[kDC * kDP];
+  __shared__ __align__(16) float sA[kDC * kDA];
+  __shared__ float sB[kDC], sBE[kDC];
+  __shared__ double sGam[kDC];
+  const int c = blockIdx.x, h = blockIdx.y, sq = blockIdx.z;
+  const int row0 = seq_row0[sq], n = seq_n[sq], t0 = c * kDC;
+  if (t0 >= n) return;  // the grid covers the longest sequence's chunks
+  const int m = min(kDC, n - t0);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, kg = lane >> 4;
   const int lw = nh * kLK;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int col = (tid >> 6) * (64 / kLpc) + lane / kLpc;  // column within this block
-  const int g = lane % kLpc;                              // keys j = kJpl g .. kJpl g + kJpl - 1
-  const int nchunks = (n + kCh - 1) / kCh;
-  static_assert(kCh * 64 == 4 * 256 && kCh * kCols <= 256 && kCh <= 64, "chunk staging layout");
-  // Loads are unconditional, from the token clamped into the sequence (n >= 1 whenever a chunk
-  // exists): rows past the end hold copies that the scan never reads, and no load is
-  // predicated, so the next chunk's loads never wait on anything.
-  float4 rq0, rq1, rq2, rq3;
-  float rv;
-  float2 rg;
-  const int vi = tid / kCols, vc = tid % kCols;
-  auto load = [&](int c) {
-    const int t0 = c * kCh;
-    const float4 *base = reinterpret_cast<const float4 *>(qk) + int64_t(h) * (2 * kLK / 4);
-    const int q4 = tid & 63, ti = tid >> 6;
-    rq0 = base[int64_t(row0 + min(t0 + ti, n - 1)) * nh * (2 * kLK / 4) + q4];
-    rq1 = base[int64_t(row0 + min(t0 + ti + 4, n - 1)) * nh * (2 * kLK / 4) + q4];
-    rq2 = base[int64_t(row0 + min(t0 + ti + 8, n - 1)) * nh * (2 * kLK / 4) + q4];
-    rq3 = base[int64_t(row0 + min(t0 + ti + 12, n - 1)) * nh * (2 * kLK / 4) + q4];
-    rv = vbuf[int64_t(row0 + min(t0 + min(vi, kCh - 1), n - 1)) * lw + h * kLK + cb * kCols + vc];
-    rg = reinterpret_cast<const float2 *>(gb)[int64_t(row0 + min(t0 + (tid & (kCh - 1)), n - 1)) * nh + h];
-    if (t0 + (tid & (kCh - 1)) >= n) rg = make_float2(1.0f, 0.0f);  // neutral token past the end
-  };
-  auto stage = [&](int b) {
-    const int q4 = tid & 63, ti = tid >> 6;
-    s_qk[b][ti][q4] = rq0;
-    s_qk[b][ti + 4][q4] = rq1;
-    s_qk[b][ti + 8][q4] = rq2;
-    s_qk[b][ti + 12][q4] = rq3;
-    if (vi < kCh) s_v[b][vi][vc] = rv;
-    if (tid < kCh) s_gb[b][tid] = rg;
-  };
-  // one token's operands for this lane, read from LDS
-  struct Tok {
-    float k[kJpl], q[kJpl], v;
-    float2 db;
-  };
-  auto fetch = [&](int b, int i, Tok &t) {
+  float *rec = ws + (ot_chunk_slot(sq, row0, c) * nh + h) * kChunkFloats;
+  // the chunk's q, k, v rows (rows past m zero); loads from the row clamped into the chunk, unpredicated
 #pragma unroll
-    for (int c = 0; c < kJpl / 4; ++c) {
-      const float4 a = s_qk[b][i][32 + g * (kJpl / 4) + c], e = s_qk[b][i][g * (kJpl / 4) + c];
-      t.k[4 * c] = a.x; t.k[4 * c + 1] = a.y; t.k[4 * c + 2] = a.z; t.k[4 * c + 3] = a.w;
-      t.q[4 * c] = e.x; t.q[4 * c + 1] = e.y; t.q[4 * c + 2] = e.z; t.q[4 * c + 3] = e.w;
-    }
-    t.v = s_v[b][i][col];
-    t.db = s_gb[b][i];
-  };
-  float S[kJpl];
-#pragma unroll
-  for (int j = 0; j < kJpl; ++j) S[j] = 0.0f;
-  if (nchunks > 0) {
-    load(0);
-    stage(0);
+  for (int e = 0; e < 4; ++e) {
+    const int idx = tid + 256 * e, i = idx >> 5, c4 = idx & 31;
+    const int64_t r = row0 + t0 + min(i, m - 1);
+    const float4 *qrow = reinterpret_cast<const float4 *>(qk + (r * nh + h) * (2 * kLK));
+    float4 qv = qrow[c4], kv = qrow[32 + c4], vv = reinterpret_cast<const float4 *>(vbuf + r * lw + h * kLK)[c4];
+    if (i >= m) qv = kv = vv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    *reinterpret_cast<float4 *>(sQ + i * kDP + 4 * c4) = qv;
+    *reinterpret_cast<float4 *>(sK + i * kDP + 4 * c4) = kv;
+    *reinterpret_cast<float4 *>(sV + i * kDP + 4 * c4) = vv;
+  }
+  if (tid < kDC) {
+    // a log-decay below -1e4 (a decay that is 0 in f32) is held at -1e4 so that differences stay finite
+    const float2 v = reinterpret_cast<const float2 *>(gb)[(row0 + t0 + min(tid, m - 1)) * int64_t(nh) + h];
+    sB[tid] = tid < m ? v.y : 0.0f;
+    sBE[tid] = tid < m ? (v.x < -1e4f ? -1e4f : v.x) : 0.0f;  // the log-decay, until the sums below
   }
   __syncthreads();
-  for (int c = 0; c < nchunks; ++c) {
-    const int b = c & 1;
-    if (c + 1 < nchunks) load(c + 1);
-    const int cnt = min(kCh, n - c * kCh);
-    // The chunk is straight-line code over all kCh tokens: staged tokens past the sequence's
-    // end carry decay 1 and beta 0, which leave S exactly unchanged (S * 1 = S, S + k * 0 = S),
-    // so no token needs a branch and the scheduler can issue LDS reads tokens ahead.
-    float oreg[kCh];
-#pragma unroll
-    for (int i = 0; i < kCh; ++i) {
-      Tok t;
-      fetch(b, i, t);
-      float p0 = 0.0f, p1 = 0.0f;
-#pragma unroll
-      for (int j = 0; j < kJpl; j += 2) {
-        S[j] *= t.db.x;
-        S[j + 1] *= t.db.x;
-        p0 = fmaf(S[j], t.k[j], p0);
-        p1 = fmaf(S[j + 1], t.k[j + 1], p1);
-      }
-      const float delta = (t.v - column_sum<kLpc>(p0 + p1)) * t.db.y;
-      float o0 = 0.0f, o1 = 0.0f;
-#pragma unroll
-      for (int j = 0; j < kJpl; j += 2) {
-        S[j] = fmaf(t.k[j], delta, S[j]);
-        S[j + 1] = fmaf(t.k[j + 1], delta, S[j + 1]);
-        o0 = fmaf(S[j], t.q[j], o0);
-        o1 = fmaf(S[j + 1], t.q[j + 1], o1);
-      }
-      oreg[i] = column_sum<kLpc>(o0 + o1);
+  if (tid == 0) {  // gam in f64, token after token
+    double gam = 0.0;
+    for (int i = 0; i < kDC; ++i) {
+      gam += double(sBE[i]);
+      sGam[i] = gam;
+      sBE[i] = sB[i] * expf(float(gam));
     }
-    if (g == 0)
+  }
+  __syncthreads();
+  // K K^T and Q K^T, 32 x 32: wave w takes the 16 x 16 block (rows 16 (w / 2), columns 16 (w % 2)); the
+  // 128-deep contraction in the order j = 16 g + 4 kg + component, the same for both operands
+  {
+    const int bt = w >> 1, bs = w & 1;
+    float4v kk = {0.0f, 0.0f, 0.0f, 0.0f}, qq = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int i = 0; i < kCh; ++i) s_o[i][col] = oreg[i];
-    __syncthreads();
-    // stage the next chunk before this chunk's stores are issued, so that waiting for its loads
-    // never waits for stores as well
-    if (c + 1 < nchunks) stage(b ^ 1);
-    for (int e = tid; e < kCh * kCols; e += 256) {
-      const int i = e / kCols, cc = e % kCols;
-      if (i < cnt) out[int64_t(row0 + c * kCh + i) * lw + h * kLK + cb * kCols + cc] = s_o[i][cc];
+    for (int g = 0; g < 8; ++g) {
+      const float4 ka = *reinterpret_cast<const float4 *>(sK + (16 * bt + li) * kDP + 16 * g + 4 * kg);
+      const float4 qa = *reinterpret_cast<const float4 *>(sQ + (16 * bt + li) * kDP + 16 * g + 4 * kg);
+      const float4 kb = *reinterpret_cast<const float4 *>(sK + (16 * bs + li) * kDP + 16 * g + 4 * kg);
+      kk = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.x, kb.x, kk, 0, 0, 0);
+      qq = __builtin_amdgcn_mfma_f32_16x16x4f32(qa.x, kb.x, qq, 0, 0, 0);
+      kk = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.y, kb.y, kk, 0, 0, 0);
+      qq = __builtin_amdgcn_mfma_f32_16x16x4f32(qa.y, kb.y, qq, 0, 0, 0);
+      kk = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.z, kb.z, kk, 0, 0, 0);
+      qq = __builtin_amdgcn_mfma_f32_16x16x4f32(qa.z, kb.z, qq, 0, 0, 0);
+      kk = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.w, kb.w, kk, 0, 0, 0);
+      qq = __builtin_amdgcn_mfma_f32_16x16x4f32(qa.w, kb.w, qq, 0, 0, 0);
     }
+    // lane: rows t = 16 bt + 4 kg + r, column s = 16 bs + li
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 16 * bt + 4 * kg + r, s = 16 * bs + li;
+      const float dec = s <= t ? expf(float(sGam[t] - sGam[s])) : 0.0f;
+      sA[t * kDA + s] = s < t ? sB[t] * dec * kk[r] : 0.0f;
+      rec[kOffP + t * kDC + s] = s <= t ? dec * qq[r] : 0.0f;
+    }
+  }
+  if (tid < kDC) {
+    rec[kOffE + tid] = expf(float(sGam[tid]));
+    rec[kOffL + tid] = expf(float(sGam[kDC - 1] - sGam[tid]));
+  }
+  __syncthreads();
+  // forward substitution, one column of X = [U | W] per thread: x_t = rhs_t - sum_{s < t} A_ts x_s, s ascending
+  {
+    const bool isU = tid < kLK;
+    const int cc = tid & (kLK - 1);
+    float x[kDC];
+#pragma unroll
+    for (int t = 0; t < kDC; ++t) {
+      float acc = isU ? sB[t] * sV[t * kDP + cc] : sBE[t] * sK[t * kDP + cc];
+#pragma unroll
+      for (int s = 0; s < t; ++s) acc = fmaf(-sA[t * kDA + s], x[s], acc);
+      x[t] = acc;
+    }
+    float *dst = rec + (isU ? kOffU : kOffW) + cc;
+#pragma unroll
+    for (int t = 0; t < kDC; ++t) dst[t * kLK] = x[t];
+  }
+}
+
+// One workgroup per (16 value columns, head, sequence): S[:, 16 cb .. 16 cb + 16) lives in MFMA
+// accumulators, wave w holding key rows 32 w .. 32 w + 31 (two 16 x 16 blocks; lane: rows
+// 32 w + 16 b + 4 kg + r, column li).  Per chunk c, two barriers:
+//   1. each wave's share of W S0 (its 32 key rows; its S accumulators serve as the B operand directly,
+//      the contraction taken as j = 32 w + 16 b + 4 kg + r), then of Q S0, whose MFMAs run on while the
+//      wave waits at the barrier;
+//   2. Delta = U - (sum of the four waves' W S0, fixed order); waves 0 and 1 meanwhile store the O rows
+//      of chunk c - 1: P Delta (MFMA) + e^gam (sum of its Q S0);
+//   3. the Q S0 shares of chunk c for its O; S = e^gam_last S + K^T (e^(gam_last - gam) Delta).
+// Only W S0 -> Delta -> S is on the chunk-to-chunk path.  K, P and the decay factors are staged in LDS,
+// double-buffered by chunk parity (K rows with their 16-float column groups XOR-swizzled by row, so the
+// K^T operand reads of a wave fall in distinct banks); W and Q are loaded two chunks ahead into one of
+// two register sets in the A-operand layout of step 1, U into the lanes that form Delta.
+struct OtPre {
+  float4v W[2][2], Q[2][2], K[4], P;
+  float U0, U1, E, L;
+};
+
+__device__ __forceinline__ int ot_kswz(int row, int col) { return row * kLK + (col ^ ((row & 3) << 4)); }
+
+__global__ __launch_bounds__(256, 1) void ot_delta_state_kernel(const float *__restrict__ qk,
+                                                                const float *__restrict__ ws,
+                                                                const int32_t *__restrict__ seq_row0,
+                                                                const int32_t *__restrict__ seq_n, int nh,
+                                                                float *__restrict__ out) {
+  __shared__ __align__(16) float sK[2][kDC * kLK];
+  __shared__ __align__(16) float sP[2][kDC * kDC];
+  __shared__ float sE[2][kDC], sL[2][kDC];
+  __shared__ __align__(16) float sD[2][kDC * 16];
+  __shared__ __align__(16) float sPW[4][kDC * 16], sPQ[4][kDC * 16];  // per wave: W S0, Q S0 [t][d]
+  // grid (heads, column blocks, sequences): consecutive workgroups go to the 8 XCDs in turn, so with
+  // x = head the eight column blocks of a head share one XCD and its L2 (each reads the whole chunk's W,
+  // Q and K)
+  const int h = blockIdx.x, cb = blockIdx.y, sq = blockIdx.z;
+  const int row0 = seq_row0[sq], n = seq_n[sq];
+  const int nch = (n + kDC - 1) / kDC;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, kg = lane >> 4;
+  const int lw = nh * kLK;
+  auto load = [&](int c, OtPre &p) {
+    const float *rec = ws + (ot_chunk_slot(sq, row0, c) * nh + h) * kChunkFloats;
+    const int t0 = c * kDC, m = min(kDC, n - t0);
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const int t = 16 * tb + li, j = 32 * w + 16 * b + 4 * kg;
+        p.W[tb][b] = *reinterpret_cast<const float4v *>(rec + kOffW + t * kLK + j);
+        const int64_t r = row0 + t0 + min(t, m - 1);
+        p.Q[tb][b] = *reinterpret_cast<const float4v *>(qk + (r * nh + h) * (2 * kLK) + j);
+      }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int idx = tid + 256 * e, i = idx >> 5, c4 = idx & 31;
+      const int64_t r = row0 + t0 + min(i, m - 1);
+      p.K[e] = reinterpret_cast<const float4v *>(qk + (r * nh + h) * (2 * kLK) + kLK)[c4];
+    }
+    p.P = reinterpret_cast<const float4v *>(rec + kOffP)[tid];
+    p.U0 = rec[kOffU + (tid >> 4) * kLK + cb * 16 + (tid & 15)];
+    p.U1 = rec[kOffU + (16 + (tid >> 4)) * kLK + cb * 16 + (tid & 15)];
+    p.E = rec[kOffE + (tid & (kDC - 1))];
+    p.L = rec[kOffL + (tid & (kDC - 1))];
+  };
+  auto stage = [&](const OtPre &p, int X) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int idx = tid + 256 * e, i = idx >> 5, c4 = idx & 31;
+      *reinterpret_cast<float4v *>(sK[X] + ot_kswz(i, 4 * c4)) = p.K[e];
+    }
+    reinterpret_cast<float4v *>(sP[X])[tid] = p.P;
+    if (tid < kDC) {
+      sE[X][tid] = p.E;
+      sL[X][tid] = p.L;
+    }
+  };
+  // O rows t = 16 w + 4 kg + r (column li) of chunk cc from LDS set Y: P Delta over the chunk's tokens
+  // s = 4 q + kg (P is zero above its diagonal), then + e^gam_t (sum of the Q S0 shares).  Kept in
+  // registers and stored by store_o at the start of the next chunk, right after the wait for that
+  // chunk's operands: a store waits in the same counter as the loads, and issued there it has a whole
+  // chunk to complete before the next such wait
+  float4v ov = {0.0f, 0.0f, 0.0f, 0.0f};
+  int o_chunk = -1;
+  auto emit_o = [&](int cc, int Y) {
+    float4v po = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int q = 0; q < kDC / 4; ++q) {
+      const int si = 4 * q + kg;
+      po = __builtin_amdgcn_mfma_f32_16x16x4f32(sP[Y][(16 * w + li) * kDC + si], sD[Y][si * 16 + li], po, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 16 * w + 4 * kg + r, e = t * 16 + li;
+      const float qs = ((sPQ[0][e] + sPQ[1][e]) + sPQ[2][e]) + sPQ[3][e];
+      ov[r] = fmaf(sE[Y][t], qs, po[r]);
+    }
+    o_chunk = cc;
+  };
+  auto store_o = [&] {
+    if (o_chunk < 0) return;
+    const int t0 = o_chunk * kDC, m = min(kDC, n - t0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 16 * w + 4 * kg + r;
+      if (t < m) out[int64_t(row0 + t0 + t) * lw + h * kLK + cb * 16 + li] = ov[r];
+    }
+    o_chunk = -1;
+  };
+  float4v S[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) S[b] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+  // chunk c from cur, which then takes chunk c + 2
+  auto body = [&](int c, OtPre &cur) {
+    const int X = c & 1;
+    stage(cur, X);
+    if (w < 2) store_o();
+    const float u0 = cur.U0, u1 = cur.U1;
+    float4v aW[2][2], aQ[2][2];
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        aW[tb][b] = cur.W[tb][b];
+        aQ[tb][b] = cur.Q[tb][b];
+      }
+    if (c + 2 < nch) load(c + 2, cur);
+    // 1. W S0 (two independent chains), then Q S0
+    float4v dw[2], dq[2];
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) dw[tb] = dq[tb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) dw[tb] = __builtin_amdgcn_mfma_f32_16x16x4f32(aW[tb][b][r], S[b][r], dw[tb], 0, 0, 0);
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sPW[w][(16 * tb + 4 * kg + r) * 16 + li] = dw[tb][r];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) dq[tb] = __builtin_amdgcn_mfma_f32_16x16x4f32(aQ[tb][b][r], S[b][r], dq[tb], 0, 0, 0);
     __syncthreads();
+    // 2. Delta: entries e = tid (t = tid / 16) and tid + 256 (t = 16 + tid / 16), d = tid % 16
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int e = tid + 256 * k;
+      const float ws0 = ((sPW[0][e] + sPW[1][e]) + sPW[2][e]) + sPW[3][e];
+      sD[X][e] = (k ? u1 : u0) - ws0;
+    }
+    if (c > 0 && w < 2) emit_o(c - 1, X ^ 1);
+    __syncthreads();
+    // 3. this chunk's Q S0 shares; S = e^gam_last S + K^T Delta_scaled over the tokens t = 4 s + kg
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sPQ[w][(16 * tb + 4 * kg + r) * 16 + li] = dq[tb][r];
+    const float gl = sE[X][kDC - 1];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) S[b] = S[b] * gl;
+#pragma unroll
+    for (int s = 0; s < kDC / 4; ++s) {
+      const int t = 4 * s + kg;
+      const float dsc = sL[X][t] * sD[X][t * 16 + li];
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+        S[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(sK[X][ot_kswz(t, 32 * w + 16 * b + li)], dsc, S[b], 0, 0, 0);
+    }
+  };
+  OtPre pa, pb;
+  if (nch > 0) load(0, pa);
+  if (nch > 1) load(1, pb);
+  for (int c = 0; c < nch; c += 2) {
+    body(c, pa);
+    if (c + 1 < nch) body(c + 1, pb);
+  }
+  __syncthreads();  // the last chunk's Q S0 shares
+  if (nch > 0 && w < 2) {
+    store_o();  // chunk nch - 2
+    emit_o(nch - 1, (nch - 1) & 1);
+    store_o();
   }
 }
 
@@ -635,11 +799,19 @@ void launch_ot_delta_prep(const float *proj, int ldp, int T, const int32_t *tok_
   HIP_CHECK(hipGetLastError());
 }
 
+size_t ot_delta_chunk_floats(int T, int nseq, int nh) { return size_t(nseq + T / kDC + 1) * nh * kChunkFloats; }
+
 void launch_ot_delta_scan(const float *qk, const float *vbuf, const float *gb, const int32_t *seq_row0,
-                          const int32_t *seq_n, int nseq, int nh, float *out, hipStream_t st) {
-  LG_REQUIRE(nseq > 0 && nh > 0 && nh <= 65535, "delta scan: bad shape nseq=%d nh=%d", nseq, nh);
-  hipLaunchKernelGGL(ot_delta_scan_kernel, dim3(nseq, nh, kLK / kCols), dim3(256), 0, st, qk, vbuf, gb, seq_row0,
-                     seq_n, nh, out);
+                          const int32_t *seq_n, int nseq, int max_n, int nh, float *chunk_ws, float *out,
+                          hipStream_t st) {
+  LG_REQUIRE(nseq > 0 && nseq <= 65535 && nh > 0 && nh <= 65535, "delta scan: bad shape nseq=%d nh=%d", nseq, nh);
+  LG_REQUIRE(max_n > 0 && chunk_ws, "delta scan: no tokens or no chunk workspace");
+  const int maxch = (max_n + kDC - 1) / kDC;
+  hipLaunchKernelGGL(ot_delta_chunk_kernel, dim3(maxch, nh, nseq), dim3(256), 0, st, qk, vbuf, gb, seq_row0, seq_n,
+                     nh, chunk_ws);
+  HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(ot_delta_state_kernel, dim3(nh, kLK / 16, nseq), dim3(256), 0, st, qk, chunk_ws, seq_row0, seq_n,
+                     nh, out);
   HIP_CHECK(hipGetLastError());
 }
 

@@ -123,20 +123,23 @@ def test_decide_matches_oracle(tiny, perms):
             assert a["choice"] == b["choice"]
 
 
-def test_full_width_layers_match_oracle(lh, po):
+@pytest.mark.parametrize("n", [160, 1437])
+def test_full_width_layers_match_oracle(lh, po, n):
     """The first four layers of the 0.8B shape (d 1024, 16 linear heads, 8/2 x 256 attention,
-    vocab 248339): three DeltaNet layers and one full-attention layer, 160 tokens."""
+    vocab 248339): three DeltaNet layers and one full-attention layer; 160 tokens, and the
+    reference's 1437-token request length (45 scan chunks of 32 tokens, the last one partial)."""
     img = lh.SynthImage("openthai-0.8b", seed=3, n_layers=4)
     eng = lh.Engine(lh.Gguf.from_bytes(img))
     om = po.OpenThai(po.Gguf(img.array()), threads=8)
-    ids = np.random.default_rng(0).integers(0, 247000, 160)
-    pos = [0, 77, 159]
-    print("openthai-0.8b (4 layers): forward n=160", flush=True)
+    ids = np.random.default_rng(n).integers(0, 247000, n)
+    pos = [0, 77, n // 2, n - 1]
+    print(f"openthai-0.8b (4 layers): forward n={n}", flush=True)
     s = eng.seq_create()
     got = eng.forward(s, ids, pos)
     eng.close()
     want = om.forward(ids, pos)
     err = float(np.abs(got - want).max())
+    print(f"openthai-0.8b (4 layers) n={n}: slot logits max abs error {err:.3e}", flush=True)
     assert err <= 2e-3, f"slot logits differ by {err:.3e}"
 
 
