@@ -196,7 +196,7 @@ void Engine::run_openthai(BatchPlan &b, lg_cancel_fn cancel, void *arg) {
       launch_ot_delta_prep(proj, ldp_delta_, T, b.tok_pos, y.conv, y.alog, y.dt, nh, qk, vb, gb, stream);
       prof.end(double(T) * (3 * lw * 4 * 2 + lw * 4 + nh * 8), 0, stream);
       prof.begin("ot_delta_scan", stream);
-      launch_ot_delta_scan(qk, vb, gb, b.seq_row0, b.seq_n, nseq, max_n, nh, ws_ot_chunk_.as<float>(), o, stream);
+      launch_ot_delta_scan(qk, vb, gb, b.seq_row0, b.seq_n, nseq, T, max_n, nh, ws_ot_chunk_.as<float>(), o, stream);
       prof.end(double(T) * (3 * lw + 2 * nh + lw) * 4, 4.0 * double(T) * nh * 128 * 128, stream);
       prof.begin("ot_delta_out", stream);
       launch_ot_delta_out(o, T, nh, y.norm, proj, ldp_delta_, 3 * lw, att, attlo, stream);

@@ -208,46 +208,127 @@ __global__ __launch_bounds__(256) void ot_delta_chunk_kernel(const float *__rest
   }
 }
 
-// One workgroup per (16 value columns, head, sequence): S[:, 16 cb .. 16 cb + 16) lives in MFMA
-// accumulators, wave w holding key rows 32 w .. 32 w + 31 (two 16 x 16 blocks; lane: rows
-// 32 w + 16 b + 4 kg + r, column li).  Per chunk c, two barriers:
-//   1. each wave's share of W S0 (its 32 key rows; its S accumulators serve as the B operand directly,
-//      the contraction taken as j = 32 w + 16 b + 4 kg + r), then of Q S0, whose MFMAs run on while the
-//      wave waits at the barrier;
-//   2. Delta = U - (sum of the four waves' W S0, fixed order); waves 0 and 1 meanwhile store the O rows
-//      of chunk c - 1: P Delta (MFMA) + e^gam (sum of its Q S0);
-//   3. the Q S0 shares of chunk c for its O; S = e^gam_last S + K^T (e^(gam_last - gam) Delta).
-// Only W S0 -> Delta -> S is on the chunk-to-chunk path.  K, P and the decay factors are staged in LDS,
-// double-buffered by chunk parity (K rows with their 16-float column groups XOR-swizzled by row, so the
-// K^T operand reads of a wave fall in distinct banks); W and Q are loaded two chunks ahead into one of
-// two register sets in the A-operand layout of step 1, U into the lanes that form Delta.
+// One workgroup per (16 value columns, head, sequence), four compute waves and one memory wave.
+// S[:, 16 cb .. 16 cb + 16) lives in the compute waves' MFMA accumulators, wave w < 4 holding key rows
+// 32 w .. 32 w + 31 (two 16 x 16 blocks; lane: rows 32 w + 16 b + 4 kg + r, column li).  Per chunk c,
+// two barriers:
+//   1. each compute wave's share of W S0 (its 32 key rows; its S accumulators serve as the B operand
+//      directly, the contraction taken as j = 32 w + 16 b + 4 kg + r), then of Q S0, whose MFMAs run
+//      on while the wave waits at the barrier;
+//   2. Delta = U - (sum of the four shares of W S0, fixed order); waves 0 and 1 meanwhile form the O rows
+//      of chunk c - 1 in LDS: P Delta (MFMA) + e^gam (sum of its Q S0 shares);
+//   3. the Q S0 shares of chunk c; S = e^gam_last S + K^T (e^(gam_last - gam) Delta).
+// Only W S0 -> Delta -> S is on the chunk-to-chunk path.  The compute waves load W and Q (two chunks
+// ahead, into one of two register sets in the A-operand layout of step 1) and nothing else; wave 4
+// loads K, P, U and the decay factors into the LDS set of the chunk (double-buffered by parity; K rows
+// with their 16-float column groups XOR-swizzled by row, so the K^T operand reads fall in distinct
+// banks) and stores the O rows, as whole 2 KB blocks of out[head][column block][T][16].  A wave's
+// loads and stores wait in one counter, so kept out of the compute waves, the stores' acknowledgements
+// never hold up a chunk.
 struct OtPre {
-  float4v W[2][2], Q[2][2], K[4], P;
-  float U0, U1, E, L;
+  float4v W[2][2], Q[2][2];
 };
+constexpr int kStateThreads = 320;
+// dynamic LDS of ot_delta_state_kernel, floats: K [2][kDC][128], P [2][kDC][kDC], U [kDC][16],
+// e^gam [2][kDC], e^(gam_last - gam) [2][kDC], Delta [2][kDC][16], W S0 and Q S0 shares [4][kDC][16]
+// each, O [kDC][16]
+constexpr int kSK = 0, kSP = kSK + 2 * kDC * kLK, kSU = kSP + 2 * kDC * kDC, kSE = kSU + kDC * 16;
+constexpr int kSL = kSE + 2 * kDC, kSD = kSL + 2 * kDC, kSPW = kSD + 2 * kDC * 16, kSPQ = kSPW + 4 * kDC * 16;
+constexpr int kSO = kSPQ + 4 * kDC * 16, kStateLdsFloats = kSO + kDC * 16;
 
 __device__ __forceinline__ int ot_kswz(int row, int col) { return row * kLK + (col ^ ((row & 3) << 4)); }
 
-__global__ __launch_bounds__(256, 1) void ot_delta_state_kernel(const float *__restrict__ qk,
-                                                                const float *__restrict__ ws,
-                                                                const int32_t *__restrict__ seq_row0,
-                                                                const int32_t *__restrict__ seq_n, int nh,
-                                                                float *__restrict__ out) {
-  __shared__ __align__(16) float sK[2][kDC * kLK];
-  __shared__ __align__(16) float sP[2][kDC * kDC];
-  __shared__ float sE[2][kDC], sL[2][kDC];
-  __shared__ __align__(16) float sD[2][kDC * 16];
-  __shared__ __align__(16) float sPW[4][kDC * 16], sPQ[4][kDC * 16];  // per wave: W S0, Q S0 [t][d]
+__global__ __launch_bounds__(kStateThreads, 1) void ot_delta_state_kernel(const float *__restrict__ qk,
+                                                                         const float *__restrict__ ws,
+                                                                         const int32_t *__restrict__ seq_row0,
+                                                                         const int32_t *__restrict__ seq_n, int nh,
+                                                                         int T, float *__restrict__ out) {
+  extern __shared__ float4v smem_v[];
+  float *smem = reinterpret_cast<float *>(smem_v);
+  float *sK[2] = {smem + kSK, smem + kSK + kDC * kLK}, *sP[2] = {smem + kSP, smem + kSP + kDC * kDC};
+  float *sE[2] = {smem + kSE, smem + kSE + kDC}, *sL[2] = {smem + kSL, smem + kSL + kDC};
+  float *sD[2] = {smem + kSD, smem + kSD + kDC * 16};
+  float *sU = smem + kSU, *sO = smem + kSO;
+  auto sPW = [&](int w) { return smem + kSPW + w * kDC * 16; };
+  auto sPQ = [&](int w) { return smem + kSPQ + w * kDC * 16; };
   // grid (heads, column blocks, sequences): consecutive workgroups go to the 8 XCDs in turn, so with
   // x = head the eight column blocks of a head share one XCD and its L2 (each reads the whole chunk's W,
   // Q and K)
   const int h = blockIdx.x, cb = blockIdx.y, sq = blockIdx.z;
   const int row0 = seq_row0[sq], n = seq_n[sq];
   const int nch = (n + kDC - 1) / kDC;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, kg = lane >> 4;
-  const int lw = nh * kLK;
+  const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, kg = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: the role branches are scalar
+  auto record = [&](int c) { return ws + (ot_chunk_slot(sq, row0, c) * nh + h) * kChunkFloats; };
+
+  if (w == 4) {
+    // ---- memory wave: stage chunk c (between the second barrier of chunk c - 1 and the first of
+    // chunk c, when nothing reads its LDS set or U), store the O rows of chunk c - 2, load chunk c + 1
+    float4v rK[16], rP[4], rU[2];
+    float rE = 0.0f, rL = 0.0f;
+    auto load = [&](int c) {
+      const float *rec = record(c);
+      const int t0 = c * kDC, m = min(kDC, n - t0);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int idx = lane + 64 * e, i = idx >> 5, c4 = idx & 31;
+        const int64_t r = row0 + t0 + min(i, m - 1);
+        rK[e] = reinterpret_cast<const float4v *>(qk + (r * nh + h) * (2 * kLK) + kLK)[c4];
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rP[e] = reinterpret_cast<const float4v *>(rec + kOffP)[lane + 64 * e];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int idx = lane + 64 * e;
+        rU[e] = *reinterpret_cast<const float4v *>(rec + kOffU + (idx >> 2) * kLK + cb * 16 + 4 * (idx & 3));
+      }
+      rE = rec[kOffE + (lane & (kDC - 1))];
+      rL = rec[kOffL + (lane & (kDC - 1))];
+    };
+    auto stage = [&](int X) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int idx = lane + 64 * e, i = idx >> 5, c4 = idx & 31;
+        *reinterpret_cast<float4v *>(sK[X] + ot_kswz(i, 4 * c4)) = rK[e];
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) reinterpret_cast<float4v *>(sP[X])[lane + 64 * e] = rP[e];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) reinterpret_cast<float4v *>(sU)[lane + 64 * e] = rU[e];
+      if (lane < kDC) {
+        sE[X][lane] = rE;
+        sL[X][lane] = rL;
+      }
+    };
+    auto store_o = [&](int cc) {
+      const int t0 = cc * kDC, m = min(kDC, n - t0);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int idx = lane + 64 * e, t = idx >> 2;
+        if (t < m)
+          *reinterpret_cast<float4v *>(out + ((int64_t(h) * (kLK / 16) + cb) * T + row0 + t0 + t) * 16 + 4 * (idx & 3)) =
+              reinterpret_cast<const float4v *>(sO)[idx];
+      }
+    };
+    if (nch > 0) load(0);
+    for (int c = 0; c < nch; ++c) {
+      stage(c & 1);
+      if (c >= 2) store_o(c - 2);
+      if (c + 1 < nch) load(c + 1);
+      __syncthreads();
+      __syncthreads();
+    }
+    __syncthreads();
+    if (nch >= 2) store_o(nch - 2);
+    __syncthreads();
+    __syncthreads();
+    if (nch >= 1) store_o(nch - 1);
+    return;
+  }
+
+  // ---- compute waves
   auto load = [&](int c, OtPre &p) {
-    const float *rec = ws + (ot_chunk_slot(sq, row0, c) * nh + h) * kChunkFloats;
+    const float *rec = record(c);
     const int t0 = c * kDC, m = min(kDC, n - t0);
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb)
@@ -258,38 +339,10 @@ __global__ __launch_bounds__(256, 1) void ot_delta_state_kernel(const float *__r
         const int64_t r = row0 + t0 + min(t, m - 1);
         p.Q[tb][b] = *reinterpret_cast<const float4v *>(qk + (r * nh + h) * (2 * kLK) + j);
       }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int idx = tid + 256 * e, i = idx >> 5, c4 = idx & 31;
-      const int64_t r = row0 + t0 + min(i, m - 1);
-      p.K[e] = reinterpret_cast<const float4v *>(qk + (r * nh + h) * (2 * kLK) + kLK)[c4];
-    }
-    p.P = reinterpret_cast<const float4v *>(rec + kOffP)[tid];
-    p.U0 = rec[kOffU + (tid >> 4) * kLK + cb * 16 + (tid & 15)];
-    p.U1 = rec[kOffU + (16 + (tid >> 4)) * kLK + cb * 16 + (tid & 15)];
-    p.E = rec[kOffE + (tid & (kDC - 1))];
-    p.L = rec[kOffL + (tid & (kDC - 1))];
-  };
-  auto stage = [&](const OtPre &p, int X) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int idx = tid + 256 * e, i = idx >> 5, c4 = idx & 31;
-      *reinterpret_cast<float4v *>(sK[X] + ot_kswz(i, 4 * c4)) = p.K[e];
-    }
-    reinterpret_cast<float4v *>(sP[X])[tid] = p.P;
-    if (tid < kDC) {
-      sE[X][tid] = p.E;
-      sL[X][tid] = p.L;
-    }
   };
   // O rows t = 16 w + 4 kg + r (column li) of chunk cc from LDS set Y: P Delta over the chunk's tokens
-  // s = 4 q + kg (P is zero above its diagonal), then + e^gam_t (sum of the Q S0 shares).  Kept in
-  // registers and stored by store_o at the start of the next chunk, right after the wait for that
-  // chunk's operands: a store waits in the same counter as the loads, and issued there it has a whole
-  // chunk to complete before the next such wait
-  float4v ov = {0.0f, 0.0f, 0.0f, 0.0f};
-  int o_chunk = -1;
-  auto emit_o = [&](int cc, int Y) {
+  // s = 4 q + kg (P is zero above its diagonal), then + e^gam_t (sum of the Q S0 shares), into sO
+  auto emit_o = [&](int Y) {
     float4v po = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int q = 0; q < kDC / 4; ++q) {
@@ -299,20 +352,9 @@ __global__ __launch_bounds__(256, 1) void ot_delta_state_kernel(const float *__r
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 16 * w + 4 * kg + r, e = t * 16 + li;
-      const float qs = ((sPQ[0][e] + sPQ[1][e]) + sPQ[2][e]) + sPQ[3][e];
-      ov[r] = fmaf(sE[Y][t], qs, po[r]);
+      const float qs = ((sPQ(0)[e] + sPQ(1)[e]) + sPQ(2)[e]) + sPQ(3)[e];
+      sO[e] = fmaf(sE[Y][t], qs, po[r]);
     }
-    o_chunk = cc;
-  };
-  auto store_o = [&] {
-    if (o_chunk < 0) return;
-    const int t0 = o_chunk * kDC, m = min(kDC, n - t0);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = 16 * w + 4 * kg + r;
-      if (t < m) out[int64_t(row0 + t0 + t) * lw + h * kLK + cb * 16 + li] = ov[r];
-    }
-    o_chunk = -1;
   };
   float4v S[2];
 #pragma unroll
@@ -320,9 +362,6 @@ __global__ __launch_bounds__(256, 1) void ot_delta_state_kernel(const float *__r
   // chunk c from cur, which then takes chunk c + 2
   auto body = [&](int c, OtPre &cur) {
     const int X = c & 1;
-    stage(cur, X);
-    if (w < 2) store_o();
-    const float u0 = cur.U0, u1 = cur.U1;
     float4v aW[2][2], aQ[2][2];
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb)
@@ -345,7 +384,7 @@ __global__ __launch_bounds__(256, 1) void ot_delta_state_kernel(const float *__r
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sPW[w][(16 * tb + 4 * kg + r) * 16 + li] = dw[tb][r];
+      for (int r = 0; r < 4; ++r) sPW(w)[(16 * tb + 4 * kg + r) * 16 + li] = dw[tb][r];
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -353,20 +392,20 @@ __global__ __launch_bounds__(256, 1) void ot_delta_state_kernel(const float *__r
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) dq[tb] = __builtin_amdgcn_mfma_f32_16x16x4f32(aQ[tb][b][r], S[b][r], dq[tb], 0, 0, 0);
     __syncthreads();
-    // 2. Delta: entries e = tid (t = tid / 16) and tid + 256 (t = 16 + tid / 16), d = tid % 16
+    // 2. Delta: entries e = tid and tid + 256 (t = e / 16, d = e % 16)
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       const int e = tid + 256 * k;
-      const float ws0 = ((sPW[0][e] + sPW[1][e]) + sPW[2][e]) + sPW[3][e];
-      sD[X][e] = (k ? u1 : u0) - ws0;
+      const float ws0 = ((sPW(0)[e] + sPW(1)[e]) + sPW(2)[e]) + sPW(3)[e];
+      sD[X][e] = sU[e] - ws0;
     }
-    if (c > 0 && w < 2) emit_o(c - 1, X ^ 1);
+    if (c > 0 && w < 2) emit_o(X ^ 1);
     __syncthreads();
     // 3. this chunk's Q S0 shares; S = e^gam_last S + K^T Delta_scaled over the tokens t = 4 s + kg
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sPQ[w][(16 * tb + 4 * kg + r) * 16 + li] = dq[tb][r];
+      for (int r = 0; r < 4; ++r) sPQ(w)[(16 * tb + 4 * kg + r) * 16 + li] = dq[tb][r];
     const float gl = sE[X][kDC - 1];
 #pragma unroll
     for (int b = 0; b < 2; ++b) S[b] = S[b] * gl;
@@ -386,12 +425,10 @@ __global__ __launch_bounds__(256, 1) void ot_delta_state_kernel(const float *__r
     body(c, pa);
     if (c + 1 < nch) body(c + 1, pb);
   }
-  __syncthreads();  // the last chunk's Q S0 shares
-  if (nch > 0 && w < 2) {
-    store_o();  // chunk nch - 2
-    emit_o(nch - 1, (nch - 1) & 1);
-    store_o();
-  }
+  __syncthreads();  // the last chunk's Q S0 shares; the memory wave then stores chunk nch - 2's O
+  __syncthreads();
+  if (nch > 0 && w < 2) emit_o((nch - 1) & 1);
+  __syncthreads();
 }
 
 // ---------------------------------------------------------------- DeltaNet: gated output norm
@@ -404,8 +441,9 @@ __global__ __launch_bounds__(256) void ot_delta_out_kernel(const float *__restri
   const int item = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (item >= T * nh) return;
   const int t = item / nh, h = item % nh, lw = nh * kLK;
-  const float *x = o + int64_t(t) * lw + h * kLK;
-  const float x0 = x[lane], x1 = x[lane + 64];
+  // o is [head][column block of 16][T][16] (the scan's layout)
+  const float *x = o + (int64_t(h) * (kLK / 16) * T + t) * 16;
+  const float x0 = x[(lane >> 4) * int64_t(T) * 16 + (lane & 15)], x1 = x[((lane >> 4) + 4) * int64_t(T) * 16 + (lane & 15)];
   const float ss = wave_sum_dpp(x0 * x0 + x1 * x1);
   const float sc = 1.0f / sqrtf(ss / 128.0f + 1e-6f);
   const float *z = proj + int64_t(t) * ldp + zcol + h * kLK;
@@ -802,16 +840,18 @@ void launch_ot_delta_prep(const float *proj, int ldp, int T, const int32_t *tok_
 size_t ot_delta_chunk_floats(int T, int nseq, int nh) { return size_t(nseq + T / kDC + 1) * nh * kChunkFloats; }
 
 void launch_ot_delta_scan(const float *qk, const float *vbuf, const float *gb, const int32_t *seq_row0,
-                          const int32_t *seq_n, int nseq, int max_n, int nh, float *chunk_ws, float *out,
+                          const int32_t *seq_n, int nseq, int T, int max_n, int nh, float *chunk_ws, float *out,
                           hipStream_t st) {
   LG_REQUIRE(nseq > 0 && nseq <= 65535 && nh > 0 && nh <= 65535, "delta scan: bad shape nseq=%d nh=%d", nseq, nh);
-  LG_REQUIRE(max_n > 0 && chunk_ws, "delta scan: no tokens or no chunk workspace");
+  LG_REQUIRE(max_n > 0 && max_n <= T && chunk_ws, "delta scan: no tokens or no chunk workspace");
   const int maxch = (max_n + kDC - 1) / kDC;
   hipLaunchKernelGGL(ot_delta_chunk_kernel, dim3(maxch, nh, nseq), dim3(256), 0, st, qk, vbuf, gb, seq_row0, seq_n,
                      nh, chunk_ws);
   HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(ot_delta_state_kernel, dim3(nh, kLK / 16, nseq), dim3(256), 0, st, qk, chunk_ws, seq_row0, seq_n,
-                     nh, out);
+  const size_t lds = size_t(kStateLdsFloats) * sizeof(float);
+  grant_lds(reinterpret_cast<const void *>(&ot_delta_state_kernel), lds);
+  hipLaunchKernelGGL(ot_delta_state_kernel, dim3(nh, kLK / 16, nseq), dim3(kStateThreads), lds, st, qk, chunk_ws,
+                     seq_row0, seq_n, nh, T, out);
   HIP_CHECK(hipGetLastError());
 }
 

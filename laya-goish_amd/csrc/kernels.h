@@ -263,14 +263,16 @@ void launch_dequant_repacked(const DevMatrix &w, float *dst, hipStream_t st);
 void launch_ot_delta_prep(const float *proj, int ldp, int T, const int32_t *tok_pos, const float *conv,
                           const float *alog, const float *dt, int nh, float *qk, float *vbuf, float *gb,
                           hipStream_t st);
-// The recurrent scan over each sequence (rows seq_row0[s] .. + seq_n[s], the longest max_n tokens):
-// out[T][nh*128], in chunks of 32 tokens (two launches: the chunks' local terms in parallel, then
-// the state carried from chunk to chunk).  chunk_ws holds ot_delta_chunk_floats(T, nseq, nh) floats.
+// The recurrent scan over each sequence (rows seq_row0[s] .. + seq_n[s] of T, the longest max_n tokens):
+// out[nh][8][T][16] (head, block of 16 value columns, row), in chunks of 32 tokens (two launches: the
+// chunks' local terms in parallel, then the state carried from chunk to chunk).  chunk_ws holds
+// ot_delta_chunk_floats(T, nseq, nh) floats.
 size_t ot_delta_chunk_floats(int T, int nseq, int nh);
 void launch_ot_delta_scan(const float *qk, const float *vbuf, const float *gb, const int32_t *seq_row0,
-                          const int32_t *seq_n, int nseq, int max_n, int nh, float *chunk_ws, float *out,
+                          const int32_t *seq_n, int nseq, int T, int max_n, int nh, float *chunk_ws, float *out,
                           hipStream_t st);
-// rms(out head, norm_w) * silu(z) with z at column zcol of the projection row -> f16 planes.
+// rms(out head, norm_w) * silu(z) with z at column zcol of the projection row -> f16 planes; out in the
+// scan's layout.
 void launch_ot_delta_out(const float *o, int T, int nh, const float *norm_w, const float *proj, int ldp, int zcol,
                          _Float16 *y, _Float16 *ylo, hipStream_t st);
 // Full attention: per-head q/k rms (weights 1 + w) + partial RoPE (tables [pos][32]) from the
