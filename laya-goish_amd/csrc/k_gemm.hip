@@ -33,6 +33,11 @@ void launch_kind(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix 
         (glu ? launch_cfg<KIND, SPLIT, 128, 1, 2, 2>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)
              : launch_cfg<KIND, SPLIT, 128, 1, 1, 2>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st)))
       return;
+    // a few hundred rows over a deep K (narrow outputs, K >= 2048): 32 x 64 tiles over two LDS stages, four
+    // times the workgroups of 64 x 128 (480 rows, N 1024: K 2048 27.6 -> 14.0 us, K 3584 47.1 -> 22.2 us)
+    if (!glu && int64_t((M + 63) / 64) * (outN / 128) < 128 && W.cols >= 2048 && W.cols % 128 == 0 &&
+        launch_cfg<KIND, SPLIT, 128, 1, 2, 2>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st))
+      return;
     // a handful of 64 x 128 tiles (a few dozen rows, narrow outputs): 64 x 64 tiles, twice again
     if (!glu && (M + 63) / 64 * (outN / 128) < 64 && W.cols % 128 == 0 &&
         launch_cfg<KIND, SPLIT, 128, 2, 2, 1>(A, Alo, M, W, epi, C, C16, C16lo, ldc, bias, st))

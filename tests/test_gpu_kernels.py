@@ -226,3 +226,22 @@ def test_exact_gemm_tilings_agree(lh, preset):
             assert_bits_equal(eng.matmul(name, x[:M]), big[:M])
             assert_bits_equal(eng.matmul(name, x[:M], bias), big_b[:M])
     eng.close()
+
+
+def test_exact_gemm_deep_k_tilings_agree(lh):
+    """Narrow outputs over a deep K (OpenThai 0.8B shape: out_proj 1024 x 2048, down_proj 1024 x 3584): a
+    few hundred rows take 32 x 64 tiles over two LDS stages, fewer take 32 x 32, 2048 rows 64 x 128; the
+    rows agree bit for bit."""
+    img = lh.SynthImage("openthai-0.8b", seed=5, n_layers=1)
+    eng = lh.Engine(lh.Gguf.from_bytes(img))
+    rng = np.random.default_rng(23)
+    for name in ("model.layers.0.linear_attn.out_proj.weight", "model.layers.0.mlp.down_proj.weight"):
+        _, dims, _ = eng.gguf.tensor(name)
+        cols, rows = dims[0], int(np.prod(dims[1:]))
+        assert cols >= 2048 and rows == 1024, (name, dims)
+        x = rng.standard_normal((2048, cols)).astype(np.float32)
+        big = eng.matmul(name, x)
+        for M in (100, 300, 480, 700):
+            print(f"openthai-0.8b {name} ({rows} x {cols}) M={M}", flush=True)
+            assert_bits_equal(eng.matmul(name, x[:M]), big[:M])
+    eng.close()
