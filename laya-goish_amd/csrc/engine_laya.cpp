@@ -184,6 +184,8 @@ void Engine::load_laya(const Gguf &g) {
     if (y.qkv.w.cols != d || y.qkv.w.rows != 3 * d || y.wo.w.cols != d || y.wo.w.rows != d || y.wi.w.cols != d ||
         y.down.w.rows != d || y.wi.w.rows != y.down.w.cols * (head ? 1 : 2))
       fail(LG_ERR_FORMAT, "inconsistent layer dimensions");
+    // the large-batch 256 x 256 GEMM's operand form (for F16 the weights themselves)
+    for (LayaLinear *x : {&y.qkv, &y.wo, &y.wi, &y.down}) add_prefill_copy(x->w);
     return y;
   };
   laya_embnorm_ = laya_norm(g, graph, 0);

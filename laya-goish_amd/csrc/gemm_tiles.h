@@ -26,6 +26,7 @@
 
 #include <algorithm>
 
+#include "act.h"
 #include "common.h"
 #include "kernels.h"
 #include "f16split.h"
@@ -41,10 +42,6 @@ enum Mode { FAST = 0, SPLIT = 1, SPLIT3 = 2 };
 
 
 __device__ __forceinline__ float silu(float g) { return g * (1.0f / (1.0f + __expf(-g))); }
-// tanh-approximated GELU of src/tensor.rs:129-131
-__device__ __forceinline__ float gelu_tanh(float x) {
-  return 0.5f * x * (1.0f + tanhf(0.7978845608028654f * x * (1.0f + 0.044715f * x * x)));
-}
 
 // f16 bits -> f32 with the hardware conversion (exact for every finite value and infinity;
 // a NaN scale gives NaN outputs either way).

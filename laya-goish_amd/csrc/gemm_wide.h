@@ -30,6 +30,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include "act.h"
 #include "common.h"
 #include "f16split.h"
 #include "kernels.h"
@@ -76,9 +77,9 @@ __device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
 
 __device__ __forceinline__ float silu_f(float g) { return g * (1.0f / (1.0f + __expf(-g))); }
 
-// EPI: Epi values (F32, ADD, SWIGLU) or kEpiRopeKv.  For SWIGLU the workgroup's 256 weight rows are 128 gate
-// rows and the 128 matching up rows: wave column wn holds gate rows in its column blocks 0-3 and
-// the up rows of the same output columns in blocks 4-7.
+// EPI: Epi values (F32, ADD, SWIGLU, GEGLU) or kEpiRopeKv.  For SWIGLU and GEGLU the workgroup's 256 weight
+// rows are 128 gate rows and the 128 matching up rows: wave column wn holds gate rows in its column blocks
+// 0-3 and the up rows of the same output columns in blocks 4-7.
 template <int EPI, int MODE>
 __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
     const _Float16 *__restrict__ A, const _Float16 *__restrict__ Alo, int M, int K,
@@ -88,7 +89,7 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
   using G = Geo<MODE>;
   constexpr bool kScaled = G::kScales;  // WQ8, WQ4: per-chunk scale FMAs over code partial sums
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  constexpr bool kGlu = EPI == int(Epi::SWIGLU);
+  constexpr bool kGlu = EPI == int(Epi::SWIGLU) || EPI == int(Epi::GEGLU);
   const int t = threadIdx.x, lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: scalar DMA setup
   const int wm = wave >> 1, wn = wave & 1;
@@ -472,7 +473,8 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int col = nt * (BN / 2) + wn * 64 + j * 16 + lr;
-          const float v = silu_f(acc[i][j][r]) * acc[i][j + 4][r];
+          const float g = acc[i][j][r];
+          const float v = (EPI == int(Epi::SWIGLU) ? silu_f(g) : gelu_tanh(g)) * acc[i][j + 4][r];
           _Float16 h, hl;
           split_f16(v, h, hl);
           C16[int64_t(row) * ldc + col] = h;

@@ -95,8 +95,10 @@ int wide_mode(int M, const DevMatrix &W, int EPI) {
     case LG_Q6_K: mode = W2; if (!W.pcl) return -1; break;
     default: return -1;
   }
-  if (EPI != int(Epi::F32) && EPI != int(Epi::ADD) && EPI != int(Epi::SWIGLU) && EPI != kEpiRopeKv) return -1;
-  const bool glu = EPI == int(Epi::SWIGLU);
+  if (EPI != int(Epi::F32) && EPI != int(Epi::ADD) && EPI != int(Epi::SWIGLU) && EPI != int(Epi::GEGLU) &&
+      EPI != kEpiRopeKv)
+    return -1;
+  const bool glu = EPI == int(Epi::SWIGLU) || EPI == int(Epi::GEGLU);
   const int N = W.rows, K = W.cols;
   if (K % BK != 0 || N % BN != 0) return -1;  // gated: 128 gate + 128 up rows a tile
   const int NT = glu ? (N / 2) / (BN / 2) : N / BN;
@@ -180,12 +182,13 @@ bool launch_gemm_wide(const _Float16 *A, const _Float16 *Alo, int M, const DevMa
   const int mode = wide_mode(M, W, int(epi));
   if (mode < 0) return false;
   LG_REQUIRE(mode != WQ4 || ks, "gemm: an exact Q4_K launch needs its activation's chunk sums");
-  const bool glu = epi == Epi::SWIGLU;
+  const bool glu = epi == Epi::SWIGLU || epi == Epi::GEGLU;
   const int N = W.rows;
   if (glu ? (C16 == nullptr || ldc < N / 2) : (C == nullptr || ldc < N)) return false;
-  const WideFn fn = epi == Epi::F32   ? wide_fn<int(Epi::F32)>(mode)
-                    : epi == Epi::ADD ? wide_fn<int(Epi::ADD)>(mode)
-                                      : wide_fn<int(Epi::SWIGLU)>(mode);
+  const WideFn fn = epi == Epi::F32      ? wide_fn<int(Epi::F32)>(mode)
+                    : epi == Epi::ADD    ? wide_fn<int(Epi::ADD)>(mode)
+                    : epi == Epi::SWIGLU ? wide_fn<int(Epi::SWIGLU)>(mode)
+                                         : wide_fn<int(Epi::GEGLU)>(mode);
   launch_wide(fn, mode, A, Alo, M, W, glu, C, C16, C16lo, ldc, bias, RopeKvOut{}, st, ks);
   return true;
 }

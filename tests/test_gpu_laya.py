@@ -77,6 +77,25 @@ def test_full_width_matches_oracle(lh, po):
     assert np.abs(gl - wl).max() <= 2e-3 and np.abs(ga - wa).max() <= 2e-3
 
 
+def test_full_width_large_batch_equals_single(lh, po):
+    """The ModernBERT-base shape with 64 inputs of 512 tokens: 32,768 rows put every trunk GEMM on the
+    256 x 256 tiles (GeGLU epilogue included), while an input alone takes the small tiles; the batch rows
+    equal the single runs bit for bit, and the oracle within 2e-3."""
+    img = lh.SynthImage("laya-english", seed=6)
+    eng = lh.Engine(lh.Gguf.from_bytes(img))
+    rng = np.random.default_rng(31)
+    inputs = [(rng.integers(0, 50000, 512), sorted(rng.choice(512, 4, replace=False).tolist()), i % 3) for i in range(64)]
+    print("laya-english: 64 x 512 batch", flush=True)
+    batch = eng.laya_forward(inputs)
+    for i in (0, 41):
+        (sl, sa), = eng.laya_forward([inputs[i]])
+        assert np.array_equal(batch[i][0], sl) and np.array_equal(batch[i][1], sa), f"input {i}"
+    eng.close()
+    om = po.Laya(po.Gguf(img.array()), threads=8)
+    wl, wa = om.forward(*inputs[41])
+    assert np.abs(batch[41][0] - wl).max() <= 2e-3 and np.abs(batch[41][1] - wa).max() <= 2e-3
+
+
 def _request(rng, nq):
     kinds = ("choice", "score", "noul")
     qs = []
