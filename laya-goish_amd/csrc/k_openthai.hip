@@ -630,21 +630,59 @@ __global__ __launch_bounds__(256, 1) void ot_attn_kernel(const float *__restrict
 // Partial (m, l, O) per item and head; ot_attn_combine_kernel merges an item's key ranges.
 constexpr int kQT = 16;    // query rows per item
 constexpr int kKC = 256;   // keys per item
-constexpr int kVTp = 36;   // padded row of the transposed V tile [256 dims][32 keys]
 constexpr int kPp = 36;    // padded row of the P tile [16 rows][32 keys]
 
-// One 32-key tile of K rows and V rows (from the projection) for 256 threads, 8 float4 each;
-// keys past khi are clamped to khi - 1 (masked by the caller).
+// One 32-key tile of K rows and V rows (from the projection) for 256 threads, 8 float4 each; keys past khi
+// are clamped to khi - 1 (masked by the caller).  K: kr[2 j + u] holds dims 8 o + 4 u .. + 3 of key i, with
+// (i, o) = ((tid + 256 j) / 32, (tid + 256 j) % 32); V: vr[u] holds dims 4 (tid % 64) .. + 3 of key
+// 8 (tid / 64) + u.  So a thread stages 8 consecutive dims of a K row, and 8 consecutive keys of each of 4
+// rows of the transposed V tile, as 16-byte groups.
 __device__ __forceinline__ void ot_load_kv(float4v (&kr)[8], float4v (&vr)[8], const float *__restrict__ Kb,
                                            const float *__restrict__ proj, int ldp, int kvw, int vcol, int kcol,
                                            int srow, int kt, int khi, int tid) {
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int e = tid + 256 * k, i = e >> 6, c4 = e & 63;
+  for (int j = 0; j < 4; ++j) {
+    const int e = tid + 256 * j, i = e >> 5, o = e & 31;
     const int key = min(kt * kAT + i, khi - 1);
-    kr[k] = reinterpret_cast<const float4v *>(Kb + int64_t(srow + key) * kvw + kcol)[c4];
-    vr[k] = reinterpret_cast<const float4v *>(proj + int64_t(srow + key) * ldp + vcol)[c4];
+    const float4v *kp = reinterpret_cast<const float4v *>(Kb + int64_t(srow + key) * kvw + kcol + 8 * o);
+    kr[2 * j] = kp[0];
+    kr[2 * j + 1] = kp[1];
   }
+  const int oc = tid >> 6, c4 = tid & 63;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int key = min(kt * kAT + 8 * oc + u, khi - 1);
+    vr[u] = reinterpret_cast<const float4v *>(proj + int64_t(srow + key) * ldp + vcol)[c4];
+  }
+}
+
+// The products on v_mfma_f32_16x16x32_f16 with every f32 operand split into f16 hi + lo (hi = f16(x),
+// lo = f16(x - hi)) and three products per pair (lo.hi, hi.lo, hi.hi; ~22 significant bits, f32
+// accumulation): Q split once into registers, each K and V tile split as it is staged, P as it is read
+// back.  LDS (dynamic): K hi and lo [32 keys][kKh], the transposed V tile hi and lo [256 dims][kVh], and each
+// wave's f32 P tile [16 rows][kPp].
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+constexpr int kKh = kHD + 8;  // halves a staged K row (16 bytes of padding)
+constexpr int kVh = kAT + 8;  // halves a staged V^T row
+constexpr int kAttnLdsBytes = 2 * (2 * kAT * kKh + 2 * kHD * kVh) + 4 * 4 * kQT * kPp;
+
+__device__ __forceinline__ void split8(float4v a, float4v b, half8v &hi, half8v &lo) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    _Float16 h, l;
+    split_f16(a[c], h, l);
+    hi[c] = h;
+    lo[c] = l;
+    split_f16(b[c], h, l);
+    hi[4 + c] = h;
+    lo[4 + c] = l;
+  }
+}
+
+__device__ __forceinline__ float4v mfma3h(half8v ah, half8v al, half8v bh, half8v bl, float4v acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, acc, 0, 0, 0);
 }
 
 __global__ __launch_bounds__(256, 1) void ot_attn_part_kernel(
@@ -652,10 +690,10 @@ __global__ __launch_bounds__(256, 1) void ot_attn_part_kernel(
     int hkv, const int32_t *__restrict__ it_row0, const int32_t *__restrict__ it_pos0,
     const int32_t *__restrict__ it_nq, const int32_t *__restrict__ it_klo, const int32_t *__restrict__ it_khi,
     float *__restrict__ part) {
-  __shared__ __align__(16) float sK[kAT * kHDp];   // [32 keys][260]
-  __shared__ __align__(16) float sVT[kHD * kVTp];  // [256 dims][36]
-  __shared__ __align__(16) float sP[4][kQT * kPp]; // per wave [16 rows][36]
-  __shared__ __align__(16) float sQ[4][kQT * kHDp]; // per wave [16 rows][260]
+  extern __shared__ float4v attn_smem[];
+  _Float16 *sKh = reinterpret_cast<_Float16 *>(attn_smem), *sKl = sKh + kAT * kKh;
+  _Float16 *sVh = sKl + kAT * kKh, *sVl = sVh + kHD * kVh;
+  float *sP = reinterpret_cast<float *>(sVl + kHD * kVh);  // [4 waves][16 rows][kPp]
   const int item = blockIdx.x;
   const int row0 = it_row0[item], pos0 = it_pos0[item], nq = it_nq[item];
   const int klo = it_klo[item], khi = it_khi[item];
@@ -665,13 +703,15 @@ __global__ __launch_bounds__(256, 1) void ot_attn_part_kernel(
   const int kh = (blockIdx.y * 4) / (hq / hkv);
   const int qw = hq * kHD, kvw = hkv * kHD;
   const int li = l & 15, kg = l >> 4;
-  // this wave's Q rows into LDS (rows past nq repeat row nq - 1 and are never written out)
-  float *myQ = sQ[w];
+  // this wave's Q rows as A operands: row li (rows past nq repeat row nq - 1 and are never written out),
+  // dims 32 s + 8 kg .. + 7 of k-step s
+  half8v qh[8], ql[8];
+  {
+    const float *qr = Qb + int64_t(row0 + min(li, nq - 1)) * qw + h * kHD;
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int e = l + 64 * k, i = e >> 6, c4 = e & 63;
-    *reinterpret_cast<float4 *>(myQ + i * kHDp + c4 * 4) =
-        reinterpret_cast<const float4 *>(Qb + int64_t(row0 + min(i, nq - 1)) * qw + h * kHD)[c4];
+    for (int st = 0; st < 8; ++st)
+      split8(*reinterpret_cast<const float4v *>(qr + 32 * st + 8 * kg),
+             *reinterpret_cast<const float4v *>(qr + 32 * st + 8 * kg + 4), qh[st], ql[st]);
   }
   float4v acc_o[16];
 #pragma unroll
@@ -685,36 +725,45 @@ __global__ __launch_bounds__(256, 1) void ot_attn_part_kernel(
   const int kt0 = klo / kAT, kt1 = (khi + kAT - 1) / kAT;
   float4v kr[8], vr[8];
   ot_load_kv(kr, vr, Kb, proj, ldp, kvw, 2 * qw + kvw + kh * kHD, kh * kHD, srow, kt0, khi, tid);
-  float *myP = sP[w];
+  float *myP = sP + w * (kQT * kPp);
   for (int kt = kt0; kt < kt1; ++kt) {
     __syncthreads();  // previous tile's readers are done
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int e = tid + 256 * k, i = e >> 6, c4 = e & 63;
-      *reinterpret_cast<float4v *>(sK + i * kHDp + c4 * 4) = kr[k];
-      sVT[(c4 * 4 + 0) * kVTp + i] = vr[k][0];
-      sVT[(c4 * 4 + 1) * kVTp + i] = vr[k][1];
-      sVT[(c4 * 4 + 2) * kVTp + i] = vr[k][2];
-      sVT[(c4 * 4 + 3) * kVTp + i] = vr[k][3];
+    for (int j = 0; j < 4; ++j) {
+      const int e = tid + 256 * j, i = e >> 5, o = e & 31;
+      half8v h8, l8;
+      split8(kr[2 * j], kr[2 * j + 1], h8, l8);
+      *reinterpret_cast<half8v *>(sKh + i * kKh + 8 * o) = h8;
+      *reinterpret_cast<half8v *>(sKl + i * kKh + 8 * o) = l8;
+    }
+    {
+      const int oc = tid >> 6, c4 = tid & 63;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        half8v h8, l8;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          _Float16 hh, ll;
+          split_f16(vr[u][c], hh, ll);
+          h8[u] = hh;
+          l8[u] = ll;
+        }
+        *reinterpret_cast<half8v *>(sVh + (4 * c4 + c) * kVh + 8 * oc) = h8;
+        *reinterpret_cast<half8v *>(sVl + (4 * c4 + c) * kVh + 8 * oc) = l8;
+      }
     }
     __syncthreads();
     // next tile's loads, unconditional (the last iteration reloads its own tile)
     ot_load_kv(kr, vr, Kb, proj, ldp, kvw, 2 * qw + kvw + kh * kHD, kh * kHD, srow, min(kt + 1, kt1 - 1), khi, tid);
-    // S = Q K^T, two 16x16 blocks of keys
+    // S = Q K^T, two 16x16 blocks of keys: B = K[16 kb + li][32 s + 8 kg .. + 7]
     float4v s0 = {0.0f, 0.0f, 0.0f, 0.0f}, s1 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int g = 0; g < 16; ++g) {
-      const float4 qg = *reinterpret_cast<const float4 *>(myQ + li * kHDp + 16 * g + 4 * kg);
-      const float4 ka = *reinterpret_cast<const float4 *>(sK + li * kHDp + 16 * g + 4 * kg);
-      const float4 kb = *reinterpret_cast<const float4 *>(sK + (16 + li) * kHDp + 16 * g + 4 * kg);
-      s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.x, ka.x, s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.x, kb.x, s1, 0, 0, 0);
-      s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.y, ka.y, s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.y, kb.y, s1, 0, 0, 0);
-      s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.z, ka.z, s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.z, kb.z, s1, 0, 0, 0);
-      s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.w, ka.w, s0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qg.w, kb.w, s1, 0, 0, 0);
+    for (int st = 0; st < 8; ++st) {
+      const int o0 = li * kKh + 32 * st + 8 * kg, o1 = (16 + li) * kKh + 32 * st + 8 * kg;
+      s0 = mfma3h(qh[st], ql[st], *reinterpret_cast<const half8v *>(sKh + o0), *reinterpret_cast<const half8v *>(sKl + o0),
+                  s0);
+      s1 = mfma3h(qh[st], ql[st], *reinterpret_cast<const half8v *>(sKh + o1), *reinterpret_cast<const half8v *>(sKl + o1),
+                  s1);
     }
     // scale, mask, online softmax; lane holds rows 4 kg + r, keys li and 16 + li
     const int key0 = kt * kAT + li, key1 = key0 + 16;
@@ -748,17 +797,16 @@ __global__ __launch_bounds__(256, 1) void ot_attn_part_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc_o[b][r] *= corr[r];
     }
-    // O += P V: A = P[li][16u + 4kg + c], B = V[16u + 4kg + c][16b + li]
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const float4 pa = *reinterpret_cast<const float4 *>(myP + li * kPp + 16 * u + 4 * kg);
+    // O += P V over the tile's 32 keys in one k-step: A = P[li][8 kg .. + 7], B = V[8 kg .. + 7][16 b + li]
+    {
+      half8v ph, pl;
+      split8(*reinterpret_cast<const float4v *>(myP + li * kPp + 8 * kg),
+             *reinterpret_cast<const float4v *>(myP + li * kPp + 8 * kg + 4), ph, pl);
 #pragma unroll
       for (int b = 0; b < 16; ++b) {
-        const float4 vb = *reinterpret_cast<const float4 *>(sVT + (16 * b + li) * kVTp + 16 * u + 4 * kg);
-        acc_o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.x, vb.x, acc_o[b], 0, 0, 0);
-        acc_o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.y, vb.y, acc_o[b], 0, 0, 0);
-        acc_o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.z, vb.z, acc_o[b], 0, 0, 0);
-        acc_o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa.w, vb.w, acc_o[b], 0, 0, 0);
+        const int o = (16 * b + li) * kVh + 8 * kg;
+        acc_o[b] = mfma3h(ph, pl, *reinterpret_cast<const half8v *>(sVh + o), *reinterpret_cast<const half8v *>(sVl + o),
+                          acc_o[b]);
       }
     }
   }
@@ -895,8 +943,9 @@ void launch_ot_attn_mfma(const float *Qb, const float *Kb, const float *proj, in
   LG_REQUIRE(nitems > 0 && ncomb > 0 && hq > 0 && hkv > 0 && hq % hkv == 0 && (hq / hkv) % 4 == 0,
              "attn: MFMA path needs groups of 4 query heads per KV head (heads %d/%d)", hq, hkv);
   LG_REQUIRE(ldp % 4 == 0 && ldp >= (2 * hq + 2 * hkv) * kHD, "attn: projection row %d too short", ldp);
-  launch_timed(ot_attn_part_kernel, dim3(nitems, hq / 4), dim3(256), 0, st, Qb, Kb, proj, ldp, hq, hkv, it_row0,
-               it_pos0, it_nq, it_klo, it_khi, part);
+  grant_lds(reinterpret_cast<const void *>(&ot_attn_part_kernel), size_t(kAttnLdsBytes));
+  launch_timed(ot_attn_part_kernel, dim3(nitems, hq / 4), dim3(256), size_t(kAttnLdsBytes), st, Qb, Kb, proj, ldp, hq,
+               hkv, it_row0, it_pos0, it_nq, it_klo, it_khi, part);
   HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(ot_attn_combine_kernel, dim3(ncomb, hq), dim3(256), 0, st, part, proj, ldp, hq, cb_row0, cb_nq,
                      cb_first, cb_n, y, ylo);
