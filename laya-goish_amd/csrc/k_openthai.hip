@@ -43,7 +43,7 @@ __device__ __forceinline__ void store_planes(_Float16 *hi, _Float16 *lo, int64_t
 // in the sequence; rows of one sequence are consecutive), silu, then per head
 // query = q / |q| / sqrt(128), key = k / |k| (|x| = sqrt(x.x + 1e-6)), log-decay and beta.
 // model.rs:306-318 (conv), :323-331 (scales, decay, beta).
-__global__ __launch_bounds__(256) void ot_delta_prep_kernel(const float *__restrict__ proj, int ldp,
+__global__ __launch_bounds__(256) void ot_delta_prep_kernel(const float *__restrict__ proj, int ldp, int T,
                                                             const int32_t *__restrict__ tok_pos,
                                                             const float *__restrict__ conv,
                                                             const float *__restrict__ alog,
@@ -51,18 +51,33 @@ __global__ __launch_bounds__(256) void ot_delta_prep_kernel(const float *__restr
                                                             float *__restrict__ qk, float *__restrict__ vbuf,
                                                             float *__restrict__ gb) {
   extern __shared__ float s_x[];
-  const int t = blockIdx.x;
+  // consecutive workgroups go to the 8 XCDs in turn: XCD x takes tokens x * per .. + per - 1, so the three
+  // rows before a token that its conv reads were read by the XCD's previous tokens and sit in its L2 (the
+  // grid is 8 * per workgroups; those past T have no token)
+  const int per = int(gridDim.x) >> 3, t = int(blockIdx.x & 7) * per + int(blockIdx.x >> 3);
+  if (t >= T) return;
   const int lw = nh * kLK, cd = 3 * lw;
   const int pos = tok_pos[t];
   const float *row = proj + int64_t(t) * ldp;
-  for (int c = threadIdx.x; c < cd; c += 256) {
-    const float4 w = reinterpret_cast<const float4 *>(conv)[c];
-    float v = 0.0f;
-    if (pos >= 3) v = v + row[c - 3 * int64_t(ldp)] * w.x;
-    if (pos >= 2) v = v + row[c - 2 * int64_t(ldp)] * w.y;
-    if (pos >= 1) v = v + row[c - int64_t(ldp)] * w.z;
-    v = v + row[c] * w.w;
-    s_x[c] = siluf_(v);
+  // four channels a thread: one 16-byte load per tap row and four of taps (conv is [channel][4 taps])
+  const float4v zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c = 4 * threadIdx.x; c < cd; c += 4 * 256) {
+    const float4v x0 = *reinterpret_cast<const float4v *>(row + c);
+    const float4v x1 = pos >= 1 ? *reinterpret_cast<const float4v *>(row + c - int64_t(ldp)) : zero4;
+    const float4v x2 = pos >= 2 ? *reinterpret_cast<const float4v *>(row + c - 2 * int64_t(ldp)) : zero4;
+    const float4v x3 = pos >= 3 ? *reinterpret_cast<const float4v *>(row + c - 3 * int64_t(ldp)) : zero4;
+    float4v o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float4 w = reinterpret_cast<const float4 *>(conv)[c + e];
+      float v = 0.0f;
+      if (pos >= 3) v = v + x3[e] * w.x;
+      if (pos >= 2) v = v + x2[e] * w.y;
+      if (pos >= 1) v = v + x1[e] * w.z;
+      v = v + x0[e] * w.w;
+      o[e] = siluf_(v);
+    }
+    *reinterpret_cast<float4v *>(s_x + c) = o;
   }
   __syncthreads();
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -77,7 +92,8 @@ __global__ __launch_bounds__(256) void ot_delta_prep_kernel(const float *__restr
     dst[lane] = x0 * sc;
     dst[lane + 64] = x1 * sc;
   }
-  for (int c = threadIdx.x; c < lw; c += 256) vbuf[int64_t(t) * lw + c] = s_x[2 * lw + c];
+  for (int c = 4 * threadIdx.x; c < lw; c += 4 * 256)
+    *reinterpret_cast<float4v *>(vbuf + int64_t(t) * lw + c) = *reinterpret_cast<const float4v *>(s_x + 2 * lw + c);
   if (threadIdx.x < nh) {
     const int h = threadIdx.x;
     const float a = row[cd + lw + h], b = row[cd + lw + nh + h];
@@ -880,7 +896,8 @@ void launch_ot_delta_prep(const float *proj, int ldp, int T, const int32_t *tok_
   LG_REQUIRE(T > 0 && nh > 0 && nh <= 32, "delta prep: bad shape T=%d nh=%d", T, nh);
   LG_REQUIRE(ldp % 4 == 0 && ldp >= 3 * nh * kLK + nh * kLK + 2 * nh, "delta prep: projection row %d too short", ldp);
   const size_t lds = size_t(3) * nh * kLK * sizeof(float);
-  hipLaunchKernelGGL(ot_delta_prep_kernel, dim3(T), dim3(256), lds, st, proj, ldp, tok_pos, conv, alog, dt, nh,
+  const int per = (T + 7) / 8;
+  hipLaunchKernelGGL(ot_delta_prep_kernel, dim3(8 * per), dim3(256), lds, st, proj, ldp, T, tok_pos, conv, alog, dt, nh,
                      qk, vbuf, gb);
   HIP_CHECK(hipGetLastError());
 }
