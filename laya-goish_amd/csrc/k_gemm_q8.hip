@@ -103,8 +103,11 @@ int wide_mode(int M, const DevMatrix &W, int EPI) {
   if (K % BK != 0 || N % BN != 0) return -1;  // gated: 128 gate + 128 up rows a tile
   const int NT = glu ? (N / 2) / (BN / 2) : N / BN;
   if (int64_t(N) * K * 2 >= (int64_t(1) << 32)) return -1;  // 32-bit buffer offsets of the weights
-  // fewer 256 x 256 tiles than CUs leaves CUs idle: the 128 x 128 tiles fill the device better
-  if (int64_t((M + BM - 1) / BM) * NT < device_cus()) return -1;
+  // fewer 256 x 256 tiles than 5/8 of the CUs leaves too many idle: the 128 x 128 tiles fill the device
+  // better.  Between that and one tile per CU the 256 x 256 tiles still win (F16 at 1437 rows x 7168 gated,
+  // 168 tiles: 50.3 against 60.0 us; 2048 x 6144, 192 tiles: 91.7 against 120.4; 3000 x 5120, 240 tiles:
+  // 57.1 against 77.2), and below it they lose (1437 x 5120, 120 tiles: 48.1 against 41.8)
+  if (int64_t((M + BM - 1) / BM) * NT * 8 < int64_t(device_cus()) * 5) return -1;
   return mode;
 }
 
