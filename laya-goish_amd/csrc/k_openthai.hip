@@ -855,37 +855,67 @@ __global__ __launch_bounds__(256) void ot_attn_combine_kernel(const float *__res
   if (r >= nq) return;
   const int64_t stride = int64_t(hq) * (kQT * kHD + 2 * kQT);
   const float *p0 = part + int64_t(first) * stride + int64_t(h) * (kQT * kHD + 2 * kQT);
+  // partials in groups of 4 whose loads issue together (entries past ns read partial ns - 1 and are
+  // skipped); the merge itself runs in partial order
+  constexpr int G = 4;
   float M = -FLT_MAX;
-  for (int s = 0; s < ns; ++s) {
-    const float *ml = p0 + s * stride + kQT * kHD + 2 * r;
-    if (ml[1] > 0.0f) M = fmaxf(M, ml[0]);
+  for (int s0 = 0; s0 < ns; s0 += G) {
+    float2 ml[G];
+#pragma unroll
+    for (int u = 0; u < G; ++u)
+      ml[u] = *reinterpret_cast<const float2 *>(p0 + min(s0 + u, ns - 1) * stride + kQT * kHD + 2 * r);
+#pragma unroll
+    for (int u = 0; u < G; ++u)
+      if (s0 + u < ns && ml[u].y > 0.0f) M = fmaxf(M, ml[u].x);
   }
-  float L = 0.0f, o[16];
+  float L = 0.0f;
+  float4v o[4];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) o[e] = 0.0f;
-  for (int s = 0; s < ns; ++s) {
-    const float *ps = p0 + s * stride;
-    const float *ml = ps + kQT * kHD + 2 * r;
-    if (!(ml[1] > 0.0f)) continue;
-    const float f = expf(ml[0] - M);
-    L += f * ml[1];
-    const float4 *src = reinterpret_cast<const float4 *>(ps + r * kHD + d0);
+  for (int e = 0; e < 4; ++e) o[e] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = 0; s0 < ns; s0 += G) {
+    float2 ml[G];
+    float4v v[G][4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float4 v = src[e];
-      o[4 * e] += f * v.x;
-      o[4 * e + 1] += f * v.y;
-      o[4 * e + 2] += f * v.z;
-      o[4 * e + 3] += f * v.w;
+    for (int u = 0; u < G; ++u) {
+      const float *ps = p0 + min(s0 + u, ns - 1) * stride;
+      ml[u] = *reinterpret_cast<const float2 *>(ps + kQT * kHD + 2 * r);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[u][e] = reinterpret_cast<const float4v *>(ps + r * kHD + d0)[e];
+    }
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      if (!(s0 + u < ns && ml[u].y > 0.0f)) continue;
+      const float f = expf(ml[u].x - M);
+      L += f * ml[u].y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[e][c] += f * v[u][e][c];
     }
   }
   const float inv = 1.0f / L;
   const int t = row0 + r;
-  const float *gate = proj + int64_t(t) * ldp + h * 2 * kHD + kHD;
+  const float4v *gate = reinterpret_cast<const float4v *>(proj + int64_t(t) * ldp + h * 2 * kHD + kHD + d0);
   const int qw = hq * kHD;
+  typedef _Float16 half8v_ __attribute__((ext_vector_type(8)));
+  half8v_ hi[2], lo[2];
 #pragma unroll
-  for (int e = 0; e < 16; ++e)
-    store_planes(y, ylo, int64_t(t) * qw + h * kHD + d0 + e, o[e] * inv * sigmoidf_(gate[d0 + e]));
+  for (int e = 0; e < 4; ++e) {
+    const float4v g = gate[e];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      _Float16 hh, ll;
+      split_f16(o[e][c] * inv * sigmoidf_(g[c]), hh, ll);
+      hi[e >> 1][4 * (e & 1) + c] = hh;
+      lo[e >> 1][4 * (e & 1) + c] = ll;
+    }
+  }
+  const int64_t at = int64_t(t) * qw + h * kHD + d0;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    reinterpret_cast<half8v_ *>(y + at)[k] = hi[k];
+    if (ylo) reinterpret_cast<half8v_ *>(ylo + at)[k] = lo[k];
+  }
 }
 
 }  // namespace
