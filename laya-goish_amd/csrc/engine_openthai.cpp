@@ -61,7 +61,8 @@ void Engine::load_openthai(const Gguf &g) {
   }
   const int lw = nh * 128, cd = 3 * lw;
   ldp_full_ = (2 * hq + 2 * hkv) * 256;
-  ldp_delta_ = (cd + lw + 2 * nh + 127) / 128 * 128;
+  // padded to a multiple of 256 rows, the 256 x 256 GEMM's tile width
+  ldp_delta_ = (cd + lw + 2 * nh + 255) / 256 * 256;
 
   // weight arena: every tensor but the embedding table as f32 at most, plus the pad rows of
   // the DeltaNet projections and the RoPE tables
@@ -72,7 +73,7 @@ void Engine::load_openthai(const Gguf &g) {
     for (auto v : t.dims) count *= v;
     total += align256(count * 4) + 512;
   }
-  total += size_t(L) * (align256(size_t(128) * d * 4) + 512) + 2 * (align256(size_t(ctx) * 32 * 4) + 512) + 4096;
+  total += size_t(L) * (align256(size_t(256) * d * 4) + 512) + 2 * (align256(size_t(ctx) * 32 * 4) + 512) + 4096;
   arena_size_ = total;
   if (hipMalloc(&arena_, arena_size_) != hipSuccess) {
     arena_ = nullptr;
@@ -104,7 +105,7 @@ void Engine::load_openthai(const Gguf &g) {
     } else {
       const std::string a = p + "linear_attn.";
       y.proj = upload_matrix(g, {a + "in_proj_qkv.weight", a + "in_proj_z.weight", a + "in_proj_a.weight", a + "in_proj_b.weight"},
-                             d, 128);
+                             d, 256);
       if (y.proj.rows != ldp_delta_ || named_[a + "in_proj_qkv.weight"].rows != cd || named_[a + "in_proj_z.weight"].rows != lw ||
           named_[a + "in_proj_a.weight"].rows != nh)
         fail(LG_ERR_FORMAT, "%slinear_attn: unexpected matrix shape", p.c_str());
@@ -119,6 +120,9 @@ void Engine::load_openthai(const Gguf &g) {
     if (y.wi.rows != 2 * f) fail(LG_ERR_FORMAT, "%smlp.gate_proj.weight: unexpected matrix shape", p.c_str());
     y.wd = upload_matrix(g, {p + "mlp.down_proj.weight"}, f);
     if (y.wd.rows != d) fail(LG_ERR_FORMAT, "%smlp.down_proj.weight: unexpected matrix shape", p.c_str());
+    // F16 matrices are their own operand form for the large-batch 256 x 256 GEMM (nothing allocated)
+    for (DevMatrix *m : {&y.proj, &y.out, &y.wi, &y.wd})
+      if (m->kind == LG_F16) add_prefill_copy(*m);
   }
   final_norm_ = upload_vector_f32(g, "model.norm.weight", d, 1.0f);
   head_ = upload_matrix(g, {"slot_head.weight"}, d);
