@@ -43,7 +43,8 @@ __device__ __forceinline__ void store_planes(_Float16 *hi, _Float16 *lo, int64_t
 // in the sequence; rows of one sequence are consecutive), silu, then per head
 // query = q / |q| / sqrt(128), key = k / |k| (|x| = sqrt(x.x + 1e-6)), log-decay and beta.
 // model.rs:306-318 (conv), :323-331 (scales, decay, beta).
-__global__ __launch_bounds__(256) void ot_delta_prep_kernel(const float *__restrict__ proj, int ldp, int T,
+constexpr int kPrepThreads = 512;
+__global__ __launch_bounds__(kPrepThreads) void ot_delta_prep_kernel(const float *__restrict__ proj, int ldp, int T,
                                                             const int32_t *__restrict__ tok_pos,
                                                             const float *__restrict__ conv,
                                                             const float *__restrict__ alog,
@@ -59,44 +60,72 @@ __global__ __launch_bounds__(256) void ot_delta_prep_kernel(const float *__restr
   const int lw = nh * kLK, cd = 3 * lw;
   const int pos = tok_pos[t];
   const float *row = proj + int64_t(t) * ldp;
-  // four channels a thread: one 16-byte load per tap row and four of taps (conv is [channel][4 taps])
+  const int h_ab = min(int(threadIdx.x), nh - 1);
+  const float a = row[cd + lw + h_ab], b = row[cd + lw + nh + h_ab];
+  // four channels a thread: one 16-byte load per tap row and four of taps (conv is [channel][4 taps]); a
+  // thread's loads for three rounds of 4 * kPrepThreads channels (every channel of a 16-head layer) are
+  // issued before any of them is used (a round past the row clamped into it: its results are not stored).
+  // q and k channels go to LDS for their norms, v channels straight out to vbuf.
   const float4v zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int c = 4 * threadIdx.x; c < cd; c += 4 * 256) {
-    const float4v x0 = *reinterpret_cast<const float4v *>(row + c);
-    const float4v x1 = pos >= 1 ? *reinterpret_cast<const float4v *>(row + c - int64_t(ldp)) : zero4;
-    const float4v x2 = pos >= 2 ? *reinterpret_cast<const float4v *>(row + c - 2 * int64_t(ldp)) : zero4;
-    const float4v x3 = pos >= 3 ? *reinterpret_cast<const float4v *>(row + c - 3 * int64_t(ldp)) : zero4;
-    float4v o;
+  constexpr int kR = 3;
+  for (int c0 = 4 * int(threadIdx.x); c0 < cd; c0 += kR * 4 * kPrepThreads) {
+    float4v x[kR][4];
+    float4 w[kR][4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float4 w = reinterpret_cast<const float4 *>(conv)[c + e];
-      float v = 0.0f;
-      if (pos >= 3) v = v + x3[e] * w.x;
-      if (pos >= 2) v = v + x2[e] * w.y;
-      if (pos >= 1) v = v + x1[e] * w.z;
-      v = v + x0[e] * w.w;
-      o[e] = siluf_(v);
+    for (int j = 0; j < kR; ++j) {
+      const int c = min(c0 + j * 4 * kPrepThreads, cd - 4);
+      x[j][0] = *reinterpret_cast<const float4v *>(row + c);
+      x[j][1] = pos >= 1 ? *reinterpret_cast<const float4v *>(row + c - int64_t(ldp)) : zero4;
+      x[j][2] = pos >= 2 ? *reinterpret_cast<const float4v *>(row + c - 2 * int64_t(ldp)) : zero4;
+      x[j][3] = pos >= 3 ? *reinterpret_cast<const float4v *>(row + c - 3 * int64_t(ldp)) : zero4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[j][e] = reinterpret_cast<const float4 *>(conv)[c + e];
     }
-    *reinterpret_cast<float4v *>(s_x + c) = o;
+#pragma unroll
+    for (int j = 0; j < kR; ++j) {
+      const int c = c0 + j * 4 * kPrepThreads;
+      if (c >= cd) break;
+      float4v o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float v = 0.0f;
+        if (pos >= 3) v = v + x[j][3][e] * w[j][e].x;
+        if (pos >= 2) v = v + x[j][2][e] * w[j][e].y;
+        if (pos >= 1) v = v + x[j][1][e] * w[j][e].z;
+        v = v + x[j][0][e] * w[j][e].w;
+        o[e] = siluf_(v);
+      }
+      if (c < 2 * lw) *reinterpret_cast<float4v *>(s_x + c) = o;
+      else *reinterpret_cast<float4v *>(vbuf + int64_t(t) * lw + (c - 2 * lw)) = o;
+    }
   }
   __syncthreads();
+  // per-head norms, four vectors of a wave at a time (vec < nh: q of head vec; else k of head vec - nh)
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  for (int vec = wv; vec < 2 * nh; vec += 4) {  // vec < nh: q of head vec; else k of head vec - nh
-    const int h = vec < nh ? vec : vec - nh;
-    const float *x = s_x + (vec < nh ? 0 : lw) + h * kLK;
-    const float x0 = x[lane], x1 = x[lane + 64];
-    const float ss = wave_sum_dpp(x0 * x0 + x1 * x1);
-    float sc = 1.0f / sqrtf(ss + 1e-6f);
-    if (vec < nh) sc = sc / sqrtf(128.0f);
-    float *dst = qk + (int64_t(t) * nh + h) * (2 * kLK) + (vec < nh ? 0 : kLK);
-    dst[lane] = x0 * sc;
-    dst[lane + 64] = x1 * sc;
+  for (int v0 = wv; v0 < 2 * nh; v0 += 4 * (kPrepThreads / 64)) {
+    float x0[4], x1[4], ss[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int vec = min(v0 + i * (kPrepThreads / 64), 2 * nh - 1);
+      x0[i] = s_x[vec * kLK + lane];
+      x1[i] = s_x[vec * kLK + lane + 64];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ss[i] = wave_sum_dpp(x0[i] * x0[i] + x1[i] * x1[i]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int vec = v0 + i * (kPrepThreads / 64);
+      if (vec >= 2 * nh) break;
+      const int h = vec < nh ? vec : vec - nh;
+      float sc = 1.0f / sqrtf(ss[i] + 1e-6f);
+      if (vec < nh) sc = sc / sqrtf(128.0f);
+      float *dst = qk + (int64_t(t) * nh + h) * (2 * kLK) + (vec < nh ? 0 : kLK);
+      dst[lane] = x0[i] * sc;
+      dst[lane + 64] = x1[i] * sc;
+    }
   }
-  for (int c = 4 * threadIdx.x; c < lw; c += 4 * 256)
-    *reinterpret_cast<float4v *>(vbuf + int64_t(t) * lw + c) = *reinterpret_cast<const float4v *>(s_x + 2 * lw + c);
   if (threadIdx.x < nh) {
     const int h = threadIdx.x;
-    const float a = row[cd + lw + h], b = row[cd + lw + nh + h];
     // the log of the decay a_t = exp(-exp(A_log) softplus(a + dt)); the chunked scan takes exp of sums of these
     gb[(int64_t(t) * nh + h) * 2] = -expf(alog[h]) * softplusf_(a + dt[h]);
     gb[(int64_t(t) * nh + h) * 2 + 1] = sigmoidf_(b);
@@ -925,9 +954,9 @@ void launch_ot_delta_prep(const float *proj, int ldp, int T, const int32_t *tok_
                           hipStream_t st) {
   LG_REQUIRE(T > 0 && nh > 0 && nh <= 32, "delta prep: bad shape T=%d nh=%d", T, nh);
   LG_REQUIRE(ldp % 4 == 0 && ldp >= 3 * nh * kLK + nh * kLK + 2 * nh, "delta prep: projection row %d too short", ldp);
-  const size_t lds = size_t(3) * nh * kLK * sizeof(float);
+  const size_t lds = size_t(2) * nh * kLK * sizeof(float);  // the q and k rows of one token
   const int per = (T + 7) / 8;
-  hipLaunchKernelGGL(ot_delta_prep_kernel, dim3(8 * per), dim3(256), lds, st, proj, ldp, T, tok_pos, conv, alog, dt, nh,
+  hipLaunchKernelGGL(ot_delta_prep_kernel, dim3(8 * per), dim3(kPrepThreads), lds, st, proj, ldp, T, tok_pos, conv, alog, dt, nh,
                      qk, vbuf, gb);
   HIP_CHECK(hipGetLastError());
 }
