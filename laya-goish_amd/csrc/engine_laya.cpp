@@ -236,11 +236,19 @@ void Engine::run_laya(BatchPlan &b, const int32_t *qtype_dev, lg_cancel_fn cance
                     nullptr, nullptr, h, stream);
   prof.end(double(T) * d * 12, 0, stream);
   auto attention = [&](const LayaLayer &y, bool rope) {
-    gemm(x16, x16lo, T, y.qkv.w, Epi::F32, qkv, nullptr, nullptr, 3 * d, y.qkv.b);
+    const float *cosT = y.full ? laya_cos_full_ : laya_cos_slide_, *sinT = y.full ? laya_sin_full_ : laya_sin_slide_;
+    // the 256 x 256 GEMM rotates q and k in its epilogue (the same bits as the RoPE kernel after it)
+    const bool fused = rope && x16lo && hd == 64 && (d / hd) % 2 == 0 && gemm_wide_takes(T, y.qkv.w, Epi::F32);
+    if (fused) {
+      const _Float16 *ks = chunk_sums(x16, x16lo, T, y.qkv.w);
+      prof.begin_kernel("gemm");
+      launch_gemm_wide_laya_rope(x16, x16lo, T, y.qkv.w, y.qkv.b, cosT, sinT, b.tok_pos, d / hd, qkv, 3 * d, stream, ks);
+      prof.end_kernel(double(y.qkv.w.bytes()) + double(T) * d * 2, 2.0 * T * double(y.qkv.w.rows) * d);
+    } else {
+      gemm(x16, x16lo, T, y.qkv.w, Epi::F32, qkv, nullptr, nullptr, 3 * d, y.qkv.b);
+    }
     prof.begin("laya_attn", stream);
-    if (rope)
-      launch_laya_rope(qkv, T, d, hd, y.full ? laya_cos_full_ : laya_cos_slide_, y.full ? laya_sin_full_ : laya_sin_slide_,
-                       b.tok_pos, stream);
+    if (rope && !fused) launch_laya_rope(qkv, T, d, hd, cosT, sinT, b.tok_pos, stream);
     launch_laya_attn(qkv, d, hd, y.full ? -1 : 64, b.tile_row0, b.tile_pos0, b.tile_n, b.tile_seq, b.seq_n, b.ntiles,
                      att, attlo, stream);
     prof.end(0, 0, stream);

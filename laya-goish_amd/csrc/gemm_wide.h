@@ -44,6 +44,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 enum Mode { WQ8 = 0, W1 = 1, W2 = 2, WQ4 = 3 };
 // epilogue of the fused q|k|v projection (RoPE, q planes, KV cache stores; RopeKvOut)
 constexpr int kEpiRopeKv = 16;
+// epilogue of the encoder's q|k|v projection: f32 rows as Epi::F32 stores them, q and k rotated
+// (head_dim 64; RopeKvOut's cosT, sinT, tok_pos and hq)
+constexpr int kEpiLayaRope = 17;
 
 constexpr int BM = 256, BN = 256, BK = 32, WAVES = 8, THREADS = 64 * WAVES;
 constexpr int ROWB = BK * 2;      // bytes per LDS row of one plane
@@ -77,7 +80,7 @@ __device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
 
 __device__ __forceinline__ float silu_f(float g) { return g * (1.0f / (1.0f + __expf(-g))); }
 
-// EPI: Epi values (F32, ADD, SWIGLU, GEGLU) or kEpiRopeKv.  For SWIGLU and GEGLU the workgroup's 256 weight
+// EPI: Epi values (F32, ADD, SWIGLU, GEGLU), kEpiRopeKv or kEpiLayaRope.  For SWIGLU and GEGLU the workgroup's 256 weight
 // rows are 128 gate rows and the 128 matching up rows: wave column wn holds gate rows in its column blocks
 // 0-3 and the up rows of the same output columns in blocks 4-7.
 template <int EPI, int MODE>
@@ -590,6 +593,43 @@ __global__ __launch_bounds__(THREADS, 1) void gemm_wide_kernel(
             }
           }
         }
+      }
+    }
+  } else if constexpr (EPI == kEpiLayaRope) {
+    // the wave's 128 columns are two 64-dim heads of q, k or v (the q width hq * 64 is a multiple of
+    // 128); q and k pairs (d, d + 32) are column blocks j and j + 2 of the same lane, rotated by
+    // rope_pair from the row's position as the encoder's RoPE kernel rotates the F32 epilogue's values
+    const int cw = nt * BN + wn * 128;
+    const bool rot = cw < 2 * ro.hq * 64;
+    float bv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) bv[j] = bias ? bias[cw + j * 16 + lr] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * 64 + i * 16 + (lane >> 4) * 4 + r;
+        if (row >= M) continue;
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          v[j] = acc[i][j][r];
+          if (bias) v[j] += bv[j];
+        }
+        if (rot) {
+          const int64_t tb = int64_t(ro.tok_pos[row]) * 64;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            if (j & 2) continue;  // blocks 0, 1, 4, 5 hold dims d < 32 of their head
+            const int64_t e = tb + (j & 1) * 16 + lr;
+            float a, c;
+            rope_pair(v[j], v[j + 2], ro.cosT[e], ro.sinT[e], ro.cosT[e + 32], ro.sinT[e + 32], a, c);
+            v[j] = a;
+            v[j + 2] = c;
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) C[int64_t(row) * ldc + cw + j * 16 + lr] = v[j];
       }
     }
   } else {

@@ -96,7 +96,7 @@ int wide_mode(int M, const DevMatrix &W, int EPI) {
     default: return -1;
   }
   if (EPI != int(Epi::F32) && EPI != int(Epi::ADD) && EPI != int(Epi::SWIGLU) && EPI != int(Epi::GEGLU) &&
-      EPI != kEpiRopeKv)
+      EPI != kEpiRopeKv && EPI != kEpiLayaRope)
     return -1;
   const bool glu = EPI == int(Epi::SWIGLU) || EPI == int(Epi::GEGLU);
   const int N = W.rows, K = W.cols;
@@ -134,7 +134,6 @@ void launch_wide(WideFn fn, int mode, const _Float16 *A, const _Float16 *Alo, in
   static const int lds_bytes[4] = {Geo<WQ8>::kLdsBytes, Geo<W1>::kLdsBytes, Geo<W2>::kLdsBytes, Geo<WQ4>::kLdsBytes};
   const int N = W.rows, K = W.cols;
   const int NT = glu ? (N / 2) / (BN / 2) : N / BN;
-  const bool rope = ro.tok_pos != nullptr;
   // activation rows per launch: the planes' buffer offsets are 32-bit
   const int64_t rows_cap = ((int64_t(1) << 31) - 1) / (int64_t(K) * 2) / BM * BM;
   LG_REQUIRE(rows_cap > 0, "gemm: K=%d too large", K);
@@ -151,13 +150,11 @@ void launch_wide(WideFn fn, int mode, const _Float16 *A, const _Float16 *Alo, in
     const _Float16 *Ac = A + int64_t(m0) * K, *Alc = Alo + int64_t(m0) * K;
     float *Cc = C ? C + int64_t(m0) * ldc : nullptr;
     _Float16 *C16c = C16 ? C16 + int64_t(m0) * ldc : nullptr, *C16lc = C16lo ? C16lo + int64_t(m0) * ldc : nullptr;
-    RopeKvOut rc = ro;
-    if (rope) {
-      rc.tok_pos += m0;
-      rc.tok_page += m0;
-      rc.q16 += int64_t(m0) * ro.hq * 128;
-      rc.q16lo += int64_t(m0) * ro.hq * 128;
-    }
+    RopeKvOut rc = ro;  // per-row tables and q planes of the rotating epilogues start at row m0
+    if (rc.tok_pos) rc.tok_pos += m0;
+    if (rc.tok_page) rc.tok_page += m0;
+    if (rc.q16) rc.q16 += int64_t(m0) * ro.hq * 128;
+    if (rc.q16lo) rc.q16lo += int64_t(m0) * ro.hq * 128;
     KqCorr kq;
     if (mode == WQ4) {
       kq.kp = W.pkp;
@@ -210,6 +207,25 @@ bool launch_gemm_wide_rope(const _Float16 *A, const _Float16 *Alo, int M, const 
   LG_REQUIRE(ro.kv_planes == 1 || ro.kv_planes == 2, "gemm rope: KV pools hold 1 or 2 planes, not %d", ro.kv_planes);
   launch_wide(wide_fn<kEpiRopeKv>(mode), mode, A, Alo, M, W, false, nullptr, nullptr, nullptr, 0, bias, ro, st, ks);
   return true;
+}
+
+void launch_gemm_wide_laya_rope(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, const float *bias,
+                                const float *cosT, const float *sinT, const int32_t *tok_pos, int heads, float *C,
+                                int ldc, hipStream_t st, const _Float16 *ks) {
+  using namespace wide;
+  LG_REQUIRE(A && Alo && C && cosT && sinT && tok_pos, "gemm laya rope: missing operand");
+  const int mode = wide_mode(M, W, kEpiLayaRope);
+  LG_REQUIRE(mode >= 0, "gemm laya rope: the 256 x 256 GEMM does not take %d rows of this matrix", M);
+  LG_REQUIRE(mode != WQ4 || ks, "gemm: an exact Q4_K launch needs its activation's chunk sums");
+  LG_REQUIRE(heads > 0 && heads % 2 == 0 && W.rows == 3 * heads * 64 && ldc >= W.rows,
+             "gemm laya rope: %d rows are not q|k|v of an even number of 64-dim heads (%d)", W.rows, heads);
+  RopeKvOut ro;
+  ro.cosT = cosT;
+  ro.sinT = sinT;
+  ro.tok_pos = tok_pos;
+  ro.hq = heads;
+  ro.hd = 64;
+  launch_wide(wide_fn<kEpiLayaRope>(mode), mode, A, Alo, M, W, false, C, nullptr, nullptr, ldc, bias, ro, st, ks);
 }
 
 }  // namespace lg

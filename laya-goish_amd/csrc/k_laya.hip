@@ -101,9 +101,10 @@ __global__ __launch_bounds__(kT) void laya_rope_kernel(float *__restrict__ qkv, 
   for (int e = threadIdx.x; e < d; e += kT) {  // 2 parts x (d / 64) heads x 32 pairs
     const int part = e / (d / 2), rem = e % (d / 2), hh = rem / 32, j = rem % 32;
     float *x = row + part * d + hh * kHD;
-    const float a = x[j], b = x[j + 32];
-    x[j] = a * cs[j] - b * sn[j];
-    x[j + 32] = b * cs[j + 32] + a * sn[j + 32];
+    float a, c;
+    rope_pair(x[j], x[j + 32], cs[j], sn[j], cs[j + 32], sn[j + 32], a, c);  // as the wide GEMM's epilogue
+    x[j] = a;
+    x[j + 32] = c;
   }
 }
 

@@ -180,6 +180,13 @@ bool launch_gemm_wide_rope(const _Float16 *A, const _Float16 *Alo, int M, const 
 // Whether the 256 x 256 exact GEMM takes an M-row launch of W with epilogue epi (shape, prefill
 // copy and tile count; pointers are checked at launch).
 bool gemm_wide_takes(int M, const DevMatrix &W, Epi epi);
+// The encoder's q|k|v projection (W rows: q, k, v of `heads` 64-dim heads, an even count) on the
+// 256 x 256 exact GEMM, its epilogue storing the f32 rows [M][ldc] with q and k rotated: the same bits
+// as the F32 GEMM followed by launch_laya_rope.  Only for launches gemm_wide_takes(M, W, Epi::F32)
+// accepts; anything else fails.  cosT, sinT: [ctx][64]; tok_pos: per row.
+void launch_gemm_wide_laya_rope(const _Float16 *A, const _Float16 *Alo, int M, const DevMatrix &W, const float *bias,
+                                const float *cosT, const float *sinT, const int32_t *tok_pos, int heads, float *C,
+                                int ldc, hipStream_t st, const _Float16 *ks = nullptr);
 // Short launches (fewer than 128 tiles of 64 x 64) of an F16 or Q8_0 q|k|v projection in the exact
 // split mode: the 32-row tile GEMM with the same rotating epilogue as launch_gemm_wide_rope (head_dim
 // 64 or 128, ro.col0 a multiple of it), the same bits as the F32 GEMM followed by the RoPE kernel.
