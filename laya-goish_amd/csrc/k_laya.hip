@@ -64,25 +64,35 @@ __global__ __launch_bounds__(kT) void layer_norm_kernel(const float *__restrict_
   }
   const float scale = 1.0f / sqrtf(block_sum_ln(q, red) / float(d) + eps);
   const float *addrow = add ? add + int64_t(sel[seq[r]]) * d : nullptr;
+  // a thread's four consecutive values: 16-byte loads of w, b and the add row, one 16-byte f32 or
+  // 8-byte store per f16 plane
+  typedef _Float16 half4_ __attribute__((ext_vector_type(4)));
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int k = threadIdx.x + i * kT;
     if (k >= n4) continue;
     const float in[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+    const float4 w4 = w ? reinterpret_cast<const float4 *>(w)[k] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    const float4 b4 = b ? reinterpret_cast<const float4 *>(b)[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float4 a4 = addrow ? reinterpret_cast<const float4 *>(addrow)[k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float wv[4] = {w4.x, w4.y, w4.z, w4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w}, av[4] = {a4.x, a4.y, a4.z, a4.w};
+    float4v o;
+    half4_ h4, l4;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int j = 4 * k + e;
-      float o = (in[e] - mean) * scale * (w ? w[j] : 1.0f) + (b ? b[j] : 0.0f);
-      if (addrow) o = o + addrow[j];
-      const int64_t at = int64_t(r) * d + j;
-      if (y32) {
-        y32[at] = o;
-      } else {
-        _Float16 h, hl;
-        split_f16(o, h, hl);
-        y16[at] = h;
-        if (y16lo) y16lo[at] = hl;
-      }
+      o[e] = (in[e] - mean) * scale * wv[e] + bv[e];
+      if (addrow) o[e] = o[e] + av[e];
+      _Float16 h, hl;
+      split_f16(o[e], h, hl);
+      h4[e] = h;
+      l4[e] = hl;
+    }
+    const int64_t at = int64_t(r) * d + 4 * k;
+    if (y32) {
+      *reinterpret_cast<float4v *>(y32 + at) = o;
+    } else {
+      *reinterpret_cast<half4_ *>(y16 + at) = h4;
+      if (y16lo) *reinterpret_cast<half4_ *>(y16lo + at) = l4;
     }
   }
 }
